@@ -1,0 +1,127 @@
+/* g4_oracle.h -- CPU restatement of the reference's speculative-verify path.
+ *
+ * TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker (or as the
+ * timed CPU baseline).  The product library never links it.
+ *
+ * Every function restates, in scalar C with explicit fmaf()/fma() calls, the
+ * fp32 operation order of the reference function it cites
+ * (dayaswaroopchavali/gemma4-e2b-laptop-cpu, files under engine/).  The file
+ * is compiled with -ffp-contract=off so the compiler adds no contraction of
+ * its own; every contraction that GCC performs in the reference build
+ * (-O3 -march=x86-64-v3, default -ffp-contract=fast) is written out here.
+ *
+ * Pinning (what checks each function): see oracle/README.md.
+ */
+#ifndef G4_ORACLE_H
+#define G4_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar numerics (engine/gemma4_engine.cpp:33-60, 318-404) ---- */
+uint16_t g4o_f2bf(float f);
+float g4o_bf2f(uint16_t b);
+float g4o_r16(float f);
+float g4o_exp8(float x);
+float g4o_gelu8(float x);
+double g4o_sumsq(const float* x, int n);
+float g4o_rms_inv(const float* x, int n);
+void g4o_rms(const float* x, const float* w, int n, float* y);
+void g4o_rms_r16_inplace(float* x, const float* w, int n);
+void g4o_rope(float* h, const float* cs, const float* sn, int hd);
+void g4o_rope_tables(int ctx, int hd, double theta, double rot_frac, float* cs, float* sn);
+float g4o_cap(float s);
+float g4o_calc_thr(float L);
+void g4o_vec_exp8(const float* x, int n, float* y);
+void g4o_vec_gelu8(const float* x, int n, float* y);
+
+/* ---- W4G32 (engine/w4g32_avx2.h) ---- */
+void g4o_prep_x(const float* x, int K, float* xe, float* xo, float* gs);
+void g4o_w4g32_rows(const uint8_t* W, const uint16_t* S, const float* xe, const float* xo,
+                    const float* gs, int K, int M, int n0, int n1, float* Y, int ldy);
+void g4o_w4g32_gemm(const uint8_t* W, const uint16_t* S, const float* X, int M, int N, int K,
+                    float* Y);
+
+/* ---- W4A8 (engine/w4a8_avx2.h) ---- */
+void g4o_w4a8_quant(const float* X, int M, int K, int8_t* q, float* sx, int32_t* sum);
+void g4o_w4a8_gemm(const uint8_t* W, const uint16_t* S, const float* X, int M, int N, int K,
+                   float* Y);
+
+/* ---- exp3-packed bf16 head (engine/bf16_exp3_head.h) ---- */
+void g4o_exp3_codebook(const uint16_t* E, int64_t n, uint8_t cb8[8]);
+int64_t g4o_exp3_count(const uint16_t* W, int N, int K, const uint8_t cb8[8], int64_t* exc_ptr);
+void g4o_exp3_pack(const uint16_t* W, int N, int K, const uint8_t cb8[8], uint8_t* data,
+                   const int64_t* exc_ptr, uint16_t* exc_col, float* exc_delta);
+float g4o_exp3_dot(const uint8_t* data, const uint8_t cb8[8], const int64_t* exc_ptr,
+                   const uint16_t* exc_col, const float* exc_delta, int K, int n, const float* x);
+void g4o_exp3_gemm(const uint8_t* data, const uint8_t cb8[8], const int64_t* exc_ptr,
+                   const uint16_t* exc_col, const float* exc_delta, int N, int K, const float* X,
+                   int M, float* Y);
+
+/* ---- certified head screen (engine/gemma4_engine.cpp:445-579, 1235-1244, 1409-1498) ---- */
+void g4o_screen_build(const uint16_t* E, int N, int K, uint8_t* Wq, uint16_t* Sq, float* coef);
+
+typedef struct {
+  int G;            /* greedy token (lowest-index tie rule) */
+  int fallback;     /* 1: full head was evaluated */
+  int ref_overflow; /* 1: the reference's single-thread scan overflows its 16384 list */
+  int nsurv;        /* survivors {U >= thr} (may exceed the limit) */
+  float Lmax, thr, vmax;
+} g4o_head_info;
+
+/* one row: h (bf16-valued, length K), full-head and screen data.  surv (capacity cap_surv)
+ * receives survivors in ascending order, sval their r16 rescored logits.  seeds: lower-bound
+ * seed rows (may be NULL). */
+void g4o_head_row(const float* h, int V, int K, const uint8_t* Wq, const uint16_t* Sq,
+                  const float* coef, const uint8_t* data, const uint8_t cb8[8],
+                  const int64_t* exc_ptr, const uint16_t* exc_col, const float* exc_delta,
+                  const int* seeds, int nseeds, int limit, int* surv, float* sval, int cap_surv,
+                  g4o_head_info* info);
+
+/* ---- split-KV attention (engine/gemma4_engine.cpp:738-877, 1019-1059) ---- */
+void g4o_attn_splitkv(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M,
+                      const float* q, int ldq, const int* pos, const int* lo, const int* skip_lo,
+                      const int* skip_hi, int kmin, int kmax, int T, float* out, int ldo,
+                      float* part_m, float* part_l);
+
+/* ---- synthetic decoder stack + verify step (engine/gemma4_engine.cpp:1256-1502, 1617-1661) ---- */
+typedef struct g4o_model g4o_model;
+g4o_model* g4o_model_new(uint64_t seed, int V, int NL, int I, int ctx);
+void g4o_model_free(g4o_model* m);
+void g4o_model_fake_ctx(g4o_model* m, int n, uint64_t seed);
+int g4o_model_bytes(const g4o_model* m, const char* what, void* dst, int64_t cap);
+
+typedef struct {
+  int nacc;      /* accepted drafts */
+  int branch;    /* 0: chain a (or none), 1: branch b */
+  int ncommit;   /* nacc + 1 */
+  int commit[8]; /* committed tokens G[path] */
+  int G[8];      /* greedy token per row, -1 where not evaluated */
+  int fallback[8];
+  int nsurv[8];
+} g4o_verify_out;
+
+/* one verify pass: toks[0] = confirmed token, toks[1..na] chain a, toks[na+1..na+nb] branch b;
+ * rows are at positions pos0.. ; fills out and commits (KV compaction for branch b). */
+void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
+                g4o_verify_out* out, float* hidden_out);
+
+/* forward of M rows that fills the KV cache only (want = false) */
+void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T);
+
+/* ---- seeded input generators (g4_rng.h formulas) ---- */
+uint64_t g4o_stream(uint64_t seed, uint64_t tag);
+void g4o_gen_normal_f32(uint64_t seed, int64_t n, float scale, float* out);
+void g4o_gen_normal_bf16(uint64_t seed, int64_t n, float scale, uint16_t* out);
+void g4o_gen_bytes(uint64_t seed, int64_t n, uint8_t* out);
+void g4o_gen_scales(uint64_t seed, int64_t n, float lo, float span, uint16_t* out);
+void g4o_gen_ints(uint64_t seed, int64_t n, int32_t lo, int32_t hi, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

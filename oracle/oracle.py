@@ -1,0 +1,345 @@
+"""ctypes bindings for the C oracle (liboracle.so) and the reference harness (_ref/libg4ref.so).
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker (or the timed CPU baseline).  The product never imports it.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_ORACLE = os.path.join(HERE, "liboracle.so")
+LIB_REF = os.path.join(HERE, "_ref", "libg4ref.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+_vp = C.c_void_p
+_i, _i64, _u64, _f, _d = C.c_int, C.c_int64, C.c_uint64, C.c_float, C.c_double
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+class HeadInfo(C.Structure):
+    _fields_ = [("G", _i), ("fallback", _i), ("ref_overflow", _i), ("nsurv", _i),
+                ("Lmax", _f), ("thr", _f), ("vmax", _f)]
+
+
+class VerifyOut(C.Structure):
+    _fields_ = [("nacc", _i), ("branch", _i), ("ncommit", _i), ("commit", _i * 8), ("G", _i * 8),
+                ("fallback", _i * 8), ("nsurv", _i * 8)]
+
+
+class Oracle:
+    """The C restatement of the reference's verify path (see g4_oracle.h)."""
+
+    def __init__(self, path=LIB_ORACLE):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (run make -C oracle)")
+        L = self.L = C.CDLL(path)
+        sig = {
+            "g4o_f2bf": (C.c_uint16, [_f]), "g4o_bf2f": (_f, [C.c_uint16]), "g4o_r16": (_f, [_f]),
+            "g4o_exp8": (_f, [_f]), "g4o_gelu8": (_f, [_f]), "g4o_sumsq": (_d, [_f32p, _i]),
+            "g4o_rms_inv": (_f, [_f32p, _i]), "g4o_rms": (None, [_f32p, _vp, _i, _f32p]),
+            "g4o_rms_r16_inplace": (None, [_f32p, _vp, _i]),
+            "g4o_rope": (None, [_f32p, _f32p, _f32p, _i]),
+            "g4o_rope_tables": (None, [_i, _i, _d, _d, _f32p, _f32p]),
+            "g4o_cap": (_f, [_f]), "g4o_calc_thr": (_f, [_f]),
+            "g4o_vec_exp8": (None, [_f32p, _i, _f32p]), "g4o_vec_gelu8": (None, [_f32p, _i, _f32p]),
+            "g4o_prep_x": (None, [_f32p, _i, _f32p, _f32p, _f32p]),
+            "g4o_w4g32_gemm": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p]),
+            "g4o_w4a8_quant": (None, [_f32p, _i, _i, _i8p, _f32p, _i32p]),
+            "g4o_w4a8_gemm": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p]),
+            "g4o_exp3_codebook": (None, [_u16p, _i64, _u8p]),
+            "g4o_exp3_count": (_i64, [_u16p, _i, _i, _u8p, _i64p]),
+            "g4o_exp3_pack": (None, [_u16p, _i, _i, _u8p, _u8p, _i64p, _u16p, _f32p]),
+            "g4o_exp3_gemm": (None, [_u8p, _u8p, _i64p, _u16p, _f32p, _i, _i, _f32p, _i, _f32p]),
+            "g4o_screen_build": (None, [_u16p, _i, _i, _u8p, _u16p, _f32p]),
+            "g4o_head_row": (None, [_f32p, _i, _i, _u8p, _u16p, _f32p, _u8p, _u8p, _i64p, _u16p,
+                                    _f32p, _vp, _i, _i, _i32p, _f32p, _i, C.POINTER(HeadInfo)]),
+            "g4o_attn_splitkv": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _i32p,
+                                        _i32p, _i, _i, _i, _f32p, _i, _vp, _vp]),
+            "g4o_model_new": (_vp, [_u64, _i, _i, _i, _i]), "g4o_model_free": (None, [_vp]),
+            "g4o_model_fake_ctx": (None, [_vp, _i, _u64]),
+            "g4o_model_bytes": (_i, [_vp, C.c_char_p, _vp, _i64]),
+            "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
+            "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
+            "g4o_stream": (_u64, [_u64, _u64]),
+            "g4o_gen_normal_f32": (None, [_u64, _i64, _f, _f32p]),
+            "g4o_gen_normal_bf16": (None, [_u64, _i64, _f, _u16p]),
+            "g4o_gen_bytes": (None, [_u64, _i64, _u8p]),
+            "g4o_gen_scales": (None, [_u64, _i64, _f, _f, _u16p]),
+            "g4o_gen_ints": (None, [_u64, _i64, C.c_int32, C.c_int32, _i32p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # ---- generators ----
+    def stream(self, seed, tag):
+        return self.L.g4o_stream(seed, tag)
+
+    def normal_f32(self, seed, n, scale=1.0):
+        out = np.empty(n, np.float32)
+        self.L.g4o_gen_normal_f32(seed, n, scale, out)
+        return out
+
+    def normal_bf16(self, seed, n, scale=1.0):
+        out = np.empty(n, np.uint16)
+        self.L.g4o_gen_normal_bf16(seed, n, scale, out)
+        return out
+
+    def rand_bytes(self, seed, n):
+        out = np.empty(n, np.uint8)
+        self.L.g4o_gen_bytes(seed, n, out)
+        return out
+
+    def scales(self, seed, n, lo=0.005, span=0.015):
+        out = np.empty(n, np.uint16)
+        self.L.g4o_gen_scales(seed, n, lo, span, out)
+        return out
+
+    def ints(self, seed, n, lo, hi):
+        out = np.empty(n, np.int32)
+        self.L.g4o_gen_ints(seed, n, lo, hi, out)
+        return out
+
+    # ---- numerics ----
+    def bf2f(self, b):
+        return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+    def r16(self, x):
+        return np.array([self.L.g4o_r16(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))
+
+    def exp8(self, x):
+        x = _c(x, np.float32)
+        y = np.empty_like(x)
+        self.L.g4o_vec_exp8(x, x.size, y)
+        return y
+
+    def gelu8(self, x):
+        x = _c(x, np.float32)
+        y = np.empty_like(x)
+        self.L.g4o_vec_gelu8(x, x.size, y)
+        return y
+
+    def w4g32(self, W, S, X):
+        X = _c(X, np.float32)
+        M, K = X.shape
+        N = W.shape[0]
+        Y = np.empty((M, N), np.float32)
+        self.L.g4o_w4g32_gemm(_c(W, np.uint8), _c(S, np.uint16), X, M, N, K, Y)
+        return Y
+
+    def w4a8(self, W, S, X):
+        X = _c(X, np.float32)
+        M, K = X.shape
+        N = W.shape[0]
+        Y = np.empty((M, N), np.float32)
+        self.L.g4o_w4a8_gemm(_c(W, np.uint8), _c(S, np.uint16), X, M, N, K, Y)
+        return Y
+
+    def w4a8_quant(self, X):
+        X = _c(X, np.float32)
+        M, K = X.shape
+        q = np.empty((M, K), np.int8)
+        sx = np.empty((M, K // 32), np.float32)
+        sm = np.empty((M, K // 32), np.int32)
+        self.L.g4o_w4a8_quant(X, M, K, q, sx, sm)
+        return q, sx, sm
+
+    def exp3_pack(self, E, N, K):
+        E = _c(E, np.uint16)
+        cb = np.empty(8, np.uint8)
+        self.L.g4o_exp3_codebook(E, N * K, cb)
+        ptr = np.empty(N + 1, np.int64)
+        ne = self.L.g4o_exp3_count(E, N, K, cb, ptr)
+        data = np.empty(N * (K // 32) * 44, np.uint8)
+        col = np.empty(max(ne, 1), np.uint16)
+        dl = np.empty(max(ne, 1), np.float32)
+        self.L.g4o_exp3_pack(E, N, K, cb, data, ptr, col, dl)
+        return dict(cb=cb, data=data, ptr=ptr, col=col, delta=dl, N=N, K=K)
+
+    def exp3_gemm(self, P, X):
+        X = _c(X, np.float32)
+        M = X.shape[0]
+        Y = np.empty((M, P["N"]), np.float32)
+        self.L.g4o_exp3_gemm(P["data"], P["cb"], P["ptr"], P["col"], P["delta"], P["N"], P["K"], X, M, Y)
+        return Y
+
+    def screen_build(self, E, N, K):
+        Wq = np.empty(N * K // 2, np.uint8)
+        Sq = np.empty(N * K // 32, np.uint16)
+        coef = np.empty(N, np.float32)
+        self.L.g4o_screen_build(_c(E, np.uint16), N, K, Wq, Sq, coef)
+        return Wq, Sq, coef
+
+    def head_row(self, h, scr, P, seeds=None, limit=30000, cap=30000):
+        Wq, Sq, coef = scr
+        V = coef.size
+        K = P["K"]
+        surv = np.zeros(cap, np.int32)
+        sval = np.zeros(cap, np.float32)
+        info = HeadInfo()
+        sd = None if seeds is None else _c(seeds, np.int32)
+        self.L.g4o_head_row(_c(h, np.float32), V, K, Wq, Sq, coef, P["data"], P["cb"], P["ptr"],
+                            P["col"], P["delta"], None if sd is None else sd.ctypes.data,
+                            0 if sd is None else sd.size, limit, surv, sval, cap, C.byref(info))
+        n = min(info.nsurv, cap)
+        return info, surv[:n].copy(), sval[:n].copy()
+
+    def attn(self, Kc, Vc, hd, nh, q, pos, lo, skip_lo, skip_hi, kmin, kmax, T, parts=False):
+        q = _c(q, np.float32)
+        M = q.shape[0]
+        out = np.empty((M, nh * hd), np.float32)
+        pm = np.empty((T, M, nh), np.float32) if parts else None
+        pl = np.empty((T, M, nh), np.float32) if parts else None
+        self.L.g4o_attn_splitkv(_c(Kc, np.uint16), _c(Vc, np.uint16), hd, nh, M, q, nh * hd,
+                                _c(pos, np.int32), _c(lo, np.int32), _c(skip_lo, np.int32),
+                                _c(skip_hi, np.int32), kmin, kmax, T, out, nh * hd,
+                                None if pm is None else pm.ctypes.data,
+                                None if pl is None else pl.ctypes.data)
+        return (out, pm, pl) if parts else out
+
+
+class Model:
+    """Oracle synthetic decoder stack (g4_oracle_model.c)."""
+
+    def __init__(self, orc, seed, V, NL, I=6144, ctx=4096):
+        self.o, self.V, self.NL, self.I, self.ctx = orc, V, NL, I, ctx
+        self.h = orc.L.g4o_model_new(seed, V, NL, I, ctx)
+
+    def close(self):
+        if self.h:
+            self.o.L.g4o_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def fake_ctx(self, n, seed=12345):
+        self.o.L.g4o_model_fake_ctx(self.h, n, seed)
+
+    def get(self, what, dtype, count):
+        out = np.empty(count, dtype)
+        rc = self.o.L.g4o_model_bytes(self.h, what.encode(), out.ctypes.data, out.nbytes)
+        if rc != 0:
+            raise KeyError(what)
+        return out
+
+    def verify(self, toks, na, nb, pos0, T=8):
+        out = VerifyOut()
+        hid = np.empty(1536, np.float32)
+        self.o.L.g4o_verify(self.h, _c(toks, np.int32), na, nb, pos0, T, C.byref(out), hid.ctypes.data)
+        return out, hid
+
+
+class Ref:
+    """The reference engine's own kernels (oracle/_ref/libg4ref.so), one worker."""
+
+    def __init__(self, path=LIB_REF):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.L = C.CDLL(path)
+        sig = {
+            "ref_start": (_i, [_i]), "ref_threads": (_i, []),
+            "ref_w4g32": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p]),
+            "ref_w4a8": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p, _i8p, _f32p, _i32p]),
+            "ref_exp8": (None, [_f32p, _i, _f32p]), "ref_gelu8": (None, [_f32p, _i, _f32p]),
+            "ref_rbf8": (None, [_f32p, _i, _f32p]), "ref_f2bf": (None, [_f32p, _i, _u16p]),
+            "ref_ss": (_d, [_f32p, _i]), "ref_rms": (None, [_f32p, _vp, _i, _f32p]),
+            "ref_rms_r16_inplace": (None, [_f32p, _vp, _i]),
+            "ref_rms_prep_x": (None, [_f32p, _f32p, _i, _vp, _f32p, _f32p, _f32p, _i]),
+            "ref_add_res_prep_x": (None, [_f32p, _f32p, _i, _f32p, _f32p, _f32p]),
+            "ref_add_res_inplace": (None, [_f32p, _f32p, _i]),
+            "ref_rope": (None, [_f32p, _f32p, _f32p, _i]),
+            "ref_prep_x": (None, [_f32p, _i, _f32p, _f32p, _f32p]),
+            "ref_calc_thr": (_f, [_f]),
+            "ref_gate_up": (None, [_u8p, _u16p, _u8p, _u16p, _i, _i, _f32p, _i, _f32p, _f32p,
+                                   _f32p, _f32p, _f32p]),
+            "ref_attn": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _i32p, _i32p,
+                                _i, _i, _i, _f32p, _i, _vp, _vp, _vp, _vp, _vp]),
+            "ref_screen": (_i, [_u8p, _u16p, _f32p, _f32p, _i, _f32p, _i32p, _i32p, _f32p,
+                                _f32p, _i32p]),
+            "ref_exp3_pack": (_i64, [_u16p, _i, _i, _u8p]),
+            "ref_exp3_get": (None, [_u8p, _i64p, _u16p, _f32p]),
+            "ref_resc": (_f, [_f32p, _i32p, _i, _f32p]),
+            "ref_head": (None, [_f32p, _i, _f32p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        L.ref_start(1)
+
+    def w4g32(self, W, S, X):
+        X = _c(X, np.float32)
+        M, K = X.shape
+        N = W.shape[0]
+        Y = np.empty((M, N), np.float32)
+        self.L.ref_w4g32(_c(W, np.uint8), _c(S, np.uint16), X, M, N, K, Y)
+        return Y
+
+    def w4a8(self, W, S, X):
+        X = _c(X, np.float32)
+        M, K = X.shape
+        N = W.shape[0]
+        Y = np.empty((M, N), np.float32)
+        q = np.empty((M, K), np.int8)
+        sx = np.empty((M, K // 32), np.float32)
+        sm = np.empty((M, K // 32), np.int32)
+        self.L.ref_w4a8(_c(W, np.uint8), _c(S, np.uint16), X, M, N, K, Y, q, sx, sm)
+        return Y, q, sx, sm
+
+    def vec(self, name, x):
+        x = _c(x, np.float32)
+        y = np.empty_like(x)
+        getattr(self.L, name)(x, x.size, y)
+        return y
+
+    def exp3_pack(self, E, N, K, cb):
+        ne = self.L.ref_exp3_pack(_c(E, np.uint16), N, K, _c(cb, np.uint8))
+        data = np.empty(N * (K // 32) * 44, np.uint8)
+        ptr = np.empty(N + 1, np.int64)
+        col = np.empty(max(ne, 1), np.uint16)
+        dl = np.empty(max(ne, 1), np.float32)
+        self.L.ref_exp3_get(data, ptr, col, dl)
+        return dict(cb=np.array(cb, np.uint8), data=data, ptr=ptr, col=col[:ne], delta=dl[:ne], N=N, K=K)
+
+    def head(self, h):
+        h = _c(h, np.float32)
+        M = h.shape[0]
+        N = 262144 if False else None
+        return M, N
+
+    def attn(self, Kc, Vc, hd, nh, q, pos, lo, skip_lo, skip_hi, kmin, kmax, T, prep=False, parts=False):
+        q = _c(q, np.float32)
+        M = q.shape[0]
+        K = nh * hd
+        out = np.empty((M, K), np.float32)
+        xe = np.empty((M, K // 2), np.float32) if prep else None
+        xo = np.empty((M, K // 2), np.float32) if prep else None
+        gs = np.empty((M, K // 32), np.float32) if prep else None
+        pm = np.empty((T, M, nh), np.float32) if parts else None
+        pl = np.empty((T, M, nh), np.float32) if parts else None
+        ptr = lambda a: None if a is None else a.ctypes.data
+        self.L.ref_attn(_c(Kc, np.uint16), _c(Vc, np.uint16), hd, nh, M, q, K, _c(pos, np.int32),
+                        _c(lo, np.int32), _c(skip_lo, np.int32), _c(skip_hi, np.int32), kmin, kmax,
+                        T, out, K, ptr(xe), ptr(xo), ptr(gs), ptr(pm), ptr(pl))
+        res = [out]
+        if prep:
+            res += [xe, xo, gs]
+        if parts:
+            res += [pm, pl]
+        return res[0] if len(res) == 1 else tuple(res)
+
+
+def ref_available():
+    return os.path.exists(LIB_REF)
