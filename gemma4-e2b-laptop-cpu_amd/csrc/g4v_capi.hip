@@ -1,0 +1,825 @@
+// g4v_capi.hip -- the C ABI (include/g4v.h): context, uploads, the standalone kernel entry
+// points and the verify-step orchestration that restates the reference's fwd()/run_req.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/g4v.h"
+#include "g4v_head.h"
+#include "g4v_internal.h"
+#include "g4v_layer.h"
+
+using namespace g4v;
+
+namespace {
+
+struct DBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  DBuf() = default;
+  DBuf(const DBuf&) = delete;
+  DBuf& operator=(const DBuf&) = delete;
+  ~DBuf() { reset(); }
+  void reset() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  template <class T>
+  T* as() const { return static_cast<T*>(p); }
+};
+
+struct Mat {
+  DBuf wr, s;
+  int N = 0, K = 0;
+  W4Dev dev() const { return W4Dev{wr.as<uint4>(), s.as<uint16_t>(), N, K}; }
+};
+
+struct Layer {
+  Mat m[7];       // q, k, v, o, gate, up, down
+  DBuf norms;     // in_ln, post_attn, pre_ff, post_ff [H each], qn, kn [HD each]
+  float scalar = 0.75f;
+  int sliding = 1;
+  LayerNorms ln() const {
+    const float* b = norms.as<float>();
+    return LayerNorms{b, b + H, b + 2 * H, b + 3 * H, b + 4 * H, b + 4 * H + HD, scalar, sliding};
+  }
+};
+
+// scratch of one head pass
+struct HeadBufs {
+  DBuf u, list, sval, small;
+  HeadScratch hs{};
+};
+
+}  // namespace
+
+struct g4v_ctx {
+  int device = 0;
+  hipStream_t st = nullptr;
+  std::string err;
+  int lds_max = 65536;
+  int cus = 0;
+  std::vector<std::unique_ptr<Mat>> mats;  // standalone GEMV handles
+  DBuf gx, gy;                              // standalone GEMV io
+  // head
+  bool head_ready = false;
+  int V = 0;
+  DBuf E, dec, exc_ptr, exc_col, exc_del, cb, scr_wr, scr_s, coef, lut;
+  HeadDev hd{};
+  HeadBufs hb1, hb2;
+  DBuf hrow, hnrow;
+  // model
+  bool model_ready = false;
+  int NL = 0, I = 0, ctxcap = 0;
+  std::vector<std::unique_ptr<Layer>> L;
+  DBuf fnorm, KC, VC, rope;  // rope: [2][ctxcap][HD/2] cos then sin
+  // step buffers
+  DBuf x, xa, q, k, v, att, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
+  StepDev* step_host = nullptr;
+  VerifyResultDev* res_host = nullptr;
+  // attention standalone
+  DBuf ak, av, aq, ao;
+  ~g4v_ctx() {
+    if (step_host) (void)hipHostFree(step_host);
+    if (res_host) (void)hipHostFree(res_host);
+    if (st) (void)hipStreamDestroy(st);
+  }
+};
+
+#define HIPCHK(expr)                                                                       \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess) {                                                                \
+      c->err = std::string(#expr) + ": " + hipGetErrorString(e_);                          \
+      return G4V_E_HIP;                                                                    \
+    }                                                                                      \
+  } while (0)
+
+#define ARGCHK(cond, msg)        \
+  do {                           \
+    if (!(cond)) {               \
+      c->err = msg;              \
+      return G4V_E_ARG;          \
+    }                            \
+  } while (0)
+
+static int dalloc(g4v_ctx* c, DBuf& b, size_t n) {
+  b.reset();
+  if (n == 0) n = 16;
+  hipError_t e = hipMalloc(&b.p, n);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    c->err = std::string("hipMalloc(") + std::to_string(n) + "): " + hipGetErrorString(e);
+    return G4V_E_NOMEM;
+  }
+  b.n = n;
+  return 0;
+}
+#define ALLOC(buf, n)                       \
+  do {                                      \
+    int r_ = dalloc(c, buf, (size_t)(n));   \
+    if (r_) return r_;                      \
+  } while (0)
+
+// GEMV over M rows in passes whose staged activations fit the LDS budget
+static void gemv_passes(g4v_ctx* c, GemvArgs a, int epi, int M) {
+  const int G = a.K / 32;
+  int per = (int)(c->lds_max / ((size_t)G * 132));
+  if (per < 1) per = 1;
+  if (per > MAXM) per = MAXM;
+  for (int m0 = 0; m0 < M; m0 += per) {
+    GemvArgs b = a;
+    b.M = std::min(per, M - m0);
+    b.x = a.x + (size_t)m0 * a.ldx;
+    for (int i = 0; i < 3; ++i)
+      if (b.y[i]) b.y[i] = a.y[i] + (size_t)m0 * a.ldy[i];
+    launch_gemv(b, epi, c->st);
+  }
+}
+
+extern "C" {
+
+int g4v_create(int device, g4v_ctx** out) {
+  if (!out) return G4V_E_ARG;
+  auto* c = new g4v_ctx();
+  c->device = device;
+  *out = nullptr;
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) {
+    delete c;
+    return G4V_E_HIP;
+  }
+  e = hipStreamCreate(&c->st);
+  if (e != hipSuccess) {
+    delete c;
+    return G4V_E_HIP;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+    c->cus = prop.multiProcessorCount;
+    c->lds_max = (int)std::min<size_t>(prop.sharedMemPerBlock, 65536);
+  }
+  if (hipHostMalloc((void**)&c->step_host, sizeof(StepDev)) != hipSuccess ||
+      hipHostMalloc((void**)&c->res_host, sizeof(VerifyResultDev)) != hipSuccess) {
+    delete c;
+    return G4V_E_NOMEM;
+  }
+  *out = c;
+  return 0;
+}
+
+void g4v_destroy(g4v_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->st);
+  delete c;
+}
+
+const char* g4v_error(const g4v_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int g4v_device_info(g4v_ctx* c, char* name, int cap, int* cus, int* lds) {
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, c->device));
+  if (name && cap > 0) {
+    std::snprintf(name, cap, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (cus) *cus = prop.multiProcessorCount;
+  if (lds) *lds = (int)prop.sharedMemPerBlock;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// W4G32
+// ---------------------------------------------------------------------------------------
+static int upload_w4(g4v_ctx* c, Mat& m, const uint8_t* w_dev_orig, const uint16_t* s_host_or_dev, bool s_on_dev,
+                     int N, int K) {
+  m.N = N;
+  m.K = K;
+  ALLOC(m.wr, (size_t)N * K / 2);
+  ALLOC(m.s, (size_t)N * K / 16);
+  launch_relayout_w4(w_dev_orig, m.wr.as<uint4>(), N, K, c->st);
+  HIPCHK(hipMemcpyAsync(m.s.p, s_host_or_dev, (size_t)N * K / 16,
+                        s_on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, c->st));
+  return 0;
+}
+
+int g4v_w4_upload(g4v_ctx* c, const uint8_t* w, const uint16_t* s, int N, int K) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(w && s && N > 0 && K > 0 && K % 256 == 0, "w4_upload: need N > 0 and K % 256 == 0");
+  HIPCHK(hipSetDevice(c->device));
+  DBuf tmp;
+  ALLOC(tmp, (size_t)N * K / 2);
+  HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)N * K / 2, hipMemcpyHostToDevice, c->st));
+  auto m = std::make_unique<Mat>();
+  int r = upload_w4(c, *m, tmp.as<uint8_t>(), s, false, N, K);
+  if (r) return r;
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->mats.push_back(std::move(m));
+  return (int)c->mats.size() - 1;
+}
+
+static int gemv_io(g4v_ctx* c, int h, int M) {
+  const Mat& m = *c->mats[h];
+  if (c->gx.n < (size_t)M * m.K * 4) ALLOC(c->gx, (size_t)MAXM * m.K * 4);
+  if (c->gy.n < (size_t)M * m.N * 4) ALLOC(c->gy, (size_t)MAXM * m.N * 4);
+  return 0;
+}
+
+static GemvArgs plain_args(const Mat& m, const float* x, float* y, int M) {
+  GemvArgs a{};
+  a.mat[0] = m.dev();
+  a.y[0] = y;
+  a.ldy[0] = m.N;
+  a.x = x;
+  a.ldx = m.K;
+  a.K = m.K;
+  a.M = M;
+  return a;
+}
+
+int g4v_w4g32_gemm(g4v_ctx* c, int h, const float* x, int M, float* y) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(h >= 0 && h < (int)c->mats.size(), "w4g32_gemm: bad handle");
+  ARGCHK(x && y && M >= 1 && M <= MAXM, "w4g32_gemm: need 1 <= M <= 8");
+  HIPCHK(hipSetDevice(c->device));
+  int r = gemv_io(c, h, M);
+  if (r) return r;
+  const Mat& m = *c->mats[h];
+  HIPCHK(hipMemcpyAsync(c->gx.p, x, (size_t)M * m.K * 4, hipMemcpyHostToDevice, c->st));
+  gemv_passes(c, plain_args(m, c->gx.as<float>(), c->gy.as<float>(), M), EPI_STORE, M);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(y, c->gy.p, (size_t)M * m.N * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(h >= 0 && h < (int)c->mats.size() && M >= 1 && M <= MAXM && iters > 0 && us, "w4g32_bench: bad args");
+  HIPCHK(hipSetDevice(c->device));
+  int r = gemv_io(c, h, M);
+  if (r) return r;
+  const Mat& m = *c->mats[h];
+  GemvArgs a = plain_args(m, c->gx.as<float>(), c->gy.as<float>(), M);
+  gemv_passes(c, a, EPI_STORE, M);
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  HIPCHK(hipEventRecord(e0, c->st));
+  for (int i = 0; i < iters; ++i) gemv_passes(c, a, EPI_STORE, M);
+  HIPCHK(hipEventRecord(e1, c->st));
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *us = ms * 1000.f / iters;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// attention
+// ---------------------------------------------------------------------------------------
+int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
+                     const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
+                     int kmin, int kmax, int nsplit, float* out) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(hd == HD && nh == NQ, "attn_splitkv: hd must be 256 and nh 8");
+  ARGCHK(M >= 1 && M <= MAXM && nsplit >= 1 && nsplit <= MAXT, "attn_splitkv: 1 <= M <= 8, 1 <= nsplit <= 16");
+  ARGCHK(kmin >= 0 && kmax < npos && kmin <= kmax, "attn_splitkv: need 0 <= kmin <= kmax < npos");
+  const int len = kmax - kmin + 1, per = (len + nsplit - 1) / nsplit;
+  ARGCHK((long)per * M <= 8448, "attn_splitkv: positions per split x rows exceeds 8448");
+  AttnGeom g{};
+  g.M = M;
+  g.kmin = kmin;
+  g.kmax = kmax;
+  g.T = nsplit;
+  for (int m = 0; m < M; ++m) {
+    ARGCHK(pos[m] < npos, "attn_splitkv: pos beyond npos");
+    g.pos[m] = pos[m];
+    g.lo[m] = lo[m];
+    g.skip_lo[m] = skip_lo[m];
+    g.skip_hi[m] = skip_hi[m];
+  }
+  HIPCHK(hipSetDevice(c->device));
+  const size_t kvb = (size_t)npos * HD * 2;
+  if (c->ak.n < kvb) ALLOC(c->ak, kvb);
+  if (c->av.n < kvb) ALLOC(c->av, kvb);
+  if (c->aq.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->aq, (size_t)MAXM * NQ * HD * 4);
+  if (c->ao.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->ao, (size_t)MAXM * NQ * HD * 4);
+  if (c->po.n < (size_t)MAXT * MAXM * NQ * HD * 4) {
+    ALLOC(c->po, (size_t)MAXT * MAXM * NQ * HD * 4);
+    ALLOC(c->pm, (size_t)MAXT * MAXM * NQ * 4);
+    ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
+  }
+  HIPCHK(hipMemcpyAsync(c->ak.p, Kc, kvb, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(c->av.p, Vc, kvb, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(c->aq.p, q, (size_t)M * NQ * HD * 4, hipMemcpyHostToDevice, c->st));
+  launch_attn_geom(c->ak.as<uint16_t>(), c->av.as<uint16_t>(), c->aq.as<float>(), NQ * HD, g, c->po.as<float>(),
+                   c->pm.as<float>(), c->pl.as<float>(), c->ao.as<float>(), NQ * HD, c->st);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(out, c->ao.p, (size_t)M * NQ * HD * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// head
+// ---------------------------------------------------------------------------------------
+static int alloc_head_bufs(g4v_ctx* c, HeadBufs& b, int V) {
+  ALLOC(b.u, (size_t)4 * V * 4);
+  ALLOC(b.list, (size_t)4 * HEAD_LIMIT * 4);
+  ALLOC(b.sval, (size_t)4 * HEAD_LIMIT * 4);
+  ALLOC(b.small, 4 * MAXM * 4);
+  int* s = b.small.as<int>();
+  b.hs.u = b.u.as<float>();
+  b.hs.list = b.list.as<int>();
+  b.hs.sval = b.sval.as<float>();
+  b.hs.cnt = s;
+  b.hs.lmax_key = s + MAXM;
+  b.hs.vmax_key = s + 2 * MAXM;
+  b.hs.best = s + 3 * MAXM;
+  return 0;
+}
+
+// build the screen, exp3 (dec16 + exceptions) and cap table from c->E (device, [V][H] bf16)
+static int head_build_dev(g4v_ctx* c, int V) {
+  c->V = V;
+  hipStream_t st = c->st;
+  DBuf hist, gcnt, rowcnt;
+  ALLOC(hist, 256 * 8);
+  HIPCHK(hipMemsetAsync(hist.p, 0, 256 * 8, st));
+  HeadBuildTmp tmp{hist.as<unsigned long long>(), nullptr, nullptr};
+  head_build(c->E.as<uint16_t>(), V, c->hd, tmp, st);
+  std::vector<unsigned long long> hh(256);
+  HIPCHK(hipMemcpyAsync(hh.data(), hist.p, 256 * 8, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
+  // E:1232-1234: the 8 most frequent exponents, stable order
+  std::vector<int> ord(256);
+  for (int i = 0; i < 256; ++i) ord[i] = i;
+  std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return hh[a] > hh[b]; });
+  uint8_t cb8[8];
+  for (int i = 0; i < 8; ++i) cb8[i] = (uint8_t)ord[i];
+  ALLOC(c->cb, 16);
+  HIPCHK(hipMemcpyAsync(c->cb.p, cb8, 8, hipMemcpyHostToDevice, st));
+  ALLOC(c->dec, (size_t)V * H * 2);
+  ALLOC(gcnt, (size_t)V * 48);
+  ALLOC(rowcnt, (size_t)V * 4);
+  c->hd = HeadDev{};
+  c->hd.dec = c->dec.as<uint4>();
+  c->hd.decw = c->dec.as<uint4>();
+  c->hd.cb = c->cb.as<uint8_t>();
+  tmp.gcnt = gcnt.as<uint8_t>();
+  tmp.rowcnt = rowcnt.as<int>();
+  head_build_dec(c->E.as<uint16_t>(), V, c->hd, tmp, st);
+  std::vector<int> rc(V), ptr(V + 1);
+  HIPCHK(hipMemcpyAsync(rc.data(), rowcnt.p, (size_t)V * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
+  ptr[0] = 0;
+  for (int n = 0; n < V; ++n) ptr[n + 1] = ptr[n] + rc[n];
+  const int ne = ptr[V];
+  ALLOC(c->exc_ptr, (size_t)(V + 1) * 4);
+  ALLOC(c->exc_col, (size_t)(ne + 1) * 2);
+  ALLOC(c->exc_del, (size_t)(ne + 1) * 4);
+  HIPCHK(hipMemcpyAsync(c->exc_ptr.p, ptr.data(), (size_t)(V + 1) * 4, hipMemcpyHostToDevice, st));
+  c->hd.exc_ptr = c->exc_ptr.as<int>();
+  c->hd.exc_col = c->exc_col.as<uint16_t>();
+  c->hd.exc_del = c->exc_del.as<float>();
+  c->hd.exc_col_w = c->exc_col.as<uint16_t>();
+  c->hd.exc_del_w = c->exc_del.as<float>();
+  head_build_exc(c->E.as<uint16_t>(), V, c->hd, st);
+  // E:1236-1243 screen
+  DBuf wq;
+  ALLOC(wq, (size_t)V * H / 2);
+  ALLOC(c->scr_s, (size_t)V * H / 16);
+  ALLOC(c->coef, (size_t)V * 4);
+  screen_build(c->E.as<uint16_t>(), V, wq.as<uint8_t>(), c->scr_s.as<uint16_t>(), c->coef.as<float>(), st);
+  ALLOC(c->scr_wr, (size_t)V * H / 2);
+  launch_relayout_w4(wq.as<uint8_t>(), c->scr_wr.as<uint4>(), V, H, st);
+  // cap(v) = r16(30 tanhf(v / 30)) over every bf16 input, with the host libm (E:1409)
+  std::vector<uint16_t> lut(65536);
+  for (int b = 0; b < 65536; ++b) lut[b] = f2bf(30.0f * tanhf(bf2f((uint16_t)b) / 30.0f));
+  ALLOC(c->lut, 65536 * 2);
+  HIPCHK(hipMemcpyAsync(c->lut.p, lut.data(), 65536 * 2, hipMemcpyHostToDevice, st));
+  int r = alloc_head_bufs(c, c->hb1, V);
+  if (r) return r;
+  r = alloc_head_bufs(c, c->hb2, V);
+  if (r) return r;
+  ALLOC(c->hrow, (size_t)4 * H * 4);
+  ALLOC(c->hnrow, 4 * 4);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipStreamSynchronize(st));
+  c->head_ready = true;
+  return 0;
+}
+
+int g4v_head_build(g4v_ctx* c, const uint16_t* E, int V) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(E && V > 0, "head_build: need E and V > 0");
+  HIPCHK(hipSetDevice(c->device));
+  ALLOC(c->E, (size_t)V * H * 2);
+  HIPCHK(hipMemcpyAsync(c->E.p, E, (size_t)V * H * 2, hipMemcpyHostToDevice, c->st));
+  return head_build_dev(c, V);
+}
+
+static HeadRun head_args(g4v_ctx* c, HeadBufs& b, const float* h, const float* hn, int MT, const int* active) {
+  HeadRun r{};
+  r.hs = b.hs;
+  r.hd = c->hd;
+  r.screen = W4Dev{c->scr_wr.as<uint4>(), c->scr_s.as<uint16_t>(), c->V, H};
+  r.coef = c->coef.as<float>();
+  r.lut = c->lut.as<uint16_t>();
+  r.h = h;
+  r.hn = hn;
+  r.active = active;
+  r.MT = MT;
+  r.V = c->V;
+  return r;
+}
+
+int g4v_head_argmax(g4v_ctx* c, const float* h, int M, int* G, int* nsurv, int* fallback) {
+  if (!c) return G4V_E_ARG;
+  if (!c->head_ready) {
+    c->err = "head_argmax: no head (g4v_head_build or g4v_model_synth first)";
+    return G4V_E_STATE;
+  }
+  ARGCHK(h && G && M >= 1 && M <= 4, "head_argmax: 1 <= M <= 4");
+  HIPCHK(hipSetDevice(c->device));
+  std::vector<float> hn(M);
+  for (int m = 0; m < M; ++m) {  // E:1417 |h| = (float)sqrt(ss_avx2(h)) in the reference's order
+    double s[16] = {0};
+    for (int i = 0; i < H; ++i) {
+      const double d = h[(size_t)m * H + i];
+      s[i % 16] = std::fma(d, d, s[i % 16]);
+    }
+    double a[4];
+    for (int l = 0; l < 4; ++l) a[l] = (s[l] + s[4 + l]) + (s[8 + l] + s[12 + l]);
+    hn[m] = (float)std::sqrt((a[0] + a[2]) + (a[1] + a[3]));
+  }
+  HIPCHK(hipMemcpyAsync(c->hrow.p, h, (size_t)M * H * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(c->hnrow.p, hn.data(), (size_t)M * 4, hipMemcpyHostToDevice, c->st));
+  head_run(head_args(c, c->hb1, c->hrow.as<float>(), c->hnrow.as<float>(), M, nullptr), c->st);
+  HIPCHK(hipGetLastError());
+  int small[4 * MAXM];
+  HIPCHK(hipMemcpyAsync(small, c->hb1.small.p, sizeof small, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  for (int m = 0; m < M; ++m) {
+    G[m] = small[3 * MAXM + m];
+    if (nsurv) nsurv[m] = small[m];
+    if (fallback) fallback[m] = small[m] > HEAD_LIMIT;
+  }
+  return 0;
+}
+
+int g4v_head_survivors(g4v_ctx* c, int m, int* idx, float* val, int cap, int* n) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(m >= 0 && m < 4 && idx && val && n, "head_survivors: bad args");
+  int cnt = 0;
+  HIPCHK(hipMemcpy(&cnt, c->hb1.hs.cnt + m, 4, hipMemcpyDeviceToHost));
+  *n = cnt;
+  if (cnt > HEAD_LIMIT) return 0;
+  const int k = std::min(cnt, cap);
+  std::vector<int> li(cnt);
+  std::vector<float> lv(cnt);
+  HIPCHK(hipMemcpy(li.data(), c->hb1.hs.list + (size_t)m * HEAD_LIMIT, (size_t)cnt * 4, hipMemcpyDeviceToHost));
+  HIPCHK(hipMemcpy(lv.data(), c->hb1.hs.sval + (size_t)m * HEAD_LIMIT, (size_t)cnt * 4, hipMemcpyDeviceToHost));
+  std::vector<int> o(cnt);
+  for (int i = 0; i < cnt; ++i) o[i] = i;
+  std::sort(o.begin(), o.end(), [&](int a, int b) { return li[a] < li[b]; });
+  for (int i = 0; i < k; ++i) {
+    idx[i] = li[o[i]];
+    val[i] = lv[o[i]];
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// synthetic model
+// ---------------------------------------------------------------------------------------
+int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(V > 0 && NL > 0 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_synth: bad shape");
+  HIPCHK(hipSetDevice(c->device));
+  hipStream_t st = c->st;
+  c->model_ready = false;
+  c->NL = NL;
+  c->I = I;
+  c->ctxcap = ctxcap;
+  // output matrix / embedding: E[n][k] = f2bf(0.02 normal(stream(seed, 1), n*H + k))
+  ALLOC(c->E, (size_t)V * H * 2);
+  launch_gen_bf16_normal(c->E.as<uint16_t>(), (size_t)V * H, rng_stream(seed, 1), 0.02f, st);
+  int r = head_build_dev(c, V);
+  if (r) return r;
+  const int Ns[7] = {NQ * HD, HD, HD, H, I, I, H}, Ks[7] = {H, H, H, NQ * HD, H, H, I};
+  DBuf tw, ts;
+  ALLOC(tw, (size_t)std::max(I, NQ * HD) * std::max(H, I) / 2);
+  ALLOC(ts, (size_t)std::max(I, NQ * HD) * std::max(H, I) / 16);
+  c->L.clear();
+  for (int l = 0; l < NL; ++l) {
+    auto lay = std::make_unique<Layer>();
+    for (int j = 0; j < 7; ++j) {
+      const size_t nb = (size_t)Ns[j] * Ks[j] / 2, ns = (size_t)Ns[j] * Ks[j] / 32;
+      launch_gen_w4(tw.as<uint8_t>(), ts.as<uint16_t>(), nb, ns, rng_stream(seed, 1000 + 10 * (uint64_t)l + j),
+                    rng_stream(seed, 2000 + 10 * (uint64_t)l + j), st);
+      r = upload_w4(c, lay->m[j], tw.as<uint8_t>(), ts.as<uint16_t>(), true, Ns[j], Ks[j]);
+      if (r) return r;
+    }
+    // norms: r16(base + span * unif(stream(seed, 3000 + 10 l + t), i))
+    std::vector<float> nv(4 * H + 2 * HD);
+    for (int t = 0; t < 6; ++t) {
+      const int n = t < 4 ? H : HD, off = t < 4 ? t * H : 4 * H + (t - 4) * HD;
+      const float base = t < 4 ? 0.5f : 0.2f, span = t < 4 ? 1.0f : 0.1f;
+      const uint64_t sn = rng_stream(seed, 3000 + 10 * (uint64_t)l + t);
+      for (int i = 0; i < n; ++i) nv[off + i] = r16(base + span * rng_unif(sn, i));
+    }
+    ALLOC(lay->norms, nv.size() * 4);
+    HIPCHK(hipMemcpyAsync(lay->norms.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(hipStreamSynchronize(st));  // nv goes out of scope
+    lay->scalar = 0.75f;
+    lay->sliding = (l % 5 != 4);
+    c->L.push_back(std::move(lay));
+  }
+  std::vector<float> fn(H);
+  const uint64_t sf = rng_stream(seed, 4000);
+  for (int i = 0; i < H; ++i) fn[i] = r16(0.5f + rng_unif(sf, i));
+  ALLOC(c->fnorm, H * 4);
+  HIPCHK(hipMemcpyAsync(c->fnorm.p, fn.data(), H * 4, hipMemcpyHostToDevice, st));
+  // KV cache and RoPE tables (E:1246-1248): sliding theta 1e4 full rotary, global 1e6 rotary 0.25
+  ALLOC(c->KC, (size_t)NL * ctxcap * HD * 2);
+  ALLOC(c->VC, (size_t)NL * ctxcap * HD * 2);
+  HIPCHK(hipMemsetAsync(c->KC.p, 0, c->KC.n, st));
+  HIPCHK(hipMemsetAsync(c->VC.p, 0, c->VC.n, st));
+  std::vector<float> rt((size_t)4 * ctxcap * (HD / 2));
+  for (int ty = 0; ty < 2; ++ty) {
+    const double theta = ty ? 1e6 : 1e4;
+    const int ra = (int)(HD * (ty ? 0.25 : 1.0)) / 2;
+    float* cs = rt.data() + (size_t)(2 * ty) * ctxcap * (HD / 2);
+    float* sn = cs + (size_t)ctxcap * (HD / 2);
+    for (int p = 0; p < ctxcap; ++p)
+      for (int j = 0; j < HD / 2; ++j) {
+        const double inv = j < ra ? 1.0 / std::pow(theta, (2.0 * j) / HD) : 0.0;
+        const double ang = p * inv;
+        cs[(size_t)p * (HD / 2) + j] = (float)std::cos(ang);
+        sn[(size_t)p * (HD / 2) + j] = (float)std::sin(ang);
+      }
+  }
+  ALLOC(c->rope, rt.size() * 4);
+  HIPCHK(hipMemcpyAsync(c->rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, st));
+  // step buffers
+  ALLOC(c->x, MAXM * H * 4);
+  ALLOC(c->xa, MAXM * H * 4);
+  ALLOC(c->q, MAXM * NQ * HD * 4);
+  ALLOC(c->k, MAXM * HD * 4);
+  ALLOC(c->v, MAXM * HD * 4);
+  ALLOC(c->att, MAXM * NQ * HD * 4);
+  ALLOC(c->o, MAXM * H * 4);
+  ALLOC(c->act, (size_t)MAXM * I * 4);
+  ALLOC(c->h, MAXM * H * 4);
+  ALLOC(c->hn, MAXM * 4);
+  ALLOC(c->h2, MAXM * H * 4);
+  ALLOC(c->hn2, MAXM * 4);
+  ALLOC(c->po, (size_t)MAXT * MAXM * NQ * HD * 4);
+  ALLOC(c->pm, (size_t)MAXT * MAXM * NQ * 4);
+  ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
+  ALLOC(c->stepd, sizeof(StepDev));
+  ALLOC(c->resd, sizeof(VerifyResultDev));
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipStreamSynchronize(st));
+  c->model_ready = true;
+  return 0;
+}
+
+int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed) {
+  if (!c) return G4V_E_ARG;
+  if (!c->model_ready) {
+    c->err = "model_fake_ctx: no model";
+    return G4V_E_STATE;
+  }
+  ARGCHK(n >= 0 && n <= c->ctxcap, "model_fake_ctx: n beyond the cache");
+  HIPCHK(hipSetDevice(c->device));
+  std::vector<uint16_t> kc((size_t)n * HD), vc((size_t)n * HD);
+  uint32_t rs = (uint32_t)seed;
+  auto rnd = [&]() {
+    rs = rs * 1664525u + 1013904223u;
+    return (float)((int)(rs >> 9) % 2001 - 1000) / 700.0f;
+  };
+  for (int l = 0; l < c->NL; ++l) {
+    for (size_t i = 0; i < (size_t)n * HD; ++i) {
+      kc[i] = f2bf(rnd());
+      vc[i] = f2bf(rnd());
+    }
+    HIPCHK(hipMemcpyAsync(c->KC.as<uint16_t>() + (size_t)l * c->ctxcap * HD, kc.data(), kc.size() * 2,
+                          hipMemcpyHostToDevice, c->st));
+    HIPCHK(hipMemcpyAsync(c->VC.as<uint16_t>() + (size_t)l * c->ctxcap * HD, vc.data(), vc.size() * 2,
+                          hipMemcpyHostToDevice, c->st));
+    HIPCHK(hipStreamSynchronize(c->st));
+  }
+  return 0;
+}
+
+int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes) {
+  if (!c || !what) return G4V_E_ARG;
+  HIPCHK(hipSetDevice(c->device));
+  const void* src = nullptr;
+  size_t nb = 0;
+  std::vector<uint8_t> tmp;
+  int l = 0, j = 0;
+  if (!std::strcmp(what, "E") && c->E.p) {
+    src = c->E.p;
+    nb = (size_t)c->V * H * 2;
+  } else if (!std::strcmp(what, "KC") && c->KC.p) {
+    src = c->KC.p;
+    nb = c->KC.n;
+  } else if (!std::strcmp(what, "VC") && c->VC.p) {
+    src = c->VC.p;
+    nb = c->VC.n;
+  } else if (!std::strcmp(what, "fnorm") && c->fnorm.p) {
+    src = c->fnorm.p;
+    nb = H * 4;
+  } else if (!std::strcmp(what, "coef") && c->coef.p) {
+    src = c->coef.p;
+    nb = (size_t)c->V * 4;
+  } else if (std::sscanf(what + 1, "%d_%d", &l, &j) == 2 && l >= 0 && l < (int)c->L.size()) {
+    const Layer& L = *c->L[l];
+    if (what[0] == 'S' && j < 7) {
+      src = L.m[j].s.p;
+      nb = L.m[j].s.n;
+    } else if (what[0] == 'N' && j < 6) {
+      src = L.norms.as<float>() + (j < 4 ? j * H : 4 * H + (j - 4) * HD);
+      nb = (j < 4 ? H : HD) * 4;
+    } else if (what[0] == 'W' && j < 7) {
+      // undo the relayout: row n, chunk c, lane j holds bytes (j, 8+j) of groups 8c..8c+7
+      const Mat& m = L.m[j];
+      nb = (size_t)m.N * m.K / 2;
+      if (nbytes) *nbytes = nb;
+      if (!dst) return 0;
+      if (cap < nb) {
+        c->err = "model_read: buffer too small";
+        return G4V_E_ARG;
+      }
+      tmp.resize(nb);
+      HIPCHK(hipMemcpy(tmp.data(), m.wr.p, nb, hipMemcpyDeviceToHost));
+      uint8_t* out = static_cast<uint8_t*>(dst);
+      const int GC = m.K / 256;
+      for (size_t n = 0; n < (size_t)m.N; ++n)
+        for (int cc = 0; cc < GC; ++cc)
+          for (int jj = 0; jj < 8; ++jj)
+            for (int k = 0; k < 8; ++k) {
+              const uint8_t* u = tmp.data() + ((n * GC + cc) * 8 + jj) * 16;
+              const int g = cc * 8 + k;
+              out[n * (m.K / 2) + g * 16 + jj] = u[2 * k];
+              out[n * (m.K / 2) + g * 16 + 8 + jj] = u[2 * k + 1];
+            }
+      if (nbytes) *nbytes = nb;
+      return 0;
+    }
+  }
+  if (!src) {
+    c->err = std::string("model_read: unknown array ") + what;
+    return G4V_E_ARG;
+  }
+  if (nbytes) *nbytes = nb;
+  if (!dst) return 0;
+  ARGCHK(cap >= nb, "model_read: buffer too small");
+  HIPCHK(hipMemcpy(dst, src, nb, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// verify step
+// ---------------------------------------------------------------------------------------
+static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
+  hipStream_t st = c->st;
+  const int NL = c->NL, I = c->I;
+  const StepDev* sp = c->stepd.as<StepDev>();
+  const float sqh = std::sqrt((float)H);
+  launch_embed(c->E.as<uint16_t>(), sp, c->L[0]->ln().in_ln, sqh, c->x.as<float>(), c->xa.as<float>(), M, st);
+  const float* rope = c->rope.as<float>();
+  for (int l = 0; l < NL; ++l) {
+    const Layer& A = *c->L[l];
+    const LayerNorms ln = A.ln();
+    uint16_t* KCl = c->KC.as<uint16_t>() + (size_t)l * c->ctxcap * HD;
+    uint16_t* VCl = c->VC.as<uint16_t>() + (size_t)l * c->ctxcap * HD;
+    // q, k, v in one launch (E:1289)
+    GemvArgs a{};
+    for (int j = 0; j < 3; ++j) a.mat[j] = A.m[j].dev();
+    a.y[0] = c->q.as<float>();
+    a.ldy[0] = NQ * HD;
+    a.y[1] = c->k.as<float>();
+    a.ldy[1] = HD;
+    a.y[2] = c->v.as<float>();
+    a.ldy[2] = HD;
+    a.x = c->xa.as<float>();
+    a.ldx = H;
+    a.K = H;
+    a.M = M;
+    gemv_passes(c, a, EPI_STORE, M);
+    const int ty = A.sliding ? 0 : 1;
+    const float* cs = rope + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
+    const float* sn = cs + (size_t)c->ctxcap * (HD / 2);
+    launch_qk_rope(c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), NQ * HD, sp, ln, cs, sn, KCl, VCl, M, st);
+    launch_attn(KCl, VCl, c->q.as<float>(), sp, A.sliding, T, c->ctxcap, c->po.as<float>(), c->pm.as<float>(),
+                c->pl.as<float>(), c->att.as<float>(), M, st);
+    gemv_passes(c, plain_args(A.m[3], c->att.as<float>(), c->o.as<float>(), M), EPI_STORE, M);  // E:1356
+    launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), ln, M, st);
+    GemvArgs gu{};  // E:1366 gate/up + gelu
+    gu.mat[0] = A.m[4].dev();
+    gu.mat[1] = A.m[5].dev();
+    gu.y[0] = c->act.as<float>();
+    gu.ldy[0] = I;
+    gu.x = c->xa.as<float>();
+    gu.ldx = H;
+    gu.K = H;
+    gu.M = M;
+    gemv_passes(c, gu, EPI_GATEUP, M);
+    gemv_passes(c, plain_args(A.m[6], c->act.as<float>(), c->o.as<float>(), M), EPI_STORE, M);  // E:1373
+    const float* next = l + 1 < NL ? c->L[l + 1]->ln().in_ln : nullptr;
+    launch_post_ff(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), ln, next, c->fnorm.as<float>(),
+                   c->h.as<float>(), c->hn.as<float>(), M, st);
+  }
+  // head of row 0, then of the branch its token selects (E:1475-1488)
+  head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);
+  VerifyResultDev* res = c->resd.as<VerifyResultDev>();
+  launch_branch(sp, c->hb1.hs.best, c->h.as<float>(), c->hn.as<float>(), c->h2.as<float>(), c->hn2.as<float>(), res,
+                st);
+  const int M2 = std::max(1, std::max(na, nb));
+  head_run(head_args(c, c->hb2, c->h2.as<float>(), c->hn2.as<float>(), M2, &res->hcount), st);
+  launch_accept(sp, c->hb1.hs.best, c->hb2.hs.best, c->hb1.hs.cnt, c->hb2.hs.cnt, res, c->KC.as<uint16_t>(),
+                c->VC.as<uint16_t>(), NL, c->ctxcap, st);
+}
+
+int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
+                    float* hidden) {
+  if (!c) return G4V_E_ARG;
+  if (!c->model_ready) {
+    c->err = "verify_step: no model (g4v_model_synth first)";
+    return G4V_E_STATE;
+  }
+  const int M = 1 + na + nb;
+  ARGCHK(toks && out && na >= 0 && nb >= 0 && na <= 4 && nb <= 4 && M <= MAXM, "verify_step: 0 <= na, nb <= 4");
+  ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
+  ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");
+  ARGCHK((long)((pos0 + M + nsplit - 1) / nsplit + 1) * M <= 8448, "verify_step: context too long for nsplit");
+  for (int i = 0; i < M; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "verify_step: token id out of range");
+  HIPCHK(hipSetDevice(c->device));
+  StepDev& s = *c->step_host;
+  std::memset(&s, 0, sizeof s);
+  s.M = M;
+  s.na = na;
+  s.nb = nb;
+  s.pos0 = pos0;
+  for (int r = 0; r < M; ++r) {
+    s.toks[r] = toks[r];
+    if (r <= na) {
+      s.rope[r] = pos0 + r;
+      s.skip_lo[r] = 1;
+      s.skip_hi[r] = 0;
+    } else {  // branch b: RoPE position by depth, skip chain a's slots (E:1292, 1326)
+      s.rope[r] = pos0 + (r - na);
+      s.skip_lo[r] = pos0 + 1;
+      s.skip_hi[r] = pos0 + na;
+    }
+  }
+  HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, c->st));
+  enqueue_verify(c, M, na, nb, nsplit);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  const VerifyResultDev& r = *c->res_host;
+  out->nacc = r.nacc;
+  out->branch = r.branch;
+  out->ncommit = r.ncommit;
+  for (int i = 0; i < 8; ++i) {
+    out->commit[i] = r.commit[i];
+    out->G[i] = r.G[i];
+    out->fallback[i] = r.fallback[i];
+    out->nsurv[i] = r.nsurv[i];
+  }
+  if (hidden) {
+    const int last = r.hrows[r.ncommit - 1];
+    HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)last * H, H * 4, hipMemcpyDeviceToHost));
+  }
+  return 0;
+}
+
+long long g4v_expf_selftest(uint32_t lo, uint32_t hi, uint32_t stride) {
+  static const uint64_t tab[32] = G4V_EXPF_TABLE;
+  long long bad = 0;
+  if (stride == 0) stride = 1;
+  for (uint64_t u = lo; u <= hi; u += stride) {
+    const float x = as_f32((uint32_t)u);
+    if (!(x <= 0.0f)) continue;
+    if (as_u32(libm_expf_neg(x, tab)) != as_u32(expf(x))) ++bad;
+  }
+  return bad;
+}
+
+}  // extern "C"

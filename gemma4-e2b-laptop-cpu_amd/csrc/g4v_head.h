@@ -1,0 +1,55 @@
+// g4v_head.h -- device data of the certified head (screen + exact rescore + argmax).
+#pragma once
+#include "g4v_internal.h"
+
+namespace g4v {
+
+// exp3 head expanded to its decoded bf16 weights plus the exception list (CSR by row)
+struct HeadDev {
+  const uint4* dec;      // [V][24][8] uint4: lane j of group pair p: w[j],w[16+j],w[8+j],w[24+j] x2
+  uint4* decw;           // writable alias used while building
+  const int* exc_ptr;    // [V+1]
+  const uint16_t* exc_col;
+  const float* exc_del;
+  uint16_t* exc_col_w;   // writable aliases used while building
+  float* exc_del_w;
+  const uint8_t* cb;     // [8] exponent codebook (device)
+};
+
+// per-call scratch for up to MAXM rows
+struct HeadScratch {
+  float* u;          // [MAXM][V]: U bounds, then full-head logits of fallback rows
+  int* list;         // [MAXM][HEAD_LIMIT] survivor indices (unordered)
+  float* sval;       // [MAXM][HEAD_LIMIT] rescored r16 logits
+  int* cnt;          // [MAXM] survivor count (may exceed the limit)
+  int32_t* lmax_key; // [MAXM] fkey(max L)
+  int32_t* vmax_key; // [MAXM] fkey(max rescored logit)
+  int* best;         // [MAXM] greedy token (lowest index of the tie set)
+};
+
+struct HeadBuildTmp {
+  unsigned long long* hist;  // [256]
+  uint8_t* gcnt;             // [V][48]
+  int* rowcnt;               // [V]
+};
+
+struct HeadRun {
+  HeadScratch hs;
+  HeadDev hd;
+  W4Dev screen;
+  const float* coef;
+  const uint16_t* lut;   // cap LUT over bf16 inputs
+  const float* h;        // [MT][H] final-normed rows (bf16-valued)
+  const float* hn;       // [MT] (float)sqrt(sum h^2)
+  const int* active;     // optional device flag: 0 -> nothing runs
+  int MT, V, grid_cap;
+};
+
+void head_build(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st);
+void head_build_dec(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st);
+void head_build_exc(const uint16_t* E, int V, HeadDev& hd, hipStream_t st);
+void screen_build(const uint16_t* E, int V, uint8_t* Wq, uint16_t* Sq, float* coef, hipStream_t st);
+void head_run(const HeadRun& r, hipStream_t st);
+size_t head_lds(int MT);
+
+}  // namespace g4v

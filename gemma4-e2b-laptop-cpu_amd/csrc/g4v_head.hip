@@ -1,0 +1,405 @@
+// g4v_head.hip -- certified head screen, exact rescore and greedy argmax on gfx950.
+//
+// Reference path (E = engine/gemma4_engine.cpp, X3 = engine/bf16_exp3_head.h):
+//   screen  E:460-538   s = W4G32(screen, h); L = s - c|h|, U = c|h| + s (fused)
+//   select  E:1453-1466 thr = calc_thr(max L) (E:1410-1414); survivors {U >= thr}; more than
+//                       30,000 -> full head (E:1489-1498)
+//   rescore E:540-571   exp3 dot in the X3:83-107 lane order, exceptions added after the
+//                       8-lane sum, v = r16(y)
+//   argmax  E:1467-1468 / E:1496  lowest index with v >= max - 2 and cap(v) == cap(max),
+//                       cap(v) = r16(30 tanh(v / 30)) read from a LUT over bf16 inputs.
+// The exp3 head is held on the device as the bf16 weights its decoder yields ("dec16",
+// lane order j, 16+j, 8+j, 24+j per group) plus the same exception list (CSR by row).
+#include "g4v_internal.h"
+#include "g4v_head.h"
+
+namespace g4v {
+
+__device__ __forceinline__ float cap_of(float v, const uint16_t* lut) { return bf2f(lut[as_u32(v) >> 16]); }
+
+// E:454-459 / E:1410-1414 calc_thr with the cap LUT (all cap arguments are bf16 values)
+__device__ float calc_thr_dev(float L, const uint16_t* lut) {
+  const float Lr = r16(L), cmL = cap_of(Lr, lut);
+  float lo = Lr - 64.0f, hi = Lr;
+  for (int it = 0; it < 40; ++it) {
+    const float mid = 0.5f * (lo + hi);
+    if (cap_of(r16(mid), lut) == cmL) hi = mid;
+    else lo = mid;
+  }
+  return hi - 0.25f;
+}
+
+__global__ void k_head_reset(HeadScratch hs, int MT) {
+  const int m = threadIdx.x;
+  if (m < MT) {
+    hs.cnt[m] = 0;
+    hs.lmax_key[m] = fkey(-INFINITY);
+    hs.vmax_key[m] = fkey(-INFINITY);
+    hs.best[m] = 0x7fffffff;
+  }
+}
+
+// survivors {U >= calc_thr(max L)}, unordered; counts beyond the limit are kept for the decision
+__global__ void k_head_select(HeadScratch hs, const uint16_t* __restrict__ lut, int MT, int V,
+                              const int* active) {
+  if (active && *active == 0) return;
+  // rows at or beyond a device-side count stay at zero survivors (and so never fall back)
+  const int MA = active ? min(MT, *active) : MT;
+  __shared__ float thr[MAXM];
+  if (threadIdx.x < MA) thr[threadIdx.x] = calc_thr_dev(fkey_inv(hs.lmax_key[threadIdx.x]), lut);
+  __syncthreads();
+  for (int m = 0; m < MA; ++m) {
+    const float* U = hs.u + (size_t)m * V;
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
+      if (U[n] >= thr[m]) {
+        const int p = atomicAdd(&hs.cnt[m], 1);
+        if (p < HEAD_LIMIT) hs.list[(size_t)m * HEAD_LIMIT + p] = n;
+      }
+    }
+  }
+}
+
+// Exact dot of dec16 row n with x (LDS float4 per (g, j) = x[32g+j], x[32g+16+j], x[32g+8+j],
+// x[32g+24+j]); lanes j = 0..7 of the calling group hold the 8 accumulators.  Returns the
+// tree-summed value in every lane of the group.
+__device__ __forceinline__ float dec_dot(const uint4* __restrict__ dec, size_t n, int j,
+                                         const float4* xh) {
+  float acc = 0.f;
+  const uint4* p = dec + n * (size_t)(24 * 8) + j;
+#pragma unroll 4
+  for (int q = 0; q < 24; ++q) {
+    const uint4 w = p[q * 8];
+    const float4 x0 = xh[(2 * q) * 8 + j], x1 = xh[(2 * q + 1) * 8 + j];
+    acc = fmaf(as_f32(w.x << 16), x0.x, acc);
+    acc = fmaf(as_f32(w.x & 0xFFFF0000u), x0.y, acc);
+    acc = fmaf(as_f32(w.y << 16), x0.z, acc);
+    acc = fmaf(as_f32(w.y & 0xFFFF0000u), x0.w, acc);
+    acc = fmaf(as_f32(w.z << 16), x1.x, acc);
+    acc = fmaf(as_f32(w.z & 0xFFFF0000u), x1.y, acc);
+    acc = fmaf(as_f32(w.w << 16), x1.z, acc);
+    acc = fmaf(as_f32(w.w & 0xFFFF0000u), x1.w, acc);
+  }
+  float v = acc;
+  v = v + __shfl_xor(v, 4, 8);
+  v = v + __shfl_xor(v, 1, 8);
+  v = v + __shfl_xor(v, 2, 8);
+  return v;
+}
+
+// stage h rows in the dec16 lane order plus the raw rows (for the exception chain)
+__device__ __forceinline__ void stage_h(const float* __restrict__ h, int MT, float4* XH, float* XR) {
+  for (int idx = threadIdx.x; idx < MT * 48 * 8; idx += blockDim.x) {
+    const int j = idx & 7, g = (idx >> 3) % 48, m = idx / (48 * 8);
+    const float* b = h + (size_t)m * H + g * 32;
+    XH[idx] = make_float4(b[j], b[16 + j], b[8 + j], b[24 + j]);
+  }
+  for (int idx = threadIdx.x; idx < MT * H; idx += blockDim.x) XR[idx] = h[idx];
+  __syncthreads();
+}
+
+// rescore the survivors of rows whose count is within the limit; 8 lanes per survivor
+__global__ __launch_bounds__(256) void k_head_rescore(HeadScratch hs, HeadDev hd, const float* __restrict__ h,
+                                                      int MT, const int* active) {
+  if (active && *active == 0) return;
+  extern __shared__ float4 lds4[];
+  float4* XH = lds4;
+  float* XR = reinterpret_cast<float*>(lds4 + MT * 48 * 8);
+  int tot = 0, cnt[MAXM];
+  for (int m = 0; m < MT; ++m) {
+    const int c = hs.cnt[m];
+    cnt[m] = c <= HEAD_LIMIT ? c : 0;
+    tot += cnt[m];
+  }
+  if (tot == 0) return;
+  stage_h(h, MT, XH, XR);
+  const int j = threadIdx.x & 7, slot = threadIdx.x >> 3, nslots = blockDim.x >> 3;
+  for (int it = blockIdx.x * nslots + slot; it < tot + (nslots - 1); it += gridDim.x * nslots) {
+    // (m, idx) of item `it`; items past the end compute row 0 and store nothing
+    int m = 0, idx = it;
+    while (m < MT - 1 && idx >= cnt[m]) idx -= cnt[m++];
+    const bool ok = it < tot && idx < cnt[m];
+    const int n = ok ? hs.list[(size_t)m * HEAD_LIMIT + idx] : 0;
+    float y = dec_dot(hd.dec, (size_t)n, j, XH + m * 48 * 8);
+    if (ok && j == 0) {
+      for (int e = hd.exc_ptr[n]; e < hd.exc_ptr[n + 1]; ++e) y = fmaf(hd.exc_del[e], XR[m * H + hd.exc_col[e]], y);
+      const float v = r16(y);
+      hs.sval[(size_t)m * HEAD_LIMIT + idx] = v;
+      atomicMax(&hs.vmax_key[m], fkey(v));
+    }
+  }
+}
+
+// full head for the rows whose survivor count exceeds the limit (E:1489-1498); the dec16 row
+// is read once for all MT activation rows
+template <int MT>
+__global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, const float* __restrict__ h,
+                                                   int V, const int* active) {
+  if (active && *active == 0) return;
+  extern __shared__ float4 lds4[];
+  float4* XH = lds4;
+  float* XR = reinterpret_cast<float*>(lds4 + MT * 48 * 8);
+  bool any = false;
+  bool fb[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    fb[m] = hs.cnt[m] > HEAD_LIMIT;
+    any |= fb[m];
+  }
+  if (!any) return;
+  stage_h(h, MT, XH, XR);
+  const int j = threadIdx.x & 7, slot = threadIdx.x >> 3, nslots = blockDim.x >> 3;
+  for (int n0 = blockIdx.x * nslots; n0 < V; n0 += gridDim.x * nslots) {
+    const int n = n0 + slot;
+    const bool ok = n < V;
+    const int nn = ok ? n : 0;
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+    const uint4* p = hd.dec + (size_t)nn * (24 * 8) + j;
+#pragma unroll 2
+    for (int q = 0; q < 24; ++q) {
+      const uint4 w = p[q * 8];
+      const float w0 = as_f32(w.x << 16), w1 = as_f32(w.x & 0xFFFF0000u), w2 = as_f32(w.y << 16),
+                  w3 = as_f32(w.y & 0xFFFF0000u), w4 = as_f32(w.z << 16), w5 = as_f32(w.z & 0xFFFF0000u),
+                  w6 = as_f32(w.w << 16), w7 = as_f32(w.w & 0xFFFF0000u);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float4 x0 = XH[(m * 48 + 2 * q) * 8 + j], x1 = XH[(m * 48 + 2 * q + 1) * 8 + j];
+        float a = acc[m];
+        a = fmaf(w0, x0.x, a);
+        a = fmaf(w1, x0.y, a);
+        a = fmaf(w2, x0.z, a);
+        a = fmaf(w3, x0.w, a);
+        a = fmaf(w4, x1.x, a);
+        a = fmaf(w5, x1.y, a);
+        a = fmaf(w6, x1.z, a);
+        a = fmaf(w7, x1.w, a);
+        acc[m] = a;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (!fb[m]) continue;
+      float y = acc[m];
+      y = y + __shfl_xor(y, 4, 8);
+      y = y + __shfl_xor(y, 1, 8);
+      y = y + __shfl_xor(y, 2, 8);
+      float v = -INFINITY;
+      if (j == 0 && ok) {
+        for (int e = hd.exc_ptr[nn]; e < hd.exc_ptr[nn + 1]; ++e) y = fmaf(hd.exc_del[e], XR[m * H + hd.exc_col[e]], y);
+        v = r16(y);
+        hs.u[(size_t)m * V + n] = v;
+      }
+      for (int s = 8; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+      if ((threadIdx.x & 63) == 0 && v > -INFINITY) atomicMax(&hs.vmax_key[m], fkey(v));
+    }
+  }
+}
+
+// lowest index satisfying the tie rule, over survivors or over the full-head logits
+__global__ void k_head_tie(HeadScratch hs, const uint16_t* __restrict__ lut, int MT, int V, const int* active) {
+  if (active && *active == 0) return;
+  for (int m = 0; m < MT; ++m) {
+    const float mx = fkey_inv(hs.vmax_key[m]);
+    const float cm = cap_of(mx, lut);
+    int best = 0x7fffffff;
+    if (hs.cnt[m] > HEAD_LIMIT) {
+      const float* lg = hs.u + (size_t)m * V;
+      for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
+        const float v = lg[n];
+        if (v >= mx - 2.0f && cap_of(v, lut) == cm) {
+          best = n;
+          break;  // later n in this thread's stride are larger
+        }
+      }
+    } else {
+      const int c = hs.cnt[m];
+      for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x) {
+        const float v = hs.sval[(size_t)m * HEAD_LIMIT + i];
+        const int n = hs.list[(size_t)m * HEAD_LIMIT + i];
+        if (v >= mx - 2.0f && cap_of(v, lut) == cm && n < best) best = n;
+      }
+    }
+    if (best != 0x7fffffff) atomicMin(&hs.best[m], best);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// head build (one-time): exponent histogram, dec16 + exception list, certified screen
+// ---------------------------------------------------------------------------------------
+__global__ void k_exp_hist(const uint16_t* __restrict__ E, size_t n, unsigned long long* hist) {
+  __shared__ unsigned int lh[256];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) lh[i] = 0;
+  __syncthreads();
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    atomicAdd(&lh[(E[i] >> 7) & 0xFF], 1u);
+  __syncthreads();
+  for (int i = threadIdx.x; i < 256; i += blockDim.x)
+    if (lh[i]) atomicAdd(&hist[i], (unsigned long long)lh[i]);
+}
+
+// X3:34-39: exact codebook index, else the first nearest exponent (an exception)
+__device__ __forceinline__ int cb_index(const uint8_t* cb, int e, bool& exc) {
+  for (int i = 0; i < 8; ++i)
+    if (cb[i] == e) {
+      exc = false;
+      return i;
+    }
+  int best = 0, bd = 1 << 30;
+  for (int i = 0; i < 8; ++i) {
+    const int dd = abs((int)cb[i] - e);
+    if (dd < bd) {
+      bd = dd;
+      best = i;
+    }
+  }
+  exc = true;
+  return best;
+}
+
+__device__ __forceinline__ uint16_t dec_weight(uint16_t w, const uint8_t* cb, bool& exc) {
+  const int e = (w >> 7) & 0xFF;
+  const int idx = cb_index(cb, e, exc);
+  return (uint16_t)((w & 0x8000) | ((uint16_t)cb[idx] << 7) | (w & 0x7F));
+}
+
+// one thread per (row, group pair): dec16 words in lane order and the per-group exception count
+__global__ void k_dec16(const uint16_t* __restrict__ E, HeadDev hd, uint8_t* __restrict__ gcnt, int V) {
+  const size_t total = (size_t)V * 24;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const size_t n = u / 24;
+    const int p = (int)(u % 24);
+    uint16_t d[2][32];
+    for (int gg = 0; gg < 2; ++gg) {
+      const int g = 2 * p + gg;
+      int c = 0;
+      for (int k = 0; k < 32; ++k) {
+        bool exc;
+        d[gg][k] = dec_weight(E[n * H + g * 32 + k], hd.cb, exc);
+        c += exc;
+      }
+      gcnt[n * 48 + g] = (uint8_t)c;
+    }
+    uint4* out = hd.decw + (n * 24 + p) * 8;
+    for (int j = 0; j < 8; ++j) {
+      uint4 v;
+      v.x = (uint32_t)d[0][j] | ((uint32_t)d[0][16 + j] << 16);
+      v.y = (uint32_t)d[0][8 + j] | ((uint32_t)d[0][24 + j] << 16);
+      v.z = (uint32_t)d[1][j] | ((uint32_t)d[1][16 + j] << 16);
+      v.w = (uint32_t)d[1][8 + j] | ((uint32_t)d[1][24 + j] << 16);
+      out[j] = v;
+    }
+  }
+}
+
+__global__ void k_rowcount(const uint8_t* __restrict__ gcnt, int* __restrict__ rowcnt, int V) {
+  for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
+    int s = 0;
+    for (int g = 0; g < 48; ++g) s += gcnt[(size_t)n * 48 + g];
+    rowcnt[n] = s;
+  }
+}
+
+// exceptions of row n in column order: col and exact delta w - dec (X3:39)
+__global__ void k_exc_fill(const uint16_t* __restrict__ E, HeadDev hd, int V) {
+  for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
+    int at = hd.exc_ptr[n];
+    for (int k = 0; k < H; ++k) {
+      const uint16_t w = E[(size_t)n * H + k];
+      bool exc;
+      const uint16_t dw = dec_weight(w, hd.cb, exc);
+      if (exc) {
+        hd.exc_col_w[at] = (uint16_t)k;
+        hd.exc_del_w[at] = bf2f(w) - bf2f(dw);
+        ++at;
+      }
+    }
+  }
+}
+
+// E:1236-1243 certified screen build, one thread per row; Wq in the reference's byte layout
+__global__ void k_screen_build(const uint16_t* __restrict__ E, uint8_t* __restrict__ Wq,
+                               uint16_t* __restrict__ Sq, float* __restrict__ coef, int V) {
+  for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
+    double e2 = 0, w2 = 0;
+    for (int g = 0; g < 48; ++g) {
+      float w[32], amax = 0.f;
+      for (int i = 0; i < 32; ++i) {
+        w[i] = bf2f(E[(size_t)n * H + g * 32 + i]);
+        const float a = fabsf(w[i]);
+        amax = (amax < a) ? a : amax;
+      }
+      const uint16_t sb = f2bf(amax / 7.0f);
+      const float sc = bf2f(sb);
+      Sq[(size_t)n * 48 + g] = sb;
+      int qv[32];
+      for (int i = 0; i < 32; ++i) {
+        int v = sc > 0 ? (int)rintf(w[i] / sc) : 0;
+        v = v < -8 ? -8 : (v > 7 ? 7 : v);
+        qv[i] = v + 8;
+        const double d = fma(-(double)v, (double)sc, (double)w[i]);
+        e2 = fma(d, d, e2);
+        w2 = fma((double)w[i], (double)w[i], w2);
+      }
+      for (int i = 0; i < 16; ++i) Wq[(size_t)n * 768 + g * 16 + i] = (uint8_t)(qv[2 * i] | (qv[2 * i + 1] << 4));
+    }
+    coef[n] = (float)fma(1e-4, sqrt(w2), sqrt(e2));  // GCC contracts the reference's sum
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------
+static inline int grid_for(size_t n, int bs, int cap = 16384) {
+  size_t g = (n + bs - 1) / bs;
+  return (int)(g > (size_t)cap ? cap : (g < 1 ? 1 : g));
+}
+
+void head_build(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st) {
+  hipLaunchKernelGGL(k_exp_hist, dim3(1024), dim3(256), 0, st, E, (size_t)V * H, tmp.hist);
+}
+
+void head_build_dec(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st) {
+  hipLaunchKernelGGL(k_dec16, dim3(grid_for((size_t)V * 24, 256)), dim3(256), 0, st, E, hd, tmp.gcnt, V);
+  hipLaunchKernelGGL(k_rowcount, dim3(grid_for(V, 256)), dim3(256), 0, st, tmp.gcnt, tmp.rowcnt, V);
+}
+
+void head_build_exc(const uint16_t* E, int V, HeadDev& hd, hipStream_t st) {
+  hipLaunchKernelGGL(k_exc_fill, dim3(grid_for(V, 256)), dim3(256), 0, st, E, hd, V);
+}
+
+void screen_build(const uint16_t* E, int V, uint8_t* Wq, uint16_t* Sq, float* coef, hipStream_t st) {
+  hipLaunchKernelGGL(k_screen_build, dim3(grid_for(V, 256)), dim3(256), 0, st, E, Wq, Sq, coef, V);
+}
+
+size_t head_lds(int MT) { return (size_t)MT * 48 * 8 * sizeof(float4) + (size_t)MT * H * sizeof(float); }
+
+void head_run(const HeadRun& r, hipStream_t st) {
+  const int MT = r.MT, V = r.V;
+  hipLaunchKernelGGL(k_head_reset, dim3(1), dim3(64), 0, st, r.hs, MT);
+  GemvArgs a{};
+  a.mat[0] = r.screen;
+  a.y[0] = r.hs.u;
+  a.ldy[0] = V;
+  a.x = r.h;
+  a.ldx = H;
+  a.K = H;
+  a.M = MT;
+  a.coef = r.coef;
+  a.hn = r.hn;
+  a.lmax_key = r.hs.lmax_key;
+  a.active = r.active;
+  launch_gemv(a, EPI_SCREEN, st, r.grid_cap);
+  hipLaunchKernelGGL(k_head_select, dim3(grid_for(V, 256, 2048)), dim3(256), 0, st, r.hs, r.lut, MT, V, r.active);
+  hipLaunchKernelGGL(k_head_rescore, dim3(256), dim3(256), head_lds(MT), st, r.hs, r.hd, r.h, MT, r.active);
+  const dim3 gf(grid_for(V, 32, r.grid_cap > 0 ? r.grid_cap : 8192));
+  switch (MT) {
+    case 1: hipLaunchKernelGGL(k_head_full<1>, gf, dim3(256), head_lds(1), st, r.hs, r.hd, r.h, V, r.active); break;
+    case 2: hipLaunchKernelGGL(k_head_full<2>, gf, dim3(256), head_lds(2), st, r.hs, r.hd, r.h, V, r.active); break;
+    case 3: hipLaunchKernelGGL(k_head_full<3>, gf, dim3(256), head_lds(3), st, r.hs, r.hd, r.h, V, r.active); break;
+    default: hipLaunchKernelGGL(k_head_full<4>, gf, dim3(256), head_lds(4), st, r.hs, r.hd, r.h, V, r.active); break;
+  }
+  hipLaunchKernelGGL(k_head_tie, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, r.hs, r.lut, MT, V, r.active);
+}
+
+}  // namespace g4v

@@ -1,0 +1,49 @@
+// g4v_internal.h -- device-side data structures and kernel launchers shared by the
+// translation units of libg4v.  Not part of the C ABI (include/g4v.h is).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "g4v_num.h"
+
+namespace g4v {
+
+constexpr int H = 1536;       // hidden size
+constexpr int HD = 256;       // head dim
+constexpr int NQ = 8;         // query heads (one KV head)
+constexpr int MAXM = 8;       // rows per verify pass
+constexpr int MAXT = 16;      // split-KV splits
+constexpr int HEAD_LIMIT = 30000;  // E:1416 LIM: more survivors -> full head
+
+// An int4 G32 matrix on the device.  wr: weights re-laid for the exact-order GEMV
+// (row n, chunk c of 8 groups, lane j: 16 bytes = bytes j and 8+j of each group);
+// s: bf16 scales in the reference's [N][K/32] layout.
+struct W4Dev {
+  const uint4* wr;
+  const uint16_t* s;
+  int N, K;
+};
+
+// Where the GEMV epilogue sends the result.
+enum GemvEpi { EPI_STORE = 0, EPI_GATEUP = 1, EPI_SCREEN = 2 };
+
+struct GemvArgs {
+  W4Dev mat[3];       // up to three matrices with the same K, processed in one launch
+  float* y[3];        // outputs [M][ldy]
+  int ldy[3];
+  int tiles[4];       // prefix sum of 32-row tiles per matrix
+  const float* x;     // activations [M][ldx]
+  int ldx;
+  int K;
+  int M;              // runtime rows (<= template MT); rows >= M are not computed
+  // EPI_SCREEN
+  const float* coef;  // [N]
+  const float* hn;    // [MT]
+  int32_t* lmax_key;  // [MT] atomic max of fkey(L)
+  const int* active;  // optional: a device count; 0 -> the launch does nothing
+};
+
+void launch_relayout_w4(const uint8_t* w, uint4* wr, int N, int K, hipStream_t st);
+void launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
+
+}  // namespace g4v

@@ -1,0 +1,189 @@
+"""ctypes binding of libg4v.so (include/g4v.h): the gfx950 speculative-verify path.
+
+Mirrors the reference engine's kernel-call surface (engine/gemma4_engine.cpp and the
+w4g32 / w4a8 / bf16_exp3_head headers) one entry point per reference function; arrays are
+numpy, all device memory is owned by the library.  There is no CPU fallback: loading fails
+loudly when libg4v.so is missing.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libg4v.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_vp = C.c_void_p
+_i = C.c_int
+
+# every symbol include/g4v.h declares, with its ctypes signature
+SIGNATURES = {
+    "g4v_create": (_i, [_i, C.POINTER(_vp)]),
+    "g4v_destroy": (None, [_vp]),
+    "g4v_error": (C.c_char_p, [_vp]),
+    "g4v_device_info": (_i, [_vp, C.c_char_p, _i, C.POINTER(_i), C.POINTER(_i)]),
+    "g4v_w4_upload": (_i, [_vp, _u8p, _u16p, _i, _i]),
+    "g4v_w4g32_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
+    "g4v_w4g32_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_attn_splitkv": (_i, [_vp, _u16p, _u16p, _i, _i, _i, _i, _f32p, _i32p, _i32p, _i32p, _i32p,
+                              _i, _i, _i, _f32p]),
+    "g4v_head_build": (_i, [_vp, _u16p, _i]),
+    "g4v_head_argmax": (_i, [_vp, _f32p, _i, _i32p, _i32p, _i32p]),
+    "g4v_head_survivors": (_i, [_vp, _i, _i32p, _f32p, _i, C.POINTER(_i)]),
+    "g4v_model_synth": (_i, [_vp, C.c_uint64, _i, _i, _i, _i]),
+    "g4v_model_fake_ctx": (_i, [_vp, _i, C.c_uint64]),
+    "g4v_model_read": (_i, [_vp, C.c_char_p, _vp, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "g4v_verify_step": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
+    "g4v_expf_selftest": (C.c_longlong, [C.c_uint32, C.c_uint32, C.c_uint32]),
+}
+
+
+class VerifyResult(C.Structure):
+    _fields_ = [("nacc", _i), ("branch", _i), ("ncommit", _i), ("commit", _i * 8), ("G", _i * 8),
+                ("fallback", _i * 8), ("nsurv", _i * 8)]
+
+    def as_dict(self):
+        return dict(nacc=self.nacc, branch=self.branch, ncommit=self.ncommit,
+                    commit=list(self.commit)[: self.ncommit], G=list(self.G),
+                    fallback=list(self.fallback), nsurv=list(self.nsurv))
+
+
+_LIB = None
+
+
+def load(path=LIB_PATH):
+    """Load libg4v.so (raises when it has not been built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() (make -C {HERE})")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+class Device:
+    """One library context on one HIP device (the engine's Pool + buffers, on the GPU)."""
+
+    def __init__(self, device=0):
+        self.L = load()
+        h = _vp()
+        rc = self.L.g4v_create(device, C.byref(h))
+        if rc != 0:
+            raise RuntimeError(f"g4v_create failed ({rc})")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.L.g4v_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.L.g4v_error(self.h).decode()} ({rc})")
+
+    def info(self):
+        name = C.create_string_buffer(256)
+        cus, lds = _i(), _i()
+        self._ok(self.L.g4v_device_info(self.h, name, 256, C.byref(cus), C.byref(lds)), "device_info")
+        return dict(name=name.value.decode(), cus=cus.value, lds_per_block=lds.value)
+
+    # ---- W4G32 (Q4 + gemm_rows_tile) ----
+    def w4_upload(self, W, S):
+        W = _c(W, np.uint8)
+        S = _c(S, np.uint16)
+        N = W.shape[0]
+        K = W.shape[1] * 2
+        h = self.L.g4v_w4_upload(self.h, W, S, N, K)
+        if h < 0:
+            self._ok(h, "w4_upload")
+        return h, N, K
+
+    def w4g32(self, mat, X):
+        h, N, K = mat
+        X = _c(X, np.float32)
+        M = X.shape[0]
+        assert X.shape[1] == K
+        Y = np.empty((M, N), np.float32)
+        self._ok(self.L.g4v_w4g32_gemm(self.h, h, X, M, Y), "w4g32_gemm")
+        return Y
+
+    def w4g32_bench(self, mat, M, iters=100):
+        us = C.c_float()
+        self._ok(self.L.g4v_w4g32_bench(self.h, mat[0], M, iters, C.byref(us)), "w4g32_bench")
+        return us.value
+
+    # ---- split-KV attention ----
+    def attn(self, Kc, Vc, hd, nh, q, pos, lo, skip_lo, skip_hi, kmin, kmax, T):
+        Kc = _c(Kc, np.uint16)
+        Vc = _c(Vc, np.uint16)
+        q = _c(q, np.float32)
+        M = q.shape[0]
+        npos = Kc.size // hd
+        out = np.empty((M, nh * hd), np.float32)
+        self._ok(self.L.g4v_attn_splitkv(self.h, Kc, Vc, npos, hd, nh, M, q, _c(pos, np.int32), _c(lo, np.int32),
+                                         _c(skip_lo, np.int32), _c(skip_hi, np.int32), kmin, kmax, T, out),
+                 "attn_splitkv")
+        return out
+
+    # ---- head ----
+    def head_build(self, E, V):
+        self._ok(self.L.g4v_head_build(self.h, _c(E, np.uint16), V), "head_build")
+
+    def head_argmax(self, h):
+        h = _c(h, np.float32).reshape(-1, 1536)
+        M = h.shape[0]
+        G = np.empty(M, np.int32)
+        ns = np.empty(M, np.int32)
+        fb = np.empty(M, np.int32)
+        self._ok(self.L.g4v_head_argmax(self.h, h, M, G, ns, fb), "head_argmax")
+        return G, ns, fb
+
+    def head_survivors(self, m, cap=30000):
+        idx = np.empty(cap, np.int32)
+        val = np.empty(cap, np.float32)
+        n = _i()
+        self._ok(self.L.g4v_head_survivors(self.h, m, idx, val, cap, C.byref(n)), "head_survivors")
+        k = min(n.value, cap)
+        return idx[:k].copy(), val[:k].copy(), n.value
+
+    # ---- model + verify ----
+    def model_synth(self, seed, V, NL, I=6144, ctxcap=4096):
+        self._ok(self.L.g4v_model_synth(self.h, seed, V, NL, I, ctxcap), "model_synth")
+
+    def fake_ctx(self, n, seed=12345):
+        self._ok(self.L.g4v_model_fake_ctx(self.h, n, seed), "model_fake_ctx")
+
+    def read(self, what, dtype):
+        nb = C.c_size_t()
+        self._ok(self.L.g4v_model_read(self.h, what.encode(), None, 0, C.byref(nb)), f"model_read {what}")
+        out = np.empty(nb.value // np.dtype(dtype).itemsize, dtype)
+        self._ok(self.L.g4v_model_read(self.h, what.encode(), out.ctypes.data, out.nbytes, C.byref(nb)),
+                 f"model_read {what}")
+        return out
+
+    def verify(self, toks, na, nb, pos0, T=8, hidden=False):
+        r = VerifyResult()
+        hid = np.empty(1536, np.float32) if hidden else None
+        self._ok(self.L.g4v_verify_step(self.h, _c(toks, np.int32), na, nb, pos0, T, C.addressof(r),
+                                        None if hid is None else hid.ctypes.data), "verify_step")
+        return (r, hid) if hidden else r

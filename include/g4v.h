@@ -1,0 +1,93 @@
+/* g4v.h -- C ABI of the MI355X (gfx950) speculative-verify path.
+ *
+ * Drop-in boundary for the verify hot path of dayaswaroopchavali/gemma4-e2b-laptop-cpu.
+ * Every entry point replaces a kernel-call surface of the reference engine (citations
+ * are reference file:line, E = engine/gemma4_engine.cpp).  Plain pointers and sizes only;
+ * the library owns all device memory.  Host pointers are used for small inputs/outputs;
+ * results are bit-identical to the reference's exact-float path (ENGINE_DECODE_INT8=0).
+ *
+ * Errors: every function returns 0 on success, a negative G4V_E* code otherwise, and never
+ * exits the process; g4v_error() describes the last failure of a context.
+ * Threading: one host thread per context; calls are stream-ordered and synchronous on return.
+ */
+#ifndef G4V_H
+#define G4V_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G4V_OK 0
+#define G4V_E_ARG (-1)      /* invalid argument or shape */
+#define G4V_E_HIP (-2)      /* HIP runtime failure */
+#define G4V_E_STATE (-3)    /* call out of order (e.g. no model) */
+#define G4V_E_NOMEM (-4)    /* device allocation failed */
+
+typedef struct g4v_ctx g4v_ctx;
+
+/* Context on HIP device `device` (the GPU replaces the reference's Pool, E:73-141). */
+int g4v_create(int device, g4v_ctx** out);
+void g4v_destroy(g4v_ctx* c);
+const char* g4v_error(const g4v_ctx* c);
+/* device name, compute units, max dynamic LDS bytes per block */
+int g4v_device_info(g4v_ctx* c, char* name, int cap, int* cus, int* lds_per_block);
+
+/* ---- int4 G32 matrices: Q4 handle (E:174-175), w4::gemm_rows_tile (engine/w4g32_avx2.h:64-96)
+ * through lin1/lin_multi (E:310-317).  w: [N][K/2] bytes, low nibble = even k, value q+8;
+ * s: [N][K/32] bf16 scales.  Returns a handle >= 0. K % 256 == 0. */
+int g4v_w4_upload(g4v_ctx* c, const uint8_t* w, const uint16_t* s, int N, int K);
+/* y[m][n] for M <= 8 rows of x [M][K] (fp32), bit-identical to gemm_rows_tile */
+int g4v_w4g32_gemm(g4v_ctx* c, int h, const float* x, int M, float* y);
+/* same GEMV with x and y already on the device; times `iters` launches, returns us/launch */
+int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
+
+/* ---- split-KV attention: attn_task + attn_merge (E:743-877, E:1019-1059) with the
+ * reference's split geometry [kmin + t*len/T, kmin + (t+1)*len/T).  Kc, Vc: [npos][hd] bf16;
+ * q: [M][nh*hd] fp32; per row: pos, lo, skip_lo, skip_hi (attn_allowed, E:740).
+ * out: [M][nh*hd] fp32, rounded to bf16 values.  hd == 256, nh == 8, M <= 8, nsplit <= 16. */
+int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
+                     const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
+                     int kmin, int kmax, int nsplit, float* out);
+
+/* ---- certified head (E:1232-1244 build; E:1406-1500 head_group).  E: [V][1536] bf16 output
+ * matrix; builds the int4 screen, the exp3 codebook + exception list and the cap table. */
+int g4v_head_build(g4v_ctx* c, const uint16_t* E, int V);
+/* head of M <= 4 final-normed rows h [M][1536] (bf16 values): greedy token G[m] (lowest-index
+ * tie rule), survivor count, 1 when the full head was evaluated. */
+int g4v_head_argmax(g4v_ctx* c, const float* h, int M, int* G, int* nsurv, int* fallback);
+/* survivors of row m of the last g4v_head_argmax (ascending index) and their r16 logits */
+int g4v_head_survivors(g4v_ctx* c, int m, int* idx, float* val, int cap, int* n);
+
+/* ---- synthetic decoder stack (35-layer Gemma-4-E2B-shaped, int4 G32, hd 256, 8q/1kv heads,
+ * l % 5 != 4 sliding-window 512) generated on device from `seed`. */
+int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap);
+/* E:1249-1250 ENGINE_FAKE_CTX: first n KV positions of every layer from the LCG seeded `seed` */
+int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
+/* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm") */
+int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes);
+
+/* ---- one verify pass (fwd E:1256-1502 + lazy head E:1453-1488 + accept E:1647-1661).
+ * toks[0] confirmed token, toks[1..na] chain a, toks[na+1..na+nb] branch b (na + nb <= 7);
+ * rows sit at positions pos0.. ; nsplit = attention splits (the reference's thread count). */
+typedef struct {
+  int nacc;      /* accepted drafts */
+  int branch;    /* 0: chain a, 1: branch b */
+  int ncommit;   /* nacc + 1 tokens committed */
+  int commit[8];
+  int G[8];      /* greedy token per row, -1 where not evaluated */
+  int fallback[8];
+  int nsurv[8];
+} g4v_verify_result;
+int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
+                    float* hidden);
+
+/* host-side self check of the expf restatement used by the split merge: mismatches against
+ * the linked libm expf over float bit patterns [lo, hi] (step `stride`) */
+long long g4v_expf_selftest(uint32_t lo, uint32_t hi, uint32_t stride);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -556,12 +556,13 @@ void g4o_head_row(const float* h, int V, int K, const uint8_t* Wq, const uint16_
   info->fallback = (ns > limit || info->ref_overflow) ? 1 : 0;
   int best = -1;
   float mx = -1e30f;
+  /* the survivors' exact logits are reported whenever the list fits, even on fallback */
+  for (int i = 0; i < ns && i < cap_surv && ns <= limit; ++i) {
+    float v = g4o_r16(g4o_exp3_dot(data, cb8, exc_ptr, exc_col, exc_delta, K, surv[i], h));
+    sval[i] = v;
+    mx = (mx < v) ? v : mx;
+  }
   if (!info->fallback) {
-    for (int i = 0; i < ns && i < cap_surv; ++i) {
-      float v = g4o_r16(g4o_exp3_dot(data, cb8, exc_ptr, exc_col, exc_delta, K, surv[i], h));
-      sval[i] = v;
-      mx = (mx < v) ? v : mx;
-    }
     float cm = g4o_cap(mx);
     for (int i = 0; i < ns && i < cap_surv; ++i)
       if (sval[i] >= mx - 2.0f && g4o_cap(sval[i]) == cm) {

@@ -1,0 +1,144 @@
+"""GPU parity of the individual verify-path kernels against the oracle (bit-exact).
+
+Each case builds seeded inputs with the oracle's generators, runs the gfx950 kernel
+through the C ABI and compares every output bit with the oracle, which is itself pinned
+to the reference's own kernels (test_oracle_ref.py) and to the committed fixtures.
+"""
+import numpy as np
+import pytest
+
+from conftest import note
+from util import first_diff, same
+
+pytestmark = pytest.mark.gpu
+
+
+def _w4(orc, seed, N, K):
+    W = orc.rand_bytes(orc.stream(seed, 1), N * K // 2).reshape(N, K // 2)
+    S = orc.scales(orc.stream(seed, 2), N * K // 32).reshape(N, K // 32)
+    return W, S
+
+
+# (M, N, K): the verify shapes (q 2048, k/v 256, o K=2048, gate/up 6144, fused 12288, down K=6144)
+GEMV_CASES = [(1, 1536, 1536), (2, 6144, 1536), (4, 1536, 6144), (8, 1536, 1536), (7, 2048, 1536),
+              (3, 256, 2048), (4, 12288, 1536), (5, 512, 6144), (6, 1536, 2048), (8, 6144, 1536)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMV_CASES)
+def test_w4g32_bit_exact(orc, dev, M, N, K):
+    seed = 1000 * M + N + K
+    W, S = _w4(orc, seed, N, K)
+    X = orc.normal_f32(orc.stream(seed, 3), M * K).reshape(M, K)
+    note(f"w4g32 M={M} N={N} K={K} seed={seed}")
+    mat = dev.w4_upload(W, S)
+    y = dev.w4g32(mat, X)
+    yo = orc.w4g32(W, S, X)
+    assert same(y, yo), first_diff(y, yo)
+
+
+def test_w4g32_bf16_inputs_and_repeat(orc, dev):
+    """bf16-valued activations (the o/down inputs) and a second call on the same handle"""
+    W, S = _w4(orc, 77, 1536, 2048)
+    mat = dev.w4_upload(W, S)
+    for M in (4, 1):
+        X = orc.normal_bf16(orc.stream(77, M), M * 2048).astype(np.uint32) << 16
+        X = X.view(np.float32).reshape(M, 2048)
+        note(f"w4g32 bf16 inputs M={M}")
+        assert same(dev.w4g32(mat, X), orc.w4g32(W, S, X))
+
+
+def _attn_case(orc, ctx, M, T, window, tree, seed):
+    hd, nh = 256, 8
+    Kc = orc.normal_bf16(orc.stream(seed, 1), (ctx + 8) * hd)
+    Vc = orc.normal_bf16(orc.stream(seed, 2), (ctx + 8) * hd)
+    q = orc.normal_f32(orc.stream(seed, 3), M * nh * hd, 1 / 16).reshape(M, nh * hd)
+    pos0 = ctx
+    pos = np.array([pos0 + m for m in range(M)], np.int32)
+    rope = pos.copy()
+    sl = np.ones(M, np.int32)
+    sh = np.zeros(M, np.int32)
+    if tree:  # rows na+1.. form branch b: RoPE by depth, skip chain a's slots
+        na = (M - 1) // 2 + (M - 1) % 2
+        for r in range(na + 1, M):
+            rope[r] = pos0 + (r - na)
+            sl[r] = pos0 + 1
+            sh[r] = pos0 + na
+    lo = np.array([max(0, rp - 511) if window else 0 for rp in rope], np.int32)
+    kmax = pos0 + M - 1
+    kmin = min(kmax, int(lo.min()))
+    return Kc, Vc, hd, nh, q, pos, lo, sl, sh, kmin, kmax, T
+
+
+ATTN_CASES = [(512, 4, 8, False, False), (2048, 4, 8, False, False), (6841, 4, 8, False, False),
+              (2048, 4, 8, True, False), (6841, 4, 8, True, False), (2048, 7, 8, False, True),
+              (2048, 7, 8, True, True), (300, 2, 6, False, False), (1000, 8, 16, True, True),
+              (64, 1, 8, False, False)]
+
+
+@pytest.mark.parametrize("ctx,M,T,window,tree", ATTN_CASES)
+def test_attn_splitkv_bit_exact(orc, dev, ctx, M, T, window, tree):
+    args = _attn_case(orc, ctx, M, T, window, tree, seed=ctx * 31 + M)
+    note(f"attn ctx={ctx} M={M} T={T} window={window} tree={tree}")
+    out = dev.attn(*args)
+    ref = orc.attn(*args)
+    assert same(out, ref), first_diff(out, ref)
+
+
+def _head_inputs(orc, V, seed):
+    E = orc.normal_bf16(orc.stream(seed, 1), V * 1536, 0.02)
+    P = orc.exp3_pack(E, V, 1536)
+    scr = orc.screen_build(E, V, 1536)
+    return E, P, scr
+
+
+def _rows(orc, E, seed, kind, M):
+    K = 1536
+    if kind == "random":
+        return orc.r16(orc.normal_f32(orc.stream(seed, 9), M * K)).reshape(M, K)
+    # aligned with a few rows at varied strengths so the screen keeps tens of candidates
+    rows = []
+    for m in range(M):
+        base = orc.bf2f(E[(777 + 13 * m) * K:(778 + 13 * m) * K]).astype(np.float32)
+        noise = orc.normal_f32(orc.stream(seed, 20 + m), K, 1.0)
+        rows.append(orc.r16(base * (12.0 + 8.0 * m) + noise))
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("V,kind,M", [(16384, "random", 1), (16384, "aligned", 3), (32768, "aligned", 4),
+                                      (16384, "random", 4)])
+def test_head_argmax_bit_exact(orc, dev, V, kind, M):
+    seed = V + M
+    E, P, scr = _head_inputs(orc, V, seed)
+    h = _rows(orc, E, seed, kind, M)
+    note(f"head V={V} kind={kind} M={M}")
+    dev.head_build(E, V)
+    G, ns, fb = dev.head_argmax(h)
+    for m in range(M):
+        info, surv, sval = orc.head_row(h[m], scr, P, limit=30000, cap=30000)
+        assert G[m] == info.G, (m, G[m], info.G)
+        assert ns[m] == info.nsurv, (m, ns[m], info.nsurv)
+        assert bool(fb[m]) == (info.nsurv > 30000)
+        if info.nsurv <= 30000:
+            idx, val, n = dev.head_survivors(m)
+            assert n == info.nsurv
+            assert same(idx, surv) and same(val, sval)
+
+
+def test_head_full_vocab(orc, dev):
+    """262,144-row head: random rows fall back to the full head, aligned rows are screened"""
+    V = 262144
+    E, P, scr = _head_inputs(orc, V, 5)
+    h = np.concatenate([_rows(orc, E, 5, "random", 2), _rows(orc, E, 5, "aligned", 2)])
+    note("head V=262144 random x2 + aligned x2")
+    dev.head_build(E, V)
+    G, ns, fb = dev.head_argmax(h)
+    for m in range(4):
+        info, surv, sval = orc.head_row(h[m], scr, P)
+        assert G[m] == info.G and ns[m] == info.nsurv, (m, G[m], info.G, ns[m], info.nsurv)
+    assert fb[0] == 1 and fb[1] == 1 and fb[2] == 0 and fb[3] == 0
+
+
+def test_expf_restatement_host(g4v):
+    """the split merge's expf restatement equals the host libm on a dense sample of x <= 0"""
+    L = g4v.load()
+    assert L.g4v_expf_selftest(0x80000000, 0xFF800000, 97) == 0

@@ -1,0 +1,97 @@
+"""GPU parity of the whole verify pass (synthetic stack, tree drafts, head, acceptance).
+
+The oracle model and the device model are generated from the same seed; the test first
+checks that the generated weights are identical, then runs verify passes whose drafts are
+chosen to hit every acceptance path: nothing accepted, chain a accepted (fully and
+partially) and branch b (the sibling) accepted with KV compaction.
+"""
+import numpy as np
+import pytest
+
+from conftest import note
+from util import first_diff, same
+
+pytestmark = pytest.mark.gpu
+
+V, NL, I, CTX, NCTX, SEED = 8192, 3, 6144, 2048, 700, 11
+
+
+@pytest.fixture(scope="module")
+def pair(orc, dev):
+    from oracle import Model
+    note(f"model synth V={V} NL={NL} ctx={CTX}")
+    dev.model_synth(SEED, V, NL, I, CTX)
+    dev.fake_ctx(NCTX, 12345)
+    om = Model(orc, SEED, V, NL, I, CTX)
+    om.fake_ctx(NCTX, 12345)
+    yield dev, om
+    om.close()
+
+
+def test_generated_weights_identical(pair):
+    dev, om = pair
+    for name, dt, cnt in [("E", np.uint16, V * 1536), ("W1_4", np.uint8, I * 768), ("S2_6", np.uint16, 1536 * I // 32),
+                          ("N0_4", np.float32, 256), ("N2_1", np.float32, 1536), ("fnorm", np.float32, 1536),
+                          ("coef", np.float32, V)]:
+        a = dev.read(name, dt)
+        b = om.get(name, dt, cnt)
+        assert same(a, b), (name, first_diff(a, b))
+    assert same(dev.read("KC", np.uint16), om.get("KC", np.uint16, NL * CTX * 256))
+
+
+def _compare(r, o, hid_g=None, hid_o=None):
+    assert r.nacc == o.nacc and r.branch == o.branch and r.ncommit == o.ncommit, (r.as_dict(), o.nacc, o.branch)
+    assert list(r.commit)[: r.ncommit] == list(o.commit)[: o.ncommit]
+    assert list(r.G) == list(o.G), (list(r.G), list(o.G))
+    for i in range(8):
+        if o.G[i] >= 0:
+            assert r.nsurv[i] == o.nsurv[i]
+    if hid_g is not None:
+        assert same(hid_g, hid_o), first_diff(hid_g, hid_o)
+
+
+def _both(pair, toks, na, nb, pos0, T=8):
+    dev, om = pair
+    note(f"verify toks={list(toks)} na={na} nb={nb} pos0={pos0} T={T}")
+    r, hg = dev.verify(np.array(toks, np.int32), na, nb, pos0, T, hidden=True)
+    o, ho = om.verify(np.array(toks, np.int32), na, nb, pos0, T)
+    _compare(r, o, hg, ho)
+    return r, o
+
+
+def test_verify_random_drafts(pair):
+    _both(pair, [5, 17, 29, 41], 3, 0, NCTX)
+    _both(pair, [5, 17, 29, 41, 53, 65, 77], 3, 3, NCTX)
+
+
+def test_verify_chain_accepted(pair):
+    """drafts equal to the model's own predictions are accepted row by row"""
+    toks = [101, 0, 0, 0]
+    for depth in range(1, 4):
+        _, o = _both(pair, toks, 3, 0, NCTX)
+        toks[depth] = o.G[depth - 1]
+    r, o = _both(pair, toks, 3, 0, NCTX)
+    assert o.nacc == 3
+
+
+def test_verify_branch_b_accepted(pair):
+    """the sibling branch holds the prediction: branch b commits and its KV rows move"""
+    _, o = _both(pair, [202, 3, 4, 5, 6, 7, 8], 3, 3, NCTX)
+    g0 = o.G[0]
+    toks = [202, (g0 + 1) % V, 4, 5, g0, 7, 8]
+    r, o = _both(pair, toks, 3, 3, NCTX)
+    assert o.branch == 1 and o.nacc >= 1
+    dev, om = pair
+    assert same(dev.read("KC", np.uint16), om.get("KC", np.uint16, NL * CTX * 256))
+    assert same(dev.read("VC", np.uint16), om.get("VC", np.uint16, NL * CTX * 256))
+
+
+def test_verify_sequence_of_steps(pair):
+    """successive passes commit tokens and advance the position, as run_req does"""
+    dev, om = pair
+    pos0, conf = NCTX + 40, 300
+    for step in range(3):
+        toks = [conf, (conf * 7 + 1) % V, (conf * 11 + 2) % V, (conf * 13 + 3) % V]
+        r, o = _both(pair, toks, 3, 0, pos0)
+        pos0 += r.ncommit
+        conf = r.commit[r.ncommit - 1]
