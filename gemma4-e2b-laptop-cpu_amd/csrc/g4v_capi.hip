@@ -54,7 +54,7 @@ struct Layer {
 
 // scratch of one head pass
 struct HeadBufs {
-  DBuf u, list, sval, small;
+  DBuf u, list, sval, small, part;
   HeadScratch hs{};
 };
 
@@ -86,7 +86,36 @@ struct g4v_ctx {
   VerifyResultDev* res_host = nullptr;
   // attention standalone
   DBuf ak, av, aq, ao;
+  // per-kernel-class HIP-event timing on the library stream (g4v_profile)
+  unsigned prof_mask = 0;
+  std::vector<hipEvent_t> evpool;
+  size_t evused = 0;
+  struct Rec {
+    int tag;
+    hipEvent_t a, b;
+    double bytes;
+  };
+  std::vector<Rec> recs;
+  hipEvent_t open_ev = nullptr;
+  double prof_ms[PT_NTAGS] = {0}, prof_bytes[PT_NTAGS] = {0};
+  long long prof_n[PT_NTAGS] = {0};
+  // captured verify steps, one per (rows, branches, splits, profile mask)
+  struct Graph {
+    long long key;
+    hipGraphExec_t exec;
+    std::vector<Rec> recs;          // profiling intervals baked into the graph
+    std::vector<hipEvent_t> events; // owned
+  };
+  std::vector<Graph> graphs;
+  std::vector<long long> warmed;  // shapes run once eagerly (first call) before capture
+  bool use_graph = true;
+  size_t step_events = 0;  // profiling events used by the last eager verify pass
   ~g4v_ctx() {
+    for (auto& g : graphs) {
+      (void)hipGraphExecDestroy(g.exec);
+      for (hipEvent_t e : g.events) (void)hipEventDestroy(e);
+    }
+    for (hipEvent_t e : evpool) (void)hipEventDestroy(e);
     if (step_host) (void)hipHostFree(step_host);
     if (res_host) (void)hipHostFree(res_host);
     if (st) (void)hipStreamDestroy(st);
@@ -128,20 +157,57 @@ static int dalloc(g4v_ctx* c, DBuf& b, size_t n) {
     if (r_) return r_;                      \
   } while (0)
 
-// GEMV over M rows in passes whose staged activations fit the LDS budget
-static void gemv_passes(g4v_ctx* c, GemvArgs a, int epi, int M) {
-  const int G = a.K / 32;
-  int per = (int)(c->lds_max / ((size_t)G * 132));
-  if (per < 1) per = 1;
-  if (per > MAXM) per = MAXM;
-  for (int m0 = 0; m0 < M; m0 += per) {
-    GemvArgs b = a;
-    b.M = std::min(per, M - m0);
-    b.x = a.x + (size_t)m0 * a.ldx;
-    for (int i = 0; i < 3; ++i)
-      if (b.y[i]) b.y[i] = a.y[i] + (size_t)m0 * a.ldy[i];
-    launch_gemv(b, epi, c->st);
+// Captured graphs hold raw device pointers: every call that frees or reallocates model, head
+// or step buffers must drop them first (a replay would touch freed memory).
+static void drop_graphs(g4v_ctx* c) {
+  (void)hipStreamSynchronize(c->st);
+  for (auto& g : c->graphs) {
+    (void)hipGraphExecDestroy(g.exec);
+    for (hipEvent_t e : g.events) (void)hipEventDestroy(e);
   }
+  c->graphs.clear();
+  c->warmed.clear();
+}
+
+// profiling hook: brackets a launch (or a group of launches) of class `tag` with events
+static void pmark(void* p, int tag, int begin, double bytes) {
+  g4v_ctx* c = static_cast<g4v_ctx*>(p);
+  if (!(c->prof_mask & (1u << tag))) return;
+  if (c->evused == c->evpool.size()) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void)hipStreamIsCapturing(c->st, &cs);
+    if (cs != hipStreamCaptureStatusNone) return;  // never create an event inside a capture
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    c->evpool.push_back(e);
+  }
+  hipEvent_t e = c->evpool[c->evused++];
+  (void)hipEventRecord(e, c->st);
+  if (begin) c->open_ev = e;
+  else c->recs.push_back({tag, c->open_ev, e, bytes});
+}
+
+// after the stream has drained: fold the recorded intervals into the per-class totals
+static void prof_collect(g4v_ctx* c, bool full_ran) {
+  for (const auto& r : c->recs) {
+    float ms = 0;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) {
+      (void)hipGetLastError();  // a failed timing query must not surface as a later launch error
+      continue;
+    }
+    c->prof_ms[r.tag] += ms;
+    c->prof_bytes[r.tag] += (r.tag == PT_HEAD_FULL && !full_ran) ? 0.0 : r.bytes;
+    c->prof_n[r.tag] += 1;
+  }
+  c->recs.clear();
+  c->evused = 0;
+}
+
+// GEMV over all M rows in one launch (the kernel stages K in phases when the activations
+// of M rows exceed its LDS budget)
+static void gemv_passes(g4v_ctx* c, GemvArgs a, int epi, int M) {
+  a.M = M;
+  launch_gemv(a, epi, c->st);
 }
 
 extern "C" {
@@ -164,7 +230,7 @@ int g4v_create(int device, g4v_ctx** out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
     c->cus = prop.multiProcessorCount;
-    c->lds_max = (int)std::min<size_t>(prop.sharedMemPerBlock, 65536);
+    c->lds_max = (int)std::min<size_t>(std::max<size_t>(prop.sharedMemPerBlock, prop.sharedMemPerBlockOptin), 163840);
   }
   if (hipHostMalloc((void**)&c->step_host, sizeof(StepDev)) != hipSuccess ||
       hipHostMalloc((void**)&c->res_host, sizeof(VerifyResultDev)) != hipSuccess) {
@@ -295,7 +361,7 @@ int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npo
   ARGCHK(M >= 1 && M <= MAXM && nsplit >= 1 && nsplit <= MAXT, "attn_splitkv: 1 <= M <= 8, 1 <= nsplit <= 16");
   ARGCHK(kmin >= 0 && kmax < npos && kmin <= kmax, "attn_splitkv: need 0 <= kmin <= kmax < npos");
   const int len = kmax - kmin + 1, per = (len + nsplit - 1) / nsplit;
-  ARGCHK((long)per * M <= 8448, "attn_splitkv: positions per split x rows exceeds 8448");
+  ARGCHK(per <= attn_pmax(), "attn_splitkv: more positions per split than the split buffer holds");
   AttnGeom g{};
   g.M = M;
   g.kmin = kmin;
@@ -315,6 +381,7 @@ int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npo
   if (c->aq.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->aq, (size_t)MAXM * NQ * HD * 4);
   if (c->ao.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->ao, (size_t)MAXM * NQ * HD * 4);
   if (c->po.n < (size_t)MAXT * MAXM * NQ * HD * 4) {
+    drop_graphs(c);  // the split partials are shared with the captured verify steps
     ALLOC(c->po, (size_t)MAXT * MAXM * NQ * HD * 4);
     ALLOC(c->pm, (size_t)MAXT * MAXM * NQ * 4);
     ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
@@ -337,7 +404,8 @@ static int alloc_head_bufs(g4v_ctx* c, HeadBufs& b, int V) {
   ALLOC(b.u, (size_t)4 * V * 4);
   ALLOC(b.list, (size_t)4 * HEAD_LIMIT * 4);
   ALLOC(b.sval, (size_t)4 * HEAD_LIMIT * 4);
-  ALLOC(b.small, 4 * MAXM * 4);
+  ALLOC(b.small, 5 * MAXM * 4);
+  ALLOC(b.part, (size_t)2 * MAXM * HEAD_MAXGRID * 4);
   int* s = b.small.as<int>();
   b.hs.u = b.u.as<float>();
   b.hs.list = b.list.as<int>();
@@ -346,11 +414,15 @@ static int alloc_head_bufs(g4v_ctx* c, HeadBufs& b, int V) {
   b.hs.lmax_key = s + MAXM;
   b.hs.vmax_key = s + 2 * MAXM;
   b.hs.best = s + 3 * MAXM;
+  b.hs.thr = reinterpret_cast<float*>(s + 4 * MAXM);
+  b.hs.lpart = b.part.as<float>();
+  b.hs.vpart = b.part.as<float>() + (size_t)MAXM * HEAD_MAXGRID;
   return 0;
 }
 
 // build the screen, exp3 (dec16 + exceptions) and cap table from c->E (device, [V][H] bf16)
 static int head_build_dev(g4v_ctx* c, int V) {
+  drop_graphs(c);
   c->V = V;
   hipStream_t st = c->st;
   DBuf hist, gcnt, rowcnt;
@@ -424,6 +496,7 @@ int g4v_head_build(g4v_ctx* c, const uint16_t* E, int V) {
   if (!c) return G4V_E_ARG;
   ARGCHK(E && V > 0, "head_build: need E and V > 0");
   HIPCHK(hipSetDevice(c->device));
+  drop_graphs(c);  // E and the head buffers are reallocated
   ALLOC(c->E, (size_t)V * H * 2);
   HIPCHK(hipMemcpyAsync(c->E.p, E, (size_t)V * H * 2, hipMemcpyHostToDevice, c->st));
   return head_build_dev(c, V);
@@ -431,6 +504,10 @@ int g4v_head_build(g4v_ctx* c, const uint16_t* E, int V) {
 
 static HeadRun head_args(g4v_ctx* c, HeadBufs& b, const float* h, const float* hn, int MT, const int* active) {
   HeadRun r{};
+  r.prof.mark = pmark;
+  r.prof.ctx = c;
+  // one full-head pass reads every decoded row (V x 1536 bf16), the row pointers and the exceptions
+  r.full_bytes = (double)c->V * H * 2 + (double)(c->V + 1) * 4 + (double)c->exc_col.n / 2 * 6;
   r.hs = b.hs;
   r.hd = c->hd;
   r.screen = W4Dev{c->scr_wr.as<uint4>(), c->scr_s.as<uint16_t>(), c->V, H};
@@ -441,6 +518,7 @@ static HeadRun head_args(g4v_ctx* c, HeadBufs& b, const float* h, const float* h
   r.active = active;
   r.MT = MT;
   r.V = c->V;
+  r.grid_cap = (c->cus > 0 ? c->cus : 256) * 8;  // grid-stride: stage the rows once per block
   return r;
 }
 
@@ -508,6 +586,7 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
   ARGCHK(V > 0 && NL > 0 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_synth: bad shape");
   HIPCHK(hipSetDevice(c->device));
   hipStream_t st = c->st;
+  drop_graphs(c);  // every model and step buffer is reallocated below
   c->model_ready = false;
   c->NL = NL;
   c->I = I;
@@ -695,12 +774,18 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
 // ---------------------------------------------------------------------------------------
 // verify step
 // ---------------------------------------------------------------------------------------
+// algorithmic bytes of an int4 G32 matrix read once: N*K/2 weight bytes + N*K/16 scale bytes
+static double w4_bytes(const Mat& m) { return (double)m.N * m.K / 2 + (double)m.N * m.K / 16; }
+
 static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
   hipStream_t st = c->st;
   const int NL = c->NL, I = c->I;
   const StepDev* sp = c->stepd.as<StepDev>();
+  const StepDev& sh = *c->step_host;
   const float sqh = std::sqrt((float)H);
+  pmark(c, PT_ROWS, 1, 0);
   launch_embed(c->E.as<uint16_t>(), sp, c->L[0]->ln().in_ln, sqh, c->x.as<float>(), c->xa.as<float>(), M, st);
+  pmark(c, PT_ROWS, 0, (double)M * H * 2);
   const float* rope = c->rope.as<float>();
   for (int l = 0; l < NL; ++l) {
     const Layer& A = *c->L[l];
@@ -720,15 +805,27 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     a.ldx = H;
     a.K = H;
     a.M = M;
+    pmark(c, PT_GEMV_QKV, 1, 0);
     gemv_passes(c, a, EPI_STORE, M);
+    pmark(c, PT_GEMV_QKV, 0, w4_bytes(A.m[0]) + w4_bytes(A.m[1]) + w4_bytes(A.m[2]));
     const int ty = A.sliding ? 0 : 1;
     const float* cs = rope + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
     const float* sn = cs + (size_t)c->ctxcap * (HD / 2);
+    pmark(c, PT_ROWS, 1, 0);
     launch_qk_rope(c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), NQ * HD, sp, ln, cs, sn, KCl, VCl, M, st);
+    pmark(c, PT_ROWS, 0, (double)M * (NQ * HD + 2 * HD) * 4 * 2);
+    int kmin = sh.pos0 + M - 1;  // E:1325-1326 keys read by the pass: [kmin, pos0 + M - 1]
+    for (int r = 0; r < M; ++r) kmin = std::min(kmin, A.sliding ? std::max(0, sh.rope[r] - 511) : 0);
+    pmark(c, PT_ATTN, 1, 0);
     launch_attn(KCl, VCl, c->q.as<float>(), sp, A.sliding, T, c->ctxcap, c->po.as<float>(), c->pm.as<float>(),
                 c->pl.as<float>(), c->att.as<float>(), M, st);
+    pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
+    pmark(c, PT_GEMV_O, 1, 0);
     gemv_passes(c, plain_args(A.m[3], c->att.as<float>(), c->o.as<float>(), M), EPI_STORE, M);  // E:1356
+    pmark(c, PT_GEMV_O, 0, w4_bytes(A.m[3]));
+    pmark(c, PT_ROWS, 1, 0);
     launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), ln, M, st);
+    pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
     GemvArgs gu{};  // E:1366 gate/up + gelu
     gu.mat[0] = A.m[4].dev();
     gu.mat[1] = A.m[5].dev();
@@ -738,21 +835,34 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     gu.ldx = H;
     gu.K = H;
     gu.M = M;
+    pmark(c, PT_GEMV_GATEUP, 1, 0);
     gemv_passes(c, gu, EPI_GATEUP, M);
+    pmark(c, PT_GEMV_GATEUP, 0, w4_bytes(A.m[4]) + w4_bytes(A.m[5]));
+    pmark(c, PT_GEMV_DOWN, 1, 0);
     gemv_passes(c, plain_args(A.m[6], c->act.as<float>(), c->o.as<float>(), M), EPI_STORE, M);  // E:1373
+    pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
     const float* next = l + 1 < NL ? c->L[l + 1]->ln().in_ln : nullptr;
+    pmark(c, PT_ROWS, 1, 0);
     launch_post_ff(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), ln, next, c->fnorm.as<float>(),
                    c->h.as<float>(), c->hn.as<float>(), M, st);
+    pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
   }
   // head of row 0, then of the branch its token selects (E:1475-1488)
-  head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);
+  HeadRun h1 = head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr);
+  head_run(h1, st);
   VerifyResultDev* res = c->resd.as<VerifyResultDev>();
+  pmark(c, PT_ACCEPT, 1, 0);
   launch_branch(sp, c->hb1.hs.best, c->h.as<float>(), c->hn.as<float>(), c->h2.as<float>(), c->hn2.as<float>(), res,
                 st);
+  pmark(c, PT_ACCEPT, 0, 0);
   const int M2 = std::max(1, std::max(na, nb));
-  head_run(head_args(c, c->hb2, c->h2.as<float>(), c->hn2.as<float>(), M2, &res->hcount), st);
+  HeadRun h2 = head_args(c, c->hb2, c->h2.as<float>(), c->hn2.as<float>(), M2, &res->hcount);
+  h2.pass2 = 1;
+  head_run(h2, st);
+  pmark(c, PT_ACCEPT, 1, 0);
   launch_accept(sp, c->hb1.hs.best, c->hb2.hs.best, c->hb1.hs.cnt, c->hb2.hs.cnt, res, c->KC.as<uint16_t>(),
                 c->VC.as<uint16_t>(), NL, c->ctxcap, st);
+  pmark(c, PT_ACCEPT, 0, 0);
 }
 
 int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
@@ -767,7 +877,7 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
   ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
   ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");
-  ARGCHK((long)((pos0 + M + nsplit - 1) / nsplit + 1) * M <= 8448, "verify_step: context too long for nsplit");
+  ARGCHK((pos0 + M + nsplit - 1) / nsplit + 1 <= attn_pmax(), "verify_step: context too long for nsplit");
   for (int i = 0; i < M; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "verify_step: token id out of range");
   HIPCHK(hipSetDevice(c->device));
   StepDev& s = *c->step_host;
@@ -788,12 +898,58 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
       s.skip_hi[r] = pos0 + na;
     }
   }
-  HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, c->st));
-  enqueue_verify(c, M, na, nb, nsplit);
-  HIPCHK(hipGetLastError());
-  HIPCHK(hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, c->st));
+  const long long key = ((((long long)M * 8 + na) * 8 + nb) * 32 + nsplit) * 65536 + c->prof_mask;
+  g4v_ctx::Graph* gr = nullptr;
+  for (auto& g : c->graphs)
+    if (g.key == key) gr = &g;
+  const bool warm = std::find(c->warmed.begin(), c->warmed.end(), key) != c->warmed.end();
+  if (gr) {  // replay: the pinned step block is copied in by the graph's first node
+    HIPCHK(hipGraphLaunch(gr->exec, c->st));
+  } else if (!c->use_graph || !warm) {  // eager (first call of a shape, or graphs disabled)
+    HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, c->st));
+    enqueue_verify(c, M, na, nb, nsplit);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, c->st));
+    c->step_events = c->evused;  // profiling events one pass of this shape needs
+    if (!warm) c->warmed.push_back(key);
+  } else {  // capture the whole pass once, then launch it
+    g4v_ctx::Graph g;
+    g.key = key;
+    const size_t ev0 = c->evpool.size();
+    for (size_t k = 0; k < c->step_events; ++k) {  // no event may be created while capturing
+      hipEvent_t e;
+      HIPCHK(hipEventCreate(&e));
+      c->evpool.push_back(e);
+    }
+    c->evused = ev0;  // the graph's profiling nodes use the fresh events
+    c->recs.clear();
+    hipGraph_t graph;
+    HIPCHK(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+    (void)hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, c->st);
+    enqueue_verify(c, M, na, nb, nsplit);
+    (void)hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, c->st);
+    HIPCHK(hipStreamEndCapture(c->st, &graph));
+    const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) {
+      c->err = std::string("hipGraphInstantiate: ") + hipGetErrorString(ei);
+      return G4V_E_HIP;
+    }
+    g.events.assign(c->evpool.begin() + ev0, c->evpool.end());
+    c->evpool.resize(ev0);
+    c->evused = 0;
+    g.recs = c->recs;
+    c->recs.clear();
+    c->graphs.push_back(std::move(g));
+    gr = &c->graphs.back();
+    HIPCHK(hipGraphLaunch(gr->exec, c->st));
+  }
   HIPCHK(hipStreamSynchronize(c->st));
   const VerifyResultDev& r = *c->res_host;
+  if (c->prof_mask) {
+    if (gr) c->recs = gr->recs;  // the graph re-records the same events on every launch
+    prof_collect(c, r.fallback[0] != 0);
+  }
   out->nacc = r.nacc;
   out->branch = r.branch;
   out->ncommit = r.ncommit;
@@ -808,6 +964,43 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
     HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)last * H, H * 4, hipMemcpyDeviceToHost));
   }
   return 0;
+}
+
+int g4v_set_graphs(g4v_ctx* c, int on) {
+  if (!c) return G4V_E_ARG;
+  c->use_graph = on != 0;
+  return 0;
+}
+
+int g4v_sync(g4v_ctx* c) {
+  if (!c) return G4V_E_ARG;
+  HIPCHK(hipSetDevice(c->device));
+  HIPCHK(hipStreamSynchronize(c->st));
+  HIPCHK(hipDeviceSynchronize());
+  return 0;
+}
+
+int g4v_profile(g4v_ctx* c, unsigned mask) {
+  if (!c) return G4V_E_ARG;
+  c->prof_mask = mask;
+  c->recs.clear();
+  c->evused = 0;
+  for (int t = 0; t < PT_NTAGS; ++t) {
+    c->prof_ms[t] = 0;
+    c->prof_bytes[t] = 0;
+    c->prof_n[t] = 0;
+  }
+  return 0;
+}
+
+int g4v_profile_read(g4v_ctx* c, double* ms, double* bytes, long long* count, int n) {
+  if (!c || n < 0) return G4V_E_ARG;
+  for (int t = 0; t < n && t < PT_NTAGS; ++t) {
+    if (ms) ms[t] = c->prof_ms[t];
+    if (bytes) bytes[t] = c->prof_bytes[t];
+    if (count) count[t] = c->prof_n[t];
+  }
+  return PT_NTAGS;
 }
 
 long long g4v_expf_selftest(uint32_t lo, uint32_t hi, uint32_t stride) {

@@ -9,12 +9,15 @@
 // Here each of those 8 accumulators lives in its own GPU lane ("chain lane" (n, j)), so the
 // fp32 rounding sequence is the reference's; the 8-lane sum uses xor-shuffles in the same
 // tree.  Weights are re-laid once at upload so a lane's two bytes of 8 consecutive groups
-// are one coalesced 16-byte load; activations are staged in LDS in the per-lane order
-// (xe_j, xe_8+j, xo_j, xo_8+j) with their per-group sums.
+// ("a chunk") are one coalesced 16-byte load; activations are staged in LDS in the per-lane
+// order (xe_j, xe_8+j, xo_j, xo_8+j) with their per-group sums.
 //
-// Parallelism: a row needs 8 lanes per activation-row slot.  For small N the M activation
-// rows are spread over MS lane groups (MS = 1, 2, 4 or 8), multiplying the lanes per
-// output row; the decode is repeated per group, the FMA chains are not.
+// Parallelism and latency: a row needs 8 lanes per activation-row slot.  For small N the M
+// activation rows are spread over MS lane groups (MS = 1, 2, 4 or 8); the decode is
+// repeated per group, the FMA chains are not.  Chunks are fetched in batches of four,
+// double-buffered, so eight chunks per lane are in flight.  When the activations of all M
+// rows do not fit the LDS budget, K is staged in phases; the chains simply continue across
+// phases, so the result does not depend on the phase size.
 #include "g4v_internal.h"
 
 namespace g4v {
@@ -48,6 +51,34 @@ void launch_relayout_w4(const uint8_t* w, uint4* wr, int N, int K, hipStream_t s
 }
 
 constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_BATCH = 4;  // chunks per prefetch batch (two batches in flight)
+constexpr size_t GEMV_LDS_BUDGET = 65536;
+
+// Stage groups [g0, g0 + GP) of M activation rows: XL[m][g - g0][j] = (x[32g+2j], x[32g+16+2j],
+// x[32g+2j+1], x[32g+17+2j]) and GS[m][g - g0] = x[32g] + x[32g+1] + ... + x[32g+31] (W:22 order).
+template <int MT>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int M, int g0, int GP, float4* XL, float* GS) {
+  for (int idx = threadIdx.x; idx < MT * GP * 8; idx += GEMV_THREADS) {
+    const int j = idx & 7, g = (idx >> 3) % GP, m = idx / (GP * 8);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m < M) {
+      const float* b = a.x + (size_t)m * a.ldx + (size_t)(g0 + g) * 32;
+      v = make_float4(b[2 * j], b[16 + 2 * j], b[2 * j + 1], b[17 + 2 * j]);
+    }
+    XL[idx] = v;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < MT * GP; idx += GEMV_THREADS) {
+    const float4* q = XL + (size_t)idx * 8;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += (i & 1) ? q[i >> 1].z : q[i >> 1].x;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += (i & 1) ? q[i >> 1].w : q[i >> 1].y;
+    GS[idx] = s;
+  }
+  __syncthreads();
+}
 
 // MT: activation rows (template bound), MS: lane groups sharing one output row,
 // EPI: epilogue.  Lane index = (rowslot * MS + mslot) * 8 + j.
@@ -60,34 +91,24 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
   if (a.active && *a.active == 0) return;
   extern __shared__ float4 lds4[];
   const int K = a.K, G = K / 32, GC = K / 256;
+  const int GP = a.kphase / 32, CP = a.kphase / 256;  // groups / chunks per phase
   const int M = a.active ? min(a.M, *a.active) : a.M;  // rows beyond a device-side count are idle
-  float4* XL = lds4;                               // [MT][G][8]
-  float* GS = reinterpret_cast<float*>(lds4 + MT * G * 8);  // [MT][G]
-  for (int idx = threadIdx.x; idx < MT * G * 8; idx += GEMV_THREADS) {
-    const int j = idx & 7, g = (idx >> 3) % G, m = idx / (G * 8);
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m < M) {
-      const float* b = a.x + (size_t)m * a.ldx + g * 32;
-      v = make_float4(b[2 * j], b[16 + 2 * j], b[2 * j + 1], b[17 + 2 * j]);
-    }
-    XL[idx] = v;
-  }
-  for (int idx = threadIdx.x; idx < MT * G; idx += GEMV_THREADS) {
-    const int g = idx % G, m = idx / G;
-    float s = 0.f;
-    if (m < M) {
-      const float* b = a.x + (size_t)m * a.ldx + g * 32;
-      for (int i = 0; i < 32; ++i) s += b[i];  // W:22 sequential group sum
-    }
-    GS[idx] = s;
-  }
-  __syncthreads();
+  float4* XL = lds4;                                       // [MT][GP][8]
+  float* GS = reinterpret_cast<float*>(lds4 + MT * GP * 8);  // [MT][GP]
+  const bool one_phase = CP == GC;
+  if (one_phase) stage_x<MT>(a, M, 0, GP, XL, GS);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 7, mslot = (lane >> 3) % MS, rslot = lane / LPR;
   const int m0 = mslot * MPL;
-  const int moff = m0 + (j < MPL ? j : MPL - 1);  // activation row of this lane's offset chain
+  // activation rows this lane reads, clamped into the staged [MT] rows (when MS * MPL > MT the
+  // last lane group has slots past MT; their results are never stored)
+  int mrow[MPL];
+#pragma unroll
+  for (int q = 0; q < MPL; ++q) mrow[q] = min(m0 + q, MT - 1);
+  const int moff = min(m0 + (j < MPL ? j : MPL - 1), MT - 1);  // row of this lane's offset chain
   const int ntiles = a.tiles[3];
+  float lrun = -INFINITY;  // EPI_SCREEN: running max of L for activation row j of this lane
 
   for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
     // which matrix / row this lane serves
@@ -110,9 +131,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
     for (int q = 0; q < MPL; ++q) row[q] = 0.f;
     float off = 0.f;
 
-    for (int c = 0; c < GC; ++c) {
-      const uint4 wv = valid ? wp[(size_t)c * 8] : make_uint4(0, 0, 0, 0);
-      const uint4 sv = valid ? sp[c] : make_uint4(0, 0, 0, 0);
+    // chunk c (global), staged group index of its first group = gl
+    auto chunk = [&](const uint4 wv, const uint4 sv, const int c, const int gl) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const uint32_t d = k == 0 ? wv.x : (k == 1 ? wv.y : (k == 2 ? wv.z : wv.w));
@@ -120,7 +140,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
         const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int g = c * 8 + 2 * k + h;
+          const int g = gl + 2 * k + h;
           const float l0 = (float)((lo >> (16 * h)) & 0xFFu);
           const float l1 = (float)((lo >> (16 * h + 8)) & 0xFFu);
           const float h0 = (float)((hi >> (16 * h)) & 0xFFu);
@@ -128,15 +148,51 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
           const float sc = h ? as_f32(s2 & 0xFFFF0000u) : as_f32(s2 << 16);
 #pragma unroll
           for (int q = 0; q < MPL; ++q) {
-            const float4 xv = XL[((m0 + q) * G + g) * 8 + j];
+            const float4 xv = XL[(mrow[q] * GP + g) * 8 + j];
             float av = l0 * xv.x;
             av = fmaf(l1, xv.y, av);
             av = fmaf(h0, xv.z, av);
             av = fmaf(h1, xv.w, av);
             row[q] = fmaf(av, sc, row[q]);
           }
-          off = fmaf(sc, GS[moff * G + g], off);
+          off = fmaf(sc, GS[moff * GP + g], off);
         }
+      }
+      (void)c;
+    };
+
+    const uint4 z4 = make_uint4(0, 0, 0, 0);
+    for (int p0 = 0; p0 < GC; p0 += CP) {  // phases of K
+      if (!one_phase) stage_x<MT>(a, M, p0 * 8, GP, XL, GS);
+      const int pend = p0 + CP;
+      uint4 wA[GEMV_BATCH], sA[GEMV_BATCH], wB[GEMV_BATCH], sB[GEMV_BATCH];
+#pragma unroll
+      for (int b = 0; b < GEMV_BATCH; ++b) {
+        const bool ok = valid && p0 + b < pend;
+        wA[b] = ok ? wp[(size_t)(p0 + b) * 8] : z4;
+        sA[b] = ok ? sp[p0 + b] : z4;
+      }
+      for (int c0 = p0; c0 < pend; c0 += 2 * GEMV_BATCH) {
+#pragma unroll
+        for (int b = 0; b < GEMV_BATCH; ++b) {  // batch B in flight while batch A is consumed
+          const int c = c0 + GEMV_BATCH + b;
+          const bool ok = valid && c < pend;
+          wB[b] = ok ? wp[(size_t)c * 8] : z4;
+          sB[b] = ok ? sp[c] : z4;
+        }
+#pragma unroll
+        for (int b = 0; b < GEMV_BATCH; ++b)
+          if (c0 + b < pend) chunk(wA[b], sA[b], c0 + b, (c0 + b - p0) * 8);
+#pragma unroll
+        for (int b = 0; b < GEMV_BATCH; ++b) {
+          const int c = c0 + 2 * GEMV_BATCH + b;
+          const bool ok = valid && c < pend;
+          wA[b] = ok ? wp[(size_t)c * 8] : z4;
+          sA[b] = ok ? sp[c] : z4;
+        }
+#pragma unroll
+        for (int b = 0; b < GEMV_BATCH; ++b)
+          if (c0 + GEMV_BATCH + b < pend) chunk(wB[b], sB[b], c0 + GEMV_BATCH + b, (c0 + GEMV_BATCH + b - p0) * 8);
       }
     }
     // 8-lane tree sum per activation row; lane j keeps the sum of row m0 + j
@@ -160,41 +216,61 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
       const float u = __shfl_down(y, LPR, 64);
       if (own && mi == 0) a.y[0][(size_t)m * a.ldy[0] + n] = r16(r16(gelu8(r16(y))) * r16(u));
     } else {  // EPI_SCREEN, E:487-491: L = s - c|h| and U = c|h| + s, both fused
-      float L = -INFINITY;
       if (own) {
         const float cf = a.coef[n], hn = a.hn[m];
-        L = fmaf(-cf, hn, y);
+        lrun = fmaxf(lrun, fmaf(-cf, hn, y));
         a.y[0][(size_t)m * a.ldy[0] + n] = fmaf(cf, hn, y);
       }
-      // max over the row slots of this wave that hold the same m (lanes with equal j, mslot)
+    }
+  }
+  if (EPI == EPI_SCREEN) {
+    // block max of L per activation row (max is order free); one partial per block, reduced
+    // by the consumer instead of a same-address atomic per wave
+    static_assert(EPI != EPI_SCREEN || MS == 1, "the screen runs one lane group per row");
+    __shared__ float wl[GEMV_THREADS / 64][8];
 #pragma unroll
-      for (int sft = LPR; sft < 64; sft <<= 1) L = fmaxf(L, __shfl_xor(L, sft, 64));
-      if (rslot == 0 && j < MPL && m < M && L > -INFINITY) atomicMax(&a.lmax_key[m], fkey(L));
+    for (int sft = 8; sft < 64; sft <<= 1) lrun = fmaxf(lrun, __shfl_xor(lrun, sft, 64));  // same j = same m
+    if (lane < 8) wl[wave][lane] = lrun;
+    __syncthreads();
+    if (threadIdx.x < MT) {
+      float v = -INFINITY;
+      for (int w = 0; w < GEMV_THREADS / 64; ++w) v = fmaxf(v, wl[w][threadIdx.x]);
+      a.lpart[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = v;
     }
   }
 }
 
+static size_t gemv_lds(int MT, int kphase) {
+  const int GP = kphase / 32;
+  return (size_t)MT * GP * 8 * sizeof(float4) + (size_t)MT * GP * sizeof(float);
+}
+
 template <int MT, int MS, int EPI>
-static void launch_t(const GemvArgs& a, hipStream_t st, int grid_cap) {
-  constexpr int MPL = (MT + MS - 1) / MS;
-  constexpr int RPW = 64 / (8 * MS);
-  constexpr int RPB = RPW * (GEMV_THREADS / 64);
-  (void)MPL;
-  (void)RPB;
-  const int G = a.K / 32;
-  const size_t lds = (size_t)MT * G * 8 * sizeof(float4) + (size_t)MT * G * sizeof(float);
-  int grid = a.tiles[3];
-  if (grid_cap > 0 && grid > grid_cap) grid = grid_cap;
+static void launch_t(const GemvArgs& a, hipStream_t st, int grid) {
+  const size_t lds = gemv_lds(MT, a.kphase);
+  if (lds > 65536) {  // gfx950 gives a workgroup up to 160 KB of LDS on request
+    static bool raised = false;
+    if (!raised) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<MT, MS, EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+      raised = true;
+    }
+  }
   hipLaunchKernelGGL((k_gemv<MT, MS, EPI>), dim3(grid), dim3(GEMV_THREADS), lds, st, a);
 }
 
 template <int MT, int EPI>
-static void launch_ms(const GemvArgs& a, int ms, hipStream_t st, int grid_cap) {
-  switch (ms) {
-    case 1: launch_t<MT, 1, EPI>(a, st, grid_cap); break;
-    case 2: if constexpr (MT >= 2) launch_t<MT, 2, EPI>(a, st, grid_cap); break;
-    case 4: if constexpr (MT >= 4) launch_t<MT, 4, EPI>(a, st, grid_cap); break;
-    default: if constexpr (MT >= 8) launch_t<MT, 8, EPI>(a, st, grid_cap); break;
+static void launch_ms(const GemvArgs& a, int ms, hipStream_t st, int grid) {
+  if constexpr (EPI != EPI_STORE) {  // fused epilogues pair rows inside a wave: one lane group per row
+    (void)ms;
+    launch_t<MT, 1, EPI>(a, st, grid);
+  } else {
+    switch (ms) {
+      case 1: launch_t<MT, 1, EPI>(a, st, grid); break;
+      case 2: if constexpr (MT >= 2) launch_t<MT, 2, EPI>(a, st, grid); break;
+      case 4: if constexpr (MT >= 4) launch_t<MT, 4, EPI>(a, st, grid); break;
+      default: if constexpr (MT >= 8) launch_t<MT, 8, EPI>(a, st, grid); break;
+    }
   }
 }
 
@@ -210,8 +286,16 @@ static int pick_ms(int MT, int Ntot, int epi) {
   return ms;
 }
 
-void launch_gemv(const GemvArgs& a_in, int epi, hipStream_t st, int grid_cap) {
-  GemvArgs a = a_in;
+// largest K phase (a multiple of 256 dividing K) whose staged activations fit the budget
+static int pick_kphase(int MT, int K) {
+  for (int parts = 1; parts <= K / 256; ++parts) {
+    if (K % parts || (K / parts) % 256) continue;
+    if (gemv_lds(MT, K / parts) <= GEMV_LDS_BUDGET) return K / parts;
+  }
+  return 256;
+}
+
+static int plan(GemvArgs& a, int epi) {
   const int MT = a.M;
   int Ntot = 0;
   for (int i = 0; i < 3; ++i) Ntot += a.mat[i].N;
@@ -223,17 +307,33 @@ void launch_gemv(const GemvArgs& a_in, int epi, hipStream_t st, int grid_cap) {
   } else {
     for (int i = 0; i < 3; ++i) a.tiles[i + 1] = a.tiles[i] + (a.mat[i].N + rpb - 1) / rpb;
   }
-#define G4V_CASE(mt)                                                  \
-  case mt:                                                            \
-    if (epi == EPI_STORE) launch_ms<mt, EPI_STORE>(a, ms, st, grid_cap);       \
-    else if (epi == EPI_GATEUP) launch_ms<mt, EPI_GATEUP>(a, ms, st, grid_cap); \
-    else launch_ms<mt, EPI_SCREEN>(a, ms, st, grid_cap);                        \
+  a.kphase = pick_kphase(MT, a.K);
+  return ms;
+}
+
+int gemv_grid(const GemvArgs& a_in, int epi, int grid_cap) {
+  GemvArgs a = a_in;
+  plan(a, epi);
+  return (grid_cap > 0 && a.tiles[3] > grid_cap) ? grid_cap : a.tiles[3];
+}
+
+int launch_gemv(const GemvArgs& a_in, int epi, hipStream_t st, int grid_cap) {
+  GemvArgs a = a_in;
+  const int MT = a.M;
+  const int ms = plan(a, epi);
+  const int grid = (grid_cap > 0 && a.tiles[3] > grid_cap) ? grid_cap : a.tiles[3];
+#define G4V_CASE(mt)                                                               \
+  case mt:                                                                         \
+    if (epi == EPI_STORE) launch_ms<mt, EPI_STORE>(a, ms, st, grid);               \
+    else if (epi == EPI_GATEUP) launch_ms<mt, EPI_GATEUP>(a, ms, st, grid);        \
+    else launch_ms<mt, EPI_SCREEN>(a, ms, st, grid);                               \
     break;
   switch (MT) {
     G4V_CASE(1) G4V_CASE(2) G4V_CASE(3) G4V_CASE(4) G4V_CASE(5) G4V_CASE(6) G4V_CASE(7) G4V_CASE(8)
     default: break;
   }
 #undef G4V_CASE
+  return grid;
 }
 
 }  // namespace g4v

@@ -25,7 +25,11 @@ struct HeadScratch {
   int32_t* lmax_key; // [MAXM] fkey(max L)
   int32_t* vmax_key; // [MAXM] fkey(max rescored logit)
   int* best;         // [MAXM] greedy token (lowest index of the tie set)
+  float* thr;        // [MAXM] calc_thr(max L)
+  float* lpart;      // [MAXM][HEAD_MAXGRID] per-block max of L from the screen
+  float* vpart;      // [MAXM][HEAD_MAXGRID] per-block max logit of the full head
 };
+constexpr int HEAD_MAXGRID = 4096;
 
 struct HeadBuildTmp {
   unsigned long long* hist;  // [256]
@@ -33,7 +37,20 @@ struct HeadBuildTmp {
   int* rowcnt;               // [V]
 };
 
+// optional hook around each launch (per-kernel-class HIP-event timing in the C ABI)
+struct ProfHook {
+  void (*mark)(void* ctx, int tag, int begin, double bytes) = nullptr;
+  void* ctx = nullptr;
+};
+enum ProfTag {
+  PT_GEMV_QKV = 0, PT_GEMV_O, PT_GEMV_GATEUP, PT_GEMV_DOWN, PT_ATTN, PT_ROWS, PT_HEAD_SCREEN, PT_HEAD_SELECT,
+  PT_HEAD_RESCORE, PT_HEAD_FULL, PT_HEAD_TIE, PT_ACCEPT, PT_HEAD2, PT_NTAGS
+};
+
 struct HeadRun {
+  ProfHook prof;
+  double full_bytes;     // algorithmic bytes of one full-head pass (for the hook)
+  int pass2;             // 1: second head pass of a verify step
   HeadScratch hs;
   HeadDev hd;
   W4Dev screen;

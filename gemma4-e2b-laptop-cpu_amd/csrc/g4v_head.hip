@@ -10,6 +10,8 @@
 //                       cap(v) = r16(30 tanh(v / 30)) read from a LUT over bf16 inputs.
 // The exp3 head is held on the device as the bf16 weights its decoder yields ("dec16",
 // lane order j, 16+j, 8+j, 24+j per group) plus the same exception list (CSR by row).
+#include <algorithm>
+
 #include "g4v_internal.h"
 #include "g4v_head.h"
 
@@ -39,14 +41,39 @@ __global__ void k_head_reset(HeadScratch hs, int MT) {
   }
 }
 
+// one block: max L over the screen's per-block partials, then calc_thr with the cap table
+// staged in LDS (the 40 bisection steps would otherwise be 40 dependent global loads)
+constexpr int THR_THREADS = 1024;
+__global__ __launch_bounds__(THR_THREADS) void k_head_thr(HeadScratch hs, const uint16_t* __restrict__ lut, int MT,
+                                                          int nb, const int* active) {
+  if (active && *active == 0) return;
+  const int MA = active ? min(MT, *active) : MT;
+  extern __shared__ uint4 lds_lut4[];
+  uint16_t* L16 = reinterpret_cast<uint16_t*>(lds_lut4);
+  __shared__ float red[THR_THREADS / 64][MAXM];
+  const uint4* g4 = reinterpret_cast<const uint4*>(lut);
+  for (int i = threadIdx.x; i < 65536 / 8; i += THR_THREADS) lds_lut4[i] = g4[i];
+  for (int m = 0; m < MA; ++m) {
+    float v = -INFINITY;
+    for (int i = threadIdx.x; i < nb; i += THR_THREADS) v = fmaxf(v, hs.lpart[(size_t)m * nb + i]);
+    for (int s = 1; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][m] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < MA) {
+    float v = -INFINITY;
+    for (int w = 0; w < THR_THREADS / 64; ++w) v = fmaxf(v, red[w][threadIdx.x]);
+    hs.thr[threadIdx.x] = calc_thr_dev(v, L16);
+  }
+}
+
 // survivors {U >= calc_thr(max L)}, unordered; counts beyond the limit are kept for the decision
-__global__ void k_head_select(HeadScratch hs, const uint16_t* __restrict__ lut, int MT, int V,
-                              const int* active) {
+__global__ void k_head_select(HeadScratch hs, int MT, int V, const int* active) {
   if (active && *active == 0) return;
   // rows at or beyond a device-side count stay at zero survivors (and so never fall back)
   const int MA = active ? min(MT, *active) : MT;
   __shared__ float thr[MAXM];
-  if (threadIdx.x < MA) thr[threadIdx.x] = calc_thr_dev(fkey_inv(hs.lmax_key[threadIdx.x]), lut);
+  if (threadIdx.x < MA) thr[threadIdx.x] = hs.thr[threadIdx.x];
   __syncthreads();
   for (int m = 0; m < MA; ++m) {
     const float* U = hs.u + (size_t)m * V;
@@ -148,6 +175,9 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
   if (!any) return;
   stage_h(h, MT, XH, XR);
   const int j = threadIdx.x & 7, slot = threadIdx.x >> 3, nslots = blockDim.x >> 3;
+  float vrun[MT];  // running max of this thread's logits (max is order free)
+#pragma unroll
+  for (int m = 0; m < MT; ++m) vrun[m] = -INFINITY;
   for (int n0 = blockIdx.x * nslots; n0 < V; n0 += gridDim.x * nslots) {
     const int n = n0 + slot;
     const bool ok = n < V;
@@ -156,7 +186,7 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.f;
     const uint4* p = hd.dec + (size_t)nn * (24 * 8) + j;
-#pragma unroll 2
+#pragma unroll 8
     for (int q = 0; q < 24; ++q) {
       const uint4 w = p[q * 8];
       const float w0 = as_f32(w.x << 16), w1 = as_f32(w.x & 0xFFFF0000u), w2 = as_f32(w.y << 16),
@@ -184,23 +214,46 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
       y = y + __shfl_xor(y, 4, 8);
       y = y + __shfl_xor(y, 1, 8);
       y = y + __shfl_xor(y, 2, 8);
-      float v = -INFINITY;
       if (j == 0 && ok) {
         for (int e = hd.exc_ptr[nn]; e < hd.exc_ptr[nn + 1]; ++e) y = fmaf(hd.exc_del[e], XR[m * H + hd.exc_col[e]], y);
-        v = r16(y);
+        const float v = r16(y);
         hs.u[(size_t)m * V + n] = v;
+        vrun[m] = fmaxf(vrun[m], v);
       }
-      for (int s = 8; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
-      if ((threadIdx.x & 63) == 0 && v > -INFINITY) atomicMax(&hs.vmax_key[m], fkey(v));
     }
+  }
+  // one partial max per block and row (reduced by the tie kernel)
+  __shared__ float red[256 / 64][MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    float v = vrun[m];
+    for (int s = 1; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][m] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < MT) {
+    float v = -INFINITY;
+    for (int w = 0; w < 256 / 64; ++w) v = fmaxf(v, red[w][threadIdx.x]);
+    hs.vpart[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = v;
   }
 }
 
 // lowest index satisfying the tie rule, over survivors or over the full-head logits
-__global__ void k_head_tie(HeadScratch hs, const uint16_t* __restrict__ lut, int MT, int V, const int* active) {
+__global__ void k_head_tie(HeadScratch hs, const uint16_t* __restrict__ lut, int MT, int V, int nbf,
+                           const int* active) {
   if (active && *active == 0) return;
+  __shared__ float red[4];
   for (int m = 0; m < MT; ++m) {
-    const float mx = fkey_inv(hs.vmax_key[m]);
+    float mx = fkey_inv(hs.vmax_key[m]);
+    if (hs.cnt[m] > HEAD_LIMIT) {  // full head: reduce its per-block maxima
+      float v = -INFINITY;
+      for (int i = threadIdx.x; i < nbf; i += blockDim.x) v = fmaxf(v, hs.vpart[(size_t)m * nbf + i]);
+      for (int s = 1; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+      __syncthreads();
+      mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+      __syncthreads();
+    }
     const float cm = cap_of(mx, lut);
     int best = 0x7fffffff;
     if (hs.cnt[m] > HEAD_LIMIT) {
@@ -376,6 +429,10 @@ size_t head_lds(int MT) { return (size_t)MT * 48 * 8 * sizeof(float4) + (size_t)
 
 void head_run(const HeadRun& r, hipStream_t st) {
   const int MT = r.MT, V = r.V;
+  // pass-2 launches (rows chosen on the device) are booked under one tag of their own
+  auto mark = [&](int tag, int begin, double bytes) {
+    if (r.prof.mark) r.prof.mark(r.prof.ctx, r.pass2 ? PT_HEAD2 : tag, begin, bytes);
+  };
   hipLaunchKernelGGL(k_head_reset, dim3(1), dim3(64), 0, st, r.hs, MT);
   GemvArgs a{};
   a.mat[0] = r.screen;
@@ -387,19 +444,38 @@ void head_run(const HeadRun& r, hipStream_t st) {
   a.M = MT;
   a.coef = r.coef;
   a.hn = r.hn;
-  a.lmax_key = r.hs.lmax_key;
+  a.lpart = r.hs.lpart;
   a.active = r.active;
-  launch_gemv(a, EPI_SCREEN, st, r.grid_cap);
-  hipLaunchKernelGGL(k_head_select, dim3(grid_for(V, 256, 2048)), dim3(256), 0, st, r.hs, r.lut, MT, V, r.active);
+  const int cap = std::min(r.grid_cap > 0 ? r.grid_cap : HEAD_MAXGRID, HEAD_MAXGRID);
+  mark(PT_HEAD_SCREEN, 1, 0);
+  const int nb = launch_gemv(a, EPI_SCREEN, st, cap);
+  mark(PT_HEAD_SCREEN, 0, (double)V * (H / 2 + H / 16 + 4));
+  mark(PT_HEAD_SELECT, 1, 0);
+  static bool thr_lds = false;
+  if (!thr_lds) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_head_thr), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              65536 * 2);
+    thr_lds = true;
+  }
+  hipLaunchKernelGGL(k_head_thr, dim3(1), dim3(THR_THREADS), 65536 * 2, st, r.hs, r.lut, MT, nb, r.active);
+  hipLaunchKernelGGL(k_head_select, dim3(grid_for(V, 256, 2048)), dim3(256), 0, st, r.hs, MT, V, r.active);
+  mark(PT_HEAD_SELECT, 0, (double)V * 4 * MT);
+  mark(PT_HEAD_RESCORE, 1, 0);
   hipLaunchKernelGGL(k_head_rescore, dim3(256), dim3(256), head_lds(MT), st, r.hs, r.hd, r.h, MT, r.active);
-  const dim3 gf(grid_for(V, 32, r.grid_cap > 0 ? r.grid_cap : 8192));
+  mark(PT_HEAD_RESCORE, 0, 0);
+  const dim3 gf(grid_for(V, 32, cap));
+  mark(PT_HEAD_FULL, 1, 0);
   switch (MT) {
     case 1: hipLaunchKernelGGL(k_head_full<1>, gf, dim3(256), head_lds(1), st, r.hs, r.hd, r.h, V, r.active); break;
     case 2: hipLaunchKernelGGL(k_head_full<2>, gf, dim3(256), head_lds(2), st, r.hs, r.hd, r.h, V, r.active); break;
     case 3: hipLaunchKernelGGL(k_head_full<3>, gf, dim3(256), head_lds(3), st, r.hs, r.hd, r.h, V, r.active); break;
     default: hipLaunchKernelGGL(k_head_full<4>, gf, dim3(256), head_lds(4), st, r.hs, r.hd, r.h, V, r.active); break;
   }
-  hipLaunchKernelGGL(k_head_tie, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, r.hs, r.lut, MT, V, r.active);
+  mark(PT_HEAD_FULL, 0, r.full_bytes);
+  mark(PT_HEAD_TIE, 1, 0);
+  hipLaunchKernelGGL(k_head_tie, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, r.hs, r.lut, MT, V, (int)gf.x,
+                     r.active);
+  mark(PT_HEAD_TIE, 0, 0);
 }
 
 }  // namespace g4v

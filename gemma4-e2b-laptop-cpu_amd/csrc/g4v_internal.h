@@ -35,15 +35,19 @@ struct GemvArgs {
   const float* x;     // activations [M][ldx]
   int ldx;
   int K;
+  int kphase;         // K elements staged in LDS at a time (set by launch_gemv)
   int M;              // runtime rows (<= template MT); rows >= M are not computed
   // EPI_SCREEN
   const float* coef;  // [N]
   const float* hn;    // [MT]
-  int32_t* lmax_key;  // [MT] atomic max of fkey(L)
+  float* lpart;       // [MT][gridDim.x] per-block max of L (reduced by the consumer)
   const int* active;  // optional: a device count; 0 -> the launch does nothing
 };
 
 void launch_relayout_w4(const uint8_t* w, uint4* wr, int N, int K, hipStream_t st);
-void launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
+// returns the grid size used (the number of EPI_SCREEN partials per activation row)
+int launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
+// grid launch_gemv would use
+int gemv_grid(const GemvArgs& a, int epi, int grid_cap);
 
 }  // namespace g4v

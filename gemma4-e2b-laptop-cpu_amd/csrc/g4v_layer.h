@@ -66,3 +66,8 @@ void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, in
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st);
 
 }  // namespace g4v
+
+namespace g4v {
+// positions per attention split the split kernel can hold
+int attn_pmax();
+}

@@ -38,8 +38,16 @@ SIGNATURES = {
     "g4v_model_fake_ctx": (_i, [_vp, _i, C.c_uint64]),
     "g4v_model_read": (_i, [_vp, C.c_char_p, _vp, C.c_size_t, C.POINTER(C.c_size_t)]),
     "g4v_verify_step": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
+    "g4v_profile": (_i, [_vp, C.c_uint]),
+    "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
+    "g4v_sync": (_i, [_vp]),
+    "g4v_set_graphs": (_i, [_vp, _i]),
     "g4v_expf_selftest": (C.c_longlong, [C.c_uint32, C.c_uint32, C.c_uint32]),
 }
+
+# kernel classes of g4v_profile (include/g4v.h)
+PROF_TAGS = ["gemv_qkv", "gemv_o", "gemv_gateup", "gemv_down", "attn", "rows", "head_screen", "head_select",
+             "head_rescore", "head_full", "head_tie", "accept", "head_pass2"]
 
 
 class VerifyResult(C.Structure):
@@ -180,6 +188,28 @@ class Device:
         self._ok(self.L.g4v_model_read(self.h, what.encode(), out.ctypes.data, out.nbytes, C.byref(nb)),
                  f"model_read {what}")
         return out
+
+    def sync(self):
+        self._ok(self.L.g4v_sync(self.h), "sync")
+
+    def set_graphs(self, on):
+        self._ok(self.L.g4v_set_graphs(self.h, 1 if on else 0), "set_graphs")
+
+    def profile(self, tags=None):
+        """start per-kernel-class event timing for `tags` (names of PROF_TAGS; None = all)"""
+        mask = 0
+        for i, t in enumerate(PROF_TAGS):
+            if tags is None or t in tags:
+                mask |= 1 << i
+        self._ok(self.L.g4v_profile(self.h, mask), "profile")
+
+    def profile_read(self):
+        n = len(PROF_TAGS)
+        ms = np.zeros(n, np.float64)
+        by = np.zeros(n, np.float64)
+        cnt = np.zeros(n, np.int64)
+        self.L.g4v_profile_read(self.h, ms.ctypes.data, by.ctypes.data, cnt.ctypes.data, n)
+        return {t: dict(ms=float(ms[i]), bytes=float(by[i]), launches=int(cnt[i])) for i, t in enumerate(PROF_TAGS)}
 
     def verify(self, toks, na, nb, pos0, T=8, hidden=False):
         r = VerifyResult()

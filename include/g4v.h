@@ -82,6 +82,21 @@ typedef struct {
 } g4v_verify_result;
 int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
                     float* hidden);
+/* Verify steps run as one captured HIP graph per shape (rows, branches, splits) from the
+ * second call of that shape on (the engine's persistent pool + job word, E:73-141, becomes a
+ * graph launch).  on = 0 launches every kernel from the host instead. */
+int g4v_set_graphs(g4v_ctx* c, int on);
+
+/* ---- measurement (replaces the reference's PROF_NM / T_* stage timers, E:66-70, E:1085):
+ * per-kernel-class HIP events on the library's stream.  Classes: 0 gemv_qkv, 1 gemv_o,
+ * 2 gemv_gateup, 3 gemv_down, 4 attn, 5 rows (norm/rope/embed), 6 head_screen, 7 head_select,
+ * 8 head_rescore, 9 head_full, 10 head_tie, 11 accept, 12 head_pass2.  Bit t of `mask` enables
+ * class t; the totals (ms, algorithmic bytes, launches) reset on every g4v_profile call. */
+#define G4V_PROF_NTAGS 13
+int g4v_profile(g4v_ctx* c, unsigned mask);
+int g4v_profile_read(g4v_ctx* c, double* ms, double* bytes, long long* count, int n);
+/* wait for all work of the context */
+int g4v_sync(g4v_ctx* c);
 
 /* host-side self check of the expf restatement used by the split merge: mismatches against
  * the linked libm expf over float bit patterns [lo, hi] (step `stride`) */

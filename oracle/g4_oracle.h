@@ -94,6 +94,7 @@ g4o_model* g4o_model_new(uint64_t seed, int V, int NL, int I, int ctx);
 void g4o_model_free(g4o_model* m);
 void g4o_model_fake_ctx(g4o_model* m, int n, uint64_t seed);
 int g4o_model_bytes(const g4o_model* m, const char* what, void* dst, int64_t cap);
+const void* g4o_model_ptr(const g4o_model* m, const char* what);
 
 typedef struct {
   int nacc;      /* accepted drafts */

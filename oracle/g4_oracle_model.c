@@ -166,6 +166,33 @@ void g4o_model_fake_ctx(g4o_model* m, int n, uint64_t seed) {
     }
 }
 
+/* borrow a pointer to a named internal array (the reference harness runs on the same weights) */
+const void* g4o_model_ptr(const g4o_model* m, const char* what) {
+  int l = 0, j = 0;
+  if (!strcmp(what, "E")) return m->E;
+  if (!strcmp(what, "Wq")) return m->Wq;
+  if (!strcmp(what, "Sq")) return m->Sq;
+  if (!strcmp(what, "coef")) return m->coef;
+  if (!strcmp(what, "cb")) return m->cb;
+  if (!strcmp(what, "x3")) return m->x3;
+  if (!strcmp(what, "xptr")) return m->xptr;
+  if (!strcmp(what, "xcol")) return m->xcol;
+  if (!strcmp(what, "xdel")) return m->xdel;
+  if (!strcmp(what, "fnorm")) return m->fnorm;
+  if (!strcmp(what, "KC")) return m->KC;
+  if (!strcmp(what, "VC")) return m->VC;
+  if (!strcmp(what, "cs0")) return m->cs[0];
+  if (!strcmp(what, "sn0")) return m->sn[0];
+  if (!strcmp(what, "cs1")) return m->cs[1];
+  if (!strcmp(what, "sn1")) return m->sn[1];
+  if (sscanf(what + 1, "%d_%d", &l, &j) == 2 && l >= 0 && l < m->NL) {
+    if (what[0] == 'W' && j < 7) return m->L[l].W[j];
+    if (what[0] == 'S' && j < 7) return m->L[l].S[j];
+    if (what[0] == 'N' && j < 6) return m->L[l].nv[j];
+  }
+  return NULL;
+}
+
 /* copy a named internal array out (tests compare generated weights and caches) */
 int g4o_model_bytes(const g4o_model* m, const char* what, void* dst, int64_t cap) {
   const void* src = NULL;

@@ -68,6 +68,7 @@ class Oracle:
             "g4o_model_new": (_vp, [_u64, _i, _i, _i, _i]), "g4o_model_free": (None, [_vp]),
             "g4o_model_fake_ctx": (None, [_vp, _i, _u64]),
             "g4o_model_bytes": (_i, [_vp, C.c_char_p, _vp, _i64]),
+            "g4o_model_ptr": (_vp, [_vp, C.c_char_p]),
             "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
             "g4o_stream": (_u64, [_u64, _u64]),
@@ -241,10 +242,24 @@ class Model:
         return out, hid
 
 
-class Ref:
-    """The reference engine's own kernels (oracle/_ref/libg4ref.so), one worker."""
+class RefLayer(C.Structure):
+    _fields_ = [("W", _vp * 7), ("S", _vp * 7), ("nv", _vp * 6), ("scalar", _f), ("sliding", _i)]
 
-    def __init__(self, path=LIB_REF):
+
+class RefModel(C.Structure):
+    _fields_ = [("V", _i), ("NL", _i), ("I", _i), ("ctx", _i), ("E", _vp), ("fnorm", _vp), ("KC", _vp), ("VC", _vp),
+                ("cs", _vp * 2), ("sn", _vp * 2), ("L", RefLayer * 64)]
+
+
+class RefOut(C.Structure):
+    _fields_ = [("nacc", _i), ("branch", _i), ("ncommit", _i), ("commit", _i * 8), ("G", _i * 8),
+                ("fallback", _i * 8), ("nsurv", _i * 8)]
+
+
+class Ref:
+    """The reference engine's own kernels (oracle/_ref/libg4ref.so) on its worker pool."""
+
+    def __init__(self, path=LIB_REF, threads=1):
         if not os.path.exists(path):
             raise FileNotFoundError(path)
         L = self.L = C.CDLL(path)
@@ -272,12 +287,42 @@ class Ref:
             "ref_exp3_get": (None, [_u8p, _i64p, _u16p, _f32p]),
             "ref_resc": (_f, [_f32p, _i32p, _i, _f32p]),
             "ref_head": (None, [_f32p, _i, _f32p]),
+            "ref_head_setup": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
+            "ref_verify": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, C.POINTER(RefOut)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        L.ref_start(1)
+        self.threads = L.ref_start(threads)
+        self.model = None
+
+    def bind_model(self, model):
+        """run ref_verify on the oracle model's own arrays (no copies of the layer weights)"""
+        o, h = model.o, model.h
+        ptr = lambda w: o.L.g4o_model_ptr(h, w.encode())
+        rm = RefModel()
+        rm.V, rm.NL, rm.I, rm.ctx = model.V, model.NL, model.I, model.ctx
+        rm.E, rm.fnorm, rm.KC, rm.VC = ptr("E"), ptr("fnorm"), ptr("KC"), ptr("VC")
+        rm.cs[0], rm.cs[1], rm.sn[0], rm.sn[1] = ptr("cs0"), ptr("cs1"), ptr("sn0"), ptr("sn1")
+        for l in range(model.NL):
+            for j in range(7):
+                rm.L[l].W[j] = ptr(f"W{l}_{j}")
+                rm.L[l].S[j] = ptr(f"S{l}_{j}")
+            for t in range(6):
+                rm.L[l].nv[t] = ptr(f"N{l}_{t}")
+            rm.L[l].scalar = 0.75
+            rm.L[l].sliding = 1 if l % 5 != 4 else 0
+        self.L.ref_head_setup(ptr("Wq"), ptr("Sq"), ptr("coef"), ptr("x3"), ptr("cb"), ptr("xptr"), ptr("xcol"),
+                              ptr("xdel"), model.V)
+        self.model = rm
+
+    def verify(self, toks, na, nb, pos0):
+        out = RefOut()
+        rc = self.L.ref_verify(C.byref(self.model), _c(toks, np.int32), na, nb, pos0, C.byref(out))
+        if rc != 0:
+            raise RuntimeError("ref_verify needs V = 262144 and at most 8 rows")
+        return out
 
     def w4g32(self, W, S, X):
         X = _c(X, np.float32)

@@ -14,6 +14,12 @@
 namespace {
 XP g_xa, g_xb;
 bool g_started = false;
+// joins the pool's workers before the pool itself is destroyed at process exit
+struct PoolStopper {
+  ~PoolStopper() {
+    if (g_started) POOL.shutdown();
+  }
+} g_stopper;
 }
 
 extern "C" {
@@ -230,6 +236,348 @@ void ref_head(const float* h, int M, float* logit) {
   HA.logit = logit;
   HA.M = M;
   head_task(&HA, 0, 1);
+}
+
+// ---------------------------------------------------------------------------------------
+// One verify pass of the synthetic stack run by the reference's own kernels on its pool:
+// the call sequence restates fwd (E:1262-1405, per-layer-embedding branch zero, every layer
+// owning its KV), head_group (E:1408-1500) and the acceptance step (E:1647-1661), extended
+// to two draft branches exactly as the C oracle does.  Used as the "reference" CPU baseline
+// and to pin the oracle's layer composition.
+// ---------------------------------------------------------------------------------------
+struct RefLayer {
+  const uint8_t* W[7];
+  const uint16_t* S[7];
+  const float* nv[6];  // in_ln, post_attn, pre_ff, post_ff, qn, kn
+  float scalar;
+  int sliding;
+};
+struct RefModel {
+  int V, NL, I, ctx;
+  const uint16_t* E;
+  const float* fnorm;
+  uint16_t* KC;  // [NL][ctx][256]
+  uint16_t* VC;
+  const float* cs[2];
+  const float* sn[2];
+  RefLayer L[64];
+};
+struct RefOut {
+  int nacc, branch, ncommit;
+  int commit[8], G[8], fallback[8], nsurv[8];
+};
+
+namespace {
+Screen g_scr;
+XP g_xh;
+}
+
+// screen + exp3 head of a 262,144-row vocabulary (the screen scan hardcodes that size)
+void ref_head_setup(const uint8_t* Wq, const uint16_t* Sq, const float* coef, const uint8_t* x3, const uint8_t* cb,
+                    const int64_t* xptr, const uint16_t* xcol, const float* xdel, int V) {
+  g_scr.w.assign(Wq, Wq + (size_t)V * 768);
+  g_scr.s.assign(Sq, Sq + (size_t)V * 48);
+  g_scr.coef.assign(coef, coef + V);
+  g_scr.on = true;
+  g_hp.N = V;
+  g_hp.K = 1536;
+  std::memset(g_hp.cb, 0, 16);
+  std::memcpy(g_hp.cb, cb, 8);
+  g_hp.data.assign(x3, x3 + (size_t)V * 48 * 44);
+  g_hp.exc_ptr.assign(xptr, xptr + V + 1);
+  g_hp.exc_col.assign(xcol, xcol + xptr[V]);
+  g_hp.exc_delta.assign(xdel, xdel + xptr[V]);
+}
+
+// E:1408-1500 head_group over rows [hf, Mend) of hbuf; G receives the greedy tokens
+static void head_group_ref(float (*hbuf)[1536], const int* toks, int M, int hf, int Mend, int chain_lazy, int* G,
+                           int* fb, int* ns) {
+  const int H = 1536, Mh = Mend - hf;
+  auto cap = [](float s) { return r16(30.0f * tanhf(s / 30.0f)); };
+  static ScrArg* SA = new ScrArg();
+  static float hn[4];
+  constexpr int LIM = 30000;
+  static int fi[LIM];
+  static float fval[LIM];
+  static float logit[4][262144];
+  g_xh.prep(&hbuf[hf][0], H, Mh);
+  for (int m = 0; m < Mh; ++m) hn[m] = (float)sqrt(ss_avx2(hbuf[hf + m], H));
+  float seed_L[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
+  int seeds[160], nseeds = 0;  // E:1419-1427 (no drafter: the fixed list)
+  for (int m = 0; m < std::min(M, 8); ++m)
+    if (toks[m] >= 0 && toks[m] < 262144) seeds[nseeds++] = toks[m];
+  const int fixed_seeds[] = {2, 106, 107, 108, 235248, 235265, 235269, 476, 573, 577, 604, 651, 688, 728, 785, 818, 947, 1024, 1154, 1280};
+  for (int s : fixed_seeds) seeds[nseeds++] = s;
+  for (int si = 0; si < nseeds; ++si) {
+    const int n = seeds[si];
+    float sd[4];
+    const uint8_t* Wn = g_scr.w.data() + (size_t)n * (H / 2);
+    const uint16_t* Scn = g_scr.s.data() + (size_t)n * (H / 32);
+    switch (Mh) {
+      case 1: w4::gemm_rows_tile<1>(Wn, Scn, g_xh.xe, g_xh.xo, g_xh.gs, H, 0, 1, sd, 1, H / 2, H / 32); break;
+      case 2: w4::gemm_rows_tile<2>(Wn, Scn, g_xh.xe, g_xh.xo, g_xh.gs, H, 0, 1, sd, 1, H / 2, H / 32); break;
+      case 3: w4::gemm_rows_tile<3>(Wn, Scn, g_xh.xe, g_xh.xo, g_xh.gs, H, 0, 1, sd, 1, H / 2, H / 32); break;
+      default: w4::gemm_rows_tile<4>(Wn, Scn, g_xh.xe, g_xh.xo, g_xh.gs, H, 0, 1, sd, 1, H / 2, H / 32); break;
+    }
+    const float c = g_scr.coef[n];
+    for (int m = 0; m < Mh; ++m) seed_L[m] = std::max(seed_L[m], sd[m] - c * hn[m]);
+  }
+  for (int m = 0; m < Mh; ++m) {
+    SA->pre_thr[m] = seed_L[m];
+    SA->shared_best[m].store(seed_L[m], std::memory_order_relaxed);
+    SA->overflow[m].store(false, std::memory_order_relaxed);
+  }
+  SA->S = &g_scr;
+  SA->x = &g_xh;
+  SA->hn = hn;
+  SA->M = Mh;
+  SA->nxt.store(0, std::memory_order_relaxed);
+  POOL.run(screen_task, SA);
+  const int actT = POOL.active_count();
+  float Lm[4];
+  for (int m = 0; m < Mh; ++m) {
+    float L = -1e30f;
+    for (int t = 0; t < actT; ++t) L = std::max(L, SA->tmax[t][m]);
+    Lm[m] = L;
+  }
+  static RescArg RA;
+  auto eval_row = [&](int m) -> bool {  // E:1453-1474
+    if (SA->overflow[m].load(std::memory_order_relaxed)) return false;
+    const float thr = calc_thr_fast(Lm[m]);
+    int tot = 0;
+    for (int t = 0; t < actT; ++t)
+      for (int k = 0; k < SA->t_cnt[t][m]; ++k)
+        if (SA->t_u[t][m][k] >= thr) {
+          if (tot >= LIM) return false;
+          fi[tot++] = SA->t_idx[t][m][k];
+        }
+    RA.P = &g_hp;
+    RA.h = hbuf[hf + m];
+    RA.fval = fval;
+    RA.idx = fi;
+    RA.cnt = tot;
+    POOL.run(resc_task, &RA);
+    float mx = -1e30f;
+    for (int t = 0; t < actT; ++t) mx = std::max(mx, RA.tmax[t]);
+    const float cm = cap(mx);
+    int best = -1;
+    for (int i = 0; i < tot; ++i)
+      if (fval[i] >= mx - 2.0f && cap(fval[i]) == cm) {
+        best = fi[i];
+        break;
+      }
+    G[hf + m] = best;
+    ns[hf + m] = tot;
+    return true;
+  };
+  bool ok = true;
+  if (chain_lazy && Mh > 1) {  // E:1475-1484 (chain rows only)
+    if (!eval_row(0)) ok = false;
+    else
+      for (int m = 1; m < Mh; ++m) {
+        if (G[hf + m - 1] != toks[hf + m]) break;
+        if (!eval_row(m)) {
+          ok = false;
+          break;
+        }
+      }
+  } else {
+    for (int m = 0; m < Mh; ++m)
+      if (!eval_row(m)) {
+        ok = false;
+        break;
+      }
+  }
+  if (!ok) {  // E:1489-1498 full head for the whole group
+    HeadArg HA;
+    HA.P = &g_hp;
+    HA.h = &hbuf[hf][0];
+    HA.logit = &logit[0][0];
+    HA.M = Mh;
+    POOL.run(head_task, &HA);
+    for (int m = 0; m < Mh; ++m) {
+      float* lg = &logit[0][0] + (size_t)m * 262144;
+      float mx = -1e30f;
+      for (int i = 0; i < 262144; ++i) {
+        lg[i] = r16(lg[i]);
+        mx = std::max(mx, lg[i]);
+      }
+      const float cm = cap(mx);
+      int best = -1;
+      for (int i = 0; i < 262144; ++i)
+        if (lg[i] >= mx - 2.0f && cap(lg[i]) == cm) {
+          best = i;
+          break;
+        }
+      G[hf + m] = best;
+      fb[hf + m] = 1;
+    }
+  }
+}
+
+int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* out) {
+  const int H = 1536, M = 1 + na + nb, NL = md->NL, I = md->I;
+  if (M > 8 || md->V != 262144) return -1;
+  const int T = POOL.active_count();
+  G_I8_ACTIVE = false;
+  alignas(64) static float x[8][1536], q[8][2048], k[8][256], v[8][256], att[8][2048], o[8][1536], tmp[1536],
+      hbuf[8][1536];
+  static std::vector<float> gbuf, ubuf, abuf;
+  gbuf.resize((size_t)8 * I);
+  ubuf.resize((size_t)8 * I);
+  abuf.resize((size_t)8 * I);
+  static XP XA, XB;
+  int rope[8], skl[8], skh[8];
+  for (int r = 0; r < M; ++r) {
+    if (r <= na) {
+      rope[r] = pos0 + r;
+      skl[r] = 1;
+      skh[r] = 0;
+    } else {
+      rope[r] = pos0 + (r - na);
+      skl[r] = pos0 + 1;
+      skh[r] = pos0 + na;
+    }
+  }
+  const __m256 vsqh = _mm256_set1_ps(sqrtf((float)H));
+  for (int m = 0; m < M; ++m) {  // E:1262-1267
+    const uint16_t* er = md->E + (size_t)toks[m] * H;
+    for (int i = 0; i < H; i += 8) _mm256_storeu_ps(x[m] + i, rbf8(_mm256_mul_ps(bf8(er + i), vsqh)));
+    rms_prep_x(x[m], md->L[0].nv[0], H, nullptr, XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2),
+               XA.gs + (size_t)m * (H / 32), false);
+  }
+  XA.K = H;
+  XA.M = M;
+  for (int l = 0; l < NL; ++l) {
+    const RefLayer& A = md->L[l];
+    Q4 qm[7];
+    const int Ns[7] = {2048, 256, 256, 1536, I, I, 1536}, Ks[7] = {1536, 1536, 1536, 2048, 1536, 1536, I};
+    for (int j = 0; j < 7; ++j) {
+      qm[j].w = A.W[j];
+      qm[j].s = A.S[j];
+      qm[j].N = Ns[j];
+      qm[j].K = Ks[j];
+    }
+    {  // E:1289
+      const Q4* qq[3] = {&qm[0], &qm[1], &qm[2]};
+      float* yy[3] = {&q[0][0], &k[0][0], &v[0][0]};
+      lin_multi(XA, 3, qq, yy);
+    }
+    const int ty = A.sliding ? 0 : 1;
+    uint16_t* KCl = md->KC + (size_t)l * md->ctx * 256;
+    uint16_t* VCl = md->VC + (size_t)l * md->ctx * 256;
+    for (int m = 0; m < M; ++m) {  // E:1307-1324
+      const float* cs = md->cs[ty] + (size_t)rope[m] * 128;
+      const float* sn = md->sn[ty] + (size_t)rope[m] * 128;
+      for (int h = 0; h < 8; ++h) {
+        rms_r16_inplace(q[m] + h * 256, A.nv[4], 256);
+        rope_avx2(q[m] + h * 256, cs, sn, 256);
+      }
+      rms_r16_inplace(k[m], A.nv[5], 256);
+      rope_avx2(k[m], cs, sn, 256);
+      rms_r16_inplace(v[m], nullptr, 256);
+      uint16_t* kd = KCl + (size_t)(pos0 + m) * 256;
+      uint16_t* vd = VCl + (size_t)(pos0 + m) * 256;
+      for (int i = 0; i < 256; i += 8) {
+        _mm_storeu_si128((__m128i*)(kd + i), f2bf8(_mm256_loadu_ps(k[m] + i)));
+        _mm_storeu_si128((__m128i*)(vd + i), f2bf8(_mm256_loadu_ps(v[m] + i)));
+      }
+    }
+    int lo[8], kmax = pos0 + M - 1, kmin = kmax;  // E:1325-1326
+    for (int m = 0; m < M; ++m) {
+      lo[m] = A.sliding ? std::max(0, rope[m] - 511) : 0;
+      kmin = std::min(kmin, lo[m]);
+    }
+    for (int g0 = 0; g0 < M; g0 += 4) {  // AttnArg holds 4 rows: same geometry, rows in groups
+      AttnArg aa;
+      aa.Kc = KCl;
+      aa.Vc = VCl;
+      aa.hd = 256;
+      aa.nh = 8;
+      aa.M = std::min(4, M - g0);
+      aa.kmin = kmin;
+      aa.kmax = kmax;
+      float* outp[4];
+      for (int mm = 0; mm < aa.M; ++mm) {
+        const int m = g0 + mm;
+        aa.q[mm] = q[m];
+        aa.pos[mm] = pos0 + m;
+        aa.lo[mm] = lo[m];
+        aa.skip_lo[mm] = skl[m];
+        aa.skip_hi[mm] = skh[m];
+        outp[mm] = att[m];
+      }
+      POOL.run(attn_task, &aa);
+      attn_merge(aa, T, outp, nullptr);
+    }
+    XB.prep(&att[0][0], 2048, M);
+    lin1(XB, qm[3], &o[0][0]);  // E:1356
+    for (int m = 0; m < M; ++m) {  // E:1358-1361
+      rbf_n(o[m], H);
+      rms(o[m], A.nv[1], H, tmp);
+      add_res_inplace(x[m], tmp, H);
+      rms_prep_x(x[m], A.nv[2], H, nullptr, XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2),
+                 XA.gs + (size_t)m * (H / 32), true);
+    }
+    XA.K = H;
+    XA.M = M;
+    XB.K = I;
+    XB.M = M;
+    GateUpArg gua{&XA, &qm[4], &qm[5], gbuf.data(), ubuf.data(), abuf.data(), &XB};
+    POOL.run(gate_up_fused_task, &gua);  // E:1366
+    lin1(XB, qm[6], &o[0][0]);           // E:1373
+    const __m256 vsc = _mm256_set1_ps(A.scalar);
+    for (int m = 0; m < M; ++m) {  // E:1375-1404, zero per-layer-embedding branch
+      rbf_n(o[m], H);
+      rms(o[m], A.nv[3], H, tmp);
+      add_res_prep_x(x[m], tmp, H, XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2), XA.gs + (size_t)m * (H / 32));
+      for (int i = 0; i < H; i += 8) _mm256_storeu_ps(x[m] + i, rbf8(_mm256_mul_ps(_mm256_loadu_ps(x[m] + i), vsc)));
+      if (l + 1 < NL)
+        rms_prep_x(x[m], md->L[l + 1].nv[0], H, nullptr, XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2),
+                   XA.gs + (size_t)m * (H / 32), false);
+      else {
+        rms(x[m], md->fnorm, H, hbuf[m]);
+        rbf_n(hbuf[m], H);
+      }
+    }
+    XA.K = H;
+    XA.M = M;
+  }
+  int G[8], fb[8], ns[8];
+  for (int r = 0; r < 8; ++r) G[r] = -1, fb[r] = 0, ns[r] = 0;
+  for (int r0 = 0; r0 < M; r0 += 4) head_group_ref(hbuf, toks, M, r0, std::min(M, r0 + 4), r0 == 0, G, fb, ns);
+  // E:1647-1661 along the branch chosen by G[0]
+  int path[8], np = 1, first = 0, len = 0, br = 0;
+  path[0] = 0;
+  if (na >= 1 && G[0] == toks[1]) {
+    first = 1;
+    len = na;
+  } else if (nb >= 1 && G[0] == toks[na + 1]) {
+    first = na + 1;
+    len = nb;
+    br = 1;
+  }
+  for (int i = 0; i < len; ++i) {
+    const int row = first + i;
+    if (G[path[np - 1]] != toks[row] || G[row] < 0) break;
+    path[np++] = row;
+  }
+  out->nacc = np - 1;
+  out->branch = np > 1 ? br : 0;
+  out->ncommit = np;
+  for (int r = 0; r < 8; ++r) {
+    out->commit[r] = r < np ? G[path[r]] : -1;
+    out->G[r] = G[r];
+    out->fallback[r] = fb[r];
+    out->nsurv[r] = ns[r];
+  }
+  if (out->branch == 1)
+    for (int l = 0; l < NL; ++l)
+      for (int i = 1; i < np; ++i) {
+        std::memcpy(md->KC + ((size_t)l * md->ctx + pos0 + i) * 256, md->KC + ((size_t)l * md->ctx + pos0 + path[i]) * 256, 512);
+        std::memcpy(md->VC + ((size_t)l * md->ctx + pos0 + i) * 256, md->VC + ((size_t)l * md->ctx + pos0 + path[i]) * 256, 512);
+      }
+  return 0;
 }
 
 }  // extern "C"

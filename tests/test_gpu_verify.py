@@ -86,6 +86,25 @@ def test_verify_branch_b_accepted(pair):
     assert same(dev.read("VC", np.uint16), om.get("VC", np.uint16, NL * CTX * 256))
 
 
+def test_graph_replays_match_eager_and_oracle(pair):
+    """the captured graph, replayed repeatedly with host work in between, equals eager launches"""
+    dev, om = pair
+    toks = [77, 1, 2, 3, 4, 5, 6]
+    results = []
+    for graphs in (False, True):
+        dev.set_graphs(graphs)
+        for rep in range(4):  # graph mode: eager warm-up, capture, then replays
+            note(f"graph={graphs} rep={rep}")
+            r, hg = dev.verify(np.array(toks, np.int32), 3, 3, NCTX + 100, 8, hidden=True)
+            results.append((r.as_dict(), hg.copy()))
+            _ = np.ones(1000).sum()  # host work between replays
+    dev.set_graphs(True)
+    o, ho = om.verify(np.array(toks, np.int32), 3, 3, NCTX + 100, 8)
+    for d, h in results:
+        assert d["G"] == list(o.G) and d["nacc"] == o.nacc
+        assert same(h, ho)
+
+
 def test_verify_sequence_of_steps(pair):
     """successive passes commit tokens and advance the position, as run_req does"""
     dev, om = pair
