@@ -279,7 +279,7 @@ class Ref:
             "ref_calc_thr": (_f, [_f]),
             "ref_gate_up": (None, [_u8p, _u16p, _u8p, _u16p, _i, _i, _f32p, _i, _f32p, _f32p,
                                    _f32p, _f32p, _f32p]),
-            "ref_attn": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _i32p, _i32p,
+            "ref_attn": (_i, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _i32p, _i32p,
                                 _i, _i, _i, _f32p, _i, _vp, _vp, _vp, _vp, _vp]),
             "ref_screen": (_i, [_u8p, _u16p, _f32p, _f32p, _i, _f32p, _i32p, _i32p, _f32p,
                                 _f32p, _i32p]),
@@ -358,12 +358,6 @@ class Ref:
         self.L.ref_exp3_get(data, ptr, col, dl)
         return dict(cb=np.array(cb, np.uint8), data=data, ptr=ptr, col=col[:ne], delta=dl[:ne], N=N, K=K)
 
-    def head(self, h):
-        h = _c(h, np.float32)
-        M = h.shape[0]
-        N = 262144 if False else None
-        return M, N
-
     def attn(self, Kc, Vc, hd, nh, q, pos, lo, skip_lo, skip_hi, kmin, kmax, T, prep=False, parts=False):
         q = _c(q, np.float32)
         M = q.shape[0]
@@ -375,9 +369,11 @@ class Ref:
         pm = np.empty((T, M, nh), np.float32) if parts else None
         pl = np.empty((T, M, nh), np.float32) if parts else None
         ptr = lambda a: None if a is None else a.ctypes.data
-        self.L.ref_attn(_c(Kc, np.uint16), _c(Vc, np.uint16), hd, nh, M, q, K, _c(pos, np.int32),
-                        _c(lo, np.int32), _c(skip_lo, np.int32), _c(skip_hi, np.int32), kmin, kmax,
-                        T, out, K, ptr(xe), ptr(xo), ptr(gs), ptr(pm), ptr(pl))
+        rc = self.L.ref_attn(_c(Kc, np.uint16), _c(Vc, np.uint16), hd, nh, M, q, K, _c(pos, np.int32),
+                             _c(lo, np.int32), _c(skip_lo, np.int32), _c(skip_hi, np.int32), kmin, kmax,
+                             T, out, K, ptr(xe), ptr(xo), ptr(gs), ptr(pm), ptr(pl))
+        if rc != 0:
+            raise ValueError("ref_attn: outside the reference's capacity (M <= 4, T <= 16, hd <= 512)")
         res = [out]
         if prep:
             res += [xe, xo, gs]

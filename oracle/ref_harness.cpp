@@ -75,13 +75,13 @@ void ref_w4a8(const uint8_t* W, const uint16_t* S, const float* X, int M, int N,
 }
 
 void ref_exp8(const float* x, int n, float* y) {
-  for (int i = 0; i < n; i += 8) _mm256_storeu_ps(y + i, exp8(_mm256_loadu_ps(x + i)));
+  for (int i = 0; i + 8 <= n; i += 8) _mm256_storeu_ps(y + i, exp8(_mm256_loadu_ps(x + i)));  // n % 8 == 0
 }
 void ref_gelu8(const float* x, int n, float* y) {
-  for (int i = 0; i < n; i += 8) _mm256_storeu_ps(y + i, gelu8(_mm256_loadu_ps(x + i)));
+  for (int i = 0; i + 8 <= n; i += 8) _mm256_storeu_ps(y + i, gelu8(_mm256_loadu_ps(x + i)));  // n % 8 == 0
 }
 void ref_rbf8(const float* x, int n, float* y) {
-  for (int i = 0; i < n; i += 8) _mm256_storeu_ps(y + i, rbf8(_mm256_loadu_ps(x + i)));
+  for (int i = 0; i + 8 <= n; i += 8) _mm256_storeu_ps(y + i, rbf8(_mm256_loadu_ps(x + i)));  // n % 8 == 0
 }
 void ref_f2bf(const float* x, int n, uint16_t* y) {
   for (int i = 0; i < n; ++i) y[i] = f2bf(x[i]);
@@ -123,10 +123,15 @@ void ref_gate_up(const uint8_t* Wg, const uint16_t* Sg, const uint8_t* Wu, const
 
 // split-KV attention: every split t of T in turn (E:743-877), then attn_merge (E:1019-1059);
 // out receives the rounded outputs, xe/xo/gs (optional) the fused o_proj prep.  M <= 4.
-void ref_attn(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
-              const int* pos, const int* lo, const int* skip_lo, const int* skip_hi, int kmin,
-              int kmax, int T, float* out, int ldo, float* xe, float* xo, float* gs, float* part_m,
-              float* part_l) {
+// Returns -1 (nothing computed) outside the reference's capacity: AttnArg holds 4 rows
+// (E:739), the partial buffers 16 splits of hd <= 512, a split at most ACH = 8192 positions.
+int ref_attn(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
+             const int* pos, const int* lo, const int* skip_lo, const int* skip_hi, int kmin,
+             int kmax, int T, float* out, int ldo, float* xe, float* xo, float* gs, float* part_m,
+             float* part_l) {
+  if (M < 1 || M > 4 || T < 1 || T > 16 || hd > 512 || nh > 8 || kmax < kmin ||
+      (kmax - kmin + 1 + T - 1) / T > ACH)
+    return -1;
   G_I8_ACTIVE = false;
   AttnArg aa;
   aa.Kc = Kc;
@@ -163,6 +168,7 @@ void ref_attn(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, con
       std::memcpy(gs + (size_t)m * K / 32, g_xb.gs + (size_t)m * K / 32, sizeof(float) * K / 32);
     }
   }
+  return 0;
 }
 
 // The screen scan (E:460-538) over the 262,144 x 1536 screen with one worker.  h: M <= 4 rows

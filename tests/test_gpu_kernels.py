@@ -136,9 +136,3 @@ def test_head_full_vocab(orc, dev):
         info, surv, sval = orc.head_row(h[m], scr, P)
         assert G[m] == info.G and ns[m] == info.nsurv, (m, G[m], info.G, ns[m], info.nsurv)
     assert fb[0] == 1 and fb[1] == 1 and fb[2] == 0 and fb[3] == 0
-
-
-def test_expf_restatement_host(g4v):
-    """the split merge's expf restatement equals the host libm on a dense sample of x <= 0"""
-    L = g4v.load()
-    assert L.g4v_expf_selftest(0x80000000, 0xFF800000, 97) == 0
