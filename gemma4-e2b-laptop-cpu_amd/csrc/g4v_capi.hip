@@ -76,7 +76,7 @@ struct g4v_ctx {
   HeadBufs hb1, hb2;
   DBuf hrow, hnrow;
   // model
-  bool model_ready = false;
+  bool model_ready = false;  // buffers allocated (model_synth or model_create)
   int NL = 0, I = 0, ctxcap = 0;
   std::vector<std::unique_ptr<Layer>> L;
   DBuf fnorm, KC, VC, rope;  // rope: [2][ctxcap][HD/2] cos then sin
@@ -581,56 +581,32 @@ int g4v_head_survivors(g4v_ctx* c, int m, int* idx, float* val, int cap, int* n)
 // ---------------------------------------------------------------------------------------
 // synthetic model
 // ---------------------------------------------------------------------------------------
-int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap) {
-  if (!c) return G4V_E_ARG;
-  ARGCHK(V > 0 && NL > 0 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_synth: bad shape");
-  HIPCHK(hipSetDevice(c->device));
+}  // extern "C"
+
+// Allocate an empty stack of NL layers: matrices unset, norms zero, KV cache zeroed, RoPE
+// tables (E:1246-1248: sliding layers theta 1e4 full rotary, global layers 1e6 rotary 0.25)
+// and the step buffers.  The weights come from model_synth or from the g4v_model_set_* calls.
+static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   hipStream_t st = c->st;
   drop_graphs(c);  // every model and step buffer is reallocated below
   c->model_ready = false;
+  c->head_ready = false;
+  c->V = V;
   c->NL = NL;
   c->I = I;
   c->ctxcap = ctxcap;
-  // output matrix / embedding: E[n][k] = f2bf(0.02 normal(stream(seed, 1), n*H + k))
   ALLOC(c->E, (size_t)V * H * 2);
-  launch_gen_bf16_normal(c->E.as<uint16_t>(), (size_t)V * H, rng_stream(seed, 1), 0.02f, st);
-  int r = head_build_dev(c, V);
-  if (r) return r;
-  const int Ns[7] = {NQ * HD, HD, HD, H, I, I, H}, Ks[7] = {H, H, H, NQ * HD, H, H, I};
-  DBuf tw, ts;
-  ALLOC(tw, (size_t)std::max(I, NQ * HD) * std::max(H, I) / 2);
-  ALLOC(ts, (size_t)std::max(I, NQ * HD) * std::max(H, I) / 16);
   c->L.clear();
   for (int l = 0; l < NL; ++l) {
     auto lay = std::make_unique<Layer>();
-    for (int j = 0; j < 7; ++j) {
-      const size_t nb = (size_t)Ns[j] * Ks[j] / 2, ns = (size_t)Ns[j] * Ks[j] / 32;
-      launch_gen_w4(tw.as<uint8_t>(), ts.as<uint16_t>(), nb, ns, rng_stream(seed, 1000 + 10 * (uint64_t)l + j),
-                    rng_stream(seed, 2000 + 10 * (uint64_t)l + j), st);
-      r = upload_w4(c, lay->m[j], tw.as<uint8_t>(), ts.as<uint16_t>(), true, Ns[j], Ks[j]);
-      if (r) return r;
-    }
-    // norms: r16(base + span * unif(stream(seed, 3000 + 10 l + t), i))
-    std::vector<float> nv(4 * H + 2 * HD);
-    for (int t = 0; t < 6; ++t) {
-      const int n = t < 4 ? H : HD, off = t < 4 ? t * H : 4 * H + (t - 4) * HD;
-      const float base = t < 4 ? 0.5f : 0.2f, span = t < 4 ? 1.0f : 0.1f;
-      const uint64_t sn = rng_stream(seed, 3000 + 10 * (uint64_t)l + t);
-      for (int i = 0; i < n; ++i) nv[off + i] = r16(base + span * rng_unif(sn, i));
-    }
-    ALLOC(lay->norms, nv.size() * 4);
-    HIPCHK(hipMemcpyAsync(lay->norms.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice, st));
-    HIPCHK(hipStreamSynchronize(st));  // nv goes out of scope
-    lay->scalar = 0.75f;
+    ALLOC(lay->norms, (size_t)(4 * H + 2 * HD) * 4);
+    HIPCHK(hipMemsetAsync(lay->norms.p, 0, lay->norms.n, st));
+    lay->scalar = 1.0f;
     lay->sliding = (l % 5 != 4);
     c->L.push_back(std::move(lay));
   }
-  std::vector<float> fn(H);
-  const uint64_t sf = rng_stream(seed, 4000);
-  for (int i = 0; i < H; ++i) fn[i] = r16(0.5f + rng_unif(sf, i));
   ALLOC(c->fnorm, H * 4);
-  HIPCHK(hipMemcpyAsync(c->fnorm.p, fn.data(), H * 4, hipMemcpyHostToDevice, st));
-  // KV cache and RoPE tables (E:1246-1248): sliding theta 1e4 full rotary, global 1e6 rotary 0.25
+  HIPCHK(hipMemsetAsync(c->fnorm.p, 0, H * 4, st));
   ALLOC(c->KC, (size_t)NL * ctxcap * HD * 2);
   ALLOC(c->VC, (size_t)NL * ctxcap * HD * 2);
   HIPCHK(hipMemsetAsync(c->KC.p, 0, c->KC.n, st));
@@ -651,7 +627,6 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
   }
   ALLOC(c->rope, rt.size() * 4);
   HIPCHK(hipMemcpyAsync(c->rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, st));
-  // step buffers
   ALLOC(c->x, MAXM * H * 4);
   ALLOC(c->xa, MAXM * H * 4);
   ALLOC(c->q, MAXM * NQ * HD * 4);
@@ -669,9 +644,161 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
   ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
   ALLOC(c->stepd, sizeof(StepDev));
   ALLOC(c->resd, sizeof(VerifyResultDev));
+  HIPCHK(hipStreamSynchronize(st));  // rt goes out of scope
+  return 0;
+}
+
+static const int kMatN[7] = {NQ * HD, HD, HD, H, 0, 0, H}, kMatK[7] = {H, H, H, NQ * HD, H, H, 0};
+static int mat_n(const g4v_ctx* c, int j) { return (j == 4 || j == 5) ? c->I : kMatN[j]; }
+static int mat_k(const g4v_ctx* c, int j) { return j == 6 ? c->I : kMatK[j]; }
+
+// every matrix, the embedding/head and the norms are present
+static bool model_complete(const g4v_ctx* c, std::string* what) {
+  if (c->L.empty()) {
+    *what = "no model";
+    return false;
+  }
+  if (!c->head_ready) {
+    *what = "embedding / head not set";
+    return false;
+  }
+  for (int l = 0; l < (int)c->L.size(); ++l)
+    for (int j = 0; j < 7; ++j)
+      if (!c->L[l]->m[j].wr.p) {
+        *what = "matrix " + std::to_string(j) + " of layer " + std::to_string(l) + " not set";
+        return false;
+      }
+  return true;
+}
+
+extern "C" {
+
+int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_synth: bad shape");
+  HIPCHK(hipSetDevice(c->device));
+  hipStream_t st = c->st;
+  int r = model_alloc(c, V, NL, I, ctxcap);
+  if (r) return r;
+  // output matrix / embedding: E[n][k] = f2bf(0.02 normal(stream(seed, 1), n*H + k))
+  launch_gen_bf16_normal(c->E.as<uint16_t>(), (size_t)V * H, rng_stream(seed, 1), 0.02f, st);
+  r = head_build_dev(c, V);
+  if (r) return r;
+  c->head_ready = true;
+  DBuf tw, ts;
+  ALLOC(tw, (size_t)std::max(I, NQ * HD) * std::max(H, I) / 2);
+  ALLOC(ts, (size_t)std::max(I, NQ * HD) * std::max(H, I) / 16);
+  std::vector<float> nv(4 * H + 2 * HD);
+  for (int l = 0; l < NL; ++l) {
+    Layer& lay = *c->L[l];
+    for (int j = 0; j < 7; ++j) {
+      const int N = mat_n(c, j), K = mat_k(c, j);
+      const size_t nb = (size_t)N * K / 2, ns = (size_t)N * K / 32;
+      launch_gen_w4(tw.as<uint8_t>(), ts.as<uint16_t>(), nb, ns, rng_stream(seed, 1000 + 10 * (uint64_t)l + j),
+                    rng_stream(seed, 2000 + 10 * (uint64_t)l + j), st);
+      r = upload_w4(c, lay.m[j], tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K);
+      if (r) return r;
+    }
+    // norms: r16(base + span * unif(stream(seed, 3000 + 10 l + t), i))
+    for (int t = 0; t < 6; ++t) {
+      const int n = t < 4 ? H : HD, off = t < 4 ? t * H : 4 * H + (t - 4) * HD;
+      const float base = t < 4 ? 0.5f : 0.2f, span = t < 4 ? 1.0f : 0.1f;
+      const uint64_t sn = rng_stream(seed, 3000 + 10 * (uint64_t)l + t);
+      for (int i = 0; i < n; ++i) nv[off + i] = r16(base + span * rng_unif(sn, i));
+    }
+    HIPCHK(hipMemcpyAsync(lay.norms.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(hipStreamSynchronize(st));  // nv is refilled for the next layer
+    lay.scalar = 0.75f;
+    lay.sliding = (l % 5 != 4);
+  }
+  std::vector<float> fn(H);
+  const uint64_t sf = rng_stream(seed, 4000);
+  for (int i = 0; i < H; ++i) fn[i] = r16(0.5f + rng_unif(sf, i));
+  HIPCHK(hipMemcpyAsync(c->fnorm.p, fn.data(), H * 4, hipMemcpyHostToDevice, st));
   HIPCHK(hipGetLastError());
   HIPCHK(hipStreamSynchronize(st));
   c->model_ready = true;
+  return 0;
+}
+
+int g4v_model_create(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_create: bad shape");
+  HIPCHK(hipSetDevice(c->device));
+  int r = model_alloc(c, V, NL, I, ctxcap);
+  if (r) return r;
+  c->model_ready = true;
+  return 0;
+}
+
+int g4v_model_set_embed(g4v_ctx* c, const uint16_t* E) {
+  if (!c || !E) return G4V_E_ARG;
+  if (c->L.empty()) {
+    c->err = "model_set_embed: no model (g4v_model_create first)";
+    return G4V_E_STATE;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  HIPCHK(hipMemcpyAsync(c->E.p, E, (size_t)c->V * H * 2, hipMemcpyHostToDevice, c->st));
+  int r = head_build_dev(c, c->V);
+  if (r) return r;
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->head_ready = true;
+  return 0;
+}
+
+int g4v_model_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint16_t* s) {
+  if (!c || !w || !s) return G4V_E_ARG;
+  ARGCHK(l >= 0 && l < (int)c->L.size() && j >= 0 && j < 7, "model_set_matrix: layer or matrix index out of range");
+  HIPCHK(hipSetDevice(c->device));
+  drop_graphs(c);  // the matrix buffers are reallocated
+  const int N = mat_n(c, j), K = mat_k(c, j);
+  DBuf tmp;
+  ALLOC(tmp, (size_t)N * K / 2);
+  HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)N * K / 2, hipMemcpyHostToDevice, c->st));
+  int r = upload_w4(c, c->L[l]->m[j], tmp.as<uint8_t>(), s, false, N, K);
+  if (r) return r;
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+int g4v_model_set_norms(g4v_ctx* c, int l, const float* const nv[6], float scalar, int sliding) {
+  if (!c || !nv) return G4V_E_ARG;
+  ARGCHK(l >= 0 && l < (int)c->L.size(), "model_set_norms: layer index out of range");
+  for (int t = 0; t < 6; ++t) ARGCHK(nv[t] != nullptr, "model_set_norms: null norm vector");
+  HIPCHK(hipSetDevice(c->device));
+  Layer& lay = *c->L[l];
+  for (int t = 0; t < 6; ++t) {
+    const int n = t < 4 ? H : HD, off = t < 4 ? t * H : 4 * H + (t - 4) * HD;
+    HIPCHK(hipMemcpyAsync(lay.norms.as<float>() + off, nv[t], (size_t)n * 4, hipMemcpyHostToDevice, c->st));
+  }
+  HIPCHK(hipStreamSynchronize(c->st));
+  if (lay.scalar != scalar || lay.sliding != (sliding != 0)) drop_graphs(c);  // both are baked into launches
+  lay.scalar = scalar;
+  lay.sliding = sliding != 0;
+  return 0;
+}
+
+int g4v_model_set_final_norm(g4v_ctx* c, const float* w) {
+  if (!c || !w) return G4V_E_ARG;
+  if (c->L.empty()) {
+    c->err = "model_set_final_norm: no model";
+    return G4V_E_STATE;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  HIPCHK(hipMemcpyAsync(c->fnorm.p, w, H * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+int g4v_model_set_kv(g4v_ctx* c, int l, int pos0, int n, const uint16_t* K, const uint16_t* V) {
+  if (!c || (n > 0 && (!K || !V))) return G4V_E_ARG;
+  ARGCHK(l >= 0 && l < (int)c->L.size() && pos0 >= 0 && n >= 0 && pos0 + n <= c->ctxcap,
+         "model_set_kv: layer or position range outside the cache");
+  HIPCHK(hipSetDevice(c->device));
+  const size_t off = ((size_t)l * c->ctxcap + pos0) * HD;
+  HIPCHK(hipMemcpyAsync(c->KC.as<uint16_t>() + off, K, (size_t)n * HD * 2, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(c->VC.as<uint16_t>() + off, V, (size_t)n * HD * 2, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
   return 0;
 }
 
@@ -868,8 +995,9 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
 int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
                     float* hidden) {
   if (!c) return G4V_E_ARG;
-  if (!c->model_ready) {
-    c->err = "verify_step: no model (g4v_model_synth first)";
+  std::string missing;
+  if (!c->model_ready || !model_complete(c, &missing)) {
+    c->err = "verify_step: model incomplete: " + (c->model_ready ? missing : std::string("no model"));
     return G4V_E_STATE;
   }
   const int M = 1 + na + nb;

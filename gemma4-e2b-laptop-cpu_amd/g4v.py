@@ -35,6 +35,12 @@ SIGNATURES = {
     "g4v_head_argmax": (_i, [_vp, _f32p, _i, _i32p, _i32p, _i32p]),
     "g4v_head_survivors": (_i, [_vp, _i, _i32p, _f32p, _i, C.POINTER(_i)]),
     "g4v_model_synth": (_i, [_vp, C.c_uint64, _i, _i, _i, _i]),
+    "g4v_model_create": (_i, [_vp, _i, _i, _i, _i]),
+    "g4v_model_set_embed": (_i, [_vp, _u16p]),
+    "g4v_model_set_matrix": (_i, [_vp, _i, _i, _u8p, _u16p]),
+    "g4v_model_set_norms": (_i, [_vp, _i, C.POINTER(_vp), C.c_float, _i]),
+    "g4v_model_set_final_norm": (_i, [_vp, _f32p]),
+    "g4v_model_set_kv": (_i, [_vp, _i, _i, _i, _u16p, _u16p]),
     "g4v_model_fake_ctx": (_i, [_vp, _i, C.c_uint64]),
     "g4v_model_read": (_i, [_vp, C.c_char_p, _vp, C.c_size_t, C.POINTER(C.c_size_t)]),
     "g4v_verify_step": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
@@ -177,6 +183,30 @@ class Device:
     # ---- model + verify ----
     def model_synth(self, seed, V, NL, I=6144, ctxcap=4096):
         self._ok(self.L.g4v_model_synth(self.h, seed, V, NL, I, ctxcap), "model_synth")
+
+    def model_create(self, V, NL, I=6144, ctxcap=4096):
+        """an empty stack; fill it with set_embed / set_matrix / set_norms / set_final_norm"""
+        self._ok(self.L.g4v_model_create(self.h, V, NL, I, ctxcap), "model_create")
+
+    def set_embed(self, E):
+        self._ok(self.L.g4v_model_set_embed(self.h, _c(E, np.uint16)), "model_set_embed")
+
+    def set_matrix(self, layer, j, w, s):
+        self._ok(self.L.g4v_model_set_matrix(self.h, layer, j, _c(w, np.uint8), _c(s, np.uint16)),
+                 "model_set_matrix")
+
+    def set_norms(self, layer, norms, scalar, sliding):
+        """norms: in_ln, post_attn, pre_ff, post_ff [1536] and q_norm, k_norm [256]"""
+        arrs = [_c(v, np.float32) for v in norms]
+        ptrs = (_vp * 6)(*[a.ctypes.data for a in arrs])
+        self._ok(self.L.g4v_model_set_norms(self.h, layer, ptrs, scalar, 1 if sliding else 0), "model_set_norms")
+
+    def set_final_norm(self, w):
+        self._ok(self.L.g4v_model_set_final_norm(self.h, _c(w, np.float32)), "model_set_final_norm")
+
+    def set_kv(self, layer, pos0, K, V):
+        K, V = _c(K, np.uint16), _c(V, np.uint16)
+        self._ok(self.L.g4v_model_set_kv(self.h, layer, pos0, K.size // 256, K, V), "model_set_kv")
 
     def fake_ctx(self, n, seed=12345):
         self._ok(self.L.g4v_model_fake_ctx(self.h, n, seed), "model_fake_ctx")

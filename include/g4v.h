@@ -63,6 +63,23 @@ int g4v_head_survivors(g4v_ctx* c, int m, int* idx, float* val, int cap, int* n)
 /* ---- synthetic decoder stack (35-layer Gemma-4-E2B-shaped, int4 G32, hd 256, 8q/1kv heads,
  * l % 5 != 4 sliding-window 512) generated on device from `seed`. */
 int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap);
+/* The same stack from the caller's own weights (the checkpoint the engine maps, E:166-176).
+ * g4v_model_create allocates an empty stack and zeroes the KV cache. Then set the
+ * embedding / tied output matrix E [V][1536] bf16 (E:1262-1267, E:1406; this also builds the
+ * certified head), the 7 matrices of every layer in the Q4 byte layout (j: 0 q [2048x1536],
+ * 1 k [256x1536], 2 v [256x1536], 3 o [1536x2048], 4 gate [Ix1536], 5 up [Ix1536],
+ * 6 down [1536xI]; E:1289, 1356, 1366, 1373), the six norm vectors of every layer (in_ln,
+ * post_attn, pre_ff, post_ff [1536]; q_norm, k_norm [256]) with the layer scalar and its
+ * attention type (sliding window 512 or global), and the final norm.  g4v_verify_step
+ * refuses a stack with any matrix or the embedding unset. */
+int g4v_model_create(g4v_ctx* c, int V, int NL, int I, int ctxcap);
+int g4v_model_set_embed(g4v_ctx* c, const uint16_t* E);
+int g4v_model_set_matrix(g4v_ctx* c, int layer, int j, const uint8_t* w, const uint16_t* s);
+int g4v_model_set_norms(g4v_ctx* c, int layer, const float* const nv[6], float scalar, int sliding);
+int g4v_model_set_final_norm(g4v_ctx* c, const float* w);
+/* KV rows [pos0, pos0 + n) of one layer, bf16 [n][256] each: a cache filled elsewhere
+ * (the engine's prefill, E:1328-1336) */
+int g4v_model_set_kv(g4v_ctx* c, int layer, int pos0, int n, const uint16_t* K, const uint16_t* V);
 /* E:1249-1250 ENGINE_FAKE_CTX: first n KV positions of every layer from the LCG seeded `seed` */
 int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
 /* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm") */

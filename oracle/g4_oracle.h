@@ -11,7 +11,26 @@
  * its own; every contraction that GCC performs in the reference build
  * (-O3 -march=x86-64-v3, default -ffp-contract=fast) is written out here.
  *
- * Pinning (what checks each function): see oracle/README.md.
+ * Pinning -- what checks each function (tests/test_golden.py against vectors written by
+ * the reference's own kernels, tests/test_oracle_vs_ref.py against those kernels live,
+ * tests/test_oracle_math.py against closed forms, bounds and brute force):
+ *   f2bf/r16, exp8, gelu8, sumsq, rms*, rope   golden + live + fp64 / RNE brute force
+ *   rope_tables                                fp64 closed form only (the reference builds
+ *                                              its tables inside main(), E:1246-1247)
+ *   cap, calc_thr                              golden + live + defining property by scan
+ *   prep_x, w4g32_*                            golden + live + fp64 closed form, row independence
+ *   w4a8_quant, w4a8_gemm                      golden + live + exact integer part
+ *   exp3_codebook                              most-frequent-exponent brute force only (the
+ *                                              reference computes it inside main(), E:1232-1234)
+ *   exp3_count/pack/dot/gemm                   golden (pack bytes, exceptions, logits) + round trip
+ *   screen_build                               soundness and tightness of the bound, scale and
+ *                                              level rule (built inside main(), E:1235-1244)
+ *   head_row                                   golden survivor sets (reference scan) + screened
+ *                                              greedy == brute-force full-head greedy
+ *   attn_splitkv                               golden + live + fp64 softmax, LSE identity, masks
+ *   model / verify                             golden passes through the reference's kernels
+ *                                              (2 layers, V 262144), acceptance brute force
+ * Generators (g4_rng.h) are pinned by the CRC-32 of every input the fixtures store.
  */
 #ifndef G4_ORACLE_H
 #define G4_ORACLE_H
