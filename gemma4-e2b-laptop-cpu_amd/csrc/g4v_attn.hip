@@ -20,21 +20,8 @@ constexpr int ATT_THREADS = 256;
 constexpr int ATT_TILE = 32;  // key rows per tile: 8 lanes per row, 32 rows
 constexpr int ATT_HB = 4;     // heads per block
 constexpr int ATT_PMAX = 1040;  // positions per split held in LDS
-
-// E:1325-1326 geometry of a verify pass
-__device__ void geom_from_step(const StepDev* sp, int sliding, int T, AttnGeom& g) {
-  g.M = sp->M;
-  g.T = T;
-  g.kmax = sp->pos0 + sp->M - 1;
-  g.kmin = g.kmax;
-  for (int r = 0; r < sp->M; ++r) {
-    g.pos[r] = sp->pos0 + r;
-    g.lo[r] = sliding ? max(0, sp->rope[r] - 511) : 0;
-    g.skip_lo[r] = sp->skip_lo[r];
-    g.skip_hi[r] = sp->skip_hi[r];
-    g.kmin = min(g.kmin, g.lo[r]);
-  }
-}
+constexpr int ATT_SW = ATT_PMAX + ATT_TILE;  // weight row length: a split plus one zero tile
+constexpr int ATT_KTS = 8 * 40 + 8;          // key tile: halfwords per position
 
 struct AttnPtrs {
   const uint16_t* KC;
@@ -46,6 +33,7 @@ struct AttnPtrs {
   float* pl;  // [T][M][NQ]
   float* out; // [M][ldo]
   int ldo;
+  float* gs;  // not null: out is written in the staged GEMV input layout, group sums here [M][ldo/32]
 };
 
 // 32 key rows x 256 bf16 = 1024 16-byte chunks: 4 per thread
@@ -53,37 +41,84 @@ __device__ __forceinline__ void tile_fetch(const uint16_t* base, int p0, int c1,
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int u = threadIdx.x + k * ATT_THREADS, rr = u >> 5, cc = u & 31, p = p0 + rr;
-    r[k] = p < c1 ? reinterpret_cast<const uint4*>(base + (size_t)p * HD)[cc] : make_uint4(0, 0, 0, 0);
+    r[k] = keep4(p < c1, reinterpret_cast<const uint4*>(base + (size_t)min(p, c1 - 1) * HD)[cc]);
   }
+}
+
+// Key tile fetch for the lane-transposed layout: thread u takes row u/8 and the chunks
+// b, b+2, b+4, b+6 (b = (q&1) + 8(q>>1), q = u%8); chunk c holds elements 8c..8c+7, one per
+// lane l = e%8, at slot (c&1)*16 + c/2 of that lane's 32-value array, so the thread's four
+// chunks land in four consecutive slots of each lane: one 8-byte LDS write per lane.
+__device__ __forceinline__ void ktile_fetch(const uint16_t* base, int p0, int c1, uint4 (&r)[4]) {
+  const int rr = threadIdx.x >> 3, q = threadIdx.x & 7, b = (q & 1) + 8 * (q >> 1), p = p0 + rr;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    r[k] = keep4(p < c1, reinterpret_cast<const uint4*>(base + (size_t)min(p, c1 - 1) * HD)[b + 2 * k]);
 }
 
 // grid (T, M, NQ / ATT_HB)
 template <bool STEP>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom gin, const StepDev* sp, int sliding,
                                                             int T) {
-  __shared__ AttnGeom g;
   __shared__ float qs[ATT_HB][8][32];              // lane l's 32 query values: s0 chain then s1 chain
-  __shared__ __align__(16) uint16_t kt[ATT_TILE][8][40];  // same per-lane order for the keys (80-byte rows)
-  __shared__ uint16_t vt[ATT_TILE][HD];
-  __shared__ float sw[ATT_HB][ATT_PMAX];
+  // key tile in the per-lane order, one 80-byte row per (position, lane) and 16 bytes of
+  // padding per position (spreads the transposing stores of different positions over the banks)
+  __shared__ __align__(16) uint16_t kt[ATT_TILE * ATT_KTS];
+  __shared__ __align__(16) uint16_t vt[ATT_TILE][HD];  // value tile, natural layout
+  __shared__ __align__(16) float sw[ATT_HB][ATT_SW];
   __shared__ float wmax[ATT_THREADS / 64][ATT_HB];
   __shared__ float smax[ATT_HB], ssum[ATT_HB];
   const int t = blockIdx.x, m = blockIdx.y, h0 = blockIdx.z * ATT_HB;
-  if (threadIdx.x == 0) {
-    if (STEP) geom_from_step(sp, sliding, T, g);
-    else g = gin;
+  // E:1325-1326 geometry: every thread reads the (uniform) parameters itself, no serial set-up
+  int M, kmin, kmax, lo_m, pos_m, sl_m, sh_m;
+  if (STEP) {
+    M = sp->M;
+    kmax = sp->pos0 + M - 1;
+    kmin = kmax;
+    for (int r = 0; r < M; ++r) kmin = min(kmin, sliding ? max(0, sp->rope[r] - 511) : 0);
+    pos_m = sp->pos0 + m;
+    lo_m = sliding ? max(0, sp->rope[m] - 511) : 0;
+    sl_m = sp->skip_lo[m];
+    sh_m = sp->skip_hi[m];
+  } else {
+    M = gin.M;
+    kmin = gin.kmin;
+    kmax = gin.kmax;
+    pos_m = gin.pos[m];
+    lo_m = gin.lo[m];
+    sl_m = gin.skip_lo[m];
+    sh_m = gin.skip_hi[m];
   }
-  __syncthreads();
-  if (m >= g.M) return;
-  // E:740 attn_allowed for this block's row, with the row's bounds held in registers
-  const int lo_m = g.lo[m], pos_m = g.pos[m], sl_m = g.skip_lo[m], sh_m = g.skip_hi[m];
+  if (m >= M) return;
+  // E:740 attn_allowed for this block's row
   auto allowed = [=](int p) { return p >= lo_m && p <= pos_m && !(p >= sl_m && p <= sh_m); };
-  const int len = g.kmax - g.kmin + 1;
-  const int c0 = g.kmin + (int)((long)t * len / T), c1 = g.kmin + (int)((long)(t + 1) * len / T);
+  // bit e: position pb + e is inside the split (< c1) and allowed, for a tile of 32 positions
+  auto bits_in = [](int a, int b, int pb) -> uint32_t {  // positions [a, b] within [pb, pb + 31]
+    const int lo = max(a - pb, 0), hi = min(b - pb, 31);
+    if (lo > hi) return 0u;
+    const uint32_t up = hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u);
+    return up & ~((1u << lo) - 1u);
+  };
+  auto tile_mask = [=](int pb, int cend) -> uint32_t {
+    return bits_in(lo_m, min(pos_m, cend - 1), pb) & ~bits_in(sl_m, sh_m, pb);
+  };
+  const int len = kmax - kmin + 1;
+  const int c0 = kmin + (int)((long)t * len / T), c1 = kmin + (int)((long)(t + 1) * len / T);
   const int PP = c1 - c0;
-  for (int idx = threadIdx.x; idx < ATT_HB * HD; idx += ATT_THREADS) {
-    const int hh = idx / HD, e = idx % HD;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
-    qs[hh][e & 7][((e >> 3) & 1) * 16 + (e >> 4)] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
+  // every global load of the prologue in flight at once: the query heads, the first key and
+  // value tiles
+  float qv[ATT_HB];
+#pragma unroll
+  for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + threadIdx.x];
+  uint4 rk[4], rv[4];
+  if (c0 < c1) {
+    ktile_fetch(P.KC, c0, c1, rk);
+    tile_fetch(P.VC, c0, c1, rv);
+  }
+  {
+    const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
+#pragma unroll
+    for (int hh = 0; hh < ATT_HB; ++hh) qs[hh][e & 7][((e >> 3) & 1) * 16 + (e >> 4)] = qv[hh];
   }
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
   float mymax[ATT_HB];
@@ -97,24 +132,29 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     for (int i = 0; i < 32; ++i) qr[hh][i] = qs[hh][l][i];
 
   // sweep 1: scores (E:750-816)
-  uint4 rk[4];
-  if (c0 < c1) tile_fetch(P.KC, c0, c1, rk);
   for (int pb = c0; pb < c1; pb += ATT_TILE) {
     __syncthreads();
+    {  // transpose the thread's 4 chunks (32 keys) into 8 lanes x 4 consecutive slots
+      const int rr = threadIdx.x >> 3, q = threadIdx.x & 7, slot0 = (q & 1) * 16 + 4 * (q >> 1);
+      const uint32_t w[4][4] = {{rk[0].x, rk[0].y, rk[0].z, rk[0].w}, {rk[1].x, rk[1].y, rk[1].z, rk[1].w},
+                                {rk[2].x, rk[2].y, rk[2].z, rk[2].w}, {rk[3].x, rk[3].y, rk[3].z, rk[3].w}};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {  // scatter the chunk's 8 keys into their lanes' arrays
-      const int u = threadIdx.x + k * ATT_THREADS, rr = u >> 5, cc = u & 31;
-      const uint32_t w4[4] = {rk[k].x, rk[k].y, rk[k].z, rk[k].w};
-      const int slot = (cc & 1) * 16 + (cc >> 1);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kt[rr][e][slot] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+      for (int e = 0; e < 8; ++e) {  // element e of each chunk belongs to lane e
+        const int sh = 16 * (e & 1);
+        const uint32_t v0 = (w[0][e >> 1] >> sh) & 0xFFFFu, v1 = (w[1][e >> 1] >> sh) & 0xFFFFu;
+        const uint32_t v2 = (w[2][e >> 1] >> sh) & 0xFFFFu, v3 = (w[3][e >> 1] >> sh) & 0xFFFFu;
+        *reinterpret_cast<uint2*>(&kt[rr * ATT_KTS + e * 40 + slot0]) = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+      }
     }
     __syncthreads();
-    if (pb + ATT_TILE < c1) tile_fetch(P.KC, pb + ATT_TILE, c1, rk);  // next tile in flight
+    if (pb + ATT_TILE < c1) ktile_fetch(P.KC, pb + ATT_TILE, c1, rk);  // next tile in flight
+    // every lane group scores its position (padding rows are zeros); only allowed positions
+    // enter the running max, and masked ones get weight 0 below
     const int p = pb + ps;
-    if (p < c1 && allowed(p)) {
+    const bool okp = (tile_mask(pb, c1) >> ps) & 1u;
+    {
       float kf[32];
-      const uint4* kv4 = reinterpret_cast<const uint4*>(&kt[ps][l][0]);
+      const uint4* kv4 = reinterpret_cast<const uint4*>(&kt[ps * ATT_KTS + l * 40]);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const uint4 u = kv4[c];
@@ -133,14 +173,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
           s0 = fmaf(qr[hh][tt], kf[tt], s0);
           s1 = fmaf(qr[hh][16 + tt], kf[16 + tt], s1);
         }
-        float v = s0 + s1;
-        v = v + __shfl_xor(v, 4, 8);
-        v = v + __shfl_xor(v, 1, 8);
-        v = v + __shfl_xor(v, 2, 8);
-        if (l == 0) {
-          sw[hh][p - c0] = v;
-          mymax[hh] = (mymax[hh] < v) ? v : mymax[hh];
-        }
+        const float v = hsum8_lanes(s0 + s1);
+        if (l == 0) sw[hh][p - c0] = v;
+        mymax[hh] = (okp && mymax[hh] < v) ? v : mymax[hh];
       }
     }
   }
@@ -157,26 +192,32 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     smax[threadIdx.x] = v;
   }
   __syncthreads();
-  // weights exp8(score - max) (E:820)
-  for (int idx = threadIdx.x; idx < ATT_HB * PP; idx += ATT_THREADS) {
-    const int hh = idx / PP, pp = idx % PP;
-    if (allowed(c0 + pp)) sw[hh][pp] = exp8(sw[hh][pp] - smax[hh]);
+  // weights exp8(score - max) (E:820); masked positions and the padding up to the next
+  // whole tile get weight 0
+  const int PPT = (PP + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
+  for (int idx = threadIdx.x; idx < ATT_HB * PPT; idx += ATT_THREADS) {
+    const int hh = idx / PPT, pp = idx % PPT;
+    sw[hh][pp] = (pp < PP && allowed(c0 + pp)) ? exp8(sw[hh][pp] - smax[hh]) : 0.f;
   }
   __syncthreads();
-  if (threadIdx.x < ATT_HB) {  // l = sum of the weights in position order (E:821)
-    const int hh = threadIdx.x;
-    float lsum = 0.f;
-    for (int pp = 0; pp < PP; ++pp)
-      if (allowed(c0 + pp)) lsum = lsum + sw[hh][pp];
-    ssum[hh] = (g.lo[m] > g.pos[m]) ? 0.0f : lsum;
+  if ((threadIdx.x & 63) == 0) {  // l = sum of the weights in position order (E:821), one wave per head
+    const int hh = threadIdx.x >> 6;
+    const float4* w4 = reinterpret_cast<const float4*>(&sw[hh][0]);
+    float lsum = 0.f;  // + 0 for a masked position leaves the (non-negative) sum unchanged
+    for (int q = 0; q < PPT / 4; q += 4) {
+      float4 r[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[k] = keep4(q + k < PPT / 4, w4[min(q + k, PPT / 4 - 1)]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lsum = (((lsum + r[k].x) + r[k].y) + r[k].z) + r[k].w;
+    }
+    ssum[hh] = (lo_m > pos_m) ? 0.0f : lsum;
   }
   // sweep 2: o_i = fma chain over positions (E:826-875), V staged tile by tile
   const int i = threadIdx.x;
   float o[ATT_HB];
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = 0.f;
-  uint4 rv[4];
-  if (c0 < c1) tile_fetch(P.VC, c0, c1, rv);
   for (int pb = c0; pb < c1; pb += ATT_TILE) {
     __syncthreads();
 #pragma unroll
@@ -186,20 +227,33 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     }
     __syncthreads();
     if (pb + ATT_TILE < c1) tile_fetch(P.VC, pb + ATT_TILE, c1, rv);
-    const int nt = min(ATT_TILE, c1 - pb);
-    for (int pp = 0; pp < nt; ++pp) {
-      if (!allowed(pb + pp)) continue;
-      const float vv = bf2f(vt[pp][i]);
+    // Masked and padding positions carry weight 0 and are given value +0 (their bits cleared
+    // with a tile mask): fma(0, 0, o) = o exactly (o is never -0), which is what skipping them
+    // in the reference leaves.  The mask is uniform, so no lane diverges and nothing branches.
+    const uint32_t tmask = tile_mask(pb, c1);
 #pragma unroll
-      for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = fmaf(sw[hh][pb + pp - c0], vv, o[hh]);
+    for (int p4 = 0; p4 < ATT_TILE; p4 += 4) {
+      float4 w4[ATT_HB];
+#pragma unroll
+      for (int hh = 0; hh < ATT_HB; ++hh) w4[hh] = *reinterpret_cast<const float4*>(&sw[hh][pb - c0 + p4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t keep = 0u - ((tmask >> (p4 + e)) & 1u);
+        const float vv = as_f32(((uint32_t)vt[p4 + e][i] << 16) & keep);
+#pragma unroll
+        for (int hh = 0; hh < ATT_HB; ++hh) {
+          const float wgt = e == 0 ? w4[hh].x : (e == 1 ? w4[hh].y : (e == 2 ? w4[hh].z : w4[hh].w));
+          o[hh] = fmaf(wgt, vv, o[hh]);
+        }
+      }
     }
   }
 #pragma unroll
-  for (int hh = 0; hh < ATT_HB; ++hh) P.po[(((size_t)t * g.M + m) * NQ + h0 + hh) * HD + i] = o[hh];
+  for (int hh = 0; hh < ATT_HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];
   __syncthreads();
   if (threadIdx.x < ATT_HB) {
-    P.pm[((size_t)t * g.M + m) * NQ + h0 + threadIdx.x] = smax[threadIdx.x];
-    P.pl[((size_t)t * g.M + m) * NQ + h0 + threadIdx.x] = ssum[threadIdx.x];
+    P.pm[((size_t)t * M + m) * NQ + h0 + threadIdx.x] = smax[threadIdx.x];
+    P.pl[((size_t)t * M + m) * NQ + h0 + threadIdx.x] = ssum[threadIdx.x];
   }
 }
 
@@ -233,7 +287,31 @@ __device__ __forceinline__ void merge_body(const AttnPtrs& P, int M, int T) {
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
     if (t < T && pl[t] > 0) acc = fmaf(po[t], sc[t], acc);
-  P.out[(size_t)m * P.ldo + h * HD + i] = r16(acc * inv);
+  const float y = r16(acc * inv);
+  if (!P.gs) {
+    P.out[(size_t)m * P.ldo + h * HD + i] = y;
+    return;
+  }
+  // the head's 256 outputs are the 8 groups 8h..8h+7 of the o_proj input: staged copy + sums
+  __shared__ __align__(16) float ys[HD];
+  ys[i] = y;
+  __syncthreads();
+  float* xs = P.out + (size_t)m * P.ldo + h * HD;
+  if (i < HD / 4) {
+    const float* b = ys + (i >> 3) * 32;
+    const int j = i & 7;
+    reinterpret_cast<float4*>(xs)[i] = make_float4(b[2 * j], b[16 + 2 * j], b[2 * j + 1], b[17 + 2 * j]);
+  }
+  if (i < HD / 32) {
+    const float4* b4 = reinterpret_cast<const float4*>(ys + i * 32);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 r = b4[k];
+      s = (((s + r.x) + r.y) + r.z) + r.w;
+    }
+    P.gs[(size_t)m * (P.ldo / 32) + h * (HD / 32) + i] = s;
+  }
 }
 
 __global__ __launch_bounds__(HD) void k_attn_merge(AttnPtrs P, int M, int T) { merge_body(P, M, T); }
@@ -244,9 +322,9 @@ __global__ __launch_bounds__(HD) void k_attn_merge_step(AttnPtrs P, const StepDe
 }
 
 void launch_attn(const uint16_t* KC, const uint16_t* VC, const float* q, const StepDev* sp, int sliding, int T,
-                 int ctxcap, float* po, float* pm, float* pl, float* att, int M, hipStream_t st) {
+                 int ctxcap, float* po, float* pm, float* pl, float* att, float* attgs, int M, hipStream_t st) {
   (void)ctxcap;
-  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, att, NQ * HD};
+  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, att, NQ * HD, attgs};
   AttnGeom g{};
   hipLaunchKernelGGL(k_attn_split<true>, dim3(T, M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, sp, sliding, T);
   hipLaunchKernelGGL(k_attn_merge_step, dim3(M, NQ), dim3(HD), 0, st, P, sp, T);
@@ -254,7 +332,7 @@ void launch_attn(const uint16_t* KC, const uint16_t* VC, const float* q, const S
 
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st) {
-  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo};
+  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr};
   hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
                      (const StepDev*)nullptr, 0, g.T);
   hipLaunchKernelGGL(k_attn_merge, dim3(g.M, NQ), dim3(HD), 0, st, P, g.M, g.T);

@@ -81,7 +81,9 @@ struct g4v_ctx {
   std::vector<std::unique_ptr<Layer>> L;
   DBuf fnorm, KC, VC, rope;  // rope: [2][ctxcap][HD/2] cos then sin
   // step buffers
-  DBuf x, xa, q, k, v, att, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
+  // xa, att and act hold GEMV inputs in the staged layout (staged_index), xgs / attgs their
+  // group sums
+  DBuf x, xa, xgs, q, k, v, att, attgs, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
   StepDev* step_host = nullptr;
   VerifyResultDev* res_host = nullptr;
   // attention standalone
@@ -629,6 +631,8 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   HIPCHK(hipMemcpyAsync(c->rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, st));
   ALLOC(c->x, MAXM * H * 4);
   ALLOC(c->xa, MAXM * H * 4);
+  ALLOC(c->xgs, MAXM * (H / 32) * 4);
+  ALLOC(c->attgs, MAXM * (NQ * HD / 32) * 4);
   ALLOC(c->q, MAXM * NQ * HD * 4);
   ALLOC(c->k, MAXM * HD * 4);
   ALLOC(c->v, MAXM * HD * 4);
@@ -911,7 +915,8 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
   const StepDev& sh = *c->step_host;
   const float sqh = std::sqrt((float)H);
   pmark(c, PT_ROWS, 1, 0);
-  launch_embed(c->E.as<uint16_t>(), sp, c->L[0]->ln().in_ln, sqh, c->x.as<float>(), c->xa.as<float>(), M, st);
+  launch_embed(c->E.as<uint16_t>(), sp, c->L[0]->ln().in_ln, sqh, c->x.as<float>(), c->xa.as<float>(),
+               c->xgs.as<float>(), M, st);
   pmark(c, PT_ROWS, 0, (double)M * H * 2);
   const float* rope = c->rope.as<float>();
   for (int l = 0; l < NL; ++l) {
@@ -928,8 +933,8 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     a.ldy[1] = HD;
     a.y[2] = c->v.as<float>();
     a.ldy[2] = HD;
-    a.x = c->xa.as<float>();
-    a.ldx = H;
+    a.xs = c->xa.as<float4>();
+    a.gs = c->xgs.as<float>();
     a.K = H;
     a.M = M;
     pmark(c, PT_GEMV_QKV, 1, 0);
@@ -945,32 +950,40 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     for (int r = 0; r < M; ++r) kmin = std::min(kmin, A.sliding ? std::max(0, sh.rope[r] - 511) : 0);
     pmark(c, PT_ATTN, 1, 0);
     launch_attn(KCl, VCl, c->q.as<float>(), sp, A.sliding, T, c->ctxcap, c->po.as<float>(), c->pm.as<float>(),
-                c->pl.as<float>(), c->att.as<float>(), M, st);
+                c->pl.as<float>(), c->att.as<float>(), c->attgs.as<float>(), M, st);
     pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
     pmark(c, PT_GEMV_O, 1, 0);
-    gemv_passes(c, plain_args(A.m[3], c->att.as<float>(), c->o.as<float>(), M), EPI_STORE, M);  // E:1356
+    GemvArgs ao = plain_args(A.m[3], nullptr, c->o.as<float>(), M);  // E:1356
+    ao.xs = c->att.as<float4>();
+    ao.gs = c->attgs.as<float>();
+    gemv_passes(c, ao, EPI_STORE, M);
     pmark(c, PT_GEMV_O, 0, w4_bytes(A.m[3]));
     pmark(c, PT_ROWS, 1, 0);
-    launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), ln, M, st);
+    launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, M, st);
     pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
     GemvArgs gu{};  // E:1366 gate/up + gelu
     gu.mat[0] = A.m[4].dev();
     gu.mat[1] = A.m[5].dev();
     gu.y[0] = c->act.as<float>();
     gu.ldy[0] = I;
-    gu.x = c->xa.as<float>();
-    gu.ldx = H;
+    gu.y_staged = 1;
+    gu.xs = c->xa.as<float4>();
+    gu.gs = c->xgs.as<float>();
     gu.K = H;
     gu.M = M;
     pmark(c, PT_GEMV_GATEUP, 1, 0);
     gemv_passes(c, gu, EPI_GATEUP, M);
     pmark(c, PT_GEMV_GATEUP, 0, w4_bytes(A.m[4]) + w4_bytes(A.m[5]));
     pmark(c, PT_GEMV_DOWN, 1, 0);
-    gemv_passes(c, plain_args(A.m[6], c->act.as<float>(), c->o.as<float>(), M), EPI_STORE, M);  // E:1373
+    GemvArgs ad = plain_args(A.m[6], nullptr, c->o.as<float>(), M);  // E:1373
+    ad.xs = c->act.as<float4>();  // group sums formed in LDS from the staged copy
+    ad.lds_budget = c->lds_max;   // 192 blocks, one per CU: stage K in two halves
+    gemv_passes(c, ad, EPI_STORE, M);
     pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
     const float* next = l + 1 < NL ? c->L[l + 1]->ln().in_ln : nullptr;
     pmark(c, PT_ROWS, 1, 0);
-    launch_post_ff(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), ln, next, c->fnorm.as<float>(),
+    launch_post_ff(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, next,
+                   c->fnorm.as<float>(),
                    c->h.as<float>(), c->hn.as<float>(), M, st);
     pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
   }

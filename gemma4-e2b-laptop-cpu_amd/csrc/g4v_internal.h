@@ -27,15 +27,29 @@ struct W4Dev {
 // Where the GEMV epilogue sends the result.
 enum GemvEpi { EPI_STORE = 0, EPI_GATEUP = 1, EPI_SCREEN = 2 };
 
+// Staged activation layout of a K-vector.  Lane j (0..7) of a W4G32 chain multiplies, in
+// group g, the four values x[32g+2j], x[32g+16+2j], x[32g+2j+1], x[32g+17+2j]; the staged
+// row stores them as one float4 at float4 index 8g + j, so a GEMV stages its activations with
+// straight 16-byte copies.  Rows of M vectors follow each other (K floats per row).  The
+// per-group sums (sequential fp32 sum of x[32g..32g+31], W:22) travel beside it as [M][K/32].
+__host__ __device__ __forceinline__ int staged_index(int n) {
+  const int g = n >> 5, i = n & 31, e = i & 15;
+  return (g * 8 + (e >> 1)) * 4 + ((e & 1) ? 2 : 0) + (i >> 4);
+}
+
 struct GemvArgs {
   W4Dev mat[3];       // up to three matrices with the same K, processed in one launch
   float* y[3];        // outputs [M][ldy]
   int ldy[3];
   int tiles[4];       // prefix sum of 32-row tiles per matrix
-  const float* x;     // activations [M][ldx]
+  const float* x;     // activations [M][ldx] (plain layout), or
+  const float4* xs;   // activations [M][K/4] in the staged layout (used when not null)
+  const float* gs;    // their group sums [M][K/32] (computed in LDS when null)
   int ldx;
   int K;
   int kphase;         // K elements staged in LDS at a time (set by launch_gemv)
+  int lds_budget;     // LDS bytes a block may stage (0: 64 KB)
+  int y_staged;       // EPI_GATEUP: write the activation in the staged layout (ldy = row length)
   int M;              // runtime rows (<= template MT); rows >= M are not computed
   // EPI_SCREEN
   const float* coef;  // [N]

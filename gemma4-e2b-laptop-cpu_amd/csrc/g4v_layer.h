@@ -38,14 +38,16 @@ struct LayerNorms {
   int sliding;
 };
 
-void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, int M,
-                  hipStream_t st);
+// xa / att / act below are written in the staged GEMV input layout (staged_index) with their
+// group sums (xgs, attgs)
+void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, float* xgs,
+                  int M, hipStream_t st);
 void launch_qk_rope(float* q, const float* k, const float* v, int ldqkv_q, const StepDev* sp, const LayerNorms& ln,
                     const float* cs, const float* sn, uint16_t* KC, uint16_t* VC, int M, hipStream_t st);
 void launch_attn(const uint16_t* KC, const uint16_t* VC, const float* q, const StepDev* sp, int sliding, int T,
-                 int ctxcap, float* po, float* pm, float* pl, float* att, int M, hipStream_t st);
-void launch_post_attn(const float* o, float* x, float* xa, const LayerNorms& ln, int M, hipStream_t st);
-void launch_post_ff(const float* o, float* x, float* xa, const LayerNorms& ln, const float* next_in_ln,
+                 int ctxcap, float* po, float* pm, float* pl, float* att, float* attgs, int M, hipStream_t st);
+void launch_post_attn(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, int M, hipStream_t st);
+void launch_post_ff(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, const float* next_in_ln,
                     const float* fnorm, float* h, float* hn, int M, hipStream_t st);
 void launch_branch(const StepDev* sp, const int* best1, const float* h, const float* hn, float* h2, float* hn2,
                    VerifyResultDev* res, hipStream_t st);

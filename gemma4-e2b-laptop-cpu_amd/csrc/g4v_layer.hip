@@ -34,11 +34,35 @@ __device__ __forceinline__ float rms_inv(double ss, int n) { return 1.0f / sqrtf
 
 constexpr int ROW_THREADS = 256;
 
-// E:1262-1267: x = rbf8(E[tok] * sqrt(H)); xa = (x * r) * in_ln
+// Write a K-vector held in LDS (v, 16-byte aligned) as one row of the staged GEMV input
+// layout (staged_index) plus its group sums, each the sequential fp32 sum of the group's 32
+// values (W:22), so the consuming GEMV stages it with plain 16-byte copies.
+__device__ void write_staged(const float* v, int K, float* xs, float* gs) {
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  for (int idx = threadIdx.x; idx < K / 4; idx += blockDim.x) {
+    const float* b = v + (idx >> 3) * 32;
+    const int j = idx & 7;
+    xs4[idx] = make_float4(b[2 * j], b[16 + 2 * j], b[2 * j + 1], b[17 + 2 * j]);
+  }
+  for (int g = threadIdx.x; g < K / 32; g += blockDim.x) {
+    const float4* b4 = reinterpret_cast<const float4*>(v + g * 32);
+    float4 r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = b4[i];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = (((s + r[i].x) + r[i].y) + r[i].z) + r[i].w;
+    gs[g] = s;
+  }
+}
+
+// E:1262-1267: x = rbf8(E[tok] * sqrt(H)); xa = (x * r) * in_ln, xa written staged (+ sums)
 __global__ __launch_bounds__(ROW_THREADS) void k_embed(const uint16_t* __restrict__ E, const StepDev* sp,
                                                        const float* __restrict__ in_ln, float sqh,
-                                                       float* __restrict__ x, float* __restrict__ xa) {
-  __shared__ float xs[H];
+                                                       float* __restrict__ x, float* __restrict__ xa,
+                                                       float* __restrict__ xgs) {
+  __shared__ __align__(16) float xs[H];
+  __shared__ __align__(16) float ys[H];
   __shared__ double red[16];
   const int m = blockIdx.x;
   const int tok = sp->toks[m];
@@ -49,46 +73,84 @@ __global__ __launch_bounds__(ROW_THREADS) void k_embed(const uint16_t* __restric
   }
   __syncthreads();
   const float r = rms_inv(block_sumsq(xs, H, red), H);
-  for (int i = threadIdx.x; i < H; i += ROW_THREADS) xa[(size_t)m * H + i] = (xs[i] * r) * in_ln[i];
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) ys[i] = (xs[i] * r) * in_ln[i];
+  __syncthreads();
+  write_staged(ys, H, xa + (size_t)m * H, xgs + (size_t)m * (H / 32));
 }
 
-// E:1358-1361: o = r16(o); tmp = rms(o, post_attn); x = r16(x + r16(tmp)); xa = r16(rms(x, pre_ff))
+// E:1358-1361: o = r16(o); tmp = rms(o, post_attn); x = r16(x + r16(tmp)); xa = r16(rms(x, pre_ff)).
+// Every global input of the row is loaded up front (one round trip), xa is written staged.
+constexpr int RPT = H / ROW_THREADS;  // elements of a row per thread
 __global__ __launch_bounds__(ROW_THREADS) void k_post_attn(const float* __restrict__ o, float* __restrict__ x,
-                                                           float* __restrict__ xa, LayerNorms ln) {
-  __shared__ float os[H], xs[H];
+                                                           float* __restrict__ xa, float* __restrict__ xgs,
+                                                           LayerNorms ln) {
+  __shared__ __align__(16) float os[H];
+  __shared__ __align__(16) float xs[H];
   __shared__ double red[16];
   const int m = blockIdx.x;
-  for (int i = threadIdx.x; i < H; i += ROW_THREADS) os[i] = r16(o[(size_t)m * H + i]);
+  float ov[RPT], xv[RPT], w1[RPT], w2[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = threadIdx.x + k * ROW_THREADS;
+    ov[k] = o[(size_t)m * H + i];
+    xv[k] = x[(size_t)m * H + i];
+    w1[k] = ln.post_attn[i];
+    w2[k] = ln.pre_ff[i];
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) os[threadIdx.x + k * ROW_THREADS] = r16(ov[k]);
   __syncthreads();
   const float r1 = rms_inv(block_sumsq(os, H, red), H);
-  for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
-    const float tmp = (os[i] * r1) * ln.post_attn[i];
-    const float v = r16(x[(size_t)m * H + i] + r16(tmp));
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = threadIdx.x + k * ROW_THREADS;
+    const float tmp = (os[i] * r1) * w1[k];
+    const float v = r16(xv[k] + r16(tmp));
     xs[i] = v;
     x[(size_t)m * H + i] = v;
   }
   __syncthreads();
   const float r2 = rms_inv(block_sumsq(xs, H, red), H);
-  for (int i = threadIdx.x; i < H; i += ROW_THREADS) xa[(size_t)m * H + i] = r16((xs[i] * r2) * ln.pre_ff[i]);
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = threadIdx.x + k * ROW_THREADS;
+    os[i] = r16((xs[i] * r2) * w2[k]);
+  }
+  __syncthreads();
+  write_staged(os, H, xa + (size_t)m * H, xgs + (size_t)m * (H / 32));
 }
 
 // E:1375-1378 and E:1390-1404 with a zero per-layer-embedding branch:
 // o = r16(o); tmp = rms(o, post_ff); x = r16(x + r16(tmp)); x = r16(x * scalar);
-// then xa = rms(x, next in_ln) or, after the last layer, h = r16(rms(x, fnorm)), hn = |h|.
+// then xa = rms(x, next in_ln) (staged) or, after the last layer, h = r16(rms(x, fnorm)), hn = |h|.
 __global__ __launch_bounds__(ROW_THREADS) void k_post_ff(const float* __restrict__ o, float* __restrict__ x,
-                                                         float* __restrict__ xa, LayerNorms ln,
-                                                         const float* __restrict__ next_in_ln,
+                                                         float* __restrict__ xa, float* __restrict__ xgs,
+                                                         LayerNorms ln, const float* __restrict__ next_in_ln,
                                                          const float* __restrict__ fnorm, float* __restrict__ h,
                                                          float* __restrict__ hn) {
-  __shared__ float os[H], xs[H];
+  __shared__ __align__(16) float os[H];
+  __shared__ __align__(16) float xs[H];
   __shared__ double red[16];
   const int m = blockIdx.x;
-  for (int i = threadIdx.x; i < H; i += ROW_THREADS) os[i] = r16(o[(size_t)m * H + i]);
+  const float* w2p = next_in_ln ? next_in_ln : fnorm;
+  float ov[RPT], xv[RPT], w1[RPT], w2[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = threadIdx.x + k * ROW_THREADS;
+    ov[k] = o[(size_t)m * H + i];
+    xv[k] = x[(size_t)m * H + i];
+    w1[k] = ln.post_ff[i];
+    w2[k] = w2p[i];
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) os[threadIdx.x + k * ROW_THREADS] = r16(ov[k]);
   __syncthreads();
   const float r1 = rms_inv(block_sumsq(os, H, red), H);
-  for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
-    const float tmp = (os[i] * r1) * ln.post_ff[i];
-    float v = r16(x[(size_t)m * H + i] + r16(tmp));
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = threadIdx.x + k * ROW_THREADS;
+    const float tmp = (os[i] * r1) * w1[k];
+    float v = r16(xv[k] + r16(tmp));
     v = r16(v * ln.scalar);
     xs[i] = v;
     x[(size_t)m * H + i] = v;
@@ -96,10 +158,18 @@ __global__ __launch_bounds__(ROW_THREADS) void k_post_ff(const float* __restrict
   __syncthreads();
   const float r2 = rms_inv(block_sumsq(xs, H, red), H);
   if (next_in_ln) {
-    for (int i = threadIdx.x; i < H; i += ROW_THREADS) xa[(size_t)m * H + i] = (xs[i] * r2) * next_in_ln[i];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = threadIdx.x + k * ROW_THREADS;
+      os[i] = (xs[i] * r2) * w2[k];
+    }
+    __syncthreads();
+    write_staged(os, H, xa + (size_t)m * H, xgs + (size_t)m * (H / 32));
   } else {
-    for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
-      const float v = r16((xs[i] * r2) * fnorm[i]);
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = threadIdx.x + k * ROW_THREADS;
+      const float v = r16((xs[i] * r2) * w2[k]);
       os[i] = v;
       h[(size_t)m * H + i] = v;
     }
@@ -239,20 +309,20 @@ __global__ void k_gen_w4(uint8_t* w, uint16_t* s, size_t nb, size_t ns, uint64_t
 // ---------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------
-void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, int M,
-                  hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, sp, in_ln, sqh, x, xa);
+void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, float* xgs,
+                  int M, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, sp, in_ln, sqh, x, xa, xgs);
 }
 void launch_qk_rope(float* q, const float* k, const float* v, int ldq, const StepDev* sp, const LayerNorms& ln,
                     const float* cs, const float* sn, uint16_t* KC, uint16_t* VC, int M, hipStream_t st) {
   hipLaunchKernelGGL(k_qk_rope, dim3(M, NQ + 1), dim3(HD), 0, st, q, k, v, ldq, sp, ln, cs, sn, KC, VC);
 }
-void launch_post_attn(const float* o, float* x, float* xa, const LayerNorms& ln, int M, hipStream_t st) {
-  hipLaunchKernelGGL(k_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, xa, ln);
+void launch_post_attn(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, int M, hipStream_t st) {
+  hipLaunchKernelGGL(k_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, xa, xgs, ln);
 }
-void launch_post_ff(const float* o, float* x, float* xa, const LayerNorms& ln, const float* next_in_ln,
+void launch_post_ff(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, const float* next_in_ln,
                     const float* fnorm, float* h, float* hn, int M, hipStream_t st) {
-  hipLaunchKernelGGL(k_post_ff, dim3(M), dim3(ROW_THREADS), 0, st, o, x, xa, ln, next_in_ln, fnorm, h, hn);
+  hipLaunchKernelGGL(k_post_ff, dim3(M), dim3(ROW_THREADS), 0, st, o, x, xa, xgs, ln, next_in_ln, fnorm, h, hn);
 }
 void launch_branch(const StepDev* sp, const int* best1, const float* h, const float* hn, float* h2, float* hn2,
                    VerifyResultDev* res, hipStream_t st) {

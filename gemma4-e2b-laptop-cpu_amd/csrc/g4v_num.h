@@ -19,6 +19,16 @@ G4V_HD uint32_t as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
 G4V_HD double as_f64(uint64_t u) { return __builtin_bit_cast(double, u); }
 G4V_HD uint64_t as_u64(double d) { return __builtin_bit_cast(uint64_t, d); }
 
+// Component-wise selects of 16-byte vectors.  A conditional expression on the vector types
+// themselves is lowered through private memory by this compiler; per-lane component selects
+// stay in registers.
+G4V_HD float4 keep4(bool ok, float4 v) {
+  return make_float4(ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f);
+}
+G4V_HD uint4 keep4(bool ok, uint4 v) {
+  return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
+}
+
 // W:15 bf16 -> fp32 widening
 G4V_HD float bf2f(uint16_t b) { return as_f32((uint32_t)b << 16); }
 
@@ -68,6 +78,34 @@ G4V_HD float gelu8(float x) {
 G4V_HD float hsum8(const float* r) {
   float a0 = r[0] + r[4], a1 = r[1] + r[5], a2 = r[2] + r[6], a3 = r[3] + r[7];
   return (a0 + a1) + (a2 + a3);
+}
+
+// The same sum over the 8 consecutive lanes of a wavefront that each hold one r[j] (lane j of
+// the group): a_j = r_j + r_{j^4}, then + lane j^1, then + lane j^2, every lane ending with
+// ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)).  Data-parallel primitive moves (within rows of 16
+// lanes) replace the LDS permute a generic shuffle would use.  (The host pass parses but never
+// runs these.)
+__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int x = __builtin_bit_cast(int, v);
+  int y;
+  switch (ctrl_sel) {  // constant after inlining
+    case 0: y = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false); break;  // row_shl:4
+    case 1: y = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false); break;  // row_shr:4
+    case 2: y = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+    default: y = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;  // quad_perm 2,3,0,1
+  }
+  return __builtin_bit_cast(float, y);
+#else
+  (void)ctrl_sel;
+  return v;
+#endif
+}
+__device__ __forceinline__ float hsum8_lanes(float v) {
+  const float up = dpp_f(v, 0), dn = dpp_f(v, 1);
+  v = v + ((threadIdx.x & 4) ? dn : up);
+  v = v + dpp_f(v, 2);
+  return v + dpp_f(v, 3);
 }
 
 // libm expf as the reference's host links it (glibc 2.35, FMA code path), used by the split
