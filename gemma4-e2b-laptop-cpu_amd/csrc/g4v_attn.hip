@@ -7,9 +7,9 @@
 //   w_p = exp8(score_p - max), l = sum of w_p in position order, o_i = fma chain over p;
 //   merge: sc_t = libm expf(max_t - M0), l = sum_t (double) l_t sc_t,
 //          out = r16((fma chain over splits of o_t sc_t) * (float)(1 / l)).
-// One block serves (split t, row m, 4 heads): the block's K/V rows are staged through LDS
+// One block serves (split t, row m, ATT_HB heads): the block's K/V rows are staged through LDS
 // tile by tile (the next tile is fetched into registers while the current one is used) and
-// shared by the 4 heads.
+// shared by the block's heads.
 #include "g4v_layer.h"
 
 namespace g4v {
@@ -18,7 +18,7 @@ __constant__ uint64_t c_expf_tab[32] = G4V_EXPF_TABLE;
 
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_TILE = 32;  // key rows per tile: 8 lanes per row, 32 rows
-constexpr int ATT_HB = 4;     // heads per block
+constexpr int ATT_HB = 2;     // heads per block (224 blocks for a 7-row pass: every CU busy)
 constexpr int ATT_PMAX = 1040;  // positions per split held in LDS
 constexpr int ATT_SW = ATT_PMAX + ATT_TILE;  // weight row length: a split plus one zero tile
 constexpr int ATT_KTS = 8 * 40 + 8;          // key tile: halfwords per position
@@ -34,7 +34,26 @@ struct AttnPtrs {
   float* out; // [M][ldo]
   int ldo;
   float* gs;  // not null: out is written in the staged GEMV input layout, group sums here [M][ldo/32]
+  // verify pass (fused E:1307-1324): q, k, v straight from the projection, normalised and
+  // rotated here; the pass's own key/value rows are formed in LDS and written to the cache
+  const float* kraw;  // [M][HD]
+  const float* vraw;  // [M][HD]
+  const float* ropestep;  // the step's RoPE factors of the layer type: [MAXM][cos | sin][HD/2]
+  const float* qn;    // q_norm / k_norm weights [HD]
+  const float* kn;
+  uint16_t* KCw;      // the layer's cache (same as KC / VC), written for the pass's rows
+  uint16_t* VCw;
 };
+
+// E:326-345 sum of squares of a 256-vector, 16 lanes x 16 steps in double, combined in the
+// reference's order; part[t] = lane t's sum (t < 16).  Returns 1 / sqrtf((float)(ss / n) + 1e-6).
+__device__ __forceinline__ float rms_inv16(const double* part) {
+  double a[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) a[l] = (part[l] + part[4 + l]) + (part[8 + l] + part[12 + l]);
+  const double ss = (a[0] + a[2]) + (a[1] + a[3]);
+  return 1.0f / sqrtf((float)(ss / HD) + 1e-6f);  // division by a power of two: exact scaling
+}
 
 // 32 key rows x 256 bf16 = 1024 16-byte chunks: 4 per thread
 __device__ __forceinline__ void tile_fetch(const uint16_t* base, int p0, int c1, uint4 (&r)[4]) {
@@ -68,6 +87,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   __shared__ __align__(16) float sw[ATT_HB][ATT_SW];
   __shared__ float wmax[ATT_THREADS / 64][ATT_HB];
   __shared__ float smax[ATT_HB], ssum[ATT_HB];
+  // verify pass: rows being normalised (4 query heads, then the pass's k and v rows), their
+  // 16-lane partial sums of squares, and the pass's finished key / value rows (bf16)
+  __shared__ float nx[STEP ? ATT_HB + 2 * MAXM : 1][HD];
+  __shared__ double npart[STEP ? ATT_HB + 2 * MAXM : 1][16];
+  __shared__ float nrinv[STEP ? ATT_HB + 2 * MAXM : 1];
+  __shared__ __align__(16) uint16_t knew[STEP ? MAXM : 1][HD];
+  __shared__ __align__(16) uint16_t vnew[STEP ? MAXM : 1][HD];
   const int t = blockIdx.x, m = blockIdx.y, h0 = blockIdx.z * ATT_HB;
   // E:1325-1326 geometry: every thread reads the (uniform) parameters itself, no serial set-up
   int M, kmin, kmax, lo_m, pos_m, sl_m, sh_m;
@@ -106,20 +132,94 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   const int c0 = kmin + (int)((long)t * len / T), c1 = kmin + (int)((long)(t + 1) * len / T);
   const int PP = c1 - c0;
   // every global load of the prologue in flight at once: the query heads, the first key and
-  // value tiles
+  // value tiles and, in a verify pass, the raw rows of the pass that fall in this split
+  const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
   float qv[ATT_HB];
 #pragma unroll
-  for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + threadIdx.x];
+  for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
   uint4 rk[4], rv[4];
   if (c0 < c1) {
     ktile_fetch(P.KC, c0, c1, rk);
     tile_fetch(P.VC, c0, c1, rv);
   }
-  {
-    const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
+  // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1)
+  const int pos0 = STEP ? sp->pos0 : 0;
+  const int rn0 = STEP ? max(c0 - pos0, 0) : 0, rn1 = STEP ? min(c1 - pos0, M) : 0;
+  if (STEP) {
+    // E:1307-1324 on the block's query heads and the pass's key/value rows of this split:
+    // x = r16((x * rms_inv) * w) (v: r16(x * rms_inv)), then NeoX rotation of q and k.  The
+    // raw rows, the norm weights and this thread's RoPE factors are all loaded up front.
+    const int i2 = e & (HD / 2 - 1);
+    float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {};
+    if (rn0 < rn1)  // only the splits holding rows of the pass
 #pragma unroll
-    for (int hh = 0; hh < ATT_HB; ++hh) qs[hh][e & 7][((e >> 3) & 1) * 16 + (e >> 4)] = qv[hh];
+    for (int r = 0; r < MAXM; ++r) {
+      const int rr = (r >= rn0 && r < rn1) ? r : rn0;
+      kv[0][r] = P.kraw[(size_t)rr * HD + e];
+      kv[1][r] = P.vraw[(size_t)rr * HD + e];
+      ck[r] = P.ropestep[(size_t)rr * HD + i2];
+      sk[r] = P.ropestep[(size_t)rr * HD + HD / 2 + i2];
+    }
+    const float qw = P.qn[e], kw = P.kn[e];
+    const float cq = P.ropestep[(size_t)m * HD + i2], sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
+#pragma unroll
+    for (int hh = 0; hh < ATT_HB; ++hh) nx[hh][e] = qv[hh];
+#pragma unroll
+    for (int r = 0; r < MAXM; ++r) {
+      nx[ATT_HB + r][e] = kv[0][r];
+      nx[ATT_HB + MAXM + r][e] = kv[1][r];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < (ATT_HB + 2 * MAXM) * 16; idx += ATT_THREADS) {
+      const int row = idx >> 4, t16 = idx & 15;
+      const bool live = row < ATT_HB || ((row - ATT_HB) % MAXM >= rn0 && (row - ATT_HB) % MAXM < rn1);
+      double sacc = 0;
+      if (live) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const double d = (double)nx[row][16 * k + t16];
+          sacc = fma(d, d, sacc);
+        }
+      }
+      npart[row][t16] = sacc;
+    }
+    __syncthreads();
+    if (threadIdx.x < ATT_HB + 2 * MAXM) nrinv[threadIdx.x] = rms_inv16(npart[threadIdx.x]);  // once per row
+    __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < ATT_HB; ++hh) nx[hh][e] = r16((qv[hh] * nrinv[hh]) * qw);
+#pragma unroll
+    for (int r = 0; r < MAXM; ++r)
+      if (r >= rn0 && r < rn1) {  // uniform
+        nx[ATT_HB + r][e] = r16((kv[0][r] * nrinv[ATT_HB + r]) * kw);
+        vnew[r][e] = f2bf(r16(kv[1][r] * nrinv[ATT_HB + MAXM + r]));
+      }
+    __syncthreads();
+    // E:394-402 NeoX halves: out_i = fma(u, c, -(w s)) and out_{i+128} = fma(w, c, u s)
+    auto rot = [&](const float* y, float c, float sn) {
+      return e < HD / 2 ? fmaf(y[e], c, -(y[e + HD / 2] * sn)) : fmaf(y[e], c, y[e - HD / 2] * sn);
+    };
+#pragma unroll
+    for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = rot(nx[hh], cq, sq);
+#pragma unroll
+    for (int r = 0; r < MAXM; ++r)
+      if (r >= rn0 && r < rn1) knew[r][e] = f2bf(rot(nx[ATT_HB + r], ck[r], sk[r]));
+    __syncthreads();
+    if (m == 0 && h0 == 0)  // one block per split writes the pass's rows that fall in it
+      for (int r = rn0; r < rn1; ++r) {
+        P.KCw[(size_t)(pos0 + r) * HD + e] = knew[r][e];
+        P.VCw[(size_t)(pos0 + r) * HD + e] = vnew[r][e];
+      }
   }
+  // a tile row at a position of the pass takes its key / value from LDS
+  auto patch = [&](const uint16_t (*src)[HD], int p, int chunk, uint4 v) {
+    if (!STEP) return v;
+    const bool own = p >= pos0 && p < c1;
+    const uint4 n = *reinterpret_cast<const uint4*>(&src[min(max(p - pos0, 0), MAXM - 1)][chunk * 8]);
+    return sel4(own, n, v);
+  };
+#pragma unroll
+  for (int hh = 0; hh < ATT_HB; ++hh) qs[hh][e & 7][((e >> 3) & 1) * 16 + (e >> 4)] = qv[hh];
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
   float mymax[ATT_HB];
 #pragma unroll
@@ -136,6 +236,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     __syncthreads();
     {  // transpose the thread's 4 chunks (32 keys) into 8 lanes x 4 consecutive slots
       const int rr = threadIdx.x >> 3, q = threadIdx.x & 7, slot0 = (q & 1) * 16 + 4 * (q >> 1);
+      const int b = (q & 1) + 8 * (q >> 1);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) rk[k] = patch(knew, pb + rr, b + 2 * k, rk[k]);
       const uint32_t w[4][4] = {{rk[0].x, rk[0].y, rk[0].z, rk[0].w}, {rk[1].x, rk[1].y, rk[1].z, rk[1].w},
                                 {rk[2].x, rk[2].y, rk[2].z, rk[2].w}, {rk[3].x, rk[3].y, rk[3].z, rk[3].w}};
 #pragma unroll
@@ -200,8 +303,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     sw[hh][pp] = (pp < PP && allowed(c0 + pp)) ? exp8(sw[hh][pp] - smax[hh]) : 0.f;
   }
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) {  // l = sum of the weights in position order (E:821), one wave per head
-    const int hh = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0 && (threadIdx.x >> 6) < ATT_HB) {  // l = sum of the weights in position
+    const int hh = threadIdx.x >> 6;                               // order (E:821), one wave per head
     const float4* w4 = reinterpret_cast<const float4*>(&sw[hh][0]);
     float lsum = 0.f;  // + 0 for a masked position leaves the (non-negative) sum unchanged
     for (int q = 0; q < PPT / 4; q += 4) {
@@ -223,7 +326,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int u = threadIdx.x + k * ATT_THREADS, rr = u >> 5, cc = u & 31;
-      *reinterpret_cast<uint4*>(&vt[rr][cc * 8]) = rv[k];
+      *reinterpret_cast<uint4*>(&vt[rr][cc * 8]) = patch(vnew, pb + rr, cc, rv[k]);
     }
     __syncthreads();
     if (pb + ATT_TILE < c1) tile_fetch(P.VC, pb + ATT_TILE, c1, rv);
@@ -321,10 +424,10 @@ __global__ __launch_bounds__(HD) void k_attn_merge_step(AttnPtrs P, const StepDe
   merge_body(P, sp->M, T);
 }
 
-void launch_attn(const uint16_t* KC, const uint16_t* VC, const float* q, const StepDev* sp, int sliding, int T,
-                 int ctxcap, float* po, float* pm, float* pl, float* att, float* attgs, int M, hipStream_t st) {
-  (void)ctxcap;
-  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, att, NQ * HD, attgs};
+void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, const float* v, const LayerNorms& ln,
+                 const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl,
+                 float* att, float* attgs, int M, hipStream_t st) {
+  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, att, NQ * HD, attgs, k, v, ropestep, ln.qn, ln.kn, KC, VC};
   AttnGeom g{};
   hipLaunchKernelGGL(k_attn_split<true>, dim3(T, M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, sp, sliding, T);
   hipLaunchKernelGGL(k_attn_merge_step, dim3(M, NQ), dim3(HD), 0, st, P, sp, T);
@@ -332,7 +435,8 @@ void launch_attn(const uint16_t* KC, const uint16_t* VC, const float* q, const S
 
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st) {
-  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr};
+  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+             nullptr};
   hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
                      (const StepDev*)nullptr, 0, g.T);
   hipLaunchKernelGGL(k_attn_merge, dim3(g.M, NQ), dim3(HD), 0, st, P, g.M, g.T);

@@ -79,7 +79,8 @@ struct g4v_ctx {
   bool model_ready = false;  // buffers allocated (model_synth or model_create)
   int NL = 0, I = 0, ctxcap = 0;
   std::vector<std::unique_ptr<Layer>> L;
-  DBuf fnorm, KC, VC, rope;  // rope: [2][ctxcap][HD/2] cos then sin
+  DBuf fnorm, KC, VC, rope;  // rope: [2 types][cos, sin][ctxcap][HD/2]
+  DBuf ropestep;             // the step's rows of it: [2 types][MAXM][cos | sin][HD/2]
   // step buffers
   // xa, att and act hold GEMV inputs in the staged layout (staged_index), xgs / attgs their
   // group sums
@@ -628,6 +629,7 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
       }
   }
   ALLOC(c->rope, rt.size() * 4);
+  ALLOC(c->ropestep, (size_t)2 * MAXM * HD * 4);
   HIPCHK(hipMemcpyAsync(c->rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, st));
   ALLOC(c->x, MAXM * H * 4);
   ALLOC(c->xa, MAXM * H * 4);
@@ -916,9 +918,8 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
   const float sqh = std::sqrt((float)H);
   pmark(c, PT_ROWS, 1, 0);
   launch_embed(c->E.as<uint16_t>(), sp, c->L[0]->ln().in_ln, sqh, c->x.as<float>(), c->xa.as<float>(),
-               c->xgs.as<float>(), M, st);
+               c->xgs.as<float>(), c->rope.as<float>(), c->ctxcap, c->ropestep.as<float>(), M, st);
   pmark(c, PT_ROWS, 0, (double)M * H * 2);
-  const float* rope = c->rope.as<float>();
   for (int l = 0; l < NL; ++l) {
     const Layer& A = *c->L[l];
     const LayerNorms ln = A.ln();
@@ -940,17 +941,13 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     pmark(c, PT_GEMV_QKV, 1, 0);
     gemv_passes(c, a, EPI_STORE, M);
     pmark(c, PT_GEMV_QKV, 0, w4_bytes(A.m[0]) + w4_bytes(A.m[1]) + w4_bytes(A.m[2]));
-    const int ty = A.sliding ? 0 : 1;
-    const float* cs = rope + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
-    const float* sn = cs + (size_t)c->ctxcap * (HD / 2);
-    pmark(c, PT_ROWS, 1, 0);
-    launch_qk_rope(c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), NQ * HD, sp, ln, cs, sn, KCl, VCl, M, st);
-    pmark(c, PT_ROWS, 0, (double)M * (NQ * HD + 2 * HD) * 4 * 2);
+    const float* rstep = c->ropestep.as<float>() + (size_t)(A.sliding ? 0 : 1) * MAXM * HD;
     int kmin = sh.pos0 + M - 1;  // E:1325-1326 keys read by the pass: [kmin, pos0 + M - 1]
     for (int r = 0; r < M; ++r) kmin = std::min(kmin, A.sliding ? std::max(0, sh.rope[r] - 511) : 0);
     pmark(c, PT_ATTN, 1, 0);
-    launch_attn(KCl, VCl, c->q.as<float>(), sp, A.sliding, T, c->ctxcap, c->po.as<float>(), c->pm.as<float>(),
-                c->pl.as<float>(), c->att.as<float>(), c->attgs.as<float>(), M, st);
+    launch_attn(KCl, VCl, c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln, rstep, sp, A.sliding, T,
+                c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), c->att.as<float>(), c->attgs.as<float>(), M,
+                st);
     pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
     pmark(c, PT_GEMV_O, 1, 0);
     GemvArgs ao = plain_args(A.m[3], nullptr, c->o.as<float>(), M);  // E:1356

@@ -40,12 +40,14 @@ struct LayerNorms {
 
 // xa / att / act below are written in the staged GEMV input layout (staged_index) with their
 // group sums (xgs, attgs)
+// rope: [2 layer types][cos, sin][ctxcap][HD/2]; ropestep: [2][MAXM][cos | sin][HD/2] of the step's rows
 void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, float* xgs,
-                  int M, hipStream_t st);
-void launch_qk_rope(float* q, const float* k, const float* v, int ldqkv_q, const StepDev* sp, const LayerNorms& ln,
-                    const float* cs, const float* sn, uint16_t* KC, uint16_t* VC, int M, hipStream_t st);
-void launch_attn(const uint16_t* KC, const uint16_t* VC, const float* q, const StepDev* sp, int sliding, int T,
-                 int ctxcap, float* po, float* pm, float* pl, float* att, float* attgs, int M, hipStream_t st);
+                  const float* rope, int ctxcap, float* ropestep, int M, hipStream_t st);
+// verify-pass attention on the raw projections q, k, v: q/k norm, RoPE and the cache rows of
+// the pass (E:1307-1324) fused into the split kernel, then the merge
+void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, const float* v, const LayerNorms& ln,
+                 const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl,
+                 float* att, float* attgs, int M, hipStream_t st);
 void launch_post_attn(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, int M, hipStream_t st);
 void launch_post_ff(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, const float* next_in_ln,
                     const float* fnorm, float* h, float* hn, int M, hipStream_t st);

@@ -1,9 +1,9 @@
-// g4v_layer.hip -- RMSNorm row kernels, q/k norm + RoPE + KV write, branch selection and
-// acceptance for one verify pass on gfx950.
+// g4v_layer.hip -- RMSNorm row kernels, branch selection and acceptance for one verify pass
+// on gfx950 (the q/k norm, RoPE and cache write of E:1307-1324 run inside the attention
+// kernel, g4v_attn.hip).
 //
-// References (E = engine/gemma4_engine.cpp): embedding E:1262-1267; q/k/v norm, RoPE and KV
-// write E:1307-1324; residual/norm blocks E:1358-1361, E:1375-1404; lazy head + acceptance
-// E:1453-1488, E:1647-1661.
+// References (E = engine/gemma4_engine.cpp): embedding E:1262-1267; residual/norm blocks
+// E:1358-1361, E:1375-1404; lazy head + acceptance E:1453-1488, E:1647-1661.
 #include "g4v_layer.h"
 
 namespace g4v {
@@ -56,16 +56,27 @@ __device__ void write_staged(const float* v, int K, float* xs, float* gs) {
   }
 }
 
-// E:1262-1267: x = rbf8(E[tok] * sqrt(H)); xa = (x * r) * in_ln, xa written staged (+ sums)
+// E:1262-1267: x = rbf8(E[tok] * sqrt(H)); xa = (x * r) * in_ln, xa written staged (+ sums).
+// Also gathers the step's RoPE factors: ropestep[ty][m] = (cos, sin) rows of the layer-type ty
+// tables at the row's position, so the attention kernels read them without a dependent load.
 __global__ __launch_bounds__(ROW_THREADS) void k_embed(const uint16_t* __restrict__ E, const StepDev* sp,
                                                        const float* __restrict__ in_ln, float sqh,
                                                        float* __restrict__ x, float* __restrict__ xa,
-                                                       float* __restrict__ xgs) {
+                                                       float* __restrict__ xgs, const float* __restrict__ rope,
+                                                       int ctxcap, float* __restrict__ ropestep) {
   __shared__ __align__(16) float xs[H];
   __shared__ __align__(16) float ys[H];
   __shared__ double red[16];
   const int m = blockIdx.x;
   const int tok = sp->toks[m];
+  {
+    const int ty = threadIdx.x >> 7, i = threadIdx.x & (HD / 2 - 1), rp = sp->rope[m];
+    const float* cs = rope + (size_t)(2 * ty) * ctxcap * (HD / 2);
+    const float* sn = cs + (size_t)ctxcap * (HD / 2);
+    float* dst = ropestep + ((size_t)ty * MAXM + m) * HD;
+    dst[i] = cs[(size_t)rp * (HD / 2) + i];
+    dst[HD / 2 + i] = sn[(size_t)rp * (HD / 2) + i];
+  }
   for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
     const float v = r16(bf2f(E[(size_t)tok * H + i]) * sqh);
     xs[i] = v;
@@ -179,47 +190,6 @@ __global__ __launch_bounds__(ROW_THREADS) void k_post_ff(const float* __restrict
   }
 }
 
-// E:1307-1324: per row m, blocks h < 8 normalise + rotate query head h (E:1312), block 8
-// normalises + rotates k (E:1316) and normalises v (E:1317), then writes both to the cache slot.
-__global__ __launch_bounds__(HD) void k_qk_rope(float* __restrict__ q, const float* __restrict__ k,
-                                                const float* __restrict__ v, int ldq, const StepDev* sp,
-                                                LayerNorms ln, const float* __restrict__ cs,
-                                                const float* __restrict__ sn, uint16_t* __restrict__ KC,
-                                                uint16_t* __restrict__ VC) {
-  __shared__ float ys[HD];
-  __shared__ double red[16];
-  const int m = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
-  const int rp = sp->rope[m], slot = sp->pos0 + m;
-  const float* src = hh < NQ ? q + (size_t)m * ldq + hh * HD : k + (size_t)m * HD;
-  const float* w = hh < NQ ? ln.qn : ln.kn;
-  ys[i] = src[i];
-  __syncthreads();
-  const float r = rms_inv(block_sumsq(ys, HD, red), HD);
-  const float y = r16((ys[i] * r) * w[i]);
-  __syncthreads();
-  ys[i] = y;
-  __syncthreads();
-  float outv;
-  if (i < HD / 2) {  // E:394-402 NeoX halves
-    const float u = ys[i], ww = ys[i + HD / 2], c = cs[(size_t)rp * (HD / 2) + i], s = sn[(size_t)rp * (HD / 2) + i];
-    outv = fmaf(u, c, -(ww * s));
-  } else {
-    const int jj = i - HD / 2;
-    const float u = ys[jj], ww = ys[i], c = cs[(size_t)rp * (HD / 2) + jj], s = sn[(size_t)rp * (HD / 2) + jj];
-    outv = fmaf(ww, c, u * s);
-  }
-  if (hh < NQ) {
-    q[(size_t)m * ldq + hh * HD + i] = outv;
-  } else {
-    KC[(size_t)slot * HD + i] = f2bf(outv);
-    __syncthreads();
-    ys[i] = v[(size_t)m * HD + i];
-    __syncthreads();
-    const float rv = rms_inv(block_sumsq(ys, HD, red), HD);
-    VC[(size_t)slot * HD + i] = f2bf(r16(ys[i] * rv));
-  }
-}
-
 // ---------------------------------------------------------------------------------------
 // branch choice between the two head passes, acceptance and KV compaction
 // ---------------------------------------------------------------------------------------
@@ -310,12 +280,9 @@ __global__ void k_gen_w4(uint8_t* w, uint16_t* s, size_t nb, size_t ns, uint64_t
 // launchers
 // ---------------------------------------------------------------------------------------
 void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, float* xgs,
-                  int M, hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, sp, in_ln, sqh, x, xa, xgs);
-}
-void launch_qk_rope(float* q, const float* k, const float* v, int ldq, const StepDev* sp, const LayerNorms& ln,
-                    const float* cs, const float* sn, uint16_t* KC, uint16_t* VC, int M, hipStream_t st) {
-  hipLaunchKernelGGL(k_qk_rope, dim3(M, NQ + 1), dim3(HD), 0, st, q, k, v, ldq, sp, ln, cs, sn, KC, VC);
+                  const float* rope, int ctxcap, float* ropestep, int M, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, sp, in_ln, sqh, x, xa, xgs, rope, ctxcap,
+                     ropestep);
 }
 void launch_post_attn(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, int M, hipStream_t st) {
   hipLaunchKernelGGL(k_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, xa, xgs, ln);

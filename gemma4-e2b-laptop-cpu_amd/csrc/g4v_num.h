@@ -28,6 +28,9 @@ G4V_HD float4 keep4(bool ok, float4 v) {
 G4V_HD uint4 keep4(bool ok, uint4 v) {
   return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
 }
+G4V_HD uint4 sel4(bool c, uint4 a, uint4 b) {
+  return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
 
 // W:15 bf16 -> fp32 widening
 G4V_HD float bf2f(uint16_t b) { return as_f32((uint32_t)b << 16); }
