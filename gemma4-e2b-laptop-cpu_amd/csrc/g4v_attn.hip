@@ -17,14 +17,14 @@ namespace g4v {
 __constant__ uint64_t c_expf_tab[32] = G4V_EXPF_TABLE;
 
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_TILE = 32;  // key rows per tile: 8 lanes per row, 32 rows
+constexpr int ATT_TILE = 32;  // positions per tile = one block of the value cache
 constexpr int ATT_HB = 2;     // heads per block (224 blocks for a 7-row pass: every CU busy)
 constexpr int ATT_PMAX = 1040;  // positions per split held in LDS
-constexpr int ATT_SW = ATT_PMAX + ATT_TILE;  // weight row length: a split plus one zero tile
-constexpr int ATT_KTS = 8 * 40 + 8;          // key tile: halfwords per position
+constexpr int ATT_SW = ATT_PMAX + 2 * ATT_TILE;  // weight row: a split widened to whole tiles
+constexpr int ATT_RING = 4;  // tiles in flight: the split's key tiles, then its value tiles
 
 struct AttnPtrs {
-  const uint16_t* KC;
+  const uint16_t* KC;  // the layer's cache in the device layout (kc_index / vc_index)
   const uint16_t* VC;
   const float* q;
   int ldq;
@@ -55,40 +55,17 @@ __device__ __forceinline__ float rms_inv16(const double* part) {
   return 1.0f / sqrtf((float)(ss / HD) + 1e-6f);  // division by a power of two: exact scaling
 }
 
-// 32 key rows x 256 bf16 = 1024 16-byte chunks: 4 per thread
-__device__ __forceinline__ void tile_fetch(const uint16_t* base, int p0, int c1, uint4 (&r)[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int u = threadIdx.x + k * ATT_THREADS, rr = u >> 5, cc = u & 31, p = p0 + rr;
-    r[k] = keep4(p < c1, reinterpret_cast<const uint4*>(base + (size_t)min(p, c1 - 1) * HD)[cc]);
-  }
-}
-
-// Key tile fetch for the lane-transposed layout: thread u takes row u/8 and the chunks
-// b, b+2, b+4, b+6 (b = (q&1) + 8(q>>1), q = u%8); chunk c holds elements 8c..8c+7, one per
-// lane l = e%8, at slot (c&1)*16 + c/2 of that lane's 32-value array, so the thread's four
-// chunks land in four consecutive slots of each lane: one 8-byte LDS write per lane.
-__device__ __forceinline__ void ktile_fetch(const uint16_t* base, int p0, int c1, uint4 (&r)[4]) {
-  const int rr = threadIdx.x >> 3, q = threadIdx.x & 7, b = (q & 1) + 8 * (q >> 1), p = p0 + rr;
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    r[k] = keep4(p < c1, reinterpret_cast<const uint4*>(base + (size_t)min(p, c1 - 1) * HD)[b + 2 * k]);
-}
-
 // grid (T, M, NQ / ATT_HB)
 template <bool STEP>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom gin, const StepDev* sp, int sliding,
                                                             int T) {
   __shared__ float qs[ATT_HB][8][32];              // lane l's 32 query values: s0 chain then s1 chain
-  // key tile in the per-lane order, one 80-byte row per (position, lane) and 16 bytes of
-  // padding per position (spreads the transposing stores of different positions over the banks)
-  __shared__ __align__(16) uint16_t kt[ATT_TILE * ATT_KTS];
-  __shared__ __align__(16) uint16_t vt[ATT_TILE][HD];  // value tile, natural layout
   __shared__ __align__(16) float sw[ATT_HB][ATT_SW];
   __shared__ float wmax[ATT_THREADS / 64][ATT_HB];
-  __shared__ float smax[ATT_HB], ssum[ATT_HB];
-  // verify pass: rows being normalised (4 query heads, then the pass's k and v rows), their
-  // 16-lane partial sums of squares, and the pass's finished key / value rows (bf16)
+  __shared__ float smax[ATT_HB];
+  // verify pass: rows being normalised (the block's query heads, then the pass's k and v rows),
+  // their 16-lane partial sums of squares, and the pass's finished key rows (bf16, in the
+  // key cache's chain-lane order) and value rows (bf16, natural order)
   __shared__ float nx[STEP ? ATT_HB + 2 * MAXM : 1][HD];
   __shared__ double npart[STEP ? ATT_HB + 2 * MAXM : 1][16];
   __shared__ float nrinv[STEP ? ATT_HB + 2 * MAXM : 1];
@@ -116,33 +93,58 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     sh_m = gin.skip_hi[m];
   }
   if (m >= M) return;
-  // E:740 attn_allowed for this block's row
-  auto allowed = [=](int p) { return p >= lo_m && p <= pos_m && !(p >= sl_m && p <= sh_m); };
-  // bit e: position pb + e is inside the split (< c1) and allowed, for a tile of 32 positions
+  const int len = kmax - kmin + 1;
+  const int c0 = kmin + (int)((long)t * len / T), c1 = kmin + (int)((long)(t + 1) * len / T);
+  const int PP = c1 - c0;
+  // E:740 attn_allowed for this block's row, restricted to the split
+  auto allowed = [=](int p) { return p >= c0 && p < c1 && p >= lo_m && p <= pos_m && !(p >= sl_m && p <= sh_m); };
+  // bit e: position pb + e is inside the split and allowed, for a tile of 32 positions
   auto bits_in = [](int a, int b, int pb) -> uint32_t {  // positions [a, b] within [pb, pb + 31]
     const int lo = max(a - pb, 0), hi = min(b - pb, 31);
     if (lo > hi) return 0u;
     const uint32_t up = hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u);
     return up & ~((1u << lo) - 1u);
   };
-  auto tile_mask = [=](int pb, int cend) -> uint32_t {
-    return bits_in(lo_m, min(pos_m, cend - 1), pb) & ~bits_in(sl_m, sh_m, pb);
+  auto tile_mask = [=](int pb) -> uint32_t {
+    return bits_in(max(lo_m, c0), min(pos_m, c1 - 1), pb) & ~bits_in(sl_m, sh_m, pb);
   };
-  const int len = kmax - kmin + 1;
-  const int c0 = kmin + (int)((long)t * len / T), c1 = kmin + (int)((long)(t + 1) * len / T);
-  const int PP = c1 - c0;
-  // every global load of the prologue in flight at once: the query heads, the first key and
-  // value tiles and, in a verify pass, the raw rows of the pass that fall in this split
+  // The split is visited in whole blocks of the value cache: tile s covers positions
+  // [pb0 + 32 s, pb0 + 32 s + 32); positions outside [c0, c1) are masked.  One stream of
+  // tile loads, ATT_RING in flight: entry s < NT is key tile s, entries NT <= s < NTp are
+  // empty (NTp rounds NT up to the ring size, so value tile v is entry NTp + v in ring slot
+  // v % ATT_RING), entry NTp + v is value tile v; the value tiles are thus in flight while the
+  // last key tiles and the softmax run.
+  const int pb0 = c0 & ~(ATT_TILE - 1);
+  const int NT = PP > 0 ? ((c1 - 1) >> 5) - (c0 >> 5) + 1 : 0;
+  const int NTp = (NT + ATT_RING - 1) / ATT_RING * ATT_RING;
+  const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;  // key sweep: position ps, chain lane l
+  // key tile: lane (ps, l) takes the 64 bytes of chain lane l at position pb + ps (clamped into
+  // the split); value tile: lane i takes dim i of the block's 32 positions (64 bytes)
+  auto kfetch = [&](int pb, uint4 (&r)[4]) {
+    const uint4* src = reinterpret_cast<const uint4*>(P.KC + (size_t)min(pb + ps, c1 - 1) * HD + l * 32);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = src[c];
+  };
+  auto vfetch = [&](int pb, uint4 (&r)[4]) {
+    const uint4* src = reinterpret_cast<const uint4*>(P.VC + (size_t)(pb >> 5) * (ATT_TILE * HD) + threadIdx.x * 32);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = src[c];
+  };
+  uint4 ring[ATT_RING][4];
+  auto issue = [&](int s, uint4 (&r)[4]) {  // uniform conditions
+    if (s < NT) kfetch(pb0 + s * ATT_TILE, r);
+    else if (s >= NTp && s < NTp + NT) vfetch(pb0 + (s - NTp) * ATT_TILE, r);
+  };
+  // every global load of the prologue in flight at once: the query heads, the first tiles and,
+  // in a verify pass, the raw rows of the pass that fall in this split
   const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
   float qv[ATT_HB];
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
-  uint4 rk[4], rv[4];
-  if (c0 < c1) {
-    ktile_fetch(P.KC, c0, c1, rk);
-    tile_fetch(P.VC, c0, c1, rv);
-  }
-  // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1)
+#pragma unroll
+  for (int k = 0; k < ATT_RING; ++k) issue(k, ring[k]);
+  // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1); they are the
+  // split's last positions
   const int pos0 = STEP ? sp->pos0 : 0;
   const int rn0 = STEP ? max(c0 - pos0, 0) : 0, rn1 = STEP ? min(c1 - pos0, M) : 0;
   if (STEP) {
@@ -203,24 +205,16 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = rot(nx[hh], cq, sq);
 #pragma unroll
     for (int r = 0; r < MAXM; ++r)
-      if (r >= rn0 && r < rn1) knew[r][e] = f2bf(rot(nx[ATT_HB + r], ck[r], sk[r]));
+      if (r >= rn0 && r < rn1) knew[r][kc_slot(e)] = f2bf(rot(nx[ATT_HB + r], ck[r], sk[r]));
     __syncthreads();
     if (m == 0 && h0 == 0)  // one block per split writes the pass's rows that fall in it
       for (int r = rn0; r < rn1; ++r) {
-        P.KCw[(size_t)(pos0 + r) * HD + e] = knew[r][e];
-        P.VCw[(size_t)(pos0 + r) * HD + e] = vnew[r][e];
+        P.KCw[(size_t)(pos0 + r) * HD + e] = knew[r][e];  // the LDS row is already in cache order
+        P.VCw[vc_index(pos0 + r, e)] = vnew[r][e];
       }
   }
-  // a tile row at a position of the pass takes its key / value from LDS
-  auto patch = [&](const uint16_t (*src)[HD], int p, int chunk, uint4 v) {
-    if (!STEP) return v;
-    const bool own = p >= pos0 && p < c1;
-    const uint4 n = *reinterpret_cast<const uint4*>(&src[min(max(p - pos0, 0), MAXM - 1)][chunk * 8]);
-    return sel4(own, n, v);
-  };
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) qs[hh][e & 7][((e >> 3) & 1) * 16 + (e >> 4)] = qv[hh];
-  const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
   float mymax[ATT_HB];
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) mymax[hh] = -1e30f;
@@ -231,55 +225,48 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 #pragma unroll
     for (int i = 0; i < 32; ++i) qr[hh][i] = qs[hh][l][i];
 
-  // sweep 1: scores (E:750-816)
-  for (int pb = c0; pb < c1; pb += ATT_TILE) {
-    __syncthreads();
-    {  // transpose the thread's 4 chunks (32 keys) into 8 lanes x 4 consecutive slots
-      const int rr = threadIdx.x >> 3, q = threadIdx.x & 7, slot0 = (q & 1) * 16 + 4 * (q >> 1);
-      const int b = (q & 1) + 8 * (q >> 1);
+  // sweep 1: scores (E:750-816) straight from the fetched key rows; ring slot k holds stream
+  // entry s = base + k.  Lane group ps scores position pb + ps; padding positions are scored
+  // from a clamped row and only allowed positions enter the running max.
+  for (int base = 0; base < NTp; base += ATT_RING)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) rk[k] = patch(knew, pb + rr, b + 2 * k, rk[k]);
-      const uint32_t w[4][4] = {{rk[0].x, rk[0].y, rk[0].z, rk[0].w}, {rk[1].x, rk[1].y, rk[1].z, rk[1].w},
-                                {rk[2].x, rk[2].y, rk[2].z, rk[2].w}, {rk[3].x, rk[3].y, rk[3].z, rk[3].w}};
+  for (int k = 0; k < ATT_RING; ++k) {
+    const int s = base + k;
+    if (s >= NT) {  // an empty entry of the stream: only its successor is issued
+      issue(s + ATT_RING, ring[k]);
+      continue;
+    }
+    const int pb = pb0 + s * ATT_TILE, p = pb + ps;
+    uint4 kr[4] = {ring[k][0], ring[k][1], ring[k][2], ring[k][3]};
+    if (STEP && pb + ATT_TILE > pos0) {  // uniform: the tile may hold rows of the pass (in LDS)
+      const bool own = p >= pos0 && p < c1;
+      const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][l * 32]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {  // element e of each chunk belongs to lane e
-        const int sh = 16 * (e & 1);
-        const uint32_t v0 = (w[0][e >> 1] >> sh) & 0xFFFFu, v1 = (w[1][e >> 1] >> sh) & 0xFFFFu;
-        const uint32_t v2 = (w[2][e >> 1] >> sh) & 0xFFFFu, v3 = (w[3][e >> 1] >> sh) & 0xFFFFu;
-        *reinterpret_cast<uint2*>(&kt[rr * ATT_KTS + e * 40 + slot0]) = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+      for (int c = 0; c < 4; ++c) kr[c] = sel4(own, n4[c], kr[c]);
+    }
+    issue(s + ATT_RING, ring[k]);  // the slot's next entry
+    const bool okp = (tile_mask(pb) >> ps) & 1u;
+    float kf[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t w4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        kf[c * 8 + 2 * q] = as_f32(w4[q] << 16);
+        kf[c * 8 + 2 * q + 1] = as_f32(w4[q] & 0xFFFF0000u);
       }
     }
-    __syncthreads();
-    if (pb + ATT_TILE < c1) ktile_fetch(P.KC, pb + ATT_TILE, c1, rk);  // next tile in flight
-    // every lane group scores its position (padding rows are zeros); only allowed positions
-    // enter the running max, and masked ones get weight 0 below
-    const int p = pb + ps;
-    const bool okp = (tile_mask(pb, c1) >> ps) & 1u;
-    {
-      float kf[32];
-      const uint4* kv4 = reinterpret_cast<const uint4*>(&kt[ps * ATT_KTS + l * 40]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint4 u = kv4[c];
-        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+    for (int hh = 0; hh < ATT_HB; ++hh) {
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kf[c * 8 + 2 * e] = as_f32(w4[e] << 16);
-          kf[c * 8 + 2 * e + 1] = as_f32(w4[e] & 0xFFFF0000u);
-        }
+      for (int tt = 0; tt < 16; ++tt) {
+        s0 = fmaf(qr[hh][tt], kf[tt], s0);
+        s1 = fmaf(qr[hh][16 + tt], kf[16 + tt], s1);
       }
-#pragma unroll
-      for (int hh = 0; hh < ATT_HB; ++hh) {
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt) {
-          s0 = fmaf(qr[hh][tt], kf[tt], s0);
-          s1 = fmaf(qr[hh][16 + tt], kf[16 + tt], s1);
-        }
-        const float v = hsum8_lanes(s0 + s1);
-        if (l == 0) sw[hh][p - c0] = v;
-        mymax[hh] = (okp && mymax[hh] < v) ? v : mymax[hh];
-      }
+      const float v = hsum8_lanes(s0 + s1);
+      if (l == 0) sw[hh][p - pb0] = v;
+      mymax[hh] = (okp && mymax[hh] < v) ? v : mymax[hh];
     }
   }
 #pragma unroll
@@ -295,68 +282,72 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     smax[threadIdx.x] = v;
   }
   __syncthreads();
-  // weights exp8(score - max) (E:820); masked positions and the padding up to the next
-  // whole tile get weight 0
-  const int PPT = (PP + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
-  for (int idx = threadIdx.x; idx < ATT_HB * PPT; idx += ATT_THREADS) {
-    const int hh = idx / PPT, pp = idx % PPT;
-    sw[hh][pp] = (pp < PP && allowed(c0 + pp)) ? exp8(sw[hh][pp] - smax[hh]) : 0.f;
+  // weights exp8(score - max) (E:820); masked positions and the padding of the whole tiles
+  // get weight 0
+  for (int idx = threadIdx.x; idx < ATT_HB * NT * ATT_TILE; idx += ATT_THREADS) {
+    const int hh = idx / (NT * ATT_TILE), pp = idx - hh * (NT * ATT_TILE);
+    sw[hh][pp] = allowed(pb0 + pp) ? exp8(sw[hh][pp] - smax[hh]) : 0.f;
   }
   __syncthreads();
-  if ((threadIdx.x & 63) == 0 && (threadIdx.x >> 6) < ATT_HB) {  // l = sum of the weights in position
-    const int hh = threadIdx.x >> 6;                               // order (E:821), one wave per head
-    const float4* w4 = reinterpret_cast<const float4*>(&sw[hh][0]);
-    float lsum = 0.f;  // + 0 for a masked position leaves the (non-negative) sum unchanged
-    for (int q = 0; q < PPT / 4; q += 4) {
-      float4 r[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) r[k] = keep4(q + k < PPT / 4, w4[min(q + k, PPT / 4 - 1)]);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) lsum = (((lsum + r[k].x) + r[k].y) + r[k].z) + r[k].w;
-    }
-    ssum[hh] = (lo_m > pos_m) ? 0.0f : lsum;
-  }
-  // sweep 2: o_i = fma chain over positions (E:826-875), V staged tile by tile
-  const int i = threadIdx.x;
-  float o[ATT_HB];
+  // sweep 2: o_i = fma chain over positions (E:826-875) straight from the fetched value
+  // blocks; value tile v is stream entry NTp + v in ring slot v % ATT_RING.  A masked or
+  // padding position (weight 0) is given value +0 by a zeroing byte select: fma(0, 0, o) = o
+  // exactly (o is never -0), which is what skipping it in the reference leaves.  The pass's
+  // rows are the split's last positions: the register pass leaves them out and they follow
+  // from LDS, in position order.  Wave hh < ATT_HB also forms head hh's l = sum of the
+  // weights in position order (E:821) from the same weight reads (+ 0 leaves the
+  // non-negative sum unchanged).
+  const int i = threadIdx.x, wave = threadIdx.x >> 6;
+  float o[ATT_HB], lsum = 0.f;
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = 0.f;
-  for (int pb = c0; pb < c1; pb += ATT_TILE) {
-    __syncthreads();
+  for (int base = 0; base < NT; base += ATT_RING)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int u = threadIdx.x + k * ATT_THREADS, rr = u >> 5, cc = u & 31;
-      *reinterpret_cast<uint4*>(&vt[rr][cc * 8]) = patch(vnew, pb + rr, cc, rv[k]);
-    }
-    __syncthreads();
-    if (pb + ATT_TILE < c1) tile_fetch(P.VC, pb + ATT_TILE, c1, rv);
-    // Masked and padding positions carry weight 0 and are given value +0 (their bits cleared
-    // with a tile mask): fma(0, 0, o) = o exactly (o is never -0), which is what skipping them
-    // in the reference leaves.  The mask is uniform, so no lane diverges and nothing branches.
-    const uint32_t tmask = tile_mask(pb, c1);
+  for (int k = 0; k < ATT_RING; ++k) {
+    const int s = base + k;
+    if (s >= NT) break;  // uniform
+    const int pb = pb0 + s * ATT_TILE;
+    const uint32_t vw[16] = {ring[k][0].x, ring[k][0].y, ring[k][0].z, ring[k][0].w,
+                             ring[k][1].x, ring[k][1].y, ring[k][1].z, ring[k][1].w,
+                             ring[k][2].x, ring[k][2].y, ring[k][2].z, ring[k][2].w,
+                             ring[k][3].x, ring[k][3].y, ring[k][3].z, ring[k][3].w};
+    issue(NTp + s + ATT_RING, ring[k]);
+    const uint32_t keep = tile_mask(pb) & (STEP ? ~bits_in(pos0, pos0 + MAXM, pb) : 0xFFFFFFFFu);
 #pragma unroll
     for (int p4 = 0; p4 < ATT_TILE; p4 += 4) {
       float4 w4[ATT_HB];
 #pragma unroll
-      for (int hh = 0; hh < ATT_HB; ++hh) w4[hh] = *reinterpret_cast<const float4*>(&sw[hh][pb - c0 + p4]);
+      for (int hh = 0; hh < ATT_HB; ++hh) w4[hh] = *reinterpret_cast<const float4*>(&sw[hh][pb - pb0 + p4]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t keep = 0u - ((tmask >> (p4 + e)) & 1u);
-        const float vv = as_f32(((uint32_t)vt[p4 + e][i] << 16) & keep);
+      for (int hh = 0; hh < ATT_HB; ++hh)
+        if (wave == hh) lsum = (((lsum + w4[hh].x) + w4[hh].y) + w4[hh].z) + w4[hh].w;  // uniform
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int pe = p4 + q;
+        // bytes of the position's half word moved to the top, or all zero when masked
+        const uint32_t sel = ((keep >> pe) & 1u) ? ((pe & 1) ? 0x03020c0cu : 0x01000c0cu) : 0x0c0c0c0cu;
+        const float vv = as_f32(__builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], sel));
 #pragma unroll
         for (int hh = 0; hh < ATT_HB; ++hh) {
-          const float wgt = e == 0 ? w4[hh].x : (e == 1 ? w4[hh].y : (e == 2 ? w4[hh].z : w4[hh].w));
+          const float wgt = q == 0 ? w4[hh].x : (q == 1 ? w4[hh].y : (q == 2 ? w4[hh].z : w4[hh].w));
           o[hh] = fmaf(wgt, vv, o[hh]);
         }
+      }
+    }
+    if (STEP && pb + ATT_TILE > pos0) {  // uniform: the pass's rows in this tile, from LDS
+      const int pa = max(max(pb, pos0), c0), pz = min(pb + ATT_TILE, c1);
+      for (int pp = pa; pp < pz; ++pp) {
+        const float vv = as_f32((uint32_t)vnew[pp - pos0][i] << 16);
+#pragma unroll
+        for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = fmaf(sw[hh][pp - pb0], vv, o[hh]);
       }
     }
   }
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];
-  __syncthreads();
-  if (threadIdx.x < ATT_HB) {
-    P.pm[((size_t)t * M + m) * NQ + h0 + threadIdx.x] = smax[threadIdx.x];
-    P.pl[((size_t)t * M + m) * NQ + h0 + threadIdx.x] = ssum[threadIdx.x];
+  if ((threadIdx.x & 63) == 0 && wave < ATT_HB) {
+    P.pm[((size_t)t * M + m) * NQ + h0 + wave] = smax[wave];
+    P.pl[((size_t)t * M + m) * NQ + h0 + wave] = (lo_m > pos_m) ? 0.0f : lsum;
   }
 }
 

@@ -77,7 +77,7 @@ struct g4v_ctx {
   DBuf hrow, hnrow;
   // model
   bool model_ready = false;  // buffers allocated (model_synth or model_create)
-  int NL = 0, I = 0, ctxcap = 0;
+  int NL = 0, I = 0, ctxcap = 0, kvcap = 0;  // kvcap: positions per layer slab of the KV cache
   std::vector<std::unique_ptr<Layer>> L;
   DBuf fnorm, KC, VC, rope;  // rope: [2 types][cos, sin][ctxcap][HD/2]
   DBuf ropestep;             // the step's rows of it: [2 types][MAXM][cos | sin][HD/2]
@@ -378,7 +378,7 @@ int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npo
     g.skip_hi[m] = skip_hi[m];
   }
   HIPCHK(hipSetDevice(c->device));
-  const size_t kvb = (size_t)npos * HD * 2;
+  const size_t kvb = (size_t)kv_cap(npos) * HD * 2;
   if (c->ak.n < kvb) ALLOC(c->ak, kvb);
   if (c->av.n < kvb) ALLOC(c->av, kvb);
   if (c->aq.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->aq, (size_t)MAXM * NQ * HD * 4);
@@ -389,8 +389,16 @@ int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npo
     ALLOC(c->pm, (size_t)MAXT * MAXM * NQ * 4);
     ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
   }
-  HIPCHK(hipMemcpyAsync(c->ak.p, Kc, kvb, hipMemcpyHostToDevice, c->st));
-  HIPCHK(hipMemcpyAsync(c->av.p, Vc, kvb, hipMemcpyHostToDevice, c->st));
+  {  // the caller's [position][256] rows into the device cache layout
+    std::vector<uint16_t> kd((size_t)kv_cap(npos) * HD, 0), vd((size_t)kv_cap(npos) * HD, 0);
+    for (int p = 0; p < npos; ++p)
+      for (int e = 0; e < HD; ++e) {
+        kd[kc_index(p, e)] = Kc[(size_t)p * HD + e];
+        vd[vc_index(p, e)] = Vc[(size_t)p * HD + e];
+      }
+    HIPCHK(hipMemcpy(c->ak.p, kd.data(), kvb, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(c->av.p, vd.data(), kvb, hipMemcpyHostToDevice));
+  }
   HIPCHK(hipMemcpyAsync(c->aq.p, q, (size_t)M * NQ * HD * 4, hipMemcpyHostToDevice, c->st));
   launch_attn_geom(c->ak.as<uint16_t>(), c->av.as<uint16_t>(), c->aq.as<float>(), NQ * HD, g, c->po.as<float>(),
                    c->pm.as<float>(), c->pl.as<float>(), c->ao.as<float>(), NQ * HD, c->st);
@@ -598,6 +606,7 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   c->NL = NL;
   c->I = I;
   c->ctxcap = ctxcap;
+  c->kvcap = kv_cap(ctxcap);
   ALLOC(c->E, (size_t)V * H * 2);
   c->L.clear();
   for (int l = 0; l < NL; ++l) {
@@ -610,8 +619,8 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   }
   ALLOC(c->fnorm, H * 4);
   HIPCHK(hipMemsetAsync(c->fnorm.p, 0, H * 4, st));
-  ALLOC(c->KC, (size_t)NL * ctxcap * HD * 2);
-  ALLOC(c->VC, (size_t)NL * ctxcap * HD * 2);
+  ALLOC(c->KC, (size_t)NL * c->kvcap * HD * 2);
+  ALLOC(c->VC, (size_t)NL * c->kvcap * HD * 2);
   HIPCHK(hipMemsetAsync(c->KC.p, 0, c->KC.n, st));
   HIPCHK(hipMemsetAsync(c->VC.p, 0, c->VC.n, st));
   std::vector<float> rt((size_t)4 * ctxcap * (HD / 2));
@@ -796,16 +805,33 @@ int g4v_model_set_final_norm(g4v_ctx* c, const float* w) {
   return 0;
 }
 
+// reference rows K, V [n][256] for positions pos0 .. pos0 + n - 1 of layer l, written in the
+// device cache layout (kc_index / vc_index); the value blocks they touch are read, patched and
+// written back so that the block's other positions keep their contents
+static int kv_upload(g4v_ctx* c, int l, int pos0, int n, const uint16_t* K, const uint16_t* V) {
+  if (n <= 0) return 0;
+  uint16_t* kslab = c->KC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
+  uint16_t* vslab = c->VC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
+  std::vector<uint16_t> kd((size_t)n * HD);
+  for (int r = 0; r < n; ++r)
+    for (int e = 0; e < HD; ++e) kd[(size_t)r * HD + kc_slot(e)] = K[(size_t)r * HD + e];
+  HIPCHK(hipMemcpy(kslab + (size_t)pos0 * HD, kd.data(), kd.size() * 2, hipMemcpyHostToDevice));
+  const int b0 = pos0 / 32, b1 = (pos0 + n - 1) / 32;
+  std::vector<uint16_t> vd((size_t)(b1 - b0 + 1) * 32 * HD);
+  uint16_t* vblk = vslab + (size_t)b0 * 32 * HD;
+  HIPCHK(hipMemcpy(vd.data(), vblk, vd.size() * 2, hipMemcpyDeviceToHost));
+  for (int r = 0; r < n; ++r)
+    for (int i = 0; i < HD; ++i) vd[vc_index(pos0 + r, i) - (size_t)b0 * 32 * HD] = V[(size_t)r * HD + i];
+  HIPCHK(hipMemcpy(vblk, vd.data(), vd.size() * 2, hipMemcpyHostToDevice));
+  return 0;
+}
+
 int g4v_model_set_kv(g4v_ctx* c, int l, int pos0, int n, const uint16_t* K, const uint16_t* V) {
   if (!c || (n > 0 && (!K || !V))) return G4V_E_ARG;
   ARGCHK(l >= 0 && l < (int)c->L.size() && pos0 >= 0 && n >= 0 && pos0 + n <= c->ctxcap,
          "model_set_kv: layer or position range outside the cache");
   HIPCHK(hipSetDevice(c->device));
-  const size_t off = ((size_t)l * c->ctxcap + pos0) * HD;
-  HIPCHK(hipMemcpyAsync(c->KC.as<uint16_t>() + off, K, (size_t)n * HD * 2, hipMemcpyHostToDevice, c->st));
-  HIPCHK(hipMemcpyAsync(c->VC.as<uint16_t>() + off, V, (size_t)n * HD * 2, hipMemcpyHostToDevice, c->st));
-  HIPCHK(hipStreamSynchronize(c->st));
-  return 0;
+  return kv_upload(c, l, pos0, n, K, V);
 }
 
 int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed) {
@@ -827,11 +853,8 @@ int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed) {
       kc[i] = f2bf(rnd());
       vc[i] = f2bf(rnd());
     }
-    HIPCHK(hipMemcpyAsync(c->KC.as<uint16_t>() + (size_t)l * c->ctxcap * HD, kc.data(), kc.size() * 2,
-                          hipMemcpyHostToDevice, c->st));
-    HIPCHK(hipMemcpyAsync(c->VC.as<uint16_t>() + (size_t)l * c->ctxcap * HD, vc.data(), vc.size() * 2,
-                          hipMemcpyHostToDevice, c->st));
-    HIPCHK(hipStreamSynchronize(c->st));
+    const int r = kv_upload(c, l, 0, n, kc.data(), vc.data());
+    if (r) return r;
   }
   return 0;
 }
@@ -846,12 +869,23 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
   if (!std::strcmp(what, "E") && c->E.p) {
     src = c->E.p;
     nb = (size_t)c->V * H * 2;
-  } else if (!std::strcmp(what, "KC") && c->KC.p) {
-    src = c->KC.p;
-    nb = c->KC.n;
-  } else if (!std::strcmp(what, "VC") && c->VC.p) {
-    src = c->VC.p;
-    nb = c->VC.n;
+  } else if ((!std::strcmp(what, "KC") || !std::strcmp(what, "VC")) && c->KC.p) {
+    // back to the reference's [layer][position][256] rows (positions 0 .. ctxcap - 1)
+    const bool key = what[0] == 'K';
+    nb = (size_t)c->NL * c->ctxcap * HD * 2;
+    if (nbytes) *nbytes = nb;
+    if (!dst) return 0;
+    ARGCHK(cap >= nb, "model_read: buffer too small");
+    std::vector<uint16_t> dev((size_t)c->NL * c->kvcap * HD);
+    HIPCHK(hipMemcpy(dev.data(), key ? c->KC.p : c->VC.p, dev.size() * 2, hipMemcpyDeviceToHost));
+    uint16_t* o = static_cast<uint16_t*>(dst);
+    for (int ll = 0; ll < c->NL; ++ll) {
+      const uint16_t* slab = dev.data() + (size_t)ll * c->kvcap * HD;
+      for (int p = 0; p < c->ctxcap; ++p)
+        for (int e = 0; e < HD; ++e)
+          o[((size_t)ll * c->ctxcap + p) * HD + e] = slab[key ? kc_index(p, e) : vc_index(p, e)];
+    }
+    return 0;
   } else if (!std::strcmp(what, "fnorm") && c->fnorm.p) {
     src = c->fnorm.p;
     nb = H * 4;
@@ -923,8 +957,8 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
   for (int l = 0; l < NL; ++l) {
     const Layer& A = *c->L[l];
     const LayerNorms ln = A.ln();
-    uint16_t* KCl = c->KC.as<uint16_t>() + (size_t)l * c->ctxcap * HD;
-    uint16_t* VCl = c->VC.as<uint16_t>() + (size_t)l * c->ctxcap * HD;
+    uint16_t* KCl = c->KC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
+    uint16_t* VCl = c->VC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
     // q, k, v in one launch (E:1289)
     GemvArgs a{};
     for (int j = 0; j < 3; ++j) a.mat[j] = A.m[j].dev();
@@ -998,7 +1032,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
   head_run(h2, st);
   pmark(c, PT_ACCEPT, 1, 0);
   launch_accept(sp, c->hb1.hs.best, c->hb2.hs.best, c->hb1.hs.cnt, c->hb2.hs.cnt, res, c->KC.as<uint16_t>(),
-                c->VC.as<uint16_t>(), NL, c->ctxcap, st);
+                c->VC.as<uint16_t>(), NL, c->kvcap, st);
   pmark(c, PT_ACCEPT, 0, 0);
 }
 

@@ -13,6 +13,19 @@ constexpr int HD = 256;       // head dim
 constexpr int NQ = 8;         // query heads (one KV head)
 constexpr int MAXM = 8;       // rows per verify pass
 constexpr int MAXT = 16;      // split-KV splits
+
+// Device KV cache layout (per layer: positions 0 .. kvcap - 1, kvcap a multiple of 32).
+// Keys: a position's 256 values in chain-lane order -- element e = 16 tt + 8 s + l (the
+// reference's score lane l, chain s, step tt) at slot l * 32 + s * 16 + tt -- so that the 8
+// lanes scoring one position each read 64 contiguous bytes.  Values: blocks of 32 positions
+// stored dim-major, so that the lane of dim i reads the block's 32 values of that dim as 64
+// contiguous bytes.  Both are permutations of the reference's [position][256] rows.
+__host__ __device__ inline int kc_slot(int e) { return (e & 7) * 32 + ((e >> 3) & 1) * 16 + (e >> 4); }
+__host__ __device__ inline size_t kc_index(int p, int e) { return (size_t)p * HD + kc_slot(e); }
+__host__ __device__ inline size_t vc_index(int p, int i) {
+  return (size_t)(p >> 5) * (32 * HD) + (size_t)i * 32 + (p & 31);
+}
+inline int kv_cap(int npos) { return (npos + 31) / 32 * 32; }  // positions of a layer's cache slab
 constexpr int HEAD_LIMIT = 30000;  // E:1416 LIM: more survivors -> full head
 
 // An int4 G32 matrix on the device.  wr: weights re-laid for the exact-order GEMV

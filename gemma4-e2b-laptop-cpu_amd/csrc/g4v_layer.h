@@ -54,7 +54,7 @@ void launch_post_ff(const float* o, float* x, float* xa, float* xgs, const Layer
 void launch_branch(const StepDev* sp, const int* best1, const float* h, const float* hn, float* h2, float* hn2,
                    VerifyResultDev* res, hipStream_t st);
 void launch_accept(const StepDev* sp, const int* best1, const int* best2, const int* cnt1, const int* cnt2,
-                   VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int ctxcap, hipStream_t st);
+                   VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int kvcap, hipStream_t st);
 
 // synthetic weights (same formulas as the oracle's generator)
 void launch_gen_bf16_normal(uint16_t* out, size_t n, uint64_t seed, float scale, hipStream_t st);

@@ -251,14 +251,16 @@ __global__ void k_accept(const StepDev* sp, const int* best1, const int* best2, 
 }
 
 // E:1651: branch b commits by moving its cache rows to the positions after row 0 (every layer)
-__global__ void k_kv_compact(const StepDev* sp, const VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int ctxcap) {
+// (cache slabs of kvcap positions in the device layout; element i of each row)
+__global__ void k_kv_compact(const StepDev* sp, const VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int kvcap) {
   if (res->branch != 1) return;
   const int l = blockIdx.x, i = threadIdx.x;
+  uint16_t* K = KC + (size_t)l * kvcap * HD;
+  uint16_t* V = VC + (size_t)l * kvcap * HD;
   for (int r = 1; r < res->ncommit; ++r) {
-    const size_t src = ((size_t)l * ctxcap + sp->pos0 + res->hrows[r]) * HD + i;
-    const size_t dst = ((size_t)l * ctxcap + sp->pos0 + r) * HD + i;
-    KC[dst] = KC[src];
-    VC[dst] = VC[src];
+    const int ps = sp->pos0 + res->hrows[r], pd = sp->pos0 + r;
+    K[(size_t)pd * HD + i] = K[(size_t)ps * HD + i];  // a key row is one contiguous permuted row
+    V[vc_index(pd, i)] = V[vc_index(ps, i)];
   }
 }
 
@@ -296,9 +298,9 @@ void launch_branch(const StepDev* sp, const int* best1, const float* h, const fl
   hipLaunchKernelGGL(k_branch, dim3(1), dim3(256), 0, st, sp, best1, h, hn, h2, hn2, res);
 }
 void launch_accept(const StepDev* sp, const int* best1, const int* best2, const int* cnt1, const int* cnt2,
-                   VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int ctxcap, hipStream_t st) {
+                   VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int kvcap, hipStream_t st) {
   hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, st, sp, best1, best2, cnt1, cnt2, res);
-  hipLaunchKernelGGL(k_kv_compact, dim3(NL), dim3(HD), 0, st, sp, res, KC, VC, ctxcap);
+  hipLaunchKernelGGL(k_kv_compact, dim3(NL), dim3(HD), 0, st, sp, res, KC, VC, kvcap);
 }
 void launch_gen_bf16_normal(uint16_t* out, size_t n, uint64_t seed, float scale, hipStream_t st) {
   size_t g = (n + 255) / 256;
