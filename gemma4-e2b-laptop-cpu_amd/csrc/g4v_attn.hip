@@ -120,20 +120,19 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;  // key sweep: position ps, chain lane l
   // key tile: lane (ps, l) takes the 64 bytes of chain lane l at position pb + ps (clamped into
   // the split); value tile: lane i takes dim i of the block's 32 positions (64 bytes)
-  auto kfetch = [&](int pb, uint4 (&r)[4]) {
-    const uint4* src = reinterpret_cast<const uint4*>(P.KC + (size_t)min(pb + ps, c1 - 1) * HD + l * 32);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = src[c];
-  };
-  auto vfetch = [&](int pb, uint4 (&r)[4]) {
-    const uint4* src = reinterpret_cast<const uint4*>(P.VC + (size_t)(pb >> 5) * (ATT_TILE * HD) + threadIdx.x * 32);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = src[c];
-  };
+  // Every stream entry issues its four loads, so each ring slot has exactly one definition
+  // per tile (no merges that would make the compiler wait on loads still in flight): empty
+  // entries and entries past the stream load a row they never use.
   uint4 ring[ATT_RING][4];
-  auto issue = [&](int s, uint4 (&r)[4]) {  // uniform conditions
-    if (s < NT) kfetch(pb0 + s * ATT_TILE, r);
-    else if (s >= NTp && s < NTp + NT) vfetch(pb0 + (s - NTp) * ATT_TILE, r);
+  const uint16_t* kbase = P.KC + l * 32;
+  const uint16_t* vbase = P.VC + threadIdx.x * 32;
+  auto issue = [&](int s, uint4 (&r)[4]) {
+    const bool key = s < NT, val = s >= NTp && s < NTp + NT;  // uniform
+    const size_t koff = (size_t)max(min(pb0 + min(s, NT - 1) * ATT_TILE + ps, c1 - 1), 0) * HD;
+    const size_t voff = (size_t)((pb0 >> 5) + max(min(s - NTp, NT - 1), 0)) * (ATT_TILE * HD);
+    const uint4* src = reinterpret_cast<const uint4*>(key || !val ? kbase + koff : vbase + voff);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = src[c];
   };
   // every global load of the prologue in flight at once: the query heads, the first tiles and,
   // in a verify pass, the raw rows of the pass that fall in this split
@@ -141,29 +140,37 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   float qv[ATT_HB];
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
-#pragma unroll
-  for (int k = 0; k < ATT_RING; ++k) issue(k, ring[k]);
   // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1); they are the
   // split's last positions
   const int pos0 = STEP ? sp->pos0 : 0;
   const int rn0 = STEP ? max(c0 - pos0, 0) : 0, rn1 = STEP ? min(c1 - pos0, M) : 0;
+  // verify pass: the raw rows, the norm weights and this thread's RoPE factors are loaded
+  // before the tiles (the in-order load counter then lets them be used while tiles land)
+  const int i2 = e & (HD / 2 - 1);
+  float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {}, qw = 0.f, kw = 0.f, cq = 0.f, sq = 0.f;
   if (STEP) {
-    // E:1307-1324 on the block's query heads and the pass's key/value rows of this split:
-    // x = r16((x * rms_inv) * w) (v: r16(x * rms_inv)), then NeoX rotation of q and k.  The
-    // raw rows, the norm weights and this thread's RoPE factors are all loaded up front.
-    const int i2 = e & (HD / 2 - 1);
-    float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {};
     if (rn0 < rn1)  // only the splits holding rows of the pass
 #pragma unroll
-    for (int r = 0; r < MAXM; ++r) {
-      const int rr = (r >= rn0 && r < rn1) ? r : rn0;
-      kv[0][r] = P.kraw[(size_t)rr * HD + e];
-      kv[1][r] = P.vraw[(size_t)rr * HD + e];
-      ck[r] = P.ropestep[(size_t)rr * HD + i2];
-      sk[r] = P.ropestep[(size_t)rr * HD + HD / 2 + i2];
-    }
-    const float qw = P.qn[e], kw = P.kn[e];
-    const float cq = P.ropestep[(size_t)m * HD + i2], sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
+      for (int r = 0; r < MAXM; ++r) {
+        const int rr = (r >= rn0 && r < rn1) ? r : rn0;
+        kv[0][r] = P.kraw[(size_t)rr * HD + e];
+        kv[1][r] = P.vraw[(size_t)rr * HD + e];
+        ck[r] = P.ropestep[(size_t)rr * HD + i2];
+        sk[r] = P.ropestep[(size_t)rr * HD + HD / 2 + i2];
+      }
+    qw = P.qn[e];
+    kw = P.kn[e];
+    cq = P.ropestep[(size_t)m * HD + i2];
+    sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the tile loads
+#pragma unroll
+  for (int k = 0; k < ATT_RING; ++k) issue(k, ring[k]);  // also when the split is empty: no paths
+                                                          // with fewer loads in flight
+  __builtin_amdgcn_sched_barrier(0);
+  if (STEP) {
+    // E:1307-1324 on the block's query heads and the pass's key/value rows of this split:
+    // x = r16((x * rms_inv) * w) (v: r16(x * rms_inv)), then NeoX rotation of q and k
 #pragma unroll
     for (int hh = 0; hh < ATT_HB; ++hh) nx[hh][e] = qv[hh];
 #pragma unroll
@@ -226,53 +233,60 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     for (int i = 0; i < 32; ++i) qr[hh][i] = qs[hh][l][i];
 
   // sweep 1: scores (E:750-816) straight from the fetched key rows; ring slot k holds stream
-  // entry s = base + k.  Lane group ps scores position pb + ps; padding positions are scored
-  // from a clamped row and only allowed positions enter the running max.
+  // entry s = base + k.  Lane group ps scores position pb + ps (positions outside the split
+  // from a clamped row: their scores are never used).
   for (int base = 0; base < NTp; base += ATT_RING)
 #pragma unroll
   for (int k = 0; k < ATT_RING; ++k) {
     const int s = base + k;
-    if (s >= NT) {  // an empty entry of the stream: only its successor is issued
-      issue(s + ATT_RING, ring[k]);
-      continue;
-    }
     const int pb = pb0 + s * ATT_TILE, p = pb + ps;
-    uint4 kr[4] = {ring[k][0], ring[k][1], ring[k][2], ring[k][3]};
-    if (STEP && pb + ATT_TILE > pos0) {  // uniform: the tile may hold rows of the pass (in LDS)
-      const bool own = p >= pos0 && p < c1;
-      const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][l * 32]);
+    if (s < NT) {  // uniform; otherwise an empty entry
+      uint4 kr[4] = {ring[k][0], ring[k][1], ring[k][2], ring[k][3]};
+      if (STEP && pb + ATT_TILE > pos0) {  // uniform: the tile may hold rows of the pass (in LDS)
+        const bool own = p >= pos0 && p < c1;
+        const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][l * 32]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kr[c] = sel4(own, n4[c], kr[c]);
-    }
-    issue(s + ATT_RING, ring[k]);  // the slot's next entry
-    const bool okp = (tile_mask(pb) >> ps) & 1u;
-    float kf[32];
+        for (int c = 0; c < 4; ++c) kr[c] = sel4(own, n4[c], kr[c]);
+      }
+      float kf[32];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t w4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t w4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        kf[c * 8 + 2 * q] = as_f32(w4[q] << 16);
-        kf[c * 8 + 2 * q + 1] = as_f32(w4[q] & 0xFFFF0000u);
+        for (int q = 0; q < 4; ++q) {
+          kf[c * 8 + 2 * q] = as_f32(w4[q] << 16);
+          kf[c * 8 + 2 * q + 1] = as_f32(w4[q] & 0xFFFF0000u);
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < ATT_HB; ++hh) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 16; ++tt) {
+          s0 = fmaf(qr[hh][tt], kf[tt], s0);
+          s1 = fmaf(qr[hh][16 + tt], kf[16 + tt], s1);
+        }
+        const float v = hsum8_lanes(s0 + s1);
+        if (l == 0) sw[hh][p - pb0] = v;
       }
     }
+    // the slot's next entry, once its current one is consumed (the loop then carries each
+    // slot in one register set: no copies, which would wait for loads in flight)
+    issue(s + ATT_RING, ring[k]);
+  }
+  __syncthreads();
+  // the running max over the allowed positions only (max is order free)
+  for (int idx = threadIdx.x; idx < ATT_HB * NT * ATT_TILE; idx += ATT_THREADS) {
+    const int hh = idx / (NT * ATT_TILE), pp = idx - hh * (NT * ATT_TILE);
+    const float v = sw[hh][pp];
 #pragma unroll
-    for (int hh = 0; hh < ATT_HB; ++hh) {
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int tt = 0; tt < 16; ++tt) {
-        s0 = fmaf(qr[hh][tt], kf[tt], s0);
-        s1 = fmaf(qr[hh][16 + tt], kf[16 + tt], s1);
-      }
-      const float v = hsum8_lanes(s0 + s1);
-      if (l == 0) sw[hh][p - pb0] = v;
-      mymax[hh] = (okp && mymax[hh] < v) ? v : mymax[hh];
-    }
+    for (int h2 = 0; h2 < ATT_HB; ++h2)
+      if (h2 == hh && allowed(pb0 + pp) && mymax[h2] < v) mymax[h2] = v;
   }
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) {
     float v = mymax[hh];
-    for (int s = 8; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    for (int s = 1; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6][hh] = v;
   }
   __syncthreads();
@@ -291,57 +305,73 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   __syncthreads();
   // sweep 2: o_i = fma chain over positions (E:826-875) straight from the fetched value
   // blocks; value tile v is stream entry NTp + v in ring slot v % ATT_RING.  A masked or
-  // padding position (weight 0) is given value +0 by a zeroing byte select: fma(0, 0, o) = o
-  // exactly (o is never -0), which is what skipping it in the reference leaves.  The pass's
+  // padding position (weight 0) is given value +0: fma(0, 0, o) = o exactly (o is never -0),
+  // which is what skipping it in the reference leaves.  The pass's
   // rows are the split's last positions: the register pass leaves them out and they follow
-  // from LDS, in position order.  Wave hh < ATT_HB also forms head hh's l = sum of the
-  // weights in position order (E:821) from the same weight reads (+ 0 leaves the
-  // non-negative sum unchanged).
+  // from LDS, in position order.  Every wave also forms the l = sum of the weights in
+  // position order (E:821) of head wave % ATT_HB (+ 0 leaves the non-negative sum unchanged);
+  // waves hh < ATT_HB store theirs.
   const int i = threadIdx.x, wave = threadIdx.x >> 6;
   float o[ATT_HB], lsum = 0.f;
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = 0.f;
-  for (int base = 0; base < NT; base += ATT_RING)
+  // a tile every position of which is allowed and none a pass row needs no masks
+  const int fa = max(lo_m, c0), fz = min(min(pos_m, c1 - 1), STEP ? pos0 - 1 : 0x7fffffff);
+  auto full_tile = [=](int pb) {
+    return pb >= fa && pb + ATT_TILE - 1 <= fz && (sl_m > sh_m || pb > sh_m || pb + ATT_TILE - 1 < sl_m);
+  };
+  for (int base = 0; base < NTp; base += ATT_RING)
 #pragma unroll
   for (int k = 0; k < ATT_RING; ++k) {
     const int s = base + k;
-    if (s >= NT) break;  // uniform
     const int pb = pb0 + s * ATT_TILE;
-    const uint32_t vw[16] = {ring[k][0].x, ring[k][0].y, ring[k][0].z, ring[k][0].w,
-                             ring[k][1].x, ring[k][1].y, ring[k][1].z, ring[k][1].w,
-                             ring[k][2].x, ring[k][2].y, ring[k][2].z, ring[k][2].w,
-                             ring[k][3].x, ring[k][3].y, ring[k][3].z, ring[k][3].w};
-    issue(NTp + s + ATT_RING, ring[k]);
-    const uint32_t keep = tile_mask(pb) & (STEP ? ~bits_in(pos0, pos0 + MAXM, pb) : 0xFFFFFFFFu);
+    if (s < NT) {  // uniform; otherwise an entry past the split
+      const uint32_t vw[16] = {ring[k][0].x, ring[k][0].y, ring[k][0].z, ring[k][0].w,
+                               ring[k][1].x, ring[k][1].y, ring[k][1].z, ring[k][1].w,
+                               ring[k][2].x, ring[k][2].y, ring[k][2].z, ring[k][2].w,
+                               ring[k][3].x, ring[k][3].y, ring[k][3].z, ring[k][3].w};
+      const bool full = full_tile(pb);
+      const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb) & (STEP ? ~bits_in(pos0, pos0 + MAXM, pb) : 0xFFFFFFFFu);
+      auto sweep = [&](const bool masked) {
 #pragma unroll
-    for (int p4 = 0; p4 < ATT_TILE; p4 += 4) {
-      float4 w4[ATT_HB];
+        for (int p4 = 0; p4 < ATT_TILE; p4 += 4) {
+          float4 w4[ATT_HB];
 #pragma unroll
-      for (int hh = 0; hh < ATT_HB; ++hh) w4[hh] = *reinterpret_cast<const float4*>(&sw[hh][pb - pb0 + p4]);
+          for (int hh = 0; hh < ATT_HB; ++hh) w4[hh] = *reinterpret_cast<const float4*>(&sw[hh][pb - pb0 + p4]);
+          {  // wave w forms head w % ATT_HB's sum (its own read: no per-head selects)
+            const float4 wl = *reinterpret_cast<const float4*>(&sw[wave % ATT_HB][pb - pb0 + p4]);
+            lsum = (((lsum + wl.x) + wl.y) + wl.z) + wl.w;
+          }
 #pragma unroll
-      for (int hh = 0; hh < ATT_HB; ++hh)
-        if (wave == hh) lsum = (((lsum + w4[hh].x) + w4[hh].y) + w4[hh].z) + w4[hh].w;  // uniform
+          for (int q = 0; q < 4; ++q) {
+            const int pe = p4 + q;
+            // the position's half word moved to the top (byte select 0x0c gives a zero byte),
+            // cleared when masked
+            uint32_t vb = __builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], (pe & 1) ? 0x03020c0cu : 0x01000c0cu);
+            if (masked) vb &= (uint32_t)((int)(keep << (31 - pe)) >> 31);
+            const float vv = as_f32(vb);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int pe = p4 + q;
-        // bytes of the position's half word moved to the top, or all zero when masked
-        const uint32_t sel = ((keep >> pe) & 1u) ? ((pe & 1) ? 0x03020c0cu : 0x01000c0cu) : 0x0c0c0c0cu;
-        const float vv = as_f32(__builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], sel));
+            for (int hh = 0; hh < ATT_HB; ++hh) {
+              const float wgt = q == 0 ? w4[hh].x : (q == 1 ? w4[hh].y : (q == 2 ? w4[hh].z : w4[hh].w));
+              o[hh] = fmaf(wgt, vv, o[hh]);
+            }
+          }
+        }
+      };
+      if (full) sweep(false);
+      else sweep(true);
+      if (STEP && pb + ATT_TILE > pos0) {  // uniform: the pass's rows in this tile, from LDS
+        const int pa = max(max(pb, pos0), c0), pz = min(pb + ATT_TILE, c1);
+        for (int pp = pa; pp < pz; ++pp) {
+          const float vv = as_f32((uint32_t)vnew[pp - pos0][i] << 16);
 #pragma unroll
-        for (int hh = 0; hh < ATT_HB; ++hh) {
-          const float wgt = q == 0 ? w4[hh].x : (q == 1 ? w4[hh].y : (q == 2 ? w4[hh].z : w4[hh].w));
-          o[hh] = fmaf(wgt, vv, o[hh]);
+          for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = fmaf(sw[hh][pp - pb0], vv, o[hh]);
         }
       }
     }
-    if (STEP && pb + ATT_TILE > pos0) {  // uniform: the pass's rows in this tile, from LDS
-      const int pa = max(max(pb, pos0), c0), pz = min(pb + ATT_TILE, c1);
-      for (int pp = pa; pp < pz; ++pp) {
-        const float vv = as_f32((uint32_t)vnew[pp - pos0][i] << 16);
-#pragma unroll
-        for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = fmaf(sw[hh][pp - pb0], vv, o[hh]);
-      }
-    }
+    // the slot's next entry (past the stream it reloads the last block): every path through
+    // the loop issues the same loads, so the wait for a tile never has to cover younger ones
+    issue(NTp + s + ATT_RING, ring[k]);
   }
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];
