@@ -37,9 +37,14 @@ struct DBuf {
 
 struct Mat {
   DBuf wr, s;
+  DBuf tw, ts;  // row-tiled copies for the row-tile GEMV (verify-pass q, k, v, o, down)
   int N = 0, K = 0;
   W4Dev dev() const { return W4Dev{wr.as<uint4>(), s.as<uint16_t>(), N, K}; }
+  W4Tile tile() const { return W4Tile{tw.as<uint4>(), ts.as<uint4>(), N}; }
 };
+
+// the layer matrices the verify pass multiplies with the row-tile GEMV: q, k, v, o, down
+static bool row_tiled(int j) { return j <= 3 || j == 6; }
 
 struct Layer {
   Mat m[7];       // q, k, v, o, gate, up, down
@@ -268,7 +273,7 @@ int g4v_device_info(g4v_ctx* c, char* name, int cap, int* cus, int* lds) {
 // W4G32
 // ---------------------------------------------------------------------------------------
 static int upload_w4(g4v_ctx* c, Mat& m, const uint8_t* w_dev_orig, const uint16_t* s_host_or_dev, bool s_on_dev,
-                     int N, int K) {
+                     int N, int K, bool tiled = false) {
   m.N = N;
   m.K = K;
   ALLOC(m.wr, (size_t)N * K / 2);
@@ -276,6 +281,11 @@ static int upload_w4(g4v_ctx* c, Mat& m, const uint8_t* w_dev_orig, const uint16
   launch_relayout_w4(w_dev_orig, m.wr.as<uint4>(), N, K, c->st);
   HIPCHK(hipMemcpyAsync(m.s.p, s_host_or_dev, (size_t)N * K / 16,
                         s_on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, c->st));
+  if (tiled) {
+    ALLOC(m.tw, (size_t)N * K / 2);
+    ALLOC(m.ts, (size_t)N * K / 16);
+    launch_tile_w4(m.wr.as<uint4>(), m.s.as<uint16_t>(), m.tw.as<uint4>(), m.ts.as<uint4>(), N, K, c->st);
+  }
   return 0;
 }
 
@@ -711,7 +721,7 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
       const size_t nb = (size_t)N * K / 2, ns = (size_t)N * K / 32;
       launch_gen_w4(tw.as<uint8_t>(), ts.as<uint16_t>(), nb, ns, rng_stream(seed, 1000 + 10 * (uint64_t)l + j),
                     rng_stream(seed, 2000 + 10 * (uint64_t)l + j), st);
-      r = upload_w4(c, lay.m[j], tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K);
+      r = upload_w4(c, lay.m[j], tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K, row_tiled(j));
       if (r) return r;
     }
     // norms: r16(base + span * unif(stream(seed, 3000 + 10 l + t), i))
@@ -770,7 +780,7 @@ int g4v_model_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint1
   DBuf tmp;
   ALLOC(tmp, (size_t)N * K / 2);
   HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)N * K / 2, hipMemcpyHostToDevice, c->st));
-  int r = upload_w4(c, c->L[l]->m[j], tmp.as<uint8_t>(), s, false, N, K);
+  int r = upload_w4(c, c->L[l]->m[j], tmp.as<uint8_t>(), s, false, N, K, row_tiled(j));
   if (r) return r;
   HIPCHK(hipStreamSynchronize(c->st));
   return 0;
@@ -960,8 +970,8 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     uint16_t* KCl = c->KC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
     uint16_t* VCl = c->VC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
     // q, k, v in one launch (E:1289)
-    GemvArgs a{};
-    for (int j = 0; j < 3; ++j) a.mat[j] = A.m[j].dev();
+    GemvTArgs a{};
+    for (int j = 0; j < 3; ++j) a.mat[j] = A.m[j].tile();
     a.y[0] = c->q.as<float>();
     a.ldy[0] = NQ * HD;
     a.y[1] = c->k.as<float>();
@@ -973,7 +983,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     a.K = H;
     a.M = M;
     pmark(c, PT_GEMV_QKV, 1, 0);
-    gemv_passes(c, a, EPI_STORE, M);
+    launch_gemv_t(a, st);
     pmark(c, PT_GEMV_QKV, 0, w4_bytes(A.m[0]) + w4_bytes(A.m[1]) + w4_bytes(A.m[2]));
     const float* rstep = c->ropestep.as<float>() + (size_t)(A.sliding ? 0 : 1) * MAXM * HD;
     int kmin = sh.pos0 + M - 1;  // E:1325-1326 keys read by the pass: [kmin, pos0 + M - 1]
@@ -984,10 +994,15 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
                 st);
     pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
     pmark(c, PT_GEMV_O, 1, 0);
-    GemvArgs ao = plain_args(A.m[3], nullptr, c->o.as<float>(), M);  // E:1356
+    GemvTArgs ao{};  // E:1356
+    ao.mat[0] = A.m[3].tile();
+    ao.y[0] = c->o.as<float>();
+    ao.ldy[0] = H;
     ao.xs = c->att.as<float4>();
     ao.gs = c->attgs.as<float>();
-    gemv_passes(c, ao, EPI_STORE, M);
+    ao.K = NQ * HD;
+    ao.M = M;
+    launch_gemv_t(ao, st);
     pmark(c, PT_GEMV_O, 0, w4_bytes(A.m[3]));
     pmark(c, PT_ROWS, 1, 0);
     launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, M, st);
@@ -1006,10 +1021,14 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     gemv_passes(c, gu, EPI_GATEUP, M);
     pmark(c, PT_GEMV_GATEUP, 0, w4_bytes(A.m[4]) + w4_bytes(A.m[5]));
     pmark(c, PT_GEMV_DOWN, 1, 0);
-    GemvArgs ad = plain_args(A.m[6], nullptr, c->o.as<float>(), M);  // E:1373
+    GemvTArgs ad{};  // E:1373
+    ad.mat[0] = A.m[6].tile();
+    ad.y[0] = c->o.as<float>();
+    ad.ldy[0] = H;
     ad.xs = c->act.as<float4>();  // group sums formed in LDS from the staged copy
-    ad.lds_budget = c->lds_max;   // 192 blocks, one per CU: stage K in two halves
-    gemv_passes(c, ad, EPI_STORE, M);
+    ad.K = I;
+    ad.M = M;
+    launch_gemv_t(ad, st);
     pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
     const float* next = l + 1 < NL ? c->L[l + 1]->ln().in_ln : nullptr;
     pmark(c, PT_ROWS, 1, 0);

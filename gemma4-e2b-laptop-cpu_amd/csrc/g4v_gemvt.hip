@@ -1,0 +1,209 @@
+// g4v_gemvt.hip -- row-tile W4G32 GEMV for the verify pass's skinny products, gfx950.
+//
+// Same arithmetic as k_gemv (g4v_gemv.hip), i.e. w4::gemm_rows_tile (engine/w4g32_avx2.h:64-96)
+// bit for bit: chain lane j of output (n, m) runs
+//   a = lo(b_j) xe_j; a = fma(lo(b_8+j), xe_8+j, a); a = fma(hi(b_j), xo_j, a);
+//   a = fma(hi(b_8+j), xo_8+j, a); r_j = fma(a, sc_g, r_j);   off = fma(sc_g, gsum_g, off)
+// over the groups g in order, and y = ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off.
+//
+// The lane mapping is transposed: a wave holds 64 consecutive output rows of one chain lane j
+// for MPL activation rows, so the activation operand of every FMA is the same for the whole
+// wave (one broadcast LDS read per group and row) and a block of 8 waves (j = 0..7) finishes
+// its 64 rows with one LDS exchange.  A block stages only its own MPL activation rows, so even
+// K = 6144 fits in one pass, and the launch has one block per (64-row tile, row subset): the
+// blocks of a tile are placed on the same XCD (round-robin block order), whose L2 then serves
+// the tile's weights to all of them.
+#include "g4v_internal.h"
+
+namespace g4v {
+
+constexpr int GT_THREADS = 512;  // 8 waves, wave j = chain lane j
+constexpr int GT_B = 4;          // chunks per weight batch (two batches in flight)
+
+// re-laid wr[n][c][j] -> tw[n/64][c][j][n%64]; scales s[n][G] (uint4 = 8 groups) -> ts[n/64][c][n%64]
+__global__ void k_tile_w4(const uint4* __restrict__ wr, const uint4* __restrict__ s4, uint4* __restrict__ tw,
+                          uint4* __restrict__ ts, int N, int K) {
+  const int GC = K / 256;
+  const size_t total = (size_t)N * GC * 8;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const int j = (int)(u & 7);
+    const size_t nc = u >> 3;
+    const int c = (int)(nc % GC);
+    const size_t n = nc / GC;
+    tw[(((n >> 6) * GC + c) * 8 + j) * 64 + (n & 63)] = wr[u];
+    if (j == 0) ts[((n >> 6) * GC + c) * 64 + (n & 63)] = s4[nc];
+  }
+}
+
+void launch_tile_w4(const uint4* wr, const uint16_t* s, uint4* tw, uint4* ts, int N, int K, hipStream_t st) {
+  const size_t total = (size_t)N * (K / 256) * 8;
+  int grid = (int)((total + 255) / 256);
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(k_tile_w4, dim3(grid), dim3(256), 0, st, wr, reinterpret_cast<const uint4*>(s), tw, ts, N, K);
+}
+
+struct GemvTDev {
+  GemvTArgs a;
+  int tiles[4];  // prefix sums of 64-row tiles per matrix
+  int nsub;      // row subsets: block slot k -> subset k % nsub, tile group k / nsub
+};
+
+// LDS: activations [MPL][G][8] float4 (staged), group sums [MPL][G], chain sums [MPL][8][64],
+// offsets [MPL][64]
+static size_t gemvt_lds(int mpl, int K) {
+  const int G = K / 32;
+  return (size_t)mpl * G * 8 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4;
+}
+
+template <int MPL>
+__global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
+  const GemvTArgs& a = d.a;
+  const int K = a.K, G = K / 32, GC = K / 256, M = a.M;
+  // block -> (tile, row subset); the tiles of XCD x (block % 8) are x, x + 8, ...
+  const int xcd = blockIdx.x & 7, kq = blockIdx.x >> 3;
+  const int sub = kq % d.nsub, t = (kq / d.nsub) * 8 + xcd;
+  if (t >= d.tiles[3]) return;
+  const int m0 = sub * MPL;
+  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
+  extern __shared__ float4 lds4[];
+  float4* XL = lds4;                                         // [MPL][G][8]
+  float* GSL = reinterpret_cast<float*>(XL + MPL * G * 8);  // [MPL][G]
+  float* RL = GSL + MPL * G;                                 // [MPL][8][64]
+  float* OFL = RL + MPL * 8 * 64;                            // [MPL][64]
+
+  const int mi = (t >= d.tiles[1]) + (t >= d.tiles[2]);
+  const W4Tile W = mi == 0 ? a.mat[0] : (mi == 1 ? a.mat[1] : a.mat[2]);
+  const int tl = t - d.tiles[mi];
+  const uint4* wp = W.w + ((size_t)tl * GC * 8 + j) * 64 + lane;  // chunk c at + c * 512
+  const uint4* sp = W.s + (size_t)tl * GC * 64 + lane;             // chunk c at + c * 64
+  uint4 wA[GT_B], sA[GT_B], wB[GT_B], sB[GT_B];
+  auto load_batch = [&](uint4 (&w)[GT_B], uint4 (&s)[GT_B], int c0) {  // indices clamped
+#pragma unroll
+    for (int b = 0; b < GT_B; ++b) {
+      const int c = min(c0 + b, GC - 1);
+      w[b] = wp[(size_t)c * 512];
+      s[b] = sp[(size_t)c * 64];
+    }
+  };
+  load_batch(wA, sA, 0);
+
+  // the block's activation rows m0 .. m0 + MPL - 1 (rows >= M staged as zeros, never stored)
+  const int RW = G * 8;
+  for (int u = threadIdx.x; u < MPL * RW; u += GT_THREADS) {
+    const int q = u / RW, m = m0 + q;
+    XL[u] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
+  }
+  if (a.gs)
+    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
+      const int q = idx / G, m = m0 + q;
+      GSL[idx] = m < M ? a.gs[(size_t)min(m, M - 1) * G + (idx - q * G)] : 0.f;
+    }
+  __syncthreads();
+  if (!a.gs) {  // W:22 each group's sequential sum, from the staged copy
+    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
+      const float4* q4 = XL + (size_t)idx * 8;
+      float4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = q4[i];
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += (i & 1) ? v[i >> 1].z : v[i >> 1].x;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += (i & 1) ? v[i >> 1].w : v[i >> 1].y;
+      GSL[idx] = s;
+    }
+    __syncthreads();
+  }
+
+  float row[MPL], off = 0.f;
+#pragma unroll
+  for (int q = 0; q < MPL; ++q) row[q] = 0.f;
+  const int qo = j % MPL;  // this wave's offset chain: activation row m0 + j % MPL
+  const float4* xw = XL + j;   // row q, group g: xw[(q * G + g) * 8], the same for the whole wave
+  const float* gw = GSL + qo * G;
+  auto chunk = [&](const uint4 wv, const uint4 sv, const int c) {
+    const float4 gs4[2] = {*reinterpret_cast<const float4*>(gw + c * 8),
+                           *reinterpret_cast<const float4*>(gw + c * 8 + 4)};
+    float4 xv[2][MPL];
+#pragma unroll
+    for (int q = 0; q < MPL; ++q) xv[0][q] = xw[(q * G + c * 8) * 8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // group 8c + i: dword i/2 of the chunk, half i%2
+      if (i + 1 < 8) {
+#pragma unroll
+        for (int q = 0; q < MPL; ++q) xv[(i + 1) & 1][q] = xw[(q * G + c * 8 + i + 1) * 8];
+      }
+      const int k = i >> 1, h = i & 1;
+      const uint32_t dw = k == 0 ? wv.x : (k == 1 ? wv.y : (k == 2 ? wv.z : wv.w));
+      const uint32_t s2 = k == 0 ? sv.x : (k == 1 ? sv.y : (k == 2 ? sv.z : sv.w));
+      uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+      // keep the two masked words: each nibble then converts with one byte-select convert
+      // instead of a bit-field extract plus a convert
+      asm volatile("" : "+v"(lo), "+v"(hi));
+      const float l0 = (float)((lo >> (16 * h)) & 0xFFu);
+      const float l1 = (float)((lo >> (16 * h + 8)) & 0xFFu);
+      const float h0 = (float)((hi >> (16 * h)) & 0xFFu);
+      const float h1 = (float)((hi >> (16 * h + 8)) & 0xFFu);
+      const float sc = h ? as_f32(s2 & 0xFFFF0000u) : as_f32(s2 << 16);
+#pragma unroll
+      for (int q = 0; q < MPL; ++q) {
+        const float4 x4 = xv[i & 1][q];
+        float av = l0 * x4.x;
+        av = fmaf(l1, x4.y, av);
+        av = fmaf(h0, x4.z, av);
+        av = fmaf(h1, x4.w, av);
+        row[q] = fmaf(av, sc, row[q]);
+      }
+      const float4 g4 = gs4[i >> 2];
+      const int e = i & 3;
+      off = fmaf(sc, e == 0 ? g4.x : (e == 1 ? g4.y : (e == 2 ? g4.z : g4.w)), off);
+    }
+  };
+  for (int cb = 0; cb < GC; cb += GT_B) {
+    load_batch(wB, sB, cb + GT_B);  // next batch in flight while this one is used
+#pragma unroll
+    for (int b = 0; b < GT_B; ++b)
+      if (cb + b < GC) chunk(wA[b], sA[b], cb + b);  // uniform condition
+#pragma unroll
+    for (int b = 0; b < GT_B; ++b) {
+      wA[b] = wB[b];
+      sA[b] = sB[b];
+    }
+  }
+
+  // the 8 chain lanes of each (row, output) meet in LDS: ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off
+#pragma unroll
+  for (int q = 0; q < MPL; ++q) RL[(q * 8 + j) * 64 + lane] = row[q];
+  if (j < MPL) OFL[j * 64 + lane] = off;
+  __syncthreads();
+  if ((int)threadIdx.x < MPL * 64) {
+    const int q = threadIdx.x >> 6, m = m0 + q;
+    const float* r = RL + q * 512 + lane;
+    const float y = (((r[0] + r[256]) + (r[64] + r[320])) + ((r[128] + r[384]) + (r[192] + r[448]))) -
+                    8.f * OFL[q * 64 + lane];
+    if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * 64 + lane] = y;
+  }
+}
+
+template <int MPL>
+static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
+  hipLaunchKernelGGL(k_gemv_t<MPL>, dim3(grid), dim3(GT_THREADS), gemvt_lds(MPL, d.a.K), st, d);
+}
+
+// mpl: activation rows per block (1 or 2; 0 picks: one row while the launch has at most two
+// blocks per CU of the 256, else two)
+int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl) {
+  GemvTDev d{};
+  d.a = a;
+  d.tiles[0] = 0;
+  for (int i = 0; i < 3; ++i) d.tiles[i + 1] = d.tiles[i] + a.mat[i].N / 64;
+  const int T = d.tiles[3], tg = (T + 7) / 8;
+  if (mpl <= 0) mpl = (tg * 8 * a.M <= 512) ? 1 : 2;
+  d.nsub = (a.M + mpl - 1) / mpl;
+  const int grid = 8 * tg * d.nsub;
+  if (mpl == 1) launch_mpl<1>(d, st, grid);
+  else launch_mpl<2>(d, st, grid);
+  return grid;
+}
+
+}  // namespace g4v

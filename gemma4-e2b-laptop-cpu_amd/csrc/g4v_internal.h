@@ -72,6 +72,30 @@ struct GemvArgs {
 };
 
 void launch_relayout_w4(const uint8_t* w, uint4* wr, int N, int K, hipStream_t st);
+
+// Row-tiled copy of a re-laid matrix for the row-tile GEMV (g4v_gemvt.hip): N a multiple of 64;
+// w: [N/64][K/256][8][64] uint4, the chunk (c, j) of the tile's 64 rows contiguous (one 1 KB
+// wave load); s: [N/64][K/256][64] uint4, the 8 bf16 scales of chunk c of each row.
+struct W4Tile {
+  const uint4* w;
+  const uint4* s;
+  int N;
+};
+void launch_tile_w4(const uint4* wr, const uint16_t* s, uint4* tw, uint4* ts, int N, int K, hipStream_t st);
+
+// Row-tile GEMV (EPI_STORE): y[mi][m][n] for up to three matrices with the same K (N multiples
+// of 64), activations in the staged layout with optional group sums (formed in LDS when null).
+struct GemvTArgs {
+  W4Tile mat[3];
+  float* y[3];
+  int ldy[3];
+  const float4* xs;  // [M][K/4] staged
+  const float* gs;   // [M][K/32] or null
+  int K;
+  int M;
+};
+// returns the grid size
+int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl = 0);
 // returns the grid size used (the number of EPI_SCREEN partials per activation row)
 int launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
 // grid launch_gemv would use
