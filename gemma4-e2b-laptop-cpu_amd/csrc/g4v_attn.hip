@@ -440,18 +440,12 @@ __device__ __forceinline__ void merge_body(const AttnPtrs& P, int M, int T) {
 
 __global__ __launch_bounds__(HD) void k_attn_merge(AttnPtrs P, int M, int T) { merge_body(P, M, T); }
 
-__global__ __launch_bounds__(HD) void k_attn_merge_step(AttnPtrs P, const StepDev* sp, int T) {
-  if ((int)blockIdx.x >= sp->M) return;
-  merge_body(P, sp->M, T);
-}
-
 void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, const float* v, const LayerNorms& ln,
-                 const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl,
-                 float* att, float* attgs, int M, hipStream_t st) {
-  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, att, NQ * HD, attgs, k, v, ropestep, ln.qn, ln.kn, KC, VC};
+                 const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl, int M,
+                 hipStream_t st) {
+  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, nullptr, NQ * HD, nullptr, k, v, ropestep, ln.qn, ln.kn, KC, VC};
   AttnGeom g{};
   hipLaunchKernelGGL(k_attn_split<true>, dim3(T, M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, sp, sliding, T);
-  hipLaunchKernelGGL(k_attn_merge_step, dim3(M, NQ), dim3(HD), 0, st, P, sp, T);
 }
 
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,

@@ -37,13 +37,15 @@ struct DBuf {
 
 struct Mat {
   DBuf wr, s;
-  DBuf tw, ts;  // row-tiled copies for the row-tile GEMV (verify-pass q, k, v, o, down)
+  DBuf tw, ts;  // row-tiled copies for the row-tile GEMV (verify-pass q, k, v, o, down; the gate
+                // matrix holds the gate / up pair)
   int N = 0, K = 0;
   W4Dev dev() const { return W4Dev{wr.as<uint4>(), s.as<uint16_t>(), N, K}; }
   W4Tile tile() const { return W4Tile{tw.as<uint4>(), ts.as<uint4>(), N}; }
 };
 
-// the layer matrices the verify pass multiplies with the row-tile GEMV: q, k, v, o, down
+// the layer matrices the verify pass multiplies with the row-tile GEMV: q, k, v, o, down (gate
+// and up as one pair, tile_gateup)
 static bool row_tiled(int j) { return j <= 3 || j == 6; }
 
 struct Layer {
@@ -87,9 +89,8 @@ struct g4v_ctx {
   DBuf fnorm, KC, VC, rope;  // rope: [2 types][cos, sin][ctxcap][HD/2]
   DBuf ropestep;             // the step's rows of it: [2 types][MAXM][cos | sin][HD/2]
   // step buffers
-  // xa, att and act hold GEMV inputs in the staged layout (staged_index), xgs / attgs their
-  // group sums
-  DBuf x, xa, xgs, q, k, v, att, attgs, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
+  // xa and act hold GEMV inputs in the staged layout (staged_index), xgs the group sums of xa
+  DBuf x, xa, xgs, q, k, v, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
   StepDev* step_host = nullptr;
   VerifyResultDev* res_host = nullptr;
   // attention standalone
@@ -272,6 +273,18 @@ int g4v_device_info(g4v_ctx* c, char* name, int cap, int* cus, int* lds) {
 // ---------------------------------------------------------------------------------------
 // W4G32
 // ---------------------------------------------------------------------------------------
+// the gate / up pair tiles of a layer, once both matrices are present
+static int tile_gateup(g4v_ctx* c, Layer& L) {
+  Mat& g = L.m[4];
+  const Mat& u = L.m[5];
+  if (!g.wr.p || !u.wr.p || g.N != u.N || g.K != u.K) return 0;
+  ALLOC(g.tw, (size_t)2 * g.N * g.K / 2);
+  ALLOC(g.ts, (size_t)2 * g.N * g.K / 16);
+  launch_tile_w4_pair(g.wr.as<uint4>(), g.s.as<uint16_t>(), u.wr.as<uint4>(), u.s.as<uint16_t>(), g.tw.as<uint4>(),
+                      g.ts.as<uint4>(), g.N, g.K, c->st);
+  return 0;
+}
+
 static int upload_w4(g4v_ctx* c, Mat& m, const uint8_t* w_dev_orig, const uint16_t* s_host_or_dev, bool s_on_dev,
                      int N, int K, bool tiled = false) {
   m.N = N;
@@ -653,11 +666,9 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   ALLOC(c->x, MAXM * H * 4);
   ALLOC(c->xa, MAXM * H * 4);
   ALLOC(c->xgs, MAXM * (H / 32) * 4);
-  ALLOC(c->attgs, MAXM * (NQ * HD / 32) * 4);
   ALLOC(c->q, MAXM * NQ * HD * 4);
   ALLOC(c->k, MAXM * HD * 4);
   ALLOC(c->v, MAXM * HD * 4);
-  ALLOC(c->att, MAXM * NQ * HD * 4);
   ALLOC(c->o, MAXM * H * 4);
   ALLOC(c->act, (size_t)MAXM * I * 4);
   ALLOC(c->h, MAXM * H * 4);
@@ -724,6 +735,8 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
       r = upload_w4(c, lay.m[j], tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K, row_tiled(j));
       if (r) return r;
     }
+    r = tile_gateup(c, lay);
+    if (r) return r;
     // norms: r16(base + span * unif(stream(seed, 3000 + 10 l + t), i))
     for (int t = 0; t < 6; ++t) {
       const int n = t < 4 ? H : HD, off = t < 4 ? t * H : 4 * H + (t - 4) * HD;
@@ -781,6 +794,8 @@ int g4v_model_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint1
   ALLOC(tmp, (size_t)N * K / 2);
   HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)N * K / 2, hipMemcpyHostToDevice, c->st));
   int r = upload_w4(c, c->L[l]->m[j], tmp.as<uint8_t>(), s, false, N, K, row_tiled(j));
+  if (r) return r;
+  if (j == 4 || j == 5) r = tile_gateup(c, *c->L[l]);
   if (r) return r;
   HIPCHK(hipStreamSynchronize(c->st));
   return 0;
@@ -990,16 +1005,17 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     for (int r = 0; r < M; ++r) kmin = std::min(kmin, A.sliding ? std::max(0, sh.rope[r] - 511) : 0);
     pmark(c, PT_ATTN, 1, 0);
     launch_attn(KCl, VCl, c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln, rstep, sp, A.sliding, T,
-                c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), c->att.as<float>(), c->attgs.as<float>(), M,
-                st);
+                c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), M, st);
     pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
     pmark(c, PT_GEMV_O, 1, 0);
-    GemvTArgs ao{};  // E:1356
+    GemvTArgs ao{};  // E:1356 on the merged attention (E:1019-1059, formed in the prologue)
     ao.mat[0] = A.m[3].tile();
     ao.y[0] = c->o.as<float>();
     ao.ldy[0] = H;
-    ao.xs = c->att.as<float4>();
-    ao.gs = c->attgs.as<float>();
+    ao.mrg_po = c->po.as<float>();
+    ao.mrg_pm = c->pm.as<float>();
+    ao.mrg_pl = c->pl.as<float>();
+    ao.mrg_T = T;
     ao.K = NQ * HD;
     ao.M = M;
     launch_gemv_t(ao, st);
@@ -1007,18 +1023,17 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     pmark(c, PT_ROWS, 1, 0);
     launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, M, st);
     pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
-    GemvArgs gu{};  // E:1366 gate/up + gelu
-    gu.mat[0] = A.m[4].dev();
-    gu.mat[1] = A.m[5].dev();
+    GemvTArgs gu{};  // E:1366 gate/up + gelu
+    gu.mat[0] = W4Tile{A.m[4].tw.as<uint4>(), A.m[4].ts.as<uint4>(), I};
+    gu.gateup = 1;
     gu.y[0] = c->act.as<float>();
     gu.ldy[0] = I;
-    gu.y_staged = 1;
     gu.xs = c->xa.as<float4>();
     gu.gs = c->xgs.as<float>();
     gu.K = H;
     gu.M = M;
     pmark(c, PT_GEMV_GATEUP, 1, 0);
-    gemv_passes(c, gu, EPI_GATEUP, M);
+    launch_gemv_t(gu, st);
     pmark(c, PT_GEMV_GATEUP, 0, w4_bytes(A.m[4]) + w4_bytes(A.m[5]));
     pmark(c, PT_GEMV_DOWN, 1, 0);
     GemvTArgs ad{};  // E:1373

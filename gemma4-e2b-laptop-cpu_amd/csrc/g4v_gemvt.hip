@@ -18,6 +18,8 @@
 namespace g4v {
 
 constexpr int GT_THREADS = 512;  // 8 waves, wave j = chain lane j
+
+__constant__ uint64_t c_expf_tab_t[32] = G4V_EXPF_TABLE;
 constexpr int GT_B = 4;          // chunks per weight batch (two batches in flight)
 
 // re-laid wr[n][c][j] -> tw[n/64][c][j][n%64]; scales s[n][G] (uint4 = 8 groups) -> ts[n/64][c][n%64]
@@ -42,6 +44,35 @@ void launch_tile_w4(const uint4* wr, const uint16_t* s, uint4* tw, uint4* ts, in
   hipLaunchKernelGGL(k_tile_w4, dim3(grid), dim3(256), 0, st, wr, reinterpret_cast<const uint4*>(s), tw, ts, N, K);
 }
 
+// gate / up pair: tile t = gate rows 32t .. 32t+31, then up rows 32t .. 32t+31 (N each, N % 32 == 0)
+__global__ void k_tile_w4_pair(const uint4* __restrict__ wg, const uint4* __restrict__ sg,
+                               const uint4* __restrict__ wu, const uint4* __restrict__ su, uint4* __restrict__ tw,
+                               uint4* __restrict__ ts, int N, int K) {
+  const int GC = K / 256;
+  const size_t total = (size_t)2 * N * GC * 8;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const int j = (int)(u & 7);
+    const size_t nc = u >> 3;
+    const int c = (int)(nc % GC);
+    const size_t r = nc / GC;  // paired row: tile r / 64, local row r % 64
+    const size_t t = r >> 6, lr = r & 63;
+    const size_t n = t * 32 + (lr & 31);
+    const bool up = lr >= 32;
+    const uint4 w = up ? wu[(n * GC + c) * 8 + j] : wg[(n * GC + c) * 8 + j];
+    tw[((t * GC + c) * 8 + j) * 64 + lr] = w;
+    if (j == 0) ts[(t * GC + c) * 64 + lr] = up ? su[n * GC + c] : sg[n * GC + c];
+  }
+}
+
+void launch_tile_w4_pair(const uint4* wg, const uint16_t* sg, const uint4* wu, const uint16_t* su, uint4* tw,
+                         uint4* ts, int N, int K, hipStream_t st) {
+  const size_t total = (size_t)2 * N * (K / 256) * 8;
+  int grid = (int)((total + 255) / 256);
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(k_tile_w4_pair, dim3(grid), dim3(256), 0, st, wg, reinterpret_cast<const uint4*>(sg), wu,
+                     reinterpret_cast<const uint4*>(su), tw, ts, N, K);
+}
+
 struct GemvTDev {
   GemvTArgs a;
   int tiles[4];  // prefix sums of 64-row tiles per matrix
@@ -49,13 +80,15 @@ struct GemvTDev {
 };
 
 // LDS: activations [MPL][G][8] float4 (staged), group sums [MPL][G], chain sums [MPL][8][64],
-// offsets [MPL][64]
+// offsets [MPL][64], outputs of the gate/up epilogue [MPL][64]
 static size_t gemvt_lds(int mpl, int K) {
   const int G = K / 32;
-  return (size_t)mpl * G * 8 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4;
+  return (size_t)mpl * G * 8 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4 * 2;
 }
 
-template <int MPL>
+// MRG: the merge prologue (GemvTArgs::mrg_po), a variant of its own so that its registers do
+// not weigh on the other launches
+template <int MPL, bool MRG>
 __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   const GemvTArgs& a = d.a;
   const int K = a.K, G = K / 32, GC = K / 256, M = a.M;
@@ -70,6 +103,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   float* GSL = reinterpret_cast<float*>(XL + MPL * G * 8);  // [MPL][G]
   float* RL = GSL + MPL * G;                                 // [MPL][8][64]
   float* OFL = RL + MPL * 8 * 64;                            // [MPL][64]
+  float* YL = OFL + MPL * 64;                                // [MPL][64]
 
   const int mi = (t >= d.tiles[1]) + (t >= d.tiles[2]);
   const W4Tile W = mi == 0 ? a.mat[0] : (mi == 1 ? a.mat[1] : a.mat[2]);
@@ -89,17 +123,68 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
 
   // the block's activation rows m0 .. m0 + MPL - 1 (rows >= M staged as zeros, never stored)
   const int RW = G * 8;
-  for (int u = threadIdx.x; u < MPL * RW; u += GT_THREADS) {
-    const int q = u / RW, m = m0 + q;
-    XL[u] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
+  if constexpr (MRG) {
+    // E:1019-1059 per element of (row, head h): sc_t = libm expf(max_t - M0) over the splits
+    // with l_t > 0, l = sum_t (double) l_t sc_t, y = r16((fma chain over t of o_t sc_t) *
+    // (float)(1 / l)); thread u takes elements 4u .. 4u+3 (one head) and stores them staged
+    const int T = a.mrg_T;
+    float* XF = reinterpret_cast<float*>(XL);
+    for (int idx = threadIdx.x; idx < MPL * (K / 4); idx += GT_THREADS) {
+      const int q = idx / (K / 4), u = idx - q * (K / 4), m = min(m0 + q, M - 1);
+      const int h = (4 * u) / HD, i = (4 * u) % HD;
+      float pl[MAXT], pm[MAXT];
+      float4 po[MAXT];
+#pragma unroll
+      for (int tt = 0; tt < MAXT; ++tt) {
+        const size_t kk = ((size_t)tt * M + m) * NQ + h;
+        pl[tt] = tt < T ? a.mrg_pl[kk] : 0.f;
+        pm[tt] = tt < T ? a.mrg_pm[kk] : 0.f;
+        po[tt] = tt < T ? *reinterpret_cast<const float4*>(a.mrg_po + kk * HD + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      float M0 = -1e30f;
+#pragma unroll
+      for (int tt = 0; tt < MAXT; ++tt)
+        if (tt < T && pl[tt] > 0) M0 = (M0 < pm[tt]) ? pm[tt] : M0;
+      double l = 0;
+      float sc[MAXT];
+#pragma unroll
+      for (int tt = 0; tt < MAXT; ++tt) {
+        sc[tt] = 0.f;
+        if (tt < T && pl[tt] > 0) {
+          sc[tt] = libm_expf_neg(pm[tt] - M0, c_expf_tab_t);
+          l = fma((double)pl[tt], (double)sc[tt], l);
+        }
+      }
+      const float inv = (float)(1.0 / l);
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int tt = 0; tt < MAXT; ++tt)
+        if (tt < T && pl[tt] > 0) {
+          acc.x = fmaf(po[tt].x, sc[tt], acc.x);
+          acc.y = fmaf(po[tt].y, sc[tt], acc.y);
+          acc.z = fmaf(po[tt].z, sc[tt], acc.z);
+          acc.w = fmaf(po[tt].w, sc[tt], acc.w);
+        }
+      const bool live = m0 + q < M;
+      float* xr = XF + (size_t)q * K;
+      xr[staged_index(4 * u)] = live ? r16(acc.x * inv) : 0.f;
+      xr[staged_index(4 * u + 1)] = live ? r16(acc.y * inv) : 0.f;
+      xr[staged_index(4 * u + 2)] = live ? r16(acc.z * inv) : 0.f;
+      xr[staged_index(4 * u + 3)] = live ? r16(acc.w * inv) : 0.f;
+    }
+  } else {
+    for (int u = threadIdx.x; u < MPL * RW; u += GT_THREADS) {
+      const int q = u / RW, m = m0 + q;
+      XL[u] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
+    }
   }
-  if (a.gs)
+  if (a.gs && !MRG)
     for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
       const int q = idx / G, m = m0 + q;
       GSL[idx] = m < M ? a.gs[(size_t)min(m, M - 1) * G + (idx - q * G)] : 0.f;
     }
   __syncthreads();
-  if (!a.gs) {  // W:22 each group's sequential sum, from the staged copy
+  if (!a.gs || MRG) {  // W:22 each group's sequential sum, from the staged copy
     for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
       const float4* q4 = XL + (size_t)idx * 8;
       float4 v[8];
@@ -181,28 +266,56 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
     const float* r = RL + q * 512 + lane;
     const float y = (((r[0] + r[256]) + (r[64] + r[320])) + ((r[128] + r[384]) + (r[192] + r[448]))) -
                     8.f * OFL[q * 64 + lane];
-    if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * 64 + lane] = y;
+    if (!a.gateup) {
+      if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * 64 + lane] = y;
+    } else {
+      YL[q * 64 + lane] = y;
+    }
+  }
+  if (a.gateup) {  // E:292-299 act = rbf8(rbf8(gelu8(rbf8 g)) * rbf8 u), written staged
+    __syncthreads();
+    if ((int)threadIdx.x < MPL * 32) {
+      const int q = threadIdx.x >> 5, l = threadIdx.x & 31, m = m0 + q;
+      const float g = YL[q * 64 + l], u = YL[q * 64 + 32 + l];
+      const float act = r16(r16(gelu8(r16(g))) * r16(u));
+      if (m < M) a.y[0][(size_t)m * a.ldy[0] + staged_index(tl * 32 + l)] = act;
+    }
   }
 }
 
 template <int MPL>
 static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
-  hipLaunchKernelGGL(k_gemv_t<MPL>, dim3(grid), dim3(GT_THREADS), gemvt_lds(MPL, d.a.K), st, d);
+  if (d.a.mrg_po) {
+    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true>), dim3(grid), dim3(GT_THREADS), gemvt_lds(MPL, d.a.K), st, d);
+  } else {
+    hipLaunchKernelGGL((k_gemv_t<MPL, false>), dim3(grid), dim3(GT_THREADS), gemvt_lds(MPL, d.a.K), st, d);
+  }
 }
 
-// mpl: activation rows per block (1 or 2; 0 picks: one row while the launch has at most two
-// blocks per CU of the 256, else two)
+// mpl: activation rows per block (1 to 4; 0 picks)
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl) {
   GemvTDev d{};
   d.a = a;
   d.tiles[0] = 0;
-  for (int i = 0; i < 3; ++i) d.tiles[i + 1] = d.tiles[i] + a.mat[i].N / 64;
+  for (int i = 0; i < 3; ++i) d.tiles[i + 1] = d.tiles[i] + (a.gateup && i ? 0 : a.mat[i].N * (a.gateup ? 2 : 1) / 64);
   const int T = d.tiles[3], tg = (T + 7) / 8;
-  if (mpl <= 0) mpl = (tg * 8 * a.M <= 512) ? 1 : 2;
+  if (mpl <= 0) {  // the fewest rows per block that keep the launch within one block per CU, else 4
+    mpl = 4;
+    for (int c : {1, 2})
+      if (8 * tg * ((a.M + c - 1) / c) <= 256) {
+        mpl = c;
+        break;
+      }
+  }
+  if (a.mrg_po && mpl > 2) mpl = 2;  // the merge variant exists for one and two rows
   d.nsub = (a.M + mpl - 1) / mpl;
   const int grid = 8 * tg * d.nsub;
-  if (mpl == 1) launch_mpl<1>(d, st, grid);
-  else launch_mpl<2>(d, st, grid);
+  switch (mpl) {
+    case 1: launch_mpl<1>(d, st, grid); break;
+    case 2: launch_mpl<2>(d, st, grid); break;
+    case 3: launch_mpl<3>(d, st, grid); break;
+    default: launch_mpl<4>(d, st, grid); break;
+  }
   return grid;
 }
 

@@ -82,9 +82,14 @@ struct W4Tile {
   int N;
 };
 void launch_tile_w4(const uint4* wr, const uint16_t* s, uint4* tw, uint4* ts, int N, int K, hipStream_t st);
+// gate / up pair of N rows each: tile t holds gate rows 32t..32t+31 then up rows 32t..32t+31
+void launch_tile_w4_pair(const uint4* wg, const uint16_t* sg, const uint4* wu, const uint16_t* su, uint4* tw,
+                         uint4* ts, int N, int K, hipStream_t st);
 
-// Row-tile GEMV (EPI_STORE): y[mi][m][n] for up to three matrices with the same K (N multiples
-// of 64), activations in the staged layout with optional group sums (formed in LDS when null).
+// Row-tile GEMV: y[mi][m][n] for up to three matrices with the same K (N multiples of 64),
+// activations in the staged layout with optional group sums (formed in LDS when null).  With
+// gateup set, mat[0] is a gate / up pair (launch_tile_w4_pair, N rows each) and y[0] receives
+// the activation gelu(gate) * up of each of the N rows, in the staged layout (row length ldy[0]).
 struct GemvTArgs {
   W4Tile mat[3];
   float* y[3];
@@ -93,6 +98,14 @@ struct GemvTArgs {
   const float* gs;   // [M][K/32] or null
   int K;
   int M;
+  int gateup;
+  // merge prologue (mrg_po not null, K = NQ * HD, xs / gs unused): the activations are the
+  // split-KV merge (E:1019-1059) of the attention partials po [T][M][NQ][HD], pm / pl
+  // [T][M][NQ], formed by every block for its own rows
+  const float* mrg_po;
+  const float* mrg_pm;
+  const float* mrg_pl;
+  int mrg_T;
 };
 // returns the grid size
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl = 0);

@@ -44,10 +44,11 @@ struct LayerNorms {
 void launch_embed(const uint16_t* E, const StepDev* sp, const float* in_ln, float sqh, float* x, float* xa, float* xgs,
                   const float* rope, int ctxcap, float* ropestep, int M, hipStream_t st);
 // verify-pass attention on the raw projections q, k, v: q/k norm, RoPE and the cache rows of
-// the pass (E:1307-1324) fused into the split kernel, then the merge
+// the pass (E:1307-1324) fused into the split kernel; the split partials po / pm / pl are
+// merged by their consumer, the o projection (GemvTArgs::mrg_po)
 void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, const float* v, const LayerNorms& ln,
-                 const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl,
-                 float* att, float* attgs, int M, hipStream_t st);
+                 const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl, int M,
+                 hipStream_t st);
 void launch_post_attn(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, int M, hipStream_t st);
 void launch_post_ff(const float* o, float* x, float* xa, float* xgs, const LayerNorms& ln, const float* next_in_ln,
                     const float* fnorm, float* h, float* hn, int M, hipStream_t st);
