@@ -90,7 +90,9 @@ struct g4v_ctx {
   DBuf ropestep;             // the step's rows of it: [2 types][MAXM][cos | sin][HD/2]
   // step buffers
   // xa and act hold GEMV inputs in the staged layout (staged_index), xgs the group sums of xa
-  DBuf x, xa, xgs, q, k, v, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
+  // x / x2: the residual stream, alternating between the two halves of a layer (a GEMV whose
+  // norm prologue updates it reads one and writes the other)
+  DBuf x, x2, xa, xgs, q, k, v, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
   StepDev* step_host = nullptr;
   VerifyResultDev* res_host = nullptr;
   // attention standalone
@@ -664,6 +666,7 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   ALLOC(c->ropestep, (size_t)2 * MAXM * HD * 4);
   HIPCHK(hipMemcpyAsync(c->rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, st));
   ALLOC(c->x, MAXM * H * 4);
+  ALLOC(c->x2, MAXM * H * 4);
   ALLOC(c->xa, MAXM * H * 4);
   ALLOC(c->xgs, MAXM * (H / 32) * 4);
   ALLOC(c->q, MAXM * NQ * HD * 4);
@@ -993,10 +996,21 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     a.ldy[1] = HD;
     a.y[2] = c->v.as<float>();
     a.ldy[2] = HD;
-    a.xs = c->xa.as<float4>();
-    a.gs = c->xgs.as<float>();
     a.K = H;
     a.M = M;
+    if (l == 0) {  // from the embedding row kernel
+      a.xs = c->xa.as<float4>();
+      a.gs = c->xgs.as<float>();
+    } else {  // the previous layer's MLP residual / norm block (E:1375-1378, E:1390-1404) as prologue
+      const LayerNorms pln = c->L[l - 1]->ln();
+      a.nrm_mode = 2;
+      a.nrm_o = c->o.as<float>();
+      a.nrm_xin = c->x2.as<float>();
+      a.nrm_xout = c->x.as<float>();
+      a.nrm_w1 = pln.post_ff;
+      a.nrm_w2 = ln.in_ln;
+      a.nrm_scalar = pln.scalar;
+    }
     pmark(c, PT_GEMV_QKV, 1, 0);
     launch_gemv_t(a, st);
     pmark(c, PT_GEMV_QKV, 0, w4_bytes(A.m[0]) + w4_bytes(A.m[1]) + w4_bytes(A.m[2]));
@@ -1020,16 +1034,17 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     ao.M = M;
     launch_gemv_t(ao, st);
     pmark(c, PT_GEMV_O, 0, w4_bytes(A.m[3]));
-    pmark(c, PT_ROWS, 1, 0);
-    launch_post_attn(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, M, st);
-    pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
-    GemvTArgs gu{};  // E:1366 gate/up + gelu
+    GemvTArgs gu{};  // E:1366 gate/up + gelu, the attention residual / norm block (E:1358-1361) as prologue
     gu.mat[0] = W4Tile{A.m[4].tw.as<uint4>(), A.m[4].ts.as<uint4>(), I};
     gu.gateup = 1;
     gu.y[0] = c->act.as<float>();
     gu.ldy[0] = I;
-    gu.xs = c->xa.as<float4>();
-    gu.gs = c->xgs.as<float>();
+    gu.nrm_mode = 1;
+    gu.nrm_o = c->o.as<float>();
+    gu.nrm_xin = c->x.as<float>();
+    gu.nrm_xout = c->x2.as<float>();
+    gu.nrm_w1 = ln.post_attn;
+    gu.nrm_w2 = ln.pre_ff;
     gu.K = H;
     gu.M = M;
     pmark(c, PT_GEMV_GATEUP, 1, 0);
@@ -1045,12 +1060,12 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     ad.M = M;
     launch_gemv_t(ad, st);
     pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
-    const float* next = l + 1 < NL ? c->L[l + 1]->ln().in_ln : nullptr;
-    pmark(c, PT_ROWS, 1, 0);
-    launch_post_ff(c->o.as<float>(), c->x.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, next,
-                   c->fnorm.as<float>(),
-                   c->h.as<float>(), c->hn.as<float>(), M, st);
-    pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
+    if (l + 1 == NL) {  // the last MLP residual block and the final norm (E:1414-1417) for the head
+      pmark(c, PT_ROWS, 1, 0);
+      launch_post_ff(c->o.as<float>(), c->x2.as<float>(), c->xa.as<float>(), c->xgs.as<float>(), ln, nullptr,
+                     c->fnorm.as<float>(), c->h.as<float>(), c->hn.as<float>(), M, st);
+      pmark(c, PT_ROWS, 0, (double)M * H * 4 * 4);
+    }
   }
   // head of row 0, then of the branch its token selects (E:1475-1488)
   HeadRun h1 = head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr);

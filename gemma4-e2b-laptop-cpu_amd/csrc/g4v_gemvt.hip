@@ -80,15 +80,17 @@ struct GemvTDev {
 };
 
 // LDS: activations [MPL][G][8] float4 (staged), group sums [MPL][G], chain sums [MPL][8][64],
-// offsets [MPL][64], outputs of the gate/up epilogue [MPL][64]
-static size_t gemvt_lds(int mpl, int K) {
+// offsets [MPL][64], outputs of the gate/up epilogue [MPL][64]; the norm prologue adds its two
+// weight rows [2][H], partial sums [MPL][16] (double) and RMS factors [2][MPL]
+static size_t gemvt_lds(int mpl, int K, bool nrm) {
   const int G = K / 32;
-  return (size_t)mpl * G * 8 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4 * 2;
+  return (size_t)mpl * G * 8 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4 * 2 +
+         (nrm ? (size_t)2 * H * 4 + (size_t)mpl * 16 * 8 + (size_t)2 * mpl * 4 : 0);
 }
 
-// MRG: the merge prologue (GemvTArgs::mrg_po), a variant of its own so that its registers do
-// not weigh on the other launches
-template <int MPL, bool MRG>
+// MRG: the merge prologue (GemvTArgs::mrg_po), NRM: the norm prologue (GemvTArgs::nrm_mode);
+// variants of their own so that their registers do not weigh on the other launches
+template <int MPL, bool MRG, bool NRM>
 __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   const GemvTArgs& a = d.a;
   const int K = a.K, G = K / 32, GC = K / 256, M = a.M;
@@ -172,19 +174,122 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
       xr[staged_index(4 * u + 2)] = live ? r16(acc.z * inv) : 0.f;
       xr[staged_index(4 * u + 3)] = live ? r16(acc.w * inv) : 0.f;
     }
+  } else if constexpr (NRM) {
+    // E:1358-1361 (mode 1) / E:1375-1378 with E:1390-1404 (mode 2, the per-layer-embedding
+    // branch zero) for the block's rows; RMS factors from the 16-lane double sum of squares
+    // (E:326-345).  XL takes the rows in plain order, is normalised in place and finally
+    // permuted in place into the staged order, one thread per (row, group).
+    constexpr int RW4 = H / 4, NV = (MPL * RW4 + GT_THREADS - 1) / GT_THREADS;
+    float* W12 = YL + MPL * 64;                                   // [2][H]
+    double* RED = reinterpret_cast<double*>(W12 + 2 * H);        // [MPL][16]
+    float* RR = reinterpret_cast<float*>(RED + MPL * 16);         // [2][MPL]
+    const float4* o4 = reinterpret_cast<const float4*>(a.nrm_o);
+    const float4* x4 = reinterpret_cast<const float4*>(a.nrm_xin);
+    float4 ov[NV], xv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {  // clamped: rows past M read row M - 1 and are zeroed
+      const int u = min((int)threadIdx.x + k * GT_THREADS, MPL * RW4 - 1), q = u / RW4;
+      const size_t src = (size_t)min(m0 + q, M - 1) * RW4 + (u - q * RW4);
+      ov[k] = o4[src];
+      xv[k] = x4[src];
+    }
+    const int wi = min((int)threadIdx.x, RW4 - 1);
+    const float4 w1 = reinterpret_cast<const float4*>(a.nrm_w1)[wi];
+    const float4 w2 = reinterpret_cast<const float4*>(a.nrm_w2)[wi];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int u = threadIdx.x + k * GT_THREADS;
+      if (u < MPL * RW4) {
+        const float4 o = ov[k];
+        XL[u] = keep4(m0 + u / RW4 < M, make_float4(r16(o.x), r16(o.y), r16(o.z), r16(o.w)));
+      }
+    }
+    if ((int)threadIdx.x < RW4) {
+      reinterpret_cast<float4*>(W12)[threadIdx.x] = w1;
+      reinterpret_cast<float4*>(W12 + H)[threadIdx.x] = w2;
+    }
+    __syncthreads();
+    const float* XP = reinterpret_cast<const float*>(XL);
+    auto rms_rows = [&](float* rinv) {  // lane t of a row sums x[16 s + t]^2 in double over s
+      if ((int)threadIdx.x < MPL * 16) {
+        const float* xr = XP + (threadIdx.x >> 4) * H;
+        double sacc = 0;
+#pragma unroll 16
+        for (int i = threadIdx.x & 15; i < H; i += 16) {
+          const double dv = (double)xr[i];
+          sacc = fma(dv, dv, sacc);
+        }
+        RED[threadIdx.x] = sacc;
+      }
+      __syncthreads();
+      if ((int)threadIdx.x < MPL) {
+        const double* p = RED + threadIdx.x * 16;
+        double q4[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) q4[l] = (p[l] + p[4 + l]) + (p[8 + l] + p[12 + l]);
+        const double ss = (q4[0] + q4[2]) + (q4[1] + q4[3]);
+        rinv[threadIdx.x] = 1.0f / sqrtf((float)(ss / H) + 1e-6f);
+      }
+      __syncthreads();
+    };
+    rms_rows(RR);
+    const bool after_mlp = a.nrm_mode == 2;
+    const float scal = a.nrm_scalar;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int u = threadIdx.x + k * GT_THREADS;
+      if (u < MPL * RW4) {
+        const int q = u / RW4, c4 = u - q * RW4;
+        const float r1 = RR[q];
+        const float4 os = XL[u], w = reinterpret_cast<const float4*>(W12)[c4], xr = xv[k];
+        float4 v = make_float4(r16(xr.x + r16((os.x * r1) * w.x)), r16(xr.y + r16((os.y * r1) * w.y)),
+                               r16(xr.z + r16((os.z * r1) * w.z)), r16(xr.w + r16((os.w * r1) * w.w)));
+        if (after_mlp) v = make_float4(r16(v.x * scal), r16(v.y * scal), r16(v.z * scal), r16(v.w * scal));
+        v = keep4(m0 + q < M, v);
+        XL[u] = v;
+        if (t == 0 && m0 + q < M) reinterpret_cast<float4*>(a.nrm_xout)[(size_t)(m0 + q) * RW4 + c4] = v;
+      }
+    }
+    __syncthreads();
+    rms_rows(RR + MPL);
+    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {  // staged copy + group sums
+      const int q = idx / G, g = idx - q * G;
+      float4* b4 = XL + (size_t)q * RW4 + g * 8;
+      const float4* w4 = reinterpret_cast<const float4*>(W12 + H) + g * 8;
+      const float r2 = RR[MPL + q];
+      float v[32];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float4 tv = b4[i], ww = w4[i];
+        v[4 * i] = (tv.x * r2) * ww.x;
+        v[4 * i + 1] = (tv.y * r2) * ww.y;
+        v[4 * i + 2] = (tv.z * r2) * ww.z;
+        v[4 * i + 3] = (tv.w * r2) * ww.w;
+      }
+      if (!after_mlp) {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) v[e] = r16(v[e]);
+      }
+      float sum = 0.f;  // W:22 the group's sequential sum
+#pragma unroll
+      for (int e = 0; e < 32; ++e) sum += v[e];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) b4[jj] = make_float4(v[2 * jj], v[16 + 2 * jj], v[2 * jj + 1], v[17 + 2 * jj]);
+      GSL[idx] = sum;
+    }
   } else {
     for (int u = threadIdx.x; u < MPL * RW; u += GT_THREADS) {
       const int q = u / RW, m = m0 + q;
       XL[u] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
     }
   }
-  if (a.gs && !MRG)
+  if (a.gs && !MRG && !NRM)
     for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
       const int q = idx / G, m = m0 + q;
       GSL[idx] = m < M ? a.gs[(size_t)min(m, M - 1) * G + (idx - q * G)] : 0.f;
     }
   __syncthreads();
-  if (!a.gs || MRG) {  // W:22 each group's sequential sum, from the staged copy
+  if ((!a.gs || MRG) && !NRM) {  // W:22 each group's sequential sum, from the staged copy
     for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
       const float4* q4 = XL + (size_t)idx * 8;
       float4 v[8];
@@ -285,10 +390,13 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
 
 template <int MPL>
 static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
+  const size_t lds = gemvt_lds(MPL, d.a.K, d.a.nrm_mode != 0);
   if (d.a.mrg_po) {
-    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true>), dim3(grid), dim3(GT_THREADS), gemvt_lds(MPL, d.a.K), st, d);
+    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false>), dim3(grid), dim3(GT_THREADS), lds, st, d);
+  } else if (d.a.nrm_mode) {
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, true>), dim3(grid), dim3(GT_THREADS), lds, st, d);
   } else {
-    hipLaunchKernelGGL((k_gemv_t<MPL, false>), dim3(grid), dim3(GT_THREADS), gemvt_lds(MPL, d.a.K), st, d);
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, false>), dim3(grid), dim3(GT_THREADS), lds, st, d);
   }
 }
 

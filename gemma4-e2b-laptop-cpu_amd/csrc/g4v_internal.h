@@ -106,6 +106,19 @@ struct GemvTArgs {
   const float* mrg_pm;
   const float* mrg_pl;
   int mrg_T;
+  // norm prologue (nrm_mode != 0, K = H, xs / gs unused): the block forms its rows' activations
+  // from the previous sub-block's output o and the residual stream xin:
+  //   x1 = r16(xin + r16((r16(o) * r1) * w1)), mode 2 (after the MLP) then x1 = r16(x1 * scalar);
+  //   xa = (x1 * r2) * w2, rounded to bf16 in mode 1 (after attention);
+  // r1, r2 the RMS factors of r16(o) and x1.  The blocks of tile 0 write x1 to xout (a buffer
+  // other than xin, which the other blocks still read).
+  int nrm_mode;
+  const float* nrm_o;
+  const float* nrm_xin;
+  float* nrm_xout;
+  const float* nrm_w1;
+  const float* nrm_w2;
+  float nrm_scalar;
 };
 // returns the grid size
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl = 0);
