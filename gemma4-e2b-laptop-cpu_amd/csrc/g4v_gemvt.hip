@@ -79,12 +79,13 @@ struct GemvTDev {
   int nsub;      // row subsets: block slot k -> subset k % nsub, tile group k / nsub
 };
 
-// LDS: activations [MPL][G][8] float4 (staged), group sums [MPL][G], chain sums [MPL][8][64],
+// LDS: activations [MPL][G][8 + 1] float4 (staged; a pad float4 after each group spreads the
+// per-group accesses of the prologue over the banks), group sums [MPL][G], chain sums [MPL][8][64],
 // offsets [MPL][64], outputs of the gate/up epilogue [MPL][64]; the norm prologue adds its two
 // weight rows [2][H], partial sums [MPL][16] (double) and RMS factors [2][MPL]
 static size_t gemvt_lds(int mpl, int K, bool nrm) {
   const int G = K / 32;
-  return (size_t)mpl * G * 8 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4 * 2 +
+  return (size_t)mpl * G * 9 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4 * 2 +
          (nrm ? (size_t)2 * H * 4 + (size_t)mpl * 16 * 8 + (size_t)2 * mpl * 4 : 0);
 }
 
@@ -102,7 +103,9 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
   extern __shared__ float4 lds4[];
   float4* XL = lds4;                                         // [MPL][G][8]
-  float* GSL = reinterpret_cast<float*>(XL + MPL * G * 8);  // [MPL][G]
+  float* GSL = reinterpret_cast<float*>(XL + MPL * G * 9);  // [MPL][G]
+  // float4 u = (row * G + group) * 8 + k of the rows is held at pad(u)
+  auto pad = [](int u) { return u + (u >> 3); };
   float* RL = GSL + MPL * G;                                 // [MPL][8][64]
   float* OFL = RL + MPL * 8 * 64;                            // [MPL][64]
   float* YL = OFL + MPL * 64;                                // [MPL][64]
@@ -168,11 +171,12 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
           acc.w = fmaf(po[tt].w, sc[tt], acc.w);
         }
       const bool live = m0 + q < M;
-      float* xr = XF + (size_t)q * K;
-      xr[staged_index(4 * u)] = live ? r16(acc.x * inv) : 0.f;
-      xr[staged_index(4 * u + 1)] = live ? r16(acc.y * inv) : 0.f;
-      xr[staged_index(4 * u + 2)] = live ? r16(acc.z * inv) : 0.f;
-      xr[staged_index(4 * u + 3)] = live ? r16(acc.w * inv) : 0.f;
+      const float yv[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const int si = staged_index(4 * u + cc);
+        XF[pad(q * (K / 4) + (si >> 2)) * 4 + (si & 3)] = live ? r16(yv[cc] * inv) : 0.f;
+      }
     }
   } else if constexpr (NRM) {
     // E:1358-1361 (mode 1) / E:1375-1378 with E:1390-1404 (mode 2, the per-layer-embedding
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
       const int u = threadIdx.x + k * GT_THREADS;
       if (u < MPL * RW4) {
         const float4 o = ov[k];
-        XL[u] = keep4(m0 + u / RW4 < M, make_float4(r16(o.x), r16(o.y), r16(o.z), r16(o.w)));
+        XL[pad(u)] = keep4(m0 + u / RW4 < M, make_float4(r16(o.x), r16(o.y), r16(o.z), r16(o.w)));
       }
     }
     if ((int)threadIdx.x < RW4) {
@@ -212,12 +216,24 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
     const float* XP = reinterpret_cast<const float*>(XL);
     auto rms_rows = [&](float* rinv) {  // lane t of a row sums x[16 s + t]^2 in double over s
       if ((int)threadIdx.x < MPL * 16) {
-        const float* xr = XP + (threadIdx.x >> 4) * H;
+        // element 16 s + lt of row rq: group s / 2, float4 4 (s % 2) + lt / 4 of it (padded)
+        const float* xb = XP + (threadIdx.x >> 4) * (G * 36) + (threadIdx.x & 15);
+        auto xr = [&](int st) { return xb[(st >> 1) * 36 + (st & 1) * 16]; };
         double sacc = 0;
-#pragma unroll 16
-        for (int i = threadIdx.x & 15; i < H; i += 16) {
-          const double dv = (double)xr[i];
-          sacc = fma(dv, dv, sacc);
+        float v[2][16];  // the values of 16 steps, read while the previous 16 are summed
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[0][k] = xr(k);
+#pragma unroll
+        for (int s0 = 0; s0 < H / 16; s0 += 16) {
+          if (s0 + 16 < H / 16) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[((s0 >> 4) + 1) & 1][k] = xr(s0 + 16 + k);
+          }
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const double dv = (double)v[(s0 >> 4) & 1][k];
+            sacc = fma(dv, dv, sacc);
+          }
         }
         RED[threadIdx.x] = sacc;
       }
@@ -241,38 +257,39 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
       if (u < MPL * RW4) {
         const int q = u / RW4, c4 = u - q * RW4;
         const float r1 = RR[q];
-        const float4 os = XL[u], w = reinterpret_cast<const float4*>(W12)[c4], xr = xv[k];
+        const float4 os = XL[pad(u)], w = reinterpret_cast<const float4*>(W12)[c4], xr = xv[k];
         float4 v = make_float4(r16(xr.x + r16((os.x * r1) * w.x)), r16(xr.y + r16((os.y * r1) * w.y)),
                                r16(xr.z + r16((os.z * r1) * w.z)), r16(xr.w + r16((os.w * r1) * w.w)));
         if (after_mlp) v = make_float4(r16(v.x * scal), r16(v.y * scal), r16(v.z * scal), r16(v.w * scal));
         v = keep4(m0 + q < M, v);
-        XL[u] = v;
+        XL[pad(u)] = v;
         if (t == 0 && m0 + q < M) reinterpret_cast<float4*>(a.nrm_xout)[(size_t)(m0 + q) * RW4 + c4] = v;
       }
     }
     __syncthreads();
     rms_rows(RR + MPL);
-    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {  // staged copy + group sums
-      const int q = idx / G, g = idx - q * G;
-      float4* b4 = XL + (size_t)q * RW4 + g * 8;
-      const float4* w4 = reinterpret_cast<const float4*>(W12 + H) + g * 8;
-      const float r2 = RR[MPL + q];
-      float v[32];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float4 tv = b4[i], ww = w4[i];
-        v[4 * i] = (tv.x * r2) * ww.x;
-        v[4 * i + 1] = (tv.y * r2) * ww.y;
-        v[4 * i + 2] = (tv.z * r2) * ww.z;
-        v[4 * i + 3] = (tv.w * r2) * ww.w;
+    for (int k = 0; k < NV; ++k) {  // xa in place, plain order
+      const int u = threadIdx.x + k * GT_THREADS;
+      if (u < MPL * RW4) {
+        const int q = u / RW4, c4 = u - q * RW4;
+        const float r2 = RR[MPL + q];
+        const float4 tv = XL[pad(u)], w = reinterpret_cast<const float4*>(W12 + H)[c4];
+        float4 v = make_float4((tv.x * r2) * w.x, (tv.y * r2) * w.y, (tv.z * r2) * w.z, (tv.w * r2) * w.w);
+        if (!after_mlp) v = make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w));
+        XL[pad(u)] = v;
       }
-      if (!after_mlp) {
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {  // staged order + group sums
+      float4* b4 = XL + (size_t)idx * 9;  // row q = idx / G, group g = idx % G: 8 float4 in plain order
+      float4 r[8];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) v[e] = r16(v[e]);
-      }
+      for (int i = 0; i < 8; ++i) r[i] = b4[i];
       float sum = 0.f;  // W:22 the group's sequential sum
 #pragma unroll
-      for (int e = 0; e < 32; ++e) sum += v[e];
+      for (int i = 0; i < 8; ++i) sum = (((sum + r[i].x) + r[i].y) + r[i].z) + r[i].w;
+      const float* v = reinterpret_cast<const float*>(r);
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) b4[jj] = make_float4(v[2 * jj], v[16 + 2 * jj], v[2 * jj + 1], v[17 + 2 * jj]);
       GSL[idx] = sum;
@@ -280,7 +297,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   } else {
     for (int u = threadIdx.x; u < MPL * RW; u += GT_THREADS) {
       const int q = u / RW, m = m0 + q;
-      XL[u] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
+      XL[pad(u)] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
     }
   }
   if (a.gs && !MRG && !NRM)
@@ -291,7 +308,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   __syncthreads();
   if ((!a.gs || MRG) && !NRM) {  // W:22 each group's sequential sum, from the staged copy
     for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
-      const float4* q4 = XL + (size_t)idx * 8;
+      const float4* q4 = XL + (size_t)idx * 9;
       float4 v[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = q4[i];
@@ -309,19 +326,19 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
 #pragma unroll
   for (int q = 0; q < MPL; ++q) row[q] = 0.f;
   const int qo = j % MPL;  // this wave's offset chain: activation row m0 + j % MPL
-  const float4* xw = XL + j;   // row q, group g: xw[(q * G + g) * 8], the same for the whole wave
+  const float4* xw = XL + j;   // row q, group g: xw[(q * G + g) * 9], the same for the whole wave
   const float* gw = GSL + qo * G;
   auto chunk = [&](const uint4 wv, const uint4 sv, const int c) {
     const float4 gs4[2] = {*reinterpret_cast<const float4*>(gw + c * 8),
                            *reinterpret_cast<const float4*>(gw + c * 8 + 4)};
     float4 xv[2][MPL];
 #pragma unroll
-    for (int q = 0; q < MPL; ++q) xv[0][q] = xw[(q * G + c * 8) * 8];
+    for (int q = 0; q < MPL; ++q) xv[0][q] = xw[(q * G + c * 8) * 9];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {  // group 8c + i: dword i/2 of the chunk, half i%2
       if (i + 1 < 8) {
 #pragma unroll
-        for (int q = 0; q < MPL; ++q) xv[(i + 1) & 1][q] = xw[(q * G + c * 8 + i + 1) * 8];
+        for (int q = 0; q < MPL; ++q) xv[(i + 1) & 1][q] = xw[(q * G + c * 8 + i + 1) * 9];
       }
       const int k = i >> 1, h = i & 1;
       const uint32_t dw = k == 0 ? wv.x : (k == 1 ? wv.y : (k == 2 ? wv.z : wv.w));
