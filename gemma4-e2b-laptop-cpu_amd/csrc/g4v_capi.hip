@@ -39,6 +39,7 @@ struct Mat {
   DBuf wr, s;
   DBuf tw, ts;  // row-tiled copies for the row-tile GEMV (verify-pass q, k, v, o, down; the gate
                 // matrix holds the gate / up pair)
+  DBuf a8w, a8s;  // W4A8 MFMA operand tiles (standalone handles with N % 16 == 0)
   int N = 0, K = 0;
   W4Dev dev() const { return W4Dev{wr.as<uint4>(), s.as<uint16_t>(), N, K}; }
   W4Tile tile() const { return W4Tile{tw.as<uint4>(), ts.as<uint4>(), N}; }
@@ -75,6 +76,7 @@ struct g4v_ctx {
   int cus = 0;
   std::vector<std::unique_ptr<Mat>> mats;  // standalone GEMV handles
   DBuf gx, gy;                              // standalone GEMV io
+  DBuf a8x, a8y, a8xq, a8sx, a8corr, a8q, a8qs, a8qsum;  // W4A8 io and quantised activations
   // head
   bool head_ready = false;
   int V = 0;
@@ -314,6 +316,11 @@ int g4v_w4_upload(g4v_ctx* c, const uint8_t* w, const uint16_t* s, int N, int K)
   auto m = std::make_unique<Mat>();
   int r = upload_w4(c, *m, tmp.as<uint8_t>(), s, false, N, K);
   if (r) return r;
+  if (N % 16 == 0) {  // operand tiles of the W4A8 path (g4v_w4a8_gemm)
+    ALLOC(m->a8w, (size_t)N * K / 2);
+    ALLOC(m->a8s, (size_t)N * K / 16);
+    launch_tile_a8(tmp.as<uint8_t>(), m->s.as<uint16_t>(), m->a8w.as<uint4>(), m->a8s.as<uint4>(), N, K, c->st);
+  }
   HIPCHK(hipStreamSynchronize(c->st));
   c->mats.push_back(std::move(m));
   return (int)c->mats.size() - 1;
@@ -368,6 +375,97 @@ int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us) {
   HIPCHK(hipEventCreate(&e1));
   HIPCHK(hipEventRecord(e0, c->st));
   for (int i = 0; i < iters; ++i) gemv_passes(c, a, EPI_STORE, M);
+  HIPCHK(hipEventRecord(e1, c->st));
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *us = ms * 1000.f / iters;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// W4A8 (engine/w4a8_avx2.h, i8_task E:303-309)
+// ---------------------------------------------------------------------------------------
+constexpr int A8_MAXM = 8192;
+
+// device copies of x [M][K] and the quantised operands for M rows
+static int a8_io(g4v_ctx* c, int M, int K, int N) {
+  const int Mpad = w4a8_mpad(M), G = K / 32;
+  auto need = [&](DBuf& b, size_t n) -> int {
+    if (b.n < n) return dalloc(c, b, n);
+    return 0;
+  };
+  int r;
+  if ((r = need(c->a8x, (size_t)M * K * 4)) || (r = need(c->a8xq, (size_t)Mpad * K * 2)) ||
+      (r = need(c->a8sx, (size_t)G * Mpad * 4)) || (r = need(c->a8corr, (size_t)G * Mpad * 4)) ||
+      (N > 0 && (r = need(c->a8y, (size_t)M * N * 4))))
+    return r;
+  return 0;
+}
+
+int g4v_w4a8_quant(g4v_ctx* c, const float* x, int M, int K, int8_t* q, float* sx, int32_t* sum) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(x && q && sx && sum && M >= 1 && M <= A8_MAXM && K > 0 && K % 256 == 0,
+         "w4a8_quant: need 1 <= M <= 8192 and K % 256 == 0");
+  HIPCHK(hipSetDevice(c->device));
+  int r = a8_io(c, M, K, 0);
+  if (r) return r;
+  const int G = K / 32;
+  if (c->a8q.n < (size_t)M * K) ALLOC(c->a8q, (size_t)M * K);
+  if (c->a8qs.n < (size_t)M * G * 4) ALLOC(c->a8qs, (size_t)M * G * 4);
+  if (c->a8qsum.n < (size_t)M * G * 4) ALLOC(c->a8qsum, (size_t)M * G * 4);
+  HIPCHK(hipMemcpyAsync(c->a8x.p, x, (size_t)M * K * 4, hipMemcpyHostToDevice, c->st));
+  launch_w4a8_quant(c->a8x.as<float>(), M, w4a8_mpad(M), K, c->a8xq.as<uint16_t>(), c->a8sx.as<float>(),
+                    c->a8corr.as<float>(), c->a8q.as<int8_t>(), c->a8qs.as<float>(), c->a8qsum.as<int32_t>(), c->st);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(q, c->a8q.p, (size_t)M * K, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipMemcpyAsync(sx, c->a8qs.p, (size_t)M * G * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipMemcpyAsync(sum, c->a8qsum.p, (size_t)M * G * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+static void a8_enqueue(g4v_ctx* c, const Mat& m, int M) {
+  launch_w4a8_quant(c->a8x.as<float>(), M, w4a8_mpad(M), m.K, c->a8xq.as<uint16_t>(), c->a8sx.as<float>(),
+                    c->a8corr.as<float>(), nullptr, nullptr, nullptr, c->st);
+  launch_w4a8_gemm(m.a8w.as<uint4>(), m.a8s.as<uint4>(), c->a8xq.as<uint16_t>(), c->a8sx.as<float>(),
+                   c->a8corr.as<float>(), c->a8y.as<float>(), M, m.N, m.K, m.N, c->st);
+}
+
+int g4v_w4a8_gemm(g4v_ctx* c, int h, const float* x, int M, float* y) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(h >= 0 && h < (int)c->mats.size(), "w4a8_gemm: bad handle");
+  ARGCHK(x && y && M >= 1 && M <= A8_MAXM, "w4a8_gemm: need 1 <= M <= 8192");
+  const Mat& m = *c->mats[h];
+  ARGCHK(m.a8w.p != nullptr, "w4a8_gemm: the matrix needs N % 16 == 0");
+  HIPCHK(hipSetDevice(c->device));
+  int r = a8_io(c, M, m.K, m.N);
+  if (r) return r;
+  HIPCHK(hipMemcpyAsync(c->a8x.p, x, (size_t)M * m.K * 4, hipMemcpyHostToDevice, c->st));
+  a8_enqueue(c, m, M);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(y, c->a8y.p, (size_t)M * m.N * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+int g4v_w4a8_bench(g4v_ctx* c, int h, int M, int iters, float* us) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(h >= 0 && h < (int)c->mats.size() && M >= 1 && M <= A8_MAXM && iters > 0 && us, "w4a8_bench: bad args");
+  const Mat& m = *c->mats[h];
+  ARGCHK(m.a8w.p != nullptr, "w4a8_bench: the matrix needs N % 16 == 0");
+  HIPCHK(hipSetDevice(c->device));
+  int r = a8_io(c, M, m.K, m.N);
+  if (r) return r;
+  HIPCHK(hipMemsetAsync(c->a8x.p, 0, (size_t)M * m.K * 4, c->st));
+  a8_enqueue(c, m, M);
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  HIPCHK(hipEventRecord(e0, c->st));
+  for (int i = 0; i < iters; ++i) a8_enqueue(c, m, M);
   HIPCHK(hipEventRecord(e1, c->st));
   HIPCHK(hipEventSynchronize(e1));
   float ms = 0;

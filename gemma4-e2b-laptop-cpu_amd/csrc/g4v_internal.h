@@ -120,6 +120,17 @@ struct GemvTArgs {
   const float* nrm_w2;
   float nrm_scalar;
 };
+// W4A8 (g4v_w4a8.hip): operand tiles of a matrix from its original bytes [N][K/2] and scales
+// [N][K/32] (N % 16 == 0): tw [N/16][K/128][64] uint4, ts [N/16][K/256][16] uint4
+void launch_tile_a8(const uint8_t* w, const uint16_t* s, uint4* tw, uint4* ts, int N, int K, hipStream_t st);
+// quantised rows: xqb [Mpad][K] bf16 (MFMA operand order), sxt / corr [K/32][Mpad]; q / sx / sum
+// (optional, plain layouts [M][K], [M][K/32]) for the quant entry point
+void launch_w4a8_quant(const float* x, int M, int Mpad, int K, uint16_t* xqb, float* sxt, float* corr, int8_t* qo,
+                       float* sxo, int32_t* sumo, hipStream_t st);
+void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, const float* sxt, const float* corr,
+                      float* y, int M, int N, int K, int ldy, hipStream_t st);
+int w4a8_mpad(int M);  // rows the quantised operand holds for M rows
+
 // returns the grid size
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl = 0);
 // returns the grid size used (the number of EPI_SCREEN partials per activation row)

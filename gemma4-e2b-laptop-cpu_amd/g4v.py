@@ -29,6 +29,9 @@ SIGNATURES = {
     "g4v_w4_upload": (_i, [_vp, _u8p, _u16p, _i, _i]),
     "g4v_w4g32_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4g32_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_w4a8_quant": (_i, [_vp, _f32p, _i, _i, _vp, _f32p, _i32p]),
+    "g4v_w4a8_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
+    "g4v_w4a8_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
     "g4v_attn_splitkv": (_i, [_vp, _u16p, _u16p, _i, _i, _i, _i, _f32p, _i32p, _i32p, _i32p, _i32p,
                               _i, _i, _i, _f32p]),
     "g4v_head_build": (_i, [_vp, _u16p, _i]),
@@ -144,6 +147,30 @@ class Device:
     def w4g32_bench(self, mat, M, iters=100):
         us = C.c_float()
         self._ok(self.L.g4v_w4g32_bench(self.h, mat[0], M, iters, C.byref(us)), "w4g32_bench")
+        return us.value
+
+    # ---- W4A8 (w4a8::quant + w4a8::tile through i8_task) ----
+    def w4a8_quant(self, X):
+        X = _c(X, np.float32)
+        M, K = X.shape
+        q = np.empty((M, K), np.int8)
+        sx = np.empty((M, K // 32), np.float32)
+        sm = np.empty((M, K // 32), np.int32)
+        self._ok(self.L.g4v_w4a8_quant(self.h, X, M, K, q.ctypes.data, sx, sm), "w4a8_quant")
+        return q, sx, sm
+
+    def w4a8(self, mat, X):
+        h, N, K = mat
+        X = _c(X, np.float32)
+        M = X.shape[0]
+        assert X.shape[1] == K
+        Y = np.empty((M, N), np.float32)
+        self._ok(self.L.g4v_w4a8_gemm(self.h, h, X, M, Y), "w4a8_gemm")
+        return Y
+
+    def w4a8_bench(self, mat, M, iters=100):
+        us = C.c_float()
+        self._ok(self.L.g4v_w4a8_bench(self.h, mat[0], M, iters, C.byref(us)), "w4a8_bench")
         return us.value
 
     # ---- split-KV attention ----

@@ -43,6 +43,17 @@ int g4v_w4g32_gemm(g4v_ctx* c, int h, const float* x, int M, float* y);
 /* same GEMV with x and y already on the device; times `iters` launches, returns us/launch */
 int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
 
+/* ---- W4A8: w4a8::quant (engine/w4a8_avx2.h:30-42) and w4a8::tile<MT> over all rows as
+ * i8_task runs it (engine/w4a8_avx2.h:46-61, E:303-309), on a handle of g4v_w4_upload with
+ * N % 16 == 0.  The engine takes this path for prefill and, with ENGINE_DECODE_INT8 set, for
+ * M >= 2 decode rows (E:311).  1 <= M <= 8192.
+ * quant: q [M][K] int8, sx [M][K/32] (amax / 127), sum [M][K/32] (sum of the integers). */
+int g4v_w4a8_quant(g4v_ctx* c, const float* x, int M, int K, int8_t* q, float* sx, int32_t* sum);
+/* y[m][n] (fp32, [M][N]) bit-identical to quant + tile */
+int g4v_w4a8_gemm(g4v_ctx* c, int h, const float* x, int M, float* y);
+/* quant + GEMM with the operands already on the device; times `iters` runs, us per run */
+int g4v_w4a8_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
+
 /* ---- split-KV attention: attn_task + attn_merge (E:743-877, E:1019-1059) with the
  * reference's split geometry [kmin + t*len/T, kmin + (t+1)*len/T).  Kc, Vc: [npos][hd] bf16;
  * q: [M][nh*hd] fp32; per row: pos, lo, skip_lo, skip_hi (attn_allowed, E:740).
