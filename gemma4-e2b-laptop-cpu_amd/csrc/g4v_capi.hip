@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -122,6 +123,9 @@ struct g4v_ctx {
   std::vector<Graph> graphs;
   std::vector<long long> warmed;  // shapes run once eagerly (first call) before capture
   bool use_graph = true;
+  // row-tile GEMV shape of the verify pass's q/k/v, o, gate/up and down products: activation
+  // rows per block and rows per tile (G4V_GEMV_CFG="a,b a,b a,b a,b" overrides, for tuning)
+  int gcfg[4][2] = {{2, 64}, {1, 64}, {4, 64}, {1, 64}};
   size_t step_events = 0;  // profiling events used by the last eager verify pass
   ~g4v_ctx() {
     for (auto& g : graphs) {
@@ -234,6 +238,14 @@ int g4v_create(int device, g4v_ctx** out) {
   if (e != hipSuccess) {
     delete c;
     return G4V_E_HIP;
+  }
+  if (const char* cfg = std::getenv("G4V_GEMV_CFG")) {
+    int v[8];
+    if (std::sscanf(cfg, "%d,%d %d,%d %d,%d %d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6], &v[7]) == 8)
+      for (int i = 0; i < 4; ++i) {
+        c->gcfg[i][0] = std::min(4, std::max(1, v[2 * i]));
+        c->gcfg[i][1] = v[2 * i + 1] == 32 ? 32 : 64;
+      }
   }
   e = hipStreamCreate(&c->st);
   if (e != hipSuccess) {
@@ -812,7 +824,8 @@ extern "C" {
 
 int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap) {
   if (!c) return G4V_E_ARG;
-  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_synth: bad shape");
+  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && I <= 6144 && ctxcap > 8,
+         "model_synth: need I % 256 == 0, I <= 6144");
   HIPCHK(hipSetDevice(c->device));
   hipStream_t st = c->st;
   int r = model_alloc(c, V, NL, I, ctxcap);
@@ -862,7 +875,8 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
 
 int g4v_model_create(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   if (!c) return G4V_E_ARG;
-  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && ctxcap > 8, "model_create: bad shape");
+  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && I <= 6144 && ctxcap > 8,
+         "model_create: need I % 256 == 0, I <= 6144");
   HIPCHK(hipSetDevice(c->device));
   int r = model_alloc(c, V, NL, I, ctxcap);
   if (r) return r;
@@ -1110,7 +1124,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
       a.nrm_scalar = pln.scalar;
     }
     pmark(c, PT_GEMV_QKV, 1, 0);
-    launch_gemv_t(a, st);
+    launch_gemv_t(a, st, c->gcfg[0][0], c->gcfg[0][1]);
     pmark(c, PT_GEMV_QKV, 0, w4_bytes(A.m[0]) + w4_bytes(A.m[1]) + w4_bytes(A.m[2]));
     const float* rstep = c->ropestep.as<float>() + (size_t)(A.sliding ? 0 : 1) * MAXM * HD;
     int kmin = sh.pos0 + M - 1;  // E:1325-1326 keys read by the pass: [kmin, pos0 + M - 1]
@@ -1130,7 +1144,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     ao.mrg_T = T;
     ao.K = NQ * HD;
     ao.M = M;
-    launch_gemv_t(ao, st);
+    launch_gemv_t(ao, st, c->gcfg[1][0], c->gcfg[1][1]);
     pmark(c, PT_GEMV_O, 0, w4_bytes(A.m[3]));
     GemvTArgs gu{};  // E:1366 gate/up + gelu, the attention residual / norm block (E:1358-1361) as prologue
     gu.mat[0] = W4Tile{A.m[4].tw.as<uint4>(), A.m[4].ts.as<uint4>(), I};
@@ -1146,7 +1160,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     gu.K = H;
     gu.M = M;
     pmark(c, PT_GEMV_GATEUP, 1, 0);
-    launch_gemv_t(gu, st);
+    launch_gemv_t(gu, st, c->gcfg[2][0], c->gcfg[2][1]);
     pmark(c, PT_GEMV_GATEUP, 0, w4_bytes(A.m[4]) + w4_bytes(A.m[5]));
     pmark(c, PT_GEMV_DOWN, 1, 0);
     GemvTArgs ad{};  // E:1373
@@ -1156,7 +1170,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     ad.xs = c->act.as<float4>();  // group sums formed in LDS from the staged copy
     ad.K = I;
     ad.M = M;
-    launch_gemv_t(ad, st);
+    launch_gemv_t(ad, st, c->gcfg[3][0], c->gcfg[3][1]);
     pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
     if (l + 1 == NL) {  // the last MLP residual block and the final norm (E:1414-1417) for the head
       pmark(c, PT_ROWS, 1, 0);

@@ -6,10 +6,11 @@
 //   a = fma(hi(b_8+j), xo_8+j, a); r_j = fma(a, sc_g, r_j);   off = fma(sc_g, gsum_g, off)
 // over the groups g in order, and y = ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off.
 //
-// The lane mapping is transposed: a wave holds 64 consecutive output rows of one chain lane j
-// for MPL activation rows, so the activation operand of every FMA is the same for the whole
-// wave (one broadcast LDS read per group and row) and a block of 8 waves (j = 0..7) finishes
-// its 64 rows with one LDS exchange.  A block stages only its own MPL activation rows, so even
+// The lane mapping is transposed: a thread holds one output row of one chain lane j for MPL
+// activation rows, and the rows of a tile (TR = 64 or 32) are consecutive lanes, so the
+// activation operand of every FMA is the same for the TR lanes of a chain lane (a broadcast
+// LDS read per group and row) and a block of 8 TR threads (j = 0..7) finishes its TR rows with
+// one LDS exchange.  A block stages only its own MPL activation rows, so even
 // K = 6144 fits in one pass, and the launch has one block per (64-row tile, row subset): the
 // blocks of a tile are placed on the same XCD (round-robin block order), whose L2 then serves
 // the tile's weights to all of them.
@@ -17,10 +18,12 @@
 
 namespace g4v {
 
-constexpr int GT_THREADS = 512;  // 8 waves, wave j = chain lane j
 
 __constant__ uint64_t c_expf_tab_t[32] = G4V_EXPF_TABLE;
-constexpr int GT_B = 4;          // chunks per weight batch (two batches in flight)
+// chunks per weight batch (two batches in flight): 2 for three and four activation rows keeps
+// the kernel within 4 waves per SIMD, i.e. two 512-thread blocks per CU
+template <int MPL>
+constexpr int gt_batch() { return MPL >= 3 ? 2 : 4; }
 
 // re-laid wr[n][c][j] -> tw[n/64][c][j][n%64]; scales s[n][G] (uint4 = 8 groups) -> ts[n/64][c][n%64]
 __global__ void k_tile_w4(const uint4* __restrict__ wr, const uint4* __restrict__ s4, uint4* __restrict__ tw,
@@ -44,7 +47,9 @@ void launch_tile_w4(const uint4* wr, const uint16_t* s, uint4* tw, uint4* ts, in
   hipLaunchKernelGGL(k_tile_w4, dim3(grid), dim3(256), 0, st, wr, reinterpret_cast<const uint4*>(s), tw, ts, N, K);
 }
 
-// gate / up pair: tile t = gate rows 32t .. 32t+31, then up rows 32t .. 32t+31 (N each, N % 32 == 0)
+// gate / up pair: 64-row tile t holds, for pairs n = 32t .. 32t+31, rows [gate 16, up 16, gate 16,
+// up 16]: gate n at local row 32 (i / 16) + i % 16 and up n at 16 more (i = n - 32t), so every
+// 32-row half holds whole pairs (N each, N % 32 == 0)
 __global__ void k_tile_w4_pair(const uint4* __restrict__ wg, const uint4* __restrict__ sg,
                                const uint4* __restrict__ wu, const uint4* __restrict__ su, uint4* __restrict__ tw,
                                uint4* __restrict__ ts, int N, int K) {
@@ -56,8 +61,8 @@ __global__ void k_tile_w4_pair(const uint4* __restrict__ wg, const uint4* __rest
     const int c = (int)(nc % GC);
     const size_t r = nc / GC;  // paired row: tile r / 64, local row r % 64
     const size_t t = r >> 6, lr = r & 63;
-    const size_t n = t * 32 + (lr & 31);
-    const bool up = lr >= 32;
+    const size_t n = t * 32 + (lr >> 5) * 16 + (lr & 15);
+    const bool up = (lr & 16) != 0;
     const uint4 w = up ? wu[(n * GC + c) * 8 + j] : wg[(n * GC + c) * 8 + j];
     tw[((t * GC + c) * 8 + j) * 64 + lr] = w;
     if (j == 0) ts[(t * GC + c) * 64 + lr] = up ? su[n * GC + c] : sg[n * GC + c];
@@ -83,16 +88,20 @@ struct GemvTDev {
 // per-group accesses of the prologue over the banks), group sums [MPL][G], chain sums [MPL][8][64],
 // offsets [MPL][64], outputs of the gate/up epilogue [MPL][64]; the norm prologue adds its two
 // weight rows [2][H], partial sums [MPL][16] (double) and RMS factors [2][MPL]
-static size_t gemvt_lds(int mpl, int K, bool nrm) {
+static size_t gemvt_lds(int mpl, int K, bool nrm, int tr, bool mrg) {
   const int G = K / 32;
-  return (size_t)mpl * G * 9 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * 64 * 4 + (size_t)mpl * 64 * 4 * 2 +
+  return (size_t)mpl * G * 9 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * tr * 4 + (size_t)mpl * tr * 4 * 2 +
+         (mrg ? (size_t)mpl * NQ * (MAXT + 1) * 4 : 0) +
          (nrm ? (size_t)2 * H * 4 + (size_t)mpl * 16 * 8 + (size_t)2 * mpl * 4 : 0);
 }
 
 // MRG: the merge prologue (GemvTArgs::mrg_po), NRM: the norm prologue (GemvTArgs::nrm_mode);
 // variants of their own so that their registers do not weigh on the other launches
-template <int MPL, bool MRG, bool NRM>
-__global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
+// TR: rows per tile (64: a wave is 64 rows of one chain lane; 32: a wave is 32 rows of two
+// chain lanes); a block is the TR x 8 (row, chain lane) pairs of one tile, 8 TR threads
+template <int MPL, bool MRG, bool NRM, int TR>
+__global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
+  constexpr int NT = TR * 8;
   const GemvTArgs& a = d.a;
   const int K = a.K, G = K / 32, GC = K / 256, M = a.M;
   // block -> (tile, row subset); the tiles of XCD x (block % 8) are x, x + 8, ...
@@ -100,21 +109,25 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
   const int sub = kq % d.nsub, t = (kq / d.nsub) * 8 + xcd;
   if (t >= d.tiles[3]) return;
   const int m0 = sub * MPL;
-  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
+  // thread -> (chain lane j, row lane of the tile); rows of a 32-row tile are one half of a
+  // 64-row tile of the storage layout
+  const int j = threadIdx.x / TR, lane = threadIdx.x % TR;
   extern __shared__ float4 lds4[];
   float4* XL = lds4;                                         // [MPL][G][8]
   float* GSL = reinterpret_cast<float*>(XL + MPL * G * 9);  // [MPL][G]
   // float4 u = (row * G + group) * 8 + k of the rows is held at pad(u)
   auto pad = [](int u) { return u + (u >> 3); };
-  float* RL = GSL + MPL * G;                                 // [MPL][8][64]
-  float* OFL = RL + MPL * 8 * 64;                            // [MPL][64]
-  float* YL = OFL + MPL * 64;                                // [MPL][64]
+  float* RL = GSL + MPL * G;                                 // [MPL][8][TR]
+  float* OFL = RL + MPL * 8 * TR;                            // [MPL][TR]
+  float* YL = OFL + MPL * TR;                                // [MPL][TR]
 
   const int mi = (t >= d.tiles[1]) + (t >= d.tiles[2]);
   const W4Tile W = mi == 0 ? a.mat[0] : (mi == 1 ? a.mat[1] : a.mat[2]);
   const int tl = t - d.tiles[mi];
-  const uint4* wp = W.w + ((size_t)tl * GC * 8 + j) * 64 + lane;  // chunk c at + c * 512
-  const uint4* sp = W.s + (size_t)tl * GC * 64 + lane;             // chunk c at + c * 64
+  const int t64 = tl / (64 / TR), r64 = (tl % (64 / TR)) * TR + lane;  // storage tile and row
+  const uint4* wp = W.w + ((size_t)t64 * GC * 8 + j) * 64 + r64;  // chunk c at + c * 512
+  const uint4* sp = W.s + (size_t)t64 * GC * 64 + r64;             // chunk c at + c * 64
+  constexpr int GT_B = gt_batch<MPL>();
   uint4 wA[GT_B], sA[GT_B], wB[GT_B], sB[GT_B];
   auto load_batch = [&](uint4 (&w)[GT_B], uint4 (&s)[GT_B], int c0) {  // indices clamped
 #pragma unroll
@@ -124,54 +137,102 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
       s[b] = sp[(size_t)c * 64];
     }
   };
-  load_batch(wA, sA, 0);
+  // The prologue's own loads (activations, partials, residual rows) are issued first and the
+  // first weight batch right after them: the load counter retires in issue order, so the
+  // prologue then waits for its operands only, while the weights stream in behind it.
+  auto weights_after = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    load_batch(wA, sA, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
   // the block's activation rows m0 .. m0 + MPL - 1 (rows >= M staged as zeros, never stored)
   const int RW = G * 8;
   if constexpr (MRG) {
-    // E:1019-1059 per element of (row, head h): sc_t = libm expf(max_t - M0) over the splits
-    // with l_t > 0, l = sum_t (double) l_t sc_t, y = r16((fma chain over t of o_t sc_t) *
-    // (float)(1 / l)); thread u takes elements 4u .. 4u+3 (one head) and stores them staged
+    // E:1019-1059 per (row, head h): M0 = max of max_t over the splits with l_t > 0,
+    // sc_t = libm expf(max_t - M0), l = sum_t (double) l_t sc_t, inv = (float)(1 / l); then per
+    // element y = r16((fma chain over those t of o_t sc_t) * inv).  Thread f < MPL * NQ forms
+    // the factors of pair f once (SCL, -1 marks a split without positions); every thread then
+    // runs the chains of its elements 4u .. 4u+3 (one head) and stores them staged.
     const int T = a.mrg_T;
     float* XF = reinterpret_cast<float*>(XL);
-    for (int idx = threadIdx.x; idx < MPL * (K / 4); idx += GT_THREADS) {
-      const int q = idx / (K / 4), u = idx - q * (K / 4), m = min(m0 + q, M - 1);
-      const int h = (4 * u) / HD, i = (4 * u) % HD;
-      float pl[MAXT], pm[MAXT];
-      float4 po[MAXT];
+    float* SCL = YL + MPL * TR;            // [MPL][NQ][MAXT]
+    float* INVL = SCL + MPL * NQ * MAXT;   // [MPL][NQ]
+    constexpr int NI = MPL * (NQ * HD / 4) / NT;  // elements groups per thread (K = NQ * HD)
+    constexpr int PT = 8;                         // splits whose partials are prefetched
+    const int f = threadIdx.x;
+    float pl[MAXT], pm[MAXT];
+    if (f < MPL * NQ) {
+      const int m = min(m0 + f / NQ, M - 1), h = f % NQ;
 #pragma unroll
       for (int tt = 0; tt < MAXT; ++tt) {
         const size_t kk = ((size_t)tt * M + m) * NQ + h;
         pl[tt] = tt < T ? a.mrg_pl[kk] : 0.f;
         pm[tt] = tt < T ? a.mrg_pm[kk] : 0.f;
-        po[tt] = tt < T ? *reinterpret_cast<const float4*>(a.mrg_po + kk * HD + i) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
+    }
+    float4 po[NI][PT];
+    auto po_load = [&](int tb) {
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const int idx = threadIdx.x + it * NT, q = idx / (K / 4), u = idx - q * (K / 4);
+        const int m = min(m0 + q, M - 1), h = (4 * u) / HD, i = (4 * u) % HD;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+          const int tt = tb + k;
+          po[it][k] = tt < T ? *reinterpret_cast<const float4*>(a.mrg_po + (((size_t)tt * M + m) * NQ + h) * HD + i)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    };
+    po_load(0);
+    weights_after();
+    if (f < MPL * NQ) {
       float M0 = -1e30f;
 #pragma unroll
       for (int tt = 0; tt < MAXT; ++tt)
         if (tt < T && pl[tt] > 0) M0 = (M0 < pm[tt]) ? pm[tt] : M0;
       double l = 0;
-      float sc[MAXT];
 #pragma unroll
       for (int tt = 0; tt < MAXT; ++tt) {
-        sc[tt] = 0.f;
+        float sc = -1.f;
         if (tt < T && pl[tt] > 0) {
-          sc[tt] = libm_expf_neg(pm[tt] - M0, c_expf_tab_t);
-          l = fma((double)pl[tt], (double)sc[tt], l);
+          sc = libm_expf_neg(pm[tt] - M0, c_expf_tab_t);
+          l = fma((double)pl[tt], (double)sc, l);
+        }
+        SCL[f * MAXT + tt] = sc;
+      }
+      INVL[f] = (float)(1.0 / l);
+    }
+    __syncthreads();
+    float4 acc[NI];
+#pragma unroll
+    for (int it = 0; it < NI; ++it) acc[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int tb = 0; tb < T; tb += PT) {
+      if (tb) po_load(tb);
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const int idx = threadIdx.x + it * NT, q = idx / (K / 4), h = (4 * (idx - q * (K / 4))) / HD;
+        const float* scp = SCL + (q * NQ + h) * MAXT + tb;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+          const float sc = scp[k];
+          if (tb + k < T && sc >= 0.f) {
+            acc[it].x = fmaf(po[it][k].x, sc, acc[it].x);
+            acc[it].y = fmaf(po[it][k].y, sc, acc[it].y);
+            acc[it].z = fmaf(po[it][k].z, sc, acc[it].z);
+            acc[it].w = fmaf(po[it][k].w, sc, acc[it].w);
+          }
         }
       }
-      const float inv = (float)(1.0 / l);
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
-      for (int tt = 0; tt < MAXT; ++tt)
-        if (tt < T && pl[tt] > 0) {
-          acc.x = fmaf(po[tt].x, sc[tt], acc.x);
-          acc.y = fmaf(po[tt].y, sc[tt], acc.y);
-          acc.z = fmaf(po[tt].z, sc[tt], acc.z);
-          acc.w = fmaf(po[tt].w, sc[tt], acc.w);
-        }
+    for (int it = 0; it < NI; ++it) {
+      const int idx = threadIdx.x + it * NT, q = idx / (K / 4), u = idx - q * (K / 4);
+      const int h = (4 * u) / HD;
+      const float inv = INVL[q * NQ + h];
       const bool live = m0 + q < M;
-      const float yv[4] = {acc.x, acc.y, acc.z, acc.w};
+      const float yv[4] = {acc[it].x, acc[it].y, acc[it].z, acc[it].w};
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
         const int si = staged_index(4 * u + cc);
@@ -183,8 +244,8 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
     // branch zero) for the block's rows; RMS factors from the 16-lane double sum of squares
     // (E:326-345).  XL takes the rows in plain order, is normalised in place and finally
     // permuted in place into the staged order, one thread per (row, group).
-    constexpr int RW4 = H / 4, NV = (MPL * RW4 + GT_THREADS - 1) / GT_THREADS;
-    float* W12 = YL + MPL * 64;                                   // [2][H]
+    constexpr int RW4 = H / 4, NV = (MPL * RW4 + NT - 1) / NT, NW = (RW4 + NT - 1) / NT;
+    float* W12 = YL + MPL * TR;                                   // [2][H]
     double* RED = reinterpret_cast<double*>(W12 + 2 * H);        // [MPL][16]
     float* RR = reinterpret_cast<float*>(RED + MPL * 16);         // [2][MPL]
     const float4* o4 = reinterpret_cast<const float4*>(a.nrm_o);
@@ -192,25 +253,34 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
     float4 ov[NV], xv[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {  // clamped: rows past M read row M - 1 and are zeroed
-      const int u = min((int)threadIdx.x + k * GT_THREADS, MPL * RW4 - 1), q = u / RW4;
+      const int u = min((int)threadIdx.x + k * NT, MPL * RW4 - 1), q = u / RW4;
       const size_t src = (size_t)min(m0 + q, M - 1) * RW4 + (u - q * RW4);
       ov[k] = o4[src];
       xv[k] = x4[src];
     }
-    const int wi = min((int)threadIdx.x, RW4 - 1);
-    const float4 w1 = reinterpret_cast<const float4*>(a.nrm_w1)[wi];
-    const float4 w2 = reinterpret_cast<const float4*>(a.nrm_w2)[wi];
+    float4 w1[NW], w2[NW];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+      const int wi = min((int)threadIdx.x + k * NT, RW4 - 1);
+      w1[k] = reinterpret_cast<const float4*>(a.nrm_w1)[wi];
+      w2[k] = reinterpret_cast<const float4*>(a.nrm_w2)[wi];
+    }
+    weights_after();
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int u = threadIdx.x + k * GT_THREADS;
+      const int u = threadIdx.x + k * NT;
       if (u < MPL * RW4) {
         const float4 o = ov[k];
         XL[pad(u)] = keep4(m0 + u / RW4 < M, make_float4(r16(o.x), r16(o.y), r16(o.z), r16(o.w)));
       }
     }
-    if ((int)threadIdx.x < RW4) {
-      reinterpret_cast<float4*>(W12)[threadIdx.x] = w1;
-      reinterpret_cast<float4*>(W12 + H)[threadIdx.x] = w2;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+      const int wi = threadIdx.x + k * NT;
+      if (wi < RW4) {
+        reinterpret_cast<float4*>(W12)[wi] = w1[k];
+        reinterpret_cast<float4*>(W12 + H)[wi] = w2[k];
+      }
     }
     __syncthreads();
     const float* XP = reinterpret_cast<const float*>(XL);
@@ -253,7 +323,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
     const float scal = a.nrm_scalar;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int u = threadIdx.x + k * GT_THREADS;
+      const int u = threadIdx.x + k * NT;
       if (u < MPL * RW4) {
         const int q = u / RW4, c4 = u - q * RW4;
         const float r1 = RR[q];
@@ -270,7 +340,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
     rms_rows(RR + MPL);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {  // xa in place, plain order
-      const int u = threadIdx.x + k * GT_THREADS;
+      const int u = threadIdx.x + k * NT;
       if (u < MPL * RW4) {
         const int q = u / RW4, c4 = u - q * RW4;
         const float r2 = RR[MPL + q];
@@ -281,7 +351,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {  // staged order + group sums
+    for (int idx = threadIdx.x; idx < MPL * G; idx += NT) {  // staged order + group sums
       float4* b4 = XL + (size_t)idx * 9;  // row q = idx / G, group g = idx % G: 8 float4 in plain order
       float4 r[8];
 #pragma unroll
@@ -295,19 +365,39 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
       GSL[idx] = sum;
     }
   } else {
-    for (int u = threadIdx.x; u < MPL * RW; u += GT_THREADS) {
-      const int q = u / RW, m = m0 + q;
-      XL[pad(u)] = keep4(m < M, a.xs[(size_t)min(m, M - 1) * RW + (u - q * RW)]);
+    // K <= 6144: at most MPL * 1536 staged float4 and MPL * 192 group sums per block
+    constexpr int NX = (MPL * 1536 + NT - 1) / NT, NG = (MPL * 192 + NT - 1) / NT;
+    float4 xr[NX];
+    float gr[NG];
+#pragma unroll
+    for (int k = 0; k < NX; ++k) {
+      const int u = min((int)threadIdx.x + k * NT, MPL * RW - 1), q = u / RW;
+      xr[k] = a.xs[(size_t)min(m0 + q, M - 1) * RW + (u - q * RW)];
+    }
+    if (a.gs) {
+#pragma unroll
+      for (int k = 0; k < NG; ++k) {
+        const int idx = min((int)threadIdx.x + k * NT, MPL * G - 1), q = idx / G;
+        gr[k] = a.gs[(size_t)min(m0 + q, M - 1) * G + (idx - q * G)];
+      }
+    }
+    weights_after();
+#pragma unroll
+    for (int k = 0; k < NX; ++k) {
+      const int u = threadIdx.x + k * NT;
+      if (u < MPL * RW) XL[pad(u)] = keep4(m0 + u / RW < M, xr[k]);
+    }
+    if (a.gs) {
+#pragma unroll
+      for (int k = 0; k < NG; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        if (idx < MPL * G) GSL[idx] = m0 + idx / G < M ? gr[k] : 0.f;
+      }
     }
   }
-  if (a.gs && !MRG && !NRM)
-    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
-      const int q = idx / G, m = m0 + q;
-      GSL[idx] = m < M ? a.gs[(size_t)min(m, M - 1) * G + (idx - q * G)] : 0.f;
-    }
   __syncthreads();
   if ((!a.gs || MRG) && !NRM) {  // W:22 each group's sequential sum, from the staged copy
-    for (int idx = threadIdx.x; idx < MPL * G; idx += GT_THREADS) {
+    for (int idx = threadIdx.x; idx < MPL * G; idx += NT) {
       const float4* q4 = XL + (size_t)idx * 9;
       float4 v[8];
 #pragma unroll
@@ -380,66 +470,73 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_t(GemvTDev d) {
 
   // the 8 chain lanes of each (row, output) meet in LDS: ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off
 #pragma unroll
-  for (int q = 0; q < MPL; ++q) RL[(q * 8 + j) * 64 + lane] = row[q];
-  if (j < MPL) OFL[j * 64 + lane] = off;
+  for (int q = 0; q < MPL; ++q) RL[(q * 8 + j) * TR + lane] = row[q];
+  if (j < MPL) OFL[j * TR + lane] = off;
   __syncthreads();
-  if ((int)threadIdx.x < MPL * 64) {
-    const int q = threadIdx.x >> 6, m = m0 + q;
-    const float* r = RL + q * 512 + lane;
-    const float y = (((r[0] + r[256]) + (r[64] + r[320])) + ((r[128] + r[384]) + (r[192] + r[448]))) -
-                    8.f * OFL[q * 64 + lane];
+  if ((int)threadIdx.x < MPL * TR) {
+    const int q = threadIdx.x / TR, rl = threadIdx.x % TR, m = m0 + q;
+    const float* r = RL + q * 8 * TR + rl;
+    const float y = (((r[0] + r[4 * TR]) + (r[TR] + r[5 * TR])) + ((r[2 * TR] + r[6 * TR]) + (r[3 * TR] + r[7 * TR]))) -
+                    8.f * OFL[q * TR + rl];
     if (!a.gateup) {
-      if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * 64 + lane] = y;
+      if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * TR + rl] = y;
     } else {
-      YL[q * 64 + lane] = y;
+      YL[q * TR + rl] = y;
     }
   }
   if (a.gateup) {  // E:292-299 act = rbf8(rbf8(gelu8(rbf8 g)) * rbf8 u), written staged
     __syncthreads();
-    if ((int)threadIdx.x < MPL * 32) {
-      const int q = threadIdx.x >> 5, l = threadIdx.x & 31, m = m0 + q;
-      const float g = YL[q * 64 + l], u = YL[q * 64 + 32 + l];
+    if ((int)threadIdx.x < MPL * TR / 2) {
+      // pair p of the tile: gate at local row 32 (p / 16) + p % 16, up 16 rows after it
+      const int q = threadIdx.x / (TR / 2), p = threadIdx.x % (TR / 2), m = m0 + q;
+      const int gl = (p >> 4) * 32 + (p & 15);
+      const float g = YL[q * TR + gl], u = YL[q * TR + gl + 16];
       const float act = r16(r16(gelu8(r16(g))) * r16(u));
-      if (m < M) a.y[0][(size_t)m * a.ldy[0] + staged_index(tl * 32 + l)] = act;
+      if (m < M) a.y[0][(size_t)m * a.ldy[0] + staged_index(tl * (TR / 2) + p)] = act;
     }
   }
 }
 
-template <int MPL>
+template <int MPL, int TR>
 static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
-  const size_t lds = gemvt_lds(MPL, d.a.K, d.a.nrm_mode != 0);
+  const size_t lds = gemvt_lds(MPL, d.a.K, d.a.nrm_mode != 0, TR, d.a.mrg_po != nullptr);
   if (d.a.mrg_po) {
-    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false>), dim3(grid), dim3(GT_THREADS), lds, st, d);
+    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false, TR>), dim3(grid), dim3(TR * 8), lds, st, d);
   } else if (d.a.nrm_mode) {
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, true>), dim3(grid), dim3(GT_THREADS), lds, st, d);
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR>), dim3(grid), dim3(TR * 8), lds, st, d);
   } else {
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, false>), dim3(grid), dim3(GT_THREADS), lds, st, d);
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR>), dim3(grid), dim3(TR * 8), lds, st, d);
   }
 }
 
-// mpl: activation rows per block (1 to 4; 0 picks)
-int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl) {
+// mpl: activation rows per block (1 to 4); tr: rows per tile (64 or 32)
+int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
+  if (a.K > 6144 || a.K % 256) return 0;  // the prologue register staging holds K <= 6144
+  if (tr != 32) tr = 64;
+  if (mpl < 1) mpl = 1;
+  if (mpl > 4) mpl = 4;
+  if (a.mrg_po && mpl > 2) mpl = 2;  // the merge variant exists for one and two rows
   GemvTDev d{};
   d.a = a;
   d.tiles[0] = 0;
-  for (int i = 0; i < 3; ++i) d.tiles[i + 1] = d.tiles[i] + (a.gateup && i ? 0 : a.mat[i].N * (a.gateup ? 2 : 1) / 64);
+  for (int i = 0; i < 3; ++i) d.tiles[i + 1] = d.tiles[i] + (a.gateup && i ? 0 : a.mat[i].N * (a.gateup ? 2 : 1) / tr);
   const int T = d.tiles[3], tg = (T + 7) / 8;
-  if (mpl <= 0) {  // the fewest rows per block that keep the launch within one block per CU, else 4
-    mpl = 4;
-    for (int c : {1, 2})
-      if (8 * tg * ((a.M + c - 1) / c) <= 256) {
-        mpl = c;
-        break;
-      }
-  }
-  if (a.mrg_po && mpl > 2) mpl = 2;  // the merge variant exists for one and two rows
   d.nsub = (a.M + mpl - 1) / mpl;
   const int grid = 8 * tg * d.nsub;
-  switch (mpl) {
-    case 1: launch_mpl<1>(d, st, grid); break;
-    case 2: launch_mpl<2>(d, st, grid); break;
-    case 3: launch_mpl<3>(d, st, grid); break;
-    default: launch_mpl<4>(d, st, grid); break;
+  if (tr == 64) {
+    switch (mpl) {
+      case 1: launch_mpl<1, 64>(d, st, grid); break;
+      case 2: launch_mpl<2, 64>(d, st, grid); break;
+      case 3: launch_mpl<3, 64>(d, st, grid); break;
+      default: launch_mpl<4, 64>(d, st, grid); break;
+    }
+  } else {
+    switch (mpl) {
+      case 1: launch_mpl<1, 32>(d, st, grid); break;
+      case 2: launch_mpl<2, 32>(d, st, grid); break;
+      case 3: launch_mpl<3, 32>(d, st, grid); break;
+      default: launch_mpl<4, 32>(d, st, grid); break;
+    }
   }
   return grid;
 }

@@ -82,7 +82,8 @@ struct W4Tile {
   int N;
 };
 void launch_tile_w4(const uint4* wr, const uint16_t* s, uint4* tw, uint4* ts, int N, int K, hipStream_t st);
-// gate / up pair of N rows each: tile t holds gate rows 32t..32t+31 then up rows 32t..32t+31
+// gate / up pair of N rows each: 64-row tile t holds pairs 32t..32t+31 as 16 gate rows, their 16
+// up rows, the next 16 gate rows and their 16 up rows
 void launch_tile_w4_pair(const uint4* wg, const uint16_t* sg, const uint4* wu, const uint16_t* su, uint4* tw,
                          uint4* ts, int N, int K, hipStream_t st);
 
@@ -131,8 +132,9 @@ void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, con
                       float* y, int M, int N, int K, int ldy, hipStream_t st);
 int w4a8_mpad(int M);  // rows the quantised operand holds for M rows
 
-// returns the grid size
-int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl = 0);
+// mpl: activation rows per block (1..4, 2 at most with the merge prologue); tr: rows per tile
+// (64 or 32).  Returns the grid size (0: K unsupported, nothing launched).
+int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr);
 // returns the grid size used (the number of EPI_SCREEN partials per activation row)
 int launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
 // grid launch_gemv would use
