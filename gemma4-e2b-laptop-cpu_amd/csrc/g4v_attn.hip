@@ -72,17 +72,48 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   __shared__ __align__(16) uint16_t knew[STEP ? MAXM : 1][HD];
   __shared__ __align__(16) uint16_t vnew[STEP ? MAXM : 1][HD];
   const int t = blockIdx.x, m = blockIdx.y, h0 = blockIdx.z * ATT_HB;
-  // E:1325-1326 geometry: every thread reads the (uniform) parameters itself, no serial set-up
-  int M, kmin, kmax, lo_m, pos_m, sl_m, sh_m;
+  const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
+  const int i2 = e & (HD / 2 - 1);
+  // Every load that does not depend on the step geometry is issued first, together with the
+  // geometry itself (one round trip): the query heads and, in a verify pass, the raw key/value
+  // rows of the pass (all of them: the split that holds some is only known from the
+  // geometry), their RoPE factors and the norm weights.
+  float qv[ATT_HB];
+#pragma unroll
+  for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
+  float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {}, qw = 0.f, kw = 0.f, cq = 0.f, sq = 0.f;
   if (STEP) {
+#pragma unroll
+    for (int r = 0; r < MAXM; ++r) {
+      kv[0][r] = P.kraw[(size_t)r * HD + e];
+      kv[1][r] = P.vraw[(size_t)r * HD + e];
+      ck[r] = P.ropestep[(size_t)r * HD + i2];
+      sk[r] = P.ropestep[(size_t)r * HD + HD / 2 + i2];
+    }
+    qw = P.qn[e];
+    kw = P.kn[e];
+    cq = P.ropestep[(size_t)m * HD + i2];
+    sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
+  }
+  // E:1325-1326 geometry: every thread reads the (uniform) parameters itself, no serial set-up;
+  // all fields are read unconditionally so that they arrive together
+  int M, kmin, kmax, lo_m, pos_m, sl_m, sh_m, pos0 = 0;
+  if (STEP) {
+    int rp[MAXM];
+#pragma unroll
+    for (int r = 0; r < MAXM; ++r) rp[r] = sp->rope[r];
+    const int rpm = sp->rope[m];
     M = sp->M;
-    kmax = sp->pos0 + M - 1;
-    kmin = kmax;
-    for (int r = 0; r < M; ++r) kmin = min(kmin, sliding ? max(0, sp->rope[r] - 511) : 0);
-    pos_m = sp->pos0 + m;
-    lo_m = sliding ? max(0, sp->rope[m] - 511) : 0;
+    pos0 = sp->pos0;
     sl_m = sp->skip_lo[m];
     sh_m = sp->skip_hi[m];
+    kmax = pos0 + M - 1;
+    kmin = kmax;
+#pragma unroll
+    for (int r = 0; r < MAXM; ++r)
+      if (r < M) kmin = min(kmin, sliding ? max(0, rp[r] - 511) : 0);
+    pos_m = pos0 + m;
+    lo_m = sliding ? max(0, rpm - 511) : 0;
   } else {
     M = gin.M;
     kmin = gin.kmin;
@@ -109,11 +140,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     return bits_in(max(lo_m, c0), min(pos_m, c1 - 1), pb) & ~bits_in(sl_m, sh_m, pb);
   };
   // The split is visited in whole blocks of the value cache: tile s covers positions
-  // [pb0 + 32 s, pb0 + 32 s + 32); positions outside [c0, c1) are masked.  One stream of
-  // tile loads, ATT_RING in flight: entry s < NT is key tile s, entries NT <= s < NTp are
-  // empty (NTp rounds NT up to the ring size, so value tile v is entry NTp + v in ring slot
-  // v % ATT_RING), entry NTp + v is value tile v; the value tiles are thus in flight while the
-  // last key tiles and the softmax run.
+  // [pb0 + 32 s, pb0 + 32 s + 32); positions outside [c0, c1) are masked.  Two streams of
+  // tile loads, ATT_RING tiles each in flight from the start: key tile s in slot s % ATT_RING
+  // of the key ring, value tile v in slot v % ATT_RING of the value ring (a split of up to
+  // ATT_RING tiles, every sliding-window split, has all of its tiles in flight at once).
   const int pb0 = c0 & ~(ATT_TILE - 1);
   const int NT = PP > 0 ? ((c1 - 1) >> 5) - (c0 >> 5) + 1 : 0;
   const int NTp = (NT + ATT_RING - 1) / ATT_RING * ATT_RING;
@@ -123,50 +153,30 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   // Every stream entry issues its four loads, so each ring slot has exactly one definition
   // per tile (no merges that would make the compiler wait on loads still in flight): empty
   // entries and entries past the stream load a row they never use.
-  uint4 ring[ATT_RING][4];
+  uint4 kring[ATT_RING][4], vring[ATT_RING][4];
   const uint16_t* kbase = P.KC + l * 32;
   const uint16_t* vbase = P.VC + threadIdx.x * 32;
-  auto issue = [&](int s, uint4 (&r)[4]) {
-    const bool key = s < NT, val = s >= NTp && s < NTp + NT;  // uniform
+  auto issue_k = [&](int s, uint4 (&r)[4]) {  // entries past the split reload its last row
     const size_t koff = (size_t)max(min(pb0 + min(s, NT - 1) * ATT_TILE + ps, c1 - 1), 0) * HD;
-    const size_t voff = (size_t)((pb0 >> 5) + max(min(s - NTp, NT - 1), 0)) * (ATT_TILE * HD);
-    const uint4* src = reinterpret_cast<const uint4*>(key || !val ? kbase + koff : vbase + voff);
+    const uint4* src = reinterpret_cast<const uint4*>(kbase + koff);
 #pragma unroll
     for (int c = 0; c < 4; ++c) r[c] = src[c];
   };
-  // every global load of the prologue in flight at once: the query heads, the first tiles and,
-  // in a verify pass, the raw rows of the pass that fall in this split
-  const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
-  float qv[ATT_HB];
+  auto issue_v = [&](int v, uint4 (&r)[4]) {  // entries past the split reload its last block
+    const size_t voff = (size_t)((pb0 >> 5) + max(min(v, NT - 1), 0)) * (ATT_TILE * HD);
+    const uint4* src = reinterpret_cast<const uint4*>(vbase + voff);
 #pragma unroll
-  for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
+    for (int c = 0; c < 4; ++c) r[c] = src[c];
+  };
   // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1); they are the
   // split's last positions
-  const int pos0 = STEP ? sp->pos0 : 0;
   const int rn0 = STEP ? max(c0 - pos0, 0) : 0, rn1 = STEP ? min(c1 - pos0, M) : 0;
-  // verify pass: the raw rows, the norm weights and this thread's RoPE factors are loaded
-  // before the tiles (the in-order load counter then lets them be used while tiles land)
-  const int i2 = e & (HD / 2 - 1);
-  float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {}, qw = 0.f, kw = 0.f, cq = 0.f, sq = 0.f;
-  if (STEP) {
-    if (rn0 < rn1)  // only the splits holding rows of the pass
+  __builtin_amdgcn_sched_barrier(0);  // keep the prologue loads ahead of the tile loads
 #pragma unroll
-      for (int r = 0; r < MAXM; ++r) {
-        const int rr = (r >= rn0 && r < rn1) ? r : rn0;
-        kv[0][r] = P.kraw[(size_t)rr * HD + e];
-        kv[1][r] = P.vraw[(size_t)rr * HD + e];
-        ck[r] = P.ropestep[(size_t)rr * HD + i2];
-        sk[r] = P.ropestep[(size_t)rr * HD + HD / 2 + i2];
-      }
-    qw = P.qn[e];
-    kw = P.kn[e];
-    cq = P.ropestep[(size_t)m * HD + i2];
-    sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
+  for (int k = 0; k < ATT_RING; ++k) {  // also when the split is empty: no paths with fewer
+    issue_k(k, kring[k]);               // loads in flight
+    issue_v(k, vring[k]);
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the tile loads
-#pragma unroll
-  for (int k = 0; k < ATT_RING; ++k) issue(k, ring[k]);  // also when the split is empty: no paths
-                                                          // with fewer loads in flight
   __builtin_amdgcn_sched_barrier(0);
   if (STEP) {
     // E:1307-1324 on the block's query heads and the pass's key/value rows of this split:
@@ -232,8 +242,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 #pragma unroll
     for (int i = 0; i < 32; ++i) qr[hh][i] = qs[hh][l][i];
 
-  // sweep 1: scores (E:750-816) straight from the fetched key rows; ring slot k holds stream
-  // entry s = base + k.  Lane group ps scores position pb + ps (positions outside the split
+  // sweep 1: scores (E:750-816) straight from the fetched key rows; key ring slot k holds
+  // key tile s = base + k.  Lane group ps scores position pb + ps (positions outside the split
   // from a clamped row: their scores are never used).
   for (int base = 0; base < NTp; base += ATT_RING)
 #pragma unroll
@@ -241,7 +251,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     const int s = base + k;
     const int pb = pb0 + s * ATT_TILE, p = pb + ps;
     if (s < NT) {  // uniform; otherwise an empty entry
-      uint4 kr[4] = {ring[k][0], ring[k][1], ring[k][2], ring[k][3]};
+      uint4 kr[4] = {kring[k][0], kring[k][1], kring[k][2], kring[k][3]};
       if (STEP && pb + ATT_TILE > pos0) {  // uniform: the tile may hold rows of the pass (in LDS)
         const bool own = p >= pos0 && p < c1;
         const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][l * 32]);
@@ -272,7 +282,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     }
     // the slot's next entry, once its current one is consumed (the loop then carries each
     // slot in one register set: no copies, which would wait for loads in flight)
-    issue(s + ATT_RING, ring[k]);
+    issue_k(s + ATT_RING, kring[k]);
   }
   __syncthreads();
   // the running max over the allowed positions only (max is order free)
@@ -304,7 +314,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   }
   __syncthreads();
   // sweep 2: o_i = fma chain over positions (E:826-875) straight from the fetched value
-  // blocks; value tile v is stream entry NTp + v in ring slot v % ATT_RING.  A masked or
+  // blocks; value ring slot k holds value tile s = base + k.  A masked or
   // padding position (weight 0) is given value +0: fma(0, 0, o) = o exactly (o is never -0),
   // which is what skipping it in the reference leaves.  The pass's
   // rows are the split's last positions: the register pass leaves them out and they follow
@@ -326,10 +336,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     const int s = base + k;
     const int pb = pb0 + s * ATT_TILE;
     if (s < NT) {  // uniform; otherwise an entry past the split
-      const uint32_t vw[16] = {ring[k][0].x, ring[k][0].y, ring[k][0].z, ring[k][0].w,
-                               ring[k][1].x, ring[k][1].y, ring[k][1].z, ring[k][1].w,
-                               ring[k][2].x, ring[k][2].y, ring[k][2].z, ring[k][2].w,
-                               ring[k][3].x, ring[k][3].y, ring[k][3].z, ring[k][3].w};
+      const uint32_t vw[16] = {vring[k][0].x, vring[k][0].y, vring[k][0].z, vring[k][0].w,
+                               vring[k][1].x, vring[k][1].y, vring[k][1].z, vring[k][1].w,
+                               vring[k][2].x, vring[k][2].y, vring[k][2].z, vring[k][2].w,
+                               vring[k][3].x, vring[k][3].y, vring[k][3].z, vring[k][3].w};
       const bool full = full_tile(pb);
       const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb) & (STEP ? ~bits_in(pos0, pos0 + MAXM, pb) : 0xFFFFFFFFu);
       auto sweep = [&](const bool masked) {
@@ -371,7 +381,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     }
     // the slot's next entry (past the stream it reloads the last block): every path through
     // the loop issues the same loads, so the wait for a tile never has to cover younger ones
-    issue(NTp + s + ATT_RING, ring[k]);
+    issue_v(s + ATT_RING, vring[k]);
   }
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];

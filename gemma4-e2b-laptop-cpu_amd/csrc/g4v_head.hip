@@ -75,14 +75,41 @@ __global__ void k_head_select(HeadScratch hs, int MT, int V, const int* active) 
   __shared__ float thr[MAXM];
   if (threadIdx.x < MA) thr[threadIdx.x] = hs.thr[threadIdx.x];
   __syncthreads();
+  // One counter update per block and row: the block counts its survivors, reserves that many
+  // slots with one atomic, and writes them there (the list order is free: the rescore and the
+  // tie rule do not depend on it).  The block covers a contiguous range of rows.
+  __shared__ int wtot[8], base_s;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int per = (V + gridDim.x - 1) / gridDim.x;
+  const int n0 = blockIdx.x * per, n1 = min(V, n0 + per);
   for (int m = 0; m < MA; ++m) {
     const float* U = hs.u + (size_t)m * V;
-    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
-      if (U[n] >= thr[m]) {
-        const int p = atomicAdd(&hs.cnt[m], 1);
-        if (p < HEAD_LIMIT) hs.list[(size_t)m * HEAD_LIMIT + p] = n;
-      }
+    const float tm = thr[m];
+    int c = 0;
+    for (int n = n0 + threadIdx.x; n < n1; n += blockDim.x) c += U[n] >= tm;
+    int inc = c;  // inclusive scan within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(inc, o);
+      if (lane >= o) inc += v;
     }
+    if (lane == 63) wtot[wv] = inc;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < nw; ++w) {
+      before += w < wv ? wtot[w] : 0;
+      total += wtot[w];
+    }
+    if (threadIdx.x == 0) base_s = total ? atomicAdd(&hs.cnt[m], total) : 0;
+    __syncthreads();
+    int p = base_s + before + inc - c;
+    if (c)
+      for (int n = n0 + threadIdx.x; n < n1; n += blockDim.x)
+        if (U[n] >= tm) {
+          if (p < HEAD_LIMIT) hs.list[(size_t)m * HEAD_LIMIT + p] = n;
+          ++p;
+        }
+    __syncthreads();  // wtot / base_s are reused by the next row
   }
 }
 
@@ -458,7 +485,7 @@ void head_run(const HeadRun& r, hipStream_t st) {
     thr_lds = true;
   }
   hipLaunchKernelGGL(k_head_thr, dim3(1), dim3(THR_THREADS), 65536 * 2, st, r.hs, r.lut, MT, nb, r.active);
-  hipLaunchKernelGGL(k_head_select, dim3(grid_for(V, 256, 2048)), dim3(256), 0, st, r.hs, MT, V, r.active);
+  hipLaunchKernelGGL(k_head_select, dim3(std::min(256, (V + 255) / 256)), dim3(256), 0, st, r.hs, MT, V, r.active);
   mark(PT_HEAD_SELECT, 0, (double)V * 4 * MT);
   mark(PT_HEAD_RESCORE, 1, 0);
   hipLaunchKernelGGL(k_head_rescore, dim3(256), dim3(256), head_lds(MT), st, r.hs, r.hd, r.h, MT, r.active);
