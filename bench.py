@@ -27,6 +27,23 @@ HBM_PEAK_GBS = 8000.0
 V, NL, I, CTXCAP, NCTX, SEED, NA, NB, NSPLIT = 262144, 35, 6144, 4096, 2048, 1, 3, 3, 8
 
 
+def hbm_traffic(cls):
+    """bytes read + written per launch of kernel class `cls`, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs summarised in profiles/hbm_traffic.md (copy-kernel calibrated); None when
+    the class was not measured"""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0] == cls:
+            try:
+                return int(cells[4].replace(",", "")) + int(cells[5].replace(",", ""))
+            except ValueError:
+                return None
+    return None
+
+
 def load_g4v():
     spec = importlib.util.spec_from_file_location("g4v", os.path.join(ROOT, "gemma4-e2b-laptop-cpu_amd", "g4v.py"))
     mod = importlib.util.module_from_spec(spec)
@@ -155,7 +172,7 @@ def main():
                    "verify_step_us": round(ms_per_step * 1e3, 1), "tokens_per_step": round(tokens / args.steps, 3),
                    "device": info["name"]},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(dominant),
                      "launch_us": round(per_launch_ms * 1e3, 2), "bytes_per_launch": int(per_launch_bytes),
                      "timing": timing},
         "kernel_classes_us_per_step": classes,
