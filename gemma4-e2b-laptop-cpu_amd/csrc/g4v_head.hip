@@ -184,7 +184,8 @@ __global__ __launch_bounds__(256) void k_head_rescore(HeadScratch hs, HeadDev hd
 }
 
 // full head for the rows whose survivor count exceeds the limit (E:1489-1498); the dec16 row
-// is read once for all MT activation rows
+// is read once for all MT activation rows.  This pass stores each row's main dot (X3:83-107,
+// before the exception deltas); k_head_exc then adds the deltas in order and rounds.
 template <int MT>
 __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, const float* __restrict__ h,
                                                    int V, const int* active) {
@@ -202,9 +203,6 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
   if (!any) return;
   stage_h(h, MT, XH, XR);
   const int j = threadIdx.x & 7, slot = threadIdx.x >> 3, nslots = blockDim.x >> 3;
-  float vrun[MT];  // running max of this thread's logits (max is order free)
-#pragma unroll
-  for (int m = 0; m < MT; ++m) vrun[m] = -INFINITY;
   for (int n0 = blockIdx.x * nslots; n0 < V; n0 += gridDim.x * nslots) {
     const int n = n0 + slot;
     const bool ok = n < V;
@@ -241,15 +239,62 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
       y = y + __shfl_xor(y, 4, 8);
       y = y + __shfl_xor(y, 1, 8);
       y = y + __shfl_xor(y, 2, 8);
-      if (j == 0 && ok) {
-        for (int e = hd.exc_ptr[nn]; e < hd.exc_ptr[nn + 1]; ++e) y = fmaf(hd.exc_del[e], XR[m * H + hd.exc_col[e]], y);
-        const float v = r16(y);
+      if (j == 0 && ok) hs.u[(size_t)m * V + n] = y;
+    }
+  }
+}
+
+// X3:103 / E:565 the exception deltas of each row after its main dot, in list order, then the
+// bf16 rounding of the logit (E:1494); one thread per row.  One partial max per block and row
+// (reduced by the tie kernel).
+template <int MT>
+__global__ __launch_bounds__(256) void k_head_exc(HeadScratch hs, HeadDev hd, const float* __restrict__ h, int V,
+                                                  const int* active) {
+  if (active && *active == 0) return;
+  extern __shared__ float4 lds4[];
+  float4* XH = lds4;
+  float* XR = reinterpret_cast<float*>(lds4 + MT * 48 * 8);
+  bool any = false;
+  bool fb[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    fb[m] = hs.cnt[m] > HEAD_LIMIT;
+    any |= fb[m];
+  }
+  if (!any) return;
+  stage_h(h, MT, XH, XR);
+  float vrun[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) vrun[m] = -INFINITY;
+  for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < V; n += gridDim.x * blockDim.x) {
+    const int e0 = hd.exc_ptr[n], e1 = hd.exc_ptr[n + 1];
+    float y[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) y[m] = fb[m] ? hs.u[(size_t)m * V + n] : 0.f;
+    for (int e = e0; e < e1; e += 4) {  // four entries per round trip, applied in order
+      float dl[4];
+      int cl[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int ek = min(e + k, e1 - 1);
+        dl[k] = hd.exc_del[ek];
+        cl[k] = hd.exc_col[ek];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (e + k < e1) {
+#pragma unroll
+          for (int m = 0; m < MT; ++m) y[m] = fmaf(dl[k], XR[m * H + cl[k]], y[m]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if (fb[m]) {
+        const float v = r16(y[m]);
         hs.u[(size_t)m * V + n] = v;
         vrun[m] = fmaxf(vrun[m], v);
       }
-    }
   }
-  // one partial max per block and row (reduced by the tie kernel)
   __shared__ float red[256 / 64][MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
@@ -498,9 +543,16 @@ void head_run(const HeadRun& r, hipStream_t st) {
     case 3: hipLaunchKernelGGL(k_head_full<3>, gf, dim3(256), head_lds(3), st, r.hs, r.hd, r.h, V, r.active); break;
     default: hipLaunchKernelGGL(k_head_full<4>, gf, dim3(256), head_lds(4), st, r.hs, r.hd, r.h, V, r.active); break;
   }
+  const dim3 ge(grid_for(V, 256, cap));
+  switch (MT) {
+    case 1: hipLaunchKernelGGL(k_head_exc<1>, ge, dim3(256), head_lds(1), st, r.hs, r.hd, r.h, V, r.active); break;
+    case 2: hipLaunchKernelGGL(k_head_exc<2>, ge, dim3(256), head_lds(2), st, r.hs, r.hd, r.h, V, r.active); break;
+    case 3: hipLaunchKernelGGL(k_head_exc<3>, ge, dim3(256), head_lds(3), st, r.hs, r.hd, r.h, V, r.active); break;
+    default: hipLaunchKernelGGL(k_head_exc<4>, ge, dim3(256), head_lds(4), st, r.hs, r.hd, r.h, V, r.active); break;
+  }
   mark(PT_HEAD_FULL, 0, r.full_bytes);
   mark(PT_HEAD_TIE, 1, 0);
-  hipLaunchKernelGGL(k_head_tie, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, r.hs, r.lut, MT, V, (int)gf.x,
+  hipLaunchKernelGGL(k_head_tie, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, r.hs, r.lut, MT, V, (int)ge.x,
                      r.active);
   mark(PT_HEAD_TIE, 0, 0);
 }
