@@ -100,6 +100,10 @@ struct g4v_ctx {
   VerifyResultDev* res_host = nullptr;
   // attention standalone
   DBuf ak, av, aq, ao;
+  // prompt-lookup history (prompt + committed tokens) and the lookup's result words
+  DBuf hist, plout;
+  int hist_len = 0, hist_cap = 0;
+  int* pl_host = nullptr;
   // per-kernel-class HIP-event timing on the library stream (g4v_profile)
   unsigned prof_mask = 0;
   std::vector<hipEvent_t> evpool;
@@ -135,6 +139,7 @@ struct g4v_ctx {
     for (hipEvent_t e : evpool) (void)hipEventDestroy(e);
     if (step_host) (void)hipHostFree(step_host);
     if (res_host) (void)hipHostFree(res_host);
+    if (pl_host) (void)hipHostFree(pl_host);
     if (st) (void)hipStreamDestroy(st);
   }
 };
@@ -1296,6 +1301,68 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
     const int last = r.hrows[r.ncommit - 1];
     HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)last * H, H * 4, hipMemcpyDeviceToHost));
   }
+  return 0;
+}
+
+// history capacity for `need` tokens; keeps the first `keep` tokens
+static int hist_reserve(g4v_ctx* c, int need, int keep) {
+  if (need <= c->hist_cap && c->hist.p) return 0;
+  const int cap = std::max(need + 4096, 2 * c->hist_cap);
+  DBuf nb;
+  int r = dalloc(c, nb, (size_t)cap * 4);
+  if (r) return r;
+  if (keep > 0) HIPCHK(hipMemcpyAsync(nb.p, c->hist.p, (size_t)keep * 4, hipMemcpyDeviceToDevice, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  std::swap(c->hist.p, nb.p);
+  std::swap(c->hist.n, nb.n);
+  c->hist_cap = cap;
+  return 0;
+}
+
+int g4v_history_set(g4v_ctx* c, const int* toks, int L) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(L >= 0 && (L == 0 || toks), "history_set: L < 0 or null tokens");
+  HIPCHK(hipSetDevice(c->device));
+  int r = hist_reserve(c, L, 0);
+  if (r) return r;
+  if (L > 0) HIPCHK(hipMemcpyAsync(c->hist.p, toks, (size_t)L * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->hist_len = L;
+  return 0;
+}
+
+int g4v_prompt_lookup(g4v_ctx* c, const int* append, int na, int n, int maxlen, int* drafts, int* nd) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(na >= 0 && na <= PL_MAXA && (na == 0 || append), "prompt_lookup: 0 <= na <= 16 appended tokens");
+  ARGCHK(n <= PL_MAXN, "prompt_lookup: n <= 256");
+  ARGCHK(maxlen <= PL_MAXD, "prompt_lookup: maxlen <= 16");
+  ARGCHK(nd && (maxlen <= 0 || drafts), "prompt_lookup: null output");
+  ARGCHK(c->hist_len <= INT32_MAX - PL_MAXA, "prompt_lookup: history full");
+  HIPCHK(hipSetDevice(c->device));
+  int r = hist_reserve(c, c->hist_len + na, c->hist_len);
+  if (r) return r;
+  if (!c->plout.p) ALLOC(c->plout, (1 + PL_MAXD) * 4);
+  if (!c->pl_host) HIPCHK(hipHostMalloc((void**)&c->pl_host, (1 + PL_MAXD) * 4, hipHostMallocDefault));
+  PlAppend app{};
+  app.n = na;
+  for (int i = 0; i < na; ++i) app.t[i] = append[i];
+  launch_prompt_lookup(c->hist.as<int>(), c->hist_len, app, n, std::max(maxlen, 0), c->plout.as<int>(), c->st);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(c->pl_host, c->plout.p, (1 + PL_MAXD) * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->hist_len += na;
+  *nd = c->pl_host[0];
+  for (int i = 0; i < *nd; ++i) drafts[i] = c->pl_host[1 + i];
+  return 0;
+}
+
+int g4v_history_read(g4v_ctx* c, int* toks, int cap, int* L) {
+  if (!c || !L) return G4V_E_ARG;
+  *L = c->hist_len;
+  if (!toks || cap <= 0 || c->hist_len == 0) return 0;
+  HIPCHK(hipSetDevice(c->device));
+  HIPCHK(hipStreamSynchronize(c->st));
+  HIPCHK(hipMemcpy(toks, c->hist.p, (size_t)std::min(cap, c->hist_len) * 4, hipMemcpyDeviceToHost));
   return 0;
 }
 

@@ -132,6 +132,15 @@ void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, con
                       float* y, int M, int N, int K, int ldy, hipStream_t st);
 int w4a8_mpad(int M);  // rows the quantised operand holds for M rows
 
+// prompt lookup (g4v_draft.hip): appends app.t[0 .. app.n) to hist [L0 ..] and writes
+// out[0] = draft count, out[1 ..] = drafts (n <= PL_MAXN, n + 1 <= L0 + app.n, maxlen <= PL_MAXD)
+constexpr int PL_MAXA = 16, PL_MAXN = 256, PL_MAXD = 16;
+struct PlAppend {
+  int n;
+  int t[PL_MAXA];
+};
+void launch_prompt_lookup(int* hist, int L0, const PlAppend& app, int n, int maxlen, int* out, hipStream_t st);
+
 // mpl: activation rows per block (1..4, 2 at most with the merge prologue); tr: rows per tile
 // (64 or 32).  Returns the grid size (0: K unsupported, nothing launched).
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr);

@@ -51,6 +51,9 @@ SIGNATURES = {
     "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
     "g4v_sync": (_i, [_vp]),
     "g4v_set_graphs": (_i, [_vp, _i]),
+    "g4v_history_set": (_i, [_vp, _i32p, _i]),
+    "g4v_prompt_lookup": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_i)]),
+    "g4v_history_read": (_i, [_vp, _vp, _i, C.POINTER(_i)]),
     "g4v_expf_selftest": (C.c_longlong, [C.c_uint32, C.c_uint32, C.c_uint32]),
 }
 
@@ -245,6 +248,28 @@ class Device:
         self._ok(self.L.g4v_model_read(self.h, what.encode(), out.ctypes.data, out.nbytes, C.byref(nb)),
                  f"model_read {what}")
         return out
+
+    # ---- prompt-lookup drafter ----
+    def history_set(self, toks):
+        toks = _c(toks, np.int32)
+        self._ok(self.L.g4v_history_set(self.h, toks if toks.size else np.zeros(1, np.int32), toks.size),
+                 "history_set")
+
+    def prompt_lookup(self, n, maxlen, append=()):
+        """append the committed tokens, then the prompt-lookup drafts (int32 array)"""
+        app = _c(np.asarray(append, np.int32).reshape(-1), np.int32)
+        out = np.zeros(max(maxlen, 1), np.int32)
+        nd = _i()
+        self._ok(self.L.g4v_prompt_lookup(self.h, app if app.size else np.zeros(1, np.int32), app.size, n,
+                                          maxlen, out, C.byref(nd)), "prompt_lookup")
+        return out[:nd.value].copy()
+
+    def history(self):
+        L = _i()
+        self._ok(self.L.g4v_history_read(self.h, None, 0, C.byref(L)), "history_read")
+        out = np.empty(max(L.value, 1), np.int32)
+        self._ok(self.L.g4v_history_read(self.h, out.ctypes.data, out.size, C.byref(L)), "history_read")
+        return out[:L.value]
 
     def sync(self):
         self._ok(self.L.g4v_sync(self.h), "sync")

@@ -115,6 +115,18 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
  * graph launch).  on = 0 launches every kernel from the host instead. */
 int g4v_set_graphs(g4v_ctx* c, int on);
 
+/* ---- prompt-lookup drafter (run_req, E:1624-1628) over a history kept on the device.
+ * history_set: seq = toks[0..L), the prompt followed by the generated tokens (E:1625). */
+int g4v_history_set(g4v_ctx* c, const int* toks, int L);
+/* Appends append[0..na) (the round's committed tokens, E:1659; na <= 16) to seq, then drafts
+ * as the reference does with NG_N = n and NG_LEN = maxlen (E:1514): the tokens that followed the
+ * most recent earlier occurrence of seq's last n tokens, at most maxlen of them and none past
+ * the end of seq.  *nd = 0 when n <= 0, |seq| <= n or the n-gram has no earlier occurrence.
+ * n <= 256, maxlen <= 16 (the reference caps NG_LEN at 7). */
+int g4v_prompt_lookup(g4v_ctx* c, const int* append, int na, int n, int maxlen, int* drafts, int* nd);
+/* *L = |seq|; copies min(cap, |seq|) tokens of it to toks (may be null) */
+int g4v_history_read(g4v_ctx* c, int* toks, int cap, int* L);
+
 /* ---- measurement (replaces the reference's PROF_NM / T_* stage timers, E:66-70, E:1085):
  * per-kernel-class HIP events on the library's stream.  Classes: 0 gemv_qkv, 1 gemv_o,
  * 2 gemv_gateup, 3 gemv_down, 4 attn, 5 rows (norm/rope/embed), 6 head_screen, 7 head_select,

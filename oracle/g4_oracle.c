@@ -245,6 +245,30 @@ void g4o_w4g32_gemm(const uint8_t* W, const uint16_t* S, const float* X, int M, 
 }
 
 /* ------------------------------------------------------------------------ */
+/* prompt lookup                                                             */
+/* ------------------------------------------------------------------------ */
+
+/* E:1624-1628: scan i = L-n-1 down to 0 for seq[i .. i+n) == seq[L-n .. L); at the first hit
+ * copy seq[i+n+j] for j < maxlen while i+n+j < L */
+int g4o_prompt_lookup(const int32_t* seq, int L, int n, int maxlen, int32_t* drafts) {
+  int nd = 0;
+  if (n <= 0 || L <= n) return 0;
+  for (int i = L - n - 1; i >= 0; --i) {
+    int eq = 1;
+    for (int t = 0; t < n; ++t)
+      if (seq[i + t] != seq[L - n + t]) {
+        eq = 0;
+        break;
+      }
+    if (eq) {
+      for (int j = 0; j < maxlen && i + n + j < L; ++j) drafts[nd++] = seq[i + n + j];
+      break;
+    }
+  }
+  return nd;
+}
+
+/* ------------------------------------------------------------------------ */
 /* W4A8                                                                      */
 /* ------------------------------------------------------------------------ */
 

@@ -65,6 +65,10 @@ void g4o_w4g32_rows(const uint8_t* W, const uint16_t* S, const float* xe, const 
 void g4o_w4g32_gemm(const uint8_t* W, const uint16_t* S, const float* X, int M, int N, int K,
                     float* Y);
 
+/* ---- prompt lookup (E:1624-1628): the most recent earlier occurrence of the last n tokens of
+ * seq [L]; up to maxlen of the tokens that followed it go to drafts.  Returns their count. ---- */
+int g4o_prompt_lookup(const int32_t* seq, int L, int n, int maxlen, int32_t* drafts);
+
 /* ---- W4A8 (engine/w4a8_avx2.h) ---- */
 void g4o_w4a8_quant(const float* X, int M, int K, int8_t* q, float* sx, int32_t* sum);
 void g4o_w4a8_gemm(const uint8_t* W, const uint16_t* S, const float* X, int M, int N, int K,

@@ -56,6 +56,7 @@ class Oracle:
             "g4o_w4g32_gemm": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p]),
             "g4o_w4a8_quant": (None, [_f32p, _i, _i, _i8p, _f32p, _i32p]),
             "g4o_w4a8_gemm": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p]),
+            "g4o_prompt_lookup": (_i, [_i32p, _i, _i, _i, _i32p]),
             "g4o_exp3_codebook": (None, [_u16p, _i64, _u8p]),
             "g4o_exp3_count": (_i64, [_u16p, _i, _i, _u8p, _i64p]),
             "g4o_exp3_pack": (None, [_u16p, _i, _i, _u8p, _u8p, _i64p, _u16p, _f32p]),
@@ -155,6 +156,12 @@ class Oracle:
         sm = np.empty((M, K // 32), np.int32)
         self.L.g4o_w4a8_quant(X, M, K, q, sx, sm)
         return q, sx, sm
+
+    def prompt_lookup(self, seq, n, maxlen):
+        seq = _c(seq, np.int32)
+        out = np.zeros(max(maxlen, 1), np.int32)
+        nd = self.L.g4o_prompt_lookup(seq, len(seq), n, maxlen, out)
+        return out[:nd]
 
     def exp3_pack(self, E, N, K):
         E = _c(E, np.uint16)

@@ -45,8 +45,7 @@ def test_no_device_is_an_error_not_a_fallback():
     """without a HIP device the context cannot be created: the call fails loudly"""
     if not os.path.exists(LIB):
         pytest.skip("libg4v.so not built")
-    import torch  # noqa: F401  (only to know whether this host has a GPU)
-    if torch.cuda.is_available():
+    if os.path.exists("/dev/kfd"):  # the ROCm kernel driver: this host has (or may have) a GPU
         pytest.skip("a GPU is present")
     g4v = load_g4v()
     with pytest.raises(RuntimeError):
