@@ -737,3 +737,89 @@ void g4o_gen_ints(uint64_t seed, int64_t n, int32_t lo, int32_t hi, int32_t* out
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i) out[i] = g4r_int(seed, (uint64_t)i, lo, hi);
 }
+
+/* ------------------------------------------------------------------------ */
+/* prefill attention                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* E:1063-1083 attn_tile, row by row: a row's result depends only on its own range
+ * [lo, pos], not on the tile of QB rows it shares K/V loads with.  Per (m, h):
+ *   s_p = hsum(s0 + s1) (s0/s1 8-lane FMA chains over hd in steps of 16), mx = max_p s_p;
+ *   in position order: w = exp8(s_p - mx), den += w, O = fma(w, v_p, O);
+ *   out = r16(O * (1 / den)). */
+void g4o_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
+                   const int* pos, const int* lo, float* out, int ldo) {
+  float* kf = (float*)malloc(sizeof(float) * hd);
+  float* O = (float*)malloc(sizeof(float) * hd);
+  for (int m = 0; m < M; ++m) {
+    const int len = pos[m] - lo[m] + 1;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(len > 0 ? len : 1));
+    for (int h = 0; h < nh; ++h) {
+      const float* qh = q + (size_t)m * ldq + (size_t)h * hd;
+      float mx = -1e30f;
+      for (int p = lo[m]; p <= pos[m]; ++p) {
+        for (int i = 0; i < hd; ++i) kf[i] = g4o_bf2f(Kc[(size_t)p * hd + i]);
+        float s0[8] = {0}, s1[8] = {0}, v[8];
+        for (int i = 0; i < hd; i += 16)
+          for (int l = 0; l < 8; ++l) {
+            s0[l] = fmaf(qh[i + l], kf[i + l], s0[l]);
+            s1[l] = fmaf(qh[i + 8 + l], kf[i + 8 + l], s1[l]);
+          }
+        for (int l = 0; l < 8; ++l) v[l] = s0[l] + s1[l];
+        const float s = hsum8(v);
+        sc[p - lo[m]] = s;
+        mx = (mx < s) ? s : mx;
+      }
+      float den = 0.f;
+      for (int i = 0; i < hd; ++i) O[i] = 0.f;
+      for (int p = lo[m]; p <= pos[m]; ++p) {
+        const float w = g4o_exp8(sc[p - lo[m]] - mx);
+        den += w;
+        for (int i = 0; i < hd; ++i) O[i] = fmaf(w, g4o_bf2f(Vc[(size_t)p * hd + i]), O[i]);
+      }
+      const float inv = 1.0f / den;
+      float* oo = out + (size_t)m * ldo + (size_t)h * hd;
+      for (int i = 0; i < hd; ++i) oo[i] = g4o_r16(O[i] * inv);
+    }
+    free(sc);
+  }
+  free(kf);
+  free(O);
+}
+
+/* E:1338-1349 run_mh (no sibling row), per (m, h):
+ *   d_p = hsum(sv) (one 8-lane FMA chain over hd in steps of 8), mx = max_p d_p;
+ *   e_p = expf(d_p - mx) (libm), den = sum_p e_p in position order;
+ *   in position order: o = fma(e_p / den, v_p, o);  out = r16(o). */
+void g4o_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
+                 const int* pos, const int* lo, float* out, int ldo) {
+  for (int m = 0; m < M; ++m) {
+    const int len = pos[m] - lo[m] + 1;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(len > 0 ? len : 1));
+    for (int h = 0; h < nh; ++h) {
+      const float* qh = q + (size_t)m * ldq + (size_t)h * hd;
+      float mx = -1e30f;
+      for (int p = lo[m]; p <= pos[m]; ++p) {
+        float sv[8] = {0};
+        for (int i = 0; i < hd; i += 8)
+          for (int l = 0; l < 8; ++l) sv[l] = fmaf(qh[i + l], g4o_bf2f(Kc[(size_t)p * hd + i + l]), sv[l]);
+        const float d = hsum8(sv);
+        sc[p - lo[m]] = d;
+        mx = (mx < d) ? d : mx;
+      }
+      float den = 0.f;
+      for (int p = lo[m]; p <= pos[m]; ++p) {
+        sc[p - lo[m]] = expf(sc[p - lo[m]] - mx);
+        den += sc[p - lo[m]];
+      }
+      float* oo = out + (size_t)m * ldo + (size_t)h * hd;
+      for (int i = 0; i < hd; ++i) oo[i] = 0.f;
+      for (int p = lo[m]; p <= pos[m]; ++p) {
+        const float wgt = sc[p - lo[m]] / den;
+        for (int i = 0; i < hd; ++i) oo[i] = fmaf(wgt, g4o_bf2f(Vc[(size_t)p * hd + i]), oo[i]);
+      }
+      for (int i = 0; i < hd; ++i) oo[i] = g4o_r16(oo[i]);
+    }
+    free(sc);
+  }
+}

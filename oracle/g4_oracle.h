@@ -28,6 +28,9 @@
  *   head_row                                   golden survivor sets (reference scan) + screened
  *                                              greedy == brute-force full-head greedy
  *   attn_splitkv                               golden + live + fp64 softmax, LSE identity, masks
+ *   attn_tile                                  live (the reference's attn_tile) + fp64 softmax
+ *   attn_mh                                    fp64 softmax only (run_mh is a lambda inside main(),
+ *                                              E:1338-1349): parity unpinned at the bit level
  *   model / verify                             golden passes through the reference's kernels
  *                                              (2 layers, V 262144), acceptance brute force
  * Generators (g4_rng.h) are pinned by the CRC-32 of every input the fixtures store.
@@ -111,6 +114,13 @@ void g4o_attn_splitkv(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, in
                       const int* skip_hi, int kmin, int kmax, int T, float* out, int ldo,
                       float* part_m, float* part_l);
 
+/* ---- prefill attention: attn_tile (E:1063-1083) and run_mh (E:1338-1349), row by row;
+ * rows [M] at pos[m] attend [lo[m], pos[m]] ---- */
+void g4o_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
+                   const int* pos, const int* lo, float* out, int ldo);
+void g4o_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
+                 const int* pos, const int* lo, float* out, int ldo);
+
 /* ---- synthetic decoder stack + verify step (engine/gemma4_engine.cpp:1256-1502, 1617-1661) ---- */
 typedef struct g4o_model g4o_model;
 g4o_model* g4o_model_new(uint64_t seed, int V, int NL, int I, int ctx);
@@ -133,6 +143,10 @@ typedef struct {
  * rows are at positions pos0.. ; fills out and commits (KV compaction for branch b). */
 void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
                 g4o_verify_out* out, float* hidden_out);
+
+/* prefill (E:1594-1599, ENGINE_PREFILL_INT8=1): toks[0..n) at pos0.. in blocks of pfb rows;
+ * fills the KV cache; hlast (optional) receives the final-normed hidden row of the last token */
+void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, float* hlast);
 
 /* forward of M rows that fills the KV cache only (want = false) */
 void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T);

@@ -223,9 +223,10 @@ int g4o_model_bytes(const g4o_model* m, const char* what, void* dst, int64_t cap
 /* forward                                                                  */
 /* ------------------------------------------------------------------------ */
 
+#define MAXROWS 32 /* MM, E:176: rows of one pass (prefill block) */
 typedef struct {
   int M, pos0;
-  int rope[8], slot[8], skip_lo[8], skip_hi[8];
+  int rope[MAXROWS], slot[MAXROWS], skip_lo[MAXROWS], skip_hi[MAXROWS];
 } rows_t;
 
 static void rows_tree(rows_t* r, int pos0, int na, int nb) {
@@ -255,9 +256,20 @@ static void rows_chain(rows_t* r, int pos0, int M) {
   }
 }
 
-/* E:1262-1405 for the rows r (M <= 8); the split-KV attention path (E:1305-1327) is used
- * for every row count.  hbuf (optional) receives r16(rms(x, fnorm)) of every row (E:1400-1402). */
-static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf) {
+/* attention path of a pass (E:1305, 1328, 1337) */
+enum { ATT_SPLIT = 0, ATT_TILE = 1, ATT_MH = 2 };
+
+/* a linear layer of the pass: lin_multi / lin1 (E:310-317) take W4A8 when G_I8_ACTIVE and the
+ * pass has M >= 2 rows, else the exact-float W4G32 GEMV */
+static void lin(int i8, const uint8_t* W, const uint16_t* S, const float* X, int M, int N, int K, float* Y) {
+  if (i8 && M >= 2) g4o_w4a8_gemm(W, S, X, M, N, K, Y);
+  else g4o_w4g32_gemm(W, S, X, M, N, K, Y);
+}
+
+/* E:1262-1405 for the rows r (M <= 32).  i8: G_I8_ACTIVE (prefill with ENGINE_PREFILL_INT8=1);
+ * amode: the attention path.  hbuf (optional) receives r16(rms(x, fnorm)) of every row
+ * (E:1400-1402). */
+static void forward_ex(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf, int i8, int amode) {
   const int M = r->M, I = m->I;
   float* x = (float*)malloc(sizeof(float) * M * H);
   float* xa = (float*)malloc(sizeof(float) * M * H);
@@ -278,10 +290,10 @@ static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float
   for (int l = 0; l < m->NL; ++l) {
     olayer* A = &m->L[l];
     const int ty = A->sliding ? 0 : 1;
-    g4o_w4g32_gemm(A->W[0], A->S[0], xa, M, A->N[0], H, q); /* E:1289 */
-    g4o_w4g32_gemm(A->W[1], A->S[1], xa, M, A->N[1], H, k);
-    g4o_w4g32_gemm(A->W[2], A->S[2], xa, M, A->N[2], H, v);
-    int pos[8], lo[8], kmax = r->pos0 + M - 1, kmin = kmax;
+    lin(i8, A->W[0], A->S[0], xa, M, A->N[0], H, q); /* E:1289 */
+    lin(i8, A->W[1], A->S[1], xa, M, A->N[1], H, k);
+    lin(i8, A->W[2], A->S[2], xa, M, A->N[2], H, v);
+    int pos[MAXROWS], lo[MAXROWS], kmax = r->pos0 + M - 1, kmin = kmax;
     for (int i = 0; i < M; ++i) { /* E:1307-1324 */
       const float* cs = m->cs[ty] + (size_t)r->rope[i] * HD / 2;
       const float* sn = m->sn[ty] + (size_t)r->rope[i] * HD / 2;
@@ -304,10 +316,14 @@ static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float
       lo[i] = A->sliding ? (r->rope[i] - 511 > 0 ? r->rope[i] - 511 : 0) : 0;
       kmin = kmin < lo[i] ? kmin : lo[i];
     }
-    g4o_attn_splitkv(m->KC + (size_t)l * m->ctx * HD, m->VC + (size_t)l * m->ctx * HD, HD, NQ, M,
-                     q, NQ * HD, pos, lo, r->skip_lo, r->skip_hi, kmin, kmax, T, att, NQ * HD,
-                     NULL, NULL);
-    g4o_w4g32_gemm(A->W[3], A->S[3], att, M, H, NQ * HD, o); /* E:1356 */
+    const uint16_t* KCl = m->KC + (size_t)l * m->ctx * HD;
+    const uint16_t* VCl = m->VC + (size_t)l * m->ctx * HD;
+    if (amode == ATT_TILE) g4o_attn_tile(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, att, NQ * HD); /* E:1335 */
+    else if (amode == ATT_MH) g4o_attn_mh(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, att, NQ * HD); /* E:1350 */
+    else
+      g4o_attn_splitkv(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, r->skip_lo, r->skip_hi, kmin, kmax, T, att,
+                       NQ * HD, NULL, NULL);
+    lin(i8, A->W[3], A->S[3], att, M, H, NQ * HD, o); /* E:1356 */
     for (int i = 0; i < M; ++i) {                             /* E:1358-1361 */
       float* oi = o + i * H;
       float* xi = x + i * H;
@@ -317,11 +333,11 @@ static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float
       g4o_rms(xi, A->nv[2], H, xa + i * H);
       for (int c = 0; c < H; ++c) xa[i * H + c] = g4o_r16(xa[i * H + c]);
     }
-    g4o_w4g32_gemm(A->W[4], A->S[4], xa, M, I, H, g); /* E:256-302 */
-    g4o_w4g32_gemm(A->W[5], A->S[5], xa, M, I, H, u);
+    lin(i8, A->W[4], A->S[4], xa, M, I, H, g); /* E:256-302 (i8: E:1368-1371) */
+    lin(i8, A->W[5], A->S[5], xa, M, I, H, u);
     for (size_t c = 0; c < (size_t)M * I; ++c)
       g[c] = g4o_r16(g4o_r16(g4o_gelu8(g4o_r16(g[c]))) * g4o_r16(u[c]));
-    g4o_w4g32_gemm(A->W[6], A->S[6], g, M, H, I, o); /* E:1373 */
+    lin(i8, A->W[6], A->S[6], g, M, H, I, o); /* E:1373 */
     for (int i = 0; i < M; ++i) {                     /* E:1375-1378, 1390-1404 */
       float* oi = o + i * H;
       float* xi = x + i * H;
@@ -346,6 +362,34 @@ static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float
   free(tmp);
   free(g);
   free(u);
+}
+
+static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf) {
+  forward_ex(m, toks, r, T, hbuf, 0, ATT_SPLIT);
+}
+
+/* E:1594-1599 prefill of toks[0..n) at positions pos0.. in blocks of pfb (<= 32) rows, with
+ * ENGINE_PREFILL_INT8=1 (G_I8_ACTIVE during prefill, E:1595) and the engine's defaults
+ * SPLITKV, TILED, ATT_PAR = 192 (E:1212-1214).  Per block of M rows at p0:
+ *   attention: split-KV when M <= 4 and p0 + M > 192 (E:1305), else attn_tile when M >= 4 and
+ *   p0 + M > 64 (E:1328), else run_mh (E:1337);  linear layers: W4A8 when M >= 2 (E:311).
+ * hlast (optional) receives r16(rms(x, fnorm)) of the last row (E:1598, hf = M - 1). */
+void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, float* hlast) {
+  if (pfb < 1) pfb = 1;
+  if (pfb > MAXROWS) pfb = MAXROWS;
+  float* hb = (float*)malloc(sizeof(float) * (size_t)MAXROWS * H);
+  for (int done = 0; done < n;) {
+    const int M = (n - done) < pfb ? (n - done) : pfb;
+    const int p0 = pos0 + done;
+    const int last = done + M == n;
+    const int amode = (M <= 4 && p0 + M > 192) ? ATT_SPLIT : (M >= 4 && p0 + M > 64) ? ATT_TILE : ATT_MH;
+    rows_t r;
+    rows_chain(&r, p0, M);
+    forward_ex(m, toks + done, &r, T, last ? hb : NULL, 1, amode);
+    if (last && hlast) memcpy(hlast, hb + (size_t)(M - 1) * H, sizeof(float) * H);
+    done += M;
+  }
+  free(hb);
 }
 
 void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T) {

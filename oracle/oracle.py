@@ -72,6 +72,9 @@ class Oracle:
             "g4o_model_ptr": (_vp, [_vp, C.c_char_p]),
             "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
+            "g4o_prefill": (None, [_vp, _i32p, _i, _i, _i, _i, _vp]),
+            "g4o_attn_tile": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _f32p, _i]),
+            "g4o_attn_mh": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _f32p, _i]),
             "g4o_stream": (_u64, [_u64, _u64]),
             "g4o_gen_normal_f32": (None, [_u64, _i64, _f, _f32p]),
             "g4o_gen_normal_bf16": (None, [_u64, _i64, _f, _u16p]),
@@ -203,6 +206,15 @@ class Oracle:
         n = min(info.nsurv, cap)
         return info, surv[:n].copy(), sval[:n].copy()
 
+    def attn_rows(self, kind, Kc, Vc, q, pos, lo):
+        """prefill attention of rows q [M][2048] at pos[m] over [lo[m], pos[m]]: kind 'tile' or 'mh'"""
+        q = _c(q, np.float32)
+        M = q.shape[0]
+        out = np.empty((M, 2048), np.float32)
+        fn = self.L.g4o_attn_tile if kind == "tile" else self.L.g4o_attn_mh
+        fn(_c(Kc, np.uint16), _c(Vc, np.uint16), 256, 8, M, q, 2048, _c(pos, np.int32), _c(lo, np.int32), out, 2048)
+        return out
+
     def attn(self, Kc, Vc, hd, nh, q, pos, lo, skip_lo, skip_hi, kmin, kmax, T, parts=False):
         q = _c(q, np.float32)
         M = q.shape[0]
@@ -241,6 +253,13 @@ class Model:
         if rc != 0:
             raise KeyError(what)
         return out
+
+    def prefill(self, toks, pos0=0, pfb=32, T=8):
+        """prefill toks at pos0.. (W4A8 linear layers); returns the last row's final-normed hidden"""
+        toks = _c(toks, np.int32)
+        hid = np.empty(1536, np.float32)
+        self.o.L.g4o_prefill(self.h, toks, toks.size, pos0, pfb, T, hid.ctypes.data)
+        return hid
 
     def verify(self, toks, na, nb, pos0, T=8):
         out = VerifyOut()
@@ -296,6 +315,10 @@ class Ref:
             "ref_head": (None, [_f32p, _i, _f32p]),
             "ref_head_setup": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
             "ref_verify": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, C.POINTER(RefOut)]),
+            "ref_attn_tile": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
+            "ref_attn_mh": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
+            "ref_prefill": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _vp]),
+            "ref_pack_reset": (None, []),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -308,6 +331,7 @@ class Ref:
         """run ref_verify on the oracle model's own arrays (no copies of the layer weights)"""
         o, h = model.o, model.h
         ptr = lambda w: o.L.g4o_model_ptr(h, w.encode())
+        self.L.ref_pack_reset()  # W4A8 repacks are keyed by weight address
         rm = RefModel()
         rm.V, rm.NL, rm.I, rm.ctx = model.V, model.NL, model.I, model.ctx
         rm.E, rm.fnorm, rm.KC, rm.VC = ptr("E"), ptr("fnorm"), ptr("KC"), ptr("VC")
@@ -323,6 +347,22 @@ class Ref:
         self.L.ref_head_setup(ptr("Wq"), ptr("Sq"), ptr("coef"), ptr("x3"), ptr("cb"), ptr("xptr"), ptr("xcol"),
                               ptr("xdel"), model.V)
         self.model = rm
+
+    def attn_rows(self, kind, Kc, Vc, sliding, q, pos0):
+        """attn_tile / run_mh of rows q [M][2048] at pos0 .. pos0+M-1 (causal, window 512 if sliding)"""
+        q = _c(q, np.float32)
+        out = np.empty((q.shape[0], 2048), np.float32)
+        fn = self.L.ref_attn_tile if kind == "tile" else self.L.ref_attn_mh
+        fn(_c(Kc, np.uint16), _c(Vc, np.uint16), 1 if sliding else 0, q, pos0, q.shape[0], out)
+        return out
+
+    def prefill(self, toks, pos0=0, pfb=32):
+        hid = np.empty(1536, np.float32)
+        toks = _c(toks, np.int32)
+        rc = self.L.ref_prefill(C.byref(self.model), toks, toks.size, pos0, pfb, hid.ctypes.data)
+        if rc != 0:
+            raise ValueError("ref_prefill: pfb must be 1..32")
+        return hid
 
     def verify(self, toks, na, nb, pos0):
         out = RefOut()

@@ -6,6 +6,8 @@
 // Used to pin the C oracle bit-for-bit and as the "reference" CPU baseline.
 // Every wrapper calls the reference's static functions unchanged; the few lines
 // that compose them restate the call sites they cite (E = engine/gemma4_engine.cpp).
+#include <map>
+#include <memory>
 #define main engine_main
 #include G4_REF_ENGINE
 #undef main
@@ -419,6 +421,224 @@ static void head_group_ref(float (*hbuf)[1536], const int* toks, int M, int hf, 
       fb[hf + m] = 1;
     }
   }
+}
+
+
+// ---------------------------------------------------------------------------------------
+// Prefill attention and the prefill pass (E:1594-1599 with ENGINE_PREFILL_INT8=1)
+// ---------------------------------------------------------------------------------------
+// attn_tile (E:1063-1083) over rows at pos0 .. pos0+M-1, tiles of QB in turn on worker slot 0
+void ref_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int sliding, const float* q, int pos0, int M, float* att) {
+  for (int t = 0; t < (M + QB - 1) / QB; ++t) attn_tile(Kc, Vc, 256, sliding != 0, q, 2048, pos0, M, att, t, 0);
+}
+
+// run_mh (E:1338-1349, no sibling row) on already normed and rotated q, as the lambda does it
+static void run_mh_rows(const uint16_t* Kc, const uint16_t* Vc, int sliding, const float* q, int pos0, int M,
+                        float* att) {
+  const int hd = 256;
+  std::vector<float> scv((size_t)pos0 + M + 8);
+  float* sc = scv.data();
+  for (int mh = 0; mh < M * 8; ++mh) {
+    const int m = mh / 8, h = mh % 8, cachepos = pos0 + m, pos = cachepos;
+    const float* qh = q + (size_t)m * 2048 + h * hd;
+    const int lo = sliding ? std::max(0, pos - 511) : 0;
+    float mx = -1e30f;
+    for (int p = lo; p <= cachepos; ++p) {
+      __m256 sv = _mm256_setzero_ps();
+      const uint16_t* kp = Kc + (size_t)p * hd;
+      for (int i = 0; i < hd; i += 8) sv = _mm256_fmadd_ps(_mm256_loadu_ps(qh + i), bf8(kp + i), sv);
+      float d = w4::hsum(sv);
+      sc[p] = d;
+      mx = std::max(mx, d);
+    }
+    float den = 0;
+    for (int p = lo; p <= cachepos; ++p) {
+      sc[p] = expf(sc[p] - mx);
+      den += sc[p];
+    }
+    float* oh = att + (size_t)m * 8 * hd + h * hd;
+    for (int i = 0; i < hd; ++i) oh[i] = 0;
+    for (int p = lo; p <= cachepos; ++p) {
+      float wgt = sc[p] / den;
+      const uint16_t* vp = Vc + (size_t)p * hd;
+      for (int i = 0; i < hd; i += 8)
+        _mm256_storeu_ps(oh + i, _mm256_fmadd_ps(_mm256_set1_ps(wgt), bf8(vp + i), _mm256_loadu_ps(oh + i)));
+    }
+    rbf_n(oh, hd);
+  }
+}
+void ref_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int sliding, const float* q, int pos0, int M, float* att) {
+  run_mh_rows(Kc, Vc, sliding, q, pos0, M, att);
+}
+
+namespace {
+std::map<const uint8_t*, std::unique_ptr<w4a8::Packed>> g_pk;  // W4A8 repack of each matrix, once
+const w4a8::Packed* packed(const uint8_t* W, const uint16_t* S, int N, int K) {
+  auto& p = g_pk[W];
+  if (!p) {
+    p.reset(new w4a8::Packed());
+    w4a8::repack_alloc(N, K, *p);
+    w4a8::repack_tiles(W, S, N, K, *p, 0, N / 8);
+  }
+  return p.get();
+}
+}  // namespace
+
+void ref_pack_reset(void) { g_pk.clear(); }
+
+// The prefill loop of run_req (E:1594-1599) over the synthetic stack with G_I8_ACTIVE = G_I8 =
+// true: fwd (E:1256-1405) per block of at most pfb rows, the engine's attention-path choice
+// (E:1305, 1328, 1337 with SPLITKV, TILED, ATT_PAR = 192) and lin_multi's W4A8 rule (M >= 2,
+// E:311).  hlast receives the last row's r16(rms(x, fnorm)).  Returns -1 for pfb outside 1..32.
+int ref_prefill(RefModel* md, const int* toks, int n, int pos0, int pfb, float* hlast) {
+  if (pfb < 1 || pfb > 32) return -1;
+  const int H = 1536, NL = md->NL, I = md->I;
+  const int T = POOL.active_count();
+  alignas(64) static float x[32][1536], a[32][1536], mlp_in[32][1536], q[32][2048], k[32][256], v[32][256],
+      att[32][2048], o[32][1536], tmp[1536];
+  static std::vector<float> gbuf, ubuf, abuf;
+  gbuf.resize((size_t)32 * I);
+  ubuf.resize((size_t)32 * I);
+  abuf.resize((size_t)32 * I);
+  static XP XA, XB;
+  const __m256 vsqh = _mm256_set1_ps(sqrtf((float)H));
+  G_I8_ACTIVE = true;
+  for (int done = 0; done < n;) {
+    const int M = std::min(pfb, n - done), p0 = pos0 + done;
+    const bool last = done + M == n;
+    const int* tk = toks + done;
+    const bool split = M <= 4 && p0 + M > 192, tiled = !split && M >= 4 && p0 + M > 64;
+    for (int m = 0; m < M; ++m) {  // E:1262-1267
+      const uint16_t* er = md->E + (size_t)tk[m] * H;
+      for (int i = 0; i < H; i += 8) _mm256_storeu_ps(x[m] + i, rbf8(_mm256_mul_ps(bf8(er + i), vsqh)));
+      rms_prep_x(x[m], md->L[0].nv[0], H, a[m], XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2),
+                 XA.gs + (size_t)m * (H / 32), false);
+    }
+    XA.K = H;
+    XA.M = M;
+    XA.src = &a[0][0];
+    XA.qdone = false;
+    for (int l = 0; l < NL; ++l) {
+      const RefLayer& A = md->L[l];
+      Q4 qm[7];
+      const int Ns[7] = {2048, 256, 256, 1536, I, I, 1536}, Ks[7] = {1536, 1536, 1536, 2048, 1536, 1536, I};
+      for (int j = 0; j < 7; ++j) {
+        qm[j].w = A.W[j];
+        qm[j].s = A.S[j];
+        qm[j].N = Ns[j];
+        qm[j].K = Ks[j];
+        qm[j].p8 = packed(A.W[j], A.S[j], Ns[j], Ks[j]);
+      }
+      {  // E:1289
+        const Q4* qq[3] = {&qm[0], &qm[1], &qm[2]};
+        float* yy[3] = {&q[0][0], &k[0][0], &v[0][0]};
+        lin_multi(XA, 3, qq, yy);
+      }
+      const int ty = A.sliding ? 0 : 1;
+      uint16_t* KCl = md->KC + (size_t)l * md->ctx * 256;
+      uint16_t* VCl = md->VC + (size_t)l * md->ctx * 256;
+      for (int m = 0; m < M; ++m) {  // E:1291-1303 / 1307-1324 / 1331-1334 / 1343-1344
+        const float* cs = md->cs[ty] + (size_t)(p0 + m) * 128;
+        const float* sn = md->sn[ty] + (size_t)(p0 + m) * 128;
+        for (int h = 0; h < 8; ++h) {
+          rms_r16_inplace(q[m] + h * 256, A.nv[4], 256);
+          rope_avx2(q[m] + h * 256, cs, sn, 256);
+        }
+        rms_r16_inplace(k[m], A.nv[5], 256);
+        rope_avx2(k[m], cs, sn, 256);
+        rms_r16_inplace(v[m], nullptr, 256);
+        uint16_t* kd = KCl + (size_t)(p0 + m) * 256;
+        uint16_t* vd = VCl + (size_t)(p0 + m) * 256;
+        for (int i = 0; i < 256; i += 8) {
+          _mm_storeu_si128((__m128i*)(kd + i), f2bf8(_mm256_loadu_ps(k[m] + i)));
+          _mm_storeu_si128((__m128i*)(vd + i), f2bf8(_mm256_loadu_ps(v[m] + i)));
+        }
+      }
+      if (split) {  // E:1325-1327
+        AttnArg aa;
+        aa.Kc = KCl;
+        aa.Vc = VCl;
+        aa.hd = 256;
+        aa.nh = 8;
+        aa.M = M;
+        aa.kmax = p0 + M - 1;
+        aa.kmin = aa.kmax;
+        float* outp[4];
+        for (int m = 0; m < M; ++m) {
+          aa.q[m] = q[m];
+          aa.pos[m] = p0 + m;
+          aa.lo[m] = A.sliding ? std::max(0, p0 + m - 511) : 0;
+          aa.skip_lo[m] = 1;
+          aa.skip_hi[m] = 0;
+          aa.kmin = std::min(aa.kmin, aa.lo[m]);
+          outp[m] = att[m];
+        }
+        POOL.run(attn_task, &aa);
+        attn_merge(aa, T, outp, nullptr);
+      } else if (tiled) {
+        ref_attn_tile(KCl, VCl, A.sliding, &q[0][0], p0, M, &att[0][0]);
+      } else {
+        run_mh_rows(KCl, VCl, A.sliding, &q[0][0], p0, M, &att[0][0]);
+      }
+      XB.prep(&att[0][0], 2048, M);
+      lin1(XB, qm[3], &o[0][0]);  // E:1356
+      for (int m = 0; m < M; ++m) {  // E:1358-1361
+        rbf_n(o[m], H);
+        rms(o[m], A.nv[1], H, tmp);
+        add_res_inplace(x[m], tmp, H);
+        rms_prep_x(x[m], A.nv[2], H, mlp_in[m], XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2),
+                   XA.gs + (size_t)m * (H / 32), true);
+      }
+      XA.K = H;
+      XA.M = M;
+      XA.src = &mlp_in[0][0];
+      XA.qdone = false;
+      if (M >= 2) {  // E:1367-1371
+        const Q4* qq[2] = {&qm[4], &qm[5]};
+        float* yy[2] = {gbuf.data(), ubuf.data()};
+        lin_multi(XA, 2, qq, yy);
+        for (int m = 0; m < M; ++m) {
+          const float* gm = gbuf.data() + (size_t)m * I;
+          const float* um = ubuf.data() + (size_t)m * I;
+          float* am = abuf.data() + (size_t)m * I;
+          for (int i = 0; i < I; i += 8) {
+            __m256 g = rbf8(_mm256_loadu_ps(gm + i)), u = rbf8(_mm256_loadu_ps(um + i));
+            _mm256_storeu_ps(am + i, rbf8(_mm256_mul_ps(rbf8(gelu8(g)), u)));
+          }
+        }
+        XB.prep(abuf.data(), I, M);
+      } else {  // E:1363-1366
+        XB.K = I;
+        XB.M = M;
+        XB.src = abuf.data();
+        XB.qdone = false;
+        GateUpArg gua{&XA, &qm[4], &qm[5], gbuf.data(), ubuf.data(), abuf.data(), &XB};
+        POOL.run(gate_up_fused_task, &gua);
+      }
+      lin1(XB, qm[6], &o[0][0]);  // E:1373
+      const __m256 vsc = _mm256_set1_ps(A.scalar);
+      for (int m = 0; m < M; ++m) {  // E:1375-1404, zero per-layer-embedding branch
+        rbf_n(o[m], H);
+        rms(o[m], A.nv[3], H, tmp);
+        add_res_prep_x(x[m], tmp, H, XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2), XA.gs + (size_t)m * (H / 32));
+        for (int i = 0; i < H; i += 8) _mm256_storeu_ps(x[m] + i, rbf8(_mm256_mul_ps(_mm256_loadu_ps(x[m] + i), vsc)));
+        if (l + 1 < NL)
+          rms_prep_x(x[m], md->L[l + 1].nv[0], H, a[m], XA.xe + (size_t)m * (H / 2), XA.xo + (size_t)m * (H / 2),
+                     XA.gs + (size_t)m * (H / 32), false);
+        else if (last && m == M - 1 && hlast) {
+          rms(x[m], md->fnorm, H, hlast);
+          rbf_n(hlast, H);
+        }
+      }
+      XA.K = H;
+      XA.M = M;
+      XA.src = &a[0][0];
+      XA.qdone = false;
+    }
+    done += M;
+  }
+  G_I8_ACTIVE = false;
+  return 0;
 }
 
 int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* out) {
