@@ -100,6 +100,10 @@ struct g4v_ctx {
   VerifyResultDev* res_host = nullptr;
   // attention standalone
   DBuf ak, av, aq, ao;
+  // prefill rows (plain [row][K] layouts), quantised activations, attention score scratch
+  DBuf pfx, pfa, pfq, pfk, pfv, pfatt, pfo, pfg, pfu, pfact, pfxq, pfsx, pfcorr, pfs, pftok, pfh;
+  int pf_rows = 0, pf_I = 0;  // rows and FFN width the buffers were sized for
+  size_t pf_sfl = 0;
   // prompt-lookup history (prompt + committed tokens) and the lookup's result words
   DBuf hist, plout;
   int hist_len = 0, hist_cap = 0;
@@ -315,6 +319,11 @@ static int upload_w4(g4v_ctx* c, Mat& m, const uint8_t* w_dev_orig, const uint16
   launch_relayout_w4(w_dev_orig, m.wr.as<uint4>(), N, K, c->st);
   HIPCHK(hipMemcpyAsync(m.s.p, s_host_or_dev, (size_t)N * K / 16,
                         s_on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, c->st));
+  if (N % 16 == 0) {  // operand tiles of the W4A8 path (prefill, g4v_w4a8_gemm)
+    ALLOC(m.a8w, (size_t)N * K / 2);
+    ALLOC(m.a8s, (size_t)N * K / 16);
+    launch_tile_a8(w_dev_orig, m.s.as<uint16_t>(), m.a8w.as<uint4>(), m.a8s.as<uint4>(), N, K, c->st);
+  }
   if (tiled) {
     ALLOC(m.tw, (size_t)N * K / 2);
     ALLOC(m.ts, (size_t)N * K / 16);
@@ -333,11 +342,6 @@ int g4v_w4_upload(g4v_ctx* c, const uint8_t* w, const uint16_t* s, int N, int K)
   auto m = std::make_unique<Mat>();
   int r = upload_w4(c, *m, tmp.as<uint8_t>(), s, false, N, K);
   if (r) return r;
-  if (N % 16 == 0) {  // operand tiles of the W4A8 path (g4v_w4a8_gemm)
-    ALLOC(m->a8w, (size_t)N * K / 2);
-    ALLOC(m->a8s, (size_t)N * K / 16);
-    launch_tile_a8(tmp.as<uint8_t>(), m->s.as<uint16_t>(), m->a8w.as<uint4>(), m->a8s.as<uint4>(), N, K, c->st);
-  }
   HIPCHK(hipStreamSynchronize(c->st));
   c->mats.push_back(std::move(m));
   return (int)c->mats.size() - 1;
@@ -1300,6 +1304,155 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
   if (hidden) {
     const int last = r.hrows[r.ncommit - 1];
     HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)last * H, H * 4, hipMemcpyDeviceToHost));
+  }
+  return 0;
+}
+
+
+// ---------------------------------------------------------------------------------------
+// prefill
+// ---------------------------------------------------------------------------------------
+// a linear layer of a prefill segment: lin_multi / lin1 (E:310-317) take W4A8 when the block has
+// M >= 2 rows (G_I8_ACTIVE during prefill), else the exact-float GEMV.  quant = false reuses the
+// quantised rows of the previous call (same x).
+static void pf_lin(g4v_ctx* c, const Mat& m, const float* x, int M, float* y, bool i8, bool quant) {
+  if (i8) {
+    if (quant)
+      launch_w4a8_quant(x, M, w4a8_mpad(M), m.K, c->pfxq.as<uint16_t>(), c->pfsx.as<float>(), c->pfcorr.as<float>(),
+                        nullptr, nullptr, nullptr, c->st);
+    launch_w4a8_gemm(m.a8w.as<uint4>(), m.a8s.as<uint4>(), c->pfxq.as<uint16_t>(), c->pfsx.as<float>(),
+                     c->pfcorr.as<float>(), y, M, m.N, m.K, m.N, c->st);
+  } else {
+    launch_gemv(plain_args(m, x, y, M), EPI_STORE, c->st);
+  }
+}
+
+static int pf_alloc(g4v_ctx* c, int rows, size_t sfl) {
+  if (rows > c->pf_rows || c->I != c->pf_I) {
+    const size_t R = (size_t)rows, Rp = (size_t)w4a8_mpad(rows), Kmax = std::max(NQ * HD, std::max(H, c->I));
+    ALLOC(c->pfx, R * H * 4);
+    ALLOC(c->pfa, R * H * 4);
+    ALLOC(c->pfq, R * NQ * HD * 4);
+    ALLOC(c->pfk, R * HD * 4);
+    ALLOC(c->pfv, R * HD * 4);
+    ALLOC(c->pfatt, R * NQ * HD * 4);
+    ALLOC(c->pfo, R * H * 4);
+    ALLOC(c->pfg, R * c->I * 4);
+    ALLOC(c->pfu, R * c->I * 4);
+    ALLOC(c->pfact, R * c->I * 4);
+    ALLOC(c->pfxq, Rp * Kmax * 2);
+    ALLOC(c->pfsx, (Kmax / 32) * Rp * 4);
+    ALLOC(c->pfcorr, (Kmax / 32) * Rp * 4);
+    ALLOC(c->pftok, R * 4);
+    if (!c->pfh.p) ALLOC(c->pfh, H * 4);
+    c->pf_rows = rows;
+    c->pf_I = c->I;
+  }
+  if (sfl > c->pf_sfl) {
+    ALLOC(c->pfs, sfl * 4);
+    c->pf_sfl = sfl;
+  }
+  return 0;
+}
+
+// rows [r0, r0 + M) of the prompt through every layer.  split: the rows form one short block that
+// takes the split-KV path (E:1305) with nsplit splits; else each row takes attn_tile or run_mh
+// by its block.  After the last layer, h = the final-normed state of segment row hrow (or none).
+static void pf_segment(g4v_ctx* c, const PfGeom& g, int r0, int M, bool i8, bool split, int nsplit, int hrow) {
+  hipStream_t st = c->st;
+  const float sqh = std::sqrt((float)H);
+  const size_t off = (size_t)r0;
+  float *x = c->pfx.as<float>() + off * H, *a = c->pfa.as<float>() + off * H, *o = c->pfo.as<float>() + off * H;
+  float *q = c->pfq.as<float>() + off * NQ * HD, *k = c->pfk.as<float>() + off * HD, *v = c->pfv.as<float>() + off * HD;
+  float* att = c->pfatt.as<float>() + off * NQ * HD;
+  float *gb = c->pfg.as<float>() + off * c->I, *ub = c->pfu.as<float>() + off * c->I,
+        *act = c->pfact.as<float>() + off * c->I;
+  const int P0 = g.pos0 + r0;
+  launch_pf_embed(c->E.as<uint16_t>(), c->pftok.as<int>() + r0, c->L[0]->ln().in_ln, sqh, x, a, M, st);
+  for (int l = 0; l < c->NL; ++l) {
+    const Layer& lay = *c->L[l];
+    const LayerNorms ln = lay.ln();
+    const int ty = lay.sliding ? 0 : 1;
+    uint16_t* KCl = c->KC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
+    uint16_t* VCl = c->VC.as<uint16_t>() + (size_t)l * c->kvcap * HD;
+    pf_lin(c, lay.m[0], a, M, q, i8, true);  // E:1289
+    pf_lin(c, lay.m[1], a, M, k, i8, false);
+    pf_lin(c, lay.m[2], a, M, v, i8, false);
+    const float* cs = c->rope.as<float>() + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
+    const float* sn = cs + (size_t)c->ctxcap * (HD / 2);
+    launch_pf_qkv(q, k, v, ln.qn, ln.kn, cs, sn, KCl, VCl, P0, M, st);
+    if (split) {  // E:1305-1327: one block of M <= 4 rows over [kmin, kmax]
+      AttnGeom ag{};
+      ag.M = M;
+      ag.kmax = P0 + M - 1;
+      ag.kmin = ag.kmax;
+      ag.T = nsplit;
+      for (int m = 0; m < M; ++m) {
+        ag.pos[m] = P0 + m;
+        ag.lo[m] = lay.sliding ? std::max(0, P0 + m - 511) : 0;
+        ag.skip_lo[m] = 1;
+        ag.skip_hi[m] = 0;
+        ag.kmin = std::min(ag.kmin, ag.lo[m]);
+      }
+      launch_attn_geom(KCl, VCl, q, NQ * HD, ag, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), att,
+                       NQ * HD, st);
+    } else {
+      launch_pf_attn(c->pfq.as<float>(), KCl, VCl, c->pfs.as<float>(), c->pfatt.as<float>(), g, r0, M, lay.sliding,
+                     st);
+    }
+    pf_lin(c, lay.m[3], att, M, o, i8, true);  // E:1356
+    launch_pf_post_attn(o, x, a, ln.post_attn, ln.pre_ff, M, st);
+    pf_lin(c, lay.m[4], a, M, gb, i8, true);  // E:1366-1371
+    pf_lin(c, lay.m[5], a, M, ub, i8, false);
+    launch_pf_act(gb, ub, act, (size_t)M * c->I, st);
+    pf_lin(c, lay.m[6], act, M, o, i8, true);  // E:1373
+    const bool lastl = l + 1 == c->NL;
+    launch_pf_post_ff(o, x, a, ln.post_ff, lastl ? nullptr : c->L[l + 1]->ln().in_ln, c->fnorm.as<float>(),
+                      lay.scalar, c->pfh.as<float>(), lastl ? hrow : -1, M, st);
+  }
+}
+
+extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int nsplit, int* G0,
+                           float* hidden) {
+  if (!c) return G4V_E_ARG;
+  std::string what;
+  if (!c->model_ready || !model_complete(c, &what)) {
+    c->err = "prefill: " + (c->model_ready ? what : std::string("no model"));
+    return G4V_E_STATE;
+  }
+  ARGCHK(toks && n >= 1 && pos0 >= 0, "prefill: need tokens, n >= 1, pos0 >= 0");
+  ARGCHK((long long)pos0 + n <= c->ctxcap, "prefill: pos0 + n beyond the context capacity");
+  ARGCHK(pfb >= 1 && pfb <= 32, "prefill: 1 <= pfb <= 32 (the engine's row block, MM = 32)");
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT, "prefill: 1 <= nsplit <= 16");
+  for (int i = 0; i < n; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "prefill: token id outside the vocabulary");
+  HIPCHK(hipSetDevice(c->device));
+  // the last block; a short one past ATT_PAR = 192 (E:1214) takes the split-KV path, a 1-row one
+  // the exact-float GEMV (lin_multi's M >= 2 rule): both run as a segment of their own
+  const int Ml = n - (n - 1) / pfb * pfb, p0l = pos0 + n - Ml;
+  const bool tsplit = Ml <= 4 && p0l + Ml > 192, tail = tsplit || Ml == 1;
+  const int nA = tail ? n - Ml : n;
+  if (tsplit)
+    ARGCHK((Ml + p0l + nsplit - 1) / nsplit <= attn_pmax(), "prefill: more positions per split than the split buffer holds");
+  size_t sfl = 0;
+  for (int l = 0; l < c->NL; ++l) {
+    sfl = std::max(sfl, (size_t)pf_score_floats(nA, pos0, c->L[l]->sliding));
+    if (tail && !tsplit) sfl = std::max(sfl, (size_t)pf_score_floats(Ml, p0l, c->L[l]->sliding));
+  }
+  int r = pf_alloc(c, n, sfl);
+  if (r) return r;
+  HIPCHK(hipMemcpyAsync(c->pftok.p, toks, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
+  const PfGeom g{n, pos0, pfb};
+  if (nA > 0) pf_segment(c, g, 0, nA, true, false, nsplit, tail ? -1 : nA - 1);
+  if (tail) pf_segment(c, g, nA, Ml, Ml >= 2, tsplit, nsplit, Ml - 1);
+  HIPCHK(hipGetLastError());
+  std::vector<float> h(H);
+  HIPCHK(hipMemcpyAsync(h.data(), c->pfh.p, H * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  if (hidden) std::memcpy(hidden, h.data(), H * 4);
+  if (G0) {
+    int ns = 0, fb = 0;
+    r = g4v_head_argmax(c, h.data(), 1, G0, &ns, &fb);
+    if (r) return r;
   }
   return 0;
 }

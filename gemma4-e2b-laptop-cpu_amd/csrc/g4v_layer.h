@@ -26,6 +26,32 @@ struct VerifyResultDev {
   int pad2[3];
 };
 
+// E:326-343 ss_avx2: lane t (0..15) accumulates x[16 s + t]^2 in double over steps s;
+// s[k][l] = lane 4k + l; a[l] = (s[0][l]+s[1][l])+(s[2][l]+s[3][l]); ss = (a0+a2)+(a1+a3).
+// x is in LDS; red16 is LDS scratch; every thread returns ss.
+__device__ inline double block_sumsq(const float* x, int n, double* red16) {
+  if (threadIdx.x < 16) {
+    double s = 0;
+#pragma unroll 16
+    for (int i = threadIdx.x; i < n; i += 16) {  // loads run ahead; the FMA chain stays in order
+      const double d = (double)x[i];
+      s = fma(d, d, s);
+    }
+    red16[threadIdx.x] = s;
+  }
+  __syncthreads();
+  double a[4];
+  for (int l = 0; l < 4; ++l) a[l] = (red16[l] + red16[4 + l]) + (red16[8 + l] + red16[12 + l]);
+  const double ss = (a[0] + a[2]) + (a[1] + a[3]);
+  __syncthreads();
+  return ss;
+}
+
+// E:345: r = 1 / sqrtf((float)(ss / n) + 1e-6)
+__device__ __forceinline__ float rms_inv(double ss, int n) { return 1.0f / sqrtf((float)(ss / n) + 1e-6f); }
+
+constexpr int ROW_THREADS = 256;
+
 // per-layer pointers for the layer kernels
 struct LayerNorms {
   const float* in_ln;      // [H]
@@ -61,6 +87,26 @@ void launch_accept(const StepDev* sp, const int* best1, const int* best2, const 
 void launch_gen_bf16_normal(uint16_t* out, size_t n, uint64_t seed, float scale, hipStream_t st);
 void launch_gen_w4(uint8_t* w, uint16_t* s, size_t nbytes, size_t nscales, uint64_t sw, uint64_t ss,
                    hipStream_t st);
+
+// prefill (g4v_prefill.hip).  Rows r of a prompt of n rows sit at positions pos0 + r, in blocks
+// of pfb rows; a kernel over a segment of rows [r0, r0 + M) takes its rows' paths from this.
+struct PfGeom {
+  int n, pos0, pfb;
+};
+void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, float sqh, float* x, float* a, int M,
+                     hipStream_t st);
+// q [M][2048] normed + rotated in place; k, v [M][256] normed into the cache rows P0 ..
+void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
+                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st);
+// score scratch (floats) of M rows starting at position Pb
+long long pf_score_floats(int M, int Pb, int sliding);
+// attn_tile / run_mh attention of segment rows [r0, r0 + M): q [n][2048] (row r at r), att likewise
+void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
+                    int r0, int M, int sliding, hipStream_t st);
+void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st);
+void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStream_t st);
+void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
+                       const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st);
 
 // raw split-KV attention with explicit geometry (C-ABI entry point)
 struct AttnGeom {

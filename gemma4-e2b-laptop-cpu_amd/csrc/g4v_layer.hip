@@ -8,31 +8,6 @@
 
 namespace g4v {
 
-// E:326-343 ss_avx2: lane t (0..15) accumulates x[16 s + t]^2 in double over steps s;
-// s[k][l] = lane 4k + l; a[l] = (s[0][l]+s[1][l])+(s[2][l]+s[3][l]); ss = (a0+a2)+(a1+a3).
-// x is in LDS; red16 is LDS scratch; every thread returns ss.
-__device__ double block_sumsq(const float* x, int n, double* red16) {
-  if (threadIdx.x < 16) {
-    double s = 0;
-#pragma unroll 16
-    for (int i = threadIdx.x; i < n; i += 16) {  // loads run ahead; the FMA chain stays in order
-      const double d = (double)x[i];
-      s = fma(d, d, s);
-    }
-    red16[threadIdx.x] = s;
-  }
-  __syncthreads();
-  double a[4];
-  for (int l = 0; l < 4; ++l) a[l] = (red16[l] + red16[4 + l]) + (red16[8 + l] + red16[12 + l]);
-  const double ss = (a[0] + a[2]) + (a[1] + a[3]);
-  __syncthreads();
-  return ss;
-}
-
-// E:345: r = 1 / sqrtf((float)(ss / n) + 1e-6)
-__device__ __forceinline__ float rms_inv(double ss, int n) { return 1.0f / sqrtf((float)(ss / n) + 1e-6f); }
-
-constexpr int ROW_THREADS = 256;
 
 // Write a K-vector held in LDS (v, 16-byte aligned) as one row of the staged GEMV input
 // layout (staged_index) plus its group sums, each the sequential fp32 sum of the group's 32

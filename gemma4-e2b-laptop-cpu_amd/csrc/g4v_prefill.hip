@@ -1,0 +1,386 @@
+// g4v_prefill.hip -- the prompt pass (prefill) on gfx950: row kernels and the prefill attention.
+//
+// Restates run_req's prefill loop (E:1594-1599) with ENGINE_PREFILL_INT8=1 for the synthetic
+// stack: fwd (E:1256-1405) over blocks of pfb rows.  The rows of every block go through the
+// layer in one pass here (layer l of a row needs the KV rows of layer l of the earlier rows
+// only, so blocks may share passes); a block's size still picks its attention path:
+//   attn_tile (E:1063-1083) when M >= 4 and p0 + M > 64, run_mh (E:1338-1349) otherwise
+// (the split-KV case of a short tail block runs through the split kernels of the verify pass).
+// The linear layers are the W4A8 matrix-core GEMM (g4v_w4a8.hip); the row kernels below hold the
+// norms, RoPE, cache writes and residuals in plain [row][K] layouts.
+//
+// Prefill attention, per row r at position P (lo = P - 511 clamped at 0 on sliding layers, else
+// 0) and query head h, with K, V in the device cache layout (kc_index / vc_index):
+//   scores (k_pf_scores): s_p = q . k_p in the path's chain order (attn_tile: two 8-lane FMA
+//     chains over hd in steps of 16, summed lane-wise, then hsum; run_mh: one 8-lane chain in
+//     steps of 8, then hsum), written to a scratch row [8][P - lo + 1];
+//   output (k_pf_attn_out): mx = max_p s_p; attn_tile: w = exp8(s - mx), den = sum w in order,
+//     O = fma(w, v, O) in position order, out = r16(O * (1 / den)); run_mh: e = expf(s - mx),
+//     den = sum e in order, O = fma(e / den, v, O) in order, out = r16(O).
+#include <algorithm>
+
+#include "g4v_layer.h"
+
+namespace g4v {
+
+namespace {
+
+// attention path of row r (E:1305, 1328, 1337): its block [b pfb, ...) of M rows at p0
+__device__ __forceinline__ bool pf_tiled(int r, const PfGeom& g) {
+  const int b = r / g.pfb, M = min(g.pfb, g.n - b * g.pfb), p0 = g.pos0 + b * g.pfb;
+  return M >= 4 && p0 + M > 64;
+}
+__device__ __forceinline__ int pf_lo(int P, int sliding) { return sliding ? max(0, P - 511) : 0; }
+// offset of the score row of segment row rr (rows r0 + j, positions Pb + j, Pb = pos0 + r0)
+__device__ __forceinline__ long long pf_soff(int rr, int Pb, int sliding) {
+  const long long R = rr;
+  if (!sliding) return 8 * (R * (Pb + 1) + R * (R - 1) / 2);
+  const long long c = min(max(512 - Pb, 0), rr);  // rows whose range starts at 0
+  return 8 * (c * (Pb + 1) + c * (c - 1) / 2 + (R - c) * 512);
+}
+
+// E:1262-1267: x = r16(E[tok] * sqrt(H)); a = (x * r) * in_ln (unrounded: the W4A8 source)
+__global__ __launch_bounds__(ROW_THREADS) void k_pf_embed(const uint16_t* __restrict__ E, const int* __restrict__ toks,
+                                                          const float* __restrict__ in_ln, float sqh,
+                                                          float* __restrict__ x, float* __restrict__ a) {
+  __shared__ __align__(16) float xs[H];
+  __shared__ double red[16];
+  const int m = blockIdx.x;
+  const int tok = toks[m];
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
+    const float v = r16(bf2f(E[(size_t)tok * H + i]) * sqh);
+    xs[i] = v;
+    x[(size_t)m * H + i] = v;
+  }
+  __syncthreads();
+  const float r = rms_inv(block_sumsq(xs, H, red), H);
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) a[(size_t)m * H + i] = (xs[i] * r) * in_ln[i];
+}
+
+// E:1291-1303 / 1307-1324 for one row: the 8 query heads and k normed with their weights, v
+// without, all rounded to bf16 values; NeoX RoPE on q and k at position P; k, v to the cache
+__global__ __launch_bounds__(HD) void k_pf_qkv(float* __restrict__ q, const float* __restrict__ k,
+                                               const float* __restrict__ v, const float* __restrict__ qn,
+                                               const float* __restrict__ kn, const float* __restrict__ cs,
+                                               const float* __restrict__ sn, uint16_t* __restrict__ KC,
+                                               uint16_t* __restrict__ VC, int P0) {
+  constexpr int NV = NQ + 2;
+  __shared__ float xv[NV][HD];
+  __shared__ double part[NV][16];
+  __shared__ float rinv[NV];
+  const int m = blockIdx.x, e = threadIdx.x, P = P0 + m;
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) xv[h][e] = q[(size_t)m * NQ * HD + h * HD + e];
+  xv[NQ][e] = k[(size_t)m * HD + e];
+  xv[NQ + 1][e] = v[(size_t)m * HD + e];
+  __syncthreads();
+  if (e < NV * 16) {  // ss_avx2 order (E:326-343): lane t16 sums x[16 s + t16]^2 over s
+    const int row = e >> 4, t16 = e & 15;
+    double s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double d = (double)xv[row][16 * i + t16];
+      s = fma(d, d, s);
+    }
+    part[row][t16] = s;
+  }
+  __syncthreads();
+  if (e < NV) {
+    const double* p = part[e];
+    double a[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) a[l] = (p[l] + p[4 + l]) + (p[8 + l] + p[12 + l]);
+    rinv[e] = rms_inv((a[0] + a[2]) + (a[1] + a[3]), HD);
+  }
+  __syncthreads();
+  float y[NV];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) y[h] = r16((xv[h][e] * rinv[h]) * qn[e]);
+  y[NQ] = r16((xv[NQ][e] * rinv[NQ]) * kn[e]);
+  y[NQ + 1] = r16(xv[NQ + 1][e] * rinv[NQ + 1]);
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < NQ + 1; ++h) xv[h][e] = y[h];
+  __syncthreads();
+  // E:394-402 NeoX halves: out_i = fma(u, c, -(w s)) and out_{i+128} = fma(w, c, u s)
+  const int i2 = e & (HD / 2 - 1);
+  const float c = cs[(size_t)P * (HD / 2) + i2], sv = sn[(size_t)P * (HD / 2) + i2];
+  auto rot = [&](const float* yy) {
+    return e < HD / 2 ? fmaf(yy[e], c, -(yy[e + HD / 2] * sv)) : fmaf(yy[e], c, yy[e - HD / 2] * sv);
+  };
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) q[(size_t)m * NQ * HD + h * HD + e] = rot(xv[h]);
+  KC[kc_index(P, e)] = f2bf(rot(xv[NQ]));
+  VC[vc_index(P, e)] = f2bf(y[NQ + 1]);
+}
+
+// scores of one row against a span of 512 positions; thread (position j, head pair hp)
+constexpr int PF_SPAN = 512, PF_SUB = 64;
+__global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, const uint16_t* __restrict__ KC,
+                                                   float* __restrict__ S, PfGeom g, int r0, int sliding) {
+  __shared__ __align__(16) float qs[NQ][HD];                      // slot order (kc_slot)
+  __shared__ __align__(16) uint16_t ks[PF_SUB][HD + 8];           // one sub-span of key rows
+  const int rr = blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
+  const int sp0 = lo + blockIdx.y * PF_SPAN;
+  if (sp0 > P) return;  // uniform
+  const bool tiled = pf_tiled(r, g);
+  for (int idx = threadIdx.x; idx < NQ * HD; idx += 256) {
+    const int h = idx >> 8, e = idx & (HD - 1);
+    qs[h][kc_slot(e)] = q[(size_t)r * NQ * HD + idx];
+  }
+  float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
+  const int j = threadIdx.x & (PF_SUB - 1), hp = threadIdx.x >> 6;
+  const int sp1 = min(P, sp0 + PF_SPAN - 1);
+  for (int sb = sp0; sb <= sp1; sb += PF_SUB) {
+    __syncthreads();  // qs written / previous sub-span consumed
+    for (int idx = threadIdx.x; idx < PF_SUB * (HD / 8); idx += 256) {  // 16-byte pieces
+      const int pj = idx >> 5, c8 = idx & 31;
+      const int p = min(sb + pj, sp1);
+      *reinterpret_cast<uint4*>(&ks[pj][c8 * 8]) = *reinterpret_cast<const uint4*>(KC + (size_t)p * HD + c8 * 8);
+    }
+    __syncthreads();
+    const int p = sb + j;
+    if (p > sp1) continue;
+    float res[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float* qh = qs[2 * hp + u];
+      const uint16_t* kr = ks[j];
+      float acc[8][2];
+      if (tiled) {
+        // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...]: slots l*32 + s*16 + tt, tt in order
+#pragma unroll
+        for (int l = 0; l < 8; ++l)
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const int b = l * 32 + s * 16;
+            float kf[16];
+            const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b), k1 = *reinterpret_cast<const uint4*>(kr + b + 8);
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              kf[2 * c] = as_f32(kw[c] << 16);
+              kf[2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+            }
+            float a = 0.f;
+#pragma unroll
+            for (int tt = 0; tt < 16; ++tt) a = fmaf(qh[b + tt], kf[tt], a);
+            acc[l][s] = a;
+          }
+        float vv[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) vv[l] = acc[l][0] + acc[l][1];
+        res[u] = hsum8(vv);
+      } else {
+        // chain l over t = 0..31 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l:
+        // slots l*32 + (t & 1)*16 + (t >> 1)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const int b = l * 32;
+          float kf[32];
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) {
+            const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c4);
+            const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              kf[8 * c4 + 2 * c] = as_f32(kw[c] << 16);
+              kf[8 * c4 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+            }
+          }
+          float a = 0.f;
+#pragma unroll
+          for (int t = 0; t < 32; ++t) {
+            const int sl = (t & 1) * 16 + (t >> 1);
+            a = fmaf(qh[b + sl], kf[sl], a);
+          }
+          acc[l][0] = a;
+        }
+        float vv[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) vv[l] = acc[l][0];
+        res[u] = hsum8(vv);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) Srow[(size_t)(2 * hp + u) * len + (p - lo)] = res[u];
+  }
+}
+
+constexpr int PF_CP = 256;  // positions per weight chunk
+__global__ __launch_bounds__(HD) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
+                                                    float* __restrict__ att, PfGeom g, int r0, int sliding,
+                                                    ExpfTab tab) {
+  __shared__ float w[NQ][PF_CP];
+  __shared__ float red[NQ][HD / 64];
+  __shared__ float mxs[NQ], dens[NQ];
+  __shared__ uint64_t T[32];
+  const int rr = blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
+  const int i = threadIdx.x, lane = i & 63, wv = i >> 6;
+  const bool tiled = pf_tiled(r, g);
+  const float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
+  if (i < 32) T[i] = tab.t[i];
+  // max per head (order-free)
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    float mx = -1e30f;
+    for (int jj = i; jj < len; jj += HD) mx = fmaxf(mx, Srow[(size_t)h * len + jj]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[h][wv] = mx;
+  }
+  __syncthreads();
+  if (i < NQ) {
+    float mx = -1e30f;
+#pragma unroll
+    for (int k = 0; k < HD / 64; ++k) mx = fmaxf(mx, red[i][k]);
+    mxs[i] = mx;
+  }
+  __syncthreads();
+  float den = 0.f;  // threads 0..7: head i's sum in position order
+  if (!tiled) {     // run_mh divides by the sum before the V pass
+    for (int c0 = 0; c0 < len; c0 += PF_CP) {
+      const int cn = min(PF_CP, len - c0);
+      for (int idx = i; idx < NQ * PF_CP; idx += HD) {
+        const int h = idx / PF_CP, jj = idx % PF_CP;
+        if (jj < cn) w[h][jj] = libm_expf_neg(Srow[(size_t)h * len + c0 + jj] - mxs[h], T);
+      }
+      __syncthreads();
+      if (i < NQ)
+        for (int jj = 0; jj < cn; ++jj) den = den + w[i][jj];
+      __syncthreads();
+    }
+    if (i < NQ) dens[i] = den;
+    __syncthreads();
+  }
+  float O[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) O[h] = 0.f;
+  for (int c0 = 0; c0 < len; c0 += PF_CP) {
+    const int cn = min(PF_CP, len - c0);
+    for (int idx = i; idx < NQ * PF_CP; idx += HD) {
+      const int h = idx / PF_CP, jj = idx % PF_CP;
+      if (jj < cn) {
+        const float d = Srow[(size_t)h * len + c0 + jj] - mxs[h];
+        w[h][jj] = tiled ? exp8(d) : libm_expf_neg(d, T) / dens[h];
+      }
+    }
+    __syncthreads();
+    for (int jj = 0; jj < cn; ++jj) {
+      const float v = bf2f(VC[vc_index(lo + c0 + jj, i)]);
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][jj], v, O[h]);
+    }
+    if (tiled && i < NQ)
+      for (int jj = 0; jj < cn; ++jj) den = den + w[i][jj];
+    __syncthreads();
+  }
+  if (tiled) {
+    if (i < NQ) dens[i] = 1.0f / den;
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) att[(size_t)r * NQ * HD + h * HD + i] = r16(O[h] * dens[h]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) att[(size_t)r * NQ * HD + h * HD + i] = r16(O[h]);
+  }
+}
+
+// E:1358-1361 (W4A8 source kept): o = r16(o); tmp = rms(o, post_attn); x = r16(x + r16(tmp));
+// a = r16(rms(x, pre_ff))
+__global__ __launch_bounds__(ROW_THREADS) void k_pf_post_attn(const float* __restrict__ o, float* __restrict__ x,
+                                                              float* __restrict__ a, const float* __restrict__ w1,
+                                                              const float* __restrict__ w2) {
+  __shared__ __align__(16) float os[H];
+  __shared__ __align__(16) float xs[H];
+  __shared__ double red[16];
+  const int m = blockIdx.x;
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) os[i] = r16(o[(size_t)m * H + i]);
+  __syncthreads();
+  const float r1 = rms_inv(block_sumsq(os, H, red), H);
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
+    const float v = r16(x[(size_t)m * H + i] + r16((os[i] * r1) * w1[i]));
+    xs[i] = v;
+    x[(size_t)m * H + i] = v;
+  }
+  __syncthreads();
+  const float r2 = rms_inv(block_sumsq(xs, H, red), H);
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) a[(size_t)m * H + i] = r16((xs[i] * r2) * w2[i]);
+}
+
+// E:1369-1370: act = r16(r16(gelu8(r16 g)) * r16 u)
+__global__ void k_pf_act(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ act, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    act[i] = r16(r16(gelu8(r16(g[i]))) * r16(u[i]));
+}
+
+// E:1375-1404 with a zero per-layer-embedding branch: o = r16(o); tmp = rms(o, post_ff);
+// x = r16(x + r16(tmp)); x = r16(x * scalar); then a = rms(x, next in_ln) (unrounded) or, after
+// the last layer and for row `hrow` only, h = r16(rms(x, fnorm))
+__global__ __launch_bounds__(ROW_THREADS) void k_pf_post_ff(const float* __restrict__ o, float* __restrict__ x,
+                                                            float* __restrict__ a, const float* __restrict__ w1,
+                                                            const float* __restrict__ next_in_ln,
+                                                            const float* __restrict__ fnorm, float scalar,
+                                                            float* __restrict__ h, int hrow) {
+  __shared__ __align__(16) float os[H];
+  __shared__ __align__(16) float xs[H];
+  __shared__ double red[16];
+  const int m = blockIdx.x;
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) os[i] = r16(o[(size_t)m * H + i]);
+  __syncthreads();
+  const float r1 = rms_inv(block_sumsq(os, H, red), H);
+  for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
+    float v = r16(x[(size_t)m * H + i] + r16((os[i] * r1) * w1[i]));
+    v = r16(v * scalar);
+    xs[i] = v;
+    x[(size_t)m * H + i] = v;
+  }
+  if (!next_in_ln && m != hrow) return;  // uniform
+  __syncthreads();
+  const float r2 = rms_inv(block_sumsq(xs, H, red), H);
+  if (next_in_ln) {
+    for (int i = threadIdx.x; i < H; i += ROW_THREADS) a[(size_t)m * H + i] = (xs[i] * r2) * next_in_ln[i];
+  } else {
+    for (int i = threadIdx.x; i < H; i += ROW_THREADS) h[i] = r16((xs[i] * r2) * fnorm[i]);
+  }
+}
+
+}  // namespace
+
+void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, float sqh, float* x, float* a, int M,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(k_pf_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, toks, in_ln, sqh, x, a);
+}
+void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
+                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st) {
+  hipLaunchKernelGGL(k_pf_qkv, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0);
+}
+long long pf_score_floats(int M, int Pb, int sliding) {
+  const long long R = M;
+  if (!sliding) return 8 * (R * (Pb + 1) + R * (R - 1) / 2);
+  const long long c = std::min<long long>(std::max(512 - Pb, 0), R);
+  return 8 * (c * (Pb + 1) + c * (c - 1) / 2 + (R - c) * 512);
+}
+void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
+                    int r0, int M, int sliding, hipStream_t st) {
+  const int Plast = g.pos0 + r0 + M - 1;
+  const int maxlen = sliding ? std::min(Plast + 1, 512) : Plast + 1;
+  const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
+  hipLaunchKernelGGL(k_pf_scores, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
+  ExpfTab tab{G4V_EXPF_TABLE};
+  hipLaunchKernelGGL(k_pf_attn_out, dim3(M), dim3(HD), 0, st, S, VC, att, g, r0, sliding, tab);
+}
+void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st) {
+  hipLaunchKernelGGL(k_pf_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, a, w1, w2);
+}
+void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStream_t st) {
+  const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_pf_act, dim3(grid), dim3(256), 0, st, g, u, act, n);
+}
+void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
+                       const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st) {
+  hipLaunchKernelGGL(k_pf_post_ff, dim3(M), dim3(ROW_THREADS), 0, st, o, x, a, w1, next_in_ln, fnorm, scalar, h,
+                     hrow);
+}
+
+}  // namespace g4v

@@ -51,6 +51,7 @@ SIGNATURES = {
     "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
     "g4v_sync": (_i, [_vp]),
     "g4v_set_graphs": (_i, [_vp, _i]),
+    "g4v_prefill": (_i, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(_i), _vp]),
     "g4v_history_set": (_i, [_vp, _i32p, _i]),
     "g4v_prompt_lookup": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_i)]),
     "g4v_history_read": (_i, [_vp, _vp, _i, C.POINTER(_i)]),
@@ -248,6 +249,16 @@ class Device:
         self._ok(self.L.g4v_model_read(self.h, what.encode(), out.ctypes.data, out.nbytes, C.byref(nb)),
                  f"model_read {what}")
         return out
+
+    # ---- prefill ----
+    def prefill(self, toks, pos0=0, pfb=32, nsplit=8, hidden=False):
+        """prompt pass; returns the first generated token (and the last row's hidden state)"""
+        toks = _c(toks, np.int32)
+        g0 = _i()
+        hid = np.empty(1536, np.float32)
+        self._ok(self.L.g4v_prefill(self.h, toks, toks.size, pos0, pfb, nsplit, C.byref(g0), hid.ctypes.data),
+                 "prefill")
+        return (g0.value, hid) if hidden else g0.value
 
     # ---- prompt-lookup drafter ----
     def history_set(self, toks):

@@ -115,6 +115,16 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
  * graph launch).  on = 0 launches every kernel from the host instead. */
 int g4v_set_graphs(g4v_ctx* c, int on);
 
+/* ---- prefill: run_req's prompt loop (E:1594-1599) with ENGINE_PREFILL_INT8=1, i.e. fwd
+ * (E:1256-1405) over blocks of pfb rows (ENGINE_PREFILL_BLOCK, 32 by default), W4A8 linear layers
+ * (w4a8::quant + tile, engine/w4a8_avx2.h:30-61) for blocks of M >= 2 rows, and the engine's
+ * attention path per block: attn_tile (E:1063-1083), run_mh (E:1338-1349) or split-KV with
+ * nsplit splits (E:1305-1327).  toks[0..n) sit at positions pos0..; every layer's KV rows are
+ * written.  G0 = greedy token of the last row (the first generated token, E:1601), hidden
+ * (optional, [1536]) = that row's final-normed state.  Needs a model (g4v_model_synth or
+ * g4v_model_create + set calls) and pos0 + n <= ctxcap. */
+int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int nsplit, int* G0, float* hidden);
+
 /* ---- prompt-lookup drafter (run_req, E:1624-1628) over a history kept on the device.
  * history_set: seq = toks[0..L), the prompt followed by the generated tokens (E:1625). */
 int g4v_history_set(g4v_ctx* c, const int* toks, int L);
