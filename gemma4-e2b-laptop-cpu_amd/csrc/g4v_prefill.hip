@@ -114,12 +114,13 @@ __global__ __launch_bounds__(HD) void k_pf_qkv(float* __restrict__ q, const floa
   VC[vc_index(P, e)] = f2bf(y[NQ + 1]);
 }
 
-// scores of one row against a span of 512 positions; thread (position j, head pair hp)
-constexpr int PF_SPAN = 512, PF_SUB = 64;
+// scores of one row against a span of 256 positions: lane = position, all 8 heads per lane (the
+// key row is read and widened once for the 8 heads); the query heads sit in LDS in slot order
+// (kc_slot), so every lane of a wave reads the same LDS word (broadcast)
+constexpr int PF_SPAN = 256;
 __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, const uint16_t* __restrict__ KC,
                                                    float* __restrict__ S, PfGeom g, int r0, int sliding) {
-  __shared__ __align__(16) float qs[NQ][HD];                      // slot order (kc_slot)
-  __shared__ __align__(16) uint16_t ks[PF_SUB][HD + 8];           // one sub-span of key rows
+  __shared__ __align__(16) float qs[NQ][HD];
   const int rr = blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
   const int sp0 = lo + blockIdx.y * PF_SPAN;
   if (sp0 > P) return;  // uniform
@@ -128,90 +129,88 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
     const int h = idx >> 8, e = idx & (HD - 1);
     qs[h][kc_slot(e)] = q[(size_t)r * NQ * HD + idx];
   }
-  float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
-  const int j = threadIdx.x & (PF_SUB - 1), hp = threadIdx.x >> 6;
-  const int sp1 = min(P, sp0 + PF_SPAN - 1);
-  for (int sb = sp0; sb <= sp1; sb += PF_SUB) {
-    __syncthreads();  // qs written / previous sub-span consumed
-    for (int idx = threadIdx.x; idx < PF_SUB * (HD / 8); idx += 256) {  // 16-byte pieces
-      const int pj = idx >> 5, c8 = idx & 31;
-      const int p = min(sb + pj, sp1);
-      *reinterpret_cast<uint4*>(&ks[pj][c8 * 8]) = *reinterpret_cast<const uint4*>(KC + (size_t)p * HD + c8 * 8);
-    }
-    __syncthreads();
-    const int p = sb + j;
-    if (p > sp1) continue;
-    float res[2];
+  __syncthreads();
+  const int p = sp0 + threadIdx.x;
+  if (p > P) return;  // no barrier follows
+  const uint16_t* kr = KC + (size_t)p * HD;
+  float vv[NQ][8];
+  if (tiled) {
+    // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...]: slots l*32 + s*16 + tt, tt in order;
+    // vv[h][l] = chain (l, 0) + chain (l, 1)
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float* qh = qs[2 * hp + u];
-      const uint16_t* kr = ks[j];
-      float acc[8][2];
-      if (tiled) {
-        // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...]: slots l*32 + s*16 + tt, tt in order
+    for (int l = 0; l < 8; ++l) {
+      float ch[NQ][2];
 #pragma unroll
-        for (int l = 0; l < 8; ++l)
+      for (int s = 0; s < 2; ++s) {
+        const int b = l * 32 + s * 16;
+        const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b), k1 = *reinterpret_cast<const uint4*>(kr + b + 8);
+        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        float kf[16];
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const int b = l * 32 + s * 16;
-            float kf[16];
-            const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b), k1 = *reinterpret_cast<const uint4*>(kr + b + 8);
-            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        for (int c = 0; c < 8; ++c) {
+          kf[2 * c] = as_f32(kw[c] << 16);
+          kf[2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+        }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-              kf[2 * c] = as_f32(kw[c] << 16);
-              kf[2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
-            }
-            float a = 0.f;
-#pragma unroll
-            for (int tt = 0; tt < 16; ++tt) a = fmaf(qh[b + tt], kf[tt], a);
-            acc[l][s] = a;
-          }
-        float vv[8];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) vv[l] = acc[l][0] + acc[l][1];
-        res[u] = hsum8(vv);
-      } else {
-        // chain l over t = 0..31 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l:
-        // slots l*32 + (t & 1)*16 + (t >> 1)
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-          const int b = l * 32;
-          float kf[32];
-#pragma unroll
-          for (int c4 = 0; c4 < 4; ++c4) {
-            const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c4);
-            const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              kf[8 * c4 + 2 * c] = as_f32(kw[c] << 16);
-              kf[8 * c4 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
-            }
-          }
+        for (int h = 0; h < NQ; ++h) {
+          const float4* q4 = reinterpret_cast<const float4*>(&qs[h][b]);
           float a = 0.f;
 #pragma unroll
-          for (int t = 0; t < 32; ++t) {
-            const int sl = (t & 1) * 16 + (t >> 1);
-            a = fmaf(qh[b + sl], kf[sl], a);
+          for (int c = 0; c < 4; ++c) {
+            const float4 qq = q4[c];
+            a = fmaf(qq.x, kf[4 * c], a);
+            a = fmaf(qq.y, kf[4 * c + 1], a);
+            a = fmaf(qq.z, kf[4 * c + 2], a);
+            a = fmaf(qq.w, kf[4 * c + 3], a);
           }
-          acc[l][0] = a;
+          ch[h][s] = a;
         }
-        float vv[8];
+      }
 #pragma unroll
-        for (int l = 0; l < 8; ++l) vv[l] = acc[l][0];
-        res[u] = hsum8(vv);
+      for (int h = 0; h < NQ; ++h) vv[h][l] = ch[h][0] + ch[h][1];
+    }
+  } else {
+    // chain l over t = 0..31 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l:
+    // slots l*32 + (t & 1)*16 + (t >> 1)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const int b = l * 32;
+      float kf[32];
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c4);
+        const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          kf[8 * c4 + 2 * c] = as_f32(kw[c] << 16);
+          kf[8 * c4 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        float a = 0.f;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+          const int sl = (t & 1) * 16 + (t >> 1);
+          a = fmaf(qs[h][b + sl], kf[sl], a);
+        }
+        vv[h][l] = a;
       }
     }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) Srow[(size_t)(2 * hp + u) * len + (p - lo)] = res[u];
   }
+  float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) Srow[(size_t)h * len + (p - lo)] = hsum8(vv[h]);
 }
 
+// output of one row: thread i = dim i of the 8 heads.  Weights of PF_CP positions at a time go
+// to LDS; the value rows are read 8 positions (16 bytes of a dim) at a time where the positions
+// are 8-aligned, one at a time at the edges of the range
 constexpr int PF_CP = 256;  // positions per weight chunk
 __global__ __launch_bounds__(HD) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
                                                     float* __restrict__ att, PfGeom g, int r0, int sliding,
                                                     ExpfTab tab) {
-  __shared__ float w[NQ][PF_CP];
+  __shared__ __align__(16) float w[NQ][PF_CP];
   __shared__ float red[NQ][HD / 64];
   __shared__ float mxs[NQ], dens[NQ];
   __shared__ uint64_t T[32];
@@ -256,6 +255,8 @@ __global__ __launch_bounds__(HD) void k_pf_attn_out(const float* __restrict__ S,
   float O[NQ];
 #pragma unroll
   for (int h = 0; h < NQ; ++h) O[h] = 0.f;
+  const uint16_t* vcol = VC + (size_t)i * 32;  // dim i of position p: vcol[(p >> 5) * 32 HD + (p & 31)]
+  auto vat = [&](int p) { return vcol + (size_t)(p >> 5) * (32 * HD) + (p & 31); };
   for (int c0 = 0; c0 < len; c0 += PF_CP) {
     const int cn = min(PF_CP, len - c0);
     for (int idx = i; idx < NQ * PF_CP; idx += HD) {
@@ -266,10 +267,32 @@ __global__ __launch_bounds__(HD) void k_pf_attn_out(const float* __restrict__ S,
       }
     }
     __syncthreads();
-    for (int jj = 0; jj < cn; ++jj) {
-      const float v = bf2f(VC[vc_index(lo + c0 + jj, i)]);
+    const int pa = lo + c0, pe = pa + cn;          // positions [pa, pe) of this chunk
+    const int a8 = min((pa + 7) & ~7, pe), e8 = max(pe & ~7, a8);
+    for (int p = pa; p < a8; ++p) {                 // leading positions up to an 8-boundary
+      const float v = bf2f(*vat(p));
 #pragma unroll
-      for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][jj], v, O[h]);
+      for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][p - pa], v, O[h]);
+    }
+    for (int p = a8; p < e8; p += 8) {              // 8 positions of dim i: one 16-byte load
+      const uint4 vq = *reinterpret_cast<const uint4*>(vat(p));
+      const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
+      float vf[8];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        vf[2 * c] = as_f32(vw[c] << 16);
+        vf[2 * c + 1] = as_f32(vw[c] & 0xFFFF0000u);
+      }
+      const int j0 = p - pa;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][j0 + t], vf[t], O[h]);
+    }
+    for (int p = e8; p < pe; ++p) {                 // trailing positions
+      const float v = bf2f(*vat(p));
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][p - pa], v, O[h]);
     }
     if (tiled && i < NQ)
       for (int jj = 0; jj < cn; ++jj) den = den + w[i][jj];
