@@ -121,7 +121,8 @@ constexpr int PF_SPAN = 256;
 __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, const uint16_t* __restrict__ KC,
                                                    float* __restrict__ S, PfGeom g, int r0, int sliding) {
   __shared__ __align__(16) float qs[NQ][HD];
-  const int rr = blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
+  // the last rows (longest ranges) first, so that the long blocks do not trail the grid
+  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
   const int sp0 = lo + blockIdx.y * PF_SPAN;
   if (sp0 > P) return;  // uniform
   const bool tiled = pf_tiled(r, g);
@@ -203,109 +204,150 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
   for (int h = 0; h < NQ; ++h) Srow[(size_t)h * len + (p - lo)] = hsum8(vv[h]);
 }
 
-// output of one row: thread i = dim i of the 8 heads.  Weights of PF_CP positions at a time go
-// to LDS; the value rows are read 8 positions (16 bytes of a dim) at a time where the positions
+// output of one row: one wave, lane l holds dims 4l .. 4l+3 of the 8 heads (32 accumulators), so
+// each weight read from LDS (wave-uniform) feeds 4 FMAs.  Weights of PF_CP positions at a time
+// go to LDS; the value rows are read 8 positions (16 bytes of a dim) at a time where positions
 // are 8-aligned, one at a time at the edges of the range
-constexpr int PF_CP = 256;  // positions per weight chunk
-__global__ __launch_bounds__(HD) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
+constexpr int PF_CP = 256;  // positions per weight chunk (4 per lane)
+__global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
                                                     float* __restrict__ att, PfGeom g, int r0, int sliding,
                                                     ExpfTab tab) {
   __shared__ __align__(16) float w[NQ][PF_CP];
-  __shared__ float red[NQ][HD / 64];
-  __shared__ float mxs[NQ], dens[NQ];
   __shared__ uint64_t T[32];
-  const int rr = blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
-  const int i = threadIdx.x, lane = i & 63, wv = i >> 6;
+  // the last rows (longest ranges) first, so that the long blocks do not trail the grid
+  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
+  const int lane = threadIdx.x;
   const bool tiled = pf_tiled(r, g);
   const float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
-  if (i < 32) T[i] = tab.t[i];
-  // max per head (order-free)
+  if (lane < 32) T[lane] = tab.t[lane];
+  float mx[NQ];  // max per head (order-free), on every lane
 #pragma unroll
   for (int h = 0; h < NQ; ++h) {
-    float mx = -1e30f;
-    for (int jj = i; jj < len; jj += HD) mx = fmaxf(mx, Srow[(size_t)h * len + jj]);
+    float m = -1e30f;
+    for (int jj = lane; jj < len; jj += 64) m = fmaxf(m, Srow[(size_t)h * len + jj]);
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) red[h][wv] = mx;
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    mx[h] = m;
   }
-  __syncthreads();
-  if (i < NQ) {
-    float mx = -1e30f;
-#pragma unroll
-    for (int k = 0; k < HD / 64; ++k) mx = fmaxf(mx, red[i][k]);
-    mxs[i] = mx;
-  }
-  __syncthreads();
-  float den = 0.f;  // threads 0..7: head i's sum in position order
+  __syncthreads();  // T
+  float den = 0.f;  // lanes 0..7: head `lane`'s sum in position order
   if (!tiled) {     // run_mh divides by the sum before the V pass
     for (int c0 = 0; c0 < len; c0 += PF_CP) {
       const int cn = min(PF_CP, len - c0);
-      for (int idx = i; idx < NQ * PF_CP; idx += HD) {
-        const int h = idx / PF_CP, jj = idx % PF_CP;
-        if (jj < cn) w[h][jj] = libm_expf_neg(Srow[(size_t)h * len + c0 + jj] - mxs[h], T);
+#pragma unroll
+      for (int k = 0; k < PF_CP / 64; ++k) {
+        const int jj = lane + 64 * k;
+        if (jj < cn)
+#pragma unroll
+          for (int h = 0; h < NQ; ++h) w[h][jj] = libm_expf_neg(Srow[(size_t)h * len + c0 + jj] - mx[h], T);
       }
       __syncthreads();
-      if (i < NQ)
-        for (int jj = 0; jj < cn; ++jj) den = den + w[i][jj];
+      if (lane < NQ)
+        for (int jj = 0; jj < cn; ++jj) den = den + w[lane][jj];
       __syncthreads();
     }
-    if (i < NQ) dens[i] = den;
-    __syncthreads();
   }
-  float O[NQ];
+  float dh[NQ];  // run_mh: the sums, on every lane
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) O[h] = 0.f;
-  const uint16_t* vcol = VC + (size_t)i * 32;  // dim i of position p: vcol[(p >> 5) * 32 HD + (p & 31)]
-  auto vat = [&](int p) { return vcol + (size_t)(p >> 5) * (32 * HD) + (p & 31); };
+  for (int h = 0; h < NQ; ++h) dh[h] = __shfl(den, h);
+  float O[NQ][4];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) O[h][d] = 0.f;
+  // dim 4 lane + d of position p: vcol + d * 32 + (p >> 5) * 32 HD + (p & 31)
+  const uint16_t* vcol = VC + (size_t)(4 * lane) * 32;
+  auto vat = [&](int p, int d) { return vcol + d * 32 + (size_t)(p >> 5) * (32 * HD) + (p & 31); };
+  float sreg[PF_CP / 64][NQ];  // scores of this lane's positions of the next chunk
+#pragma unroll
+  for (int k = 0; k < PF_CP / 64; ++k)
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) sreg[k][h] = lane + 64 * k < len ? Srow[(size_t)h * len + lane + 64 * k] : 0.f;
   for (int c0 = 0; c0 < len; c0 += PF_CP) {
     const int cn = min(PF_CP, len - c0);
-    for (int idx = i; idx < NQ * PF_CP; idx += HD) {
-      const int h = idx / PF_CP, jj = idx % PF_CP;
-      if (jj < cn) {
-        const float d = Srow[(size_t)h * len + c0 + jj] - mxs[h];
-        w[h][jj] = tiled ? exp8(d) : libm_expf_neg(d, T) / dens[h];
-      }
+#pragma unroll
+    for (int k = 0; k < PF_CP / 64; ++k) {
+      const int jj = lane + 64 * k;
+      if (jj < cn)
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) {
+          const float dd = sreg[k][h] - mx[h];
+          w[h][jj] = tiled ? exp8(dd) : libm_expf_neg(dd, T) / dh[h];
+        }
     }
     __syncthreads();
-    const int pa = lo + c0, pe = pa + cn;          // positions [pa, pe) of this chunk
-    const int a8 = min((pa + 7) & ~7, pe), e8 = max(pe & ~7, a8);
-    for (int p = pa; p < a8; ++p) {                 // leading positions up to an 8-boundary
-      const float v = bf2f(*vat(p));
 #pragma unroll
-      for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][p - pa], v, O[h]);
+    for (int k = 0; k < PF_CP / 64; ++k) {
+      const int jj = c0 + PF_CP + lane + 64 * k;
+      if (jj < len)
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) sreg[k][h] = Srow[(size_t)h * len + jj];
     }
-    for (int p = a8; p < e8; p += 8) {              // 8 positions of dim i: one 16-byte load
-      const uint4 vq = *reinterpret_cast<const uint4*>(vat(p));
-      const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
-      float vf[8];
+    const int pa = lo + c0, pe = pa + cn;  // positions [pa, pe) of this chunk
+    const int a8 = min((pa + 7) & ~7, pe), e8 = max(pe & ~7, a8);
+    for (int p = pa; p < a8; ++p) {        // leading positions up to an 8-boundary
+      float v[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        vf[2 * c] = as_f32(vw[c] << 16);
-        vf[2 * c + 1] = as_f32(vw[c] & 0xFFFF0000u);
+      for (int d = 0; d < 4; ++d) v[d] = bf2f(*vat(p, d));
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        const float ww = w[h][p - pa];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) O[h][d] = fmaf(ww, v[d], O[h][d]);
       }
+    }
+    for (int p = a8; p < e8; p += 8) {     // 8 positions of each of the lane's 4 dims
+      uint4 vq[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) vq[d] = *reinterpret_cast<const uint4*>(vat(p, d));
       const int j0 = p - pa;
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
+      for (int t2 = 0; t2 < 4; ++t2) {     // positions j0 + 2 t2, j0 + 2 t2 + 1
+        float va[4], vb[4];
 #pragma unroll
-        for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][j0 + t], vf[t], O[h]);
-    }
-    for (int p = e8; p < pe; ++p) {                 // trailing positions
-      const float v = bf2f(*vat(p));
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t u = t2 == 0 ? vq[d].x : (t2 == 1 ? vq[d].y : (t2 == 2 ? vq[d].z : vq[d].w));
+          va[d] = as_f32(u << 16);
+          vb[d] = as_f32(u & 0xFFFF0000u);
+        }
 #pragma unroll
-      for (int h = 0; h < NQ; ++h) O[h] = fmaf(w[h][p - pa], v, O[h]);
+        for (int h = 0; h < NQ; ++h) {
+          const float wa = w[h][j0 + 2 * t2], wb = w[h][j0 + 2 * t2 + 1];  // j0 may be odd
+#pragma unroll
+          for (int d = 0; d < 4; ++d) O[h][d] = fmaf(wa, va[d], O[h][d]);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) O[h][d] = fmaf(wb, vb[d], O[h][d]);
+        }
+      }
     }
-    if (tiled && i < NQ)
-      for (int jj = 0; jj < cn; ++jj) den = den + w[i][jj];
+    for (int p = e8; p < pe; ++p) {        // trailing positions
+      float v[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) v[d] = bf2f(*vat(p, d));
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        const float ww = w[h][p - pa];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) O[h][d] = fmaf(ww, v[d], O[h][d]);
+      }
+    }
+    if (tiled && lane < NQ)
+      for (int jj = 0; jj < cn; ++jj) den = den + w[lane][jj];
     __syncthreads();
   }
+  float* orow = att + (size_t)r * NQ * HD + 4 * lane;
   if (tiled) {
-    if (i < NQ) dens[i] = 1.0f / den;
-    __syncthreads();
+    const float inv = 1.0f / den;  // lanes 0..7
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) att[(size_t)r * NQ * HD + h * HD + i] = r16(O[h] * dens[h]);
+    for (int h = 0; h < NQ; ++h) {
+      const float ih = __shfl(inv, h);
+      *reinterpret_cast<float4*>(orow + h * HD) =
+          make_float4(r16(O[h][0] * ih), r16(O[h][1] * ih), r16(O[h][2] * ih), r16(O[h][3] * ih));
+    }
   } else {
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) att[(size_t)r * NQ * HD + h * HD + i] = r16(O[h]);
+    for (int h = 0; h < NQ; ++h)
+      *reinterpret_cast<float4*>(orow + h * HD) = make_float4(r16(O[h][0]), r16(O[h][1]), r16(O[h][2]), r16(O[h][3]));
   }
 }
 
@@ -391,7 +433,7 @@ void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, floa
   const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
   hipLaunchKernelGGL(k_pf_scores, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
   ExpfTab tab{G4V_EXPF_TABLE};
-  hipLaunchKernelGGL(k_pf_attn_out, dim3(M), dim3(HD), 0, st, S, VC, att, g, r0, sliding, tab);
+  hipLaunchKernelGGL(k_pf_attn_out, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab);
 }
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st) {
   hipLaunchKernelGGL(k_pf_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, a, w1, w2);

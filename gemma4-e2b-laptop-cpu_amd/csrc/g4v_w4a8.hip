@@ -205,24 +205,35 @@ __global__ __launch_bounds__(256) void k_w4a8_gemm(const uint4* __restrict__ tw,
     }
 }
 
-// Register-blocked variant for long M (prefill): one wave per NT consecutive 16-column tiles and
-// MT m-tiles, so that every activation fragment (and its correction and row scales) feeds NT
-// MFMAs and every decoded weight fragment MT of them.  Same arithmetic as k_w4a8_gemm.
-template <int MT, int NT>
-__global__ __launch_bounds__(256) void k_w4a8_gemm_rb(const uint4* __restrict__ tw, const uint4* __restrict__ ts,
-                                                      const uint16_t* __restrict__ xqb, const float* __restrict__ sxt,
-                                                      const float* __restrict__ corr, float* __restrict__ y, int M,
-                                                      int Mpad, int N, int K, int ldy) {
-  const int lane = threadIdx.x & 63;
+// LDS-staged variant for long M (prefill): a block of 4 waves covers 64 rows (MT = 4 m-tiles)
+// and 4 x NT 16-column tiles.  The block's activation fragments, corrections and row scales of
+// a chunk of 4 groups are loaded once per block (not once per wave) a chunk ahead into
+// registers, then written to the other half of a double-buffered LDS stage; one barrier per
+// chunk.  Same arithmetic, in the same order, as k_w4a8_gemm.
+constexpr int A8_ROWB = 128 * 2 + 16;  // bytes of one staged row: 4 groups x 32 bf16, + pad
+template <int NT>
+__global__ __launch_bounds__(256) void k_w4a8_gemm_lds(const uint4* __restrict__ tw, const uint4* __restrict__ ts,
+                                                       const uint16_t* __restrict__ xqb, const float* __restrict__ sxt,
+                                                       const float* __restrict__ corr, float* __restrict__ y, int M,
+                                                       int Mpad, int N, int K, int ldy) {
+  constexpr int MT = 4;
+  __shared__ __align__(16) uint8_t As[2][64 * A8_ROWB];
+  __shared__ __align__(16) float Cs[2][4][64], Ss[2][4][64];
+  const int lane = threadIdx.x & 63, tid = threadIdx.x;
   const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * NT;  // first 16-column tile of the wave
-  if (t0 >= N / 16) return;  // whole waves; N / 16 is a multiple of NT (checked by the launcher)
-  const int m0 = blockIdx.y * 16 * MT;
+  const bool active = t0 < N / 16;                            // idle waves still stage and wait
+  const int m0 = blockIdx.y * 64;
   const int r = lane & 15, h = lane >> 4;
-  const int G = K / 32;
-  const uint4* wp = tw + (size_t)t0 * (G / 4) * 64 + lane;  // tile t0 + u, chunk c at + (u * G / 4 + c) * 64
-  const uint4* sp = ts + (size_t)t0 * (G / 8) * 16 + r;     // tile t0 + u, 8 groups c8 at + (u * G / 8 + c8) * 16
-  const uint16_t* ap = xqb + (size_t)(m0 + r) * K + 8 * h;   // m-tile mt, group g at + 16 mt K + 32 g
-  const int mrow = m0 + 4 * h;
+  const int G = K / 32, NC = G / 4;
+  const int tt0 = active ? t0 : 0;
+  const uint4* wp = tw + (size_t)tt0 * (G / 4) * 64 + lane;
+  const uint4* sp = ts + (size_t)tt0 * (G / 8) * 16 + r;
+  // staging roles: thread tid loads 16-byte pieces tid, tid + 256, tid + 512, tid + 768 of the
+  // 64 x 256-byte chunk (row = piece / 16, column piece % 16), i.e. column tid % 16 of rows
+  // tid / 16 + 16 k, and entry tid of the 4 x 64 corrections / scales
+  const int sg = tid >> 6, sm = tid & 63;
+  const uint16_t* arow = xqb + (size_t)(m0 + (tid >> 4)) * K + 8 * (tid & 15);  // piece tid; + 16 rows per k
+  const int aoff = (tid >> 4) * A8_ROWB + 16 * (tid & 15);
   float acc[MT][NT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -236,45 +247,78 @@ __global__ __launch_bounds__(256) void k_w4a8_gemm_rb(const uint4* __restrict__ 
     wv[u] = wp[(size_t)u * (G / 4) * 64];
     sv[u] = sp[(size_t)u * (G / 8) * 16];
   }
-  for (int c = 0; c < G / 4; ++c) {
+  uint4 a0 = *reinterpret_cast<const uint4*>(arow), a1 = *reinterpret_cast<const uint4*>(arow + 16 * K),
+        a2 = *reinterpret_cast<const uint4*>(arow + 32 * K), a3 = *reinterpret_cast<const uint4*>(arow + 48 * K);
+  float crn = corr[(size_t)sg * Mpad + m0 + sm], sxn = sxt[(size_t)sg * Mpad + m0 + sm];
+  *reinterpret_cast<uint4*>(&As[0][aoff]) = a0;
+  *reinterpret_cast<uint4*>(&As[0][aoff + 16 * A8_ROWB]) = a1;
+  *reinterpret_cast<uint4*>(&As[0][aoff + 32 * A8_ROWB]) = a2;
+  *reinterpret_cast<uint4*>(&As[0][aoff + 48 * A8_ROWB]) = a3;
+  Cs[0][sg][sm] = crn;
+  Ss[0][sg][sm] = sxn;
+  __syncthreads();
+  for (int c = 0; c < NC; ++c) {
+    const int b = c & 1;
+    if (c + 1 < NC) {  // uniform: the next chunk's rows, corrections and scales
+      const uint16_t* an = arow + 128 * (c + 1);
+      a0 = *reinterpret_cast<const uint4*>(an);
+      a1 = *reinterpret_cast<const uint4*>(an + 16 * K);
+      a2 = *reinterpret_cast<const uint4*>(an + 32 * K);
+      a3 = *reinterpret_cast<const uint4*>(an + 48 * K);
+      crn = corr[(size_t)(4 * (c + 1) + sg) * Mpad + m0 + sm];
+      sxn = sxt[(size_t)(4 * (c + 1) + sg) * Mpad + m0 + sm];
+    }
     uint4 wcur[NT], scur[NT];
 #pragma unroll
     for (int u = 0; u < NT; ++u) {
       wcur[u] = wv[u];
       scur[u] = sv[u];
-      if (c + 1 < G / 4) wv[u] = wp[((size_t)u * (G / 4) + c + 1) * 64];
-      if ((c & 1) && c + 1 < G / 4) sv[u] = sp[((size_t)u * (G / 8) + ((c + 1) >> 1)) * 16];
+      if (c + 1 < NC) wv[u] = wp[((size_t)u * (G / 4) + c + 1) * 64];
+      if ((c & 1) && c + 1 < NC) sv[u] = sp[((size_t)u * (G / 8) + ((c + 1) >> 1)) * 16];
     }
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * c + i, gi = 4 * (c & 1) + i;
-      bf16x8_t B[NT];
-      float sw[NT];
-#pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        const uint32_t d = i == 0 ? wcur[u].x : (i == 1 ? wcur[u].y : (i == 2 ? wcur[u].z : wcur[u].w));
-        B[u] = a8_decode(d);
-        const uint32_t s2 = gi < 2 ? scur[u].x : (gi < 4 ? scur[u].y : (gi < 6 ? scur[u].z : scur[u].w));
-        sw[u] = as_f32((gi & 1) ? (s2 & 0xFFFF0000u) : (s2 << 16));
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint4 av = *reinterpret_cast<const uint4*>(ap + (size_t)mt * 16 * K + 32 * g);
-        const float4 cr = *reinterpret_cast<const float4*>(corr + (size_t)g * Mpad + mrow + 16 * mt);
-        const float4 sx = *reinterpret_cast<const float4*>(sxt + (size_t)g * Mpad + mrow + 16 * mt);
-        const f32x4_t cin = {cr.x, cr.y, cr.z, cr.w};
-        const bf16x8_t A = __builtin_bit_cast(bf16x8_t, av);
+      for (int i = 0; i < 4; ++i) {
+        const int gi = 4 * (c & 1) + i;
+        bf16x8_t B[NT];
+        float sw[NT];
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
-          const f32x4_t a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[u], cin, 0, 0, 0);
-          acc[mt][u][0] = fmaf(a[0], sw[u] * sx.x, acc[mt][u][0]);  // A8:59
-          acc[mt][u][1] = fmaf(a[1], sw[u] * sx.y, acc[mt][u][1]);
-          acc[mt][u][2] = fmaf(a[2], sw[u] * sx.z, acc[mt][u][2]);
-          acc[mt][u][3] = fmaf(a[3], sw[u] * sx.w, acc[mt][u][3]);
+          const uint32_t d = i == 0 ? wcur[u].x : (i == 1 ? wcur[u].y : (i == 2 ? wcur[u].z : wcur[u].w));
+          B[u] = a8_decode(d);
+          const uint32_t s2 = gi < 2 ? scur[u].x : (gi < 4 ? scur[u].y : (gi < 6 ? scur[u].z : scur[u].w));
+          sw[u] = as_f32((gi & 1) ? (s2 & 0xFFFF0000u) : (s2 << 16));
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint4 av = *reinterpret_cast<const uint4*>(&As[b][(16 * mt + r) * A8_ROWB + 64 * i + 16 * h]);
+          const float4 cr = *reinterpret_cast<const float4*>(&Cs[b][i][16 * mt + 4 * h]);
+          const float4 sx = *reinterpret_cast<const float4*>(&Ss[b][i][16 * mt + 4 * h]);
+          const f32x4_t cin = {cr.x, cr.y, cr.z, cr.w};
+          const bf16x8_t A = __builtin_bit_cast(bf16x8_t, av);
+#pragma unroll
+          for (int u = 0; u < NT; ++u) {
+            const f32x4_t a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[u], cin, 0, 0, 0);
+            acc[mt][u][0] = fmaf(a[0], sw[u] * sx.x, acc[mt][u][0]);  // A8:59
+            acc[mt][u][1] = fmaf(a[1], sw[u] * sx.y, acc[mt][u][1]);
+            acc[mt][u][2] = fmaf(a[2], sw[u] * sx.z, acc[mt][u][2]);
+            acc[mt][u][3] = fmaf(a[3], sw[u] * sx.w, acc[mt][u][3]);
+          }
         }
       }
     }
+    if (c + 1 < NC) {  // the other half: last read before the previous barrier
+      *reinterpret_cast<uint4*>(&As[b ^ 1][aoff]) = a0;
+      *reinterpret_cast<uint4*>(&As[b ^ 1][aoff + 16 * A8_ROWB]) = a1;
+      *reinterpret_cast<uint4*>(&As[b ^ 1][aoff + 32 * A8_ROWB]) = a2;
+      *reinterpret_cast<uint4*>(&As[b ^ 1][aoff + 48 * A8_ROWB]) = a3;
+      Cs[b ^ 1][sg][sm] = crn;
+      Ss[b ^ 1][sg][sm] = sxn;
+    }
+    __syncthreads();
   }
+  if (!active) return;
+  const int mrow = m0 + 4 * h;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -296,9 +340,9 @@ int w4a8_mpad(int M) {
 void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, const float* sxt, const float* corr,
                       float* y, int M, int N, int K, int ldy, hipStream_t st) {
   const int MT = w4a8_mt(M), Mpad = w4a8_mpad(M);
-  if (MT == 4 && (N / 16) % 4 == 0) {  // long M: 4 x 4 tiles per wave
+  if (MT == 4 && (N / 16) % 4 == 0 && K % 128 == 0) {  // long M: 4 x 4 tiles per wave, staged rows
     const dim3 grid((N / 16 / 4 + 3) / 4, Mpad / 64);
-    hipLaunchKernelGGL((k_w4a8_gemm_rb<4, 4>), grid, dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
+    hipLaunchKernelGGL(k_w4a8_gemm_lds<4>, grid, dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
     return;
   }
   const dim3 grid((N / 16 + 3) / 4, Mpad / (16 * MT));
