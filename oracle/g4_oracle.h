@@ -31,6 +31,8 @@
  *   attn_tile                                  live (the reference's attn_tile) + fp64 softmax
  *   attn_mh                                    fp64 softmax only (run_mh is a lambda inside main(),
  *                                              E:1338-1349): parity unpinned at the bit level
+ *   drafter (b16 gemv, draft step)             b16 gemv live against b16_rows; the step against
+ *                                              the harness composition of the engine's kernels
  *   model / verify                             golden passes through the reference's kernels
  *                                              (2 layers, V 262144), acceptance brute force
  * Generators (g4_rng.h) are pinned by the CRC-32 of every input the fixtures store.
@@ -150,6 +152,18 @@ void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T,
 
 /* forward of M rows that fills the KV cache only (want = false) */
 void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T);
+
+/* ---- MTP drafter step (E:1534-1563) on the synthetic target; see g4_oracle_draft.c ---- */
+typedef struct g4o_drafter g4o_drafter;
+g4o_drafter* g4o_drafter_new(uint64_t seed, int V);
+void g4o_drafter_free(g4o_drafter* d);
+const void* g4o_drafter_ptr(const g4o_drafter* d, const char* what);
+int g4o_model_ctx(const g4o_model* m);
+/* b16_rows (E:586-614): y [N] = W [N][K] bf16 . x [K] */
+void g4o_b16_gemv(const uint16_t* W, int N, int K, const float* x, float* y);
+/* one draft step: returns the draft token; b_out [1536], sec, gap as E:1553, 1559 */
+int g4o_draft_step(const g4o_model* m, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
+                   float* b_out, int* sec, float* gap);
 
 /* ---- seeded input generators (g4_rng.h formulas) ---- */
 uint64_t g4o_stream(uint64_t seed, uint64_t tag);

@@ -166,6 +166,8 @@ void g4o_model_fake_ctx(g4o_model* m, int n, uint64_t seed) {
     }
 }
 
+int g4o_model_ctx(const g4o_model* m) { return m->ctx; }
+
 /* borrow a pointer to a named internal array (the reference harness runs on the same weights) */
 const void* g4o_model_ptr(const g4o_model* m, const char* what) {
   int l = 0, j = 0;

@@ -73,6 +73,10 @@ class Oracle:
             "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
             "g4o_prefill": (None, [_vp, _i32p, _i, _i, _i, _i, _vp]),
+            "g4o_drafter_new": (_vp, [C.c_uint64, _i]), "g4o_drafter_free": (None, [_vp]),
+            "g4o_drafter_ptr": (_vp, [_vp, C.c_char_p]),
+            "g4o_b16_gemv": (None, [_u16p, _i, _i, _f32p, _f32p]),
+            "g4o_draft_step": (_i, [_vp, _vp, _i, _f32p, _i, _i, _i, _f32p, C.POINTER(_i), C.POINTER(_f)]),
             "g4o_attn_tile": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _f32p, _i]),
             "g4o_attn_mh": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _f32p, _i]),
             "g4o_stream": (_u64, [_u64, _u64]),
@@ -268,6 +272,32 @@ class Model:
         return out, hid
 
 
+class Drafter:
+    """Oracle synthetic MTP drafter (g4_oracle_draft.c) on a target Model."""
+
+    def __init__(self, orc, seed, V):
+        self.o, self.V, self.C = orc, V, V // 128
+        self.h = orc.L.g4o_drafter_new(seed, V)
+
+    def close(self):
+        if self.h:
+            self.o.L.g4o_drafter_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def ptr(self, what):
+        return self.o.L.g4o_drafter_ptr(self.h, what.encode())
+
+    def step(self, model, tok, h, pos, P, T=6):
+        """one draft step: (token, b_out [1536], second-best token, gap)"""
+        b = np.empty(1536, np.float32)
+        sec, gap = _i(), _f()
+        t = self.o.L.g4o_draft_step(model.h, self.h, tok, _c(h, np.float32), pos, P, T, b, C.byref(sec), C.byref(gap))
+        return t, b, sec.value, gap.value
+
+
 class RefLayer(C.Structure):
     _fields_ = [("W", _vp * 7), ("S", _vp * 7), ("nv", _vp * 6), ("scalar", _f), ("sliding", _i)]
 
@@ -275,6 +305,12 @@ class RefLayer(C.Structure):
 class RefModel(C.Structure):
     _fields_ = [("V", _i), ("NL", _i), ("I", _i), ("ctx", _i), ("E", _vp), ("fnorm", _vp), ("KC", _vp), ("VC", _vp),
                 ("cs", _vp * 2), ("sn", _vp * 2), ("L", RefLayer * 64)]
+
+
+class RefDrafter(C.Structure):
+    _fields_ = [("pre", _vp), ("post", _vp), ("cent", _vp), ("emb", _vp), ("q", _vp * 4), ("o", _vp * 4),
+                ("gate", _vp * 4), ("up", _vp * 4), ("down", _vp * 4), ("nv", (_vp * 5) * 4), ("dnorm", _vp),
+                ("order", _vp), ("C", _i)]
 
 
 class RefOut(C.Structure):
@@ -319,6 +355,9 @@ class Ref:
             "ref_attn_mh": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_prefill": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _vp]),
             "ref_pack_reset": (None, []),
+            "ref_b16": (None, [_u16p, _i, _i, _f32p, _f32p]),
+            "ref_draft_step": (_i, [C.POINTER(RefModel), C.POINTER(RefDrafter), _i, _f32p, _i, _i, _i, _f32p,
+                                    C.POINTER(_i), C.POINTER(_f)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -347,6 +386,33 @@ class Ref:
         self.L.ref_head_setup(ptr("Wq"), ptr("Sq"), ptr("coef"), ptr("x3"), ptr("cb"), ptr("xptr"), ptr("xcol"),
                               ptr("xdel"), model.V)
         self.model = rm
+
+    def bind_drafter(self, dr):
+        rd = RefDrafter()
+        for f in ("pre", "post", "cent", "emb", "order"):
+            setattr(rd, f, dr.ptr(f))
+        rd.dnorm = dr.ptr("dnorm")
+        for l in range(4):
+            rd.q[l], rd.o[l], rd.gate[l], rd.up[l], rd.down[l] = (dr.ptr(f"L{l}_{t}") for t in range(5))
+            for t in range(5):
+                rd.nv[l][t] = dr.ptr(f"L{l}_{10 + t}")
+        rd.C = dr.C
+        self.drafter = rd
+
+    def draft_step(self, tok, h, pos, P, T=6):
+        b = np.empty(1536, np.float32)
+        sec, gap = _i(), _f()
+        t = self.L.ref_draft_step(C.byref(self.model), C.byref(self.drafter), tok, _c(h, np.float32), pos, P, T, b,
+                                  C.byref(sec), C.byref(gap))
+        if t < 0:
+            raise ValueError("ref_draft_step: needs 1 <= T <= 16 and a target of at least 15 layers")
+        return t, b, sec.value, gap.value
+
+    def b16(self, W, x):
+        W = _c(W, np.uint16)
+        y = np.empty(W.shape[0], np.float32)
+        self.L.ref_b16(W, W.shape[0], W.shape[1], _c(x, np.float32), y)
+        return y
 
     def attn_rows(self, kind, Kc, Vc, sliding, q, pos0):
         """attn_tile / run_mh of rows q [M][2048] at pos0 .. pos0+M-1 (causal, window 512 if sliding)"""

@@ -641,6 +641,154 @@ int ref_prefill(RefModel* md, const int* toks, int n, int pos0, int pfb, float* 
   return 0;
 }
 
+
+// ---------------------------------------------------------------------------------------
+// MTP drafter step (E:1534-1563) on a synthetic drafter: the engine's b16_rows (through
+// b16_multi), d_gate_up_task, dcand_task, attn_task + attn_merge, rms, rms_r16_inplace,
+// rope_avx2, composed as draft_step does; the top-32 and best / second-best scans restate the
+// lambda's lines.  Tensors come from the oracle's drafter (g4o_drafter_ptr names).
+// ---------------------------------------------------------------------------------------
+struct RefDrafter {
+  const uint16_t *pre, *post, *cent, *emb;
+  const uint16_t *q[4], *o[4], *gate[4], *up[4], *down[4];
+  const float* nv[4][5];
+  const float* dnorm;
+  const int64_t* order;
+  int C;
+};
+
+void ref_b16(const uint16_t* W, int N, int K, const float* x, float* y) {
+  B16 m{W, N, K};
+  b16_1(x, m, y);
+}
+
+int ref_draft_step(RefModel* md, const RefDrafter* d, int tok, const float* h, int pos, int P, int T, float* b_out,
+                   int* sec_out, float* gap_out) {
+  const int H = 1536;
+  if (T < 1 || T > 16 || md->NL < 15) return -1;
+  alignas(32) static float dcomb[3072], dx[256], da[256], dq[1024], dopt[1024], dtmp[256], dgate[2048], dup[2048],
+      dact[2048], dh[256];
+  static std::vector<float> dscore;
+  static int cand[4096];
+  static float cscore[4096];
+  dscore.resize(d->C);
+  G_I8_ACTIVE = false;
+  const __m256 vsqh = _mm256_set1_ps(sqrtf((float)H));
+  const uint16_t* er = md->E + (size_t)tok * H;
+  for (int i = 0; i < H; i += 8) _mm256_storeu_ps(dcomb + i, rbf8(_mm256_mul_ps(bf8(er + i), vsqh)));
+  std::memcpy(dcomb + H, h, H * 4);
+  b16_1(dcomb, B16{d->pre, 256, 3072}, dx);
+  rbf_n(dx, 256);
+  for (int l = 0; l < 4; ++l) {
+    const int hd = 256, ty = l < 3 ? 0 : 1, ol = l < 3 ? 13 : 14;
+    const float* cs = md->cs[ty] + (size_t)pos * hd / 2;
+    const float* sn = md->sn[ty] + (size_t)pos * hd / 2;
+    rms(dx, d->nv[l][0], 256, da);
+    b16_1(da, B16{d->q[l], 1024, 256}, dq);
+    for (int h2 = 0; h2 < 4; ++h2) {
+      float* qh = dq + h2 * hd;
+      rms_r16_inplace(qh, d->nv[l][4], hd);
+      rope_avx2(qh, cs, sn, hd);
+    }
+    {
+      AttnArg aa;
+      aa.Kc = md->KC + (size_t)ol * md->ctx * 256;
+      aa.Vc = md->VC + (size_t)ol * md->ctx * 256;
+      aa.hd = hd;
+      aa.nh = 4;
+      aa.M = 1;
+      aa.q[0] = dq;
+      aa.pos[0] = P;
+      aa.skip_lo[0] = 1;
+      aa.skip_hi[0] = 0;
+      aa.lo[0] = l < 3 ? std::max(0, pos - 511) : 0;
+      aa.kmin = aa.lo[0];
+      aa.kmax = P;
+      float* outp[1] = {dopt};
+      for (int t = 0; t < T; ++t) attn_task(&aa, t, T);
+      attn_merge(aa, T, outp);
+    }
+    b16_1(dopt, B16{d->o[l], 256, 1024}, da);
+    rbf_n(da, 256);
+    rms(da, d->nv[l][1], 256, dtmp);
+    add_res_inplace(dx, dtmp, 256);
+    rms(dx, d->nv[l][2], 256, da);
+    rbf_n(da, 256);
+    {
+      B16 gm{d->gate[l], 2048, 256}, um{d->up[l], 2048, 256};
+      DGateUpArg dgua{da, &gm, &um, dgate, dup, dact};
+      POOL.run(d_gate_up_task, &dgua);
+    }
+    b16_1(dact, B16{d->down[l], 256, 2048}, da);
+    rbf_n(da, 256);
+    rms(da, d->nv[l][3], 256, dtmp);
+    add_res_inplace(dx, dtmp, 256);
+    const __m256 vdsc = _mm256_set1_ps(0.75f);
+    for (int i = 0; i < 256; i += 8) _mm256_storeu_ps(dx + i, rbf8(_mm256_mul_ps(_mm256_loadu_ps(dx + i), vdsc)));
+  }
+  rms(dx, d->dnorm, 256, dh);
+  rbf_n(dh, 256);
+  {
+    B16 pm{d->post, 1536, 256}, cm{d->cent, d->C, 256};
+    const B16* mm[2] = {&pm, &cm};
+    float* yy[2] = {b_out, dscore.data()};
+    b16_multi(dh, 2, mm, yy);
+  }
+  rbf_n(b_out, H);
+  int top[32];
+  {
+    float thr[32];
+    int cnt = 0;
+    for (int c = 0; c < d->C; ++c) {
+      float s = dscore[c];
+      if (cnt < 32) {
+        int j = cnt++;
+        while (j > 0 && thr[j - 1] < s) {
+          thr[j] = thr[j - 1];
+          top[j] = top[j - 1];
+          --j;
+        }
+        thr[j] = s;
+        top[j] = c;
+      } else if (s > thr[31]) {
+        int j = 31;
+        while (j > 0 && thr[j - 1] < s) {
+          thr[j] = thr[j - 1];
+          top[j] = top[j - 1];
+          --j;
+        }
+        thr[j] = s;
+        top[j] = c;
+      }
+    }
+  }
+  int nc = 0;
+  for (int t = 0; t < 32; ++t)
+    for (int j = 0; j < 128; ++j) cand[nc++] = (int)d->order[(size_t)top[t] * 128 + j];
+  {
+    DCandArg dca{d->emb, cand, dh, cscore, nc};
+    POOL.run(dcand_task, &dca);
+  }
+  int bestc = cand[0];
+  float bs = -1e30f, bs2 = -1e30f;
+  int sec = -1;
+  for (int ci = 0; ci < nc; ++ci) {
+    float sc2 = cscore[ci];
+    if (sc2 > bs) {
+      bs2 = bs;
+      sec = bestc;
+      bs = sc2;
+      bestc = cand[ci];
+    } else if (sc2 > bs2) {
+      bs2 = sc2;
+      sec = cand[ci];
+    }
+  }
+  if (sec_out) *sec_out = sec;
+  if (gap_out) *gap_out = bs - bs2;
+  return bestc;
+}
+
 int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* out) {
   const int H = 1536, M = 1 + na + nb, NL = md->NL, I = md->I;
   if (M > 8 || md->V != 262144) return -1;
