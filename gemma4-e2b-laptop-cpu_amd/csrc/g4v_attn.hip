@@ -459,12 +459,12 @@ void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, con
 }
 
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
-                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st) {
+                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh) {
   AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
              nullptr};
-  hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
+  hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
                      (const StepDev*)nullptr, 0, g.T);
-  hipLaunchKernelGGL(k_attn_merge, dim3(g.M, NQ), dim3(HD), 0, st, P, g.M, g.T);
+  hipLaunchKernelGGL(k_attn_merge, dim3(g.M, nh), dim3(HD), 0, st, P, g.M, g.T);
 }
 
 int attn_pmax() { return ATT_PMAX; }

@@ -104,6 +104,12 @@ struct g4v_ctx {
   DBuf pfx, pfa, pfq, pfk, pfv, pfatt, pfo, pfg, pfu, pfact, pfxq, pfsx, pfcorr, pfs, pftok, pfh;
   int pf_rows = 0, pf_I = 0;  // rows and FFN width the buffers were sized for
   size_t pf_sfl = 0;
+  // MTP drafter: tensors, then scratch of a chain (dx, da, y, q, att, act, dh, two hidden
+  // states, centroid scores, candidates and their scores, tokens, runners-up, gaps)
+  bool dr_ready = false;
+  int dr_C = 0;
+  DBuf dr_pre, dr_post, dr_cent, dr_emb, dr_order, dr_norms, dr_q[4], dr_o[4], dr_g[4], dr_u[4], dr_d[4], dr_s;
+  int last_hrow = -1;  // row of c->h holding the last verify step's committed hidden state
   // prompt-lookup history (prompt + committed tokens) and the lookup's result words
   DBuf hist, plout;
   int hist_len = 0, hist_cap = 0;
@@ -1301,10 +1307,9 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
     out->fallback[i] = r.fallback[i];
     out->nsurv[i] = r.nsurv[i];
   }
-  if (hidden) {
-    const int last = r.hrows[r.ncommit - 1];
-    HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)last * H, H * 4, hipMemcpyDeviceToHost));
-  }
+  c->last_hrow = r.hrows[r.ncommit - 1];
+  if (hidden)
+    HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)c->last_hrow * H, H * 4, hipMemcpyDeviceToHost));
   return 0;
 }
 
@@ -1454,6 +1459,212 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
     r = g4v_head_argmax(c, h.data(), 1, G0, &ns, &fb);
     if (r) return r;
   }
+  return 0;
+}
+
+
+// ---------------------------------------------------------------------------------------
+// MTP drafter
+// ---------------------------------------------------------------------------------------
+namespace {
+constexpr int DR_H = 256, DR_Q = 4, DR_F = 2048, DR_NC = 32 * 128;
+// scratch layout (floats / ints) of a drafter chain
+struct DrScratch {
+  float *dx[2], *yo, *ydown, *dq, *dopt, *act, *dh, *bout[2], *hin, *dscore, *cscore, *gap;
+  int *top, *tok, *sec;
+};
+DrScratch dr_scratch(g4v_ctx* c) {
+  float* f = c->dr_s.as<float>();
+  DrScratch d;
+  d.dx[0] = f;
+  d.dx[1] = d.dx[0] + DR_H;
+  d.yo = d.dx[1] + DR_H;
+  d.ydown = d.yo + DR_H;
+  d.dq = d.ydown + DR_H;
+  d.dopt = d.dq + DR_Q * DR_H;
+  d.act = d.dopt + DR_Q * DR_H;
+  d.dh = d.act + DR_F;
+  d.bout[0] = d.dh + DR_H;
+  d.bout[1] = d.bout[0] + H;
+  d.hin = d.bout[1] + H;
+  d.dscore = d.hin + H;
+  d.cscore = d.dscore + 4096;
+  d.gap = d.cscore + DR_NC;
+  int* ip = reinterpret_cast<int*>(d.gap + 16);
+  d.top = ip;
+  d.tok = d.top + 32;
+  d.sec = d.tok + 16;
+  return d;
+}
+constexpr size_t DR_SCRATCH_BYTES =
+    (size_t)(5 * DR_H + 2 * DR_Q * DR_H + DR_F + 3 * H + 4096 + DR_NC + 16) * 4 + (size_t)(32 + 16 + 16) * 4;
+}  // namespace
+
+extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
+  if (!c) return G4V_E_ARG;
+  if (!c->model_ready) {
+    c->err = "drafter_synth: no model";
+    return G4V_E_STATE;
+  }
+  ARGCHK(c->V % 2048 == 0 && c->V / 128 >= 32 && c->V / 128 <= 4096,
+         "drafter_synth: the vocabulary must be 128 x C tokens with 32 <= C <= 4096 centroids, C % 16 == 0");
+  ARGCHK(c->NL >= 15, "drafter_synth: the drafter reads the KV cache of target layers 13 and 14");
+  HIPCHK(hipSetDevice(c->device));
+  hipStream_t st = c->st;
+  const int V = c->V, C = V / 128;
+  auto gen = [&](DBuf& b, size_t n, uint64_t tag, float scale) -> int {
+    ALLOC(b, n * 2);
+    launch_gen_bf16_normal(b.as<uint16_t>(), n, rng_stream(seed, tag), scale, st);
+    return 0;
+  };
+  int r;
+  if ((r = gen(c->dr_pre, (size_t)DR_H * 2 * H, 5000, 0.02f))) return r;
+  for (int l = 0; l < 4; ++l) {
+    if ((r = gen(c->dr_q[l], (size_t)DR_Q * DR_H * DR_H, 5100 + 10 * l, 0.06f)) ||
+        (r = gen(c->dr_o[l], (size_t)DR_H * DR_Q * DR_H, 5101 + 10 * l, 0.03f)) ||
+        (r = gen(c->dr_g[l], (size_t)DR_F * DR_H, 5102 + 10 * l, 0.06f)) ||
+        (r = gen(c->dr_u[l], (size_t)DR_F * DR_H, 5103 + 10 * l, 0.06f)) ||
+        (r = gen(c->dr_d[l], (size_t)DR_H * DR_F, 5104 + 10 * l, 0.02f)))
+      return r;
+  }
+  if ((r = gen(c->dr_post, (size_t)H * DR_H, 5300, 0.06f)) || (r = gen(c->dr_cent, (size_t)C * DR_H, 5301, 0.06f)) ||
+      (r = gen(c->dr_emb, (size_t)V * DR_H, 5303, 0.06f)))
+    return r;
+  // norms [4][5][256] (in_ln, post_attn, pre_ff, post_ff, q_norm) then the final norm [256]
+  std::vector<float> nv(21 * DR_H);
+  for (int l = 0; l < 4; ++l)
+    for (int t = 0; t < 5; ++t) {
+      const uint64_t sn = rng_stream(seed, 5200 + 10 * (uint64_t)l + t);
+      const float base = t < 4 ? 0.5f : 0.2f, span = t < 4 ? 1.0f : 0.1f;
+      for (int i = 0; i < DR_H; ++i) nv[(l * 5 + t) * DR_H + i] = r16(base + span * rng_unif(sn, i));
+    }
+  {
+    const uint64_t sn = rng_stream(seed, 5302);
+    for (int i = 0; i < DR_H; ++i) nv[20 * DR_H + i] = r16(0.5f + rng_unif(sn, i));
+  }
+  std::vector<int> order(V);
+  for (int i = 0; i < V; ++i) order[i] = i;
+  const uint64_t so = rng_stream(seed, 5304);
+  for (int i = V - 1; i >= 1; --i) std::swap(order[i], order[(int)(rng_hash(so, (uint64_t)i) % (uint64_t)(i + 1))]);
+  ALLOC(c->dr_norms, nv.size() * 4);
+  ALLOC(c->dr_order, (size_t)V * 4);
+  ALLOC(c->dr_s, DR_SCRATCH_BYTES);
+  HIPCHK(hipMemcpyAsync(c->dr_norms.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(c->dr_order.p, order.data(), (size_t)V * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipStreamSynchronize(st));
+  c->dr_C = C;
+  c->dr_ready = true;
+  return 0;
+}
+
+extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, int nsplit, int* drafts, int* sec,
+                             float* gap, float* hidden) {
+  if (!c) return G4V_E_ARG;
+  if (!c->dr_ready) {
+    c->err = "draft_mtp: no drafter (g4v_drafter_synth first)";
+    return G4V_E_STATE;
+  }
+  ARGCHK(drafts && k >= 1 && k <= 8 && P >= 0 && P + k < c->ctxcap, "draft_mtp: 1 <= k <= 8, P + k < ctxcap");
+  ARGCHK(tok >= 0 && tok < c->V, "draft_mtp: token outside the vocabulary");
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT && (P + 1 + nsplit - 1) / nsplit <= attn_pmax(),
+         "draft_mtp: 1 <= nsplit <= 16 and no more positions per split than the split buffer holds");
+  if (!h && c->last_hrow < 0) {
+    c->err = "draft_mtp: no hidden state given and no verify step ran";
+    return G4V_E_STATE;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  hipStream_t st = c->st;
+  const DrScratch d = dr_scratch(c);
+  const float* nv = c->dr_norms.as<float>();
+  auto nrm = [&](int l, int t) { return nv + (l * 5 + t) * DR_H; };
+  const float* hsrc = c->h.as<float>() + (size_t)std::max(c->last_hrow, 0) * H;
+  if (h) {
+    HIPCHK(hipMemcpyAsync(d.hin, h, H * 4, hipMemcpyHostToDevice, st));
+    hsrc = d.hin;
+  }
+  HIPCHK(hipMemcpyAsync(d.tok, &tok, 4, hipMemcpyHostToDevice, st));
+  for (int j = 0; j < k; ++j) {  // E:1631-1633: step j at position P + 1 + j, keys up to P
+    const int pos = P + 1 + j;
+    const float* hj = j == 0 ? hsrc : d.bout[(j - 1) & 1];
+    float* dxc = d.dx[0];  // the residual ping-pongs between d.dx[0] and d.dx[1]
+    auto next_dx = [&]() { return dxc == d.dx[0] ? d.dx[1] : d.dx[0]; };
+    {
+      B16Launch L;
+      L.W = c->dr_pre.as<uint16_t>(), L.N = DR_H, L.K = 2 * H, L.x = hj, L.y = dxc, L.pro = 3, L.epi = 1;
+      L.E = c->E.as<uint16_t>(), L.tok = d.tok + j;
+      launch_b16(L, st);
+    }
+    for (int l = 0; l < 4; ++l) {
+      const bool sliding = l < 3;
+      const int ty = sliding ? 0 : 1, ol = sliding ? 13 : 14;
+      const float* cs = c->rope.as<float>() + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
+      const float* sn = cs + (size_t)c->ctxcap * (HD / 2);
+      {  // q (E:1541), with the previous layer's post-FFN block in front (E:1548-1550)
+        B16Launch L;
+        L.W = c->dr_q[l].as<uint16_t>(), L.N = DR_Q * DR_H, L.K = DR_H, L.x = dxc, L.y = d.dq, L.nw = nrm(l, 0);
+        if (l == 0) {
+          L.pro = 1;
+        } else {
+          L.pro = 5, L.yin = d.ydown, L.w1 = nrm(l - 1, 3), L.scalar = 0.75f, L.dxout = next_dx();
+          dxc = L.dxout;
+        }
+        launch_b16(L, st);
+      }
+      launch_dr_qnorm(d.dq, nrm(l, 4), cs, sn, pos, st);
+      AttnGeom ag{};
+      ag.M = 1;
+      ag.T = nsplit;
+      ag.pos[0] = P;
+      ag.lo[0] = sliding ? std::max(0, pos - 511) : 0;
+      ag.skip_lo[0] = 1;
+      ag.skip_hi[0] = 0;
+      ag.kmin = ag.lo[0];
+      ag.kmax = P;
+      launch_attn_geom(c->KC.as<uint16_t>() + (size_t)ol * c->kvcap * HD, c->VC.as<uint16_t>() + (size_t)ol * c->kvcap * HD,
+                       d.dq, DR_Q * DR_H, ag, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), d.dopt,
+                       DR_Q * DR_H, st, DR_Q);
+      {  // o (E:1545)
+        B16Launch L;
+        L.W = c->dr_o[l].as<uint16_t>(), L.N = DR_H, L.K = DR_Q * DR_H, L.x = d.dopt, L.y = d.yo;
+        launch_b16(L, st);
+      }
+      {  // gate / up + activation (E:1547), with the post-attention block in front (E:1545-1546)
+        B16Launch L;
+        L.W = c->dr_g[l].as<uint16_t>(), L.W2 = c->dr_u[l].as<uint16_t>(), L.N = DR_F, L.K = DR_H, L.x = dxc;
+        L.y = d.act, L.pro = 4, L.epi = 2, L.yin = d.yo, L.w1 = nrm(l, 1), L.nw = nrm(l, 2), L.dxout = next_dx();
+        dxc = L.dxout;
+        launch_b16(L, st);
+      }
+      {  // down (E:1548)
+        B16Launch L;
+        L.W = c->dr_d[l].as<uint16_t>(), L.N = DR_H, L.K = DR_F, L.x = d.act, L.y = d.ydown;
+        launch_b16(L, st);
+      }
+    }
+    {  // the last post-FFN block, the final norm (E:1551), post-projection and centroid scores
+      B16Launch L;
+      L.W = c->dr_post.as<uint16_t>(), L.N = H, L.K = DR_H, L.x = dxc, L.y = d.bout[j & 1], L.pro = 6, L.epi = 1;
+      L.yin = d.ydown, L.w1 = nrm(3, 3), L.scalar = 0.75f, L.nw = nrm(4, 0), L.xout = d.dh;
+      launch_b16(L, st);
+      L.W = c->dr_cent.as<uint16_t>(), L.N = c->dr_C, L.y = d.dscore, L.epi = 0, L.xout = nullptr;
+      launch_b16(L, st);
+    }
+    launch_dr_rank(d.dscore, c->dr_C, d.top, st);
+    {  // the 32 x 128 candidates against dh (E:1556-1557)
+      B16Launch L;
+      L.W = c->dr_emb.as<uint16_t>(), L.N = DR_NC, L.K = DR_H, L.x = d.dh, L.y = d.cscore;
+      L.top = d.top, L.order = c->dr_order.as<int>();
+      launch_b16(L, st);
+    }
+    launch_dr_best(d.cscore, d.top, c->dr_order.as<int>(), DR_NC, d.tok + j + 1, d.sec + j, d.gap + j, st);
+  }
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(drafts, d.tok + 1, (size_t)k * 4, hipMemcpyDeviceToHost, st));
+  if (sec) HIPCHK(hipMemcpyAsync(sec, d.sec, (size_t)k * 4, hipMemcpyDeviceToHost, st));
+  if (gap) HIPCHK(hipMemcpyAsync(gap, d.gap, (size_t)k * 4, hipMemcpyDeviceToHost, st));
+  if (hidden) HIPCHK(hipMemcpyAsync(hidden, d.bout[(k - 1) & 1], H * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
   return 0;
 }
 

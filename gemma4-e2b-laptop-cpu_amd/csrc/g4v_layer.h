@@ -108,13 +108,43 @@ void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStre
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
                        const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st);
 
+// MTP drafter (g4v_mtp.hip): one bf16 product y[n] = W[row(n)] . input, input prologue `pro`
+// (0 x, 1 rms(x, nw), 2 r16(rms(x, nw)), 3 [r16(E[*tok] sqrt H), x], 4-6 the layer's residual
+// blocks folded in front, see g4v_mtp.hip) and epilogue `epi` (0 store, 1 r16, 2 gate/up
+// activation with W2 the up matrix)
+struct B16Launch {
+  const uint16_t* W = nullptr;
+  const uint16_t* W2 = nullptr;
+  const int* rows = nullptr;
+  const int* top = nullptr;
+  const int* order = nullptr;
+  int N = 0, K = 0;
+  const float* x = nullptr;
+  const float* nw = nullptr;
+  const uint16_t* E = nullptr;
+  const int* tok = nullptr;
+  float* y = nullptr;
+  float* xout = nullptr;
+  const float* yin = nullptr;
+  const float* w1 = nullptr;
+  float* dxout = nullptr;
+  float scalar = 0.f;
+  int pro = 0, epi = 0;
+};
+void launch_b16(const B16Launch& L, hipStream_t st);
+void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, int pos, hipStream_t st);
+void launch_dr_rank(const float* score, int C, int* top, hipStream_t st);
+void launch_dr_best(const float* cs, const int* top, const int* order, int nc, int* tok, int* sec, float* gap,
+                    hipStream_t st);
+
 // raw split-KV attention with explicit geometry (C-ABI entry point)
 struct AttnGeom {
   int M, kmin, kmax, T;
   int pos[MAXM], lo[MAXM], skip_lo[MAXM], skip_hi[MAXM];
 };
+// nh query heads (a multiple of 2, at most 8) of q rows [M][ldq]; partials keep the 8-head layout
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
-                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st);
+                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);
 
 }  // namespace g4v
 

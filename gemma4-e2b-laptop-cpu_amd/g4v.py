@@ -52,6 +52,8 @@ SIGNATURES = {
     "g4v_sync": (_i, [_vp]),
     "g4v_set_graphs": (_i, [_vp, _i]),
     "g4v_prefill": (_i, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(_i), _vp]),
+    "g4v_drafter_synth": (_i, [_vp, C.c_uint64]),
+    "g4v_draft_mtp": (_i, [_vp, _i, _vp, _i, _i, _i, _i32p, _vp, _vp, _vp]),
     "g4v_history_set": (_i, [_vp, _i32p, _i]),
     "g4v_prompt_lookup": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_i)]),
     "g4v_history_read": (_i, [_vp, _vp, _i, C.POINTER(_i)]),
@@ -259,6 +261,22 @@ class Device:
         self._ok(self.L.g4v_prefill(self.h, toks, toks.size, pos0, pfb, nsplit, C.byref(g0), hid.ctypes.data),
                  "prefill")
         return (g0.value, hid) if hidden else g0.value
+
+    # ---- MTP drafter ----
+    def drafter_synth(self, seed):
+        self._ok(self.L.g4v_drafter_synth(self.h, seed), "drafter_synth")
+
+    def draft_mtp(self, tok, h, P, k, nsplit=6):
+        """k chained draft steps; h = None takes the last verify step's hidden state.
+        Returns (drafts, runners-up, gaps, last hidden state)"""
+        d = np.empty(k, np.int32)
+        sec = np.empty(k, np.int32)
+        gap = np.empty(k, np.float32)
+        hid = np.empty(1536, np.float32)
+        hp = None if h is None else _c(h, np.float32)
+        self._ok(self.L.g4v_draft_mtp(self.h, tok, None if hp is None else hp.ctypes.data, P, k, nsplit, d,
+                                      sec.ctypes.data, gap.ctypes.data, hid.ctypes.data), "draft_mtp")
+        return d, sec, gap, hid
 
     # ---- prompt-lookup drafter ----
     def history_set(self, toks):

@@ -125,6 +125,21 @@ int g4v_set_graphs(g4v_ctx* c, int on);
  * g4v_model_create + set calls) and pos0 + n <= ctxcap. */
 int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int nsplit, int* G0, float* hidden);
 
+/* ---- MTP drafter: draft_step (E:1534-1563) chained as run_req chains it (E:1631-1646), on the
+ * device.  g4v_drafter_synth builds a synthetic drafter for the current model (4 layers of
+ * hidden 256, 4 query heads of head_dim 256 attending the target's KV cache of layers 13 and
+ * 14, FFN 2048, V / 128 centroids, bf16 weights from `seed`); it needs V = 128 C with
+ * 32 <= C <= 4096, C % 16 == 0, and at least 15 target layers.
+ * g4v_draft_mtp runs k steps: step j drafts from token t_j (t_0 = tok) and hidden state h_j
+ * (h_0 = h, or the last g4v_verify_step's committed hidden state when h is null; h_j = the
+ * previous step's output) at query position P + 1 + j over the target keys [lo, P] with nsplit
+ * splits (the reference's pool size, 6 by default).  drafts[j] = t_{j+1}; sec[j] / gap[j]
+ * (optional) = runner-up token and score gap (g_sec, g_gap); hidden (optional, [1536]) = the
+ * last step's output state.  1 <= k <= 8. */
+int g4v_drafter_synth(g4v_ctx* c, uint64_t seed);
+int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, int nsplit, int* drafts, int* sec, float* gap,
+                  float* hidden);
+
 /* ---- prompt-lookup drafter (run_req, E:1624-1628) over a history kept on the device.
  * history_set: seq = toks[0..L), the prompt followed by the generated tokens (E:1625). */
 int g4v_history_set(g4v_ctx* c, const int* toks, int L);

@@ -1,0 +1,94 @@
+"""GPU parity of the MTP drafter (draft_step E:1534-1563, chained as E:1631-1646) against the
+oracle: every draft, runner-up, score gap and the last hidden state bit for bit, for chains
+that start from a given hidden state and from the last verify step's committed state."""
+import numpy as np
+import pytest
+
+from conftest import note
+from util import first_diff, same
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_chain(d, m, tok, h, P, k, T):
+    toks, secs, gaps = [], [], []
+    for j in range(k):
+        tok, h, s, g = d.step(m, tok, h, P + 1 + j, P, T)
+        toks.append(tok)
+        secs.append(s)
+        gaps.append(g)
+    return toks, secs, np.array(gaps, np.float32), h
+
+
+# (V, P, T, k): C = V / 128 centroids (32: every centroid is in the top 32; 128 and 2048: a
+# real selection), contexts inside and past the 512 window, the reference's 6 splits and 8
+CASES = [(4096, 300, 6, 3), (16384, 700, 6, 3), (16384, 40, 8, 2), (16384, 1500, 8, 4), (262144, 900, 6, 3)]
+
+
+@pytest.mark.parametrize("V,P,T,k", CASES)
+def test_draft_chain_matches_oracle(orc, g4v, V, P, T, k):
+    from oracle import Drafter, Model
+    NL, I, ctx, seed = 15, 512, 2048, 41
+    note(f"mtp chain V={V} P={P} T={T} k={k}")
+    rng = np.random.default_rng(P)
+    dev = g4v.Device(0)
+    m = Model(orc, seed, V, NL, I, ctx)
+    d = Drafter(orc, seed + 1, V)
+    try:
+        dev.model_synth(seed, V, NL, I, ctx)
+        dev.fake_ctx(P + 1, 5150)
+        m.fake_ctx(P + 1, 5150)
+        dev.drafter_synth(seed + 1)
+        h = (rng.standard_normal(1536).astype(np.float32).view(np.uint32) & 0xFFFF0000).view(np.float32)
+        tok = int(rng.integers(0, V))
+        got = dev.draft_mtp(tok, h, P, k, T)
+        want = oracle_chain(d, m, tok, h, P, k, T)
+        assert got[0].tolist() == want[0], (got[0], want[0])
+        assert got[1].tolist() == want[1], (got[1], want[1])
+        assert same(got[2], want[2]), (got[2], want[2])
+        assert same(got[3], want[3]), first_diff(got[3], want[3])
+    finally:
+        d.close()
+        m.close()
+        dev.close()
+
+
+def test_draft_after_verify(orc, g4v):
+    """h = None: the chain starts from the committed hidden state the verify step left on the device"""
+    from oracle import Drafter, Model
+    V, NL, I, ctx, seed, P = 16384, 15, 512, 1024, 43, 600
+    note("mtp chain after a verify step")
+    dev = g4v.Device(0)
+    m = Model(orc, seed, V, NL, I, ctx)
+    d = Drafter(orc, seed + 1, V)
+    try:
+        dev.model_synth(seed, V, NL, I, ctx)
+        dev.fake_ctx(P, 77)
+        m.fake_ctx(P, 77)
+        dev.drafter_synth(seed + 1)
+        block = np.array([5, 5, 5, 9], np.int32)
+        r = dev.verify(block, 3, 0, P, 8)
+        o, ho = m.verify(block, 3, 0, P, 8)
+        assert list(r.commit[:r.ncommit]) == list(o.commit[:o.ncommit])
+        Pn = P + r.ncommit - 1
+        conf = r.commit[r.ncommit - 1]
+        got = dev.draft_mtp(conf, None, Pn, 3, 6)
+        want = oracle_chain(d, m, conf, ho, Pn, 3, 6)
+        assert got[0].tolist() == want[0] and got[1].tolist() == want[1]
+        assert same(got[2], want[2]) and same(got[3], want[3])
+    finally:
+        d.close()
+        m.close()
+        dev.close()
+
+
+def test_draft_argument_errors(g4v):
+    dev = g4v.Device(0)
+    try:
+        with pytest.raises(RuntimeError):
+            dev.drafter_synth(1)  # no model
+        dev.model_synth(3, 4096, 2, 512, 256)
+        with pytest.raises(RuntimeError):
+            dev.drafter_synth(1)  # fewer than 15 target layers
+    finally:
+        dev.close()
