@@ -43,6 +43,7 @@ struct AttnPtrs {
   const float* kn;
   uint16_t* KCw;      // the layer's cache (same as KC / VC), written for the pass's rows
   uint16_t* VCw;
+  const AttnGeom* gdev;  // raw attention: the geometry in device memory (replaces the argument)
 };
 
 // E:326-345 sum of squares of a 256-vector, 16 lanes x 16 steps in double, combined in the
@@ -115,13 +116,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     pos_m = pos0 + m;
     lo_m = sliding ? max(0, rpm - 511) : 0;
   } else {
-    M = gin.M;
-    kmin = gin.kmin;
-    kmax = gin.kmax;
-    pos_m = gin.pos[m];
-    lo_m = gin.lo[m];
-    sl_m = gin.skip_lo[m];
-    sh_m = gin.skip_hi[m];
+    const AttnGeom& G = P.gdev ? *P.gdev : gin;
+    M = G.M;
+    kmin = G.kmin;
+    kmax = G.kmax;
+    pos_m = G.pos[m];
+    lo_m = G.lo[m];
+    sl_m = G.skip_lo[m];
+    sh_m = G.skip_hi[m];
   }
   if (m >= M) return;
   const int len = kmax - kmin + 1;
@@ -465,6 +467,18 @@ void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, in
   hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
                      (const StepDev*)nullptr, 0, g.T);
   hipLaunchKernelGGL(k_attn_merge, dim3(g.M, nh), dim3(HD), 0, st, P, g.M, g.T);
+}
+
+void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
+                          int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh) {
+  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+             nullptr, gdev};
+  AttnGeom g{};
+  g.M = M;
+  g.T = T;
+  hipLaunchKernelGGL(k_attn_split<false>, dim3(T, M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
+                     (const StepDev*)nullptr, 0, T);
+  hipLaunchKernelGGL(k_attn_merge, dim3(M, nh), dim3(HD), 0, st, P, M, T);
 }
 
 int attn_pmax() { return ATT_PMAX; }

@@ -110,6 +110,8 @@ struct g4v_ctx {
   int dr_C = 0;
   DBuf dr_pre, dr_post, dr_cent, dr_emb, dr_order, dr_norms, dr_q[4], dr_o[4], dr_g[4], dr_u[4], dr_d[4], dr_s;
   int last_hrow = -1;  // row of c->h holding the last verify step's committed hidden state
+  int* dr_in_host = nullptr;   // pinned chain inputs {tok, P, hrow, _, h[1536]}
+  int* dr_out_host = nullptr;  // pinned chain outputs {tok[8], sec[8], gap[8], hidden[1536]}
   // prompt-lookup history (prompt + committed tokens) and the lookup's result words
   DBuf hist, plout;
   int hist_len = 0, hist_cap = 0;
@@ -150,6 +152,8 @@ struct g4v_ctx {
     if (step_host) (void)hipHostFree(step_host);
     if (res_host) (void)hipHostFree(res_host);
     if (pl_host) (void)hipHostFree(pl_host);
+    if (dr_in_host) (void)hipHostFree(dr_in_host);
+    if (dr_out_host) (void)hipHostFree(dr_out_host);
     if (st) (void)hipStreamDestroy(st);
   }
 };
@@ -1469,9 +1473,11 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
 namespace {
 constexpr int DR_H = 256, DR_Q = 4, DR_F = 2048, DR_NC = 32 * 128;
 // scratch layout (floats / ints) of a drafter chain
+constexpr int DR_IN_WORDS = 4 + H, DR_OUT_WORDS = 24 + H;
 struct DrScratch {
   float *dx[2], *yo, *ydown, *dq, *dopt, *act, *dh, *bout[2], *hin, *dscore, *cscore, *gap;
-  int *top, *tok, *sec;
+  int *top, *tok, *sec, *din;
+  AttnGeom* geo;  // [2 * 8]
 };
 DrScratch dr_scratch(g4v_ctx* c) {
   float* f = c->dr_s.as<float>();
@@ -1494,10 +1500,12 @@ DrScratch dr_scratch(g4v_ctx* c) {
   d.top = ip;
   d.tok = d.top + 32;
   d.sec = d.tok + 16;
+  d.din = d.sec + 16;
+  d.geo = reinterpret_cast<AttnGeom*>(d.din + DR_IN_WORDS);
   return d;
 }
-constexpr size_t DR_SCRATCH_BYTES =
-    (size_t)(5 * DR_H + 2 * DR_Q * DR_H + DR_F + 3 * H + 4096 + DR_NC + 16) * 4 + (size_t)(32 + 16 + 16) * 4;
+constexpr size_t DR_SCRATCH_BYTES = (size_t)(5 * DR_H + 2 * DR_Q * DR_H + DR_F + 3 * H + 4096 + DR_NC + 16) * 4 +
+                                    (size_t)(32 + 16 + 16 + DR_IN_WORDS) * 4 + 16 * sizeof(AttnGeom);
 }  // namespace
 
 extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
@@ -1510,8 +1518,11 @@ extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
          "drafter_synth: the vocabulary must be 128 x C tokens with 32 <= C <= 4096 centroids, C % 16 == 0");
   ARGCHK(c->NL >= 15, "drafter_synth: the drafter reads the KV cache of target layers 13 and 14");
   HIPCHK(hipSetDevice(c->device));
+  drop_graphs(c);  // captured chains hold the drafter buffers
   hipStream_t st = c->st;
   const int V = c->V, C = V / 128;
+  if (!c->dr_in_host) HIPCHK(hipHostMalloc((void**)&c->dr_in_host, DR_IN_WORDS * 4, hipHostMallocDefault));
+  if (!c->dr_out_host) HIPCHK(hipHostMalloc((void**)&c->dr_out_host, DR_OUT_WORDS * 4, hipHostMallocDefault));
   auto gen = [&](DBuf& b, size_t n, uint64_t tag, float scale) -> int {
     ALLOC(b, n * 2);
     launch_gen_bf16_normal(b.as<uint16_t>(), n, rng_stream(seed, tag), scale, st);
@@ -1558,35 +1569,18 @@ extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
   return 0;
 }
 
-extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, int nsplit, int* drafts, int* sec,
-                             float* gap, float* hidden) {
-  if (!c) return G4V_E_ARG;
-  if (!c->dr_ready) {
-    c->err = "draft_mtp: no drafter (g4v_drafter_synth first)";
-    return G4V_E_STATE;
-  }
-  ARGCHK(drafts && k >= 1 && k <= 8 && P >= 0 && P + k < c->ctxcap, "draft_mtp: 1 <= k <= 8, P + k < ctxcap");
-  ARGCHK(tok >= 0 && tok < c->V, "draft_mtp: token outside the vocabulary");
-  ARGCHK(nsplit >= 1 && nsplit <= MAXT && (P + 1 + nsplit - 1) / nsplit <= attn_pmax(),
-         "draft_mtp: 1 <= nsplit <= 16 and no more positions per split than the split buffer holds");
-  if (!h && c->last_hrow < 0) {
-    c->err = "draft_mtp: no hidden state given and no verify step ran";
-    return G4V_E_STATE;
-  }
-  HIPCHK(hipSetDevice(c->device));
+// the kernels of a k-step chain with nsplit attention splits; inputs from the pinned input
+// block, outputs to the pinned output block (both copies are part of the sequence, so that a
+// captured chain replays them)
+static void enqueue_draft(g4v_ctx* c, int k, int nsplit) {
   hipStream_t st = c->st;
   const DrScratch d = dr_scratch(c);
   const float* nv = c->dr_norms.as<float>();
   auto nrm = [&](int l, int t) { return nv + (l * 5 + t) * DR_H; };
-  const float* hsrc = c->h.as<float>() + (size_t)std::max(c->last_hrow, 0) * H;
-  if (h) {
-    HIPCHK(hipMemcpyAsync(d.hin, h, H * 4, hipMemcpyHostToDevice, st));
-    hsrc = d.hin;
-  }
-  HIPCHK(hipMemcpyAsync(d.tok, &tok, 4, hipMemcpyHostToDevice, st));
+  (void)hipMemcpyAsync(d.din, c->dr_in_host, DR_IN_WORDS * 4, hipMemcpyHostToDevice, st);
+  launch_dr_setup(d.din, c->h.as<float>(), d.hin, d.tok, d.geo, k, nsplit, st);
   for (int j = 0; j < k; ++j) {  // E:1631-1633: step j at position P + 1 + j, keys up to P
-    const int pos = P + 1 + j;
-    const float* hj = j == 0 ? hsrc : d.bout[(j - 1) & 1];
+    const float* hj = j == 0 ? d.hin : d.bout[(j - 1) & 1];
     float* dxc = d.dx[0];  // the residual ping-pongs between d.dx[0] and d.dx[1]
     auto next_dx = [&]() { return dxc == d.dx[0] ? d.dx[1] : d.dx[0]; };
     {
@@ -1611,19 +1605,11 @@ extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, 
         }
         launch_b16(L, st);
       }
-      launch_dr_qnorm(d.dq, nrm(l, 4), cs, sn, pos, st);
-      AttnGeom ag{};
-      ag.M = 1;
-      ag.T = nsplit;
-      ag.pos[0] = P;
-      ag.lo[0] = sliding ? std::max(0, pos - 511) : 0;
-      ag.skip_lo[0] = 1;
-      ag.skip_hi[0] = 0;
-      ag.kmin = ag.lo[0];
-      ag.kmax = P;
-      launch_attn_geom(c->KC.as<uint16_t>() + (size_t)ol * c->kvcap * HD, c->VC.as<uint16_t>() + (size_t)ol * c->kvcap * HD,
-                       d.dq, DR_Q * DR_H, ag, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), d.dopt,
-                       DR_Q * DR_H, st, DR_Q);
+      launch_dr_qnorm(d.dq, nrm(l, 4), cs, sn, d.din + 1, j, st);
+      launch_attn_geom_dev(c->KC.as<uint16_t>() + (size_t)ol * c->kvcap * HD,
+                           c->VC.as<uint16_t>() + (size_t)ol * c->kvcap * HD, d.dq, DR_Q * DR_H, d.geo + 2 * j + ty, 1,
+                           nsplit, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), d.dopt, DR_Q * DR_H, st,
+                           DR_Q);
       {  // o (E:1545)
         B16Launch L;
         L.W = c->dr_o[l].as<uint16_t>(), L.N = DR_H, L.K = DR_Q * DR_H, L.x = d.dopt, L.y = d.yo;
@@ -1659,12 +1645,69 @@ extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, 
     }
     launch_dr_best(d.cscore, d.top, c->dr_order.as<int>(), DR_NC, d.tok + j + 1, d.sec + j, d.gap + j, st);
   }
-  HIPCHK(hipGetLastError());
-  HIPCHK(hipMemcpyAsync(drafts, d.tok + 1, (size_t)k * 4, hipMemcpyDeviceToHost, st));
-  if (sec) HIPCHK(hipMemcpyAsync(sec, d.sec, (size_t)k * 4, hipMemcpyDeviceToHost, st));
-  if (gap) HIPCHK(hipMemcpyAsync(gap, d.gap, (size_t)k * 4, hipMemcpyDeviceToHost, st));
-  if (hidden) HIPCHK(hipMemcpyAsync(hidden, d.bout[(k - 1) & 1], H * 4, hipMemcpyDeviceToHost, st));
-  HIPCHK(hipStreamSynchronize(st));
+  int* o = c->dr_out_host;
+  (void)hipMemcpyAsync(o, d.tok + 1, (size_t)k * 4, hipMemcpyDeviceToHost, st);
+  (void)hipMemcpyAsync(o + 8, d.sec, (size_t)k * 4, hipMemcpyDeviceToHost, st);
+  (void)hipMemcpyAsync(o + 16, d.gap, (size_t)k * 4, hipMemcpyDeviceToHost, st);
+  (void)hipMemcpyAsync(o + 24, d.bout[(k - 1) & 1], H * 4, hipMemcpyDeviceToHost, st);
+}
+
+extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, int nsplit, int* drafts, int* sec,
+                             float* gap, float* hidden) {
+  if (!c) return G4V_E_ARG;
+  if (!c->dr_ready) {
+    c->err = "draft_mtp: no drafter (g4v_drafter_synth first)";
+    return G4V_E_STATE;
+  }
+  ARGCHK(drafts && k >= 1 && k <= 8 && P >= 0 && P + k < c->ctxcap, "draft_mtp: 1 <= k <= 8, P + k < ctxcap");
+  ARGCHK(tok >= 0 && tok < c->V, "draft_mtp: token outside the vocabulary");
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT && (P + 1 + nsplit - 1) / nsplit <= attn_pmax(),
+         "draft_mtp: 1 <= nsplit <= 16 and no more positions per split than the split buffer holds");
+  if (!h && c->last_hrow < 0) {
+    c->err = "draft_mtp: no hidden state given and no verify step ran";
+    return G4V_E_STATE;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  int* in = c->dr_in_host;
+  in[0] = tok;
+  in[1] = P;
+  in[2] = h ? -1 : c->last_hrow;
+  if (h) std::memcpy(in + 4, h, H * 4);
+  // captured once per (k, splits) after one eager run, like the verify pass; keys below zero
+  const long long key = -1 - ((long long)k * 32 + nsplit);
+  g4v_ctx::Graph* gr = nullptr;
+  for (auto& g : c->graphs)
+    if (g.key == key) gr = &g;
+  const bool warm = std::find(c->warmed.begin(), c->warmed.end(), key) != c->warmed.end();
+  if (gr) {
+    HIPCHK(hipGraphLaunch(gr->exec, c->st));
+  } else if (!c->use_graph || !warm) {
+    enqueue_draft(c, k, nsplit);
+    HIPCHK(hipGetLastError());
+    if (!warm) c->warmed.push_back(key);
+  } else {
+    g4v_ctx::Graph g;
+    g.key = key;
+    hipGraph_t graph;
+    HIPCHK(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+    enqueue_draft(c, k, nsplit);
+    HIPCHK(hipStreamEndCapture(c->st, &graph));
+    const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) {
+      c->err = std::string("hipGraphInstantiate: ") + hipGetErrorString(ei);
+      return G4V_E_HIP;
+    }
+    c->graphs.push_back(std::move(g));
+    HIPCHK(hipGraphLaunch(c->graphs.back().exec, c->st));
+  }
+  HIPCHK(hipStreamSynchronize(c->st));
+  const int* o = c->dr_out_host;
+  for (int j = 0; j < k; ++j) drafts[j] = o[j];
+  if (sec)
+    for (int j = 0; j < k; ++j) sec[j] = o[8 + j];
+  if (gap) std::memcpy(gap, o + 16, (size_t)k * 4);
+  if (hidden) std::memcpy(hidden, o + 24, H * 4);
   return 0;
 }
 

@@ -108,6 +108,8 @@ void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStre
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
                        const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st);
 
+struct AttnGeom;
+
 // MTP drafter (g4v_mtp.hip): one bf16 product y[n] = W[row(n)] . input, input prologue `pro`
 // (0 x, 1 rms(x, nw), 2 r16(rms(x, nw)), 3 [r16(E[*tok] sqrt H), x], 4-6 the layer's residual
 // blocks folded in front, see g4v_mtp.hip) and epilogue `epi` (0 store, 1 r16, 2 gate/up
@@ -132,7 +134,12 @@ struct B16Launch {
   int pro = 0, epi = 0;
 };
 void launch_b16(const B16Launch& L, hipStream_t st);
-void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, int pos, hipStream_t st);
+// q heads normed and rotated at position *Pp + 1 + j
+void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, const int* Pp, int j, hipStream_t st);
+// a chain's inputs: in = {tok, P, hrow, _, h[1536]}; hin = h (hrow < 0) or hbase row hrow;
+// tok[0] = tok; geo[2 j + s] = the attention geometry of step j on sliding (s = 0) / global layers
+void launch_dr_setup(const int* in, const float* hbase, float* hin, int* tok, AttnGeom* geo, int k, int T,
+                     hipStream_t st);
 void launch_dr_rank(const float* score, int C, int* top, hipStream_t st);
 void launch_dr_best(const float* cs, const int* top, const int* order, int nc, int* tok, int* sec, float* gap,
                     hipStream_t st);
@@ -145,6 +152,9 @@ struct AttnGeom {
 // nh query heads (a multiple of 2, at most 8) of q rows [M][ldq]; partials keep the 8-head layout
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);
+// the same with the geometry read from device memory (M rows and T splits fixed by the launch)
+void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
+                          int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);
 
 }  // namespace g4v
 

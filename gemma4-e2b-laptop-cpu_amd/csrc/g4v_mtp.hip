@@ -98,8 +98,24 @@ __global__ __launch_bounds__(256) void k_b16(B16Args a) {
   const uint16_t* w2 = EPI == B16_GATEUP ? a.W2 + row * K + l : nullptr;
   float acc = 0.f, acc2 = 0.f;
   if (live) {
+    // chain l: elements l, 16 + l, ... in order; the weights of 32 steps are loaded ahead of
+    // their FMAs (K is a multiple of 512 here or the tail loop takes the rest)
+    int k = 0;
+    for (; k + 512 <= K; k += 512) {
+      uint16_t wb[32], wb2[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        wb[u] = w[k + 16 * u];
+        if (EPI == B16_GATEUP) wb2[u] = w2[k + 16 * u];
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        acc = fmaf(bf2f(wb[u]), xs[k + 16 * u + l], acc);
+        if (EPI == B16_GATEUP) acc2 = fmaf(bf2f(wb2[u]), xs[k + 16 * u + l], acc2);
+      }
+    }
 #pragma unroll 8
-    for (int k = 0; k < K; k += 16) {  // chain l: elements l, 16 + l, ... in order
+    for (; k < K; k += 16) {
       acc = fmaf(bf2f(w[k]), xs[k + l], acc);
       if (EPI == B16_GATEUP) acc2 = fmaf(bf2f(w2[k]), xs[k + l], acc2);
     }
@@ -122,8 +138,10 @@ __global__ __launch_bounds__(256) void k_b16(B16Args a) {
 
 // per head (4): x = r16((x * r) * qn), then NeoX RoPE at the step's position (E:1542)
 __global__ __launch_bounds__(HD) void k_dr_qnorm(float* __restrict__ q, const float* __restrict__ qn,
-                                                 const float* __restrict__ cs, const float* __restrict__ sn, int pos) {
+                                                 const float* __restrict__ cs, const float* __restrict__ sn,
+                                                 const int* __restrict__ Pp, int j) {
   constexpr int NV = 4;
+  const int pos = *Pp + 1 + j;
   __shared__ float xv[NV][HD];
   __shared__ double part[NV][16];
   __shared__ float rinv[NV];
@@ -162,6 +180,31 @@ __global__ __launch_bounds__(HD) void k_dr_qnorm(float* __restrict__ q, const fl
 #pragma unroll
   for (int h = 0; h < NV; ++h)
     q[h * HD + e] = e < HD / 2 ? fmaf(xv[h][e], c, -(xv[h][e + HD / 2] * sv)) : fmaf(xv[h][e], c, xv[h][e - HD / 2] * sv);
+}
+
+// a chain's inputs (E:1631-1633): the hidden state, the first token and, per step j, the
+// attention geometry (M = 1, keys [lo, P], lo = pos - 511 clamped at 0 on sliding layers,
+// pos = P + 1 + j, E:1543)
+__global__ __launch_bounds__(256) void k_dr_setup(const int* __restrict__ in, const float* __restrict__ hbase,
+                                                  float* __restrict__ hin, int* __restrict__ tok,
+                                                  AttnGeom* __restrict__ geo, int k, int T) {
+  const int t0 = in[0], P = in[1], hrow = in[2];
+  const float* src = hrow >= 0 ? hbase + (size_t)hrow * H : reinterpret_cast<const float*>(in + 4);
+  for (int i = threadIdx.x; i < H; i += 256) hin[i] = src[i];
+  if (threadIdx.x == 0) tok[0] = t0;
+  if (threadIdx.x < 2 * k) {
+    const int j = threadIdx.x >> 1, sl = (threadIdx.x & 1) == 0;
+    AttnGeom g{};
+    g.M = 1;
+    g.T = T;
+    g.pos[0] = P;
+    g.lo[0] = sl ? max(0, P + 1 + j - 511) : 0;
+    g.skip_lo[0] = 1;
+    g.skip_hi[0] = 0;
+    g.kmin = g.lo[0];
+    g.kmax = P;
+    geo[threadIdx.x] = g;
+  }
 }
 
 // E:1554-1555 top-32 centroids (descending, equal scores in index order): centroid c's place is
@@ -270,8 +313,12 @@ void launch_b16(const B16Launch& L, hipStream_t st) {
 #undef G4V_B16
 }
 
-void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, int pos, hipStream_t st) {
-  hipLaunchKernelGGL(k_dr_qnorm, dim3(1), dim3(HD), 0, st, q, qn, cs, sn, pos);
+void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, const int* Pp, int j, hipStream_t st) {
+  hipLaunchKernelGGL(k_dr_qnorm, dim3(1), dim3(HD), 0, st, q, qn, cs, sn, Pp, j);
+}
+void launch_dr_setup(const int* in, const float* hbase, float* hin, int* tok, AttnGeom* geo, int k, int T,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(k_dr_setup, dim3(1), dim3(256), 0, st, in, hbase, hin, tok, geo, k, T);
 }
 void launch_dr_rank(const float* score, int C, int* top, hipStream_t st) {
   hipLaunchKernelGGL(k_dr_rank, dim3((C + 63) / 64), dim3(256), 0, st, score, C, top);
