@@ -14,7 +14,8 @@ the timed region) and the reference's own AVX2 kernels timed on this host as a b
 --workload long_prompt runs the long-prompt case instead: a 6,841-token prompt (a seeded
 64-token motif repeated, 5% uniform noise tokens) prefilled through the same stack (W4A8
 linear layers on the matrix cores), then 256 speculative decode rounds with prompt-lookup
-drafts (n-gram 3, up to 3 drafts) verified as a chain.  A step is one prefill + 256 rounds.
+drafts (n-gram 3, up to 3 drafts), or 3 MTP drafts from the synthetic drafter when the lookup
+finds none, verified as a chain.  A step is one prefill + 256 rounds.
 """
 import argparse
 import importlib.util
@@ -108,7 +109,7 @@ def cpu_baseline(seconds_cap=30.0):
                       f"{dt * 1e3 / steps:.1f} ms/step"}
 
 
-LP_N, LP_ROUNDS, LP_NGRAM, LP_NGLEN, LP_CTX = 6841, 256, 3, 3, 8192
+LP_N, LP_ROUNDS, LP_NGRAM, LP_NGLEN, LP_CTX, LP_K, LP_DSPLIT = 6841, 256, 3, 3, 8192, 3, 6
 
 
 def long_prompt_tokens():
@@ -121,15 +122,20 @@ def long_prompt_tokens():
 
 
 def long_prompt_run(dev, prompt):
-    """prefill, then LP_ROUNDS rounds of run_req's loop (E:1617-1661) with prompt-lookup drafts"""
+    """prefill, then LP_ROUNDS rounds of run_req's loop (E:1617-1661): prompt-lookup drafts, and
+    the MTP drafter's chain of LP_K when the lookup finds none (E:1624-1646 with the sibling
+    policy off)"""
     dev.sync()
     t0 = time.perf_counter()
-    g0 = dev.prefill(prompt)
+    g0, h0 = dev.prefill(prompt, hidden=True)
     t1 = time.perf_counter()
     dev.history_set(np.concatenate([prompt, [g0]]))
-    gen, P, app, acc, nd = [g0], len(prompt) - 1, [], 0, 0
-    for _ in range(LP_ROUNDS):
+    gen, P, app, acc, nd, nmtp = [g0], len(prompt) - 1, [], 0, 0, 0
+    for rnd in range(LP_ROUNDS):
         d = dev.prompt_lookup(LP_NGRAM, LP_NGLEN, app)
+        if d.size == 0:  # the chain starts from the prefill's (then the last verify step's) hidden state
+            d = dev.draft_mtp(gen[-1], h0 if rnd == 0 else None, P, LP_K, LP_DSPLIT)[0]
+            nmtp += 1
         r = dev.verify(np.array([gen[-1]] + d.tolist(), np.int32), len(d), 0, P + 1, NSPLIT)
         app = list(r.commit[:r.ncommit])
         gen += app
@@ -138,7 +144,8 @@ def long_prompt_run(dev, prompt):
         nd += len(d)
     dev.sync()
     t2 = time.perf_counter()
-    return {"prefill_s": t1 - t0, "decode_s": t2 - t1, "tokens": len(gen) - 1, "accepted": acc, "drafted": nd}
+    return {"prefill_s": t1 - t0, "decode_s": t2 - t1, "tokens": len(gen) - 1, "accepted": acc, "drafted": nd,
+            "mtp_rounds": nmtp}
 
 
 def cpu_prefill_baseline(prompt, nrows=64):
@@ -164,6 +171,7 @@ def main_long_prompt(args, g4v):
     dev = g4v.Device(0)
     info = dev.info()
     dev.model_synth(SEED, V, NL, I, LP_CTX)
+    dev.drafter_synth(SEED + 1)
     prompt = long_prompt_tokens()
     for _ in range(args.warmup):
         long_prompt_run(dev, prompt)
@@ -186,10 +194,12 @@ def main_long_prompt(args, g4v):
         "dtype": "fp32 (prefill linear layers: int8 x int4 on the matrix cores)",
         "data": "synthetic (seeded random-init weights, seeded motif prompt)",
         "config": {"workload": f"long prompt: {LP_N}-token motif prompt prefilled (blocks of 32), then {LP_ROUNDS} "
-                               f"speculative rounds with prompt-lookup drafts (n-gram {LP_NGRAM}, <= {LP_NGLEN})",
+                               f"speculative rounds with prompt-lookup drafts (n-gram {LP_NGRAM}, <= {LP_NGLEN}), "
+                               f"else {LP_K} MTP drafts",
                    "prefill_ms": round(pf * 1e3, 2), "prefill_tok_s": round(LP_N / pf, 1),
                    "decode_ms": round(dc * 1e3, 2), "tokens_per_step": round(last["tokens"] / LP_ROUNDS, 3),
-                   "drafts_accepted": f"{last['accepted']}/{last['drafted']}", "device": info["name"]},
+                   "drafts_accepted": f"{last['accepted']}/{last['drafted']}",
+                   "mtp_rounds": last["mtp_rounds"], "device": info["name"]},
     }
     if not args.no_cpu:
         try:

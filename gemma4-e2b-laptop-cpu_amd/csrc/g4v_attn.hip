@@ -19,7 +19,7 @@ __constant__ uint64_t c_expf_tab[32] = G4V_EXPF_TABLE;
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_TILE = 32;  // positions per tile = one block of the value cache
 constexpr int ATT_HB = 2;     // heads per block (224 blocks for a 7-row pass: every CU busy)
-constexpr int ATT_PMAX = 1040;  // positions per split held in LDS
+constexpr int ATT_PMAX = 2080;  // positions per split held in LDS (6 splits cover 12,480 keys)
 constexpr int ATT_SW = ATT_PMAX + 2 * ATT_TILE;  // weight row: a split widened to whole tiles
 constexpr int ATT_RING = 4;  // tiles in flight: the split's key tiles, then its value tiles
 

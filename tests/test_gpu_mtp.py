@@ -92,3 +92,56 @@ def test_draft_argument_errors(g4v):
             dev.drafter_synth(1)  # fewer than 15 target layers
     finally:
         dev.close()
+
+
+def test_run_req_loop_matches_oracle(orc, g4v):
+    """run_req end to end (E:1594-1661, sibling policy off): prefill, then rounds of prompt-lookup
+    drafts or, when the lookup finds none, a 3-step MTP chain, each verified as a chain"""
+    from oracle import Drafter, Model
+    V, NL, I, ctx, seed = 16384, 15, 512, 1024, 47
+    rng = np.random.default_rng(8)
+    motif = rng.integers(0, V, 24)
+    prompt = np.resize(motif, 200).astype(np.int32)
+    noise = rng.random(200) < 0.2
+    prompt[noise] = rng.integers(0, V, int(noise.sum()))
+    note("run_req loop: prefill 200 + 24 rounds (lookup / MTP)")
+    dev = g4v.Device(0)
+    m = Model(orc, seed, V, NL, I, ctx)
+    d = Drafter(orc, seed + 1, V)
+    try:
+        dev.model_synth(seed, V, NL, I, ctx)
+        dev.drafter_synth(seed + 1)
+        g0, hd = dev.prefill(prompt, hidden=True)
+        ho = m.prefill(prompt)
+        assert same(hd, ho)
+        G, _, _ = dev.head_argmax(ho[None, :])
+        assert g0 == G[0]
+        gen, P, app, h_or, kinds = [g0], len(prompt) - 1, [], ho, set()
+        dev.history_set(np.concatenate([prompt, [g0]]))
+        for rnd in range(24):
+            drafts = dev.prompt_lookup(3, 3, app)
+            seq = np.concatenate([prompt, gen]).astype(np.int32)
+            assert drafts.tolist() == orc.prompt_lookup(seq, 3, 3).tolist(), rnd
+            if drafts.size == 0:
+                drafts = dev.draft_mtp(gen[-1], hd if rnd == 0 else None, P, 3, 6)[0]
+                want = oracle_chain(d, m, gen[-1], h_or, P, 3, 6)[0]
+                assert drafts.tolist() == want, rnd
+                kinds.add("mtp")
+            else:
+                kinds.add("lookup")
+            block = np.array([gen[-1]] + drafts.tolist(), np.int32)
+            r = dev.verify(block, len(drafts), 0, P + 1, 8)
+            o, h_or = m.verify(block, len(drafts), 0, P + 1, 8)
+            assert r.nacc == o.nacc and list(r.commit[:r.ncommit]) == list(o.commit[:o.ncommit]), rnd
+            app = list(r.commit[:r.ncommit])
+            gen += app
+            P += r.ncommit
+        assert kinds == {"mtp", "lookup"}, kinds  # both drafters took part
+        for what in ("KC", "VC"):
+            a = dev.read(what, np.uint16).reshape(NL, -1, 256)[:, :P + 1]
+            b = m.get(what, np.uint16, NL * ctx * 256).reshape(NL, ctx, 256)[:, :P + 1]
+            assert same(a, b), what
+    finally:
+        d.close()
+        m.close()
+        dev.close()
