@@ -173,11 +173,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
   const int ntiles = a.tiles[3];
   float lrun = -INFINITY;  // EPI_SCREEN: running max of L for activation row j of this lane
 
-  // which matrix / output row this lane serves in tile t, and its weight / scale streams
-  // (rows past N read row 0 and are never stored)
+  // which matrix / output row this lane serves in tile t, and its weight stream (rows past N
+  // read row 0 and are never stored); the scales go through LDS (scales_issue / scales_commit)
   int mi = 0, n = 0;
   bool valid = false;
-  const uint4 *wp = nullptr, *sp = nullptr;
+  const uint4* wp = nullptr;
   auto tile_ptrs = [&](int t) {
     if (EPI == EPI_GATEUP) {
       // row slots alternate gate / up for the same n: slot 2p -> gate, 2p+1 -> up
@@ -190,7 +190,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
     const W4Dev W = mi == 0 ? a.mat[0] : (mi == 1 ? a.mat[1] : a.mat[2]);
     valid = t < ntiles && n < W.N;
     wp = W.wr + ((size_t)(valid ? n : 0) * GC) * 8 + j;
-    sp = reinterpret_cast<const uint4*>(W.s + (size_t)(valid ? n : 0) * G);
   };
   // the bf16 scales of the tile's RPB rows, staged in LDS once per tile (row slot = the
   // lane's wave * RPW + rslot; rows past N get zeros): entries u = slot * GC + c, at most
