@@ -112,6 +112,17 @@ struct g4v_ctx {
   int last_hrow = -1;  // row of c->h holding the last verify step's committed hidden state
   int* dr_in_host = nullptr;   // pinned chain inputs {tok, P, hrow, _, h[1536]}
   int* dr_out_host = nullptr;  // pinned chain outputs {tok[8], sec[8], gap[8], hidden[1536]}
+  // prefix cache: the active KV (KC / VC) with its keys, plus stored slots (each a full KV copy)
+  struct Slot {
+    DBuf KC, VC;
+    std::vector<int> keys;
+    int kv_len = 0;
+    uint64_t stamp = 0;
+  };
+  std::vector<std::unique_ptr<Slot>> slots;
+  std::vector<int> act_keys;
+  int act_kv_len = 0, min_reuse = 32;
+  uint64_t act_stamp = 0, clock_tick = 0;
   // prompt-lookup history (prompt + committed tokens) and the lookup's result words
   DBuf hist, plout;
   int hist_len = 0, hist_cap = 0;
@@ -1708,6 +1719,105 @@ extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, 
     for (int j = 0; j < k; ++j) sec[j] = o[8 + j];
   if (gap) std::memcpy(gap, o + 16, (size_t)k * 4);
   if (hidden) std::memcpy(hidden, o + 24, H * 4);
+  return 0;
+}
+
+
+// ---------------------------------------------------------------------------------------
+// prefix cache (run_req, E:1568-1593)
+// ---------------------------------------------------------------------------------------
+extern "C" int g4v_slots_init(g4v_ctx* c, int nslot, int min_reuse) {
+  if (!c) return G4V_E_ARG;
+  if (!c->model_ready) {
+    c->err = "slots_init: no model";
+    return G4V_E_STATE;
+  }
+  ARGCHK(nslot >= 1 && nslot <= 64, "slots_init: 1 <= nslot <= 64");
+  HIPCHK(hipSetDevice(c->device));
+  c->slots.clear();
+  const size_t bytes = c->KC.n;
+  for (int i = 0; i + 1 < nslot; ++i) {
+    auto sl = std::make_unique<g4v_ctx::Slot>();
+    ALLOC(sl->KC, bytes);
+    ALLOC(sl->VC, bytes);
+    c->slots.push_back(std::move(sl));
+  }
+  c->act_keys.clear();
+  c->act_kv_len = 0;
+  c->min_reuse = min_reuse;
+  c->act_stamp = c->clock_tick = 0;
+  return 0;
+}
+
+// the active KV and stored slot s exchange places (E:1576 swap_with): contents are swapped on the
+// device, so captured passes keep pointing at the active cache
+static int slot_swap(g4v_ctx* c, g4v_ctx::Slot& sl) {
+  launch_swap16(c->KC.p, sl.KC.p, c->KC.n, c->st);
+  launch_swap16(c->VC.p, sl.VC.p, c->VC.n, c->st);
+  HIPCHK(hipGetLastError());
+  std::swap(c->act_keys, sl.keys);
+  std::swap(c->act_kv_len, sl.kv_len);
+  std::swap(c->act_stamp, sl.stamp);
+  return 0;
+}
+
+extern "C" int g4v_slot_begin(g4v_ctx* c, const int* toks, int n, int* start, int* slot_used) {
+  if (!c) return G4V_E_ARG;
+  if (!c->model_ready) {
+    c->err = "slot_begin: no model";
+    return G4V_E_STATE;
+  }
+  ARGCHK(toks && n >= 1 && start, "slot_begin: need n >= 1 tokens");
+  HIPCHK(hipSetDevice(c->device));
+  auto lcp_of = [&](const std::vector<int>& k, int klen) {  // E:1585
+    int m = 0;
+    while (m < klen && m < n && k[m] == toks[m]) ++m;
+    return m;
+  };
+  int common = lcp_of(c->act_keys, c->act_kv_len), used = 0;
+  ++c->clock_tick;
+  if (!c->slots.empty()) {  // E:1587-1592
+    int best = -1, bc = common;
+    for (int i = 0; i < (int)c->slots.size(); ++i) {
+      const int m = lcp_of(c->slots[i]->keys, c->slots[i]->kv_len);
+      if (m > bc) {
+        bc = m;
+        best = i;
+      }
+    }
+    if (best >= 0) {  // a stored conversation shares more: switch to it, park the active one there
+      c->act_stamp = c->clock_tick;
+      int r = slot_swap(c, *c->slots[best]);
+      if (r) return r;
+      used = best + 1;
+      common = bc;
+    } else if (bc < c->min_reuse) {  // nothing worth reusing: the LRU slot takes the active one
+      int v = 0;
+      for (int i = 1; i < (int)c->slots.size(); ++i)
+        if (c->slots[i]->stamp < c->slots[v]->stamp) v = i;
+      c->act_stamp = c->clock_tick;
+      int r = slot_swap(c, *c->slots[v]);
+      if (r) return r;
+      c->act_kv_len = 0;
+      c->act_keys.clear();
+      common = 0;
+      used = v + 1;
+    }
+    c->act_stamp = c->clock_tick;
+  }
+  *start = std::min(common, n - 1);  // E:1594: the last prompt token always runs again
+  if (slot_used) *slot_used = used;
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+extern "C" int g4v_slot_end(g4v_ctx* c, const int* toks, int n, const int* gen, int ngen, int P) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(toks && n >= 1 && ngen >= 0 && (ngen == 0 || gen) && P >= n - 1, "slot_end: bad request record");
+  // E:1671: the KV holds the prompt, then the generated tokens up to position P
+  c->act_keys.assign(toks, toks + n);
+  for (int i = 0; i <= P - n && i < ngen; ++i) c->act_keys.push_back(gen[i]);
+  c->act_kv_len = std::min<int>(P + 1, (int)c->act_keys.size());
   return 0;
 }
 

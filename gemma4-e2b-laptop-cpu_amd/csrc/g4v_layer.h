@@ -83,6 +83,9 @@ void launch_branch(const StepDev* sp, const int* best1, const float* h, const fl
 void launch_accept(const StepDev* sp, const int* best1, const int* best2, const int* cnt1, const int* cnt2,
                    VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int kvcap, hipStream_t st);
 
+// exchange the contents of two device buffers of `bytes` (a multiple of 16)
+void launch_swap16(void* a, void* b, size_t bytes, hipStream_t st);
+
 // synthetic weights (same formulas as the oracle's generator)
 void launch_gen_bf16_normal(uint16_t* out, size_t n, uint64_t seed, float scale, hipStream_t st);
 void launch_gen_w4(uint8_t* w, uint16_t* s, size_t nbytes, size_t nscales, uint64_t sw, uint64_t ss,

@@ -4,6 +4,8 @@
 //
 // References (E = engine/gemma4_engine.cpp): embedding E:1262-1267; residual/norm blocks
 // E:1358-1361, E:1375-1404; lazy head + acceptance E:1453-1488, E:1647-1661.
+#include <algorithm>
+
 #include "g4v_layer.h"
 
 namespace g4v {
@@ -277,6 +279,20 @@ void launch_accept(const StepDev* sp, const int* best1, const int* best2, const 
   hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, st, sp, best1, best2, cnt1, cnt2, res);
   hipLaunchKernelGGL(k_kv_compact, dim3(NL), dim3(HD), 0, st, sp, res, KC, VC, kvcap);
 }
+// exchange two KV slabs (uint4 words): the prefix cache's slot switch
+__global__ void k_swap16(uint4* __restrict__ a, uint4* __restrict__ b, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const uint4 x = a[i];
+    a[i] = b[i];
+    b[i] = x;
+  }
+}
+void launch_swap16(void* a, void* b, size_t bytes, hipStream_t st) {
+  const size_t n = bytes / 16;
+  const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
+  if (n) hipLaunchKernelGGL(k_swap16, dim3(grid), dim3(256), 0, st, (uint4*)a, (uint4*)b, n);
+}
+
 void launch_gen_bf16_normal(uint16_t* out, size_t n, uint64_t seed, float scale, hipStream_t st) {
   size_t g = (n + 255) / 256;
   hipLaunchKernelGGL(k_gen_bf16_normal, dim3(g > 65536 ? 65536 : (unsigned)g), dim3(256), 0, st, out, n, seed, scale);

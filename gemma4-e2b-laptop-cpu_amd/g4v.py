@@ -54,6 +54,9 @@ SIGNATURES = {
     "g4v_prefill": (_i, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(_i), _vp]),
     "g4v_drafter_synth": (_i, [_vp, C.c_uint64]),
     "g4v_draft_mtp": (_i, [_vp, _i, _vp, _i, _i, _i, _i32p, _vp, _vp, _vp]),
+    "g4v_slots_init": (_i, [_vp, _i, _i]),
+    "g4v_slot_begin": (_i, [_vp, _i32p, _i, C.POINTER(_i), C.POINTER(_i)]),
+    "g4v_slot_end": (_i, [_vp, _i32p, _i, _vp, _i, _i]),
     "g4v_history_set": (_i, [_vp, _i32p, _i]),
     "g4v_prompt_lookup": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_i)]),
     "g4v_history_read": (_i, [_vp, _vp, _i, C.POINTER(_i)]),
@@ -277,6 +280,23 @@ class Device:
         self._ok(self.L.g4v_draft_mtp(self.h, tok, None if hp is None else hp.ctypes.data, P, k, nsplit, d,
                                       sec.ctypes.data, gap.ctypes.data, hid.ctypes.data), "draft_mtp")
         return d, sec, gap, hid
+
+    # ---- prefix cache ----
+    def slots_init(self, nslot, min_reuse=32):
+        self._ok(self.L.g4v_slots_init(self.h, nslot, min_reuse), "slots_init")
+
+    def slot_begin(self, toks):
+        """(start, slot used) for a request with prompt toks"""
+        toks = _c(toks, np.int32)
+        st, used = _i(), _i()
+        self._ok(self.L.g4v_slot_begin(self.h, toks, toks.size, C.byref(st), C.byref(used)), "slot_begin")
+        return st.value, used.value
+
+    def slot_end(self, toks, gen, P):
+        toks = _c(toks, np.int32)
+        gen = _c(np.asarray(gen, np.int32).reshape(-1), np.int32)
+        self._ok(self.L.g4v_slot_end(self.h, toks, toks.size, gen.ctypes.data if gen.size else None, gen.size, P),
+                 "slot_end")
 
     # ---- prompt-lookup drafter ----
     def history_set(self, toks):

@@ -140,6 +140,18 @@ int g4v_drafter_synth(g4v_ctx* c, uint64_t seed);
 int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, int nsplit, int* drafts, int* sec, float* gap,
                   float* hidden);
 
+/* ---- prefix cache (run_req, E:1568-1593, E:1671): the active KV cache plus nslot - 1 stored
+ * conversations (ENGINE_SLOTS; each a full cache copy on the device), reuse threshold min_reuse
+ * (ENGINE_SLOT_MIN_REUSE, 32).  Per request: g4v_slot_begin picks the conversation that shares
+ * the longest prefix with toks (switching slots, or parking the active one in the least recently
+ * used slot when nothing reaches min_reuse) and returns start = the positions whose KV is reused
+ * (at most n - 1) and the slot used (0 = the active one); the caller prefills toks[start..n) at
+ * position start and decodes; g4v_slot_end records what the cache now holds: the prompt and
+ * gen[i] for i <= P - n, valid up to position P. */
+int g4v_slots_init(g4v_ctx* c, int nslot, int min_reuse);
+int g4v_slot_begin(g4v_ctx* c, const int* toks, int n, int* start, int* slot_used);
+int g4v_slot_end(g4v_ctx* c, const int* toks, int n, const int* gen, int ngen, int P);
+
 /* ---- prompt-lookup drafter (run_req, E:1624-1628) over a history kept on the device.
  * history_set: seq = toks[0..L), the prompt followed by the generated tokens (E:1625). */
 int g4v_history_set(g4v_ctx* c, const int* toks, int L);
