@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void k_w4a8_gemm(const uint4* __restrict__ tw,
 }
 
 // LDS-staged variant for long M (prefill): a block of 4 waves covers 64 rows (MT = 4 m-tiles)
-// and 4 x NT 16-column tiles.  The block's activation fragments, corrections and row scales of
+// and 4 x NT 16-column tiles (NT = 2: 145 VGPRs, 3 waves per SIMD).  The block's activation fragments, corrections and row scales of
 // a chunk of 4 groups are loaded once per block (not once per wave) a chunk ahead into
 // registers, then written to the other half of a double-buffered LDS stage; one barrier per
 // chunk.  Same arithmetic, in the same order, as k_w4a8_gemm.
@@ -340,9 +340,9 @@ int w4a8_mpad(int M) {
 void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, const float* sxt, const float* corr,
                       float* y, int M, int N, int K, int ldy, hipStream_t st) {
   const int MT = w4a8_mt(M), Mpad = w4a8_mpad(M);
-  if (MT == 4 && (N / 16) % 4 == 0 && K % 128 == 0) {  // long M: 4 x 4 tiles per wave, staged rows
-    const dim3 grid((N / 16 / 4 + 3) / 4, Mpad / 64);
-    hipLaunchKernelGGL(k_w4a8_gemm_lds<4>, grid, dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
+  if (MT == 4 && (N / 16) % 2 == 0 && K % 128 == 0) {  // long M: 4 x 2 tiles per wave, staged rows
+    const dim3 grid((N / 16 / 2 + 3) / 4, Mpad / 64);
+    hipLaunchKernelGGL(k_w4a8_gemm_lds<2>, grid, dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
     return;
   }
   const dim3 grid((N / 16 + 3) / 4, Mpad / (16 * MT));
