@@ -96,6 +96,7 @@ struct g4v_ctx {
   // x / x2: the residual stream, alternating between the two halves of a layer (a GEMV whose
   // norm prologue updates it reads one and writes the other)
   DBuf x, x2, xa, xgs, q, k, v, o, act, h, hn, h2, hn2, po, pm, pl, stepd, resd;
+  DBuf vatt, vsc;  // a pass's attn_tile / run_mh output (staged) and its score scratch
   StepDev* step_host = nullptr;
   VerifyResultDev* res_host = nullptr;
   // attention standalone
@@ -822,6 +823,8 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   ALLOC(c->pm, (size_t)MAXT * MAXM * NQ * 4);
   ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
   ALLOC(c->stepd, sizeof(StepDev));
+  ALLOC(c->vatt, (size_t)MAXM * NQ * HD * 4);
+  ALLOC(c->vsc, (size_t)8 * MAXM * ctxcap * 4);
   ALLOC(c->resd, sizeof(VerifyResultDev));
   HIPCHK(hipStreamSynchronize(st));  // rt goes out of scope
   return 0;
@@ -1114,7 +1117,16 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
 // algorithmic bytes of an int4 G32 matrix read once: N*K/2 weight bytes + N*K/16 scale bytes
 static double w4_bytes(const Mat& m) { return (double)m.N * m.K / 2 + (double)m.N * m.K / 16; }
 
-static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
+// the attention path of a pass (E:1305 / 1328 / 1337 with SPLITKV, TILED, ATT_PAR = 192):
+// 0 split-KV when M <= 4 and pos0 + M > 192, else 1 attn_tile when M >= 4 and pos0 + M > 64,
+// else 2 run_mh; passes with branch rows (the two-branch tree generalises the engine's single
+// sibling row) take the split-KV path for every size
+static int pass_path(int M, int pos0, int nb) {
+  if (nb > 0 || (M <= 4 && pos0 + M > 192)) return 0;
+  return (M >= 4 && pos0 + M > 64) ? 1 : 2;
+}
+
+static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
   hipStream_t st = c->st;
   const int NL = c->NL, I = c->I;
   const StepDev* sp = c->stepd.as<StepDev>();
@@ -1160,18 +1172,31 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T) {
     int kmin = sh.pos0 + M - 1;  // E:1325-1326 keys read by the pass: [kmin, pos0 + M - 1]
     for (int r = 0; r < M; ++r) kmin = std::min(kmin, A.sliding ? std::max(0, sh.rope[r] - 511) : 0);
     pmark(c, PT_ATTN, 1, 0);
-    launch_attn(KCl, VCl, c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln, rstep, sp, A.sliding, T,
-                c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), M, st);
+    if (path == 0) {
+      launch_attn(KCl, VCl, c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln, rstep, sp, A.sliding, T,
+                  c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), M, st);
+    } else {  // a chain pass below ATT_PAR or of more than 4 rows: the prefill kernels (chain rows:
+              // RoPE position = cache slot = pos0 + m), output staged for the o projection
+      const float* cs = c->rope.as<float>() + (size_t)(2 * (A.sliding ? 0 : 1)) * c->ctxcap * (HD / 2);
+      launch_pf_qkv(c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln.qn, ln.kn, cs,
+                    cs + (size_t)c->ctxcap * (HD / 2), KCl, VCl, sh.pos0, M, st);
+      launch_pf_attn(c->q.as<float>(), KCl, VCl, c->vsc.as<float>(), c->vatt.as<float>(), PfGeom{M, sh.pos0, M}, 0,
+                     M, A.sliding, st, true);
+    }
     pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
     pmark(c, PT_GEMV_O, 1, 0);
     GemvTArgs ao{};  // E:1356 on the merged attention (E:1019-1059, formed in the prologue)
     ao.mat[0] = A.m[3].tile();
     ao.y[0] = c->o.as<float>();
     ao.ldy[0] = H;
-    ao.mrg_po = c->po.as<float>();
-    ao.mrg_pm = c->pm.as<float>();
-    ao.mrg_pl = c->pl.as<float>();
-    ao.mrg_T = T;
+    if (path == 0) {
+      ao.mrg_po = c->po.as<float>();
+      ao.mrg_pm = c->pm.as<float>();
+      ao.mrg_pl = c->pl.as<float>();
+      ao.mrg_T = T;
+    } else {
+      ao.xs = c->vatt.as<float4>();  // group sums formed in LDS from the staged copy
+    }
     ao.K = NQ * HD;
     ao.M = M;
     launch_gemv_t(ao, st, c->gcfg[1][0], c->gcfg[1][1]);
@@ -1261,16 +1286,18 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
       s.skip_hi[r] = pos0 + na;
     }
   }
+  const int path = pass_path(M, pos0, nb);
   const long long key = ((((long long)M * 8 + na) * 8 + nb) * 32 + nsplit) * 65536 + c->prof_mask;
   g4v_ctx::Graph* gr = nullptr;
   for (auto& g : c->graphs)
-    if (g.key == key) gr = &g;
+    if (g.key == key && path == 0) gr = &g;  // only split-KV passes are captured
   const bool warm = std::find(c->warmed.begin(), c->warmed.end(), key) != c->warmed.end();
   if (gr) {  // replay: the pinned step block is copied in by the graph's first node
     HIPCHK(hipGraphLaunch(gr->exec, c->st));
-  } else if (!c->use_graph || !warm) {  // eager (first call of a shape, or graphs disabled)
+  } else if (!c->use_graph || !warm || path != 0) {  // eager (first call of a shape, graphs disabled, or
+                                                     // a pass whose attention kernels take pos0 as an argument)
     HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, c->st));
-    enqueue_verify(c, M, na, nb, nsplit);
+    enqueue_verify(c, M, na, nb, nsplit, path);
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, c->st));
     c->step_events = c->evused;  // profiling events one pass of this shape needs
@@ -1289,7 +1316,7 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
     hipGraph_t graph;
     HIPCHK(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
     (void)hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, c->st);
-    enqueue_verify(c, M, na, nb, nsplit);
+    enqueue_verify(c, M, na, nb, nsplit, 0);
     (void)hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, c->st);
     HIPCHK(hipStreamEndCapture(c->st, &graph));
     const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);

@@ -104,8 +104,9 @@ void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, co
 // score scratch (floats) of M rows starting at position Pb
 long long pf_score_floats(int M, int Pb, int sliding);
 // attn_tile / run_mh attention of segment rows [r0, r0 + M): q [n][2048] (row r at r), att likewise
+// staged: att rows in the staged GEMV input layout (staged_index) instead of plain
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
-                    int r0, int M, int sliding, hipStream_t st);
+                    int r0, int M, int sliding, hipStream_t st, bool staged = false);
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st);
 void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStream_t st);
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
 constexpr int PF_CP = 256;  // positions per weight chunk (4 per lane)
 __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
                                                     float* __restrict__ att, PfGeom g, int r0, int sliding,
-                                                    ExpfTab tab) {
+                                                    ExpfTab tab, int staged) {
   __shared__ __align__(16) float w[NQ][PF_CP];
   __shared__ uint64_t T[32];
   // the last rows (longest ranges) first, so that the long blocks do not trail the grid
@@ -335,19 +335,21 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
       for (int jj = 0; jj < cn; ++jj) den = den + w[lane][jj];
     __syncthreads();
   }
-  float* orow = att + (size_t)r * NQ * HD + 4 * lane;
-  if (tiled) {
-    const float inv = 1.0f / den;  // lanes 0..7
+  const float inv = tiled ? 1.0f / den : 1.0f;  // lanes 0..7
+  float* orow = att + (size_t)r * NQ * HD;
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      const float ih = __shfl(inv, h);
-      *reinterpret_cast<float4*>(orow + h * HD) =
-          make_float4(r16(O[h][0] * ih), r16(O[h][1] * ih), r16(O[h][2] * ih), r16(O[h][3] * ih));
+  for (int h = 0; h < NQ; ++h) {
+    const float ih = __shfl(inv, h);
+    float v[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) v[d] = tiled ? r16(O[h][d] * ih) : r16(O[h][d]);
+    const int n0 = h * HD + 4 * lane;
+    if (staged) {  // the staged GEMV input layout of the o projection (staged_index)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) orow[staged_index(n0 + d)] = v[d];
+    } else {
+      *reinterpret_cast<float4*>(orow + n0) = make_float4(v[0], v[1], v[2], v[3]);
     }
-  } else {
-#pragma unroll
-    for (int h = 0; h < NQ; ++h)
-      *reinterpret_cast<float4*>(orow + h * HD) = make_float4(r16(O[h][0]), r16(O[h][1]), r16(O[h][2]), r16(O[h][3]));
   }
 }
 
@@ -427,13 +429,13 @@ long long pf_score_floats(int M, int Pb, int sliding) {
   return 8 * (c * (Pb + 1) + c * (c - 1) / 2 + (R - c) * 512);
 }
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
-                    int r0, int M, int sliding, hipStream_t st) {
+                    int r0, int M, int sliding, hipStream_t st, bool staged) {
   const int Plast = g.pos0 + r0 + M - 1;
   const int maxlen = sliding ? std::min(Plast + 1, 512) : Plast + 1;
   const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
   hipLaunchKernelGGL(k_pf_scores, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
   ExpfTab tab{G4V_EXPF_TABLE};
-  hipLaunchKernelGGL(k_pf_attn_out, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab);
+  hipLaunchKernelGGL(k_pf_attn_out, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
 }
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st) {
   hipLaunchKernelGGL(k_pf_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, a, w1, w2);

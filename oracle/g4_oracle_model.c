@@ -366,8 +366,18 @@ static void forward_ex(g4o_model* m, const int* toks, const rows_t* r, int T, fl
   free(u);
 }
 
-static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf) {
-  forward_ex(m, toks, r, T, hbuf, 0, ATT_SPLIT);
+/* the attention path of a decode pass of M rows at pos0 (E:1305, 1328, 1337 with SPLITKV, TILED,
+ * ATT_PAR = 192): split-KV when M <= 4 and pos0 + M > 192, else attn_tile when M >= 4 and
+ * pos0 + M > 64 and the pass has no branch rows, else run_mh.  Passes with branch rows (the
+ * two-branch tree, a generalisation of the engine's single sibling row) keep the split-KV path
+ * for every size. */
+static int pass_amode(int M, int pos0, int nb) {
+  if (nb > 0 || (M <= 4 && pos0 + M > 192)) return ATT_SPLIT;
+  return (M >= 4 && pos0 + M > 64) ? ATT_TILE : ATT_MH;
+}
+
+static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf, int nb) {
+  forward_ex(m, toks, r, T, hbuf, 0, pass_amode(r->M, r->pos0, nb));
 }
 
 /* E:1594-1599 prefill of toks[0..n) at positions pos0.. in blocks of pfb (<= 32) rows, with
@@ -398,7 +408,7 @@ void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T) {
   for (int b = 0; b < M; b += 8) {
     rows_t r;
     rows_chain(&r, pos0 + b, (M - b) < 8 ? (M - b) : 8);
-    forward(m, toks + b, &r, T, NULL);
+    forward(m, toks + b, &r, T, NULL, 0);
   }
 }
 
@@ -433,7 +443,7 @@ void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
   rows_tree(&r, pos0, na, nb);
   const int M = r.M;
   float* hb = (float*)malloc(sizeof(float) * M * H);
-  forward(m, toks, &r, T, hb);
+  forward(m, toks, &r, T, hb, nb);
   memset(out, 0, sizeof *out);
   for (int i = 0; i < 8; ++i) out->G[i] = -1;
   eval_row(m, hb, toks, M, out, 0);

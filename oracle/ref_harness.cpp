@@ -862,7 +862,12 @@ int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* 
       lo[m] = A.sliding ? std::max(0, rope[m] - 511) : 0;
       kmin = std::min(kmin, lo[m]);
     }
-    for (int g0 = 0; g0 < M; g0 += 4) {  // AttnArg holds 4 rows: same geometry, rows in groups
+    // E:1305 / 1328 / 1337 (SPLITKV, TILED, ATT_PAR = 192) for a chain pass; passes with branch
+    // rows keep the split path (the generalised tree)
+    const bool split = nb > 0 || (M <= 4 && pos0 + M > 192);
+    if (!split && M >= 4 && pos0 + M > 64) ref_attn_tile(KCl, VCl, A.sliding, &q[0][0], pos0, M, &att[0][0]);
+    else if (!split) run_mh_rows(KCl, VCl, A.sliding, &q[0][0], pos0, M, &att[0][0]);
+    for (int g0 = 0; split && g0 < M; g0 += 4) {  // AttnArg holds 4 rows: same geometry, rows in groups
       AttnArg aa;
       aa.Kc = KCl;
       aa.Vc = VCl;

@@ -114,3 +114,30 @@ def test_verify_sequence_of_steps(pair):
         r, o = _both(pair, toks, 3, 0, pos0)
         pos0 += r.ncommit
         conf = r.commit[r.ncommit - 1]
+
+
+@pytest.mark.parametrize("na,pos0", [(4, 600), (3, 100), (2, 50), (0, 30), (3, 600), (4, 150)])
+def test_chain_pass_attention_paths(orc, g4v, na, pos0):
+    """decode passes take the engine's attention path (E:1305 / 1328 / 1337): attn_tile for 5 rows
+    and for 4 rows below ATT_PAR, run_mh for short passes near the start, split-KV past ATT_PAR;
+    the same shape on both sides of the threshold alternates between a captured and an eager pass"""
+    from oracle import Model
+    note(f"chain pass path na={na} pos0={pos0}")
+    dev = g4v.Device(0)
+    om = Model(orc, 23, 8192, 3, 6144, 1024)
+    try:
+        dev.model_synth(23, 8192, 3, 6144, 1024)
+        for p in (pos0, 600, pos0):  # the graph of the split shape must not serve the other path
+            dev.fake_ctx(700, 4242)
+            om.fake_ctx(700, 4242)
+            toks = np.array([17 + 29 * k for k in range(na + 1)], np.int32)
+            r, hg = dev.verify(toks, na, 0, p, 8, hidden=True)
+            o, ho = om.verify(toks, na, 0, p, 8)
+            assert r.nacc == o.nacc and list(r.commit[:r.ncommit]) == list(o.commit[:o.ncommit]), p
+            assert same(hg, ho), (p, first_diff(hg, ho))
+            kc, kco = dev.read("KC", np.uint16), om.get("KC", np.uint16, 3 * 1024 * 256)
+            vc, vco = dev.read("VC", np.uint16), om.get("VC", np.uint16, 3 * 1024 * 256)
+            assert same(kc, kco) and same(vc, vco), p
+    finally:
+        om.close()
+        dev.close()

@@ -1,0 +1,43 @@
+"""The attention path of a decode pass (E:1305 / 1328 / 1337: split-KV for at most 4 rows past
+ATT_PAR = 192 keys, attn_tile for 4+ rows past 64, run_mh otherwise): the oracle's verify pass
+against the reference's kernels composed the same way (oracle/_ref), token for token and KV byte
+for byte."""
+import numpy as np
+import pytest
+
+from util import first_diff, same
+
+V, NL, I, CTX, NFAKE = 262144, 2, 6144, 1024, 600
+# (chain length, pos0): 8 rows tiled; 4 rows below ATT_PAR, tiled; 3 rows, run_mh; 1 row at the
+# start of the cache, run_mh; 4 rows past ATT_PAR, split-KV
+CASES = [(7, 600), (3, 100), (2, 50), (0, 30), (3, 600)]
+
+
+@pytest.fixture(scope="module")
+def pair(orc, ref):
+    from oracle import Model
+    om, rm = Model(orc, 9, V, NL, I, CTX), Model(orc, 9, V, NL, I, CTX)
+    ref.bind_model(rm)
+    yield om, rm
+    om.close()
+    rm.close()
+
+
+@pytest.mark.parametrize("na,pos0", CASES)
+def test_chain_pass_paths(orc, ref, pair, na, pos0):
+    om, rm = pair
+    om.fake_ctx(NFAKE, 3)
+    rm.fake_ctx(NFAKE, 3)
+    toks = np.array([17 + 29 * k for k in range(na + 1)], np.int32)
+    o, _ = om.verify(toks, na, 0, pos0)
+    r = ref.verify(toks, na, 0, pos0)
+    assert (o.nacc, o.ncommit) == (r.nacc, r.ncommit)
+    assert list(o.commit[:o.ncommit]) == list(r.commit[:r.ncommit])
+    # rows the lazy head evaluates; past the first 4 rows the engine scores its second head group
+    # in full (E:1406-1500 per 4-row group), the oracle only along the accepted path
+    for i in range(na + 1):
+        if o.G[i] >= 0:
+            assert o.G[i] == r.G[i], (i, list(o.G), list(r.G))
+    for what in ("KC", "VC"):
+        a, b = om.get(what, np.uint16, NL * CTX * 256), rm.get(what, np.uint16, NL * CTX * 256)
+        assert same(a, b), (what, first_diff(a, b))
