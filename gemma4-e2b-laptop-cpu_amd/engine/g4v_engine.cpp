@@ -1,0 +1,263 @@
+// g4v_engine.cpp -- the engine's process boundary over the gfx950 library: the same command line
+// and line protocol as the reference engine (engine/gemma4_engine.cpp, cited as E), so that a
+// front-end written for it (its server, bench scripts) drives the GPU path unchanged.
+//
+//   g4v_engine <model> <index> <prompt.ids> <nnew>          one request (E:1211, 1689)
+//   ENGINE_SERVE=1 g4v_engine <model> <index> - 0           requests on stdin (E:1681-1688):
+//     "N id id ..."  -> FIRST <id> after the prefill, TOK <ids> per round (ENGINE_STREAM), then
+//                       GEN: <ids> and a TIMING line (E:1604, 1612-1614, 1672-1679)
+//     "BENCH_MODE k tree" -> MODE k=.. tree=.. / MODE_ERROR (E:1683)
+//
+// <model> names the synthetic stack "synth:SEED:V:NL:I" (the library has no checkpoint loader
+// yet); <index> is ignored.  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
+// (g4v_slot_*), the prefill (g4v_prefill), and decode rounds whose drafts come from prompt
+// lookup (ENGINE_NGRAM / ENGINE_NGLEN) or, when it finds none, the MTP drafter (ENGINE_K, a
+// synthetic drafter, seed ENGINE_DRAFTER_SEED), verified as a chain (g4v_verify_step).  The
+// sibling row of E:1634-1655 is not proposed (the engine with ENGINE_SIB_GAP=-1), and the
+// drafts of a round are capped at 4 (the verify step's chain).
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/g4v.h"
+
+namespace {
+
+g4v_ctx* G = nullptr;
+
+void check(int rc, const char* what) {
+  if (rc != 0) {
+    fprintf(stderr, "g4v %s: %s (%d)\n", what, g4v_error(G), rc);
+    fflush(stderr);
+    exit(1);
+  }
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
+bool is_stop(int t) { return t == 106 || t == 1; }  // E:1609
+
+struct Engine {
+  int V = 0, ctx = 4096, pfb = 32, T = 6, ng_n = 0, ng_len = 3, k_draft = 3;
+  bool drafter = false, stream = false;
+  double now() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+  }
+
+  // E:1584-1679 for one request
+  void run_req(const std::vector<int>& prompt, int nnew, bool print) {
+    const int n = (int)prompt.size();
+    int start = 0, slot = 0;
+    check(g4v_slot_begin(G, prompt.data(), n, &start, &slot), "slot_begin");
+    const double t0 = now();
+    int g0 = 0;
+    std::vector<float> hprev(1536);
+    check(g4v_prefill(G, prompt.data() + start, n - start, start, pfb, T, &g0, hprev.data()), "prefill");
+    const double tp = now() - t0;
+    std::vector<int> gen{g0};
+    if (print && nnew > 0) {
+      printf("FIRST %d\n", g0);
+      fflush(stdout);
+    }
+    if (nnew <= 0) {
+      check(g4v_slot_end(G, prompt.data(), n, nullptr, 0, n - 1), "slot_end");
+      if (print) {
+        printf("GEN:\nTIMING prompt=%d reused=%d new=%d prefill_s=%.3f decode_tokens=0 decode_s=0 decode_tok_s=0 "
+               "tokens_per_round=0 ngram_rounds=0/0 ngram_acc_per_round=0\n",
+               n, start, n - start, tp);
+        fflush(stdout);
+      }
+      return;
+    }
+    const double t1 = now();
+    size_t emitted = 1;
+    auto emit = [&]() {  // E:1612-1614
+      if (!stream || !print) return;
+      const size_t lim = std::min<size_t>(gen.size(), (size_t)nnew);
+      std::string o;
+      size_t i = emitted;
+      for (; i < lim; ++i) {
+        o += ' ' + std::to_string(gen[i]);
+        if (is_stop(gen[i])) {
+          ++i;
+          break;
+        }
+      }
+      if (i > emitted) {
+        printf("TOK%s\n", o.c_str());
+        fflush(stdout);
+        emitted = is_stop(gen[i - 1]) ? lim : i;
+      }
+    };
+    long rounds = 0, ng_rounds = 0, ng_acc = 0;
+    int P;
+    g4v_verify_result R;
+    if (k_draft == 0 || (!drafter && ng_n <= 0)) {  // E:1615: plain decode
+      for (int i = 1; i < nnew && !is_stop(gen.back()); ++i) {
+        const int t = gen.back();
+        check(g4v_verify_step(G, &t, 0, 0, n + i - 1, T, &R, nullptr), "verify_step");
+        gen.push_back(R.commit[0]);
+        emit();
+      }
+      P = n + std::max(0, nnew - 1) - 1;
+    } else {  // E:1617-1661
+      P = n - 1;
+      int conf = gen.back();
+      bool stopped = is_stop(conf), first = true;
+      if (ng_n > 0) {  // seq = prompt + generated (E:1625), kept on the device
+        std::vector<int> seq(prompt);
+        seq.push_back(g0);
+        check(g4v_history_set(G, seq.data(), (int)seq.size()), "history_set");
+      }
+      std::vector<int> app;
+      while ((int)gen.size() < nnew && !stopped) {
+        emit();
+        int block[8], nd = 0;
+        block[0] = conf;
+        bool used_ng = false;
+        if (ng_n > 0) {  // E:1624-1628, the round's committed tokens appended first
+          check(g4v_prompt_lookup(G, app.data(), (int)app.size(), ng_n, ng_len, block + 1, &nd), "prompt_lookup");
+          if (nd > 0) {
+            used_ng = true;
+            ++ng_rounds;
+          }
+        }
+        if (!used_ng && drafter) {  // E:1631-1645 (TAU 0: every draft is kept)
+          const int k = std::min(k_draft, 3);
+          check(g4v_draft_mtp(G, conf, first ? hprev.data() : nullptr, P, k, T, block + 1, nullptr, nullptr, nullptr),
+                "draft_mtp");
+          nd = k;
+        }
+        check(g4v_verify_step(G, block, nd, 0, P + 1, T, &R, nullptr), "verify_step");  // E:1648
+        ++rounds;
+        first = false;
+        const int nacc = R.nacc;  // E:1657-1660
+        if (used_ng) ng_acc += nacc;
+        app.clear();
+        for (int i = 0; i <= nacc; ++i) {
+          gen.push_back(R.commit[i]);
+          app.push_back(R.commit[i]);
+          if (is_stop(R.commit[i])) {
+            stopped = true;
+            break;
+          }
+        }
+        conf = R.commit[nacc];
+        P += nacc + 1;
+      }
+    }
+    emit();
+    const double td = now() - t1;
+    // E:1671: the cache holds the prompt and gen[0 .. P - n]
+    check(g4v_slot_end(G, prompt.data(), n, gen.data(), (int)gen.size(), P), "slot_end");
+    if ((int)gen.size() > nnew) gen.resize(nnew);
+    for (size_t i = 0; i < gen.size(); ++i)
+      if (is_stop(gen[i])) {
+        gen.resize(i + 1);
+        break;
+      }
+    if (print) {
+      printf("GEN:");
+      for (int g : gen) printf(" %d", g);
+      printf("\n");
+      const int produced = std::max(0, (int)gen.size() - 1);
+      printf("TIMING prompt=%d reused=%d new=%d prefill_s=%.3f decode_tokens=%d decode_s=%.3f decode_tok_s=%.2f "
+             "tokens_per_round=%.2f ngram_rounds=%ld/%ld ngram_acc_per_round=%.2f slot=%d\n",
+             n, start, n - start, tp, produced, td, produced / td, rounds ? (double)produced / rounds : 1.0,
+             ng_rounds, rounds, ng_rounds ? (double)ng_acc / ng_rounds : 0.0, slot);
+      fflush(stdout);
+    }
+  }
+};
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 5) {
+    fprintf(stderr, "usage: %s synth:SEED:V:NL:I <index> <prompt.ids | -> <nnew>\n", argv[0]);
+    return 2;
+  }
+  unsigned long long seed = 0;
+  int V = 0, NL = 0, I = 0;
+  if (sscanf(argv[1], "synth:%llu:%d:%d:%d", &seed, &V, &NL, &I) != 4) {
+    fprintf(stderr, "model must be synth:SEED:V:NL:I (no checkpoint loader yet)\n");
+    return 2;
+  }
+  Engine e;
+  e.V = V;
+  e.ctx = env_int("ENGINE_CTX", 4096);
+  e.pfb = env_int("ENGINE_PREFILL_BLOCK", 32);
+  e.ng_n = env_int("ENGINE_NGRAM", 0);
+  e.ng_len = std::min(4, std::min(7, env_int("ENGINE_NGLEN", 3)));  // E:1514, capped at the 4-draft chain
+  e.k_draft = env_int("ENGINE_K", 3);
+  e.stream = getenv("ENGINE_STREAM") != nullptr;
+  {  // the pool size (E:75-77): one split per worker
+    int ncpu = 6;
+    if (const char* c = getenv("ENGINE_CPUS")) {
+      ncpu = 1;
+      for (const char* p = c; *p; ++p) ncpu += *p == ',';
+    }
+    e.T = std::max(1, std::min(16, ncpu));
+  }
+  check(g4v_create(0, &G), "create");
+  check(g4v_model_synth(G, seed, V, NL, I, e.ctx), "model_synth");
+  if (e.k_draft > 0 && NL >= 15 && V % 2048 == 0) {
+    check(g4v_drafter_synth(G, (uint64_t)env_int("ENGINE_DRAFTER_SEED", (int)seed + 1)), "drafter_synth");
+    e.drafter = true;
+  }
+  check(g4v_slots_init(G, std::max(1, env_int("ENGINE_SLOTS", 1)), env_int("ENGINE_SLOT_MIN_REUSE", 32)), "slots_init");
+  {  // E:1578: one warm-up pass at position 0 (the cache is not marked valid by it)
+    const int w = 2;
+    int g = 0;
+    check(g4v_prefill(G, &w, 1, 0, e.pfb, e.T, &g, nullptr), "warm-up");
+  }
+  if (getenv("ENGINE_SERVE")) {
+    std::string line;
+    while (std::getline(std::cin, line)) {
+      if (line.rfind("BENCH_MODE ", 0) == 0) {  // E:1683
+        std::stringstream ms(line);
+        std::string cmd;
+        int k = -1, tree = -1;
+        ms >> cmd >> k >> tree;
+        if (k >= 1 && k <= 3 && tree == 0 && e.drafter) {
+          e.k_draft = k;
+          printf("MODE k=%d tree=%d\n", k, tree);
+        } else {
+          printf("MODE_ERROR\n");
+        }
+        fflush(stdout);
+        continue;
+      }
+      std::stringstream ss(line);
+      int nn;
+      if (!(ss >> nn)) continue;
+      std::vector<int> pr;
+      std::string w;
+      while (ss >> w) pr.push_back(atoi(w.c_str()));
+      if (pr.empty()) continue;
+      e.run_req(pr, nn, true);
+    }
+  } else {
+    std::vector<int> prompt;
+    std::ifstream f(argv[3]);
+    int v;
+    while (f >> v) prompt.push_back(v);
+    if (prompt.empty()) {
+      fprintf(stderr, "empty prompt %s\n", argv[3]);
+      return 2;
+    }
+    e.run_req(prompt, atoi(argv[4]), true);
+  }
+  fflush(stdout);
+  g4v_destroy(G);
+  return 0;
+}

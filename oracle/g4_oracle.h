@@ -150,6 +150,9 @@ void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
  * fills the KV cache; hlast (optional) receives the final-normed hidden row of the last token */
 void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, float* hlast);
 
+/* the head of one final-normed row (E:1406-1500); toks[0..nt) (nt <= 8) seed the screen */
+int g4o_model_head(g4o_model* m, const float* h, const int* toks, int nt);
+
 /* forward of M rows that fills the KV cache only (want = false) */
 void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T);
 

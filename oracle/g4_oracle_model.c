@@ -433,6 +433,14 @@ static void eval_row(g4o_model* m, const float* h, const int* toks, int M, g4o_v
   free(sval);
 }
 
+/* the greedy token of one final-normed row h (E:1406-1500 for a single row, seeds: toks[0..nt)) */
+int g4o_model_head(g4o_model* m, const float* h, const int* toks, int nt) {
+  g4o_verify_out out;
+  memset(&out, 0, sizeof out);
+  eval_row(m, h, toks, nt, &out, 0);
+  return out.G[0];
+}
+
 /* E:1453-1488 lazy head evaluation and E:1647-1661 acceptance, generalised to two branches:
  * branch a is walked when G[0] == toks[1]; otherwise branch b when G[0] == toks[b1]
  * (the reference's sibling test, E:1477).  Row r is evaluated only when the draft it holds

@@ -73,6 +73,7 @@ class Oracle:
             "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
             "g4o_prefill": (None, [_vp, _i32p, _i, _i, _i, _i, _vp]),
+            "g4o_model_head": (_i, [_vp, _f32p, _i32p, _i]),
             "g4o_drafter_new": (_vp, [C.c_uint64, _i]), "g4o_drafter_free": (None, [_vp]),
             "g4o_drafter_ptr": (_vp, [_vp, C.c_char_p]),
             "g4o_b16_gemv": (None, [_u16p, _i, _i, _f32p, _f32p]),
@@ -264,6 +265,11 @@ class Model:
         hid = np.empty(1536, np.float32)
         self.o.L.g4o_prefill(self.h, toks, toks.size, pos0, pfb, T, hid.ctypes.data)
         return hid
+
+    def head(self, h, seeds=()):
+        """greedy token of one final-normed row"""
+        sd = np.asarray(list(seeds)[:8] or [0], np.int32)
+        return self.o.L.g4o_model_head(self.h, _c(h, np.float32), sd, len(list(seeds)[:8]))
 
     def verify(self, toks, na, nb, pos0, T=8):
         out = VerifyOut()
