@@ -1118,12 +1118,14 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
 static double w4_bytes(const Mat& m) { return (double)m.N * m.K / 2 + (double)m.N * m.K / 16; }
 
 // the attention path of a pass (E:1305 / 1328 / 1337 with SPLITKV, TILED, ATT_PAR = 192):
-// 0 split-KV when M <= 4 and pos0 + M > 192, else 1 attn_tile when M >= 4 and pos0 + M > 64,
-// else 2 run_mh; passes with branch rows (the two-branch tree generalises the engine's single
-// sibling row) take the split-KV path for every size
+// 0 split-KV when M <= 4 and pos0 + M > 192, else 1 attn_tile when M >= 4 and pos0 + M > 64 and
+// the pass has no sibling row, else 2 run_mh.  One branch row in at most 4 rows is the engine's
+// sibling form; larger trees (two branches of several rows, which the engine does not form) take
+// the split-KV path for every size
 static int pass_path(int M, int pos0, int nb) {
-  if (nb > 0 || (M <= 4 && pos0 + M > 192)) return 0;
-  return (M >= 4 && pos0 + M > 64) ? 1 : 2;
+  if (nb > 1 || (nb == 1 && M > 4)) return 0;
+  if (M <= 4 && pos0 + M > 192) return 0;
+  return (nb == 0 && M >= 4 && pos0 + M > 64) ? 1 : 2;
 }
 
 static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
@@ -1175,13 +1177,15 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     if (path == 0) {
       launch_attn(KCl, VCl, c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln, rstep, sp, A.sliding, T,
                   c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), M, st);
-    } else {  // a chain pass below ATT_PAR or of more than 4 rows: the prefill kernels (chain rows:
-              // RoPE position = cache slot = pos0 + m), output staged for the o projection
+    } else {  // a chain pass below ATT_PAR or of more than 4 rows, or the sibling form below ATT_PAR:
+              // the prefill kernels (RoPE position = cache slot = pos0 + m, the sibling's pos0 + 1),
+              // output staged for the o projection
       const float* cs = c->rope.as<float>() + (size_t)(2 * (A.sliding ? 0 : 1)) * c->ctxcap * (HD / 2);
+      const int sib = nb == 1 ? na + 1 : -1;
       launch_pf_qkv(c->q.as<float>(), c->k.as<float>(), c->v.as<float>(), ln.qn, ln.kn, cs,
-                    cs + (size_t)c->ctxcap * (HD / 2), KCl, VCl, sh.pos0, M, st);
-      launch_pf_attn(c->q.as<float>(), KCl, VCl, c->vsc.as<float>(), c->vatt.as<float>(), PfGeom{M, sh.pos0, M}, 0,
-                     M, A.sliding, st, true);
+                    cs + (size_t)c->ctxcap * (HD / 2), KCl, VCl, sh.pos0, M, st, sib);
+      launch_pf_attn(c->q.as<float>(), KCl, VCl, c->vsc.as<float>(), c->vatt.as<float>(),
+                     PfGeom{M, sh.pos0, M, sib}, 0, M, A.sliding, st, true);
     }
     pmark(c, PT_ATTN, 0, (double)(sh.pos0 + M - kmin) * HD * 2 * 2);
     pmark(c, PT_GEMV_O, 1, 0);
@@ -1252,8 +1256,23 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
   pmark(c, PT_ACCEPT, 0, 0);
 }
 
+static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, int b_ok,
+                       g4v_verify_result* out, float* hidden);
+
 int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
                     float* hidden) {
+  return verify_pass(c, toks, na, nb, pos0, nsplit, 1, out, hidden);
+}
+
+int g4v_verify_sibling(g4v_ctx* c, const int* toks, int nd, int pos0, int nsplit, int allow_hit,
+                       g4v_verify_result* out, float* hidden) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(nd >= 1 && nd <= 2, "verify_sibling: 1 <= nd <= 2 (the sibling form has at most 4 rows)");
+  return verify_pass(c, toks, nd, 1, pos0, nsplit, allow_hit ? 1 : 0, out, hidden);
+}
+
+static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, int b_ok,
+                       g4v_verify_result* out, float* hidden) {
   if (!c) return G4V_E_ARG;
   std::string missing;
   if (!c->model_ready || !model_complete(c, &missing)) {
@@ -1274,6 +1293,7 @@ int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int n
   s.na = na;
   s.nb = nb;
   s.pos0 = pos0;
+  s.b_ok = b_ok;
   for (int r = 0; r < M; ++r) {
     s.toks[r] = toks[r];
     if (r <= na) {
@@ -1488,7 +1508,7 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
   int r = pf_alloc(c, n, sfl);
   if (r) return r;
   HIPCHK(hipMemcpyAsync(c->pftok.p, toks, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
-  const PfGeom g{n, pos0, pfb};
+  const PfGeom g{n, pos0, pfb, -1};
   if (nA > 0) pf_segment(c, g, 0, nA, true, false, nsplit, tail ? -1 : nA - 1);
   if (tail) pf_segment(c, g, nA, Ml, Ml >= 2, tsplit, nsplit, Ml - 1);
   HIPCHK(hipGetLastError());

@@ -13,6 +13,7 @@ struct StepDev {
   int rope[MAXM];
   int skip_lo[MAXM];
   int skip_hi[MAXM];
+  int b_ok;  // 0: branch b is never committed (the sibling row when the tree hit is not taken)
 };
 
 struct VerifyResultDev {
@@ -93,14 +94,18 @@ void launch_gen_w4(uint8_t* w, uint16_t* s, size_t nbytes, size_t nscales, uint6
 
 // prefill (g4v_prefill.hip).  Rows r of a prompt of n rows sit at positions pos0 + r, in blocks
 // of pfb rows; a kernel over a segment of rows [r0, r0 + M) takes its rows' paths from this.
+// rows pos0 .. pos0 + n - 1 in blocks of pfb; sib >= 0: that row is the engine's sibling row
+// (E:1292, 1340-1345): RoPE position and window from pos0 + 1, positions pos0 + 1 .. its own slot - 1
+// skipped, and its pass never takes attn_tile (E:1328)
 struct PfGeom {
-  int n, pos0, pfb;
+  int n, pos0, pfb, sib;
 };
 void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, float sqh, float* x, float* a, int M,
                      hipStream_t st);
-// q [M][2048] normed + rotated in place; k, v [M][256] normed into the cache rows P0 ..
+// q [M][2048] normed + rotated in place; k, v [M][256] normed into the cache rows P0 ..; row sib
+// (>= 0) is rotated at position P0 + 1 (the sibling row)
 void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
-                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st);
+                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib = -1);
 // score scratch (floats) of M rows starting at position Pb
 long long pf_score_floats(int M, int Pb, int sliding);
 // attn_tile / run_mh attention of segment rows [r0, r0 + M): q [n][2048] (row r at r), att likewise

@@ -183,7 +183,7 @@ __global__ void k_branch(const StepDev* sp, const int* best1, const float* __res
     if (sp->na >= 1 && sp->toks[1] == G0) {
       first = 1;
       cnt = sp->na;
-    } else if (sp->nb >= 1 && sp->toks[sp->na + 1] == G0) {
+    } else if (sp->nb >= 1 && sp->b_ok && sp->toks[sp->na + 1] == G0) {
       first = sp->na + 1;
       cnt = sp->nb;
     }

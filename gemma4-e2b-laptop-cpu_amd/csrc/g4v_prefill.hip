@@ -28,15 +28,29 @@ namespace {
 // attention path of row r (E:1305, 1328, 1337): its block [b pfb, ...) of M rows at p0
 __device__ __forceinline__ bool pf_tiled(int r, const PfGeom& g) {
   const int b = r / g.pfb, M = min(g.pfb, g.n - b * g.pfb), p0 = g.pos0 + b * g.pfb;
-  return M >= 4 && p0 + M > 64;
+  return g.sib < 0 && M >= 4 && p0 + M > 64;
 }
 __device__ __forceinline__ int pf_lo(int P, int sliding) { return sliding ? max(0, P - 511) : 0; }
+// first key of row r (slot P): the window runs from its RoPE position (pos0 + 1 for the sibling)
+__device__ __forceinline__ int pf_row_lo(int r, int P, const PfGeom& g, int sliding) {
+  return pf_lo(r == g.sib ? g.pos0 + 1 : P, sliding);
+}
+// E:1345 valid(p) of row r at slot P
+__device__ __forceinline__ bool pf_valid(int r, int P, int p, const PfGeom& g) {
+  return r != g.sib || p <= g.pos0 || p == P;
+}
 // offset of the score row of segment row rr (rows r0 + j, positions Pb + j, Pb = pos0 + r0)
 __device__ __forceinline__ long long pf_soff(int rr, int Pb, int sliding) {
   const long long R = rr;
   if (!sliding) return 8 * (R * (Pb + 1) + R * (R - 1) / 2);
   const long long c = min(max(512 - Pb, 0), rr);  // rows whose range starts at 0
   return 8 * (c * (Pb + 1) + c * (c - 1) / 2 + (R - c) * 512);
+}
+
+// score row of segment row rr of a launch over nrows rows (the sibling row's, whose window may be
+// longer, after all of them)
+__device__ __forceinline__ long long pf_srow(int rr, int r, int nrows, int Pb, int sliding, const PfGeom& g) {
+  return r == g.sib ? pf_soff(nrows, Pb, sliding) : pf_soff(rr, Pb, sliding);
 }
 
 // E:1262-1267: x = r16(E[tok] * sqrt(H)); a = (x * r) * in_ln (unrounded: the W4A8 source)
@@ -63,7 +77,7 @@ __global__ __launch_bounds__(HD) void k_pf_qkv(float* __restrict__ q, const floa
                                                const float* __restrict__ v, const float* __restrict__ qn,
                                                const float* __restrict__ kn, const float* __restrict__ cs,
                                                const float* __restrict__ sn, uint16_t* __restrict__ KC,
-                                               uint16_t* __restrict__ VC, int P0) {
+                                               uint16_t* __restrict__ VC, int P0, int sib) {
   constexpr int NV = NQ + 2;
   __shared__ float xv[NV][HD];
   __shared__ double part[NV][16];
@@ -103,8 +117,8 @@ __global__ __launch_bounds__(HD) void k_pf_qkv(float* __restrict__ q, const floa
   for (int h = 0; h < NQ + 1; ++h) xv[h][e] = y[h];
   __syncthreads();
   // E:394-402 NeoX halves: out_i = fma(u, c, -(w s)) and out_{i+128} = fma(w, c, u s)
-  const int i2 = e & (HD / 2 - 1);
-  const float c = cs[(size_t)P * (HD / 2) + i2], sv = sn[(size_t)P * (HD / 2) + i2];
+  const int i2 = e & (HD / 2 - 1), PR = m == sib ? P0 + 1 : P;  // E:1292 the sibling's RoPE position
+  const float c = cs[(size_t)PR * (HD / 2) + i2], sv = sn[(size_t)PR * (HD / 2) + i2];
   auto rot = [&](const float* yy) {
     return e < HD / 2 ? fmaf(yy[e], c, -(yy[e + HD / 2] * sv)) : fmaf(yy[e], c, yy[e - HD / 2] * sv);
   };
@@ -122,7 +136,8 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
                                                    float* __restrict__ S, PfGeom g, int r0, int sliding) {
   __shared__ __align__(16) float qs[NQ][HD];
   // the last rows (longest ranges) first, so that the long blocks do not trail the grid
-  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
+  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_row_lo(r, P, g, sliding);
+  const int len = P - lo + 1;
   const int sp0 = lo + blockIdx.y * PF_SPAN;
   if (sp0 > P) return;  // uniform
   const bool tiled = pf_tiled(r, g);
@@ -199,9 +214,10 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
       }
     }
   }
-  float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
+  float* Srow = S + pf_srow(rr, r, gridDim.x, g.pos0 + r0, sliding, g);
+  const bool ok = pf_valid(r, P, p, g);  // a skipped position never wins the maximum
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) Srow[(size_t)h * len + (p - lo)] = hsum8(vv[h]);
+  for (int h = 0; h < NQ; ++h) Srow[(size_t)h * len + (p - lo)] = ok ? hsum8(vv[h]) : -INFINITY;
 }
 
 // output of one row: one wave, lane l holds dims 4l .. 4l+3 of the 8 heads (32 accumulators), so
@@ -215,10 +231,11 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
   __shared__ __align__(16) float w[NQ][PF_CP];
   __shared__ uint64_t T[32];
   // the last rows (longest ranges) first, so that the long blocks do not trail the grid
-  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_lo(P, sliding), len = P - lo + 1;
+  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_row_lo(r, P, g, sliding);
+  const int len = P - lo + 1;
   const int lane = threadIdx.x;
   const bool tiled = pf_tiled(r, g);
-  const float* Srow = S + pf_soff(rr, g.pos0 + r0, sliding);
+  const float* Srow = S + pf_srow(rr, r, gridDim.x, g.pos0 + r0, sliding, g);
   if (lane < 32) T[lane] = tab.t[lane];
   float mx[NQ];  // max per head (order-free), on every lane
 #pragma unroll
@@ -237,9 +254,11 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
 #pragma unroll
       for (int k = 0; k < PF_CP / 64; ++k) {
         const int jj = lane + 64 * k;
-        if (jj < cn)
+        if (jj < cn) {
+          const bool ok = pf_valid(r, P, lo + c0 + jj, g);  // skipped positions weigh 0 (den + 0 is exact)
 #pragma unroll
-          for (int h = 0; h < NQ; ++h) w[h][jj] = libm_expf_neg(Srow[(size_t)h * len + c0 + jj] - mx[h], T);
+          for (int h = 0; h < NQ; ++h) w[h][jj] = ok ? libm_expf_neg(Srow[(size_t)h * len + c0 + jj] - mx[h], T) : 0.f;
+        }
       }
       __syncthreads();
       if (lane < NQ)
@@ -268,12 +287,14 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
 #pragma unroll
     for (int k = 0; k < PF_CP / 64; ++k) {
       const int jj = lane + 64 * k;
-      if (jj < cn)
+      if (jj < cn) {
+        const bool ok = pf_valid(r, P, lo + c0 + jj, g);  // fma(0, v, O) leaves O as it is
 #pragma unroll
         for (int h = 0; h < NQ; ++h) {
           const float dd = sreg[k][h] - mx[h];
-          w[h][jj] = tiled ? exp8(dd) : libm_expf_neg(dd, T) / dh[h];
+          w[h][jj] = !ok ? 0.f : (tiled ? exp8(dd) : libm_expf_neg(dd, T) / dh[h]);
         }
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -419,8 +440,8 @@ void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, flo
   hipLaunchKernelGGL(k_pf_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, toks, in_ln, sqh, x, a);
 }
 void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
-                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st) {
-  hipLaunchKernelGGL(k_pf_qkv, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0);
+                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib) {
+  hipLaunchKernelGGL(k_pf_qkv, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib);
 }
 long long pf_score_floats(int M, int Pb, int sliding) {
   const long long R = M;
@@ -431,7 +452,8 @@ long long pf_score_floats(int M, int Pb, int sliding) {
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
                     int r0, int M, int sliding, hipStream_t st, bool staged) {
   const int Plast = g.pos0 + r0 + M - 1;
-  const int maxlen = sliding ? std::min(Plast + 1, 512) : Plast + 1;
+  // the sibling's window (from pos0 + 1) can be longer than 512 by the rows it skips
+  const int maxlen = sliding ? std::min(Plast + 1, g.sib >= 0 ? Plast - g.pos0 + 511 : 512) : Plast + 1;
   const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
   hipLaunchKernelGGL(k_pf_scores, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
   ExpfTab tab{G4V_EXPF_TABLE};

@@ -12,9 +12,10 @@
 // yet); <index> is ignored.  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
 // (g4v_slot_*), the prefill (g4v_prefill), and decode rounds whose drafts come from prompt
 // lookup (ENGINE_NGRAM / ENGINE_NGLEN) or, when it finds none, the MTP drafter (ENGINE_K, a
-// synthetic drafter, seed ENGINE_DRAFTER_SEED), verified as a chain (g4v_verify_step).  The
-// sibling row of E:1634-1655 is not proposed (the engine with ENGINE_SIB_GAP=-1), and the
-// drafts of a round are capped at 4 (the verify step's chain).
+// synthetic drafter, seed ENGINE_DRAFTER_SEED), verified as a chain (g4v_verify_step) or, when
+// the drafter's runner-up is proposed as a sibling row (E:1634-1655: ENGINE_SIB_GAP,
+// ENGINE_SIB_LONG, ENGINE_TREE / BENCH_MODE k 1, ENGINE_POLICY), with g4v_verify_sibling.
+// Prompt-lookup drafts of a round are capped at 4 (the verify step's chain).
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -46,9 +47,15 @@ int env_int(const char* name, int dflt) {
 
 bool is_stop(int t) { return t == 106 || t == 1; }  // E:1609
 
+constexpr int ATT_PAR = 192;  // E:1214
+
 struct Engine {
   int V = 0, ctx = 4096, pfb = 32, T = 6, ng_n = 0, ng_len = 3, k_draft = 3;
-  bool drafter = false, stream = false;
+  bool drafter = false, stream = false, tree = false, sib_long = false;
+  float sib_gap = 1.0f;      // E:1629 ENGINE_SIB_GAP: the sibling row is proposed when >= 0
+  int pol[3] = {-1, -1, -1};  // E:1513 ENGINE_POLICY: draft count cap per state
+  long r1_n = 0, r1_top1 = 0, r1_top2 = 0;  // E:1084, 1659 (over the process)
+  long tree_attempts = 0, tree_hits = 0;    // E:1583 (per request), 1648, 1650
   double now() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
   }
@@ -57,6 +64,7 @@ struct Engine {
   void run_req(const std::vector<int>& prompt, int nnew, bool print) {
     const int n = (int)prompt.size();
     int start = 0, slot = 0;
+    tree_attempts = tree_hits = 0;
     check(g4v_slot_begin(G, prompt.data(), n, &start, &slot), "slot_begin");
     const double t0 = now();
     int g0 = 0;
@@ -111,7 +119,7 @@ struct Engine {
       P = n + std::max(0, nnew - 1) - 1;
     } else {  // E:1617-1661
       P = n - 1;
-      int conf = gen.back();
+      int conf = gen.back(), state = 1;
       bool stopped = is_stop(conf), first = true;
       if (ng_n > 0) {  // seq = prompt + generated (E:1625), kept on the device
         std::vector<int> seq(prompt);
@@ -119,10 +127,17 @@ struct Engine {
         check(g4v_history_set(G, seq.data(), (int)seq.size()), "history_set");
       }
       std::vector<int> app;
+      auto commit = [&](int t) {
+        gen.push_back(t);
+        app.push_back(t);
+      };
       while ((int)gen.size() < nnew && !stopped) {
         emit();
         int block[8], nd = 0;
         block[0] = conf;
+        int k = std::min(k_draft, 3);
+        if (pol[0] >= 0) k = std::min(k, pol[state]);
+        if (tree) k = std::min(k, 2);
         bool used_ng = false;
         if (ng_n > 0) {  // E:1624-1628, the round's committed tokens appended first
           check(g4v_prompt_lookup(G, app.data(), (int)app.size(), ng_n, ng_len, block + 1, &nd), "prompt_lookup");
@@ -131,21 +146,56 @@ struct Engine {
             ++ng_rounds;
           }
         }
-        if (!used_ng && drafter) {  // E:1631-1645 (TAU 0: every draft is kept)
-          const int k = std::min(k_draft, 3);
-          check(g4v_draft_mtp(G, conf, first ? hprev.data() : nullptr, P, k, T, block + 1, nullptr, nullptr, nullptr),
-                "draft_mtp");
-          nd = k;
-        }
-        check(g4v_verify_step(G, block, nd, 0, P + 1, T, &R, nullptr), "verify_step");  // E:1648
-        ++rounds;
-        first = false;
-        const int nacc = R.nacc;  // E:1657-1660
-        if (used_ng) ng_acc += nacc;
         app.clear();
+        int sec1 = -1;
+        float gap1 = -1.0f;
+        bool use_sib = false;
+        if (!used_ng && drafter && k > 0) {  // E:1632-1645 (TAU 0: every draft is kept)
+          int d[3], sec[3];
+          float gap[3];
+          check(g4v_draft_mtp(G, conf, first ? hprev.data() : nullptr, P, k, T, d, sec, gap, nullptr), "draft_mtp");
+          sec1 = sec[0];
+          gap1 = gap[0];
+          const bool allow_sib = sib_gap >= 0.0f && rounds >= 1 && state < 2 && k >= 2 && sec1 >= 0 && sec1 != d[0];
+          const bool sib_cond = (P + 1 + k > ATT_PAR)
+                                    ? (sib_long && (gap1 <= 0.85f || (gap1 >= 1.65f && gap1 <= 2.55f)))
+                                    : (gap1 <= ((rounds <= 3 || state == 1) ? 2.55f : 1.80f));
+          use_sib = allow_sib && sib_cond;  // E:1639-1641: the chain stops after its first draft
+          nd = use_sib ? 1 : k;
+          for (int j = 0; j < nd; ++j) block[1 + j] = d[j];
+        }
+        first = false;
+        // E:1647-1649
+        const int sibling = ((tree || use_sib) && !used_ng && nd >= 1 && sec1 >= 0 && sec1 != block[1]) ? nd + 1 : -1;
+        if (sibling >= 0) {
+          block[sibling] = sec1;
+          ++tree_attempts;
+          const bool allow_hit = tree || (P + 1 + sibling <= ATT_PAR && gap1 >= 0.25f);  // E:1650
+          check(g4v_verify_sibling(G, block, nd, P + 1, T, allow_hit ? 1 : 0, &R, nullptr), "verify_sibling");
+        } else {
+          check(g4v_verify_step(G, block, nd, 0, P + 1, T, &R, nullptr), "verify_step");  // E:1649
+        }
+        ++rounds;
+        if (R.branch == 1) {  // E:1650-1653 the tree hit: row 0's token and the sibling's
+          ++tree_hits;
+          commit(R.commit[0]);
+          if (!is_stop(R.commit[0]) && (int)gen.size() < nnew) commit(R.commit[1]);
+          stopped = is_stop(gen.back());
+          conf = R.commit[1];
+          P += 2;
+          state = 1;
+          continue;
+        }
+        if (!used_ng && nd >= 1) {  // E:1655
+          ++r1_n;
+          if (block[1] == R.G[0]) ++r1_top1;
+          else if (sec1 == R.G[0]) ++r1_top2;
+        }
+        const int nacc = R.nacc;  // E:1656-1660
+        if (used_ng) ng_acc += nacc;
+        state = nacc == 0 ? 0 : ((!use_sib && nacc == nd) ? 2 : 1);
         for (int i = 0; i <= nacc; ++i) {
-          gen.push_back(R.commit[i]);
-          app.push_back(R.commit[i]);
+          commit(R.commit[i]);
           if (is_stop(R.commit[i])) {
             stopped = true;
             break;
@@ -166,6 +216,9 @@ struct Engine {
         break;
       }
     if (print) {
+      fprintf(stderr, "RANK1 rounds=%ld top1=%ld top2_only=%ld TREE attempts=%ld hits=%ld\n", r1_n, r1_top1, r1_top2,
+              tree_attempts, tree_hits);  // E:1673
+      fflush(stderr);
       printf("GEN:");
       for (int g : gen) printf(" %d", g);
       printf("\n");
@@ -200,6 +253,10 @@ int main(int argc, char** argv) {
   e.ng_len = std::min(4, std::min(7, env_int("ENGINE_NGLEN", 3)));  // E:1514, capped at the 4-draft chain
   e.k_draft = env_int("ENGINE_K", 3);
   e.stream = getenv("ENGINE_STREAM") != nullptr;
+  e.tree = env_int("ENGINE_TREE", 0) == 1;
+  e.sib_long = getenv("ENGINE_SIB_LONG") != nullptr;
+  if (const char* g = getenv("ENGINE_SIB_GAP")) e.sib_gap = (float)atof(g);
+  if (const char* pp = getenv("ENGINE_POLICY")) sscanf(pp, "%d,%d,%d", &e.pol[0], &e.pol[1], &e.pol[2]);
   {  // the pool size (E:75-77): one split per worker
     int ncpu = 6;
     if (const char* c = getenv("ENGINE_CPUS")) {
@@ -228,8 +285,9 @@ int main(int argc, char** argv) {
         std::string cmd;
         int k = -1, tree = -1;
         ms >> cmd >> k >> tree;
-        if (k >= 1 && k <= 3 && tree == 0 && e.drafter) {
+        if (k >= 1 && k <= 3 && tree >= 0 && tree <= 1 && e.drafter) {
           e.k_draft = k;
+          e.tree = tree == 1;
           printf("MODE k=%d tree=%d\n", k, tree);
         } else {
           printf("MODE_ERROR\n");

@@ -47,6 +47,7 @@ SIGNATURES = {
     "g4v_model_fake_ctx": (_i, [_vp, _i, C.c_uint64]),
     "g4v_model_read": (_i, [_vp, C.c_char_p, _vp, C.c_size_t, C.POINTER(C.c_size_t)]),
     "g4v_verify_step": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
+    "g4v_verify_sibling": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
     "g4v_profile": (_i, [_vp, C.c_uint]),
     "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
     "g4v_sync": (_i, [_vp]),
@@ -347,4 +348,13 @@ class Device:
         hid = np.empty(1536, np.float32) if hidden else None
         self._ok(self.L.g4v_verify_step(self.h, _c(toks, np.int32), na, nb, pos0, T, C.addressof(r),
                                         None if hid is None else hid.ctypes.data), "verify_step")
+        return (r, hid) if hidden else r
+
+    def verify_sibling(self, toks, nd, pos0, T=8, allow_hit=True, hidden=False):
+        """the engine's pass with drafts toks[1..nd] and the sibling row toks[nd + 1]"""
+        r = VerifyResult()
+        hid = np.empty(1536, np.float32) if hidden else None
+        self._ok(self.L.g4v_verify_sibling(self.h, _c(toks, np.int32), nd, pos0, T, 1 if allow_hit else 0,
+                                           C.addressof(r), None if hid is None else hid.ctypes.data),
+                 "verify_sibling")
         return (r, hid) if hidden else r

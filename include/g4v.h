@@ -110,6 +110,15 @@ typedef struct {
 } g4v_verify_result;
 int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
                     float* hidden);
+/* the engine's pass with a sibling row (E:1634-1655): toks[0] confirmed, toks[1..nd] MTP drafts
+ * (nd 1 or 2), toks[nd+1] the drafter's runner-up for the first draft, at RoPE position pos0 + 1
+ * and slot pos0 + nd + 1, attending rows up to pos0 and itself (E:1345).  allow_hit is the
+ * engine's (TREE || (P + 1 + sibling <= ATT_PAR && gap1 >= 0.25)) of E:1650: when set and row 0's
+ * token equals the sibling's (but not the first draft's), the sibling commits (branch 1, its KV
+ * moved to slot pos0 + 1); otherwise only chain acceptance applies.  Replaces fwd(block, nd + 2,
+ * P + 1, true, 0, nullptr, sibling) and the tree-hit test of engine/gemma4_engine.cpp:1647-1656. */
+int g4v_verify_sibling(g4v_ctx* c, const int* toks, int nd, int pos0, int nsplit, int allow_hit,
+                       g4v_verify_result* out, float* hidden);
 /* Verify steps run as one captured HIP graph per shape (rows, branches, splits) from the
  * second call of that shape on (the engine's persistent pool + job word, E:73-141, becomes a
  * graph launch).  on = 0 launches every kernel from the host instead. */

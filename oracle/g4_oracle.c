@@ -792,14 +792,18 @@ void g4o_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M
  *   e_p = expf(d_p - mx) (libm), den = sum_p e_p in position order;
  *   in position order: o = fma(e_p / den, v_p, o);  out = r16(o). */
 void g4o_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
-                 const int* pos, const int* lo, float* out, int ldo) {
+                 const int* pos, const int* lo, const int* skip_lo, const int* skip_hi, float* out, int ldo) {
   for (int m = 0; m < M; ++m) {
     const int len = pos[m] - lo[m] + 1;
+    /* E:1345 valid(p): the sibling row skips the chain rows between row 0 and itself */
+    const int s0 = skip_lo ? skip_lo[m] : 1, s1 = skip_hi ? skip_hi[m] : 0;
+#define MH_VALID(p) (!((p) >= s0 && (p) <= s1))
     float* sc = (float*)malloc(sizeof(float) * (size_t)(len > 0 ? len : 1));
     for (int h = 0; h < nh; ++h) {
       const float* qh = q + (size_t)m * ldq + (size_t)h * hd;
       float mx = -1e30f;
       for (int p = lo[m]; p <= pos[m]; ++p) {
+        if (!MH_VALID(p)) continue;
         float sv[8] = {0};
         for (int i = 0; i < hd; i += 8)
           for (int l = 0; l < 8; ++l) sv[l] = fmaf(qh[i + l], g4o_bf2f(Kc[(size_t)p * hd + i + l]), sv[l]);
@@ -809,17 +813,20 @@ void g4o_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, 
       }
       float den = 0.f;
       for (int p = lo[m]; p <= pos[m]; ++p) {
+        if (!MH_VALID(p)) continue;
         sc[p - lo[m]] = expf(sc[p - lo[m]] - mx);
         den += sc[p - lo[m]];
       }
       float* oo = out + (size_t)m * ldo + (size_t)h * hd;
       for (int i = 0; i < hd; ++i) oo[i] = 0.f;
       for (int p = lo[m]; p <= pos[m]; ++p) {
+        if (!MH_VALID(p)) continue;
         const float wgt = sc[p - lo[m]] / den;
         for (int i = 0; i < hd; ++i) oo[i] = fmaf(wgt, g4o_bf2f(Vc[(size_t)p * hd + i]), oo[i]);
       }
       for (int i = 0; i < hd; ++i) oo[i] = g4o_r16(oo[i]);
     }
+#undef MH_VALID
     free(sc);
   }
 }

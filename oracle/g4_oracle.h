@@ -120,8 +120,9 @@ void g4o_attn_splitkv(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, in
  * rows [M] at pos[m] attend [lo[m], pos[m]] ---- */
 void g4o_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
                    const int* pos, const int* lo, float* out, int ldo);
+/* skip_lo / skip_hi (optional): row m ignores positions skip_lo[m] .. skip_hi[m] (the sibling row) */
 void g4o_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
-                 const int* pos, const int* lo, float* out, int ldo);
+                 const int* pos, const int* lo, const int* skip_lo, const int* skip_hi, float* out, int ldo);
 
 /* ---- synthetic decoder stack + verify step (engine/gemma4_engine.cpp:1256-1502, 1617-1661) ---- */
 typedef struct g4o_model g4o_model;
@@ -145,6 +146,8 @@ typedef struct {
  * rows are at positions pos0.. ; fills out and commits (KV compaction for branch b). */
 void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
                 g4o_verify_out* out, float* hidden_out);
+void g4o_verify_ex(g4o_model* m, const int* toks, int na, int nb, int pos0, int T, int allow_b,
+                   g4o_verify_out* out, float* hidden_out);
 
 /* prefill (E:1594-1599, ENGINE_PREFILL_INT8=1): toks[0..n) at pos0.. in blocks of pfb rows;
  * fills the KV cache; hlast (optional) receives the final-normed hidden row of the last token */

@@ -321,7 +321,8 @@ static void forward_ex(g4o_model* m, const int* toks, const rows_t* r, int T, fl
     const uint16_t* KCl = m->KC + (size_t)l * m->ctx * HD;
     const uint16_t* VCl = m->VC + (size_t)l * m->ctx * HD;
     if (amode == ATT_TILE) g4o_attn_tile(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, att, NQ * HD); /* E:1335 */
-    else if (amode == ATT_MH) g4o_attn_mh(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, att, NQ * HD); /* E:1350 */
+    else if (amode == ATT_MH) /* E:1337-1354, the sibling row's valid(p) (E:1345) as its skip range */
+      g4o_attn_mh(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, r->skip_lo, r->skip_hi, att, NQ * HD);
     else
       g4o_attn_splitkv(KCl, VCl, HD, NQ, M, q, NQ * HD, pos, lo, r->skip_lo, r->skip_hi, kmin, kmax, T, att,
                        NQ * HD, NULL, NULL);
@@ -368,12 +369,14 @@ static void forward_ex(g4o_model* m, const int* toks, const rows_t* r, int T, fl
 
 /* the attention path of a decode pass of M rows at pos0 (E:1305, 1328, 1337 with SPLITKV, TILED,
  * ATT_PAR = 192): split-KV when M <= 4 and pos0 + M > 192, else attn_tile when M >= 4 and
- * pos0 + M > 64 and the pass has no branch rows, else run_mh.  Passes with branch rows (the
- * two-branch tree, a generalisation of the engine's single sibling row) keep the split-KV path
- * for every size. */
+ * pos0 + M > 64 and the pass has no sibling row, else run_mh.  A pass with one branch row and
+ * at most 4 rows is the engine's sibling form (the branch row is `sibling`) and follows that
+ * rule; larger trees (two branches of several rows, a generalisation the engine does not form)
+ * keep the split-KV path for every size. */
 static int pass_amode(int M, int pos0, int nb) {
-  if (nb > 0 || (M <= 4 && pos0 + M > 192)) return ATT_SPLIT;
-  return (M >= 4 && pos0 + M > 64) ? ATT_TILE : ATT_MH;
+  if (nb > 1 || (nb == 1 && M > 4)) return ATT_SPLIT;
+  if (M <= 4 && pos0 + M > 192) return ATT_SPLIT;
+  return (nb == 0 && M >= 4 && pos0 + M > 64) ? ATT_TILE : ATT_MH;
 }
 
 static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf, int nb) {
@@ -447,6 +450,14 @@ int g4o_model_head(g4o_model* m, const float* h, const int* toks, int nt) {
  * was accepted.  Branch b commits by copying its KV slots into place (E:1651). */
 void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
                 g4o_verify_out* out, float* hidden_out) {
+  g4o_verify_ex(m, toks, na, nb, pos0, T, 1, out, hidden_out);
+}
+
+/* allow_b = 0: branch b is never walked -- the engine's sibling row when its tree hit is not
+ * taken (E:1650: neither TREE nor P + 1 + sibling <= ATT_PAR with gap1 >= 0.25), so acceptance
+ * follows the chain alone (E:1656) */
+void g4o_verify_ex(g4o_model* m, const int* toks, int na, int nb, int pos0, int T, int allow_b,
+                   g4o_verify_out* out, float* hidden_out) {
   rows_t r;
   rows_tree(&r, pos0, na, nb);
   const int M = r.M;
@@ -462,7 +473,7 @@ void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
     first = 1;
     len = na;
     br = 0;
-  } else if (nb >= 1 && out->G[0] == toks[na + 1]) {
+  } else if (allow_b && nb >= 1 && out->G[0] == toks[na + 1]) {
     first = na + 1;
     len = nb;
     br = 1;

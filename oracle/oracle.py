@@ -71,6 +71,7 @@ class Oracle:
             "g4o_model_bytes": (_i, [_vp, C.c_char_p, _vp, _i64]),
             "g4o_model_ptr": (_vp, [_vp, C.c_char_p]),
             "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
+            "g4o_verify_ex": (None, [_vp, _i32p, _i, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
             "g4o_prefill": (None, [_vp, _i32p, _i, _i, _i, _i, _vp]),
             "g4o_model_head": (_i, [_vp, _f32p, _i32p, _i]),
@@ -79,7 +80,8 @@ class Oracle:
             "g4o_b16_gemv": (None, [_u16p, _i, _i, _f32p, _f32p]),
             "g4o_draft_step": (_i, [_vp, _vp, _i, _f32p, _i, _i, _i, _f32p, C.POINTER(_i), C.POINTER(_f)]),
             "g4o_attn_tile": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _f32p, _i]),
-            "g4o_attn_mh": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, _f32p, _i]),
+            "g4o_attn_mh": (None, [_u16p, _u16p, _i, _i, _i, _f32p, _i, _i32p, _i32p, C.c_void_p, C.c_void_p, _f32p,
+                                   _i]),
             "g4o_stream": (_u64, [_u64, _u64]),
             "g4o_gen_normal_f32": (None, [_u64, _i64, _f, _f32p]),
             "g4o_gen_normal_bf16": (None, [_u64, _i64, _f, _u16p]),
@@ -211,13 +213,20 @@ class Oracle:
         n = min(info.nsurv, cap)
         return info, surv[:n].copy(), sval[:n].copy()
 
-    def attn_rows(self, kind, Kc, Vc, q, pos, lo):
-        """prefill attention of rows q [M][2048] at pos[m] over [lo[m], pos[m]]: kind 'tile' or 'mh'"""
+    def attn_rows(self, kind, Kc, Vc, q, pos, lo, skip=None):
+        """prefill attention of rows q [M][2048] at pos[m] over [lo[m], pos[m]]: kind 'tile' or 'mh';
+        skip (mh only): (skip_lo, skip_hi) per row, positions the row ignores"""
         q = _c(q, np.float32)
         M = q.shape[0]
         out = np.empty((M, 2048), np.float32)
-        fn = self.L.g4o_attn_tile if kind == "tile" else self.L.g4o_attn_mh
-        fn(_c(Kc, np.uint16), _c(Vc, np.uint16), 256, 8, M, q, 2048, _c(pos, np.int32), _c(lo, np.int32), out, 2048)
+        args = (_c(Kc, np.uint16), _c(Vc, np.uint16), 256, 8, M, q, 2048, _c(pos, np.int32), _c(lo, np.int32))
+        if kind == "tile":
+            self.L.g4o_attn_tile(*args, out, 2048)
+        else:
+            sl = None if skip is None else _c(skip[0], np.int32)
+            sh = None if skip is None else _c(skip[1], np.int32)
+            self.L.g4o_attn_mh(*args, None if sl is None else sl.ctypes.data, None if sh is None else sh.ctypes.data,
+                               out, 2048)
         return out
 
     def attn(self, Kc, Vc, hd, nh, q, pos, lo, skip_lo, skip_hi, kmin, kmax, T, parts=False):
@@ -271,10 +280,13 @@ class Model:
         sd = np.asarray(list(seeds)[:8] or [0], np.int32)
         return self.o.L.g4o_model_head(self.h, _c(h, np.float32), sd, len(list(seeds)[:8]))
 
-    def verify(self, toks, na, nb, pos0, T=8):
+    def verify(self, toks, na, nb, pos0, T=8, allow_b=True):
+        """one verify pass (tree of na chain rows and nb branch rows); allow_b False: branch b is
+        never committed (the engine's sibling row when the tree hit is not taken)"""
         out = VerifyOut()
         hid = np.empty(1536, np.float32)
-        self.o.L.g4o_verify(self.h, _c(toks, np.int32), na, nb, pos0, T, C.byref(out), hid.ctypes.data)
+        self.o.L.g4o_verify_ex(self.h, _c(toks, np.int32), na, nb, pos0, T, 1 if allow_b else 0, C.byref(out),
+                               hid.ctypes.data)
         return out, hid
 
 
@@ -357,6 +369,7 @@ class Ref:
             "ref_head": (None, [_f32p, _i, _f32p]),
             "ref_head_setup": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
             "ref_verify": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, C.POINTER(RefOut)]),
+            "ref_verify_ex": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _i, C.POINTER(RefOut)]),
             "ref_attn_tile": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_attn_mh": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_prefill": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _vp]),
@@ -436,9 +449,10 @@ class Ref:
             raise ValueError("ref_prefill: pfb must be 1..32")
         return hid
 
-    def verify(self, toks, na, nb, pos0):
+    def verify(self, toks, na, nb, pos0, allow_b=True):
         out = RefOut()
-        rc = self.L.ref_verify(C.byref(self.model), _c(toks, np.int32), na, nb, pos0, C.byref(out))
+        rc = self.L.ref_verify_ex(C.byref(self.model), _c(toks, np.int32), na, nb, pos0, 1 if allow_b else 0,
+                                  C.byref(out))
         if rc != 0:
             raise RuntimeError("ref_verify needs V = 262144 and at most 8 rows")
         return out

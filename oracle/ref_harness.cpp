@@ -299,7 +299,7 @@ void ref_head_setup(const uint8_t* Wq, const uint16_t* Sq, const float* coef, co
 
 // E:1408-1500 head_group over rows [hf, Mend) of hbuf; G receives the greedy tokens
 static void head_group_ref(float (*hbuf)[1536], const int* toks, int M, int hf, int Mend, int chain_lazy, int* G,
-                           int* fb, int* ns) {
+                           int* fb, int* ns, int sibling = -1) {
   const int H = 1536, Mh = Mend - hf;
   auto cap = [](float s) { return r16(30.0f * tanhf(s / 30.0f)); };
   static ScrArg* SA = new ScrArg();
@@ -379,16 +379,20 @@ static void head_group_ref(float (*hbuf)[1536], const int* toks, int M, int hf, 
     return true;
   };
   bool ok = true;
-  if (chain_lazy && Mh > 1) {  // E:1475-1484 (chain rows only)
+  if (chain_lazy && Mh > 1) {  // E:1475-1484: the chain rows, or the sibling row when it holds G[0]
     if (!eval_row(0)) ok = false;
-    else
-      for (int m = 1; m < Mh; ++m) {
+    else if (sibling > 0 && G[0] != toks[1] && G[0] == toks[sibling]) {
+      if (!eval_row(sibling)) ok = false;
+    } else {
+      const int chain_end = sibling > 0 ? sibling : Mh;
+      for (int m = 1; m < chain_end; ++m) {
         if (G[hf + m - 1] != toks[hf + m]) break;
         if (!eval_row(m)) {
           ok = false;
           break;
         }
       }
+    }
   } else {
     for (int m = 0; m < Mh; ++m)
       if (!eval_row(m)) {
@@ -432,18 +436,21 @@ void ref_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int sliding, const fl
   for (int t = 0; t < (M + QB - 1) / QB; ++t) attn_tile(Kc, Vc, 256, sliding != 0, q, 2048, pos0, M, att, t, 0);
 }
 
-// run_mh (E:1338-1349, no sibling row) on already normed and rotated q, as the lambda does it
+// run_mh (E:1338-1349) on already normed and rotated q, as the lambda does it; sibling >= 0: that
+// row's window starts from position pos0 + 1 and it skips the rows between row 0 and itself (E:1345)
 static void run_mh_rows(const uint16_t* Kc, const uint16_t* Vc, int sliding, const float* q, int pos0, int M,
-                        float* att) {
+                        float* att, int sibling = -1) {
   const int hd = 256;
   std::vector<float> scv((size_t)pos0 + M + 8);
   float* sc = scv.data();
   for (int mh = 0; mh < M * 8; ++mh) {
-    const int m = mh / 8, h = mh % 8, cachepos = pos0 + m, pos = cachepos;
+    const int m = mh / 8, h = mh % 8, cachepos = pos0 + m, pos = m == sibling ? pos0 + 1 : cachepos;
     const float* qh = q + (size_t)m * 2048 + h * hd;
     const int lo = sliding ? std::max(0, pos - 511) : 0;
+    auto valid = [&](int p) { return m != sibling || p <= pos0 || p == cachepos; };
     float mx = -1e30f;
     for (int p = lo; p <= cachepos; ++p) {
+      if (!valid(p)) continue;
       __m256 sv = _mm256_setzero_ps();
       const uint16_t* kp = Kc + (size_t)p * hd;
       for (int i = 0; i < hd; i += 8) sv = _mm256_fmadd_ps(_mm256_loadu_ps(qh + i), bf8(kp + i), sv);
@@ -453,12 +460,14 @@ static void run_mh_rows(const uint16_t* Kc, const uint16_t* Vc, int sliding, con
     }
     float den = 0;
     for (int p = lo; p <= cachepos; ++p) {
+      if (!valid(p)) continue;
       sc[p] = expf(sc[p] - mx);
       den += sc[p];
     }
     float* oh = att + (size_t)m * 8 * hd + h * hd;
     for (int i = 0; i < hd; ++i) oh[i] = 0;
     for (int p = lo; p <= cachepos; ++p) {
+      if (!valid(p)) continue;
       float wgt = sc[p] / den;
       const uint16_t* vp = Vc + (size_t)p * hd;
       for (int i = 0; i < hd; i += 8)
@@ -789,7 +798,12 @@ int ref_draft_step(RefModel* md, const RefDrafter* d, int tok, const float* h, i
   return bestc;
 }
 
+int ref_verify_ex(RefModel* md, const int* toks, int na, int nb, int pos0, int allow_b, RefOut* out);
 int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* out) {
+  return ref_verify_ex(md, toks, na, nb, pos0, 1, out);
+}
+// allow_b = 0: branch b is never committed (E:1650 when the sibling's tree hit is not taken)
+int ref_verify_ex(RefModel* md, const int* toks, int na, int nb, int pos0, int allow_b, RefOut* out) {
   const int H = 1536, M = 1 + na + nb, NL = md->NL, I = md->I;
   if (M > 8 || md->V != 262144) return -1;
   const int T = POOL.active_count();
@@ -862,11 +876,13 @@ int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* 
       lo[m] = A.sliding ? std::max(0, rope[m] - 511) : 0;
       kmin = std::min(kmin, lo[m]);
     }
-    // E:1305 / 1328 / 1337 (SPLITKV, TILED, ATT_PAR = 192) for a chain pass; passes with branch
-    // rows keep the split path (the generalised tree)
-    const bool split = nb > 0 || (M <= 4 && pos0 + M > 192);
-    if (!split && M >= 4 && pos0 + M > 64) ref_attn_tile(KCl, VCl, A.sliding, &q[0][0], pos0, M, &att[0][0]);
-    else if (!split) run_mh_rows(KCl, VCl, A.sliding, &q[0][0], pos0, M, &att[0][0]);
+    // E:1305 / 1328 / 1337 (SPLITKV, TILED, ATT_PAR = 192): a chain pass, or the engine's sibling
+    // form (one branch row, at most 4 rows; no attn_tile with a sibling); larger trees (the
+    // generalisation the engine does not form) keep the split path
+    const int sibling = (nb == 1 && M <= 4) ? na + 1 : -1;
+    const bool split = nb > 1 || (nb == 1 && M > 4) || (M <= 4 && pos0 + M > 192);
+    if (!split && nb == 0 && M >= 4 && pos0 + M > 64) ref_attn_tile(KCl, VCl, A.sliding, &q[0][0], pos0, M, &att[0][0]);
+    else if (!split) run_mh_rows(KCl, VCl, A.sliding, &q[0][0], pos0, M, &att[0][0], sibling);
     for (int g0 = 0; split && g0 < M; g0 += 4) {  // AttnArg holds 4 rows: same geometry, rows in groups
       AttnArg aa;
       aa.Kc = KCl;
@@ -924,14 +940,15 @@ int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* 
   }
   int G[8], fb[8], ns[8];
   for (int r = 0; r < 8; ++r) G[r] = -1, fb[r] = 0, ns[r] = 0;
-  for (int r0 = 0; r0 < M; r0 += 4) head_group_ref(hbuf, toks, M, r0, std::min(M, r0 + 4), r0 == 0, G, fb, ns);
+  const int sib = (nb == 1 && M <= 4) ? na + 1 : -1;
+  for (int r0 = 0; r0 < M; r0 += 4) head_group_ref(hbuf, toks, M, r0, std::min(M, r0 + 4), r0 == 0, G, fb, ns, sib);
   // E:1647-1661 along the branch chosen by G[0]
   int path[8], np = 1, first = 0, len = 0, br = 0;
   path[0] = 0;
   if (na >= 1 && G[0] == toks[1]) {
     first = 1;
     len = na;
-  } else if (nb >= 1 && G[0] == toks[na + 1]) {
+  } else if (allow_b && nb >= 1 && G[0] == toks[na + 1]) {
     first = na + 1;
     len = nb;
     br = 1;

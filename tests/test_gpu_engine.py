@@ -1,7 +1,8 @@
 """The engine front-end (gemma4-e2b-laptop-cpu_amd/g4v_engine): the reference engine's line
 protocol (E:1681-1689) over the library, driven as the reference's server drives it.  Every
-request's FIRST / TOK / GEN lines are checked against run_req (E:1584-1679, sibling row off)
-restated over the oracle: prefix reuse, prefill, prompt-lookup or MTP drafts, chain verify."""
+request's FIRST / TOK / GEN lines are checked against run_req (E:1584-1679) restated over the
+oracle: prefix reuse, prefill, prompt-lookup or MTP drafts, the sibling row (ENGINE_SIB_GAP 1,
+and the tree mode of BENCH_MODE k 1), chain or sibling verify."""
 import os
 import subprocess
 
@@ -36,7 +37,7 @@ class OracleEngine:
         self.d.close()
         self.m.close()
 
-    def run_req(self, prompt, nnew):
+    def run_req(self, prompt, nnew, k_draft=3, tree=False):
         n = len(prompt)
         common = 0
         while common < self.kv_len and common < n and self.keys[common] == prompt[common]:
@@ -44,18 +45,51 @@ class OracleEngine:
         start = min(common, n - 1)
         h = self.m.prefill(np.array(prompt[start:], np.int32), pos0=start, T=T)
         g0 = self.m.head(h, prompt[start:][-8:])
-        gen, P, stopped, toks_out = [g0], n - 1, is_stop(g0), []
-        hprev = h
+        gen, P, stopped = [g0], n - 1, is_stop(g0)
+        hprev, state, rounds, self.sib_rounds, self.hits = h, 1, 0, 0, 0
         while len(gen) < nnew and not stopped:
+            k = min(k_draft, 3)
+            if tree:
+                k = min(k, 2)
             seq = np.array(prompt + gen, np.int32)
             drafts = self.orc.prompt_lookup(seq, 3, 3).tolist()
-            if not drafts:
+            used_ng, sec1, gap1, use_sib = bool(drafts), -1, -1.0, False
+            if not used_ng:  # E:1632-1645
                 tok, hh = gen[-1], hprev
-                for j in range(3):
-                    tok, hh, _, _ = self.d.step(self.m, tok, hh, P + 1 + j, P, T)
+                for j in range(k):
+                    tok, hh, sec, gap = self.d.step(self.m, tok, hh, P + 1 + j, P, T)
+                    if j == 0:
+                        sec1, gap1 = sec, gap
+                        allow = rounds >= 1 and state < 2 and k >= 2 and sec1 >= 0 and sec1 != tok
+                        if P + 1 + k > 192:
+                            cond = False  # ENGINE_SIB_LONG unset
+                        else:
+                            cond = gap1 <= (2.55 if (rounds <= 3 or state == 1) else 1.80)
+                        if allow and cond:
+                            drafts.append(tok)
+                            use_sib = True
+                            break
                     drafts.append(tok)
-            block = np.array([gen[-1]] + drafts, np.int32)
-            o, hprev = self.m.verify(block, len(drafts), 0, P + 1, T)
+            nd = len(drafts)
+            sib = nd + 1 if ((tree or use_sib) and not used_ng and nd >= 1 and sec1 >= 0 and sec1 != drafts[0]) else -1
+            block = np.array([gen[-1]] + drafts + ([sec1] if sib > 0 else []), np.int32)
+            if sib > 0:
+                self.sib_rounds += 1
+                allow_hit = tree or (P + 1 + sib <= 192 and gap1 >= 0.25)
+                o, hprev = self.m.verify(block, nd, 1, P + 1, T, allow_b=allow_hit)
+            else:
+                o, hprev = self.m.verify(block, nd, 0, P + 1, T)
+            rounds += 1
+            if o.branch == 1:  # E:1650-1653
+                self.hits += 1
+                gen.append(o.commit[0])
+                if not is_stop(o.commit[0]) and len(gen) < nnew:
+                    gen.append(o.commit[1])
+                stopped = is_stop(gen[-1])
+                P += 2
+                state = 1
+                continue
+            state = 0 if o.nacc == 0 else (2 if (not use_sib and o.nacc == nd) else 1)
             for i in range(o.nacc + 1):
                 gen.append(o.commit[i])
                 if is_stop(o.commit[i]):
@@ -80,10 +114,17 @@ def test_engine_protocol_matches_oracle(orc):
     motif = rng.integers(0, V, 16).tolist()
     a = (motif * 8)[:100]
     b = rng.integers(0, V, 40).tolist()
-    requests = [(a, 20), (b, 10), (a, 15), (a + [5, 6, 7], 8)]
-    note("engine protocol: 4 requests over a 15-layer synthetic stack")
+    c = rng.integers(0, V, 30).tolist()
+    # (prompt, nnew, k_draft, tree): the last two after "BENCH_MODE 2 1" (the tree mode)
+    requests = [(a, 20, 3, False), (b, 10, 3, False), (a, 15, 3, False), (a + [5, 6, 7], 8, 3, False),
+                (c, 24, 3, False), (b + [9], 16, 2, True), (c + [4], 12, 2, True)]
+    note("engine protocol: 7 requests over a 15-layer synthetic stack")
     env = dict(os.environ, **ENV)
-    lines = "".join(f"{nn} {' '.join(map(str, p))}\n" for p, nn in requests)
+    lines = ""
+    for i, (p, nn, _, _) in enumerate(requests):
+        if i == 5:
+            lines += "BENCH_MODE 2 1\n"
+        lines += f"{nn} {' '.join(map(str, p))}\n"
     proc = subprocess.run([exe, f"synth:{SEED}:{V}:{NL}:{I}", "-", "-", "0"], input=lines, env=env,
                           capture_output=True, text=True, timeout=240)
     assert proc.returncode == 0, proc.stderr[-2000:]
@@ -91,8 +132,15 @@ def test_engine_protocol_matches_oracle(orc):
     oe = OracleEngine(orc)
     try:
         it = iter(out)
-        for k, (prompt, nn) in enumerate(requests):
-            g0, gen, start = oe.run_req(prompt, nn)
+        sib_rounds = hits = 0
+        per_req = []
+        for k, (prompt, nn, kd, tree) in enumerate(requests):
+            if k == 5:
+                assert next(it) == "MODE k=2 tree=1"
+            g0, gen, start = oe.run_req(prompt, nn, kd, tree)
+            sib_rounds += oe.sib_rounds
+            hits += oe.hits
+            per_req.append((oe.sib_rounds, oe.hits))
             first = next(it)
             assert first == f"FIRST {g0}", (k, first, g0)
             streamed = []
@@ -106,5 +154,12 @@ def test_engine_protocol_matches_oracle(orc):
             assert [g0] + streamed == gen, (k, streamed)
             timing = next(it)
             assert timing.startswith("TIMING") and f"reused={start} " in timing, (k, timing)
+        # E:1673 per request: the sibling rows proposed (TREE attempts) and committed (hits)
+        rank1 = [ln for ln in proc.stderr.splitlines() if ln.startswith("RANK1")]
+        assert len(rank1) == len(requests), proc.stderr[-1000:]
+        for k, ln in enumerate(rank1):
+            assert f"TREE attempts={per_req[k][0]} hits={per_req[k][1]}" in ln, (k, ln, per_req[k])
+        note(f"sibling rounds {sib_rounds}, tree hits {hits}")
+        assert sib_rounds > 0
     finally:
         oe.close()

@@ -141,3 +141,41 @@ def test_chain_pass_attention_paths(orc, g4v, na, pos0):
     finally:
         om.close()
         dev.close()
+
+
+@pytest.mark.parametrize("nd,pos0,allow", [(1, 100, True), (2, 150, True), (1, 190, True), (1, 100, False),
+                                           (2, 40, True)])
+def test_sibling_pass_paths(orc, g4v, nd, pos0, allow):
+    """the engine's sibling form (E:1634-1655): run_mh with the sibling's RoPE position and skip
+    range below ATT_PAR (no attn_tile even for 4 rows), split-KV past it; the tree hit commits the
+    sibling and moves its KV row, and with the hit not allowed only the chain is accepted"""
+    from oracle import Model
+    note(f"sibling pass nd={nd} pos0={pos0} allow={allow}")
+    dev = g4v.Device(0)
+    om = Model(orc, 23, 8192, 3, 6144, 1024)
+    try:
+        dev.model_synth(23, 8192, 3, 6144, 1024)
+        dev.fake_ctx(700, 4242)
+        om.fake_ctx(700, 4242)
+        toks = np.array([19 + 37 * k for k in range(nd + 2)], np.int32)
+        o, _ = om.verify(toks, nd, 1, pos0, 8, allow_b=False)  # row 0's token on the same attention path
+        toks[nd + 1] = o.G[0]  # the runner-up draft holds row 0's greedy token
+        if toks[1] == o.G[0]:
+            toks[1] += 1
+        for hit_expected in (True, False):
+            if not hit_expected:
+                toks[nd + 1] = (o.G[0] + 5) % 8192
+            dev.fake_ctx(700, 4242)
+            om.fake_ctx(700, 4242)
+            r, hg = dev.verify_sibling(toks, nd, pos0, 8, allow_hit=allow, hidden=True)
+            oo, ho = om.verify(toks, nd, 1, pos0, 8, allow_b=allow)
+            assert (r.nacc, r.branch, r.ncommit) == (oo.nacc, oo.branch, oo.ncommit), (hit_expected, r.as_dict())
+            assert r.ncommit == (2 if (allow and hit_expected) else 1)
+            assert list(r.commit[:r.ncommit]) == list(oo.commit[:oo.ncommit])
+            assert same(hg, ho), first_diff(hg, ho)
+            kc, kco = dev.read("KC", np.uint16), om.get("KC", np.uint16, 3 * 1024 * 256)
+            vc, vco = dev.read("VC", np.uint16), om.get("VC", np.uint16, 3 * 1024 * 256)
+            assert same(kc, kco) and same(vc, vco)
+    finally:
+        om.close()
+        dev.close()

@@ -41,3 +41,33 @@ def test_chain_pass_paths(orc, ref, pair, na, pos0):
     for what in ("KC", "VC"):
         a, b = om.get(what, np.uint16, NL * CTX * 256), rm.get(what, np.uint16, NL * CTX * 256)
         assert same(a, b), (what, first_diff(a, b))
+
+
+# the engine's sibling form (E:1634-1655): drafts toks[1..na], sibling row toks[na + 1] at RoPE
+# position pos0 + 1.  (na, pos0, allow_b): 3 rows, run_mh; 4 rows below ATT_PAR, run_mh (no
+# attn_tile with a sibling); 3 rows past ATT_PAR, split-KV; the tree hit not taken
+SIB_CASES = [(1, 100, True), (2, 150, True), (1, 190, True), (1, 100, False)]
+
+
+@pytest.mark.parametrize("na,pos0,allow_b", SIB_CASES)
+def test_sibling_pass_paths(orc, ref, pair, na, pos0, allow_b):
+    om, rm = pair
+    om.fake_ctx(NFAKE, 3)
+    toks = np.array([23 + 31 * k for k in range(na + 2)], np.int32)
+    o, _ = om.verify(toks, na, 1, pos0, allow_b=False)  # row 0's token on the same attention path
+    toks[na + 1] = o.G[0]  # the sibling holds row 0's greedy token: the tree hit
+    if toks[1] == o.G[0]:
+        toks[1] += 1
+    om.fake_ctx(NFAKE, 3)
+    rm.fake_ctx(NFAKE, 3)
+    o, _ = om.verify(toks, na, 1, pos0, allow_b=allow_b)
+    r = ref.verify(toks, na, 1, pos0, allow_b=allow_b)
+    assert o.ncommit == (2 if allow_b else 1) and o.branch == (1 if allow_b else 0)
+    assert (o.nacc, o.ncommit, o.branch) == (r.nacc, r.ncommit, r.branch)
+    assert list(o.commit[:o.ncommit]) == list(r.commit[:r.ncommit])
+    for i in range(na + 2):
+        if o.G[i] >= 0:
+            assert o.G[i] == r.G[i], (i, list(o.G), list(r.G))
+    for what in ("KC", "VC"):
+        a, b = om.get(what, np.uint16, NL * CTX * 256), rm.get(what, np.uint16, NL * CTX * 256)
+        assert same(a, b), (what, first_diff(a, b))
