@@ -179,3 +179,24 @@ def test_sibling_pass_paths(orc, g4v, nd, pos0, allow):
     finally:
         om.close()
         dev.close()
+
+
+def test_verify_argument_errors(g4v):
+    """shapes the verify entry points do not serve fail on the host with an error, before any
+    launch, and leave the context usable"""
+    dev = g4v.Device(0)
+    try:
+        dev.model_synth(23, 8192, 3, 6144, 1024)
+        dev.fake_ctx(700, 4242)
+        toks = np.array([5, 6, 7, 8, 9], np.int32)
+        for nd in (0, 3):  # the sibling form holds 1 or 2 drafts
+            with pytest.raises(RuntimeError):
+                dev.verify_sibling(toks, nd, 100, 8)
+        with pytest.raises(RuntimeError):  # branch b without a chain
+            dev.verify(toks[:2], 0, 1, 100, 8)
+        with pytest.raises(RuntimeError):  # past the cache
+            dev.verify(toks[:4], 3, 0, 1022, 8)
+        r = dev.verify_sibling(toks[:3], 1, 100, 8)
+        assert r.ncommit >= 1
+    finally:
+        dev.close()
