@@ -8,20 +8,32 @@
 //                       GEN: <ids> and a TIMING line (E:1604, 1612-1614, 1672-1679)
 //     "BENCH_MODE k tree" -> MODE k=.. tree=.. / MODE_ERROR (E:1683)
 //
-// <model> names the synthetic stack "synth:SEED:V:NL:I" (the library has no checkpoint loader
-// yet); <index> is ignored.  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
+// <model> is a checkpoint directory holding model.safetensors and <index> its tensor index (one
+// line per tensor: name, dtype, byte offset in the file, byte count, shape; E:1218-1222), or
+// "synth:SEED:V:NL:I" for the synthetic stack (<index> ignored).  A checkpoint is read for the
+// stack the library runs: every layer with its own q/k/v projections of 8 x 256 / 256 / 256
+// rows, a uniform MLP width and no per-layer-embedding tensors; the Gemma-4-E2B layout
+// (hd-512 global layers, KV-shared layers 15-34, PLE) is refused with a message.  The MTP
+// drafter is the synthetic one (ENGINE_DRAFTER_SEED; with a checkpoint only when set).  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
 // (g4v_slot_*), the prefill (g4v_prefill), and decode rounds whose drafts come from prompt
 // lookup (ENGINE_NGRAM / ENGINE_NGLEN) or, when it finds none, the MTP drafter (ENGINE_K, a
 // synthetic drafter, seed ENGINE_DRAFTER_SEED), verified as a chain (g4v_verify_step) or, when
 // the drafter's runner-up is proposed as a sibling row (E:1634-1655: ENGINE_SIB_GAP,
 // ENGINE_SIB_LONG, ENGINE_TREE / BENCH_MODE k 1, ENGINE_POLICY), with g4v_verify_sibling.
 // Prompt-lookup drafts of a round are capped at 4 (the verify step's chain).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <chrono>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <iostream>
+#include <map>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -48,6 +60,127 @@ int env_int(const char* name, int dflt) {
 bool is_stop(int t) { return t == 106 || t == 1; }  // E:1609
 
 constexpr int ATT_PAR = 192;  // E:1214
+
+// ---- checkpoint (E:147-175, 1218-1231) ----
+struct Tensor {
+  std::string dtype;
+  size_t off = 0, nbytes = 0;
+  std::vector<long long> shape;
+};
+
+struct Checkpoint {
+  std::map<std::string, Tensor> idx;
+  const uint8_t* base = nullptr;
+  size_t size = 0;
+
+  [[noreturn]] static void fail(const std::string& m) {
+    fprintf(stderr, "checkpoint: %s\n", m.c_str());
+    exit(2);
+  }
+  void open_files(const std::string& dir, const std::string& index) {
+    std::ifstream f(index);
+    if (!f) fail("cannot read index " + index);
+    std::string line;
+    while (std::getline(f, line)) {  // name \t dtype \t offset \t nbytes \t shape (comma separated)
+      std::stringstream ss(line);
+      std::string n, d, o, b, sh;
+      if (!std::getline(ss, n, '\t') || !std::getline(ss, d, '\t') || !std::getline(ss, o, '\t') ||
+          !std::getline(ss, b, '\t'))
+        continue;
+      std::getline(ss, sh, '\t');
+      Tensor t;
+      t.dtype = d;
+      t.off = std::stoull(o);
+      t.nbytes = std::stoull(b);
+      std::stringstream s2(sh);
+      std::string x;
+      while (std::getline(s2, x, ',')) t.shape.push_back(std::stoll(x));
+      idx[n] = t;
+    }
+    const std::string path = dir + "/model.safetensors";
+    const int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) fail("cannot open " + path);
+    struct stat st;
+    fstat(fd, &st);
+    size = (size_t)st.st_size;
+    void* p = mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (p == MAP_FAILED) fail("cannot map " + path);
+    base = (const uint8_t*)p;
+  }
+  // E:170: the language model's prefix first
+  const Tensor* find(const std::string& n) const {
+    auto it = idx.find("model.language_model." + n);
+    if (it == idx.end()) it = idx.find(n);
+    return it == idx.end() ? nullptr : &it->second;
+  }
+  const Tensor& get(const std::string& n, const char* dtype, size_t nbytes) const {
+    const Tensor* t = find(n);
+    if (!t) fail("missing tensor " + n);
+    if (t->dtype != dtype) fail(n + ": dtype " + t->dtype + ", expected " + dtype);
+    if (t->nbytes != nbytes) fail(n + ": " + std::to_string(t->nbytes) + " bytes, expected " + std::to_string(nbytes));
+    if (t->off + t->nbytes > size) fail(n + ": beyond the end of the file");
+    return *t;
+  }
+  const uint8_t* data(const Tensor& t) const { return base + t.off; }
+  std::vector<float> vec(const std::string& n, size_t len) const {  // bf16 vector widened (E:172)
+    const Tensor& t = get(n, "BF16", len * 2);
+    std::vector<float> v(len);
+    const uint16_t* p = (const uint16_t*)data(t);
+    for (size_t i = 0; i < len; ++i) {
+      const uint32_t u = (uint32_t)p[i] << 16;
+      std::memcpy(&v[i], &u, 4);
+    }
+    return v;
+  }
+};
+
+// the stack of a checkpoint into the library (g4v_model_create + setters); returns V
+int load_checkpoint(const Checkpoint& ck, int ctx) {
+  const int H = 1536;
+  const Tensor* emb = ck.find("embed_tokens.weight");
+  if (!emb || emb->shape.size() != 2 || emb->shape[1] != H) Checkpoint::fail("embed_tokens.weight [V][1536] missing");
+  const int V = (int)emb->shape[0];
+  int NL = 0;
+  while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
+  if (NL == 0) Checkpoint::fail("no layers");
+  const Tensor* g0 = ck.find("layers.0.mlp.gate_proj.weight_packed");
+  if (!g0 || g0->shape.size() != 2) Checkpoint::fail("layers.0.mlp.gate_proj.weight_packed missing");
+  const int I = (int)g0->shape[0];
+  if (ck.find("per_layer_model_projection.weight_packed") || ck.find("embed_tokens_per_layer.weight"))
+    Checkpoint::fail("per-layer embeddings (the Gemma-4-E2B layout) are not run by this build yet");
+  check(g4v_model_create(G, V, NL, I, ctx), "model_create");
+  check(g4v_model_set_embed(G, (const uint16_t*)ck.data(ck.get("embed_tokens.weight", "BF16", (size_t)V * H * 2))),
+        "model_set_embed");
+  const char* names[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                          "mlp.gate_proj",    "mlp.up_proj",      "mlp.down_proj"};
+  const int Ns[7] = {2048, 256, 256, H, I, I, H}, Ks[7] = {H, H, H, 2048, H, H, I};
+  for (int l = 0; l < NL; ++l) {
+    const std::string p = "layers." + std::to_string(l) + ".";
+    if (!ck.find(p + "self_attn.k_proj.weight_packed"))
+      Checkpoint::fail(p + ": no k_proj (a KV-shared layer of the Gemma-4-E2B layout) is not run by this build yet");
+    for (int j = 0; j < 7; ++j) {  // E:175 int4 G32: [N][K/8] int32 words = [N][K/2] bytes, scales [N][K/32]
+      const std::string b = p + names[j];
+      const Tensor* w = ck.find(b + ".weight_packed");
+      if (w && w->shape.size() == 2 && (w->shape[0] != Ns[j] || w->shape[1] * 8 != Ks[j]))
+        Checkpoint::fail(b + ": shape " + std::to_string(w->shape[0]) + " x " + std::to_string(w->shape[1] * 8) +
+                         ", this build runs " + std::to_string(Ns[j]) + " x " + std::to_string(Ks[j]) +
+                         " (hd-512 global layers and double-wide MLPs come with the Gemma-4-E2B layout)");
+      const Tensor& wt = ck.get(b + ".weight_packed", "I32", (size_t)Ns[j] * Ks[j] / 2);
+      const Tensor& st = ck.get(b + ".weight_scale", "BF16", (size_t)Ns[j] * (Ks[j] / 32) * 2);
+      check(g4v_model_set_matrix(G, l, j, ck.data(wt), (const uint16_t*)ck.data(st)), "model_set_matrix");
+    }
+    const std::vector<float> nv[6] = {
+        ck.vec(p + "input_layernorm.weight", H),          ck.vec(p + "post_attention_layernorm.weight", H),
+        ck.vec(p + "pre_feedforward_layernorm.weight", H), ck.vec(p + "post_feedforward_layernorm.weight", H),
+        ck.vec(p + "self_attn.q_norm.weight", 256),        ck.vec(p + "self_attn.k_norm.weight", 256)};
+    const float* nvp[6] = {nv[0].data(), nv[1].data(), nv[2].data(), nv[3].data(), nv[4].data(), nv[5].data()};
+    const float scalar = ck.vec(p + "layer_scalar", 1)[0];
+    check(g4v_model_set_norms(G, l, nvp, scalar, l % 5 != 4), "model_set_norms");  // E:1225 sliding
+  }
+  check(g4v_model_set_final_norm(G, ck.vec("norm.weight", H).data()), "model_set_final_norm");
+  return V;
+}
 
 struct Engine {
   int V = 0, ctx = 4096, pfb = 32, T = 6, ng_n = 0, ng_len = 3, k_draft = 3;
@@ -236,15 +369,12 @@ struct Engine {
 
 int main(int argc, char** argv) {
   if (argc < 5) {
-    fprintf(stderr, "usage: %s synth:SEED:V:NL:I <index> <prompt.ids | -> <nnew>\n", argv[0]);
+    fprintf(stderr, "usage: %s <checkpoint dir | synth:SEED:V:NL:I> <index> <prompt.ids | -> <nnew>\n", argv[0]);
     return 2;
   }
   unsigned long long seed = 0;
   int V = 0, NL = 0, I = 0;
-  if (sscanf(argv[1], "synth:%llu:%d:%d:%d", &seed, &V, &NL, &I) != 4) {
-    fprintf(stderr, "model must be synth:SEED:V:NL:I (no checkpoint loader yet)\n");
-    return 2;
-  }
+  const bool synth = sscanf(argv[1], "synth:%llu:%d:%d:%d", &seed, &V, &NL, &I) == 4;
   Engine e;
   e.V = V;
   e.ctx = env_int("ENGINE_CTX", 4096);
@@ -266,9 +396,19 @@ int main(int argc, char** argv) {
     e.T = std::max(1, std::min(16, ncpu));
   }
   check(g4v_create(0, &G), "create");
-  check(g4v_model_synth(G, seed, V, NL, I, e.ctx), "model_synth");
-  if (e.k_draft > 0 && NL >= 15 && V % 2048 == 0) {
-    check(g4v_drafter_synth(G, (uint64_t)env_int("ENGINE_DRAFTER_SEED", (int)seed + 1)), "drafter_synth");
+  Checkpoint ck;
+  if (synth) {
+    check(g4v_model_synth(G, seed, V, NL, I, e.ctx), "model_synth");
+  } else {
+    ck.open_files(argv[1], argv[2]);
+    V = load_checkpoint(ck, e.ctx);
+    e.V = V;
+    NL = 0;
+    while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
+  }
+  const char* dseed = getenv("ENGINE_DRAFTER_SEED");
+  if (e.k_draft > 0 && NL >= 15 && V % 2048 == 0 && (synth || dseed)) {
+    check(g4v_drafter_synth(G, dseed ? strtoull(dseed, nullptr, 10) : seed + 1), "drafter_synth");
     e.drafter = true;
   }
   check(g4v_slots_init(G, std::max(1, env_int("ENGINE_SLOTS", 1)), env_int("ENGINE_SLOT_MIN_REUSE", 32)), "slots_init");

@@ -163,3 +163,79 @@ def test_engine_protocol_matches_oracle(orc):
         assert sib_rounds > 0
     finally:
         oe.close()
+
+
+def write_checkpoint(om, d, V, NL, I):
+    """the oracle's stack as a safetensors checkpoint with the engine's tensor index beside it
+    (name, dtype, absolute byte offset, byte count, shape: the format the engine reads, E:1218-1222)"""
+    import json
+    H = 1536
+    names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+             "mlp.up_proj", "mlp.down_proj"]
+    Ns, Ks = [2048, 256, 256, H, I, I, H], [H, H, H, 2048, H, H, I]
+    norms = ["input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm", "post_feedforward_layernorm",
+             "self_attn.q_norm", "self_attn.k_norm"]
+    bf = lambda f: (np.ascontiguousarray(f, np.float32).view(np.uint32) >> 16).astype(np.uint16)  # exact: bf16 values
+    tensors = [("embed_tokens.weight", "BF16", [V, H], om.get("E", np.uint16, V * H)),
+               ("norm.weight", "BF16", [H], bf(om.get("fnorm", np.float32, H)))]
+    for l in range(NL):
+        p = f"layers.{l}."
+        for j in range(7):
+            w = om.get(f"W{l}_{j}", np.uint8, Ns[j] * Ks[j] // 2)
+            s = om.get(f"S{l}_{j}", np.uint16, Ns[j] * Ks[j] // 32)
+            tensors.append((p + names[j] + ".weight_packed", "I32", [Ns[j], Ks[j] // 8], w))
+            tensors.append((p + names[j] + ".weight_scale", "BF16", [Ns[j], Ks[j] // 32], s))
+        for t, nm in enumerate(norms):
+            n = H if t < 4 else 256
+            tensors.append((p + nm + ".weight", "BF16", [n], bf(om.get(f"N{l}_{t}", np.float32, n))))
+        tensors.append((p + "layer_scalar", "BF16", [1], bf(np.array([0.75], np.float32))))
+    header, off = {}, 0
+    for name, dt, shape, arr in tensors:
+        header["model.language_model." + name] = {"dtype": dt, "shape": shape, "data_offsets": [off, off + arr.nbytes]}
+        off += arr.nbytes
+    hb = json.dumps(header).encode()
+    hb += b" " * (-len(hb) % 8)
+    with open(os.path.join(d, "model.safetensors"), "wb") as f:
+        f.write(np.uint64(len(hb)).tobytes())
+        f.write(hb)
+        for _, _, _, arr in tensors:
+            f.write(np.ascontiguousarray(arr).tobytes())
+    with open(os.path.join(d, "index.tsv"), "w") as f:
+        for name, v in header.items():
+            a, b = v["data_offsets"]
+            f.write(f"{name}\t{v['dtype']}\t{8 + len(hb) + a}\t{b - a}\t{','.join(map(str, v['shape']))}\n")
+
+
+def test_engine_loads_checkpoint(orc, tmp_path):
+    """the engine on a checkpoint of the synthetic stack (model.safetensors + tensor index)
+    answers exactly as on the stack generated in place: the loader maps every tensor"""
+    from oracle import Model
+    exe = os.path.join(PKG, "g4v_engine")
+    NLc = 15
+    om = Model(orc, SEED, V, NLc, I, CTX)
+    try:
+        write_checkpoint(om, str(tmp_path), V, NLc, I)
+    finally:
+        om.close()
+    rng = np.random.default_rng(9)
+    motif = rng.integers(0, V, 12).tolist()
+    requests = [((motif * 6)[:60], 16), (rng.integers(0, V, 25).tolist(), 12)]
+    lines = "".join(f"{nn} {' '.join(map(str, p))}\n" for p, nn in requests)
+    env = dict(os.environ, **ENV, ENGINE_DRAFTER_SEED=str(SEED + 1))
+    outs = []
+    for model, index in ((f"synth:{SEED}:{V}:{NLc}:{I}", "-"), (str(tmp_path), str(tmp_path / "index.tsv"))):
+        note(f"engine on {model}")
+        proc = subprocess.run([exe, model, index, "-", "0"], input=lines, env=env, capture_output=True, text=True,
+                              timeout=240)
+        assert proc.returncode == 0, proc.stderr[-2000:]
+        outs.append([ln for ln in proc.stdout.splitlines() if not ln.startswith("TIMING")])
+    assert outs[0] == outs[1]
+    assert sum(ln.startswith("GEN:") for ln in outs[1]) == len(requests)
+    # a layer without its own k/v projections (the KV-shared layers of Gemma-4-E2B) is refused
+    with open(tmp_path / "index.tsv") as f:
+        kept = [ln for ln in f if ".layers.1.self_attn.k_proj." not in ln]
+    with open(tmp_path / "shared.tsv", "w") as f:
+        f.writelines(kept)
+    proc = subprocess.run([exe, str(tmp_path), str(tmp_path / "shared.tsv"), "-", "0"], input=lines, env=env,
+                          capture_output=True, text=True, timeout=240)
+    assert proc.returncode == 2 and "KV-shared" in proc.stderr, (proc.returncode, proc.stderr[-500:])
