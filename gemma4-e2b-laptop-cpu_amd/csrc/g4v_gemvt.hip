@@ -87,12 +87,12 @@ struct GemvTDev {
 // LDS: activations [MPL][G][8 + 1] float4 (staged; a pad float4 after each group spreads the
 // per-group accesses of the prologue over the banks), group sums [MPL][G], chain sums [MPL][8][64],
 // offsets [MPL][64], outputs of the gate/up epilogue [MPL][64]; the norm prologue adds its two
-// weight rows [2][H], partial sums [MPL][16] (double) and RMS factors [2][MPL]
+// weight rows [2][H] and RMS factors [2][MPL]
 static size_t gemvt_lds(int mpl, int K, bool nrm, int tr, bool mrg) {
   const int G = K / 32;
   return (size_t)mpl * G * 9 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * tr * 4 + (size_t)mpl * tr * 4 * 2 +
          (mrg ? (size_t)mpl * NQ * (MAXT + 1) * 4 : 0) +
-         (nrm ? (size_t)2 * H * 4 + (size_t)mpl * 16 * 8 + (size_t)2 * mpl * 4 : 0);
+         (nrm ? (size_t)2 * H * 4 + (size_t)2 * mpl * 4 : 0);
 }
 
 // MRG: the merge prologue (GemvTArgs::mrg_po), NRM: the norm prologue (GemvTArgs::nrm_mode);
@@ -246,8 +246,7 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
     // permuted in place into the staged order, one thread per (row, group).
     constexpr int RW4 = H / 4, NV = (MPL * RW4 + NT - 1) / NT, NW = (RW4 + NT - 1) / NT;
     float* W12 = YL + MPL * TR;                                   // [2][H]
-    double* RED = reinterpret_cast<double*>(W12 + 2 * H);        // [MPL][16]
-    float* RR = reinterpret_cast<float*>(RED + MPL * 16);         // [2][MPL]
+    float* RR = W12 + 2 * H;                                      // [2][MPL]
     const float4* o4 = reinterpret_cast<const float4*>(a.nrm_o);
     const float4* x4 = reinterpret_cast<const float4*>(a.nrm_xin);
     float4 ov[NV], xv[NV];
@@ -305,16 +304,16 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
             sacc = fma(dv, dv, sacc);
           }
         }
-        RED[threadIdx.x] = sacc;
-      }
-      __syncthreads();
-      if ((int)threadIdx.x < MPL) {
-        const double* p = RED + threadIdx.x * 16;
+        // the row's 16 lanes meet through shuffles, in the reference's order (E:336-343)
+        const int base = threadIdx.x & ~15;
+        double p[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) p[l] = __shfl(sacc, base + l);
         double q4[4];
 #pragma unroll
         for (int l = 0; l < 4; ++l) q4[l] = (p[l] + p[4 + l]) + (p[8 + l] + p[12 + l]);
         const double ss = (q4[0] + q4[2]) + (q4[1] + q4[3]);
-        rinv[threadIdx.x] = 1.0f / sqrtf((float)(ss / H) + 1e-6f);
+        if ((threadIdx.x & 15) == 0) rinv[threadIdx.x >> 4] = 1.0f / sqrtf((float)(ss / H) + 1e-6f);
       }
       __syncthreads();
     };
