@@ -1032,12 +1032,34 @@ int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed) {
   return 0;
 }
 
+// copies a re-laid int4 matrix back in the reference's [N][K/2] byte layout: row n, chunk c,
+// lane j of the device layout holds bytes (j, 8+j) of groups 8c..8c+7
+static int read_relaid_w4(g4v_ctx* c, const void* wr, int N, int K, void* dst, size_t cap, size_t* nbytes) {
+  const size_t nb = (size_t)N * K / 2;
+  if (nbytes) *nbytes = nb;
+  if (!dst) return 0;
+  ARGCHK(cap >= nb, "model_read: buffer too small");
+  std::vector<uint8_t> tmp(nb);
+  HIPCHK(hipMemcpy(tmp.data(), wr, nb, hipMemcpyDeviceToHost));
+  uint8_t* out = static_cast<uint8_t*>(dst);
+  const int GC = K / 256;
+  for (size_t n = 0; n < (size_t)N; ++n)
+    for (int cc = 0; cc < GC; ++cc)
+      for (int jj = 0; jj < 8; ++jj)
+        for (int k = 0; k < 8; ++k) {
+          const uint8_t* u = tmp.data() + ((n * GC + cc) * 8 + jj) * 16;
+          const int g = cc * 8 + k;
+          out[n * (K / 2) + g * 16 + jj] = u[2 * k];
+          out[n * (K / 2) + g * 16 + 8 + jj] = u[2 * k + 1];
+        }
+  return 0;
+}
+
 int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes) {
   if (!c || !what) return G4V_E_ARG;
   HIPCHK(hipSetDevice(c->device));
   const void* src = nullptr;
   size_t nb = 0;
-  std::vector<uint8_t> tmp;
   int l = 0, j = 0;
   if (!std::strcmp(what, "E") && c->E.p) {
     src = c->E.p;
@@ -1065,6 +1087,11 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
   } else if (!std::strcmp(what, "coef") && c->coef.p) {
     src = c->coef.p;
     nb = (size_t)c->V * 4;
+  } else if (!std::strcmp(what, "Sq") && c->scr_s.p) {  // screen scales, [V][48] bf16
+    src = c->scr_s.p;
+    nb = (size_t)c->V * (H / 32) * 2;
+  } else if (!std::strcmp(what, "Wq") && c->scr_wr.p) {  // screen int4, [V][768] bytes
+    return read_relaid_w4(c, c->scr_wr.p, c->V, H, dst, cap, nbytes);
   } else if (std::sscanf(what + 1, "%d_%d", &l, &j) == 2 && l >= 0 && l < (int)c->L.size()) {
     const Layer& L = *c->L[l];
     if (what[0] == 'S' && j < 7) {
@@ -1074,30 +1101,8 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
       src = L.norms.as<float>() + (j < 4 ? j * H : 4 * H + (j - 4) * HD);
       nb = (j < 4 ? H : HD) * 4;
     } else if (what[0] == 'W' && j < 7) {
-      // undo the relayout: row n, chunk c, lane j holds bytes (j, 8+j) of groups 8c..8c+7
       const Mat& m = L.m[j];
-      nb = (size_t)m.N * m.K / 2;
-      if (nbytes) *nbytes = nb;
-      if (!dst) return 0;
-      if (cap < nb) {
-        c->err = "model_read: buffer too small";
-        return G4V_E_ARG;
-      }
-      tmp.resize(nb);
-      HIPCHK(hipMemcpy(tmp.data(), m.wr.p, nb, hipMemcpyDeviceToHost));
-      uint8_t* out = static_cast<uint8_t*>(dst);
-      const int GC = m.K / 256;
-      for (size_t n = 0; n < (size_t)m.N; ++n)
-        for (int cc = 0; cc < GC; ++cc)
-          for (int jj = 0; jj < 8; ++jj)
-            for (int k = 0; k < 8; ++k) {
-              const uint8_t* u = tmp.data() + ((n * GC + cc) * 8 + jj) * 16;
-              const int g = cc * 8 + k;
-              out[n * (m.K / 2) + g * 16 + jj] = u[2 * k];
-              out[n * (m.K / 2) + g * 16 + 8 + jj] = u[2 * k + 1];
-            }
-      if (nbytes) *nbytes = nb;
-      return 0;
+      return read_relaid_w4(c, m.wr.p, m.N, m.K, dst, cap, nbytes);
     }
   }
   if (!src) {

@@ -93,7 +93,8 @@ int g4v_model_set_final_norm(g4v_ctx* c, const float* w);
 int g4v_model_set_kv(g4v_ctx* c, int layer, int pos0, int n, const uint16_t* K, const uint16_t* V);
 /* E:1249-1250 ENGINE_FAKE_CTX: first n KV positions of every layer from the LCG seeded `seed` */
 int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
-/* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm") */
+/* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm",
+ * and the head screen "Wq" [V][768], "Sq" [V][48] bf16, "coef" [V] f32, in the reference's layouts) */
 int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes);
 
 /* ---- one verify pass (fwd E:1256-1502 + lazy head E:1453-1488 + accept E:1647-1661).

@@ -96,3 +96,69 @@ def screen_h(o, E):
         base = o.bf2f(E[n * K:(n + 1) * K]).astype(np.float32)
         rows.append(o.r16(base * 60 + o.normal_f32(o.stream(SCREEN_SEED, 10 + m), K, 0.3)))
     return np.stack(rows).astype(np.float32)
+
+
+# ---- screen build run by the reference engine's own main() (E:1235-1244) ----
+# embedding: the synthetic stack's E at seed 1 (V = 262,144, the bench workload's), with the rows
+# of SCREEN_TIE_ROWS replaced by screen_tie_rows(): groups whose weights sit exactly on
+# half-integer multiples of the group scale (nearbyintf's ties go to even), one bf16 step either
+# side of such ties, groups at the clamp ends, zero groups and negative zeros.
+SCREEN_BUILD_SEED = 1
+SCREEN_TIE_ROWS = [17 + 10007 * i for i in range(24)]
+
+
+def screen_tie_rows():
+    """{row: 1536 bf16 bits}; every group g has amax = 7 * sc with sc a bf16 power of two or
+    1.5 times one, so f2bf(amax / 7) == sc exactly and (k + 1/2) * sc divides to an exact tie"""
+    rows = {}
+    for r, n in enumerate(SCREEN_TIE_ROWS):
+        vals = np.zeros(1536, np.float32)
+        for g in range(48):
+            kind = (r + g) % 6
+            e = -12 + (r * 7 + g * 5) % 9                      # scale exponents 2^-12 .. 2^-4
+            sc = np.float32(2.0 ** e) * (np.float32(1.5) if (g + r) % 2 else np.float32(1.0))
+            w = np.zeros(32, np.float32)
+            sign = np.float32(1.0 if (r + g) % 3 else -1.0)
+            w[0] = sign * np.float32(7.0) * sc                 # the group's amax
+            ks = np.arange(-7, 7, dtype=np.float32)            # ties (k + 1/2) sc, |.| <= 6.5 sc
+            if kind == 0:                                      # ties only
+                w[1:] = [(ks[i % 14] + np.float32(0.5)) * sc for i in range(31)]
+            elif kind == 1:                                    # ties and exact multiples
+                w[1:] = [(ks[i % 14] + np.float32(0.5 * (i % 2))) * sc for i in range(31)]
+            elif kind == 2:                                    # one bf16 step above / below a tie
+                for i in range(1, 32):
+                    t = (ks[i % 14] + np.float32(0.5)) * sc
+                    tb = np.float32(t).view(np.uint32)
+                    step = np.uint32(1 << 16) if i % 2 else np.uint32(0)
+                    if t != 0 and i % 4 >= 2:
+                        tb = np.uint32(tb - (1 << 16)) if i % 2 else np.uint32(tb + (1 << 16))
+                    else:
+                        tb = np.uint32(tb + step)
+                    w[i] = np.uint32(tb).view(np.float32)
+            elif kind == 3:                                    # the clamp ends: -7 sc .. 7 sc, -6.5, 6.5
+                w[1:] = [(-7.0, 7.0, -6.5, 6.5, -0.5, 0.5)[i % 6] * sc for i in range(31)]
+            elif kind == 4:                                    # zero group (sc = 0), negative zeros
+                w[:] = 0.0
+                w[1::2] = -0.0
+            else:                                              # ties at +-1/2, +-3/2 only
+                w[1:] = [(-1.5, -0.5, 0.5, 1.5)[i % 4] * sc for i in range(31)]
+            vals[g * 32:(g + 1) * 32] = w
+        bits = (vals.view(np.uint32) >> 16).astype(np.uint16)
+        assert np.all((vals.view(np.uint32) & 0xFFFF) == 0)
+        rows[n] = bits
+    return rows
+
+
+def screen_build_embedding(o):
+    """the 262,144 x 1536 bf16 embedding the reference engine builds its screen from"""
+    from oracle import Model
+    m = Model(o, SCREEN_BUILD_SEED, HEAD_V, 1, 512, 16)
+    E = m.get("E", np.uint16, HEAD_V * 1536)
+    m.close()
+    for n, bits in screen_tie_rows().items():
+        E[n * 1536:(n + 1) * 1536] = bits
+    return E
+
+
+# rows of the reference's screen kept verbatim in the fixture besides the tie rows
+SCREEN_SAMPLE_ROWS = [0, 1, 777, 4095, 65536, 131071, 200001, 262143]

@@ -14,8 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
 
 from golden_cases import (ATTN_CASES, CTHR_L, EXP3_CASE, GATEUP_CASE, HEAD_V, SCREEN_SEED,  # noqa: E402
-                          VERIFY_CASES, VERIFY_MODEL, W4_CASES, attn_inputs, crc, exp3_inputs, gateup_inputs,
-                          screen_h, vec_inputs, w4_inputs)
+                          SCREEN_TIE_ROWS, VERIFY_CASES, VERIFY_MODEL, W4_CASES, attn_inputs, crc, exp3_inputs,
+                          gateup_inputs, screen_build_embedding, screen_h, vec_inputs, w4_inputs)
 from util import first_diff, same  # noqa: E402
 
 
@@ -113,6 +113,32 @@ def screen_case(orc):
     hh = screen_h(orc, E)
     P = orc.exp3_pack(E, HEAD_V, 1536)
     return E, scr, hh, P
+
+
+def test_screen_build_engine_main(orc):
+    """the oracle's screen build against the screen the reference engine's own main() builds
+    (E:1235-1244, run unchanged by oracle/_ref/ref_engine_screen; tests/golden/
+    make_screen_build.py): int4 bytes, bf16 scales and coefficients of all 262,144 rows, on the
+    seed-1 embedding with rows of exact nearbyintf ties, near-ties, clamp ends and zero groups"""
+    g = load("screen_build")
+    E = screen_build_embedding(orc)
+    assert crc(E) == int(g["crc_E"][0])
+    Wq, Sq, coef = orc.screen_build(E, HEAD_V, 1536)
+    rows = g["rows"]
+    Wq2, Sq2 = Wq.reshape(HEAD_V, 768), Sq.reshape(HEAD_V, 48)
+    assert same(Wq2[rows], g["Wq_rows"]), first_diff(Wq2[rows], g["Wq_rows"])
+    assert same(Sq2[rows], g["Sq_rows"]), first_diff(Sq2[rows], g["Sq_rows"])
+    assert same(coef[rows], g["coef_rows"]), first_diff(coef[rows], g["coef_rows"])
+    assert crc(Sq) == int(g["crc_Sq"][0])
+    assert crc(coef) == int(g["crc_coef"][0])
+    assert crc(Wq) == int(g["crc_Wq"][0])
+    # the tie rows really hold ties: some weights sit exactly on (k + 1/2) * sc
+    n = SCREEN_TIE_ROWS[0]
+    w = orc.bf2f(E[n * 1536:(n + 1) * 1536]).astype(np.float32).reshape(48, 32)
+    sc = orc.bf2f(Sq2[n]).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = np.where(sc[:, None] > 0, w / sc[:, None], 0)
+    assert np.sum(t - np.floor(t) == 0.5) > 100
 
 
 def test_screen_build_and_survivors(orc, screen_case):

@@ -136,3 +136,26 @@ def test_head_full_vocab(orc, dev):
         info, surv, sval = orc.head_row(h[m], scr, P)
         assert G[m] == info.G and ns[m] == info.nsurv, (m, G[m], info.G, ns[m], info.nsurv)
     assert fb[0] == 1 and fb[1] == 1 and fb[2] == 0 and fb[3] == 0
+
+
+def test_head_build_vs_reference_engine(orc, dev):
+    """the device's screen build (int4 bytes, bf16 scales, coefficients of all 262,144 rows)
+    against the screen the reference engine's own main() builds (E:1235-1244;
+    tests/golden/screen_build.npz from tests/golden/make_screen_build.py) on the seed-1
+    embedding with rows of exact nearbyintf ties, near-ties, clamp ends and zero groups"""
+    import os
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from golden_cases import HEAD_V, crc, screen_build_embedding
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "screen_build.npz"))
+    E = screen_build_embedding(orc)
+    assert crc(E) == int(g["crc_E"][0])
+    note("head build V=262144 on the reference-engine fixture embedding")
+    dev.head_build(E, HEAD_V)
+    Wq = dev.read("Wq", np.uint8).reshape(HEAD_V, 768)
+    Sq = dev.read("Sq", np.uint16).reshape(HEAD_V, 48)
+    coef = dev.read("coef", np.float32)
+    rows = g["rows"]
+    assert same(Wq[rows], g["Wq_rows"]), first_diff(Wq[rows], g["Wq_rows"])
+    assert same(Sq[rows], g["Sq_rows"]) and same(coef[rows], g["coef_rows"])
+    assert crc(Wq) == int(g["crc_Wq"][0]) and crc(Sq) == int(g["crc_Sq"][0]) and crc(coef) == int(g["crc_coef"][0])
