@@ -370,6 +370,7 @@ class Ref:
             "ref_head_setup": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
             "ref_verify": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, C.POINTER(RefOut)]),
             "ref_verify_ex": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _i, C.POINTER(RefOut)]),
+            "ref_last_hidden": (None, [_f32p]),
             "ref_attn_tile": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_attn_mh": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_prefill": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _vp]),
@@ -456,6 +457,12 @@ class Ref:
         if rc != 0:
             raise RuntimeError("ref_verify needs V = 262144 and at most 8 rows")
         return out
+
+    def last_hidden(self):
+        """the final-normed hidden state of the last verify pass's last committed row"""
+        h = np.empty(1536, np.float32)
+        self.L.ref_last_hidden(h)
+        return h
 
     def w4g32(self, W, S, X):
         X = _c(X, np.float32)

@@ -799,6 +799,10 @@ int ref_draft_step(RefModel* md, const RefDrafter* d, int tok, const float* h, i
 }
 
 int ref_verify_ex(RefModel* md, const int* toks, int na, int nb, int pos0, int allow_b, RefOut* out);
+// the final-normed hidden state of the last verify pass's last committed row (the next draft
+// chain starts from it)
+static float g_last_hidden[1536];
+void ref_last_hidden(float* out) { std::memcpy(out, g_last_hidden, sizeof g_last_hidden); }
 int ref_verify(RefModel* md, const int* toks, int na, int nb, int pos0, RefOut* out) {
   return ref_verify_ex(md, toks, na, nb, pos0, 1, out);
 }
@@ -961,6 +965,7 @@ int ref_verify_ex(RefModel* md, const int* toks, int na, int nb, int pos0, int a
   out->nacc = np - 1;
   out->branch = np > 1 ? br : 0;
   out->ncommit = np;
+  std::memcpy(g_last_hidden, hbuf[path[np - 1]], sizeof g_last_hidden);  // E:1660 hprev = hbuf[nacc]
   for (int r = 0; r < 8; ++r) {
     out->commit[r] = r < np ? G[path[r]] : -1;
     out->G[r] = G[r];

@@ -162,3 +162,8 @@ def screen_build_embedding(o):
 
 # rows of the reference's screen kept verbatim in the fixture besides the tie rows
 SCREEN_SAMPLE_ROWS = [0, 1, 777, 4095, 65536, 131071, 200001, 262143]
+
+
+# ---- the long-prompt workload at its full size (bench.py --workload long_prompt) ----
+LONG_PROMPT = dict(seed=1, V=262144, NL=35, I=6144, ctx=8192, dseed=2, rounds=256, ngram=3, nglen=3, k=3, dsplit=6,
+                   nsplit=8)
