@@ -481,6 +481,25 @@ void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q
   hipLaunchKernelGGL(k_attn_merge, dim3(M, nh), dim3(HD), 0, st, P, M, T);
 }
 
+// the caller's [position][256] key / value rows (device) into the device cache layout
+// (kc_index / vc_index), positions npos .. kv_cap(npos) - 1 zero
+__global__ void k_kv_to_cache(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int npos,
+                              uint16_t* __restrict__ KC, uint16_t* __restrict__ VC) {
+  const size_t total = (size_t)((npos + 31) / 32 * 32) * HD;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const int p = (int)(u / HD), e = (int)(u % HD);
+    KC[kc_index(p, e)] = p < npos ? K[u] : (uint16_t)0;
+    VC[vc_index(p, e)] = p < npos ? V[u] : (uint16_t)0;
+  }
+}
+
+void launch_kv_to_cache(const uint16_t* K, const uint16_t* V, int npos, uint16_t* KC, uint16_t* VC, hipStream_t st) {
+  const size_t total = (size_t)kv_cap(npos) * HD;
+  int grid = (int)((total + 255) / 256);
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(k_kv_to_cache, dim3(grid), dim3(256), 0, st, K, V, npos, KC, VC);
+}
+
 int attn_pmax() { return ATT_PMAX; }
 
 }  // namespace g4v

@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -260,6 +261,34 @@ static void gemv_passes(g4v_ctx* c, GemvArgs a, int epi, int M) {
 
 extern "C" {
 
+// ---------------------------------------------------------------------------------------
+// scratch of g4v_attn_splitkv_noalloc: a file-scope device array (each GPU holds its own copy
+// until the process ends) with the caller's key and value rows in the device cache layout
+// (NA_NPOS positions each) and the split partials po [MAXT][MAXM][NQ][HD], pm, pl [MAXT][MAXM][NQ].
+// Host code never uses the array's name as an address: its device address is taken once per
+// device with hipGetSymbolAddress (at the device's first g4v_create) and kept in na_scratch.
+constexpr int NA_NPOS = 4096;
+constexpr size_t NA_KV = (size_t)NA_NPOS * HD * 2;
+constexpr size_t NA_PO = (size_t)MAXT * MAXM * NQ * HD * 4;
+constexpr size_t NA_PML = (size_t)MAXT * MAXM * NQ * 4;
+constexpr size_t NA_BYTES = 2 * NA_KV + NA_PO + 2 * NA_PML;  // 5,259,264
+static __device__ __align__(256) uint8_t scratch[NA_BYTES];
+constexpr int NA_MAXDEV = 64;
+static std::mutex na_mu;
+static uint8_t* na_scratch[NA_MAXDEV];
+
+// with `device` current: the device address of its scratch (taken once)
+static hipError_t na_scratch_init(int device) {
+  if (device < 0 || device >= NA_MAXDEV) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(na_mu);
+  if (na_scratch[device]) return hipSuccess;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  na_scratch[device] = static_cast<uint8_t*>(p);
+  return hipSuccess;
+}
+
 int g4v_create(int device, g4v_ctx** out) {
   if (!out) return G4V_E_ARG;
   auto* c = new g4v_ctx();
@@ -280,6 +309,10 @@ int g4v_create(int device, g4v_ctx** out) {
   }
   e = hipStreamCreate(&c->st);
   if (e != hipSuccess) {
+    delete c;
+    return G4V_E_HIP;
+  }
+  if (na_scratch_init(device) != hipSuccess) {
     delete c;
     return G4V_E_HIP;
   }
@@ -570,6 +603,47 @@ int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npo
                    c->pm.as<float>(), c->pl.as<float>(), c->ao.as<float>(), NQ * HD, c->st);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(out, c->ao.p, (size_t)M * NQ * HD * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+// the same split-KV attention on device buffers, allocating nothing: the relaid key / value rows
+// and the split partials live in the file-scope scratch (NA_NPOS positions at most)
+int g4v_attn_splitkv_noalloc(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
+                             const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
+                             int kmin, int kmax, int nsplit, float* out) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(Kc && Vc && q && out && pos && lo && skip_lo && skip_hi, "attn_splitkv_noalloc: null pointer");
+  ARGCHK(hd == HD && nh == NQ, "attn_splitkv_noalloc: hd must be 256 and nh 8");
+  ARGCHK(M >= 1 && M <= MAXM && nsplit >= 1 && nsplit <= MAXT,
+         "attn_splitkv_noalloc: 1 <= M <= 8, 1 <= nsplit <= 16");
+  ARGCHK(npos >= 1 && npos <= NA_NPOS, "attn_splitkv_noalloc: npos beyond the scratch's 4096 positions");
+  ARGCHK(kmin >= 0 && kmax < npos && kmin <= kmax, "attn_splitkv_noalloc: need 0 <= kmin <= kmax < npos");
+  const int len = kmax - kmin + 1, per = (len + nsplit - 1) / nsplit;
+  ARGCHK(per <= attn_pmax(), "attn_splitkv_noalloc: more positions per split than the split buffer holds");
+  AttnGeom g{};
+  g.M = M;
+  g.kmin = kmin;
+  g.kmax = kmax;
+  g.T = nsplit;
+  for (int m = 0; m < M; ++m) {
+    ARGCHK(pos[m] >= 0 && pos[m] < npos, "attn_splitkv_noalloc: pos beyond npos");
+    g.pos[m] = pos[m];
+    g.lo[m] = lo[m];
+    g.skip_lo[m] = skip_lo[m];
+    g.skip_hi[m] = skip_hi[m];
+  }
+  HIPCHK(hipSetDevice(c->device));
+  uint8_t* sc = c->device < NA_MAXDEV ? na_scratch[c->device] : nullptr;
+  ARGCHK(sc != nullptr, "attn_splitkv_noalloc: no scratch on this device");
+  uint16_t* kd = reinterpret_cast<uint16_t*>(sc);
+  uint16_t* vd = reinterpret_cast<uint16_t*>(sc + NA_KV);
+  float* po = reinterpret_cast<float*>(sc + 2 * NA_KV);
+  float* pm = reinterpret_cast<float*>(sc + 2 * NA_KV + NA_PO);
+  float* pl = reinterpret_cast<float*>(sc + 2 * NA_KV + NA_PO + NA_PML);
+  launch_kv_to_cache(Kc, Vc, npos, kd, vd, c->st);
+  launch_attn_geom(kd, vd, q, NQ * HD, g, po, pm, pl, out, NQ * HD, c->st);
+  HIPCHK(hipGetLastError());
   HIPCHK(hipStreamSynchronize(c->st));
   return 0;
 }

@@ -170,4 +170,6 @@ void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q
 namespace g4v {
 // positions per attention split the split kernel can hold
 int attn_pmax();
+// device [npos][256] key / value rows into the device cache layout (kv_cap(npos) positions)
+void launch_kv_to_cache(const uint16_t* K, const uint16_t* V, int npos, uint16_t* KC, uint16_t* VC, hipStream_t st);
 }

@@ -34,6 +34,8 @@ SIGNATURES = {
     "g4v_w4a8_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
     "g4v_attn_splitkv": (_i, [_vp, _u16p, _u16p, _i, _i, _i, _i, _f32p, _i32p, _i32p, _i32p, _i32p,
                               _i, _i, _i, _f32p]),
+    "g4v_attn_splitkv_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i32p, _i32p, _i32p, _i32p,
+                                      _i, _i, _i, _vp]),
     "g4v_head_build": (_i, [_vp, _u16p, _i]),
     "g4v_head_argmax": (_i, [_vp, _f32p, _i, _i32p, _i32p, _i32p]),
     "g4v_head_survivors": (_i, [_vp, _i, _i32p, _f32p, _i, C.POINTER(_i)]),
@@ -195,6 +197,12 @@ class Device:
                                          _c(skip_lo, np.int32), _c(skip_hi, np.int32), kmin, kmax, T, out),
                  "attn_splitkv")
         return out
+
+    def attn_noalloc(self, Kd, Vd, npos, q_d, M, pos, lo, skip_lo, skip_hi, kmin, kmax, T, out_d):
+        """g4v_attn_splitkv_noalloc on device pointers (Kd, Vd, q_d, out_d: integers)"""
+        self._ok(self.L.g4v_attn_splitkv_noalloc(self.h, Kd, Vd, npos, 256, 8, M, q_d, _c(pos, np.int32),
+                                                 _c(lo, np.int32), _c(skip_lo, np.int32), _c(skip_hi, np.int32),
+                                                 kmin, kmax, T, out_d), "attn_splitkv_noalloc")
 
     # ---- head ----
     def head_build(self, E, V):

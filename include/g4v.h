@@ -61,6 +61,15 @@ int g4v_w4a8_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
 int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
                      const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
                      int kmin, int kmax, int nsplit, float* out);
+/* The same attention on device buffers, allocating nothing (no hipMalloc, hipFree or allocating
+ * library call): Kc, Vc, q and out are device pointers (same layouts as above), pos / lo /
+ * skip_lo / skip_hi host arrays.  No counterpart in the reference: it is for callers that cannot
+ * allocate (HIP graph capture, tight serving loops).  Its scratch (the relaid key / value rows and
+ * the split partials, 5.3 MB) is a file-scope device array, one per GPU, held until the process
+ * ends and shared by every call on that GPU: npos <= 4096; calls that overlap on one GPU race. */
+int g4v_attn_splitkv_noalloc(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
+                             const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
+                             int kmin, int kmax, int nsplit, float* out);
 
 /* ---- certified head (E:1232-1244 build; E:1406-1500 head_group).  E: [V][1536] bf16 output
  * matrix; builds the int4 screen, the exp3 codebook + exception list and the cap table. */
