@@ -152,6 +152,7 @@ struct g4v_ctx {
   std::vector<Graph> graphs;
   std::vector<long long> warmed;  // shapes run once eagerly (first call) before capture
   bool use_graph = true;
+  bool pf_i8 = true;  // G_I8 (ENGINE_PREFILL_INT8=1): prefill blocks of two rows or more run W4A8
   // row-tile GEMV shape of the verify pass's q/k/v, o, gate/up and down products: activation
   // rows per block and rows per tile (G4V_GEMV_CFG="a,b a,b a,b a,b" overrides, for tuning)
   int gcfg[4][2] = {{2, 64}, {1, 64}, {4, 64}, {1, 64}};
@@ -1468,8 +1469,9 @@ static void pf_lin(g4v_ctx* c, const Mat& m, const float* x, int M, float* y, bo
                         nullptr, nullptr, nullptr, c->st);
     launch_w4a8_gemm(m.a8w.as<uint4>(), m.a8s.as<uint4>(), c->pfxq.as<uint16_t>(), c->pfsx.as<float>(),
                      c->pfcorr.as<float>(), y, M, m.N, m.K, m.N, c->st);
-  } else {
-    launch_gemv(plain_args(m, x, y, M), EPI_STORE, c->st);
+  } else {  // the exact-float GEMV, MAXM rows a launch (each row's result is independent of the others)
+    for (int r = 0; r < M; r += MAXM)
+      launch_gemv(plain_args(m, x + (size_t)r * m.K, y + (size_t)r * m.N, std::min(MAXM, M - r)), EPI_STORE, c->st);
   }
 }
 
@@ -1569,6 +1571,12 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
   ARGCHK(toks && n >= 1 && pos0 >= 0, "prefill: need tokens, n >= 1, pos0 >= 0");
   ARGCHK((long long)pos0 + n <= c->ctxcap, "prefill: pos0 + n beyond the context capacity");
   ARGCHK(pfb >= 1 && pfb <= 32, "prefill: 1 <= pfb <= 32 (the engine's row block, MM = 32)");
+  // a block before the last one of at most 4 rows past ATT_PAR takes the split-KV path (E:1305),
+  // of one row the exact-float products (E:311): only the last block is run that way here
+  ARGCHK(pfb >= 5 || (n - 1) / pfb == 0 || pos0 + (n - 1) / pfb * pfb <= 192,
+         "prefill: pfb < 5 with blocks before the last past position 192 (split-KV blocks) is not supported");
+  ARGCHK(pfb >= 2 || n == 1 || !c->pf_i8,
+         "prefill: pfb 1 (one exact-float row per block) with W4A8 prefill is not supported for n > 1");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "prefill: 1 <= nsplit <= 16");
   for (int i = 0; i < n; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "prefill: token id outside the vocabulary");
   HIPCHK(hipSetDevice(c->device));
@@ -1588,8 +1596,8 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
   if (r) return r;
   HIPCHK(hipMemcpyAsync(c->pftok.p, toks, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
   const PfGeom g{n, pos0, pfb, -1};
-  if (nA > 0) pf_segment(c, g, 0, nA, true, false, nsplit, tail ? -1 : nA - 1);
-  if (tail) pf_segment(c, g, nA, Ml, Ml >= 2, tsplit, nsplit, Ml - 1);
+  if (nA > 0) pf_segment(c, g, 0, nA, c->pf_i8, false, nsplit, tail ? -1 : nA - 1);
+  if (tail) pf_segment(c, g, nA, Ml, c->pf_i8 && Ml >= 2, tsplit, nsplit, Ml - 1);
   HIPCHK(hipGetLastError());
   std::vector<float> h(H);
   HIPCHK(hipMemcpyAsync(h.data(), c->pfh.p, H * 4, hipMemcpyDeviceToHost, c->st));
@@ -2006,6 +2014,12 @@ int g4v_history_read(g4v_ctx* c, int* toks, int cap, int* L) {
   HIPCHK(hipSetDevice(c->device));
   HIPCHK(hipStreamSynchronize(c->st));
   HIPCHK(hipMemcpy(toks, c->hist.p, (size_t)std::min(cap, c->hist_len) * 4, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int g4v_set_prefill_int8(g4v_ctx* c, int on) {
+  if (!c) return G4V_E_ARG;
+  c->pf_i8 = on != 0;
   return 0;
 }
 

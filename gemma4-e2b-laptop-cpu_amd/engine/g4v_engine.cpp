@@ -183,7 +183,23 @@ int load_checkpoint(const Checkpoint& ck, int ctx) {
 }
 
 struct Engine {
-  int V = 0, ctx = 4096, pfb = 32, T = 6, ng_n = 0, ng_len = 3, k_draft = 3;
+  int V = 0, ctx = 4096, pfb = 32, ng_n = 0, ng_len = 3, k_draft = 3;
+  // The reference splits attention over its pool's active workers (attn_task, E:1327, 1544): T0 =
+  // the ENGINE_CPUS count at start, then set_active(a) (clamped to [1, T0], E:110-112) by every
+  // draft step (E:1535: 6, or under ENGINE_ADAPTIVE_THREADS with ENGINE_DRAFT_SAME 8 past the
+  // cutoff) and, under ENGINE_ADAPTIVE_THREADS only, by every forward pass (E:1257: 8 when its
+  // last position passes the cutoff, else 6).  The count persists between the calls.
+  int T0 = 6, active = 6, cut = 192;
+  bool adaptive = false, draft_same = true;
+  int clamp_active(int a) const { return a < 1 ? T0 : std::min(a, T0); }
+  int fwd_splits(int pos0, int M) {  // E:1257 then attn_task's split count
+    if (adaptive) active = clamp_active(pos0 + M > cut ? 8 : 6);
+    return active;
+  }
+  int draft_splits(int P) {  // E:1535
+    active = clamp_active(draft_same && adaptive && P + 1 > cut ? 8 : 6);
+    return active;
+  }
   bool drafter = false, stream = false, tree = false, sib_long = false;
   float sib_gap = 1.0f;      // E:1629 ENGINE_SIB_GAP: the sibling row is proposed when >= 0
   int pol[3] = {-1, -1, -1};  // E:1513 ENGINE_POLICY: draft count cap per state
@@ -202,7 +218,11 @@ struct Engine {
     const double t0 = now();
     int g0 = 0;
     std::vector<float> hprev(1536);
-    check(g4v_prefill(G, prompt.data() + start, n - start, start, pfb, T, &g0, hprev.data()), "prefill");
+    {  // every prompt block is a forward pass (E:1597-1598); only the last block attends split-KV
+      const int np = n - start;
+      for (int b = 0; b < np; b += pfb) fwd_splits(start + b, std::min(pfb, np - b));
+    }
+    check(g4v_prefill(G, prompt.data() + start, n - start, start, pfb, active, &g0, hprev.data()), "prefill");
     const double tp = now() - t0;
     std::vector<int> gen{g0};
     if (print && nnew > 0) {
@@ -245,7 +265,7 @@ struct Engine {
     if (k_draft == 0 || (!drafter && ng_n <= 0)) {  // E:1615: plain decode
       for (int i = 1; i < nnew && !is_stop(gen.back()); ++i) {
         const int t = gen.back();
-        check(g4v_verify_step(G, &t, 0, 0, n + i - 1, T, &R, nullptr), "verify_step");
+        check(g4v_verify_step(G, &t, 0, 0, n + i - 1, fwd_splits(n + i - 1, 1), &R, nullptr), "verify_step");
         gen.push_back(R.commit[0]);
         emit();
       }
@@ -286,7 +306,8 @@ struct Engine {
         if (!used_ng && drafter && k > 0) {  // E:1632-1645 (TAU 0: every draft is kept)
           int d[3], sec[3];
           float gap[3];
-          check(g4v_draft_mtp(G, conf, first ? hprev.data() : nullptr, P, k, T, d, sec, gap, nullptr), "draft_mtp");
+          check(g4v_draft_mtp(G, conf, first ? hprev.data() : nullptr, P, k, draft_splits(P), d, sec, gap, nullptr),
+                "draft_mtp");
           sec1 = sec[0];
           gap1 = gap[0];
           const bool allow_sib = sib_gap >= 0.0f && rounds >= 1 && state < 2 && k >= 2 && sec1 >= 0 && sec1 != d[0];
@@ -304,9 +325,10 @@ struct Engine {
           block[sibling] = sec1;
           ++tree_attempts;
           const bool allow_hit = tree || (P + 1 + sibling <= ATT_PAR && gap1 >= 0.25f);  // E:1650
-          check(g4v_verify_sibling(G, block, nd, P + 1, T, allow_hit ? 1 : 0, &R, nullptr), "verify_sibling");
+          check(g4v_verify_sibling(G, block, nd, P + 1, fwd_splits(P + 1, nd + 2), allow_hit ? 1 : 0, &R, nullptr),
+                "verify_sibling");
         } else {
-          check(g4v_verify_step(G, block, nd, 0, P + 1, T, &R, nullptr), "verify_step");  // E:1649
+          check(g4v_verify_step(G, block, nd, 0, P + 1, fwd_splits(P + 1, nd + 1), &R, nullptr), "verify_step");  // E:1649
         }
         ++rounds;
         if (R.branch == 1) {  // E:1650-1653 the tree hit: row 0's token and the sibling's
@@ -387,15 +409,36 @@ int main(int argc, char** argv) {
   e.sib_long = getenv("ENGINE_SIB_LONG") != nullptr;
   if (const char* g = getenv("ENGINE_SIB_GAP")) e.sib_gap = (float)atof(g);
   if (const char* pp = getenv("ENGINE_POLICY")) sscanf(pp, "%d,%d,%d", &e.pol[0], &e.pol[1], &e.pol[2]);
-  {  // the pool size (E:75-77): one split per worker
+  {  // the pool size (E:75-77, E:1215): one split per active worker
     int ncpu = 6;
     if (const char* c = getenv("ENGINE_CPUS")) {
       ncpu = 1;
       for (const char* p = c; *p; ++p) ncpu += *p == ',';
     }
-    e.T = std::max(1, std::min(16, ncpu));
+    e.T0 = e.active = std::max(1, std::min(16, ncpu));
+    e.adaptive = getenv("ENGINE_ADAPTIVE_THREADS") != nullptr;
+    e.cut = env_int("ENGINE_THREAD_CUTOFF", 192);  // E:1257 (default ATT_PAR), E:1533
+    e.draft_same = !(getenv("ENGINE_DRAFT_SAME") && atoi(getenv("ENGINE_DRAFT_SAME")) == 0);  // E:1532
+  }
+  // E:1210 G_I8 and E:1600 DEC_I8: the prompt's linear layers run W4A8 when ENGINE_PREFILL_INT8=1,
+  // and then the decode's verify passes too unless ENGINE_DECODE_INT8=0; the library decodes in
+  // exact float only
+  // settings whose reference paths this engine does not restate
+  if (env_int("ENGINE_ATT_PAR", ATT_PAR) != ATT_PAR || env_int("ENGINE_FAKE_CTX", 0) != 0 ||
+      env_int("ENGINE_SPLITKV", 1) == 0) {
+    fprintf(stderr, "g4v_engine: ENGINE_ATT_PAR other than %d, ENGINE_FAKE_CTX and ENGINE_SPLITKV=0 are not "
+                    "supported (E:1211-1214)\n", ATT_PAR);
+    return 2;
+  }
+  const bool g_i8 = env_int("ENGINE_PREFILL_INT8", 0) == 1;
+  const bool dec_i8 = !(getenv("ENGINE_DECODE_INT8") && atoi(getenv("ENGINE_DECODE_INT8")) == 0);
+  if (g_i8 && dec_i8) {
+    fprintf(stderr, "g4v_engine: ENGINE_PREFILL_INT8=1 decodes with W4A8 verify passes unless ENGINE_DECODE_INT8=0 "
+                    "(E:1600); this engine decodes in exact float: set ENGINE_DECODE_INT8=0\n");
+    return 2;
   }
   check(g4v_create(0, &G), "create");
+  check(g4v_set_prefill_int8(G, g_i8 ? 1 : 0), "set_prefill_int8");
   Checkpoint ck;
   if (synth) {
     check(g4v_model_synth(G, seed, V, NL, I, e.ctx), "model_synth");
@@ -415,7 +458,7 @@ int main(int argc, char** argv) {
   {  // E:1578: one warm-up pass at position 0 (the cache is not marked valid by it)
     const int w = 2;
     int g = 0;
-    check(g4v_prefill(G, &w, 1, 0, e.pfb, e.T, &g, nullptr), "warm-up");
+    check(g4v_prefill(G, &w, 1, 0, e.pfb, e.fwd_splits(0, 1), &g, nullptr), "warm-up");
   }
   if (getenv("ENGINE_SERVE")) {
     std::string line;

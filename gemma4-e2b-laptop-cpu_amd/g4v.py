@@ -54,6 +54,7 @@ SIGNATURES = {
     "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
     "g4v_sync": (_i, [_vp]),
     "g4v_set_graphs": (_i, [_vp, _i]),
+    "g4v_set_prefill_int8": (_i, [_vp, _i]),
     "g4v_prefill": (_i, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(_i), _vp]),
     "g4v_drafter_synth": (_i, [_vp, C.c_uint64]),
     "g4v_draft_mtp": (_i, [_vp, _i, _vp, _i, _i, _i, _i32p, _vp, _vp, _vp]),
@@ -334,6 +335,9 @@ class Device:
 
     def set_graphs(self, on):
         self._ok(self.L.g4v_set_graphs(self.h, 1 if on else 0), "set_graphs")
+
+    def set_prefill_int8(self, on):
+        self._ok(self.L.g4v_set_prefill_int8(self.h, 1 if on else 0), "set_prefill_int8")
 
     def profile(self, tags=None):
         """start per-kernel-class event timing for `tags` (names of PROF_TAGS; None = all)"""

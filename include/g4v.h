@@ -133,6 +133,9 @@ int g4v_verify_sibling(g4v_ctx* c, const int* toks, int nd, int pos0, int nsplit
  * second call of that shape on (the engine's persistent pool + job word, E:73-141, becomes a
  * graph launch).  on = 0 launches every kernel from the host instead. */
 int g4v_set_graphs(g4v_ctx* c, int on);
+/* E:1210 G_I8 (ENGINE_PREFILL_INT8=1, the default here): g4v_prefill multiplies blocks of two
+ * rows or more W4A8 (lin_multi, E:311); 0: exact float throughout, the reference's default */
+int g4v_set_prefill_int8(g4v_ctx* c, int on);
 
 /* ---- prefill: run_req's prompt loop (E:1594-1599) with ENGINE_PREFILL_INT8=1, i.e. fwd
  * (E:1256-1405) over blocks of pfb rows (ENGINE_PREFILL_BLOCK, 32 by default), W4A8 linear layers

@@ -152,6 +152,7 @@ void g4o_verify_ex(g4o_model* m, const int* toks, int na, int nb, int pos0, int 
 /* prefill (E:1594-1599, ENGINE_PREFILL_INT8=1): toks[0..n) at pos0.. in blocks of pfb rows;
  * fills the KV cache; hlast (optional) receives the final-normed hidden row of the last token */
 void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, float* hlast);
+void g4o_prefill_ex(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, int i8, float* hlast);
 
 /* the head of one final-normed row (E:1406-1500); toks[0..nt) (nt <= 8) seed the screen */
 int g4o_model_head(g4o_model* m, const float* h, const int* toks, int nt);

@@ -390,6 +390,12 @@ static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float
  *   p0 + M > 64 (E:1328), else run_mh (E:1337);  linear layers: W4A8 when M >= 2 (E:311).
  * hlast (optional) receives r16(rms(x, fnorm)) of the last row (E:1598, hf = M - 1). */
 void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, float* hlast) {
+  g4o_prefill_ex(m, toks, n, pos0, pfb, T, 1, hlast);
+}
+
+/* i8: G_I8 (ENGINE_PREFILL_INT8=1, E:1210): blocks of two rows or more multiply W4A8 (lin_multi,
+ * E:311); 0: exact float throughout (the engine's default, G_I8 false) */
+void g4o_prefill_ex(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T, int i8, float* hlast) {
   if (pfb < 1) pfb = 1;
   if (pfb > MAXROWS) pfb = MAXROWS;
   float* hb = (float*)malloc(sizeof(float) * (size_t)MAXROWS * H);
@@ -400,7 +406,7 @@ void g4o_prefill(g4o_model* m, const int* toks, int n, int pos0, int pfb, int T,
     const int amode = (M <= 4 && p0 + M > 192) ? ATT_SPLIT : (M >= 4 && p0 + M > 64) ? ATT_TILE : ATT_MH;
     rows_t r;
     rows_chain(&r, p0, M);
-    forward_ex(m, toks + done, &r, T, last ? hb : NULL, 1, amode);
+    forward_ex(m, toks + done, &r, T, last ? hb : NULL, i8, amode);
     if (last && hlast) memcpy(hlast, hb + (size_t)(M - 1) * H, sizeof(float) * H);
     done += M;
   }

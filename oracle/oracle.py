@@ -74,6 +74,7 @@ class Oracle:
             "g4o_verify_ex": (None, [_vp, _i32p, _i, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
             "g4o_prefill": (None, [_vp, _i32p, _i, _i, _i, _i, _vp]),
+            "g4o_prefill_ex": (None, [_vp, _i32p, _i, _i, _i, _i, _i, _vp]),
             "g4o_model_head": (_i, [_vp, _f32p, _i32p, _i]),
             "g4o_drafter_new": (_vp, [C.c_uint64, _i]), "g4o_drafter_free": (None, [_vp]),
             "g4o_drafter_ptr": (_vp, [_vp, C.c_char_p]),
@@ -268,11 +269,12 @@ class Model:
             raise KeyError(what)
         return out
 
-    def prefill(self, toks, pos0=0, pfb=32, T=8):
-        """prefill toks at pos0.. (W4A8 linear layers); returns the last row's final-normed hidden"""
+    def prefill(self, toks, pos0=0, pfb=32, T=8, i8=True):
+        """prefill toks at pos0.. (W4A8 linear layers for blocks of two rows or more; i8 False:
+        exact float throughout); returns the last row's final-normed hidden"""
         toks = _c(toks, np.int32)
         hid = np.empty(1536, np.float32)
-        self.o.L.g4o_prefill(self.h, toks, toks.size, pos0, pfb, T, hid.ctypes.data)
+        self.o.L.g4o_prefill_ex(self.h, toks, toks.size, pos0, pfb, T, 1 if i8 else 0, hid.ctypes.data)
         return hid
 
     def head(self, h, seeds=()):
@@ -374,6 +376,7 @@ class Ref:
             "ref_attn_tile": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_attn_mh": (None, [_u16p, _u16p, _i, _f32p, _i, _i, _f32p]),
             "ref_prefill": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _vp]),
+            "ref_prefill_ex": (_i, [C.POINTER(RefModel), _i32p, _i, _i, _i, _i, _vp]),
             "ref_pack_reset": (None, []),
             "ref_b16": (None, [_u16p, _i, _i, _f32p, _f32p]),
             "ref_draft_step": (_i, [C.POINTER(RefModel), C.POINTER(RefDrafter), _i, _f32p, _i, _i, _i, _f32p,
@@ -442,10 +445,10 @@ class Ref:
         fn(_c(Kc, np.uint16), _c(Vc, np.uint16), 1 if sliding else 0, q, pos0, q.shape[0], out)
         return out
 
-    def prefill(self, toks, pos0=0, pfb=32):
+    def prefill(self, toks, pos0=0, pfb=32, i8=True):
         hid = np.empty(1536, np.float32)
         toks = _c(toks, np.int32)
-        rc = self.L.ref_prefill(C.byref(self.model), toks, toks.size, pos0, pfb, hid.ctypes.data)
+        rc = self.L.ref_prefill_ex(C.byref(self.model), toks, toks.size, pos0, pfb, 1 if i8 else 0, hid.ctypes.data)
         if rc != 0:
             raise ValueError("ref_prefill: pfb must be 1..32")
         return hid

@@ -499,7 +499,13 @@ void ref_pack_reset(void) { g_pk.clear(); }
 // true: fwd (E:1256-1405) per block of at most pfb rows, the engine's attention-path choice
 // (E:1305, 1328, 1337 with SPLITKV, TILED, ATT_PAR = 192) and lin_multi's W4A8 rule (M >= 2,
 // E:311).  hlast receives the last row's r16(rms(x, fnorm)).  Returns -1 for pfb outside 1..32.
+int ref_prefill_ex(RefModel* md, const int* toks, int n, int pos0, int pfb, int i8, float* hlast);
 int ref_prefill(RefModel* md, const int* toks, int n, int pos0, int pfb, float* hlast) {
+  return ref_prefill_ex(md, toks, n, pos0, pfb, 1, hlast);
+}
+// i8: G_I8 (ENGINE_PREFILL_INT8=1, E:1210), the prompt's blocks of two rows or more multiply
+// W4A8; 0: exact float throughout (G_I8_ACTIVE false, E:1363)
+int ref_prefill_ex(RefModel* md, const int* toks, int n, int pos0, int pfb, int i8, float* hlast) {
   if (pfb < 1 || pfb > 32) return -1;
   const int H = 1536, NL = md->NL, I = md->I;
   const int T = POOL.active_count();
@@ -511,7 +517,7 @@ int ref_prefill(RefModel* md, const int* toks, int n, int pos0, int pfb, float* 
   abuf.resize((size_t)32 * I);
   static XP XA, XB;
   const __m256 vsqh = _mm256_set1_ps(sqrtf((float)H));
-  G_I8_ACTIVE = true;
+  G_I8_ACTIVE = i8 != 0;
   for (int done = 0; done < n;) {
     const int M = std::min(pfb, n - done), p0 = pos0 + done;
     const bool last = done + M == n;
@@ -602,7 +608,7 @@ int ref_prefill(RefModel* md, const int* toks, int n, int pos0, int pfb, float* 
       XA.M = M;
       XA.src = &mlp_in[0][0];
       XA.qdone = false;
-      if (M >= 2) {  // E:1367-1371
+      if (G_I8_ACTIVE && M >= 2) {  // E:1367-1371
         const Q4* qq[2] = {&qm[4], &qm[5]};
         float* yy[2] = {gbuf.data(), ubuf.data()};
         lin_multi(XA, 2, qq, yy);

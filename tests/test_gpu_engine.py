@@ -23,15 +23,37 @@ def is_stop(t):
 
 
 class OracleEngine:
-    """run_req over the oracle with one active cache (ENGINE_SLOTS=1)"""
+    """run_req over the oracle with one active cache (ENGINE_SLOTS=1).  Attention splits over
+    the pool's active workers (E:1327, 1544): t0 = the ENGINE_CPUS count, set_active clamps to
+    [1, t0] (E:110-112), draft steps set 6 (8 past the cutoff with ENGINE_ADAPTIVE_THREADS and
+    ENGINE_DRAFT_SAME, E:1535), forward passes set 6 / 8 only with ENGINE_ADAPTIVE_THREADS
+    (E:1257), and the count persists.  i8: ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8=0."""
 
-    def __init__(self, orc):
+    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False):
         from oracle import Drafter, Model
         self.orc = orc
+        self.t0, self.active, self.adaptive, self.draft_same, self.cut, self.i8 = t0, t0, adaptive, draft_same, cut, i8
         self.m = Model(orc, SEED, V, NL, I, CTX)
         self.d = Drafter(orc, SEED + 1, V)
         self.keys, self.kv_len = [], 0
-        self.m.prefill(np.array([2], np.int32), T=T)  # E:1578 warm-up at position 0
+        self.splits_seen = set()
+        self.prefill(np.array([2], np.int32), 0)  # E:1578 warm-up at position 0
+
+    def set_active(self, a):
+        self.active = self.t0 if a < 1 else min(a, self.t0)
+        self.splits_seen.add(self.active)
+        return self.active
+
+    def fwd_splits(self, pos0, M):
+        if self.adaptive:
+            self.set_active(8 if pos0 + M > self.cut else 6)
+        self.splits_seen.add(self.active)
+        return self.active
+
+    def prefill(self, toks, pos0):
+        for b in range(0, len(toks), 32):
+            self.fwd_splits(pos0 + b, min(32, len(toks) - b))
+        return self.m.prefill(toks, pos0=pos0, T=self.active, i8=self.i8)
 
     def close(self):
         self.d.close()
@@ -43,7 +65,7 @@ class OracleEngine:
         while common < self.kv_len and common < n and self.keys[common] == prompt[common]:
             common += 1
         start = min(common, n - 1)
-        h = self.m.prefill(np.array(prompt[start:], np.int32), pos0=start, T=T)
+        h = self.prefill(np.array(prompt[start:], np.int32), start)
         g0 = self.m.head(h, prompt[start:][-8:])
         gen, P, stopped = [g0], n - 1, is_stop(g0)
         hprev, state, rounds, self.sib_rounds, self.hits = h, 1, 0, 0, 0
@@ -57,7 +79,8 @@ class OracleEngine:
             if not used_ng:  # E:1632-1645
                 tok, hh = gen[-1], hprev
                 for j in range(k):
-                    tok, hh, sec, gap = self.d.step(self.m, tok, hh, P + 1 + j, P, T)
+                    ts = self.set_active(8 if self.draft_same and self.adaptive and P + 1 > self.cut else 6)
+                    tok, hh, sec, gap = self.d.step(self.m, tok, hh, P + 1 + j, P, ts)
                     if j == 0:
                         sec1, gap1 = sec, gap
                         allow = rounds >= 1 and state < 2 and k >= 2 and sec1 >= 0 and sec1 != tok
@@ -76,9 +99,9 @@ class OracleEngine:
             if sib > 0:
                 self.sib_rounds += 1
                 allow_hit = tree or (P + 1 + sib <= 192 and gap1 >= 0.25)
-                o, hprev = self.m.verify(block, nd, 1, P + 1, T, allow_b=allow_hit)
+                o, hprev = self.m.verify(block, nd, 1, P + 1, self.fwd_splits(P + 1, len(block)), allow_b=allow_hit)
             else:
-                o, hprev = self.m.verify(block, nd, 0, P + 1, T)
+                o, hprev = self.m.verify(block, nd, 0, P + 1, self.fwd_splits(P + 1, len(block)))
             rounds += 1
             if o.branch == 1:  # E:1650-1653
                 self.hits += 1
@@ -106,36 +129,29 @@ class OracleEngine:
         return g0, gen, start
 
 
-def test_engine_protocol_matches_oracle(orc):
+def run_protocol(orc, requests, tree_from, env_extra, **engine):
+    """send the requests (prompt, nnew, k_draft, tree) to the engine, "BENCH_MODE 2 1" before
+    request tree_from, and check every line against OracleEngine(orc, **engine)"""
     exe = os.path.join(PKG, "g4v_engine")
     if not os.path.exists(exe):
         pytest.fail("g4v_engine not built (make -C gemma4-e2b-laptop-cpu_amd)")
-    rng = np.random.default_rng(5)
-    motif = rng.integers(0, V, 16).tolist()
-    a = (motif * 8)[:100]
-    b = rng.integers(0, V, 40).tolist()
-    c = rng.integers(0, V, 30).tolist()
-    # (prompt, nnew, k_draft, tree): the last two after "BENCH_MODE 2 1" (the tree mode)
-    requests = [(a, 20, 3, False), (b, 10, 3, False), (a, 15, 3, False), (a + [5, 6, 7], 8, 3, False),
-                (c, 24, 3, False), (b + [9], 16, 2, True), (c + [4], 12, 2, True)]
-    note("engine protocol: 7 requests over a 15-layer synthetic stack")
-    env = dict(os.environ, **ENV)
+    env = dict(os.environ, **dict(ENV, **env_extra))
     lines = ""
     for i, (p, nn, _, _) in enumerate(requests):
-        if i == 5:
+        if i == tree_from:
             lines += "BENCH_MODE 2 1\n"
         lines += f"{nn} {' '.join(map(str, p))}\n"
     proc = subprocess.run([exe, f"synth:{SEED}:{V}:{NL}:{I}", "-", "-", "0"], input=lines, env=env,
                           capture_output=True, text=True, timeout=240)
     assert proc.returncode == 0, proc.stderr[-2000:]
     out = proc.stdout.splitlines()
-    oe = OracleEngine(orc)
+    oe = OracleEngine(orc, **engine)
     try:
         it = iter(out)
         sib_rounds = hits = 0
         per_req = []
         for k, (prompt, nn, kd, tree) in enumerate(requests):
-            if k == 5:
+            if k == tree_from:
                 assert next(it) == "MODE k=2 tree=1"
             g0, gen, start = oe.run_req(prompt, nn, kd, tree)
             sib_rounds += oe.sib_rounds
@@ -159,10 +175,57 @@ def test_engine_protocol_matches_oracle(orc):
         assert len(rank1) == len(requests), proc.stderr[-1000:]
         for k, ln in enumerate(rank1):
             assert f"TREE attempts={per_req[k][0]} hits={per_req[k][1]}" in ln, (k, ln, per_req[k])
-        note(f"sibling rounds {sib_rounds}, tree hits {hits}")
-        assert sib_rounds > 0
+        note(f"sibling rounds {sib_rounds}, tree hits {hits}, split counts {sorted(oe.splits_seen)}")
+        return sib_rounds, oe.splits_seen
     finally:
         oe.close()
+
+
+def test_engine_protocol_matches_oracle(orc):
+    rng = np.random.default_rng(5)
+    motif = rng.integers(0, V, 16).tolist()
+    a = (motif * 8)[:100]
+    b = rng.integers(0, V, 40).tolist()
+    c = rng.integers(0, V, 30).tolist()
+    requests = [(a, 20, 3, False), (b, 10, 3, False), (a, 15, 3, False), (a + [5, 6, 7], 8, 3, False),
+                (c, 24, 3, False), (b + [9], 16, 2, True), (c + [4], 12, 2, True)]
+    note("engine protocol: 7 requests over a 15-layer synthetic stack")
+    sib_rounds, _ = run_protocol(orc, requests, 5, {})
+    assert sib_rounds > 0
+
+
+@pytest.mark.parametrize("cpus,extra", [
+    (8, {}),  # the first prompt splits 8 ways, every later pass 6 (the drafter's set_active persists)
+    (8, dict(ENGINE_ADAPTIVE_THREADS="1")),  # 6 / 8 either side of position 192, per pass
+    (8, dict(ENGINE_ADAPTIVE_THREADS="1", ENGINE_DRAFT_SAME="0", ENGINE_THREAD_CUTOFF="150")),
+    (4, dict(ENGINE_ADAPTIVE_THREADS="1")),  # set_active clamps to the pool
+])
+def test_engine_split_counts_follow_pool(orc, cpus, extra):
+    """the split-KV count of every pass follows the reference pool's active workers"""
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, V, 176).tolist()
+    b = rng.integers(0, V, 230).tolist()
+    requests = [(a, 40, 3, False), (b, 12, 3, False), (a + [7], 10, 3, False)]
+    note(f"engine split counts: {cpus} CPUs, {extra}")
+    env = dict(extra, ENGINE_CPUS=",".join(str(2 * i) for i in range(cpus)))
+    _, seen = run_protocol(orc, requests, len(requests), env, t0=cpus,
+                           adaptive="ENGINE_ADAPTIVE_THREADS" in extra,
+                           draft_same=extra.get("ENGINE_DRAFT_SAME") != "0",
+                           cut=int(extra.get("ENGINE_THREAD_CUTOFF", 192)))
+    assert seen == ({4} if cpus == 4 else {6, 8}), seen
+
+
+def test_engine_prefill_int8(orc):
+    """ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8=0: W4A8 prompt blocks, exact-float decode
+    (E:1210, 1596, 1600); with the decode's W4A8 left on (its default) the engine refuses"""
+    rng = np.random.default_rng(12)
+    requests = [(rng.integers(0, V, 70).tolist(), 12, 3, False), (rng.integers(0, V, 33).tolist(), 8, 3, False)]
+    run_protocol(orc, requests, len(requests), dict(ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="0"), i8=True)
+    exe = os.path.join(PKG, "g4v_engine")
+    for extra in (dict(ENGINE_PREFILL_INT8="1"), dict(ENGINE_ATT_PAR="128"), dict(ENGINE_SPLITKV="0")):
+        proc = subprocess.run([exe, f"synth:{SEED}:{V}:{NL}:{I}", "-", "-", "0"], input="4 1 2 3\n",
+                              env=dict(os.environ, **dict(ENV, **extra)), capture_output=True, text=True, timeout=120)
+        assert proc.returncode == 2 and "g4v_engine:" in proc.stderr, (extra, proc.returncode, proc.stderr[-500:])
 
 
 def write_checkpoint(om, d, V, NL, I):

@@ -1,6 +1,6 @@
-"""Prefill (E:1594-1599 with ENGINE_PREFILL_INT8=1): the oracle's attention paths and its
-block composition against the reference's own kernels (oracle/_ref), and the attention paths
-against an fp64 softmax."""
+"""Prefill (E:1594-1599, with ENGINE_PREFILL_INT8=1 and in the default exact float): the
+oracle's attention paths and its block composition against the reference's own kernels
+(oracle/_ref), and the attention paths against an fp64 softmax."""
 import numpy as np
 import pytest
 
@@ -65,16 +65,19 @@ def test_attention_paths_vs_reference(orc, ref, kind, pos0, M, sliding):
 CASES = [(34, 2, 256), (100, 2, 256), (193, 2, 256), (196, 5, 256), (600, 1, 640)]
 
 
+@pytest.mark.parametrize("i8", [True, False])
 @pytest.mark.parametrize("n,NL,ctx", CASES)
-def test_prefill_vs_reference(orc, ref, n, NL, ctx):
+def test_prefill_vs_reference(orc, ref, n, NL, ctx, i8):
+    """i8: ENGINE_PREFILL_INT8=1 (W4A8 for blocks of two rows or more); else the engine's
+    default, exact float throughout (E:1210, 1363)"""
     from oracle import Model
     V, I, seed = 4096, 512, 31
     toks = RNG.integers(0, V, n).astype(np.int32)
     om, rm = Model(orc, seed, V, NL, I, ctx), Model(orc, seed, V, NL, I, ctx)
     try:
-        ho = om.prefill(toks)
+        ho = om.prefill(toks, i8=i8, T=ref.threads)  # the split-KV tail splits over the pool's workers
         ref.bind_model(rm)
-        hr = ref.prefill(toks)
+        hr = ref.prefill(toks, i8=i8)
         assert same(ho, hr), first_diff(ho, hr)
         for what in ("KC", "VC"):
             a, b = om.get(what, np.uint16, NL * ctx * 256), rm.get(what, np.uint16, NL * ctx * 256)
