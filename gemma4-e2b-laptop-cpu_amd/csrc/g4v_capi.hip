@@ -78,6 +78,7 @@ struct g4v_ctx {
   int cus = 0;
   std::vector<std::unique_ptr<Mat>> mats;  // standalone GEMV handles
   DBuf gx, gy;                              // standalone GEMV io
+  DBuf nrmio;                               // g4v_w4g32_norm_gemm io: o, xin, x1 [MAXM][H], w1, w2 [H]
   DBuf a8x, a8y, a8xq, a8sx, a8corr, a8q, a8qs, a8qsum;  // W4A8 io and quantised activations
   // head
   bool head_ready = false;
@@ -459,6 +460,52 @@ int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us) {
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   *us = ms * 1000.f / iters;
+  return 0;
+}
+
+int g4v_w4g32_norm_gemm(g4v_ctx* c, int h, int mode, const float* o, const float* xin, const float* w1,
+                        const float* w2, float scalar, int M, int rows_per_block, int tile_rows, float* y, float* x1) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(h >= 0 && h < (int)c->mats.size(), "w4g32_norm_gemm: bad handle");
+  ARGCHK(mode == 1 || mode == 2, "w4g32_norm_gemm: mode 1 (after attention) or 2 (after the MLP)");
+  ARGCHK(o && xin && w1 && w2 && y && x1 && M >= 1 && M <= MAXM, "w4g32_norm_gemm: need 1 <= M <= 8");
+  ARGCHK(rows_per_block >= 1 && rows_per_block <= 4 && (tile_rows == 32 || tile_rows == 64),
+         "w4g32_norm_gemm: 1 <= rows_per_block <= 4, tile_rows 32 or 64");
+  Mat& m = *c->mats[h];
+  ARGCHK(m.K == H && m.N % 64 == 0, "w4g32_norm_gemm: the matrix needs K = 1536 and N % 64 == 0");
+  HIPCHK(hipSetDevice(c->device));
+  if (!m.tw.p) {  // the row-tiled copy, once per handle
+    ALLOC(m.tw, (size_t)m.N * m.K / 2);
+    ALLOC(m.ts, (size_t)m.N * m.K / 16);
+    launch_tile_w4(m.wr.as<uint4>(), m.s.as<uint16_t>(), m.tw.as<uint4>(), m.ts.as<uint4>(), m.N, m.K, c->st);
+  }
+  int r = gemv_io(c, h, M);
+  if (r) return r;
+  if (!c->nrmio.p) ALLOC(c->nrmio, ((size_t)3 * MAXM * H + 2 * H) * 4);
+  float* od = c->nrmio.as<float>();
+  float *xd = od + MAXM * H, *x1d = xd + MAXM * H, *w1d = x1d + MAXM * H, *w2d = w1d + H;
+  HIPCHK(hipMemcpyAsync(od, o, (size_t)M * H * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(xd, xin, (size_t)M * H * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(w1d, w1, (size_t)H * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(w2d, w2, (size_t)H * 4, hipMemcpyHostToDevice, c->st));
+  GemvTArgs a{};
+  a.mat[0] = m.tile();
+  a.y[0] = c->gy.as<float>();
+  a.ldy[0] = m.N;
+  a.K = H;
+  a.M = M;
+  a.nrm_mode = mode;
+  a.nrm_o = od;
+  a.nrm_xin = xd;
+  a.nrm_xout = x1d;
+  a.nrm_w1 = w1d;
+  a.nrm_w2 = w2d;
+  a.nrm_scalar = scalar;
+  launch_gemv_t(a, c->st, rows_per_block, tile_rows);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(y, c->gy.p, (size_t)M * m.N * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipMemcpyAsync(x1, x1d, (size_t)M * H * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
   return 0;
 }
 

@@ -29,6 +29,7 @@ SIGNATURES = {
     "g4v_w4_upload": (_i, [_vp, _u8p, _u16p, _i, _i]),
     "g4v_w4g32_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4g32_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_w4g32_norm_gemm": (_i, [_vp, _i, _i, _f32p, _f32p, _f32p, _f32p, C.c_float, _i, _i, _i, _f32p, _f32p]),
     "g4v_w4a8_quant": (_i, [_vp, _f32p, _i, _i, _vp, _f32p, _i32p]),
     "g4v_w4a8_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4a8_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
@@ -156,6 +157,16 @@ class Device:
         Y = np.empty((M, N), np.float32)
         self._ok(self.L.g4v_w4g32_gemm(self.h, h, X, M, Y), "w4g32_gemm")
         return Y
+
+    def w4g32_norm(self, mat, mode, o, xin, w1, w2, scalar, rows_per_block=2, tile_rows=64):
+        h, N, K = mat
+        o, xin = _c(o, np.float32), _c(xin, np.float32)
+        M = o.shape[0]
+        Y = np.empty((M, N), np.float32)
+        X1 = np.empty((M, K), np.float32)
+        self._ok(self.L.g4v_w4g32_norm_gemm(self.h, h, mode, o, xin, _c(w1, np.float32), _c(w2, np.float32),
+                                            scalar, M, rows_per_block, tile_rows, Y, X1), "w4g32_norm_gemm")
+        return Y, X1
 
     def w4g32_bench(self, mat, M, iters=100):
         us = C.c_float()

@@ -42,6 +42,17 @@ int g4v_w4_upload(g4v_ctx* c, const uint8_t* w, const uint16_t* s, int N, int K)
 int g4v_w4g32_gemm(g4v_ctx* c, int h, const float* x, int M, float* y);
 /* same GEMV with x and y already on the device; times `iters` launches, returns us/launch */
 int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
+/* the residual and RMS-norm block between two sub-blocks fused into the next product, as the
+ * verify pass runs it: mode 1 (after attention, E:1358-1361):
+ *   x1 = r16(xin + r16(rms(r16(o), w1))), y = W r16(rms(x1, w2));
+ * mode 2 (after the MLP, E:1375-1378 and E:1390-1404 with the per-layer-embedding branch zero):
+ *   x1 = r16(r16(xin + r16(rms(r16(o), w1))) * scalar), y = W rms(x1, w2);
+ * rms(v, w) = (v * r) * w with r = 1 / sqrtf((float)(sum of squares / 1536) + 1e-6f), the sum
+ * in double over 16 lanes (E:326-352).  o, xin, x1: [M][1536]; w1, w2: [1536]; the handle's
+ * K = 1536, N % 64 == 0; 1 <= M <= 8.  rows_per_block (1..4) and tile_rows (32, 64) choose the
+ * launch shape the verify pass tunes per product. */
+int g4v_w4g32_norm_gemm(g4v_ctx* c, int h, int mode, const float* o, const float* xin, const float* w1,
+                        const float* w2, float scalar, int M, int rows_per_block, int tile_rows, float* y, float* x1);
 
 /* ---- W4A8: w4a8::quant (engine/w4a8_avx2.h:30-42) and w4a8::tile<MT> over all rows as
  * i8_task runs it (engine/w4a8_avx2.h:46-61, E:303-309), on a handle of g4v_w4_upload with

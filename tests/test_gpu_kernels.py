@@ -47,6 +47,73 @@ def test_w4g32_bf16_inputs_and_repeat(orc, dev):
         assert same(dev.w4g32(mat, X), orc.w4g32(W, S, X))
 
 
+def _norm_expected(orc, W, S, mode, o, xin, w1, w2, scalar):
+    """the residual / RMS block between sub-blocks (E:1358-1361 mode 1, E:1375-1404 mode 2) and
+    the product it feeds, composed from the oracle's rms and r16 (both pinned by golden vectors)"""
+    M, H = o.shape
+    xa = np.empty((M, H), np.float32)
+    x1 = np.empty((M, H), np.float32)
+    tmp = np.empty(H, np.float32)
+    for i in range(M):
+        oi = orc.r16(o[i])
+        orc.L.g4o_rms(oi, w1.ctypes.data, H, tmp)
+        x = orc.r16(xin[i] + orc.r16(tmp))
+        if mode == 2:
+            x = orc.r16(x * np.float32(scalar))
+        orc.L.g4o_rms(np.ascontiguousarray(x), w2.ctypes.data, H, tmp)
+        xa[i] = orc.r16(tmp) if mode == 1 else tmp
+        x1[i] = x
+    return orc.w4g32(W, S, xa), x1
+
+
+def _norm_inputs(orc, kind, M, seed):
+    """o, xin rows: 'normal' (one sum per lane in any order is exact), 'wide' (every lane needs
+    the ordered chain: magnitudes from 2^-60 to 2^20), 'mixed' (a few lanes of each row wide),
+    'edge' (a zero row, a one-element row, fp32 subnormals)"""
+    H = 1536
+    rng = np.random.default_rng(seed)
+    o = orc.normal_f32(orc.stream(seed, 5), M * H).reshape(M, H)
+    xin = orc.r16(orc.normal_f32(orc.stream(seed, 6), M * H).reshape(M, H) * 2)
+    if kind == "wide":
+        o = o * np.exp2(rng.integers(-60, 21, (M, H))).astype(np.float32)
+        xin = orc.r16(xin * np.exp2(rng.integers(-60, 21, (M, H))).astype(np.float32))
+    elif kind == "mixed":
+        for i in range(M):
+            j = rng.choice(H, 6, replace=False)
+            o[i, j] *= np.float32(2.0 ** -40)
+            xin[i, j] = orc.r16(xin[i, j] * np.float32(2.0 ** -45))
+    elif kind == "edge":
+        o[0] = 0
+        if M > 1:
+            o[1] = 0
+            o[1, 17] = 3.0
+        if M > 2:
+            o[2, ::3] = np.float32(1e-40)
+            xin[2, ::5] = 0
+    return np.ascontiguousarray(o, np.float32), np.ascontiguousarray(xin, np.float32)
+
+
+@pytest.mark.parametrize("mode,kind,M,rpb,tr", [
+    (1, "normal", 7, 4, 64), (2, "normal", 7, 2, 64), (1, "wide", 7, 4, 64), (2, "wide", 7, 2, 64),
+    (1, "mixed", 8, 3, 64), (2, "mixed", 5, 1, 64), (1, "edge", 3, 2, 32), (2, "edge", 7, 4, 32),
+    (2, "wide", 1, 1, 32), (1, "mixed", 7, 4, 32)])
+def test_norm_gemm_bit_exact(orc, dev, mode, kind, M, rpb, tr):
+    """the norm prologue of the row-tile GEMV (both RMS factors, residual, layer scalar) against
+    the oracle's composition, for sums that any order gives exactly and sums that need the
+    reference's order"""
+    seed = 500 + 10 * mode + M + rpb
+    W, S = _w4(orc, seed, 256, 1536)
+    o, xin = _norm_inputs(orc, kind, M, seed)
+    w1 = orc.r16(0.5 + orc.normal_f32(orc.stream(seed, 7), 1536) ** 2 / 4)
+    w2 = orc.r16(0.5 + orc.normal_f32(orc.stream(seed, 8), 1536) ** 2 / 4)
+    note(f"norm gemm mode={mode} kind={kind} M={M} rows/block={rpb} tile={tr}")
+    mat = dev.w4_upload(W, S)
+    y, x1 = dev.w4g32_norm(mat, mode, o, xin, w1, w2, 0.75, rpb, tr)
+    ye, x1e = _norm_expected(orc, W, S, mode, o, xin, w1, w2, 0.75)
+    assert same(x1, x1e), first_diff(x1, x1e)
+    assert same(y, ye), first_diff(y, ye)
+
+
 def _attn_case(orc, ctx, M, T, window, tree, seed):
     hd, nh = 256, 8
     Kc = orc.normal_bf16(orc.stream(seed, 1), (ctx + 8) * hd)
