@@ -699,10 +699,11 @@ int g4v_attn_splitkv_noalloc(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc,
 // ---------------------------------------------------------------------------------------
 // head
 // ---------------------------------------------------------------------------------------
+// one head pass scores up to MAXM rows (a chain of 7 drafts evaluates 7 rows in its second pass)
 static int alloc_head_bufs(g4v_ctx* c, HeadBufs& b, int V) {
-  ALLOC(b.u, (size_t)4 * V * 4);
-  ALLOC(b.list, (size_t)4 * HEAD_LIMIT * 4);
-  ALLOC(b.sval, (size_t)4 * HEAD_LIMIT * 4);
+  ALLOC(b.u, (size_t)MAXM * V * 4);
+  ALLOC(b.list, (size_t)MAXM * HEAD_LIMIT * 4);
+  ALLOC(b.sval, (size_t)MAXM * HEAD_LIMIT * 4);
   ALLOC(b.small, 5 * MAXM * 4);
   ALLOC(b.part, (size_t)2 * MAXM * HEAD_MAXGRID * 4);
   int* s = b.small.as<int>();
@@ -1407,7 +1408,10 @@ static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, in
     return G4V_E_STATE;
   }
   const int M = 1 + na + nb;
-  ARGCHK(toks && out && na >= 0 && nb >= 0 && na <= 4 && nb <= 4 && M <= MAXM, "verify_step: 0 <= na, nb <= 4");
+  // a chain of up to 7 drafts (E:1514 ENGINE_NGLEN <= 7, M <= 8 rows through attn_tile or run_mh,
+  // E:1328-1349), or a tree of two branches of up to 4 drafts each
+  ARGCHK(toks && out && na >= 0 && nb >= 0 && M <= MAXM && ((nb == 0 && na <= 7) || (na <= 4 && nb <= 4)),
+         "verify_step: a chain of 0 <= na <= 7 drafts, or 0 <= na, nb <= 4");
   ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
   ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");

@@ -533,23 +533,30 @@ void head_run(const HeadRun& r, hipStream_t st) {
   hipLaunchKernelGGL(k_head_select, dim3(std::min(256, (V + 255) / 256)), dim3(256), 0, st, r.hs, MT, V, r.active);
   mark(PT_HEAD_SELECT, 0, (double)V * 4 * MT);
   mark(PT_HEAD_RESCORE, 1, 0);
+  static bool big_lds = false;  // rows 6 to 8 stage more than 64 KB
+  if (!big_lds) {
+    const void* fns[] = {reinterpret_cast<const void*>(&k_head_rescore), reinterpret_cast<const void*>(&k_head_full<6>),
+                         reinterpret_cast<const void*>(&k_head_full<7>), reinterpret_cast<const void*>(&k_head_full<8>),
+                         reinterpret_cast<const void*>(&k_head_exc<6>), reinterpret_cast<const void*>(&k_head_exc<7>),
+                         reinterpret_cast<const void*>(&k_head_exc<8>)};
+    for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)head_lds(MAXM));
+    big_lds = true;
+  }
   hipLaunchKernelGGL(k_head_rescore, dim3(256), dim3(256), head_lds(MT), st, r.hs, r.hd, r.h, MT, r.active);
   mark(PT_HEAD_RESCORE, 0, 0);
-  const dim3 gf(grid_for(V, 32, cap));
+  const dim3 gf(grid_for(V, 32, cap)), ge(grid_for(V, 256, cap));
   mark(PT_HEAD_FULL, 1, 0);
+#define G4V_HEAD_ROWS(mt)                                                                                       \
+  case mt:                                                                                                     \
+    hipLaunchKernelGGL(k_head_full<mt>, gf, dim3(256), head_lds(mt), st, r.hs, r.hd, r.h, V, r.active);       \
+    hipLaunchKernelGGL(k_head_exc<mt>, ge, dim3(256), head_lds(mt), st, r.hs, r.hd, r.h, V, r.active);        \
+    break;
   switch (MT) {
-    case 1: hipLaunchKernelGGL(k_head_full<1>, gf, dim3(256), head_lds(1), st, r.hs, r.hd, r.h, V, r.active); break;
-    case 2: hipLaunchKernelGGL(k_head_full<2>, gf, dim3(256), head_lds(2), st, r.hs, r.hd, r.h, V, r.active); break;
-    case 3: hipLaunchKernelGGL(k_head_full<3>, gf, dim3(256), head_lds(3), st, r.hs, r.hd, r.h, V, r.active); break;
-    default: hipLaunchKernelGGL(k_head_full<4>, gf, dim3(256), head_lds(4), st, r.hs, r.hd, r.h, V, r.active); break;
+    G4V_HEAD_ROWS(1) G4V_HEAD_ROWS(2) G4V_HEAD_ROWS(3) G4V_HEAD_ROWS(4)
+    G4V_HEAD_ROWS(5) G4V_HEAD_ROWS(6) G4V_HEAD_ROWS(7) G4V_HEAD_ROWS(8)
+    default: break;
   }
-  const dim3 ge(grid_for(V, 256, cap));
-  switch (MT) {
-    case 1: hipLaunchKernelGGL(k_head_exc<1>, ge, dim3(256), head_lds(1), st, r.hs, r.hd, r.h, V, r.active); break;
-    case 2: hipLaunchKernelGGL(k_head_exc<2>, ge, dim3(256), head_lds(2), st, r.hs, r.hd, r.h, V, r.active); break;
-    case 3: hipLaunchKernelGGL(k_head_exc<3>, ge, dim3(256), head_lds(3), st, r.hs, r.hd, r.h, V, r.active); break;
-    default: hipLaunchKernelGGL(k_head_exc<4>, ge, dim3(256), head_lds(4), st, r.hs, r.hd, r.h, V, r.active); break;
-  }
+#undef G4V_HEAD_ROWS
   mark(PT_HEAD_FULL, 0, r.full_bytes);
   mark(PT_HEAD_TIE, 1, 0);
   hipLaunchKernelGGL(k_head_tie, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, r.hs, r.lut, MT, V, (int)ge.x,

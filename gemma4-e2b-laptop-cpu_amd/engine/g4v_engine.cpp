@@ -402,7 +402,7 @@ int main(int argc, char** argv) {
   e.ctx = env_int("ENGINE_CTX", 4096);
   e.pfb = env_int("ENGINE_PREFILL_BLOCK", 32);
   e.ng_n = env_int("ENGINE_NGRAM", 0);
-  e.ng_len = std::min(4, std::min(7, env_int("ENGINE_NGLEN", 3)));  // E:1514, capped at the 4-draft chain
+  e.ng_len = std::min(7, env_int("ENGINE_NGLEN", 3));  // E:1514
   e.k_draft = env_int("ENGINE_K", 3);
   e.stream = getenv("ENGINE_STREAM") != nullptr;
   e.tree = env_int("ENGINE_TREE", 0) == 1;

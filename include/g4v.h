@@ -118,7 +118,8 @@ int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
 int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes);
 
 /* ---- one verify pass (fwd E:1256-1502 + lazy head E:1453-1488 + accept E:1647-1661).
- * toks[0] confirmed token, toks[1..na] chain a, toks[na+1..na+nb] branch b (na + nb <= 7);
+ * toks[0] confirmed token, toks[1..na] chain a, toks[na+1..na+nb] branch b: a chain of up to 7
+ * drafts (nb = 0, E:1514), or two branches of up to 4 drafts each (na + nb <= 7);
  * rows sit at positions pos0.. ; nsplit = attention splits (the reference's thread count). */
 typedef struct {
   int nacc;      /* accepted drafts */

@@ -29,10 +29,11 @@ class OracleEngine:
     ENGINE_DRAFT_SAME, E:1535), forward passes set 6 / 8 only with ENGINE_ADAPTIVE_THREADS
     (E:1257), and the count persists.  i8: ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8=0."""
 
-    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False):
+    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False, nglen=3):
         from oracle import Drafter, Model
         self.orc = orc
         self.t0, self.active, self.adaptive, self.draft_same, self.cut, self.i8 = t0, t0, adaptive, draft_same, cut, i8
+        self.nglen = nglen
         self.m = Model(orc, SEED, V, NL, I, CTX)
         self.d = Drafter(orc, SEED + 1, V)
         self.keys, self.kv_len = [], 0
@@ -74,7 +75,7 @@ class OracleEngine:
             if tree:
                 k = min(k, 2)
             seq = np.array(prompt + gen, np.int32)
-            drafts = self.orc.prompt_lookup(seq, 3, 3).tolist()
+            drafts = self.orc.prompt_lookup(seq, 3, self.nglen).tolist()
             used_ng, sec1, gap1, use_sib = bool(drafts), -1, -1.0, False
             if not used_ng:  # E:1632-1645
                 tok, hh = gen[-1], hprev
@@ -213,6 +214,16 @@ def test_engine_split_counts_follow_pool(orc, cpus, extra):
                            draft_same=extra.get("ENGINE_DRAFT_SAME") != "0",
                            cut=int(extra.get("ENGINE_THREAD_CUTOFF", 192)))
     assert seen == ({4} if cpus == 4 else {6, 8}), seen
+
+
+@pytest.mark.parametrize("nglen", [5, 7])
+def test_engine_long_lookup_chains(orc, nglen):
+    """ENGINE_NGLEN up to 7 (E:1514): prompt-lookup chains of up to 7 drafts verified in one pass"""
+    rng = np.random.default_rng(13)
+    motif = rng.integers(0, V, 24).tolist()
+    requests = [((motif * 9)[:200], 30, 3, False), ((motif * 3)[:50] + [11, 12], 20, 3, False)]
+    note(f"engine lookup chains, ENGINE_NGLEN={nglen}")
+    run_protocol(orc, requests, len(requests), dict(ENGINE_NGLEN=str(nglen)), nglen=nglen)
 
 
 def test_engine_prefill_int8(orc):

@@ -116,6 +116,41 @@ def test_verify_sequence_of_steps(pair):
         conf = r.commit[r.ncommit - 1]
 
 
+@pytest.mark.parametrize("na,pos0", [(7, 600), (6, 100), (5, 30), (7, 20)])
+def test_long_chain_accepted(orc, g4v, na, pos0):
+    """chains of 5 to 7 drafts (E:1514 ENGINE_NGLEN <= 7) built from the model's own greedy
+    tokens, so that every row is accepted: 6 to 8 rows through attn_tile or run_mh (E:1328-1349),
+    the second head pass over up to 7 rows, with the full vocabulary (V = 262,144: the screen
+    overflows and the full head scores the rows)"""
+    from oracle import Model
+    Vb, NLb, Ib, CTXb = 262144, 2, 512, 1024
+    note(f"long chain na={na} pos0={pos0} V={Vb}")
+    dev = g4v.Device(0)
+    om = Model(orc, 31, Vb, NLb, Ib, CTXb)
+    try:
+        dev.model_synth(31, Vb, NLb, Ib, CTXb)
+        toks = [4242]
+        for j in range(na):  # extend the chain by the greedy token of its last row
+            om.fake_ctx(700, 77)
+            o, _ = om.verify(np.array(toks, np.int32), j, 0, pos0, 8)
+            assert o.nacc == j
+            toks.append(int(o.G[j]))
+        toks = np.array(toks, np.int32)
+        dev.fake_ctx(700, 77)
+        om.fake_ctx(700, 77)
+        r, hg = dev.verify(toks, na, 0, pos0, 8, hidden=True)
+        o, ho = om.verify(toks, na, 0, pos0, 8)
+        _compare(r, o, hg, ho)
+        assert r.nacc == na and r.ncommit == na + 1
+        note(f"fallback rows {list(r.fallback)}")
+        kc, kco = dev.read("KC", np.uint16), om.get("KC", np.uint16, NLb * CTXb * 256)
+        vc, vco = dev.read("VC", np.uint16), om.get("VC", np.uint16, NLb * CTXb * 256)
+        assert same(kc, kco) and same(vc, vco)
+    finally:
+        om.close()
+        dev.close()
+
+
 @pytest.mark.parametrize("na,pos0", [(4, 600), (3, 100), (2, 50), (0, 30), (3, 600), (4, 150)])
 def test_chain_pass_attention_paths(orc, g4v, na, pos0):
     """decode passes take the engine's attention path (E:1305 / 1328 / 1337): attn_tile for 5 rows
@@ -196,6 +231,11 @@ def test_verify_argument_errors(g4v):
             dev.verify(toks[:2], 0, 1, 100, 8)
         with pytest.raises(RuntimeError):  # past the cache
             dev.verify(toks[:4], 3, 0, 1022, 8)
+        long9 = np.arange(9, dtype=np.int32) + 5
+        with pytest.raises(RuntimeError):  # a chain of 8 drafts: 9 rows
+            dev.verify(long9, 8, 0, 100, 8)
+        with pytest.raises(RuntimeError):  # a tree branch of 5 drafts
+            dev.verify(long9[:8], 2, 5, 100, 8)
         r = dev.verify_sibling(toks[:3], 1, 100, 8)
         assert r.ncommit >= 1
     finally:

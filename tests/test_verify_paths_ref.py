@@ -43,6 +43,30 @@ def test_chain_pass_paths(orc, ref, pair, na, pos0):
         assert same(a, b), (what, first_diff(a, b))
 
 
+@pytest.mark.parametrize("na,pos0", [(7, 600), (6, 100), (5, 30), (7, 20)])
+def test_long_chain_accepted(orc, ref, pair, na, pos0):
+    """chains of 5 to 7 drafts (ENGINE_NGLEN <= 7, E:1514) taken from the model's greedy tokens,
+    accepted in full: 6 to 8 rows through attn_tile or run_mh and both of the engine's 4-row head
+    groups"""
+    om, rm = pair
+    toks = [4242]
+    for j in range(na):
+        om.fake_ctx(NFAKE, 3)
+        o, _ = om.verify(np.array(toks, np.int32), j, 0, pos0)
+        toks.append(int(o.G[j]))
+    toks = np.array(toks, np.int32)
+    om.fake_ctx(NFAKE, 3)
+    rm.fake_ctx(NFAKE, 3)
+    o, _ = om.verify(toks, na, 0, pos0)
+    r = ref.verify(toks, na, 0, pos0)
+    assert o.nacc == na and (r.nacc, r.ncommit) == (o.nacc, o.ncommit)
+    assert list(o.commit[:o.ncommit]) == list(r.commit[:r.ncommit])
+    assert list(o.G[:na + 1]) == list(r.G[:na + 1])
+    for what in ("KC", "VC"):
+        a, b = om.get(what, np.uint16, NL * CTX * 256), rm.get(what, np.uint16, NL * CTX * 256)
+        assert same(a, b), (what, first_diff(a, b))
+
+
 # the engine's sibling form (E:1634-1655): drafts toks[1..na], sibling row toks[na + 1] at RoPE
 # position pos0 + 1.  (na, pos0, allow_b): 3 rows, run_mh; 4 rows below ATT_PAR, run_mh (no
 # attn_tile with a sibling); 3 rows past ATT_PAR, split-KV; the tree hit not taken
