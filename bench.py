@@ -9,7 +9,12 @@ advance the position by the committed tokens, as the engine's run_req does.
 
 Prints one JSON line: accepted tokens per second (value), the verify-step time, the
 dominant kernel class against the HBM roofline (HIP events on the library's stream over
-the timed region) and the reference's own AVX2 kernels timed on this host as a baseline.
+the timed region), the whole step's algorithmic bytes against peak HBM (step_hbm_frac), an
+accepted-path run (drafts the model takes, in branch a and branch b in turn, so acceptance
+and KV compaction are timed), the reference's own AVX2 kernels timed on this host (one
+thread per physical core and 8 threads, each in a child process, interleaved with a second
+GPU run, with the host's read bandwidth and lscpu summary), and the long-prompt workload's
+prefill and decode times.
 
 --workload long_prompt runs the long-prompt case instead: a 6,841-token prompt (a seeded
 64-token motif repeated, 5% uniform noise tokens) prefilled through the same stack (W4A8
@@ -31,6 +36,13 @@ METRIC = "accepted tok/s + verify-step µs at 1 GPU; achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 
 V, NL, I, CTXCAP, NCTX, SEED, NA, NB, NSPLIT = 262144, 35, 6144, 4096, 2048, 1, 3, 3, 8
+H, HD = 1536, 256
+# algorithmic bytes of a step: every layer's int4 matrices with their bf16 scales (N K / 2 + N K / 16
+# for q 2048, k 256, v 256, o, gate, up, down), the head screen (int4 + scales + coef), and the
+# K and V rows of every layer up to the step's position
+LAYER_BYTES = sum(n * k // 2 + n * k // 16 for n, k in [(2048, H), (256, H), (256, H), (H, 2048), (I, H), (I, H),
+                                                         (H, I)])
+SCREEN_BYTES = V * H // 2 + V * H // 16 + V * 4
 
 
 def hbm_traffic(cls):
@@ -65,20 +77,63 @@ def drafts(step, conf):
     return np.concatenate([[conf], d]).astype(np.int32)
 
 
-def run_steps(verify, nsteps, pos0, conf, step0):
+def accepted_drafts(step, conf):
+    """drafts the model accepts: the random-init stack's greedy token repeats the row's own token,
+    so a branch of copies of the confirmed token is its greedy chain.  Even steps put that chain
+    in branch a, odd steps in branch b (committing branch b compacts its KV rows into place)."""
+    d = drafts(step, conf)
+    if step % 2 == 0:
+        d[1:1 + NA] = conf
+    else:
+        d[1 + NA:] = conf
+    return d
+
+
+def run_steps(verify, nsteps, pos0, conf, step0, draft=None):
     tokens = 0
+    draft = draft or drafts
+    stats = {"branch_b": 0, "nacc": 0}
     for s in range(nsteps):
-        r = verify(drafts(step0 + s, conf), pos0)
+        r = verify(draft(step0 + s, conf), pos0)
         tokens += r.ncommit
         pos0 += r.ncommit
         conf = r.commit[r.ncommit - 1]
+        stats["branch_b"] += r.branch
+        stats["nacc"] += r.nacc
+    run_steps.stats = stats
     return tokens, pos0, conf
 
 
-def cpu_baseline(seconds_cap=30.0):
-    """the reference's own kernels (oracle/_ref, 8 worker threads as the engine uses past
-    1,024 tokens) on this host over a bounded sample of the same workload; falls back to the
-    scalar C oracle when the harness was not built"""
+def host_topology():
+    """the host's CPUs as this process may use them: lscpu's summary, the allowed logical CPUs,
+    and one logical CPU per physical core (sysfs core / package ids)"""
+    import subprocess
+    allowed = sorted(os.sched_getaffinity(0))
+    info = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "CPU(s)", "Thread(s) per core", "Core(s) per socket", "Socket(s)"):
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    cores, seen = [], set()
+    for c in allowed:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            key = (open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip())
+        except OSError:
+            key = ("?", str(c))
+        if key not in seen:
+            seen.add(key)
+            cores.append(c)
+    return {"lscpu": info, "allowed_cpus": len(allowed), "physical_cores": len(cores)}, allowed, cores
+
+
+def cpu_baseline_run(cpus, seconds=10.0):
+    """the reference's own kernels (oracle/_ref) with its worker pool pinned to `cpus`, over a
+    bounded sample of the same verify steps; the scalar C oracle when the harness was not built"""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Model, Oracle, Ref, ref_available
 
@@ -86,13 +141,13 @@ def cpu_baseline(seconds_cap=30.0):
     m = Model(orc, SEED, V, NL, I, CTXCAP)
     m.fake_ctx(NCTX, 12345)
     if ref_available():
-        ref = Ref(threads=8)
+        ref = Ref(cpus=cpus)
         ref.bind_model(m)
         verify = lambda toks, p: ref.verify(toks, NA, NB, p)
         kind, cores = "reference", ref.threads
     else:
         verify = lambda toks, p: m.verify(toks, NA, NB, p, NSPLIT)[0]
-        kind, cores = "port", int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        kind, cores = "port", 1
     verify(drafts(0, 11), NCTX)  # warm-up
     t0 = time.perf_counter()
     tokens, steps, pos0, conf = 0, 0, NCTX, 11
@@ -100,13 +155,23 @@ def cpu_baseline(seconds_cap=30.0):
         t, pos0, conf = run_steps(verify, 1, pos0, conf, steps)
         tokens += t
         steps += 1
-        if time.perf_counter() - t0 > min(seconds_cap, 10.0) and steps >= 3:
+        if time.perf_counter() - t0 > seconds and steps >= 3:
             break
     dt = time.perf_counter() - t0
+    bw = orc.host_read_gbs(cpus)
     m.close()
-    return {"value": tokens / dt, "unit": "tok/s", "cores": cores, "kind": kind,
-            "sample": f"{steps} verify steps (2x3 tree, ctx 2048, 35 layers, V 262144) on the host, "
-                      f"{dt * 1e3 / steps:.1f} ms/step"}
+    return {"value": tokens / dt, "unit": "tok/s", "cores": cores, "kind": kind, "cpus": list(cpus),
+            "ms_per_step": round(dt * 1e3 / steps, 2), "steps": steps, "host_read_gbs": round(bw, 1)}
+
+
+def cpu_baseline_child(cpus):
+    """cpu_baseline_run in a child process (the reference pool starts once per process)"""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-only", ",".join(map(str, cpus))]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"value": None, "error": r.stderr[-400:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 LP_N, LP_ROUNDS, LP_NGRAM, LP_NGLEN, LP_CTX, LP_K, LP_DSPLIT = 6841, 256, 3, 3, 8192, 3, 6
@@ -167,6 +232,22 @@ def cpu_prefill_baseline(prompt, nrows=64):
             "sample": f"prefill of the first {nrows} prompt tokens (35 layers, W4A8, blocks of 32), {dt:.2f} s"}
 
 
+def long_prompt_summary(g4v):
+    """the long-prompt workload (one warm-up run, one timed run) for the verify line"""
+    dev = g4v.Device(0)
+    dev.model_synth(SEED, V, NL, I, LP_CTX)
+    dev.drafter_synth(SEED + 1)
+    prompt = long_prompt_tokens()
+    long_prompt_run(dev, prompt)
+    r = long_prompt_run(dev, prompt)
+    dev.close()
+    return {"workload": f"{LP_N}-token motif prompt prefilled (blocks of 32), then {LP_ROUNDS} speculative rounds",
+            "prefill_ms": round(r["prefill_s"] * 1e3, 2), "prefill_tok_s": round(LP_N / r["prefill_s"], 1),
+            "decode_ms": round(r["decode_s"] * 1e3, 2), "decode_tok_s": round(r["tokens"] / r["decode_s"], 1),
+            "tokens_per_round": round(r["tokens"] / LP_ROUNDS, 3),
+            "drafts_accepted": f"{r['accepted']}/{r['drafted']}", "mtp_rounds": r["mtp_rounds"]}
+
+
 def main_long_prompt(args, g4v):
     dev = g4v.Device(0)
     info = dev.info()
@@ -216,7 +297,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workload", choices=["verify", "long_prompt"], default="verify")
+    ap.add_argument("--cpu-only", default=None, help=argparse.SUPPRESS)  # child process of the CPU baseline
+    ap.add_argument("--no-long-prompt", action="store_true", help="skip the long-prompt sub-measurement")
     args = ap.parse_args()
+    if args.cpu_only is not None:
+        print(json.dumps(cpu_baseline_run([int(c) for c in args.cpu_only.split(",")])), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the verify path is single-GPU by design (asked for {args.gpus})",
               file=sys.stderr)
@@ -258,7 +344,18 @@ def main():
     prof = prof_all[dominant]
     timing = "hip events around each launch on the library stream, eager launches of the same steps"
 
+    # the accepted path: drafts the model takes, branch a and branch b (KV compaction) in turn
+    dev.sync()
+    nacc_steps = max(8, args.steps // 2)
+    t1 = time.perf_counter()
+    acc_tokens, pos0, conf = run_steps(verify, nacc_steps, pos0, conf, 0, accepted_drafts)
+    dev.sync()
+    dt_acc = time.perf_counter() - t1
+    acc_stats = dict(run_steps.stats)
+
     ms_per_step = dt * 1e3 / args.steps
+    step_ctx = NCTX + args.warmup + tokens // 2  # mean position of the timed steps
+    step_bytes = NL * LAYER_BYTES + SCREEN_BYTES + NL * step_ctx * HD * 2 * 2
     per_launch_ms = prof["ms"] / max(prof["launches"], 1)
     per_launch_bytes = prof["bytes"] / max(prof["launches"], 1)
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9 if per_launch_ms > 0 else 0.0
@@ -285,15 +382,43 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(dominant),
                      "launch_us": round(per_launch_ms * 1e3, 2), "bytes_per_launch": int(per_launch_bytes),
                      "timing": timing},
+        "step_hbm_frac": round(step_bytes / (ms_per_step * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "step_bytes": int(step_bytes),
+        "accepted_path": {"ms_per_step": round(dt_acc * 1e3 / nacc_steps, 4), "steps": nacc_steps,
+                          "tokens_per_step": round(acc_tokens / nacc_steps, 3),
+                          "tok_s": round(acc_tokens / dt_acc, 1), "branch_b_commits": acc_stats["branch_b"],
+                          "drafts_accepted": acc_stats["nacc"]},
         "kernel_classes_us_per_step": classes,
         "setup_s": round(setup_s, 1),
     }
-    dev.close()
     if not args.no_cpu:
+        # A (GPU) and B (CPU) interleaved: A1 above, B1 one thread per physical core, A2, B2 8 threads
         try:
-            out["cpu_baseline"] = cpu_baseline()
+            topo, allowed, cores = host_topology()
+            per_core = cores[:16]
+            eight = (cores if len(cores) >= 8 else allowed)[:8]
+            b1 = cpu_baseline_child(per_core)
+            dev.sync()
+            t2 = time.perf_counter()
+            tok2, pos0, conf = run_steps(verify, args.steps, pos0, conf, 7000)
+            dev.sync()
+            a2_ms = (time.perf_counter() - t2) * 1e3 / args.steps
+            b2 = cpu_baseline_child(eight)
+            best = b1 if (b1.get("value") or 0) >= (b2.get("value") or 0) else b2
+            out["cpu_baseline"] = {
+                "value": best.get("value"), "unit": "tok/s", "cores": best.get("cores"), "kind": best.get("kind"),
+                "sample": "bounded sample (about 10 s) of the same verify steps (2x3 tree, ctx 2048, 35 layers, "
+                          "V 262144) with the reference's own kernels (oracle/_ref) on this host",
+                "one_thread_per_core": b1, "eight_threads": b2, "host": topo,
+                "abab_gpu_ms_per_step": [round(ms_per_step, 4), round(a2_ms, 4)]}
         except Exception as e:  # the baseline is reported, never required
             out["cpu_baseline"] = {"value": None, "error": str(e)}
+    dev.close()
+    if not args.no_long_prompt:
+        try:
+            out["long_prompt"] = long_prompt_summary(g4v)
+        except Exception as e:
+            out["long_prompt"] = {"error": str(e)}
     print(json.dumps(out), flush=True)
 
 

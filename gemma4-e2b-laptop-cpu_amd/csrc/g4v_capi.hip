@@ -439,6 +439,44 @@ int g4v_w4g32_gemm(g4v_ctx* c, int h, const float* x, int M, float* y) {
   return 0;
 }
 
+int g4v_w4g32_gemm_multi(g4v_ctx* c, int nmat, const int* h, const float* x, int M, float* const* y) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(nmat >= 1 && nmat <= 3 && h && x && y && M >= 1 && M <= MAXM, "w4g32_gemm_multi: 1 to 3 matrices, 1 <= M <= 8");
+  size_t ntot = 0;
+  for (int j = 0; j < nmat; ++j) {
+    ARGCHK(h[j] >= 0 && h[j] < (int)c->mats.size() && y[j], "w4g32_gemm_multi: bad handle or output");
+    ARGCHK(c->mats[h[j]]->K == c->mats[h[0]]->K, "w4g32_gemm_multi: the matrices need the same K");
+    ntot += c->mats[h[j]]->N;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  const int K = c->mats[h[0]]->K;
+  if (c->gx.n < (size_t)MAXM * K * 4) ALLOC(c->gx, (size_t)MAXM * K * 4);
+  if (c->gy.n < (size_t)M * ntot * 4) ALLOC(c->gy, (size_t)MAXM * ntot * 4);
+  HIPCHK(hipMemcpyAsync(c->gx.p, x, (size_t)M * K * 4, hipMemcpyHostToDevice, c->st));
+  GemvArgs a{};
+  size_t off = 0;
+  for (int j = 0; j < nmat; ++j) {  // matrix j's rows [M][N_j] after those of the matrices before it
+    const Mat& m = *c->mats[h[j]];
+    a.mat[j] = m.dev();
+    a.y[j] = c->gy.as<float>() + off;
+    a.ldy[j] = m.N;
+    off += (size_t)M * m.N;
+  }
+  a.x = c->gx.as<float>();
+  a.ldx = K;
+  a.K = K;
+  gemv_passes(c, a, EPI_STORE, M);
+  HIPCHK(hipGetLastError());
+  off = 0;
+  for (int j = 0; j < nmat; ++j) {
+    const size_t n = (size_t)M * c->mats[h[j]]->N;
+    HIPCHK(hipMemcpyAsync(y[j], c->gy.as<float>() + off, n * 4, hipMemcpyDeviceToHost, c->st));
+    off += n;
+  }
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
 int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us) {
   if (!c) return G4V_E_ARG;
   ARGCHK(h >= 0 && h < (int)c->mats.size() && M >= 1 && M <= MAXM && iters > 0 && us, "w4g32_bench: bad args");

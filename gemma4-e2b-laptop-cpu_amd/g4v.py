@@ -29,6 +29,7 @@ SIGNATURES = {
     "g4v_w4_upload": (_i, [_vp, _u8p, _u16p, _i, _i]),
     "g4v_w4g32_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4g32_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_w4g32_gemm_multi": (_i, [_vp, _i, _i32p, _f32p, _i, C.POINTER(C.c_void_p)]),
     "g4v_w4g32_norm_gemm": (_i, [_vp, _i, _i, _f32p, _f32p, _f32p, _f32p, C.c_float, _i, _i, _i, _f32p, _f32p]),
     "g4v_w4a8_quant": (_i, [_vp, _f32p, _i, _i, _vp, _f32p, _i32p]),
     "g4v_w4a8_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
@@ -167,6 +168,15 @@ class Device:
         self._ok(self.L.g4v_w4g32_norm_gemm(self.h, h, mode, o, xin, _c(w1, np.float32), _c(w2, np.float32),
                                             scalar, M, rows_per_block, tile_rows, Y, X1), "w4g32_norm_gemm")
         return Y, X1
+
+    def w4g32_multi(self, mats, X):
+        X = _c(X, np.float32)
+        M = X.shape[0]
+        hs = np.array([m[0] for m in mats], np.int32)
+        Ys = [np.empty((M, m[1]), np.float32) for m in mats]
+        ptrs = (C.c_void_p * len(mats))(*[y.ctypes.data for y in Ys])
+        self._ok(self.L.g4v_w4g32_gemm_multi(self.h, len(mats), hs, X, M, ptrs), "w4g32_gemm_multi")
+        return Ys
 
     def w4g32_bench(self, mat, M, iters=100):
         us = C.c_float()

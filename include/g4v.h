@@ -40,6 +40,9 @@ int g4v_device_info(g4v_ctx* c, char* name, int cap, int* cus, int* lds_per_bloc
 int g4v_w4_upload(g4v_ctx* c, const uint8_t* w, const uint16_t* s, int N, int K);
 /* y[m][n] for M <= 8 rows of x [M][K] (fp32), bit-identical to gemm_rows_tile */
 int g4v_w4g32_gemm(g4v_ctx* c, int h, const float* x, int M, float* y);
+/* lin_multi (E:310-317): 1 to 3 matrices with the same K over the same rows in one launch (the
+ * q / k / v phase); y[j] [M][N_j] for handle h[j] */
+int g4v_w4g32_gemm_multi(g4v_ctx* c, int nmat, const int* h, const float* x, int M, float* const* y);
 /* same GEMV with x and y already on the device; times `iters` launches, returns us/launch */
 int g4v_w4g32_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
 /* the residual and RMS-norm block between two sub-blocks fused into the next product, as the

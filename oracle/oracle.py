@@ -89,11 +89,16 @@ class Oracle:
             "g4o_gen_bytes": (None, [_u64, _i64, _u8p]),
             "g4o_gen_scales": (None, [_u64, _i64, _f, _f, _u16p]),
             "g4o_gen_ints": (None, [_u64, _i64, C.c_int32, C.c_int32, _i32p]),
+            "g4h_read_gbs": (_d, [_i32p, _i, C.c_size_t, _i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+
+    def host_read_gbs(self, cpus, nbytes=1 << 30, passes=6):
+        """host read bandwidth with one pinned thread per CPU in `cpus` (host_stream.c)"""
+        return self.L.g4h_read_gbs(np.ascontiguousarray(cpus, np.int32), len(cpus), nbytes, passes)
 
     # ---- generators ----
     def stream(self, seed, tag):
@@ -341,12 +346,12 @@ class RefOut(C.Structure):
 class Ref:
     """The reference engine's own kernels (oracle/_ref/libg4ref.so) on its worker pool."""
 
-    def __init__(self, path=LIB_REF, threads=1):
+    def __init__(self, path=LIB_REF, threads=1, cpus=None):
         if not os.path.exists(path):
             raise FileNotFoundError(path)
         L = self.L = C.CDLL(path)
         sig = {
-            "ref_start": (_i, [_i]), "ref_threads": (_i, []),
+            "ref_start": (_i, [_i]), "ref_threads": (_i, []), "ref_start_cpus": (_i, [_i32p, _i]),
             "ref_w4g32": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p]),
             "ref_w4a8": (None, [_u8p, _u16p, _f32p, _i, _i, _i, _f32p, _i8p, _f32p, _i32p]),
             "ref_exp8": (None, [_f32p, _i, _f32p]), "ref_gelu8": (None, [_f32p, _i, _f32p]),
@@ -386,7 +391,10 @@ class Ref:
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        self.threads = L.ref_start(threads)
+        if cpus is not None:
+            self.threads = L.ref_start_cpus(np.ascontiguousarray(cpus, np.int32), len(cpus))
+        else:
+            self.threads = L.ref_start(threads)
         self.model = None
 
     def bind_model(self, model):

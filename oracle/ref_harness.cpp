@@ -43,6 +43,19 @@ int ref_start(int T) {
   return POOL.T;
 }
 
+// the pool on the given CPUs (the engine's ENGINE_CPUS list, E:1216-1217)
+int ref_start_cpus(const int* cpus, int n) {
+  if (g_started) return POOL.T;
+  cpu_set_t keep;
+  CPU_ZERO(&keep);
+  pthread_getaffinity_np(pthread_self(), sizeof keep, &keep);
+  std::vector<int> v(cpus, cpus + std::max(1, std::min(n, 16)));
+  POOL.start(v);
+  pthread_setaffinity_np(pthread_self(), sizeof keep, &keep);
+  g_started = true;
+  return POOL.T;
+}
+
 int ref_threads(void) { return POOL.active_count(); }
 
 // W4G32 through the engine's XP::prep + lin1 (E:180-194, 241-255, 310-317), exact-float mode

@@ -36,6 +36,22 @@ def test_w4g32_bit_exact(orc, dev, M, N, K):
     assert same(y, yo), first_diff(y, yo)
 
 
+@pytest.mark.parametrize("M,Ns", [(7, (2048, 256, 256)), (1, (1536,)), (4, (512, 1536))])
+def test_w4g32_multi_matches_single(orc, dev, M, Ns):
+    """lin_multi's phase (E:310-317): the matrices of one launch give each matrix's own product"""
+    K = 1536
+    X = orc.normal_f32(orc.stream(900 + M, 3), M * K).reshape(M, K)
+    WS = [_w4(orc, 900 + j, N, K) for j, N in enumerate(Ns)]
+    mats = [dev.w4_upload(W, S) for W, S in WS]
+    note(f"w4g32 multi M={M} N={Ns}")
+    for (W, S), y in zip(WS, dev.w4g32_multi(mats, X)):
+        yo = orc.w4g32(W, S, X)
+        assert same(y, yo), first_diff(y, yo)
+    with pytest.raises(RuntimeError):  # different K
+        W2, S2 = _w4(orc, 999, 256, 2048)
+        dev.w4g32_multi([mats[0], dev.w4_upload(W2, S2)], X)
+
+
 def test_w4g32_bf16_inputs_and_repeat(orc, dev):
     """bf16-valued activations (the o/down inputs) and a second call on the same handle"""
     W, S = _w4(orc, 77, 1536, 2048)
