@@ -15,26 +15,31 @@
  * the reference's own kernels, tests/test_oracle_vs_ref.py against those kernels live,
  * tests/test_oracle_math.py against closed forms, bounds and brute force):
  *   f2bf/r16, exp8, gelu8, sumsq, rms*, rope   golden + live + fp64 / RNE brute force
- *   rope_tables                                fp64 closed form only (the reference builds
- *                                              its tables inside main(), E:1246-1247)
+ *   rope_tables                                fp64 closed form + the reference's main() (the
+ *                                              Gemma-layout tokens below use both tables)
  *   cap, calc_thr                              golden + live + defining property by scan
  *   prep_x, w4g32_*                            golden + live + fp64 closed form, row independence
  *   w4a8_quant, w4a8_gemm                      golden + live + exact integer part
  *   exp3_codebook                              most-frequent-exponent brute force only (the
  *                                              reference computes it inside main(), E:1232-1234)
  *   exp3_count/pack/dot/gemm                   golden (pack bytes, exceptions, logits) + round trip
- *   screen_build                               soundness and tightness of the bound, scale and
- *                                              level rule (built inside main(), E:1235-1244)
+ *   screen_build                               the screen main() builds (E:1235-1244), bit for
+ *                                              bit, plus soundness and tightness of the bound
  *   head_row                                   golden survivor sets (reference scan) + screened
  *                                              greedy == brute-force full-head greedy
  *   attn_splitkv                               golden + live + fp64 softmax, LSE identity, masks
  *   attn_tile                                  live (the reference's attn_tile) + fp64 softmax
- *   attn_mh                                    fp64 softmax only (run_mh is a lambda inside main(),
- *                                              E:1338-1349): parity unpinned at the bit level
+ *   attn_mh                                    fp64 softmax + the reference's main() through the
+ *                                              Gemma-layout tokens (run_mh, E:1338-1349, is a
+ *                                              lambda inside main()); no bit-level vector of it
  *   drafter (b16 gemv, draft step)             b16 gemv live against b16_rows; the step against
  *                                              the harness composition of the engine's kernels
  *   model / verify                             golden passes through the reference's kernels
  *                                              (2 layers, V 262144), acceptance brute force
+ *   gemma (the Gemma-4-E2B layout)             FIRST / GEN tokens of the reference engine's main()
+ *                                              run unchanged on the same synthetic checkpoint
+ *                                              (tests/test_gemma_oracle.py), which change when
+ *                                              the split count or the per-layer inputs do
  * Generators (g4_rng.h) are pinned by the CRC-32 of every input the fixtures store.
  */
 #ifndef G4_ORACLE_H
@@ -123,6 +128,38 @@ void g4o_attn_tile(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M
 /* skip_lo / skip_hi (optional): row m ignores positions skip_lo[m] .. skip_hi[m] (the sibling row) */
 void g4o_attn_mh(const uint16_t* Kc, const uint16_t* Vc, int hd, int nh, int M, const float* q, int ldq,
                  const int* pos, const int* lo, const int* skip_lo, const int* skip_hi, float* out, int ldo);
+
+/* ---- the Gemma-4-E2B layer layout (g4_oracle_gemma.c): 35 layers, head_dim 256 / 512,
+ * KV sharing past layer 14, per-layer MLP widths, per-layer inputs (E:1222-1232, 1256-1405).
+ * Tensors by pointer, as the checkpoint holds them: int4 [N][K/2] + bf16 scales [N][K/32],
+ * bf16 vectors.  The per-layer embedding table is the rows ple_rows [nple][35 * 256] of the
+ * ascending ids ple_ids (other rows zero). ---- */
+typedef struct {
+  const uint8_t* w;
+  const uint16_t* s;
+  int32_t N, K;
+} g4o_q4;
+typedef struct {
+  g4o_q4 q, k, v, o, gate, up, down, pg, pp; /* k, v: layers 0..14 */
+  const uint16_t *in_ln, *post_attn, *pre_ff, *post_ff, *post_ple, *qn, *kn;
+  uint16_t scalar;
+} g4o_glayer_in;
+typedef struct {
+  g4o_glayer_in L[35];
+  g4o_q4 plproj;
+  const uint16_t *plnorm, *fnorm, *E;
+  int32_t V, nple;
+  const int32_t* ple_ids;
+  const uint16_t* ple_rows;
+} g4o_gemma_in;
+typedef struct g4o_gemma g4o_gemma;
+g4o_gemma* g4o_gemma_new(const g4o_gemma_in* in, int ctx);
+void g4o_gemma_free(g4o_gemma* g);
+/* fwd of M <= 32 rows at pos0.. (T attention splits, sibling row index or -1); hbuf [M][1536]
+ * receives the final-normed rows m >= hf (may be NULL) */
+void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, int sibling, float* hbuf, int hf);
+/* owner layer l's key (v = 0) or value (v = 1) cache [ctx][hd] */
+const uint16_t* g4o_gemma_cache(const g4o_gemma* g, int l, int v);
 
 /* ---- synthetic decoder stack + verify step (engine/gemma4_engine.cpp:1256-1502, 1617-1661) ---- */
 typedef struct g4o_model g4o_model;

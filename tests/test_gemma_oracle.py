@@ -1,0 +1,63 @@
+"""The oracle's Gemma-4-E2B layer layout (oracle/g4_oracle_gemma.c: head_dim 256 / 512 layers,
+KV sharing past layer 14, per-layer MLP widths, per-layer inputs, partial RoPE) against the
+reference engine's main() run unchanged on the same synthetic checkpoint
+(tests/golden/make_gemma_layout.py, oracle/_ref/gemma4_engine): FIRST and GEN tokens of three
+prompts whose prefill blocks and decode passes take run_mh, attn_tile and split-KV (6 splits).
+
+The fixture pins bit-level arithmetic through the tokens: planting either of two mistakes in
+the oracle -- 8 attention splits for 6, or the per-layer embedding rows dropped -- changes the
+tokens of the 196-token prompt."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+
+import gemma_layout as gl  # noqa: E402
+
+FX = os.path.join(HERE, "golden", "gemma_layout.npz")
+
+
+@pytest.fixture(scope="module")
+def ckpt(orc, tmp_path_factory):
+    d = str(tmp_path_factory.mktemp("gemma_ckpt"))
+    gl.write_checkpoint(orc, d)
+    fx = np.load(FX)
+    prompts = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])
+    gens = np.split(fx["gens"], np.cumsum(fx["gen_lens"])[:-1])
+    return d, fx, prompts, gens
+
+
+@pytest.mark.parametrize("i", [0, 1, 2])
+def test_gemma_layout_matches_reference_engine(orc, ckpt, i):
+    d, fx, prompts, gens = ckpt
+    go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
+    try:
+        gen = gl.run_req_k0(go, [int(t) for t in prompts[i]], int(fx["nnew"][0]), int(fx["cpus"][0]))
+    finally:
+        go.close()
+    assert gen[0] == int(fx["first"][i])
+    assert gen == [int(t) for t in gens[i]], (gen, list(gens[i]))
+
+
+def test_gemma_fixture_detects_planted_mistakes(orc, ckpt):
+    d, fx, prompts, gens = ckpt
+    want = [int(t) for t in gens[2]]
+    go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
+    try:  # 8 splits where the engine ran 6
+        assert gl.run_req_k0(go, [int(t) for t in prompts[2]], int(fx["nnew"][0]), 8) != want
+    finally:
+        go.close()
+    ids = gl.PLE_IDS
+    gl.PLE_IDS = [1]  # the per-layer embedding rows dropped
+    try:
+        go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
+        try:
+            assert gl.run_req_k0(go, [int(t) for t in prompts[2]], int(fx["nnew"][0]), int(fx["cpus"][0])) != want
+        finally:
+            go.close()
+    finally:
+        gl.PLE_IDS = ids
