@@ -1,0 +1,157 @@
+// g4v_attn_hd.hip -- split-KV attention (E:743-877) and its merge (E:1019-1059) for a head dim
+// D other than 256: the 512-wide global layers of the Gemma-4-E2B layout.  Same arithmetic as
+// g4v_attn.hip, in a plainer form (global layers are one in five):
+//   split t covers keys [kmin + t len / T, kmin + (t + 1) len / T);
+//   score_p = hsum8(s0 + s1), s0 / s1 the two 8-lane FMA chains over the head dim in steps of
+//     16 (lane l, chain s: elements 16 tt + 8 s + l in tt order);
+//   w_p = exp8(score_p - max) over the allowed positions; l = sum of w_p in position order;
+//     o_i = fma chain of w_p v_p,i in position order (disallowed positions skipped);
+//   merge: sc_t = libm expf(max_t - M0), l = sum_t (double) l_t sc_t,
+//     out = r16((fma chain over splits of o_t sc_t) * (float)(1 / l)).
+// One block per (split, row, head); q rows arrive normalised and rotated (k_pf_qkv).
+#include "g4v_layer.h"
+
+namespace g4v {
+
+__constant__ uint64_t c_expf_tab_hd[32] = G4V_EXPF_TABLE;
+
+constexpr int AHD_THREADS = 256;
+
+template <int D>
+__global__ __launch_bounds__(AHD_THREADS) void k_attn_split_d(const uint16_t* __restrict__ KC,
+                                                              const uint16_t* __restrict__ VC,
+                                                              const float* __restrict__ q, int ldq, AttnGeom g,
+                                                              float* __restrict__ po, float* __restrict__ pm,
+                                                              float* __restrict__ pl) {
+  __shared__ __align__(16) float qs[D];       // the head's query in key-slot order (kc_slot_d)
+  __shared__ float sw[ATT_SPLIT_MAX];         // scores, then weights, of the split's positions
+  __shared__ float red[AHD_THREADS / 64];
+  const int t = blockIdx.x, m = blockIdx.y, h = blockIdx.z, T = g.T;
+  const int M = g.M;
+  if (m >= M) return;  // uniform
+  const int len = g.kmax - g.kmin + 1;
+  const int c0 = g.kmin + (int)((long)t * len / T), c1 = g.kmin + (int)((long)(t + 1) * len / T);
+  const int lo = g.lo[m], pos = g.pos[m], sl = g.skip_lo[m], sh = g.skip_hi[m];
+  auto allowed = [=](int p) { return p >= lo && p <= pos && !(p >= sl && p <= sh); };  // E:740
+  for (int e = threadIdx.x; e < D; e += AHD_THREADS) qs[kc_slot_d<D>(e)] = q[(size_t)m * ldq + h * D + e];
+  __syncthreads();
+  // scores: 8 lanes per position, 32 positions per pass
+  const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
+  for (int p0 = c0; p0 < c1; p0 += AHD_THREADS / 8) {
+    const int p = min(p0 + ps, c1 - 1);  // the tail's extra lanes repeat the last position
+    const uint16_t* kr = KC + (size_t)p * D + l * (D / 8);
+    float s[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float a = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < D / 16; tt += 8) {
+        const uint4 kk = *reinterpret_cast<const uint4*>(kr + c * (D / 16) + tt);
+        const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          a = fmaf(qs[l * (D / 8) + c * (D / 16) + tt + 2 * k], as_f32(kw[k] << 16), a);
+          a = fmaf(qs[l * (D / 8) + c * (D / 16) + tt + 2 * k + 1], as_f32(kw[k] & 0xFFFF0000u), a);
+        }
+      }
+      s[c] = a;
+    }
+    const float v = hsum8_lanes(s[0] + s[1]);
+    if (l == 0 && p0 + ps < c1) sw[p - c0] = v;
+  }
+  __syncthreads();
+  // the max over the allowed positions (order free)
+  float mx = -1e30f;
+  for (int p = c0 + threadIdx.x; p < c1; p += AHD_THREADS)
+    if (allowed(p)) mx = fmaxf(mx, sw[p - c0]);
+  for (int s = 1; s < 64; s <<= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < AHD_THREADS / 64; ++w) mx = fmaxf(mx, red[w]);
+  __syncthreads();
+  for (int p = c0 + threadIdx.x; p < c1; p += AHD_THREADS)
+    sw[p - c0] = allowed(p) ? exp8(sw[p - c0] - mx) : 0.f;  // E:820
+  __syncthreads();
+  // o_i in position order over the allowed positions; every thread also forms l (E:821)
+  constexpr int DT = D / AHD_THREADS;  // dims per thread
+  float o[DT], lsum = 0.f;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) o[d] = 0.f;
+  for (int p = c0; p < c1; ++p) {
+    if (!allowed(p)) continue;  // uniform
+    const float w = sw[p - c0];
+    lsum = lsum + w;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = fmaf(w, bf2f(VC[vc_index_d<D>(p, threadIdx.x + d * AHD_THREADS)]), o[d]);
+  }
+  const size_t k = ((size_t)t * M + m) * NQ + h;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) po[k * D + threadIdx.x + d * AHD_THREADS] = o[d];
+  if (threadIdx.x == 0) {
+    pm[k] = mx;
+    pl[k] = lsum;  // 0 when the split holds no allowed position: the merge then skips it
+  }
+}
+
+// E:1019-1059, one block per (row m, head h), one thread per dim; out staged (the o-projection
+// input, staged_index) with its group sums when gs is given, else plain [M][ldo]
+template <int D>
+__global__ __launch_bounds__(D) void k_attn_merge_d(const float* __restrict__ po, const float* __restrict__ pm,
+                                                    const float* __restrict__ pl, int M, int T, float* __restrict__ out,
+                                                    int ldo, float* __restrict__ gs) {
+  __shared__ __align__(16) float ys[D];
+  const int m = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+  float M0 = -1e30f;
+  for (int t = 0; t < T; ++t) {
+    const size_t k = ((size_t)t * M + m) * NQ + h;
+    if (pl[k] > 0) M0 = (M0 < pm[k]) ? pm[k] : M0;
+  }
+  double l = 0;
+  float acc = 0.f;
+  for (int t = 0; t < T; ++t) {
+    const size_t k = ((size_t)t * M + m) * NQ + h;
+    if (pl[k] > 0) {
+      const float sc = libm_expf_neg(pm[k] - M0, c_expf_tab_hd);
+      l = fma((double)pl[k], (double)sc, l);
+      acc = fmaf(po[k * D + i], sc, acc);
+    }
+  }
+  const float y = r16(acc * (float)(1.0 / l));
+  if (!gs) {
+    out[(size_t)m * ldo + h * D + i] = y;
+    return;
+  }
+  ys[i] = y;
+  __syncthreads();
+  float* xs = out + (size_t)m * ldo + h * D;
+  if (i < D / 4) {  // float4 index 8 g + j of the head's groups g (staged_index)
+    const float* b = ys + (i >> 3) * 32;
+    const int j = i & 7;
+    reinterpret_cast<float4*>(xs)[i] = make_float4(b[2 * j], b[16 + 2 * j], b[2 * j + 1], b[17 + 2 * j]);
+  }
+  if (i < D / 32) {
+    const float4* b4 = reinterpret_cast<const float4*>(ys + i * 32);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 r = b4[k];
+      s = (((s + r.x) + r.y) + r.z) + r.w;
+    }
+    gs[(size_t)m * (ldo / 32) + h * (D / 32) + i] = s;
+  }
+}
+
+int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g, int hd,
+                        float* po, float* pm, float* pl, float* out, int ldo, float* gs, hipStream_t st) {
+  if (hd != 512 || g.M < 1 || g.M > MAXM || g.T < 1 || g.T > MAXT) return -1;
+  const int len = g.kmax - g.kmin + 1;
+  if (len < 1 || (len + g.T - 1) / g.T + 1 > ATT_SPLIT_MAX) return -1;
+  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(g.T, g.M, NQ), dim3(AHD_THREADS), 0, st, KC, VC, q, ldq, g, po, pm,
+                     pl);
+  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(g.M, NQ), dim3(512), 0, st, po, pm, pl, g.M, g.T, out, ldo, gs);
+  return 0;
+}
+
+}  // namespace g4v

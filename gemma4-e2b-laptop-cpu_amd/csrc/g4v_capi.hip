@@ -103,6 +103,7 @@ struct g4v_ctx {
   VerifyResultDev* res_host = nullptr;
   // attention standalone
   DBuf ak, av, aq, ao;
+  DBuf po5, pm5, pl5;  // split partials at head dim 512
   // prefill rows (plain [row][K] layouts), quantised activations, attention score scratch
   DBuf pfx, pfa, pfq, pfk, pfv, pfatt, pfo, pfg, pfu, pfact, pfxq, pfsx, pfcorr, pfs, pftok, pfh;
   int pf_rows = 0, pf_I = 0;  // rows and FFN width the buffers were sized for
@@ -641,15 +642,66 @@ int g4v_w4a8_bench(g4v_ctx* c, int h, int M, int iters, float* us) {
 // ---------------------------------------------------------------------------------------
 // attention
 // ---------------------------------------------------------------------------------------
+// head dim 512 (the global layers of the Gemma-4-E2B layout): g4v_attn_hd.hip
+static int attn_splitkv_512(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int M, const float* q,
+                            const int* pos, const int* lo, const int* skip_lo, const int* skip_hi, int kmin, int kmax,
+                            int nsplit, float* out) {
+  constexpr int D = 512;
+  AttnGeom g{};
+  g.M = M;
+  g.kmin = kmin;
+  g.kmax = kmax;
+  g.T = nsplit;
+  for (int m = 0; m < M; ++m) {
+    ARGCHK(pos[m] < npos, "attn_splitkv: pos beyond npos");
+    g.pos[m] = pos[m];
+    g.lo[m] = lo[m];
+    g.skip_lo[m] = skip_lo[m];
+    g.skip_hi[m] = skip_hi[m];
+  }
+  HIPCHK(hipSetDevice(c->device));
+  const size_t kvb = (size_t)kv_cap(npos) * D * 2;
+  if (c->ak.n < kvb) ALLOC(c->ak, kvb);
+  if (c->av.n < kvb) ALLOC(c->av, kvb);
+  if (c->aq.n < (size_t)MAXM * NQ * D * 4) ALLOC(c->aq, (size_t)MAXM * NQ * D * 4);
+  if (c->ao.n < (size_t)MAXM * NQ * D * 4) ALLOC(c->ao, (size_t)MAXM * NQ * D * 4);
+  if (c->po5.n < (size_t)MAXT * MAXM * NQ * D * 4) {
+    ALLOC(c->po5, (size_t)MAXT * MAXM * NQ * D * 4);
+    ALLOC(c->pm5, (size_t)MAXT * MAXM * NQ * 4);
+    ALLOC(c->pl5, (size_t)MAXT * MAXM * NQ * 4);
+  }
+  {  // the caller's [position][512] rows into the device cache layout
+    std::vector<uint16_t> kd((size_t)kv_cap(npos) * D, 0), vd((size_t)kv_cap(npos) * D, 0);
+    for (int p = 0; p < npos; ++p)
+      for (int e = 0; e < D; ++e) {
+        kd[kc_index_d<D>(p, e)] = Kc[(size_t)p * D + e];
+        vd[vc_index_d<D>(p, e)] = Vc[(size_t)p * D + e];
+      }
+    HIPCHK(hipMemcpy(c->ak.p, kd.data(), kvb, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(c->av.p, vd.data(), kvb, hipMemcpyHostToDevice));
+  }
+  HIPCHK(hipMemcpyAsync(c->aq.p, q, (size_t)M * NQ * D * 4, hipMemcpyHostToDevice, c->st));
+  ARGCHK(launch_attn_geom_hd(c->ak.as<uint16_t>(), c->av.as<uint16_t>(), c->aq.as<float>(), NQ * D, g, D,
+                             c->po5.as<float>(), c->pm5.as<float>(), c->pl5.as<float>(), c->ao.as<float>(), NQ * D,
+                             nullptr, c->st) == 0,
+         "attn_splitkv: shape not served at head dim 512");
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(out, c->ao.p, (size_t)M * NQ * D * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
 int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
                      const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
                      int kmin, int kmax, int nsplit, float* out) {
   if (!c) return G4V_E_ARG;
-  ARGCHK(hd == HD && nh == NQ, "attn_splitkv: hd must be 256 and nh 8");
+  ARGCHK((hd == HD || hd == 512) && nh == NQ, "attn_splitkv: hd must be 256 or 512 and nh 8");
   ARGCHK(M >= 1 && M <= MAXM && nsplit >= 1 && nsplit <= MAXT, "attn_splitkv: 1 <= M <= 8, 1 <= nsplit <= 16");
   ARGCHK(kmin >= 0 && kmax < npos && kmin <= kmax, "attn_splitkv: need 0 <= kmin <= kmax < npos");
   const int len = kmax - kmin + 1, per = (len + nsplit - 1) / nsplit;
-  ARGCHK(per <= attn_pmax(), "attn_splitkv: more positions per split than the split buffer holds");
+  ARGCHK(per <= (hd == HD ? attn_pmax() : ATT_SPLIT_MAX - 1),
+         "attn_splitkv: more positions per split than the split buffer holds");
+  if (hd == 512) return attn_splitkv_512(c, Kc, Vc, npos, M, q, pos, lo, skip_lo, skip_hi, kmin, kmax, nsplit, out);
   AttnGeom g{};
   g.M = M;
   g.kmin = kmin;

@@ -26,6 +26,16 @@ __host__ __device__ inline size_t vc_index(int p, int i) {
   return (size_t)(p >> 5) * (32 * HD) + (size_t)i * 32 + (p & 31);
 }
 inline int kv_cap(int npos) { return (npos + 31) / 32 * 32; }  // positions of a layer's cache slab
+// the same layouts for a head dim D (256 or 512: the global layers of the Gemma-4-E2B layout):
+// element e = 16 tt + 8 s + l (tt < D / 16) of a key row at slot l * D / 8 + s * D / 16 + tt
+template <int D>
+__host__ __device__ inline int kc_slot_d(int e) { return (e & 7) * (D / 8) + ((e >> 3) & 1) * (D / 16) + (e >> 4); }
+template <int D>
+__host__ __device__ inline size_t kc_index_d(int p, int e) { return (size_t)p * D + kc_slot_d<D>(e); }
+template <int D>
+__host__ __device__ inline size_t vc_index_d(int p, int i) {
+  return (size_t)(p >> 5) * (32 * D) + (size_t)i * 32 + (p & 31);
+}
 constexpr int HEAD_LIMIT = 30000;  // E:1416 LIM: more survivors -> full head
 
 // An int4 G32 matrix on the device.  wr: weights re-laid for the exact-order GEMV

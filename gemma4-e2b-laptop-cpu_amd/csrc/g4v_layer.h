@@ -102,16 +102,18 @@ struct PfGeom {
 };
 void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, float sqh, float* x, float* a, int M,
                      hipStream_t st);
-// q [M][2048] normed + rotated in place; k, v [M][256] normed into the cache rows P0 ..; row sib
-// (>= 0) is rotated at position P0 + 1 (the sibling row)
+// q [M][8 hd] normed + rotated in place; k, v [M][hd] normed into the cache rows P0 .. (own = 0:
+// q only, the layer reads another layer's cache); row sib (>= 0) is rotated at position P0 + 1
+// (the sibling row).  hd 256 or 512; cs / sn the layer type's RoPE tables [ctx][hd / 2].
 void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
-                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib = -1);
+                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib = -1,
+                   int hd = HD, int own = 1);
 // score scratch (floats) of M rows starting at position Pb
 long long pf_score_floats(int M, int Pb, int sliding);
 // attn_tile / run_mh attention of segment rows [r0, r0 + M): q [n][2048] (row r at r), att likewise
 // staged: att rows in the staged GEMV input layout (staged_index) instead of plain
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
-                    int r0, int M, int sliding, hipStream_t st, bool staged = false);
+                    int r0, int M, int sliding, hipStream_t st, bool staged = false, int hd = HD);
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st);
 void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStream_t st);
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
@@ -161,6 +163,12 @@ struct AttnGeom {
 // nh query heads (a multiple of 2, at most 8) of q rows [M][ldq]; partials keep the 8-head layout
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);
+// the same for head dim 512 (g4v_attn_hd.hip), 8 heads, partials [T][M][8][512]; out plain
+// [M][ldo] or, with gs, staged (staged_index) with its group sums [M][ldo / 32].  Returns -1
+// (nothing launched) for a shape it does not serve: a split longer than ATT_SPLIT_MAX keys.
+constexpr int ATT_SPLIT_MAX = 4096;
+int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g, int hd,
+                        float* po, float* pm, float* pl, float* out, int ldo, float* gs, hipStream_t st);
 // the same with the geometry read from device memory (M rows and T splits fixed by the launch)
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
                           int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);

@@ -73,26 +73,28 @@ __global__ __launch_bounds__(ROW_THREADS) void k_pf_embed(const uint16_t* __rest
 
 // E:1291-1303 / 1307-1324 for one row: the 8 query heads and k normed with their weights, v
 // without, all rounded to bf16 values; NeoX RoPE on q and k at position P; k, v to the cache
-__global__ __launch_bounds__(HD) void k_pf_qkv(float* __restrict__ q, const float* __restrict__ k,
-                                               const float* __restrict__ v, const float* __restrict__ qn,
-                                               const float* __restrict__ kn, const float* __restrict__ cs,
-                                               const float* __restrict__ sn, uint16_t* __restrict__ KC,
-                                               uint16_t* __restrict__ VC, int P0, int sib) {
+// (own = 0: a layer that reads another layer's cache, E:1288, 1304: q only).  D: the head dim.
+template <int D>
+__global__ __launch_bounds__(D) void k_pf_qkv(float* __restrict__ q, const float* __restrict__ k,
+                                              const float* __restrict__ v, const float* __restrict__ qn,
+                                              const float* __restrict__ kn, const float* __restrict__ cs,
+                                              const float* __restrict__ sn, uint16_t* __restrict__ KC,
+                                              uint16_t* __restrict__ VC, int P0, int sib, int own) {
   constexpr int NV = NQ + 2;
-  __shared__ float xv[NV][HD];
+  __shared__ float xv[NV][D];
   __shared__ double part[NV][16];
   __shared__ float rinv[NV];
   const int m = blockIdx.x, e = threadIdx.x, P = P0 + m;
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) xv[h][e] = q[(size_t)m * NQ * HD + h * HD + e];
-  xv[NQ][e] = k[(size_t)m * HD + e];
-  xv[NQ + 1][e] = v[(size_t)m * HD + e];
+  for (int h = 0; h < NQ; ++h) xv[h][e] = q[(size_t)m * NQ * D + h * D + e];
+  xv[NQ][e] = own ? k[(size_t)m * D + e] : 0.f;
+  xv[NQ + 1][e] = own ? v[(size_t)m * D + e] : 0.f;
   __syncthreads();
   if (e < NV * 16) {  // ss_avx2 order (E:326-343): lane t16 sums x[16 s + t16]^2 over s
     const int row = e >> 4, t16 = e & 15;
     double s = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < D / 16; ++i) {
       const double d = (double)xv[row][16 * i + t16];
       s = fma(d, d, s);
     }
@@ -104,75 +106,82 @@ __global__ __launch_bounds__(HD) void k_pf_qkv(float* __restrict__ q, const floa
     double a[4];
 #pragma unroll
     for (int l = 0; l < 4; ++l) a[l] = (p[l] + p[4 + l]) + (p[8 + l] + p[12 + l]);
-    rinv[e] = rms_inv((a[0] + a[2]) + (a[1] + a[3]), HD);
+    rinv[e] = rms_inv((a[0] + a[2]) + (a[1] + a[3]), D);
   }
   __syncthreads();
   float y[NV];
 #pragma unroll
   for (int h = 0; h < NQ; ++h) y[h] = r16((xv[h][e] * rinv[h]) * qn[e]);
-  y[NQ] = r16((xv[NQ][e] * rinv[NQ]) * kn[e]);
+  y[NQ] = own ? r16((xv[NQ][e] * rinv[NQ]) * kn[e]) : 0.f;
   y[NQ + 1] = r16(xv[NQ + 1][e] * rinv[NQ + 1]);
   __syncthreads();
 #pragma unroll
   for (int h = 0; h < NQ + 1; ++h) xv[h][e] = y[h];
   __syncthreads();
-  // E:394-402 NeoX halves: out_i = fma(u, c, -(w s)) and out_{i+128} = fma(w, c, u s)
-  const int i2 = e & (HD / 2 - 1), PR = m == sib ? P0 + 1 : P;  // E:1292 the sibling's RoPE position
-  const float c = cs[(size_t)PR * (HD / 2) + i2], sv = sn[(size_t)PR * (HD / 2) + i2];
+  // E:394-402 NeoX halves: out_i = fma(u, c, -(w s)) and out_{i+D/2} = fma(w, c, u s)
+  const int i2 = e & (D / 2 - 1), PR = m == sib ? P0 + 1 : P;  // E:1292 the sibling's RoPE position
+  const float c = cs[(size_t)PR * (D / 2) + i2], sv = sn[(size_t)PR * (D / 2) + i2];
   auto rot = [&](const float* yy) {
-    return e < HD / 2 ? fmaf(yy[e], c, -(yy[e + HD / 2] * sv)) : fmaf(yy[e], c, yy[e - HD / 2] * sv);
+    return e < D / 2 ? fmaf(yy[e], c, -(yy[e + D / 2] * sv)) : fmaf(yy[e], c, yy[e - D / 2] * sv);
   };
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) q[(size_t)m * NQ * HD + h * HD + e] = rot(xv[h]);
-  KC[kc_index(P, e)] = f2bf(rot(xv[NQ]));
-  VC[vc_index(P, e)] = f2bf(y[NQ + 1]);
+  for (int h = 0; h < NQ; ++h) q[(size_t)m * NQ * D + h * D + e] = rot(xv[h]);
+  if (own) {
+    KC[kc_index_d<D>(P, e)] = f2bf(rot(xv[NQ]));
+    VC[vc_index_d<D>(P, e)] = f2bf(y[NQ + 1]);
+  }
 }
 
 // scores of one row against a span of 256 positions: lane = position, all 8 heads per lane (the
 // key row is read and widened once for the 8 heads); the query heads sit in LDS in slot order
 // (kc_slot), so every lane of a wave reads the same LDS word (broadcast)
 constexpr int PF_SPAN = 256;
+template <int D>
 __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, const uint16_t* __restrict__ KC,
                                                    float* __restrict__ S, PfGeom g, int r0, int sliding) {
-  __shared__ __align__(16) float qs[NQ][HD];
+  __shared__ __align__(16) float qs[NQ][D];
   // the last rows (longest ranges) first, so that the long blocks do not trail the grid
   const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_row_lo(r, P, g, sliding);
   const int len = P - lo + 1;
   const int sp0 = lo + blockIdx.y * PF_SPAN;
   if (sp0 > P) return;  // uniform
   const bool tiled = pf_tiled(r, g);
-  for (int idx = threadIdx.x; idx < NQ * HD; idx += 256) {
-    const int h = idx >> 8, e = idx & (HD - 1);
-    qs[h][kc_slot(e)] = q[(size_t)r * NQ * HD + idx];
+  for (int idx = threadIdx.x; idx < NQ * D; idx += 256) {
+    const int h = idx / D, e = idx % D;
+    qs[h][kc_slot_d<D>(e)] = q[(size_t)r * NQ * D + idx];
   }
   __syncthreads();
   const int p = sp0 + threadIdx.x;
   if (p > P) return;  // no barrier follows
-  const uint16_t* kr = KC + (size_t)p * HD;
+  const uint16_t* kr = KC + (size_t)p * D;
+  constexpr int CL = D / 16;  // steps of one chain
   float vv[NQ][8];
   if (tiled) {
-    // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...]: slots l*32 + s*16 + tt, tt in order;
-    // vv[h][l] = chain (l, 0) + chain (l, 1)
+    // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...]: slots l*D/8 + s*D/16 + tt, tt in
+    // order; vv[h][l] = chain (l, 0) + chain (l, 1)
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       float ch[NQ][2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int b = l * 32 + s * 16;
-        const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b), k1 = *reinterpret_cast<const uint4*>(kr + b + 8);
-        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-        float kf[16];
+        const int b = l * (D / 8) + s * CL;
+        float kf[CL];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          kf[2 * c] = as_f32(kw[c] << 16);
-          kf[2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+        for (int c8 = 0; c8 < CL / 8; ++c8) {
+          const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c8);
+          const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            kf[8 * c8 + 2 * c] = as_f32(kw[c] << 16);
+            kf[8 * c8 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+          }
         }
 #pragma unroll
         for (int h = 0; h < NQ; ++h) {
           const float4* q4 = reinterpret_cast<const float4*>(&qs[h][b]);
           float a = 0.f;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
+          for (int c = 0; c < CL / 4; ++c) {
             const float4 qq = q4[c];
             a = fmaf(qq.x, kf[4 * c], a);
             a = fmaf(qq.y, kf[4 * c + 1], a);
@@ -186,28 +195,28 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
       for (int h = 0; h < NQ; ++h) vv[h][l] = ch[h][0] + ch[h][1];
     }
   } else {
-    // chain l over t = 0..31 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l:
-    // slots l*32 + (t & 1)*16 + (t >> 1)
+    // chain l over t = 0 .. D/8 - 1 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l:
+    // slots l*D/8 + (t & 1)*D/16 + (t >> 1)
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
-      const int b = l * 32;
-      float kf[32];
+      const int b = l * (D / 8);
+      float kf[D / 8];
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) {
-        const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c4);
+      for (int c8 = 0; c8 < D / 64; ++c8) {
+        const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c8);
         const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          kf[8 * c4 + 2 * c] = as_f32(kw[c] << 16);
-          kf[8 * c4 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+          kf[8 * c8 + 2 * c] = as_f32(kw[c] << 16);
+          kf[8 * c8 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
         }
       }
 #pragma unroll
       for (int h = 0; h < NQ; ++h) {
         float a = 0.f;
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
-          const int sl = (t & 1) * 16 + (t >> 1);
+        for (int t = 0; t < D / 8; ++t) {
+          const int sl = (t & 1) * CL + (t >> 1);
           a = fmaf(qs[h][b + sl], kf[sl], a);
         }
         vv[h][l] = a;
@@ -225,6 +234,7 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
 // go to LDS; the value rows are read 8 positions (16 bytes of a dim) at a time where positions
 // are 8-aligned, one at a time at the edges of the range
 constexpr int PF_CP = 256;  // positions per weight chunk (4 per lane)
+template <int D>
 __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
                                                     float* __restrict__ att, PfGeom g, int r0, int sliding,
                                                     ExpfTab tab, int staged) {
@@ -269,14 +279,15 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
   float dh[NQ];  // run_mh: the sums, on every lane
 #pragma unroll
   for (int h = 0; h < NQ; ++h) dh[h] = __shfl(den, h);
-  float O[NQ][4];
+  constexpr int DL = D / 64;  // dims per lane
+  float O[NQ][DL];
 #pragma unroll
   for (int h = 0; h < NQ; ++h)
 #pragma unroll
-    for (int d = 0; d < 4; ++d) O[h][d] = 0.f;
-  // dim 4 lane + d of position p: vcol + d * 32 + (p >> 5) * 32 HD + (p & 31)
-  const uint16_t* vcol = VC + (size_t)(4 * lane) * 32;
-  auto vat = [&](int p, int d) { return vcol + d * 32 + (size_t)(p >> 5) * (32 * HD) + (p & 31); };
+    for (int d = 0; d < DL; ++d) O[h][d] = 0.f;
+  // dim DL lane + d of position p: vcol + d * 32 + (p >> 5) * 32 D + (p & 31)
+  const uint16_t* vcol = VC + (size_t)(DL * lane) * 32;
+  auto vat = [&](int p, int d) { return vcol + d * 32 + (size_t)(p >> 5) * (32 * D) + (p & 31); };
   float sreg[PF_CP / 64][NQ];  // scores of this lane's positions of the next chunk
 #pragma unroll
   for (int k = 0; k < PF_CP / 64; ++k)
@@ -307,26 +318,26 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
     const int pa = lo + c0, pe = pa + cn;  // positions [pa, pe) of this chunk
     const int a8 = min((pa + 7) & ~7, pe), e8 = max(pe & ~7, a8);
     for (int p = pa; p < a8; ++p) {        // leading positions up to an 8-boundary
-      float v[4];
+      float v[DL];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) v[d] = bf2f(*vat(p, d));
+      for (int d = 0; d < DL; ++d) v[d] = bf2f(*vat(p, d));
 #pragma unroll
       for (int h = 0; h < NQ; ++h) {
         const float ww = w[h][p - pa];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) O[h][d] = fmaf(ww, v[d], O[h][d]);
+        for (int d = 0; d < DL; ++d) O[h][d] = fmaf(ww, v[d], O[h][d]);
       }
     }
     for (int p = a8; p < e8; p += 8) {     // 8 positions of each of the lane's 4 dims
-      uint4 vq[4];
+      uint4 vq[DL];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) vq[d] = *reinterpret_cast<const uint4*>(vat(p, d));
+      for (int d = 0; d < DL; ++d) vq[d] = *reinterpret_cast<const uint4*>(vat(p, d));
       const int j0 = p - pa;
 #pragma unroll
       for (int t2 = 0; t2 < 4; ++t2) {     // positions j0 + 2 t2, j0 + 2 t2 + 1
-        float va[4], vb[4];
+        float va[DL], vb[DL];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
+        for (int d = 0; d < DL; ++d) {
           const uint32_t u = t2 == 0 ? vq[d].x : (t2 == 1 ? vq[d].y : (t2 == 2 ? vq[d].z : vq[d].w));
           va[d] = as_f32(u << 16);
           vb[d] = as_f32(u & 0xFFFF0000u);
@@ -335,21 +346,21 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
         for (int h = 0; h < NQ; ++h) {
           const float wa = w[h][j0 + 2 * t2], wb = w[h][j0 + 2 * t2 + 1];  // j0 may be odd
 #pragma unroll
-          for (int d = 0; d < 4; ++d) O[h][d] = fmaf(wa, va[d], O[h][d]);
+          for (int d = 0; d < DL; ++d) O[h][d] = fmaf(wa, va[d], O[h][d]);
 #pragma unroll
-          for (int d = 0; d < 4; ++d) O[h][d] = fmaf(wb, vb[d], O[h][d]);
+          for (int d = 0; d < DL; ++d) O[h][d] = fmaf(wb, vb[d], O[h][d]);
         }
       }
     }
     for (int p = e8; p < pe; ++p) {        // trailing positions
-      float v[4];
+      float v[DL];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) v[d] = bf2f(*vat(p, d));
+      for (int d = 0; d < DL; ++d) v[d] = bf2f(*vat(p, d));
 #pragma unroll
       for (int h = 0; h < NQ; ++h) {
         const float ww = w[h][p - pa];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) O[h][d] = fmaf(ww, v[d], O[h][d]);
+        for (int d = 0; d < DL; ++d) O[h][d] = fmaf(ww, v[d], O[h][d]);
       }
     }
     if (tiled && lane < NQ)
@@ -357,19 +368,21 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
     __syncthreads();
   }
   const float inv = tiled ? 1.0f / den : 1.0f;  // lanes 0..7
-  float* orow = att + (size_t)r * NQ * HD;
+  float* orow = att + (size_t)r * NQ * D;
 #pragma unroll
   for (int h = 0; h < NQ; ++h) {
     const float ih = __shfl(inv, h);
-    float v[4];
+    float v[DL];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) v[d] = tiled ? r16(O[h][d] * ih) : r16(O[h][d]);
-    const int n0 = h * HD + 4 * lane;
+    for (int d = 0; d < DL; ++d) v[d] = tiled ? r16(O[h][d] * ih) : r16(O[h][d]);
+    const int n0 = h * D + DL * lane;
     if (staged) {  // the staged GEMV input layout of the o projection (staged_index)
 #pragma unroll
-      for (int d = 0; d < 4; ++d) orow[staged_index(n0 + d)] = v[d];
+      for (int d = 0; d < DL; ++d) orow[staged_index(n0 + d)] = v[d];
     } else {
-      *reinterpret_cast<float4*>(orow + n0) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+      for (int d4 = 0; d4 < DL; d4 += 4)
+        *reinterpret_cast<float4*>(orow + n0 + d4) = make_float4(v[d4], v[d4 + 1], v[d4 + 2], v[d4 + 3]);
     }
   }
 }
@@ -440,8 +453,12 @@ void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, flo
   hipLaunchKernelGGL(k_pf_embed, dim3(M), dim3(ROW_THREADS), 0, st, E, toks, in_ln, sqh, x, a);
 }
 void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
-                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib) {
-  hipLaunchKernelGGL(k_pf_qkv, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib);
+                   const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib, int hd,
+                   int own) {
+  if (hd == 512)
+    hipLaunchKernelGGL(k_pf_qkv<512>, dim3(M), dim3(512), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib, own);
+  else
+    hipLaunchKernelGGL(k_pf_qkv<HD>, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib, own);
 }
 long long pf_score_floats(int M, int Pb, int sliding) {
   const long long R = M;
@@ -450,14 +467,19 @@ long long pf_score_floats(int M, int Pb, int sliding) {
   return 8 * (c * (Pb + 1) + c * (c - 1) / 2 + (R - c) * 512);
 }
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
-                    int r0, int M, int sliding, hipStream_t st, bool staged) {
+                    int r0, int M, int sliding, hipStream_t st, bool staged, int hd) {
   const int Plast = g.pos0 + r0 + M - 1;
   // the sibling's window (from pos0 + 1) can be longer than 512 by the rows it skips
   const int maxlen = sliding ? std::min(Plast + 1, g.sib >= 0 ? Plast - g.pos0 + 511 : 512) : Plast + 1;
   const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
-  hipLaunchKernelGGL(k_pf_scores, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
   ExpfTab tab{G4V_EXPF_TABLE};
-  hipLaunchKernelGGL(k_pf_attn_out, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+  if (hd == 512) {
+    hipLaunchKernelGGL(k_pf_scores<512>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
+    hipLaunchKernelGGL(k_pf_attn_out<512>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+  } else {
+    hipLaunchKernelGGL(k_pf_scores<HD>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
+    hipLaunchKernelGGL(k_pf_attn_out<HD>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+  }
 }
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st) {
   hipLaunchKernelGGL(k_pf_post_attn, dim3(M), dim3(ROW_THREADS), 0, st, o, x, a, w1, w2);

@@ -71,7 +71,8 @@ int g4v_w4a8_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
 /* ---- split-KV attention: attn_task + attn_merge (E:743-877, E:1019-1059) with the
  * reference's split geometry [kmin + t*len/T, kmin + (t+1)*len/T).  Kc, Vc: [npos][hd] bf16;
  * q: [M][nh*hd] fp32; per row: pos, lo, skip_lo, skip_hi (attn_allowed, E:740).
- * out: [M][nh*hd] fp32, rounded to bf16 values.  hd == 256, nh == 8, M <= 8, nsplit <= 16. */
+ * out: [M][nh*hd] fp32, rounded to bf16 values.  hd 256 or 512 (the global layers of the
+ * Gemma-4-E2B layout, E:1225), nh == 8, M <= 8, nsplit <= 16. */
 int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
                      const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
                      int kmin, int kmax, int nsplit, float* out);

@@ -130,8 +130,8 @@ def test_norm_gemm_bit_exact(orc, dev, mode, kind, M, rpb, tr):
     assert same(y, ye), first_diff(y, ye)
 
 
-def _attn_case(orc, ctx, M, T, window, tree, seed):
-    hd, nh = 256, 8
+def _attn_case(orc, ctx, M, T, window, tree, seed, hd=256):
+    nh = 8
     Kc = orc.normal_bf16(orc.stream(seed, 1), (ctx + 8) * hd)
     Vc = orc.normal_bf16(orc.stream(seed, 2), (ctx + 8) * hd)
     q = orc.normal_f32(orc.stream(seed, 3), M * nh * hd, 1 / 16).reshape(M, nh * hd)
@@ -162,6 +162,18 @@ ATTN_CASES = [(512, 4, 8, False, False), (2048, 4, 8, False, False), (6841, 4, 8
 def test_attn_splitkv_bit_exact(orc, dev, ctx, M, T, window, tree):
     args = _attn_case(orc, ctx, M, T, window, tree, seed=ctx * 31 + M)
     note(f"attn ctx={ctx} M={M} T={T} window={window} tree={tree}")
+    out = dev.attn(*args)
+    ref = orc.attn(*args)
+    assert same(out, ref), first_diff(out, ref)
+
+
+@pytest.mark.parametrize("ctx,M,T,tree", [(700, 1, 8, False), (2048, 4, 6, False), (6841, 4, 8, False),
+                                          (2048, 7, 8, True), (40, 3, 6, False), (1000, 8, 16, True)])
+def test_attn_splitkv_hd512_bit_exact(orc, dev, ctx, M, T, tree):
+    """the 512-wide global layers of the Gemma-4-E2B layout (E:1225): the same split geometry,
+    chains over 32 steps"""
+    args = _attn_case(orc, ctx, M, T, False, tree, seed=ctx * 17 + M, hd=512)
+    note(f"attn hd=512 ctx={ctx} M={M} T={T} tree={tree}")
     out = dev.attn(*args)
     ref = orc.attn(*args)
     assert same(out, ref), first_diff(out, ref)

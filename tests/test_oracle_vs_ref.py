@@ -21,10 +21,13 @@ def test_w4g32_w4a8_live(orc, ref, M, N, K, seed):
     assert same(orc.w4a8(W, S, X), y8)
 
 
-@pytest.mark.parametrize("ctx,M,T,window,sib", [(1024, 4, 8, True, True), (4097, 3, 16, False, False),
-                                                (64, 1, 8, False, False), (9, 4, 8, False, True)])
-def test_attention_live(orc, ref, ctx, M, T, window, sib):
-    hd, nh = 256, 8
+@pytest.mark.parametrize("ctx,M,T,window,sib,hd", [(1024, 4, 8, True, True, 256), (4097, 3, 16, False, False, 256),
+                                                   (64, 1, 8, False, False, 256), (9, 4, 8, False, True, 256),
+                                                   (2100, 4, 6, False, True, 512), (700, 1, 8, False, False, 512),
+                                                   (33, 2, 6, False, False, 512)])
+def test_attention_live(orc, ref, ctx, M, T, window, sib, hd):
+    """attn_task + attn_merge (E:743-877, 1019-1059) at head dim 256 and 512 (global layers)"""
+    nh = 8
     Kc = orc.normal_bf16(orc.stream(ctx, 11), (ctx + 8) * hd)
     Vc = orc.normal_bf16(orc.stream(ctx, 12), (ctx + 8) * hd)
     q = orc.normal_f32(orc.stream(ctx, 13), M * nh * hd, 1 / 16).reshape(M, nh * hd)
