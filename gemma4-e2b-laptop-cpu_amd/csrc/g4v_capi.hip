@@ -104,6 +104,25 @@ struct g4v_ctx {
   // attention standalone
   DBuf ak, av, aq, ao;
   DBuf po5, pm5, pl5;  // split partials at head dim 512
+  // the Gemma-4-E2B layout (g4v_model_create_gemma): per-layer geometry, the per-layer-input
+  // branch, the owners' caches and the row buffers of its passes
+  bool gemma = false;
+  struct GmLayer {
+    int hd = 256, own = 1, I = 0;
+    Mat pg, pp;   // per_layer_input_gate [256][1536], per_layer_projection [1536][256]
+    DBuf nv;      // in_ln, post_attn, pre_ff, post_ff, post_ple [1536 each], qn, kn [hd each]
+    float scalar = 1.0f;
+    bool normed = false;
+  };
+  GmLayer gm[35];
+  Mat gm_plproj;                  // per_layer_model_projection [8960][1536]
+  DBuf gm_plnorm, gm_ple;         // per_layer_projection_norm [256]; the table [V][8960] bf16
+  DBuf gm_kv;                     // layer l < 15: K at gm_koff[l], V at gm_voff[l], [kvcap][hd] each
+  size_t gm_koff[15] = {}, gm_voff[15] = {};
+  DBuf gm_rope;                   // global layers' RoPE: cos, sin [ctxcap][256]
+  DBuf gm_rows, gm_tok, gm_s;     // row buffers of a pass (32 rows), its tokens, score scratch
+  int gm_Imax = 0;
+  bool gm_plready = false;
   // prefill rows (plain [row][K] layouts), quantised activations, attention score scratch
   DBuf pfx, pfa, pfq, pfk, pfv, pfatt, pfo, pfg, pfu, pfact, pfxq, pfsx, pfcorr, pfs, pftok, pfh;
   int pf_rows = 0, pf_I = 0;  // rows and FFN width the buffers were sized for
@@ -981,6 +1000,7 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   drop_graphs(c);  // every model and step buffer is reallocated below
   c->model_ready = false;
   c->head_ready = false;
+  c->gemma = false;
   c->V = V;
   c->NL = NL;
   c->I = I;
@@ -1145,8 +1165,14 @@ int g4v_model_set_embed(g4v_ctx* c, const uint16_t* E) {
   return 0;
 }
 
+static int gm_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint16_t* s);
+
 int g4v_model_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint16_t* s) {
   if (!c || !w || !s) return G4V_E_ARG;
+  if (c->gemma) {
+    HIPCHK(hipSetDevice(c->device));
+    return gm_set_matrix(c, l, j, w, s);
+  }
   ARGCHK(l >= 0 && l < (int)c->L.size() && j >= 0 && j < 7, "model_set_matrix: layer or matrix index out of range");
   HIPCHK(hipSetDevice(c->device));
   drop_graphs(c);  // the matrix buffers are reallocated
@@ -1293,6 +1319,24 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
         for (int e = 0; e < HD; ++e)
           o[((size_t)ll * c->ctxcap + p) * HD + e] = slab[key ? kc_index(p, e) : vc_index(p, e)];
     }
+    return 0;
+  } else if ((what[0] == 'G' && (what[1] == 'K' || what[1] == 'V')) && c->gemma &&
+             std::sscanf(what + 2, "%d", &l) == 1 && l >= 0 && l < 15) {
+    // the Gemma layout: owner layer l's cache as the reference's [position][hd] rows
+    const bool key = what[1] == 'K';
+    const int hd = c->gm[l].hd;
+    nb = (size_t)c->ctxcap * hd * 2;
+    if (nbytes) *nbytes = nb;
+    if (!dst) return 0;
+    ARGCHK(cap >= nb, "model_read: buffer too small");
+    std::vector<uint16_t> dev((size_t)c->kvcap * hd);
+    HIPCHK(hipMemcpy(dev.data(), c->gm_kv.as<uint16_t>() + (key ? c->gm_koff[l] : c->gm_voff[l]), dev.size() * 2,
+                     hipMemcpyDeviceToHost));
+    uint16_t* o = static_cast<uint16_t*>(dst);
+    for (int p = 0; p < c->ctxcap; ++p)
+      for (int e = 0; e < hd; ++e)
+        o[(size_t)p * hd + e] = dev[hd == 512 ? (key ? kc_index_d<512>(p, e) : vc_index_d<512>(p, e))
+                                              : (key ? kc_index(p, e) : vc_index(p, e))];
     return 0;
   } else if (!std::strcmp(what, "fnorm") && c->fnorm.p) {
     src = c->fnorm.p;
@@ -1476,6 +1520,8 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
 
 static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, int b_ok,
                        g4v_verify_result* out, float* hidden);
+static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, int b_ok,
+                     g4v_verify_result* out, float* hidden);
 
 int g4v_verify_step(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, g4v_verify_result* out,
                     float* hidden) {
@@ -1491,6 +1537,7 @@ int g4v_verify_sibling(g4v_ctx* c, const int* toks, int nd, int pos0, int nsplit
 
 static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, int b_ok,
                        g4v_verify_result* out, float* hidden) {
+  if (c && c->gemma) return gm_verify(c, toks, na, nb, pos0, nsplit, b_ok, out, hidden);
   if (!c) return G4V_E_ARG;
   std::string missing;
   if (!c->model_ready || !model_complete(c, &missing)) {
@@ -1701,9 +1748,388 @@ static void pf_segment(g4v_ctx* c, const PfGeom& g, int r0, int M, bool i8, bool
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// The Gemma-4-E2B layer layout (E:1222-1232, fwd E:1256-1405): 35 layers of head dim 256
+// (l % 5 != 4, window 512) or 512 (global: RoPE theta 1e6 on the first quarter of the
+// frequencies, E:1246-1247), k / v projections and caches in layers 0..14 only (layer l >= 15
+// reads the cache of layer 13 or 14, E:1251), each layer's MLP width, and the per-layer-input
+// branch (ple_fused_task E:615-660 once per pass, pg_fused_task E:405-443 + per_layer_projection
+// + post_per_layer_input_norm per layer, E:1379-1404).  A pass of M <= 32 rows runs as the
+// prefill path runs a block (plain row layouts, the exact-float GEMV or, for prompt blocks with
+// g4v_set_prefill_int8, W4A8), eagerly; the head and acceptance are the verify pass's own.
+// ---------------------------------------------------------------------------------------
+namespace {
+constexpr int GM_NL = 35, GM_PD = 256, GM_ROWS = 32, GM_PLN = GM_NL * GM_PD;
+int gm_hd(int l) { return l % 5 != 4 ? 256 : 512; }
+int gm_owner(int l) { return l < 15 ? l : (l % 5 != 4 ? 13 : 14); }  // E:1251
+
+struct GmRows {
+  float *x, *a, *o, *q, *k, *v, *att, *g, *u, *act, *pr, *pli, *pgv, *g2;
+};
+GmRows gm_rows(g4v_ctx* c) {
+  float* f = c->gm_rows.as<float>();
+  const size_t R = GM_ROWS, I = c->gm_Imax;
+  GmRows r;
+  r.x = f;
+  r.a = r.x + R * H;
+  r.o = r.a + R * H;
+  r.q = r.o + R * H;
+  r.k = r.q + R * NQ * 512;
+  r.v = r.k + R * 512;
+  r.att = r.v + R * 512;
+  r.g = r.att + R * NQ * 512;
+  r.u = r.g + R * I;
+  r.act = r.u + R * I;
+  r.pr = r.act + R * I;
+  r.pli = r.pr + R * GM_PLN;
+  r.pgv = r.pli + R * GM_PLN;
+  r.g2 = r.pgv + R * GM_PD;
+  return r;
+}
+size_t gm_rows_floats(int Imax) {
+  const size_t R = GM_ROWS;
+  return R * (3 * H + 2 * NQ * 512 + 2 * 512 + 3 * (size_t)Imax + 2 * GM_PLN + 2 * GM_PD);
+}
+
+// matrix j of layer l: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 per_layer_input_gate, 8 per_layer_projection
+void gm_shape(const g4v_ctx* c, int l, int j, int* N, int* K) {
+  const int hd = gm_hd(l), I = c->gm[l].I;
+  const int n[9] = {NQ * hd, hd, hd, H, I, I, H, GM_PD, H}, k[9] = {H, H, H, NQ * hd, H, H, I, H, GM_PD};
+  *N = n[j];
+  *K = k[j];
+}
+Mat& gm_mat(g4v_ctx* c, int l, int j) { return j < 7 ? c->L[l]->m[j] : (j == 7 ? c->gm[l].pg : c->gm[l].pp); }
+
+bool gm_complete(const g4v_ctx* c, std::string* what) {
+  if (!c->head_ready) {
+    *what = "embedding / head not set";
+    return false;
+  }
+  if (!c->gm_plready) {
+    *what = "per_layer_model_projection not set";
+    return false;
+  }
+  for (int l = 0; l < GM_NL; ++l) {
+    for (int j = 0; j < 9; ++j)
+      if ((j != 1 && j != 2) || c->gm[l].own)
+        if (!gm_mat(const_cast<g4v_ctx*>(c), l, j).wr.p) {
+          *what = "matrix " + std::to_string(j) + " of layer " + std::to_string(l) + " not set";
+          return false;
+        }
+    if (!c->gm[l].normed) {
+      *what = "norms of layer " + std::to_string(l) + " not set";
+      return false;
+    }
+  }
+  return true;
+}
+
+// fwd (E:1256-1405) of the M rows whose tokens are in gm_tok, at positions pos0 .. pos0 + M - 1,
+// row sib (>= 0) the sibling row (E:1292, 1340-1345); i8: W4A8 linear layers (M >= 2).  Rows
+// m >= hrow (hrow >= 0) leave their final-normed state in h [M - hrow][1536] and |h| in hn.
+void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool i8, float* h, float* hn) {
+  hipStream_t st = c->st;
+  const GmRows R = gm_rows(c);
+  const float sqh = std::sqrt((float)H);
+  const int* tok = c->gm_tok.as<int>();
+  i8 = i8 && M >= 2;  // lin_multi's rule (E:311)
+  launch_pf_embed(c->E.as<uint16_t>(), tok, c->gm[0].nv.as<float>(), sqh, R.x, R.a, M, st);  // E:1262-1267
+  pf_lin(c, c->gm_plproj, R.x, M, R.pr, i8, true);                                            // E:615-660
+  launch_gm_ple(R.pr, tok, c->gm_ple.as<uint16_t>(), c->gm_plnorm.as<float>(), R.pli, M, st);
+  for (int l = 0; l < GM_NL; ++l) {
+    const auto& G = c->gm[l];
+    const Layer& lay = *c->L[l];
+    const int hd = G.hd, ty = hd == 512, own = G.own, ol = gm_owner(l);
+    const bool sliding = !ty;
+    const float* nv = G.nv.as<float>();
+    const float *in_ln = nv, *post_attn = nv + H, *pre_ff = nv + 2 * H, *post_ff = nv + 3 * H, *post_ple = nv + 4 * H,
+                *qn = nv + 5 * H, *kn = nv + 5 * H + hd;
+    (void)in_ln;
+    uint16_t* KCo = c->gm_kv.as<uint16_t>() + c->gm_koff[ol];
+    uint16_t* VCo = c->gm_kv.as<uint16_t>() + c->gm_voff[ol];
+    pf_lin(c, lay.m[0], R.a, M, R.q, i8, true);  // E:1287-1288
+    if (own) {
+      pf_lin(c, lay.m[1], R.a, M, R.k, i8, false);
+      pf_lin(c, lay.m[2], R.a, M, R.v, i8, false);
+    }
+    const float* cs = ty ? c->gm_rope.as<float>() : c->rope.as<float>();
+    const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
+    launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own);
+    if (M <= 4 && pos0 + M > 192) {  // E:1305-1327
+      AttnGeom ag{};
+      ag.M = M;
+      ag.kmax = pos0 + M - 1;
+      ag.kmin = ag.kmax;
+      ag.T = nsplit;
+      for (int m = 0; m < M; ++m) {
+        const int rp = m == sib ? pos0 + 1 : pos0 + m;
+        ag.pos[m] = pos0 + m;
+        ag.lo[m] = sliding ? std::max(0, rp - 511) : 0;
+        ag.skip_lo[m] = m == sib ? pos0 + 1 : 1;
+        ag.skip_hi[m] = m == sib ? pos0 + m - 1 : 0;
+        ag.kmin = std::min(ag.kmin, ag.lo[m]);
+      }
+      if (hd == 512)
+        (void)launch_attn_geom_hd(KCo, VCo, R.q, NQ * 512, ag, 512, c->po5.as<float>(), c->pm5.as<float>(),
+                                  c->pl5.as<float>(), R.att, NQ * 512, nullptr, st);
+      else
+        launch_attn_geom(KCo, VCo, R.q, NQ * HD, ag, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), R.att,
+                         NQ * HD, st);
+    } else {  // attn_tile (M >= 4 past 64 keys, no sibling) or run_mh: one block of M rows
+      launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, PfGeom{M, pos0, M, sib}, 0, M, sliding, st, false,
+                     hd);
+    }
+    pf_lin(c, lay.m[3], R.att, M, R.o, i8, true);                       // E:1356
+    launch_pf_post_attn(R.o, R.x, R.a, post_attn, pre_ff, M, st);       // E:1358-1361
+    pf_lin(c, lay.m[4], R.a, M, R.g, i8, true);                         // E:1363-1371
+    pf_lin(c, lay.m[5], R.a, M, R.u, i8, false);
+    launch_pf_act(R.g, R.u, R.act, (size_t)M * G.I, st);
+    pf_lin(c, lay.m[6], R.act, M, R.o, i8, true);                                               // E:1373
+    launch_pf_post_ff(R.o, R.x, R.a, post_ff, nullptr, nullptr, 1.0f, nullptr, -1, M, st);      // E:1375-1377
+    pf_lin(c, G.pg, R.x, M, R.pgv, i8, true);                                                   // E:1379-1384
+    launch_gm_pg_act(R.pgv, R.pli, l, M, R.g2, st);
+    pf_lin(c, G.pp, R.g2, M, R.o, i8, true);                                                    // E:1386
+    const bool last = l + 1 == GM_NL;                                                           // E:1387-1404
+    launch_pf_post_ff(R.o, R.x, R.a, post_ple, last ? nullptr : c->gm[l + 1].nv.as<float>(), c->fnorm.as<float>(),
+                      G.scalar, h, last ? hrow : -1, M, st, hn);
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int g4v_model_create_gemma(g4v_ctx* c, int V, const int* mlp, int ctxcap) {
+  if (!c || !mlp) return G4V_E_ARG;
+  ARGCHK(V > 0 && ctxcap > 8 && ctxcap <= 131072, "model_create_gemma: need V > 0 and 8 < ctxcap <= 131072");
+  int Imax = 0;
+  for (int l = 0; l < GM_NL; ++l) {
+    ARGCHK(mlp[l] > 0 && mlp[l] % 256 == 0 && mlp[l] <= 16384, "model_create_gemma: MLP widths % 256 == 0, <= 16384");
+    Imax = std::max(Imax, mlp[l]);
+  }
+  HIPCHK(hipSetDevice(c->device));
+  int r = model_alloc(c, V, GM_NL, 256, ctxcap);
+  if (r) return r;
+  c->gemma = true;
+  c->gm_Imax = Imax;
+  c->gm_plready = false;
+  size_t off = 0;
+  for (int l = 0; l < GM_NL; ++l) {
+    auto& G = c->gm[l];
+    for (DBuf* b : {&G.pg.wr, &G.pg.s, &G.pg.tw, &G.pg.ts, &G.pg.a8w, &G.pg.a8s, &G.pp.wr, &G.pp.s, &G.pp.tw, &G.pp.ts,
+                    &G.pp.a8w, &G.pp.a8s})
+      b->reset();
+    G.normed = false;
+    G.scalar = 1.0f;
+    G.hd = gm_hd(l);
+    G.own = l < 15;
+    G.I = mlp[l];
+    ALLOC(G.nv, (size_t)(5 * H + 2 * G.hd) * 4);
+    HIPCHK(hipMemsetAsync(G.nv.p, 0, G.nv.n, c->st));
+    if (G.own) {
+      c->gm_koff[l] = off;
+      off += (size_t)c->kvcap * G.hd;
+      c->gm_voff[l] = off;
+      off += (size_t)c->kvcap * G.hd;
+    }
+  }
+  ALLOC(c->gm_kv, off * 2);
+  HIPCHK(hipMemsetAsync(c->gm_kv.p, 0, c->gm_kv.n, c->st));
+  ALLOC(c->gm_ple, (size_t)V * GM_PLN * 2);
+  HIPCHK(hipMemsetAsync(c->gm_ple.p, 0, c->gm_ple.n, c->st));
+  ALLOC(c->gm_plnorm, GM_PD * 4);
+  {  // E:1246-1247, the global type: theta 1e6 on the first quarter of the 256 frequencies
+    std::vector<float> rt((size_t)2 * ctxcap * 256);
+    for (int p = 0; p < ctxcap; ++p)
+      for (int j = 0; j < 256; ++j) {
+        const double inv = j < 64 ? 1.0 / std::pow(1e6, (2.0 * j) / 512) : 0.0;
+        const double ang = p * inv;
+        rt[(size_t)p * 256 + j] = (float)std::cos(ang);
+        rt[(size_t)ctxcap * 256 + (size_t)p * 256 + j] = (float)std::sin(ang);
+      }
+    ALLOC(c->gm_rope, rt.size() * 4);
+    HIPCHK(hipMemcpy(c->gm_rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice));
+  }
+  ALLOC(c->gm_rows, gm_rows_floats(Imax) * 4);
+  ALLOC(c->gm_tok, GM_ROWS * 4);
+  ALLOC(c->gm_s, (size_t)pf_score_floats(GM_ROWS, ctxcap, 0) * 4);
+  const size_t Kmax = std::max<size_t>(NQ * 512, std::max<size_t>(H, Imax)), Rp = (size_t)w4a8_mpad(GM_ROWS);
+  ALLOC(c->pfxq, Rp * Kmax * 2);  // W4A8 operands of a prompt block
+  ALLOC(c->pfsx, (Kmax / 32) * Rp * 4);
+  ALLOC(c->pfcorr, (Kmax / 32) * Rp * 4);
+  ALLOC(c->po5, (size_t)MAXT * MAXM * NQ * 512 * 4);
+  ALLOC(c->pm5, (size_t)MAXT * MAXM * NQ * 4);
+  ALLOC(c->pl5, (size_t)MAXT * MAXM * NQ * 4);
+  c->pf_rows = 0;  // the synthetic stack's prefill buffers are not sized for this layout
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->model_ready = true;
+  return 0;
+}
+
+int g4v_model_set_norms_gemma(g4v_ctx* c, int l, const float* const nv[7], float scalar) {
+  if (!c || !nv) return G4V_E_ARG;
+  ARGCHK(c->gemma && l >= 0 && l < GM_NL, "model_set_norms_gemma: no Gemma layout, or layer out of range");
+  auto& G = c->gm[l];
+  for (int t = 0; t < 7; ++t)
+    ARGCHK(nv[t] != nullptr || (t == 6 && !G.own), "model_set_norms_gemma: null norm vector");
+  HIPCHK(hipSetDevice(c->device));
+  for (int t = 0; t < 7; ++t) {
+    if (!nv[t]) continue;
+    const size_t n = t < 5 ? H : G.hd, o = t < 5 ? (size_t)t * H : 5 * H + (size_t)(t - 5) * G.hd;
+    HIPCHK(hipMemcpyAsync(G.nv.as<float>() + o, nv[t], n * 4, hipMemcpyHostToDevice, c->st));
+  }
+  HIPCHK(hipStreamSynchronize(c->st));
+  G.scalar = scalar;
+  G.normed = true;
+  return 0;
+}
+
+int g4v_model_set_ple(g4v_ctx* c, const uint8_t* w, const uint16_t* s, const float* plnorm) {
+  if (!c || !w || !s || !plnorm) return G4V_E_ARG;
+  ARGCHK(c->gemma, "model_set_ple: no Gemma layout (g4v_model_create_gemma first)");
+  HIPCHK(hipSetDevice(c->device));
+  DBuf tmp;
+  ALLOC(tmp, (size_t)GM_PLN * H / 2);
+  HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)GM_PLN * H / 2, hipMemcpyHostToDevice, c->st));
+  int r = upload_w4(c, c->gm_plproj, tmp.as<uint8_t>(), s, false, GM_PLN, H);
+  if (r) return r;
+  HIPCHK(hipMemcpyAsync(c->gm_plnorm.p, plnorm, GM_PD * 4, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->gm_plready = true;
+  return 0;
+}
+
+int g4v_model_set_ple_rows(g4v_ctx* c, int tok0, int n, const uint16_t* rows) {
+  if (!c || !rows) return G4V_E_ARG;
+  ARGCHK(c->gemma && tok0 >= 0 && n >= 0 && (long long)tok0 + n <= c->V, "model_set_ple_rows: rows outside the table");
+  HIPCHK(hipSetDevice(c->device));
+  HIPCHK(hipMemcpy(c->gm_ple.as<uint16_t>() + (size_t)tok0 * GM_PLN, rows, (size_t)n * GM_PLN * 2,
+                   hipMemcpyHostToDevice));
+  return 0;
+}
+
+}  // extern "C"
+
+static int gm_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint16_t* s) {
+  ARGCHK(l >= 0 && l < GM_NL && j >= 0 && j < 9, "model_set_matrix: layer or matrix index out of range");
+  ARGCHK(c->gm[l].own || (j != 1 && j != 2), "model_set_matrix: layers past 14 have no k / v projection (E:1251)");
+  int N, K;
+  gm_shape(c, l, j, &N, &K);
+  DBuf tmp;
+  ALLOC(tmp, (size_t)N * K / 2);
+  HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)N * K / 2, hipMemcpyHostToDevice, c->st));
+  int r = upload_w4(c, gm_mat(c, l, j), tmp.as<uint8_t>(), s, false, N, K);
+  if (r) return r;
+  HIPCHK(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+// the verify pass on the Gemma layout: a chain of up to 7 drafts or the sibling form (nb = 1,
+// at most 4 rows); fwd as one block, then the head passes and acceptance of the verify pass
+static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int nsplit, int b_ok,
+                     g4v_verify_result* out, float* hidden) {
+  std::string what;
+  if (!c->model_ready || !gm_complete(c, &what)) {
+    c->err = "verify_step: " + (c->model_ready ? what : std::string("no model"));
+    return G4V_E_STATE;
+  }
+  const int M = 1 + na + nb;
+  ARGCHK(toks && out && na >= 0 && nb >= 0 && na <= 7 && nb <= 1 && M <= MAXM && (nb == 0 || M <= 4),
+         "verify_step: the Gemma layout takes a chain of up to 7 drafts or the sibling form");
+  ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
+  ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");
+  ARGCHK((pos0 + M + nsplit - 1) / nsplit + 1 <= std::min(attn_pmax(), ATT_SPLIT_MAX - 1),
+         "verify_step: context too long for nsplit");
+  for (int i = 0; i < M; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "verify_step: token id out of range");
+  HIPCHK(hipSetDevice(c->device));
+  hipStream_t st = c->st;
+  StepDev& s = *c->step_host;
+  std::memset(&s, 0, sizeof s);
+  s.M = M;
+  s.na = na;
+  s.nb = nb;
+  s.pos0 = pos0;
+  s.b_ok = b_ok;
+  for (int r = 0; r < M; ++r) {
+    s.toks[r] = toks[r];
+    s.rope[r] = r <= na ? pos0 + r : pos0 + 1;
+    s.skip_lo[r] = r <= na ? 1 : pos0 + 1;
+    s.skip_hi[r] = r <= na ? 0 : pos0 + na;
+  }
+  HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks, (size_t)M * 4, hipMemcpyHostToDevice, st));
+  const int sib = nb == 1 ? na + 1 : -1;
+  gm_forward(c, M, pos0, nsplit, sib, 0, false, c->h.as<float>(), c->hn.as<float>());
+  const StepDev* sp = c->stepd.as<StepDev>();
+  VerifyResultDev* res = c->resd.as<VerifyResultDev>();
+  head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);  // E:1453-1488
+  launch_branch(sp, c->hb1.hs.best, c->h.as<float>(), c->hn.as<float>(), c->h2.as<float>(), c->hn2.as<float>(), res,
+                st);
+  HeadRun h2 = head_args(c, c->hb2, c->h2.as<float>(), c->hn2.as<float>(), std::max(1, std::max(na, nb)),
+                         &res->hcount);
+  h2.pass2 = 1;
+  head_run(h2, st);
+  launch_accept(sp, c->hb1.hs.best, c->hb2.hs.best, c->hb1.hs.cnt, c->hb2.hs.cnt, res, nullptr, nullptr, 0, 0, st);
+  for (int l = 0; l < 15; ++l)  // E:1651: the sibling's rows move into place in every owner cache
+    launch_kv_compact_hd(sp, res, c->gm_kv.as<uint16_t>() + c->gm_koff[l], c->gm_kv.as<uint16_t>() + c->gm_voff[l],
+                         c->gm[l].hd, st);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
+  const VerifyResultDev& r = *c->res_host;
+  out->nacc = r.nacc;
+  out->branch = r.branch;
+  out->ncommit = r.ncommit;
+  for (int i = 0; i < 8; ++i) {
+    out->commit[i] = r.commit[i];
+    out->G[i] = r.G[i];
+    out->fallback[i] = r.fallback[i];
+    out->nsurv[i] = r.nsurv[i];
+  }
+  c->last_hrow = r.hrows[r.ncommit - 1];
+  if (hidden)
+    HIPCHK(hipMemcpy(hidden, c->h.as<float>() + (size_t)c->last_hrow * H, H * 4, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+// run_req's prompt loop (E:1594-1599) on the Gemma layout: blocks of pfb rows from pos0, the last
+// block's last row to the head
+static int gm_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int nsplit, int* G0, float* hidden) {
+  std::string what;
+  if (!c->model_ready || !gm_complete(c, &what)) {
+    c->err = "prefill: " + (c->model_ready ? what : std::string("no model"));
+    return G4V_E_STATE;
+  }
+  ARGCHK(toks && n >= 1 && pos0 >= 0 && (long long)pos0 + n <= c->ctxcap, "prefill: positions beyond the cache");
+  ARGCHK(pfb >= 1 && pfb <= GM_ROWS, "prefill: 1 <= pfb <= 32 (the engine's row block, MM = 32)");
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT, "prefill: 1 <= nsplit <= 16");
+  ARGCHK((pos0 + n + nsplit - 1) / nsplit + 1 <= std::min(attn_pmax(), ATT_SPLIT_MAX - 1),
+         "prefill: more positions per split than the split buffer holds");
+  for (int i = 0; i < n; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "prefill: token id outside the vocabulary");
+  HIPCHK(hipSetDevice(c->device));
+  for (int b = 0; b < n; b += pfb) {
+    const int M = std::min(pfb, n - b);
+    const bool last = b + M == n;
+    HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks + b, (size_t)M * 4, hipMemcpyHostToDevice, c->st));
+    gm_forward(c, M, pos0 + b, nsplit, -1, last ? M - 1 : -1, c->pf_i8, c->h.as<float>(), c->hn.as<float>());
+  }
+  HIPCHK(hipGetLastError());
+  std::vector<float> h(H);
+  HIPCHK(hipMemcpyAsync(h.data(), c->h.p, H * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->last_hrow = 0;  // the prompt's last row: the state a drafter chain would start from
+  if (hidden) std::memcpy(hidden, h.data(), H * 4);
+  if (G0) {
+    int ns = 0, fb = 0;
+    return g4v_head_argmax(c, h.data(), 1, G0, &ns, &fb);
+  }
+  return 0;
+}
+
 extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int nsplit, int* G0,
                            float* hidden) {
   if (!c) return G4V_E_ARG;
+  if (c->gemma) return gm_prefill(c, toks, n, pos0, pfb, nsplit, G0, hidden);
   std::string what;
   if (!c->model_ready || !model_complete(c, &what)) {
     c->err = "prefill: " + (c->model_ready ? what : std::string("no model"));

@@ -117,7 +117,16 @@ void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, floa
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st);
 void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStream_t st);
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
-                       const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st);
+                       const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st,
+                       float* hn = nullptr);
+// the per-layer-input branch of the Gemma-4-E2B layout: pli [M][35][256] from the projection rows
+// pr [M][35 * 256] (E:615-660); g2 [M][256] for layer l from the gate rows pgv (E:405-443)
+void launch_gm_ple(const float* pr, const int* toks, const uint16_t* ple, const float* plnorm, float* pli, int M,
+                   hipStream_t st);
+void launch_gm_pg_act(const float* pgv, const float* pli, int l, int M, float* g2, hipStream_t st);
+// E:1651 for an owner cache of head dim hd (256 or 512): the committed branch rows moved into place
+void launch_kv_compact_hd(const StepDev* sp, const VerifyResultDev* res, uint16_t* K, uint16_t* V, int hd,
+                          hipStream_t st);
 
 struct AttnGeom;
 

@@ -241,6 +241,17 @@ __global__ void k_kv_compact(const StepDev* sp, const VerifyResultDev* res, uint
   }
 }
 
+template <int D>
+__global__ void k_kv_compact_d(const StepDev* sp, const VerifyResultDev* res, uint16_t* K, uint16_t* V) {
+  if (res->branch != 1) return;
+  const int i = threadIdx.x;
+  for (int r = 1; r < res->ncommit; ++r) {
+    const int ps = sp->pos0 + res->hrows[r], pd = sp->pos0 + r;
+    K[(size_t)pd * D + i] = K[(size_t)ps * D + i];
+    V[vc_index_d<D>(pd, i)] = V[vc_index_d<D>(ps, i)];
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // synthetic weights
 // ---------------------------------------------------------------------------------------
@@ -277,7 +288,12 @@ void launch_branch(const StepDev* sp, const int* best1, const float* h, const fl
 void launch_accept(const StepDev* sp, const int* best1, const int* best2, const int* cnt1, const int* cnt2,
                    VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int kvcap, hipStream_t st) {
   hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, st, sp, best1, best2, cnt1, cnt2, res);
-  hipLaunchKernelGGL(k_kv_compact, dim3(NL), dim3(HD), 0, st, sp, res, KC, VC, kvcap);
+  if (NL > 0) hipLaunchKernelGGL(k_kv_compact, dim3(NL), dim3(HD), 0, st, sp, res, KC, VC, kvcap);
+}
+void launch_kv_compact_hd(const StepDev* sp, const VerifyResultDev* res, uint16_t* K, uint16_t* V, int hd,
+                          hipStream_t st) {
+  if (hd == 512) hipLaunchKernelGGL(k_kv_compact_d<512>, dim3(1), dim3(512), 0, st, sp, res, K, V);
+  else hipLaunchKernelGGL(k_kv_compact_d<HD>, dim3(1), dim3(HD), 0, st, sp, res, K, V);
 }
 // exchange two KV slabs (uint4 words): the prefix cache's slot switch
 __global__ void k_swap16(uint4* __restrict__ a, uint4* __restrict__ b, size_t n) {

@@ -417,12 +417,15 @@ __global__ void k_pf_act(const float* __restrict__ g, const float* __restrict__ 
 
 // E:1375-1404 with a zero per-layer-embedding branch: o = r16(o); tmp = rms(o, post_ff);
 // x = r16(x + r16(tmp)); x = r16(x * scalar); then a = rms(x, next in_ln) (unrounded) or, after
-// the last layer and for row `hrow` only, h = r16(rms(x, fnorm))
+// the last layer and for rows m >= hrow (hrow >= 0), h[m - hrow] = r16(rms(x, fnorm)) and, when
+// hn is given, hn[m - hrow] = |h| (E:1417).  The same block with the per-layer-input branch
+// (E:1387-1404) takes the per_layer_projection output as o and post_per_layer_input_norm as w1;
+// with scalar 1, no next norm and hrow -1 it is the plain residual block of E:1375-1377.
 __global__ __launch_bounds__(ROW_THREADS) void k_pf_post_ff(const float* __restrict__ o, float* __restrict__ x,
                                                             float* __restrict__ a, const float* __restrict__ w1,
                                                             const float* __restrict__ next_in_ln,
                                                             const float* __restrict__ fnorm, float scalar,
-                                                            float* __restrict__ h, int hrow) {
+                                                            float* __restrict__ h, int hrow, float* __restrict__ hn) {
   __shared__ __align__(16) float os[H];
   __shared__ __align__(16) float xs[H];
   __shared__ double red[16];
@@ -436,14 +439,52 @@ __global__ __launch_bounds__(ROW_THREADS) void k_pf_post_ff(const float* __restr
     xs[i] = v;
     x[(size_t)m * H + i] = v;
   }
-  if (!next_in_ln && m != hrow) return;  // uniform
+  if (!next_in_ln && (hrow < 0 || m < hrow)) return;  // uniform
   __syncthreads();
   const float r2 = rms_inv(block_sumsq(xs, H, red), H);
   if (next_in_ln) {
     for (int i = threadIdx.x; i < H; i += ROW_THREADS) a[(size_t)m * H + i] = (xs[i] * r2) * next_in_ln[i];
   } else {
-    for (int i = threadIdx.x; i < H; i += ROW_THREADS) h[i] = r16((xs[i] * r2) * fnorm[i]);
+    float* hr = h + (size_t)(m - hrow) * H;
+    for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
+      const float v = r16((xs[i] * r2) * fnorm[i]);
+      os[i] = v;
+      hr[i] = v;
+    }
+    if (!hn) return;  // uniform
+    __syncthreads();
+    const double ss = block_sumsq(os, H, red);
+    if (threadIdx.x == 0) hn[m - hrow] = (float)sqrt(ss);
   }
+}
+
+// E:615-660 ple_fused_task after its product, one block per (row m, layer l): pr = the
+// per_layer_model_projection row (8960 = 35 x 256), prl = r16(pr_l / sqrt(1536)),
+// pj = rms(prl, per_layer_projection_norm), pli_l = (pj + r16(16 PLE[tok][l])) * 0.70710678118
+__global__ __launch_bounds__(256) void k_gm_ple(const float* __restrict__ pr, const int* __restrict__ toks,
+                                                const uint16_t* __restrict__ ple, const float* __restrict__ plnorm,
+                                                float* __restrict__ pli) {
+  constexpr int PD = 256, NLG = 35;
+  __shared__ float xs[PD];
+  __shared__ double red[16];
+  const int m = blockIdx.x, l = blockIdx.y, i = threadIdx.x;
+  const size_t base = (size_t)m * NLG * PD + (size_t)l * PD;
+  const float s1 = 1.0f / sqrtf((float)H);
+  xs[i] = r16(pr[base + i] * s1);
+  __syncthreads();
+  const float r = rms_inv(block_sumsq(xs, PD, red), PD);
+  const float pj = (xs[i] * r) * plnorm[i];
+  const float pev = r16(bf2f(ple[(size_t)toks[m] * NLG * PD + (size_t)l * PD + i]) * 16.0f);
+  pli[base + i] = (pj + pev) * 0.70710678118f;
+}
+
+// E:405-443 pg_fused_task after its product: g2 = r16(r16(gelu8(r16 pgv)) * r16(pli_l)), rows of 256
+__global__ void k_gm_pg_act(const float* __restrict__ pgv, const float* __restrict__ pli, int l, int M,
+                            float* __restrict__ g2) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * 256) return;
+  const int m = idx >> 8, i = idx & 255;
+  g2[idx] = r16(r16(gelu8(r16(pgv[idx]))) * r16(pli[(size_t)m * 35 * 256 + (size_t)l * 256 + i]));
 }
 
 }  // namespace
@@ -489,9 +530,16 @@ void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStre
   hipLaunchKernelGGL(k_pf_act, dim3(grid), dim3(256), 0, st, g, u, act, n);
 }
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
-                       const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st) {
+                       const float* fnorm, float scalar, float* h, int hrow, int M, hipStream_t st, float* hn) {
   hipLaunchKernelGGL(k_pf_post_ff, dim3(M), dim3(ROW_THREADS), 0, st, o, x, a, w1, next_in_ln, fnorm, scalar, h,
-                     hrow);
+                     hrow, hn);
+}
+void launch_gm_ple(const float* pr, const int* toks, const uint16_t* ple, const float* plnorm, float* pli, int M,
+                   hipStream_t st) {
+  hipLaunchKernelGGL(k_gm_ple, dim3(M, 35), dim3(256), 0, st, pr, toks, ple, plnorm, pli);
+}
+void launch_gm_pg_act(const float* pgv, const float* pli, int l, int M, float* g2, hipStream_t st) {
+  hipLaunchKernelGGL(k_gm_pg_act, dim3((M * 256 + 255) / 256), dim3(256), 0, st, pgv, pli, l, M, g2);
 }
 
 }  // namespace g4v

@@ -29,6 +29,10 @@ SIGNATURES = {
     "g4v_w4_upload": (_i, [_vp, _u8p, _u16p, _i, _i]),
     "g4v_w4g32_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4g32_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_model_create_gemma": (_i, [_vp, _i, _i32p, _i]),
+    "g4v_model_set_norms_gemma": (_i, [_vp, _i, C.POINTER(C.c_void_p), C.c_float]),
+    "g4v_model_set_ple": (_i, [_vp, _u8p, _u16p, _f32p]),
+    "g4v_model_set_ple_rows": (_i, [_vp, _i, _i, _u16p]),
     "g4v_w4g32_gemm_multi": (_i, [_vp, _i, _i32p, _f32p, _i, C.POINTER(C.c_void_p)]),
     "g4v_w4g32_norm_gemm": (_i, [_vp, _i, _i, _f32p, _f32p, _f32p, _f32p, C.c_float, _i, _i, _i, _f32p, _f32p]),
     "g4v_w4a8_quant": (_i, [_vp, _f32p, _i, _i, _vp, _f32p, _i32p]),
@@ -267,6 +271,23 @@ class Device:
         arrs = [_c(v, np.float32) for v in norms]
         ptrs = (_vp * 6)(*[a.ctypes.data for a in arrs])
         self._ok(self.L.g4v_model_set_norms(self.h, layer, ptrs, scalar, 1 if sliding else 0), "model_set_norms")
+
+    def model_create_gemma(self, V, mlp, ctxcap=4096):
+        self._ok(self.L.g4v_model_create_gemma(self.h, V, _c(mlp, np.int32), ctxcap), "model_create_gemma")
+
+    def set_norms_gemma(self, layer, norms, scalar):
+        """norms: 7 float vectors (k_norm None past layer 14)"""
+        keep = [None if v is None else _c(v, np.float32) for v in norms]
+        arr = (C.c_void_p * 7)(*[None if v is None else v.ctypes.data for v in keep])
+        self._ok(self.L.g4v_model_set_norms_gemma(self.h, layer, arr, scalar), "model_set_norms_gemma")
+
+    def set_ple(self, w, s, plnorm):
+        self._ok(self.L.g4v_model_set_ple(self.h, _c(w, np.uint8), _c(s, np.uint16), _c(plnorm, np.float32)),
+                 "model_set_ple")
+
+    def set_ple_rows(self, tok0, rows):
+        rows = _c(rows, np.uint16)
+        self._ok(self.L.g4v_model_set_ple_rows(self.h, tok0, rows.shape[0], rows), "model_set_ple_rows")
 
     def set_final_norm(self, w):
         self._ok(self.L.g4v_model_set_final_norm(self.h, _c(w, np.float32)), "model_set_final_norm")

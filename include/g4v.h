@@ -112,12 +112,30 @@ int g4v_model_set_embed(g4v_ctx* c, const uint16_t* E);
 int g4v_model_set_matrix(g4v_ctx* c, int layer, int j, const uint8_t* w, const uint16_t* s);
 int g4v_model_set_norms(g4v_ctx* c, int layer, const float* const nv[6], float scalar, int sliding);
 int g4v_model_set_final_norm(g4v_ctx* c, const float* w);
+/* ---- the Gemma-4-E2B layer layout (E:1222-1232, fwd E:1256-1405): 35 layers, head_dim 256
+ * (l % 5 != 4, window 512) or 512 (global; RoPE theta 1e6 on the first quarter of the
+ * frequencies), k / v projections and caches in layers 0..14 only (later layers read layer 13's
+ * or 14's cache), the MLP width mlp[l] of each layer, and the per-layer-input branch.  After
+ * this call: g4v_model_set_embed, g4v_model_set_final_norm, g4v_model_set_matrix for j = 0 q,
+ * 1 k, 2 v (layers < 15), 3 o, 4 gate, 5 up, 6 down, 7 per_layer_input_gate [256][1536],
+ * 8 per_layer_projection [1536][256], g4v_model_set_norms_gemma, g4v_model_set_ple and the
+ * table rows; then g4v_prefill, g4v_verify_step (a chain of up to 7 drafts) and
+ * g4v_verify_sibling run that layout. */
+int g4v_model_create_gemma(g4v_ctx* c, int V, const int* mlp, int ctxcap);
+/* nv: in_ln, post_attn, pre_ff, post_ff, post_per_layer_input_norm [1536 each], q_norm, k_norm
+ * [hd each; k_norm null past layer 14]; scalar: layer_scalar */
+int g4v_model_set_norms_gemma(g4v_ctx* c, int layer, const float* const nv[7], float scalar);
+/* per_layer_model_projection (int4 [8960][1536], scales [8960][48]) and per_layer_projection_norm [256] */
+int g4v_model_set_ple(g4v_ctx* c, const uint8_t* w, const uint16_t* s, const float* plnorm);
+/* rows tok0 .. tok0 + n - 1 of the per-layer embedding table, bf16 [n][35 * 256] (zero until set) */
+int g4v_model_set_ple_rows(g4v_ctx* c, int tok0, int n, const uint16_t* rows);
 /* KV rows [pos0, pos0 + n) of one layer, bf16 [n][256] each: a cache filled elsewhere
  * (the engine's prefill, E:1328-1336) */
 int g4v_model_set_kv(g4v_ctx* c, int layer, int pos0, int n, const uint16_t* K, const uint16_t* V);
 /* E:1249-1250 ENGINE_FAKE_CTX: first n KV positions of every layer from the LCG seeded `seed` */
 int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
 /* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm",
+ * the Gemma layout's owner caches "GK<l>" / "GV<l>" [ctxcap][hd] (l < 15),
  * and the head screen "Wq" [V][768], "Sq" [V][48] bf16, "coef" [V] f32, in the reference's layouts) */
 int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes);
 

@@ -158,6 +158,8 @@ void g4o_gemma_free(g4o_gemma* g);
 /* fwd of M <= 32 rows at pos0.. (T attention splits, sibling row index or -1); hbuf [M][1536]
  * receives the final-normed rows m >= hf (may be NULL) */
 void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, int sibling, float* hbuf, int hf);
+/* ENGINE_PREFILL_INT8=1 for the passes that follow: blocks of M >= 2 rows take W4A8 products */
+void g4o_gemma_set_i8(g4o_gemma* g, int on);
 /* owner layer l's key (v = 0) or value (v = 1) cache [ctx][hd] */
 const uint16_t* g4o_gemma_cache(const g4o_gemma* g, int l, int v);
 

@@ -36,6 +36,7 @@ struct g4o_gemma {
   float *plnorm, *fnorm;
   uint16_t *KC[15], *VC[15]; /* owners' caches [ctx][hd] */
   float *cs[2], *sn[2];
+  int i8; /* G_I8_ACTIVE: the linear layers of blocks of M >= 2 rows run W4A8 (E:311) */
 };
 
 static float* widen(const uint16_t* b, int n) {
@@ -100,9 +101,15 @@ const uint16_t* g4o_gemma_cache(const g4o_gemma* g, int l, int v) {
   return v ? g->VC[l] : g->KC[l];
 }
 
-static void gemv(const g4o_q4* q, const float* X, int M, float* Y) {
-  g4o_w4g32_gemm(q->w, q->s, X, M, q->N, q->K, Y);
+/* lin_multi (E:310-318): W4A8 for blocks of two rows or more while prompt blocks run int8 --
+ * every matrix of the layout has its int8 tiles then (E:175, E:1505-1507), the per-layer-input
+ * ones included (E:1270, E:1382-1385) -- else the exact W4G32 product */
+static void gemv(int i8, const g4o_q4* q, const float* X, int M, float* Y) {
+  if (i8 && M >= 2) g4o_w4a8_gemm(q->w, q->s, X, M, q->N, q->K, Y);
+  else g4o_w4g32_gemm(q->w, q->s, X, M, q->N, q->K, Y);
 }
+
+void g4o_gemma_set_i8(g4o_gemma* g, int on) { g->i8 = on != 0; }
 
 /* the token's row of the per-layer embedding table (zero for ids not listed) */
 static const uint16_t* ple_row(const g4o_gemma* g, int tok) {
@@ -147,7 +154,7 @@ void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, in
   /* E:615-660 ple_fused_task: per_layer_model_projection of the (un-normed) rows, then per
    * layer r16(. / sqrt(H)), rms over 256 with per_layer_projection_norm, plus r16(16 PLE row),
    * times 0.70710678118 */
-  gemv(&in->plproj, x, M, pr);
+  gemv(g->i8, &in->plproj, x, M, pr);
   const float s1 = 1.0f / sqrtf((float)H);
   for (int m = 0; m < M; ++m) {
     const uint16_t* pe = ple_row(g, toks[m]);
@@ -166,10 +173,10 @@ void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, in
   for (int l = 0; l < NLG; ++l) {
     const g4o_glayer_in* A = &in->L[l];
     const int hd = layer_hd(l), ty = l % 5 != 4 ? 0 : 1, sliding = ty == 0, own = l < 15, ol = owner_of(l);
-    gemv(&A->q, xa, M, q); /* E:1287-1288 */
+    gemv(g->i8, &A->q, xa, M, q); /* E:1287-1288 */
     if (own) {
-      gemv(&A->k, xa, M, k);
-      gemv(&A->v, xa, M, v);
+      gemv(g->i8, &A->k, xa, M, k);
+      gemv(g->i8, &A->v, xa, M, v);
     }
     const int split = M <= 4 && pos0 + M > 192; /* E:1305 (ATT_PAR 192, SPLITKV) */
     const int tiled = !split && sibling < 0 && M >= 4 && pos0 + M > 64;
@@ -216,7 +223,7 @@ void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, in
       }
       g4o_attn_mh(Kc, Vc, hd, NQ, M, q, NQ * hd, pos, lo, sl, sh, att, NQ * hd);
     }
-    gemv(&A->o, att, M, o); /* E:1356 */
+    gemv(g->i8, &A->o, att, M, o); /* E:1356 */
     for (int m = 0; m < M; ++m) { /* E:1358-1361 */
       float* om = o + m * H;
       float* xm = x + m * H;
@@ -227,10 +234,10 @@ void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, in
       for (int c = 0; c < H; ++c) xa[m * H + c] = g4o_r16(xa[m * H + c]);
     }
     const int I = A->gate.N; /* E:1363-1367, gate_up_fused_task (E:256-302) */
-    gemv(&A->gate, xa, M, gt);
-    gemv(&A->up, xa, M, up);
+    gemv(g->i8, &A->gate, xa, M, gt);
+    gemv(g->i8, &A->up, xa, M, up);
     for (size_t c = 0; c < (size_t)M * I; ++c) gt[c] = g4o_r16(g4o_r16(g4o_gelu8(g4o_r16(gt[c]))) * g4o_r16(up[c]));
-    gemv(&A->down, gt, M, o); /* E:1373 */
+    gemv(g->i8, &A->down, gt, M, o); /* E:1373 */
     for (int m = 0; m < M; ++m) { /* E:1375-1378: add_res_prep_x, the rows feed the gate as they are */
       float* om = o + m * H;
       float* xm = x + m * H;
@@ -238,13 +245,13 @@ void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, in
       g4o_rms(om, g->nv[l][3], H, tmp);
       for (int c = 0; c < H; ++c) xm[c] = g4o_r16(xm[c] + g4o_r16(tmp[c]));
     }
-    gemv(&A->pg, x, M, pgv); /* E:405-443 pg_fused_task */
+    gemv(g->i8, &A->pg, x, M, pgv); /* E:405-443 pg_fused_task */
     for (int m = 0; m < M; ++m) {
       const float* pl = pli + (size_t)m * NLG * PD + l * PD;
       for (int i = 0; i < PD; ++i)
         g2[m * PD + i] = g4o_r16(g4o_r16(g4o_gelu8(g4o_r16(pgv[m * PD + i]))) * g4o_r16(pl[i]));
     }
-    gemv(&A->pp, g2, M, o); /* E:1386 */
+    gemv(g->i8, &A->pp, g2, M, o); /* E:1386 */
     for (int m = 0; m < M; ++m) { /* E:1387-1404 */
       float* om = o + m * H;
       float* xm = x + m * H;

@@ -140,7 +140,7 @@ class GemmaOracle:
     """the oracle's Gemma-layout forward over a checkpoint directory (tensors mapped in place)
     and the head of the synthetic model with the same embedding"""
 
-    def __init__(self, orc, d, ctx=1024):
+    def __init__(self, orc, d, ctx=1024, i8=False):
         from oracle import Model
         L = orc.L
         L.g4o_gemma_new.restype = C.c_void_p
@@ -148,6 +148,7 @@ class GemmaOracle:
         L.g4o_gemma_free.argtypes = [C.c_void_p]
         L.g4o_gemma_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                         C.c_int]
+        L.g4o_gemma_set_i8.argtypes = [C.c_void_p, C.c_int]
         L.g4o_gemma_cache.restype = C.c_void_p
         L.g4o_gemma_cache.argtypes = [C.c_void_p, C.c_int, C.c_int]
         self.orc, self.ctx = orc, ctx
@@ -185,6 +186,7 @@ class GemmaOracle:
         gi.nple, gi.ple_ids, gi.ple_rows = len(PLE_IDS), self.ple_ids.ctypes.data, self.ple.ctypes.data
         self.gi = gi
         self.h = L.g4o_gemma_new(C.byref(gi), ctx)
+        L.g4o_gemma_set_i8(self.h, 1 if i8 else 0)  # ENGINE_PREFILL_INT8=1: W4A8 blocks of >= 2 rows
         self.head = Model(orc, EMBED_SEED, V, 1, 256, 64)
 
     def close(self):

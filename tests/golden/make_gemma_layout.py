@@ -2,10 +2,11 @@
 
 oracle/_ref/gemma4_engine is engine/gemma4_engine.cpp compiled by `make -C oracle` from its own
 source.  It runs here on the synthetic checkpoint of gemma_layout.write_checkpoint (35 layers of
-head_dim 256 / 512, KV sharing, per-layer inputs, V = 262,144), exact float (ENGINE_PREFILL_INT8
-unset, ENGINE_DECODE_INT8=0), ENGINE_K=0 (prefill, then one-row decode passes), the certified
-head (ENGINE_HEAD_SCREEN=1) and ENGINE_CPUS of 6 CPUs (6 attention splits).  Each prompt of
-gemma_layout_cases() is one engine run; its FIRST and GEN lines are stored.
+head_dim 256 / 512, KV sharing, per-layer inputs, V = 262,144), ENGINE_DECODE_INT8=0,
+ENGINE_K=0 (prefill, then one-row decode passes), the certified head (ENGINE_HEAD_SCREEN=1) and
+ENGINE_CPUS of 6 CPUs (6 attention splits), twice: exact float prefill (ENGINE_PREFILL_INT8
+unset: first, gens) and W4A8 prefill blocks (ENGINE_PREFILL_INT8=1: first_i8, gens_i8).  Each
+prompt of cases() is one engine run; its FIRST and GEN lines are stored.
 
 Run from the repository root after `make -C oracle`:
     python tests/golden/make_gemma_layout.py
@@ -48,34 +49,40 @@ def main():
         sys.exit("oracle/_ref/gemma4_engine is not built (make -C oracle with the reference sources)")
     orc = Oracle()
     prompts = cases(orc)
-    firsts, gens = [], []
+    out = {}
     with tempfile.TemporaryDirectory() as d:
         gl.write_checkpoint(orc, d)
-        env = dict(os.environ, ENGINE_CPUS=",".join(str(c) for c in range(CPUS)), ENGINE_K="0",
-                   ENGINE_HEAD_SCREEN="1", ENGINE_DECODE_INT8="0", ENGINE_CTX=str(CTX))
-        for k in ("ENGINE_PREFILL_INT8", "ENGINE_SERVE", "ENGINE_STREAM", "ENGINE_ADAPTIVE_THREADS"):
-            env.pop(k, None)
-        for i, p in enumerate(prompts):
-            pf = os.path.join(d, f"prompt{i}.txt")
-            with open(pf, "w") as f:
-                f.write(" ".join(map(str, p)) + "\n")
-            r = subprocess.run([EXE, d, os.path.join(d, "index.tsv"), pf, str(NNEW)], env=env, capture_output=True,
-                               text=True, timeout=1800)
-            if r.returncode != 0:
-                sys.exit(f"engine failed ({r.returncode}): {r.stderr[-2000:]}")
-            lines = r.stdout.splitlines()
-            first = int([ln for ln in lines if ln.startswith("FIRST")][0].split()[1])
-            gen = [int(x) for x in [ln for ln in lines if ln.startswith("GEN:")][0].split()[1:]]
-            print(f"prompt {i} ({len(p)} tokens): FIRST {first} GEN {gen}", flush=True)
-            firsts.append(first)
-            gens.append(np.array(gen, np.int32))
+        for sfx, i8 in (("", False), ("_i8", True)):
+            env = dict(os.environ, ENGINE_CPUS=",".join(str(c) for c in range(CPUS)), ENGINE_K="0",
+                       ENGINE_HEAD_SCREEN="1", ENGINE_DECODE_INT8="0", ENGINE_CTX=str(CTX))
+            for k in ("ENGINE_PREFILL_INT8", "ENGINE_SERVE", "ENGINE_STREAM", "ENGINE_ADAPTIVE_THREADS"):
+                env.pop(k, None)
+            if i8:
+                env["ENGINE_PREFILL_INT8"] = "1"
+            firsts, gens = [], []
+            for i, p in enumerate(prompts):
+                pf = os.path.join(d, f"prompt{i}.txt")
+                with open(pf, "w") as f:
+                    f.write(" ".join(map(str, p)) + "\n")
+                r = subprocess.run([EXE, d, os.path.join(d, "index.tsv"), pf, str(NNEW)], env=env,
+                                   capture_output=True, text=True, timeout=1800)
+                if r.returncode != 0:
+                    sys.exit(f"engine failed ({r.returncode}): {r.stderr[-2000:]}")
+                lines = r.stdout.splitlines()
+                first = int([ln for ln in lines if ln.startswith("FIRST")][0].split()[1])
+                gen = [int(x) for x in [ln for ln in lines if ln.startswith("GEN:")][0].split()[1:]]
+                print(f"prompt {i} ({len(p)} tokens, int8 prefill {i8}): FIRST {first} GEN {gen}", flush=True)
+                firsts.append(first)
+                gens.append(np.array(gen, np.int32))
+            out["first" + sfx] = np.array(firsts, np.int32)
+            out["gen_lens" + sfx] = np.array([len(g) for g in gens])
+            out["gens" + sfx] = np.concatenate(gens)
         raw = np.memmap(os.path.join(d, "model.safetensors"), np.uint8, "r")
         file_crc = crc(np.asarray(raw[:gl.V * gl.H * 2 + (64 << 20)]))
     path = os.path.join(HERE, "gemma_layout.npz")
     np.savez_compressed(path, cpus=np.array([CPUS]), nnew=np.array([NNEW]), ctx=np.array([CTX]),
                         prompt_lens=np.array([len(p) for p in prompts]), prompts=np.concatenate(prompts),
-                        first=np.array(firsts, np.int32), gen_lens=np.array([len(g) for g in gens]),
-                        gens=np.concatenate(gens), crc_head=np.array([file_crc], np.uint32))
+                        crc_head=np.array([file_crc], np.uint32), **out)
     print(f"gemma_layout.npz: {os.path.getsize(path)} bytes", flush=True)
 
 

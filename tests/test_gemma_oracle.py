@@ -2,7 +2,8 @@
 KV sharing past layer 14, per-layer MLP widths, per-layer inputs, partial RoPE) against the
 reference engine's main() run unchanged on the same synthetic checkpoint
 (tests/golden/make_gemma_layout.py, oracle/_ref/gemma4_engine): FIRST and GEN tokens of three
-prompts whose prefill blocks and decode passes take run_mh, attn_tile and split-KV (6 splits).
+prompts whose prefill blocks and decode passes take run_mh, attn_tile and split-KV (6 splits),
+with exact float prompt blocks and with W4A8 ones (ENGINE_PREFILL_INT8=1).
 
 The fixture pins bit-level arithmetic through the tokens: planting either of two mistakes in
 the oracle -- 8 attention splits for 6, or the per-layer embedding rows dropped -- changes the
@@ -31,16 +32,18 @@ def ckpt(orc, tmp_path_factory):
     return d, fx, prompts, gens
 
 
-@pytest.mark.parametrize("i", [0, 1, 2])
-def test_gemma_layout_matches_reference_engine(orc, ckpt, i):
+@pytest.mark.parametrize("i,i8", [(0, False), (1, False), (2, False), (2, True)])
+def test_gemma_layout_matches_reference_engine(orc, ckpt, i, i8):
     d, fx, prompts, gens = ckpt
-    go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
+    sfx = "_i8" if i8 else ""
+    want = np.split(fx["gens" + sfx], np.cumsum(fx["gen_lens" + sfx])[:-1])[i]
+    go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]), i8=i8)
     try:
         gen = gl.run_req_k0(go, [int(t) for t in prompts[i]], int(fx["nnew"][0]), int(fx["cpus"][0]))
     finally:
         go.close()
-    assert gen[0] == int(fx["first"][i])
-    assert gen == [int(t) for t in gens[i]], (gen, list(gens[i]))
+    assert gen[0] == int(fx["first" + sfx][i])
+    assert gen == [int(t) for t in want], (gen, list(want))
 
 
 def test_gemma_fixture_detects_planted_mistakes(orc, ckpt):

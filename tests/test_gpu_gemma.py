@@ -1,0 +1,190 @@
+"""The Gemma-4-E2B layer layout on the device (g4v_model_create_gemma): head_dim 256 / 512
+layers, KV sharing past layer 14, per-layer MLP widths and the per-layer-input branch, on the
+synthetic checkpoint of tests/golden/gemma_layout.py uploaded through the C ABI.
+
+  * run_req with ENGINE_K=0 (prefill in blocks of 32, then one-row decode passes, 6 splits)
+    gives the FIRST / GEN tokens the reference engine's own main() gave on the same checkpoint
+    (tests/golden/gemma_layout.npz), with exact float prompt blocks and with W4A8 ones
+    (ENGINE_PREFILL_INT8=1, g4v_set_prefill_int8);
+  * a prompt's final-normed state and every owner cache equal the oracle's (bit for bit), in
+    both prefill modes;
+  * a chain pass of greedy drafts and the sibling form commit what the oracle's rows give."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import note
+from util import first_diff, same
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+import gemma_layout as gl  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+FX = os.path.join(HERE, "golden", "gemma_layout.npz")
+
+
+def upload(dev, d, ctx):
+    """the checkpoint in d onto the device, tensor by tensor as the engine's loader would"""
+    raw = np.memmap(os.path.join(d, "model.safetensors"), np.uint8, "r")
+    idx = {}
+    for line in open(os.path.join(d, "index.tsv")):
+        n, dt, o, nb, sh = line.rstrip("\n").split("\t")
+        idx[n.replace("model.language_model.", "")] = (int(o), int(nb), tuple(int(x) for x in sh.split(",")))
+    get = lambda n, dt=np.uint8: np.asarray(raw[idx[n][0]:idx[n][0] + idx[n][1]]).view(dt)
+    bfv = lambda n: (get(n, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    dev.model_create_gemma(gl.V, gl.MLP, ctx)
+    dev.set_embed(get("embed_tokens.weight", np.uint16))
+    names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+             "mlp.up_proj", "mlp.down_proj", "per_layer_input_gate", "per_layer_projection"]
+    for l in range(gl.NL):
+        p = f"layers.{l}."
+        for j, nm in enumerate(names):
+            if j in (1, 2) and l >= 15:
+                continue
+            N, K8 = idx[p + nm + ".weight_packed"][2]
+            dev.set_matrix(l, j, get(p + nm + ".weight_packed").reshape(N, K8 * 4),
+                           get(p + nm + ".weight_scale", np.uint16))
+        nv = [bfv(p + n + ".weight") for n in ("input_layernorm", "post_attention_layernorm",
+                                                "pre_feedforward_layernorm", "post_feedforward_layernorm",
+                                                "post_per_layer_input_norm", "self_attn.q_norm")]
+        nv.append(bfv(p + "self_attn.k_norm.weight") if l < 15 else None)
+        dev.set_norms_gemma(l, nv, float(bfv(p + "layer_scalar")[0]))
+    N, K8 = idx["per_layer_model_projection.weight_packed"][2]
+    dev.set_ple(get("per_layer_model_projection.weight_packed").reshape(N, K8 * 4),
+                get("per_layer_model_projection.weight_scale", np.uint16), bfv("per_layer_projection_norm.weight"))
+    ple = np.asarray(raw[idx["embed_tokens_per_layer.weight"][0]:]).view(np.uint16)
+    for t in gl.PLE_IDS:
+        dev.set_ple_rows(t, ple[t * gl.NL * gl.PD:(t + 1) * gl.NL * gl.PD].reshape(1, -1))
+    dev.set_final_norm(bfv("norm.weight"))
+
+
+@pytest.fixture(scope="module")
+def gemma(orc, g4v, tmp_path_factory):
+    d = str(tmp_path_factory.mktemp("gemma_dev"))
+    note("writing the synthetic Gemma-layout checkpoint")
+    gl.write_checkpoint(orc, d)
+    fx = np.load(FX)
+    ctx = int(fx["ctx"][0])
+    dev = g4v.Device(0)
+    note("uploading it")
+    upload(dev, d, ctx)
+    dev.set_prefill_int8(False)  # exact float prompt blocks unless a test asks for W4A8
+    yield dev, d, fx, ctx
+    dev.close()
+
+
+def device_run_req_k0(dev, prompt, nnew, T):
+    """run_req (E:1584-1661) with ENGINE_K=0 over the library: prefill, then one-row passes"""
+    n = len(prompt)
+    gen = [int(dev.prefill(np.array(prompt, np.int32), 0, 32, T))]
+    for i in range(1, nnew):
+        if gen[-1] in (106, 1):
+            break
+        r = dev.verify(np.array([gen[-1]], np.int32), 0, 0, n + i - 1, T)
+        gen.append(int(r.commit[0]))
+    gen = gen[:nnew]
+    for i, g in enumerate(gen):
+        if g in (106, 1):
+            return gen[:i + 1]
+    return gen
+
+
+@pytest.mark.parametrize("i8", [False, True])
+@pytest.mark.parametrize("i", [0, 1, 2])
+def test_gemma_tokens_match_reference_engine(gemma, i, i8):
+    dev, d, fx, ctx = gemma
+    sfx = "_i8" if i8 else ""
+    prompts = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])
+    want = np.split(fx["gens" + sfx], np.cumsum(fx["gen_lens" + sfx])[:-1])[i]
+    note(f"gemma run_req prompt {i} ({len(prompts[i])} tokens), int8 prefill {i8}")
+    dev.set_prefill_int8(i8)
+    try:
+        got = device_run_req_k0(dev, [int(t) for t in prompts[i]], int(fx["nnew"][0]), int(fx["cpus"][0]))
+    finally:
+        dev.set_prefill_int8(False)
+    assert got[0] == int(fx["first" + sfx][i])
+    assert got == [int(t) for t in want], (got, list(want))
+
+
+@pytest.mark.parametrize("i8", [False, True])
+def test_gemma_prefill_state_and_caches(orc, gemma, i8):
+    dev, d, fx, ctx = gemma
+    prompt = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])[2]  # 196 tokens: split-KV tail
+    go = gl.GemmaOracle(orc, d, ctx, i8=i8)
+    dev.set_prefill_int8(i8)
+    try:
+        note(f"gemma prefill of 196 tokens against the oracle, int8 {i8}")
+        hd_ = None
+        for b in range(0, len(prompt), 32):
+            blk = [int(t) for t in prompt[b:b + 32]]
+            last = b + len(blk) == len(prompt)
+            hb = go.forward(blk, b, 6, len(blk) - 1 if last else len(blk))
+            if last:
+                hd_ = hb[len(blk) - 1]
+        g0, h = dev.prefill(np.array(prompt, np.int32), 0, 32, 6, hidden=True)
+        assert same(h, hd_), first_diff(h, hd_)
+        n = len(prompt)
+        for l in range(15):
+            hdl = gl.layer_hd(l)
+            for v, nm in ((0, "GK"), (1, "GV")):
+                a = dev.read(f"{nm}{l}", np.uint16)[:n * hdl]
+                b = go.cache(l, v)[:n * hdl]
+                assert same(a, b), (nm, l, first_diff(a, b))
+    finally:
+        dev.set_prefill_int8(False)
+        go.close()
+
+
+@pytest.mark.parametrize("kind,pos0", [("chain", 210), ("chain", 40), ("sibling", 150), ("sibling", 240)])
+def test_gemma_multirow_passes(orc, gemma, kind, pos0):
+    """a chain of 3 greedy drafts (split-KV past 192 keys, run_mh below) and the sibling form
+    (nd 2 + the runner-up at RoPE position pos0 + 1, E:1634-1655) after a prefill, against the
+    oracle's rows: committed tokens and the committed row's state"""
+    dev, d, fx, ctx = gemma
+    prompt = [int(t) for t in np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])[2]][:pos0]
+    while len(prompt) < pos0:
+        prompt = prompt + prompt[:pos0 - len(prompt)]
+    go = gl.GemmaOracle(orc, d, ctx)
+    try:
+        for b in range(0, pos0, 32):
+            blk = prompt[b:b + 32]
+            hb = go.forward(blk, b, 6, len(blk) - 1 if b + len(blk) == pos0 else len(blk))
+        g0 = go.greedy(hb[len(blk) - 1], blk)
+        dev.prefill(np.array(prompt, np.int32), 0, 32, 6)
+        # greedy chain from the oracle (one-row passes on a copy of the state would move its cache,
+        # so the chain is taken as the model's own continuation of a fresh forward per step)
+        if kind == "chain":
+            toks = [g0]
+            for j in range(3):
+                hh = go.forward(toks[:j + 1], pos0, 6, 0)
+                toks.append(go.greedy(hh[j], toks[:j + 1]))
+            hh = go.forward(toks, pos0, 6, 0)
+            G = [go.greedy(hh[m], toks) for m in range(4)]
+            r, h = dev.verify(np.array(toks, np.int32), 3, 0, pos0, 6, hidden=True)
+            note(f"chain at {pos0}: oracle G {G}, device commit {list(r.commit[:r.ncommit])}")
+            assert r.nacc == 3 and list(r.commit[:4]) == G
+            assert same(h, hh[3]), first_diff(h, hh[3])
+        else:
+            # row 0's greedy token does not depend on the later rows' tokens: take it from a
+            # first pass, then put it into the sibling row and a different token into draft 1
+            toks = [g0, 11, 7, 13]
+            G0 = go.greedy(go.forward(toks, pos0, 6, 0, sibling=3)[0], toks)
+            toks = [g0, G0 + 1, 7, G0]
+            hs = go.forward(toks, pos0, 6, 0, sibling=3)
+            assert go.greedy(hs[0], toks) == G0
+            G3 = go.greedy(hs[3], toks)
+            r, h = dev.verify_sibling(np.array(toks, np.int32), 2, pos0, 6, True, hidden=True)
+            note(f"sibling at {pos0}: oracle G0 {G0} G3 {G3}, device {r.as_dict()}")
+            assert (r.nacc, r.branch, r.ncommit) == (1, 1, 2) and list(r.commit[:2]) == [G0, G3]
+            assert same(h, hs[3]), first_diff(h, hs[3])
+            for l in range(15):  # the sibling's rows moved into place (E:1651)
+                hdl = gl.layer_hd(l)
+                for v, nm in ((0, "GK"), (1, "GV")):
+                    a = dev.read(f"{nm}{l}", np.uint16)[(pos0 + 1) * hdl:(pos0 + 2) * hdl]
+                    b = go.cache(l, v)[(pos0 + 3) * hdl:(pos0 + 4) * hdl]
+                    assert same(a, b), (nm, l)
+    finally:
+        go.close()
