@@ -2436,11 +2436,14 @@ extern "C" int g4v_slots_init(g4v_ctx* c, int nslot, int min_reuse) {
   ARGCHK(nslot >= 1 && nslot <= 64, "slots_init: 1 <= nslot <= 64");
   HIPCHK(hipSetDevice(c->device));
   c->slots.clear();
-  const size_t bytes = c->KC.n;
   for (int i = 0; i + 1 < nslot; ++i) {
     auto sl = std::make_unique<g4v_ctx::Slot>();
-    ALLOC(sl->KC, bytes);
-    ALLOC(sl->VC, bytes);
+    if (c->gemma) {  // the owner caches of the Gemma layout: one buffer
+      ALLOC(sl->KC, c->gm_kv.n);
+    } else {
+      ALLOC(sl->KC, c->KC.n);
+      ALLOC(sl->VC, c->VC.n);
+    }
     c->slots.push_back(std::move(sl));
   }
   c->act_keys.clear();
@@ -2453,8 +2456,12 @@ extern "C" int g4v_slots_init(g4v_ctx* c, int nslot, int min_reuse) {
 // the active KV and stored slot s exchange places (E:1576 swap_with): contents are swapped on the
 // device, so captured passes keep pointing at the active cache
 static int slot_swap(g4v_ctx* c, g4v_ctx::Slot& sl) {
-  launch_swap16(c->KC.p, sl.KC.p, c->KC.n, c->st);
-  launch_swap16(c->VC.p, sl.VC.p, c->VC.n, c->st);
+  if (c->gemma) {
+    launch_swap16(c->gm_kv.p, sl.KC.p, c->gm_kv.n, c->st);
+  } else {
+    launch_swap16(c->KC.p, sl.KC.p, c->KC.n, c->st);
+    launch_swap16(c->VC.p, sl.VC.p, c->VC.n, c->st);
+  }
   HIPCHK(hipGetLastError());
   std::swap(c->act_keys, sl.keys);
   std::swap(c->act_kv_len, sl.kv_len);

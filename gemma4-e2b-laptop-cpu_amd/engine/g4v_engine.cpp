@@ -10,11 +10,13 @@
 //
 // <model> is a checkpoint directory holding model.safetensors and <index> its tensor index (one
 // line per tensor: name, dtype, byte offset in the file, byte count, shape; E:1218-1222), or
-// "synth:SEED:V:NL:I" for the synthetic stack (<index> ignored).  A checkpoint is read for the
-// stack the library runs: every layer with its own q/k/v projections of 8 x 256 / 256 / 256
-// rows, a uniform MLP width and no per-layer-embedding tensors; the Gemma-4-E2B layout
-// (hd-512 global layers, KV-shared layers 15-34, PLE) is refused with a message.  The MTP
-// drafter is the synthetic one (ENGINE_DRAFTER_SEED; with a checkpoint only when set).  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
+// "synth:SEED:V:NL:I" for the synthetic stack (<index> ignored).  A checkpoint holding the
+// per-layer-input tensors is the Gemma-4-E2B layout main() loads (E:1222-1231: 35 layers of head
+// dim 256 / 512, k/v projections in layers 0..14, per-layer MLP widths, the per-layer embedding
+// table) and runs through g4v_model_create_gemma; that layout decodes with ENGINE_K=0 (one-row
+// passes, E:1615).  Any other checkpoint is read as a uniform stack: every layer with its
+// own q/k/v projections of 8 x 256 / 256 / 256 rows and one MLP width.  The MTP drafter is the
+// synthetic one (ENGINE_DRAFTER_SEED; with a uniform checkpoint only when set).  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
 // (g4v_slot_*), the prefill (g4v_prefill), and decode rounds whose drafts come from prompt
 // lookup (ENGINE_NGRAM / ENGINE_NGLEN) or, when it finds none, the MTP drafter (ENGINE_K, a
 // synthetic drafter, seed ENGINE_DRAFTER_SEED), verified as a chain (g4v_verify_step) or, when
@@ -135,20 +137,82 @@ struct Checkpoint {
   }
 };
 
+// an int4 G32 matrix (E:175): [N][K/8] int32 words = [N][K/2] bytes, bf16 scales [N][K/32]
+void set_q4(const Checkpoint& ck, int l, int j, const std::string& b, int N, int K) {
+  const Tensor* w = ck.find(b + ".weight_packed");
+  if (w && w->shape.size() == 2 && (w->shape[0] != N || w->shape[1] * 8 != K))
+    Checkpoint::fail(b + ": shape " + std::to_string(w->shape[0]) + " x " + std::to_string(w->shape[1] * 8) +
+                     ", expected " + std::to_string(N) + " x " + std::to_string(K));
+  const Tensor& wt = ck.get(b + ".weight_packed", "I32", (size_t)N * K / 2);
+  const Tensor& st = ck.get(b + ".weight_scale", "BF16", (size_t)N * (K / 32) * 2);
+  check(g4v_model_set_matrix(G, l, j, ck.data(wt), (const uint16_t*)ck.data(st)), "model_set_matrix");
+}
+
+// main()'s layout (E:1222-1231) into the library (g4v_model_create_gemma + setters)
+void load_gemma(const Checkpoint& ck, int V, int ctx) {
+  const int H = 1536, NL = 35, PD = 256;
+  if (ck.find("layers.35.input_layernorm.weight") || !ck.find("layers.34.input_layernorm.weight"))
+    Checkpoint::fail("the per-layer-input layout has 35 layers (E:1222)");
+  std::vector<int> mlp(NL);
+  for (int l = 0; l < NL; ++l) {
+    const Tensor* g = ck.find("layers." + std::to_string(l) + ".mlp.gate_proj.weight_packed");
+    if (!g || g->shape.size() != 2) Checkpoint::fail("layers." + std::to_string(l) + ".mlp.gate_proj missing");
+    mlp[l] = (int)g->shape[0];
+  }
+  check(g4v_model_create_gemma(G, V, mlp.data(), ctx), "model_create_gemma");
+  check(g4v_model_set_embed(G, (const uint16_t*)ck.data(ck.get("embed_tokens.weight", "BF16", (size_t)V * H * 2))),
+        "model_set_embed");
+  const char* names[9] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                          "mlp.gate_proj",    "mlp.up_proj",      "mlp.down_proj",    "per_layer_input_gate",
+                          "per_layer_projection"};
+  for (int l = 0; l < NL; ++l) {  // E:1224-1229
+    const std::string p = "layers." + std::to_string(l) + ".";
+    const int hd = l % 5 != 4 ? 256 : 512, I = mlp[l];
+    const bool owner = l < 15;
+    const int Ns[9] = {8 * hd, hd, hd, H, I, I, H, PD, H}, Ks[9] = {H, H, H, 8 * hd, H, H, I, H, PD};
+    for (int j = 0; j < 9; ++j)
+      if (owner || (j != 1 && j != 2)) set_q4(ck, l, j, p + names[j], Ns[j], Ks[j]);
+    std::vector<float> nv[7] = {ck.vec(p + "input_layernorm.weight", H), ck.vec(p + "post_attention_layernorm.weight", H),
+                                ck.vec(p + "pre_feedforward_layernorm.weight", H),
+                                ck.vec(p + "post_feedforward_layernorm.weight", H),
+                                ck.vec(p + "post_per_layer_input_norm.weight", H), ck.vec(p + "self_attn.q_norm.weight", hd)};
+    if (owner) nv[6] = ck.vec(p + "self_attn.k_norm.weight", hd);
+    const float* nvp[7] = {nv[0].data(), nv[1].data(), nv[2].data(), nv[3].data(), nv[4].data(), nv[5].data(),
+                           owner ? nv[6].data() : nullptr};
+    check(g4v_model_set_norms_gemma(G, l, nvp, ck.vec(p + "layer_scalar", 1)[0]), "model_set_norms_gemma");
+  }
+  {  // E:1230-1231: the projection, its norm and the table (uploaded in slices of the mapped file)
+    const int N = NL * PD;
+    const Tensor& wt = ck.get("per_layer_model_projection.weight_packed", "I32", (size_t)N * H / 2);
+    const Tensor& st = ck.get("per_layer_model_projection.weight_scale", "BF16", (size_t)N * (H / 32) * 2);
+    check(g4v_model_set_ple(G, ck.data(wt), (const uint16_t*)ck.data(st),
+                            ck.vec("per_layer_projection_norm.weight", PD).data()),
+          "model_set_ple");
+    const Tensor& tb = ck.get("embed_tokens_per_layer.weight", "BF16", (size_t)V * N * 2);
+    const uint16_t* rows = (const uint16_t*)ck.data(tb);
+    for (int t0 = 0; t0 < V; t0 += 8192)
+      check(g4v_model_set_ple_rows(G, t0, std::min(8192, V - t0), rows + (size_t)t0 * N), "model_set_ple_rows");
+  }
+  check(g4v_model_set_final_norm(G, ck.vec("norm.weight", H).data()), "model_set_final_norm");
+}
+
 // the stack of a checkpoint into the library (g4v_model_create + setters); returns V
-int load_checkpoint(const Checkpoint& ck, int ctx) {
+int load_checkpoint(const Checkpoint& ck, int ctx, bool* gemma) {
   const int H = 1536;
   const Tensor* emb = ck.find("embed_tokens.weight");
   if (!emb || emb->shape.size() != 2 || emb->shape[1] != H) Checkpoint::fail("embed_tokens.weight [V][1536] missing");
   const int V = (int)emb->shape[0];
+  *gemma = ck.find("per_layer_model_projection.weight_packed") || ck.find("embed_tokens_per_layer.weight");
+  if (*gemma) {
+    load_gemma(ck, V, ctx);
+    return V;
+  }
   int NL = 0;
   while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
   if (NL == 0) Checkpoint::fail("no layers");
   const Tensor* g0 = ck.find("layers.0.mlp.gate_proj.weight_packed");
   if (!g0 || g0->shape.size() != 2) Checkpoint::fail("layers.0.mlp.gate_proj.weight_packed missing");
   const int I = (int)g0->shape[0];
-  if (ck.find("per_layer_model_projection.weight_packed") || ck.find("embed_tokens_per_layer.weight"))
-    Checkpoint::fail("per-layer embeddings (the Gemma-4-E2B layout) are not run by this build yet");
   check(g4v_model_create(G, V, NL, I, ctx), "model_create");
   check(g4v_model_set_embed(G, (const uint16_t*)ck.data(ck.get("embed_tokens.weight", "BF16", (size_t)V * H * 2))),
         "model_set_embed");
@@ -158,18 +222,8 @@ int load_checkpoint(const Checkpoint& ck, int ctx) {
   for (int l = 0; l < NL; ++l) {
     const std::string p = "layers." + std::to_string(l) + ".";
     if (!ck.find(p + "self_attn.k_proj.weight_packed"))
-      Checkpoint::fail(p + ": no k_proj (a KV-shared layer of the Gemma-4-E2B layout) is not run by this build yet");
-    for (int j = 0; j < 7; ++j) {  // E:175 int4 G32: [N][K/8] int32 words = [N][K/2] bytes, scales [N][K/32]
-      const std::string b = p + names[j];
-      const Tensor* w = ck.find(b + ".weight_packed");
-      if (w && w->shape.size() == 2 && (w->shape[0] != Ns[j] || w->shape[1] * 8 != Ks[j]))
-        Checkpoint::fail(b + ": shape " + std::to_string(w->shape[0]) + " x " + std::to_string(w->shape[1] * 8) +
-                         ", this build runs " + std::to_string(Ns[j]) + " x " + std::to_string(Ks[j]) +
-                         " (hd-512 global layers and double-wide MLPs come with the Gemma-4-E2B layout)");
-      const Tensor& wt = ck.get(b + ".weight_packed", "I32", (size_t)Ns[j] * Ks[j] / 2);
-      const Tensor& st = ck.get(b + ".weight_scale", "BF16", (size_t)Ns[j] * (Ks[j] / 32) * 2);
-      check(g4v_model_set_matrix(G, l, j, ck.data(wt), (const uint16_t*)ck.data(st)), "model_set_matrix");
-    }
+      Checkpoint::fail(p + ": no k_proj: a KV-shared layer outside the per-layer-input layout");
+    for (int j = 0; j < 7; ++j) set_q4(ck, l, j, p + names[j], Ns[j], Ks[j]);
     const std::vector<float> nv[6] = {
         ck.vec(p + "input_layernorm.weight", H),          ck.vec(p + "post_attention_layernorm.weight", H),
         ck.vec(p + "pre_feedforward_layernorm.weight", H), ck.vec(p + "post_feedforward_layernorm.weight", H),
@@ -440,17 +494,22 @@ int main(int argc, char** argv) {
   check(g4v_create(0, &G), "create");
   check(g4v_set_prefill_int8(G, g_i8 ? 1 : 0), "set_prefill_int8");
   Checkpoint ck;
+  bool gemma = false;
   if (synth) {
     check(g4v_model_synth(G, seed, V, NL, I, e.ctx), "model_synth");
   } else {
     ck.open_files(argv[1], argv[2]);
-    V = load_checkpoint(ck, e.ctx);
+    V = load_checkpoint(ck, e.ctx, &gemma);
     e.V = V;
     NL = 0;
     while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
   }
   const char* dseed = getenv("ENGINE_DRAFTER_SEED");
-  if (e.k_draft > 0 && NL >= 15 && V % 2048 == 0 && (synth || dseed)) {
+  if (gemma && e.k_draft > 0) {  // E:1519-1528: rounds without lookup drafts would need the drafter
+    fprintf(stderr, "g4v_engine: the per-layer-input layout runs without the MTP drafter here: set ENGINE_K=0\n");
+    return 2;
+  }
+  if (!gemma && e.k_draft > 0 && NL >= 15 && V % 2048 == 0 && (synth || dseed)) {
     check(g4v_drafter_synth(G, dseed ? strtoull(dseed, nullptr, 10) : seed + 1), "drafter_synth");
     e.drafter = true;
   }

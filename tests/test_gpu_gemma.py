@@ -10,6 +10,7 @@ synthetic checkpoint of tests/golden/gemma_layout.py uploaded through the C ABI.
     both prefill modes;
   * a chain pass of greedy drafts and the sibling form commit what the oracle's rows give."""
 import os
+import subprocess
 import sys
 
 import numpy as np
@@ -188,3 +189,43 @@ def test_gemma_multirow_passes(orc, gemma, kind, pos0):
                     assert same(a, b), (nm, l)
     finally:
         go.close()
+
+
+@pytest.mark.parametrize("i8", [False, True])
+def test_gemma_engine_matches_reference_engine(gemma, i8):
+    """g4v_engine on the checkpoint directory and its index, as main() is run (E:1211-1231), in
+    serve mode over the three prompts: FIRST / GEN lines equal the reference engine's"""
+    dev, d, fx, ctx = gemma
+    exe = os.path.join(os.path.dirname(HERE), "gemma4-e2b-laptop-cpu_amd", "g4v_engine")
+    sfx = "_i8" if i8 else ""
+    prompts = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])
+    gens = np.split(fx["gens" + sfx], np.cumsum(fx["gen_lens" + sfx])[:-1])
+    nnew = int(fx["nnew"][0])
+    env = dict(os.environ, ENGINE_SERVE="1", ENGINE_K="0", ENGINE_CTX=str(ctx), ENGINE_DECODE_INT8="0",
+               ENGINE_CPUS=",".join(str(c) for c in range(int(fx["cpus"][0]))))
+    for k in ("ENGINE_PREFILL_INT8", "ENGINE_ADAPTIVE_THREADS", "ENGINE_NGRAM", "ENGINE_STREAM"):
+        env.pop(k, None)
+    if i8:
+        env["ENGINE_PREFILL_INT8"] = "1"
+    lines = "".join(f"{nnew} {' '.join(map(str, p))}\n" for p in prompts)
+    note(f"g4v_engine on the Gemma-layout checkpoint, int8 prefill {i8}")
+    proc = subprocess.run([exe, d, os.path.join(d, "index.tsv"), "-", "0"], input=lines, env=env,
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    firsts = [int(ln.split()[1]) for ln in proc.stdout.splitlines() if ln.startswith("FIRST")]
+    got = [[int(x) for x in ln.split()[1:]] for ln in proc.stdout.splitlines() if ln.startswith("GEN:")]
+    assert firsts == [int(t) for t in fx["first" + sfx]]
+    assert got == [[int(t) for t in g] for g in gens], (got, gens)
+
+
+def test_gemma_engine_refuses_drafting(gemma):
+    """the layout's drafter rounds (ENGINE_K > 0, E:1519-1563) are refused with a message"""
+    dev, d, fx, ctx = gemma
+    exe = os.path.join(os.path.dirname(HERE), "gemma4-e2b-laptop-cpu_amd", "g4v_engine")
+    env = dict(os.environ, ENGINE_K="3", ENGINE_CTX=str(ctx))
+    pf = os.path.join(d, "p.ids")
+    with open(pf, "w") as f:
+        f.write("5 6 7\n")
+    proc = subprocess.run([exe, d, os.path.join(d, "index.tsv"), pf, "4"], env=env, capture_output=True, text=True,
+                          timeout=300)
+    assert proc.returncode == 2 and "ENGINE_K=0" in proc.stderr, (proc.returncode, proc.stderr[-500:])
