@@ -17,12 +17,15 @@ __constant__ uint64_t c_expf_tab_hd[32] = G4V_EXPF_TABLE;
 
 constexpr int AHD_THREADS = 256;
 
+// geometry from the launch (gv) or, when gp is given, from device memory (a drafter chain's steps)
 template <int D>
 __global__ __launch_bounds__(AHD_THREADS) void k_attn_split_d(const uint16_t* __restrict__ KC,
                                                               const uint16_t* __restrict__ VC,
-                                                              const float* __restrict__ q, int ldq, AttnGeom g,
+                                                              const float* __restrict__ q, int ldq, AttnGeom gv,
+                                                              const AttnGeom* __restrict__ gp,
                                                               float* __restrict__ po, float* __restrict__ pm,
                                                               float* __restrict__ pl) {
+  const AttnGeom& g = gp ? *gp : gv;
   __shared__ __align__(16) float qs[D];       // the head's query in key-slot order (kc_slot_d)
   __shared__ float sw[ATT_SPLIT_MAX];         // scores, then weights, of the split's positions
   __shared__ float red[AHD_THREADS / 64];
@@ -148,10 +151,21 @@ int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, 
   if (hd != 512 || g.M < 1 || g.M > MAXM || g.T < 1 || g.T > MAXT) return -1;
   const int len = g.kmax - g.kmin + 1;
   if (len < 1 || (len + g.T - 1) / g.T + 1 > ATT_SPLIT_MAX) return -1;
-  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(g.T, g.M, NQ), dim3(AHD_THREADS), 0, st, KC, VC, q, ldq, g, po, pm,
-                     pl);
+  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(g.T, g.M, NQ), dim3(AHD_THREADS), 0, st, KC, VC, q, ldq, g,
+                     (const AttnGeom*)nullptr, po, pm, pl);
   hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(g.M, NQ), dim3(512), 0, st, po, pm, pl, g.M, g.T, out, ldo, gs);
   return 0;
+}
+
+void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev,
+                             int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st) {
+  AttnGeom g{};
+  g.M = M;
+  g.T = T;
+  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(T, M, nh), dim3(AHD_THREADS), 0, st, KC, VC, q, ldq, g, gdev, po, pm,
+                     pl);
+  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(M, nh), dim3(512), 0, st, po, pm, pl, M, T, out, ldo,
+                     (float*)nullptr);
 }
 
 }  // namespace g4v

@@ -131,6 +131,8 @@ struct g4v_ctx {
   // states, centroid scores, candidates and their scores, tokens, runners-up, gaps)
   bool dr_ready = false;
   int dr_C = 0;
+  int dr_hd[4] = {256, 256, 256, 256};  // layer head dims (the global layer 3: 256 synthetic, 512 loaded)
+  float dr_scalar[4] = {0.75f, 0.75f, 0.75f, 0.75f};
   DBuf dr_pre, dr_post, dr_cent, dr_emb, dr_order, dr_norms, dr_q[4], dr_o[4], dr_g[4], dr_u[4], dr_d[4], dr_s;
   int last_hrow = -1;  // row of c->h holding the last verify step's committed hidden state
   int* dr_in_host = nullptr;   // pinned chain inputs {tok, P, hrow, _, h[1536]}
@@ -1758,6 +1760,8 @@ static void pf_segment(g4v_ctx* c, const PfGeom& g, int r0, int M, bool i8, bool
 // prefill path runs a block (plain row layouts, the exact-float GEMV or, for prompt blocks with
 // g4v_set_prefill_int8, W4A8), eagerly; the head and acceptance are the verify pass's own.
 // ---------------------------------------------------------------------------------------
+}  // extern "C"
+
 namespace {
 constexpr int GM_NL = 35, GM_PD = 256, GM_ROWS = 32, GM_PLN = GM_NL * GM_PD;
 int gm_hd(int l) { return l % 5 != 4 ? 256 : 512; }
@@ -2009,6 +2013,8 @@ int g4v_model_set_ple_rows(g4v_ctx* c, int tok0, int n, const uint16_t* rows) {
 
 }  // extern "C"
 
+extern "C" {
+
 static int gm_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint16_t* s) {
   ARGCHK(l >= 0 && l < GM_NL && j >= 0 && j < 9, "model_set_matrix: layer or matrix index out of range");
   ARGCHK(c->gm[l].own || (j != 1 && j != 2), "model_set_matrix: layers past 14 have no k / v projection (E:1251)");
@@ -2183,7 +2189,10 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
 // MTP drafter
 // ---------------------------------------------------------------------------------------
 namespace {
-constexpr int DR_H = 256, DR_Q = 4, DR_F = 2048, DR_NC = 32 * 128;
+constexpr int DR_H = 256, DR_Q = 4, DR_F = 2048, DR_NC = 32 * 128, DR_HDMAX = 512;
+// drafter norms on the device: [4 layers][5: in_ln, post_attn, pre_ff, post_ff, q_norm][512],
+// then the final norm [256]
+constexpr int DR_NSTRIDE = 512, DR_NORM_FLOATS = 20 * DR_NSTRIDE + DR_H;
 // scratch layout (floats / ints) of a drafter chain
 constexpr int DR_IN_WORDS = 4 + H, DR_OUT_WORDS = 24 + H;
 struct DrScratch {
@@ -2199,8 +2208,8 @@ DrScratch dr_scratch(g4v_ctx* c) {
   d.yo = d.dx[1] + DR_H;
   d.ydown = d.yo + DR_H;
   d.dq = d.ydown + DR_H;
-  d.dopt = d.dq + DR_Q * DR_H;
-  d.act = d.dopt + DR_Q * DR_H;
+  d.dopt = d.dq + DR_Q * DR_HDMAX;
+  d.act = d.dopt + DR_Q * DR_HDMAX;
   d.dh = d.act + DR_F;
   d.bout[0] = d.dh + DR_H;
   d.bout[1] = d.bout[0] + H;
@@ -2216,7 +2225,7 @@ DrScratch dr_scratch(g4v_ctx* c) {
   d.geo = reinterpret_cast<AttnGeom*>(d.din + DR_IN_WORDS);
   return d;
 }
-constexpr size_t DR_SCRATCH_BYTES = (size_t)(5 * DR_H + 2 * DR_Q * DR_H + DR_F + 3 * H + 4096 + DR_NC + 16) * 4 +
+constexpr size_t DR_SCRATCH_BYTES = (size_t)(5 * DR_H + 2 * DR_Q * DR_HDMAX + DR_F + 3 * H + 4096 + DR_NC + 16) * 4 +
                                     (size_t)(32 + 16 + 16 + DR_IN_WORDS) * 4 + 16 * sizeof(AttnGeom);
 }  // namespace
 
@@ -2229,8 +2238,14 @@ extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
   ARGCHK(c->V % 2048 == 0 && c->V / 128 >= 32 && c->V / 128 <= 4096,
          "drafter_synth: the vocabulary must be 128 x C tokens with 32 <= C <= 4096 centroids, C % 16 == 0");
   ARGCHK(c->NL >= 15, "drafter_synth: the drafter reads the KV cache of target layers 13 and 14");
+  ARGCHK(!c->gemma, "drafter_synth: the Gemma layout's layer 14 has head dim 512: load a drafter checkpoint "
+                    "(g4v_drafter_load)");
   HIPCHK(hipSetDevice(c->device));
   drop_graphs(c);  // captured chains hold the drafter buffers
+  for (int l = 0; l < 4; ++l) {
+    c->dr_hd[l] = HD;
+    c->dr_scalar[l] = 0.75f;
+  }
   hipStream_t st = c->st;
   const int V = c->V, C = V / 128;
   if (!c->dr_in_host) HIPCHK(hipHostMalloc((void**)&c->dr_in_host, DR_IN_WORDS * 4, hipHostMallocDefault));
@@ -2253,17 +2268,17 @@ extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
   if ((r = gen(c->dr_post, (size_t)H * DR_H, 5300, 0.06f)) || (r = gen(c->dr_cent, (size_t)C * DR_H, 5301, 0.06f)) ||
       (r = gen(c->dr_emb, (size_t)V * DR_H, 5303, 0.06f)))
     return r;
-  // norms [4][5][256] (in_ln, post_attn, pre_ff, post_ff, q_norm) then the final norm [256]
-  std::vector<float> nv(21 * DR_H);
+  // norms (in_ln, post_attn, pre_ff, post_ff, q_norm per layer) then the final norm
+  std::vector<float> nv(DR_NORM_FLOATS, 0.f);
   for (int l = 0; l < 4; ++l)
     for (int t = 0; t < 5; ++t) {
       const uint64_t sn = rng_stream(seed, 5200 + 10 * (uint64_t)l + t);
       const float base = t < 4 ? 0.5f : 0.2f, span = t < 4 ? 1.0f : 0.1f;
-      for (int i = 0; i < DR_H; ++i) nv[(l * 5 + t) * DR_H + i] = r16(base + span * rng_unif(sn, i));
+      for (int i = 0; i < DR_H; ++i) nv[(l * 5 + t) * DR_NSTRIDE + i] = r16(base + span * rng_unif(sn, i));
     }
   {
     const uint64_t sn = rng_stream(seed, 5302);
-    for (int i = 0; i < DR_H; ++i) nv[20 * DR_H + i] = r16(0.5f + rng_unif(sn, i));
+    for (int i = 0; i < DR_H; ++i) nv[20 * DR_NSTRIDE + i] = r16(0.5f + rng_unif(sn, i));
   }
   std::vector<int> order(V);
   for (int i = 0; i < V; ++i) order[i] = i;
@@ -2281,6 +2296,74 @@ extern "C" int g4v_drafter_synth(g4v_ctx* c, uint64_t seed) {
   return 0;
 }
 
+// E:1519-1528: a drafter checkpoint's tensors onto the device
+extern "C" int g4v_drafter_load(g4v_ctx* c, const g4v_drafter_tensors* t) {
+  if (!c || !t) return G4V_E_ARG;
+  if (!c->model_ready) {
+    c->err = "drafter_load: no model";
+    return G4V_E_STATE;
+  }
+  ARGCHK(c->NL >= 15, "drafter_load: the drafter reads the KV cache of target layers 13 and 14");
+  const int C = t->C, V = c->V;
+  ARGCHK(C >= 32 && C <= 4096 && C % 16 == 0 && (long long)C * 128 == V,
+         "drafter_load: the vocabulary must be 128 x C tokens with 32 <= C <= 4096 centroids, C % 16 == 0");
+  const int hd14 = c->gemma ? c->gm[14].hd : HD;
+  for (int l = 0; l < 4; ++l)
+    ARGCHK(t->hd[l] == (l < 3 ? HD : hd14),
+           "drafter_load: layers 0..2 have head dim 256, layer 3 that of the target's layer 14 (E:1525)");
+  ARGCHK(t->pre && t->post && t->cent && t->emb && t->norm && t->order, "drafter_load: null tensor");
+  for (int l = 0; l < 4; ++l) {
+    ARGCHK(t->q[l] && t->o[l] && t->gate[l] && t->up[l] && t->down[l], "drafter_load: null tensor");
+    for (int k = 0; k < 5; ++k) ARGCHK(t->nv[l][k], "drafter_load: null norm");
+  }
+  for (long long i = 0; i < V; ++i)
+    ARGCHK(t->order[i] >= 0 && t->order[i] < V, "drafter_load: token ordering outside the vocabulary");
+  HIPCHK(hipSetDevice(c->device));
+  drop_graphs(c);  // captured chains hold the drafter buffers
+  hipStream_t st = c->st;
+  if (!c->dr_in_host) HIPCHK(hipHostMalloc((void**)&c->dr_in_host, DR_IN_WORDS * 4, hipHostMallocDefault));
+  if (!c->dr_out_host) HIPCHK(hipHostMalloc((void**)&c->dr_out_host, DR_OUT_WORDS * 4, hipHostMallocDefault));
+  auto put = [&](DBuf& b, const uint16_t* src, size_t n) -> int {
+    ALLOC(b, n * 2);
+    HIPCHK(hipMemcpyAsync(b.p, src, n * 2, hipMemcpyHostToDevice, st));
+    return 0;
+  };
+  int r;
+  if ((r = put(c->dr_pre, t->pre, (size_t)DR_H * 2 * H)) || (r = put(c->dr_post, t->post, (size_t)H * DR_H)) ||
+      (r = put(c->dr_cent, t->cent, (size_t)C * DR_H)) || (r = put(c->dr_emb, t->emb, (size_t)V * DR_H)))
+    return r;
+  auto bf = [](uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+  };
+  std::vector<float> nv(DR_NORM_FLOATS, 0.f);
+  for (int l = 0; l < 4; ++l) {
+    const int hd = t->hd[l];
+    if ((r = put(c->dr_q[l], t->q[l], (size_t)DR_Q * hd * DR_H)) || (r = put(c->dr_o[l], t->o[l], (size_t)DR_H * DR_Q * hd)) ||
+        (r = put(c->dr_g[l], t->gate[l], (size_t)DR_F * DR_H)) || (r = put(c->dr_u[l], t->up[l], (size_t)DR_F * DR_H)) ||
+        (r = put(c->dr_d[l], t->down[l], (size_t)DR_H * DR_F)))
+      return r;
+    for (int k = 0; k < 5; ++k)
+      for (int i = 0; i < (k < 4 ? DR_H : hd); ++i) nv[(l * 5 + k) * DR_NSTRIDE + i] = bf(t->nv[l][k][i]);
+    c->dr_hd[l] = hd;
+    c->dr_scalar[l] = bf(t->scalar[l]);
+  }
+  for (int i = 0; i < DR_H; ++i) nv[20 * DR_NSTRIDE + i] = bf(t->norm[i]);
+  std::vector<int> order(V);
+  for (int i = 0; i < V; ++i) order[i] = (int)t->order[i];
+  ALLOC(c->dr_norms, nv.size() * 4);
+  ALLOC(c->dr_order, (size_t)V * 4);
+  ALLOC(c->dr_s, DR_SCRATCH_BYTES);
+  HIPCHK(hipMemcpyAsync(c->dr_norms.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(c->dr_order.p, order.data(), (size_t)V * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(hipStreamSynchronize(st));
+  c->dr_C = C;
+  c->dr_ready = true;
+  return 0;
+}
+
 // the kernels of a k-step chain with nsplit attention splits; inputs from the pinned input
 // block, outputs to the pinned output block (both copies are part of the sequence, so that a
 // captured chain replays them)
@@ -2288,7 +2371,7 @@ static void enqueue_draft(g4v_ctx* c, int k, int nsplit) {
   hipStream_t st = c->st;
   const DrScratch d = dr_scratch(c);
   const float* nv = c->dr_norms.as<float>();
-  auto nrm = [&](int l, int t) { return nv + (l * 5 + t) * DR_H; };
+  auto nrm = [&](int l, int t) { return nv + (l * 5 + t) * DR_NSTRIDE; };
   (void)hipMemcpyAsync(d.din, c->dr_in_host, DR_IN_WORDS * 4, hipMemcpyHostToDevice, st);
   launch_dr_setup(d.din, c->h.as<float>(), d.hin, d.tok, d.geo, k, nsplit, st);
   for (int j = 0; j < k; ++j) {  // E:1631-1633: step j at position P + 1 + j, keys up to P
@@ -2303,28 +2386,37 @@ static void enqueue_draft(g4v_ctx* c, int k, int nsplit) {
     }
     for (int l = 0; l < 4; ++l) {
       const bool sliding = l < 3;
-      const int ty = sliding ? 0 : 1, ol = sliding ? 13 : 14;
-      const float* cs = c->rope.as<float>() + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
-      const float* sn = cs + (size_t)c->ctxcap * (HD / 2);
+      const int ty = sliding ? 0 : 1, ol = sliding ? 13 : 14, hd = c->dr_hd[l];  // E:1540
+      // the target's RoPE table of the layer type ([ctxcap][hd / 2] cos, then sin) and cache of
+      // layer 13 / 14: the synthetic stack's, or the Gemma layout's owner caches
+      const float* cs = c->gemma && ty ? c->gm_rope.as<float>()
+                                       : c->rope.as<float>() + (size_t)(2 * ty) * c->ctxcap * (HD / 2);
+      const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
+      const uint16_t* Kl = c->gemma ? c->gm_kv.as<uint16_t>() + c->gm_koff[ol]
+                                    : c->KC.as<uint16_t>() + (size_t)ol * c->kvcap * HD;
+      const uint16_t* Vl = c->gemma ? c->gm_kv.as<uint16_t>() + c->gm_voff[ol]
+                                    : c->VC.as<uint16_t>() + (size_t)ol * c->kvcap * HD;
       {  // q (E:1541), with the previous layer's post-FFN block in front (E:1548-1550)
         B16Launch L;
-        L.W = c->dr_q[l].as<uint16_t>(), L.N = DR_Q * DR_H, L.K = DR_H, L.x = dxc, L.y = d.dq, L.nw = nrm(l, 0);
+        L.W = c->dr_q[l].as<uint16_t>(), L.N = DR_Q * hd, L.K = DR_H, L.x = dxc, L.y = d.dq, L.nw = nrm(l, 0);
         if (l == 0) {
           L.pro = 1;
         } else {
-          L.pro = 5, L.yin = d.ydown, L.w1 = nrm(l - 1, 3), L.scalar = 0.75f, L.dxout = next_dx();
+          L.pro = 5, L.yin = d.ydown, L.w1 = nrm(l - 1, 3), L.scalar = c->dr_scalar[l - 1], L.dxout = next_dx();
           dxc = L.dxout;
         }
         launch_b16(L, st);
       }
-      launch_dr_qnorm(d.dq, nrm(l, 4), cs, sn, d.din + 1, j, st);
-      launch_attn_geom_dev(c->KC.as<uint16_t>() + (size_t)ol * c->kvcap * HD,
-                           c->VC.as<uint16_t>() + (size_t)ol * c->kvcap * HD, d.dq, DR_Q * DR_H, d.geo + 2 * j + ty, 1,
-                           nsplit, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), d.dopt, DR_Q * DR_H, st,
-                           DR_Q);
+      launch_dr_qnorm(d.dq, nrm(l, 4), cs, sn, d.din + 1, j, hd, st);
+      if (hd == 512)
+        launch_attn_geom_dev_hd(Kl, Vl, d.dq, DR_Q * hd, d.geo + 2 * j + ty, 1, nsplit, DR_Q, c->po5.as<float>(),
+                                c->pm5.as<float>(), c->pl5.as<float>(), d.dopt, DR_Q * hd, st);
+      else
+        launch_attn_geom_dev(Kl, Vl, d.dq, DR_Q * hd, d.geo + 2 * j + ty, 1, nsplit, c->po.as<float>(),
+                             c->pm.as<float>(), c->pl.as<float>(), d.dopt, DR_Q * hd, st, DR_Q);
       {  // o (E:1545)
         B16Launch L;
-        L.W = c->dr_o[l].as<uint16_t>(), L.N = DR_H, L.K = DR_Q * DR_H, L.x = d.dopt, L.y = d.yo;
+        L.W = c->dr_o[l].as<uint16_t>(), L.N = DR_H, L.K = DR_Q * hd, L.x = d.dopt, L.y = d.yo;
         launch_b16(L, st);
       }
       {  // gate / up + activation (E:1547), with the post-attention block in front (E:1545-1546)
@@ -2343,7 +2435,7 @@ static void enqueue_draft(g4v_ctx* c, int k, int nsplit) {
     {  // the last post-FFN block, the final norm (E:1551), post-projection and centroid scores
       B16Launch L;
       L.W = c->dr_post.as<uint16_t>(), L.N = H, L.K = DR_H, L.x = dxc, L.y = d.bout[j & 1], L.pro = 6, L.epi = 1;
-      L.yin = d.ydown, L.w1 = nrm(3, 3), L.scalar = 0.75f, L.nw = nrm(4, 0), L.xout = d.dh;
+      L.yin = d.ydown, L.w1 = nrm(3, 3), L.scalar = c->dr_scalar[3], L.nw = nrm(4, 0), L.xout = d.dh;
       launch_b16(L, st);
       L.W = c->dr_cent.as<uint16_t>(), L.N = c->dr_C, L.y = d.dscore, L.epi = 0, L.xout = nullptr;
       launch_b16(L, st);
@@ -2373,7 +2465,8 @@ extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, 
   }
   ARGCHK(drafts && k >= 1 && k <= 8 && P >= 0 && P + k < c->ctxcap, "draft_mtp: 1 <= k <= 8, P + k < ctxcap");
   ARGCHK(tok >= 0 && tok < c->V, "draft_mtp: token outside the vocabulary");
-  ARGCHK(nsplit >= 1 && nsplit <= MAXT && (P + 1 + nsplit - 1) / nsplit <= attn_pmax(),
+  ARGCHK(nsplit >= 1 && nsplit <= MAXT && (P + 1 + nsplit - 1) / nsplit <= attn_pmax() &&
+             (P + 1 + nsplit - 1) / nsplit + 1 <= ATT_SPLIT_MAX,
          "draft_mtp: 1 <= nsplit <= 16 and no more positions per split than the split buffer holds");
   if (!h && c->last_hrow < 0) {
     c->err = "draft_mtp: no hidden state given and no verify step ran";

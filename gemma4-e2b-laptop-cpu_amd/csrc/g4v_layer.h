@@ -155,7 +155,8 @@ struct B16Launch {
 };
 void launch_b16(const B16Launch& L, hipStream_t st);
 // q heads normed and rotated at position *Pp + 1 + j
-void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, const int* Pp, int j, hipStream_t st);
+void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, const int* Pp, int j, int hd,
+                     hipStream_t st);
 // a chain's inputs: in = {tok, P, hrow, _, h[1536]}; hin = h (hrow < 0) or hbase row hrow;
 // tok[0] = tok; geo[2 j + s] = the attention geometry of step j on sliding (s = 0) / global layers
 void launch_dr_setup(const int* in, const float* hbase, float* hin, int* tok, AttnGeom* geo, int k, int T,
@@ -178,6 +179,10 @@ void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, in
 constexpr int ATT_SPLIT_MAX = 4096;
 int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g, int hd,
                         float* po, float* pm, float* pl, float* out, int ldo, float* gs, hipStream_t st);
+// head dim 512 with the geometry read from device memory (M rows, T splits and nh heads fixed by
+// the launch; at most ATT_SPLIT_MAX keys per split, which the caller checks), out plain [M][ldo]
+void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev,
+                             int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st);
 // the same with the geometry read from device memory (M rows and T splits fixed by the launch)
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
                           int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);

@@ -136,24 +136,26 @@ __global__ __launch_bounds__(256) void k_b16(B16Args a) {
   }
 }
 
-// per head (4): x = r16((x * r) * qn), then NeoX RoPE at the step's position (E:1542)
-__global__ __launch_bounds__(HD) void k_dr_qnorm(float* __restrict__ q, const float* __restrict__ qn,
-                                                 const float* __restrict__ cs, const float* __restrict__ sn,
-                                                 const int* __restrict__ Pp, int j) {
+// per head (4): x = r16((x * r) * qn), then NeoX RoPE at the step's position (E:1542); D the
+// layer's head dim (256, or 512 for the global layer of a drafter checkpoint)
+template <int D>
+__global__ __launch_bounds__(D) void k_dr_qnorm(float* __restrict__ q, const float* __restrict__ qn,
+                                                const float* __restrict__ cs, const float* __restrict__ sn,
+                                                const int* __restrict__ Pp, int j) {
   constexpr int NV = 4;
   const int pos = *Pp + 1 + j;
-  __shared__ float xv[NV][HD];
+  __shared__ float xv[NV][D];
   __shared__ double part[NV][16];
   __shared__ float rinv[NV];
   const int e = threadIdx.x;
 #pragma unroll
-  for (int h = 0; h < NV; ++h) xv[h][e] = q[h * HD + e];
+  for (int h = 0; h < NV; ++h) xv[h][e] = q[h * D + e];
   __syncthreads();
-  if (e < NV * 16) {
+  if (e < NV * 16) {  // ss_avx2 order (E:326-343): lane t16 sums x[16 i + t16]^2 over i
     const int row = e >> 4, t16 = e & 15;
     double s = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < D / 16; ++i) {
       const double d = (double)xv[row][16 * i + t16];
       s = fma(d, d, s);
     }
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(HD) void k_dr_qnorm(float* __restrict__ q, const fl
     double a[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) a[k] = (p[k] + p[4 + k]) + (p[8 + k] + p[12 + k]);
-    rinv[e] = rms_inv((a[0] + a[2]) + (a[1] + a[3]), HD);
+    rinv[e] = rms_inv((a[0] + a[2]) + (a[1] + a[3]), D);
   }
   __syncthreads();
   float y[NV];
@@ -175,11 +177,11 @@ __global__ __launch_bounds__(HD) void k_dr_qnorm(float* __restrict__ q, const fl
 #pragma unroll
   for (int h = 0; h < NV; ++h) xv[h][e] = y[h];
   __syncthreads();
-  const int i2 = e & (HD / 2 - 1);
-  const float c = cs[(size_t)pos * (HD / 2) + i2], sv = sn[(size_t)pos * (HD / 2) + i2];
+  const int i2 = e & (D / 2 - 1);
+  const float c = cs[(size_t)pos * (D / 2) + i2], sv = sn[(size_t)pos * (D / 2) + i2];
 #pragma unroll
   for (int h = 0; h < NV; ++h)
-    q[h * HD + e] = e < HD / 2 ? fmaf(xv[h][e], c, -(xv[h][e + HD / 2] * sv)) : fmaf(xv[h][e], c, xv[h][e - HD / 2] * sv);
+    q[h * D + e] = e < D / 2 ? fmaf(xv[h][e], c, -(xv[h][e + D / 2] * sv)) : fmaf(xv[h][e], c, xv[h][e - D / 2] * sv);
 }
 
 // a chain's inputs (E:1631-1633): the hidden state, the first token and, per step j, the
@@ -313,8 +315,10 @@ void launch_b16(const B16Launch& L, hipStream_t st) {
 #undef G4V_B16
 }
 
-void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, const int* Pp, int j, hipStream_t st) {
-  hipLaunchKernelGGL(k_dr_qnorm, dim3(1), dim3(HD), 0, st, q, qn, cs, sn, Pp, j);
+void launch_dr_qnorm(float* q, const float* qn, const float* cs, const float* sn, const int* Pp, int j, int hd,
+                     hipStream_t st) {
+  if (hd == 512) hipLaunchKernelGGL(k_dr_qnorm<512>, dim3(1), dim3(512), 0, st, q, qn, cs, sn, Pp, j);
+  else hipLaunchKernelGGL(k_dr_qnorm<HD>, dim3(1), dim3(HD), 0, st, q, qn, cs, sn, Pp, j);
 }
 void launch_dr_setup(const int* in, const float* hbase, float* hin, int* tok, AttnGeom* geo, int k, int T,
                      hipStream_t st) {

@@ -13,8 +13,8 @@
 // "synth:SEED:V:NL:I" for the synthetic stack (<index> ignored).  A checkpoint holding the
 // per-layer-input tensors is the Gemma-4-E2B layout main() loads (E:1222-1231: 35 layers of head
 // dim 256 / 512, k/v projections in layers 0..14, per-layer MLP widths, the per-layer embedding
-// table) and runs through g4v_model_create_gemma; that layout decodes with ENGINE_K=0 (one-row
-// passes, E:1615).  Any other checkpoint is read as a uniform stack: every layer with its
+// table) and runs through g4v_model_create_gemma; its MTP drafter is the drafter checkpoint
+// main() loads with ENGINE_K > 0 (ENGINE_DRAFTER_DIR / ENGINE_DRAFTER_INDEX, E:1519-1528).  Any other checkpoint is read as a uniform stack: every layer with its
 // own q/k/v projections of 8 x 256 / 256 / 256 rows and one MLP width.  The MTP drafter is the
 // synthetic one (ENGINE_DRAFTER_SEED; with a uniform checkpoint only when set).  run_req (E:1584-1676) is restated over the C ABI: the prefix cache
 // (g4v_slot_*), the prefill (g4v_prefill), and decode rounds whose drafts come from prompt
@@ -194,6 +194,44 @@ void load_gemma(const Checkpoint& ck, int V, int ctx) {
       check(g4v_model_set_ple_rows(G, t0, std::min(8192, V - t0), rows + (size_t)t0 * N), "model_set_ple_rows");
   }
   check(g4v_model_set_final_norm(G, ck.vec("norm.weight", H).data()), "model_set_final_norm");
+}
+
+// E:1519-1528: the drafter checkpoint (bf16 tensors, the token ordering int64) into the library
+void load_drafter(const Checkpoint& dk) {
+  const int DH = 256, H = 1536, F = 2048;
+  const Tensor* ce = dk.find("masked_embedding.centroids.weight");
+  const Tensor* em = dk.find("model.embed_tokens.weight");
+  if (!ce || ce->shape.size() != 2 || !em || em->shape.size() != 2)
+    Checkpoint::fail("drafter: masked_embedding.centroids.weight / model.embed_tokens.weight missing");
+  const int C = (int)ce->shape[0], V = (int)em->shape[0];
+  auto bf = [&](const std::string& n, size_t count) {
+    return (const uint16_t*)dk.data(dk.get(n, "BF16", count * 2));
+  };
+  g4v_drafter_tensors t{};
+  t.C = C;
+  t.pre = bf("pre_projection.weight", (size_t)DH * 2 * H);
+  t.post = bf("post_projection.weight", (size_t)H * DH);
+  t.cent = bf("masked_embedding.centroids.weight", (size_t)C * DH);
+  t.emb = bf("model.embed_tokens.weight", (size_t)V * DH);
+  t.norm = bf("model.norm.weight", DH);
+  t.order = (const int64_t*)dk.data(dk.get("masked_embedding.token_ordering", "I64", (size_t)V * 8));
+  const char* nn[5] = {"input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                       "post_feedforward_layernorm", "self_attn.q_norm"};
+  for (int l = 0; l < 4; ++l) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    const Tensor* q = dk.find(p + "self_attn.q_proj.weight");
+    if (!q || q->shape.size() != 2) Checkpoint::fail("drafter: " + p + "self_attn.q_proj.weight missing");
+    const int hd = (int)q->shape[0] / 4;
+    t.hd[l] = hd;
+    t.q[l] = bf(p + "self_attn.q_proj.weight", (size_t)4 * hd * DH);
+    t.o[l] = bf(p + "self_attn.o_proj.weight", (size_t)DH * 4 * hd);
+    t.gate[l] = bf(p + "mlp.gate_proj.weight", (size_t)F * DH);
+    t.up[l] = bf(p + "mlp.up_proj.weight", (size_t)F * DH);
+    t.down[l] = bf(p + "mlp.down_proj.weight", (size_t)DH * F);
+    for (int k = 0; k < 5; ++k) t.nv[l][k] = bf(p + nn[k] + ".weight", k < 4 ? DH : hd);
+    t.scalar[l] = bf(p + "layer_scalar", 1)[0];
+  }
+  check(g4v_drafter_load(G, &t), "drafter_load");
 }
 
 // the stack of a checkpoint into the library (g4v_model_create + setters); returns V
@@ -505,9 +543,13 @@ int main(int argc, char** argv) {
     while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
   }
   const char* dseed = getenv("ENGINE_DRAFTER_SEED");
-  if (gemma && e.k_draft > 0) {  // E:1519-1528: rounds without lookup drafts would need the drafter
-    fprintf(stderr, "g4v_engine: the per-layer-input layout runs without the MTP drafter here: set ENGINE_K=0\n");
-    return 2;
+  Checkpoint dk;
+  if (gemma && e.k_draft > 0) {  // E:1519-1528: the drafter checkpoint main() loads when ENGINE_K > 0
+    const char* dc = getenv("ENGINE_DRAFTER_DIR") ? getenv("ENGINE_DRAFTER_DIR") : "ckpt-e2b-assistant";
+    const char* di = getenv("ENGINE_DRAFTER_INDEX") ? getenv("ENGINE_DRAFTER_INDEX") : "runs/drafter_index.tsv";
+    dk.open_files(dc, di);
+    load_drafter(dk);
+    e.drafter = true;
   }
   if (!gemma && e.k_draft > 0 && NL >= 15 && V % 2048 == 0 && (synth || dseed)) {
     check(g4v_drafter_synth(G, dseed ? strtoull(dseed, nullptr, 10) : seed + 1), "drafter_synth");

@@ -63,6 +63,7 @@ SIGNATURES = {
     "g4v_set_prefill_int8": (_i, [_vp, _i]),
     "g4v_prefill": (_i, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(_i), _vp]),
     "g4v_drafter_synth": (_i, [_vp, C.c_uint64]),
+    "g4v_drafter_load": (_i, [_vp, _vp]),
     "g4v_draft_mtp": (_i, [_vp, _i, _vp, _i, _i, _i, _i32p, _vp, _vp, _vp]),
     "g4v_slots_init": (_i, [_vp, _i, _i]),
     "g4v_slot_begin": (_i, [_vp, _i32p, _i, C.POINTER(_i), C.POINTER(_i)]),
@@ -76,6 +77,13 @@ SIGNATURES = {
 # kernel classes of g4v_profile (include/g4v.h)
 PROF_TAGS = ["gemv_qkv", "gemv_o", "gemv_gateup", "gemv_down", "attn", "rows", "head_screen", "head_select",
              "head_rescore", "head_full", "head_tie", "accept", "head_pass2"]
+
+
+class DrafterTensors(C.Structure):
+    """g4v_drafter_tensors (include/g4v.h)"""
+    _fields_ = [(n, _vp) for n in ("pre", "post", "cent", "emb", "norm", "order")] + \
+               [(n, _vp * 4) for n in ("q", "o", "gate", "up", "down")] + \
+               [("nv", (_vp * 5) * 4), ("scalar", C.c_uint16 * 4), ("C", C.c_int32), ("hd", C.c_int32 * 4)]
 
 
 class VerifyResult(C.Structure):
@@ -320,6 +328,31 @@ class Device:
     # ---- MTP drafter ----
     def drafter_synth(self, seed):
         self._ok(self.L.g4v_drafter_synth(self.h, seed), "drafter_synth")
+
+    def drafter_load(self, t):
+        """t: dict of the drafter checkpoint's arrays (DrafterTensors names; per-layer lists)"""
+        keep = []
+
+        def p(a, dt):
+            a = np.ascontiguousarray(a, dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        dt = DrafterTensors()
+        for n in ("pre", "post", "cent", "emb", "norm"):
+            setattr(dt, n, p(t[n], np.uint16))
+        dt.order = p(t["order"], np.int64)
+        for n in ("q", "o", "gate", "up", "down"):
+            arr = getattr(dt, n)
+            for l in range(4):
+                arr[l] = p(t[n][l], np.uint16)
+        for l in range(4):
+            for k in range(5):
+                dt.nv[l][k] = p(t["nv"][l][k], np.uint16)
+            dt.scalar[l] = int(t["scalar"][l])
+            dt.hd[l] = int(t["hd"][l])
+        dt.C = int(t["C"])
+        self._ok(self.L.g4v_drafter_load(self.h, C.addressof(dt)), "drafter_load")
 
     def draft_mtp(self, tok, h, P, k, nsplit=6):
         """k chained draft steps; h = None takes the last verify step's hidden state.

@@ -193,6 +193,23 @@ int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int nspli
  * (optional) = runner-up token and score gap (g_sec, g_gap); hidden (optional, [1536]) = the
  * last step's output state.  1 <= k <= 8. */
 int g4v_drafter_synth(g4v_ctx* c, uint64_t seed);
+/* A drafter checkpoint (replaces E:1519-1528, the ENGINE_DRAFTER_DIR / ENGINE_DRAFTER_INDEX
+ * loader of main()): bf16 tensors as stored.  pre_projection [256][3072], post_projection
+ * [1536][256], masked_embedding.centroids [C][256], model.embed_tokens [V][256], model.norm [256],
+ * masked_embedding.token_ordering int64 [V]; per layer l: q_proj [4 hd][256], o_proj [256][4 hd],
+ * gate_proj / up_proj [2048][256], down_proj [256][2048], norms nv[l] = input_layernorm,
+ * post_attention_layernorm, pre_feedforward_layernorm, post_feedforward_layernorm [256] and
+ * q_norm [hd], layer_scalar.  hd[l] = 256 for l < 3; layer 3 has the head dim of the target's
+ * layer 14 (512 on the Gemma-4-E2B layout, 256 on the synthetic stack).  V = 128 C. */
+typedef struct {
+  const uint16_t *pre, *post, *cent, *emb, *norm;
+  const int64_t* order;
+  const uint16_t *q[4], *o[4], *gate[4], *up[4], *down[4];
+  const uint16_t* nv[4][5];
+  uint16_t scalar[4];
+  int32_t C, hd[4];
+} g4v_drafter_tensors;
+int g4v_drafter_load(g4v_ctx* c, const g4v_drafter_tensors* t);
 int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, int nsplit, int* drafts, int* sec, float* gap,
                   float* hidden);
 

@@ -160,6 +160,11 @@ void g4o_gemma_free(g4o_gemma* g);
 void g4o_gemma_forward(g4o_gemma* g, const int* toks, int M, int pos0, int T, int sibling, float* hbuf, int hf);
 /* ENGINE_PREFILL_INT8=1 for the passes that follow: blocks of M >= 2 rows take W4A8 products */
 void g4o_gemma_set_i8(g4o_gemma* g, int on);
+/* the drafter's view of the layout: embedding, owner caches 13 / 14, RoPE tables, head dims */
+void g4o_gemma_target(const g4o_gemma* g, const uint16_t** E, const uint16_t** K, const uint16_t** V,
+                      const float** cs, const float** sn, int* hd);
+/* E:1651: KV rows of slot `from` copied to slot `to` in the 15 owner caches */
+void g4o_gemma_kv_move(g4o_gemma* g, int from, int to);
 /* owner layer l's key (v = 0) or value (v = 1) cache [ctx][hd] */
 const uint16_t* g4o_gemma_cache(const g4o_gemma* g, int l, int v);
 
@@ -202,12 +207,24 @@ void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T);
 /* ---- MTP drafter step (E:1534-1563) on the synthetic target; see g4_oracle_draft.c ---- */
 typedef struct g4o_drafter g4o_drafter;
 g4o_drafter* g4o_drafter_new(uint64_t seed, int V);
+/* a drafter checkpoint (E:1519-1528), tensors as stored (bf16; token ordering int64) */
+typedef struct {
+  const uint16_t *pre, *post, *cent, *emb, *dnorm;
+  const int64_t* order;
+  const uint16_t *q[4], *o[4], *gate[4], *up[4], *down[4];
+  const uint16_t* nv[4][5]; /* input, post-attention, pre-FFN, post-FFN layernorms; q_norm */
+  uint16_t scalar[4];
+  int32_t V, C, hd[4];
+} g4o_drafter_in;
+g4o_drafter* g4o_drafter_load(const g4o_drafter_in* in);
 void g4o_drafter_free(g4o_drafter* d);
 const void* g4o_drafter_ptr(const g4o_drafter* d, const char* what);
 int g4o_model_ctx(const g4o_model* m);
 /* b16_rows (E:586-614): y [N] = W [N][K] bf16 . x [K] */
 void g4o_b16_gemv(const uint16_t* W, int N, int K, const float* x, float* y);
 /* one draft step: returns the draft token; b_out [1536], sec, gap as E:1553, 1559 */
+int g4o_gemma_draft_step(const g4o_gemma* g, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
+                         float* b_out, int* sec_out, float* gap_out);
 int g4o_draft_step(const g4o_model* m, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
                    float* b_out, int* sec, float* gap);
 

@@ -7,6 +7,10 @@
  * (E:1557-1559).  The drafter attends the target's KV cache of layer 13 (sliding layers) and
  * 14 (the global layer) with T splits (attn_task + attn_merge, E:1544-1545).
  *
+ * g4o_drafter_load takes a drafter checkpoint's tensors instead (E:1519-1528: layer 3 of head
+ * dim 512, layer scalars from the file), and g4o_gemma_draft_step runs a step against the
+ * Gemma-4-E2B layout's owner caches 13 (head dim 256) and 14 (512).
+ *
  * Synthetic drafter (the product's generator implements the same formulas): 4 layers of
  * hidden 256, 4 query heads of head_dim 256 (the reference's global drafter layer has
  * head_dim 512 like the target's layer 14; the synthetic target's layer 14 has 256), FFN 2048,
@@ -33,7 +37,9 @@
 #define DF 2048
 
 struct g4o_drafter {
-  int V, C;
+  int V, C, owned; /* owned: the bf16 tensors were generated here (else they are the caller's) */
+  int hd[4];       /* layer head dims: 256, and the global layer's (256 synthetic, 512 loaded) */
+  float scalar[4];
   uint16_t *pre, *post, *cent, *emb;
   uint16_t *q[4], *o[4], *gate[4], *up[4], *down[4];
   float *nv[4][5]; /* in_ln, post_attn, pre_ff, post_ff, qn */
@@ -59,6 +65,11 @@ g4o_drafter* g4o_drafter_new(uint64_t seed, int V) {
   g4o_drafter* d = (g4o_drafter*)calloc(1, sizeof(g4o_drafter));
   d->V = V;
   d->C = V / 128;
+  d->owned = 1;
+  for (int l = 0; l < 4; ++l) {
+    d->hd[l] = DH;
+    d->scalar[l] = 0.75f;
+  }
   d->pre = gen_bf16(seed, 5000, (size_t)DH * 2 * H, 0.02f);
   for (int l = 0; l < 4; ++l) {
     d->q[l] = gen_bf16(seed, 5100 + 10 * l, (size_t)DQ * DH * DH, 0.06f);
@@ -85,22 +96,57 @@ g4o_drafter* g4o_drafter_new(uint64_t seed, int V) {
   return d;
 }
 
+/* E:1519-1528: a drafter checkpoint's tensors (kept by the caller), norms widened here */
+static float* widen_bf16(const uint16_t* b, int n) {
+  float* f = (float*)malloc(sizeof(float) * n);
+  for (int i = 0; i < n; ++i) f[i] = g4o_bf2f(b[i]);
+  return f;
+}
+
+g4o_drafter* g4o_drafter_load(const g4o_drafter_in* in) {
+  g4o_drafter* d = (g4o_drafter*)calloc(1, sizeof(g4o_drafter));
+  d->V = in->V;
+  d->C = in->C;
+  d->owned = 0;
+  d->pre = (uint16_t*)in->pre;
+  d->post = (uint16_t*)in->post;
+  d->cent = (uint16_t*)in->cent;
+  d->emb = (uint16_t*)in->emb;
+  d->order = (int64_t*)in->order;
+  d->dnorm = widen_bf16(in->dnorm, DH);
+  for (int l = 0; l < 4; ++l) {
+    d->hd[l] = in->hd[l];
+    d->scalar[l] = g4o_bf2f(in->scalar[l]);
+    d->q[l] = (uint16_t*)in->q[l];
+    d->o[l] = (uint16_t*)in->o[l];
+    d->gate[l] = (uint16_t*)in->gate[l];
+    d->up[l] = (uint16_t*)in->up[l];
+    d->down[l] = (uint16_t*)in->down[l];
+    for (int t = 0; t < 5; ++t) d->nv[l][t] = widen_bf16(in->nv[l][t], t < 4 ? DH : in->hd[l]);
+  }
+  return d;
+}
+
 void g4o_drafter_free(g4o_drafter* d) {
   if (!d) return;
-  free(d->pre);
-  free(d->post);
-  free(d->cent);
-  free(d->emb);
+  if (d->owned) {
+    free(d->pre);
+    free(d->post);
+    free(d->cent);
+    free(d->emb);
+    free(d->order);
+  }
   for (int l = 0; l < 4; ++l) {
-    free(d->q[l]);
-    free(d->o[l]);
-    free(d->gate[l]);
-    free(d->up[l]);
-    free(d->down[l]);
+    if (d->owned) {
+      free(d->q[l]);
+      free(d->o[l]);
+      free(d->gate[l]);
+      free(d->up[l]);
+      free(d->down[l]);
+    }
     for (int t = 0; t < 5; ++t) free(d->nv[l][t]);
   }
   free(d->dnorm);
-  free(d->order);
   free(d);
 }
 
@@ -146,35 +192,42 @@ static void r16n(float* p, int n) {
   for (int i = 0; i < n; ++i) p[i] = g4o_r16(p[i]);
 }
 
+/* the target as the drafter sees it: its embedding, the KV caches [ctx][hd] of layers 13
+ * (type 0, the sliding drafter layers) and 14 (type 1, the global one) and the RoPE tables of
+ * both types [ctx][hd / 2] */
+typedef struct {
+  const uint16_t* E;
+  const uint16_t *K[2], *V[2];
+  const float *cs[2], *sn[2];
+  int hd[2];
+} dr_target;
+
 /* E:1534-1563 draft_step(tok, h, pos, P): the next draft token; b_out [1536] receives the
- * drafter's next hidden state, sec / gap the runner-up and the score gap (E:1559).
- * m: the target (its embedding, RoPE tables and the KV cache of layers 13 and 14). */
-int g4o_draft_step(const g4o_model* m, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
-                   float* b_out, int* sec_out, float* gap_out) {
-  const uint16_t* E = (const uint16_t*)g4o_model_ptr(m, "E");
-  const uint16_t* KC = (const uint16_t*)g4o_model_ptr(m, "KC");
-  const uint16_t* VC = (const uint16_t*)g4o_model_ptr(m, "VC");
-  const int ctx = g4o_model_ctx(m);
-  float comb[2 * H], dx[DH], da[DH], dq[DQ * DH], dopt[DQ * DH], dtmp[DH], act[DF], g[DF], u[DF], dh[DH];
+ * drafter's next hidden state, sec / gap the runner-up and the score gap (E:1559).  -1 when the
+ * drafter's global layer and the target's layer 14 differ in head dim. */
+static int draft_core(const dr_target* tg, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
+                      float* b_out, int* sec_out, float* gap_out) {
+  if (d->hd[3] != tg->hd[1] || d->hd[0] != tg->hd[0]) return -1;
+  float comb[2 * H], dx[DH], da[DH], dq[DQ * 512], dopt[DQ * 512], dtmp[DH], act[DF], g[DF], u[DF], dh[DH];
   const float sqh = sqrtf((float)H);
-  for (int i = 0; i < H; ++i) comb[i] = g4o_r16(g4o_bf2f(E[(size_t)tok * H + i]) * sqh); /* E:1537 */
+  for (int i = 0; i < H; ++i) comb[i] = g4o_r16(g4o_bf2f(tg->E[(size_t)tok * H + i]) * sqh); /* E:1537 */
   memcpy(comb + H, h, sizeof(float) * H);
   g4o_b16_gemv(d->pre, DH, 2 * H, comb, dx); /* E:1539 */
   r16n(dx, DH);
   for (int l = 0; l < 4; ++l) {
-    const int sliding = l < 3, ty = sliding ? 0 : 1, ol = sliding ? 13 : 14;
-    const float* cs = (const float*)g4o_model_ptr(m, ty ? "cs1" : "cs0") + (size_t)pos * DH / 2;
-    const float* sn = (const float*)g4o_model_ptr(m, ty ? "sn1" : "sn0") + (size_t)pos * DH / 2;
+    const int sliding = l < 3, ty = sliding ? 0 : 1, hd = d->hd[l]; /* E:1540: layer 13 / 14 */
+    const float* cs = tg->cs[ty] + (size_t)pos * hd / 2;
+    const float* sn = tg->sn[ty] + (size_t)pos * hd / 2;
     g4o_rms(dx, d->nv[l][0], DH, da); /* E:1541 */
-    g4o_b16_gemv(d->q[l], DQ * DH, DH, da, dq);
+    g4o_b16_gemv(d->q[l], DQ * hd, DH, da, dq);
     for (int h2 = 0; h2 < DQ; ++h2) {
-      g4o_rms_r16_inplace(dq + h2 * DH, d->nv[l][4], DH);
-      g4o_rope(dq + h2 * DH, cs, sn, DH);
+      g4o_rms_r16_inplace(dq + h2 * hd, d->nv[l][4], hd);
+      g4o_rope(dq + h2 * hd, cs, sn, hd);
     }
     int apos = P, alo = sliding ? (pos - 511 > 0 ? pos - 511 : 0) : 0, sl = 1, sh = 0; /* E:1543 */
-    g4o_attn_splitkv(KC + (size_t)ol * ctx * DH, VC + (size_t)ol * ctx * DH, DH, DQ, 1, dq, DQ * DH, &apos, &alo,
-                     &sl, &sh, alo, P, T, dopt, DQ * DH, NULL, NULL);
-    g4o_b16_gemv(d->o[l], DH, DQ * DH, dopt, da); /* E:1545 */
+    g4o_attn_splitkv(tg->K[ty], tg->V[ty], hd, DQ, 1, dq, DQ * hd, &apos, &alo, &sl, &sh, alo, P, T, dopt, DQ * hd,
+                     NULL, NULL);
+    g4o_b16_gemv(d->o[l], DH, DQ * hd, dopt, da); /* E:1545 */
     r16n(da, DH);
     g4o_rms(da, d->nv[l][1], DH, dtmp);
     for (int i = 0; i < DH; ++i) dx[i] = g4o_r16(dx[i] + g4o_r16(dtmp[i]));
@@ -187,7 +240,7 @@ int g4o_draft_step(const g4o_model* m, const g4o_drafter* d, int tok, const floa
     r16n(da, DH);
     g4o_rms(da, d->nv[l][3], DH, dtmp);
     for (int i = 0; i < DH; ++i) dx[i] = g4o_r16(dx[i] + g4o_r16(dtmp[i]));
-    for (int i = 0; i < DH; ++i) dx[i] = g4o_r16(dx[i] * 0.75f); /* E:1549-1550 */
+    for (int i = 0; i < DH; ++i) dx[i] = g4o_r16(dx[i] * d->scalar[l]); /* E:1549-1550 */
   }
   g4o_rms(dx, d->dnorm, DH, dh); /* E:1551 */
   r16n(dh, DH);
@@ -242,4 +295,31 @@ int g4o_draft_step(const g4o_model* m, const g4o_drafter* d, int tok, const floa
   if (sec_out) *sec_out = sec;
   if (gap_out) *gap_out = bs - bs2;
   return bestc;
+}
+
+/* m: the synthetic target (its embedding, RoPE tables and the KV cache of layers 13 and 14) */
+int g4o_draft_step(const g4o_model* m, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
+                   float* b_out, int* sec_out, float* gap_out) {
+  const uint16_t* KC = (const uint16_t*)g4o_model_ptr(m, "KC");
+  const uint16_t* VC = (const uint16_t*)g4o_model_ptr(m, "VC");
+  const size_t ctx = (size_t)g4o_model_ctx(m);
+  dr_target t;
+  t.E = (const uint16_t*)g4o_model_ptr(m, "E");
+  for (int ty = 0; ty < 2; ++ty) {
+    const int ol = 13 + ty;
+    t.K[ty] = KC + ol * ctx * DH;
+    t.V[ty] = VC + ol * ctx * DH;
+    t.cs[ty] = (const float*)g4o_model_ptr(m, ty ? "cs1" : "cs0");
+    t.sn[ty] = (const float*)g4o_model_ptr(m, ty ? "sn1" : "sn0");
+    t.hd[ty] = DH;
+  }
+  return draft_core(&t, d, tok, h, pos, P, T, b_out, sec_out, gap_out);
+}
+
+/* g: the Gemma-4-E2B layout (owner caches 13 and 14 of head dim 256 / 512, E:1540) */
+int g4o_gemma_draft_step(const g4o_gemma* g, const g4o_drafter* d, int tok, const float* h, int pos, int P, int T,
+                         float* b_out, int* sec_out, float* gap_out) {
+  dr_target t;
+  g4o_gemma_target(g, &t.E, t.K, t.V, t.cs, t.sn, t.hd);
+  return draft_core(&t, d, tok, h, pos, P, T, b_out, sec_out, gap_out);
 }

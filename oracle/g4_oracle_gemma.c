@@ -96,6 +96,29 @@ void g4o_gemma_free(g4o_gemma* g) {
   free(g);
 }
 
+/* what the drafter reads of the target (E:1537, 1540-1543): the embedding, owner caches 13 and
+ * 14, and the RoPE tables of both layer types */
+void g4o_gemma_target(const g4o_gemma* g, const uint16_t** E, const uint16_t** K, const uint16_t** V,
+                      const float** cs, const float** sn, int* hd) {
+  *E = g->in.E;
+  for (int ty = 0; ty < 2; ++ty) {
+    K[ty] = g->KC[13 + ty];
+    V[ty] = g->VC[13 + ty];
+    cs[ty] = g->cs[ty];
+    sn[ty] = g->sn[ty];
+    hd[ty] = ty ? 512 : 256;
+  }
+}
+
+/* E:1651: the KV rows of slot `from` copied to slot `to` in every owner cache */
+void g4o_gemma_kv_move(g4o_gemma* g, int from, int to) {
+  for (int l = 0; l < 15; ++l) {
+    const int hd = layer_hd(l);
+    memcpy(g->KC[l] + (size_t)to * hd, g->KC[l] + (size_t)from * hd, sizeof(uint16_t) * hd);
+    memcpy(g->VC[l] + (size_t)to * hd, g->VC[l] + (size_t)from * hd, sizeof(uint16_t) * hd);
+  }
+}
+
 const uint16_t* g4o_gemma_cache(const g4o_gemma* g, int l, int v) {
   if (l < 0 || l >= 15) return NULL;
   return v ? g->VC[l] : g->KC[l];

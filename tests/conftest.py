@@ -51,3 +51,15 @@ def dev(g4v):
 def note(msg):
     """print the case about to run on the GPU (flushed, so a crash still names it)"""
     print(f"\n[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="session")
+def gemma_ckpt(orc, tmp_path_factory):
+    """the synthetic Gemma-4-E2B-layout checkpoint and its drafter checkpoint, written once"""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import gemma_layout as gl
+    d = str(tmp_path_factory.mktemp("gemma_ckpt"))
+    note("writing the synthetic Gemma-layout checkpoint and drafter")
+    E = gl.write_checkpoint(orc, d)
+    gl.write_drafter(orc, d, E)
+    return d

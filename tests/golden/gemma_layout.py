@@ -10,6 +10,17 @@ only for the ids in PLE_IDS (a sparse region of the file, zero elsewhere).
 
 run_req_k0 restates run_req (E:1584-1661) with ENGINE_K=0: the prompt in blocks of 32 rows,
 then one-row decode passes (E:1615), greedy tokens from the certified head, over the oracle.
+
+write_drafter writes a drafter checkpoint in the form main() loads with ENGINE_K > 0 (E:1519-1528:
+bf16 tensors, 4 layers of hidden 256 with 4 query heads, head dim 256 in layers 0..2 and 512 in
+layer 3, FFN 2048, 2048 centroids of 128 tokens).  Its weights are drawn so that its drafts are
+often right on this target: the pre-projection reads only the token's embedding (the hidden-state
+half is zero; A ternary), so the residual stream starts at u_tok ~ A e_tok; the layers add small
+contributions (post-attention / post-FFN norm weights near 0.03); the tokens are ordered into
+clusters by 11 balanced sign splits of u_t along random directions, each centroid being the sum
+of its signed directions, and each token's drafter embedding is u_t / |u_t| scaled by 0.12-0.2.
+The drafter then mostly proposes its input token again (the target's continuations repeat
+tokens here), with score gaps around the sibling thresholds of E:1639-1641.
 """
 import ctypes as C
 import os
@@ -113,6 +124,94 @@ def write_checkpoint(orc, d):
     return E
 
 
+DRAFTER_SEED = 88
+DR_H, DR_F, DR_C = 256, 2048, 2048
+
+
+def bf16_of(x):
+    """round-to-nearest-even bf16 bits of finite float32 values"""
+    u = np.array(x, np.float32).view(np.uint32)
+    r = (u >> 16) & 1
+    u += 0x7FFF
+    u += r
+    u >>= 16
+    return u.astype(np.uint16)
+
+
+def drafter_tensors(orc, E):
+    """(name, dtype, array, shape) of the drafter checkpoint (E:1523-1528) for the target embedding E"""
+    st = lambda tag: orc.stream(DRAFTER_SEED, tag)
+    nrm = lambda tag, n, s=1.0: orc.normal_f32(st(tag), n, s)
+    # A and R ternary: every sum below is exact in float64 (bf16 inputs), so the clustering does
+    # not depend on the summation order of the machine's BLAS
+    A = orc.ints(st(1), DR_H * H, -1, 1).reshape(DR_H, H).astype(np.float64)
+    U = np.empty((V, DR_H), np.float64)
+    buf = np.empty((16384, H), np.uint32)  # one slice of the embedding widened at a time
+    for r0 in range(0, V, 16384):
+        buf[:] = E[r0:r0 + 16384]
+        buf <<= 16
+        U[r0:r0 + 16384] = buf.view(np.float32).astype(np.float64) @ A.T
+    R = orc.ints(st(2), 11 * DR_H, -1, 1).reshape(11, DR_H).astype(np.float64)
+    groups = [np.arange(V)]
+    for i in range(11):  # balanced median splits: cluster index bits, level 0 the most significant
+        nxt = []
+        for g in groups:
+            o = g[np.argsort(U[g] @ R[i], kind="stable")]
+            nxt += [o[:len(o) // 2], o[len(o) // 2:]]
+        groups = nxt
+    order = np.concatenate(groups).astype(np.int64)
+    bits = ((np.arange(DR_C)[:, None] >> (10 - np.arange(11))[None, :]) & 1) * 2.0 - 1.0
+    cent = (bits @ R).astype(np.float32) * np.float32(0.05)
+    un = U / np.sqrt((U * U).sum(axis=1, keepdims=True))
+    sc = 0.12 + 0.08 * (orc.normal_f32(st(3), V) % 1.0)
+    emb = (un * sc[:, None]).astype(np.float32)
+    out = []
+    pre = np.zeros((DR_H, 2 * H), np.float32)
+    pre[:, :H] = A * 2.0 ** -5
+    out.append(("pre_projection.weight", "BF16", bf16_of(pre), (DR_H, 2 * H)))
+    for l in range(4):
+        hd = 256 if l < 3 else 512
+        p = f"model.layers.{l}."
+        t0 = 100 + 20 * l
+        out.append((p + "self_attn.q_proj.weight", "BF16", bf16_of(nrm(t0, 4 * hd * DR_H, 0.06)), (4 * hd, DR_H)))
+        out.append((p + "self_attn.o_proj.weight", "BF16", bf16_of(nrm(t0 + 1, DR_H * 4 * hd, 0.03)), (DR_H, 4 * hd)))
+        out.append((p + "mlp.gate_proj.weight", "BF16", bf16_of(nrm(t0 + 2, DR_F * DR_H, 0.06)), (DR_F, DR_H)))
+        out.append((p + "mlp.up_proj.weight", "BF16", bf16_of(nrm(t0 + 3, DR_F * DR_H, 0.06)), (DR_F, DR_H)))
+        out.append((p + "mlp.down_proj.weight", "BF16", bf16_of(nrm(t0 + 4, DR_H * DR_F, 0.02)), (DR_H, DR_F)))
+        u = lambda tag, n, b, w: bf16_of(b + w * (orc.normal_f32(st(tag), n) % 1.0))
+        out.append((p + "input_layernorm.weight", "BF16", u(t0 + 5, DR_H, 0.5, 1.0), (DR_H,)))
+        out.append((p + "post_attention_layernorm.weight", "BF16", u(t0 + 6, DR_H, 0.02, 0.02), (DR_H,)))
+        out.append((p + "pre_feedforward_layernorm.weight", "BF16", u(t0 + 7, DR_H, 0.5, 1.0), (DR_H,)))
+        out.append((p + "post_feedforward_layernorm.weight", "BF16", u(t0 + 8, DR_H, 0.02, 0.02), (DR_H,)))
+        out.append((p + "self_attn.q_norm.weight", "BF16", u(t0 + 9, hd, 0.2, 0.1), (hd,)))
+        out.append((p + "layer_scalar", "BF16", np.array([[0x3F80, 0x3F40, 0x3F80, 0x3F60][l]], np.uint16), (1,)))
+    out.append(("post_projection.weight", "BF16", bf16_of(nrm(4, H * DR_H, 0.06)), (H, DR_H)))
+    out.append(("masked_embedding.centroids.weight", "BF16", bf16_of(cent), (DR_C, DR_H)))
+    out.append(("model.norm.weight", "BF16", bf16_of(0.9 + 0.2 * (orc.normal_f32(st(5), DR_H) % 1.0)), (DR_H,)))
+    out.append(("model.embed_tokens.weight", "BF16", bf16_of(emb), (V, DR_H)))
+    out.append(("masked_embedding.token_ordering", "I64", order, (V,)))
+    return out
+
+
+def write_drafter(orc, d, E):
+    """the drafter checkpoint: d/drafter/model.safetensors and d/drafter_index.tsv (the
+    ENGINE_DRAFTER_DIR / ENGINE_DRAFTER_INDEX of E:1519)"""
+    os.makedirs(os.path.join(d, "drafter"), exist_ok=True)
+    rows, off = [], 0
+    with open(os.path.join(d, "drafter", "model.safetensors"), "wb") as f:
+        for name, dt, arr, shape in drafter_tensors(orc, E):
+            b = np.ascontiguousarray(arr).tobytes()
+            f.write(b)
+            rows.append((name, dt, off, len(b), ",".join(map(str, shape))))
+            off += len(b)
+            pad = (-off) % 64
+            f.write(b"\0" * pad)
+            off += pad
+    with open(os.path.join(d, "drafter_index.tsv"), "w") as f:
+        for name, dt, o, nb, shape in rows:
+            f.write(f"{name}\t{dt}\t{o}\t{nb}\t{shape}\n")
+
+
 def ple_rows(orc, toks):
     """the per-layer embedding rows of the listed ids (bf16 [n][35 * 256])"""
     out = np.empty((len(toks), NL * PD), np.uint16)
@@ -149,6 +248,7 @@ class GemmaOracle:
         L.g4o_gemma_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                         C.c_int]
         L.g4o_gemma_set_i8.argtypes = [C.c_void_p, C.c_int]
+        L.g4o_gemma_kv_move.argtypes = [C.c_void_p, C.c_int, C.c_int]
         L.g4o_gemma_cache.restype = C.c_void_p
         L.g4o_gemma_cache.argtypes = [C.c_void_p, C.c_int, C.c_int]
         self.orc, self.ctx = orc, ctx
@@ -195,6 +295,14 @@ class GemmaOracle:
             self.h = None
             self.head.close()
 
+    def set_i8(self, on):
+        """W4A8 products for passes of two rows or more from now on (ENGINE_PREFILL_INT8 blocks)"""
+        self.orc.L.g4o_gemma_set_i8(self.h, 1 if on else 0)
+
+    def kv_move(self, src, dst):
+        """E:1651: the KV rows of slot src copied to slot dst in every owner cache"""
+        self.orc.L.g4o_gemma_kv_move(self.h, src, dst)
+
     def forward(self, toks, pos0, T, hf, sibling=-1):
         toks = np.ascontiguousarray(toks, np.int32)
         M = len(toks)
@@ -209,6 +317,105 @@ class GemmaOracle:
         hd = layer_hd(l)
         p = self.orc.L.g4o_gemma_cache(self.h, l, v)
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), (self.ctx * hd,)).copy()
+
+
+class DrafterIn(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("pre", "post", "cent", "emb", "dnorm", "order")] + \
+               [(n, C.c_void_p * 4) for n in ("q", "o", "gate", "up", "down")] + \
+               [("nv", (C.c_void_p * 5) * 4), ("scalar", C.c_uint16 * 4), ("V", C.c_int32), ("C", C.c_int32),
+                ("hd", C.c_int32 * 4)]
+
+
+class GemmaDrafter:
+    """the oracle's drafter over a drafter checkpoint (write_drafter's files, tensors mapped in place)"""
+
+    def __init__(self, orc, d):
+        L = orc.L
+        L.g4o_drafter_load.restype = C.c_void_p
+        L.g4o_drafter_load.argtypes = [C.POINTER(DrafterIn)]
+        L.g4o_drafter_free.argtypes = [C.c_void_p]
+        L.g4o_gemma_draft_step.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                           C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_float)]
+        self.orc = orc
+        self.raw = np.memmap(os.path.join(d, "drafter", "model.safetensors"), np.uint8, "r")
+        idx = {}
+        for line in open(os.path.join(d, "drafter_index.tsv")):
+            n, dt, o, nb, sh = line.rstrip("\n").split("\t")
+            idx[n] = (int(o), int(nb), tuple(int(x) for x in sh.split(",")))
+        ptr = lambda n: self.raw.ctypes.data + idx[n][0]
+        di = DrafterIn()
+        di.pre, di.post = ptr("pre_projection.weight"), ptr("post_projection.weight")
+        di.cent, di.emb = ptr("masked_embedding.centroids.weight"), ptr("model.embed_tokens.weight")
+        di.dnorm, di.order = ptr("model.norm.weight"), ptr("masked_embedding.token_ordering")
+        for l in range(4):
+            p = f"model.layers.{l}."
+            di.q[l], di.o[l] = ptr(p + "self_attn.q_proj.weight"), ptr(p + "self_attn.o_proj.weight")
+            di.gate[l], di.up[l] = ptr(p + "mlp.gate_proj.weight"), ptr(p + "mlp.up_proj.weight")
+            di.down[l] = ptr(p + "mlp.down_proj.weight")
+            for t, n in enumerate(("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                                   "post_feedforward_layernorm", "self_attn.q_norm")):
+                di.nv[l][t] = ptr(p + n + ".weight")
+            o = idx[p + "layer_scalar"][0]
+            di.scalar[l] = int(self.raw[o:o + 2].view(np.uint16)[0])
+            di.hd[l] = idx[p + "self_attn.q_proj.weight"][2][0] // 4
+        di.V, di.C = idx["model.embed_tokens.weight"][2][0], idx["masked_embedding.centroids.weight"][2][0]
+        self.di = di
+        self.h = L.g4o_drafter_load(C.byref(di))
+
+    def close(self):
+        if self.h:
+            self.orc.L.g4o_drafter_free(self.h)
+            self.h = None
+
+    def step(self, go, tok, h, pos, P, T):
+        """one draft step on the Gemma oracle go: (token, next hidden, runner-up, gap)"""
+        b = np.empty(H, np.float32)
+        sec, gap = C.c_int(), C.c_float()
+        hh = np.ascontiguousarray(h, np.float32)
+        t = self.orc.L.g4o_gemma_draft_step(go.h, self.h, tok, hh.ctypes.data, pos, P, T, b.ctypes.data,
+                                            C.byref(sec), C.byref(gap))
+        return t, b, sec.value, gap.value
+
+
+class GemmaTarget:
+    """the Gemma oracle and its drafter as a run_req target (tests/protocol.py)"""
+
+    def __init__(self, go, dr=None):
+        self.go, self.dr = go, dr
+
+    def prefill(self, toks, pos0, T, i8):
+        n = len(toks)
+        self.go.set_i8(i8)
+        try:
+            for b in range(0, n, 32):  # E:1594-1599
+                blk = toks[b:b + 32]
+                last = b + len(blk) == n
+                hb = self.go.forward(blk, pos0 + b, T, len(blk) - 1 if last else len(blk))
+        finally:
+            self.go.set_i8(False)
+        return hb[len(blk) - 1]
+
+    def head(self, h, seeds):
+        return self.go.greedy(h, seeds)
+
+    def verify(self, block, nd, nb, pos0, T, allow_b):
+        """fwd of the block (E:1649), the lazy head (E:1475-1488) and acceptance (E:1650-1660)"""
+        from types import SimpleNamespace
+        block = [int(t) for t in block]
+        sib = nd + 1 if nb else -1
+        hb = self.go.forward(block, pos0, T, 0, sibling=sib)
+        G0 = self.head(hb[0], block)
+        if sib > 0 and allow_b and block[1] != G0 and block[sib] == G0:  # the sibling row holds row 0's token
+            Gs = self.head(hb[sib], block)
+            self.go.kv_move(pos0 + sib, pos0 + 1)
+            return SimpleNamespace(nacc=1, branch=1, commit=[G0, Gs], G0=G0), hb[sib]
+        G = [G0]
+        while len(G) - 1 < nd and block[len(G)] == G[-1]:
+            G.append(self.head(hb[len(G)], block))
+        return SimpleNamespace(nacc=len(G) - 1, branch=0, commit=G, G0=G0), hb[len(G) - 1]
+
+    def draft(self, tok, h, pos, P, T):
+        return self.dr.step(self.go, tok, h, pos, P, T)
 
 
 def run_req_k0(go, prompt, nnew, T, pfb=32):

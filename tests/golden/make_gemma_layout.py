@@ -8,6 +8,13 @@ ENGINE_CPUS of 6 CPUs (6 attention splits), twice: exact float prefill (ENGINE_P
 unset: first, gens) and W4A8 prefill blocks (ENGINE_PREFILL_INT8=1: first_i8, gens_i8).  Each
 prompt of cases() is one engine run; its FIRST and GEN lines are stored.
 
+Then, with the drafter checkpoint of gemma_layout.write_drafter (ENGINE_DRAFTER_DIR /
+ENGINE_DRAFTER_INDEX), three serve-mode sessions (ENGINE_SERVE=1, the three prompts in order,
+NNEW_D tokens each) in the drafting modes of DRAFT_MODES: per request the FIRST and GEN lines
+and the stderr line "RANK1 rounds= top1= top2_only= TREE attempts= hits=" (E:1673; the RANK1
+counts run over the session) are stored as first_<mode>, gens_<mode>, gen_lens_<mode>,
+rank1_<mode> [3][5].
+
 Run from the repository root after `make -C oracle`:
     python tests/golden/make_gemma_layout.py
 """
@@ -29,6 +36,25 @@ from oracle import Oracle  # noqa: E402
 
 EXE = os.path.join(ROOT, "oracle", "_ref", "gemma4_engine")
 CPUS, NNEW, CTX = 6, 12, 1024
+NNEW_D = 24
+# name -> engine settings of a drafting session (SIB_GAP 1, the default, lets the sibling row in)
+DRAFT_MODES = {"k3": dict(ENGINE_K="3"), "tree": dict(ENGINE_K="2", ENGINE_TREE="1"),
+               "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5")}
+
+
+def base_env():
+    env = dict(os.environ, ENGINE_CPUS=",".join(str(c) for c in range(CPUS)), ENGINE_HEAD_SCREEN="1",
+               ENGINE_DECODE_INT8="0", ENGINE_CTX=str(CTX))
+    for k in ("ENGINE_PREFILL_INT8", "ENGINE_SERVE", "ENGINE_STREAM", "ENGINE_ADAPTIVE_THREADS", "ENGINE_K",
+              "ENGINE_TREE", "ENGINE_NGRAM", "ENGINE_NGLEN", "ENGINE_SIB_GAP", "ENGINE_SIB_LONG", "ENGINE_POLICY",
+              "ENGINE_TAU", "ENGINE_DRAFT_SAMEPOS", "ENGINE_SLOTS"):
+        env.pop(k, None)
+    return env
+
+
+def parse_rank1(line):
+    """RANK1 rounds=a top1=b top2_only=c TREE attempts=d hits=e -> [a, b, c, d, e]"""
+    return [int(w.split("=")[1]) for w in line.split() if "=" in w]
 
 
 def cases(orc):
@@ -53,10 +79,7 @@ def main():
     with tempfile.TemporaryDirectory() as d:
         gl.write_checkpoint(orc, d)
         for sfx, i8 in (("", False), ("_i8", True)):
-            env = dict(os.environ, ENGINE_CPUS=",".join(str(c) for c in range(CPUS)), ENGINE_K="0",
-                       ENGINE_HEAD_SCREEN="1", ENGINE_DECODE_INT8="0", ENGINE_CTX=str(CTX))
-            for k in ("ENGINE_PREFILL_INT8", "ENGINE_SERVE", "ENGINE_STREAM", "ENGINE_ADAPTIVE_THREADS"):
-                env.pop(k, None)
+            env = dict(base_env(), ENGINE_K="0")
             if i8:
                 env["ENGINE_PREFILL_INT8"] = "1"
             firsts, gens = [], []
@@ -77,10 +100,36 @@ def main():
             out["first" + sfx] = np.array(firsts, np.int32)
             out["gen_lens" + sfx] = np.array([len(g) for g in gens])
             out["gens" + sfx] = np.concatenate(gens)
+        from oracle import Model
+        m = Model(orc, gl.EMBED_SEED, gl.V, 1, 256, 64)
+        E = m.get("E", np.uint16, gl.V * gl.H).reshape(gl.V, gl.H)
+        m.close()
+        gl.write_drafter(orc, d, E)
+        lines = "".join(f"{NNEW_D} {' '.join(map(str, p))}\n" for p in prompts)
+        for mode, extra in DRAFT_MODES.items():
+            env = dict(base_env(), ENGINE_SERVE="1", ENGINE_DRAFTER_DIR=os.path.join(d, "drafter"),
+                       ENGINE_DRAFTER_INDEX=os.path.join(d, "drafter_index.tsv"), **extra)
+            r = subprocess.run([EXE, d, os.path.join(d, "index.tsv"), "-", "0"], input=lines, env=env,
+                               capture_output=True, text=True, timeout=3600)
+            if r.returncode != 0:
+                sys.exit(f"engine failed ({r.returncode}): {r.stderr[-2000:]}")
+            out_lines = r.stdout.splitlines()
+            firsts = [int(ln.split()[1]) for ln in out_lines if ln.startswith("FIRST")]
+            gens = [np.array([int(x) for x in ln.split()[1:]], np.int32) for ln in out_lines if ln.startswith("GEN:")]
+            rank1 = [parse_rank1(ln) for ln in r.stderr.splitlines() if ln.startswith("RANK1")]
+            if not (len(firsts) == len(gens) == len(rank1) == len(prompts)):
+                sys.exit(f"mode {mode}: unexpected output\n{r.stdout[-2000:]}\n{r.stderr[-2000:]}")
+            for i in range(len(prompts)):
+                print(f"mode {mode} prompt {i}: GEN {list(gens[i])} RANK1 {rank1[i]}", flush=True)
+            out["first_" + mode] = np.array(firsts, np.int32)
+            out["gen_lens_" + mode] = np.array([len(g) for g in gens])
+            out["gens_" + mode] = np.concatenate(gens)
+            out["rank1_" + mode] = np.array(rank1, np.int64)
         raw = np.memmap(os.path.join(d, "model.safetensors"), np.uint8, "r")
         file_crc = crc(np.asarray(raw[:gl.V * gl.H * 2 + (64 << 20)]))
     path = os.path.join(HERE, "gemma_layout.npz")
     np.savez_compressed(path, cpus=np.array([CPUS]), nnew=np.array([NNEW]), ctx=np.array([CTX]),
+                        nnew_d=np.array([NNEW_D]),
                         prompt_lens=np.array([len(p) for p in prompts]), prompts=np.concatenate(prompts),
                         crc_head=np.array([file_crc], np.uint32), **out)
     print(f"gemma_layout.npz: {os.path.getsize(path)} bytes", flush=True)

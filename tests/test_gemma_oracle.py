@@ -5,6 +5,10 @@ reference engine's main() run unchanged on the same synthetic checkpoint
 prompts whose prefill blocks and decode passes take run_mh, attn_tile and split-KV (6 splits),
 with exact float prompt blocks and with W4A8 ones (ENGINE_PREFILL_INT8=1).
 
+With the drafter checkpoint of gemma_layout.write_drafter, run_req restated over the oracle
+(tests/protocol.py: MTP drafts with the sibling row, tree mode, prompt lookup) reproduces the
+reference engine's drafting sessions: FIRST / GEN lines and the RANK1 / TREE counts (E:1673).
+
 The fixture pins bit-level arithmetic through the tokens: planting either of two mistakes in
 the oracle -- 8 attention splits for 6, or the per-layer embedding rows dropped -- changes the
 tokens of the 196-token prompt."""
@@ -18,14 +22,17 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
 
 import gemma_layout as gl  # noqa: E402
+from protocol import RunReq  # noqa: E402
+
+# the drafting sessions of tests/golden/make_gemma_layout.py: (k, tree, ngram, nglen)
+MODES = {"k3": (3, False, 0, 3), "tree": (2, True, 0, 3), "ng": (3, False, 2, 5)}
 
 FX = os.path.join(HERE, "golden", "gemma_layout.npz")
 
 
 @pytest.fixture(scope="module")
-def ckpt(orc, tmp_path_factory):
-    d = str(tmp_path_factory.mktemp("gemma_ckpt"))
-    gl.write_checkpoint(orc, d)
+def ckpt(orc, gemma_ckpt):
+    d = gemma_ckpt
     fx = np.load(FX)
     prompts = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])
     gens = np.split(fx["gens"], np.cumsum(fx["gen_lens"])[:-1])
@@ -64,3 +71,22 @@ def test_gemma_fixture_detects_planted_mistakes(orc, ckpt):
             go.close()
     finally:
         gl.PLE_IDS = ids
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_gemma_drafting_matches_reference_engine(orc, ckpt, mode):
+    d, fx, prompts, gens = ckpt
+    k, tree, ngram, nglen = MODES[mode]
+    want = np.split(fx["gens_" + mode], np.cumsum(fx["gen_lens_" + mode])[:-1])
+    go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
+    dr = gl.GemmaDrafter(orc, d)
+    try:
+        rr = RunReq(orc, gl.GemmaTarget(go, dr), t0=int(fx["cpus"][0]), ngram=ngram, nglen=nglen)
+        for i, p in enumerate(prompts):
+            g0, gen, start = rr.run_req([int(t) for t in p], int(fx["nnew_d"][0]), k, tree)
+            assert start == 0 and g0 == int(fx["first_" + mode][i])
+            assert gen == [int(t) for t in want[i]], (mode, i, gen, list(want[i]))
+            assert rr.rank1() == [int(v) for v in fx["rank1_" + mode][i]], (mode, i, rr.rank1())
+    finally:
+        dr.close()
+        go.close()

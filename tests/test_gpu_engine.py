@@ -5,11 +5,13 @@ oracle: prefix reuse, prefill, prompt-lookup or MTP drafts, the sibling row (ENG
 and the tree mode of BENCH_MODE k 1), chain or sibling verify."""
 import os
 import subprocess
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
 
 from conftest import PKG, note
+from protocol import RunReq
 
 pytestmark = pytest.mark.gpu
 
@@ -18,116 +20,42 @@ ENV = dict(ENGINE_SERVE="1", ENGINE_STREAM="1", ENGINE_NGRAM="3", ENGINE_NGLEN="
            ENGINE_CTX=str(CTX), ENGINE_CPUS="0,2,4,6,8,10")
 
 
-def is_stop(t):
-    return t in (106, 1)
+class SynthTarget:
+    """the synthetic stack and drafter of the oracle as a run_req target (tests/protocol.py)"""
 
-
-class OracleEngine:
-    """run_req over the oracle with one active cache (ENGINE_SLOTS=1).  Attention splits over
-    the pool's active workers (E:1327, 1544): t0 = the ENGINE_CPUS count, set_active clamps to
-    [1, t0] (E:110-112), draft steps set 6 (8 past the cutoff with ENGINE_ADAPTIVE_THREADS and
-    ENGINE_DRAFT_SAME, E:1535), forward passes set 6 / 8 only with ENGINE_ADAPTIVE_THREADS
-    (E:1257), and the count persists.  i8: ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8=0."""
-
-    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False, nglen=3):
+    def __init__(self, orc):
         from oracle import Drafter, Model
-        self.orc = orc
-        self.t0, self.active, self.adaptive, self.draft_same, self.cut, self.i8 = t0, t0, adaptive, draft_same, cut, i8
-        self.nglen = nglen
         self.m = Model(orc, SEED, V, NL, I, CTX)
         self.d = Drafter(orc, SEED + 1, V)
-        self.keys, self.kv_len = [], 0
-        self.splits_seen = set()
-        self.prefill(np.array([2], np.int32), 0)  # E:1578 warm-up at position 0
 
-    def set_active(self, a):
-        self.active = self.t0 if a < 1 else min(a, self.t0)
-        self.splits_seen.add(self.active)
-        return self.active
+    def prefill(self, toks, pos0, T, i8):
+        return self.m.prefill(toks, pos0=pos0, T=T, i8=i8)
 
-    def fwd_splits(self, pos0, M):
-        if self.adaptive:
-            self.set_active(8 if pos0 + M > self.cut else 6)
-        self.splits_seen.add(self.active)
-        return self.active
+    def head(self, h, seeds):
+        return self.m.head(h, seeds)
 
-    def prefill(self, toks, pos0):
-        for b in range(0, len(toks), 32):
-            self.fwd_splits(pos0 + b, min(32, len(toks) - b))
-        return self.m.prefill(toks, pos0=pos0, T=self.active, i8=self.i8)
+    def verify(self, block, nd, nb, pos0, T, allow_b):
+        o, hid = self.m.verify(block, nd, nb, pos0, T, allow_b=allow_b)
+        return SimpleNamespace(nacc=o.nacc, branch=o.branch, commit=list(o.commit)[:o.ncommit], G0=o.G[0]), hid
+
+    def draft(self, tok, h, pos, P, T):
+        return self.d.step(self.m, tok, h, pos, P, T)
 
     def close(self):
         self.d.close()
         self.m.close()
 
-    def run_req(self, prompt, nnew, k_draft=3, tree=False):
-        n = len(prompt)
-        common = 0
-        while common < self.kv_len and common < n and self.keys[common] == prompt[common]:
-            common += 1
-        start = min(common, n - 1)
-        h = self.prefill(np.array(prompt[start:], np.int32), start)
-        g0 = self.m.head(h, prompt[start:][-8:])
-        gen, P, stopped = [g0], n - 1, is_stop(g0)
-        hprev, state, rounds, self.sib_rounds, self.hits = h, 1, 0, 0, 0
-        while len(gen) < nnew and not stopped:
-            k = min(k_draft, 3)
-            if tree:
-                k = min(k, 2)
-            seq = np.array(prompt + gen, np.int32)
-            drafts = self.orc.prompt_lookup(seq, 3, self.nglen).tolist()
-            used_ng, sec1, gap1, use_sib = bool(drafts), -1, -1.0, False
-            if not used_ng:  # E:1632-1645
-                tok, hh = gen[-1], hprev
-                for j in range(k):
-                    ts = self.set_active(8 if self.draft_same and self.adaptive and P + 1 > self.cut else 6)
-                    tok, hh, sec, gap = self.d.step(self.m, tok, hh, P + 1 + j, P, ts)
-                    if j == 0:
-                        sec1, gap1 = sec, gap
-                        allow = rounds >= 1 and state < 2 and k >= 2 and sec1 >= 0 and sec1 != tok
-                        if P + 1 + k > 192:
-                            cond = False  # ENGINE_SIB_LONG unset
-                        else:
-                            cond = gap1 <= (2.55 if (rounds <= 3 or state == 1) else 1.80)
-                        if allow and cond:
-                            drafts.append(tok)
-                            use_sib = True
-                            break
-                    drafts.append(tok)
-            nd = len(drafts)
-            sib = nd + 1 if ((tree or use_sib) and not used_ng and nd >= 1 and sec1 >= 0 and sec1 != drafts[0]) else -1
-            block = np.array([gen[-1]] + drafts + ([sec1] if sib > 0 else []), np.int32)
-            if sib > 0:
-                self.sib_rounds += 1
-                allow_hit = tree or (P + 1 + sib <= 192 and gap1 >= 0.25)
-                o, hprev = self.m.verify(block, nd, 1, P + 1, self.fwd_splits(P + 1, len(block)), allow_b=allow_hit)
-            else:
-                o, hprev = self.m.verify(block, nd, 0, P + 1, self.fwd_splits(P + 1, len(block)))
-            rounds += 1
-            if o.branch == 1:  # E:1650-1653
-                self.hits += 1
-                gen.append(o.commit[0])
-                if not is_stop(o.commit[0]) and len(gen) < nnew:
-                    gen.append(o.commit[1])
-                stopped = is_stop(gen[-1])
-                P += 2
-                state = 1
-                continue
-            state = 0 if o.nacc == 0 else (2 if (not use_sib and o.nacc == nd) else 1)
-            for i in range(o.nacc + 1):
-                gen.append(o.commit[i])
-                if is_stop(o.commit[i]):
-                    stopped = True
-                    break
-            P += o.nacc + 1
-        self.keys = list(prompt) + [g for i, g in enumerate(gen) if i <= P - n]
-        self.kv_len = min(P + 1, len(self.keys))
-        gen = gen[:nnew]
-        for i, g in enumerate(gen):
-            if is_stop(g):
-                gen = gen[:i + 1]
-                break
-        return g0, gen, start
+
+class OracleEngine(RunReq):
+    """run_req over the oracle's synthetic stack with prompt lookup (ENGINE_NGRAM=3)"""
+
+    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False, nglen=3):
+        self.target = SynthTarget(orc)
+        super().__init__(orc, self.target, t0=t0, adaptive=adaptive, draft_same=draft_same, cut=cut, i8=i8, ngram=3,
+                         nglen=nglen)
+
+    def close(self):
+        self.target.close()
 
 
 def run_protocol(orc, requests, tree_from, env_extra, **engine):

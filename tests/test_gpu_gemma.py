@@ -63,10 +63,8 @@ def upload(dev, d, ctx):
 
 
 @pytest.fixture(scope="module")
-def gemma(orc, g4v, tmp_path_factory):
-    d = str(tmp_path_factory.mktemp("gemma_dev"))
-    note("writing the synthetic Gemma-layout checkpoint")
-    gl.write_checkpoint(orc, d)
+def gemma(orc, g4v, gemma_ckpt):
+    d = gemma_ckpt
     fx = np.load(FX)
     ctx = int(fx["ctx"][0])
     dev = g4v.Device(0)
@@ -218,14 +216,107 @@ def test_gemma_engine_matches_reference_engine(gemma, i8):
     assert got == [[int(t) for t in g] for g in gens], (got, gens)
 
 
-def test_gemma_engine_refuses_drafting(gemma):
-    """the layout's drafter rounds (ENGINE_K > 0, E:1519-1563) are refused with a message"""
+def drafter_arrays(d):
+    """the drafter checkpoint of gemma_layout.write_drafter as Device.drafter_load's dict"""
+    raw = np.memmap(os.path.join(d, "drafter", "model.safetensors"), np.uint8, "r")
+    idx = {}
+    for line in open(os.path.join(d, "drafter_index.tsv")):
+        n, dt, o, nb, sh = line.rstrip("\n").split("\t")
+        idx[n] = (int(o), int(nb), tuple(int(x) for x in sh.split(",")))
+    get = lambda n, dt=np.uint16: np.asarray(raw[idx[n][0]:idx[n][0] + idx[n][1]]).view(dt)
+    t = dict(pre=get("pre_projection.weight"), post=get("post_projection.weight"),
+             cent=get("masked_embedding.centroids.weight"), emb=get("model.embed_tokens.weight"),
+             norm=get("model.norm.weight"), order=get("masked_embedding.token_ordering", np.int64),
+             C=idx["masked_embedding.centroids.weight"][2][0])
+    for n, key in (("q", "self_attn.q_proj"), ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"),
+                   ("up", "mlp.up_proj"), ("down", "mlp.down_proj")):
+        t[n] = [get(f"model.layers.{l}.{key}.weight") for l in range(4)]
+    t["nv"] = [[get(f"model.layers.{l}.{k}.weight") for k in ("input_layernorm", "post_attention_layernorm",
+                                                                "pre_feedforward_layernorm",
+                                                                "post_feedforward_layernorm", "self_attn.q_norm")]
+               for l in range(4)]
+    t["scalar"] = [int(get(f"model.layers.{l}.layer_scalar")[0]) for l in range(4)]
+    t["hd"] = [idx[f"model.layers.{l}.self_attn.q_proj.weight"][2][0] // 4 for l in range(4)]
+    return t
+
+
+@pytest.mark.parametrize("P", [60, 195, 300])
+def test_gemma_drafter_chain(orc, gemma, P):
+    """the drafter checkpoint on the device (g4v_drafter_load: layer 3 of head dim 512 over the
+    layout's owner cache 14, layers 0..2 over cache 13): a 3-step chain after a prefill of P + 1
+    tokens equals the oracle's draft steps (tokens, runners-up, gaps, last hidden state)"""
+    dev, d, fx, ctx = gemma
+    prompt = [int(t) for t in np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])[2]]
+    while len(prompt) < P + 1:
+        prompt = prompt + prompt[:P + 1 - len(prompt)]
+    prompt = prompt[:P + 1]
+    dev.drafter_load(drafter_arrays(d))
+    go = gl.GemmaOracle(orc, d, ctx)
+    dr = gl.GemmaDrafter(orc, d)
+    try:
+        note(f"gemma drafter chain after {P + 1} prompt tokens")
+        h = gl.GemmaTarget(go).prefill(np.array(prompt, np.int32), 0, 6, False)
+        g0, hd_ = dev.prefill(np.array(prompt, np.int32), 0, 32, 6, hidden=True)
+        assert same(hd_, h)
+        tok, hh, want = g0, h, []
+        for j in range(3):
+            tok, hh, sec, gap = dr.step(go, tok, hh, P + 1 + j, P, 6)
+            want.append((tok, sec, gap))
+        drafts, secs, gaps, hid = dev.draft_mtp(g0, h, P, 3, 6)
+        note(f"oracle {want}, device {list(drafts)} {list(secs)} {list(gaps)}")
+        assert [int(x) for x in drafts] == [w[0] for w in want]
+        assert [int(x) for x in secs] == [w[1] for w in want]
+        assert same(np.array(gaps, np.float32), np.array([w[2] for w in want], np.float32))
+        assert same(hid, hh), first_diff(hid, hh)
+    finally:
+        dr.close()
+        go.close()
+
+
+# the drafting sessions of tests/golden/make_gemma_layout.py
+DRAFT_MODES = {"k3": dict(ENGINE_K="3"), "tree": dict(ENGINE_K="2", ENGINE_TREE="1"),
+               "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5")}
+
+
+@pytest.mark.parametrize("mode", list(DRAFT_MODES))
+def test_gemma_engine_drafting_matches_reference_engine(gemma, mode):
+    """g4v_engine with the drafter checkpoint (ENGINE_DRAFTER_DIR / ENGINE_DRAFTER_INDEX) in serve
+    mode: FIRST / GEN lines and the RANK1 / TREE counts equal the reference engine's session"""
     dev, d, fx, ctx = gemma
     exe = os.path.join(os.path.dirname(HERE), "gemma4-e2b-laptop-cpu_amd", "g4v_engine")
-    env = dict(os.environ, ENGINE_K="3", ENGINE_CTX=str(ctx))
+    prompts = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])
+    gens = np.split(fx["gens_" + mode], np.cumsum(fx["gen_lens_" + mode])[:-1])
+    nnew = int(fx["nnew_d"][0])
+    env = dict(os.environ, ENGINE_SERVE="1", ENGINE_CTX=str(ctx), ENGINE_DECODE_INT8="0",
+               ENGINE_CPUS=",".join(str(c) for c in range(int(fx["cpus"][0]))),
+               ENGINE_DRAFTER_DIR=os.path.join(d, "drafter"), ENGINE_DRAFTER_INDEX=os.path.join(d, "drafter_index.tsv"))
+    for k in ("ENGINE_PREFILL_INT8", "ENGINE_ADAPTIVE_THREADS", "ENGINE_NGRAM", "ENGINE_NGLEN", "ENGINE_STREAM",
+              "ENGINE_TREE", "ENGINE_SIB_GAP", "ENGINE_SIB_LONG", "ENGINE_POLICY"):
+        env.pop(k, None)
+    env.update(DRAFT_MODES[mode])
+    lines = "".join(f"{nnew} {' '.join(map(str, p))}\n" for p in prompts)
+    note(f"g4v_engine drafting session {mode} on the Gemma-layout checkpoint")
+    proc = subprocess.run([exe, d, os.path.join(d, "index.tsv"), "-", "0"], input=lines, env=env,
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    firsts = [int(ln.split()[1]) for ln in proc.stdout.splitlines() if ln.startswith("FIRST")]
+    got = [[int(x) for x in ln.split()[1:]] for ln in proc.stdout.splitlines() if ln.startswith("GEN:")]
+    rank1 = [[int(w.split("=")[1]) for w in ln.split() if "=" in w] for ln in proc.stderr.splitlines()
+             if ln.startswith("RANK1")]
+    assert firsts == [int(t) for t in fx["first_" + mode]]
+    assert got == [[int(t) for t in g] for g in gens], (got, gens)
+    assert rank1 == [[int(v) for v in r] for r in fx["rank1_" + mode]], rank1
+
+
+def test_gemma_engine_needs_drafter_files(gemma):
+    """ENGINE_K > 0 without the drafter checkpoint ends with a message, as main() needs it (E:1519)"""
+    dev, d, fx, ctx = gemma
+    exe = os.path.join(os.path.dirname(HERE), "gemma4-e2b-laptop-cpu_amd", "g4v_engine")
+    env = dict(os.environ, ENGINE_K="3", ENGINE_CTX=str(ctx), ENGINE_DRAFTER_DIR=os.path.join(d, "none"),
+               ENGINE_DRAFTER_INDEX=os.path.join(d, "none.tsv"))
     pf = os.path.join(d, "p.ids")
     with open(pf, "w") as f:
         f.write("5 6 7\n")
     proc = subprocess.run([exe, d, os.path.join(d, "index.tsv"), pf, "4"], env=env, capture_output=True, text=True,
                           timeout=300)
-    assert proc.returncode == 2 and "ENGINE_K=0" in proc.stderr, (proc.returncode, proc.stderr[-500:])
+    assert proc.returncode == 2 and "none.tsv" in proc.stderr, (proc.returncode, proc.stderr[-500:])
