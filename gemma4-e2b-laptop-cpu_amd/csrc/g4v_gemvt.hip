@@ -99,11 +99,13 @@ static size_t gemvt_lds(int mpl, int K, bool nrm, int tr, bool mrg) {
 // variants of their own so that their registers do not weigh on the other launches
 // TR: rows per tile (64: a wave is 64 rows of one chain lane; 32: a wave is 32 rows of two
 // chain lanes); a block is the TR x 8 (row, chain lane) pairs of one tile, 8 TR threads
-template <int MPL, bool MRG, bool NRM, int TR>
+// KT: the reduction length when fixed at compile time (0: a.K), so that the LDS addresses of the
+// staged activations fold into instruction offsets
+template <int MPL, bool MRG, bool NRM, int TR, int KT = 0>
 __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
   constexpr int NT = TR * 8;
   const GemvTArgs& a = d.a;
-  const int K = a.K, G = K / 32, GC = K / 256, M = a.M;
+  const int K = KT ? KT : a.K, G = K / 32, GC = K / 256, M = a.M;
   // block -> (tile, row subset); the tiles of XCD x (block % 8) are x, x + 8, ...
   const int xcd = blockIdx.x & 7, kq = blockIdx.x >> 3;
   const int sub = kq % d.nsub, t = (kq / d.nsub) * 8 + xcd;
@@ -499,12 +501,34 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
 template <int MPL, int TR>
 static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
   const size_t lds = gemvt_lds(MPL, d.a.K, d.a.nrm_mode != 0, TR, d.a.mrg_po != nullptr);
-  if (d.a.mrg_po) {
-    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false, TR>), dim3(grid), dim3(TR * 8), lds, st, d);
+  const dim3 g(grid), b(TR * 8);
+  const int K = d.a.K;
+  // the verify pass's shapes at their default tiles get a fixed K: q/k/v and gate/up (norm
+  // prologue, K 1536), down (K 6144)
+  if (d.a.mrg_po) {  // (a fixed K costs the merge variant registers: it stays generic)
+    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false, TR>), g, b, lds, st, d);
   } else if (d.a.nrm_mode) {
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR>), dim3(grid), dim3(TR * 8), lds, st, d);
+    if constexpr ((MPL == 2 || MPL == 4) && TR == 64) {
+      if (K == 1536) {
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR, 1536>), g, b, lds, st, d);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR>), g, b, lds, st, d);
   } else {
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR>), dim3(grid), dim3(TR * 8), lds, st, d);
+    if constexpr (MPL == 1 && TR == 64) {
+      if (K == 6144) {
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 6144>), g, b, lds, st, d);
+        return;
+      }
+    }
+    if constexpr (MPL == 2 && TR == 64) {
+      if (K == 1536) {
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 1536>), g, b, lds, st, d);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR>), g, b, lds, st, d);
   }
 }
 

@@ -309,6 +309,8 @@ void g4o_w4a8_gemm(const uint8_t* W, const uint16_t* S, const float* X, int M, i
   float* sx = (float*)malloc(sizeof(float) * (size_t)M * G);
   int32_t* sm = (int32_t*)malloc(sizeof(int32_t) * (size_t)M * G);
   g4o_w4a8_quant(X, M, K, q, sx, sm);
+  /* every output is its own sequential chain: outputs split over threads freely */
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m)
     for (int n = 0; n < N; ++n) {
       float row = 0.f;
