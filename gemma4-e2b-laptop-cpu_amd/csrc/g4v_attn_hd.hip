@@ -15,32 +15,33 @@ namespace g4v {
 
 __constant__ uint64_t c_expf_tab_hd[32] = G4V_EXPF_TABLE;
 
-constexpr int AHD_THREADS = 256;
-
-// geometry from the launch (gv) or, when gp is given, from device memory (a drafter chain's steps)
+// geometry from the launch (gv) or, when gp is given, from device memory (a drafter chain's steps);
+// D threads: 8 lanes per position for the scores, one output dim per thread for the values.
+// Scores and weights live in sw indexed from pa, the 8-aligned position at or below c0, so that
+// the value pass reads 8 positions of its dim (16 bytes of the cache) and 8 weights at a time.
 template <int D>
-__global__ __launch_bounds__(AHD_THREADS) void k_attn_split_d(const uint16_t* __restrict__ KC,
-                                                              const uint16_t* __restrict__ VC,
-                                                              const float* __restrict__ q, int ldq, AttnGeom gv,
-                                                              const AttnGeom* __restrict__ gp,
-                                                              float* __restrict__ po, float* __restrict__ pm,
-                                                              float* __restrict__ pl) {
+__global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__ KC, const uint16_t* __restrict__ VC,
+                                                   const float* __restrict__ q, int ldq, AttnGeom gv,
+                                                   const AttnGeom* __restrict__ gp, float* __restrict__ po,
+                                                   float* __restrict__ pm, float* __restrict__ pl) {
+  constexpr int NTH = D;
   const AttnGeom& g = gp ? *gp : gv;
-  __shared__ __align__(16) float qs[D];       // the head's query in key-slot order (kc_slot_d)
-  __shared__ float sw[ATT_SPLIT_MAX];         // scores, then weights, of the split's positions
-  __shared__ float red[AHD_THREADS / 64];
+  __shared__ __align__(16) float qs[D];                   // the head's query in key-slot order
+  __shared__ __align__(16) float sw[ATT_SPLIT_MAX + 16];  // scores, then weights, from position pa
+  __shared__ float red[NTH / 64];
   const int t = blockIdx.x, m = blockIdx.y, h = blockIdx.z, T = g.T;
   const int M = g.M;
   if (m >= M) return;  // uniform
   const int len = g.kmax - g.kmin + 1;
   const int c0 = g.kmin + (int)((long)t * len / T), c1 = g.kmin + (int)((long)(t + 1) * len / T);
+  const int pa = c0 & ~7, pe = (c1 + 7) & ~7;
   const int lo = g.lo[m], pos = g.pos[m], sl = g.skip_lo[m], sh = g.skip_hi[m];
   auto allowed = [=](int p) { return p >= lo && p <= pos && !(p >= sl && p <= sh); };  // E:740
-  for (int e = threadIdx.x; e < D; e += AHD_THREADS) qs[kc_slot_d<D>(e)] = q[(size_t)m * ldq + h * D + e];
+  for (int e = threadIdx.x; e < D; e += NTH) qs[kc_slot_d<D>(e)] = q[(size_t)m * ldq + h * D + e];
   __syncthreads();
-  // scores: 8 lanes per position, 32 positions per pass
+  // scores: 8 lanes per position, NTH / 8 positions per pass
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
-  for (int p0 = c0; p0 < c1; p0 += AHD_THREADS / 8) {
+  for (int p0 = c0; p0 < c1; p0 += NTH / 8) {
     const int p = min(p0 + ps, c1 - 1);  // the tail's extra lanes repeat the last position
     const uint16_t* kr = KC + (size_t)p * D + l * (D / 8);
     float s[2];
@@ -60,38 +61,49 @@ __global__ __launch_bounds__(AHD_THREADS) void k_attn_split_d(const uint16_t* __
       s[c] = a;
     }
     const float v = hsum8_lanes(s[0] + s[1]);
-    if (l == 0 && p0 + ps < c1) sw[p - c0] = v;
+    if (l == 0 && p0 + ps < c1) sw[p - pa] = v;
   }
   __syncthreads();
   // the max over the allowed positions (order free)
   float mx = -1e30f;
-  for (int p = c0 + threadIdx.x; p < c1; p += AHD_THREADS)
-    if (allowed(p)) mx = fmaxf(mx, sw[p - c0]);
+  for (int p = c0 + threadIdx.x; p < c1; p += NTH)
+    if (allowed(p)) mx = fmaxf(mx, sw[p - pa]);
   for (int s = 1; s < 64; s <<= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = red[0];
 #pragma unroll
-  for (int w = 1; w < AHD_THREADS / 64; ++w) mx = fmaxf(mx, red[w]);
+  for (int w = 1; w < NTH / 64; ++w) mx = fmaxf(mx, red[w]);
+  // weights exp8(score - max) of the allowed positions (E:820), 0 for every other slot of
+  // [pa, pe); each thread rewrites only the slots it reads
+  for (int j = threadIdx.x; j < pe - pa; j += NTH) {
+    const int p = pa + j;
+    sw[j] = (p >= c0 && p < c1 && allowed(p)) ? exp8(sw[j] - mx) : 0.f;
+  }
   __syncthreads();
-  for (int p = c0 + threadIdx.x; p < c1; p += AHD_THREADS)
-    sw[p - c0] = allowed(p) ? exp8(sw[p - c0] - mx) : 0.f;  // E:820
-  __syncthreads();
-  // o_i in position order over the allowed positions; every thread also forms l (E:821)
-  constexpr int DT = D / AHD_THREADS;  // dims per thread
-  float o[DT], lsum = 0.f;
+  // o_d = fma chain over the positions in order (E:821-875), l = the weights' sum in order;
+  // a zero weight (not allowed, outside the split) leaves both unchanged: its value is taken
+  // as +0 and o is never -0
+  const int d = threadIdx.x;
+  const uint16_t* vcol = VC + (size_t)d * 32;
+  float o = 0.f, lsum = 0.f;
+  for (int j8 = 0; j8 < pe - pa; j8 += 8) {
+    const int p8 = pa + j8;  // 8-aligned: the 8 positions of dim d are 16 contiguous bytes
+    const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (p8 & 31));
+    const float4 wa = *reinterpret_cast<const float4*>(&sw[j8]);
+    const float4 wb = *reinterpret_cast<const float4*>(&sw[j8 + 4]);
+    const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    const uint32_t u4[4] = {vq.x, vq.y, vq.z, vq.w};
 #pragma unroll
-  for (int d = 0; d < DT; ++d) o[d] = 0.f;
-  for (int p = c0; p < c1; ++p) {
-    if (!allowed(p)) continue;  // uniform
-    const float w = sw[p - c0];
-    lsum = lsum + w;
-#pragma unroll
-    for (int d = 0; d < DT; ++d) o[d] = fmaf(w, bf2f(VC[vc_index_d<D>(p, threadIdx.x + d * AHD_THREADS)]), o[d]);
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t u = u4[k >> 1];
+      const float vv = w8[k] != 0.f ? as_f32((k & 1) ? (u & 0xFFFF0000u) : (u << 16)) : 0.f;
+      o = fmaf(w8[k], vv, o);
+      lsum = lsum + w8[k];
+    }
   }
   const size_t k = ((size_t)t * M + m) * NQ + h;
-#pragma unroll
-  for (int d = 0; d < DT; ++d) po[k * D + threadIdx.x + d * AHD_THREADS] = o[d];
+  po[k * D + d] = o;
   if (threadIdx.x == 0) {
     pm[k] = mx;
     pl[k] = lsum;  // 0 when the split holds no allowed position: the merge then skips it
@@ -151,7 +163,7 @@ int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, 
   if (hd != 512 || g.M < 1 || g.M > MAXM || g.T < 1 || g.T > MAXT) return -1;
   const int len = g.kmax - g.kmin + 1;
   if (len < 1 || (len + g.T - 1) / g.T + 1 > ATT_SPLIT_MAX) return -1;
-  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(g.T, g.M, NQ), dim3(AHD_THREADS), 0, st, KC, VC, q, ldq, g,
+  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(g.T, g.M, NQ), dim3(512), 0, st, KC, VC, q, ldq, g,
                      (const AttnGeom*)nullptr, po, pm, pl);
   hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(g.M, NQ), dim3(512), 0, st, po, pm, pl, g.M, g.T, out, ldo, gs);
   return 0;
@@ -162,8 +174,7 @@ void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float
   AttnGeom g{};
   g.M = M;
   g.T = T;
-  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(T, M, nh), dim3(AHD_THREADS), 0, st, KC, VC, q, ldq, g, gdev, po, pm,
-                     pl);
+  hipLaunchKernelGGL(k_attn_split_d<512>, dim3(T, M, nh), dim3(512), 0, st, KC, VC, q, ldq, g, gdev, po, pm, pl);
   hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(M, nh), dim3(512), 0, st, po, pm, pl, M, T, out, ldo,
                      (float*)nullptr);
 }

@@ -387,6 +387,100 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
   }
 }
 
+// The same output for a pass of few rows (a verify pass, M <= 8): one block per (row, head), one
+// output dim per thread, so that every dim's chain over the positions has a thread of its own
+// (the kernel above gives a whole row to one wave).  Arithmetic as above: the max over the row's
+// scores; run_mh: den = the sum in position order of libm expf(s - max) (one thread, chunk by
+// chunk), w = expf(s - max) / den, out = r16(fma chain of w v in position order); attn_tile:
+// w = exp8(s - max), out = r16(chain * (1 / den)) with den the sum of w in order.  Weights are
+// staged per chunk of PF_RC positions from the 8-aligned position at or below lo, 0 where not
+// valid, so the value reads take 8 positions (16 bytes of a dim) at a time; a zero weight leaves
+// the chain unchanged (its value is taken as +0 and the chain is never -0).
+constexpr int PF_RC = 512;
+template <int D>
+__global__ __launch_bounds__(D) void k_pf_attn_rows(const float* __restrict__ S, const uint16_t* __restrict__ VC,
+                                                   float* __restrict__ att, PfGeom g, int r0, int sliding,
+                                                   ExpfTab tab, int staged) {
+  __shared__ __align__(16) float w[PF_RC];
+  __shared__ uint64_t T[32];
+  __shared__ float red[D / 64];
+  __shared__ float dens;
+  const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_row_lo(r, P, g, sliding);
+  const int h = blockIdx.y, d = threadIdx.x;
+  const int len = P - lo + 1;
+  const bool tiled = pf_tiled(r, g);
+  const float* Sh = S + pf_srow(rr, r, gridDim.x, g.pos0 + r0, sliding, g) + (size_t)h * len;
+  if (d < 32) T[d] = tab.t[d];
+  float mx = -1e30f;  // order free
+  for (int jj = d; jj < len; jj += D) mx = fmaxf(mx, Sh[jj]);
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((d & 63) == 0) red[d >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int k = 1; k < D / 64; ++k) mx = fmaxf(mx, red[k]);
+  const int pa = lo & ~7, pend = P + 1;  // chunks cover [pa, P]; slots before lo weigh 0
+  float den = 0.f;                        // thread 0: the sum in position order
+  if (!tiled) {  // run_mh divides by the sum before the value pass
+    for (int c0 = pa; c0 < pend; c0 += PF_RC) {
+      const int cn = min(PF_RC, pend - c0);
+      __syncthreads();  // the previous chunk's weights are summed
+      for (int j = d; j < cn; j += D) {
+        const int p = c0 + j;
+        w[j] = (p >= lo && pf_valid(r, P, p, g)) ? libm_expf_neg(Sh[p - lo] - mx, T) : 0.f;
+      }
+      __syncthreads();
+      if (d == 0)
+        for (int j = 0; j < cn; ++j) den = den + w[j];
+    }
+    if (d == 0) dens = den;
+    __syncthreads();
+    den = dens;
+  }
+  const uint16_t* vcol = VC + (size_t)d * 32;
+  float O = 0.f;
+  for (int c0 = pa; c0 < pend; c0 += PF_RC) {
+    const int cn = min(PF_RC, pend - c0);
+    const int cn8 = (cn + 7) & ~7;
+    __syncthreads();  // the previous chunk is used
+    for (int j = d; j < cn8; j += D) {
+      const int p = c0 + j;
+      float v = 0.f;
+      if (j < cn && p >= lo && pf_valid(r, P, p, g)) {
+        const float dd = Sh[p - lo] - mx;
+        v = tiled ? exp8(dd) : libm_expf_neg(dd, T) / den;
+      }
+      w[j] = v;
+    }
+    __syncthreads();
+    for (int j8 = 0; j8 < cn8; j8 += 8) {
+      const int p8 = c0 + j8;
+      const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (p8 & 31));
+      const float4 wa = *reinterpret_cast<const float4*>(&w[j8]);
+      const float4 wb = *reinterpret_cast<const float4*>(&w[j8 + 4]);
+      const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+      const uint32_t u4[4] = {vq.x, vq.y, vq.z, vq.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t u = u4[k >> 1];
+        const float vv = w8[k] != 0.f ? as_f32((k & 1) ? (u & 0xFFFF0000u) : (u << 16)) : 0.f;
+        O = fmaf(w8[k], vv, O);
+      }
+    }
+    if (tiled && d == 0)
+      for (int j = 0; j < cn; ++j) den = den + w[j];
+  }
+  if (tiled) {
+    if (d == 0) dens = den;
+    __syncthreads();
+    den = dens;
+  }
+  const float y = tiled ? r16(O * (1.0f / den)) : r16(O);
+  float* orow = att + (size_t)r * NQ * D;
+  const int n = h * D + d;
+  orow[staged ? staged_index(n) : n] = y;
+}
+
 // E:1358-1361 (W4A8 source kept): o = r16(o); tmp = rms(o, post_attn); x = r16(x + r16(tmp));
 // a = r16(rms(x, pre_ff))
 __global__ __launch_bounds__(ROW_THREADS) void k_pf_post_attn(const float* __restrict__ o, float* __restrict__ x,
@@ -514,12 +608,23 @@ void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, floa
   const int maxlen = sliding ? std::min(Plast + 1, g.sib >= 0 ? Plast - g.pos0 + 511 : 512) : Plast + 1;
   const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
   ExpfTab tab{G4V_EXPF_TABLE};
+  // a pass of few rows gives every (row, head) a block; a prompt block keeps a wave per row (it
+  // reads each value row once for the 8 heads)
+  const bool rows = M <= MAXM;
   if (hd == 512) {
     hipLaunchKernelGGL(k_pf_scores<512>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
-    hipLaunchKernelGGL(k_pf_attn_out<512>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+    if (rows)
+      hipLaunchKernelGGL(k_pf_attn_rows<512>, dim3(M, NQ), dim3(512), 0, st, S, VC, att, g, r0, sliding, tab,
+                         staged ? 1 : 0);
+    else
+      hipLaunchKernelGGL(k_pf_attn_out<512>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
   } else {
     hipLaunchKernelGGL(k_pf_scores<HD>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
-    hipLaunchKernelGGL(k_pf_attn_out<HD>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+    if (rows)
+      hipLaunchKernelGGL(k_pf_attn_rows<HD>, dim3(M, NQ), dim3(HD), 0, st, S, VC, att, g, r0, sliding, tab,
+                         staged ? 1 : 0);
+    else
+      hipLaunchKernelGGL(k_pf_attn_out<HD>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
   }
 }
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st) {
