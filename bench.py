@@ -248,6 +248,41 @@ def long_prompt_summary(g4v):
             "drafts_accepted": f"{r['accepted']}/{r['drafted']}", "mtp_rounds": r["mtp_rounds"]}
 
 
+GM_MLP = [6144 if l < 15 else 12288 for l in range(35)]  # the checkpoint's MLP widths
+GM_CTX = 2048
+
+
+def gemma_layout_summary(g4v, reps=10):
+    """verify passes on the Gemma-4-E2B layer layout at the checkpoint's sizes (device-generated
+    weights): a 2048-token context prefilled with W4A8 blocks, then one-row decode passes and
+    chain passes of 3 and 7 drafts at position 2048 (the passes re-run at the same position)"""
+    dev = g4v.Device(0)
+    dev.model_synth_gemma(SEED + 7, V, GM_MLP, 4096)
+    dev.set_prefill_int8(True)
+    rng = np.random.default_rng(11)
+    ctx = rng.integers(0, V, GM_CTX).astype(np.int32)
+    dev.prefill(ctx, 0, 32, 6)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.prefill(ctx, 0, 32, 6)
+    dev.sync()
+    out = {"workload": f"Gemma-4-E2B layout (35 layers, head dim 256 / 512, KV shared past layer 14, MLP 6144 / "
+                       f"12288, per-layer inputs, V {V}), context {GM_CTX}, 6 KV splits",
+           "prefill_ms": round((time.perf_counter() - t0) * 1e3, 2)}
+    for M in (1, 4, 8):
+        blk = rng.integers(0, V, M).astype(np.int32)
+        for _ in range(2):
+            dev.verify(blk, M - 1, 0, GM_CTX, 6)
+        dev.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            dev.verify(blk, M - 1, 0, GM_CTX, 6)
+        dev.sync()
+        out[f"verify_{M}_rows_ms"] = round((time.perf_counter() - t0) * 1e3 / reps, 3)
+    dev.close()
+    return out
+
+
 def main_long_prompt(args, g4v):
     dev = g4v.Device(0)
     info = dev.info()
@@ -299,6 +334,7 @@ def main():
     ap.add_argument("--workload", choices=["verify", "long_prompt"], default="verify")
     ap.add_argument("--cpu-only", default=None, help=argparse.SUPPRESS)  # child process of the CPU baseline
     ap.add_argument("--no-long-prompt", action="store_true", help="skip the long-prompt sub-measurement")
+    ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-E2B layout sub-measurement")
     args = ap.parse_args()
     if args.cpu_only is not None:
         print(json.dumps(cpu_baseline_run([int(c) for c in args.cpu_only.split(",")])), flush=True)
@@ -419,6 +455,11 @@ def main():
             out["long_prompt"] = long_prompt_summary(g4v)
         except Exception as e:
             out["long_prompt"] = {"error": str(e)}
+    if not args.no_gemma:
+        try:
+            out["gemma_layout"] = gemma_layout_summary(g4v)
+        except Exception as e:
+            out["gemma_layout"] = {"error": str(e)}
     print(json.dumps(out), flush=True)
 
 

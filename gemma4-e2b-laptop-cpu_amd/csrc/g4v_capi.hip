@@ -120,7 +120,9 @@ struct g4v_ctx {
   DBuf gm_kv;                     // layer l < 15: K at gm_koff[l], V at gm_voff[l], [kvcap][hd] each
   size_t gm_koff[15] = {}, gm_voff[15] = {};
   DBuf gm_rope;                   // global layers' RoPE: cos, sin [ctxcap][256]
-  DBuf gm_rows, gm_tok, gm_s;     // row buffers of a pass (32 rows), its tokens, score scratch
+  DBuf gm_rows, gm_tok, gm_s;     // row buffers of a pass (gm_cap rows), its tokens, score scratch
+  int gm_cap = 0;                 // rows the row buffers, tokens and W4A8 operands hold
+  size_t gm_sfl = 0;              // floats of the score scratch
   int gm_Imax = 0;
   bool gm_plready = false;
   // prefill rows (plain [row][K] layouts), quantised activations, attention score scratch
@@ -1665,6 +1667,28 @@ static void pf_lin(g4v_ctx* c, const Mat& m, const float* x, int M, float* y, bo
   }
 }
 
+// up to three products of the same input (same K) in one launch per MAXM rows: q / k / v, gate / up
+static void pf_lin_multi(g4v_ctx* c, int n, const Mat* const* m, const float* x, int M, float* const* y, bool i8) {
+  if (i8) {
+    for (int j = 0; j < n; ++j) pf_lin(c, *m[j], x, M, y[j], true, j == 0);
+    return;
+  }
+  const int K = m[0]->K;
+  for (int r = 0; r < M; r += MAXM) {
+    GemvArgs a{};
+    for (int j = 0; j < n; ++j) {
+      a.mat[j] = m[j]->dev();
+      a.y[j] = y[j] + (size_t)r * m[j]->N;
+      a.ldy[j] = m[j]->N;
+    }
+    a.x = x + (size_t)r * K;
+    a.ldx = K;
+    a.K = K;
+    a.M = std::min(MAXM, M - r);
+    launch_gemv(a, EPI_STORE, c->st);
+  }
+}
+
 static int pf_alloc(g4v_ctx* c, int rows, size_t sfl) {
   if (rows > c->pf_rows || c->I != c->pf_I) {
     const size_t R = (size_t)rows, Rp = (size_t)w4a8_mpad(rows), Kmax = std::max(NQ * HD, std::max(H, c->I));
@@ -1772,7 +1796,7 @@ struct GmRows {
 };
 GmRows gm_rows(g4v_ctx* c) {
   float* f = c->gm_rows.as<float>();
-  const size_t R = GM_ROWS, I = c->gm_Imax;
+  const size_t R = c->gm_cap, I = c->gm_Imax;
   GmRows r;
   r.x = f;
   r.a = r.x + R * H;
@@ -1790,9 +1814,28 @@ GmRows gm_rows(g4v_ctx* c) {
   r.g2 = r.pgv + R * GM_PD;
   return r;
 }
-size_t gm_rows_floats(int Imax) {
-  const size_t R = GM_ROWS;
+size_t gm_rows_floats(int Imax, int rows) {
+  const size_t R = rows;
   return R * (3 * H + 2 * NQ * 512 + 2 * 512 + 3 * (size_t)Imax + 2 * GM_PLN + 2 * GM_PD);
+}
+
+// row buffers, token slots and W4A8 operands for passes of up to `rows` rows, score scratch of
+// `sfl` floats (grown, never shrunk)
+int gm_reserve(g4v_ctx* c, int rows, size_t sfl) {
+  if (rows > c->gm_cap) {
+    ALLOC(c->gm_rows, gm_rows_floats(c->gm_Imax, rows) * 4);
+    ALLOC(c->gm_tok, (size_t)rows * 4);
+    const size_t Kmax = std::max<size_t>(NQ * 512, std::max<size_t>(H, c->gm_Imax)), Rp = (size_t)w4a8_mpad(rows);
+    ALLOC(c->pfxq, Rp * Kmax * 2);
+    ALLOC(c->pfsx, (Kmax / 32) * Rp * 4);
+    ALLOC(c->pfcorr, (Kmax / 32) * Rp * 4);
+    c->gm_cap = rows;
+  }
+  if (sfl > c->gm_sfl) {
+    ALLOC(c->gm_s, sfl * 4);
+    c->gm_sfl = sfl;
+  }
+  return 0;
 }
 
 // matrix j of layer l: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 per_layer_input_gate, 8 per_layer_projection
@@ -1831,7 +1874,10 @@ bool gm_complete(const g4v_ctx* c, std::string* what) {
 // fwd (E:1256-1405) of the M rows whose tokens are in gm_tok, at positions pos0 .. pos0 + M - 1,
 // row sib (>= 0) the sibling row (E:1292, 1340-1345); i8: W4A8 linear layers (M >= 2).  Rows
 // m >= hrow (hrow >= 0) leave their final-normed state in h [M - hrow][1536] and |h| in hn.
-void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool i8, float* h, float* hn) {
+// pg: the rows are a run of whole prompt blocks (pg->pfb rows each, at least 5): each block's
+// rows take that block's attention path (attn_tile or run_mh, E:1328-1337), in one pass.
+void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool i8, float* h, float* hn,
+                const PfGeom* pg = nullptr) {
   hipStream_t st = c->st;
   const GmRows R = gm_rows(c);
   const float sqh = std::sqrt((float)H);
@@ -1851,15 +1897,15 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
     (void)in_ln;
     uint16_t* KCo = c->gm_kv.as<uint16_t>() + c->gm_koff[ol];
     uint16_t* VCo = c->gm_kv.as<uint16_t>() + c->gm_voff[ol];
-    pf_lin(c, lay.m[0], R.a, M, R.q, i8, true);  // E:1287-1288
-    if (own) {
-      pf_lin(c, lay.m[1], R.a, M, R.k, i8, false);
-      pf_lin(c, lay.m[2], R.a, M, R.v, i8, false);
+    {  // E:1287-1288: q (and k, v on the owner layers) in one launch
+      const Mat* mq[3] = {&lay.m[0], &lay.m[1], &lay.m[2]};
+      float* yq[3] = {R.q, R.k, R.v};
+      pf_lin_multi(c, own ? 3 : 1, mq, R.a, M, yq, i8);
     }
     const float* cs = ty ? c->gm_rope.as<float>() : c->rope.as<float>();
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
     launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own);
-    if (M <= 4 && pos0 + M > 192) {  // E:1305-1327
+    if (!pg && M <= 4 && pos0 + M > 192) {  // E:1305-1327
       AttnGeom ag{};
       ag.M = M;
       ag.kmax = pos0 + M - 1;
@@ -1880,13 +1926,16 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
         launch_attn_geom(KCo, VCo, R.q, NQ * HD, ag, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), R.att,
                          NQ * HD, st);
     } else {  // attn_tile (M >= 4 past 64 keys, no sibling) or run_mh: one block of M rows
-      launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, PfGeom{M, pos0, M, sib}, 0, M, sliding, st, false,
-                     hd);
+      launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, pg ? *pg : PfGeom{M, pos0, M, sib}, 0, M, sliding,
+                     st, false, hd);
     }
     pf_lin(c, lay.m[3], R.att, M, R.o, i8, true);                       // E:1356
     launch_pf_post_attn(R.o, R.x, R.a, post_attn, pre_ff, M, st);       // E:1358-1361
-    pf_lin(c, lay.m[4], R.a, M, R.g, i8, true);                         // E:1363-1371
-    pf_lin(c, lay.m[5], R.a, M, R.u, i8, false);
+    {  // E:1363-1371: gate and up in one launch
+      const Mat* mg[2] = {&lay.m[4], &lay.m[5]};
+      float* yg[2] = {R.g, R.u};
+      pf_lin_multi(c, 2, mg, R.a, M, yg, i8);
+    }
     launch_pf_act(R.g, R.u, R.act, (size_t)M * G.I, st);
     pf_lin(c, lay.m[6], R.act, M, R.o, i8, true);                                               // E:1373
     launch_pf_post_ff(R.o, R.x, R.a, post_ff, nullptr, nullptr, 1.0f, nullptr, -1, M, st);      // E:1375-1377
@@ -1953,13 +2002,10 @@ int g4v_model_create_gemma(g4v_ctx* c, int V, const int* mlp, int ctxcap) {
     ALLOC(c->gm_rope, rt.size() * 4);
     HIPCHK(hipMemcpy(c->gm_rope.p, rt.data(), rt.size() * 4, hipMemcpyHostToDevice));
   }
-  ALLOC(c->gm_rows, gm_rows_floats(Imax) * 4);
-  ALLOC(c->gm_tok, GM_ROWS * 4);
-  ALLOC(c->gm_s, (size_t)pf_score_floats(GM_ROWS, ctxcap, 0) * 4);
-  const size_t Kmax = std::max<size_t>(NQ * 512, std::max<size_t>(H, Imax)), Rp = (size_t)w4a8_mpad(GM_ROWS);
-  ALLOC(c->pfxq, Rp * Kmax * 2);  // W4A8 operands of a prompt block
-  ALLOC(c->pfsx, (Kmax / 32) * Rp * 4);
-  ALLOC(c->pfcorr, (Kmax / 32) * Rp * 4);
+  c->gm_cap = 0;
+  c->gm_sfl = 0;
+  r = gm_reserve(c, GM_ROWS, (size_t)pf_score_floats(GM_ROWS, ctxcap, 0));  // a prompt block / verify pass
+  if (r) return r;
   ALLOC(c->po5, (size_t)MAXT * MAXM * NQ * 512 * 4);
   ALLOC(c->pm5, (size_t)MAXT * MAXM * NQ * 4);
   ALLOC(c->pl5, (size_t)MAXT * MAXM * NQ * 4);
@@ -2014,6 +2060,67 @@ int g4v_model_set_ple_rows(g4v_ctx* c, int tok0, int n, const uint16_t* rows) {
 }  // extern "C"
 
 extern "C" {
+
+// a Gemma-4-E2B layout with weights generated on the device from `seed` (no checkpoint): the
+// embedding f2bf(0.02 normal), int4 matrices with scales as g4v_model_synth draws them, norm
+// vectors r16(0.5 + unif) (q / k norms r16(0.2 + 0.1 unif)), layer scalars 0.75, the per-layer
+// embedding table f2bf(0.5 normal) for every token
+extern "C" int g4v_model_synth_gemma(g4v_ctx* c, uint64_t seed, int V, const int* mlp, int ctxcap) {
+  int r = g4v_model_create_gemma(c, V, mlp, ctxcap);
+  if (r) return r;
+  hipStream_t st = c->st;
+  launch_gen_bf16_normal(c->E.as<uint16_t>(), (size_t)V * H, rng_stream(seed, 1), 0.02f, st);
+  r = head_build_dev(c, V);
+  if (r) return r;
+  c->head_ready = true;
+  size_t maxw = (size_t)GM_PLN * H;
+  for (int l = 0; l < GM_NL; ++l)
+    for (int j = 0; j < 9; ++j) {
+      int N, K;
+      gm_shape(c, l, j, &N, &K);
+      maxw = std::max(maxw, (size_t)N * K);
+    }
+  DBuf tw, ts;
+  ALLOC(tw, maxw / 2);
+  ALLOC(ts, maxw / 16);
+  auto gen_mat = [&](Mat& m, int N, int K, uint64_t tag) -> int {
+    launch_gen_w4(tw.as<uint8_t>(), ts.as<uint16_t>(), (size_t)N * K / 2, (size_t)N * K / 32, rng_stream(seed, tag),
+                  rng_stream(seed, tag + 500000), st);
+    return upload_w4(c, m, tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K);
+  };
+  for (int l = 0; l < GM_NL; ++l) {
+    auto& G = c->gm[l];
+    for (int j = 0; j < 9; ++j) {
+      if (!G.own && (j == 1 || j == 2)) continue;
+      int N, K;
+      gm_shape(c, l, j, &N, &K);
+      if ((r = gen_mat(gm_mat(c, l, j), N, K, 1000 + 10 * (uint64_t)l + j))) return r;
+    }
+    std::vector<float> nv(5 * H + 2 * G.hd, 0.f);
+    for (int t = 0; t < 7; ++t) {
+      if (t == 6 && !G.own) continue;
+      const int n = t < 5 ? H : G.hd, off = t < 5 ? t * H : 5 * H + (t - 5) * G.hd;
+      const float base = t < 5 ? 0.5f : 0.2f, span = t < 5 ? 1.0f : 0.1f;
+      const uint64_t sn = rng_stream(seed, 3000 + 10 * (uint64_t)l + t);
+      for (int i = 0; i < n; ++i) nv[off + i] = r16(base + span * rng_unif(sn, i));
+    }
+    HIPCHK(hipMemcpy(G.nv.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice));
+    G.scalar = 0.75f;
+    G.normed = true;
+  }
+  if ((r = gen_mat(c->gm_plproj, GM_PLN, H, 900))) return r;
+  std::vector<float> pn(GM_PD), fn(H);
+  const uint64_t sp = rng_stream(seed, 901), sf = rng_stream(seed, 4000);
+  for (int i = 0; i < GM_PD; ++i) pn[i] = r16(0.5f + rng_unif(sp, i));
+  for (int i = 0; i < H; ++i) fn[i] = r16(0.5f + rng_unif(sf, i));
+  HIPCHK(hipMemcpy(c->gm_plnorm.p, pn.data(), GM_PD * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->fnorm.p, fn.data(), H * 4, hipMemcpyHostToDevice));
+  launch_gen_bf16_normal(c->gm_ple.as<uint16_t>(), (size_t)V * GM_PLN, rng_stream(seed, 902), 0.5f, st);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipStreamSynchronize(st));
+  c->gm_plready = true;
+  return 0;
+}
 
 static int gm_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint16_t* s) {
   ARGCHK(l >= 0 && l < GM_NL && j >= 0 && j < 9, "model_set_matrix: layer or matrix index out of range");
@@ -2113,7 +2220,20 @@ static int gm_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int
          "prefill: more positions per split than the split buffer holds");
   for (int i = 0; i < n; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "prefill: token id outside the vocabulary");
   HIPCHK(hipSetDevice(c->device));
-  for (int b = 0; b < n; b += pfb) {
+  // blocks of 5 rows or more take attn_tile / run_mh only (E:1305, 1328): every block but a last
+  // one that is short (split-KV past ATT_PAR) or a single row (exact float, E:311) runs in one
+  // pass; smaller blocks run one by one
+  const int Ml = n - (n - 1) / pfb * pfb, p0l = pos0 + n - Ml;
+  const bool tail = (Ml <= 4 && p0l + Ml > 192) || Ml == 1;
+  const int nA = pfb >= 5 ? (tail ? n - Ml : n) : 0;
+  if (nA > 0) {
+    int r = gm_reserve(c, nA, (size_t)pf_score_floats(nA, pos0, 0));
+    if (r) return r;
+    HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks, (size_t)nA * 4, hipMemcpyHostToDevice, c->st));
+    const PfGeom g{n, pos0, pfb, -1};
+    gm_forward(c, nA, pos0, nsplit, -1, nA == n ? nA - 1 : -1, c->pf_i8, c->h.as<float>(), c->hn.as<float>(), &g);
+  }
+  for (int b = nA; b < n; b += pfb) {
     const int M = std::min(pfb, n - b);
     const bool last = b + M == n;
     HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks + b, (size_t)M * 4, hipMemcpyHostToDevice, c->st));

@@ -30,6 +30,7 @@ SIGNATURES = {
     "g4v_w4g32_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4g32_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
     "g4v_model_create_gemma": (_i, [_vp, _i, _i32p, _i]),
+    "g4v_model_synth_gemma": (_i, [_vp, C.c_uint64, _i, _i32p, _i]),
     "g4v_model_set_norms_gemma": (_i, [_vp, _i, C.POINTER(C.c_void_p), C.c_float]),
     "g4v_model_set_ple": (_i, [_vp, _u8p, _u16p, _f32p]),
     "g4v_model_set_ple_rows": (_i, [_vp, _i, _i, _u16p]),
@@ -282,6 +283,10 @@ class Device:
 
     def model_create_gemma(self, V, mlp, ctxcap=4096):
         self._ok(self.L.g4v_model_create_gemma(self.h, V, _c(mlp, np.int32), ctxcap), "model_create_gemma")
+
+    def model_synth_gemma(self, seed, V, mlp, ctxcap=4096):
+        """the Gemma-4-E2B layout with device-generated weights"""
+        self._ok(self.L.g4v_model_synth_gemma(self.h, seed, V, _c(mlp, np.int32), ctxcap), "model_synth_gemma")
 
     def set_norms_gemma(self, layer, norms, scalar):
         """norms: 7 float vectors (k_norm None past layer 14)"""

@@ -122,6 +122,9 @@ int g4v_model_set_final_norm(g4v_ctx* c, const float* w);
  * table rows; then g4v_prefill, g4v_verify_step (a chain of up to 7 drafts) and
  * g4v_verify_sibling run that layout. */
 int g4v_model_create_gemma(g4v_ctx* c, int V, const int* mlp, int ctxcap);
+/* the same layout with every tensor generated on the device from seed (no reference
+ * counterpart: the benchmark's Gemma-4-E2B workload without a checkpoint) */
+int g4v_model_synth_gemma(g4v_ctx* c, uint64_t seed, int V, const int* mlp, int ctxcap);
 /* nv: in_ln, post_attn, pre_ff, post_ff, post_per_layer_input_norm [1536 each], q_norm, k_norm
  * [hd each; k_norm null past layer 14]; scalar: layer_scalar */
 int g4v_model_set_norms_gemma(g4v_ctx* c, int layer, const float* const nv[7], float scalar);

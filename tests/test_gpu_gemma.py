@@ -320,3 +320,24 @@ def test_gemma_engine_needs_drafter_files(gemma):
     proc = subprocess.run([exe, d, os.path.join(d, "index.tsv"), pf, "4"], env=env, capture_output=True, text=True,
                           timeout=300)
     assert proc.returncode == 2 and "none.tsv" in proc.stderr, (proc.returncode, proc.stderr[-500:])
+
+
+def test_gemma_synth_layout(g4v):
+    """g4v_model_synth_gemma (the benchmark's Gemma-4-E2B workload, weights generated on the
+    device) runs prefill, decode and chain passes; two contexts from one seed agree bit for bit"""
+    outs = []
+    for _ in range(2):
+        dev = g4v.Device(0)
+        try:
+            dev.model_synth_gemma(17, 16384, [512] * 15 + [1024] * 20, 1024)
+            toks = (np.arange(300, dtype=np.int32) * 37) % 16384
+            g0, h = dev.prefill(toks, 0, 32, 6, hidden=True)
+            r1, h1 = dev.verify(np.array([g0], np.int32), 0, 0, 300, 6, hidden=True)
+            r4, h4 = dev.verify(np.array([g0, 5, 6, 7], np.int32), 3, 0, 300, 6, hidden=True)
+            outs.append((g0, h, r1.commit[0], h1, r4.as_dict(), h4))
+        finally:
+            dev.close()
+    a, b = outs
+    assert a[0] == b[0] and a[2] == b[2] and a[4] == b[4]
+    assert same(a[1], b[1]) and same(a[3], b[3]) and same(a[5], b[5])
+    assert a[4]["G"][0] == a[2]  # row 0 of the chain pass is the decode pass's row
