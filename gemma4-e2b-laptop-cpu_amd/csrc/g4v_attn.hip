@@ -76,14 +76,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
   const int i2 = e & (HD / 2 - 1);
   // Every load that does not depend on the step geometry is issued first, together with the
-  // geometry itself (one round trip): the query heads and, in a verify pass, the raw key/value
-  // rows of the pass (all of them: the split that holds some is only known from the
-  // geometry), their RoPE factors and the norm weights.
+  // geometry itself (one round trip): the query heads and, in a verify pass, their norm weights
+  // and RoPE factors.  The pass's raw key/value rows are the context's last positions: the last
+  // two splits load them (and their RoPE factors) up front, any other split only when the
+  // geometry puts some of them in it (a context shorter than T rows per split).
   float qv[ATT_HB];
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
   float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {}, qw = 0.f, kw = 0.f, cq = 0.f, sq = 0.f;
-  if (STEP) {
+  auto load_rows = [&]() {
 #pragma unroll
     for (int r = 0; r < MAXM; ++r) {
       kv[0][r] = P.kraw[(size_t)r * HD + e];
@@ -91,10 +92,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
       ck[r] = P.ropestep[(size_t)r * HD + i2];
       sk[r] = P.ropestep[(size_t)r * HD + HD / 2 + i2];
     }
+  };
+  if (STEP) {
     qw = P.qn[e];
     kw = P.kn[e];
     cq = P.ropestep[(size_t)m * HD + i2];
     sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
+    if (t >= T - 2) load_rows();
   }
   // E:1325-1326 geometry: every thread reads the (uniform) parameters itself, no serial set-up;
   // all fields are read unconditionally so that they arrive together
@@ -127,7 +131,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   }
   if (m >= M) return;
   const int len = kmax - kmin + 1;
-  const int c0 = kmin + (int)((long)t * len / T), c1 = kmin + (int)((long)(t + 1) * len / T);
+  // (t + 1) len < 2^31 for every launch: 32-bit division
+  const int c0 = kmin + (int)((unsigned)(t * len) / (unsigned)T),
+            c1 = kmin + (int)((unsigned)((t + 1) * len) / (unsigned)T);
   const int PP = c1 - c0;
   // E:740 attn_allowed for this block's row, restricted to the split
   auto allowed = [=](int p) { return p >= c0 && p < c1 && p >= lo_m && p <= pos_m && !(p >= sl_m && p <= sh_m); };
@@ -173,12 +179,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1); they are the
   // split's last positions
   const int rn0 = STEP ? max(c0 - pos0, 0) : 0, rn1 = STEP ? min(c1 - pos0, M) : 0;
+  if (STEP && t < T - 2 && rn0 < rn1) load_rows();
   __builtin_amdgcn_sched_barrier(0);  // keep the prologue loads ahead of the tile loads
+  // the key tiles now (also when the split is empty: no paths with fewer loads in flight); the
+  // value tiles once the pass's rows have arrived, so that they do not queue in front of them
 #pragma unroll
-  for (int k = 0; k < ATT_RING; ++k) {  // also when the split is empty: no paths with fewer
-    issue_k(k, kring[k]);               // loads in flight
-    issue_v(k, vring[k]);
-  }
+  for (int k = 0; k < ATT_RING; ++k) issue_k(k, kring[k]);
   __builtin_amdgcn_sched_barrier(0);
   if (STEP) {
     // E:1307-1324 on the block's query heads and the pass's key/value rows of this split:
@@ -186,10 +192,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 #pragma unroll
     for (int hh = 0; hh < ATT_HB; ++hh) nx[hh][e] = qv[hh];
 #pragma unroll
-    for (int r = 0; r < MAXM; ++r) {
-      nx[ATT_HB + r][e] = kv[0][r];
-      nx[ATT_HB + MAXM + r][e] = kv[1][r];
-    }
+    for (int r = 0; r < MAXM; ++r)
+      if (r >= rn0 && r < rn1) {  // uniform
+        nx[ATT_HB + r][e] = kv[0][r];
+        nx[ATT_HB + MAXM + r][e] = kv[1][r];
+      }
     __syncthreads();
     for (int idx = threadIdx.x; idx < (ATT_HB + 2 * MAXM) * 16; idx += ATT_THREADS) {
       const int row = idx >> 4, t16 = idx & 15;
@@ -232,6 +239,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
         P.VCw[vc_index(pos0 + r, e)] = vnew[r][e];
       }
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < ATT_RING; ++k) issue_v(k, vring[k]);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) qs[hh][e & 7][((e >> 3) & 1) * 16 + (e >> 4)] = qv[hh];
   float mymax[ATT_HB];
@@ -246,7 +257,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 
   // sweep 1: scores (E:750-816) straight from the fetched key rows; key ring slot k holds
   // key tile s = base + k.  Lane group ps scores position pb + ps (positions outside the split
-  // from a clamped row: their scores are never used).
+  // from a clamped row: their scores are never used); its lane 0 keeps the running max over
+  // the allowed positions (max is order free).
   for (int base = 0; base < NTp; base += ATT_RING)
 #pragma unroll
   for (int k = 0; k < ATT_RING; ++k) {
@@ -279,21 +291,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
           s1 = fmaf(qr[hh][16 + tt], kf[16 + tt], s1);
         }
         const float v = hsum8_lanes(s0 + s1);
-        if (l == 0) sw[hh][p - pb0] = v;
+        if (l == 0) {
+          sw[hh][p - pb0] = v;
+          if (allowed(p) && mymax[hh] < v) mymax[hh] = v;
+        }
       }
     }
     // the slot's next entry, once its current one is consumed (the loop then carries each
     // slot in one register set: no copies, which would wait for loads in flight)
     issue_k(s + ATT_RING, kring[k]);
-  }
-  __syncthreads();
-  // the running max over the allowed positions only (max is order free)
-  for (int idx = threadIdx.x; idx < ATT_HB * NT * ATT_TILE; idx += ATT_THREADS) {
-    const int hh = idx / (NT * ATT_TILE), pp = idx - hh * (NT * ATT_TILE);
-    const float v = sw[hh][pp];
-#pragma unroll
-    for (int h2 = 0; h2 < ATT_HB; ++h2)
-      if (h2 == hh && allowed(pb0 + pp) && mymax[h2] < v) mymax[h2] = v;
   }
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) {
@@ -344,19 +350,22 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
                                vring[k][3].x, vring[k][3].y, vring[k][3].z, vring[k][3].w};
       const bool full = full_tile(pb);
       const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb) & (STEP ? ~bits_in(pos0, pos0 + MAXM, pb) : 0xFFFFFFFFu);
+      // the tile's weights read up front (one LDS round trip per tile instead of one per 4
+      // positions); wave w forms head w % ATT_HB's sum from its own copy (no per-head selects)
+      float4 w4[ATT_HB][ATT_TILE / 4], wl[ATT_TILE / 4];
+#pragma unroll
+      for (int p4 = 0; p4 < ATT_TILE / 4; ++p4) {
+#pragma unroll
+        for (int hh = 0; hh < ATT_HB; ++hh) w4[hh][p4] = *reinterpret_cast<const float4*>(&sw[hh][pb - pb0 + 4 * p4]);
+        wl[p4] = *reinterpret_cast<const float4*>(&sw[wave % ATT_HB][pb - pb0 + 4 * p4]);
+      }
       auto sweep = [&](const bool masked) {
 #pragma unroll
-        for (int p4 = 0; p4 < ATT_TILE; p4 += 4) {
-          float4 w4[ATT_HB];
-#pragma unroll
-          for (int hh = 0; hh < ATT_HB; ++hh) w4[hh] = *reinterpret_cast<const float4*>(&sw[hh][pb - pb0 + p4]);
-          {  // wave w forms head w % ATT_HB's sum (its own read: no per-head selects)
-            const float4 wl = *reinterpret_cast<const float4*>(&sw[wave % ATT_HB][pb - pb0 + p4]);
-            lsum = (((lsum + wl.x) + wl.y) + wl.z) + wl.w;
-          }
+        for (int p4 = 0; p4 < ATT_TILE / 4; ++p4) {
+          lsum = (((lsum + wl[p4].x) + wl[p4].y) + wl[p4].z) + wl[p4].w;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int pe = p4 + q;
+            const int pe = 4 * p4 + q;
             // the position's half word moved to the top (byte select 0x0c gives a zero byte),
             // cleared when masked
             uint32_t vb = __builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], (pe & 1) ? 0x03020c0cu : 0x01000c0cu);
@@ -364,7 +373,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
             const float vv = as_f32(vb);
 #pragma unroll
             for (int hh = 0; hh < ATT_HB; ++hh) {
-              const float wgt = q == 0 ? w4[hh].x : (q == 1 ? w4[hh].y : (q == 2 ? w4[hh].z : w4[hh].w));
+              const float4 w = w4[hh][p4];
+              const float wgt = q == 0 ? w.x : (q == 1 ? w.y : (q == 2 ? w.z : w.w));
               o[hh] = fmaf(wgt, vv, o[hh]);
             }
           }
