@@ -91,7 +91,7 @@ struct GemvTDev {
 static size_t gemvt_lds(int mpl, int K, bool nrm, int tr, bool mrg) {
   const int G = K / 32;
   return (size_t)mpl * G * 9 * 16 + (size_t)mpl * G * 4 + (size_t)mpl * 8 * tr * 4 + (size_t)mpl * tr * 4 * 2 +
-         (mrg ? (size_t)mpl * NQ * (MAXT + 1) * 4 : 0) +
+         (mrg ? (size_t)mpl * NQ * (3 * MAXT + 1) * 4 : 0) +
          (nrm ? (size_t)2 * H * 4 + (size_t)2 * mpl * 4 : 0);
 }
 
@@ -101,15 +101,43 @@ static size_t gemvt_lds(int mpl, int K, bool nrm, int tr, bool mrg) {
 // chain lanes); a block is the TR x 8 (row, chain lane) pairs of one tile, 8 TR threads
 // KT: the reduction length when fixed at compile time (0: a.K), so that the LDS addresses of the
 // staged activations fold into instruction offsets
-template <int MPL, bool MRG, bool NRM, int TR, int KT = 0>
+// XM: the Gemma per-layer-input gate (GemvTArgs::epi_pli; NRM prologue in mode 3)
+template <int MPL, bool MRG, bool NRM, int TR, int KT = 0, int XM = 0>
 __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
   constexpr int NT = TR * 8;
   const GemvTArgs& a = d.a;
-  const int K = KT ? KT : a.K, G = K / 32, GC = K / 256, M = a.M;
+  // The launch's argument block is cold in the scalar cache: the arguments the block needs
+  // before its first vector loads are read into registers together, ahead of the first branch
+  // (one round trip; the compiler would otherwise fetch them in three dependent rounds, around
+  // the division and the early exit, and fetch the chosen matrix again by a computed address).
+  int nsub = d.nsub, tl1 = d.tiles[1], tl2 = d.tiles[2], tl3 = d.tiles[3], M = a.M, T = 0, nmode = 0;
+  const uint4 *w0w = a.mat[0].w, *w0s = a.mat[0].s, *w1w = a.mat[1].w, *w1s = a.mat[1].s, *w2w = a.mat[2].w,
+              *w2s = a.mat[2].s;
+  const float *pa = nullptr, *pb = nullptr, *pc = nullptr, *pd = nullptr;
+  if constexpr (MRG) {
+    pa = a.mrg_po;
+    pb = a.mrg_pm;
+    pc = a.mrg_pl;
+    T = a.mrg_T;
+  } else if constexpr (NRM) {
+    pa = a.nrm_o;
+    pb = a.nrm_xin;
+    pc = a.nrm_w1;
+    pd = a.nrm_w2;
+    nmode = a.nrm_mode;
+  } else {
+    pa = reinterpret_cast<const float*>(a.xs);
+    pb = a.gs;
+  }
+  // (the pointers are inputs only, so that they keep their global address space)
+  asm volatile(""
+               : "+s"(nsub), "+s"(tl1), "+s"(tl2), "+s"(tl3), "+s"(M), "+s"(T), "+s"(nmode)
+               : "s"(w0w), "s"(w0s), "s"(w1w), "s"(w1s), "s"(w2w), "s"(w2s), "s"(pa), "s"(pb), "s"(pc), "s"(pd));
+  const int K = KT ? KT : a.K, G = K / 32, GC = K / 256;
   // block -> (tile, row subset); the tiles of XCD x (block % 8) are x, x + 8, ...
   const int xcd = blockIdx.x & 7, kq = blockIdx.x >> 3;
-  const int sub = kq % d.nsub, t = (kq / d.nsub) * 8 + xcd;
-  if (t >= d.tiles[3]) return;
+  const int sub = kq % nsub, t = (kq / nsub) * 8 + xcd;
+  if (t >= tl3) return;
   const int m0 = sub * MPL;
   // thread -> (chain lane j, row lane of the tile); rows of a 32-row tile are one half of a
   // 64-row tile of the storage layout
@@ -123,12 +151,13 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
   float* OFL = RL + MPL * 8 * TR;                            // [MPL][TR]
   float* YL = OFL + MPL * TR;                                // [MPL][TR]
 
-  const int mi = (t >= d.tiles[1]) + (t >= d.tiles[2]);
-  const W4Tile W = mi == 0 ? a.mat[0] : (mi == 1 ? a.mat[1] : a.mat[2]);
-  const int tl = t - d.tiles[mi];
+  const int mi = (t >= tl1) + (t >= tl2);
+  const uint4* Ww = mi == 0 ? w0w : (mi == 1 ? w1w : w2w);
+  const uint4* Ws = mi == 0 ? w0s : (mi == 1 ? w1s : w2s);
+  const int tl = t - (mi == 0 ? 0 : (mi == 1 ? tl1 : tl2));
   const int t64 = tl / (64 / TR), r64 = (tl % (64 / TR)) * TR + lane;  // storage tile and row
-  const uint4* wp = W.w + ((size_t)t64 * GC * 8 + j) * 64 + r64;  // chunk c at + c * 512
-  const uint4* sp = W.s + (size_t)t64 * GC * 64 + r64;             // chunk c at + c * 64
+  const uint4* wp = Ww + ((size_t)t64 * GC * 8 + j) * 64 + r64;  // chunk c at + c * 512
+  const uint4* sp = Ws + (size_t)t64 * GC * 64 + r64;             // chunk c at + c * 64
   constexpr int GT_B = gt_batch<MPL>();
   uint4 wA[GT_B], sA[GT_B], wB[GT_B], sB[GT_B];
   auto load_batch = [&](uint4 (&w)[GT_B], uint4 (&s)[GT_B], int c0) {  // indices clamped
@@ -156,22 +185,25 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
     // element y = r16((fma chain over those t of o_t sc_t) * inv).  Thread f < MPL * NQ forms
     // the factors of pair f once (SCL, -1 marks a split without positions); every thread then
     // runs the chains of its elements 4u .. 4u+3 (one head) and stores them staged.
-    const int T = a.mrg_T;
     float* XF = reinterpret_cast<float*>(XL);
     float* SCL = YL + MPL * TR;            // [MPL][NQ][MAXT]
     float* INVL = SCL + MPL * NQ * MAXT;   // [MPL][NQ]
     constexpr int NI = MPL * (NQ * HD / 4) / NT;  // elements groups per thread (K = NQ * HD)
     constexpr int PT = 8;                         // splits whose partials are prefetched
-    const int f = threadIdx.x;
-    float pl[MAXT], pm[MAXT];
-    if (f < MPL * NQ) {
-      const int m = min(m0 + f / NQ, M - 1), h = f % NQ;
-#pragma unroll
-      for (int tt = 0; tt < MAXT; ++tt) {
-        const size_t kk = ((size_t)tt * M + m) * NQ + h;
-        pl[tt] = tt < T ? a.mrg_pl[kk] : 0.f;
-        pm[tt] = tt < T ? a.mrg_pm[kk] : 0.f;
-      }
+    // thread f < MPL * NQ * MAXT takes split ft of pair fp (row, head): the factors of the
+    // splits are formed in parallel, only the sum l runs over them in order
+    const int f = threadIdx.x, fp = f / MAXT, ft = f % MAXT;
+    float* PLL = INVL + MPL * NQ;           // [MPL][NQ][MAXT]
+    float* PML = PLL + MPL * NQ * MAXT;     // [MPL][NQ][MAXT]
+    // the expf table goes to LDS with the partials (no dependent constant-memory load per split)
+    __shared__ uint64_t ETAB[32];
+    const uint64_t etv = c_expf_tab_t[f & 31];
+    float plv = 0.f, pmv = 0.f;
+    if (f < MPL * NQ * MAXT && ft < T) {
+      const int m = min(m0 + fp / NQ, M - 1), h = fp % NQ;
+      const size_t kk = ((size_t)ft * M + m) * NQ + h;
+      plv = pc[kk];
+      pmv = pb[kk];
     }
     float4 po[NI][PT];
     auto po_load = [&](int tb) {
@@ -182,27 +214,33 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
 #pragma unroll
         for (int k = 0; k < PT; ++k) {
           const int tt = tb + k;
-          po[it][k] = tt < T ? *reinterpret_cast<const float4*>(a.mrg_po + (((size_t)tt * M + m) * NQ + h) * HD + i)
+          po[it][k] = tt < T ? *reinterpret_cast<const float4*>(pa + (((size_t)tt * M + m) * NQ + h) * HD + i)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
     };
     po_load(0);
     weights_after();
-    if (f < MPL * NQ) {
-      float M0 = -1e30f;
+    if (f < MPL * NQ * MAXT) {
+      PLL[f] = plv;
+      PML[f] = pmv;
+    }
+    if (f < 32) ETAB[f] = etv;
+    __syncthreads();
+    if (f < MPL * NQ * MAXT) {
+      float M0 = -1e30f;  // (max is order free)
 #pragma unroll
       for (int tt = 0; tt < MAXT; ++tt)
-        if (tt < T && pl[tt] > 0) M0 = (M0 < pm[tt]) ? pm[tt] : M0;
+        if (tt < T && PLL[fp * MAXT + tt] > 0) M0 = (M0 < PML[fp * MAXT + tt]) ? PML[fp * MAXT + tt] : M0;
+      SCL[f] = (ft < T && plv > 0) ? libm_expf_neg(pmv - M0, ETAB) : -1.f;
+    }
+    __syncthreads();
+    if (f < MPL * NQ) {
       double l = 0;
 #pragma unroll
       for (int tt = 0; tt < MAXT; ++tt) {
-        float sc = -1.f;
-        if (tt < T && pl[tt] > 0) {
-          sc = libm_expf_neg(pm[tt] - M0, c_expf_tab_t);
-          l = fma((double)pl[tt], (double)sc, l);
-        }
-        SCL[f * MAXT + tt] = sc;
+        const float sc = SCL[f * MAXT + tt];
+        if (tt < T && sc >= 0.f) l = fma((double)PLL[f * MAXT + tt], (double)sc, l);
       }
       INVL[f] = (float)(1.0 / l);
     }
@@ -249,8 +287,8 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
     constexpr int RW4 = H / 4, NV = (MPL * RW4 + NT - 1) / NT, NW = (RW4 + NT - 1) / NT;
     float* W12 = YL + MPL * TR;                                   // [2][H]
     float* RR = W12 + 2 * H;                                      // [2][MPL]
-    const float4* o4 = reinterpret_cast<const float4*>(a.nrm_o);
-    const float4* x4 = reinterpret_cast<const float4*>(a.nrm_xin);
+    const float4* o4 = reinterpret_cast<const float4*>(pa);
+    const float4* x4 = reinterpret_cast<const float4*>(pb);
     float4 ov[NV], xv[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {  // clamped: rows past M read row M - 1 and are zeroed
@@ -263,8 +301,8 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
 #pragma unroll
     for (int k = 0; k < NW; ++k) {
       const int wi = min((int)threadIdx.x + k * NT, RW4 - 1);
-      w1[k] = reinterpret_cast<const float4*>(a.nrm_w1)[wi];
-      w2[k] = reinterpret_cast<const float4*>(a.nrm_w2)[wi];
+      w1[k] = reinterpret_cast<const float4*>(pc)[wi];
+      w2[k] = reinterpret_cast<const float4*>(pd)[wi];
     }
     weights_after();
 #pragma unroll
@@ -320,7 +358,7 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
       __syncthreads();
     };
     rms_rows(RR);
-    const bool after_mlp = a.nrm_mode == 2;
+    const bool after_mlp = nmode == 2;
     const float scal = a.nrm_scalar;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -338,20 +376,22 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
       }
     }
     __syncthreads();
-    rms_rows(RR + MPL);
+    if constexpr (XM == 0) {  // (XM 1, mode 3: x1 itself is the product's input)
+      rms_rows(RR + MPL);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {  // xa in place, plain order
-      const int u = threadIdx.x + k * NT;
-      if (u < MPL * RW4) {
-        const int q = u / RW4, c4 = u - q * RW4;
-        const float r2 = RR[MPL + q];
-        const float4 tv = XL[pad(u)], w = reinterpret_cast<const float4*>(W12 + H)[c4];
-        float4 v = make_float4((tv.x * r2) * w.x, (tv.y * r2) * w.y, (tv.z * r2) * w.z, (tv.w * r2) * w.w);
-        if (!after_mlp) v = make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w));
-        XL[pad(u)] = v;
+      for (int k = 0; k < NV; ++k) {  // xa in place, plain order
+        const int u = threadIdx.x + k * NT;
+        if (u < MPL * RW4) {
+          const int q = u / RW4, c4 = u - q * RW4;
+          const float r2 = RR[MPL + q];
+          const float4 tv = XL[pad(u)], w = reinterpret_cast<const float4*>(W12 + H)[c4];
+          float4 v = make_float4((tv.x * r2) * w.x, (tv.y * r2) * w.y, (tv.z * r2) * w.z, (tv.w * r2) * w.w);
+          if (!after_mlp) v = make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w));
+          XL[pad(u)] = v;
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
     for (int idx = threadIdx.x; idx < MPL * G; idx += NT) {  // staged order + group sums
       float4* b4 = XL + (size_t)idx * 9;  // row q = idx / G, group g = idx % G: 8 float4 in plain order
       float4 r[8];
@@ -373,13 +413,13 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
 #pragma unroll
     for (int k = 0; k < NX; ++k) {
       const int u = min((int)threadIdx.x + k * NT, MPL * RW - 1), q = u / RW;
-      xr[k] = a.xs[(size_t)min(m0 + q, M - 1) * RW + (u - q * RW)];
+      xr[k] = reinterpret_cast<const float4*>(pa)[(size_t)min(m0 + q, M - 1) * RW + (u - q * RW)];
     }
-    if (a.gs) {
+    if (pb) {
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
         const int idx = min((int)threadIdx.x + k * NT, MPL * G - 1), q = idx / G;
-        gr[k] = a.gs[(size_t)min(m0 + q, M - 1) * G + (idx - q * G)];
+        gr[k] = pb[(size_t)min(m0 + q, M - 1) * G + (idx - q * G)];
       }
     }
     weights_after();
@@ -479,7 +519,12 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
     const float* r = RL + q * 8 * TR + rl;
     const float y = (((r[0] + r[4 * TR]) + (r[TR] + r[5 * TR])) + ((r[2 * TR] + r[6 * TR]) + (r[3 * TR] + r[7 * TR]))) -
                     8.f * OFL[q * TR + rl];
-    if (!a.gateup) {
+    if constexpr (XM == 1) {  // E:421-427 g2 = r16(r16(gelu8(r16 y)) * r16(pli)), staged for the next product
+      const int n = tl * TR + rl;
+      if (m < M)
+        a.y[0][(size_t)m * a.ldy[0] + staged_index(n)] =
+            r16(r16(gelu8(r16(y))) * r16(a.epi_pli[(size_t)m * a.epi_pli_ld + n]));
+    } else if (!a.gateup) {
       if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * TR + rl] = y;
     } else {
       YL[q * TR + rl] = y;
@@ -507,6 +552,8 @@ static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
   // prologue, K 1536), down (K 6144)
   if (d.a.mrg_po) {  // (a fixed K costs the merge variant registers: it stays generic)
     if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false, TR>), g, b, lds, st, d);
+  } else if (d.a.epi_pli) {
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR, 0, 1>), g, b, lds, st, d);
   } else if (d.a.nrm_mode) {
     if constexpr ((MPL == 2 || MPL == 4) && TR == 64) {
       if (K == 1536) {

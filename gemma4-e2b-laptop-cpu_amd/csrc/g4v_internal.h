@@ -130,6 +130,12 @@ struct GemvTArgs {
   const float* nrm_w1;
   const float* nrm_w2;
   float nrm_scalar;
+  // the per-layer-input gate of the Gemma-4-E2B layout (E:1375-1386, pg_fused_task E:405-443):
+  // with epi_pli set, the norm prologue stops at x1 (mode 3: the MLP residual without scalar or
+  // second norm, x1 the product's input) and the output is g2 = r16(r16(gelu8(r16 y)) *
+  // r16(epi_pli[m * epi_pli_ld + n])), written staged into y[0] ([M][ldy]) for the next product
+  const float* epi_pli;
+  int epi_pli_ld;
 };
 // W4A8 (g4v_w4a8.hip): operand tiles of a matrix from its original bytes [N][K/2] and scales
 // [N][K/32] (N % 16 == 0): tw [N/16][K/128][64] uint4, ts [N/16][K/256][16] uint4
