@@ -83,7 +83,7 @@ struct g4v_ctx {
   // head
   bool head_ready = false;
   int V = 0;
-  DBuf E, dec, exc_ptr, exc_col, exc_del, cb, scr_wr, scr_s, coef, lut;
+  DBuf E, dec, x3sm, x3ix, exc_ptr, exc_col, exc_del, cb, scr_wr, scr_s, coef, lut;
   HeadDev hd{};
   HeadBufs hb1, hb2;
   DBuf hrow, hnrow;
@@ -880,6 +880,13 @@ static int head_build_dev(g4v_ctx* c, int V) {
   c->hd.exc_col_w = c->exc_col.as<uint16_t>();
   c->hd.exc_del_w = c->exc_del.as<float>();
   head_build_exc(c->E.as<uint16_t>(), V, c->hd, st);
+  ALLOC(c->x3sm, (size_t)V * 24 * 8 * 8);
+  ALLOC(c->x3ix, (size_t)V * 24 * 8 * 4);
+  c->hd.x3sm = c->x3sm.as<uint2>();
+  c->hd.x3ix = c->x3ix.as<uint32_t>();
+  c->hd.x3smw = c->x3sm.as<uint2>();
+  c->hd.x3ixw = c->x3ix.as<uint32_t>();
+  head_build_x3(V, c->hd, st);
   // E:1236-1243 screen
   DBuf wq;
   ALLOC(wq, (size_t)V * H / 2);
@@ -920,7 +927,7 @@ static HeadRun head_args(g4v_ctx* c, HeadBufs& b, const float* h, const float* h
   r.prof.mark = pmark;
   r.prof.ctx = c;
   // one full-head pass reads every decoded row (V x 1536 bf16), the row pointers and the exceptions
-  r.full_bytes = (double)c->V * H * 2 + (double)(c->V + 1) * 4 + (double)c->exc_col.n / 2 * 6;
+  r.full_bytes = (double)c->V * 24 * 8 * 12 + (double)(c->V + 1) * 4 + (double)c->exc_col.n / 2 * 6;
   r.hs = b.hs;
   r.hd = c->hd;
   r.screen = W4Dev{c->scr_wr.as<uint4>(), c->scr_s.as<uint16_t>(), c->V, H};
@@ -1351,6 +1358,18 @@ int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* 
   } else if (!std::strcmp(what, "Sq") && c->scr_s.p) {  // screen scales, [V][48] bf16
     src = c->scr_s.p;
     nb = (size_t)c->V * (H / 32) * 2;
+  } else if (!std::strcmp(what, "cb") && c->cb.p) {
+    src = c->cb.p;
+    nb = 8;
+  } else if (!std::strcmp(what, "dec") && c->dec.p) {
+    src = c->dec.p;
+    nb = (size_t)c->V * H * 2;
+  } else if (!std::strcmp(what, "x3sm") && c->x3sm.p) {
+    src = c->x3sm.p;
+    nb = (size_t)c->V * 24 * 8 * 8;
+  } else if (!std::strcmp(what, "x3ix") && c->x3ix.p) {
+    src = c->x3ix.p;
+    nb = (size_t)c->V * 24 * 8 * 4;
   } else if (!std::strcmp(what, "Wq") && c->scr_wr.p) {  // screen int4, [V][768] bytes
     return read_relaid_w4(c, c->scr_wr.p, c->V, H, dst, cap, nbytes);
   } else if (std::sscanf(what + 1, "%d_%d", &l, &j) == 2 && l >= 0 && l < (int)c->L.size()) {

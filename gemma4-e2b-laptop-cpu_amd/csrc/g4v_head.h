@@ -14,6 +14,13 @@ struct HeadDev {
   uint16_t* exc_col_w;   // writable aliases used while building
   float* exc_del_w;
   const uint8_t* cb;     // [8] exponent codebook (device)
+  // the exp3 form streamed by the full head (X3:1-4 packing, laid out for the lane order of
+  // dec): per (row, group pair p, lane j) the sign|mantissa bytes of dec's 8 weights w0..w7 as
+  // {w0 w2 w4 w6 | w1 w3 w5 w7} and their codebook indices, byte b = idx(w_2b) | idx(w_2b+1) << 4
+  const uint2* x3sm;     // [V][24][8]
+  const uint32_t* x3ix;  // [V][24][8]
+  uint2* x3smw;          // writable aliases used while building
+  uint32_t* x3ixw;
 };
 
 // per-call scratch for up to MAXM rows
@@ -65,6 +72,7 @@ struct HeadRun {
 void head_build(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st);
 void head_build_dec(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st);
 void head_build_exc(const uint16_t* E, int V, HeadDev& hd, hipStream_t st);
+void head_build_x3(int V, HeadDev& hd, hipStream_t st);
 void screen_build(const uint16_t* E, int V, uint8_t* Wq, uint16_t* Sq, float* coef, hipStream_t st);
 void head_run(const HeadRun& r, hipStream_t st);
 size_t head_lds(int MT);

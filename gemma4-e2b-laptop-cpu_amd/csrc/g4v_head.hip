@@ -186,6 +186,54 @@ __global__ __launch_bounds__(256) void k_head_rescore(HeadScratch hs, HeadDev hd
 // full head for the rows whose survivor count exceeds the limit (E:1489-1498); the dec16 row
 // is read once for all MT activation rows.  This pass stores each row's main dot (X3:83-107,
 // before the exception deltas); k_head_exc then adds the deltas in order and rounds.
+// the 8 weights of one (row, group pair, lane) entry of the exp3 form (HeadDev::x3sm / x3ix):
+// exponent bytes from the 8-entry codebook by byte permutes, then the bf16 bit patterns
+// (hi = sign | e >> 1, lo = (e & 1) << 7 | mantissa) moved to the top of each fp32 word
+__device__ __forceinline__ void x3_decode(uint2 sm, uint32_t ix, uint32_t cblo, uint32_t cbhi, float (&w)[8]) {
+  const uint32_t ee = __builtin_amdgcn_perm(cbhi, cblo, ix & 0x0F0F0F0Fu);
+  const uint32_t eo = __builtin_amdgcn_perm(cbhi, cblo, (ix >> 4) & 0x0F0F0F0Fu);
+  const uint32_t he = (sm.x & 0x80808080u) | ((ee >> 1) & 0x7F7F7F7Fu), le = ((ee << 7) & 0x80808080u) | (sm.x & 0x7F7F7F7Fu);
+  const uint32_t ho = (sm.y & 0x80808080u) | ((eo >> 1) & 0x7F7F7F7Fu), lo = ((eo << 7) & 0x80808080u) | (sm.y & 0x7F7F7F7Fu);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t sel = ((uint32_t)(4 + b) << 24) | ((uint32_t)b << 16) | 0x0C0Cu;
+    w[2 * b] = as_f32(__builtin_amdgcn_perm(he, le, sel));
+    w[2 * b + 1] = as_f32(__builtin_amdgcn_perm(ho, lo, sel));
+  }
+}
+
+// the exp3 form from the decoded head (every decoded exponent is a codebook entry)
+__global__ void k_x3_pack(HeadDev hd, int V) {
+  uint8_t cb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cb[i] = hd.cb[i];
+  const size_t total = (size_t)V * 24 * 8;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const uint4 v = hd.dec[u];
+    const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+    uint32_t se = 0, so = 0, ix = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t b = (wd[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      const uint32_t smb = ((b >> 8) & 0x80u) | (b & 0x7Fu), e = (b >> 7) & 0xFFu;
+      uint32_t idx = 0;
+#pragma unroll
+      for (int i = 7; i >= 0; --i)
+        if (cb[i] == e) idx = i;
+      const int sh = 8 * (k >> 1);
+      if (k & 1) {
+        so |= smb << sh;
+        ix |= idx << (sh + 4);
+      } else {
+        se |= smb << sh;
+        ix |= idx << sh;
+      }
+    }
+    hd.x3smw[u] = make_uint2(se, so);
+    hd.x3ixw[u] = ix;
+  }
+}
+
 template <int MT>
 __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, const float* __restrict__ h,
                                                    int V, const int* active) {
@@ -202,6 +250,7 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
   }
   if (!any) return;
   stage_h(h, MT, XH, XR);
+  const uint32_t cblo = reinterpret_cast<const uint32_t*>(hd.cb)[0], cbhi = reinterpret_cast<const uint32_t*>(hd.cb)[1];
   const int j = threadIdx.x & 7, slot = threadIdx.x >> 3, nslots = blockDim.x >> 3;
   for (int n0 = blockIdx.x * nslots; n0 < V; n0 += gridDim.x * nslots) {
     const int n = n0 + slot;
@@ -210,13 +259,13 @@ __global__ __launch_bounds__(256) void k_head_full(HeadScratch hs, HeadDev hd, c
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.f;
-    const uint4* p = hd.dec + (size_t)nn * (24 * 8) + j;
+    const uint2* ps = hd.x3sm + (size_t)nn * (24 * 8) + j;
+    const uint32_t* pi = hd.x3ix + (size_t)nn * (24 * 8) + j;
 #pragma unroll 8
     for (int q = 0; q < 24; ++q) {
-      const uint4 w = p[q * 8];
-      const float w0 = as_f32(w.x << 16), w1 = as_f32(w.x & 0xFFFF0000u), w2 = as_f32(w.y << 16),
-                  w3 = as_f32(w.y & 0xFFFF0000u), w4 = as_f32(w.z << 16), w5 = as_f32(w.z & 0xFFFF0000u),
-                  w6 = as_f32(w.w << 16), w7 = as_f32(w.w & 0xFFFF0000u);
+      float wd[8];
+      x3_decode(ps[q * 8], pi[q * 8], cblo, cbhi, wd);
+      const float w0 = wd[0], w1 = wd[1], w2 = wd[2], w3 = wd[3], w4 = wd[4], w5 = wd[5], w6 = wd[6], w7 = wd[7];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         const float4 x0 = XH[(m * 48 + 2 * q) * 8 + j], x1 = XH[(m * 48 + 2 * q + 1) * 8 + j];
@@ -487,6 +536,10 @@ void head_build(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStr
 void head_build_dec(const uint16_t* E, int V, HeadDev& hd, HeadBuildTmp& tmp, hipStream_t st) {
   hipLaunchKernelGGL(k_dec16, dim3(grid_for((size_t)V * 24, 256)), dim3(256), 0, st, E, hd, tmp.gcnt, V);
   hipLaunchKernelGGL(k_rowcount, dim3(grid_for(V, 256)), dim3(256), 0, st, tmp.gcnt, tmp.rowcnt, V);
+}
+
+void head_build_x3(int V, HeadDev& hd, hipStream_t st) {
+  hipLaunchKernelGGL(k_x3_pack, dim3(grid_for((size_t)V * 24 * 8, 256)), dim3(256), 0, st, hd, V);
 }
 
 void head_build_exc(const uint16_t* E, int V, HeadDev& hd, hipStream_t st) {

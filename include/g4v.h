@@ -139,7 +139,10 @@ int g4v_model_set_kv(g4v_ctx* c, int layer, int pos0, int n, const uint16_t* K, 
 int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
 /* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm",
  * the Gemma layout's owner caches "GK<l>" / "GV<l>" [ctxcap][hd] (l < 15),
- * and the head screen "Wq" [V][768], "Sq" [V][48] bf16, "coef" [V] f32, in the reference's layouts) */
+ * the head screen "Wq" [V][768], "Sq" [V][48] bf16, "coef" [V] f32, in the reference's layouts,
+ * and the exact head's device forms: "cb" the 8-entry exponent codebook, "dec" the decoded bf16
+ * weights [V][24][8][8] in the fma-lane order, "x3sm" [V][24][8] uint2 and "x3ix" [V][24][8]
+ * uint32 the exp3 form the full head streams) */
 int g4v_model_read(g4v_ctx* c, const char* what, void* dst, size_t cap, size_t* nbytes);
 
 /* ---- one verify pass (fwd E:1256-1502 + lazy head E:1453-1488 + accept E:1647-1661).

@@ -233,6 +233,41 @@ def test_head_full_vocab(orc, dev):
     assert fb[0] == 1 and fb[1] == 1 and fb[2] == 0 and fb[3] == 0
 
 
+def test_head_exp3_form(orc, dev):
+    """the exp3 form the full head streams (x3sm / x3ix, laid out in the fma-lane order of the
+    decoded head) carries exactly the oracle's X3 packing (X3:25-43): the codebook, every weight's
+    sign|mantissa byte and codebook index (the nearest entry for an exception); and decoding it
+    by the documented byte rule gives the decoded head weight for weight"""
+    V, K = 16384, 1536
+    E, P, _ = _head_inputs(orc, V, 31)
+    note("exp3 form V=16384")
+    dev.head_build(E, V)
+    cb = dev.read("cb", np.uint8)
+    assert same(cb, P["cb"])
+    sm = dev.read("x3sm", np.uint32).reshape(V, 24, 8, 2)
+    ix = dev.read("x3ix", np.uint32).reshape(V, 24, 8)
+    dec = dev.read("dec", np.uint16).reshape(V, 24, 8, 8)
+    # oracle X3 data: per (row, group) 32 sign|mantissa bytes then three 4-byte index bit planes
+    data = P["data"].reshape(V, K // 32, 44)
+    smo = data[:, :, :32]
+    planes = data[:, :, 32:].copy().view(np.uint32).reshape(V, K // 32, 3)
+    # entry (p, j), weight k: group 2p + k // 4, position [j, 16 + j, 8 + j, 24 + j][k % 4]
+    j = np.arange(8)
+    for k in range(8):
+        g = 2 * np.arange(24)[:, None] + k // 4
+        pos = np.array([0, 16, 8, 24])[k % 4] + j[None, :]
+        want_sm = smo[:, g, pos]
+        bits = (planes[:, g, :] >> pos[None, :, :, None].astype(np.uint32)) & 1
+        want_ix = bits[..., 0] | (bits[..., 1] << 1) | (bits[..., 2] << 2)
+        got_sm = (sm[..., k & 1] >> (8 * (k >> 1))) & 0xFF
+        got_ix = (ix >> (8 * (k >> 1) + 4 * (k & 1))) & 0xF
+        assert same(got_sm.astype(np.uint8), want_sm), k
+        assert same(got_ix, want_ix.astype(np.uint32)), k
+        bf = ((got_sm & 0x80) << 8) | (cb[got_ix].astype(np.uint32) << 7) | (got_sm & 0x7F)
+        assert same(bf.astype(np.uint16), dec[..., k]), k
+    assert P["ptr"][-1] > 0  # the fixture holds exceptions (nearest-entry indices are exercised)
+
+
 def test_head_build_vs_reference_engine(orc, dev):
     """the device's screen build (int4 bytes, bf16 scales, coefficients of all 262,144 rows)
     against the screen the reference engine's own main() builds (E:1235-1244;
