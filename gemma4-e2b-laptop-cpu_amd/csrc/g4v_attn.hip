@@ -471,8 +471,8 @@ void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, con
 }
 
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
-                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh) {
-  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh, float* gs) {
+  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
              nullptr};
   hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
                      (const StepDev*)nullptr, 0, g.T);

@@ -1865,6 +1865,9 @@ void gm_shape(const g4v_ctx* c, int l, int j, int* N, int* K) {
   *K = k[j];
 }
 Mat& gm_mat(g4v_ctx* c, int l, int j) { return j < 7 ? c->L[l]->m[j] : (j == 7 ? c->gm[l].pg : c->gm[l].pp); }
+// the matrices the verify pass multiplies with the row-tile GEMV (row-tiled copies): all but gate
+// and up (paired by tile_gateup) and a down projection longer than the tile GEMV's K (12288)
+bool gm_tiled(int j, int K) { return j != 4 && j != 5 && K <= 6144; }
 
 bool gm_complete(const g4v_ctx* c, std::string* what) {
   if (!c->head_ready) {
@@ -1965,6 +1968,168 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
     launch_pf_post_ff(R.o, R.x, R.a, post_ple, last ? nullptr : c->gm[l + 1].nv.as<float>(), c->fnorm.as<float>(),
                       G.scalar, h, last ? hrow : -1, M, st, hn);
   }
+}
+
+// fwd of a verify pass (M <= MAXM rows, exact float) with the row-tile GEMV: every residual / norm
+// block folded into the prologue of the product that consumes it, as the synthetic stack's
+// verify pass does.  Per layer: q/k/v (prologue: the previous layer's per-layer-input residual,
+// scalar and input norm, E:1390-1404), q/k norm + RoPE + cache rows, attention (split-KV past
+// ATT_PAR for up to 4 rows, else attn_tile / run_mh, output staged), o, gate/up + gelu
+// (prologue: attention residual and pre-FF norm, E:1358-1361), down, the per-layer-input gate
+// (prologue: the MLP residual, E:1375-1377; epilogue: gelu x per-layer input, E:1379-1385) and
+// its projection (E:1386).  Residual rows: xa at a layer's start, xb after attention, xc after
+// the MLP (R.x, R.a, R.g); the products' outputs meet their consumers in R.o.  The last row
+// block's final-normed state goes to h / hn (row 0 on).
+void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* h, float* hn) {
+  hipStream_t st = c->st;
+  const GmRows R = gm_rows(c);
+  float *xa = R.x, *xb = R.a, *xc = R.g, *attgs = R.u;
+  const float sqh = std::sqrt((float)H);
+  const int* tok = c->gm_tok.as<int>();
+  launch_pf_embed(c->E.as<uint16_t>(), tok, c->gm[0].nv.as<float>(), sqh, xa, xb, M, st);  // E:1262-1267
+  pf_lin(c, c->gm_plproj, xa, M, R.pr, false, true);                                       // E:615-660
+  launch_gm_ple(R.pr, tok, c->gm_ple.as<uint16_t>(), c->gm_plnorm.as<float>(), R.pli, M, st);
+  for (int l = 0; l < GM_NL; ++l) {
+    const auto& G = c->gm[l];
+    const Layer& lay = *c->L[l];
+    const int hd = G.hd, own = G.own, ol = gm_owner(l);
+    const bool sliding = hd != 512;
+    const float* nv = G.nv.as<float>();
+    const float *post_attn = nv + H, *pre_ff = nv + 2 * H, *post_ff = nv + 3 * H, *qn = nv + 5 * H, *kn = nv + 5 * H + hd;
+    uint16_t* KCo = c->gm_kv.as<uint16_t>() + c->gm_koff[ol];
+    uint16_t* VCo = c->gm_kv.as<uint16_t>() + c->gm_voff[ol];
+    if (l == 0) {  // E:1287-1288 from the embedding row's norm
+      const Mat* mq[3] = {&lay.m[0], &lay.m[1], &lay.m[2]};
+      float* yq[3] = {R.q, R.k, R.v};
+      pf_lin_multi(c, own ? 3 : 1, mq, xb, M, yq, false);
+    } else {
+      const auto& P = c->gm[l - 1];
+      const float* pnv = P.nv.as<float>();
+      GemvTArgs a{};
+      const int nm = own ? 3 : 1;
+      float* ys[3] = {R.q, R.k, R.v};
+      const int ld[3] = {NQ * hd, hd, hd};
+      for (int j = 0; j < nm; ++j) {
+        a.mat[j] = lay.m[j].tile();
+        a.y[j] = ys[j];
+        a.ldy[j] = ld[j];
+      }
+      a.K = H;
+      a.M = M;
+      a.nrm_mode = 2;
+      a.nrm_o = R.o;
+      a.nrm_xin = xc;
+      a.nrm_xout = xa;
+      a.nrm_w1 = pnv + 4 * H;  // post_per_layer_input_norm of layer l - 1
+      a.nrm_w2 = nv;           // input_layernorm of layer l
+      a.nrm_scalar = P.scalar;
+      launch_gemv_t(a, st, c->gcfg[0][0], c->gcfg[0][1]);
+    }
+    const float* cs = hd == 512 ? c->gm_rope.as<float>() : c->rope.as<float>();
+    const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
+    launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own);
+    const float* ogs = nullptr;  // group sums of the staged attention rows (split path)
+    if (M <= 4 && pos0 + M > 192) {  // E:1305-1327
+      AttnGeom ag{};
+      ag.M = M;
+      ag.kmax = pos0 + M - 1;
+      ag.kmin = ag.kmax;
+      ag.T = nsplit;
+      for (int m = 0; m < M; ++m) {
+        const int rp = m == sib ? pos0 + 1 : pos0 + m;
+        ag.pos[m] = pos0 + m;
+        ag.lo[m] = sliding ? std::max(0, rp - 511) : 0;
+        ag.skip_lo[m] = m == sib ? pos0 + 1 : 1;
+        ag.skip_hi[m] = m == sib ? pos0 + m - 1 : 0;
+        ag.kmin = std::min(ag.kmin, ag.lo[m]);
+      }
+      if (hd == 512)
+        (void)launch_attn_geom_hd(KCo, VCo, R.q, NQ * 512, ag, 512, c->po5.as<float>(), c->pm5.as<float>(),
+                                  c->pl5.as<float>(), R.att, NQ * 512, attgs, st);
+      else
+        launch_attn_geom(KCo, VCo, R.q, NQ * HD, ag, c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), R.att,
+                         NQ * HD, st, NQ, attgs);
+      ogs = attgs;
+    } else {  // attn_tile (M >= 4 past 64 keys, no sibling) or run_mh
+      launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, PfGeom{M, pos0, M, sib}, 0, M, sliding, st, true, hd);
+    }
+    {  // E:1356
+      GemvTArgs a{};
+      a.mat[0] = lay.m[3].tile();
+      a.y[0] = R.o;
+      a.ldy[0] = H;
+      a.xs = reinterpret_cast<const float4*>(R.att);
+      a.gs = ogs;
+      a.K = NQ * hd;
+      a.M = M;
+      launch_gemv_t(a, st, c->gcfg[1][0], c->gcfg[1][1]);
+    }
+    {  // E:1358-1371: the attention residual and pre-FF norm, then gate / up and gelu
+      GemvTArgs a{};
+      a.mat[0] = W4Tile{lay.m[4].tw.as<uint4>(), lay.m[4].ts.as<uint4>(), G.I};
+      a.gateup = 1;
+      a.y[0] = R.act;
+      a.ldy[0] = G.I;
+      a.nrm_mode = 1;
+      a.nrm_o = R.o;
+      a.nrm_xin = xa;
+      a.nrm_xout = xb;
+      a.nrm_w1 = post_attn;
+      a.nrm_w2 = pre_ff;
+      a.K = H;
+      a.M = M;
+      launch_gemv_t(a, st, c->gcfg[2][0], c->gcfg[2][1]);
+    }
+    if (G.I <= 6144) {  // E:1373
+      GemvTArgs a{};
+      a.mat[0] = lay.m[6].tile();
+      a.y[0] = R.o;
+      a.ldy[0] = H;
+      a.xs = reinterpret_cast<const float4*>(R.act);
+      a.K = G.I;
+      a.M = M;
+      launch_gemv_t(a, st, c->gcfg[3][0], c->gcfg[3][1]);
+    } else {
+      GemvArgs a{};
+      a.mat[0] = lay.m[6].dev();
+      a.y[0] = R.o;
+      a.ldy[0] = H;
+      a.xs = reinterpret_cast<const float4*>(R.act);
+      a.K = G.I;
+      a.M = M;
+      launch_gemv(a, EPI_STORE, st);
+    }
+    {  // E:1375-1385: the MLP residual, then the per-layer-input gate, gelu x the layer's input
+      GemvTArgs a{};
+      a.mat[0] = G.pg.tile();
+      a.y[0] = R.g2;
+      a.ldy[0] = GM_PD;
+      a.nrm_mode = 3;
+      a.nrm_o = R.o;
+      a.nrm_xin = xb;
+      a.nrm_xout = xc;
+      a.nrm_w1 = post_ff;
+      a.nrm_w2 = post_ff;  // (no second norm in this mode)
+      a.epi_pli = R.pli + (size_t)l * GM_PD;
+      a.epi_pli_ld = GM_PLN;
+      a.K = H;
+      a.M = M;
+      launch_gemv_t(a, st, 1, 64);
+    }
+    {  // E:1386
+      GemvTArgs a{};
+      a.mat[0] = G.pp.tile();
+      a.y[0] = R.o;
+      a.ldy[0] = H;
+      a.xs = reinterpret_cast<const float4*>(R.g2);
+      a.K = GM_PD;
+      a.M = M;
+      launch_gemv_t(a, st, 1, 64);
+    }
+  }
+  // E:1387-1404 and 1414-1417 of the last layer: its per-layer-input residual, scalar, final norm
+  const auto& L = c->gm[GM_NL - 1];
+  launch_pf_post_ff(R.o, xc, xb, L.nv.as<float>() + 4 * H, nullptr, c->fnorm.as<float>(), L.scalar, h, 0, M, st, hn);
 }
 }  // namespace
 
@@ -2102,10 +2267,10 @@ extern "C" int g4v_model_synth_gemma(g4v_ctx* c, uint64_t seed, int V, const int
   DBuf tw, ts;
   ALLOC(tw, maxw / 2);
   ALLOC(ts, maxw / 16);
-  auto gen_mat = [&](Mat& m, int N, int K, uint64_t tag) -> int {
+  auto gen_mat = [&](Mat& m, int N, int K, uint64_t tag, bool tiled = false) -> int {
     launch_gen_w4(tw.as<uint8_t>(), ts.as<uint16_t>(), (size_t)N * K / 2, (size_t)N * K / 32, rng_stream(seed, tag),
                   rng_stream(seed, tag + 500000), st);
-    return upload_w4(c, m, tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K);
+    return upload_w4(c, m, tw.as<uint8_t>(), ts.as<uint16_t>(), true, N, K, tiled);
   };
   for (int l = 0; l < GM_NL; ++l) {
     auto& G = c->gm[l];
@@ -2113,8 +2278,9 @@ extern "C" int g4v_model_synth_gemma(g4v_ctx* c, uint64_t seed, int V, const int
       if (!G.own && (j == 1 || j == 2)) continue;
       int N, K;
       gm_shape(c, l, j, &N, &K);
-      if ((r = gen_mat(gm_mat(c, l, j), N, K, 1000 + 10 * (uint64_t)l + j))) return r;
+      if ((r = gen_mat(gm_mat(c, l, j), N, K, 1000 + 10 * (uint64_t)l + j, gm_tiled(j, K)))) return r;
     }
+    if ((r = tile_gateup(c, *c->L[l]))) return r;
     std::vector<float> nv(5 * H + 2 * G.hd, 0.f);
     for (int t = 0; t < 7; ++t) {
       if (t == 6 && !G.own) continue;
@@ -2149,8 +2315,9 @@ static int gm_set_matrix(g4v_ctx* c, int l, int j, const uint8_t* w, const uint1
   DBuf tmp;
   ALLOC(tmp, (size_t)N * K / 2);
   HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)N * K / 2, hipMemcpyHostToDevice, c->st));
-  int r = upload_w4(c, gm_mat(c, l, j), tmp.as<uint8_t>(), s, false, N, K);
+  int r = upload_w4(c, gm_mat(c, l, j), tmp.as<uint8_t>(), s, false, N, K, gm_tiled(j, K));
   if (r) return r;
+  if ((j == 4 || j == 5) && (r = tile_gateup(c, *c->L[l]))) return r;
   HIPCHK(hipStreamSynchronize(c->st));
   return 0;
 }
@@ -2191,7 +2358,7 @@ static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int 
   HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, st));
   HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks, (size_t)M * 4, hipMemcpyHostToDevice, st));
   const int sib = nb == 1 ? na + 1 : -1;
-  gm_forward(c, M, pos0, nsplit, sib, 0, false, c->h.as<float>(), c->hn.as<float>());
+  gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>());
   const StepDev* sp = c->stepd.as<StepDev>();
   VerifyResultDev* res = c->resd.as<VerifyResultDev>();
   head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);  // E:1453-1488

@@ -171,8 +171,11 @@ struct AttnGeom {
   int pos[MAXM], lo[MAXM], skip_lo[MAXM], skip_hi[MAXM];
 };
 // nh query heads (a multiple of 2, at most 8) of q rows [M][ldq]; partials keep the 8-head layout
+// gs not null: out written in the staged GEMV input layout (staged_index) with its group sums
+// [M][ldo / 32]
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
-                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);
+                      float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ,
+                      float* gs = nullptr);
 // the same for head dim 512 (g4v_attn_hd.hip), 8 heads, partials [T][M][8][512]; out plain
 // [M][ldo] or, with gs, staged (staged_index) with its group sums [M][ldo / 32].  Returns -1
 // (nothing launched) for a shape it does not serve: a split longer than ATT_SPLIT_MAX keys.
