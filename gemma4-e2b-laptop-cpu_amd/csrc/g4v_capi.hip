@@ -1866,8 +1866,8 @@ void gm_shape(const g4v_ctx* c, int l, int j, int* N, int* K) {
 }
 Mat& gm_mat(g4v_ctx* c, int l, int j) { return j < 7 ? c->L[l]->m[j] : (j == 7 ? c->gm[l].pg : c->gm[l].pp); }
 // the matrices the verify pass multiplies with the row-tile GEMV (row-tiled copies): all but gate
-// and up (paired by tile_gateup) and a down projection longer than the tile GEMV's K (12288)
-bool gm_tiled(int j, int K) { return j != 4 && j != 5 && K <= 6144; }
+// and up (paired by tile_gateup)
+bool gm_tiled(int j, int K) { return j != 4 && j != 5 && K <= 12288; }
 
 bool gm_complete(const g4v_ctx* c, std::string* what) {
   if (!c->head_ready) {
@@ -1984,6 +1984,9 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
   hipStream_t st = c->st;
   const GmRows R = gm_rows(c);
   float *xa = R.x, *xb = R.a, *xc = R.g, *attgs = R.u;
+  // a one-row pass runs 32-row tiles (twice the blocks of a 64-row tile: one subset only)
+  auto rows_of = [&](int cls) { return M == 1 ? 1 : c->gcfg[cls][0]; };
+  auto tile_of = [&](int cls) { return M == 1 ? 32 : c->gcfg[cls][1]; };
   const float sqh = std::sqrt((float)H);
   const int* tok = c->gm_tok.as<int>();
   launch_pf_embed(c->E.as<uint16_t>(), tok, c->gm[0].nv.as<float>(), sqh, xa, xb, M, st);  // E:1262-1267
@@ -2023,7 +2026,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.nrm_w1 = pnv + 4 * H;  // post_per_layer_input_norm of layer l - 1
       a.nrm_w2 = nv;           // input_layernorm of layer l
       a.nrm_scalar = P.scalar;
-      launch_gemv_t(a, st, c->gcfg[0][0], c->gcfg[0][1]);
+      launch_gemv_t(a, st, rows_of(0), tile_of(0));
     }
     const float* cs = hd == 512 ? c->gm_rope.as<float>() : c->rope.as<float>();
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
@@ -2062,7 +2065,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.gs = ogs;
       a.K = NQ * hd;
       a.M = M;
-      launch_gemv_t(a, st, c->gcfg[1][0], c->gcfg[1][1]);
+      launch_gemv_t(a, st, rows_of(1), tile_of(1));
     }
     {  // E:1358-1371: the attention residual and pre-FF norm, then gate / up and gelu
       GemvTArgs a{};
@@ -2078,9 +2081,10 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.nrm_w2 = pre_ff;
       a.K = H;
       a.M = M;
-      launch_gemv_t(a, st, c->gcfg[2][0], c->gcfg[2][1]);
+      launch_gemv_t(a, st, rows_of(2), tile_of(2));
     }
-    if (G.I <= 6144) {  // E:1373
+    bool down_done = false;  // E:1373
+    if (lay.m[6].tw.p) {
       GemvTArgs a{};
       a.mat[0] = lay.m[6].tile();
       a.y[0] = R.o;
@@ -2088,8 +2092,11 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.xs = reinterpret_cast<const float4*>(R.act);
       a.K = G.I;
       a.M = M;
-      launch_gemv_t(a, st, c->gcfg[3][0], c->gcfg[3][1]);
-    } else {
+      // the wide shape runs one activation row per 64-row tile (a one-row pass: the plain GEMV)
+      const bool wide = G.I > 6144;
+      if (!wide || M > 1) down_done = launch_gemv_t(a, st, wide ? 1 : rows_of(3), wide ? 64 : tile_of(3)) > 0;
+    }
+    if (!down_done) {
       GemvArgs a{};
       a.mat[0] = lay.m[6].dev();
       a.y[0] = R.o;
@@ -2114,7 +2121,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.epi_pli_ld = GM_PLN;
       a.K = H;
       a.M = M;
-      launch_gemv_t(a, st, 1, 64);
+      launch_gemv_t(a, st, 1, M == 1 ? 32 : 64);
     }
     {  // E:1386
       GemvTArgs a{};
@@ -2124,7 +2131,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.xs = reinterpret_cast<const float4*>(R.g2);
       a.K = GM_PD;
       a.M = M;
-      launch_gemv_t(a, st, 1, 64);
+      launch_gemv_t(a, st, 1, M == 1 ? 32 : 64);
     }
   }
   // E:1387-1404 and 1414-1417 of the last layer: its per-layer-input residual, scalar, final norm

@@ -406,8 +406,10 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
       GSL[idx] = sum;
     }
   } else {
-    // K <= 6144: at most MPL * 1536 staged float4 and MPL * 192 group sums per block
-    constexpr int NX = (MPL * 1536 + NT - 1) / NT, NG = (MPL * 192 + NT - 1) / NT;
+    // K <= 6144 (or the fixed K, up to 12288): at most MPL * K / 4 staged float4 and MPL * K / 32
+    // group sums per block
+    constexpr int KMX = KT > 6144 ? KT : 6144;
+    constexpr int NX = (MPL * (KMX / 4) + NT - 1) / NT, NG = (MPL * (KMX / 32) + NT - 1) / NT;
     float4 xr[NX];
     float gr[NG];
 #pragma unroll
@@ -568,6 +570,10 @@ static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
         hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 6144>), g, b, lds, st, d);
         return;
       }
+      if (K == 12288) {  // the Gemma-4-E2B layout's wide down projections
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 12288>), g, b, lds, st, d);
+        return;
+      }
     }
     if constexpr (MPL == 2 && TR == 64) {
       if (K == 1536) {
@@ -581,7 +587,9 @@ static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
 
 // mpl: activation rows per block (1 to 4); tr: rows per tile (64 or 32)
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
-  if (a.K > 6144 || a.K % 256) return 0;  // the prologue register staging holds K <= 6144
+  // the prologue register staging holds K <= 6144, and K = 12288 for one activation row per block
+  // of a 64-row tile without a prologue of its own
+  if (a.K % 256 || (a.K > 6144 && !(a.K == 12288 && mpl == 1 && tr == 64 && !a.nrm_mode && !a.mrg_po))) return 0;
   if (tr != 32) tr = 64;
   if (mpl < 1) mpl = 1;
   if (mpl > 4) mpl = 4;
