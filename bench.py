@@ -9,9 +9,10 @@ advance the position by the committed tokens, as the engine's run_req does.
 
 Prints one JSON line: accepted tokens per second (value), the verify-step time, the
 dominant kernel class against the HBM roofline (HIP events on the library's stream over
-the timed region), the whole step's algorithmic bytes against peak HBM (step_hbm_frac), an
-accepted-path run (drafts the model takes, in branch a and branch b in turn, so acceptance
-and KV compaction are timed), the reference's own AVX2 kernels timed on this host (one
+the timed region), the whole step's algorithmic bytes against peak HBM (step_hbm_frac), the
+device's read and copy bandwidth over 2 GiB / 1 GiB buffers (hbm_stream), an accepted-path
+run (drafts the model takes, in branch a and branch b in turn, so acceptance and KV compaction
+are timed), the reference's own AVX2 kernels timed on this host (one
 thread per physical core and 8 threads, each in a child process, interleaved with a second
 GPU run, with the host's read bandwidth and lscpu summary), and the long-prompt workload's
 prefill and decode times.
@@ -21,6 +22,10 @@ prefill and decode times.
 linear layers on the matrix cores), then 256 speculative decode rounds with prompt-lookup
 drafts (n-gram 3, up to 3 drafts), or 3 MTP drafts from the synthetic drafter when the lookup
 finds none, verified as a chain.  A step is one prefill + 256 rounds.
+
+--workload gemma_layout runs the Gemma-4-E2B layout's passes alone (device-generated weights at
+the checkpoint's sizes: a 2,048-token prefill, then verify passes of 1, 4 and 8 rows) and prints
+that sub-object of the default line as its own line.
 """
 import argparse
 import importlib.util
@@ -331,7 +336,7 @@ def main():
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--workload", choices=["verify", "long_prompt"], default="verify")
+    ap.add_argument("--workload", choices=["verify", "long_prompt", "gemma_layout"], default="verify")
     ap.add_argument("--cpu-only", default=None, help=argparse.SUPPRESS)  # child process of the CPU baseline
     ap.add_argument("--no-long-prompt", action="store_true", help="skip the long-prompt sub-measurement")
     ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-E2B layout sub-measurement")
@@ -345,6 +350,9 @@ def main():
         sys.exit(2)
     if args.workload == "long_prompt":
         main_long_prompt(args, load_g4v())
+        return
+    if args.workload == "gemma_layout":  # the Gemma-4-E2B layout's passes alone (its sub-object as a line)
+        print(json.dumps(gemma_layout_summary(load_g4v())), flush=True)
         return
 
     g4v = load_g4v()
@@ -427,6 +435,10 @@ def main():
         "kernel_classes_us_per_step": classes,
         "setup_s": round(setup_s, 1),
     }
+    # the device's streaming bandwidth beside the 8 TB/s peak (bench/stream_bw.cpp:10-19 method)
+    out["hbm_stream"] = {"read_gbs": round(dev.hbm_stream(2 << 30, 5), 1),
+                         "copy_gbs": round(dev.hbm_stream(1 << 30, 5, copy=True), 1), "read_buffer": 2 << 30,
+                         "copy_buffer": 1 << 30, "passes": 5}
     if not args.no_cpu:
         # A (GPU) and B (CPU) interleaved: A1 above, B1 one thread per physical core, A2, B2 8 threads
         try:

@@ -3009,6 +3009,37 @@ int g4v_set_graphs(g4v_ctx* c, int on) {
   return 0;
 }
 
+// device read / copy bandwidth (the method of bench/stream_bw.cpp:10-19 on the GPU): a buffer of
+// `bytes` streamed `passes` times after one warm-up pass, timed with events on the library stream
+int g4v_hbm_stream(g4v_ctx* c, size_t bytes, int passes, int mode, double* gbps) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(gbps && bytes >= ((size_t)1 << 20) && bytes % 16 == 0 && passes >= 1 && passes <= 1000 &&
+             (mode == 0 || mode == 1),
+         "hbm_stream: bytes >= 1 MiB, a multiple of 16; 1 <= passes <= 1000; mode 0 (read) or 1 (copy)");
+  HIPCHK(hipSetDevice(c->device));
+  hipStream_t st = c->st;
+  DBuf src, dst;
+  ALLOC(src, bytes);
+  ALLOC(dst, mode == 1 ? bytes : (size_t)stream_grid() * 256 * 16);
+  const size_t n16 = bytes / 16;
+  launch_stream(2, nullptr, src.as<uint4>(), n16, st);
+  launch_stream(mode, src.as<uint4>(), dst.as<uint4>(), n16, st);
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  HIPCHK(hipEventRecord(e0, st));
+  for (int p = 0; p < passes; ++p) launch_stream(mode, src.as<uint4>(), dst.as<uint4>(), n16, st);
+  HIPCHK(hipEventRecord(e1, st));
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  HIPCHK(hipGetLastError());
+  *gbps = (double)passes * (double)bytes * (mode == 1 ? 2.0 : 1.0) / ((double)ms * 1e-3) / 1e9;
+  return 0;
+}
+
 int g4v_sync(g4v_ctx* c) {
   if (!c) return G4V_E_ARG;
   HIPCHK(hipSetDevice(c->device));

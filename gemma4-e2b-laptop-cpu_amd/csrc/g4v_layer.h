@@ -195,6 +195,10 @@ void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q
 namespace g4v {
 // positions per attention split the split kernel can hold
 int attn_pmax();
+// device bandwidth probe (g4v_stream.hip): mode 0 reads src (one word per thread to dst, a sink
+// of stream_grid() x 256 uint4), 1 copies src to dst, 2 fills dst with a pattern
+int stream_grid();
+void launch_stream(int mode, const uint4* src, uint4* dst, size_t n16, hipStream_t st);
 // device [npos][256] key / value rows into the device cache layout (kv_cap(npos) positions)
 void launch_kv_to_cache(const uint16_t* K, const uint16_t* V, int npos, uint16_t* KC, uint16_t* VC, hipStream_t st);
 }

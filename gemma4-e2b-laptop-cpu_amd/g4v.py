@@ -59,6 +59,7 @@ SIGNATURES = {
     "g4v_verify_sibling": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
     "g4v_profile": (_i, [_vp, C.c_uint]),
     "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
+    "g4v_hbm_stream": (_i, [_vp, C.c_size_t, _i, _i, _vp]),
     "g4v_sync": (_i, [_vp]),
     "g4v_set_graphs": (_i, [_vp, _i]),
     "g4v_set_prefill_int8": (_i, [_vp, _i]),
@@ -412,6 +413,12 @@ class Device:
 
     def sync(self):
         self._ok(self.L.g4v_sync(self.h), "sync")
+
+    def hbm_stream(self, nbytes, passes=10, copy=False):
+        """device read (or copy: read + write bytes) bandwidth in GB/s over a buffer of nbytes"""
+        g = C.c_double()
+        self._ok(self.L.g4v_hbm_stream(self.h, nbytes, passes, 1 if copy else 0, C.byref(g)), "hbm_stream")
+        return g.value
 
     def set_graphs(self, on):
         self._ok(self.L.g4v_set_graphs(self.h, 1 if on else 0), "set_graphs")

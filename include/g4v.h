@@ -251,6 +251,14 @@ int g4v_history_read(g4v_ctx* c, int* toks, int cap, int* L);
 #define G4V_PROF_NTAGS 13
 int g4v_profile(g4v_ctx* c, unsigned mask);
 int g4v_profile_read(g4v_ctx* c, double* ms, double* bytes, long long* count, int n);
+
+/* device read (mode 0) or copy (mode 1, read + write bytes counted) bandwidth in GB/s over a
+ * buffer of `bytes` (>= 1 MiB, a multiple of 16) streamed `passes` times.  No counterpart in the
+ * verify path: the device restatement of the reference's host probe bench/stream_bw.cpp:10-19
+ * (the bandwidth figures beside the roofline), and the copy of known bytes that calibrates the
+ * FETCH_SIZE / WRITE_SIZE counters. */
+int g4v_hbm_stream(g4v_ctx* c, size_t bytes, int passes, int mode, double* gbps);
+
 /* wait for all work of the context */
 int g4v_sync(g4v_ctx* c);
 

@@ -268,6 +268,18 @@ def test_head_exp3_form(orc, dev):
     assert P["ptr"][-1] > 0  # the fixture holds exceptions (nearest-entry indices are exercised)
 
 
+def test_hbm_stream_probe(dev):
+    """the device bandwidth probe (bench/stream_bw.cpp:10-19 method): a 2 GiB buffer, far past the
+    last-level cache, read and copied at a rate between 1 TB/s and the 8 TB/s HBM peak"""
+    note("hbm stream probe 2 GiB")
+    rd = dev.hbm_stream(2 << 30, 5)
+    cp = dev.hbm_stream(1 << 30, 5, copy=True)
+    assert 1000.0 < rd < 8000.0, rd
+    assert 1000.0 < cp < 8000.0, cp
+    with pytest.raises(RuntimeError):
+        dev.hbm_stream(1000, 1)
+
+
 def test_head_build_vs_reference_engine(orc, dev):
     """the device's screen build (int4 bytes, bf16 scales, coefficients of all 262,144 rows)
     against the screen the reference engine's own main() builds (E:1235-1244;
