@@ -171,7 +171,11 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
   // The prologue's own loads (activations, partials, residual rows) are issued first and the
   // first weight batch right after them: the load counter retires in issue order, so the
   // prologue then waits for its operands only, while the weights stream in behind it.
+  // An execution barrier (no memory wait) first: every wave of the block has issued its prologue
+  // loads before any wave's weights queue behind them in the CU's memory pipeline.
   auto weights_after = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     load_batch(wA, sA, 0);
     __builtin_amdgcn_sched_barrier(0);
