@@ -2092,9 +2092,9 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.xs = reinterpret_cast<const float4*>(R.act);
       a.K = G.I;
       a.M = M;
-      // the wide shape runs one activation row per 64-row tile (a one-row pass: the plain GEMV)
+      // the wide shape runs one activation row per block
       const bool wide = G.I > 6144;
-      if (!wide || M > 1) down_done = launch_gemv_t(a, st, wide ? 1 : rows_of(3), wide ? 64 : tile_of(3)) > 0;
+      down_done = launch_gemv_t(a, st, wide ? 1 : rows_of(3), wide ? (M == 1 ? 32 : 64) : tile_of(3)) > 0;
     }
     if (!down_done) {
       GemvArgs a{};

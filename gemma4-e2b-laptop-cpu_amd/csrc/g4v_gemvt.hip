@@ -574,6 +574,8 @@ static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
         hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 6144>), g, b, lds, st, d);
         return;
       }
+    }
+    if constexpr (MPL == 1) {
       if (K == 12288) {  // the Gemma-4-E2B layout's wide down projections
         hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 12288>), g, b, lds, st, d);
         return;
@@ -592,8 +594,9 @@ static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
 // mpl: activation rows per block (1 to 4); tr: rows per tile (64 or 32)
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
   // the prologue register staging holds K <= 6144, and K = 12288 for one activation row per block
-  // of a 64-row tile without a prologue of its own
-  if (a.K % 256 || (a.K > 6144 && !(a.K == 12288 && mpl == 1 && tr == 64 && !a.nrm_mode && !a.mrg_po))) return 0;
+  // without a prologue of its own
+  if (a.K % 256 || (a.K > 6144 && !(a.K == 12288 && mpl == 1 && !a.nrm_mode && !a.mrg_po && !a.epi_pli)))
+    return 0;
   if (tr != 32) tr = 64;
   if (mpl < 1) mpl = 1;
   if (mpl > 4) mpl = 4;
