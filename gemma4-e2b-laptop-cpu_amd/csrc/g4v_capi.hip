@@ -1101,8 +1101,8 @@ extern "C" {
 
 int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap) {
   if (!c) return G4V_E_ARG;
-  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && I <= 6144 && ctxcap > 8,
-         "model_synth: need I % 256 == 0, I <= 6144");
+  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && (I <= 6144 || I == 12288) && ctxcap > 8,
+         "model_synth: need I % 256 == 0, I <= 6144 or I = 12288");
   HIPCHK(hipSetDevice(c->device));
   hipStream_t st = c->st;
   int r = model_alloc(c, V, NL, I, ctxcap);
@@ -1152,8 +1152,8 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
 
 int g4v_model_create(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   if (!c) return G4V_E_ARG;
-  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && I <= 6144 && ctxcap > 8,
-         "model_create: need I % 256 == 0, I <= 6144");
+  ARGCHK(V > 0 && NL > 0 && NL <= 64 && I > 0 && I % 256 == 0 && (I <= 6144 || I == 12288) && ctxcap > 8,
+         "model_create: need I % 256 == 0, I <= 6144 or I = 12288");
   HIPCHK(hipSetDevice(c->device));
   int r = model_alloc(c, V, NL, I, ctxcap);
   if (r) return r;
@@ -1514,7 +1514,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     ad.xs = c->act.as<float4>();  // group sums formed in LDS from the staged copy
     ad.K = I;
     ad.M = M;
-    launch_gemv_t(ad, st, c->gcfg[3][0], c->gcfg[3][1]);
+    launch_gemv_t(ad, st, I > 6144 ? 1 : c->gcfg[3][0], c->gcfg[3][1]);  // (K 12288: one row per block)
     pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
     if (l + 1 == NL) {  // the last MLP residual block and the final norm (E:1414-1417) for the head
       pmark(c, PT_ROWS, 1, 0);
