@@ -178,6 +178,9 @@ struct g4v_ctx {
   std::vector<long long> warmed;  // shapes run once eagerly (first call) before capture
   bool use_graph = true;
   bool pf_i8 = true;  // G_I8 (ENGINE_PREFILL_INT8=1): prefill blocks of two rows or more run W4A8
+  // ENGINE_DECODE_INT8 (E:1600): with pf_i8, the decode keeps G_I8_ACTIVE, so verify passes of
+  // two rows or more run W4A8 too (Gemma layout)
+  bool dec_i8 = false;
   // row-tile GEMV shape of the verify pass's q/k/v, o, gate/up and down products: activation
   // rows per block and rows per tile (G4V_GEMV_CFG="a,b a,b a,b a,b" overrides, for tuning)
   int gcfg[4][2] = {{2, 64}, {1, 64}, {4, 64}, {1, 64}};
@@ -1572,6 +1575,8 @@ static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, in
   // E:1328-1349), or a tree of two branches of up to 4 drafts each
   ARGCHK(toks && out && na >= 0 && nb >= 0 && M <= MAXM && ((nb == 0 && na <= 7) || (na <= 4 && nb <= 4)),
          "verify_step: a chain of 0 <= na <= 7 drafts, or 0 <= na, nb <= 4");
+  ARGCHK(!(c->dec_i8 && c->pf_i8) || M == 1,
+         "verify_step: W4A8 verify passes (g4v_set_decode_int8) are built for the Gemma layout only");
   ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
   ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");
@@ -2365,7 +2370,10 @@ static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int 
   HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, st));
   HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks, (size_t)M * 4, hipMemcpyHostToDevice, st));
   const int sib = nb == 1 ? na + 1 : -1;
-  gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>());
+  if (c->dec_i8 && c->pf_i8 && M >= 2)  // G_I8_ACTIVE in the decode (E:1600), lin_multi's M >= 2 (E:311)
+    gm_forward(c, M, pos0, nsplit, sib, 0, true, c->h.as<float>(), c->hn.as<float>());
+  else
+    gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>());
   const StepDev* sp = c->stepd.as<StepDev>();
   VerifyResultDev* res = c->resd.as<VerifyResultDev>();
   head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);  // E:1453-1488
@@ -3000,6 +3008,12 @@ int g4v_history_read(g4v_ctx* c, int* toks, int cap, int* L) {
 int g4v_set_prefill_int8(g4v_ctx* c, int on) {
   if (!c) return G4V_E_ARG;
   c->pf_i8 = on != 0;
+  return 0;
+}
+
+int g4v_set_decode_int8(g4v_ctx* c, int on) {
+  if (!c) return G4V_E_ARG;
+  c->dec_i8 = on != 0;
   return 0;
 }
 

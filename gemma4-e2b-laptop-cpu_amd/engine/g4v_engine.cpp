@@ -513,8 +513,8 @@ int main(int argc, char** argv) {
     e.draft_same = !(getenv("ENGINE_DRAFT_SAME") && atoi(getenv("ENGINE_DRAFT_SAME")) == 0);  // E:1532
   }
   // E:1210 G_I8 and E:1600 DEC_I8: the prompt's linear layers run W4A8 when ENGINE_PREFILL_INT8=1,
-  // and then the decode's verify passes too unless ENGINE_DECODE_INT8=0; the library decodes in
-  // exact float only
+  // and then the decode's verify passes of two rows or more too unless ENGINE_DECODE_INT8=0
+  // (g4v_set_decode_int8; the library builds that mode for the Gemma layout)
   // settings whose reference paths this engine does not restate
   if (env_int("ENGINE_ATT_PAR", ATT_PAR) != ATT_PAR || env_int("ENGINE_FAKE_CTX", 0) != 0 ||
       env_int("ENGINE_SPLITKV", 1) == 0) {
@@ -524,11 +524,6 @@ int main(int argc, char** argv) {
   }
   const bool g_i8 = env_int("ENGINE_PREFILL_INT8", 0) == 1;
   const bool dec_i8 = !(getenv("ENGINE_DECODE_INT8") && atoi(getenv("ENGINE_DECODE_INT8")) == 0);
-  if (g_i8 && dec_i8) {
-    fprintf(stderr, "g4v_engine: ENGINE_PREFILL_INT8=1 decodes with W4A8 verify passes unless ENGINE_DECODE_INT8=0 "
-                    "(E:1600); this engine decodes in exact float: set ENGINE_DECODE_INT8=0\n");
-    return 2;
-  }
   check(g4v_create(0, &G), "create");
   check(g4v_set_prefill_int8(G, g_i8 ? 1 : 0), "set_prefill_int8");
   Checkpoint ck;
@@ -541,6 +536,14 @@ int main(int argc, char** argv) {
     e.V = V;
     NL = 0;
     while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
+  }
+  if (g_i8 && dec_i8) {
+    if (!gemma) {
+      fprintf(stderr, "g4v_engine: ENGINE_PREFILL_INT8=1 decodes with W4A8 verify passes unless ENGINE_DECODE_INT8=0 "
+                      "(E:1600); the library runs them for the Gemma layout only: set ENGINE_DECODE_INT8=0\n");
+      return 2;
+    }
+    check(g4v_set_decode_int8(G, 1), "set_decode_int8");
   }
   const char* dseed = getenv("ENGINE_DRAFTER_SEED");
   Checkpoint dk;

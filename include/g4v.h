@@ -176,6 +176,13 @@ int g4v_set_graphs(g4v_ctx* c, int on);
 /* E:1210 G_I8 (ENGINE_PREFILL_INT8=1, the default here): g4v_prefill multiplies blocks of two
  * rows or more W4A8 (lin_multi, E:311); 0: exact float throughout, the reference's default */
 int g4v_set_prefill_int8(g4v_ctx* c, int on);
+/* E:1600 DEC_I8 (ENGINE_DECODE_INT8, on by default in the reference when ENGINE_PREFILL_INT8=1):
+ * on = 1 with prefill int8 on keeps G_I8_ACTIVE in the decode, so verify passes of two rows or
+ * more (g4v_verify_step / g4v_verify_sibling) multiply W4A8 as lin_multi does (E:311) and take
+ * the engine's unfused structure of that mode (E:1268-1289, 1363-1388).  Off by default here
+ * (exact float decode).  Gemma layout only: the synthetic stack's verify_step refuses M >= 2
+ * rows while it is on. */
+int g4v_set_decode_int8(g4v_ctx* c, int on);
 
 /* ---- prefill: run_req's prompt loop (E:1594-1599) with ENGINE_PREFILL_INT8=1, i.e. fwd
  * (E:1256-1405) over blocks of pfb rows (ENGINE_PREFILL_BLOCK, 32 by default), W4A8 linear layers

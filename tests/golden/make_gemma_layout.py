@@ -13,7 +13,11 @@ ENGINE_DRAFTER_INDEX), three serve-mode sessions (ENGINE_SERVE=1, the three prom
 NNEW_D tokens each) in the drafting modes of DRAFT_MODES: per request the FIRST and GEN lines
 and the stderr line "RANK1 rounds= top1= top2_only= TREE attempts= hits=" (E:1673; the RANK1
 counts run over the session) are stored as first_<mode>, gens_<mode>, gen_lens_<mode>,
-rank1_<mode> [3][5].
+rank1_<mode> [3][5].  Mode k3_i8 is the server's environment (E:1600): W4A8 prompt blocks
+(ENGINE_PREFILL_INT8=1) and W4A8 verify passes of two rows or more (ENGINE_DECODE_INT8 on).
+
+`--modes m1,m2` runs only those drafting sessions and adds their arrays to the fixture already
+written (the checkpoint is rebuilt from the same seeds).
 
 Run from the repository root after `make -C oracle`:
     python tests/golden/make_gemma_layout.py
@@ -39,7 +43,8 @@ CPUS, NNEW, CTX = 6, 12, 1024
 NNEW_D = 24
 # name -> engine settings of a drafting session (SIB_GAP 1, the default, lets the sibling row in)
 DRAFT_MODES = {"k3": dict(ENGINE_K="3"), "tree": dict(ENGINE_K="2", ENGINE_TREE="1"),
-               "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5")}
+               "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5"),
+               "k3_i8": dict(ENGINE_K="3", ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="1")}
 
 
 def base_env():
@@ -73,12 +78,19 @@ def cases(orc):
 def main():
     if not os.path.exists(EXE):
         sys.exit("oracle/_ref/gemma4_engine is not built (make -C oracle with the reference sources)")
+    only = sys.argv[sys.argv.index("--modes") + 1].split(",") if "--modes" in sys.argv else None
     orc = Oracle()
     prompts = cases(orc)
     out = {}
+    path = os.path.join(HERE, "gemma_layout.npz")
+    if only:
+        with np.load(path) as f:
+            out = {k: f[k] for k in f.files}
+        if not np.array_equal(out["prompts"], np.concatenate(prompts)):
+            sys.exit("the fixture's prompts differ from cases(): regenerate it whole")
     with tempfile.TemporaryDirectory() as d:
         gl.write_checkpoint(orc, d)
-        for sfx, i8 in (("", False), ("_i8", True)):
+        for sfx, i8 in (("", False), ("_i8", True)) if not only else ():
             env = dict(base_env(), ENGINE_K="0")
             if i8:
                 env["ENGINE_PREFILL_INT8"] = "1"
@@ -107,6 +119,8 @@ def main():
         gl.write_drafter(orc, d, E)
         lines = "".join(f"{NNEW_D} {' '.join(map(str, p))}\n" for p in prompts)
         for mode, extra in DRAFT_MODES.items():
+            if only and mode not in only:
+                continue
             env = dict(base_env(), ENGINE_SERVE="1", ENGINE_DRAFTER_DIR=os.path.join(d, "drafter"),
                        ENGINE_DRAFTER_INDEX=os.path.join(d, "drafter_index.tsv"), **extra)
             r = subprocess.run([EXE, d, os.path.join(d, "index.tsv"), "-", "0"], input=lines, env=env,
@@ -127,11 +141,12 @@ def main():
             out["rank1_" + mode] = np.array(rank1, np.int64)
         raw = np.memmap(os.path.join(d, "model.safetensors"), np.uint8, "r")
         file_crc = crc(np.asarray(raw[:gl.V * gl.H * 2 + (64 << 20)]))
-    path = os.path.join(HERE, "gemma_layout.npz")
-    np.savez_compressed(path, cpus=np.array([CPUS]), nnew=np.array([NNEW]), ctx=np.array([CTX]),
-                        nnew_d=np.array([NNEW_D]),
-                        prompt_lens=np.array([len(p) for p in prompts]), prompts=np.concatenate(prompts),
-                        crc_head=np.array([file_crc], np.uint32), **out)
+    if only and int(out["crc_head"][0]) != file_crc:
+        sys.exit("the checkpoint's CRC differs from the fixture's: regenerate it whole")
+    out.update(cpus=np.array([CPUS]), nnew=np.array([NNEW]), ctx=np.array([CTX]), nnew_d=np.array([NNEW_D]),
+               prompt_lens=np.array([len(p) for p in prompts]), prompts=np.concatenate(prompts),
+               crc_head=np.array([file_crc], np.uint32))
+    np.savez_compressed(path, **out)
     print(f"gemma_layout.npz: {os.path.getsize(path)} bytes", flush=True)
 
 

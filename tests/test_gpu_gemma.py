@@ -8,7 +8,10 @@ synthetic checkpoint of tests/golden/gemma_layout.py uploaded through the C ABI.
     (ENGINE_PREFILL_INT8=1, g4v_set_prefill_int8);
   * a prompt's final-normed state and every owner cache equal the oracle's (bit for bit), in
     both prefill modes;
-  * a chain pass of greedy drafts and the sibling form commit what the oracle's rows give."""
+  * a chain pass of greedy drafts and the sibling form commit what the oracle's rows give, in
+    exact float and with W4A8 verify passes (ENGINE_DECODE_INT8, g4v_set_decode_int8);
+  * g4v_engine's drafting sessions, the server's environment (W4A8 prompt and verify) among them,
+    print what the reference engine printed."""
 import os
 import subprocess
 import sys
@@ -137,16 +140,21 @@ def test_gemma_prefill_state_and_caches(orc, gemma, i8):
         go.close()
 
 
-@pytest.mark.parametrize("kind,pos0", [("chain", 210), ("chain", 40), ("sibling", 150), ("sibling", 240)])
-def test_gemma_multirow_passes(orc, gemma, kind, pos0):
+@pytest.mark.parametrize("kind,pos0,i8", [("chain", 210, False), ("chain", 40, False), ("sibling", 150, False),
+                                          ("sibling", 240, False), ("chain", 210, True), ("chain", 40, True),
+                                          ("sibling", 240, True)])
+def test_gemma_multirow_passes(orc, gemma, kind, pos0, i8):
     """a chain of 3 greedy drafts (split-KV past 192 keys, run_mh below) and the sibling form
     (nd 2 + the runner-up at RoPE position pos0 + 1, E:1634-1655) after a prefill, against the
-    oracle's rows: committed tokens and the committed row's state"""
+    oracle's rows: committed tokens and the committed row's state.  i8: ENGINE_PREFILL_INT8=1
+    with ENGINE_DECODE_INT8 on (E:1600), W4A8 prompt blocks and verify passes on both sides"""
     dev, d, fx, ctx = gemma
     prompt = [int(t) for t in np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])[2]][:pos0]
     while len(prompt) < pos0:
         prompt = prompt + prompt[:pos0 - len(prompt)]
-    go = gl.GemmaOracle(orc, d, ctx)
+    go = gl.GemmaOracle(orc, d, ctx, i8=i8)
+    dev.set_prefill_int8(i8)
+    dev.set_decode_int8(i8)
     try:
         for b in range(0, pos0, 32):
             blk = prompt[b:b + 32]
@@ -186,6 +194,8 @@ def test_gemma_multirow_passes(orc, gemma, kind, pos0):
                     b = go.cache(l, v)[(pos0 + 3) * hdl:(pos0 + 4) * hdl]
                     assert same(a, b), (nm, l)
     finally:
+        dev.set_prefill_int8(False)
+        dev.set_decode_int8(False)
         go.close()
 
 
@@ -274,8 +284,10 @@ def test_gemma_drafter_chain(orc, gemma, P):
 
 
 # the drafting sessions of tests/golden/make_gemma_layout.py
+# k3_i8: the server's environment, W4A8 prompt blocks and verify passes (E:1600)
 DRAFT_MODES = {"k3": dict(ENGINE_K="3"), "tree": dict(ENGINE_K="2", ENGINE_TREE="1"),
-               "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5")}
+               "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5"),
+               "k3_i8": dict(ENGINE_K="3", ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="1")}
 
 
 @pytest.mark.parametrize("mode", list(DRAFT_MODES))
