@@ -260,7 +260,8 @@ GM_CTX = 2048
 def gemma_layout_summary(g4v, reps=10):
     """verify passes on the Gemma-4-E2B layer layout at the checkpoint's sizes (device-generated
     weights): a 2048-token context prefilled with W4A8 blocks, then one-row decode passes and
-    chain passes of 3 and 7 drafts at position 2048 (the passes re-run at the same position)"""
+    chain passes of 3 and 7 drafts at position 2048 (the passes re-run at the same position), in
+    exact float and, for the chains, with W4A8 products (ENGINE_DECODE_INT8, the server's mode)"""
     dev = g4v.Device(0)
     dev.model_synth_gemma(SEED + 7, V, GM_MLP, 4096)
     dev.set_prefill_int8(True)
@@ -274,7 +275,8 @@ def gemma_layout_summary(g4v, reps=10):
     out = {"workload": f"Gemma-4-E2B layout (35 layers, head dim 256 / 512, KV shared past layer 14, MLP 6144 / "
                        f"12288, per-layer inputs, V {V}), context {GM_CTX}, 6 KV splits",
            "prefill_ms": round((time.perf_counter() - t0) * 1e3, 2)}
-    for M in (1, 4, 8):
+    for M, i8 in ((1, False), (4, False), (8, False), (4, True), (8, True)):
+        dev.set_decode_int8(i8)
         blk = rng.integers(0, V, M).astype(np.int32)
         for _ in range(2):
             dev.verify(blk, M - 1, 0, GM_CTX, 6)
@@ -283,7 +285,8 @@ def gemma_layout_summary(g4v, reps=10):
         for _ in range(reps):
             dev.verify(blk, M - 1, 0, GM_CTX, 6)
         dev.sync()
-        out[f"verify_{M}_rows_ms"] = round((time.perf_counter() - t0) * 1e3 / reps, 3)
+        out[f"verify_{M}_rows{'_w4a8' if i8 else ''}_ms"] = round((time.perf_counter() - t0) * 1e3 / reps, 3)
+    dev.set_decode_int8(False)
     dev.close()
     return out
 
