@@ -331,6 +331,72 @@ __global__ __launch_bounds__(256) void k_w4a8_gemm_lds(const uint4* __restrict__
 }
 
 // y [M][ldy] from the quantised rows; Mpad = M rounded up to 16 MT for the chosen MT
+// Decode rows (M <= 8, Mpad 16): one block per 16-column tile t.  The tile's K walk is split by
+// phases of DEC_PG groups: the four waves compute the phase's group dots (exact integers, the
+// same MFMA and operands as k_w4a8_gemm<1>) and the factors sc = sw * sx, and store them for
+// rows 0..7 in LDS; after a barrier lane (m, r) of the first 128 threads continues its chain
+// row = fma(a32, sc, row) over the phase's groups in group order (A8:59).  Every value and every
+// rounding is the one k_w4a8_gemm<1> computes; the group dots of a phase run on four waves at
+// once instead of one after another.  K % 256 == 0 (whole chunks of 4 groups, scale blocks of 8).
+constexpr int DEC_PG = 64;
+__global__ __launch_bounds__(256) void k_w4a8_dec(const uint4* __restrict__ tw, const uint4* __restrict__ ts,
+                                                  const uint16_t* __restrict__ xqb, const float* __restrict__ sxt,
+                                                  const float* __restrict__ corr, float* __restrict__ y, int M,
+                                                  int Mpad, int N, int K, int ldy) {
+  __shared__ float2 S[DEC_PG][32][4];  // [group in phase][lane of rows 0..7][D register]: (a32, sc)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int t = blockIdx.x;  // gridDim.x == N / 16
+  const int r = lane & 15, h = lane >> 4;
+  const int G = K / 32;
+  const uint4* wp = tw + (size_t)t * (G / 4) * 64 + lane;  // chunk c at + 64 c
+  const uint4* sp = ts + (size_t)t * (G / 8) * 16 + r;     // scales of groups 8 c8 .. at + 16 c8
+  const uint16_t* ap = xqb + (size_t)r * K + 8 * h;         // group g at + 32 g
+  const int mrow = 4 * h;
+  const int cm = tid >> 4, cr = tid & 15;                   // chain lane: row cm, column cr
+  const int cl = ((cm >> 2) << 4) | cr, ci = cm & 3;
+  float acc = 0.f;
+  for (int p = 0; p < G; p += DEC_PG) {
+    const int nc = min(DEC_PG, G - p) / 4;  // chunks in this phase
+    for (int q = w; q < nc; q += 4) {
+      const int c = p / 4 + q;
+      const uint4 wcur = wp[(size_t)c * 64];
+      const uint4 scur = sp[(size_t)(c >> 1) * 16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int g = 4 * c + i;
+        const uint32_t d = i == 0 ? wcur.x : (i == 1 ? wcur.y : (i == 2 ? wcur.z : wcur.w));
+        const bf16x8_t B = a8_decode(d);
+        const int gi = 4 * (c & 1) + i;
+        const uint32_t s2 = gi < 2 ? scur.x : (gi < 4 ? scur.y : (gi < 6 ? scur.z : scur.w));
+        const float sw = as_f32((gi & 1) ? (s2 & 0xFFFF0000u) : (s2 << 16));
+        const uint4 av = *reinterpret_cast<const uint4*>(ap + 32 * (size_t)g);
+        const float4 crv = *reinterpret_cast<const float4*>(corr + (size_t)g * Mpad + mrow);
+        const float4 sx = *reinterpret_cast<const float4*>(sxt + (size_t)g * Mpad + mrow);
+        const f32x4_t cin = {crv.x, crv.y, crv.z, crv.w};
+        const f32x4_t a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), B, cin, 0, 0, 0);
+        if (h < 2) {
+          float2* o = S[g - p][lane];
+          o[0] = make_float2(a[0], sw * sx.x);
+          o[1] = make_float2(a[1], sw * sx.y);
+          o[2] = make_float2(a[2], sw * sx.z);
+          o[3] = make_float2(a[3], sw * sx.w);
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < 128) {
+      const int ng = nc * 4;
+#pragma unroll 8
+      for (int j = 0; j < ng; ++j) {
+        const float2 v = S[j][cl][ci];
+        acc = fmaf(v.x, v.y, acc);
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < 128 && cm < M) y[(size_t)cm * ldy + 16 * t + cr] = acc;
+}
+
 int w4a8_mt(int M) { return M <= 16 ? 1 : (M <= 64 ? 2 : 4); }
 int w4a8_mpad(int M) {
   const int bm = 16 * w4a8_mt(M);
@@ -340,6 +406,10 @@ int w4a8_mpad(int M) {
 void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, const float* sxt, const float* corr,
                       float* y, int M, int N, int K, int ldy, hipStream_t st) {
   const int MT = w4a8_mt(M), Mpad = w4a8_mpad(M);
+  if (M <= 8 && N % 16 == 0 && K % 256 == 0) {  // decode rows: group dots split over the block's waves
+    hipLaunchKernelGGL(k_w4a8_dec, dim3(N / 16), dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
+    return;
+  }
   if (MT == 4 && (N / 16) % 2 == 0 && K % 128 == 0) {  // long M: 4 x 2 tiles per wave, staged rows
     const dim3 grid((N / 16 / 2 + 3) / 4, Mpad / 64);
     hipLaunchKernelGGL(k_w4a8_gemm_lds<2>, grid, dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);

@@ -38,7 +38,10 @@ def test_w4a8_golden(orc, dev, i):
 
 # (M, N, K): decode rows 1..8 on the verify shapes, then prefill row blocks
 A8_CASES = [(1, 1536, 1536), (2, 6144, 1536), (4, 1536, 6144), (8, 12288, 1536), (3, 256, 2048),
-            (7, 2048, 1536), (17, 1536, 1536), (64, 2048, 1536), (200, 1536, 2048)]
+            (7, 2048, 1536), (17, 1536, 1536), (64, 2048, 1536), (200, 1536, 2048),
+            # decode kernel: a full and a partial phase of 64 groups, six phases at M = 8; and
+            # the 16-row tile kernel at M = 12
+            (5, 512, 2560), (8, 256, 12288), (12, 512, 2560)]
 
 
 @pytest.mark.parametrize("M,N,K", A8_CASES)
