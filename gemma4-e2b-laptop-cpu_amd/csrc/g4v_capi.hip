@@ -1694,6 +1694,24 @@ static void pf_lin(g4v_ctx* c, const Mat& m, const float* x, int M, float* y, bo
 // up to three products of the same input (same K) in one launch per MAXM rows: q / k / v, gate / up
 static void pf_lin_multi(g4v_ctx* c, int n, const Mat* const* m, const float* x, int M, float* const* y, bool i8) {
   if (i8) {
+    bool n16 = true;
+    for (int j = 0; j < n; ++j) n16 = n16 && m[j]->N % 16 == 0;
+    if (M <= 8 && n16) {  // decode rows: the n products in one launch (i8_task over nj matrices, E:303-309)
+      launch_w4a8_quant(x, M, w4a8_mpad(M), m[0]->K, c->pfxq.as<uint16_t>(), c->pfsx.as<float>(),
+                        c->pfcorr.as<float>(), nullptr, nullptr, nullptr, c->st);
+      A8Dec d{};
+      for (int j = 0; j < n; ++j) {
+        d.tw[j] = m[j]->a8w.as<uint4>();
+        d.ts[j] = m[j]->a8s.as<uint4>();
+        d.y[j] = y[j];
+        d.ldy[j] = m[j]->N;
+        d.t0[j + 1] = d.t0[j] + m[j]->N / 16;
+      }
+      for (int j = n + 1; j < 4; ++j) d.t0[j] = d.t0[n];
+      if (launch_w4a8_dec(d, n, c->pfxq.as<uint16_t>(), c->pfsx.as<float>(), c->pfcorr.as<float>(), M, m[0]->K,
+                          c->st))
+        return;
+    }
     for (int j = 0; j < n; ++j) pf_lin(c, *m[j], x, M, y[j], true, j == 0);
     return;
   }

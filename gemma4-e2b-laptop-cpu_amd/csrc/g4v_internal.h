@@ -144,6 +144,17 @@ void launch_tile_a8(const uint8_t* w, const uint16_t* s, uint4* tw, uint4* ts, i
 // (optional, plain layouts [M][K], [M][K/32]) for the quant entry point
 void launch_w4a8_quant(const float* x, int M, int Mpad, int K, uint16_t* xqb, float* sxt, float* corr, int8_t* qo,
                        float* sxo, int32_t* sumo, hipStream_t st);
+// W4A8 products of decode rows (M <= 8) over up to three matrices of one input (N_j % 16 == 0):
+// matrix j's tiles are blocks t0[j] .. t0[j + 1] - 1; t0[j] = t0[n] for j >= n.
+struct A8Dec {
+  const uint4* tw[3];
+  const uint4* ts[3];
+  float* y[3];
+  int ldy[3];
+  int t0[4];
+};
+int launch_w4a8_dec(const A8Dec& m, int n, const uint16_t* xqb, const float* sxt, const float* corr, int M, int K,
+                    hipStream_t st);
 void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, const float* sxt, const float* corr,
                       float* y, int M, int N, int K, int ldy, hipStream_t st);
 int w4a8_mpad(int M);  // rows the quantised operand holds for M rows

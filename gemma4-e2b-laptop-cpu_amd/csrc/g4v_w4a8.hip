@@ -338,14 +338,21 @@ __global__ __launch_bounds__(256) void k_w4a8_gemm_lds(const uint4* __restrict__
 // row = fma(a32, sc, row) over the phase's groups in group order (A8:59).  Every value and every
 // rounding is the one k_w4a8_gemm<1> computes; the group dots of a phase run on four waves at
 // once instead of one after another.  K % 256 == 0 (whole chunks of 4 groups, scale blocks of 8).
+// Up to three matrices of the same input in one launch (i8_task over nj matrices, E:303-309):
+// block b runs tile b - t0[j] of matrix j, t0[j] <= b < t0[j + 1], t0[j + 1] - t0[j] = N_j / 16.
 constexpr int DEC_PG = 64;
-__global__ __launch_bounds__(256) void k_w4a8_dec(const uint4* __restrict__ tw, const uint4* __restrict__ ts,
-                                                  const uint16_t* __restrict__ xqb, const float* __restrict__ sxt,
-                                                  const float* __restrict__ corr, float* __restrict__ y, int M,
-                                                  int Mpad, int N, int K, int ldy) {
+__global__ __launch_bounds__(256) void k_w4a8_dec(A8Dec m, const uint16_t* __restrict__ xqb,
+                                                  const float* __restrict__ sxt, const float* __restrict__ corr,
+                                                  int M, int Mpad, int K) {
   __shared__ float2 S[DEC_PG][32][4];  // [group in phase][lane of rows 0..7][D register]: (a32, sc)
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int t = blockIdx.x;  // gridDim.x == N / 16
+  const int b = blockIdx.x;  // gridDim.x == t0[n]
+  const int j = b < m.t0[1] ? 0 : (b < m.t0[2] ? 1 : 2);
+  const int t = b - m.t0[j];
+  const uint4* __restrict__ tw = m.tw[j];
+  const uint4* __restrict__ ts = m.ts[j];
+  float* __restrict__ y = m.y[j];
+  const int ldy = m.ldy[j];
   const int r = lane & 15, h = lane >> 4;
   const int G = K / 32;
   const uint4* wp = tw + (size_t)t * (G / 4) * 64 + lane;  // chunk c at + 64 c
@@ -407,7 +414,13 @@ void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, con
                       float* y, int M, int N, int K, int ldy, hipStream_t st) {
   const int MT = w4a8_mt(M), Mpad = w4a8_mpad(M);
   if (M <= 8 && N % 16 == 0 && K % 256 == 0) {  // decode rows: group dots split over the block's waves
-    hipLaunchKernelGGL(k_w4a8_dec, dim3(N / 16), dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
+    A8Dec m{};
+    m.tw[0] = tw;
+    m.ts[0] = ts;
+    m.y[0] = y;
+    m.ldy[0] = ldy;
+    m.t0[1] = m.t0[2] = m.t0[3] = N / 16;
+    hipLaunchKernelGGL(k_w4a8_dec, dim3(N / 16), dim3(256), 0, st, m, xqb, sxt, corr, M, Mpad, K);
     return;
   }
   if (MT == 4 && (N / 16) % 2 == 0 && K % 128 == 0) {  // long M: 4 x 2 tiles per wave, staged rows
@@ -427,6 +440,13 @@ void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, con
       hipLaunchKernelGGL(k_w4a8_gemm<4>, grid, dim3(256), 0, st, tw, ts, xqb, sxt, corr, y, M, Mpad, N, K, ldy);
       break;
   }
+}
+
+int launch_w4a8_dec(const A8Dec& m, int n, const uint16_t* xqb, const float* sxt, const float* corr, int M, int K,
+                    hipStream_t st) {
+  if (n < 1 || n > 3 || M < 1 || M > 8 || K % 256) return 0;
+  hipLaunchKernelGGL(k_w4a8_dec, dim3(m.t0[n]), dim3(256), 0, st, m, xqb, sxt, corr, M, w4a8_mpad(M), K);
+  return 1;
 }
 
 }  // namespace g4v
