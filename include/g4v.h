@@ -4,7 +4,8 @@
  * Every entry point replaces a kernel-call surface of the reference engine (citations
  * are reference file:line, E = engine/gemma4_engine.cpp).  Plain pointers and sizes only;
  * the library owns all device memory.  Host pointers are used for small inputs/outputs;
- * results are bit-identical to the reference's exact-float path (ENGINE_DECODE_INT8=0).
+ * results are bit-identical to the reference's exact-float path (ENGINE_DECODE_INT8=0) and,
+ * with g4v_set_prefill_int8 / g4v_set_decode_int8, to its W4A8 prefill and decode (E:1210, 1600).
  *
  * Errors: every function returns 0 on success, a negative G4V_E* code otherwise, and never
  * exits the process; g4v_error() describes the last failure of a context.
