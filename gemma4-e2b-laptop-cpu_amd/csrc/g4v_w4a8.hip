@@ -332,16 +332,16 @@ __global__ __launch_bounds__(256) void k_w4a8_gemm_lds(const uint4* __restrict__
 
 // y [M][ldy] from the quantised rows; Mpad = M rounded up to 16 MT for the chosen MT
 // Decode rows (M <= 8, Mpad 16): one block per 16-column tile t.  The tile's K walk is split by
-// phases of DEC_PG groups: the eight waves compute the phase's group dots (exact integers, the
+// phases of DEC_PG groups: the sixteen waves compute the phase's group dots (exact integers, the
 // same MFMA and operands as k_w4a8_gemm<1>) and the factors sc = sw * sx, and store them for
 // rows 0..7 in LDS; after a barrier lane (m, r) of the first 128 threads continues its chain
 // row = fma(a32, sc, row) over the phase's groups in group order (A8:59).  Every value and every
-// rounding is the one k_w4a8_gemm<1> computes; the group dots of a phase run on eight waves at
+// rounding is the one k_w4a8_gemm<1> computes; the group dots of a phase run on sixteen waves at
 // once instead of one after another.  K % 256 == 0 (whole chunks of 4 groups, scale blocks of 8).
 // Up to three matrices of the same input in one launch (i8_task over nj matrices, E:303-309):
 // block b runs tile b - t0[j] of matrix j, t0[j] <= b < t0[j + 1], t0[j + 1] - t0[j] = N_j / 16.
 constexpr int DEC_PG = 64;
-__global__ __launch_bounds__(512) void k_w4a8_dec(A8Dec m, const uint16_t* __restrict__ xqb,
+__global__ __launch_bounds__(1024) void k_w4a8_dec(A8Dec m, const uint16_t* __restrict__ xqb,
                                                   const float* __restrict__ sxt, const float* __restrict__ corr,
                                                   int M, int Mpad, int K) {
   __shared__ float2 S[DEC_PG][32][4];  // [group in phase][lane of rows 0..7][D register]: (a32, sc)
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(512) void k_w4a8_dec(A8Dec m, const uint16_t* __res
   float acc = 0.f;
   for (int p = 0; p < G; p += DEC_PG) {
     const int nc = min(DEC_PG, G - p) / 4;  // chunks in this phase
-    for (int q = w; q < nc; q += 8) {
+    for (int q = w; q < nc; q += 16) {
       const int c = p / 4 + q;
       const uint4 wcur = wp[(size_t)c * 64];
       const uint4 scur = sp[(size_t)(c >> 1) * 16];
@@ -420,7 +420,7 @@ void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, con
     m.y[0] = y;
     m.ldy[0] = ldy;
     m.t0[1] = m.t0[2] = m.t0[3] = N / 16;
-    hipLaunchKernelGGL(k_w4a8_dec, dim3(N / 16), dim3(512), 0, st, m, xqb, sxt, corr, M, Mpad, K);
+    hipLaunchKernelGGL(k_w4a8_dec, dim3(N / 16), dim3(1024), 0, st, m, xqb, sxt, corr, M, Mpad, K);
     return;
   }
   if (MT == 4 && (N / 16) % 2 == 0 && K % 128 == 0) {  // long M: 4 x 2 tiles per wave, staged rows
@@ -445,7 +445,7 @@ void launch_w4a8_gemm(const uint4* tw, const uint4* ts, const uint16_t* xqb, con
 int launch_w4a8_dec(const A8Dec& m, int n, const uint16_t* xqb, const float* sxt, const float* corr, int M, int K,
                     hipStream_t st) {
   if (n < 1 || n > 3 || M < 1 || M > 8 || K % 256) return 0;
-  hipLaunchKernelGGL(k_w4a8_dec, dim3(m.t0[n]), dim3(512), 0, st, m, xqb, sxt, corr, M, w4a8_mpad(M), K);
+  hipLaunchKernelGGL(k_w4a8_dec, dim3(m.t0[n]), dim3(1024), 0, st, m, xqb, sxt, corr, M, w4a8_mpad(M), K);
   return 1;
 }
 
