@@ -7,9 +7,10 @@
 //   w_p = exp8(score_p - max), l = sum of w_p in position order, o_i = fma chain over p;
 //   merge: sc_t = libm expf(max_t - M0), l = sum_t (double) l_t sc_t,
 //          out = r16((fma chain over splits of o_t sc_t) * (float)(1 / l)).
-// One block serves (split t, row m, ATT_HB heads): the block's K/V rows are staged through LDS
-// tile by tile (the next tile is fetched into registers while the current one is used) and
-// shared by the block's heads.
+// Two kernels: k_attn_rows, the verify pass's attention (q/k norm, RoPE and the pass's cache rows
+// fused, partials merged by the o projection), and k_attn_split + k_attn_merge, the split-KV
+// attention of the standalone entry points on a geometry given by the caller.  Both visit a
+// split's value cache in whole blocks of 32 positions, fetched into registers ahead of use.
 #include "g4v_layer.h"
 
 namespace g4v {
@@ -39,96 +40,28 @@ struct AttnPtrs {
   const float* kraw;  // [M][HD]
   const float* vraw;  // [M][HD]
   const float* ropestep;  // the step's RoPE factors of the layer type: [MAXM][cos | sin][HD/2]
-  const float* qn;    // q_norm / k_norm weights [HD]
+  const float* qn;    // q_norm / k_norm weights [HD] (the verify pass: in the 16-lane head order)
   const float* kn;
   uint16_t* KCw;      // the layer's cache (same as KC / VC), written for the pass's rows
   uint16_t* VCw;
   const AttnGeom* gdev;  // raw attention: the geometry in device memory (replaces the argument)
 };
 
-// E:326-345 sum of squares of a 256-vector, 16 lanes x 16 steps in double, combined in the
-// reference's order; part[t] = lane t's sum (t < 16).  Returns 1 / sqrtf((float)(ss / n) + 1e-6).
-__device__ __forceinline__ float rms_inv16(const double* part) {
-  double a[4];
-#pragma unroll
-  for (int l = 0; l < 4; ++l) a[l] = (part[l] + part[4 + l]) + (part[8 + l] + part[12 + l]);
-  const double ss = (a[0] + a[2]) + (a[1] + a[3]);
-  return 1.0f / sqrtf((float)(ss / HD) + 1e-6f);  // division by a power of two: exact scaling
-}
-
-// grid (T, M, NQ / ATT_HB)
-template <bool STEP>
-__global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom gin, const StepDev* sp, int sliding,
-                                                            int T) {
+// grid (T, M, NQ / ATT_HB); the geometry as the argument gin or in device memory (P.gdev)
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom gin, int T) {
   __shared__ float qs[ATT_HB][8][32];              // lane l's 32 query values: s0 chain then s1 chain
   __shared__ __align__(16) float sw[ATT_HB][ATT_SW];
   __shared__ float wmax[ATT_THREADS / 64][ATT_HB];
   __shared__ float smax[ATT_HB];
-  // verify pass: rows being normalised (the block's query heads, then the pass's k and v rows),
-  // their 16-lane partial sums of squares, and the pass's finished key rows (bf16, in the
-  // key cache's chain-lane order) and value rows (bf16, natural order)
-  __shared__ float nx[STEP ? ATT_HB + 2 * MAXM : 1][HD];
-  __shared__ double npart[STEP ? ATT_HB + 2 * MAXM : 1][16];
-  __shared__ float nrinv[STEP ? ATT_HB + 2 * MAXM : 1];
-  __shared__ __align__(16) uint16_t knew[STEP ? MAXM : 1][HD];
-  __shared__ __align__(16) uint16_t vnew[STEP ? MAXM : 1][HD];
   const int t = blockIdx.x, m = blockIdx.y, h0 = blockIdx.z * ATT_HB;
   const int e = threadIdx.x;  // element e: chain s = (e/8)%2, step tt = e/16, lane e%8
-  const int i2 = e & (HD / 2 - 1);
-  // Every load that does not depend on the step geometry is issued first, together with the
-  // geometry itself (one round trip): the query heads and, in a verify pass, their norm weights
-  // and RoPE factors.  The pass's raw key/value rows are the context's last positions: the last
-  // two splits load them (and their RoPE factors) up front, any other split only when the
-  // geometry puts some of them in it (a context shorter than T rows per split).
+  // the query heads first, together with the geometry (one round trip)
   float qv[ATT_HB];
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = P.q[(size_t)m * P.ldq + (h0 + hh) * HD + e];
-  float kv[2][MAXM] = {}, ck[MAXM] = {}, sk[MAXM] = {}, qw = 0.f, kw = 0.f, cq = 0.f, sq = 0.f;
-  auto load_rows = [&]() {
-#pragma unroll
-    for (int r = 0; r < MAXM; ++r) {
-      kv[0][r] = P.kraw[(size_t)r * HD + e];
-      kv[1][r] = P.vraw[(size_t)r * HD + e];
-      ck[r] = P.ropestep[(size_t)r * HD + i2];
-      sk[r] = P.ropestep[(size_t)r * HD + HD / 2 + i2];
-    }
-  };
-  if (STEP) {
-    qw = P.qn[e];
-    kw = P.kn[e];
-    cq = P.ropestep[(size_t)m * HD + i2];
-    sq = P.ropestep[(size_t)m * HD + HD / 2 + i2];
-    if (t >= T - 2) load_rows();
-  }
-  // E:1325-1326 geometry: every thread reads the (uniform) parameters itself, no serial set-up;
-  // all fields are read unconditionally so that they arrive together
-  int M, kmin, kmax, lo_m, pos_m, sl_m, sh_m, pos0 = 0;
-  if (STEP) {
-    int rp[MAXM];
-#pragma unroll
-    for (int r = 0; r < MAXM; ++r) rp[r] = sp->rope[r];
-    const int rpm = sp->rope[m];
-    M = sp->M;
-    pos0 = sp->pos0;
-    sl_m = sp->skip_lo[m];
-    sh_m = sp->skip_hi[m];
-    kmax = pos0 + M - 1;
-    kmin = kmax;
-#pragma unroll
-    for (int r = 0; r < MAXM; ++r)
-      if (r < M) kmin = min(kmin, sliding ? max(0, rp[r] - 511) : 0);
-    pos_m = pos0 + m;
-    lo_m = sliding ? max(0, rpm - 511) : 0;
-  } else {
-    const AttnGeom& G = P.gdev ? *P.gdev : gin;
-    M = G.M;
-    kmin = G.kmin;
-    kmax = G.kmax;
-    pos_m = G.pos[m];
-    lo_m = G.lo[m];
-    sl_m = G.skip_lo[m];
-    sh_m = G.skip_hi[m];
-  }
+  const AttnGeom& G = P.gdev ? *P.gdev : gin;
+  const int M = G.M, kmin = G.kmin, kmax = G.kmax, pos_m = G.pos[m], lo_m = G.lo[m], sl_m = G.skip_lo[m],
+            sh_m = G.skip_hi[m];
   if (m >= M) return;
   const int len = kmax - kmin + 1;
   // (t + 1) len < 2^31 for every launch: 32-bit division
@@ -176,69 +109,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 #pragma unroll
     for (int c = 0; c < 4; ++c) r[c] = src[c];
   };
-  // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1); they are the
-  // split's last positions
-  const int rn0 = STEP ? max(c0 - pos0, 0) : 0, rn1 = STEP ? min(c1 - pos0, M) : 0;
-  if (STEP && t < T - 2 && rn0 < rn1) load_rows();
-  __builtin_amdgcn_sched_barrier(0);  // keep the prologue loads ahead of the tile loads
-  // the key tiles now (also when the split is empty: no paths with fewer loads in flight); the
-  // value tiles once the pass's rows have arrived, so that they do not queue in front of them
 #pragma unroll
   for (int k = 0; k < ATT_RING; ++k) issue_k(k, kring[k]);
-  __builtin_amdgcn_sched_barrier(0);
-  if (STEP) {
-    // E:1307-1324 on the block's query heads and the pass's key/value rows of this split:
-    // x = r16((x * rms_inv) * w) (v: r16(x * rms_inv)), then NeoX rotation of q and k
-#pragma unroll
-    for (int hh = 0; hh < ATT_HB; ++hh) nx[hh][e] = qv[hh];
-#pragma unroll
-    for (int r = 0; r < MAXM; ++r)
-      if (r >= rn0 && r < rn1) {  // uniform
-        nx[ATT_HB + r][e] = kv[0][r];
-        nx[ATT_HB + MAXM + r][e] = kv[1][r];
-      }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < (ATT_HB + 2 * MAXM) * 16; idx += ATT_THREADS) {
-      const int row = idx >> 4, t16 = idx & 15;
-      const bool live = row < ATT_HB || ((row - ATT_HB) % MAXM >= rn0 && (row - ATT_HB) % MAXM < rn1);
-      double sacc = 0;
-      if (live) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const double d = (double)nx[row][16 * k + t16];
-          sacc = fma(d, d, sacc);
-        }
-      }
-      npart[row][t16] = sacc;
-    }
-    __syncthreads();
-    if (threadIdx.x < ATT_HB + 2 * MAXM) nrinv[threadIdx.x] = rms_inv16(npart[threadIdx.x]);  // once per row
-    __syncthreads();
-#pragma unroll
-    for (int hh = 0; hh < ATT_HB; ++hh) nx[hh][e] = r16((qv[hh] * nrinv[hh]) * qw);
-#pragma unroll
-    for (int r = 0; r < MAXM; ++r)
-      if (r >= rn0 && r < rn1) {  // uniform
-        nx[ATT_HB + r][e] = r16((kv[0][r] * nrinv[ATT_HB + r]) * kw);
-        vnew[r][e] = f2bf(r16(kv[1][r] * nrinv[ATT_HB + MAXM + r]));
-      }
-    __syncthreads();
-    // E:394-402 NeoX halves: out_i = fma(u, c, -(w s)) and out_{i+128} = fma(w, c, u s)
-    auto rot = [&](const float* y, float c, float sn) {
-      return e < HD / 2 ? fmaf(y[e], c, -(y[e + HD / 2] * sn)) : fmaf(y[e], c, y[e - HD / 2] * sn);
-    };
-#pragma unroll
-    for (int hh = 0; hh < ATT_HB; ++hh) qv[hh] = rot(nx[hh], cq, sq);
-#pragma unroll
-    for (int r = 0; r < MAXM; ++r)
-      if (r >= rn0 && r < rn1) knew[r][kc_slot(e)] = f2bf(rot(nx[ATT_HB + r], ck[r], sk[r]));
-    __syncthreads();
-    if (m == 0 && h0 == 0)  // one block per split writes the pass's rows that fall in it
-      for (int r = rn0; r < rn1; ++r) {
-        P.KCw[(size_t)(pos0 + r) * HD + e] = knew[r][e];  // the LDS row is already in cache order
-        P.VCw[vc_index(pos0 + r, e)] = vnew[r][e];
-      }
-  }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int k = 0; k < ATT_RING; ++k) issue_v(k, vring[k]);
@@ -266,12 +138,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     const int pb = pb0 + s * ATT_TILE, p = pb + ps;
     if (s < NT) {  // uniform; otherwise an empty entry
       uint4 kr[4] = {kring[k][0], kring[k][1], kring[k][2], kring[k][3]};
-      if (STEP && pb + ATT_TILE > pos0) {  // uniform: the tile may hold rows of the pass (in LDS)
-        const bool own = p >= pos0 && p < c1;
-        const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][l * 32]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) kr[c] = sel4(own, n4[c], kr[c]);
-      }
       float kf[32];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -334,7 +200,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 #pragma unroll
   for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = 0.f;
   // a tile every position of which is allowed and none a pass row needs no masks
-  const int fa = max(lo_m, c0), fz = min(min(pos_m, c1 - 1), STEP ? pos0 - 1 : 0x7fffffff);
+  const int fa = max(lo_m, c0), fz = min(pos_m, c1 - 1);
   auto full_tile = [=](int pb) {
     return pb >= fa && pb + ATT_TILE - 1 <= fz && (sl_m > sh_m || pb > sh_m || pb + ATT_TILE - 1 < sl_m);
   };
@@ -349,7 +215,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
                                vring[k][2].x, vring[k][2].y, vring[k][2].z, vring[k][2].w,
                                vring[k][3].x, vring[k][3].y, vring[k][3].z, vring[k][3].w};
       const bool full = full_tile(pb);
-      const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb) & (STEP ? ~bits_in(pos0, pos0 + MAXM, pb) : 0xFFFFFFFFu);
+      const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb);
       // the tile's weights read up front (one LDS round trip per tile instead of one per 4
       // positions); wave w forms head w % ATT_HB's sum from its own copy (no per-head selects)
       float4 w4[ATT_HB][ATT_TILE / 4], wl[ATT_TILE / 4];
@@ -382,14 +248,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
       };
       if (full) sweep(false);
       else sweep(true);
-      if (STEP && pb + ATT_TILE > pos0) {  // uniform: the pass's rows in this tile, from LDS
-        const int pa = max(max(pb, pos0), c0), pz = min(pb + ATT_TILE, c1);
-        for (int pp = pa; pp < pz; ++pp) {
-          const float vv = as_f32((uint32_t)vnew[pp - pos0][i] << 16);
-#pragma unroll
-          for (int hh = 0; hh < ATT_HB; ++hh) o[hh] = fmaf(sw[hh][pp - pb0], vv, o[hh]);
-        }
-      }
     }
     // the slot's next entry (past the stream it reloads the last block): every path through
     // the loop issues the same loads, so the wait for a tile never has to cover younger ones
@@ -399,6 +257,402 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   for (int hh = 0; hh < ATT_HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];
   if ((threadIdx.x & 63) == 0 && wave < ATT_HB) {
     P.pm[((size_t)t * M + m) * NQ + h0 + wave] = smax[wave];
+    P.pl[((size_t)t * M + m) * NQ + h0 + wave] = (lo_m > pos_m) ? 0.0f : lsum;
+  }
+}
+
+// ---- the verify pass's attention: one block per (split t, row m, HB heads) ----
+//
+// A row of 16 lanes (lane n) holds a 256-vector as the 16 elements e = 16 tt + n, tt = 0..15.
+// That is at once the reference's sum-of-squares lane (ss_avx2 accumulator lane n, E:326-345),
+// its score chain (s0 lane n for n < 8, s1 lane n - 8 otherwise, E:763-776) and a pair of
+// RoPE halves (elements e and e + 128 are tt and tt + 8 of the same lane, E:394-402).  So the
+// q/k norm, the rotation and the score of a position each run inside one row, and the rows of
+// 16 lanes meet through data-parallel moves instead of LDS round trips and block barriers.  The
+// projection writes q, k and v in that order (head16_index), so a lane's 16 values are four
+// 16-byte words; the step's RoPE factors and the q/k norm weights are kept in the same order.
+constexpr int AR_THREADS = 256;  // 16 rows of 16 lanes; the value sweep: lane = dim
+constexpr int AR_KRING = 6;      // key positions in flight per row of lanes (a sliding-window split: all)
+constexpr int AR_HB = 2;         // heads per block: 224 blocks for a 7-row pass
+
+// lane n of a 16-lane row takes lane n + N of the row (row_shl:N; lanes past the row get 0)
+template <int N>
+__device__ __forceinline__ float shl_f(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return as_f32((uint32_t)__builtin_amdgcn_update_dpp(0, (int)as_u32(v), 0x100 + N, 0xF, 0xF, false));
+#else
+  return v;
+#endif
+}
+template <int N>
+__device__ __forceinline__ double shl_d(double v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint64_t u = as_u64(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x100 + N, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x100 + N, 0xF, 0xF, false);
+  return as_f64(((uint64_t)hi << 32) | lo);
+#else
+  return v;
+#endif
+}
+// lane 0 of each 16-lane row to the whole row (row_newbcast:0)
+__device__ __forceinline__ double bcast0_d(double v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint64_t u = as_u64(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x150, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x150, 0xF, 0xF, false);
+  return as_f64(((uint64_t)hi << 32) | lo);
+#else
+  return v;
+#endif
+}
+
+// E:326-345 1 / sqrtf((float)(ss / 256) + 1e-6) of the row's 256-vector: lane n's double chain
+// over tt is accumulator lane n; p_n meet as a_l = (p_l + p_{l+4}) + (p_{l+8} + p_{l+12}),
+// ss = (a_0 + a_2) + (a_1 + a_3).  Every lane of the row returns the factor.
+__device__ __forceinline__ float row_rms_inv(const float (&x)[16]) {
+  double s = 0;
+#pragma unroll
+  for (int tt = 0; tt < 16; ++tt) {
+    const double d = (double)x[tt];
+    s = fma(d, d, s);
+  }
+  const double b = s + shl_d<4>(s);  // lane n: p_n + p_{n+4}
+  const double c = b + shl_d<8>(b);  // lanes 0..3: a_l
+  const double d = c + shl_d<2>(c);  // lanes 0, 1: a_0 + a_2, a_1 + a_3
+  const double e = d + shl_d<1>(d);  // lane 0: ss
+  const double ss = bcast0_d(e);
+  return 1.0f / sqrtf((float)(ss / HD) + 1e-6f);  // division by a power of two: exact scaling
+}
+
+// W:41-44 / E:776 score = hsum8(s0 + s1) of the row's 16 chains (s0 lanes 0..7, s1 lanes 8..15):
+// v_j = s0_j + s1_j, then ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), in lane 0 of the row
+__device__ __forceinline__ float row_score(float acc) {
+  const float u = acc + shl_f<8>(acc);  // lanes 0..7: v_j
+  const float w = u + shl_f<4>(u);      // lanes 0..3: v_j + v_{j+4}
+  const float z = w + shl_f<1>(w);      // lanes 0, 2: (w0 + w1), (w2 + w3)
+  return z + shl_f<2>(z);               // lane 0
+}
+
+// E:1307-1324 on one row's 256-vector x held as above: q / k rows r16((x * rinv) * w) rotated
+// with the row's factors (cos c[tt], sin s[tt] of elements 16 tt + n, tt < 8)
+__device__ __forceinline__ void row_norm_rope(float (&x)[16], const float (&w)[16], const float (&cs)[16]) {
+  const float r = row_rms_inv(x);
+#pragma unroll
+  for (int tt = 0; tt < 16; ++tt) x[tt] = r16((x[tt] * r) * w[tt]);
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt) {
+    const float u = x[tt], v = x[tt + 8];
+    x[tt] = fmaf(u, cs[tt], -(v * cs[8 + tt]));
+    x[tt + 8] = fmaf(v, cs[tt], u * cs[8 + tt]);
+  }
+}
+
+// Range-checked 16-byte loads through a buffer resource: a lane whose offset lies past the
+// resource's num_records bytes reads zeros and moves no data (the key / value streams read
+// exactly their split, without clamped duplicate fetches).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  uint4 u;
+  __builtin_memcpy(&u, &v, 16);
+  return u;
+}
+
+// 16 floats of a lane: four 16-byte words at p
+__device__ __forceinline__ void load16(float (&x)[16], const float* p) {
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float4 v = p4[k];
+    x[4 * k] = v.x;
+    x[4 * k + 1] = v.y;
+    x[4 * k + 2] = v.z;
+    x[4 * k + 3] = v.w;
+  }
+}
+
+// grid (T, M, NQ / HB): the blocks of split t are t, t + 8, ... in launch order, i.e. all on one
+// XCD, whose L2 then fetches the split's key and value tiles once
+// The arguments the block needs first lead the list, ahead of the pointer block, so that they
+// arrive preloaded in scalar registers (kernel-argument preloading) rather than through a
+// dependent load of the argument segment.
+template <int HB>
+__global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restrict__ sp, const float* __restrict__ q,
+                                                          const float* __restrict__ ropestep,
+                                                          const float* __restrict__ qnp, const uint16_t* __restrict__ KC,
+                                                          const uint16_t* __restrict__ VC, int sliding, int T,
+                                                          AttnPtrs P) {
+  __shared__ __align__(16) float sw[HB][ATT_SW];     // scores, then weights, of the split's tiles
+  __shared__ float rmx[AR_THREADS / 16][HB];         // per row of lanes: max of its allowed scores
+  __shared__ __align__(16) uint16_t knew[MAXM][HD];  // the pass's key rows, bf16 in cache order
+  __shared__ __align__(16) uint16_t vnew[MAXM][HD];  // the pass's value rows, bf16 natural order
+  const int t = blockIdx.x, m = blockIdx.y, h0 = blockIdx.z * HB;
+  const int tid = threadIdx.x, rho = tid >> 4, n = tid & 15, ls = n & 7, ss = n >> 3;
+  // 1. loads that need no geometry first: the block's query heads, their norm weights and the
+  // row's RoPE factors, 16 values per lane (head16_index order)
+  // (the first row of lanes of each wave loads and forms them; the wave's other rows take
+  // copies in step 4: one fetch per wave instead of one per row)
+  // The other rows' offsets lie past the resources: they read zeros and move no data.
+  const uint32_t roff = (rho & 3) == 0 ? (uint32_t)n * 64 : 0x7FFFFFF0u;
+  float qx[HB][16], qw[16], cs[16];
+  auto load16b = [&](float (&x)[16], __amdgpu_buffer_rsrc_t r, uint32_t off) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 v = buf_load16(r, off + 16 * k);
+      x[4 * k] = as_f32(v.x);
+      x[4 * k + 1] = as_f32(v.y);
+      x[4 * k + 2] = as_f32(v.z);
+      x[4 * k + 3] = as_f32(v.w);
+    }
+  };
+  {
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(q + (size_t)m * (NQ * HD) + h0 * HD, HB * HD * 4);
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh) load16b(qx[hh], rq, roff + hh * HD * 4);
+    load16b(qw, buf_rsrc(qnp, HD * 4), roff);
+    load16b(cs, buf_rsrc(ropestep + (size_t)m * HD, HD * 4), roff);
+  }
+  // E:1325-1326 geometry from the step parameters (uniform)
+  int rp[MAXM];
+#pragma unroll
+  for (int r = 0; r < MAXM; ++r) rp[r] = sp->rope[r];
+  const int M = sp->M, pos0 = sp->pos0, sl_m = sp->skip_lo[m], sh_m = sp->skip_hi[m], rpm = sp->rope[m];
+  const int kmax = pos0 + M - 1;
+  int kmin = kmax;
+#pragma unroll
+  for (int r = 0; r < MAXM; ++r)
+    if (r < M) kmin = min(kmin, sliding ? max(0, rp[r] - 511) : 0);
+  const int pos_m = pos0 + m, lo_m = sliding ? max(0, rpm - 511) : 0;
+  if (m >= M) return;
+  const int len = kmax - kmin + 1;
+  // (t + 1) len < 2^31 for every launch: 32-bit division
+  const int c0 = kmin + (int)((unsigned)(t * len) / (unsigned)T),
+            c1 = kmin + (int)((unsigned)((t + 1) * len) / (unsigned)T);
+  const int PP = c1 - c0;
+  // E:740 attn_allowed for this block's row, restricted to the split
+  auto allowed = [=](int p) { return p >= c0 && p < c1 && p >= lo_m && p <= pos_m && !(p >= sl_m && p <= sh_m); };
+  auto bits_in = [](int a, int b, int pb) -> uint32_t {  // positions [a, b] within [pb, pb + 31]
+    const int lo = max(a - pb, 0), hi = min(b - pb, 31);
+    if (lo > hi) return 0u;
+    const uint32_t up = hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u);
+    return up & ~((1u << lo) - 1u);
+  };
+  auto tile_mask = [=](int pb) -> uint32_t {
+    return bits_in(max(lo_m, c0), min(pos_m, c1 - 1), pb) & ~bits_in(sl_m, sh_m, pb);
+  };
+  const int pb0 = c0 & ~(ATT_TILE - 1);
+  const int NT = PP > 0 ? ((c1 - 1) >> 5) - (c0 >> 5) + 1 : 0;
+  const int NTp = (NT + ATT_RING - 1) / ATT_RING * ATT_RING;
+  // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1): the split's last ones
+  const int rn0 = max(c0 - pos0, 0), rn1 = min(c1 - pos0, M);
+
+  // 2. the split's first value tiles (lane = dim) and key positions: row rho scores positions
+  // c0 + rho + 16 k; lane n's 16 key values (slots 32 ls + 16 ss + tt) are two 16-byte words.
+  // Keys from the cache stop before pos0 (the pass's rows come from LDS); entries past them
+  // reload a position in range, never used.
+  // value tiles: the split's NT blocks of 32 positions from pb0 (entries past them read zeros);
+  // lane i reads dim i of a tile, 64 bytes
+  uint4 vring[ATT_RING][4];
+  const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(VC + (size_t)(pb0 >> 5) * (ATT_TILE * HD), (uint32_t)NT * ATT_TILE * HD * 2);
+  auto issue_v = [&](int v, uint4 (&r)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = buf_load16(vrs, (uint32_t)v * (ATT_TILE * HD * 2) + tid * 64 + c * 16);
+  };
+  // key positions below gend = min(c1, pos0) from the cache (the pass's rows come from LDS;
+  // entries past gend read zeros, never used)
+  const int KN = (PP + 15) >> 4, KNp = (KN + AR_KRING - 1) / AR_KRING * AR_KRING;
+  const int gend = min(c1, pos0);
+  const __amdgpu_buffer_rsrc_t krs = buf_rsrc(KC, (uint32_t)max(gend, 0) * HD * 2);
+  uint4 kring[AR_KRING][2];
+  auto issue_k = [&](int k, uint4 (&r)[2]) {
+    const uint32_t off = (uint32_t)(c0 + rho + 16 * k) * (HD * 2) + (4 * ls + 2 * ss) * 16;
+    r[0] = buf_load16(krs, off);
+    r[1] = buf_load16(krs, off + 16);
+  };
+#pragma unroll
+  for (int k = 0; k < AR_KRING; ++k) issue_k(k, kring[k]);
+#pragma unroll
+  for (int k = 0; k < ATT_RING; ++k) issue_v(k, vring[k]);
+
+  // 3. E:1307-1324 the pass's key / value rows in this split (rows of lanes 0..7: key row rho,
+  // 8..15: value row rho - 8): k = rot(r16((k * rinv) * kn)), v = r16(v * rinv), bf16 into LDS;
+  // the block (m 0, h 0) of the split also writes them into the cache
+  if (rn0 < rn1) {  // uniform
+    const int pr = rho & 7;
+    const bool prow = pr >= rn0 && pr < rn1;  // uniform per row of lanes
+    float px[16];
+    if (rho < 8) {  // uniform per wave
+      float pw[16], pc[16];
+      load16(px, P.kraw + (size_t)pr * HD + 16 * n);
+      load16(pw, P.kn + 16 * n);
+      load16(pc, ropestep + (size_t)pr * HD + 16 * n);
+      row_norm_rope(px, pw, pc);
+      if (prow) {
+        uint32_t wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv[i] = (uint32_t)f2bf(px[2 * i]) | ((uint32_t)f2bf(px[2 * i + 1]) << 16);
+        uint4* dst = reinterpret_cast<uint4*>(&knew[pr][0]) + 4 * ls + 2 * ss;
+        dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+        dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+      }
+    } else {
+      load16(px, P.vraw + (size_t)pr * HD + 16 * n);
+      const float r = row_rms_inv(px);
+      if (prow) {
+#pragma unroll
+        for (int tt = 0; tt < 16; ++tt) vnew[pr][16 * tt + n] = f2bf(r16(px[tt] * r));
+      }
+    }
+    __syncthreads();
+    if (m == 0 && h0 == 0)
+      for (int r = rn0; r < rn1; ++r) {
+        P.KCw[(size_t)(pos0 + r) * HD + tid] = knew[r][tid];  // the LDS row is already in cache order
+        P.VCw[vc_index(pos0 + r, tid)] = vnew[r][tid];
+      }
+  }
+
+  // 4. the query heads, formed by the first row of lanes of each wave and copied to its others
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) row_norm_rope(qx[hh], qw, cs);
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+    for (int tt = 0; tt < 16; ++tt)
+      qx[hh][tt] = as_f32((uint32_t)__builtin_amdgcn_ds_bpermute(n * 4, (int)as_u32(qx[hh][tt])));
+
+  // 5. E:750-816 scores of positions c0 + rho + 16 k; lane 0 of the row stores them and keeps the
+  // running max over the allowed positions (max is order free)
+  float rowmax[HB];
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) rowmax[hh] = -1e30f;
+  for (int base = 0; base < KNp; base += AR_KRING)
+#pragma unroll
+    for (int k = 0; k < AR_KRING; ++k) {
+      const int kk = base + k;
+      if (kk < KN) {  // uniform
+        const int p = c0 + rho + 16 * kk;
+        uint4 ka = kring[k][0], kb = kring[k][1];
+        if (c0 + 16 * kk + 15 >= pos0) {  // uniform: the step may reach the pass's rows (in LDS)
+          const bool own = p >= pos0 && p < c1;
+          const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][0]) + 4 * ls + 2 * ss;
+          ka = sel4(own, n4[0], ka);
+          kb = sel4(own, n4[1], kb);
+        }
+        const uint32_t kw[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+        float acc[HB];
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh) acc[hh] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float k0 = as_f32(kw[i] << 16), k1 = as_f32(kw[i] & 0xFFFF0000u);
+#pragma unroll
+          for (int hh = 0; hh < HB; ++hh) {
+            acc[hh] = fmaf(qx[hh][2 * i], k0, acc[hh]);
+            acc[hh] = fmaf(qx[hh][2 * i + 1], k1, acc[hh]);
+          }
+        }
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh) {
+          const float sc = row_score(acc[hh]);
+          if (n == 0 && p < c1) {
+            sw[hh][p - pb0] = sc;
+            if (allowed(p) && rowmax[hh] < sc) rowmax[hh] = sc;
+          }
+        }
+      }
+      issue_k(base + k + AR_KRING, kring[k]);
+    }
+  if (n == 0)
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh) rmx[rho][hh] = rowmax[hh];
+  __syncthreads();
+  float mx[HB];
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) {
+    mx[hh] = -1e30f;
+#pragma unroll
+    for (int r = 0; r < AR_THREADS / 16; ++r) mx[hh] = (mx[hh] < rmx[r][hh]) ? rmx[r][hh] : mx[hh];
+  }
+  // weights exp8(score - max) (E:820); masked positions and the padding of the whole tiles get 0
+  for (int idx = tid; idx < HB * NT * ATT_TILE; idx += AR_THREADS) {
+    const int hh = idx / (NT * ATT_TILE), pp = idx - hh * (NT * ATT_TILE);
+    float mh = mx[0];
+#pragma unroll
+    for (int k = 1; k < HB; ++k) mh = hh == k ? mx[k] : mh;
+    sw[hh][pp] = allowed(pb0 + pp) ? exp8(sw[hh][pp] - mh) : 0.f;
+  }
+  __syncthreads();
+
+  // 6. E:826-875 o_i = fma chain over the positions in order, lane = dim i; a masked or padding
+  // position (weight 0) gets value +0: fma(0, 0, o) = o exactly (o is never -0).  The pass's rows
+  // follow from LDS after the tile's other positions (they are the split's last).  Wave w forms
+  // l = the sum of the weights of head w % HB in position order (E:821); waves w < HB store it.
+  const int i = tid, wave = tid >> 6;
+  float o[HB], lsum = 0.f;
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) o[hh] = 0.f;
+  const int fa = max(lo_m, c0), fz = min(min(pos_m, c1 - 1), pos0 - 1);
+  auto full_tile = [=](int pb) {
+    return pb >= fa && pb + ATT_TILE - 1 <= fz && (sl_m > sh_m || pb > sh_m || pb + ATT_TILE - 1 < sl_m);
+  };
+  for (int base = 0; base < NTp; base += ATT_RING)
+#pragma unroll
+    for (int k = 0; k < ATT_RING; ++k) {
+      const int s = base + k;
+      const int pb = pb0 + s * ATT_TILE;
+      if (s < NT) {  // uniform
+        const uint32_t vw[16] = {vring[k][0].x, vring[k][0].y, vring[k][0].z, vring[k][0].w,
+                                 vring[k][1].x, vring[k][1].y, vring[k][1].z, vring[k][1].w,
+                                 vring[k][2].x, vring[k][2].y, vring[k][2].z, vring[k][2].w,
+                                 vring[k][3].x, vring[k][3].y, vring[k][3].z, vring[k][3].w};
+        const bool full = full_tile(pb);
+        const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb) & ~bits_in(pos0, pos0 + MAXM, pb);
+        // the tile's weights one per lane: half g of the tile (16 positions) in lane n of every
+        // row; wl: those of head wave % HB for the sum l
+        float wr[2][HB], wl[2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+#pragma unroll
+          for (int hh = 0; hh < HB; ++hh) wr[g][hh] = sw[hh][pb - pb0 + 16 * g + n];
+          wl[g] = sw[wave % HB][pb - pb0 + 16 * g + n];
+        }
+        auto sweep = [&](const bool masked) {
+          auto half = [&](auto G) {
+            constexpr int g = decltype(G)::value;
+            auto pos = [&](auto Kc) {
+              constexpr int k = decltype(Kc)::value, pe = 16 * g + k;
+              uint32_t vb = __builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], (pe & 1) ? 0x03020c0cu : 0x01000c0cu);
+              if (masked) vb &= (uint32_t)((int)(keep << (31 - pe)) >> 31);
+              const float vv = as_f32(vb);
+              lsum = add_bc<k>(lsum, wl[g]);
+#pragma unroll
+              for (int hh = 0; hh < HB; ++hh) o[hh] = fmac_bc<k>(o[hh], wr[g][hh], vv);
+            };
+            unroll_n<16>(pos);
+          };
+          half(std::integral_constant<int, 0>{});
+          half(std::integral_constant<int, 1>{});
+        };
+        if (full) sweep(false);
+        else sweep(true);
+        if (pb + ATT_TILE > pos0) {  // uniform: the pass's rows in this tile, from LDS
+          const int pa = max(max(pb, pos0), c0), pz = min(pb + ATT_TILE, c1);
+          for (int pp = pa; pp < pz; ++pp) {
+            const float vv = as_f32((uint32_t)vnew[pp - pos0][i] << 16);
+#pragma unroll
+            for (int hh = 0; hh < HB; ++hh) o[hh] = fmaf(sw[hh][pp - pb0], vv, o[hh]);
+          }
+        }
+      }
+      issue_v(s + ATT_RING, vring[k]);
+    }
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];
+  if ((tid & 63) == 0 && wave < HB) {
+    P.pm[((size_t)t * M + m) * NQ + h0 + wave] = mx[wave % HB];
     P.pl[((size_t)t * M + m) * NQ + h0 + wave] = (lo_m > pos_m) ? 0.0f : lsum;
   }
 }
@@ -465,17 +719,16 @@ __global__ __launch_bounds__(HD) void k_attn_merge(AttnPtrs P, int M, int T) { m
 void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, const float* v, const LayerNorms& ln,
                  const float* ropestep, const StepDev* sp, int sliding, int T, float* po, float* pm, float* pl, int M,
                  hipStream_t st) {
-  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, nullptr, NQ * HD, nullptr, k, v, ropestep, ln.qn, ln.kn, KC, VC};
-  AttnGeom g{};
-  hipLaunchKernelGGL(k_attn_split<true>, dim3(T, M, NQ / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, sp, sliding, T);
+  AttnPtrs P{KC, VC, q, NQ * HD, po, pm, pl, nullptr, NQ * HD, nullptr, k, v, ropestep, ln.qnp, ln.knp, KC, VC};
+  hipLaunchKernelGGL(k_attn_rows<AR_HB>, dim3(T, M, NQ / AR_HB), dim3(AR_THREADS), 0, st, sp, q, ropestep, ln.qnp,
+                     (const uint16_t*)KC, (const uint16_t*)VC, sliding, T, P);
 }
 
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh, float* gs) {
   AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
              nullptr};
-  hipLaunchKernelGGL(k_attn_split<false>, dim3(g.T, g.M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
-                     (const StepDev*)nullptr, 0, g.T);
+  hipLaunchKernelGGL(k_attn_split, dim3(g.T, g.M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, g.T);
   hipLaunchKernelGGL(k_attn_merge, dim3(g.M, nh), dim3(HD), 0, st, P, g.M, g.T);
 }
 
@@ -486,8 +739,7 @@ void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q
   AttnGeom g{};
   g.M = M;
   g.T = T;
-  hipLaunchKernelGGL(k_attn_split<false>, dim3(T, M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g,
-                     (const StepDev*)nullptr, 0, T);
+  hipLaunchKernelGGL(k_attn_split, dim3(T, M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, T);
   hipLaunchKernelGGL(k_attn_merge, dim3(M, nh), dim3(HD), 0, st, P, M, T);
 }
 

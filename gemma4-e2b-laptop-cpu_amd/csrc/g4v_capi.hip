@@ -53,12 +53,21 @@ static bool row_tiled(int j) { return j <= 3 || j == 6; }
 
 struct Layer {
   Mat m[7];       // q, k, v, o, gate, up, down
-  DBuf norms;     // in_ln, post_attn, pre_ff, post_ff [H each], qn, kn [HD each]
+  DBuf norms;     // in_ln, post_attn, pre_ff, post_ff [H each], qn, kn [HD each], qn, kn in the
+                  // 16-lane head order [HD each] (head16_index; refreshed by perm_norms)
   float scalar = 0.75f;
   int sliding = 1;
   LayerNorms ln() const {
     const float* b = norms.as<float>();
-    return LayerNorms{b, b + H, b + 2 * H, b + 3 * H, b + 4 * H, b + 4 * H + HD, scalar, sliding};
+    return LayerNorms{b,           b + H, b + 2 * H, b + 3 * H, b + 4 * H, b + 4 * H + HD, b + 4 * H + 2 * HD,
+                      b + 4 * H + 3 * HD, scalar, sliding};
+  }
+  // the q / k norm weights' copies in the attention's 16-lane order, after a write of the norms
+  void perm_norms(hipStream_t st) const {
+    const float* b = norms.as<float>();
+    float* d = const_cast<float*>(b) + 4 * H + 2 * HD;
+    launch_perm16(b + 4 * H, d, st);
+    launch_perm16(b + 4 * H + HD, d + HD, st);
   }
 };
 
@@ -1024,7 +1033,7 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   c->L.clear();
   for (int l = 0; l < NL; ++l) {
     auto lay = std::make_unique<Layer>();
-    ALLOC(lay->norms, (size_t)(4 * H + 2 * HD) * 4);
+    ALLOC(lay->norms, (size_t)(4 * H + 4 * HD) * 4);
     HIPCHK(hipMemsetAsync(lay->norms.p, 0, lay->norms.n, st));
     lay->scalar = 1.0f;
     lay->sliding = (l % 5 != 4);
@@ -1139,6 +1148,7 @@ int g4v_model_synth(g4v_ctx* c, uint64_t seed, int V, int NL, int I, int ctxcap)
       for (int i = 0; i < n; ++i) nv[off + i] = r16(base + span * rng_unif(sn, i));
     }
     HIPCHK(hipMemcpyAsync(lay.norms.p, nv.data(), nv.size() * 4, hipMemcpyHostToDevice, st));
+    lay.perm_norms(st);
     HIPCHK(hipStreamSynchronize(st));  // nv is refilled for the next layer
     lay.scalar = 0.75f;
     lay.sliding = (l % 5 != 4);
@@ -1212,6 +1222,8 @@ int g4v_model_set_norms(g4v_ctx* c, int l, const float* const nv[6], float scala
     const int n = t < 4 ? H : HD, off = t < 4 ? t * H : 4 * H + (t - 4) * HD;
     HIPCHK(hipMemcpyAsync(lay.norms.as<float>() + off, nv[t], (size_t)n * 4, hipMemcpyHostToDevice, c->st));
   }
+  lay.perm_norms(c->st);
+  HIPCHK(hipGetLastError());
   HIPCHK(hipStreamSynchronize(c->st));
   if (lay.scalar != scalar || lay.sliding != (sliding != 0)) drop_graphs(c);  // both are baked into launches
   lay.scalar = scalar;
@@ -1442,6 +1454,7 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     a.ldy[2] = HD;
     a.K = H;
     a.M = M;
+    a.yperm = path == 0 ? 7 : 0;  // the split-KV attention reads q, k, v in the 16-lane head order
     if (l == 0) {  // from the embedding row kernel
       a.xs = c->xa.as<float4>();
       a.gs = c->xgs.as<float>();

@@ -102,37 +102,23 @@ static size_t gemvt_lds(int mpl, int K, bool nrm, int tr, bool mrg) {
 // KT: the reduction length when fixed at compile time (0: a.K), so that the LDS addresses of the
 // staged activations fold into instruction offsets
 // XM: the Gemma per-layer-input gate (GemvTArgs::epi_pli; NRM prologue in mode 3)
+// The arguments a block needs before its first loads lead the list (up to 16 dwords), so that
+// they arrive preloaded in scalar registers at launch (kernel-argument preloading) instead of
+// through a load of the argument segment: the prologue's four input pointers pa..pd (MRG: po, pm,
+// pl; NRM: o, xin, w1, w2; otherwise xs, gs), matrix 0's tiles, and the geometry packed in two
+// words -- gx = nsub | (MRG: T, NRM: nmode) << 8 | M << 16, tlp = tiles[1] | tiles[2] << 10 |
+// tiles[3] << 20 (14 dwords: all that the launch preloads).
+// The rest (matrices 1 and 2, the outputs, the epilogue's operands) comes from the argument
+// block d, read while the prologue's loads are in flight.
 template <int MPL, bool MRG, bool NRM, int TR, int KT = 0, int XM = 0>
-__global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
+__global__ __launch_bounds__(TR * 8) void k_gemv_t(const float* __restrict__ pa, const float* __restrict__ pb,
+                                                   const float* __restrict__ pc, const float* __restrict__ pd,
+                                                   const uint4* __restrict__ w0w, const uint4* __restrict__ w0s,
+                                                   int gx, int tlp, GemvTDev d) {
   constexpr int NT = TR * 8;
   const GemvTArgs& a = d.a;
-  // The launch's argument block is cold in the scalar cache: the arguments the block needs
-  // before its first vector loads are read into registers together, ahead of the first branch
-  // (one round trip; the compiler would otherwise fetch them in three dependent rounds, around
-  // the division and the early exit, and fetch the chosen matrix again by a computed address).
-  int nsub = d.nsub, tl1 = d.tiles[1], tl2 = d.tiles[2], tl3 = d.tiles[3], M = a.M, T = 0, nmode = 0;
-  const uint4 *w0w = a.mat[0].w, *w0s = a.mat[0].s, *w1w = a.mat[1].w, *w1s = a.mat[1].s, *w2w = a.mat[2].w,
-              *w2s = a.mat[2].s;
-  const float *pa = nullptr, *pb = nullptr, *pc = nullptr, *pd = nullptr;
-  if constexpr (MRG) {
-    pa = a.mrg_po;
-    pb = a.mrg_pm;
-    pc = a.mrg_pl;
-    T = a.mrg_T;
-  } else if constexpr (NRM) {
-    pa = a.nrm_o;
-    pb = a.nrm_xin;
-    pc = a.nrm_w1;
-    pd = a.nrm_w2;
-    nmode = a.nrm_mode;
-  } else {
-    pa = reinterpret_cast<const float*>(a.xs);
-    pb = a.gs;
-  }
-  // (the pointers are inputs only, so that they keep their global address space)
-  asm volatile(""
-               : "+s"(nsub), "+s"(tl1), "+s"(tl2), "+s"(tl3), "+s"(M), "+s"(T), "+s"(nmode)
-               : "s"(w0w), "s"(w0s), "s"(w1w), "s"(w1s), "s"(w2w), "s"(w2s), "s"(pa), "s"(pb), "s"(pc), "s"(pd));
+  const int nsub = gx & 0xFF, M = gx >> 16, tl1 = tlp & 0x3FF, tl2 = (tlp >> 10) & 0x3FF, tl3 = tlp >> 20;
+  const int T = MRG ? (gx >> 8) & 0xFF : 0, nmode = NRM ? (gx >> 8) & 0xFF : 0;
   const int K = KT ? KT : a.K, G = K / 32, GC = K / 256;
   // block -> (tile, row subset); the tiles of XCD x (block % 8) are x, x + 8, ...
   const int xcd = blockIdx.x & 7, kq = blockIdx.x >> 3;
@@ -152,12 +138,17 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
   float* YL = OFL + MPL * TR;                                // [MPL][TR]
 
   const int mi = (t >= tl1) + (t >= tl2);
-  const uint4* Ww = mi == 0 ? w0w : (mi == 1 ? w1w : w2w);
-  const uint4* Ws = mi == 0 ? w0s : (mi == 1 ? w1s : w2s);
   const int tl = t - (mi == 0 ? 0 : (mi == 1 ? tl1 : tl2));
   const int t64 = tl / (64 / TR), r64 = (tl % (64 / TR)) * TR + lane;  // storage tile and row
-  const uint4* wp = Ww + ((size_t)t64 * GC * 8 + j) * 64 + r64;  // chunk c at + c * 512
-  const uint4* sp = Ws + (size_t)t64 * GC * 64 + r64;             // chunk c at + c * 64
+  // the tiles of matrices 1 and 2 come from the argument block: chosen in weights_after, once the
+  // prologue's loads are on their way
+  const uint4 *wp = nullptr, *sp = nullptr;  // chunk c at wp + c * 512, sp + c * 64
+  auto choose_mat = [&]() {
+    const uint4* Ww = mi == 0 ? w0w : (mi == 1 ? a.mat[1].w : a.mat[2].w);
+    const uint4* Ws = mi == 0 ? w0s : (mi == 1 ? a.mat[1].s : a.mat[2].s);
+    wp = Ww + ((size_t)t64 * GC * 8 + j) * 64 + r64;
+    sp = Ws + (size_t)t64 * GC * 64 + r64;
+  };
   constexpr int GT_B = gt_batch<MPL>();
   uint4 wA[GT_B], sA[GT_B], wB[GT_B], sB[GT_B];
   auto load_batch = [&](uint4 (&w)[GT_B], uint4 (&s)[GT_B], int c0) {  // indices clamped
@@ -177,6 +168,7 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    choose_mat();
     load_batch(wA, sA, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -434,7 +426,7 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
       const int u = threadIdx.x + k * NT;
       if (u < MPL * RW) XL[pad(u)] = keep4(m0 + u / RW < M, xr[k]);
     }
-    if (a.gs) {
+    if (pb) {  // (the group sums a.gs)
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
         const int idx = threadIdx.x + k * NT;
@@ -443,7 +435,7 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
     }
   }
   __syncthreads();
-  if ((!a.gs || MRG) && !NRM) {  // W:22 each group's sequential sum, from the staged copy
+  if ((!pb || MRG) && !NRM) {  // W:22 each group's sequential sum, from the staged copy
     for (int idx = threadIdx.x; idx < MPL * G; idx += NT) {
       const float4* q4 = XL + (size_t)idx * 9;
       float4 v[8];
@@ -531,7 +523,8 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
         a.y[0][(size_t)m * a.ldy[0] + staged_index(n)] =
             r16(r16(gelu8(r16(y))) * r16(a.epi_pli[(size_t)m * a.epi_pli_ld + n]));
     } else if (!a.gateup) {
-      if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + (size_t)tl * TR + rl] = y;
+      const int n = tl * TR + rl, np = ((a.yperm >> mi) & 1) ? head16_index(n) : n;
+      if (m < M) a.y[mi][(size_t)m * a.ldy[mi] + np] = y;
     } else {
       YL[q * TR + rl] = y;
     }
@@ -549,47 +542,82 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(GemvTDev d) {
   }
 }
 
+// the leading (preloaded) arguments of a launch of k_gemv_t: see the kernel
+struct GemvTLead {
+  const float *pa, *pb, *pc, *pd;
+  const uint4 *w0w, *w0s;
+  int gx, tl;
+};
+static GemvTLead gemvt_lead(const GemvTDev& d) {
+  const GemvTArgs& a = d.a;
+  GemvTLead L{};
+  int hi = 0;
+  if (a.mrg_po) {
+    L.pa = a.mrg_po;
+    L.pb = a.mrg_pm;
+    L.pc = a.mrg_pl;
+    hi = a.mrg_T;
+  } else if (a.nrm_mode) {
+    L.pa = a.nrm_o;
+    L.pb = a.nrm_xin;
+    L.pc = a.nrm_w1;
+    L.pd = a.nrm_w2;
+    hi = a.nrm_mode;
+  } else {
+    L.pa = reinterpret_cast<const float*>(a.xs);
+    L.pb = a.gs;
+  }
+  L.w0w = a.mat[0].w;
+  L.w0s = a.mat[0].s;
+  L.gx = d.nsub | (hi << 8) | (a.M << 16);
+  L.tl = d.tiles[1] | (d.tiles[2] << 10) | (d.tiles[3] << 20);
+  return L;
+}
+
+#define G4V_GEMVT_ARGS L.pa, L.pb, L.pc, L.pd, L.w0w, L.w0s, L.gx, L.tl, d
 template <int MPL, int TR>
 static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
   const size_t lds = gemvt_lds(MPL, d.a.K, d.a.nrm_mode != 0, TR, d.a.mrg_po != nullptr);
   const dim3 g(grid), b(TR * 8);
   const int K = d.a.K;
+  const GemvTLead L = gemvt_lead(d);
   // the verify pass's shapes at their default tiles get a fixed K: q/k/v and gate/up (norm
   // prologue, K 1536), down (K 6144)
   if (d.a.mrg_po) {  // (a fixed K costs the merge variant registers: it stays generic)
-    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false, TR>), g, b, lds, st, d);
+    if constexpr (MPL <= 2) hipLaunchKernelGGL((k_gemv_t<MPL, true, false, TR>), g, b, lds, st, G4V_GEMVT_ARGS);
   } else if (d.a.epi_pli) {
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR, 0, 1>), g, b, lds, st, d);
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR, 0, 1>), g, b, lds, st, G4V_GEMVT_ARGS);
   } else if (d.a.nrm_mode) {
     if constexpr ((MPL == 2 || MPL == 4) && TR == 64) {
       if (K == 1536) {
-        hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR, 1536>), g, b, lds, st, d);
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR, 1536>), g, b, lds, st, G4V_GEMVT_ARGS);
         return;
       }
     }
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR>), g, b, lds, st, d);
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, true, TR>), g, b, lds, st, G4V_GEMVT_ARGS);
   } else {
     if constexpr (MPL == 1 && TR == 64) {
       if (K == 6144) {
-        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 6144>), g, b, lds, st, d);
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 6144>), g, b, lds, st, G4V_GEMVT_ARGS);
         return;
       }
     }
     if constexpr (MPL == 1) {
       if (K == 12288) {  // the Gemma-4-E2B layout's wide down projections
-        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 12288>), g, b, lds, st, d);
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 12288>), g, b, lds, st, G4V_GEMVT_ARGS);
         return;
       }
     }
     if constexpr (MPL == 2 && TR == 64) {
       if (K == 1536) {
-        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 1536>), g, b, lds, st, d);
+        hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR, 1536>), g, b, lds, st, G4V_GEMVT_ARGS);
         return;
       }
     }
-    hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR>), g, b, lds, st, d);
+    hipLaunchKernelGGL((k_gemv_t<MPL, false, false, TR>), g, b, lds, st, G4V_GEMVT_ARGS);
   }
 }
+#undef G4V_GEMVT_ARGS
 
 // mpl: activation rows per block (1 to 4); tr: rows per tile (64 or 32)
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
@@ -606,6 +634,7 @@ int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
   d.tiles[0] = 0;
   for (int i = 0; i < 3; ++i) d.tiles[i + 1] = d.tiles[i] + (a.gateup && i ? 0 : a.mat[i].N * (a.gateup ? 2 : 1) / tr);
   const int T = d.tiles[3], tg = (T + 7) / 8;
+  if (T >= 1024 || a.M > 0x7FFF || (a.mrg_po && a.mrg_T > 255)) return 0;  // the packed launch geometry
   d.nsub = (a.M + mpl - 1) / mpl;
   const int grid = 8 * tg * d.nsub;
   if (tr == 64) {

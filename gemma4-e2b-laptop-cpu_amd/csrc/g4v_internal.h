@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "g4v_num.h"
 
 namespace g4v {
@@ -58,6 +60,58 @@ enum GemvEpi { EPI_STORE = 0, EPI_GATEUP = 1, EPI_SCREEN = 2 };
 __host__ __device__ __forceinline__ int staged_index(int n) {
   const int g = n >> 5, i = n & 31, e = i & 15;
   return (g * 8 + (e >> 1)) * 4 + ((e & 1) ? 2 : 0) + (i >> 4);
+}
+
+// ---- operands broadcast within rows of 16 lanes (DPP row_newbcast) ----
+// A VGPR whose lane k (of every row of 16 lanes) holds value k serves 16 wave-uniform operands:
+// the instruction reads lane k of its row.  The source registers of these are written by LDS or
+// memory loads only, never by a VALU instruction just before (the DPP read-after-VALU-write hazard).
+// d = x[k] * w
+template <int K>
+__device__ __forceinline__ float mul_bc(float x, float w) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  float d;
+  asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "=v"(d) : "v"(x), "v"(w), "n"(K));
+  return d;
+#else
+  return x * w;
+#endif
+}
+// o = w[k] * v + o
+template <int K>
+__device__ __forceinline__ float fmac_bc(float o, float w, float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(o) : "v"(w), "v"(v), "n"(K));
+  return o;
+#else
+  return fmaf(w, v, o);
+#endif
+}
+// l = l + w[k]
+template <int K>
+__device__ __forceinline__ float add_bc(float l, float w) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_add_f32_dpp %0, %1, %0 row_newbcast:%2 row_mask:0xf bank_mask:0xf" : "+v"(l) : "v"(w), "n"(K));
+  return l;
+#else
+  return l + w;
+#endif
+}
+// f(integral_constant<int, k>) for k = 0 .. N-1, each k a compile-time constant
+template <typename F, int... K>
+__device__ __forceinline__ void unroll_impl(F& f, std::integer_sequence<int, K...>) {
+  (f(std::integral_constant<int, K>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll_n(F& f) {
+  unroll_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// The 16-lane head order of a 256-wide head: element e = 16 tt + n at n * 16 + tt, so that lane n
+// of a row of 16 lanes reads its 16 elements (its sum-of-squares lane, score chain and RoPE
+// pairs, tt and tt + 8) as four 16-byte words.  Applied per head of 256 to wider rows.
+__host__ __device__ __forceinline__ int head16_index(int e) {
+  return (e & ~255) | ((e & 15) << 4) | ((e >> 4) & 15);
 }
 
 struct GemvArgs {
@@ -136,6 +190,9 @@ struct GemvTArgs {
   // r16(epi_pli[m * epi_pli_ld + n])), written staged into y[0] ([M][ldy]) for the next product
   const float* epi_pli;
   int epi_pli_ld;
+  // bit mi set: matrix mi's outputs are written in the 16-lane head order (head16_index), the
+  // order the verify pass's attention reads its query, key and value rows in
+  int yperm;
 };
 // W4A8 (g4v_w4a8.hip): operand tiles of a matrix from its original bytes [N][K/2] and scales
 // [N][K/32] (N % 16 == 0): tw [N/16][K/128][64] uint4, ts [N/16][K/256][16] uint4

@@ -61,6 +61,8 @@ struct LayerNorms {
   const float* post_ff;    // [H]
   const float* qn;         // [HD]
   const float* kn;         // [HD]
+  const float* qnp;        // qn, kn in the 16-lane head order (head16_index)
+  const float* knp;
   float scalar;
   int sliding;
 };
@@ -83,6 +85,9 @@ void launch_branch(const StepDev* sp, const int* best1, const float* h, const fl
                    VerifyResultDev* res, hipStream_t st);
 void launch_accept(const StepDev* sp, const int* best1, const int* best2, const int* cnt1, const int* cnt2,
                    VerifyResultDev* res, uint16_t* KC, uint16_t* VC, int NL, int kvcap, hipStream_t st);
+
+// dst = the 256-vector src in the 16-lane head order (head16_index)
+void launch_perm16(const float* src, float* dst, hipStream_t st);
 
 // exchange the contents of two device buffers of `bytes` (a multiple of 16)
 void launch_swap16(void* a, void* b, size_t bytes, hipStream_t st);

@@ -34,8 +34,9 @@ __device__ void write_staged(const float* v, int K, float* xs, float* gs) {
 }
 
 // E:1262-1267: x = rbf8(E[tok] * sqrt(H)); xa = (x * r) * in_ln, xa written staged (+ sums).
-// Also gathers the step's RoPE factors: ropestep[ty][m] = (cos, sin) rows of the layer-type ty
-// tables at the row's position, so the attention kernels read them without a dependent load.
+// Also gathers the step's RoPE factors: ropestep[ty][m] = the (cos, sin) rows of the layer-type ty
+// tables at the row's position, in the order of the attention's 16-lane rows (lane n: cos then
+// sin of elements 16 tt + n, tt < 8), so the attention kernel reads them without a dependent load.
 __global__ __launch_bounds__(ROW_THREADS) void k_embed(const uint16_t* __restrict__ E, const StepDev* sp,
                                                        const float* __restrict__ in_ln, float sqh,
                                                        float* __restrict__ x, float* __restrict__ xa,
@@ -50,9 +51,11 @@ __global__ __launch_bounds__(ROW_THREADS) void k_embed(const uint16_t* __restric
     const int ty = threadIdx.x >> 7, i = threadIdx.x & (HD / 2 - 1), rp = sp->rope[m];
     const float* cs = rope + (size_t)(2 * ty) * ctxcap * (HD / 2);
     const float* sn = cs + (size_t)ctxcap * (HD / 2);
-    float* dst = ropestep + ((size_t)ty * MAXM + m) * HD;
-    dst[i] = cs[(size_t)rp * (HD / 2) + i];
-    dst[HD / 2 + i] = sn[(size_t)rp * (HD / 2) + i];
+    // lane n = i % 16 of a 16-lane row holds elements 16 tt + n, tt < 8 of the rotation's first
+    // half: its 8 cos then 8 sin factors at n * 16
+    float* dst = ropestep + ((size_t)ty * MAXM + m) * HD + (i & 15) * 16 + (i >> 4);
+    dst[0] = cs[(size_t)rp * (HD / 2) + i];
+    dst[8] = sn[(size_t)rp * (HD / 2) + i];
   }
   for (int i = threadIdx.x; i < H; i += ROW_THREADS) {
     const float v = r16(bf2f(E[(size_t)tok * H + i]) * sqh);
@@ -264,6 +267,14 @@ __global__ void k_gen_w4(uint8_t* w, uint16_t* s, size_t nb, size_t ns, uint64_t
     w[i] = (uint8_t)((rng_hash(sw, i) >> 24) & 0xFF);
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ns; i += (size_t)gridDim.x * blockDim.x)
     s[i] = f2bf(0.005f + 0.015f * rng_unif(ss, i));
+}
+
+// a 256-vector into the 16-lane head order (head16_index)
+__global__ void k_perm16(const float* __restrict__ src, float* __restrict__ dst) {
+  dst[head16_index(threadIdx.x)] = src[threadIdx.x];
+}
+void launch_perm16(const float* src, float* dst, hipStream_t st) {
+  hipLaunchKernelGGL(k_perm16, dim3(1), dim3(HD), 0, st, src, dst);
 }
 
 // ---------------------------------------------------------------------------------------
