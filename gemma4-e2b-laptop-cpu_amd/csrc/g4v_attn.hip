@@ -275,38 +275,6 @@ constexpr int AR_THREADS = 256;  // 16 rows of 16 lanes; the value sweep: lane =
 constexpr int AR_KRING = 6;      // key positions in flight per row of lanes (a sliding-window split: all)
 constexpr int AR_HB = 2;         // heads per block: 224 blocks for a 7-row pass
 
-// lane n of a 16-lane row takes lane n + N of the row (row_shl:N; lanes past the row get 0)
-template <int N>
-__device__ __forceinline__ float shl_f(float v) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  return as_f32((uint32_t)__builtin_amdgcn_update_dpp(0, (int)as_u32(v), 0x100 + N, 0xF, 0xF, false));
-#else
-  return v;
-#endif
-}
-template <int N>
-__device__ __forceinline__ double shl_d(double v) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const uint64_t u = as_u64(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x100 + N, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x100 + N, 0xF, 0xF, false);
-  return as_f64(((uint64_t)hi << 32) | lo);
-#else
-  return v;
-#endif
-}
-// lane 0 of each 16-lane row to the whole row (row_newbcast:0)
-__device__ __forceinline__ double bcast0_d(double v) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const uint64_t u = as_u64(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x150, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x150, 0xF, 0xF, false);
-  return as_f64(((uint64_t)hi << 32) | lo);
-#else
-  return v;
-#endif
-}
-
 // E:326-345 1 / sqrtf((float)(ss / 256) + 1e-6) of the row's 256-vector: lane n's double chain
 // over tt is accumulator lane n; p_n meet as a_l = (p_l + p_{l+4}) + (p_{l+8} + p_{l+12}),
 // ss = (a_0 + a_2) + (a_1 + a_3).  Every lane of the row returns the factor.

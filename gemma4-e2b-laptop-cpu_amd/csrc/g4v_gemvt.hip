@@ -277,117 +277,113 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(const float* __restrict__ pa,
     }
   } else if constexpr (NRM) {
     // E:1358-1361 (mode 1) / E:1375-1378 with E:1390-1404 (mode 2, the per-layer-embedding
-    // branch zero) for the block's rows; RMS factors from the 16-lane double sum of squares
-    // (E:326-345).  XL takes the rows in plain order, is normalised in place and finally
-    // permuted in place into the staged order, one thread per (row, group).
-    constexpr int RW4 = H / 4, NV = (MPL * RW4 + NT - 1) / NT, NW = (RW4 + NT - 1) / NT;
-    float* W12 = YL + MPL * TR;                                   // [2][H]
-    float* RR = W12 + 2 * H;                                      // [2][MPL]
-    const float4* o4 = reinterpret_cast<const float4*>(pa);
-    const float4* x4 = reinterpret_cast<const float4*>(pb);
-    float4 ov[NV], xv[NV];
+    // branch zero) for the block's rows.  Wave q forms row q in registers (6 float4 per lane)
+    // without block barriers: x1 = r16(xin + r16((r16(o) * r1) * w1)), then xa from x1 and r2,
+    // written to XL in plain order; XL is then permuted in place into the staged order, one
+    // thread per (row, group).
+    //
+    constexpr int RW4 = H / 4, PER = RW4 / 64;
+    static_assert(NT / 64 >= MPL, "a wave per activation row");
+    const int wq = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    const bool rowwave = wq < MPL;            // uniform per wave
+    const bool live = rowwave && m0 + wq < M;  // rows past M are staged as zeros
+    const int mr = min(m0 + wq, M - 1);
+    const float4* o4 = reinterpret_cast<const float4*>(pa) + (size_t)mr * RW4 + ln;
+    const float4* x4 = reinterpret_cast<const float4*>(pb) + (size_t)mr * RW4 + ln;
+    const float4* w14 = reinterpret_cast<const float4*>(pc) + ln;
+    const float4* w24 = reinterpret_cast<const float4*>(pd) + ln;
+    float4 ov[PER], xv[PER];
+    if (rowwave) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {  // clamped: rows past M read row M - 1 and are zeroed
-      const int u = min((int)threadIdx.x + k * NT, MPL * RW4 - 1), q = u / RW4;
-      const size_t src = (size_t)min(m0 + q, M - 1) * RW4 + (u - q * RW4);
-      ov[k] = o4[src];
-      xv[k] = x4[src];
-    }
-    float4 w1[NW], w2[NW];
-#pragma unroll
-    for (int k = 0; k < NW; ++k) {
-      const int wi = min((int)threadIdx.x + k * NT, RW4 - 1);
-      w1[k] = reinterpret_cast<const float4*>(pc)[wi];
-      w2[k] = reinterpret_cast<const float4*>(pd)[wi];
+      for (int k = 0; k < PER; ++k) {
+        ov[k] = o4[64 * k];
+        xv[k] = x4[64 * k];
+      }
     }
     weights_after();
+    if (rowwave) {
+      float4* XR = XL + (size_t)wq * G * 9;  // row wq, plain order (padded)
+      auto xl_at = [&](int k) -> float4& { const int u = ln + 64 * k; return XR[u + (u >> 3)]; };
+      // E:326-345: lane t of the reference's ss_avx2 sums x[16 s + t]^2 in double over s in
+      // order, and the 16 lane sums meet as a_l = (p_l + p_{l+4}) + (p_{l+8} + p_{l+12}),
+      // ss = (a_0 + a_2) + (a_1 + a_3).  The wave writes its row into its XL region chain-major
+      // (chain t at 100 t: the 96 values of one chain contiguous, rows of chains spread over the
+      // banks), lanes 0..15 run the 16 chains, and the sums meet through data-parallel moves.
+      float* CR = reinterpret_cast<float*>(XR);
+      auto rms_row = [&](const float4 (&v)[PER]) -> float {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int u = threadIdx.x + k * NT;
-      if (u < MPL * RW4) {
-        const float4 o = ov[k];
-        XL[pad(u)] = keep4(m0 + u / RW4 < M, make_float4(r16(o.x), r16(o.y), r16(o.z), r16(o.w)));
-      }
-    }
+        for (int k = 0; k < PER; ++k) {
+          const float f[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
 #pragma unroll
-    for (int k = 0; k < NW; ++k) {
-      const int wi = threadIdx.x + k * NT;
-      if (wi < RW4) {
-        reinterpret_cast<float4*>(W12)[wi] = w1[k];
-        reinterpret_cast<float4*>(W12 + H)[wi] = w2[k];
-      }
-    }
-    __syncthreads();
-    const float* XP = reinterpret_cast<const float*>(XL);
-    auto rms_rows = [&](float* rinv) {  // lane t of a row sums x[16 s + t]^2 in double over s
-      if ((int)threadIdx.x < MPL * 16) {
-        // element 16 s + lt of row rq: group s / 2, float4 4 (s % 2) + lt / 4 of it (padded)
-        const float* xb = XP + (threadIdx.x >> 4) * (G * 36) + (threadIdx.x & 15);
-        auto xr = [&](int st) { return xb[(st >> 1) * 36 + (st & 1) * 16]; };
-        double sacc = 0;
-        float v[2][16];  // the values of 16 steps, read while the previous 16 are summed
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[0][k] = xr(k);
-#pragma unroll
-        for (int s0 = 0; s0 < H / 16; s0 += 16) {
-          if (s0 + 16 < H / 16) {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[((s0 >> 4) + 1) & 1][k] = xr(s0 + 16 + k);
-          }
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            const double dv = (double)v[(s0 >> 4) & 1][k];
-            sacc = fma(dv, dv, sacc);
+          for (int c = 0; c < 4; ++c) {
+            const int e = 4 * (ln + 64 * k) + c;  // element e: chain e % 16, step e / 16
+            CR[(e & 15) * 100 + (e >> 4)] = f[c];
           }
         }
-        // the row's 16 lanes meet through shuffles, in the reference's order (E:336-343)
-        const int base = threadIdx.x & ~15;
-        double p[16];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        double part = 0;
+        if (ln < 16) {
+          const float4* ch = reinterpret_cast<const float4*>(CR + ln * 100);
 #pragma unroll
-        for (int l = 0; l < 16; ++l) p[l] = __shfl(sacc, base + l);
-        double q4[4];
+          for (int i = 0; i < H / 64; ++i) {
+            const float4 q = ch[i];
+            const double d0 = (double)q.x, d1 = (double)q.y, d2 = (double)q.z, d3 = (double)q.w;
+            part = fma(d0, d0, part);
+            part = fma(d1, d1, part);
+            part = fma(d2, d2, part);
+            part = fma(d3, d3, part);
+          }
+        }
+        const double b2 = part + shl_d<4>(part);  // lane l: p_l + p_{l+4}
+        const double c2 = b2 + shl_d<8>(b2);      // lanes 0..3: a_l
+        const double d2 = c2 + shl_d<2>(c2);      // lanes 0, 1: a_0 + a_2, a_1 + a_3
+        const double e2 = d2 + shl_d<1>(d2);      // lane 0: ss
+        const uint64_t u = as_u64(e2);
+        const double ss = as_f64(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 0) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 0));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        return 1.0f / sqrtf((float)(ss / H) + 1e-6f);
+      };
+      const bool after_mlp = nmode == 2;
+      const float scal = a.nrm_scalar;
+      float4 w1[PER];
 #pragma unroll
-        for (int l = 0; l < 4; ++l) q4[l] = (p[l] + p[4 + l]) + (p[8 + l] + p[12 + l]);
-        const double ss = (q4[0] + q4[2]) + (q4[1] + q4[3]);
-        if ((threadIdx.x & 15) == 0) rinv[threadIdx.x >> 4] = 1.0f / sqrtf((float)(ss / H) + 1e-6f);
-      }
-      __syncthreads();
-    };
-    rms_rows(RR);
-    const bool after_mlp = nmode == 2;
-    const float scal = a.nrm_scalar;
+      for (int k = 0; k < PER; ++k) w1[k] = w14[64 * k];
+      float4 os[PER];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int u = threadIdx.x + k * NT;
-      if (u < MPL * RW4) {
-        const int q = u / RW4, c4 = u - q * RW4;
-        const float r1 = RR[q];
-        const float4 os = XL[pad(u)], w = reinterpret_cast<const float4*>(W12)[c4], xr = xv[k];
-        float4 v = make_float4(r16(xr.x + r16((os.x * r1) * w.x)), r16(xr.y + r16((os.y * r1) * w.y)),
-                               r16(xr.z + r16((os.z * r1) * w.z)), r16(xr.w + r16((os.w * r1) * w.w)));
+      for (int k = 0; k < PER; ++k)
+        os[k] = keep4(live, make_float4(r16(ov[k].x), r16(ov[k].y), r16(ov[k].z), r16(ov[k].w)));
+      const float r1 = rms_row(os);
+      float4 x1[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const float4 o = os[k], w = w1[k], xr = xv[k];
+        float4 v = make_float4(r16(xr.x + r16((o.x * r1) * w.x)), r16(xr.y + r16((o.y * r1) * w.y)),
+                               r16(xr.z + r16((o.z * r1) * w.z)), r16(xr.w + r16((o.w * r1) * w.w)));
         if (after_mlp) v = make_float4(r16(v.x * scal), r16(v.y * scal), r16(v.z * scal), r16(v.w * scal));
-        v = keep4(m0 + q < M, v);
-        XL[pad(u)] = v;
-        if (t == 0 && m0 + q < M) reinterpret_cast<float4*>(a.nrm_xout)[(size_t)(m0 + q) * RW4 + c4] = v;
+        x1[k] = keep4(live, v);
+        if (t == 0 && live) reinterpret_cast<float4*>(a.nrm_xout)[(size_t)(m0 + wq) * RW4 + ln + 64 * k] = x1[k];
       }
-    }
-    __syncthreads();
-    if constexpr (XM == 0) {  // (XM 1, mode 3: x1 itself is the product's input)
-      rms_rows(RR + MPL);
+      if constexpr (XM == 1) {  // (mode 3: x1 itself is the product's input)
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {  // xa in place, plain order
-        const int u = threadIdx.x + k * NT;
-        if (u < MPL * RW4) {
-          const int q = u / RW4, c4 = u - q * RW4;
-          const float r2 = RR[MPL + q];
-          const float4 tv = XL[pad(u)], w = reinterpret_cast<const float4*>(W12 + H)[c4];
+        for (int k = 0; k < PER; ++k) xl_at(k) = x1[k];
+      } else {
+        float4 w2[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) w2[k] = w24[64 * k];
+        const float r2 = rms_row(x1);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+          const float4 tv = x1[k], w = w2[k];
           float4 v = make_float4((tv.x * r2) * w.x, (tv.y * r2) * w.y, (tv.z * r2) * w.z, (tv.w * r2) * w.w);
           if (!after_mlp) v = make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w));
-          XL[pad(u)] = v;
+          xl_at(k) = v;
         }
       }
-      __syncthreads();
     }
+    __syncthreads();
     for (int idx = threadIdx.x; idx < MPL * G; idx += NT) {  // staged order + group sums
       float4* b4 = XL + (size_t)idx * 9;  // row q = idx / G, group g = idx % G: 8 float4 in plain order
       float4 r[8];

@@ -62,6 +62,38 @@ __host__ __device__ __forceinline__ int staged_index(int n) {
   return (g * 8 + (e >> 1)) * 4 + ((e & 1) ? 2 : 0) + (i >> 4);
 }
 
+// lane n of a 16-lane row takes lane n + N of the row (row_shl:N; lanes past the row get 0)
+template <int N>
+__device__ __forceinline__ float shl_f(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return as_f32((uint32_t)__builtin_amdgcn_update_dpp(0, (int)as_u32(v), 0x100 + N, 0xF, 0xF, false));
+#else
+  return v;
+#endif
+}
+template <int N>
+__device__ __forceinline__ double shl_d(double v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint64_t u = as_u64(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x100 + N, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x100 + N, 0xF, 0xF, false);
+  return as_f64(((uint64_t)hi << 32) | lo);
+#else
+  return v;
+#endif
+}
+// lane 0 of each 16-lane row to the whole row (row_newbcast:0)
+__device__ __forceinline__ double bcast0_d(double v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint64_t u = as_u64(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x150, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x150, 0xF, 0xF, false);
+  return as_f64(((uint64_t)hi << 32) | lo);
+#else
+  return v;
+#endif
+}
+
 // ---- operands broadcast within rows of 16 lanes (DPP row_newbcast) ----
 // A VGPR whose lane k (of every row of 16 lanes) holds value k serves 16 wave-uniform operands:
 // the instruction reads lane k of its row.  The source registers of these are written by LDS or
