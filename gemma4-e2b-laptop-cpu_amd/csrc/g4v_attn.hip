@@ -701,14 +701,40 @@ void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, in
 }
 
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
-                          int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh) {
-  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                          int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh,
+                          float* gs) {
+  AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
              nullptr, gdev};
   AttnGeom g{};
   g.M = M;
   g.T = T;
   hipLaunchKernelGGL(k_attn_split, dim3(T, M, nh / ATT_HB), dim3(ATT_THREADS), 0, st, P, g, T);
   hipLaunchKernelGGL(k_attn_merge, dim3(M, nh), dim3(HD), 0, st, P, M, T);
+}
+
+// E:1325-1326 per layer type: keys [kmin, pos0 + M - 1], row m at slot pos0 + m with its window
+// from its RoPE position (sliding: 512 keys) and the step's skipped range
+__global__ void k_step_geom(const StepDev* __restrict__ sp, int T, AttnGeom* __restrict__ geo) {
+  const int ty = threadIdx.x;  // 0 sliding, 1 global
+  if (ty > 1) return;
+  AttnGeom g{};
+  const int M = sp->M, pos0 = sp->pos0;
+  g.M = M;
+  g.T = T;
+  g.kmax = pos0 + M - 1;
+  g.kmin = g.kmax;
+  for (int m = 0; m < MAXM; ++m) {
+    if (m >= M) break;
+    g.pos[m] = pos0 + m;
+    g.lo[m] = ty == 0 ? max(0, sp->rope[m] - 511) : 0;
+    g.skip_lo[m] = sp->skip_lo[m];
+    g.skip_hi[m] = sp->skip_hi[m];
+    g.kmin = min(g.kmin, g.lo[m]);
+  }
+  geo[ty] = g;
+}
+void launch_step_geom(const StepDev* sp, int T, AttnGeom* geo, hipStream_t st) {
+  hipLaunchKernelGGL(k_step_geom, dim3(1), dim3(64), 0, st, sp, T, geo);
 }
 
 // the caller's [position][256] key / value rows (device) into the device cache layout

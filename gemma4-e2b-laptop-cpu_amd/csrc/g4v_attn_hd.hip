@@ -170,13 +170,13 @@ int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, 
 }
 
 void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev,
-                             int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st) {
+                             int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st,
+                             float* gs) {
   AttnGeom g{};
   g.M = M;
   g.T = T;
   hipLaunchKernelGGL(k_attn_split_d<512>, dim3(T, M, nh), dim3(512), 0, st, KC, VC, q, ldq, g, gdev, po, pm, pl);
-  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(M, nh), dim3(512), 0, st, po, pm, pl, M, T, out, ldo,
-                     (float*)nullptr);
+  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(M, nh), dim3(512), 0, st, po, pm, pl, M, T, out, ldo, gs);
 }
 
 }  // namespace g4v

@@ -130,6 +130,7 @@ struct g4v_ctx {
   size_t gm_koff[15] = {}, gm_voff[15] = {};
   DBuf gm_rope;                   // global layers' RoPE: cos, sin [ctxcap][256]
   DBuf gm_rows, gm_tok, gm_s;     // row buffers of a pass (gm_cap rows), its tokens, score scratch
+  DBuf gm_geo;                    // a verify pass's split geometry per layer type (launch_step_geom)
   int gm_cap = 0;                 // rows the row buffers, tokens and W4A8 operands hold
   size_t gm_sfl = 0;              // floats of the score scratch
   int gm_Imax = 0;
@@ -1877,6 +1878,7 @@ size_t gm_rows_floats(int Imax, int rows) {
 // row buffers, token slots and W4A8 operands for passes of up to `rows` rows, score scratch of
 // `sfl` floats (grown, never shrunk)
 int gm_reserve(g4v_ctx* c, int rows, size_t sfl) {
+  if (rows > c->gm_cap || sfl > c->gm_sfl) drop_graphs(c);  // captured passes hold these buffers
   if (rows > c->gm_cap) {
     ALLOC(c->gm_rows, gm_rows_floats(c->gm_Imax, rows) * 4);
     ALLOC(c->gm_tok, (size_t)rows * 4);
@@ -1934,12 +1936,19 @@ bool gm_complete(const g4v_ctx* c, std::string* what) {
 // m >= hrow (hrow >= 0) leave their final-normed state in h [M - hrow][1536] and |h| in hn.
 // pg: the rows are a run of whole prompt blocks (pg->pfb rows each, at least 5): each block's
 // rows take that block's attention path (attn_tile or run_mh, E:1328-1337), in one pass.
+// spd not null (a verify pass): the rows' tokens and positions are read from the step parameters
+// on the device (pos0 here only picks the attention path), so that the pass can be captured once
+// and replayed at any position
 void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool i8, float* h, float* hn,
-                const PfGeom* pg = nullptr) {
+                const PfGeom* pg = nullptr, const StepDev* spd = nullptr) {
   hipStream_t st = c->st;
   const GmRows R = gm_rows(c);
   const float sqh = std::sqrt((float)H);
-  const int* tok = c->gm_tok.as<int>();
+  const int* tok = spd ? spd->toks : c->gm_tok.as<int>();
+  const int* dpos = spd ? &spd->pos0 : nullptr;
+  const bool split = !pg && M <= 4 && pos0 + M > 192;  // E:1305-1327
+  AttnGeom* geo = c->gm_geo.as<AttnGeom>();
+  if (spd && split) launch_step_geom(spd, nsplit, geo, st);
   i8 = i8 && M >= 2;  // lin_multi's rule (E:311)
   launch_pf_embed(c->E.as<uint16_t>(), tok, c->gm[0].nv.as<float>(), sqh, R.x, R.a, M, st);  // E:1262-1267
   pf_lin(c, c->gm_plproj, R.x, M, R.pr, i8, true);                                            // E:615-660
@@ -1962,8 +1971,15 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
     }
     const float* cs = ty ? c->gm_rope.as<float>() : c->rope.as<float>();
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
-    launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own);
-    if (!pg && M <= 4 && pos0 + M > 192) {  // E:1305-1327
+    launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own, dpos);
+    if (split && spd) {
+      if (hd == 512)
+        launch_attn_geom_dev_hd(KCo, VCo, R.q, NQ * 512, geo + ty, M, nsplit, NQ, c->po5.as<float>(),
+                                c->pm5.as<float>(), c->pl5.as<float>(), R.att, NQ * 512, st);
+      else
+        launch_attn_geom_dev(KCo, VCo, R.q, NQ * HD, geo + ty, M, nsplit, c->po.as<float>(), c->pm.as<float>(),
+                             c->pl.as<float>(), R.att, NQ * HD, st);
+    } else if (split) {
       AttnGeom ag{};
       ag.M = M;
       ag.kmax = pos0 + M - 1;
@@ -1985,7 +2001,7 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
                          NQ * HD, st);
     } else {  // attn_tile (M >= 4 past 64 keys, no sibling) or run_mh: one block of M rows
       launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, pg ? *pg : PfGeom{M, pos0, M, sib}, 0, M, sliding,
-                     st, false, hd);
+                     st, false, hd, dpos, c->ctxcap);
     }
     pf_lin(c, lay.m[3], R.att, M, R.o, i8, true);                       // E:1356
     launch_pf_post_attn(R.o, R.x, R.a, post_attn, pre_ff, M, st);       // E:1358-1361
@@ -2016,15 +2032,19 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
 // its projection (E:1386).  Residual rows: xa at a layer's start, xb after attention, xc after
 // the MLP (R.x, R.a, R.g); the products' outputs meet their consumers in R.o.  The last row
 // block's final-normed state goes to h / hn (row 0 on).
-void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* h, float* hn) {
+void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* h, float* hn, const StepDev* spd) {
   hipStream_t st = c->st;
   const GmRows R = gm_rows(c);
+  const int* dpos = spd ? &spd->pos0 : nullptr;
+  const bool split = M <= 4 && pos0 + M > 192;  // E:1305-1327
+  AttnGeom* geo = c->gm_geo.as<AttnGeom>();
+  if (spd && split) launch_step_geom(spd, nsplit, geo, st);
   float *xa = R.x, *xb = R.a, *xc = R.g, *attgs = R.u;
   // a one-row pass runs 32-row tiles (twice the blocks of a 64-row tile: one subset only)
   auto rows_of = [&](int cls) { return M == 1 ? 1 : c->gcfg[cls][0]; };
   auto tile_of = [&](int cls) { return M == 1 ? 32 : c->gcfg[cls][1]; };
   const float sqh = std::sqrt((float)H);
-  const int* tok = c->gm_tok.as<int>();
+  const int* tok = spd ? spd->toks : c->gm_tok.as<int>();
   launch_pf_embed(c->E.as<uint16_t>(), tok, c->gm[0].nv.as<float>(), sqh, xa, xb, M, st);  // E:1262-1267
   pf_lin(c, c->gm_plproj, xa, M, R.pr, false, true);                                       // E:615-660
   launch_gm_ple(R.pr, tok, c->gm_ple.as<uint16_t>(), c->gm_plnorm.as<float>(), R.pli, M, st);
@@ -2066,9 +2086,18 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
     }
     const float* cs = hd == 512 ? c->gm_rope.as<float>() : c->rope.as<float>();
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
-    launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own);
+    launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own, dpos);
     const float* ogs = nullptr;  // group sums of the staged attention rows (split path)
-    if (M <= 4 && pos0 + M > 192) {  // E:1305-1327
+    if (split && spd) {
+      const int ty = hd == 512;
+      if (hd == 512)
+        launch_attn_geom_dev_hd(KCo, VCo, R.q, NQ * 512, geo + ty, M, nsplit, NQ, c->po5.as<float>(),
+                                c->pm5.as<float>(), c->pl5.as<float>(), R.att, NQ * 512, st, attgs);
+      else
+        launch_attn_geom_dev(KCo, VCo, R.q, NQ * HD, geo + ty, M, nsplit, c->po.as<float>(), c->pm.as<float>(),
+                             c->pl.as<float>(), R.att, NQ * HD, st, NQ, attgs);
+      ogs = attgs;
+    } else if (split) {
       AttnGeom ag{};
       ag.M = M;
       ag.kmax = pos0 + M - 1;
@@ -2090,7 +2119,8 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
                          NQ * HD, st, NQ, attgs);
       ogs = attgs;
     } else {  // attn_tile (M >= 4 past 64 keys, no sibling) or run_mh
-      launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, PfGeom{M, pos0, M, sib}, 0, M, sliding, st, true, hd);
+      launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, PfGeom{M, pos0, M, sib}, 0, M, sliding, st, true, hd,
+                     dpos, c->ctxcap);
     }
     {  // E:1356
       GemvTArgs a{};
@@ -2189,6 +2219,7 @@ int g4v_model_create_gemma(g4v_ctx* c, int V, const int* mlp, int ctxcap) {
   HIPCHK(hipSetDevice(c->device));
   int r = model_alloc(c, V, GM_NL, 256, ctxcap);
   if (r) return r;
+  ALLOC(c->gm_geo, 2 * sizeof(AttnGeom));
   c->gemma = true;
   c->gm_Imax = Imax;
   c->gm_plready = false;
@@ -2255,6 +2286,7 @@ int g4v_model_set_norms_gemma(g4v_ctx* c, int l, const float* const nv[7], float
     HIPCHK(hipMemcpyAsync(G.nv.as<float>() + o, nv[t], n * 4, hipMemcpyHostToDevice, c->st));
   }
   HIPCHK(hipStreamSynchronize(c->st));
+  if (G.scalar != scalar) drop_graphs(c);  // the layer scalar is baked into captured passes
   G.scalar = scalar;
   G.normed = true;
   return 0;
@@ -2264,6 +2296,7 @@ int g4v_model_set_ple(g4v_ctx* c, const uint8_t* w, const uint16_t* s, const flo
   if (!c || !w || !s || !plnorm) return G4V_E_ARG;
   ARGCHK(c->gemma, "model_set_ple: no Gemma layout (g4v_model_create_gemma first)");
   HIPCHK(hipSetDevice(c->device));
+  drop_graphs(c);  // the projection's buffers are reallocated
   DBuf tmp;
   ALLOC(tmp, (size_t)GM_PLN * H / 2);
   HIPCHK(hipMemcpyAsync(tmp.p, w, (size_t)GM_PLN * H / 2, hipMemcpyHostToDevice, c->st));
@@ -2398,28 +2431,63 @@ static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int 
     s.skip_lo[r] = r <= na ? 1 : pos0 + 1;
     s.skip_hi[r] = r <= na ? 0 : pos0 + na;
   }
-  HIPCHK(hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, st));
-  HIPCHK(hipMemcpyAsync(c->gm_tok.p, toks, (size_t)M * 4, hipMemcpyHostToDevice, st));
+  // The pass reads its tokens and positions from the step parameters on the device (copied in by
+  // its first node from the pinned step block), so a shape is captured once as a graph (after one
+  // eager run) and replayed at every position; the key holds what the launches bake in: rows,
+  // branches, splits, the attention path (E:1305-1337) and the W4A8 mode.
   const int sib = nb == 1 ? na + 1 : -1;
-  if (c->dec_i8 && c->pf_i8 && M >= 2)  // G_I8_ACTIVE in the decode (E:1600), lin_multi's M >= 2 (E:311)
-    gm_forward(c, M, pos0, nsplit, sib, 0, true, c->h.as<float>(), c->hn.as<float>());
-  else
-    gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>());
-  const StepDev* sp = c->stepd.as<StepDev>();
-  VerifyResultDev* res = c->resd.as<VerifyResultDev>();
-  head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);  // E:1453-1488
-  launch_branch(sp, c->hb1.hs.best, c->h.as<float>(), c->hn.as<float>(), c->h2.as<float>(), c->hn2.as<float>(), res,
-                st);
-  HeadRun h2 = head_args(c, c->hb2, c->h2.as<float>(), c->hn2.as<float>(), std::max(1, std::max(na, nb)),
-                         &res->hcount);
-  h2.pass2 = 1;
-  head_run(h2, st);
-  launch_accept(sp, c->hb1.hs.best, c->hb2.hs.best, c->hb1.hs.cnt, c->hb2.hs.cnt, res, nullptr, nullptr, 0, 0, st);
-  for (int l = 0; l < 15; ++l)  // E:1651: the sibling's rows move into place in every owner cache
-    launch_kv_compact_hd(sp, res, c->gm_kv.as<uint16_t>() + c->gm_koff[l], c->gm_kv.as<uint16_t>() + c->gm_voff[l],
-                         c->gm[l].hd, st);
-  HIPCHK(hipGetLastError());
-  HIPCHK(hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, st));
+  const bool i8p = c->dec_i8 && c->pf_i8 && M >= 2;  // G_I8_ACTIVE in the decode (E:1600), lin_multi's M >= 2 (E:311)
+  const int path = (M <= 4 && pos0 + M > 192) ? 0 : 1;
+  const long long key =
+      (1LL << 62) | ((((((long long)M * 8 + na) * 8 + nb) * 32 + nsplit) * 2 + path) * 2 + (i8p ? 1 : 0));
+  auto enqueue = [&]() {
+    (void)hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, st);
+    const StepDev* sp = c->stepd.as<StepDev>();
+    if (i8p)
+      gm_forward(c, M, pos0, nsplit, sib, 0, true, c->h.as<float>(), c->hn.as<float>(), nullptr, sp);
+    else
+      gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>(), sp);
+    VerifyResultDev* res = c->resd.as<VerifyResultDev>();
+    head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);  // E:1453-1488
+    launch_branch(sp, c->hb1.hs.best, c->h.as<float>(), c->hn.as<float>(), c->h2.as<float>(), c->hn2.as<float>(),
+                  res, st);
+    HeadRun h2 = head_args(c, c->hb2, c->h2.as<float>(), c->hn2.as<float>(), std::max(1, std::max(na, nb)),
+                           &res->hcount);
+    h2.pass2 = 1;
+    head_run(h2, st);
+    launch_accept(sp, c->hb1.hs.best, c->hb2.hs.best, c->hb1.hs.cnt, c->hb2.hs.cnt, res, nullptr, nullptr, 0, 0, st);
+    for (int l = 0; l < 15; ++l)  // E:1651: the sibling's rows move into place in every owner cache
+      launch_kv_compact_hd(sp, res, c->gm_kv.as<uint16_t>() + c->gm_koff[l], c->gm_kv.as<uint16_t>() + c->gm_voff[l],
+                           c->gm[l].hd, st);
+    (void)hipMemcpyAsync(c->res_host, c->resd.p, sizeof(VerifyResultDev), hipMemcpyDeviceToHost, st);
+  };
+  g4v_ctx::Graph* gr = nullptr;
+  for (auto& g : c->graphs)
+    if (g.key == key) gr = &g;
+  const bool warm = std::find(c->warmed.begin(), c->warmed.end(), key) != c->warmed.end();
+  if (gr) {
+    HIPCHK(hipGraphLaunch(gr->exec, st));
+  } else if (!c->use_graph || !warm) {  // the first pass of a shape (or graphs disabled) runs eagerly
+    enqueue();
+    HIPCHK(hipGetLastError());
+    if (!warm) c->warmed.push_back(key);
+  } else {
+    g4v_ctx::Graph g;
+    g.key = key;
+    hipGraph_t graph;
+    HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    enqueue();
+    HIPCHK(hipStreamEndCapture(st, &graph));
+    const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) {
+      c->err = std::string("hipGraphInstantiate: ") + hipGetErrorString(ei);
+      return G4V_E_HIP;
+    }
+    c->graphs.push_back(std::move(g));
+    gr = &c->graphs.back();
+    HIPCHK(hipGraphLaunch(gr->exec, st));
+  }
   HIPCHK(hipStreamSynchronize(st));
   const VerifyResultDev& r = *c->res_host;
   out->nacc = r.nacc;

@@ -112,13 +112,16 @@ void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, flo
 // (the sibling row).  hd 256 or 512; cs / sn the layer type's RoPE tables [ctx][hd / 2].
 void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
                    const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib = -1,
-                   int hd = HD, int own = 1);
+                   int hd = HD, int own = 1, const int* dpos = nullptr);
 // score scratch (floats) of M rows starting at position Pb
 long long pf_score_floats(int M, int Pb, int sliding);
 // attn_tile / run_mh attention of segment rows [r0, r0 + M): q [n][2048] (row r at r), att likewise
-// staged: att rows in the staged GEMV input layout (staged_index) instead of plain
+// staged: att rows in the staged GEMV input layout (staged_index) instead of plain.
+// dpos (launch_pf_qkv too): not null, g.pos0 (P0) is read from that device word when the kernels
+// run, so that a captured pass serves every position; the grid then covers positions below maxpos.
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
-                    int r0, int M, int sliding, hipStream_t st, bool staged = false, int hd = HD);
+                    int r0, int M, int sliding, hipStream_t st, bool staged = false, int hd = HD,
+                    const int* dpos = nullptr, int maxpos = 0);
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st);
 void launch_pf_act(const float* g, const float* u, float* act, size_t n, hipStream_t st);
 void launch_pf_post_ff(const float* o, float* x, float* a, const float* w1, const float* next_in_ln,
@@ -189,11 +192,18 @@ int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, 
                         float* po, float* pm, float* pl, float* out, int ldo, float* gs, hipStream_t st);
 // head dim 512 with the geometry read from device memory (M rows, T splits and nh heads fixed by
 // the launch; at most ATT_SPLIT_MAX keys per split, which the caller checks), out plain [M][ldo]
+// or, with gs, staged with its group sums
 void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev,
-                             int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st);
+                             int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st,
+                             float* gs = nullptr);
 // the same with the geometry read from device memory (M rows and T splits fixed by the launch)
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
-                          int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ);
+                          int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ,
+                          float* gs = nullptr);
+// E:1325-1326 the split geometry of a verify pass from its step parameters: geo[0] for the
+// sliding-window layers, geo[1] for the global ones (window 512 from each row's RoPE position),
+// T splits
+void launch_step_geom(const StepDev* sp, int T, AttnGeom* geo, hipStream_t st);
 
 }  // namespace g4v
 

@@ -79,8 +79,10 @@ __global__ __launch_bounds__(D) void k_pf_qkv(float* __restrict__ q, const float
                                               const float* __restrict__ v, const float* __restrict__ qn,
                                               const float* __restrict__ kn, const float* __restrict__ cs,
                                               const float* __restrict__ sn, uint16_t* __restrict__ KC,
-                                              uint16_t* __restrict__ VC, int P0, int sib, int own) {
+                                              uint16_t* __restrict__ VC, int P0, int sib, int own,
+                                              const int* __restrict__ dpos) {
   constexpr int NV = NQ + 2;
+  if (dpos) P0 = *dpos;  // a captured verify pass: the position from the step parameters
   __shared__ float xv[NV][D];
   __shared__ double part[NV][16];
   __shared__ float rinv[NV];
@@ -138,8 +140,10 @@ __global__ __launch_bounds__(D) void k_pf_qkv(float* __restrict__ q, const float
 constexpr int PF_SPAN = 256;
 template <int D>
 __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, const uint16_t* __restrict__ KC,
-                                                   float* __restrict__ S, PfGeom g, int r0, int sliding) {
+                                                   float* __restrict__ S, PfGeom g, int r0, int sliding,
+                                                   const int* __restrict__ dpos) {
   __shared__ __align__(16) float qs[NQ][D];
+  if (dpos) g.pos0 = *dpos;  // a captured verify pass: the position from the step parameters
   // the last rows (longest ranges) first, so that the long blocks do not trail the grid
   const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_row_lo(r, P, g, sliding);
   const int len = P - lo + 1;
@@ -237,8 +241,9 @@ constexpr int PF_CP = 256;  // positions per weight chunk (4 per lane)
 template <int D>
 __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S, const uint16_t* __restrict__ VC,
                                                     float* __restrict__ att, PfGeom g, int r0, int sliding,
-                                                    ExpfTab tab, int staged) {
+                                                    ExpfTab tab, int staged, const int* __restrict__ dpos) {
   __shared__ __align__(16) float w[NQ][PF_CP];
+  if (dpos) g.pos0 = *dpos;
   __shared__ uint64_t T[32];
   // the last rows (longest ranges) first, so that the long blocks do not trail the grid
   const int rr = gridDim.x - 1 - blockIdx.x, r = r0 + rr, P = g.pos0 + r, lo = pf_row_lo(r, P, g, sliding);
@@ -400,8 +405,9 @@ constexpr int PF_RC = 512;
 template <int D>
 __global__ __launch_bounds__(D) void k_pf_attn_rows(const float* __restrict__ S, const uint16_t* __restrict__ VC,
                                                    float* __restrict__ att, PfGeom g, int r0, int sliding,
-                                                   ExpfTab tab, int staged) {
+                                                   ExpfTab tab, int staged, const int* __restrict__ dpos) {
   __shared__ __align__(16) float w[PF_RC];
+  if (dpos) g.pos0 = *dpos;
   __shared__ uint64_t T[32];
   __shared__ float red[D / 64];
   __shared__ float dens;
@@ -589,11 +595,11 @@ void launch_pf_embed(const uint16_t* E, const int* toks, const float* in_ln, flo
 }
 void launch_pf_qkv(float* q, const float* k, const float* v, const float* qn, const float* kn, const float* cs,
                    const float* sn, uint16_t* KC, uint16_t* VC, int P0, int M, hipStream_t st, int sib, int hd,
-                   int own) {
+                   int own, const int* dpos) {
   if (hd == 512)
-    hipLaunchKernelGGL(k_pf_qkv<512>, dim3(M), dim3(512), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib, own);
+    hipLaunchKernelGGL(k_pf_qkv<512>, dim3(M), dim3(512), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib, own, dpos);
   else
-    hipLaunchKernelGGL(k_pf_qkv<HD>, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib, own);
+    hipLaunchKernelGGL(k_pf_qkv<HD>, dim3(M), dim3(HD), 0, st, q, k, v, qn, kn, cs, sn, KC, VC, P0, sib, own, dpos);
 }
 long long pf_score_floats(int M, int Pb, int sliding) {
   const long long R = M;
@@ -602,29 +608,31 @@ long long pf_score_floats(int M, int Pb, int sliding) {
   return 8 * (c * (Pb + 1) + c * (c - 1) / 2 + (R - c) * 512);
 }
 void launch_pf_attn(const float* q, const uint16_t* KC, const uint16_t* VC, float* S, float* att, const PfGeom& g,
-                    int r0, int M, int sliding, hipStream_t st, bool staged, int hd) {
-  const int Plast = g.pos0 + r0 + M - 1;
+                    int r0, int M, int sliding, hipStream_t st, bool staged, int hd, const int* dpos, int maxpos) {
+  // (dpos: the position comes from device memory; the grid then covers positions below maxpos,
+  // and the score blocks past a row's range return at once)
+  const int Plast = dpos ? maxpos - 1 : g.pos0 + r0 + M - 1;
   // the sibling's window (from pos0 + 1) can be longer than 512 by the rows it skips
-  const int maxlen = sliding ? std::min(Plast + 1, g.sib >= 0 ? Plast - g.pos0 + 511 : 512) : Plast + 1;
+  const int maxlen = sliding ? std::min(Plast + 1, g.sib >= 0 ? r0 + M - 1 + 511 : 512) : Plast + 1;
   const int spans = (maxlen + PF_SPAN - 1) / PF_SPAN;
   ExpfTab tab{G4V_EXPF_TABLE};
   // a pass of few rows gives every (row, head) a block; a prompt block keeps a wave per row (it
   // reads each value row once for the 8 heads)
   const bool rows = M <= MAXM;
   if (hd == 512) {
-    hipLaunchKernelGGL(k_pf_scores<512>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
+    hipLaunchKernelGGL(k_pf_scores<512>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding, dpos);
     if (rows)
       hipLaunchKernelGGL(k_pf_attn_rows<512>, dim3(M, NQ), dim3(512), 0, st, S, VC, att, g, r0, sliding, tab,
-                         staged ? 1 : 0);
+                         staged ? 1 : 0, dpos);
     else
-      hipLaunchKernelGGL(k_pf_attn_out<512>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+      hipLaunchKernelGGL(k_pf_attn_out<512>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0, dpos);
   } else {
-    hipLaunchKernelGGL(k_pf_scores<HD>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding);
+    hipLaunchKernelGGL(k_pf_scores<HD>, dim3(M, spans), dim3(256), 0, st, q, KC, S, g, r0, sliding, dpos);
     if (rows)
       hipLaunchKernelGGL(k_pf_attn_rows<HD>, dim3(M, NQ), dim3(HD), 0, st, S, VC, att, g, r0, sliding, tab,
-                         staged ? 1 : 0);
+                         staged ? 1 : 0, dpos);
     else
-      hipLaunchKernelGGL(k_pf_attn_out<HD>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0);
+      hipLaunchKernelGGL(k_pf_attn_out<HD>, dim3(M), dim3(64), 0, st, S, VC, att, g, r0, sliding, tab, staged ? 1 : 0, dpos);
   }
 }
 void launch_pf_post_attn(const float* o, float* x, float* a, const float* w1, const float* w2, int M, hipStream_t st) {
