@@ -191,6 +191,7 @@ struct g4v_ctx {
   // ENGINE_DECODE_INT8 (E:1600): with pf_i8, the decode keeps G_I8_ACTIVE, so verify passes of
   // two rows or more run W4A8 too (Gemma layout)
   bool dec_i8 = false;
+  bool dr_same = false;  // ENGINE_DRAFT_SAMEPOS (E:1516, 1633): every draft step at position P + 1
   // row-tile GEMV shape of the verify pass's q/k/v, o, gate/up and down products: activation
   // rows per block and rows per tile (G4V_GEMV_CFG="a,b a,b a,b a,b" overrides, for tuning)
   int gcfg[4][2] = {{2, 64}, {1, 64}, {4, 64}, {1, 64}};
@@ -1281,12 +1282,30 @@ int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed) {
   }
   ARGCHK(n >= 0 && n <= c->ctxcap, "model_fake_ctx: n beyond the cache");
   HIPCHK(hipSetDevice(c->device));
-  std::vector<uint16_t> kc((size_t)n * HD), vc((size_t)n * HD);
   uint32_t rs = (uint32_t)seed;
   auto rnd = [&]() {
     rs = rs * 1664525u + 1013904223u;
     return (float)((int)(rs >> 9) % 2001 - 1000) / 700.0f;
   };
+  if (c->gemma) {  // the owner caches of layers 0..14 at their head dims, in the device layouts
+    for (int l = 0; l < 15; ++l) {
+      const int hd = c->gm[l].hd;
+      std::vector<uint16_t> kd((size_t)c->kvcap * hd), vd((size_t)c->kvcap * hd);
+      uint16_t* kdev = c->gm_kv.as<uint16_t>() + c->gm_koff[l];
+      uint16_t* vdev = c->gm_kv.as<uint16_t>() + c->gm_voff[l];
+      HIPCHK(hipMemcpy(kd.data(), kdev, kd.size() * 2, hipMemcpyDeviceToHost));
+      HIPCHK(hipMemcpy(vd.data(), vdev, vd.size() * 2, hipMemcpyDeviceToHost));
+      for (int p = 0; p < n; ++p)
+        for (int e = 0; e < hd; ++e) {  // E:1250: element i = p * hd + e, K then V
+          kd[hd == 512 ? kc_index_d<512>(p, e) : kc_index(p, e)] = f2bf(rnd());
+          vd[hd == 512 ? vc_index_d<512>(p, e) : vc_index(p, e)] = f2bf(rnd());
+        }
+      HIPCHK(hipMemcpy(kdev, kd.data(), kd.size() * 2, hipMemcpyHostToDevice));
+      HIPCHK(hipMemcpy(vdev, vd.data(), vd.size() * 2, hipMemcpyHostToDevice));
+    }
+    return 0;
+  }
+  std::vector<uint16_t> kc((size_t)n * HD), vc((size_t)n * HD);
   for (int l = 0; l < c->NL; ++l) {
     for (size_t i = 0; i < (size_t)n * HD; ++i) {
       kc[i] = f2bf(rnd());
@@ -2413,7 +2432,9 @@ static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int 
   ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
   ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");
-  ARGCHK((pos0 + M + nsplit - 1) / nsplit + 1 <= std::min(attn_pmax(), ATT_SPLIT_MAX - 1),
+  // only a pass of at most 4 rows past ATT_PAR takes the split-KV path (E:1305): the per-split
+  // limit of the split buffer applies to it alone
+  ARGCHK(!(M <= 4 && pos0 + M > 192) || (pos0 + M + nsplit - 1) / nsplit + 1 <= std::min(attn_pmax(), ATT_SPLIT_MAX - 1),
          "verify_step: context too long for nsplit");
   for (int i = 0; i < M; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "verify_step: token id out of range");
   HIPCHK(hipSetDevice(c->device));
@@ -2516,16 +2537,19 @@ static int gm_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int
   ARGCHK(toks && n >= 1 && pos0 >= 0 && (long long)pos0 + n <= c->ctxcap, "prefill: positions beyond the cache");
   ARGCHK(pfb >= 1 && pfb <= GM_ROWS, "prefill: 1 <= pfb <= 32 (the engine's row block, MM = 32)");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "prefill: 1 <= nsplit <= 16");
-  ARGCHK((pos0 + n + nsplit - 1) / nsplit + 1 <= std::min(attn_pmax(), ATT_SPLIT_MAX - 1),
-         "prefill: more positions per split than the split buffer holds");
   for (int i = 0; i < n; ++i) ARGCHK(toks[i] >= 0 && toks[i] < c->V, "prefill: token id outside the vocabulary");
-  HIPCHK(hipSetDevice(c->device));
   // blocks of 5 rows or more take attn_tile / run_mh only (E:1305, 1328): every block but a last
   // one that is short (split-KV past ATT_PAR) or a single row (exact float, E:311) runs in one
   // pass; smaller blocks run one by one
   const int Ml = n - (n - 1) / pfb * pfb, p0l = pos0 + n - Ml;
   const bool tail = (Ml <= 4 && p0l + Ml > 192) || Ml == 1;
   const int nA = pfb >= 5 ? (tail ? n - Ml : n) : 0;
+  // the per-split limit of the split buffer binds only the blocks that take the split-KV path
+  // (at most 4 rows past ATT_PAR, E:1305), the last of which ends at pos0 + n
+  const bool split_blocks = pfb >= 5 ? (tail && Ml <= 4 && p0l + Ml > 192) : pos0 + n > 192;
+  ARGCHK(!split_blocks || (pos0 + n + nsplit - 1) / nsplit + 1 <= std::min(attn_pmax(), ATT_SPLIT_MAX - 1),
+         "prefill: more positions per split than the split buffer holds");
+  HIPCHK(hipSetDevice(c->device));
   if (nA > 0) {
     int r = gm_reserve(c, nA, (size_t)pf_score_floats(nA, pos0, 0));
     if (r) return r;
@@ -2897,6 +2921,7 @@ extern "C" int g4v_draft_mtp(g4v_ctx* c, int tok, const float* h, int P, int k, 
   in[0] = tok;
   in[1] = P;
   in[2] = h ? -1 : c->last_hrow;
+  in[3] = c->dr_same ? 1 : 0;
   if (h) std::memcpy(in + 4, h, H * 4);
   // captured once per (k, splits) after one eager run, like the verify pass; keys below zero
   const long long key = -1 - ((long long)k * 32 + nsplit);
@@ -3116,6 +3141,12 @@ int g4v_set_decode_int8(g4v_ctx* c, int on) {
   return 0;
 }
 
+int g4v_set_draft_samepos(g4v_ctx* c, int on) {
+  if (!c) return G4V_E_ARG;
+  c->dr_same = on != 0;
+  return 0;
+}
+
 int g4v_set_graphs(g4v_ctx* c, int on) {
   if (!c) return G4V_E_ARG;
   c->use_graph = on != 0;
@@ -3137,18 +3168,23 @@ int g4v_hbm_stream(g4v_ctx* c, size_t bytes, int passes, int mode, double* gbps)
   const size_t n16 = bytes / 16;
   launch_stream(2, nullptr, src.as<uint4>(), n16, st);
   launch_stream(mode, src.as<uint4>(), dst.as<uint4>(), n16, st);
-  hipEvent_t e0, e1;
-  HIPCHK(hipEventCreate(&e0));
-  HIPCHK(hipEventCreate(&e1));
-  HIPCHK(hipEventRecord(e0, st));
+  HIPCHK(hipGetLastError());  // the fill and warm-up launches
+  struct Events {  // destroyed on every return path
+    hipEvent_t e[2] = {nullptr, nullptr};
+    ~Events() {
+      for (hipEvent_t x : e)
+        if (x) (void)hipEventDestroy(x);
+    }
+  } ev;
+  HIPCHK(hipEventCreate(&ev.e[0]));
+  HIPCHK(hipEventCreate(&ev.e[1]));
+  HIPCHK(hipEventRecord(ev.e[0], st));
   for (int p = 0; p < passes; ++p) launch_stream(mode, src.as<uint4>(), dst.as<uint4>(), n16, st);
-  HIPCHK(hipEventRecord(e1, st));
-  HIPCHK(hipEventSynchronize(e1));
-  float ms = 0.f;
-  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
   HIPCHK(hipGetLastError());
+  HIPCHK(hipEventRecord(ev.e[1], st));
+  HIPCHK(hipEventSynchronize(ev.e[1]));
+  float ms = 0.f;
+  HIPCHK(hipEventElapsedTime(&ms, ev.e[0], ev.e[1]));
   *gbps = (double)passes * (double)bytes * (mode == 1 ? 2.0 : 1.0) / ((double)ms * 1e-3) / 1e9;
   return 0;
 }

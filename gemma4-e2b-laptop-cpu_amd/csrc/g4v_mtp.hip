@@ -136,14 +136,15 @@ __global__ __launch_bounds__(256) void k_b16(B16Args a) {
   }
 }
 
-// per head (4): x = r16((x * r) * qn), then NeoX RoPE at the step's position (E:1542); D the
-// layer's head dim (256, or 512 for the global layer of a drafter checkpoint)
+// per head (4): x = r16((x * r) * qn), then NeoX RoPE at the step's position (E:1542): P + 1 + j,
+// or P + 1 for every step with ENGINE_DRAFT_SAMEPOS (Pp[2] set, E:1516, 1633); D the layer's head
+// dim (256, or 512 for the global layer of a drafter checkpoint)
 template <int D>
 __global__ __launch_bounds__(D) void k_dr_qnorm(float* __restrict__ q, const float* __restrict__ qn,
                                                 const float* __restrict__ cs, const float* __restrict__ sn,
                                                 const int* __restrict__ Pp, int j) {
   constexpr int NV = 4;
-  const int pos = *Pp + 1 + j;
+  const int pos = Pp[0] + 1 + (Pp[2] ? 0 : j);
   __shared__ float xv[NV][D];
   __shared__ double part[NV][16];
   __shared__ float rinv[NV];
@@ -186,11 +187,11 @@ __global__ __launch_bounds__(D) void k_dr_qnorm(float* __restrict__ q, const flo
 
 // a chain's inputs (E:1631-1633): the hidden state, the first token and, per step j, the
 // attention geometry (M = 1, keys [lo, P], lo = pos - 511 clamped at 0 on sliding layers,
-// pos = P + 1 + j, E:1543)
+// pos = P + 1 + j, E:1543, or P + 1 with ENGINE_DRAFT_SAMEPOS: in[3] set, E:1633)
 __global__ __launch_bounds__(256) void k_dr_setup(const int* __restrict__ in, const float* __restrict__ hbase,
                                                   float* __restrict__ hin, int* __restrict__ tok,
                                                   AttnGeom* __restrict__ geo, int k, int T) {
-  const int t0 = in[0], P = in[1], hrow = in[2];
+  const int t0 = in[0], P = in[1], hrow = in[2], same = in[3];
   const float* src = hrow >= 0 ? hbase + (size_t)hrow * H : reinterpret_cast<const float*>(in + 4);
   for (int i = threadIdx.x; i < H; i += 256) hin[i] = src[i];
   if (threadIdx.x == 0) tok[0] = t0;
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void k_dr_setup(const int* __restrict__ in, co
     g.M = 1;
     g.T = T;
     g.pos[0] = P;
-    g.lo[0] = sl ? max(0, P + 1 + j - 511) : 0;
+    g.lo[0] = sl ? max(0, P + 1 + (same ? 0 : j) - 511) : 0;
     g.skip_lo[0] = 1;
     g.skip_hi[0] = 0;
     g.kmin = g.lo[0];

@@ -394,8 +394,8 @@ __global__ __launch_bounds__(1024) void k_w4a8_dec(A8Dec m, const uint16_t* __re
     if (tid < 128) {
       const int ng = nc * 4;
 #pragma unroll 8
-      for (int j = 0; j < ng; ++j) {
-        const float2 v = S[j][cl][ci];
+      for (int gi = 0; gi < ng; ++gi) {
+        const float2 v = S[gi][cl][ci];
         acc = fmaf(v.x, v.y, acc);
       }
     }

@@ -293,6 +293,10 @@ struct Engine {
     return active;
   }
   bool drafter = false, stream = false, tree = false, sib_long = false;
+  // E:1211 ENGINE_FAKE_CTX: the caches hold fake_n positions of the LCG (E:1249-1250, filled once at
+  // start); every request then sits at positions fake_n + ... (E:1599, 1615, 1617) and leaves no
+  // reusable prefix (E:1675: kv_len = 0)
+  int fake_n = 0;
   float sib_gap = 1.0f;      // E:1629 ENGINE_SIB_GAP: the sibling row is proposed when >= 0
   int pol[3] = {-1, -1, -1};  // E:1513 ENGINE_POLICY: draft count cap per state
   long r1_n = 0, r1_top1 = 0, r1_top2 = 0;  // E:1084, 1659 (over the process)
@@ -306,15 +310,16 @@ struct Engine {
     const int n = (int)prompt.size();
     int start = 0, slot = 0;
     tree_attempts = tree_hits = 0;
-    check(g4v_slot_begin(G, prompt.data(), n, &start, &slot), "slot_begin");
+    if (fake_n == 0) check(g4v_slot_begin(G, prompt.data(), n, &start, &slot), "slot_begin");
+    const int F = fake_n;
     const double t0 = now();
     int g0 = 0;
     std::vector<float> hprev(1536);
     {  // every prompt block is a forward pass (E:1597-1598); only the last block attends split-KV
       const int np = n - start;
-      for (int b = 0; b < np; b += pfb) fwd_splits(start + b, std::min(pfb, np - b));
+      for (int b = 0; b < np; b += pfb) fwd_splits(F + start + b, std::min(pfb, np - b));
     }
-    check(g4v_prefill(G, prompt.data() + start, n - start, start, pfb, active, &g0, hprev.data()), "prefill");
+    check(g4v_prefill(G, prompt.data() + start, n - start, F + start, pfb, active, &g0, hprev.data()), "prefill");
     const double tp = now() - t0;
     std::vector<int> gen{g0};
     if (print && nnew > 0) {
@@ -322,7 +327,7 @@ struct Engine {
       fflush(stdout);
     }
     if (nnew <= 0) {
-      check(g4v_slot_end(G, prompt.data(), n, nullptr, 0, n - 1), "slot_end");
+      if (F == 0) check(g4v_slot_end(G, prompt.data(), n, nullptr, 0, n - 1), "slot_end");
       if (print) {
         printf("GEN:\nTIMING prompt=%d reused=%d new=%d prefill_s=%.3f decode_tokens=0 decode_s=0 decode_tok_s=0 "
                "tokens_per_round=0 ngram_rounds=0/0 ngram_acc_per_round=0\n",
@@ -357,13 +362,13 @@ struct Engine {
     if (k_draft == 0 || (!drafter && ng_n <= 0)) {  // E:1615: plain decode
       for (int i = 1; i < nnew && !is_stop(gen.back()); ++i) {
         const int t = gen.back();
-        check(g4v_verify_step(G, &t, 0, 0, n + i - 1, fwd_splits(n + i - 1, 1), &R, nullptr), "verify_step");
+        check(g4v_verify_step(G, &t, 0, 0, F + n + i - 1, fwd_splits(F + n + i - 1, 1), &R, nullptr), "verify_step");
         gen.push_back(R.commit[0]);
         emit();
       }
-      P = n + std::max(0, nnew - 1) - 1;
+      P = F + n + std::max(0, nnew - 1) - 1;
     } else {  // E:1617-1661
-      P = n - 1;
+      P = F + n - 1;
       int conf = gen.back(), state = 1;
       bool stopped = is_stop(conf), first = true;
       if (ng_n > 0) {  // seq = prompt + generated (E:1625), kept on the device
@@ -454,8 +459,8 @@ struct Engine {
     }
     emit();
     const double td = now() - t1;
-    // E:1671: the cache holds the prompt and gen[0 .. P - n]
-    check(g4v_slot_end(G, prompt.data(), n, gen.data(), (int)gen.size(), P), "slot_end");
+    // E:1671: the cache holds the prompt and gen[0 .. P - n] (E:1675: nothing reusable past a fake context)
+    if (F == 0) check(g4v_slot_end(G, prompt.data(), n, gen.data(), (int)gen.size(), P), "slot_end");
     if ((int)gen.size() > nnew) gen.resize(nnew);
     for (size_t i = 0; i < gen.size(); ++i)
       if (is_stop(gen[i])) {
@@ -515,13 +520,23 @@ int main(int argc, char** argv) {
   // E:1210 G_I8 and E:1600 DEC_I8: the prompt's linear layers run W4A8 when ENGINE_PREFILL_INT8=1,
   // and then the decode's verify passes of two rows or more too unless ENGINE_DECODE_INT8=0
   // (g4v_set_decode_int8; the library builds that mode for the Gemma layout)
-  // settings whose reference paths this engine does not restate
-  if (env_int("ENGINE_ATT_PAR", ATT_PAR) != ATT_PAR || env_int("ENGINE_FAKE_CTX", 0) != 0 ||
-      env_int("ENGINE_SPLITKV", 1) == 0) {
-    fprintf(stderr, "g4v_engine: ENGINE_ATT_PAR other than %d, ENGINE_FAKE_CTX and ENGINE_SPLITKV=0 are not "
-                    "supported (E:1211-1214)\n", ATT_PAR);
+  // settings whose reference paths this engine does not restate end the process (exit code 2)
+  // rather than run another path silently: the split-KV threshold and switch (E:1212-1214), the
+  // attn_tile switch ENGINE_NO_TILED (E:1213, 1328: run_mh for blocks attn_tile takes), and the
+  // draft chain's probability cut ENGINE_TAU > 0 (E:1515, 1561, 1644); a fake context with more
+  // than one cache slot (E:1573-1593 would park and swap the fake rows)
+  if (env_int("ENGINE_ATT_PAR", ATT_PAR) != ATT_PAR || env_int("ENGINE_SPLITKV", 1) == 0 ||
+      getenv("ENGINE_NO_TILED") || (getenv("ENGINE_TAU") && atof(getenv("ENGINE_TAU")) > 0.0)) {
+    fprintf(stderr, "g4v_engine: ENGINE_ATT_PAR other than %d, ENGINE_SPLITKV=0, ENGINE_NO_TILED and ENGINE_TAU > 0 "
+                    "are not supported (E:1212-1214, 1515)\n", ATT_PAR);
     return 2;
   }
+  e.fake_n = env_int("ENGINE_FAKE_CTX", 0);
+  if (e.fake_n < 0 || e.fake_n >= e.ctx || (e.fake_n > 0 && env_int("ENGINE_SLOTS", 1) > 1)) {
+    fprintf(stderr, "g4v_engine: ENGINE_FAKE_CTX needs 0 <= n < ENGINE_CTX and one cache slot (E:1211, 1573)\n");
+    return 2;
+  }
+  const bool samepos = env_int("ENGINE_DRAFT_SAMEPOS", 0) == 1;  // E:1516
   const bool g_i8 = env_int("ENGINE_PREFILL_INT8", 0) == 1;
   const bool dec_i8 = !(getenv("ENGINE_DECODE_INT8") && atoi(getenv("ENGINE_DECODE_INT8")) == 0);
   check(g4v_create(0, &G), "create");
@@ -559,6 +574,8 @@ int main(int argc, char** argv) {
     e.drafter = true;
   }
   check(g4v_slots_init(G, std::max(1, env_int("ENGINE_SLOTS", 1)), env_int("ENGINE_SLOT_MIN_REUSE", 32)), "slots_init");
+  if (samepos) check(g4v_set_draft_samepos(G, 1), "set_draft_samepos");
+  if (e.fake_n > 0) check(g4v_model_fake_ctx(G, e.fake_n, 12345), "model_fake_ctx");  // E:1249-1250, before the warm-up
   {  // E:1578: one warm-up pass at position 0 (the cache is not marked valid by it)
     const int w = 2;
     int g = 0;

@@ -64,6 +64,7 @@ SIGNATURES = {
     "g4v_set_graphs": (_i, [_vp, _i]),
     "g4v_set_prefill_int8": (_i, [_vp, _i]),
     "g4v_set_decode_int8": (_i, [_vp, _i]),
+    "g4v_set_draft_samepos": (_i, [_vp, _i]),
     "g4v_prefill": (_i, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(_i), _vp]),
     "g4v_drafter_synth": (_i, [_vp, C.c_uint64]),
     "g4v_drafter_load": (_i, [_vp, _vp]),
@@ -430,6 +431,10 @@ class Device:
     def set_decode_int8(self, on):
         """ENGINE_DECODE_INT8 (E:1600): W4A8 verify passes of two rows or more while prefill int8 is on"""
         self._ok(self.L.g4v_set_decode_int8(self.h, 1 if on else 0), "set_decode_int8")
+
+    def set_draft_samepos(self, on):
+        """ENGINE_DRAFT_SAMEPOS (E:1516, 1633): every draft step of a chain at position P + 1"""
+        self._ok(self.L.g4v_set_draft_samepos(self.h, 1 if on else 0), "set_draft_samepos")
 
     def profile(self, tags=None):
         """start per-kernel-class event timing for `tags` (names of PROF_TAGS; None = all)"""

@@ -80,9 +80,11 @@ int g4v_attn_splitkv(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npo
 /* The same attention on device buffers, allocating nothing (no hipMalloc, hipFree or allocating
  * library call): Kc, Vc, q and out are device pointers (same layouts as above), pos / lo /
  * skip_lo / skip_hi host arrays.  No counterpart in the reference: it is for callers that cannot
- * allocate (HIP graph capture, tight serving loops).  Its scratch (the relaid key / value rows and
- * the split partials, 5.3 MB) is a file-scope device array, one per GPU, held until the process
- * ends and shared by every call on that GPU: npos <= 4096; calls that overlap on one GPU race. */
+ * allocate (tight serving loops, harnesses that forbid allocation).  The call is synchronous: it
+ * launches on the context's own stream and waits for it, so it is not for a caller's stream
+ * capture.  Its scratch (the relaid key / value rows and the split partials, 5.3 MB) is a
+ * file-scope device array, one per GPU, held until the process ends and shared by every call on
+ * that GPU: npos <= 4096; calls that overlap on one GPU race. */
 int g4v_attn_splitkv_noalloc(g4v_ctx* c, const uint16_t* Kc, const uint16_t* Vc, int npos, int hd, int nh, int M,
                              const float* q, const int* pos, const int* lo, const int* skip_lo, const int* skip_hi,
                              int kmin, int kmax, int nsplit, float* out);
@@ -136,7 +138,9 @@ int g4v_model_set_ple_rows(g4v_ctx* c, int tok0, int n, const uint16_t* rows);
 /* KV rows [pos0, pos0 + n) of one layer, bf16 [n][256] each: a cache filled elsewhere
  * (the engine's prefill, E:1328-1336) */
 int g4v_model_set_kv(g4v_ctx* c, int layer, int pos0, int n, const uint16_t* K, const uint16_t* V);
-/* E:1249-1250 ENGINE_FAKE_CTX: first n KV positions of every layer from the LCG seeded `seed` */
+/* E:1249-1250 ENGINE_FAKE_CTX: first n KV positions of every layer from the LCG seeded `seed`
+ * (the reference's seed is 12345); on the Gemma-4-E2B layout the 15 owner caches (layers 0..14,
+ * each at its head dim), which are the caches main() fills */
 int g4v_model_fake_ctx(g4v_ctx* c, int n, uint64_t seed);
 /* copy a named model array to the host ("E", "W<l>_<j>", "S<l>_<j>", "N<l>_<t>", "KC", "VC", "fnorm",
  * the Gemma layout's owner caches "GK<l>" / "GV<l>" [ctxcap][hd] (l < 15),
@@ -184,6 +188,10 @@ int g4v_set_prefill_int8(g4v_ctx* c, int on);
  * (exact float decode).  Gemma layout only: the synthetic stack's verify_step refuses M >= 2
  * rows while it is on. */
 int g4v_set_decode_int8(g4v_ctx* c, int on);
+/* E:1516 SAMEPOS (ENGINE_DRAFT_SAMEPOS=1): g4v_draft_mtp runs every step of a chain at query
+ * position P + 1 (its RoPE angle and sliding window), as draft_step(..., SAMEPOS ? P + 1 :
+ * P + 1 + j, ...) does (E:1633); 0 (the default): step j at P + 1 + j. */
+int g4v_set_draft_samepos(g4v_ctx* c, int on);
 
 /* ---- prefill: run_req's prompt loop (E:1594-1599) with ENGINE_PREFILL_INT8=1, i.e. fwd
  * (E:1256-1405) over blocks of pfb rows (ENGINE_PREFILL_BLOCK, 32 by default), W4A8 linear layers

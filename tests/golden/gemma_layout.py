@@ -138,6 +138,29 @@ def bf16_of(x):
     return u.astype(np.uint16)
 
 
+def fake_ctx_rows(n, seed=12345):
+    """E:1249-1250 ENGINE_FAKE_CTX: owner layer l < 15 gets n positions of bf16 K and V rows from
+    one LCG (rs = rs * 1664525 + 1013904223 mod 2^32, value ((rs >> 9) % 2001 - 1000) / 700 in
+    float32), element i = p * hd + e drawing K then V, the layers in order.  Returns [(K, V)] of
+    [n][hd] uint16 per layer.  The sequence is formed in closed form: rs_k = a^k rs_0 + c (1 + a +
+    ... + a^(k-1)) in wrapping uint32 arithmetic."""
+    a, c = np.uint32(1664525), np.uint32(1013904223)
+    counts = [2 * n * layer_hd(l) for l in range(15)]
+    N = sum(counts)
+    with np.errstate(over="ignore"):
+        A = np.cumprod(np.full(N, a, np.uint32), dtype=np.uint32)          # a^k, k = 1..N
+        Sg = np.cumsum(np.concatenate([np.ones(1, np.uint32), A[:-1]]), dtype=np.uint32)  # 1 + ... + a^(k-1)
+        rs = A * np.uint32(seed) + c * Sg
+    vals = ((rs >> 9).astype(np.int64) % 2001 - 1000).astype(np.float32) / np.float32(700.0)
+    out, o = [], 0
+    for l in range(15):
+        hd = layer_hd(l)
+        v = bf16_of(vals[o:o + counts[l]]).reshape(n, hd, 2)
+        out.append((np.ascontiguousarray(v[:, :, 0]), np.ascontiguousarray(v[:, :, 1])))
+        o += counts[l]
+    return out
+
+
 def drafter_tensors(orc, E):
     """(name, dtype, array, shape) of the drafter checkpoint (E:1523-1528) for the target embedding E"""
     st = lambda tag: orc.stream(DRAFTER_SEED, tag)
@@ -313,6 +336,15 @@ class GemmaOracle:
     def greedy(self, h, seeds):
         return self.head.head(h, list(seeds)[:8])
 
+    def fake_ctx(self, n, seed=12345):
+        """E:1249-1250: the first n positions of the owner caches from the LCG (fake_ctx_rows)"""
+        for l, (K, V) in enumerate(fake_ctx_rows(n, seed)):
+            hd = layer_hd(l)
+            for v, rows in ((0, K), (1, V)):
+                p = self.orc.L.g4o_gemma_cache(self.h, l, v)
+                dst = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), (self.ctx * hd,))
+                dst[:n * hd] = rows.reshape(-1)
+
     def cache(self, l, v):
         hd = layer_hd(l)
         p = self.orc.L.g4o_gemma_cache(self.h, l, v)
@@ -416,6 +448,9 @@ class GemmaTarget:
 
     def draft(self, tok, h, pos, P, T):
         return self.dr.step(self.go, tok, h, pos, P, T)
+
+    def fake_ctx(self, n):
+        self.go.fake_ctx(n)
 
 
 def run_req_k0(go, prompt, nnew, T, pfb=32):

@@ -15,6 +15,9 @@ and the stderr line "RANK1 rounds= top1= top2_only= TREE attempts= hits=" (E:167
 counts run over the session) are stored as first_<mode>, gens_<mode>, gen_lens_<mode>,
 rank1_<mode> [3][5].  Mode k3_i8 is the server's environment (E:1600): W4A8 prompt blocks
 (ENGINE_PREFILL_INT8=1) and W4A8 verify passes of two rows or more (ENGINE_DECODE_INT8 on).
+Mode k3_same runs every draft step at position P + 1 (ENGINE_DRAFT_SAMEPOS=1, E:1633); mode fake
+starts from a fake context of FAKE_N positions (ENGINE_FAKE_CTX, E:1211, 1249-1250: the caches'
+first positions from the engine's LCG, every request after them, no prefix reuse).
 
 `--modes m1,m2` runs only those drafting sessions and adds their arrays to the fixture already
 written (the checkpoint is rebuilt from the same seeds).
@@ -41,10 +44,13 @@ from oracle import Oracle  # noqa: E402
 EXE = os.path.join(ROOT, "oracle", "_ref", "gemma4_engine")
 CPUS, NNEW, CTX = 6, 12, 1024
 NNEW_D = 24
+FAKE_N = 300
 # name -> engine settings of a drafting session (SIB_GAP 1, the default, lets the sibling row in)
 DRAFT_MODES = {"k3": dict(ENGINE_K="3"), "tree": dict(ENGINE_K="2", ENGINE_TREE="1"),
                "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5"),
-               "k3_i8": dict(ENGINE_K="3", ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="1")}
+               "k3_i8": dict(ENGINE_K="3", ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="1"),
+               "k3_same": dict(ENGINE_K="3", ENGINE_DRAFT_SAMEPOS="1"),
+               "fake": dict(ENGINE_K="3", ENGINE_FAKE_CTX=str(FAKE_N))}
 
 
 def base_env():
@@ -52,7 +58,7 @@ def base_env():
                ENGINE_DECODE_INT8="0", ENGINE_CTX=str(CTX))
     for k in ("ENGINE_PREFILL_INT8", "ENGINE_SERVE", "ENGINE_STREAM", "ENGINE_ADAPTIVE_THREADS", "ENGINE_K",
               "ENGINE_TREE", "ENGINE_NGRAM", "ENGINE_NGLEN", "ENGINE_SIB_GAP", "ENGINE_SIB_LONG", "ENGINE_POLICY",
-              "ENGINE_TAU", "ENGINE_DRAFT_SAMEPOS", "ENGINE_SLOTS"):
+              "ENGINE_TAU", "ENGINE_DRAFT_SAMEPOS", "ENGINE_SLOTS", "ENGINE_FAKE_CTX", "ENGINE_NO_TILED"):
         env.pop(k, None)
     return env
 

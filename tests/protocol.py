@@ -9,6 +9,8 @@ A target provides
       nd chain drafts and nb (0 / 1) sibling rows; result.nacc, .branch, .commit, .G0, and the
       committed row's final-normed state (E:1647-1661)
   draft(tok, h, pos, P, T)  -> (token, next hidden, runner-up, gap) (draft_step, E:1534-1563)
+  fake_ctx(n)               -> (ENGINE_FAKE_CTX only) the caches' first n positions from the LCG
+                               (E:1249-1250)
 """
 import numpy as np
 
@@ -25,13 +27,19 @@ class RunReq:
     persists.  i8: ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8=0.  ngram / nglen: ENGINE_NGRAM
     (0: no prompt lookup) and ENGINE_NGLEN; sib_long: ENGINE_SIB_LONG.  r1 holds the process's
     RANK1 counts (E:1655: rounds with MTP drafts, top-1 hits, runner-up-only hits); sib_rounds and
-    hits the last request's TREE attempts and hits (E:1583, 1648-1650)."""
+    hits the last request's TREE attempts and hits (E:1583, 1648-1650).  samepos: ENGINE_DRAFT_SAMEPOS
+    (every draft step at position P + 1, E:1633); fake_n: ENGINE_FAKE_CTX (the caches' first fake_n
+    positions from the LCG before the warm-up, every request at fake_n + its positions, no prefix
+    reuse: E:1249-1250, 1599, 1615-1617, 1675)."""
 
     def __init__(self, orc, target, t0=6, adaptive=False, draft_same=True, cut=192, i8=False, ngram=3, nglen=3,
-                 sib_long=False):
+                 sib_long=False, samepos=False, fake_n=0):
         self.orc, self.t = orc, target
         self.t0, self.active, self.adaptive, self.draft_same, self.cut, self.i8 = t0, t0, adaptive, draft_same, cut, i8
         self.ngram, self.nglen, self.sib_long = ngram, nglen, sib_long
+        self.samepos, self.fake_n = samepos, fake_n
+        if fake_n:
+            target.fake_ctx(fake_n)
         self.keys, self.kv_len = [], 0
         self.splits_seen = set()
         self.r1 = [0, 0, 0]
@@ -61,18 +69,20 @@ class RunReq:
         while common < self.kv_len and common < n and self.keys[common] == prompt[common]:
             common += 1
         start = min(common, n - 1)
-        h = self.prefill(prompt[start:], start)
+        F = self.fake_n
+        h = self.prefill(prompt[start:], F + start)
         g0 = self.t.head(h, prompt[start:][-8:])
-        gen, P, stopped = [g0], n - 1, is_stop(g0)
+        gen, P, stopped = [g0], F + n - 1, is_stop(g0)
         hprev, state, rounds, self.sib_rounds, self.hits = h, 1, 0, 0, 0
         if k_draft == 0:  # E:1615: one-row passes
             for i in range(1, nnew):
                 if stopped:
                     break
-                o, _ = self.t.verify(np.array([gen[-1]], np.int32), 0, 0, n + i - 1, self.fwd_splits(n + i - 1, 1))
+                o, _ = self.t.verify(np.array([gen[-1]], np.int32), 0, 0, F + n + i - 1,
+                                     self.fwd_splits(F + n + i - 1, 1))
                 gen.append(o.commit[0])
                 stopped = is_stop(gen[-1])
-            P = n + max(0, nnew - 1) - 1
+            P = F + n + max(0, nnew - 1) - 1
         while k_draft > 0 and len(gen) < nnew and not stopped:  # E:1617-1661
             k = min(k_draft, 3)
             if tree:
@@ -86,7 +96,7 @@ class RunReq:
                 tok, hh = gen[-1], hprev
                 for j in range(k):
                     ts = self.set_active(8 if self.draft_same and self.adaptive and P + 1 > self.cut else 6)
-                    tok, hh, sec, gap = self.t.draft(tok, hh, P + 1 + j, P, ts)
+                    tok, hh, sec, gap = self.t.draft(tok, hh, P + 1 + (0 if self.samepos else j), P, ts)
                     if j == 0:
                         sec1, gap1 = sec, gap
                         allow = rounds >= 1 and state < 2 and k >= 2 and sec1 >= 0 and sec1 != tok
@@ -131,8 +141,8 @@ class RunReq:
                     stopped = True
                     break
             P += o.nacc + 1
-        self.keys = list(prompt) + [g for i, g in enumerate(gen) if i <= P - n]
-        self.kv_len = min(P + 1, len(self.keys))
+        self.keys = list(prompt) + [g for i, g in enumerate(gen) if i <= P - F - n]
+        self.kv_len = 0 if F else min(P + 1, len(self.keys))
         gen = gen[:nnew]
         for i, g in enumerate(gen):
             if is_stop(g):

@@ -25,7 +25,9 @@ import gemma_layout as gl  # noqa: E402
 from protocol import RunReq  # noqa: E402
 
 # the drafting sessions of tests/golden/make_gemma_layout.py: (k, tree, ngram, nglen)
-MODES = {"k3": (3, False, 0, 3), "tree": (2, True, 0, 3), "ng": (3, False, 2, 5)}
+# mode -> (ENGINE_K, ENGINE_TREE, ENGINE_NGRAM, ENGINE_NGLEN, ENGINE_DRAFT_SAMEPOS, ENGINE_FAKE_CTX)
+MODES = {"k3": (3, False, 0, 3, False, 0), "tree": (2, True, 0, 3, False, 0), "ng": (3, False, 2, 5, False, 0),
+         "k3_same": (3, False, 0, 3, True, 0), "fake": (3, False, 0, 3, False, 300)}
 
 FX = os.path.join(HERE, "golden", "gemma_layout.npz")
 
@@ -76,12 +78,13 @@ def test_gemma_fixture_detects_planted_mistakes(orc, ckpt):
 @pytest.mark.parametrize("mode", list(MODES))
 def test_gemma_drafting_matches_reference_engine(orc, ckpt, mode):
     d, fx, prompts, gens = ckpt
-    k, tree, ngram, nglen = MODES[mode]
+    k, tree, ngram, nglen, samepos, fake_n = MODES[mode]
     want = np.split(fx["gens_" + mode], np.cumsum(fx["gen_lens_" + mode])[:-1])
     go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
     dr = gl.GemmaDrafter(orc, d)
     try:
-        rr = RunReq(orc, gl.GemmaTarget(go, dr), t0=int(fx["cpus"][0]), ngram=ngram, nglen=nglen)
+        rr = RunReq(orc, gl.GemmaTarget(go, dr), t0=int(fx["cpus"][0]), ngram=ngram, nglen=nglen, samepos=samepos,
+                    fake_n=fake_n)
         for i, p in enumerate(prompts):
             g0, gen, start = rr.run_req([int(t) for t in p], int(fx["nnew_d"][0]), k, tree)
             assert start == 0 and g0 == int(fx["first_" + mode][i])

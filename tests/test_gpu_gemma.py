@@ -287,7 +287,9 @@ def test_gemma_drafter_chain(orc, gemma, P):
 # k3_i8: the server's environment, W4A8 prompt blocks and verify passes (E:1600)
 DRAFT_MODES = {"k3": dict(ENGINE_K="3"), "tree": dict(ENGINE_K="2", ENGINE_TREE="1"),
                "ng": dict(ENGINE_K="3", ENGINE_NGRAM="2", ENGINE_NGLEN="5"),
-               "k3_i8": dict(ENGINE_K="3", ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="1")}
+               "k3_i8": dict(ENGINE_K="3", ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="1"),
+               "k3_same": dict(ENGINE_K="3", ENGINE_DRAFT_SAMEPOS="1"),  # E:1516, 1633
+               "fake": dict(ENGINE_K="3", ENGINE_FAKE_CTX="300")}         # E:1211, 1249-1250
 
 
 @pytest.mark.parametrize("mode", list(DRAFT_MODES))
@@ -303,7 +305,8 @@ def test_gemma_engine_drafting_matches_reference_engine(gemma, mode):
                ENGINE_CPUS=",".join(str(c) for c in range(int(fx["cpus"][0]))),
                ENGINE_DRAFTER_DIR=os.path.join(d, "drafter"), ENGINE_DRAFTER_INDEX=os.path.join(d, "drafter_index.tsv"))
     for k in ("ENGINE_PREFILL_INT8", "ENGINE_ADAPTIVE_THREADS", "ENGINE_NGRAM", "ENGINE_NGLEN", "ENGINE_STREAM",
-              "ENGINE_TREE", "ENGINE_SIB_GAP", "ENGINE_SIB_LONG", "ENGINE_POLICY"):
+              "ENGINE_TREE", "ENGINE_SIB_GAP", "ENGINE_SIB_LONG", "ENGINE_POLICY", "ENGINE_DRAFT_SAMEPOS",
+              "ENGINE_FAKE_CTX", "ENGINE_TAU", "ENGINE_NO_TILED", "ENGINE_SLOTS"):
         env.pop(k, None)
     env.update(DRAFT_MODES[mode])
     lines = "".join(f"{nnew} {' '.join(map(str, p))}\n" for p in prompts)
@@ -353,3 +356,28 @@ def test_gemma_synth_layout(g4v):
     assert a[0] == b[0] and a[2] == b[2] and a[4] == b[4]
     assert same(a[1], b[1]) and same(a[3], b[3]) and same(a[5], b[5])
     assert a[4]["G"][0] == a[2]  # row 0 of the chain pass is the decode pass's row
+
+
+def test_gemma_split_limit_binds_split_blocks_only(g4v):
+    """the per-split limit of the split buffer binds only passes that take the split-KV path (at
+    most 4 rows past ATT_PAR, E:1305): a 3,000-token prompt in blocks of 32 (attn_tile, E:1328)
+    runs with one split and gives the state six splits give; a 1-row pass there with one split is
+    refused, and runs with six"""
+    V, n = 16384, 3000
+    toks = (np.arange(n, dtype=np.int32) * 101 + 7) % V
+    outs = []
+    for ns in (1, 6):
+        dev = g4v.Device(0)
+        try:
+            dev.model_synth_gemma(23, V, [512] * 15 + [1024] * 20, 4096)
+            note(f"gemma prefill n={n} pfb=32 nsplit={ns}")
+            g0, h = dev.prefill(toks, 0, 32, ns, hidden=True)
+            if ns == 1:
+                with pytest.raises(RuntimeError, match="context too long for nsplit"):
+                    dev.verify(np.array([g0], np.int32), 0, 0, n, 1)
+            r1 = dev.verify(np.array([g0], np.int32), 0, 0, n, 6)
+            outs.append((g0, h, r1.commit[0]))
+        finally:
+            dev.close()
+    assert outs[0][0] == outs[1][0] and outs[0][2] == outs[1][2]
+    assert same(outs[0][1], outs[1][1])

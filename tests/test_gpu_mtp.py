@@ -10,10 +10,10 @@ from util import first_diff, same
 pytestmark = pytest.mark.gpu
 
 
-def oracle_chain(d, m, tok, h, P, k, T):
+def oracle_chain(d, m, tok, h, P, k, T, samepos=False):
     toks, secs, gaps = [], [], []
     for j in range(k):
-        tok, h, s, g = d.step(m, tok, h, P + 1 + j, P, T)
+        tok, h, s, g = d.step(m, tok, h, P + 1 + (0 if samepos else j), P, T)
         toks.append(tok)
         secs.append(s)
         gaps.append(g)
@@ -47,6 +47,36 @@ def test_draft_chain_matches_oracle(orc, g4v, V, P, T, k):
         assert got[1].tolist() == want[1], (got[1], want[1])
         assert same(got[2], want[2]), (got[2], want[2])
         assert same(got[3], want[3]), first_diff(got[3], want[3])
+    finally:
+        d.close()
+        m.close()
+        dev.close()
+
+
+@pytest.mark.parametrize("P", [300, 700])
+def test_draft_chain_same_position(orc, g4v, P):
+    """ENGINE_DRAFT_SAMEPOS (E:1516, 1633): every step at position P + 1 (its RoPE angle and, past
+    the 512 window, its window start); then the setting off again gives the P + 1 + j chain"""
+    from oracle import Drafter, Model
+    V, NL, I, ctx, seed, k, T = 16384, 15, 512, 2048, 45, 4, 6
+    note(f"mtp chain same position P={P}")
+    rng = np.random.default_rng(P + 1)
+    dev = g4v.Device(0)
+    m = Model(orc, seed, V, NL, I, ctx)
+    d = Drafter(orc, seed + 1, V)
+    try:
+        dev.model_synth(seed, V, NL, I, ctx)
+        dev.fake_ctx(P + 1, 5151)
+        m.fake_ctx(P + 1, 5151)
+        dev.drafter_synth(seed + 1)
+        h = (rng.standard_normal(1536).astype(np.float32).view(np.uint32) & 0xFFFF0000).view(np.float32)
+        tok = int(rng.integers(0, V))
+        for samepos in (True, False):
+            dev.set_draft_samepos(samepos)
+            got = dev.draft_mtp(tok, h, P, k, T)
+            want = oracle_chain(d, m, tok, h, P, k, T, samepos)
+            assert got[0].tolist() == want[0] and got[1].tolist() == want[1], (samepos, got[0], want[0])
+            assert same(got[2], want[2]) and same(got[3], want[3]), samepos
     finally:
         d.close()
         m.close()
