@@ -90,13 +90,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
   const int NTp = (NT + ATT_RING - 1) / ATT_RING * ATT_RING;
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;  // key sweep: position ps, chain lane l
   // key tile: lane (ps, l) takes the 64 bytes of chain lane l at position pb + ps (clamped into
-  // the split); value tile: lane i takes dim i of the block's 32 positions (64 bytes)
+  // the split); value tile: lane i takes dim i of the block's 32 positions (4 parts of 16 bytes)
   // Every stream entry issues its four loads, so each ring slot has exactly one definition
   // per tile (no merges that would make the compiler wait on loads still in flight): empty
   // entries and entries past the stream load a row they never use.
   uint4 kring[ATT_RING][4], vring[ATT_RING][4];
   const uint16_t* kbase = P.KC + l * 32;
-  const uint16_t* vbase = P.VC + threadIdx.x * 32;
+  const uint16_t* vbase = P.VC + threadIdx.x * 8;
   auto issue_k = [&](int s, uint4 (&r)[4]) {  // entries past the split reload its last row
     const size_t koff = (size_t)max(min(pb0 + min(s, NT - 1) * ATT_TILE + ps, c1 - 1), 0) * HD;
     const uint4* src = reinterpret_cast<const uint4*>(kbase + koff);
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
     const size_t voff = (size_t)((pb0 >> 5) + max(min(v, NT - 1), 0)) * (ATT_TILE * HD);
     const uint4* src = reinterpret_cast<const uint4*>(vbase + voff);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = src[c];
+    for (int c = 0; c < 4; ++c) r[c] = src[c * (8 * HD / 8)];  // part c: 8 HD bf16 further
   };
 #pragma unroll
   for (int k = 0; k < ATT_RING; ++k) issue_k(k, kring[k]);
@@ -422,12 +422,12 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
   // Keys from the cache stop before pos0 (the pass's rows come from LDS); entries past them
   // reload a position in range, never used.
   // value tiles: the split's NT blocks of 32 positions from pb0 (entries past them read zeros);
-  // lane i reads dim i of a tile, 64 bytes
+  // lane i reads dim i of a tile, 4 parts of 16 bytes (each load one contiguous 1 KB per wave)
   uint4 vring[ATT_RING][4];
   const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(VC + (size_t)(pb0 >> 5) * (ATT_TILE * HD), (uint32_t)NT * ATT_TILE * HD * 2);
   auto issue_v = [&](int v, uint4 (&r)[4]) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = buf_load16(vrs, (uint32_t)v * (ATT_TILE * HD * 2) + tid * 64 + c * 16);
+    for (int c = 0; c < 4; ++c) r[c] = buf_load16(vrs, (uint32_t)v * (ATT_TILE * HD * 2) + c * (8 * HD * 2) + tid * 16);
   };
   // key positions below gend = min(c1, pos0) from the cache (the pass's rows come from LDS;
   // entries past gend read zeros, never used)

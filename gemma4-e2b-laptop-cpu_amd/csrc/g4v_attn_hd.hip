@@ -85,11 +85,11 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
   // a zero weight (not allowed, outside the split) leaves both unchanged: its value is taken
   // as +0 and o is never -0
   const int d = threadIdx.x;
-  const uint16_t* vcol = VC + (size_t)d * 32;
+  const uint16_t* vcol = VC + (size_t)d * 8;
   float o = 0.f, lsum = 0.f;
   for (int j8 = 0; j8 < pe - pa; j8 += 8) {
     const int p8 = pa + j8;  // 8-aligned: the 8 positions of dim d are 16 contiguous bytes
-    const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (p8 & 31));
+    const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (size_t)((p8 >> 3) & 3) * (8 * D));
     const float4 wa = *reinterpret_cast<const float4*>(&sw[j8]);
     const float4 wb = *reinterpret_cast<const float4*>(&sw[j8 + 4]);
     const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};

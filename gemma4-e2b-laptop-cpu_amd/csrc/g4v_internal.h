@@ -19,13 +19,15 @@ constexpr int MAXT = 16;      // split-KV splits
 // Device KV cache layout (per layer: positions 0 .. kvcap - 1, kvcap a multiple of 32).
 // Keys: a position's 256 values in chain-lane order -- element e = 16 tt + 8 s + l (the
 // reference's score lane l, chain s, step tt) at slot l * 32 + s * 16 + tt -- so that the 8
-// lanes scoring one position each read 64 contiguous bytes.  Values: blocks of 32 positions
-// stored dim-major, so that the lane of dim i reads the block's 32 values of that dim as 64
-// contiguous bytes.  Both are permutations of the reference's [position][256] rows.
+// lanes scoring one position each read 64 contiguous bytes.  Values: blocks of 32 positions in
+// four parts of 8 positions, each part dim-major (8 values of a dim = 16 bytes), so that the
+// lane of dim i reads part c of a block as 16 bytes and a wave's 64 lanes read one part of 64
+// dims as 1 KB in one contiguous load.  Both are permutations of the reference's [position][256]
+// rows.
 __host__ __device__ inline int kc_slot(int e) { return (e & 7) * 32 + ((e >> 3) & 1) * 16 + (e >> 4); }
 __host__ __device__ inline size_t kc_index(int p, int e) { return (size_t)p * HD + kc_slot(e); }
 __host__ __device__ inline size_t vc_index(int p, int i) {
-  return (size_t)(p >> 5) * (32 * HD) + (size_t)i * 32 + (p & 31);
+  return (size_t)(p >> 5) * (32 * HD) + (size_t)((p >> 3) & 3) * (8 * HD) + (size_t)i * 8 + (p & 7);
 }
 inline int kv_cap(int npos) { return (npos + 31) / 32 * 32; }  // positions of a layer's cache slab
 // the same layouts for a head dim D (256 or 512: the global layers of the Gemma-4-E2B layout):
@@ -36,7 +38,7 @@ template <int D>
 __host__ __device__ inline size_t kc_index_d(int p, int e) { return (size_t)p * D + kc_slot_d<D>(e); }
 template <int D>
 __host__ __device__ inline size_t vc_index_d(int p, int i) {
-  return (size_t)(p >> 5) * (32 * D) + (size_t)i * 32 + (p & 31);
+  return (size_t)(p >> 5) * (32 * D) + (size_t)((p >> 3) & 3) * (8 * D) + (size_t)i * 8 + (p & 7);
 }
 constexpr int HEAD_LIMIT = 30000;  // E:1416 LIM: more survivors -> full head
 

@@ -290,9 +290,8 @@ __global__ __launch_bounds__(64) void k_pf_attn_out(const float* __restrict__ S,
   for (int h = 0; h < NQ; ++h)
 #pragma unroll
     for (int d = 0; d < DL; ++d) O[h][d] = 0.f;
-  // dim DL lane + d of position p: vcol + d * 32 + (p >> 5) * 32 D + (p & 31)
-  const uint16_t* vcol = VC + (size_t)(DL * lane) * 32;
-  auto vat = [&](int p, int d) { return vcol + d * 32 + (size_t)(p >> 5) * (32 * D) + (p & 31); };
+  // dim DL lane + d of position p in the cache layout (vc_index_d)
+  auto vat = [&](int p, int d) { return VC + vc_index_d<D>(p, DL * lane + d); };
   float sreg[PF_CP / 64][NQ];  // scores of this lane's positions of the next chunk
 #pragma unroll
   for (int k = 0; k < PF_CP / 64; ++k)
@@ -443,7 +442,7 @@ __global__ __launch_bounds__(D) void k_pf_attn_rows(const float* __restrict__ S,
     __syncthreads();
     den = dens;
   }
-  const uint16_t* vcol = VC + (size_t)d * 32;
+  const uint16_t* vcol = VC + (size_t)d * 8;
   float O = 0.f;
   for (int c0 = pa; c0 < pend; c0 += PF_RC) {
     const int cn = min(PF_RC, pend - c0);
@@ -461,7 +460,7 @@ __global__ __launch_bounds__(D) void k_pf_attn_rows(const float* __restrict__ S,
     __syncthreads();
     for (int j8 = 0; j8 < cn8; j8 += 8) {
       const int p8 = c0 + j8;
-      const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (p8 & 31));
+      const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (size_t)((p8 >> 3) & 3) * (8 * D));
       const float4 wa = *reinterpret_cast<const float4*>(&w[j8]);
       const float4 wb = *reinterpret_cast<const float4*>(&w[j8 + 4]);
       const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
