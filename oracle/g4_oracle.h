@@ -16,7 +16,8 @@
  * tests/test_oracle_math.py against closed forms, bounds and brute force):
  *   f2bf/r16, exp8, gelu8, sumsq, rms*, rope   golden + live + fp64 / RNE brute force
  *   rope_tables                                fp64 closed form + the reference's main() (the
- *                                              Gemma-layout tokens below use both tables)
+ *                                              Gemma-layout tokens and logit lines below use
+ *                                              both tables)
  *   cap, calc_thr                              golden + live + defining property by scan
  *   prep_x, w4g32_*                            golden + live + fp64 closed form, row independence
  *   w4a8_quant, w4a8_gemm                      golden + live + exact integer part
@@ -30,8 +31,9 @@
  *   attn_splitkv                               golden + live + fp64 softmax, LSE identity, masks
  *   attn_tile                                  live (the reference's attn_tile) + fp64 softmax
  *   attn_mh                                    fp64 softmax + the reference's main() through the
- *                                              Gemma-layout tokens (run_mh, E:1338-1349, is a
- *                                              lambda inside main()); no bit-level vector of it
+ *                                              Gemma-layout tokens and, per head row, its two
+ *                                              largest logits printed by ENGINE_DEBUG_GAP (run_mh,
+ *                                              E:1338-1349, is a lambda inside main())
  *   drafter (b16 gemv, draft step)             b16 gemv live against b16_rows; the step against
  *                                              the harness composition of the engine's kernels
  *   model / verify                             golden passes through the reference's kernels

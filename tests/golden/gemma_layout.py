@@ -453,8 +453,9 @@ class GemmaTarget:
         self.go.fake_ctx(n)
 
 
-def run_req_k0(go, prompt, nnew, T, pfb=32):
-    """run_req (E:1584-1661) with ENGINE_K=0 on an empty cache: FIRST and the GEN tokens"""
+def run_req_k0(go, prompt, nnew, T, pfb=32, rows=None):
+    """run_req (E:1584-1661) with ENGINE_K=0 on an empty cache: FIRST and the GEN tokens; rows
+    (a list) receives the final-normed hidden row of every head evaluation in order"""
     n = len(prompt)
     G = None
     for b in range(0, n, pfb):  # E:1594-1599 (the last block's last row feeds the head)
@@ -463,6 +464,8 @@ def run_req_k0(go, prompt, nnew, T, pfb=32):
         hb = go.forward(blk, b, T, len(blk) - 1 if last else len(blk))
         if last:
             G = go.greedy(hb[len(blk) - 1], blk)
+            if rows is not None:
+                rows.append(hb[len(blk) - 1].copy())
     gen = [G]
     is_stop = lambda t: t in (106, 1)
     for i in range(1, nnew):  # E:1615
@@ -470,8 +473,23 @@ def run_req_k0(go, prompt, nnew, T, pfb=32):
             break
         hb = go.forward([gen[-1]], n + i - 1, T, 0)
         gen.append(go.greedy(hb[0], [gen[-1]]))
+        if rows is not None:
+            rows.append(hb[0].copy())
     gen = gen[:nnew]
     for i, g in enumerate(gen):
         if is_stop(g):
             return gen[:i + 1]
     return gen
+
+
+def gap_line(orc, P, h, chosen):
+    """E:1497 the engine's debug line of one head row: the full head's r16 logits (exp3 form, as
+    head_task computes them), the largest t1 at its first index id1, the largest of the others t2 at
+    its first index id2, printed as "GAP %.4f %.4f id1=%d id2=%d chosen=%d" with t1 - t2 in float"""
+    lg = orc.r16(orc.exp3_gemm(P, np.asarray(h, np.float32)[None])[0])
+    i1 = int(np.argmax(lg))
+    rest = lg.copy()
+    rest[i1] = -np.inf
+    i2 = int(np.argmax(rest))
+    t1, t2 = np.float32(lg[i1]), np.float32(lg[i2])
+    return "GAP %.4f %.4f id1=%d id2=%d chosen=%d" % (float(t1), float(np.float32(t1 - t2)), i1, i2, chosen)

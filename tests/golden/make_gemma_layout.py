@@ -22,6 +22,12 @@ first positions from the engine's LCG, every request after them, no prefix reuse
 `--modes m1,m2` runs only those drafting sessions and adds their arrays to the fixture already
 written (the checkpoint is rebuilt from the same seeds).
 
+`--gap` (also part of a full run) runs each prompt once more with the full head and its debug
+line (ENGINE_HEAD_SCREEN unset, ENGINE_DEBUG_GAP=1, ENGINE_K=0, exact float prefill): per head
+row the engine prints "GAP t1 t1-t2 id1= id2= chosen=" (E:1497), the row's two largest r16
+logits and their ids, so the logits of run_mh (hd 256 and 512, the 40-token prompt) and of the
+RoPE tables are pinned at the printed resolution, not only through tokens.  Stored as gap_<i>.
+
 Run from the repository root after `make -C oracle`:
     python tests/golden/make_gemma_layout.py
 """
@@ -85,6 +91,9 @@ def main():
     if not os.path.exists(EXE):
         sys.exit("oracle/_ref/gemma4_engine is not built (make -C oracle with the reference sources)")
     only = sys.argv[sys.argv.index("--modes") + 1].split(",") if "--modes" in sys.argv else None
+    gap_only = "--gap" in sys.argv
+    if gap_only:
+        only = ["(none)"]
     orc = Oracle()
     prompts = cases(orc)
     out = {}
@@ -118,6 +127,24 @@ def main():
             out["first" + sfx] = np.array(firsts, np.int32)
             out["gen_lens" + sfx] = np.array([len(g) for g in gens])
             out["gens" + sfx] = np.concatenate(gens)
+        for i, p in enumerate(prompts) if (not only or gap_only) else ():
+            env = dict(base_env(), ENGINE_K="0", ENGINE_DEBUG_GAP="1")
+            env.pop("ENGINE_HEAD_SCREEN", None)
+            pf = os.path.join(d, f"gprompt{i}.txt")
+            with open(pf, "w") as f:
+                f.write(" ".join(map(str, p)) + "\n")
+            r = subprocess.run([EXE, d, os.path.join(d, "index.tsv"), pf, str(NNEW)], env=env,
+                               capture_output=True, text=True, timeout=1800)
+            if r.returncode != 0:
+                sys.exit(f"engine failed ({r.returncode}): {r.stderr[-2000:]}")
+            gaps = [ln.strip() for ln in r.stderr.splitlines() if ln.startswith("GAP ")]
+            gen = [int(x) for x in [ln for ln in r.stdout.splitlines() if ln.startswith("GEN:")][0].split()[1:]]
+            want = np.split(out["gens"], np.cumsum(out["gen_lens"])[:-1])[i]
+            # one line per head row: the warm-up pass at position 0 (E:1578), then FIRST and each GEN row
+            if gen != [int(t) for t in want] or len(gaps) != len(gen) + 1:
+                sys.exit(f"prompt {i}: full-head run differs from the screened one: {gen} / {list(want)} / {len(gaps)}")
+            print(f"prompt {i}: {len(gaps)} GAP lines, first {gaps[0]}", flush=True)
+            out[f"gap_{i}"] = np.array(gaps)
         from oracle import Model
         m = Model(orc, gl.EMBED_SEED, gl.V, 1, 256, 64)
         E = m.get("E", np.uint16, gl.V * gl.H).reshape(gl.V, gl.H)

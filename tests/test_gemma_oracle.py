@@ -55,6 +55,35 @@ def test_gemma_layout_matches_reference_engine(orc, ckpt, i, i8):
     assert gen == [int(t) for t in want], (gen, list(want))
 
 
+def test_gemma_head_logits_match_reference_engine(orc, ckpt):
+    """the logits, not only the tokens: the reference engine run unchanged with its full head and
+    ENGINE_DEBUG_GAP=1 prints, for every head row (the warm-up pass at position 0, then the
+    prompt's last row and each decode row), the two largest r16 logits and their ids (E:1497).
+    The oracle's hidden states through its full exp3 head reproduce every line: run_mh in the
+    40-token prompt's prefill and decode (head dim 256 and, in the global layers, 512), attn_tile
+    and split-KV in the others, and the RoPE tables of both layer types"""
+    d, fx, prompts, gens = ckpt
+    from oracle import Model
+    m = Model(orc, gl.EMBED_SEED, gl.V, 1, 256, 64)
+    E = m.get("E", np.uint16, gl.V * gl.H).reshape(gl.V, gl.H)
+    m.close()
+    P = orc.exp3_pack(E, gl.V, gl.H)
+    T, nnew = int(fx["cpus"][0]), int(fx["nnew"][0])
+    for i, p in enumerate(prompts):
+        want = [str(x) for x in fx[f"gap_{i}"]]
+        go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
+        try:
+            hw = go.forward([2], 0, T, 0)[0]  # E:1578 the warm-up pass
+            rows = [hw]
+            chosen = [go.greedy(hw, [2])]
+            gen = gl.run_req_k0(go, [int(t) for t in p], nnew, T, rows=rows)
+        finally:
+            go.close()
+        chosen += gen
+        got = [gl.gap_line(orc, P, h, c) for h, c in zip(rows, chosen)]
+        assert got == want, (i, [(a, b) for a, b in zip(got, want) if a != b][:3])
+
+
 def test_gemma_fixture_detects_planted_mistakes(orc, ckpt):
     d, fx, prompts, gens = ckpt
     want = [int(t) for t in gens[2]]
