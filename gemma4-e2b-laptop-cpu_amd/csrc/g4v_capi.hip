@@ -2051,7 +2051,13 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
 // its projection (E:1386).  Residual rows: xa at a layer's start, xb after attention, xc after
 // the MLP (R.x, R.a, R.g); the products' outputs meet their consumers in R.o.  The last row
 // block's final-normed state goes to h / hn (row 0 on).
-void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* h, float* hn, const StepDev* spd) {
+// a8 (G_I8_ACTIVE in the decode, 2 <= M <= 8): every product multiplies W4A8 (lin_multi, E:310-317)
+// through the same structure -- the W4A8 kernel takes the same prologues and epilogues and
+// quantises its activation rows itself -- so the values that reach the products are the ones the
+// exact pass forms, as in the reference, where only lin_multi's branch differs (E:1268-1289,
+// 1363-1388 compute the same rows in either mode).
+void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* h, float* hn, const StepDev* spd,
+                       bool a8 = false) {
   hipStream_t st = c->st;
   const GmRows R = gm_rows(c);
   const int* dpos = spd ? &spd->pos0 : nullptr;
@@ -2062,10 +2068,26 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
   // a one-row pass runs 32-row tiles (twice the blocks of a 64-row tile: one subset only)
   auto rows_of = [&](int cls) { return M == 1 ? 1 : c->gcfg[cls][0]; };
   auto tile_of = [&](int cls) { return M == 1 ? 32 : c->gcfg[cls][1]; };
+  a8 = a8 && M >= 2;  // lin_multi's rule (E:311)
+  // a product: the W4A8 kernel on the a8 tiles of the same matrices, or the row-tile GEMV
+  auto a8t = [](const Mat& m) { return W4Tile{m.a8w.as<uint4>(), m.a8s.as<uint4>(), m.N}; };
+  // the quantised rows of the W4A8 products of staged rows (K * 8 and K bytes): the prompt path's
+  // operand buffers (at least 16 rows of K bf16 and of K / 32 floats), which this pass uses only
+  // before its first such product (the per-layer-input projection and layer 0's q / k / v)
+  uint64_t* qa = c->pfxq.as<uint64_t>();
+  float* qsx = c->pfsx.as<float>();
+  auto product = [&](GemvTArgs& a, const Mat* const* ms, int nm, int mpl, int tr) {
+    if (a8) {
+      for (int j = 0; j < nm; ++j) a.mat[j] = a8t(*ms[j]);
+      (void)launch_gemv_a8(a, qa, qsx, st);
+    } else {
+      (void)launch_gemv_t(a, st, mpl, tr);
+    }
+  };
   const float sqh = std::sqrt((float)H);
   const int* tok = spd ? spd->toks : c->gm_tok.as<int>();
   launch_pf_embed(c->E.as<uint16_t>(), tok, c->gm[0].nv.as<float>(), sqh, xa, xb, M, st);  // E:1262-1267
-  pf_lin(c, c->gm_plproj, xa, M, R.pr, false, true);                                       // E:615-660
+  pf_lin(c, c->gm_plproj, xa, M, R.pr, a8, true);                                          // E:615-660
   launch_gm_ple(R.pr, tok, c->gm_ple.as<uint16_t>(), c->gm_plnorm.as<float>(), R.pli, M, st);
   for (int l = 0; l < GM_NL; ++l) {
     const auto& G = c->gm[l];
@@ -2079,7 +2101,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
     if (l == 0) {  // E:1287-1288 from the embedding row's norm
       const Mat* mq[3] = {&lay.m[0], &lay.m[1], &lay.m[2]};
       float* yq[3] = {R.q, R.k, R.v};
-      pf_lin_multi(c, own ? 3 : 1, mq, xb, M, yq, false);
+      pf_lin_multi(c, own ? 3 : 1, mq, xb, M, yq, a8);
     } else {
       const auto& P = c->gm[l - 1];
       const float* pnv = P.nv.as<float>();
@@ -2101,7 +2123,8 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.nrm_w1 = pnv + 4 * H;  // post_per_layer_input_norm of layer l - 1
       a.nrm_w2 = nv;           // input_layernorm of layer l
       a.nrm_scalar = P.scalar;
-      launch_gemv_t(a, st, rows_of(0), tile_of(0));
+      const Mat* ms[3] = {&lay.m[0], &lay.m[1], &lay.m[2]};
+      product(a, ms, nm, rows_of(0), tile_of(0));
     }
     const float* cs = hd == 512 ? c->gm_rope.as<float>() : c->rope.as<float>();
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
@@ -2150,7 +2173,8 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.gs = ogs;
       a.K = NQ * hd;
       a.M = M;
-      launch_gemv_t(a, st, rows_of(1), tile_of(1));
+      const Mat* ms[1] = {&lay.m[3]};
+      product(a, ms, 1, rows_of(1), tile_of(1));
     }
     {  // E:1358-1371: the attention residual and pre-FF norm, then gate / up and gelu
       GemvTArgs a{};
@@ -2166,10 +2190,26 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.nrm_w2 = pre_ff;
       a.K = H;
       a.M = M;
-      launch_gemv_t(a, st, rows_of(2), tile_of(2));
+      if (a8) {  // the gate and up matrices' own a8 tiles (their pairs meet in one block)
+        a.mat[0] = a8t(lay.m[4]);
+        a.mat[1] = a8t(lay.m[5]);
+        (void)launch_gemv_a8(a, qa, qsx, st);
+      } else {
+        launch_gemv_t(a, st, rows_of(2), tile_of(2));
+      }
     }
     bool down_done = false;  // E:1373
-    if (lay.m[6].tw.p) {
+    if (a8) {
+      GemvTArgs a{};
+      a.mat[0] = a8t(lay.m[6]);
+      a.y[0] = R.o;
+      a.ldy[0] = H;
+      a.xs = reinterpret_cast<const float4*>(R.act);
+      a.K = G.I;
+      a.M = M;
+      (void)launch_gemv_a8(a, qa, qsx, st);
+      down_done = true;
+    } else if (lay.m[6].tw.p) {
       GemvTArgs a{};
       a.mat[0] = lay.m[6].tile();
       a.y[0] = R.o;
@@ -2206,7 +2246,8 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.epi_pli_ld = GM_PLN;
       a.K = H;
       a.M = M;
-      launch_gemv_t(a, st, 1, M == 1 ? 32 : 64);
+      const Mat* ms[1] = {&G.pg};
+      product(a, ms, 1, 1, M == 1 ? 32 : 64);
     }
     {  // E:1386
       GemvTArgs a{};
@@ -2216,7 +2257,8 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.xs = reinterpret_cast<const float4*>(R.g2);
       a.K = GM_PD;
       a.M = M;
-      launch_gemv_t(a, st, 1, M == 1 ? 32 : 64);
+      const Mat* ms[1] = {&G.pp};
+      product(a, ms, 1, 1, M == 1 ? 32 : 64);
     }
   }
   // E:1387-1404 and 1414-1417 of the last layer: its per-layer-input residual, scalar, final norm
@@ -2464,10 +2506,7 @@ static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int 
   auto enqueue = [&]() {
     (void)hipMemcpyAsync(c->stepd.p, &s, sizeof s, hipMemcpyHostToDevice, st);
     const StepDev* sp = c->stepd.as<StepDev>();
-    if (i8p)
-      gm_forward(c, M, pos0, nsplit, sib, 0, true, c->h.as<float>(), c->hn.as<float>(), nullptr, sp);
-    else
-      gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>(), sp);
+    gm_verify_forward(c, M, pos0, nsplit, sib, c->h.as<float>(), c->hn.as<float>(), sp, i8p);
     VerifyResultDev* res = c->resd.as<VerifyResultDev>();
     head_run(head_args(c, c->hb1, c->h.as<float>(), c->hn.as<float>(), 1, nullptr), st);  // E:1453-1488
     launch_branch(sp, c->hb1.hs.best, c->h.as<float>(), c->hn.as<float>(), c->h2.as<float>(), c->hn2.as<float>(),

@@ -1,0 +1,511 @@
+// g4v_gemva8.hip -- W4A8 products of a verify pass (M <= 8 activation rows) for gfx950.
+//
+// lin_multi with G_I8_ACTIVE (E:310-317) over decode rows: quant (engine/w4a8_avx2.h:30-42) of
+// every activation row, then tile<MT> (engine/w4a8_avx2.h:46-61).  Per output (m, n):
+//   a32[g] = sum_i u[n][32g+i] q[m][32g+i] - 8 sum[m][g]            (exact integer)
+//   row    = fma((float)a32[g], sw[n][g] * sx[m][g], row)             over the groups g in order
+// with sx = amax / 127, inv = sx > 0 ? 1 / sx : 0, q = RNE(x * inv), sum = sum of the q of the
+// group (the same restatement as g4v_w4a8.hip, whose header shows that q never saturates).
+//
+// The group dots run on the matrix cores, one v_mfma_i32_16x16x32_i8 per (group, 16 outputs):
+// A the quantised rows (rows >= M zero), B the weight nibbles as the signed bytes u - 8, so that
+// D = sum_i q_i (u_i - 8) = a32 with no correction term (q unsaturated, every product and partial
+// sum an integer far below 2^31); D is stored as float (|a32| < 2^24, exact).  Lane (m, n) then
+// runs its chain over the groups in order on the VALU.
+//
+// The operand words: word h of (row m, group g) holds elements 8h + (0, 2, 4, 6, 1, 3, 5, 7) as
+// int8, the order of the weight nibbles in a8 tiles (low nibbles, then high nibbles, of the
+// group's bytes 4h .. 4h+3).
+//
+// Kernels, one launch per product of the fused verify pass:
+//   k_a8_quant_rows  quantises staged activation rows into QA [G][4][8] words and SX [G][8];
+//   k_gemv_a8p       a product of such rows (o, down, the per-layer projection): a block per
+//                    16 outputs walks K in phases of PG groups, the next phase's weight and
+//                    operand words in flight while the current one is multiplied and chained;
+//   k_gemv_a8n       a product whose prologue forms its rows as k_gemv_t's norm prologue does
+//                    (q/k/v, gate/up, the per-layer-input gate; K = 1536, one phase) and
+//                    quantises them in LDS; epilogues: y, the gate / up activation (staged) or
+//                    the per-layer-input gate (staged).
+#include "g4v_internal.h"
+
+namespace g4v {
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// quant of one 32-group (engine/w4a8_avx2.h:33-41) into its four operand words
+__device__ __forceinline__ float a8_quant_group(const float (&v)[32], uint64_t (&aq)[4]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float sx = amax / 127.0f, inv = sx > 0.f ? 1.0f / sx : 0.0f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int q = (int)__builtin_rintf(v[8 * h + i] * inv);  // RNE, as _mm256_cvtps_epi32 in the default mode
+      q = q > 127 ? 127 : (q < -128 ? -128 : q);
+      const uint32_t b = (uint32_t)q & 0xFFu;
+      if (i & 1)
+        hi |= b << (8 * (i >> 1));
+      else
+        lo |= b << (8 * (i >> 1));
+    }
+    aq[h] = (uint64_t)lo | ((uint64_t)hi << 32);
+  }
+  return sx;
+}
+
+// the B operand of one group: the lane's dword of weight nibbles (elements 8h .. 8h+7 of its
+// output row) as the eight signed bytes u - 8, low nibbles first
+__device__ __forceinline__ long a8_wbytes(uint32_t d) {
+  uint32_t lo = (d & 0x0F0F0F0Fu) ^ 0x08080808u, hi = ((d >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+  // a byte t = u ^ 8 holds u - 8 where u >= 8; where u < 8 (bit 3 of t set) u - 8 = t - 16: set
+  // the high nibble
+  lo |= (lo & 0x08080808u) * 0x1Eu;
+  hi |= (hi & 0x08080808u) * 0x1Eu;
+  return (long)((uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+__device__ __forceinline__ float a8_scale(uint4 s4, int e) {  // bf16 scale e of a word of 8
+  const uint32_t s2 = (e >> 1) == 0 ? s4.x : ((e >> 1) == 1 ? s4.y : ((e >> 1) == 2 ? s4.z : s4.w));
+  return as_f32((e & 1) ? (s2 & 0xFFFF0000u) : (s2 << 16));
+}
+
+// ---- quantised rows: thread (g, m); rows m >= M are written as zeros ----
+__global__ void k_a8_quant_rows(const float4* __restrict__ xs, int M, int K, uint64_t* __restrict__ QA,
+                                float* __restrict__ SX) {
+  const int G = K / 32, idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= 8 * G) return;
+  const int g = idx >> 3, m = idx & 7;
+  uint64_t* q = QA + (size_t)g * 32 + m;  // word h at q[8 h]
+  if (m >= M) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) q[8 * h] = 0;
+    SX[idx] = 0.f;
+    return;
+  }
+  // staged rows: float4 jj of a group holds elements 2jj, 16 + 2jj, 2jj + 1, 17 + 2jj
+  const float4* src = xs + ((size_t)m * K + 32 * g) / 4;
+  float v[32];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const float4 f = src[jj];
+    v[2 * jj] = f.x;
+    v[16 + 2 * jj] = f.y;
+    v[2 * jj + 1] = f.z;
+    v[17 + 2 * jj] = f.w;
+  }
+  uint64_t aq[4];
+  SX[idx] = a8_quant_group(v, aq);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) q[8 * h] = aq[h];
+}
+
+// ---- a product of quantised rows ----
+// Block: the 16 outputs of one a8 tile (tiles of up to three matrices, in order), 512 threads.
+// Phase p: wave w multiplies chunks (4 groups) w + 8k, k < NU, of the phase; lanes 0..127 chain.
+// LDS: A32 [PG][8][16] float, SXL [PG][8] float, SWL [PG / 8][16] uint4 (the tile's scales)
+constexpr int A8P_PG = 64;
+template <int PG>
+constexpr size_t a8p_lds() {
+  return (size_t)PG * 8 * 16 * 4 + (size_t)PG * 8 * 4 + (size_t)(PG / 8) * 16 * 16;
+}
+template <int PG>
+__global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a, const uint64_t* __restrict__ QA,
+                                                  const float* __restrict__ SX) {
+  constexpr int PC = PG / 4, NU = PC / 8;
+  static_assert(PC % 8 == 0, "whole chunks per wave");
+  extern __shared__ float4 lds4[];
+  float* A32 = reinterpret_cast<float*>(lds4);
+  float* SXL = A32 + PG * 8 * 16;
+  uint4* SWL = reinterpret_cast<uint4*>(SXL + PG * 8);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int M = a.M, K = a.K, G = K / 32, GC4 = G / 4, G8 = G / 8, nph = (G + PG - 1) / PG;
+  const int t = blockIdx.x, tl1 = a.mat[0].N / 16, tl2 = tl1 + a.mat[1].N / 16;
+  const int j = (t >= tl1) + (t >= tl2), mt = t - (j == 0 ? 0 : (j == 1 ? tl1 : tl2));
+  const uint4* wp = (j == 0 ? a.mat[0].w : (j == 1 ? a.mat[1].w : a.mat[2].w)) + (size_t)mt * GC4 * 64 + lane;
+  const uint4* sp = (j == 0 ? a.mat[0].s : (j == 1 ? a.mat[1].s : a.mat[2].s)) + (size_t)mt * G8 * 16;
+  const int ar = lane & 15, ah = lane >> 4;
+  const uint64_t* qp = QA + ah * 8 + (ar & 7);  // group g's word at + 32 g (rows >= 8 read as zero)
+
+  // the phase's weight words and operand words of this wave's chunks
+  uint4 wA[NU], wB[NU];
+  uint64_t qA[NU][4], qB[NU][4];
+  auto issue = [&](int p, uint4 (&wv)[NU], uint64_t (&qv)[NU][4]) {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int c = p * PC + w + 8 * k;
+      if (c < GC4) {
+        wv[k] = wp[(size_t)c * 64];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[k][i] = ar < 8 ? qp[(size_t)(4 * c + i) * 32] : 0;
+      }
+    }
+  };
+  // the phase's activation scales (thread f < 2 PG: 4 floats of SX) and weight scales (thread
+  // 2 PG <= f < 4 PG: a word of the tile's scales), staged through one register
+  uint4 stg = make_uint4(0, 0, 0, 0);
+  auto issue_s = [&](int p) {
+    const int gb = p * PG;
+    const bool sxw = tid < 2 * PG;
+    const int f = sxw ? tid : tid - 2 * PG;
+    const uint4* src = sxw ? reinterpret_cast<const uint4*>(SX + (size_t)gb * 8) + f
+                           : sp + (size_t)(gb / 8 + (f >> 4)) * 16 + (f & 15);
+    const bool ok = tid < 4 * PG && (sxw ? gb + f / 2 < G : gb / 8 + (f >> 4) < G8);
+    if (ok) stg = *src;
+  };
+  uint4* stg_dst = tid < 2 * PG ? reinterpret_cast<uint4*>(SXL) + tid : SWL + (tid - 2 * PG);
+  issue(0, wA, qA);
+  issue_s(0);
+  const int cm = (tid >> 4) & 7, cn = tid & 15;
+  const bool chain = tid < 128 && cm < M;
+  float acc = 0.f;
+  for (int p = 0; p < nph; ++p) {
+    const int gb = p * PG, ng = min(PG, G - gb);
+    if (p + 1 < nph) issue(p + 1, wB, qB);
+    if (tid < 4 * PG) *stg_dst = stg;
+    if (p + 1 < nph) issue_s(p + 1);
+    // the group dots of this wave's chunks
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int cl = w + 8 * k;
+      if (gb + 4 * cl < G) {  // (uniform per wave)
+        const uint4 wv = wA[k];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t d = i == 0 ? wv.x : (i == 1 ? wv.y : (i == 2 ? wv.z : wv.w));
+          const i32x4_t D = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)qA[k][i], a8_wbytes(d), i32x4_t{0, 0, 0, 0},
+                                                                  0, 0, 0);
+          if (ah < 2) {
+            float* o = A32 + ((size_t)(4 * cl + i) * 8 + 4 * ah) * 16 + ar;
+            o[0] = (float)D[0];
+            o[16] = (float)D[1];
+            o[32] = (float)D[2];
+            o[48] = (float)D[3];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // the chains over the phase's groups, in order (A8:59)
+    if (chain) {
+      const float* ap = A32 + cm * 16 + cn;
+#pragma unroll
+      for (int k8 = 0; k8 < PG / 8; ++k8) {
+        if (8 * k8 < ng) {  // (ng is a multiple of 8)
+          const uint4 s4 = SWL[k8 * 16 + cn];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int gl = 8 * k8 + e;
+            acc = fmaf(ap[(size_t)gl * 128], a8_scale(s4, e) * SXL[gl * 8 + cm], acc);
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      wA[k] = wB[k];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qA[k][i] = qB[k][i];
+    }
+  }
+  if (chain) {
+    float* y = j == 0 ? a.y[0] : (j == 1 ? a.y[1] : a.y[2]);
+    const int ldy = j == 0 ? a.ldy[0] : (j == 1 ? a.ldy[1] : a.ldy[2]);
+    y[(size_t)cm * ldy + 16 * mt + cn] = acc;
+  }
+}
+
+// ---- a product with the norm prologue (K = H: one phase of G = 48 groups) ----
+// Block: CG a8 tiles of 16 outputs (CG = 2: the gate tile and the up tile of the same 16 pairs),
+// all M rows, 512 threads.  Wave w multiplies the (column group, chunk) units w + 8k.
+// LDS: U (the prologue's rows [8][A8_XPS], then A32 [48][CG][8][16]), AQ [8][48][4] uint64,
+// SXL [48][8], SWL [CG][6][16] uint4, YL [CG][8][16]
+constexpr int A8_XPS = 1600;  // row stride of the prologue's rows in LDS (16 RMS chains of 100)
+template <int CG>
+constexpr int a8n_ufloats() {
+  return (48 * CG * 8 * 16 > 8 * A8_XPS) ? 48 * CG * 8 * 16 : 8 * A8_XPS;
+}
+template <int CG>
+constexpr size_t a8n_lds() {
+  return (size_t)a8n_ufloats<CG>() * 4 + (size_t)8 * 48 * 4 * 8 + (size_t)48 * 8 * 4 + (size_t)CG * 6 * 16 * 16 +
+         (size_t)CG * 8 * 16 * 4;
+}
+template <int XM, int CG>
+__global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
+  constexpr int G = H / 32, GC4 = G / 4, G8 = G / 8, NU = (CG * GC4 + 7) / 8;
+  extern __shared__ float4 lds4[];
+  float* U = reinterpret_cast<float*>(lds4);
+  uint64_t* AQ = reinterpret_cast<uint64_t*>(U + a8n_ufloats<CG>());
+  float* SXL = reinterpret_cast<float*>(AQ + 8 * G * 4);
+  uint4* SWL = reinterpret_cast<uint4*>(SXL + G * 8);
+  float* YL = reinterpret_cast<float*>(SWL + CG * G8 * 16);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int M = a.M;
+
+  // column group cg: matrix mj (CG = 2: cg itself) and 16-row tile mt (CG = 2: the block)
+  int mj0, mt0;
+  {
+    const int t = blockIdx.x, tl1 = a.mat[0].N / 16, tl2 = tl1 + a.mat[1].N / 16;
+    mj0 = CG == 2 ? 0 : (t >= tl1) + (t >= tl2);
+    mt0 = CG == 2 ? t : t - (mj0 == 0 ? 0 : (mj0 == 1 ? tl1 : tl2));
+  }
+  auto matw = [&](int cg) -> const uint4* {
+    const int j = CG == 2 ? cg : mj0;
+    return (j == 0 ? a.mat[0].w : (j == 1 ? a.mat[1].w : a.mat[2].w)) + (size_t)mt0 * GC4 * 64 + lane;
+  };
+  auto mats = [&](int cg) -> const uint4* {
+    const int j = CG == 2 ? cg : mj0;
+    return (j == 0 ? a.mat[0].s : (j == 1 ? a.mat[1].s : a.mat[2].s)) + (size_t)mt0 * G8 * 16;
+  };
+  // this wave's units u = w + 8k: column group u % CG, chunk u / CG
+  uint4 wA[NU];
+  auto issue_w = [&]() {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = w + 8 * k;
+      if (u < CG * GC4) wA[k] = matw(u % CG)[(size_t)(u / CG) * 64];
+    }
+  };
+  // the tiles' scales: thread f < CG * 96 stages word f % 96 (word k8 of row r) of tile f / 96
+  uint4 swr = make_uint4(0, 0, 0, 0);
+  if (tid < CG * G8 * 16) swr = mats(tid / (G8 * 16))[tid % (G8 * 16)];
+
+  {
+    // E:1358-1361 (mode 1) / E:1375-1378 with E:1390-1404 (mode 2) / E:1375-1377 (mode 3: x1 is
+    // the product's input) for row w, as k_gemv_t's norm prologue forms it; the row goes to U in
+    // plain order (stride A8_XPS).  Rows past M are not formed (their operand words are zero).
+    constexpr int RW4 = H / 4, PER = RW4 / 64;
+    const bool live = w < M;
+    const int mr = min(w, M - 1);
+    const float4* o4 = reinterpret_cast<const float4*>(a.nrm_o) + (size_t)mr * RW4 + lane;
+    const float4* x4 = reinterpret_cast<const float4*>(a.nrm_xin) + (size_t)mr * RW4 + lane;
+    const float4* w14 = reinterpret_cast<const float4*>(a.nrm_w1) + lane;
+    const float4* w24 = reinterpret_cast<const float4*>(a.nrm_w2) + lane;
+    float4 ov[PER], xv[PER];
+    if (live) {
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        ov[k] = o4[64 * k];
+        xv[k] = x4[64 * k];
+      }
+    }
+    issue_w();
+    if (live) {
+      float* XR = U + (size_t)w * A8_XPS;
+      float* CR = XR;  // E:326-345, chains t = e % 16 at 100 t (see k_gemv_t)
+      auto rms_row = [&](const float4 (&v)[PER]) -> float {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+          const float f[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int e = 4 * (lane + 64 * k) + c;
+            CR[(e & 15) * 100 + (e >> 4)] = f[c];
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        double part = 0;
+        if (lane < 16) {
+          const float4* ch = reinterpret_cast<const float4*>(CR + lane * 100);
+#pragma unroll
+          for (int i = 0; i < H / 64; ++i) {
+            const float4 q = ch[i];
+            const double d0 = (double)q.x, d1 = (double)q.y, d2 = (double)q.z, d3 = (double)q.w;
+            part = fma(d0, d0, part);
+            part = fma(d1, d1, part);
+            part = fma(d2, d2, part);
+            part = fma(d3, d3, part);
+          }
+        }
+        const double b2 = part + shl_d<4>(part);
+        const double c2 = b2 + shl_d<8>(b2);
+        const double d2 = c2 + shl_d<2>(c2);
+        const double e2 = d2 + shl_d<1>(d2);
+        const uint64_t u = as_u64(e2);
+        const double ss = as_f64(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 0) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 0));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        return 1.0f / sqrtf((float)(ss / H) + 1e-6f);
+      };
+      const int nmode = a.nrm_mode;
+      const bool after_mlp = nmode == 2;
+      const float scal = a.nrm_scalar;
+      float4 w1[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) w1[k] = w14[64 * k];
+      float4 os[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) os[k] = make_float4(r16(ov[k].x), r16(ov[k].y), r16(ov[k].z), r16(ov[k].w));
+      const float r1 = rms_row(os);
+      float4 x1[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const float4 o = os[k], wv = w1[k], xr = xv[k];
+        float4 v = make_float4(r16(xr.x + r16((o.x * r1) * wv.x)), r16(xr.y + r16((o.y * r1) * wv.y)),
+                               r16(xr.z + r16((o.z * r1) * wv.z)), r16(xr.w + r16((o.w * r1) * wv.w)));
+        if (after_mlp) v = make_float4(r16(v.x * scal), r16(v.y * scal), r16(v.z * scal), r16(v.w * scal));
+        x1[k] = v;
+        if (blockIdx.x == 0) reinterpret_cast<float4*>(a.nrm_xout)[(size_t)w * RW4 + lane + 64 * k] = v;
+      }
+      float4 fin[PER];
+      if constexpr (XM == 1) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) fin[k] = x1[k];
+      } else {
+        float4 w2[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) w2[k] = w24[64 * k];
+        const float r2 = rms_row(x1);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+          const float4 tv = x1[k], wv = w2[k];
+          float4 v = make_float4((tv.x * r2) * wv.x, (tv.y * r2) * wv.y, (tv.z * r2) * wv.z, (tv.w * r2) * wv.w);
+          if (!after_mlp) v = make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w));
+          fin[k] = v;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < PER; ++k) reinterpret_cast<float4*>(XR)[lane + 64 * k] = fin[k];
+    }
+    if (tid < CG * G8 * 16) SWL[tid] = swr;
+    __syncthreads();
+  }
+  // quantise the rows: thread (m, g), rows >= M zero
+  if (tid < 8 * G) {
+    const int m = tid / G, g = tid - m * G;
+    uint64_t* aq = AQ + (size_t)(m * G + g) * 4;
+    if (m < M) {
+      const float4* src = reinterpret_cast<const float4*>(U + (size_t)m * A8_XPS + 32 * g);
+      float v[32];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float4 f = src[k];
+        v[4 * k] = f.x;
+        v[4 * k + 1] = f.y;
+        v[4 * k + 2] = f.z;
+        v[4 * k + 3] = f.w;
+      }
+      uint64_t q[4];
+      SXL[g * 8 + m] = a8_quant_group(v, q);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) aq[h] = q[h];
+    } else {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) aq[h] = 0;
+      SXL[g * 8 + m] = 0.f;
+    }
+  }
+  __syncthreads();
+  // the group dots of this wave's units
+  {
+    const int ar = lane & 15, ah = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = w + 8 * k, cg = u % CG, cl = u / CG;
+      if (u < CG * GC4) {  // (uniform per wave)
+        const uint4 wv = wA[k];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = 4 * cl + i;
+          const uint32_t d = i == 0 ? wv.x : (i == 1 ? wv.y : (i == 2 ? wv.z : wv.w));
+          const uint64_t A = ar < 8 ? AQ[(size_t)(ar * G + g) * 4 + ah] : 0;
+          const i32x4_t D = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)A, a8_wbytes(d), i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+          if (ah < 2) {
+            float* o = U + ((size_t)(g * CG + cg) * 8 + 4 * ah) * 16 + ar;
+            o[0] = (float)D[0];
+            o[16] = (float)D[1];
+            o[32] = (float)D[2];
+            o[48] = (float)D[3];
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // the chains (A8:59): lane (column group, m, n)
+  const int ccg = tid >> 7, cm = (tid >> 4) & 7, cn = tid & 15;
+  const bool chain = tid < CG * 128 && cm < M;
+  float acc = 0.f;
+  if (chain) {
+    const float* ap = U + ((size_t)ccg * 8 + cm) * 16 + cn;
+#pragma unroll
+    for (int k8 = 0; k8 < G8; ++k8) {
+      const uint4 s4 = SWL[(ccg * G8 + k8) * 16 + cn];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int g = 8 * k8 + e;
+        acc = fmaf(ap[(size_t)g * CG * 128], a8_scale(s4, e) * SXL[g * 8 + cm], acc);
+      }
+    }
+  }
+  if constexpr (CG == 2) {  // E:292-299 act = rbf8(rbf8(gelu8(rbf8 g)) * rbf8 u), written staged
+    if (tid < 256) YL[(ccg * 8 + cm) * 16 + cn] = acc;
+    __syncthreads();
+    if (tid < 128 && cm < M) {
+      const float g = YL[cm * 16 + cn], u = YL[(8 + cm) * 16 + cn];
+      a.y[0][(size_t)cm * a.ldy[0] + staged_index(16 * mt0 + cn)] = r16(r16(gelu8(r16(g))) * r16(u));
+    }
+  } else if (chain) {
+    const int n = 16 * mt0 + cn;
+    if constexpr (XM == 1) {  // E:421-427 g2 = r16(r16(gelu8(r16 y)) * r16(pli)), staged
+      a.y[0][(size_t)cm * a.ldy[0] + staged_index(n)] =
+          r16(r16(gelu8(r16(acc))) * r16(a.epi_pli[(size_t)cm * a.epi_pli_ld + n]));
+    } else {
+      const int j = mj0;
+      float* y = j == 0 ? a.y[0] : (j == 1 ? a.y[1] : a.y[2]);
+      const int ldy = j == 0 ? a.ldy[0] : (j == 1 ? a.ldy[1] : a.ldy[2]);
+      y[(size_t)cm * ldy + n] = acc;
+    }
+  }
+}
+
+// mat[j]: a8 tiles (launch_tile_a8) of matrices with N_j % 16 == 0; gateup: mat[0] the gate and
+// mat[1] the up matrix (equal N), y[0] the staged activation.  A product of staged rows (xs)
+// quantises them first into qa / sx (scratch of at least K / 32 * 256 and K / 32 * 32 bytes).
+// Returns the grid of the product (0: refused, nothing launched).
+int launch_gemv_a8(const GemvTArgs& a, uint64_t* qa, float* sx, hipStream_t st) {
+  if (a.M < 1 || a.M > 8 || a.K % 256 || a.mrg_po || a.yperm) return 0;
+  int tiles = 0;
+  for (int j = 0; j < 3; ++j) {
+    if (a.mat[j].N % 16 || (a.mat[j].N && (!a.mat[j].w || !a.mat[j].s))) return 0;
+    tiles += a.mat[j].N / 16;
+  }
+  const dim3 b(512);
+  if (!a.nrm_mode) {
+    if (!a.xs || a.gateup || a.epi_pli || !qa || !sx) return 0;
+    const int G = a.K / 32;
+    hipLaunchKernelGGL(k_a8_quant_rows, dim3((8 * G + 255) / 256), dim3(256), 0, st, a.xs, a.M, a.K, qa, sx);
+    hipLaunchKernelGGL(k_gemv_a8p<A8P_PG>, dim3(tiles), b, a8p_lds<A8P_PG>(), st, a, qa, sx);
+    return tiles;
+  }
+  if (a.K != H) return 0;
+  static bool raised = false;  // the norm variants stage more than 64 KB (gfx950: up to 160 KB on request)
+  if (!raised) {
+    const void* fns[] = {reinterpret_cast<const void*>(&k_gemv_a8n<0, 2>),
+                         reinterpret_cast<const void*>(&k_gemv_a8n<1, 1>),
+                         reinterpret_cast<const void*>(&k_gemv_a8n<0, 1>)};
+    for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 81920);
+    raised = true;
+  }
+  if (a.gateup) {
+    if (a.epi_pli || a.mat[0].N != a.mat[1].N || a.mat[2].N) return 0;
+    const int grid = a.mat[0].N / 16;
+    hipLaunchKernelGGL((k_gemv_a8n<0, 2>), dim3(grid), b, (a8n_lds<2>()), st, a);
+    return grid;
+  }
+  if (a.epi_pli) {
+    if (a.nrm_mode != 3 || a.mat[1].N || a.mat[2].N) return 0;
+    hipLaunchKernelGGL((k_gemv_a8n<1, 1>), dim3(tiles), b, (a8n_lds<1>()), st, a);
+  } else {
+    if (a.nrm_mode == 3) return 0;
+    hipLaunchKernelGGL((k_gemv_a8n<0, 1>), dim3(tiles), b, (a8n_lds<1>()), st, a);
+  }
+  return tiles;
+}
+
+}  // namespace g4v

@@ -142,12 +142,13 @@ def test_gemma_prefill_state_and_caches(orc, gemma, i8):
 
 @pytest.mark.parametrize("kind,pos0,i8", [("chain", 210, False), ("chain", 40, False), ("sibling", 150, False),
                                           ("sibling", 240, False), ("chain", 210, True), ("chain", 40, True),
-                                          ("sibling", 240, True)])
+                                          ("sibling", 240, True), ("chain7", 210, True), ("chain7", 210, False)])
 def test_gemma_multirow_passes(orc, gemma, kind, pos0, i8):
-    """a chain of 3 greedy drafts (split-KV past 192 keys, run_mh below) and the sibling form
-    (nd 2 + the runner-up at RoPE position pos0 + 1, E:1634-1655) after a prefill, against the
-    oracle's rows: committed tokens and the committed row's state.  i8: ENGINE_PREFILL_INT8=1
-    with ENGINE_DECODE_INT8 on (E:1600), W4A8 prompt blocks and verify passes on both sides"""
+    """a chain of 3 greedy drafts (split-KV past 192 keys, run_mh below), of 7 (attn_tile) and the
+    sibling form (nd 2 + the runner-up at RoPE position pos0 + 1, E:1634-1655) after a prefill,
+    against the oracle's rows: committed tokens and the committed row's state.  i8:
+    ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8 on (E:1600), W4A8 prompt blocks and verify
+    passes on both sides"""
     dev, d, fx, ctx = gemma
     prompt = [int(t) for t in np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])[2]][:pos0]
     while len(prompt) < pos0:
@@ -163,17 +164,18 @@ def test_gemma_multirow_passes(orc, gemma, kind, pos0, i8):
         dev.prefill(np.array(prompt, np.int32), 0, 32, 6)
         # greedy chain from the oracle (one-row passes on a copy of the state would move its cache,
         # so the chain is taken as the model's own continuation of a fresh forward per step)
-        if kind == "chain":
+        if kind.startswith("chain"):
+            nd = 7 if kind == "chain7" else 3
             toks = [g0]
-            for j in range(3):
+            for j in range(nd):
                 hh = go.forward(toks[:j + 1], pos0, 6, 0)
                 toks.append(go.greedy(hh[j], toks[:j + 1]))
             hh = go.forward(toks, pos0, 6, 0)
-            G = [go.greedy(hh[m], toks) for m in range(4)]
-            r, h = dev.verify(np.array(toks, np.int32), 3, 0, pos0, 6, hidden=True)
-            note(f"chain at {pos0}: oracle G {G}, device commit {list(r.commit[:r.ncommit])}")
-            assert r.nacc == 3 and list(r.commit[:4]) == G
-            assert same(h, hh[3]), first_diff(h, hh[3])
+            G = [go.greedy(hh[m], toks) for m in range(nd + 1)]
+            r, h = dev.verify(np.array(toks, np.int32), nd, 0, pos0, 6, hidden=True)
+            note(f"chain of {nd} at {pos0}: oracle G {G}, device commit {list(r.commit[:r.ncommit])}")
+            assert r.nacc == nd and list(r.commit[:nd + 1]) == G
+            assert same(h, hh[nd]), first_diff(h, hh[nd])
         else:
             # row 0's greedy token does not depend on the later rows' tokens: take it from a
             # first pass, then put it into the sibling row and a different token into draft 1
