@@ -30,6 +30,11 @@ MODES = {"k3": (3, False, 0, 3, False, 0), "tree": (2, True, 0, 3, False, 0), "n
          "k3_same": (3, False, 0, 3, True, 0), "fake": (3, False, 0, 3, False, 300)}
 
 FX = os.path.join(HERE, "golden", "gemma_layout.npz")
+# the sessions of a setting (same-position drafts, the fake context) and the logit lines are pinned
+# on the first prompt (40 tokens: run_mh in prefill and decode, both head dims); G4V_ORACLE_ALL=1
+# checks every prompt
+ALL = os.environ.get("G4V_ORACLE_ALL") == "1"
+ONE_PROMPT = {"k3_same", "fake"}
 
 
 @pytest.fixture(scope="module")
@@ -69,7 +74,7 @@ def test_gemma_head_logits_match_reference_engine(orc, ckpt):
     m.close()
     P = orc.exp3_pack(E, gl.V, gl.H)
     T, nnew = int(fx["cpus"][0]), int(fx["nnew"][0])
-    for i, p in enumerate(prompts):
+    for i, p in enumerate(prompts if ALL else prompts[:1]):
         want = [str(x) for x in fx[f"gap_{i}"]]
         go = gl.GemmaOracle(orc, d, int(fx["ctx"][0]))
         try:
@@ -114,7 +119,7 @@ def test_gemma_drafting_matches_reference_engine(orc, ckpt, mode):
     try:
         rr = RunReq(orc, gl.GemmaTarget(go, dr), t0=int(fx["cpus"][0]), ngram=ngram, nglen=nglen, samepos=samepos,
                     fake_n=fake_n)
-        for i, p in enumerate(prompts):
+        for i, p in enumerate(prompts if ALL or mode not in ONE_PROMPT else prompts[:1]):
             g0, gen, start = rr.run_req([int(t) for t in p], int(fx["nnew_d"][0]), k, tree)
             assert start == 0 and g0 == int(fx["first_" + mode][i])
             assert gen == [int(t) for t in want[i]], (mode, i, gen, list(want[i]))
