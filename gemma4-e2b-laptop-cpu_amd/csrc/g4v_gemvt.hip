@@ -538,6 +538,129 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(const float* __restrict__ pa,
   }
 }
 
+// One activation row, a product of the staged row (xs; group sums gs, or formed here) and one
+// matrix, K = 2048 NX: the chains of k_gemv_t with their terms formed by eight waves.  A block
+// takes 8 output rows; phase p covers chunks 8p .. 8p+7, and wave s < 8 forms the group terms
+//   a = lo(b_j) xe_j; a = fma(lo(b_8+j), xe_8+j, a); a = fma(hi(b_j), xo_j, a); a = fma(hi(b_8+j), xo_8+j, a)
+// of chunk 8p + s for the 8 rows x 8 chain lanes into LDS, with the groups' scales, while wave 8
+// continues the chains of phase p - 1 from the other buffer: lane (j, r) row = fma(a, sc, row)
+// over the phase's groups in order, and the row's off = fma(sc, gsum, off).  Every value and
+// every rounding is k_gemv_t's (one row per block).
+constexpr int GS_PG = 64;  // groups per phase (8 chunks)
+static size_t gemvs_lds(int K) {
+  const int G = K / 32;
+  return (size_t)G * 9 * 16 + (size_t)G * 4 + (size_t)2 * GS_PG * 64 * 4 + (size_t)2 * GS_PG * 8 * 4 + 64 * 4 + 8 * 4;
+}
+// NX = K / 2048: float4 of the row each of the first 512 threads stages, and phases
+template <int NX>
+__global__ __launch_bounds__(576) void k_gemv_s(const float4* __restrict__ xs, const float* __restrict__ gs,
+                                                W4Tile mat, float* __restrict__ y) {
+  constexpr int K = NX * 2048, G = K / 32, GC = K / 256;
+  extern __shared__ float4 lds4[];
+  float4* XL = lds4;                                    // staged row, float4 u at u + u / 8
+  float* GSL = reinterpret_cast<float*>(XL + G * 9);  // [G]
+  float* AL = GSL + G;                                  // [2][GS_PG][8 j][8 rows]
+  float* SCL = AL + 2 * GS_PG * 64;                     // [2][GS_PG][8 rows]
+  float* RL = SCL + 2 * GS_PG * 8;                      // [8 j][8 rows]
+  float* OFL = RL + 64;                                 // [8 rows]
+  const int tid = threadIdx.x, s = tid >> 6, j = (tid >> 3) & 7, r = tid & 7;
+  const int n0 = blockIdx.x * 8, t64 = n0 >> 6, r64 = (n0 & 63) + r;
+  // this wave's chunk of every phase (8p + s), all in flight from the start
+  uint4 wv[NX], sv[NX];
+  if (s < 8) {
+    const uint4* wp = mat.w + ((size_t)t64 * GC * 8 + j) * 64 + r64;  // chunk c at + 512 c
+    const uint4* sp = mat.s + (size_t)t64 * GC * 64 + r64;             // chunk c at + 64 c
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+      wv[p] = wp[(size_t)(8 * p + s) * 512];
+      sv[p] = sp[(size_t)(8 * p + s) * 64];
+    }
+  }
+  if (tid < 512) {  // the row: every load issued before the first store
+    float4 xr[NX];
+    float gr = 0.f;
+#pragma unroll
+    for (int k = 0; k < NX; ++k) xr[k] = xs[tid + 512 * k];
+    if (gs && tid < G) gr = gs[tid];
+#pragma unroll
+    for (int k = 0; k < NX; ++k) {
+      const int u = tid + 512 * k;
+      XL[u + (u >> 3)] = xr[k];
+    }
+    if (gs && tid < G) GSL[tid] = gr;
+  }
+  __syncthreads();
+  if (!gs) {  // W:22 each group's sequential sum, from the staged copy (G <= 384)
+    if (const int g = tid; g < G) {
+      const float4* q4 = XL + (size_t)g * 9;
+      float4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = q4[i];
+      float sm = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm += (i & 1) ? v[i >> 1].z : v[i >> 1].x;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm += (i & 1) ? v[i >> 1].w : v[i >> 1].y;
+      GSL[g] = sm;
+    }
+    __syncthreads();
+  }
+  const float4* xw = XL + j;  // group g: xw[9 g]
+  float row = 0.f, off = 0.f;
+#pragma unroll
+  for (int p = 0; p <= NX; ++p) {
+    if (s < 8) {
+      if (p < NX) {  // the terms of phase p
+        const int c = 8 * p + s;
+        float* al = AL + (p & 1) * GS_PG * 64;
+        float* scl = SCL + (p & 1) * GS_PG * 8;
+        const uint4 wA = wv[p < NX ? p : 0], sA = sv[p < NX ? p : 0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int k = i >> 1, h = i & 1, g = 8 * c + i, gl = 8 * s + i;
+          const uint32_t dw = k == 0 ? wA.x : (k == 1 ? wA.y : (k == 2 ? wA.z : wA.w));
+          const uint32_t s2 = k == 0 ? sA.x : (k == 1 ? sA.y : (k == 2 ? sA.z : sA.w));
+          uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+          asm volatile("" : "+v"(lo), "+v"(hi));
+          const float l0 = (float)((lo >> (16 * h)) & 0xFFu);
+          const float l1 = (float)((lo >> (16 * h + 8)) & 0xFFu);
+          const float h0 = (float)((hi >> (16 * h)) & 0xFFu);
+          const float h1 = (float)((hi >> (16 * h + 8)) & 0xFFu);
+          const float sc = h ? as_f32(s2 & 0xFFFF0000u) : as_f32(s2 << 16);
+          const float4 x4 = xw[(size_t)g * 9];
+          float av = l0 * x4.x;
+          av = fmaf(l1, x4.y, av);
+          av = fmaf(h0, x4.z, av);
+          av = fmaf(h1, x4.w, av);
+          al[(gl * 8 + j) * 8 + r] = av;
+          if (j == 0) scl[gl * 8 + r] = sc;
+        }
+      }
+    } else if (p >= 1) {  // wave 8: the chains of phase p - 1 (every lane runs its row's off chain)
+      const float* al = AL + ((p - 1) & 1) * GS_PG * 64 + j * 8 + r;
+      const float* scl = SCL + ((p - 1) & 1) * GS_PG * 8 + r;
+      const float* gsp = GSL + GS_PG * (p - 1);
+#pragma unroll 8
+      for (int gl = 0; gl < GS_PG; ++gl) {
+        const float sc = scl[gl * 8];
+        row = fmaf(al[gl * 64], sc, row);
+        off = fmaf(sc, gsp[gl], off);
+      }
+    }
+    __syncthreads();
+  }
+  // the 8 chain lanes of each row meet: ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off
+  if (s == 8) {
+    RL[j * 8 + r] = row;
+    if (j == 0) OFL[r] = off;
+  }
+  __syncthreads();
+  if (tid < 8) {
+    const float* q = RL + tid;
+    y[n0 + tid] = (((q[0] + q[32]) + (q[8] + q[40])) + ((q[16] + q[48]) + (q[24] + q[56]))) - 8.f * OFL[tid];
+  }
+}
+
 // the leading (preloaded) arguments of a launch of k_gemv_t: see the kernel
 struct GemvTLead {
   const float *pa, *pb, *pc, *pd;
@@ -617,6 +740,26 @@ static void launch_mpl(const GemvTDev& d, hipStream_t st, int grid) {
 
 // mpl: activation rows per block (1 to 4); tr: rows per tile (64 or 32)
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
+  // one activation row of a plain product with K >= 1024: the chains' terms formed by 8 waves
+  const int nx = a.K / 2048;
+  if (a.M == 1 && !a.mrg_po && !a.nrm_mode && !a.gateup && !a.epi_pli && !a.yperm && a.xs && a.mat[0].N % 64 == 0 &&
+      a.mat[1].N == 0 && a.mat[2].N == 0 && a.K % 2048 == 0 && (nx == 1 || nx == 2 || nx == 3 || nx == 6)) {
+    const size_t lds = gemvs_lds(a.K);
+    static bool raised = false;  // more than 64 KB for K > 6144 (gfx950: up to 160 KB on request)
+    if (!raised) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_s<6>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                163840);
+      raised = true;
+    }
+    const int grid = a.mat[0].N / 8;
+    switch (nx) {
+      case 1: hipLaunchKernelGGL(k_gemv_s<1>, dim3(grid), dim3(576), lds, st, a.xs, a.gs, a.mat[0], a.y[0]); break;
+      case 2: hipLaunchKernelGGL(k_gemv_s<2>, dim3(grid), dim3(576), lds, st, a.xs, a.gs, a.mat[0], a.y[0]); break;
+      case 3: hipLaunchKernelGGL(k_gemv_s<3>, dim3(grid), dim3(576), lds, st, a.xs, a.gs, a.mat[0], a.y[0]); break;
+      default: hipLaunchKernelGGL(k_gemv_s<6>, dim3(grid), dim3(576), lds, st, a.xs, a.gs, a.mat[0], a.y[0]); break;
+    }
+    return grid;
+  }
   // the prologue register staging holds K <= 6144, and K = 12288 for one activation row per block
   // without a prologue of its own
   if (a.K % 256 || (a.K > 6144 && !(a.K == 12288 && mpl == 1 && !a.nrm_mode && !a.mrg_po && !a.epi_pli)))

@@ -142,10 +142,11 @@ def test_gemma_prefill_state_and_caches(orc, gemma, i8):
 
 @pytest.mark.parametrize("kind,pos0,i8", [("chain", 210, False), ("chain", 40, False), ("sibling", 150, False),
                                           ("sibling", 240, False), ("chain", 210, True), ("chain", 40, True),
-                                          ("sibling", 240, True), ("chain7", 210, True), ("chain7", 210, False)])
+                                          ("sibling", 240, True), ("chain7", 210, True), ("chain7", 210, False),
+                                          ("chain0", 210, False), ("chain0", 40, False)])
 def test_gemma_multirow_passes(orc, gemma, kind, pos0, i8):
-    """a chain of 3 greedy drafts (split-KV past 192 keys, run_mh below), of 7 (attn_tile) and the
-    sibling form (nd 2 + the runner-up at RoPE position pos0 + 1, E:1634-1655) after a prefill,
+    """a chain of 3 greedy drafts (split-KV past 192 keys, run_mh below), of 7 (attn_tile), a one-row
+    pass (no drafts) and the sibling form (nd 2 + the runner-up at RoPE position pos0 + 1, E:1634-1655) after a prefill,
     against the oracle's rows: committed tokens and the committed row's state.  i8:
     ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8 on (E:1600), W4A8 prompt blocks and verify
     passes on both sides"""
@@ -165,7 +166,7 @@ def test_gemma_multirow_passes(orc, gemma, kind, pos0, i8):
         # greedy chain from the oracle (one-row passes on a copy of the state would move its cache,
         # so the chain is taken as the model's own continuation of a fresh forward per step)
         if kind.startswith("chain"):
-            nd = 7 if kind == "chain7" else 3
+            nd = {"chain7": 7, "chain0": 0}.get(kind, 3)
             toks = [g0]
             for j in range(nd):
                 hh = go.forward(toks[:j + 1], pos0, 6, 0)
