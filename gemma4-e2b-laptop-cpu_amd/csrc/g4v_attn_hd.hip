@@ -39,18 +39,29 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
   auto allowed = [=](int p) { return p >= lo && p <= pos && !(p >= sl && p <= sh); };  // E:740
   for (int e = threadIdx.x; e < D; e += NTH) qs[kc_slot_d<D>(e)] = q[(size_t)m * ldq + h * D + e];
   __syncthreads();
-  // scores: 8 lanes per position, NTH / 8 positions per pass
+  // scores: 8 lanes per position, NTH / 8 positions per pass; the next pass's key words are in
+  // flight while this pass's are used
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
-  for (int p0 = c0; p0 < c1; p0 += NTH / 8) {
+  constexpr int KW = D / 64;  // uint4 of a key row per lane (two chains)
+  auto load_k = [&](int p0, uint4 (&kk)[KW]) {
     const int p = min(p0 + ps, c1 - 1);  // the tail's extra lanes repeat the last position
     const uint16_t* kr = KC + (size_t)p * D + l * (D / 8);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int tt = 0; tt < D / 16; tt += 8) kk[c * (D / 128) + tt / 8] = *reinterpret_cast<const uint4*>(kr + c * (D / 16) + tt);
+  };
+  uint4 kA[KW], kB[KW];
+  if (c0 < c1) load_k(c0, kA);
+  for (int p0 = c0; p0 < c1; p0 += NTH / 8) {
+    if (p0 + NTH / 8 < c1) load_k(p0 + NTH / 8, kB);
     float s[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       float a = 0.f;
 #pragma unroll
       for (int tt = 0; tt < D / 16; tt += 8) {
-        const uint4 kk = *reinterpret_cast<const uint4*>(kr + c * (D / 16) + tt);
+        const uint4 kk = kA[c * (D / 128) + tt / 8];
         const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -61,7 +72,10 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
       s[c] = a;
     }
     const float v = hsum8_lanes(s[0] + s[1]);
+    const int p = min(p0 + ps, c1 - 1);
     if (l == 0 && p0 + ps < c1) sw[p - pa] = v;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) kA[k] = kB[k];
   }
   __syncthreads();
   // the max over the allowed positions (order free)
@@ -87,19 +101,36 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
   const int d = threadIdx.x;
   const uint16_t* vcol = VC + (size_t)d * 8;
   float o = 0.f, lsum = 0.f;
-  for (int j8 = 0; j8 < pe - pa; j8 += 8) {
-    const int p8 = pa + j8;  // 8-aligned: the 8 positions of dim d are 16 contiguous bytes
-    const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (size_t)((p8 >> 3) & 3) * (8 * D));
-    const float4 wa = *reinterpret_cast<const float4*>(&sw[j8]);
-    const float4 wb = *reinterpret_cast<const float4*>(&sw[j8 + 4]);
-    const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-    const uint32_t u4[4] = {vq.x, vq.y, vq.z, vq.w};
+  // the value words of 8 positions of dim d (16 contiguous bytes of the cache), VR steps in flight
+  constexpr int VR = 8;
+  const int n8 = (pe - pa) / 8;
+  auto load_v = [&](int j) {
+    const int p8 = pa + 8 * j;
+    return *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (size_t)((p8 >> 3) & 3) * (8 * D));
+  };
+  uint4 ring[VR];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t u = u4[k >> 1];
-      const float vv = w8[k] != 0.f ? as_f32((k & 1) ? (u & 0xFFFF0000u) : (u << 16)) : 0.f;
-      o = fmaf(w8[k], vv, o);
-      lsum = lsum + w8[k];
+  for (int i = 0; i < VR; ++i)
+    if (i < n8) ring[i] = load_v(i);
+  for (int jb = 0; jb < n8; jb += VR) {
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      if (jb + i < n8) {  // (uniform)
+        const uint4 vq = ring[i];
+        if (jb + VR + i < n8) ring[i] = load_v(jb + VR + i);
+        const int j8 = 8 * (jb + i);
+        const float4 wa = *reinterpret_cast<const float4*>(&sw[j8]);
+        const float4 wb = *reinterpret_cast<const float4*>(&sw[j8 + 4]);
+        const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        const uint32_t u4[4] = {vq.x, vq.y, vq.z, vq.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t u = u4[k >> 1];
+          const float vv = w8[k] != 0.f ? as_f32((k & 1) ? (u & 0xFFFF0000u) : (u << 16)) : 0.f;
+          o = fmaf(w8[k], vv, o);
+          lsum = lsum + w8[k];
+        }
+      }
     }
   }
   const size_t k = ((size_t)t * M + m) * NQ + h;
