@@ -67,6 +67,23 @@ def hbm_traffic(cls):
     return None
 
 
+def trace_avg_us(cls):
+    """the average device duration of kernel class `cls` in the committed rocprofv3 kernel trace of
+    this bench (profiles/verify_step_kernels.md, table `class | kernel | launches | avg us`); None
+    when the class is not listed"""
+    path = os.path.join(ROOT, "profiles", "verify_step_kernels.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 4 and cells[0] == cls:
+            try:
+                return float(cells[3])
+            except ValueError:
+                return None
+    return None
+
+
 def load_g4v():
     spec = importlib.util.spec_from_file_location("g4v", os.path.join(ROOT, "gemma4-e2b-laptop-cpu_amd", "g4v.py"))
     mod = importlib.util.module_from_spec(spec)
@@ -257,6 +274,24 @@ GM_MLP = [6144 if l < 15 else 12288 for l in range(35)]  # the checkpoint's MLP 
 GM_CTX = 2048
 
 
+def gemma_pass_bytes(M, pos0=GM_CTX):
+    """algorithmic bytes of one verify pass of M rows at pos0 on the Gemma-4-E2B layout: every
+    layer's int4 matrices with their bf16 group scales (q/k/v of the owner layers, o, gate, up,
+    down, the per-layer-input gate and projection), the per-layer-input projection and the rows'
+    per-layer embeddings, the head screen, and the K / V rows each layer attends (window 512 for
+    head dim 256, the whole context for 512)"""
+    q4 = lambda n, k: n * k // 2 + n * k // 16
+    b = q4(35 * 256, H) + M * 35 * 256 * 2 + SCREEN_BYTES
+    for l in range(35):
+        hd = 512 if l % 5 == 4 else 256
+        b += q4(8 * hd, H) + q4(H, 8 * hd) + 2 * q4(GM_MLP[l], H) + q4(H, GM_MLP[l]) + q4(256, H) + q4(H, 256)
+        if l < 15:
+            b += 2 * q4(hd, H)
+        npos = pos0 + M if hd == 512 else min(pos0 + M, 512 + M - 1)
+        b += npos * hd * 2 * 2
+    return b
+
+
 def gemma_layout_summary(g4v, reps=10):
     """verify passes on the Gemma-4-E2B layer layout at the checkpoint's sizes (device-generated
     weights): a 2048-token context prefilled with W4A8 blocks, then one-row decode passes and
@@ -285,7 +320,10 @@ def gemma_layout_summary(g4v, reps=10):
         for _ in range(reps):
             dev.verify(blk, M - 1, 0, GM_CTX, 6)
         dev.sync()
-        out[f"verify_{M}_rows{'_w4a8' if i8 else ''}_ms"] = round((time.perf_counter() - t0) * 1e3 / reps, 3)
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        out[f"verify_{M}_rows{'_w4a8' if i8 else ''}_ms"] = round(ms, 3)
+        out[f"verify_{M}_rows{'_w4a8' if i8 else ''}_hbm_frac"] = round(
+            gemma_pass_bytes(M) / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)
     dev.set_decode_int8(False)
     dev.close()
     return out
@@ -438,6 +476,12 @@ def main():
         "kernel_classes_us_per_step": classes,
         "setup_s": round(setup_s, 1),
     }
+    tus = trace_avg_us(dominant)
+    if tus:  # the same bytes over the kernel's device duration in the committed trace (no launch overhead)
+        out["roofline"].update({"trace_us": tus, "trace_achieved": round(per_launch_bytes / (tus * 1e-6) / 1e9, 1),
+                                "trace_frac": round(per_launch_bytes / (tus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "trace_source": "profiles/verify_step_kernels.md (rocprofv3 --kernel-trace --stats "
+                                                "of this bench, device kernel durations)"})
     # the device's streaming bandwidth beside the 8 TB/s peak (bench/stream_bw.cpp:10-19 method)
     out["hbm_stream"] = {"read_gbs": round(dev.hbm_stream(2 << 30, 5), 1),
                          "copy_gbs": round(dev.hbm_stream(1 << 30, 5, copy=True), 1), "read_buffer": 2 << 30,
