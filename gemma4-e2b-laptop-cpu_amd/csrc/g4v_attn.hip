@@ -316,19 +316,6 @@ __device__ __forceinline__ void row_norm_rope(float (&x)[16], const float (&w)[1
   }
 }
 
-// Range-checked 16-byte loads through a buffer resource: a lane whose offset lies past the
-// resource's num_records bytes reads zeros and moves no data (the key / value streams read
-// exactly their split, without clamped duplicate fetches).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-  uint4 u;
-  __builtin_memcpy(&u, &v, 16);
-  return u;
-}
-
 // 16 floats of a lane: four 16-byte words at p
 __device__ __forceinline__ void load16(float (&x)[16], const float* p) {
   const float4* p4 = reinterpret_cast<const float4*>(p);

@@ -27,42 +27,44 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
   constexpr int NTH = D;
   const AttnGeom& g = gp ? *gp : gv;
   __shared__ __align__(16) float qs[D];                   // the head's query in key-slot order
-  __shared__ __align__(16) float sw[ATT_SPLIT_MAX + 16];  // scores, then weights, from position pa
+  constexpr int SW_PAD = ATT_SPLIT_MAX + 80;  // slots [0, SW_PAD): scores, then weights, from pa
+  __shared__ __align__(16) float sw[SW_PAD + 64];
   __shared__ float red[NTH / 64];
   const int t = blockIdx.x, m = blockIdx.y, h = blockIdx.z, T = g.T;
   const int M = g.M;
   if (m >= M) return;  // uniform
   const int len = g.kmax - g.kmin + 1;
-  const int c0 = g.kmin + (int)((long)t * len / T), c1 = g.kmin + (int)((long)(t + 1) * len / T);
+  // (uniform; readfirstlane says so, so that the loops below count in scalar registers)
+  const int c0 = __builtin_amdgcn_readfirstlane(g.kmin + (int)((long)t * len / T));
+  const int c1 = __builtin_amdgcn_readfirstlane(g.kmin + (int)((long)(t + 1) * len / T));
   const int pa = c0 & ~7, pe = (c1 + 7) & ~7;
   const int lo = g.lo[m], pos = g.pos[m], sl = g.skip_lo[m], sh = g.skip_hi[m];
   auto allowed = [=](int p) { return p >= lo && p <= pos && !(p >= sl && p <= sh); };  // E:740
   for (int e = threadIdx.x; e < D; e += NTH) qs[kc_slot_d<D>(e)] = q[(size_t)m * ldq + h * D + e];
   __syncthreads();
-  // scores: 8 lanes per position, NTH / 8 positions per pass; the next pass's key words are in
-  // flight while this pass's are used
+  // scores: 8 lanes per position, NP = NTH / 8 positions per pass, the key words of KR passes in
+  // flight.  The keys are read through a resource over rows [0, c1): a lane past c1 reads zeros
+  // and its score is not stored, so the ring runs without branches (a pass past the split only
+  // computes)
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
-  constexpr int KW = D / 64;  // uint4 of a key row per lane (two chains)
+  constexpr int KW = D / 64, NP = NTH / 8, KR = 4;  // uint4 of a key row per lane (two chains)
+  const __amdgpu_buffer_rsrc_t krs = buf_rsrc(KC, (uint32_t)c1 * (D * 2));
   auto load_k = [&](int p0, uint4 (&kk)[KW]) {
-    const int p = min(p0 + ps, c1 - 1);  // the tail's extra lanes repeat the last position
-    const uint16_t* kr = KC + (size_t)p * D + l * (D / 8);
+    const uint32_t off = ((uint32_t)(p0 + ps) * D + l * (D / 8)) * 2;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int tt = 0; tt < D / 16; tt += 8) kk[c * (D / 128) + tt / 8] = *reinterpret_cast<const uint4*>(kr + c * (D / 16) + tt);
+      for (int tt = 0; tt < D / 16; tt += 8) kk[c * (D / 128) + tt / 8] = buf_load16(krs, off + (c * (D / 16) + tt) * 2);
   };
-  uint4 kA[KW], kB[KW];
-  if (c0 < c1) load_k(c0, kA);
-  for (int p0 = c0; p0 < c1; p0 += NTH / 8) {
-    if (p0 + NTH / 8 < c1) load_k(p0 + NTH / 8, kB);
+  auto score = [&](int p0, const uint4 (&kk)[KW]) {
     float s[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       float a = 0.f;
 #pragma unroll
       for (int tt = 0; tt < D / 16; tt += 8) {
-        const uint4 kk = kA[c * (D / 128) + tt / 8];
-        const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+        const uint4 k4 = kk[c * (D / 128) + tt / 8];
+        const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           a = fmaf(qs[l * (D / 8) + c * (D / 16) + tt + 2 * k], as_f32(kw[k] << 16), a);
@@ -72,10 +74,24 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
       s[c] = a;
     }
     const float v = hsum8_lanes(s[0] + s[1]);
-    const int p = min(p0 + ps, c1 - 1);
-    if (l == 0 && p0 + ps < c1) sw[p - pa] = v;
+    // lane 0 of a position's 8 holds its score; the other lanes and the positions past c1 write
+    // pad slots past every slot read (no branch in the ring's loop)
+    sw[(l == 0 && p0 + ps < c1) ? p0 + ps - pa : SW_PAD + (threadIdx.x & 63)] = v;
+  };
+  uint4 kr[KR][KW];
 #pragma unroll
-    for (int k = 0; k < KW; ++k) kA[k] = kB[k];
+  for (int i = 0; i < KR; ++i) {  // in slot order, as the loop reloads them
+    load_k(c0 + i * NP, kr[i]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int p0 = c0; p0 < c1; p0 += KR * NP) {
+#pragma unroll
+    for (int i = 0; i < KR; ++i) {
+      score(p0 + i * NP, kr[i]);
+      __builtin_amdgcn_sched_barrier(0);  // the slot is used before its next load
+      load_k(p0 + (i + KR) * NP, kr[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   __syncthreads();
   // the max over the allowed positions (order free)
@@ -89,8 +105,10 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
 #pragma unroll
   for (int w = 1; w < NTH / 64; ++w) mx = fmaxf(mx, red[w]);
   // weights exp8(score - max) of the allowed positions (E:820), 0 for every other slot of
-  // [pa, pe); each thread rewrites only the slots it reads
-  for (int j = threadIdx.x; j < pe - pa; j += NTH) {
+  // [pa, pa + 8 nv); each thread rewrites only the slots it reads
+  constexpr int VR = 8;  // value steps in flight
+  const int n8 = (pe - pa) / 8, nv = (n8 + VR - 1) / VR * VR;  // 8 nv <= ATT_SPLIT_MAX + 69
+  for (int j = threadIdx.x; j < 8 * nv; j += NTH) {
     const int p = pa + j;
     sw[j] = (p >= c0 && p < c1 && allowed(p)) ? exp8(sw[j] - mx) : 0.f;
   }
@@ -99,37 +117,41 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
   // a zero weight (not allowed, outside the split) leaves both unchanged: its value is taken
   // as +0 and o is never -0
   const int d = threadIdx.x;
-  const uint16_t* vcol = VC + (size_t)d * 8;
   float o = 0.f, lsum = 0.f;
-  // the value words of 8 positions of dim d (16 contiguous bytes of the cache), VR steps in flight
-  constexpr int VR = 8;
-  const int n8 = (pe - pa) / 8;
+  // the value words of 8 positions of dim d (16 contiguous bytes of the cache), VR steps in
+  // flight with no branch between a load and its use, through a resource over the cache parts
+  // of 32 positions up to the one holding pe - 1 (within the slab); the steps past n8 weigh 0
+  const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(VC, (uint32_t)(((pe - 1) >> 5) + 1) * (32 * D * 2));
   auto load_v = [&](int j) {
     const int p8 = pa + 8 * j;
-    return *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (size_t)((p8 >> 3) & 3) * (8 * D));
+    return buf_load16(vrs, (uint32_t)((p8 >> 5) * (32 * D) + ((p8 >> 3) & 3) * (8 * D)) * 2 + d * 16);
   };
   uint4 ring[VR];
 #pragma unroll
-  for (int i = 0; i < VR; ++i)
-    if (i < n8) ring[i] = load_v(i);
-  for (int jb = 0; jb < n8; jb += VR) {
+  for (int i = 0; i < VR; ++i) {  // in slot order, as the loop reloads them
+    ring[i] = load_v(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int jb = 0; jb < nv; jb += VR) {
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
-      if (jb + i < n8) {  // (uniform)
-        const uint4 vq = ring[i];
-        if (jb + VR + i < n8) ring[i] = load_v(jb + VR + i);
-        const int j8 = 8 * (jb + i);
-        const float4 wa = *reinterpret_cast<const float4*>(&sw[j8]);
-        const float4 wb = *reinterpret_cast<const float4*>(&sw[j8 + 4]);
-        const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-        const uint32_t u4[4] = {vq.x, vq.y, vq.z, vq.w};
+      // the slot's words are unpacked before its next load is issued into the same registers
+      const uint32_t u4[4] = {ring[i].x, ring[i].y, ring[i].z, ring[i].w};
+      float v8[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t u = u4[k >> 1];
-          const float vv = w8[k] != 0.f ? as_f32((k & 1) ? (u & 0xFFFF0000u) : (u << 16)) : 0.f;
-          o = fmaf(w8[k], vv, o);
-          lsum = lsum + w8[k];
-        }
+      for (int k = 0; k < 8; ++k) v8[k] = as_f32((k & 1) ? (u4[k >> 1] & 0xFFFF0000u) : (u4[k >> 1] << 16));
+      __builtin_amdgcn_sched_barrier(0);
+      ring[i] = load_v(jb + VR + i);
+      __builtin_amdgcn_sched_barrier(0);
+      const int j8 = 8 * (jb + i);
+      const float4 wa = *reinterpret_cast<const float4*>(&sw[j8]);
+      const float4 wb = *reinterpret_cast<const float4*>(&sw[j8 + 4]);
+      const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float vv = w8[k] != 0.f ? v8[k] : 0.f;
+        o = fmaf(w8[k], vv, o);
+        lsum = lsum + w8[k];
       }
     }
   }

@@ -64,6 +64,21 @@ __host__ __device__ __forceinline__ int staged_index(int n) {
   return (g * 8 + (e >> 1)) * 4 + ((e & 1) ? 2 : 0) + (i >> 4);
 }
 
+// Range-checked 16-byte loads through a buffer resource: a lane whose offset lies past the
+// resource's num_records bytes reads zeros and moves no data (a stream reads exactly its range,
+// without clamped duplicate fetches).  The base must be uniform over the wave.  Being intrinsic
+// calls rather than plain loads, a ring of them carried across a loop's back edge stays a ring
+// (plain loads there get folded into loads at the top of the next iteration).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  uint4 u;
+  __builtin_memcpy(&u, &v, 16);
+  return u;
+}
+
 // lane n of a 16-lane row takes lane n + N of the row (row_shl:N; lanes past the row get 0)
 template <int N>
 __device__ __forceinline__ float shl_f(float v) {

@@ -442,13 +442,15 @@ __global__ __launch_bounds__(D) void k_pf_attn_rows(const float* __restrict__ S,
     __syncthreads();
     den = dens;
   }
-  const uint16_t* vcol = VC + (size_t)d * 8;
+  // the cache parts of 32 positions up to the one holding P (within the slab of kv_cap positions)
+  const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(VC, (uint32_t)((P >> 5) + 1) * (32 * D * 2));
   float O = 0.f;
   for (int c0 = pa; c0 < pend; c0 += PF_RC) {
+    constexpr int VR = 8;  // value steps in flight
     const int cn = min(PF_RC, pend - c0);
-    const int cn8 = (cn + 7) & ~7;
+    const int n8 = (cn + 7) >> 3, nv = (n8 + VR - 1) / VR * VR;  // steps of 8 positions; 8 nv <= PF_RC
     __syncthreads();  // the previous chunk is used
-    for (int j = d; j < cn8; j += D) {
+    for (int j = d; j < 8 * nv; j += D) {
       const int p = c0 + j;
       float v = 0.f;
       if (j < cn && p >= lo && pf_valid(r, P, p, g)) {
@@ -458,27 +460,45 @@ __global__ __launch_bounds__(D) void k_pf_attn_rows(const float* __restrict__ S,
       w[j] = v;
     }
     __syncthreads();
-    for (int j8 = 0; j8 < cn8; j8 += 8) {
-      const int p8 = c0 + j8;
-      const uint4 vq = *reinterpret_cast<const uint4*>(vcol + (size_t)(p8 >> 5) * (32 * D) + (size_t)((p8 >> 3) & 3) * (8 * D));
-      const float4 wa = *reinterpret_cast<const float4*>(&w[j8]);
-      const float4 wb = *reinterpret_cast<const float4*>(&w[j8 + 4]);
-      const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-      const uint32_t u4[4] = {vq.x, vq.y, vq.z, vq.w};
+    // the value words of 8 positions of dim d (16 contiguous bytes of the cache), VR steps in
+    // flight with no branch between a load and its use; the steps past n8 read positions past P
+    // (zeros beyond P's 32-position part, stale words within it) and weigh 0.  attn_tile's den =
+    // the sum of the weights in position order runs in every lane beside the value chain (the
+    // zero weights leave it unchanged)
+    auto load_v = [&](int j) {
+      const int p8 = c0 + 8 * j;
+      return buf_load16(vrs, (uint32_t)((p8 >> 5) * (32 * D) + ((p8 >> 3) & 3) * (8 * D)) * 2 + d * 16);
+    };
+    uint4 ring[VR];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t u = u4[k >> 1];
-        const float vv = w8[k] != 0.f ? as_f32((k & 1) ? (u & 0xFFFF0000u) : (u << 16)) : 0.f;
-        O = fmaf(w8[k], vv, O);
+    for (int i = 0; i < VR; ++i) {  // in slot order, as the loop reloads them
+      ring[i] = load_v(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int jb = 0; jb < nv; jb += VR) {
+#pragma unroll
+      for (int i = 0; i < VR; ++i) {
+        // the slot's words are unpacked before its next load is issued into the same registers
+        // (a value live across that load would make the ring rotate through copies)
+        const uint32_t u4[4] = {ring[i].x, ring[i].y, ring[i].z, ring[i].w};
+        float v8[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v8[k] = as_f32((k & 1) ? (u4[k >> 1] & 0xFFFF0000u) : (u4[k >> 1] << 16));
+        __builtin_amdgcn_sched_barrier(0);
+        ring[i] = load_v(jb + VR + i);
+        __builtin_amdgcn_sched_barrier(0);  // issued here, VR steps ahead of its use
+        const int j8 = 8 * (jb + i);
+        const float4 wa = *reinterpret_cast<const float4*>(&w[j8]);
+        const float4 wb = *reinterpret_cast<const float4*>(&w[j8 + 4]);
+        const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float vv = w8[k] != 0.f ? v8[k] : 0.f;
+          O = fmaf(w8[k], vv, O);
+          if (tiled) den = den + w8[k];
+        }
       }
     }
-    if (tiled && d == 0)
-      for (int j = 0; j < cn; ++j) den = den + w[j];
-  }
-  if (tiled) {
-    if (d == 0) dens = den;
-    __syncthreads();
-    den = dens;
   }
   const float y = tiled ? r16(O * (1.0f / den)) : r16(O);
   float* orow = att + (size_t)r * NQ * D;
