@@ -292,12 +292,19 @@ def gemma_pass_bytes(M, pos0=GM_CTX):
     return b
 
 
-def gemma_layout_summary(g4v, reps=10):
+GM_SHAPES = ((1, False), (4, False), (8, False), (4, True), (8, True))
+
+
+def gemma_layout_summary(g4v, reps=10, shapes=GM_SHAPES, graphs=True):
     """verify passes on the Gemma-4-E2B layer layout at the checkpoint's sizes (device-generated
     weights): a 2048-token context prefilled with W4A8 blocks, then one-row decode passes and
     chain passes of 3 and 7 drafts at position 2048 (the passes re-run at the same position), in
-    exact float and, for the chains, with W4A8 products (ENGINE_DECODE_INT8, the server's mode)"""
+    exact float and, for the chains, with W4A8 products (ENGINE_DECODE_INT8, the server's mode).
+    shapes: (rows, W4A8) of the passes timed; graphs = False launches their kernels eagerly (for a
+    kernel trace: the tracer follows graph replays less reliably)"""
     dev = g4v.Device(0)
+    if not graphs:
+        dev.set_graphs(False)
     dev.model_synth_gemma(SEED + 7, V, GM_MLP, 4096)
     dev.set_prefill_int8(True)
     rng = np.random.default_rng(11)
@@ -310,7 +317,7 @@ def gemma_layout_summary(g4v, reps=10):
     out = {"workload": f"Gemma-4-E2B layout (35 layers, head dim 256 / 512, KV shared past layer 14, MLP 6144 / "
                        f"12288, per-layer inputs, V {V}), context {GM_CTX}, 6 KV splits",
            "prefill_ms": round((time.perf_counter() - t0) * 1e3, 2)}
-    for M, i8 in ((1, False), (4, False), (8, False), (4, True), (8, True)):
+    for M, i8 in shapes:
         dev.set_decode_int8(i8)
         blk = rng.integers(0, V, M).astype(np.int32)
         for _ in range(2):
@@ -381,6 +388,9 @@ def main():
     ap.add_argument("--cpu-only", default=None, help=argparse.SUPPRESS)  # child process of the CPU baseline
     ap.add_argument("--no-long-prompt", action="store_true", help="skip the long-prompt sub-measurement")
     ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-E2B layout sub-measurement")
+    ap.add_argument("--gemma-shapes", default=None,
+                    help="gemma_layout: the passes to time, e.g. 1,4,8,4i8,8i8 (rows; i8: W4A8 products)")
+    ap.add_argument("--no-graphs", action="store_true", help="gemma_layout: launch the passes' kernels eagerly")
     args = ap.parse_args()
     if args.cpu_only is not None:
         print(json.dumps(cpu_baseline_run([int(c) for c in args.cpu_only.split(",")])), flush=True)
@@ -393,7 +403,11 @@ def main():
         main_long_prompt(args, load_g4v())
         return
     if args.workload == "gemma_layout":  # the Gemma-4-E2B layout's passes alone (its sub-object as a line)
-        print(json.dumps(gemma_layout_summary(load_g4v())), flush=True)
+        shapes = GM_SHAPES
+        if args.gemma_shapes:
+            shapes = tuple((int(t[:-2] if t.endswith("i8") else t), t.endswith("i8"))
+                           for t in args.gemma_shapes.split(","))
+        print(json.dumps(gemma_layout_summary(load_g4v(), shapes=shapes, graphs=not args.no_graphs)), flush=True)
         return
 
     g4v = load_g4v()
