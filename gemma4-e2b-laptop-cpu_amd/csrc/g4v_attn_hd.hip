@@ -49,12 +49,12 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
   const int ps = threadIdx.x >> 3, l = threadIdx.x & 7;
   constexpr int KW = D / 64, NP = NTH / 8, KR = 4;  // uint4 of a key row per lane (two chains)
   const __amdgpu_buffer_rsrc_t krs = buf_rsrc(KC, (uint32_t)c1 * (D * 2));
+  static_assert(D == 512, "the key slot layout read here is kc_slot_d<512>'s");
+  // lane l's word k (chain k / 4, steps 8 (k % 4) .. + 7) is 16-byte word 8 k + l of the row
   auto load_k = [&](int p0, uint4 (&kk)[KW]) {
-    const uint32_t off = ((uint32_t)(p0 + ps) * D + l * (D / 8)) * 2;
+    const uint32_t off = (uint32_t)(p0 + ps) * (D * 2) + l * 16;
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int tt = 0; tt < D / 16; tt += 8) kk[c * (D / 128) + tt / 8] = buf_load16(krs, off + (c * (D / 16) + tt) * 2);
+    for (int k = 0; k < KW; ++k) kk[k] = buf_load16(krs, off + k * 128);
   };
   auto score = [&](int p0, const uint4 (&kk)[KW]) {
     float s[2];
@@ -66,9 +66,9 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
         const uint4 k4 = kk[c * (D / 128) + tt / 8];
         const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          a = fmaf(qs[l * (D / 8) + c * (D / 16) + tt + 2 * k], as_f32(kw[k] << 16), a);
-          a = fmaf(qs[l * (D / 8) + c * (D / 16) + tt + 2 * k + 1], as_f32(kw[k] & 0xFFFF0000u), a);
+        for (int k = 0; k < 4; ++k) {  // the query in the same slots: kc_slot_d of step tt + 2 k (+ 1)
+          a = fmaf(qs[64 * (4 * c + tt / 8) + 8 * l + 2 * k], as_f32(kw[k] << 16), a);
+          a = fmaf(qs[64 * (4 * c + tt / 8) + 8 * l + 2 * k + 1], as_f32(kw[k] & 0xFFFF0000u), a);
         }
       }
       s[c] = a;

@@ -30,10 +30,19 @@ __host__ __device__ inline size_t vc_index(int p, int i) {
   return (size_t)(p >> 5) * (32 * HD) + (size_t)((p >> 3) & 3) * (8 * HD) + (size_t)i * 8 + (p & 7);
 }
 inline int kv_cap(int npos) { return (npos + 31) / 32 * 32; }  // positions of a layer's cache slab
-// the same layouts for a head dim D (256 or 512: the global layers of the Gemma-4-E2B layout):
-// element e = 16 tt + 8 s + l (tt < D / 16) of a key row at slot l * D / 8 + s * D / 16 + tt
+// the same layouts for a head dim D (256 or 512: the global layers of the Gemma-4-E2B layout).
+// Keys, D = 256: as above.  D = 512: element e = 16 tt + 8 s + l (tt < 32) at slot
+// 64 (4 s + tt / 8) + 8 l + tt % 8, i.e. lane l's k-th 16 bytes (k = 4 s + tt / 8, the 8 steps
+// tt of chain s from 8 (k % 4)) are 16-byte word 8 k + l of the row: the 8 lanes scoring a
+// position read 128 contiguous bytes per load, 8 loads a row.  In both, the 8 steps of a chain
+// from a multiple of 8 are 8 contiguous slots.
 template <int D>
-__host__ __device__ inline int kc_slot_d(int e) { return (e & 7) * (D / 8) + ((e >> 3) & 1) * (D / 16) + (e >> 4); }
+__host__ __device__ inline int kc_slot_d(int e) {
+  if constexpr (D == 512)
+    return (4 * ((e >> 3) & 1) + (e >> 7)) * 64 + (e & 7) * 8 + ((e >> 4) & 7);
+  else
+    return (e & 7) * (D / 8) + ((e >> 3) & 1) * (D / 16) + (e >> 4);
+}
 template <int D>
 __host__ __device__ inline size_t kc_index_d(int p, int e) { return (size_t)p * D + kc_slot_d<D>(e); }
 template <int D>

@@ -159,20 +159,22 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
   if (p > P) return;  // no barrier follows
   const uint16_t* kr = KC + (size_t)p * D;
   constexpr int CL = D / 16;  // steps of one chain
+  // sb(l, s, c8): the slot of step 8 c8 of chain (l, s), element 128 c8 + 8 s + l, the first of
+  // 8 contiguous slots holding steps 8 c8 .. 8 c8 + 7 (kc_slot_d, either head dim)
+  auto sb = [](int l, int s, int c8) { return kc_slot_d<D>(128 * c8 + 8 * s + l); };
   float vv[NQ][8];
   if (tiled) {
-    // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...]: slots l*D/8 + s*D/16 + tt, tt in
-    // order; vv[h][l] = chain (l, 0) + chain (l, 1)
+    // chain (l, s) = sum over tt of q[16 tt + 8 s + l] k[...], tt in order; vv[h][l] = chain
+    // (l, 0) + chain (l, 1)
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       float ch[NQ][2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int b = l * (D / 8) + s * CL;
         float kf[CL];
 #pragma unroll
         for (int c8 = 0; c8 < CL / 8; ++c8) {
-          const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c8);
+          const uint4 kk = *reinterpret_cast<const uint4*>(kr + sb(l, s, c8));
           const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
@@ -182,15 +184,18 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
         }
 #pragma unroll
         for (int h = 0; h < NQ; ++h) {
-          const float4* q4 = reinterpret_cast<const float4*>(&qs[h][b]);
           float a = 0.f;
 #pragma unroll
-          for (int c = 0; c < CL / 4; ++c) {
-            const float4 qq = q4[c];
-            a = fmaf(qq.x, kf[4 * c], a);
-            a = fmaf(qq.y, kf[4 * c + 1], a);
-            a = fmaf(qq.z, kf[4 * c + 2], a);
-            a = fmaf(qq.w, kf[4 * c + 3], a);
+          for (int c8 = 0; c8 < CL / 8; ++c8) {
+            const float4* q4 = reinterpret_cast<const float4*>(&qs[h][sb(l, s, c8)]);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              const float4 qq = q4[c];
+              a = fmaf(qq.x, kf[8 * c8 + 4 * c], a);
+              a = fmaf(qq.y, kf[8 * c8 + 4 * c + 1], a);
+              a = fmaf(qq.z, kf[8 * c8 + 4 * c + 2], a);
+              a = fmaf(qq.w, kf[8 * c8 + 4 * c + 3], a);
+            }
           }
           ch[h][s] = a;
         }
@@ -199,29 +204,30 @@ __global__ __launch_bounds__(256) void k_pf_scores(const float* __restrict__ q, 
       for (int h = 0; h < NQ; ++h) vv[h][l] = ch[h][0] + ch[h][1];
     }
   } else {
-    // chain l over t = 0 .. D/8 - 1 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l:
-    // slots l*D/8 + (t & 1)*D/16 + (t >> 1)
+    // chain l over t = 0 .. D/8 - 1 of element 8 t + l = 16 (t >> 1) + 8 (t & 1) + l: chain
+    // (l, t & 1)'s step t >> 1; kf[s CL + tt] holds step tt of chain (l, s)
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
-      const int b = l * (D / 8);
       float kf[D / 8];
 #pragma unroll
-      for (int c8 = 0; c8 < D / 64; ++c8) {
-        const uint4 kk = *reinterpret_cast<const uint4*>(kr + b + 8 * c8);
-        const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          kf[8 * c8 + 2 * c] = as_f32(kw[c] << 16);
-          kf[8 * c8 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+        for (int c8 = 0; c8 < CL / 8; ++c8) {
+          const uint4 kk = *reinterpret_cast<const uint4*>(kr + sb(l, s, c8));
+          const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            kf[s * CL + 8 * c8 + 2 * c] = as_f32(kw[c] << 16);
+            kf[s * CL + 8 * c8 + 2 * c + 1] = as_f32(kw[c] & 0xFFFF0000u);
+          }
         }
-      }
 #pragma unroll
       for (int h = 0; h < NQ; ++h) {
         float a = 0.f;
 #pragma unroll
         for (int t = 0; t < D / 8; ++t) {
-          const int sl = (t & 1) * CL + (t >> 1);
-          a = fmaf(qs[h][b + sl], kf[sl], a);
+          const int s = t & 1, tt = t >> 1;
+          a = fmaf(qs[h][sb(l, s, tt >> 3) + (tt & 7)], kf[s * CL + tt], a);
         }
         vv[h][l] = a;
       }
