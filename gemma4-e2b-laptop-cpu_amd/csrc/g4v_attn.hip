@@ -271,9 +271,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(AttnPtrs P, AttnGeom
 // 16 lanes meet through data-parallel moves instead of LDS round trips and block barriers.  The
 // projection writes q, k and v in that order (head16_index), so a lane's 16 values are four
 // 16-byte words; the step's RoPE factors and the q/k norm weights are kept in the same order.
-constexpr int AR_THREADS = 256;  // 16 rows of 16 lanes; the value sweep: lane = dim
+constexpr int AR_THREADS = 512;  // 32 rows of 16 lanes; the value sweep: lane = (head, dim)
 constexpr int AR_KRING = 6;      // key positions in flight per row of lanes (a sliding-window split: all)
 constexpr int AR_HB = 2;         // heads per block: 224 blocks for a 7-row pass
+constexpr int AR_VRING = 4;      // value tiles in flight
 
 // E:326-345 1 / sqrtf((float)(ss / 256) + 1e-6) of the row's 256-vector: lane n's double chain
 // over tt is accumulator lane n; p_n meet as a_l = (p_l + p_{l+4}) + (p_{l+8} + p_{l+12}),
@@ -334,25 +335,33 @@ __device__ __forceinline__ void load16(float (&x)[16], const float* p) {
 // The arguments the block needs first lead the list, ahead of the pointer block, so that they
 // arrive preloaded in scalar registers (kernel-argument preloading) rather than through a
 // dependent load of the argument segment.
+// 512 threads: two waves on each SIMD (a wave issues an instruction only every few cycles, so a
+// lone wave leaves most of its SIMD idle).  Rows of lanes 0..15 (waves 0-3) form the pass's
+// key / value rows while rows 16 + 4 hh (waves 4, 5) form query head hh; 32 rows of lanes score
+// positions; in the value sweep thread (hv, i) runs the chain of head hv, dim i.
 template <int HB>
 __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restrict__ sp, const float* __restrict__ q,
                                                           const float* __restrict__ ropestep,
                                                           const float* __restrict__ qnp, const uint16_t* __restrict__ KC,
                                                           const uint16_t* __restrict__ VC, int sliding, int T,
                                                           AttnPtrs P) {
+  static_assert(HB * HD == AR_THREADS, "one head per thread in the value sweep");
+  constexpr int NR = AR_THREADS / 16;                // rows of 16 lanes
   __shared__ __align__(16) float sw[HB][ATT_SW];     // scores, then weights, of the split's tiles
-  __shared__ float rmx[AR_THREADS / 16][HB];         // per row of lanes: max of its allowed scores
+  __shared__ float rmx[NR][HB];                      // per row of lanes: max of its allowed scores
   __shared__ __align__(16) uint16_t knew[MAXM][HD];  // the pass's key rows, bf16 in cache order
   __shared__ __align__(16) uint16_t vnew[MAXM][HD];  // the pass's value rows, bf16 natural order
+  __shared__ __align__(16) float qsh[HB][16][16];    // query head hh, lane n's 16 values at [hh][n]
   const int t = blockIdx.x, m = blockIdx.y, h0 = blockIdx.z * HB;
   const int tid = threadIdx.x, rho = tid >> 4, n = tid & 15, ls = n & 7, ss = n >> 3;
-  // 1. loads that need no geometry first: the block's query heads, their norm weights and the
-  // row's RoPE factors, 16 values per lane (head16_index order)
-  // (the first row of lanes of each wave loads and forms them; the wave's other rows take
-  // copies in step 4: one fetch per wave instead of one per row)
-  // The other rows' offsets lie past the resources: they read zeros and move no data.
-  const uint32_t roff = (rho & 3) == 0 ? (uint32_t)n * 64 : 0x7FFFFFF0u;
-  float qx[HB][16], qw[16], cs[16];
+  // 1. loads that need no geometry first: query head qh of the block, its norm weights and the
+  // row's RoPE factors, 16 values per lane (head16_index order), for the rows of lanes that form
+  // them (rows 16 + 4 qh); the other rows' offsets lie past the resources: they read zeros and
+  // move no data.
+  const int qh = (rho - 16) >> 2;
+  const bool qrow = rho >= 16 && (rho & 3) == 0 && qh < HB;  // uniform per row
+  const uint32_t roff = qrow ? (uint32_t)n * 64 : 0x7FFFFFF0u;
+  float qx[16], qw[16], cs[16];
   auto load16b = [&](float (&x)[16], __amdgpu_buffer_rsrc_t r, uint32_t off) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -365,8 +374,7 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
   };
   {
     const __amdgpu_buffer_rsrc_t rq = buf_rsrc(q + (size_t)m * (NQ * HD) + h0 * HD, HB * HD * 4);
-#pragma unroll
-    for (int hh = 0; hh < HB; ++hh) load16b(qx[hh], rq, roff + hh * HD * 4);
+    load16b(qx, rq, qrow ? roff + qh * HD * 4 : roff);
     load16b(qw, buf_rsrc(qnp, HD * 4), roff);
     load16b(cs, buf_rsrc(ropestep + (size_t)m * HD, HD * 4), roff);
   }
@@ -400,42 +408,49 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
   };
   const int pb0 = c0 & ~(ATT_TILE - 1);
   const int NT = PP > 0 ? ((c1 - 1) >> 5) - (c0 >> 5) + 1 : 0;
-  const int NTp = (NT + ATT_RING - 1) / ATT_RING * ATT_RING;
+  const int NTp = (NT + AR_VRING - 1) / AR_VRING * AR_VRING;
   // the pass's rows r in [rn0, rn1) have positions pos0 + r inside [c0, c1): the split's last ones
   const int rn0 = max(c0 - pos0, 0), rn1 = min(c1 - pos0, M);
 
   // 2. the split's first value tiles (lane = dim) and key positions: row rho scores positions
-  // c0 + rho + 16 k; lane n's 16 key values (slots 32 ls + 16 ss + tt) are two 16-byte words.
+  // c0 + rho + NR k; lane n's 16 key values (slots 32 ls + 16 ss + tt) are two 16-byte words.
   // Keys from the cache stop before pos0 (the pass's rows come from LDS); entries past them
-  // reload a position in range, never used.
+  // read zeros, never used.
   // value tiles: the split's NT blocks of 32 positions from pb0 (entries past them read zeros);
   // lane i reads dim i of a tile, 4 parts of 16 bytes (each load one contiguous 1 KB per wave)
-  uint4 vring[ATT_RING][4];
+  // the value sweep: wave w's lanes 0..31 run head 0, lanes 32..63 head 1, for dims 32 w + lane % 32;
+  // a lane loads the two parts of 8 positions of its dim that its half of the tile holds (head 0's
+  // lanes positions 0..15, head 1's 16..31) and the two halves swap them (v_permlane32_swap), so
+  // each tile is read once per block for both heads
+  const int hv = (tid >> 5) & 1, i = 32 * (tid >> 6) + (tid & 31);
+  uint4 vring[AR_VRING][2];
   const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(VC + (size_t)(pb0 >> 5) * (ATT_TILE * HD), (uint32_t)NT * ATT_TILE * HD * 2);
-  auto issue_v = [&](int v, uint4 (&r)[4]) {
+  auto issue_v = [&](int v, uint4 (&r)[2]) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = buf_load16(vrs, (uint32_t)v * (ATT_TILE * HD * 2) + c * (8 * HD * 2) + tid * 16);
+    for (int c = 0; c < 2; ++c)
+      r[c] = buf_load16(vrs, (uint32_t)v * (ATT_TILE * HD * 2) + (2 * hv + c) * (8 * HD * 2) + i * 16);
   };
   // key positions below gend = min(c1, pos0) from the cache (the pass's rows come from LDS;
   // entries past gend read zeros, never used)
-  const int KN = (PP + 15) >> 4, KNp = (KN + AR_KRING - 1) / AR_KRING * AR_KRING;
+  const int KN = (PP + NR - 1) / NR, KNp = (KN + AR_KRING - 1) / AR_KRING * AR_KRING;
   const int gend = min(c1, pos0);
   const __amdgpu_buffer_rsrc_t krs = buf_rsrc(KC, (uint32_t)max(gend, 0) * HD * 2);
   uint4 kring[AR_KRING][2];
   auto issue_k = [&](int k, uint4 (&r)[2]) {
-    const uint32_t off = (uint32_t)(c0 + rho + 16 * k) * (HD * 2) + (4 * ls + 2 * ss) * 16;
+    const uint32_t off = (uint32_t)(c0 + rho + NR * k) * (HD * 2) + (4 * ls + 2 * ss) * 16;
     r[0] = buf_load16(krs, off);
     r[1] = buf_load16(krs, off + 16);
   };
 #pragma unroll
   for (int k = 0; k < AR_KRING; ++k) issue_k(k, kring[k]);
 #pragma unroll
-  for (int k = 0; k < ATT_RING; ++k) issue_v(k, vring[k]);
+  for (int k = 0; k < AR_VRING; ++k) issue_v(k, vring[k]);
 
   // 3. E:1307-1324 the pass's key / value rows in this split (rows of lanes 0..7: key row rho,
   // 8..15: value row rho - 8): k = rot(r16((k * rinv) * kn)), v = r16(v * rinv), bf16 into LDS;
-  // the block (m 0, h 0) of the split also writes them into the cache
-  if (rn0 < rn1) {  // uniform
+  // the block (m 0, h 0) of the split also writes them into the cache.
+  // At the same time, 4. the query heads: row 16 + 4 qh forms head qh (E:1307-1324) into LDS.
+  if (rn0 < rn1 && rho < 16) {  // uniform per wave
     const int pr = rho & 7;
     const bool prow = pr >= rn0 && pr < rn1;  // uniform per row of lanes
     float px[16];
@@ -448,7 +463,7 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
       if (prow) {
         uint32_t wv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wv[i] = (uint32_t)f2bf(px[2 * i]) | ((uint32_t)f2bf(px[2 * i + 1]) << 16);
+        for (int k = 0; k < 8; ++k) wv[k] = (uint32_t)f2bf(px[2 * k]) | ((uint32_t)f2bf(px[2 * k + 1]) << 16);
         uint4* dst = reinterpret_cast<uint4*>(&knew[pr][0]) + 4 * ls + 2 * ss;
         dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
         dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
@@ -461,24 +476,34 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
         for (int tt = 0; tt < 16; ++tt) vnew[pr][16 * tt + n] = f2bf(r16(px[tt] * r));
       }
     }
-    __syncthreads();
-    if (m == 0 && h0 == 0)
-      for (int r = rn0; r < rn1; ++r) {
-        P.KCw[(size_t)(pos0 + r) * HD + tid] = knew[r][tid];  // the LDS row is already in cache order
-        P.VCw[vc_index(pos0 + r, tid)] = vnew[r][tid];
-      }
+  }
+  if (qrow) {  // uniform per row
+    row_norm_rope(qx, qw, cs);
+    float4* d4 = reinterpret_cast<float4*>(&qsh[qh][n][0]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d4[k] = make_float4(qx[4 * k], qx[4 * k + 1], qx[4 * k + 2], qx[4 * k + 3]);
+  }
+  __syncthreads();
+  if (rn0 < rn1 && m == 0 && h0 == 0 && tid < HD)
+    for (int r = rn0; r < rn1; ++r) {
+      P.KCw[(size_t)(pos0 + r) * HD + tid] = knew[r][tid];  // the LDS row is already in cache order
+      P.VCw[vc_index(pos0 + r, tid)] = vnew[r][tid];
+    }
+  float qv[HB][16];  // this lane's query values of the block's heads
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) {
+    const float4* s4 = reinterpret_cast<const float4*>(&qsh[hh][n][0]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 v = s4[k];
+      qv[hh][4 * k] = v.x;
+      qv[hh][4 * k + 1] = v.y;
+      qv[hh][4 * k + 2] = v.z;
+      qv[hh][4 * k + 3] = v.w;
+    }
   }
 
-  // 4. the query heads, formed by the first row of lanes of each wave and copied to its others
-#pragma unroll
-  for (int hh = 0; hh < HB; ++hh) row_norm_rope(qx[hh], qw, cs);
-#pragma unroll
-  for (int hh = 0; hh < HB; ++hh)
-#pragma unroll
-    for (int tt = 0; tt < 16; ++tt)
-      qx[hh][tt] = as_f32((uint32_t)__builtin_amdgcn_ds_bpermute(n * 4, (int)as_u32(qx[hh][tt])));
-
-  // 5. E:750-816 scores of positions c0 + rho + 16 k; lane 0 of the row stores them and keeps the
+  // 5. E:750-816 scores of positions c0 + rho + NR k; lane 0 of the row stores them and keeps the
   // running max over the allowed positions (max is order free)
   float rowmax[HB];
 #pragma unroll
@@ -488,9 +513,9 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
     for (int k = 0; k < AR_KRING; ++k) {
       const int kk = base + k;
       if (kk < KN) {  // uniform
-        const int p = c0 + rho + 16 * kk;
+        const int p = c0 + rho + NR * kk;
         uint4 ka = kring[k][0], kb = kring[k][1];
-        if (c0 + 16 * kk + 15 >= pos0) {  // uniform: the step may reach the pass's rows (in LDS)
+        if (c0 + NR * kk + NR - 1 >= pos0) {  // uniform: the step may reach the pass's rows (in LDS)
           const bool own = p >= pos0 && p < c1;
           const uint4* n4 = reinterpret_cast<const uint4*>(&knew[min(max(p - pos0, 0), MAXM - 1)][0]) + 4 * ls + 2 * ss;
           ka = sel4(own, n4[0], ka);
@@ -501,12 +526,12 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh) acc[hh] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float k0 = as_f32(kw[i] << 16), k1 = as_f32(kw[i] & 0xFFFF0000u);
+        for (int j = 0; j < 8; ++j) {
+          const float k0 = as_f32(kw[j] << 16), k1 = as_f32(kw[j] & 0xFFFF0000u);
 #pragma unroll
           for (int hh = 0; hh < HB; ++hh) {
-            acc[hh] = fmaf(qx[hh][2 * i], k0, acc[hh]);
-            acc[hh] = fmaf(qx[hh][2 * i + 1], k1, acc[hh]);
+            acc[hh] = fmaf(qv[hh][2 * j], k0, acc[hh]);
+            acc[hh] = fmaf(qv[hh][2 * j + 1], k1, acc[hh]);
           }
         }
 #pragma unroll
@@ -529,7 +554,7 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
   for (int hh = 0; hh < HB; ++hh) {
     mx[hh] = -1e30f;
 #pragma unroll
-    for (int r = 0; r < AR_THREADS / 16; ++r) mx[hh] = (mx[hh] < rmx[r][hh]) ? rmx[r][hh] : mx[hh];
+    for (int r = 0; r < NR; ++r) mx[hh] = (mx[hh] < rmx[r][hh]) ? rmx[r][hh] : mx[hh];
   }
   // weights exp8(score - max) (E:820); masked positions and the padding of the whole tiles get 0
   for (int idx = tid; idx < HB * NT * ATT_TILE; idx += AR_THREADS) {
@@ -541,55 +566,60 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
   }
   __syncthreads();
 
-  // 6. E:826-875 o_i = fma chain over the positions in order, lane = dim i; a masked or padding
-  // position (weight 0) gets value +0: fma(0, 0, o) = o exactly (o is never -0).  The pass's rows
-  // follow from LDS after the tile's other positions (they are the split's last).  Wave w forms
-  // l = the sum of the weights of head w % HB in position order (E:821); waves w < HB store it.
-  const int i = tid, wave = tid >> 6;
-  float o[HB], lsum = 0.f;
-#pragma unroll
-  for (int hh = 0; hh < HB; ++hh) o[hh] = 0.f;
+  // 6. E:826-875 o_i = fma chain over the positions in order, lane (hv, i): head hv, dim i; a
+  // masked or padding position (weight 0) gets value +0: fma(0, 0, o) = o exactly (o is never
+  // -0).  The pass's rows follow from LDS after the tile's other positions (they are the split's
+  // last).  Every lane also forms l = the sum of its head's weights in position order (E:821);
+  // the lane of head hv, dim 0 (wave 0) stores it.
+  float o = 0.f, lsum = 0.f;
   const int fa = max(lo_m, c0), fz = min(min(pos_m, c1 - 1), pos0 - 1);
   auto full_tile = [=](int pb) {
     return pb >= fa && pb + ATT_TILE - 1 <= fz && (sl_m > sh_m || pb > sh_m || pb + ATT_TILE - 1 < sl_m);
   };
-  for (int base = 0; base < NTp; base += ATT_RING)
+  for (int base = 0; base < NTp; base += AR_VRING)
 #pragma unroll
-    for (int k = 0; k < ATT_RING; ++k) {
+    for (int k = 0; k < AR_VRING; ++k) {
       const int s = base + k;
       const int pb = pb0 + s * ATT_TILE;
       if (s < NT) {  // uniform
-        const uint32_t vw[16] = {vring[k][0].x, vring[k][0].y, vring[k][0].z, vring[k][0].w,
-                                 vring[k][1].x, vring[k][1].y, vring[k][1].z, vring[k][1].w,
-                                 vring[k][2].x, vring[k][2].y, vring[k][2].z, vring[k][2].w,
-                                 vring[k][3].x, vring[k][3].y, vring[k][3].z, vring[k][3].w};
+        // vw[0..7]: parts 0, 1 (positions 0..15) of dim i, vw[8..15]: parts 2, 3; the swap
+        // exchanges lanes 32..63 of its first operand with lanes 0..31 of its second
+        uint32_t vw[16];
+        {
+          const uint32_t y[8] = {vring[k][0].x, vring[k][0].y, vring[k][0].z, vring[k][0].w,
+                                 vring[k][1].x, vring[k][1].y, vring[k][1].z, vring[k][1].w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const auto sw2 = __builtin_amdgcn_permlane32_swap(y[j], y[j], false, false);
+            vw[j] = sw2[0];
+            vw[8 + j] = sw2[1];
+          }
+        }
         const bool full = full_tile(pb);
         const uint32_t keep = full ? 0xFFFFFFFFu : tile_mask(pb) & ~bits_in(pos0, pos0 + MAXM, pb);
-        // the tile's weights one per lane: half g of the tile (16 positions) in lane n of every
-        // row; wl: those of head wave % HB for the sum l
-        float wr[2][HB], wl[2];
+        // the tile's 32 weights of head hv in every lane of its half wave (LDS broadcast reads):
+        // plain VGPR operands, so the two chains need no cross-lane moves (a DPP broadcast
+        // operand would also make each chain step wait two instructions for the previous one)
+        float wt[ATT_TILE];
+        {
+          const float4* w4 = reinterpret_cast<const float4*>(&sw[hv][pb - pb0]);
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-#pragma unroll
-          for (int hh = 0; hh < HB; ++hh) wr[g][hh] = sw[hh][pb - pb0 + 16 * g + n];
-          wl[g] = sw[wave % HB][pb - pb0 + 16 * g + n];
+          for (int q4 = 0; q4 < ATT_TILE / 4; ++q4) {
+            const float4 v = w4[q4];
+            wt[4 * q4] = v.x;
+            wt[4 * q4 + 1] = v.y;
+            wt[4 * q4 + 2] = v.z;
+            wt[4 * q4 + 3] = v.w;
+          }
         }
         auto sweep = [&](const bool masked) {
-          auto half = [&](auto G) {
-            constexpr int g = decltype(G)::value;
-            auto pos = [&](auto Kc) {
-              constexpr int k = decltype(Kc)::value, pe = 16 * g + k;
-              uint32_t vb = __builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], (pe & 1) ? 0x03020c0cu : 0x01000c0cu);
-              if (masked) vb &= (uint32_t)((int)(keep << (31 - pe)) >> 31);
-              const float vv = as_f32(vb);
-              lsum = add_bc<k>(lsum, wl[g]);
 #pragma unroll
-              for (int hh = 0; hh < HB; ++hh) o[hh] = fmac_bc<k>(o[hh], wr[g][hh], vv);
-            };
-            unroll_n<16>(pos);
-          };
-          half(std::integral_constant<int, 0>{});
-          half(std::integral_constant<int, 1>{});
+          for (int pe = 0; pe < ATT_TILE; ++pe) {
+            uint32_t vb = __builtin_amdgcn_perm(vw[pe >> 1], vw[pe >> 1], (pe & 1) ? 0x03020c0cu : 0x01000c0cu);
+            if (masked) vb &= (uint32_t)((int)(keep << (31 - pe)) >> 31);
+            lsum = lsum + wt[pe];
+            o = fmaf(wt[pe], as_f32(vb), o);
+          }
         };
         if (full) sweep(false);
         else sweep(true);
@@ -597,18 +627,16 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(const StepDev* __restr
           const int pa = max(max(pb, pos0), c0), pz = min(pb + ATT_TILE, c1);
           for (int pp = pa; pp < pz; ++pp) {
             const float vv = as_f32((uint32_t)vnew[pp - pos0][i] << 16);
-#pragma unroll
-            for (int hh = 0; hh < HB; ++hh) o[hh] = fmaf(sw[hh][pp - pb0], vv, o[hh]);
+            o = fmaf(sw[hv][pp - pb0], vv, o);
           }
         }
       }
-      issue_v(s + ATT_RING, vring[k]);
+      issue_v(s + AR_VRING, vring[k]);
     }
-#pragma unroll
-  for (int hh = 0; hh < HB; ++hh) P.po[(((size_t)t * M + m) * NQ + h0 + hh) * HD + i] = o[hh];
-  if ((tid & 63) == 0 && wave < HB) {
-    P.pm[((size_t)t * M + m) * NQ + h0 + wave] = mx[wave % HB];
-    P.pl[((size_t)t * M + m) * NQ + h0 + wave] = (lo_m > pos_m) ? 0.0f : lsum;
+  P.po[(((size_t)t * M + m) * NQ + h0 + hv) * HD + i] = o;
+  if (i == 0) {
+    P.pm[((size_t)t * M + m) * NQ + h0 + hv] = mx[hv];
+    P.pl[((size_t)t * M + m) * NQ + h0 + hv] = (lo_m > pos_m) ? 0.0f : lsum;
   }
 }
 
