@@ -2071,15 +2071,10 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
   a8 = a8 && M >= 2;  // lin_multi's rule (E:311)
   // a product: the W4A8 kernel on the a8 tiles of the same matrices, or the row-tile GEMV
   auto a8t = [](const Mat& m) { return W4Tile{m.a8w.as<uint4>(), m.a8s.as<uint4>(), m.N}; };
-  // the quantised rows of the W4A8 products of staged rows (K * 8 and K bytes): the prompt path's
-  // operand buffers (at least 16 rows of K bf16 and of K / 32 floats), which this pass uses only
-  // before its first such product (the per-layer-input projection and layer 0's q / k / v)
-  uint64_t* qa = c->pfxq.as<uint64_t>();
-  float* qsx = c->pfsx.as<float>();
   auto product = [&](GemvTArgs& a, const Mat* const* ms, int nm, int mpl, int tr) {
     if (a8) {
       for (int j = 0; j < nm; ++j) a.mat[j] = a8t(*ms[j]);
-      (void)launch_gemv_a8(a, qa, qsx, st);
+      (void)launch_gemv_a8(a, st);
     } else {
       (void)launch_gemv_t(a, st, mpl, tr);
     }
@@ -2193,7 +2188,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       if (a8) {  // the gate and up matrices' own a8 tiles (their pairs meet in one block)
         a.mat[0] = a8t(lay.m[4]);
         a.mat[1] = a8t(lay.m[5]);
-        (void)launch_gemv_a8(a, qa, qsx, st);
+        (void)launch_gemv_a8(a, st);
       } else {
         launch_gemv_t(a, st, rows_of(2), tile_of(2));
       }
@@ -2207,7 +2202,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.xs = reinterpret_cast<const float4*>(R.act);
       a.K = G.I;
       a.M = M;
-      (void)launch_gemv_a8(a, qa, qsx, st);
+      (void)launch_gemv_a8(a, st);
       down_done = true;
     } else if (lay.m[6].tw.p) {
       GemvTArgs a{};

@@ -18,10 +18,10 @@
 // group's bytes 4h .. 4h+3).
 //
 // Kernels, one launch per product of the fused verify pass:
-//   k_a8_quant_rows  quantises staged activation rows into QA [G][4][8] words and SX [G][8];
-//   k_gemv_a8p       a product of such rows (o, down, the per-layer projection): a block per
-//                    16 outputs walks K in phases of PG groups, the next phase's weight and
-//                    operand words in flight while the current one is multiplied and chained;
+//   k_gemv_a8p       a product of staged rows (o, down, the per-layer projection): a block per
+//                    16 outputs walks K in phases of PG groups, quantises the phase's groups of
+//                    every row into LDS, the next phase's weight words and row floats in flight
+//                    while the current one is multiplied and chained;
 //   k_gemv_a8n       a product whose prologue forms its rows as k_gemv_t's norm prologue does
 //                    (q/k/v, gate/up, the per-layer-input gate; K = 1536, one phase) and
 //                    quantises them in LDS; epilogues: y, the gate / up activation (staged) or
@@ -72,54 +72,29 @@ __device__ __forceinline__ float a8_scale(uint4 s4, int e) {  // bf16 scale e of
   return as_f32((e & 1) ? (s2 & 0xFFFF0000u) : (s2 << 16));
 }
 
-// ---- quantised rows: thread (g, m); rows m >= M are written as zeros ----
-__global__ void k_a8_quant_rows(const float4* __restrict__ xs, int M, int K, uint64_t* __restrict__ QA,
-                                float* __restrict__ SX) {
-  const int G = K / 32, idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= 8 * G) return;
-  const int g = idx >> 3, m = idx & 7;
-  uint64_t* q = QA + (size_t)g * 32 + m;  // word h at q[8 h]
-  if (m >= M) {
-#pragma unroll
-    for (int h = 0; h < 4; ++h) q[8 * h] = 0;
-    SX[idx] = 0.f;
-    return;
-  }
-  // staged rows: float4 jj of a group holds elements 2jj, 16 + 2jj, 2jj + 1, 17 + 2jj
-  const float4* src = xs + ((size_t)m * K + 32 * g) / 4;
-  float v[32];
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const float4 f = src[jj];
-    v[2 * jj] = f.x;
-    v[16 + 2 * jj] = f.y;
-    v[2 * jj + 1] = f.z;
-    v[17 + 2 * jj] = f.w;
-  }
-  uint64_t aq[4];
-  SX[idx] = a8_quant_group(v, aq);
-#pragma unroll
-  for (int h = 0; h < 4; ++h) q[8 * h] = aq[h];
-}
-
 // ---- a product of quantised rows ----
 // Block: the 16 outputs of one a8 tile (tiles of up to three matrices, in order), 512 threads.
-// Phase p: wave w multiplies chunks (4 groups) w + 8k, k < NU, of the phase; lanes 0..127 chain.
-// LDS: A32 [PG][8][16] float, SXL [PG][8] float, SWL [PG / 8][16] uint4 (the tile's scales)
+// Phase p covers PG groups: thread (group gl = tid / 8, row m = tid % 8) quantises its group of
+// its staged row into LDS (rows m >= M as zeros; the row's floats were fetched during the
+// previous phase), then wave w multiplies chunks (4 groups) w + 8k, k < NU, of the phase with
+// the operand words from LDS, and lanes 0..127 chain.  Every block quantises every row it
+// multiplies (a few hundred instructions a thread per phase: cheaper than a launch of its own).
+// LDS: A32 [PG][8][16] float, SXL [PG][8] float, SWL [PG / 8][16] uint4 (the tile's scales),
+// AQL [PG][4][8] operand words
 constexpr int A8P_PG = 64;
 template <int PG>
 constexpr size_t a8p_lds() {
-  return (size_t)PG * 8 * 16 * 4 + (size_t)PG * 8 * 4 + (size_t)(PG / 8) * 16 * 16;
+  return (size_t)PG * 8 * 16 * 4 + (size_t)PG * 8 * 4 + (size_t)(PG / 8) * 16 * 16 + (size_t)PG * 32 * 8;
 }
 template <int PG>
-__global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a, const uint64_t* __restrict__ QA,
-                                                  const float* __restrict__ SX) {
+__global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
   constexpr int PC = PG / 4, NU = PC / 8;
-  static_assert(PC % 8 == 0, "whole chunks per wave");
+  static_assert(PC % 8 == 0 && PG * 8 == 512, "whole chunks per wave; a thread per (group, row)");
   extern __shared__ float4 lds4[];
   float* A32 = reinterpret_cast<float*>(lds4);
   float* SXL = A32 + PG * 8 * 16;
   uint4* SWL = reinterpret_cast<uint4*>(SXL + PG * 8);
+  uint64_t* AQL = reinterpret_cast<uint64_t*>(SWL + (PG / 8) * 16);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int M = a.M, K = a.K, G = K / 32, GC4 = G / 4, G8 = G / 8, nph = (G + PG - 1) / PG;
   const int t = blockIdx.x, tl1 = a.mat[0].N / 16, tl2 = tl1 + a.mat[1].N / 16;
@@ -127,45 +102,73 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a, const uint64_t* _
   const uint4* wp = (j == 0 ? a.mat[0].w : (j == 1 ? a.mat[1].w : a.mat[2].w)) + (size_t)mt * GC4 * 64 + lane;
   const uint4* sp = (j == 0 ? a.mat[0].s : (j == 1 ? a.mat[1].s : a.mat[2].s)) + (size_t)mt * G8 * 16;
   const int ar = lane & 15, ah = lane >> 4;
-  const uint64_t* qp = QA + ah * 8 + (ar & 7);  // group g's word at + 32 g (rows >= 8 read as zero)
 
-  // the phase's weight words and operand words of this wave's chunks
+  // the phase's weight words of this wave's chunks
   uint4 wA[NU], wB[NU];
-  uint64_t qA[NU][4], qB[NU][4];
-  auto issue = [&](int p, uint4 (&wv)[NU], uint64_t (&qv)[NU][4]) {
+  auto issue = [&](int p, uint4 (&wv)[NU]) {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
       const int c = p * PC + w + 8 * k;
-      if (c < GC4) {
-        wv[k] = wp[(size_t)c * 64];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qv[k][i] = ar < 8 ? qp[(size_t)(4 * c + i) * 32] : 0;
-      }
+      if (c < GC4) wv[k] = wp[(size_t)c * 64];
     }
   };
-  // the phase's activation scales (thread f < 2 PG: 4 floats of SX) and weight scales (thread
-  // 2 PG <= f < 4 PG: a word of the tile's scales), staged through one register
+  // the staged floats of this thread's (group, row) of a phase: float4 jj of a group holds
+  // elements 2jj, 16 + 2jj, 2jj + 1, 17 + 2jj
+  const int qg = tid >> 3, qm = tid & 7;
+  float4 xr[8];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) xr[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto issue_x = [&](int p) {
+    const int g = p * PG + qg;
+    if (qm < M && g < G) {
+      const float4* src = reinterpret_cast<const float4*>(a.xs) + ((size_t)qm * K + 32 * g) / 4;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) xr[jj] = src[jj];
+    }
+  };
+  // the phase's weight scales (thread f < 2 PG: a word of the tile's scales), staged through
+  // one register
   uint4 stg = make_uint4(0, 0, 0, 0);
   auto issue_s = [&](int p) {
     const int gb = p * PG;
-    const bool sxw = tid < 2 * PG;
-    const int f = sxw ? tid : tid - 2 * PG;
-    const uint4* src = sxw ? reinterpret_cast<const uint4*>(SX + (size_t)gb * 8) + f
-                           : sp + (size_t)(gb / 8 + (f >> 4)) * 16 + (f & 15);
-    const bool ok = tid < 4 * PG && (sxw ? gb + f / 2 < G : gb / 8 + (f >> 4) < G8);
-    if (ok) stg = *src;
+    if (tid < 2 * PG && gb / 8 + (tid >> 4) < G8) stg = sp[(size_t)(gb / 8 + (tid >> 4)) * 16 + (tid & 15)];
   };
-  uint4* stg_dst = tid < 2 * PG ? reinterpret_cast<uint4*>(SXL) + tid : SWL + (tid - 2 * PG);
-  issue(0, wA, qA);
+  issue(0, wA);
+  issue_x(0);
   issue_s(0);
   const int cm = (tid >> 4) & 7, cn = tid & 15;
   const bool chain = tid < 128 && cm < M;
   float acc = 0.f;
   for (int p = 0; p < nph; ++p) {
     const int gb = p * PG, ng = min(PG, G - gb);
-    if (p + 1 < nph) issue(p + 1, wB, qB);
-    if (tid < 4 * PG) *stg_dst = stg;
-    if (p + 1 < nph) issue_s(p + 1);
+    if (p + 1 < nph) issue(p + 1, wB);
+    // quant (engine/w4a8_avx2.h:33-41) of this thread's group into its operand words
+    {
+      float v[32];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        v[2 * jj] = xr[jj].x;
+        v[16 + 2 * jj] = xr[jj].y;
+        v[2 * jj + 1] = xr[jj].z;
+        v[17 + 2 * jj] = xr[jj].w;
+      }
+      uint64_t aq[4];
+      float sx = a8_quant_group(v, aq);
+      if (qm >= M || gb + qg >= G) {
+        sx = 0.f;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) aq[h] = 0;
+      }
+      SXL[qg * 8 + qm] = sx;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) AQL[qg * 32 + h * 8 + qm] = aq[h];
+    }
+    if (tid < 2 * PG) SWL[tid] = stg;
+    if (p + 1 < nph) {
+      issue_x(p + 1);
+      issue_s(p + 1);
+    }
+    __syncthreads();
     // the group dots of this wave's chunks
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
@@ -175,8 +178,8 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a, const uint64_t* _
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t d = i == 0 ? wv.x : (i == 1 ? wv.y : (i == 2 ? wv.z : wv.w));
-          const i32x4_t D = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)qA[k][i], a8_wbytes(d), i32x4_t{0, 0, 0, 0},
-                                                                  0, 0, 0);
+          const uint64_t qw = ar < 8 ? AQL[(4 * cl + i) * 32 + ah * 8 + ar] : 0;  // rows >= 8 zero
+          const i32x4_t D = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)qw, a8_wbytes(d), i32x4_t{0, 0, 0, 0}, 0, 0, 0);
           if (ah < 2) {
             float* o = A32 + ((size_t)(4 * cl + i) * 8 + 4 * ah) * 16 + ar;
             o[0] = (float)D[0];
@@ -205,11 +208,7 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a, const uint64_t* _
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < NU; ++k) {
-      wA[k] = wB[k];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qA[k][i] = qB[k][i];
-    }
+    for (int k = 0; k < NU; ++k) wA[k] = wB[k];
   }
   if (chain) {
     float* y = j == 0 ? a.y[0] : (j == 1 ? a.y[1] : a.y[2]);
@@ -466,9 +465,8 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
 
 // mat[j]: a8 tiles (launch_tile_a8) of matrices with N_j % 16 == 0; gateup: mat[0] the gate and
 // mat[1] the up matrix (equal N), y[0] the staged activation.  A product of staged rows (xs)
-// quantises them first into qa / sx (scratch of at least K / 32 * 256 and K / 32 * 32 bytes).
-// Returns the grid of the product (0: refused, nothing launched).
-int launch_gemv_a8(const GemvTArgs& a, uint64_t* qa, float* sx, hipStream_t st) {
+// quantises them in each block.  Returns the grid of the product (0: refused, nothing launched).
+int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
   if (a.M < 1 || a.M > 8 || a.K % 256 || a.mrg_po || a.yperm) return 0;
   int tiles = 0;
   for (int j = 0; j < 3; ++j) {
@@ -477,10 +475,8 @@ int launch_gemv_a8(const GemvTArgs& a, uint64_t* qa, float* sx, hipStream_t st) 
   }
   const dim3 b(512);
   if (!a.nrm_mode) {
-    if (!a.xs || a.gateup || a.epi_pli || !qa || !sx) return 0;
-    const int G = a.K / 32;
-    hipLaunchKernelGGL(k_a8_quant_rows, dim3((8 * G + 255) / 256), dim3(256), 0, st, a.xs, a.M, a.K, qa, sx);
-    hipLaunchKernelGGL(k_gemv_a8p<A8P_PG>, dim3(tiles), b, a8p_lds<A8P_PG>(), st, a, qa, sx);
+    if (!a.xs || a.gateup || a.epi_pli) return 0;
+    hipLaunchKernelGGL(k_gemv_a8p<A8P_PG>, dim3(tiles), b, a8p_lds<A8P_PG>(), st, a);
     return tiles;
   }
   if (a.K != H) return 0;

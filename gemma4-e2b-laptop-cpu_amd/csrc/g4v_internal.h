@@ -288,10 +288,9 @@ void launch_prompt_lookup(int* hist, int L0, const PlAppend& app, int n, int max
 int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr);
 // W4A8 products of a verify pass (g4v_gemva8.hip): the same arguments with mat[j] the a8 tiles
 // (launch_tile_a8) and, with gateup set, mat[0] / mat[1] the gate / up matrices; M <= 8, the
-// staged input xs (quantised first into qa / sx: K / 32 * 256 and K / 32 * 32 bytes of scratch)
-// or a norm prologue (modes 1 and 2, or 3 with epi_pli).  Returns the grid size of the product
-// (0: refused, nothing launched).
-int launch_gemv_a8(const GemvTArgs& a, uint64_t* qa, float* sx, hipStream_t st);
+// staged input xs (quantised in the product's blocks) or a norm prologue (modes 1 and 2, or 3
+// with epi_pli).  Returns the grid size of the product (0: refused, nothing launched).
+int launch_gemv_a8(const GemvTArgs& a, hipStream_t st);
 // returns the grid size used (the number of EPI_SCREEN partials per activation row)
 int launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
 // grid launch_gemv would use
