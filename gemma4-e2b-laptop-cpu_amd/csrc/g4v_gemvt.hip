@@ -453,7 +453,11 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(const float* __restrict__ pa,
   const int qo = j % MPL;  // this wave's offset chain: activation row m0 + j % MPL
   const float4* xw = XL + j;   // row q, group g: xw[(q * G + g) * 9], the same for the whole wave
   const float* gw = GSL + qo * G;
-  auto chunk = [&](const uint4 wv, const uint4 sv, const int c) {
+  // off is used from the waves j < MPL only (OFL below): with 64-row tiles a wave is one chain
+  // lane, so the other waves run the chunks without the off chain (two copies of the loop, no
+  // branch per group)
+  auto chunk = [&](const uint4 wv, const uint4 sv, const int c, auto OFF) {
+    constexpr bool with_off = decltype(OFF)::value;
     const float4 gs4[2] = {*reinterpret_cast<const float4*>(gw + c * 8),
                            *reinterpret_cast<const float4*>(gw + c * 8 + 4)};
     float4 xv[2][MPL];
@@ -486,22 +490,30 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(const float* __restrict__ pa,
         av = fmaf(h1, x4.w, av);
         row[q] = fmaf(av, sc, row[q]);
       }
-      const float4 g4 = gs4[i >> 2];
-      const int e = i & 3;
-      off = fmaf(sc, e == 0 ? g4.x : (e == 1 ? g4.y : (e == 2 ? g4.z : g4.w)), off);
+      if constexpr (with_off) {
+        const float4 g4 = gs4[i >> 2];
+        const int e = i & 3;
+        off = fmaf(sc, e == 0 ? g4.x : (e == 1 ? g4.y : (e == 2 ? g4.z : g4.w)), off);
+      }
     }
   };
-  for (int cb = 0; cb < GC; cb += GT_B) {
-    load_batch(wB, sB, cb + GT_B);  // next batch in flight while this one is used
+  auto sweep = [&](auto OFF) {
+    for (int cb = 0; cb < GC; cb += GT_B) {
+      load_batch(wB, sB, cb + GT_B);  // next batch in flight while this one is used
 #pragma unroll
-    for (int b = 0; b < GT_B; ++b)
-      if (cb + b < GC) chunk(wA[b], sA[b], cb + b);  // uniform condition
+      for (int b = 0; b < GT_B; ++b)
+        if (cb + b < GC) chunk(wA[b], sA[b], cb + b, OFF);  // uniform condition
 #pragma unroll
-    for (int b = 0; b < GT_B; ++b) {
-      wA[b] = wB[b];
-      sA[b] = sB[b];
+      for (int b = 0; b < GT_B; ++b) {
+        wA[b] = wB[b];
+        sA[b] = sB[b];
+      }
     }
-  }
+  };
+  if (TR == 64 && __builtin_amdgcn_readfirstlane(j) >= MPL)  // uniform: a wave of one chain lane
+    sweep(std::false_type{});
+  else
+    sweep(std::true_type{});
 
   // the 8 chain lanes of each (row, output) meet in LDS: ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off
 #pragma unroll
