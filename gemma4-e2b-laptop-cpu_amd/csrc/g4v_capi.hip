@@ -147,6 +147,7 @@ struct g4v_ctx {
   float dr_scalar[4] = {0.75f, 0.75f, 0.75f, 0.75f};
   DBuf dr_pre, dr_post, dr_cent, dr_emb, dr_order, dr_norms, dr_q[4], dr_o[4], dr_g[4], dr_u[4], dr_d[4], dr_s;
   int last_hrow = -1;  // row of c->h holding the last verify step's committed hidden state
+  int pf_nsurv = 0, pf_fallback = 0;  // the last prefill's head row: screen survivors, fallback
   int* dr_in_host = nullptr;   // pinned chain inputs {tok, P, hrow, _, h[1536]}
   int* dr_out_host = nullptr;  // pinned chain outputs {tok[8], sec[8], gap[8], hidden[1536]}
   // prefix cache: the active KV (KC / VC) with its keys, plus stored slots (each a full KV copy)
@@ -987,6 +988,7 @@ int g4v_head_argmax(g4v_ctx* c, const float* h, int M, int* G, int* nsurv, int* 
     if (nsurv) nsurv[m] = small[m];
     if (fallback) fallback[m] = small[m] > HEAD_LIMIT;
   }
+  if (c->prof_mask) prof_collect(c, small[0] > HEAD_LIMIT);
   return 0;
 }
 
@@ -1991,6 +1993,7 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
     const float* cs = ty ? c->gm_rope.as<float>() : c->rope.as<float>();
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
     launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own, dpos);
+    if (split) pmark(c, PT_ATTN, 1, 0);  // the split-KV attention (E:1327 T_ATT)
     if (split && spd) {
       if (hd == 512)
         launch_attn_geom_dev_hd(KCo, VCo, R.q, NQ * 512, geo + ty, M, nsplit, NQ, c->po5.as<float>(),
@@ -2022,6 +2025,7 @@ void gm_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, int hrow, bool
       launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, pg ? *pg : PfGeom{M, pos0, M, sib}, 0, M, sliding,
                      st, false, hd, dpos, c->ctxcap);
     }
+    if (split) pmark(c, PT_ATTN, 0, 0);
     pf_lin(c, lay.m[3], R.att, M, R.o, i8, true);                       // E:1356
     launch_pf_post_attn(R.o, R.x, R.a, post_attn, pre_ff, M, st);       // E:1358-1361
     {  // E:1363-1371: gate and up in one launch
@@ -2125,6 +2129,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
     launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own, dpos);
     const float* ogs = nullptr;  // group sums of the staged attention rows (split path)
+    if (split) pmark(c, PT_ATTN, 1, 0);  // the split-KV attention (E:1327 T_ATT)
     if (split && spd) {
       const int ty = hd == 512;
       if (hd == 512)
@@ -2159,6 +2164,7 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       launch_pf_attn(R.q, KCo, VCo, c->gm_s.as<float>(), R.att, PfGeom{M, pos0, M, sib}, 0, M, sliding, st, true, hd,
                      dpos, c->ctxcap);
     }
+    if (split) pmark(c, PT_ATTN, 0, 0);
     {  // E:1356
       GemvTArgs a{};
       a.mat[0] = lay.m[3].tile();
@@ -2545,6 +2551,16 @@ static int gm_verify(g4v_ctx* c, const int* toks, int na, int nb, int pos0, int 
   }
   HIPCHK(hipStreamSynchronize(st));
   const VerifyResultDev& r = *c->res_host;
+  // per-class timing (g4v_profile) of a pass launched eagerly; a captured pass's launches record
+  // no events of their own here, so profiling these passes wants graphs off (g4v_set_graphs(0))
+  if (c->prof_mask) {
+    if (gr) {
+      c->recs.clear();
+      c->evused = 0;
+    } else {
+      prof_collect(c, r.fallback[0] != 0);
+    }
+  }
   out->nacc = r.nacc;
   out->branch = r.branch;
   out->ncommit = r.ncommit;
@@ -2605,7 +2621,10 @@ static int gm_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb, int
   if (hidden) std::memcpy(hidden, h.data(), H * 4);
   if (G0) {
     int ns = 0, fb = 0;
-    return g4v_head_argmax(c, h.data(), 1, G0, &ns, &fb);
+    const int rr = g4v_head_argmax(c, h.data(), 1, G0, &ns, &fb);
+    c->pf_nsurv = ns;
+    c->pf_fallback = fb;
+    return rr;
   }
   return 0;
 }
@@ -2658,6 +2677,8 @@ extern "C" int g4v_prefill(g4v_ctx* c, const int* toks, int n, int pos0, int pfb
     int ns = 0, fb = 0;
     r = g4v_head_argmax(c, h.data(), 1, G0, &ns, &fb);
     if (r) return r;
+    c->pf_nsurv = ns;
+    c->pf_fallback = fb;
   }
   return 0;
 }
@@ -3241,6 +3262,13 @@ int g4v_profile(g4v_ctx* c, unsigned mask) {
     c->prof_bytes[t] = 0;
     c->prof_n[t] = 0;
   }
+  return 0;
+}
+
+int g4v_prefill_head_stats(g4v_ctx* c, int* nsurv, int* fallback) {
+  if (!c) return G4V_E_ARG;
+  if (nsurv) *nsurv = c->pf_nsurv;
+  if (fallback) *fallback = c->pf_fallback;
   return 0;
 }
 

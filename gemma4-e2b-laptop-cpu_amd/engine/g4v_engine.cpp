@@ -301,8 +301,61 @@ struct Engine {
   int pol[3] = {-1, -1, -1};  // E:1513 ENGINE_POLICY: draft count cap per state
   long r1_n = 0, r1_top1 = 0, r1_top2 = 0;  // E:1084, 1659 (over the process)
   long tree_attempts = 0, tree_hits = 0;    // E:1583 (per request), 1648, 1650
+  // E:1235 SCR.on (ENGINE_HEAD_SCREEN=1) and the head's screen statistics (E:1245, 1472, 1489;
+  // printed at E:1690): rows screened, their survivors, the largest count, and head calls that
+  // fell back to the full head.  The library's head always screens; this counts what it reports.
+  bool scr_on = false;
+  long scr_rows = 0, scr_surv = 0, scr_max = 0, scr_fallback = 0;
+  // the stage timers (E:1085 T_LAYERS, T_ATT, T_HEAD, T_DRAFT, N_FWD; E:1672 DECODE_STAGE, E:1691
+  // STAGES): forward calls, their wall time less the head's device time, the split-KV attention's
+  // and the head's device time from the library's per-class events (g4v_profile, eager launches),
+  // and the drafter chains' wall time
+  bool stage_prof = false;
+  long n_fwd = 0;
+  double t_layers = 0, t_att = 0, t_head = 0, t_draft = 0;
   double now() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+  }
+  double prof_ms(int a, int b) {  // classes a..b of g4v_profile, ms since it was started
+    double ms[G4V_PROF_NTAGS] = {0};
+    (void)g4v_profile_read(G, ms, nullptr, nullptr, G4V_PROF_NTAGS);
+    double t = 0;
+    for (int i = a; i <= b; ++i) t += ms[i];
+    return t;
+  }
+  // one forward call (nf of the reference's fwd calls): N_FWD, T_LAYERS, T_ATT, T_HEAD
+  template <class F>
+  void fwd_call(int nf, F&& f) {
+    const double h0 = stage_prof ? prof_ms(6, 12) : 0.0, a0 = stage_prof ? prof_ms(4, 4) : 0.0;
+    const double t = now();
+    f();
+    const double dt = now() - t;
+    n_fwd += nf;
+    if (stage_prof) {
+      const double dh = (prof_ms(6, 12) - h0) * 1e-3, da = (prof_ms(4, 4) - a0) * 1e-3;
+      t_head += dh;
+      t_att += da;
+      t_layers += std::max(0.0, dt - dh);
+    }
+  }
+  // one head call's rows in evaluation order (row 0, then the lazily evaluated path, E:1475-1488):
+  // rows count until the first that overflows the screen, which counts the call's fallback
+  void screen_rows(const int* Gr, const int* nsurv, const int* fallback, int n) {
+    for (int r = 0; r < n; ++r) {
+      if (Gr[r] < 0) continue;
+      if (fallback[r]) {
+        ++scr_fallback;
+        return;
+      }
+      ++scr_rows;
+      scr_surv += nsurv[r];
+      scr_max = std::max<long>(scr_max, nsurv[r]);
+    }
+  }
+  void prefill_head() {  // the prefill's head row (E:1472 / 1489 for its head call)
+    int ns = 0, fb = 0, g = 0;
+    check(g4v_prefill_head_stats(G, &ns, &fb), "prefill_head_stats");
+    screen_rows(&g, &ns, &fb, 1);
   }
 
   // E:1584-1679 for one request
@@ -319,7 +372,10 @@ struct Engine {
       const int np = n - start;
       for (int b = 0; b < np; b += pfb) fwd_splits(F + start + b, std::min(pfb, np - b));
     }
-    check(g4v_prefill(G, prompt.data() + start, n - start, F + start, pfb, active, &g0, hprev.data()), "prefill");
+    fwd_call((n - start + pfb - 1) / pfb, [&] {  // every block a forward pass (E:1597-1598)
+      check(g4v_prefill(G, prompt.data() + start, n - start, F + start, pfb, active, &g0, hprev.data()), "prefill");
+    });
+    prefill_head();
     const double tp = now() - t0;
     std::vector<int> gen{g0};
     if (print && nnew > 0) {
@@ -337,6 +393,8 @@ struct Engine {
       return;
     }
     const double t1 = now();
+    const double layers0 = t_layers, att0 = t_att, head0 = t_head, draft0 = t_draft;  // E:1605
+    const long fwd0 = n_fwd;
     size_t emitted = 1;
     auto emit = [&]() {  // E:1612-1614
       if (!stream || !print) return;
@@ -362,7 +420,10 @@ struct Engine {
     if (k_draft == 0 || (!drafter && ng_n <= 0)) {  // E:1615: plain decode
       for (int i = 1; i < nnew && !is_stop(gen.back()); ++i) {
         const int t = gen.back();
-        check(g4v_verify_step(G, &t, 0, 0, F + n + i - 1, fwd_splits(F + n + i - 1, 1), &R, nullptr), "verify_step");
+        fwd_call(1, [&] {
+          check(g4v_verify_step(G, &t, 0, 0, F + n + i - 1, fwd_splits(F + n + i - 1, 1), &R, nullptr), "verify_step");
+        });
+        screen_rows(R.G, R.nsurv, R.fallback, 8);
         gen.push_back(R.commit[0]);
         emit();
       }
@@ -403,8 +464,10 @@ struct Engine {
         if (!used_ng && drafter && k > 0) {  // E:1632-1645 (TAU 0: every draft is kept)
           int d[3], sec[3];
           float gap[3];
+          const double td0 = now();  // E:1646 T_DRAFT
           check(g4v_draft_mtp(G, conf, first ? hprev.data() : nullptr, P, k, draft_splits(P), d, sec, gap, nullptr),
                 "draft_mtp");
+          t_draft += now() - td0;
           sec1 = sec[0];
           gap1 = gap[0];
           const bool allow_sib = sib_gap >= 0.0f && rounds >= 1 && state < 2 && k >= 2 && sec1 >= 0 && sec1 != d[0];
@@ -422,11 +485,16 @@ struct Engine {
           block[sibling] = sec1;
           ++tree_attempts;
           const bool allow_hit = tree || (P + 1 + sibling <= ATT_PAR && gap1 >= 0.25f);  // E:1650
-          check(g4v_verify_sibling(G, block, nd, P + 1, fwd_splits(P + 1, nd + 2), allow_hit ? 1 : 0, &R, nullptr),
-                "verify_sibling");
+          fwd_call(1, [&] {
+            check(g4v_verify_sibling(G, block, nd, P + 1, fwd_splits(P + 1, nd + 2), allow_hit ? 1 : 0, &R, nullptr),
+                  "verify_sibling");
+          });
         } else {
-          check(g4v_verify_step(G, block, nd, 0, P + 1, fwd_splits(P + 1, nd + 1), &R, nullptr), "verify_step");  // E:1649
+          fwd_call(1, [&] {  // E:1649
+            check(g4v_verify_step(G, block, nd, 0, P + 1, fwd_splits(P + 1, nd + 1), &R, nullptr), "verify_step");
+          });
         }
+        screen_rows(R.G, R.nsurv, R.fallback, 8);
         ++rounds;
         if (R.branch == 1) {  // E:1650-1653 the tree hit: row 0's token and the sibling's
           ++tree_hits;
@@ -459,6 +527,10 @@ struct Engine {
     }
     emit();
     const double td = now() - t1;
+    if (getenv("ENGINE_DECODE_STAGE"))  // E:1672
+      fprintf(stderr, "DECODE_STAGE forwards=%ld layers_ms=%.1f split_att_ms=%.1f head_ms=%.1f draft_ms=%.1f total_ms=%.1f\n",
+              n_fwd - fwd0, (t_layers - layers0) * 1000, (t_att - att0) * 1000, (t_head - head0) * 1000,
+              (t_draft - draft0) * 1000, td * 1000);
     // E:1671: the cache holds the prompt and gen[0 .. P - n] (E:1675: nothing reusable past a fake context)
     if (F == 0) check(g4v_slot_end(G, prompt.data(), n, gen.data(), (int)gen.size(), P), "slot_end");
     if ((int)gen.size() > nnew) gen.resize(nnew);
@@ -540,6 +612,12 @@ int main(int argc, char** argv) {
   const bool g_i8 = env_int("ENGINE_PREFILL_INT8", 0) == 1;
   const bool dec_i8 = !(getenv("ENGINE_DECODE_INT8") && atoi(getenv("ENGINE_DECODE_INT8")) == 0);
   check(g4v_create(0, &G), "create");
+  e.scr_on = getenv("ENGINE_HEAD_SCREEN") && atoi(getenv("ENGINE_HEAD_SCREEN")) == 1;  // E:1235
+  e.stage_prof = getenv("ENGINE_DECODE_STAGE") || getenv("ENGINE_STAGE_PROF");
+  if (e.stage_prof) {  // per-class events on eagerly launched passes (a replayed graph records none)
+    check(g4v_set_graphs(G, 0), "set_graphs");
+    check(g4v_profile(G, (1u << G4V_PROF_NTAGS) - 1), "profile");
+  }
   check(g4v_set_prefill_int8(G, g_i8 ? 1 : 0), "set_prefill_int8");
   Checkpoint ck;
   bool gemma = false;
@@ -579,7 +657,8 @@ int main(int argc, char** argv) {
   {  // E:1578: one warm-up pass at position 0 (the cache is not marked valid by it)
     const int w = 2;
     int g = 0;
-    check(g4v_prefill(G, &w, 1, 0, e.pfb, e.fwd_splits(0, 1), &g, nullptr), "warm-up");
+    e.fwd_call(1, [&] { check(g4v_prefill(G, &w, 1, 0, e.pfb, e.fwd_splits(0, 1), &g, nullptr), "warm-up"); });
+    e.prefill_head();
   }
   if (getenv("ENGINE_SERVE")) {
     std::string line;
@@ -618,7 +697,14 @@ int main(int argc, char** argv) {
       return 2;
     }
     e.run_req(prompt, atoi(argv[4]), true);
+    if (e.scr_on && e.scr_rows)  // E:1690
+      fprintf(stderr, "SCREEN rows=%ld survivors mean=%.1f max=%ld fallbacks=%ld\n", e.scr_rows,
+              (double)e.scr_surv / e.scr_rows, e.scr_max, e.scr_fallback);
   }
+  if (getenv("ENGINE_STAGE_PROF"))  // E:1691
+    fprintf(stderr, "STAGES total over %ld fwd calls (ms): layers %.0f (of which split-KV attention %.0f) | head %.0f | "
+                    "drafter %.0f\n", e.n_fwd, e.t_layers * 1e3, e.t_att * 1e3, e.t_head * 1e3, e.t_draft * 1e3);
+  fflush(stderr);
   fflush(stdout);
   g4v_destroy(G);
   return 0;

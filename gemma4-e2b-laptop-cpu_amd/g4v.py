@@ -59,6 +59,7 @@ SIGNATURES = {
     "g4v_verify_sibling": (_i, [_vp, _i32p, _i, _i, _i, _i, _vp, _vp]),
     "g4v_profile": (_i, [_vp, C.c_uint]),
     "g4v_profile_read": (_i, [_vp, _vp, _vp, _vp, _i]),
+    "g4v_prefill_head_stats": (_i, [_vp, _i32p, _i32p]),
     "g4v_hbm_stream": (_i, [_vp, C.c_size_t, _i, _i, _vp]),
     "g4v_sync": (_i, [_vp]),
     "g4v_set_graphs": (_i, [_vp, _i]),
@@ -451,6 +452,13 @@ class Device:
         cnt = np.zeros(n, np.int64)
         self.L.g4v_profile_read(self.h, ms.ctypes.data, by.ctypes.data, cnt.ctypes.data, n)
         return {t: dict(ms=float(ms[i]), bytes=float(by[i]), launches=int(cnt[i])) for i, t in enumerate(PROF_TAGS)}
+
+    def prefill_head_stats(self):
+        """(screen survivors, fallback) of the last prefill's head row"""
+        ns = np.zeros(1, np.int32)
+        fb = np.zeros(1, np.int32)
+        self._ok(self.L.g4v_prefill_head_stats(self.h, ns, fb), "prefill_head_stats")
+        return int(ns[0]), bool(fb[0])
 
     def verify(self, toks, na, nb, pos0, T=8, hidden=False):
         r = VerifyResult()

@@ -267,6 +267,11 @@ int g4v_history_read(g4v_ctx* c, int* toks, int cap, int* L);
 #define G4V_PROF_NTAGS 13
 int g4v_profile(g4v_ctx* c, unsigned mask);
 int g4v_profile_read(g4v_ctx* c, double* ms, double* bytes, long long* count, int n);
+/* the last g4v_prefill's head row (its G0): screen survivors and whether it fell back to the full
+ * head (more than 30,000 survivors), as g4v_verify_result reports them per row -- what the
+ * reference's SCREEN statistics count per evaluated row (E:1472 scr_rows / scr_surv / scr_max,
+ * E:1489 scr_fallback, printed at E:1690) */
+int g4v_prefill_head_stats(g4v_ctx* c, int* nsurv, int* fallback);
 
 /* device read (mode 0) or copy (mode 1, read + write bytes counted) bandwidth in GB/s over a
  * buffer of `bytes` (>= 1 MiB, a multiple of 16) streamed `passes` times.  No counterpart in the

@@ -13,6 +13,7 @@ synthetic checkpoint of tests/golden/gemma_layout.py uploaded through the C ABI.
   * g4v_engine's drafting sessions, the server's environment (W4A8 prompt and verify) among them,
     print what the reference engine printed."""
 import os
+import re
 import subprocess
 import sys
 
@@ -227,6 +228,81 @@ def test_gemma_engine_matches_reference_engine(gemma, i8):
     got = [[int(x) for x in ln.split()[1:]] for ln in proc.stdout.splitlines() if ln.startswith("GEN:")]
     assert firsts == [int(t) for t in fx["first" + sfx]]
     assert got == [[int(t) for t in g] for g in gens], (got, gens)
+
+
+def test_gemma_engine_stage_lines(gemma, tmp_path):
+    """g4v_engine's observability lines on the 196-token prompt, plain decode (ENGINE_K=0):
+    SCREEN (E:1690) counts every head call -- the warm-up pass, the prompt's last row and one row
+    per decode step -- as a screened row or a fallback; DECODE_STAGE (E:1672) one forward per
+    decode step, with split-KV attention time (positions past 192) and no drafter time; STAGES
+    (E:1691) every forward call (the warm-up, 7 prompt blocks of 32, the decode steps).  The
+    tokens equal the reference engine's."""
+    dev, d, fx, ctx = gemma
+    exe = os.path.join(os.path.dirname(HERE), "gemma4-e2b-laptop-cpu_amd", "g4v_engine")
+    prompt = np.split(fx["prompts"], np.cumsum(fx["prompt_lens"])[:-1])[2]
+    want = [int(t) for t in np.split(fx["gens"], np.cumsum(fx["gen_lens"])[:-1])[2]]
+    nnew = int(fx["nnew"][0])
+    pf = tmp_path / "prompt.ids"
+    pf.write_text(" ".join(str(int(t)) for t in prompt) + "\n")
+    env = dict(os.environ, ENGINE_K="0", ENGINE_CTX=str(ctx), ENGINE_DECODE_INT8="0", ENGINE_HEAD_SCREEN="1",
+               ENGINE_DECODE_STAGE="1", ENGINE_STAGE_PROF="1",
+               ENGINE_CPUS=",".join(str(c) for c in range(int(fx["cpus"][0]))))
+    for k in ("ENGINE_PREFILL_INT8", "ENGINE_ADAPTIVE_THREADS", "ENGINE_NGRAM", "ENGINE_STREAM", "ENGINE_SERVE"):
+        env.pop(k, None)
+    note(f"g4v_engine stage lines, prompt of {len(prompt)} tokens, {nnew} new")
+    proc = subprocess.run([exe, d, os.path.join(d, "index.tsv"), str(pf), str(nnew)], env=env, capture_output=True,
+                          text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    gen = [[int(x) for x in ln.split()[1:]] for ln in proc.stdout.splitlines() if ln.startswith("GEN:")]
+    assert gen == [want]
+    steps = len(want) - 1
+    lines = {ln.split()[0]: ln for ln in proc.stderr.splitlines() if ln.split()}
+    assert {"DECODE_STAGE", "STAGES"} <= set(lines), proc.stderr[-3000:]
+    # the same head calls through the library, counted by the reference's rule (E:1472, 1489): a
+    # row's survivors until the call's first row that overflows the screen, which counts one
+    # fallback; the line is printed only when some row was screened (E:1690)
+    T = int(fx["cpus"][0])
+    cnt = dict(rows=0, surv=0, max=0, fb=0)
+
+    def count(G, ns, fbk):
+        for g, n, f in zip(G, ns, fbk):
+            if g < 0:
+                continue
+            if f:
+                cnt["fb"] += 1
+                return
+            cnt["rows"] += 1
+            cnt["surv"] += n
+            cnt["max"] = max(cnt["max"], n)
+
+    dev.prefill(np.array([2], np.int32), 0, 32, T)  # the warm-up pass (E:1578)
+    ns, f = dev.prefill_head_stats()
+    count([0], [ns], [f])
+    toks = [int(dev.prefill(np.array(prompt, np.int32), 0, 32, T))]
+    ns, f = dev.prefill_head_stats()
+    count([0], [ns], [f])
+    for i in range(1, len(want)):
+        r = dev.verify(np.array([toks[-1]], np.int32), 0, 0, len(prompt) + i - 1, T)
+        toks.append(int(r.commit[0]))
+        count(list(r.G), list(r.nsurv), list(r.fallback))
+    assert toks == want
+    assert cnt["rows"] + cnt["fb"] == steps + 2
+    if cnt["rows"]:
+        scr = re.match(r"SCREEN rows=(\d+) survivors mean=([0-9.]+) max=(\d+) fallbacks=(\d+)$", lines["SCREEN"])
+        assert (int(scr[1]), int(scr[3]), int(scr[4])) == (cnt["rows"], cnt["max"], cnt["fb"]), lines["SCREEN"]
+        assert abs(float(scr[2]) - cnt["surv"] / cnt["rows"]) <= 0.051, lines["SCREEN"]
+    else:
+        assert "SCREEN" not in lines, lines["SCREEN"]
+    ds = re.match(r"DECODE_STAGE forwards=(\d+) layers_ms=([0-9.]+) split_att_ms=([0-9.]+) head_ms=([0-9.]+) "
+                  r"draft_ms=([0-9.]+) total_ms=([0-9.]+)$", lines["DECODE_STAGE"])
+    fwd, lay, att, head, dr, tot = int(ds[1]), *(float(ds[i]) for i in range(2, 7))
+    assert fwd == steps, lines["DECODE_STAGE"]
+    assert 0 < att < lay and head > 0 and dr == 0, lines["DECODE_STAGE"]
+    assert lay + head <= tot + 1.0, lines["DECODE_STAGE"]
+    st = re.match(r"STAGES total over (\d+) fwd calls \(ms\): layers (\d+) \(of which split-KV attention (\d+)\) \| "
+                  r"head (\d+) \| drafter (\d+)$", lines["STAGES"])
+    assert int(st[1]) == 1 + (len(prompt) + 31) // 32 + steps, lines["STAGES"]
+    assert int(st[5]) == 0, lines["STAGES"]
 
 
 def drafter_arrays(d):
