@@ -292,6 +292,57 @@ def gemma_pass_bytes(M, pos0=GM_CTX):
     return b
 
 
+def components_summary(dev, iters=30):
+    """configs 1-3 of the workload on their own, device-timed per launch (g4v_*_time): warm (the
+    launches repeat, operands stay in the caches) and cold (a 512 MB read before each launch evicts
+    the 256 MB last-level cache, outside the timed events).  The head of one row (config 1); the
+    W4G32 products 1536 x 1536, 6144 x 1536, the fused gate + up pair (2 x 6144 x 1536) and the
+    down projection (1536 x 6144) at 1, 2, 4 and 8 rows, and their W4A8 form at 2, 4 and 8 rows
+    (config 2); split-KV attention of 4 rows, 8 splits, at ctx 512, 2048, 6841 and with the 512
+    window at 6841 (config 3).  Bytes are the algorithmic ones (int4 + bf16 scales; K and V rows
+    attended), hbm_frac = bytes / cold time / 8 TB/s."""
+    rng = np.random.default_rng(SEED + 3)
+
+    def mat(N, K):
+        W = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+        s = rng.uniform(0.005, 0.02, (N, K // 32)).astype(np.float32)
+        return dev.w4_upload(W, (s.view(np.uint32) >> 16).astype(np.uint16))
+
+    frac = lambda b, us: round(b / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)
+    out = {"timing": "device events per launch on the library stream; cold = 512 MB read before each launch",
+           "iters": iters}
+    hrow = rng.standard_normal(1536).astype(np.float32)
+    hw, ns, fb = dev.head_time(hrow, iters, False)
+    hc = dev.head_time(hrow, iters, True)[0]
+    out["head_1row"] = {"bytes": SCREEN_BYTES, "warm_us": round(hw, 2), "cold_us": round(hc, 2),
+                        "survivors": ns, "fallback_full_head": fb, "cold_hbm_frac_screen_bytes": frac(SCREEN_BYTES, hc)}
+    g = {}
+    for name, shp in (("1536x1536", [(1536, 1536)]), ("6144x1536", [(6144, 1536)]),
+                      ("gate_up_2x6144x1536", [(6144, 1536), (6144, 1536)]), ("down_1536x6144", [(1536, 6144)])):
+        ms = [mat(N, K) for N, K in shp]
+        nb = sum(N * K // 2 + N * K // 16 for N, K in shp)
+        row = {"bytes": nb}
+        for M in (1, 2, 4, 8):
+            w = dev.w4g32_time(ms, M, iters, cold=False)
+            c = dev.w4g32_time(ms, M, iters, cold=True)
+            row[f"m{M}"] = {"warm_us": round(w, 2), "cold_us": round(c, 2), "cold_hbm_frac": frac(nb, c)}
+        for M in (2, 4, 8):
+            c = dev.w4g32_time(ms, M, iters, cold=True, w4a8=True)
+            row[f"w4a8_m{M}"] = {"cold_us": round(c, 2), "cold_hbm_frac": frac(nb, c)}
+        g[name] = row
+    out["w4g32"] = g
+    a = {}
+    for ctx, window in ((512, False), (2048, False), (6841, False), (6841, True)):
+        keys = min(ctx, 512 + 3) if window else ctx
+        nb = keys * HD * 2 * 2
+        w = dev.attn_time(ctx, 4, 8, window, iters, cold=False)
+        c = dev.attn_time(ctx, 4, 8, window, iters, cold=True)
+        a[f"ctx{ctx}" + ("_window512" if window else "")] = {"bytes": nb, "warm_us": round(w, 2), "cold_us": round(c, 2),
+                                                          "cold_hbm_frac": frac(nb, c)}
+    out["attn_4rows_8splits"] = a
+    return out
+
+
 GM_SHAPES = ((1, False), (4, False), (8, False), (4, True), (8, True))
 
 
@@ -384,10 +435,12 @@ def main():
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--workload", choices=["verify", "long_prompt", "gemma_layout"], default="verify")
+    ap.add_argument("--workload", choices=["verify", "long_prompt", "gemma_layout", "components"], default="verify")
     ap.add_argument("--cpu-only", default=None, help=argparse.SUPPRESS)  # child process of the CPU baseline
     ap.add_argument("--no-long-prompt", action="store_true", help="skip the long-prompt sub-measurement")
     ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-E2B layout sub-measurement")
+    ap.add_argument("--no-components", action="store_true",
+                    help="skip the components sub-measurement (head, products, attention on their own)")
     ap.add_argument("--gemma-shapes", default=None,
                     help="gemma_layout: the passes to time, e.g. 1,4,8,4i8,8i8 (rows; i8: W4A8 products)")
     ap.add_argument("--no-graphs", action="store_true", help="gemma_layout: launch the passes' kernels eagerly")
@@ -401,6 +454,12 @@ def main():
         sys.exit(2)
     if args.workload == "long_prompt":
         main_long_prompt(args, load_g4v())
+        return
+    if args.workload == "components":  # configs 1-3 on their own (the line's sub-object as a line)
+        g4v = load_g4v()
+        dev = g4v.Device(0)
+        dev.model_synth(SEED, V, NL, I, CTXCAP)
+        print(json.dumps(components_summary(dev)), flush=True)
         return
     if args.workload == "gemma_layout":  # the Gemma-4-E2B layout's passes alone (its sub-object as a line)
         shapes = GM_SHAPES
@@ -500,6 +559,8 @@ def main():
     out["hbm_stream"] = {"read_gbs": round(dev.hbm_stream(2 << 30, 5), 1),
                          "copy_gbs": round(dev.hbm_stream(1 << 30, 5, copy=True), 1), "read_buffer": 2 << 30,
                          "copy_buffer": 1 << 30, "passes": 5}
+    if not args.no_components:  # configs 1-3 on their own, warm and cold
+        out["components"] = components_summary(dev)
     if not args.no_cpu:
         # A (GPU) and B (CPU) interleaved: A1 above, B1 one thread per physical core, A2, B2 8 threads
         try:

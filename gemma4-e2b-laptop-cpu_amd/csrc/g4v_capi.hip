@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -3242,6 +3243,156 @@ int g4v_hbm_stream(g4v_ctx* c, size_t bytes, int passes, int mode, double* gbps)
   HIPCHK(hipEventElapsedTime(&ms, ev.e[0], ev.e[1]));
   *gbps = (double)passes * (double)bytes * (mode == 1 ? 2.0 : 1.0) / ((double)ms * 1e-3) / 1e9;
   return 0;
+}
+
+// ---- the components on their own, device-timed: one launch (or launch pair) at a time between
+// two events on the library's stream.  Warm: the launches repeat on the same operands, which stay
+// in the caches (4 MB L2 per XCD, 256 MB last-level cache).  Cold: before each timed launch a
+// read of a 512 MB buffer (twice the last-level cache) evicts them, outside the events.
+static int time_launches(g4v_ctx* c, int iters, int cold, const std::function<void()>& launch, float* us) {
+  hipStream_t st = c->st;
+  DBuf src, dst;
+  const size_t ebytes = (size_t)512 << 20, n16 = ebytes / 16;
+  if (cold) {
+    ALLOC(src, ebytes);
+    ALLOC(dst, (size_t)stream_grid() * 256 * 16);
+    launch_stream(2, nullptr, src.as<uint4>(), n16, st);
+  }
+  launch();  // warm-up (and code load)
+  HIPCHK(hipGetLastError());
+  struct Events {
+    hipEvent_t e[2] = {nullptr, nullptr};
+    ~Events() {
+      for (hipEvent_t x : e)
+        if (x) (void)hipEventDestroy(x);
+    }
+  } ev;
+  HIPCHK(hipEventCreate(&ev.e[0]));
+  HIPCHK(hipEventCreate(&ev.e[1]));
+  double tot = 0;
+  for (int i = 0; i < iters; ++i) {
+    if (cold) launch_stream(0, src.as<uint4>(), dst.as<uint4>(), n16, st);
+    HIPCHK(hipEventRecord(ev.e[0], st));
+    launch();
+    HIPCHK(hipEventRecord(ev.e[1], st));
+    HIPCHK(hipEventSynchronize(ev.e[1]));
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, ev.e[0], ev.e[1]));
+    tot += ms;
+  }
+  HIPCHK(hipGetLastError());
+  *us = (float)(tot * 1000.0 / iters);
+  return 0;
+}
+
+int g4v_w4g32_time(g4v_ctx* c, int nmat, const int* h, int M, int iters, int flags, float* us) {
+  if (!c) return G4V_E_ARG;
+  const int cold = flags & 1;
+  const bool a8 = (flags & 2) != 0;
+  ARGCHK(nmat >= 1 && nmat <= 3 && h && us && M >= 1 && M <= MAXM && iters >= 1 && iters <= 10000,
+         "w4g32_time: 1 to 3 matrices, 1 <= M <= 8, 1 <= iters <= 10000");
+  size_t ntot = 0;
+  for (int j = 0; j < nmat; ++j) {
+    ARGCHK(h[j] >= 0 && h[j] < (int)c->mats.size(), "w4g32_time: bad handle");
+    ARGCHK(c->mats[h[j]]->K == c->mats[h[0]]->K && c->mats[h[j]]->N % 64 == 0,
+           "w4g32_time: the matrices need the same K and N % 64 == 0");
+    ntot += c->mats[h[j]]->N;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  const int K = c->mats[h[0]]->K;
+  for (int j = 0; j < nmat; ++j) {  // the row-tiled copies, once per handle
+    Mat& m = *c->mats[h[j]];
+    ARGCHK(!a8 || m.a8w.p, "w4g32_time: W4A8 needs the matrices' operand tiles (N % 16 == 0)");
+    if (!a8 && !m.tw.p) {
+      ALLOC(m.tw, (size_t)m.N * m.K / 2);
+      ALLOC(m.ts, (size_t)m.N * m.K / 16);
+      launch_tile_w4(m.wr.as<uint4>(), m.s.as<uint16_t>(), m.tw.as<uint4>(), m.ts.as<uint4>(), m.N, m.K, c->st);
+    }
+  }
+  if (c->gx.n < (size_t)MAXM * K * 4) ALLOC(c->gx, (size_t)MAXM * K * 4);
+  if (c->gy.n < (size_t)M * ntot * 4) ALLOC(c->gy, (size_t)MAXM * ntot * 4);
+  HIPCHK(hipMemsetAsync(c->gx.p, 0, (size_t)M * K * 4, c->st));  // staged rows (values do not matter)
+  GemvTArgs a{};
+  size_t off = 0;
+  for (int j = 0; j < nmat; ++j) {
+    const Mat& m = *c->mats[h[j]];
+    a.mat[j] = a8 ? W4Tile{m.a8w.as<uint4>(), m.a8s.as<uint4>(), m.N} : m.tile();
+    a.y[j] = c->gy.as<float>() + off;
+    a.ldy[j] = m.N;
+    off += (size_t)M * m.N;
+  }
+  a.xs = c->gx.as<float4>();
+  a.K = K;
+  a.M = M;
+  // the verify pass's launch shapes: one row a block at M = 1 (32-row tiles; plain products of
+  // K % 2048 == 0 on the one-row kernel), else 2 rows (4 for a pair, 1 past K 1536) on 64-row tiles;
+  // W4A8: the verify pass's product of staged rows (quantised in its blocks)
+  const int mpl = M == 1 ? 1 : (nmat >= 2 ? std::min(4, M) : (K > H ? 1 : 2)), tr = M == 1 ? 32 : 64;
+  if (a8) ARGCHK(K % 256 == 0, "w4g32_time: W4A8 needs K % 256 == 0");
+  return time_launches(c, iters, cold, [&] {
+    if (a8)
+      (void)launch_gemv_a8(a, c->st);
+    else
+      (void)launch_gemv_t(a, c->st, mpl, tr);
+  }, us);
+}
+
+int g4v_attn_time(g4v_ctx* c, int npos, int M, int nsplit, int window, int iters, int cold, float* us) {
+  if (!c) return G4V_E_ARG;
+  ARGCHK(us && npos >= M && npos <= 65536 && M >= 1 && M <= MAXM && nsplit >= 1 && nsplit <= MAXT && iters >= 1 &&
+             iters <= 10000,
+         "attn_time: M <= npos <= 65536, 1 <= M <= 8, 1 <= nsplit <= 16, 1 <= iters <= 10000");
+  AttnGeom g{};
+  g.M = M;
+  g.kmax = npos - 1;
+  g.kmin = g.kmax;
+  g.T = nsplit;
+  for (int m = 0; m < M; ++m) {
+    g.pos[m] = npos - M + m;
+    g.lo[m] = window ? std::max(0, g.pos[m] - 511) : 0;
+    g.skip_lo[m] = 1;
+    g.skip_hi[m] = 0;
+    g.kmin = std::min(g.kmin, g.lo[m]);
+  }
+  const int len = g.kmax - g.kmin + 1;
+  ARGCHK((len + nsplit - 1) / nsplit <= attn_pmax(), "attn_time: more positions per split than the split buffer holds");
+  HIPCHK(hipSetDevice(c->device));
+  const size_t kvb = (size_t)kv_cap(npos) * HD * 2;
+  if (c->ak.n < kvb) ALLOC(c->ak, kvb);
+  if (c->av.n < kvb) ALLOC(c->av, kvb);
+  if (c->aq.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->aq, (size_t)MAXM * NQ * HD * 4);
+  if (c->ao.n < (size_t)MAXM * NQ * HD * 4) ALLOC(c->ao, (size_t)MAXM * NQ * HD * 4);
+  if (c->po.n < (size_t)MAXT * MAXM * NQ * HD * 4) {
+    drop_graphs(c);  // the split partials are shared with the captured verify steps
+    ALLOC(c->po, (size_t)MAXT * MAXM * NQ * HD * 4);
+    ALLOC(c->pm, (size_t)MAXT * MAXM * NQ * 4);
+    ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
+  }
+  // finite operands (bf16 0x3c3c, fp32 0x3c3c3c3c): the values do not change the work
+  HIPCHK(hipMemsetAsync(c->ak.p, 0x3c, kvb, c->st));
+  HIPCHK(hipMemsetAsync(c->av.p, 0x3c, kvb, c->st));
+  HIPCHK(hipMemsetAsync(c->aq.p, 0x3c, (size_t)M * NQ * HD * 4, c->st));
+  return time_launches(c, iters, cold, [&] {
+    launch_attn_geom(c->ak.as<uint16_t>(), c->av.as<uint16_t>(), c->aq.as<float>(), NQ * HD, g, c->po.as<float>(),
+                     c->pm.as<float>(), c->pl.as<float>(), c->ao.as<float>(), NQ * HD, c->st);
+  }, us);
+}
+
+int g4v_head_time(g4v_ctx* c, const float* h, int iters, int cold, float* us, int* nsurv, int* fallback) {
+  if (!c) return G4V_E_ARG;
+  if (!c->head_ready) {
+    c->err = "head_time: no head (g4v_head_build or g4v_model_synth first)";
+    return G4V_E_STATE;
+  }
+  ARGCHK(h && us && iters >= 1 && iters <= 10000, "head_time: need h and 1 <= iters <= 10000");
+  int G = 0, ns = 0, fb = 0;
+  int r = g4v_head_argmax(c, h, 1, &G, &ns, &fb);  // uploads the row and its norm (E:1417)
+  if (r) return r;
+  if (nsurv) *nsurv = ns;
+  if (fallback) *fallback = fb;
+  return time_launches(c, iters, cold, [&] {
+    head_run(head_args(c, c->hb1, c->hrow.as<float>(), c->hnrow.as<float>(), 1, nullptr), c->st);
+  }, us);
 }
 
 int g4v_sync(g4v_ctx* c) {

@@ -39,6 +39,9 @@ SIGNATURES = {
     "g4v_w4a8_quant": (_i, [_vp, _f32p, _i, _i, _vp, _f32p, _i32p]),
     "g4v_w4a8_gemm": (_i, [_vp, _i, _f32p, _i, _f32p]),
     "g4v_w4a8_bench": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_w4g32_time": (_i, [_vp, _i, _i32p, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_attn_time": (_i, [_vp, _i, _i, _i, _i, _i, _i, C.POINTER(C.c_float)]),
+    "g4v_head_time": (_i, [_vp, _f32p, _i, _i, C.POINTER(C.c_float), _i32p, _i32p]),
     "g4v_attn_splitkv": (_i, [_vp, _u16p, _u16p, _i, _i, _i, _i, _f32p, _i32p, _i32p, _i32p, _i32p,
                               _i, _i, _i, _f32p]),
     "g4v_attn_splitkv_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i32p, _i32p, _i32p, _i32p,
@@ -218,6 +221,31 @@ class Device:
         Y = np.empty((M, N), np.float32)
         self._ok(self.L.g4v_w4a8_gemm(self.h, h, X, M, Y), "w4a8_gemm")
         return Y
+
+    def w4g32_time(self, mats, M, iters=50, cold=False, w4a8=False):
+        """device us per launch of the row-tile GEMV (w4a8: the W4A8 product) over the matrices
+        `mats` (handles) on M rows"""
+        us = C.c_float()
+        h = np.array([m[0] for m in mats], np.int32)
+        fl = (1 if cold else 0) | (2 if w4a8 else 0)
+        self._ok(self.L.g4v_w4g32_time(self.h, len(mats), h, M, iters, fl, C.byref(us)), "w4g32_time")
+        return us.value
+
+    def attn_time(self, npos, M, T=8, window=False, iters=50, cold=False):
+        """device us per split-KV attention (split + merge) of M rows at the end of npos positions"""
+        us = C.c_float()
+        self._ok(self.L.g4v_attn_time(self.h, npos, M, T, 1 if window else 0, iters, 1 if cold else 0, C.byref(us)),
+                 "attn_time")
+        return us.value
+
+    def head_time(self, h, iters=20, cold=False):
+        """(device us per head pass of row h, its survivors, whether it fell back to the full head)"""
+        us = C.c_float()
+        ns = np.zeros(1, np.int32)
+        fb = np.zeros(1, np.int32)
+        self._ok(self.L.g4v_head_time(self.h, _c(h, np.float32), iters, 1 if cold else 0, C.byref(us), ns, fb),
+                 "head_time")
+        return us.value, int(ns[0]), bool(fb[0])
 
     def w4a8_bench(self, mat, M, iters=100):
         us = C.c_float()

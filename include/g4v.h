@@ -68,6 +68,23 @@ int g4v_w4a8_quant(g4v_ctx* c, const float* x, int M, int K, int8_t* q, float* s
 int g4v_w4a8_gemm(g4v_ctx* c, int h, const float* x, int M, float* y);
 /* quant + GEMM with the operands already on the device; times `iters` runs, us per run */
 int g4v_w4a8_bench(g4v_ctx* c, int h, int M, int iters, float* us_per_launch);
+/* ---- the components on their own, device-timed (the reference times its kernels alone in
+ * bench/attn_bench.cpp:16-34, warm and cold): *us = the mean of `iters` launches, each between two
+ * events on the library's stream.  cold = 0: the launches repeat on operands that stay in the
+ * caches; cold = 1: a read of 512 MB (twice the last-level cache) before each launch, outside the
+ * events, evicts them.
+ * g4v_w4g32_time: one launch of the verify pass's row-tile GEMV over nmat matrices of the same K
+ * (N % 64 == 0; two of them = the fused gate/up pair) on M staged rows (E:1289, 1363-1371); flags
+ * bit 0 = cold, bit 1 = the W4A8 product instead (lin_multi with G_I8_ACTIVE, E:311; the rows
+ * quantised in the product's blocks). */
+int g4v_w4g32_time(g4v_ctx* c, int nmat, const int* h, int M, int iters, int flags, float* us);
+/* split-KV attention (k_attn_split + k_attn_merge) of M rows at positions npos - M .. npos - 1 over
+ * keys [0 or pos - 511 with window, pos], nsplit splits, on a device cache of npos positions
+ * (E:1305-1327, the ATT_PAR path) */
+int g4v_attn_time(g4v_ctx* c, int npos, int M, int nsplit, int window, int iters, int cold, float* us);
+/* the head (screen, threshold, survivors, rescore, and the full head on an overflow) of one row h
+ * [1536] (E:1406-1500); nsurv / fallback as g4v_head_argmax reports them for that row */
+int g4v_head_time(g4v_ctx* c, const float* h, int iters, int cold, float* us, int* nsurv, int* fallback);
 
 /* ---- split-KV attention: attn_task + attn_merge (E:743-877, E:1019-1059) with the
  * reference's split geometry [kmin + t*len/T, kmin + (t+1)*len/T).  Kc, Vc: [npos][hd] bf16;

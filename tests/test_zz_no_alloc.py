@@ -1,7 +1,8 @@
 """GPU parity of the allocation-free split-KV attention entry point (g4v_attn_splitkv_noalloc)
-against g4v_attn_splitkv on the same inputs: device buffers in and out, scratch in the library's
-file-scope device array, two calls in a row with the second on a smaller input (the scratch
-keeps the first call's contents), bit for bit."""
+against g4v_attn_splitkv and the oracle's split-KV attention (E:743-877, E:1019-1059) on the same
+inputs: device buffers in and out, scratch in the library's file-scope device array, two calls in
+a row with the second on a smaller input (the scratch keeps the first call's contents), bit for
+bit."""
 import ctypes as C
 
 import numpy as np
@@ -63,6 +64,8 @@ def test_noalloc_matches_attn_splitkv(orc, dev):
             dev.attn_noalloc(hip.put(Kc), hip.put(Vc), npos, hip.put(q), M, pos, lo, sl, sh, kmin, kmax, T, od)
             got = hip.get(od, (M, 2048), np.float32)
             assert same(got, want), first_diff(got, want)
+            ref = orc.attn(Kc, Vc, 256, 8, q, pos, lo, sl, sh, kmin, kmax, T)
+            assert same(got, ref), first_diff(got, ref)
     finally:
         hip.free()
 
