@@ -559,6 +559,18 @@ def main():
     out["hbm_stream"] = {"read_gbs": round(dev.hbm_stream(2 << 30, 5), 1),
                          "copy_gbs": round(dev.hbm_stream(1 << 30, 5, copy=True), 1), "read_buffer": 2 << 30,
                          "copy_buffer": 1 << 30, "passes": 5}
+    # the same steps with W4A8 products (ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8 on, E:1600:
+    # the reference server's mode), replayed graphs
+    dev.set_prefill_int8(True)
+    dev.set_decode_int8(True)
+    run_steps(verify, 2, pos0, conf, 8000)
+    dev.sync()
+    t3 = time.perf_counter()
+    tok3, _, _ = run_steps(verify, args.steps, pos0, conf, 8000)
+    dev.sync()
+    out["w4a8_step"] = {"ms_per_step": round((time.perf_counter() - t3) * 1e3 / args.steps, 4), "steps": args.steps,
+                        "tokens_per_step": round(tok3 / args.steps, 3)}
+    dev.set_decode_int8(False)
     if not args.no_components:  # configs 1-3 on their own, warm and cold
         out["components"] = components_summary(dev)
     if not args.no_cpu:

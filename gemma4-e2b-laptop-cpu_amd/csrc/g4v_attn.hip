@@ -707,6 +707,13 @@ void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, con
                      (const uint16_t*)KC, (const uint16_t*)VC, sliding, T, P);
 }
 
+void launch_attn_merge(const float* po, const float* pm, const float* pl, int M, int T, float* out, int ldo,
+                       float* gs, hipStream_t st) {
+  AttnPtrs P{nullptr, nullptr, nullptr, 0, const_cast<float*>(po), const_cast<float*>(pm), const_cast<float*>(pl),
+             out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  hipLaunchKernelGGL(k_attn_merge, dim3(M, NQ), dim3(HD), 0, st, P, M, T);
+}
+
 void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g,
                       float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh, float* gs) {
   AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,

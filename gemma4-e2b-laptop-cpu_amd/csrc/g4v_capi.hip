@@ -113,6 +113,7 @@ struct g4v_ctx {
   VerifyResultDev* res_host = nullptr;
   // attention standalone
   DBuf ak, av, aq, ao;
+  DBuf vags;  // group sums of the merged attention rows of a W4A8 verify pass [MAXM][NQ * HD / 32]
   DBuf po5, pm5, pl5;  // split partials at head dim 512
   // the Gemma-4-E2B layout (g4v_model_create_gemma): per-layer geometry, the per-layer-input
   // branch, the owners' caches and the row buffers of its passes
@@ -1085,6 +1086,7 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   ALLOC(c->pl, (size_t)MAXT * MAXM * NQ * 4);
   ALLOC(c->stepd, sizeof(StepDev));
   ALLOC(c->vatt, (size_t)MAXM * NQ * HD * 4);
+  ALLOC(c->vags, (size_t)MAXM * NQ * HD / 32 * 4);
   ALLOC(c->vsc, (size_t)8 * MAXM * ctxcap * 4);
   ALLOC(c->resd, sizeof(VerifyResultDev));
   HIPCHK(hipStreamSynchronize(st));  // rt goes out of scope
@@ -1454,6 +1456,10 @@ static int pass_path(int M, int pos0, int nb) {
 static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
   hipStream_t st = c->st;
   const int NL = c->NL, I = c->I;
+  // G_I8_ACTIVE in the decode (E:1600) and lin_multi's M >= 2 (E:311): W4A8 products, on the
+  // matrices' a8 operand tiles; the same pass otherwise (every other value is exact either way)
+  const bool a8 = c->dec_i8 && c->pf_i8 && M >= 2;
+  auto a8t = [](const Mat& m) { return W4Tile{m.a8w.as<uint4>(), m.a8s.as<uint4>(), m.N}; };
   const StepDev* sp = c->stepd.as<StepDev>();
   const StepDev& sh = *c->step_host;
   const float sqh = std::sqrt((float)H);
@@ -1492,7 +1498,12 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
       a.nrm_scalar = pln.scalar;
     }
     pmark(c, PT_GEMV_QKV, 1, 0);
-    launch_gemv_t(a, st, c->gcfg[0][0], c->gcfg[0][1]);
+    if (a8) {
+      for (int j = 0; j < 3; ++j) a.mat[j] = a8t(A.m[j]);
+      (void)launch_gemv_a8(a, st);
+    } else {
+      launch_gemv_t(a, st, c->gcfg[0][0], c->gcfg[0][1]);
+    }
     pmark(c, PT_GEMV_QKV, 0, w4_bytes(A.m[0]) + w4_bytes(A.m[1]) + w4_bytes(A.m[2]));
     const float* rstep = c->ropestep.as<float>() + (size_t)(A.sliding ? 0 : 1) * MAXM * HD;
     int kmin = sh.pos0 + M - 1;  // E:1325-1326 keys read by the pass: [kmin, pos0 + M - 1]
@@ -1517,17 +1528,25 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     ao.mat[0] = A.m[3].tile();
     ao.y[0] = c->o.as<float>();
     ao.ldy[0] = H;
-    if (path == 0) {
+    if (path == 0 && !a8) {
       ao.mrg_po = c->po.as<float>();
       ao.mrg_pm = c->pm.as<float>();
       ao.mrg_pl = c->pl.as<float>();
       ao.mrg_T = T;
     } else {
+      if (path == 0)  // W4A8: the merge on its own (E:1019-1059), staged, then the product
+        launch_attn_merge(c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), M, T, c->vatt.as<float>(), NQ * HD,
+                          c->vags.as<float>(), st);
       ao.xs = c->vatt.as<float4>();  // group sums formed in LDS from the staged copy
     }
     ao.K = NQ * HD;
     ao.M = M;
-    launch_gemv_t(ao, st, c->gcfg[1][0], c->gcfg[1][1]);
+    if (a8) {
+      ao.mat[0] = a8t(A.m[3]);
+      (void)launch_gemv_a8(ao, st);
+    } else {
+      launch_gemv_t(ao, st, c->gcfg[1][0], c->gcfg[1][1]);
+    }
     pmark(c, PT_GEMV_O, 0, w4_bytes(A.m[3]));
     GemvTArgs gu{};  // E:1366 gate/up + gelu, the attention residual / norm block (E:1358-1361) as prologue
     gu.mat[0] = W4Tile{A.m[4].tw.as<uint4>(), A.m[4].ts.as<uint4>(), I};
@@ -1543,7 +1562,13 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     gu.K = H;
     gu.M = M;
     pmark(c, PT_GEMV_GATEUP, 1, 0);
-    launch_gemv_t(gu, st, c->gcfg[2][0], c->gcfg[2][1]);
+    if (a8) {  // the gate and up matrices' own tiles (the pair-tiled copy is the exact GEMV's)
+      gu.mat[0] = a8t(A.m[4]);
+      gu.mat[1] = a8t(A.m[5]);
+      (void)launch_gemv_a8(gu, st);
+    } else {
+      launch_gemv_t(gu, st, c->gcfg[2][0], c->gcfg[2][1]);
+    }
     pmark(c, PT_GEMV_GATEUP, 0, w4_bytes(A.m[4]) + w4_bytes(A.m[5]));
     pmark(c, PT_GEMV_DOWN, 1, 0);
     GemvTArgs ad{};  // E:1373
@@ -1553,7 +1578,12 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     ad.xs = c->act.as<float4>();  // group sums formed in LDS from the staged copy
     ad.K = I;
     ad.M = M;
-    launch_gemv_t(ad, st, I > 6144 ? 1 : c->gcfg[3][0], c->gcfg[3][1]);  // (K 12288: one row per block)
+    if (a8) {
+      ad.mat[0] = a8t(A.m[6]);
+      (void)launch_gemv_a8(ad, st);
+    } else {
+      launch_gemv_t(ad, st, I > 6144 ? 1 : c->gcfg[3][0], c->gcfg[3][1]);  // (K 12288: one row per block)
+    }
     pmark(c, PT_GEMV_DOWN, 0, w4_bytes(A.m[6]));
     if (l + 1 == NL) {  // the last MLP residual block and the final norm (E:1414-1417) for the head
       pmark(c, PT_ROWS, 1, 0);
@@ -1611,8 +1641,6 @@ static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, in
   // E:1328-1349), or a tree of two branches of up to 4 drafts each
   ARGCHK(toks && out && na >= 0 && nb >= 0 && M <= MAXM && ((nb == 0 && na <= 7) || (na <= 4 && nb <= 4)),
          "verify_step: a chain of 0 <= na <= 7 drafts, or 0 <= na, nb <= 4");
-  ARGCHK(!(c->dec_i8 && c->pf_i8) || M == 1,
-         "verify_step: W4A8 verify passes (g4v_set_decode_int8) are built for the Gemma layout only");
   ARGCHK(nb == 0 || na >= 1, "verify_step: branch b needs a chain a");
   ARGCHK(pos0 >= 1 && pos0 + M <= c->ctxcap, "verify_step: positions beyond the cache");
   ARGCHK(nsplit >= 1 && nsplit <= MAXT, "verify_step: 1 <= nsplit <= 16");
@@ -1639,7 +1667,8 @@ static int verify_pass(g4v_ctx* c, const int* toks, int na, int nb, int pos0, in
     }
   }
   const int path = pass_path(M, pos0, nb);
-  const long long key = ((((long long)M * 8 + na) * 8 + nb) * 32 + nsplit) * 65536 + c->prof_mask;
+  const bool a8 = c->dec_i8 && c->pf_i8 && M >= 2;  // the pass's products (enqueue_verify)
+  const long long key = (((((long long)M * 8 + na) * 8 + nb) * 32 + nsplit) * 2 + (a8 ? 1 : 0)) * 65536 + c->prof_mask;
   g4v_ctx::Graph* gr = nullptr;
   for (auto& g : c->graphs)
     if (g.key == key && path == 0) gr = &g;  // only split-KV passes are captured

@@ -213,7 +213,8 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
   if (chain) {
     float* y = j == 0 ? a.y[0] : (j == 1 ? a.y[1] : a.y[2]);
     const int ldy = j == 0 ? a.ldy[0] : (j == 1 ? a.ldy[1] : a.ldy[2]);
-    y[(size_t)cm * ldy + 16 * mt + cn] = acc;
+    const int n = 16 * mt + cn;
+    y[(size_t)cm * ldy + (((a.yperm >> j) & 1) ? head16_index(n) : n)] = acc;
   }
 }
 
@@ -458,16 +459,17 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
       const int j = mj0;
       float* y = j == 0 ? a.y[0] : (j == 1 ? a.y[1] : a.y[2]);
       const int ldy = j == 0 ? a.ldy[0] : (j == 1 ? a.ldy[1] : a.ldy[2]);
-      y[(size_t)cm * ldy + n] = acc;
+      y[(size_t)cm * ldy + (((a.yperm >> j) & 1) ? head16_index(n) : n)] = acc;
     }
   }
 }
 
 // mat[j]: a8 tiles (launch_tile_a8) of matrices with N_j % 16 == 0; gateup: mat[0] the gate and
-// mat[1] the up matrix (equal N), y[0] the staged activation.  A product of staged rows (xs)
+// mat[1] the up matrix (equal N), y[0] the staged activation; yperm as GemvTArgs says (plain
+// outputs only).  A product of staged rows (xs)
 // quantises them in each block.  Returns the grid of the product (0: refused, nothing launched).
 int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
-  if (a.M < 1 || a.M > 8 || a.K % 256 || a.mrg_po || a.yperm) return 0;
+  if (a.M < 1 || a.M > 8 || a.K % 256 || a.mrg_po || (a.yperm && (a.gateup || a.epi_pli))) return 0;
   int tiles = 0;
   for (int j = 0; j < 3; ++j) {
     if (a.mat[j].N % 16 || (a.mat[j].N && (!a.mat[j].w || !a.mat[j].s))) return 0;

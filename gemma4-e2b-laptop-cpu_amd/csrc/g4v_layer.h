@@ -178,6 +178,10 @@ struct AttnGeom {
   int M, kmin, kmax, T;
   int pos[MAXM], lo[MAXM], skip_lo[MAXM], skip_hi[MAXM];
 };
+// E:1019-1059 alone: the merge of T splits' partials po [T][M][8][256], pm, pl (as k_attn_rows leaves
+// them) into out [M][ldo]; with gs, out staged (staged_index) with its group sums [M][ldo / 32]
+void launch_attn_merge(const float* po, const float* pm, const float* pl, int M, int T, float* out, int ldo,
+                       float* gs, hipStream_t st);
 // nh query heads (a multiple of 2, at most 8) of q rows [M][ldq]; partials keep the 8-head layout
 // gs not null: out written in the staged GEMV input layout (staged_index) with its group sums
 // [M][ldo / 32]

@@ -591,7 +591,7 @@ int main(int argc, char** argv) {
   }
   // E:1210 G_I8 and E:1600 DEC_I8: the prompt's linear layers run W4A8 when ENGINE_PREFILL_INT8=1,
   // and then the decode's verify passes of two rows or more too unless ENGINE_DECODE_INT8=0
-  // (g4v_set_decode_int8; the library builds that mode for the Gemma layout)
+  // (g4v_set_decode_int8)
   // settings whose reference paths this engine does not restate end the process (exit code 2)
   // rather than run another path silently: the split-KV threshold and switch (E:1212-1214), the
   // attn_tile switch ENGINE_NO_TILED (E:1213, 1328: run_mh for blocks attn_tile takes), and the
@@ -630,14 +630,7 @@ int main(int argc, char** argv) {
     NL = 0;
     while (ck.find("layers." + std::to_string(NL) + ".input_layernorm.weight")) ++NL;
   }
-  if (g_i8 && dec_i8) {
-    if (!gemma) {
-      fprintf(stderr, "g4v_engine: ENGINE_PREFILL_INT8=1 decodes with W4A8 verify passes unless ENGINE_DECODE_INT8=0 "
-                      "(E:1600); the library runs them for the Gemma layout only: set ENGINE_DECODE_INT8=0\n");
-      return 2;
-    }
-    check(g4v_set_decode_int8(G, 1), "set_decode_int8");
-  }
+  if (g_i8 && dec_i8) check(g4v_set_decode_int8(G, 1), "set_decode_int8");
   const char* dseed = getenv("ENGINE_DRAFTER_SEED");
   Checkpoint dk;
   if (gemma && e.k_draft > 0) {  // E:1519-1528: the drafter checkpoint main() loads when ENGINE_K > 0

@@ -200,10 +200,10 @@ int g4v_set_graphs(g4v_ctx* c, int on);
 int g4v_set_prefill_int8(g4v_ctx* c, int on);
 /* E:1600 DEC_I8 (ENGINE_DECODE_INT8, on by default in the reference when ENGINE_PREFILL_INT8=1):
  * on = 1 with prefill int8 on keeps G_I8_ACTIVE in the decode, so verify passes of two rows or
- * more (g4v_verify_step / g4v_verify_sibling) multiply W4A8 as lin_multi does (E:311) and take
- * the engine's unfused structure of that mode (E:1268-1289, 1363-1388).  Off by default here
- * (exact float decode).  Gemma layout only: the synthetic stack's verify_step refuses M >= 2
- * rows while it is on. */
+ * more (g4v_verify_step / g4v_verify_sibling) multiply W4A8 as lin_multi does (E:311), on both the
+ * Gemma layout and the synthetic stack (the same passes with W4A8 products; the values equal the
+ * engine's unfused structure of that mode, E:1268-1289, 1363-1388).  Off by default here (exact
+ * float decode). */
 int g4v_set_decode_int8(g4v_ctx* c, int on);
 /* E:1516 SAMEPOS (ENGINE_DRAFT_SAMEPOS=1): g4v_draft_mtp runs every step of a chain at query
  * position P + 1 (its RoPE angle and sliding window), as draft_step(..., SAMEPOS ? P + 1 :

@@ -194,6 +194,9 @@ void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
                 g4o_verify_out* out, float* hidden_out);
 void g4o_verify_ex(g4o_model* m, const int* toks, int na, int nb, int pos0, int T, int allow_b,
                    g4o_verify_out* out, float* hidden_out);
+/* the same with i8 = G_I8_ACTIVE in the decode: W4A8 linear layers for passes of M >= 2 rows */
+void g4o_verify_i8(g4o_model* m, const int* toks, int na, int nb, int pos0, int T, int allow_b, int i8,
+                   g4o_verify_out* out, float* hidden_out);
 
 /* prefill (E:1594-1599, ENGINE_PREFILL_INT8=1): toks[0..n) at pos0.. in blocks of pfb rows;
  * fills the KV cache; hlast (optional) receives the final-normed hidden row of the last token */

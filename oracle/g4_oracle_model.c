@@ -379,8 +379,8 @@ static int pass_amode(int M, int pos0, int nb) {
   return (nb == 0 && M >= 4 && pos0 + M > 64) ? ATT_TILE : ATT_MH;
 }
 
-static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf, int nb) {
-  forward_ex(m, toks, r, T, hbuf, 0, pass_amode(r->M, r->pos0, nb));
+static void forward(g4o_model* m, const int* toks, const rows_t* r, int T, float* hbuf, int nb, int i8) {
+  forward_ex(m, toks, r, T, hbuf, i8, pass_amode(r->M, r->pos0, nb));
 }
 
 /* E:1594-1599 prefill of toks[0..n) at positions pos0.. in blocks of pfb (<= 32) rows, with
@@ -417,7 +417,7 @@ void g4o_forward_fill(g4o_model* m, const int* toks, int M, int pos0, int T) {
   for (int b = 0; b < M; b += 8) {
     rows_t r;
     rows_chain(&r, pos0 + b, (M - b) < 8 ? (M - b) : 8);
-    forward(m, toks + b, &r, T, NULL, 0);
+    forward(m, toks + b, &r, T, NULL, 0, 0);
   }
 }
 
@@ -464,11 +464,18 @@ void g4o_verify(g4o_model* m, const int* toks, int na, int nb, int pos0, int T,
  * follows the chain alone (E:1656) */
 void g4o_verify_ex(g4o_model* m, const int* toks, int na, int nb, int pos0, int T, int allow_b,
                    g4o_verify_out* out, float* hidden_out) {
+  g4o_verify_i8(m, toks, na, nb, pos0, T, allow_b, 0, out, hidden_out);
+}
+
+/* i8: G_I8_ACTIVE in the decode (ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8 on, E:1600): the
+ * pass's linear layers take W4A8 when it has two rows or more (lin, E:311) */
+void g4o_verify_i8(g4o_model* m, const int* toks, int na, int nb, int pos0, int T, int allow_b, int i8,
+                   g4o_verify_out* out, float* hidden_out) {
   rows_t r;
   rows_tree(&r, pos0, na, nb);
   const int M = r.M;
   float* hb = (float*)malloc(sizeof(float) * M * H);
-  forward(m, toks, &r, T, hb, nb);
+  forward(m, toks, &r, T, hb, nb, i8);
   memset(out, 0, sizeof *out);
   for (int i = 0; i < 8; ++i) out->G[i] = -1;
   eval_row(m, hb, toks, M, out, 0);

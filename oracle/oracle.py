@@ -72,6 +72,7 @@ class Oracle:
             "g4o_model_ptr": (_vp, [_vp, C.c_char_p]),
             "g4o_verify": (None, [_vp, _i32p, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_verify_ex": (None, [_vp, _i32p, _i, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
+            "g4o_verify_i8": (None, [_vp, _i32p, _i, _i, _i, _i, _i, _i, C.POINTER(VerifyOut), _vp]),
             "g4o_forward_fill": (None, [_vp, _i32p, _i, _i, _i]),
             "g4o_prefill": (None, [_vp, _i32p, _i, _i, _i, _i, _vp]),
             "g4o_prefill_ex": (None, [_vp, _i32p, _i, _i, _i, _i, _i, _vp]),
@@ -287,13 +288,14 @@ class Model:
         sd = np.asarray(list(seeds)[:8] or [0], np.int32)
         return self.o.L.g4o_model_head(self.h, _c(h, np.float32), sd, len(list(seeds)[:8]))
 
-    def verify(self, toks, na, nb, pos0, T=8, allow_b=True):
+    def verify(self, toks, na, nb, pos0, T=8, allow_b=True, i8=False):
         """one verify pass (tree of na chain rows and nb branch rows); allow_b False: branch b is
-        never committed (the engine's sibling row when the tree hit is not taken)"""
+        never committed (the engine's sibling row when the tree hit is not taken); i8: W4A8 linear
+        layers for passes of two rows or more (G_I8_ACTIVE in the decode, E:311, E:1600)"""
         out = VerifyOut()
         hid = np.empty(1536, np.float32)
-        self.o.L.g4o_verify_ex(self.h, _c(toks, np.int32), na, nb, pos0, T, 1 if allow_b else 0, C.byref(out),
-                               hid.ctypes.data)
+        self.o.L.g4o_verify_i8(self.h, _c(toks, np.int32), na, nb, pos0, T, 1 if allow_b else 0, 1 if i8 else 0,
+                               C.byref(out), hid.ctypes.data)
         return out, hid
 
 

@@ -23,10 +23,11 @@ ENV = dict(ENGINE_SERVE="1", ENGINE_STREAM="1", ENGINE_NGRAM="3", ENGINE_NGLEN="
 class SynthTarget:
     """the synthetic stack and drafter of the oracle as a run_req target (tests/protocol.py)"""
 
-    def __init__(self, orc):
+    def __init__(self, orc, dec_i8=False):
         from oracle import Drafter, Model
         self.m = Model(orc, SEED, V, NL, I, CTX)
         self.d = Drafter(orc, SEED + 1, V)
+        self.dec_i8 = dec_i8  # G_I8_ACTIVE in the decode (E:1600): W4A8 passes of two rows or more
 
     def prefill(self, toks, pos0, T, i8):
         return self.m.prefill(toks, pos0=pos0, T=T, i8=i8)
@@ -35,7 +36,7 @@ class SynthTarget:
         return self.m.head(h, seeds)
 
     def verify(self, block, nd, nb, pos0, T, allow_b):
-        o, hid = self.m.verify(block, nd, nb, pos0, T, allow_b=allow_b)
+        o, hid = self.m.verify(block, nd, nb, pos0, T, allow_b=allow_b, i8=self.dec_i8)
         return SimpleNamespace(nacc=o.nacc, branch=o.branch, commit=list(o.commit)[:o.ncommit], G0=o.G[0]), hid
 
     def draft(self, tok, h, pos, P, T):
@@ -49,8 +50,8 @@ class SynthTarget:
 class OracleEngine(RunReq):
     """run_req over the oracle's synthetic stack with prompt lookup (ENGINE_NGRAM=3)"""
 
-    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False, nglen=3):
-        self.target = SynthTarget(orc)
+    def __init__(self, orc, t0=T, adaptive=False, draft_same=True, cut=192, i8=False, nglen=3, dec_i8=False):
+        self.target = SynthTarget(orc, dec_i8)
         super().__init__(orc, self.target, t0=t0, adaptive=adaptive, draft_same=draft_same, cut=cut, i8=i8, ngram=3,
                          nglen=nglen)
 
@@ -156,12 +157,17 @@ def test_engine_long_lookup_chains(orc, nglen):
 
 def test_engine_prefill_int8(orc):
     """ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8=0: W4A8 prompt blocks, exact-float decode
-    (E:1210, 1596, 1600); with the decode's W4A8 left on (its default) the engine refuses"""
+    (E:1210, 1596, 1600); with the decode's W4A8 left on (its default, the server's mode) the
+    verify passes of two rows or more multiply W4A8 too, drafting and the tree mode included.
+    Settings the engine does not restate end it with exit status 2."""
     rng = np.random.default_rng(12)
     requests = [(rng.integers(0, V, 70).tolist(), 12, 3, False), (rng.integers(0, V, 33).tolist(), 8, 3, False)]
     run_protocol(orc, requests, len(requests), dict(ENGINE_PREFILL_INT8="1", ENGINE_DECODE_INT8="0"), i8=True)
+    requests = [(rng.integers(0, V, 70).tolist(), 16, 3, False), (rng.integers(0, V, 40).tolist(), 12, 3, False),
+                (rng.integers(0, V, 50).tolist(), 12, 2, True)]
+    run_protocol(orc, requests, 2, dict(ENGINE_PREFILL_INT8="1"), i8=True, dec_i8=True)
     exe = os.path.join(PKG, "g4v_engine")
-    for extra in (dict(ENGINE_PREFILL_INT8="1"), dict(ENGINE_ATT_PAR="128"), dict(ENGINE_SPLITKV="0")):
+    for extra in (dict(ENGINE_ATT_PAR="128"), dict(ENGINE_SPLITKV="0")):
         proc = subprocess.run([exe, f"synth:{SEED}:{V}:{NL}:{I}", "-", "-", "0"], input="4 1 2 3\n",
                               env=dict(os.environ, **dict(ENV, **extra)), capture_output=True, text=True, timeout=120)
         assert proc.returncode == 2 and "g4v_engine:" in proc.stderr, (extra, proc.returncode, proc.stderr[-500:])

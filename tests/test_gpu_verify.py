@@ -116,6 +116,44 @@ def test_verify_sequence_of_steps(pair):
         conf = r.commit[r.ncommit - 1]
 
 
+@pytest.mark.parametrize("na,nb,pos0", [(3, 3, 700), (3, 0, 740), (7, 0, 760), (1, 0, 100), (5, 0, 60), (0, 0, 720)])
+def test_w4a8_verify_passes(orc, g4v, na, nb, pos0):
+    """ENGINE_PREFILL_INT8=1 with ENGINE_DECODE_INT8 on (E:1600): passes of two rows or more take
+    W4A8 products (lin_multi, E:311) -- the tree and chains past ATT_PAR, a chain of 7 drafts and
+    the short passes through the prefill attention kernels -- and a one-row pass stays exact;
+    eager and replayed-graph passes equal the oracle's i8 verify pass, drafts the model takes
+    included (the accepted rows' heads and the branch-b KV move)"""
+    from oracle import Model
+    note(f"w4a8 verify na={na} nb={nb} pos0={pos0}")
+    dev = g4v.Device(0)
+    om = Model(orc, 31, 8192, 3, 6144, 1024)
+    try:
+        dev.model_synth(31, 8192, 3, 6144, 1024)
+        dev.set_prefill_int8(True)
+        dev.set_decode_int8(True)
+        toks = np.array([40 + 37 * k for k in range(1 + na + nb)], np.int32)
+        o0 = None
+        for rep in range(3):  # eager, capture, replay (graphs serve split-KV passes)
+            dev.fake_ctx(700, 99)
+            om.fake_ctx(700, 99)
+            if rep == 0:  # drafts the model takes: chain a from its own predictions
+                o0, _ = om.verify(toks, na, nb, pos0, 8, i8=True)
+                om.fake_ctx(700, 99)
+                if na >= 1:
+                    toks[1] = o0.G[0]
+            r, hg = dev.verify(toks, na, nb, pos0, 8, hidden=True)
+            o, ho = om.verify(toks, na, nb, pos0, 8, i8=True)
+            _compare(r, o, hg, ho)
+            assert same(dev.read("KC", np.uint16), om.get("KC", np.uint16, 3 * 1024 * 256)), rep
+            assert same(dev.read("VC", np.uint16), om.get("VC", np.uint16, 3 * 1024 * 256)), rep
+        if na >= 2 or nb >= 1:  # the W4A8 pass differs from the exact one somewhere
+            oe, hoe = om.verify(toks, na, nb, pos0, 8, i8=False)
+            assert not same(hoe, ho) or list(oe.G) != list(o.G)
+    finally:
+        om.close()
+        dev.close()
+
+
 @pytest.mark.parametrize("na,pos0", [(7, 600), (6, 100), (5, 30), (7, 20)])
 def test_long_chain_accepted(orc, g4v, na, pos0):
     """chains of 5 to 7 drafts (E:1514 ENGINE_NGLEN <= 7) built from the model's own greedy
