@@ -32,26 +32,28 @@ namespace g4v {
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-// quant of one 32-group (engine/w4a8_avx2.h:33-41) into its four operand words
+// quant of one 32-group (engine/w4a8_avx2.h:33-41) into its four operand words.  q = RNE(x * inv)
+// clamped to [-128, 127] is formed as y = med3(x * inv, -128, 127) + 1.5 * 2^23: the add rounds to
+// the nearest integer, ties to even (the ulp there is 1), as cvtps_epi32 does in the default mode,
+// and clamping before rounding gives the same integer (the bounds are integers, rounding is
+// monotonic); the low byte of y's bits is then q in two's complement.
 __device__ __forceinline__ float a8_quant_group(const float (&v)[32], uint64_t (&aq)[4]) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
   const float sx = amax / 127.0f, inv = sx > 0.f ? 1.0f / sx : 0.0f;
+  uint32_t qb[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    qb[i] = __float_as_uint(__builtin_amdgcn_fmed3f(v[i] * inv, -128.0f, 127.0f) + 12582912.0f);
+  // operand word h: low dword elements 8h + 0, 2, 4, 6, high dword 8h + 1, 3, 5, 7 (low bytes)
+  auto pack4 = [](uint32_t a, uint32_t b, uint32_t c, uint32_t d) -> uint32_t {
+    return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | (__builtin_amdgcn_perm(d, c, 0x0c0c0400u) << 16);
+  };
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int q = (int)__builtin_rintf(v[8 * h + i] * inv);  // RNE, as _mm256_cvtps_epi32 in the default mode
-      q = q > 127 ? 127 : (q < -128 ? -128 : q);
-      const uint32_t b = (uint32_t)q & 0xFFu;
-      if (i & 1)
-        hi |= b << (8 * (i >> 1));
-      else
-        lo |= b << (8 * (i >> 1));
-    }
-    aq[h] = (uint64_t)lo | ((uint64_t)hi << 32);
+    const uint32_t* q = qb + 8 * h;
+    aq[h] = (uint64_t)pack4(q[0], q[2], q[4], q[6]) | ((uint64_t)pack4(q[1], q[3], q[5], q[7]) << 32);
   }
   return sx;
 }
@@ -73,28 +75,41 @@ __device__ __forceinline__ float a8_scale(uint4 s4, int e) {  // bf16 scale e of
 }
 
 // ---- a product of quantised rows ----
-// Block: the 16 outputs of one a8 tile (tiles of up to three matrices, in order), 512 threads.
-// Phase p covers PG groups: thread (group gl = tid / 8, row m = tid % 8) quantises its group of
-// its staged row into LDS (rows m >= M as zeros; the row's floats were fetched during the
-// previous phase), then wave w multiplies chunks (4 groups) w + 8k, k < NU, of the phase with
-// the operand words from LDS, and lanes 0..127 chain.  Every block quantises every row it
-// multiplies (a few hundred instructions a thread per phase: cheaper than a launch of its own).
-// LDS: A32 [PG][8][16] float, SXL [PG][8] float, SWL [PG / 8][16] uint4 (the tile's scales),
-// AQL [PG][4][8] operand words
-constexpr int A8P_PG = 64;
+// Block: the 16 outputs of one a8 tile (tiles of up to three matrices, in order), 512 threads in
+// two roles.  K runs in phases of PG groups:
+//   - every weight word of the block is requested at the start (at most A8P_NPM phases), so
+//     the phases wait on one memory latency, not one each;
+//   - waves 2-7 quantise the phase's groups of every row into LDS (a task per (group, row), the
+//     rows padded to 2, 4 or 8; at most two tasks a thread, their floats fetched during the
+//     previous phase) and stage the tile's scales;
+//   - all eight waves multiply the phase's chunks (4 groups) w + 8k, k < NU, on the matrix cores
+//     and store each (row, output, group)'s a32 as float, chain-major (rows past M are not
+//     stored);
+//   - waves 0-1 (a lane per (row, output)) run the phase's chain, forming sw * sx from the
+//     staged scales as they go, while waves 2-7 quantise the next phase.
+// The block's LDS traffic bounds the phases (a CU's LDS moves about 128 bytes a cycle): the
+// chain reads 16-byte words of 4 groups, and only the matrix-core results go through LDS.
+// One LDS barrier after the quantisation, one after the products (the weight words stay in
+// flight across them).
+// LDS: A32 [128][PG + 4] float (the chains' a32; the row stride puts a quarter wave's 16-byte
+// reads on distinct banks), SXT [2][8][PG + 4] float (row scales) and SWL [2][PG / 8][16] uint4
+// (weight scales), both by phase parity (the chain of a phase reads them while the next phase's
+// are staged), AQL [PG][4][8] operand words
+constexpr int A8P_PG = 64, A8P_NPM = 6;  // K <= 32 * 64 * 6 = 12288
 template <int PG>
 constexpr size_t a8p_lds() {
-  return (size_t)PG * 8 * 16 * 4 + (size_t)PG * 8 * 4 + (size_t)(PG / 8) * 16 * 16 + (size_t)PG * 32 * 8;
+  return (size_t)128 * (PG + 4) * 4 + (size_t)2 * 8 * (PG + 4) * 4 + (size_t)2 * (PG / 8) * 16 * 16 +
+         (size_t)PG * 32 * 8;
 }
 template <int PG>
 __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
-  constexpr int PC = PG / 4, NU = PC / 8;
-  static_assert(PC % 8 == 0 && PG * 8 == 512, "whole chunks per wave; a thread per (group, row)");
+  constexpr int PC = PG / 4, NU = PC / 8, S = PG + 4, QT = 384, QR = (PG * 8 + QT - 1) / QT;
+  static_assert(PC % 8 == 0 && 2 * PG <= QT && QR <= 2, "whole chunks per wave; a scale word per staging thread");
   extern __shared__ float4 lds4[];
   float* A32 = reinterpret_cast<float*>(lds4);
-  float* SXL = A32 + PG * 8 * 16;
-  uint4* SWL = reinterpret_cast<uint4*>(SXL + PG * 8);
-  uint64_t* AQL = reinterpret_cast<uint64_t*>(SWL + (PG / 8) * 16);
+  float* SXT = A32 + 128 * S;
+  uint4* SWL = reinterpret_cast<uint4*>(SXT + 2 * 8 * S);
+  uint64_t* AQL = reinterpret_cast<uint64_t*>(SWL + 2 * (PG / 8) * 16);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int M = a.M, K = a.K, G = K / 32, GC4 = G / 4, G8 = G / 8, nph = (G + PG - 1) / PG;
   const int t = blockIdx.x, tl1 = a.mat[0].N / 16, tl2 = tl1 + a.mat[1].N / 16;
@@ -102,113 +117,173 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
   const uint4* wp = (j == 0 ? a.mat[0].w : (j == 1 ? a.mat[1].w : a.mat[2].w)) + (size_t)mt * GC4 * 64 + lane;
   const uint4* sp = (j == 0 ? a.mat[0].s : (j == 1 ? a.mat[1].s : a.mat[2].s)) + (size_t)mt * G8 * 16;
   const int ar = lane & 15, ah = lane >> 4;
+  const bool producer = w >= 2;  // (uniform per wave)
+  const int tq = tid - 128;
+  const int msh = M <= 2 ? 1 : (M <= 4 ? 2 : 3);
 
-  // the phase's weight words of this wave's chunks
-  uint4 wA[NU], wB[NU];
-  auto issue = [&](int p, uint4 (&wv)[NU]) {
+  // the staged floats of a producer's tasks (k = tq + QT r: group k >> msh of the phase, row
+  // k & (2^msh - 1)); float4 jj of a group holds elements 2jj, 16 + 2jj, 2jj + 1, 17 + 2jj.  A task
+  // past the rows or the groups reads zeros (offset past the resource).
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(a.xs, (uint32_t)M * K * 4);
+  float4 xr[QR][8];
+  auto issue_x = [&](int p) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int k = tq + QT * r, g = p * PG + (k >> msh), m = k & ((1 << msh) - 1);
+      const bool ok = tq >= 0 && k < (PG << msh) && m < M && g < G;
+      const uint32_t off = ok ? ((uint32_t)m * K + 32u * g) * 4u : 0x7FFFFF00u;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const uint4 u = buf_load16(xrs, off + 16 * jj);
+        xr[r][jj] = make_float4(as_f32(u.x), as_f32(u.y), as_f32(u.z), as_f32(u.w));
+      }
+    }
+  };
+  // the phase's weight scales (producer thread tq < 2 PG: a word of the tile's scales; other
+  // threads read zeros)
+  const __amdgpu_buffer_rsrc_t srs = buf_rsrc(sp, (uint32_t)G8 * 16 * 16);
+  uint4 stg;
+  auto issue_s = [&](int p) {
+    const int c8 = p * (PG / 8) + (tq >> 4);
+    const bool ok = tq >= 0 && tq < 2 * PG && c8 < G8;
+    stg = buf_load16(srs, ok ? ((uint32_t)c8 * 16 + (tq & 15)) * 16 : 0x7FFFFF00u);
+  };
+  // quant (engine/w4a8_avx2.h:33-41) of the producer's tasks into their operand words; rows
+  // past M (and groups past G) get zeros
+  auto quant = [&](int p) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int k = tq + QT * r, gl = k >> msh, m = k & ((1 << msh) - 1);
+      if (k < (PG << msh)) {
+        float v[32];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          v[2 * jj] = xr[r][jj].x;
+          v[16 + 2 * jj] = xr[r][jj].y;
+          v[2 * jj + 1] = xr[r][jj].z;
+          v[17 + 2 * jj] = xr[r][jj].w;
+        }
+        uint64_t aq[4];
+        float sx = a8_quant_group(v, aq);
+        if (m >= M || p * PG + gl >= G) {
+          sx = 0.f;
+#pragma unroll
+          for (int h = 0; h < 4; ++h) aq[h] = 0;
+        }
+        SXT[((p & 1) * 8 + m) * S + gl] = sx;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) AQL[gl * 32 + h * 8 + m] = aq[h];
+      }
+    }
+    if (tq < 2 * PG) SWL[(p & 1) * (PG / 8) * 16 + tq] = stg;
+  };
+
+  // The first phase's floats first, then every phase's weight words of this wave's chunks
+  // (chunks past the matrix read zeros): loads complete in issue order, so the first
+  // quantisation waits for its floats alone.  Every wave issues the same loads (the chain
+  // waves' row and scale loads read past their resources): the waits on the weight words then
+  // count the same younger loads in both roles.
+  issue_x(0);
+  issue_s(0);
+  const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(wp - lane, (uint32_t)GC4 * 64 * 16);
+  uint4 wq[A8P_NPM][NU];
+#pragma unroll
+  for (int p = 0; p < A8P_NPM; ++p)
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
       const int c = p * PC + w + 8 * k;
-      if (c < GC4) wv[k] = wp[(size_t)c * 64];
+      wq[p][k] = buf_load16(wrs, c < GC4 ? ((uint32_t)c * 64 + lane) * 16 : 0x7FFFFF00u);
     }
-  };
-  // the staged floats of this thread's (group, row) of a phase: float4 jj of a group holds
-  // elements 2jj, 16 + 2jj, 2jj + 1, 17 + 2jj
-  const int qg = tid >> 3, qm = tid & 7;
-  float4 xr[8];
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) xr[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto issue_x = [&](int p) {
-    const int g = p * PG + qg;
-    if (qm < M && g < G) {
-      const float4* src = reinterpret_cast<const float4*>(a.xs) + ((size_t)qm * K + 32 * g) / 4;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) xr[jj] = src[jj];
-    }
-  };
-  // the phase's weight scales (thread f < 2 PG: a word of the tile's scales), staged through
-  // one register
-  uint4 stg = make_uint4(0, 0, 0, 0);
-  auto issue_s = [&](int p) {
-    const int gb = p * PG;
-    if (tid < 2 * PG && gb / 8 + (tid >> 4) < G8) stg = sp[(size_t)(gb / 8 + (tid >> 4)) * 16 + (tid & 15)];
-  };
-  issue(0, wA);
-  issue_x(0);
-  issue_s(0);
+  if (producer) quant(0);
+  if (nph > 1) {
+    issue_x(1);
+    issue_s(1);
+  }
   const int cm = (tid >> 4) & 7, cn = tid & 15;
   const bool chain = tid < 128 && cm < M;
   float acc = 0.f;
-  for (int p = 0; p < nph; ++p) {
+#pragma unroll
+  for (int p = 0; p < A8P_NPM; ++p) {
+    if (p >= nph) break;  // (uniform)
     const int gb = p * PG, ng = min(PG, G - gb);
-    if (p + 1 < nph) issue(p + 1, wB);
-    // quant (engine/w4a8_avx2.h:33-41) of this thread's group into its operand words
+    lds_barrier();  // the phase's operand words, row scales and weight scales are staged; A32 is free
+    // the group dots of this wave's chunks: every operand read first, then the eight independent
+    // products, then one 16-byte store per row and chunk (groups past G hold zero operand words
+    // and are never chained)
     {
-      float v[32];
+      uint64_t qw[NU][4];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        v[2 * jj] = xr[jj].x;
-        v[16 + 2 * jj] = xr[jj].y;
-        v[2 * jj + 1] = xr[jj].z;
-        v[17 + 2 * jj] = xr[jj].w;
-      }
-      uint64_t aq[4];
-      float sx = a8_quant_group(v, aq);
-      if (qm >= M || gb + qg >= G) {
-        sx = 0.f;
+      for (int k = 0; k < NU; ++k)
 #pragma unroll
-        for (int h = 0; h < 4; ++h) aq[h] = 0;
-      }
-      SXL[qg * 8 + qm] = sx;
+        for (int i = 0; i < 4; ++i) qw[k][i] = AQL[(4 * (w + 8 * k) + i) * 32 + ah * 8 + (ar & 7)];  // word ah of row ar
+      i32x4_t D[NU][4];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) AQL[qg * 32 + h * 8 + qm] = aq[h];
-    }
-    if (tid < 2 * PG) SWL[tid] = stg;
-    if (p + 1 < nph) {
-      issue_x(p + 1);
-      issue_s(p + 1);
-    }
-    __syncthreads();
-    // the group dots of this wave's chunks
-#pragma unroll
-    for (int k = 0; k < NU; ++k) {
-      const int cl = w + 8 * k;
-      if (gb + 4 * cl < G) {  // (uniform per wave)
-        const uint4 wv = wA[k];
+      for (int k = 0; k < NU; ++k) {
+        const uint4 wv = wq[p][k];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t d = i == 0 ? wv.x : (i == 1 ? wv.y : (i == 2 ? wv.z : wv.w));
-          const uint64_t qw = ar < 8 ? AQL[(4 * cl + i) * 32 + ah * 8 + ar] : 0;  // rows >= 8 zero
-          const i32x4_t D = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)qw, a8_wbytes(d), i32x4_t{0, 0, 0, 0}, 0, 0, 0);
-          if (ah < 2) {
-            float* o = A32 + ((size_t)(4 * cl + i) * 8 + 4 * ah) * 16 + ar;
-            o[0] = (float)D[0];
-            o[16] = (float)D[1];
-            o[32] = (float)D[2];
-            o[48] = (float)D[3];
-          }
+          D[k][i] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(ar < 8 ? qw[k][i] : 0), a8_wbytes(d),
+                                                         i32x4_t{0, 0, 0, 0}, 0, 0, 0);  // rows >= 8 zero
         }
       }
-    }
-    __syncthreads();
-    // the chains over the phase's groups, in order (A8:59)
-    if (chain) {
-      const float* ap = A32 + cm * 16 + cn;
+      if (ah < 2 && 4 * ah < M) {  // rows 4 ah .. 4 ah + 3 of output ar
 #pragma unroll
-      for (int k8 = 0; k8 < PG / 8; ++k8) {
-        if (8 * k8 < ng) {  // (ng is a multiple of 8)
-          const uint4 s4 = SWL[k8 * 16 + cn];
+        for (int k = 0; k < NU; ++k)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<float4*>(A32 + ((4 * ah + r) * 16 + ar) * S + 4 * (w + 8 * k)) =
+                make_float4((float)D[k][0][r], (float)D[k][1][r], (float)D[k][2][r], (float)D[k][3][r]);
+      }
+    }
+    lds_barrier();
+    if (!producer) {
+      // the chain over the phase's groups, in order (A8:59): row = fma(a32, sw * sx, row)
+      if (chain) {
+        const float4* a4 = reinterpret_cast<const float4*>(A32 + (cm * 16 + cn) * S);
+        const float4* x4 = reinterpret_cast<const float4*>(SXT + ((p & 1) * 8 + cm) * S);
+        const uint4* sw4 = SWL + (p & 1) * (PG / 8) * 16;
+        // groups in blocks of 8: the next block's words are read while this one is chained
+        float4 av[2][2], xv[2][2];
+        uint4 sv[2];
+        auto rd = [&](int g8, int b) {
+          sv[b] = sw4[g8 * 16 + cn];
+          av[b][0] = a4[2 * g8];
+          av[b][1] = a4[2 * g8 + 1];
+          xv[b][0] = x4[2 * g8];
+          xv[b][1] = x4[2 * g8 + 1];
+        };
+        auto steps8 = [&](int b) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const int gl = 8 * k8 + e;
-            acc = fmaf(ap[(size_t)gl * 128], a8_scale(s4, e) * SXL[gl * 8 + cm], acc);
+            const float4 a = av[b][e >> 2], x = xv[b][e >> 2];
+            const int c = e & 3;
+            const float ae = c == 0 ? a.x : (c == 1 ? a.y : (c == 2 ? a.z : a.w));
+            const float xe = c == 0 ? x.x : (c == 1 ? x.y : (c == 2 ? x.z : x.w));
+            acc = fmaf(ae, a8_scale(sv[b], e) * xe, acc);
+          }
+        };
+        if (ng == PG) {
+          rd(0, 0);
+#pragma unroll
+          for (int g8 = 0; g8 < PG / 8; ++g8) {
+            if (g8 + 1 < PG / 8) rd(g8 + 1, (g8 + 1) & 1);
+            steps8(g8 & 1);
+          }
+        } else {
+          for (int g8 = 0; g8 < ng / 8; ++g8) {  // (ng is a multiple of 8)
+            rd(g8, 0);
+            steps8(0);
           }
         }
       }
+    } else if (p + 1 < nph) {
+      quant(p + 1);  // the products of phase p are done with AQL; its scales stay in the other half
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < NU; ++k) wA[k] = wB[k];
+    if (p + 2 < nph) {
+      issue_x(p + 2);
+      issue_s(p + 2);
+    }
   }
   if (chain) {
     float* y = j == 0 ? a.y[0] : (j == 1 ? a.y[1] : a.y[2]);
@@ -477,7 +552,13 @@ int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
   }
   const dim3 b(512);
   if (!a.nrm_mode) {
-    if (!a.xs || a.gateup || a.epi_pli) return 0;
+    if (!a.xs || a.gateup || a.epi_pli || a.K > 32 * A8P_PG * A8P_NPM) return 0;
+    static bool raised_p = false;  // more than 64 KB of LDS (gfx950: up to 160 KB on request)
+    if (!raised_p) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_a8p<A8P_PG>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)a8p_lds<A8P_PG>());
+      raised_p = true;
+    }
     hipLaunchKernelGGL(k_gemv_a8p<A8P_PG>, dim3(tiles), b, a8p_lds<A8P_PG>(), st, a);
     return tiles;
   }

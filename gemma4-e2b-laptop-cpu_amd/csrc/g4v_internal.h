@@ -78,6 +78,15 @@ __host__ __device__ __forceinline__ int staged_index(int n) {
 // without clamped duplicate fetches).  The base must be uniform over the wave.  Being intrinsic
 // calls rather than plain loads, a ring of them carried across a loop's back edge stays a ring
 // (plain loads there get folded into loads at the top of the next iteration).
+// A block barrier that orders LDS only: each wave's LDS operations complete before it, while
+// its global loads stay in flight across it (__syncthreads' workgroup fence also waits for every
+// outstanding global load, so register prefetches issued before it would all land there).  For
+// blocks whose waves exchange data through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
