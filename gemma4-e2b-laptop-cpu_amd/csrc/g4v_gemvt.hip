@@ -561,7 +561,8 @@ __global__ __launch_bounds__(TR * 8) void k_gemv_t(const float* __restrict__ pa,
 constexpr int GS_PG = 64;  // groups per phase (8 chunks)
 static size_t gemvs_lds(int K) {
   const int G = K / 32;
-  return (size_t)G * 9 * 16 + (size_t)G * 4 + (size_t)2 * GS_PG * 64 * 4 + (size_t)2 * GS_PG * 8 * 4 + 64 * 4 + 8 * 4;
+  return (size_t)G * 9 * 16 + (size_t)G * 4 + (size_t)2 * GS_PG * 64 * 4 + (size_t)2 * GS_PG * 8 * 4 + 64 * 4 + 8 * 4 +
+         64 * 16 + 576 * 4;
 }
 // NX = K / 2048: float4 of the row each of the first 512 threads stages, and phases
 template <int NX>
@@ -575,33 +576,53 @@ __global__ __launch_bounds__(576) void k_gemv_s(const float4* __restrict__ xs, c
   float* SCL = AL + 2 * GS_PG * 64;                     // [2][GS_PG][8 rows]
   float* RL = SCL + 2 * GS_PG * 8;                      // [8 j][8 rows]
   float* OFL = RL + 64;                                 // [8 rows]
+  float4* PADX = reinterpret_cast<float4*>(OFL + 8);    // [64]: the staging stores of wave 8
+  float* PADG = reinterpret_cast<float*>(PADX + 64);    // [576]: the group-sum stores past G
   const int tid = threadIdx.x, s = tid >> 6, j = (tid >> 3) & 7, r = tid & 7;
   const int n0 = blockIdx.x * 8, t64 = n0 >> 6, r64 = (n0 & 63) + r;
-  // this wave's chunk of every phase (8p + s), all in flight from the start
-  uint4 wv[NX], sv[NX];
-  if (s < 8) {
-    const uint4* wp = mat.w + ((size_t)t64 * GC * 8 + j) * 64 + r64;  // chunk c at + 512 c
-    const uint4* sp = mat.s + (size_t)t64 * GC * 64 + r64;             // chunk c at + 64 c
-#pragma unroll
-    for (int p = 0; p < NX; ++p) {
-      wv[p] = wp[(size_t)(8 * p + s) * 512];
-      sv[p] = sp[(size_t)(8 * p + s) * 64];
-    }
-  }
-  if (tid < 512) {  // the row: every load issued before the first store
-    float4 xr[NX];
-    float gr = 0.f;
-#pragma unroll
-    for (int k = 0; k < NX; ++k) xr[k] = xs[tid + 512 * k];
-    if (gs && tid < G) gr = gs[tid];
+  // The row's loads first, then this wave's chunk of every phase (8p + s), all in flight from the
+  // start: loads retire in issue order, so the staging waits for the row alone, and the LDS-only
+  // barriers below leave the weights in flight (phase p waits for its own words only).
+  // Every wave issues the same loads (buffer loads; a thread with nothing to fetch reads past the
+  // resource and gets zeros), so the waits count the same younger loads in every wave.
+  constexpr uint32_t OOB = 0x7FFFFF00u;
+  float4 xr[NX];
+  float gr;
+  {
+    const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(xs, (uint32_t)K * 4);
 #pragma unroll
     for (int k = 0; k < NX; ++k) {
-      const int u = tid + 512 * k;
-      XL[u + (u >> 3)] = xr[k];
+      const uint4 u = buf_load16(xrs, tid < 512 ? (uint32_t)(tid + 512 * k) * 16 : OOB);
+      xr[k] = make_float4(as_f32(u.x), as_f32(u.y), as_f32(u.z), as_f32(u.w));
     }
-    if (gs && tid < G) GSL[tid] = gr;
+    const __amdgpu_buffer_rsrc_t grs = buf_rsrc(gs, gs ? (uint32_t)G * 4 : 0u);
+    gr = as_f32((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(grs, tid < G ? tid * 4 : (int)OOB, 0, 0));
   }
-  __syncthreads();
+  // (issue order: the row's loads before the weights, also through the IR passes)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 wv[NX], sv[NX];
+  {
+    // the tile's words: chunk c of row slot (j, r64) at 512 c + 64 j + r64, its scales at 64 c + r64
+    const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(mat.w + (size_t)t64 * GC * 512, (uint32_t)GC * 512 * 16);
+    const __amdgpu_buffer_rsrc_t srs = buf_rsrc(mat.s + (size_t)t64 * GC * 64, (uint32_t)GC * 64 * 16);
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+      const int c = 8 * p + s;
+      wv[p] = buf_load16(wrs, s < 8 ? (uint32_t)(512 * c + 64 * j + r64) * 16 : OOB);
+      sv[p] = buf_load16(srs, s < 8 ? (uint32_t)(64 * c + r64) * 16 : OOB);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // the row into LDS: every thread stores (the threads past the row into the pads), so the row's
+  // loads are used where they are issued and stay ahead of the weights
+#pragma unroll
+  for (int k = 0; k < NX; ++k) {
+    const int u = tid + 512 * k;
+    *(tid < 512 ? XL + u + (u >> 3) : PADX + (tid - 512)) = xr[k];
+  }
+  *(tid < G ? GSL + tid : PADG + tid) = gr;  // (without gs, the sums are formed below)
+  lds_barrier();
   if (!gs) {  // W:22 each group's sequential sum, from the staged copy (G <= 384)
     if (const int g = tid; g < G) {
       const float4* q4 = XL + (size_t)g * 9;
@@ -615,7 +636,7 @@ __global__ __launch_bounds__(576) void k_gemv_s(const float4* __restrict__ xs, c
       for (int i = 0; i < 16; ++i) sm += (i & 1) ? v[i >> 1].w : v[i >> 1].y;
       GSL[g] = sm;
     }
-    __syncthreads();
+    lds_barrier();
   }
   const float4* xw = XL + j;  // group g: xw[9 g]
   float row = 0.f, off = 0.f;
@@ -659,14 +680,14 @@ __global__ __launch_bounds__(576) void k_gemv_s(const float4* __restrict__ xs, c
         off = fmaf(sc, gsp[gl], off);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   // the 8 chain lanes of each row meet: ((r0+r4)+(r1+r5))+((r2+r6)+(r3+r7)) - 8 off
   if (s == 8) {
     RL[j * 8 + r] = row;
     if (j == 0) OFL[r] = off;
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < 8) {
     const float* q = RL + tid;
     y[n0 + tid] = (((q[0] + q[32]) + (q[8] + q[40])) + ((q[16] + q[48]) + (q[24] + q[56]))) - 8.f * OFL[tid];
@@ -757,10 +778,11 @@ int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr) {
   if (a.M == 1 && !a.mrg_po && !a.nrm_mode && !a.gateup && !a.epi_pli && !a.yperm && a.xs && a.mat[0].N % 64 == 0 &&
       a.mat[1].N == 0 && a.mat[2].N == 0 && a.K % 2048 == 0 && (nx == 1 || nx == 2 || nx == 3 || nx == 6)) {
     const size_t lds = gemvs_lds(a.K);
-    static bool raised = false;  // more than 64 KB for K > 6144 (gfx950: up to 160 KB on request)
+    static bool raised = false;  // more than 64 KB for K >= 6144 (gfx950: up to 160 KB on request)
     if (!raised) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_s<6>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                163840);
+      const void* fns[] = {reinterpret_cast<const void*>(&k_gemv_s<1>), reinterpret_cast<const void*>(&k_gemv_s<2>),
+                           reinterpret_cast<const void*>(&k_gemv_s<3>), reinterpret_cast<const void*>(&k_gemv_s<6>)};
+      for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
       raised = true;
     }
     const int grid = a.mat[0].N / 8;
