@@ -94,12 +94,14 @@ __device__ __forceinline__ float a8_scale(uint4 s4, int e) {  // bf16 scale e of
 // LDS: A32 [128][PG + 4] float (the chains' a32; the row stride puts a quarter wave's 16-byte
 // reads on distinct banks), SXT [2][8][PG + 4] float (row scales) and SWL [2][PG / 8][16] uint4
 // (weight scales), both by phase parity (the chain of a phase reads them while the next phase's
-// are staged), AQL [PG][4][8] operand words
+// are staged), AQL [PG][A8P_QS] operand words (word h of row m at 8 h + m; the group stride of 36
+// spreads a wave's quantisation stores of 16 groups over the banks)
 constexpr int A8P_PG = 64, A8P_NPM = 6;  // K <= 32 * 64 * 6 = 12288
+constexpr int A8P_QS = 36;                // operand words per group in LDS (32 + padding)
 template <int PG>
 constexpr size_t a8p_lds() {
   return (size_t)128 * (PG + 4) * 4 + (size_t)2 * 8 * (PG + 4) * 4 + (size_t)2 * (PG / 8) * 16 * 16 +
-         (size_t)PG * 32 * 8;
+         (size_t)PG * A8P_QS * 8;
 }
 template <int PG>
 __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
         }
         SXT[((p & 1) * 8 + m) * S + gl] = sx;
 #pragma unroll
-        for (int h = 0; h < 4; ++h) AQL[gl * 32 + h * 8 + m] = aq[h];
+        for (int h = 0; h < 4; ++h) AQL[gl * A8P_QS + h * 8 + m] = aq[h];
       }
     }
     if (tq < 2 * PG) SWL[(p & 1) * (PG / 8) * 16 + tq] = stg;
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
 #pragma unroll
       for (int k = 0; k < NU; ++k)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qw[k][i] = AQL[(4 * (w + 8 * k) + i) * 32 + ah * 8 + (ar & 7)];  // word ah of row ar
+        for (int i = 0; i < 4; ++i) qw[k][i] = AQL[(4 * (w + 8 * k) + i) * A8P_QS + ah * 8 + (ar & 7)];  // word ah of row ar
       i32x4_t D[NU][4];
 #pragma unroll
       for (int k = 0; k < NU; ++k) {
@@ -296,16 +298,19 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
 // ---- a product with the norm prologue (K = H: one phase of G = 48 groups) ----
 // Block: CG a8 tiles of 16 outputs (CG = 2: the gate tile and the up tile of the same 16 pairs),
 // all M rows, 512 threads.  Wave w multiplies the (column group, chunk) units w + 8k.
-// LDS: U (the prologue's rows [8][A8_XPS], then A32 [48][CG][8][16]), AQ [8][48][4] uint64,
+// LDS: U (the prologue's rows [8][A8_XPS], then A32 [48][CG][8][16]), AQ [48][A8N_QS] uint64 (word h
+// of row m at 8 h + m: a wave's operand reads of one group are 32 consecutive words),
 // SXL [48][8], SWL [CG][6][16] uint4, YL [CG][8][16]
 constexpr int A8_XPS = 1600;  // row stride of the prologue's rows in LDS (16 RMS chains of 100)
+constexpr int A8N_QS = 33;    // operand words per group in LDS (32 + 1: the quantisation stores of
+                              // consecutive groups on distinct banks)
 template <int CG>
 constexpr int a8n_ufloats() {
   return (48 * CG * 8 * 16 > 8 * A8_XPS) ? 48 * CG * 8 * 16 : 8 * A8_XPS;
 }
 template <int CG>
 constexpr size_t a8n_lds() {
-  return (size_t)a8n_ufloats<CG>() * 4 + (size_t)8 * 48 * 4 * 8 + (size_t)48 * 8 * 4 + (size_t)CG * 6 * 16 * 16 +
+  return (size_t)a8n_ufloats<CG>() * 4 + (size_t)48 * A8N_QS * 8 + (size_t)48 * 8 * 4 + (size_t)CG * 6 * 16 * 16 +
          (size_t)CG * 8 * 16 * 4;
 }
 template <int XM, int CG>
@@ -314,7 +319,7 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
   extern __shared__ float4 lds4[];
   float* U = reinterpret_cast<float*>(lds4);
   uint64_t* AQ = reinterpret_cast<uint64_t*>(U + a8n_ufloats<CG>());
-  float* SXL = reinterpret_cast<float*>(AQ + 8 * G * 4);
+  float* SXL = reinterpret_cast<float*>(AQ + G * A8N_QS);
   uint4* SWL = reinterpret_cast<uint4*>(SXL + G * 8);
   float* YL = reinterpret_cast<float*>(SWL + CG * G8 * 16);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -453,7 +458,7 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
   // quantise the rows: thread (m, g), rows >= M zero
   if (tid < 8 * G) {
     const int m = tid / G, g = tid - m * G;
-    uint64_t* aq = AQ + (size_t)(m * G + g) * 4;
+    uint64_t* aq = AQ + (size_t)g * A8N_QS + m;  // word h at aq[8 h]
     if (m < M) {
       const float4* src = reinterpret_cast<const float4*>(U + (size_t)m * A8_XPS + 32 * g);
       float v[32];
@@ -468,10 +473,10 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
       uint64_t q[4];
       SXL[g * 8 + m] = a8_quant_group(v, q);
 #pragma unroll
-      for (int h = 0; h < 4; ++h) aq[h] = q[h];
+      for (int h = 0; h < 4; ++h) aq[8 * h] = q[h];
     } else {
 #pragma unroll
-      for (int h = 0; h < 4; ++h) aq[h] = 0;
+      for (int h = 0; h < 4; ++h) aq[8 * h] = 0;
       SXL[g * 8 + m] = 0.f;
     }
   }
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int g = 4 * cl + i;
           const uint32_t d = i == 0 ? wv.x : (i == 1 ? wv.y : (i == 2 ? wv.z : wv.w));
-          const uint64_t A = ar < 8 ? AQ[(size_t)(ar * G + g) * 4 + ah] : 0;
+          const uint64_t A = ar < 8 ? AQ[(size_t)g * A8N_QS + ah * 8 + ar] : 0;
           const i32x4_t D = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)A, a8_wbytes(d), i32x4_t{0, 0, 0, 0}, 0, 0, 0);
           if (ah < 2) {
             float* o = U + ((size_t)(g * CG + cg) * 8 + 4 * ah) * 16 + ar;
