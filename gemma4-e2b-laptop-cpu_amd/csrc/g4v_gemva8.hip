@@ -296,7 +296,9 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
 }
 
 // ---- a product with the norm prologue (K = H: one phase of G = 48 groups) ----
-// Block: CG a8 tiles of 16 outputs (CG = 2: the gate tile and the up tile of the same 16 pairs),
+// Block: CG a8 tiles of 16 outputs (CG = 4: the gate and up tiles of 32 pairs, column group cg the
+// tile cg / 2 of the block's pairs in the gate (cg even) or up (cg odd) matrix: one 512-thread block
+// per CU for the 192 blocks of a 6144-wide MLP; CG = 2 for wider ones),
 // all M rows, 512 threads.  Wave w multiplies the (column group, chunk) units w + 8k.
 // LDS: U (the prologue's rows [8][A8_XPS], then A32 [48][CG][8][16]), AQ [48][A8N_QS] uint64 (word h
 // of row m at 8 h + m: a wave's operand reads of one group are 32 consecutive words),
@@ -325,20 +327,22 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int M = a.M;
 
-  // column group cg: matrix mj (CG = 2: cg itself) and 16-row tile mt (CG = 2: the block)
+  // column group cg: matrix mj (pairs: cg % 2) and 16-row tile mt (pairs: the block's first tile
+  // plus cg / 2)
+  constexpr bool PAIRS = CG >= 2;
   int mj0, mt0;
   {
     const int t = blockIdx.x, tl1 = a.mat[0].N / 16, tl2 = tl1 + a.mat[1].N / 16;
-    mj0 = CG == 2 ? 0 : (t >= tl1) + (t >= tl2);
-    mt0 = CG == 2 ? t : t - (mj0 == 0 ? 0 : (mj0 == 1 ? tl1 : tl2));
+    mj0 = PAIRS ? 0 : (t >= tl1) + (t >= tl2);
+    mt0 = PAIRS ? (CG / 2) * t : t - (mj0 == 0 ? 0 : (mj0 == 1 ? tl1 : tl2));
   }
   auto matw = [&](int cg) -> const uint4* {
-    const int j = CG == 2 ? cg : mj0;
-    return (j == 0 ? a.mat[0].w : (j == 1 ? a.mat[1].w : a.mat[2].w)) + (size_t)mt0 * GC4 * 64 + lane;
+    const int j = PAIRS ? (cg & 1) : mj0, mt = PAIRS ? mt0 + (cg >> 1) : mt0;
+    return (j == 0 ? a.mat[0].w : (j == 1 ? a.mat[1].w : a.mat[2].w)) + (size_t)mt * GC4 * 64 + lane;
   };
   auto mats = [&](int cg) -> const uint4* {
-    const int j = CG == 2 ? cg : mj0;
-    return (j == 0 ? a.mat[0].s : (j == 1 ? a.mat[1].s : a.mat[2].s)) + (size_t)mt0 * G8 * 16;
+    const int j = PAIRS ? (cg & 1) : mj0, mt = PAIRS ? mt0 + (cg >> 1) : mt0;
+    return (j == 0 ? a.mat[0].s : (j == 1 ? a.mat[1].s : a.mat[2].s)) + (size_t)mt * G8 * 16;
   };
   // this wave's units u = w + 8k: column group u % CG, chunk u / CG
   uint4 wA[NU];
@@ -523,12 +527,13 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
       }
     }
   }
-  if constexpr (CG == 2) {  // E:292-299 act = rbf8(rbf8(gelu8(rbf8 g)) * rbf8 u), written staged
-    if (tid < 256) YL[(ccg * 8 + cm) * 16 + cn] = acc;
+  if constexpr (PAIRS) {  // E:292-299 act = rbf8(rbf8(gelu8(rbf8 g)) * rbf8 u), written staged
+    if (tid < CG * 128) YL[(ccg * 8 + cm) * 16 + cn] = acc;
     __syncthreads();
-    if (tid < 128 && cm < M) {
-      const float g = YL[cm * 16 + cn], u = YL[(8 + cm) * 16 + cn];
-      a.y[0][(size_t)cm * a.ldy[0] + staged_index(16 * mt0 + cn)] = r16(r16(gelu8(r16(g))) * r16(u));
+    if (tid < CG * 64 && cm < M) {  // pair tile pt = tid / 128: gate group 2 pt, up group 2 pt + 1
+      const int pt = tid >> 7;
+      const float g = YL[((2 * pt) * 8 + cm) * 16 + cn], u = YL[((2 * pt + 1) * 8 + cm) * 16 + cn];
+      a.y[0][(size_t)cm * a.ldy[0] + staged_index(16 * (mt0 + pt) + cn)] = r16(r16(gelu8(r16(g))) * r16(u));
     }
   } else if (chain) {
     const int n = 16 * mt0 + cn;
@@ -570,14 +575,21 @@ int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
   if (a.K != H) return 0;
   static bool raised = false;  // the norm variants stage more than 64 KB (gfx950: up to 160 KB on request)
   if (!raised) {
-    const void* fns[] = {reinterpret_cast<const void*>(&k_gemv_a8n<0, 2>),
+    const void* fns[] = {reinterpret_cast<const void*>(&k_gemv_a8n<0, 4>), reinterpret_cast<const void*>(&k_gemv_a8n<0, 2>),
                          reinterpret_cast<const void*>(&k_gemv_a8n<1, 1>),
                          reinterpret_cast<const void*>(&k_gemv_a8n<0, 1>)};
-    for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 81920);
+    for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
     raised = true;
   }
   if (a.gateup) {
     if (a.epi_pli || a.mat[0].N != a.mat[1].N || a.mat[2].N) return 0;
+    // 4 tiles a block while that leaves one block per CU (a 6144-wide MLP: 192 blocks), else 2
+    // (two blocks a CU: the 12288-wide MLP's 768 blocks)
+    if (a.mat[0].N % 32 == 0 && a.mat[0].N / 32 <= 256) {
+      const int grid = a.mat[0].N / 32;
+      hipLaunchKernelGGL((k_gemv_a8n<0, 4>), dim3(grid), b, (a8n_lds<4>()), st, a);
+      return grid;
+    }
     const int grid = a.mat[0].N / 16;
     hipLaunchKernelGGL((k_gemv_a8n<0, 2>), dim3(grid), b, (a8n_lds<2>()), st, a);
     return grid;
