@@ -45,6 +45,10 @@ struct AttnPtrs {
   uint16_t* KCw;      // the layer's cache (same as KC / VC), written for the pass's rows
   uint16_t* VCw;
   const AttnGeom* gdev;  // raw attention: the geometry in device memory (replaces the argument)
+  // with gs: the merged rows also quantised for a W4A8 product (engine/w4a8_avx2.h:33-41), the
+  // four operand words of group g of row m at xq[(m * ldo / 32 + g) * 4], its scale at xqs
+  uint64_t* xq;
+  float* xqs;
 };
 
 // grid (T, M, NQ / ATT_HB); the geometry as the argument gin or in device memory (P.gdev)
@@ -695,6 +699,16 @@ __device__ __forceinline__ void merge_body(const AttnPtrs& P, int M, int T) {
     }
     P.gs[(size_t)m * (P.ldo / 32) + h * (HD / 32) + i] = s;
   }
+  if (P.xq && i < HD / 32) {  // the head's 8 groups of the row, one a thread (ys in plain order)
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = ys[i * 32 + k];
+    uint64_t q[4];
+    const size_t gq = (size_t)m * (P.ldo / 32) + h * (HD / 32) + i;
+    P.xqs[gq] = a8_quant_group(v, q);
+#pragma unroll
+    for (int hw = 0; hw < 4; ++hw) P.xq[gq * 4 + hw] = q[hw];
+  }
 }
 
 __global__ __launch_bounds__(HD) void k_attn_merge(AttnPtrs P, int M, int T) { merge_body(P, M, T); }
@@ -708,9 +722,9 @@ void launch_attn(uint16_t* KC, uint16_t* VC, const float* q, const float* k, con
 }
 
 void launch_attn_merge(const float* po, const float* pm, const float* pl, int M, int T, float* out, int ldo,
-                       float* gs, hipStream_t st) {
+                       float* gs, hipStream_t st, uint64_t* xq, float* xqs) {
   AttnPtrs P{nullptr, nullptr, nullptr, 0, const_cast<float*>(po), const_cast<float*>(pm), const_cast<float*>(pl),
-             out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+             out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, xq, xqs};
   hipLaunchKernelGGL(k_attn_merge, dim3(M, NQ), dim3(HD), 0, st, P, M, T);
 }
 
@@ -724,9 +738,9 @@ void launch_attn_geom(const uint16_t* KC, const uint16_t* VC, const float* q, in
 
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
                           int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh,
-                          float* gs) {
+                          float* gs, uint64_t* xq, float* xqs) {
   AttnPtrs P{KC, VC, q, ldq, po, pm, pl, out, ldo, gs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-             nullptr, gdev};
+             nullptr, gdev, xq, xqs};
   AttnGeom g{};
   g.M = M;
   g.T = T;

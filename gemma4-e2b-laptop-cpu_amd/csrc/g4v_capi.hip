@@ -114,6 +114,9 @@ struct g4v_ctx {
   // attention standalone
   DBuf ak, av, aq, ao;
   DBuf vags;  // group sums of the merged attention rows of a W4A8 verify pass [MAXM][NQ * HD / 32]
+  // W4A8 verify passes: the rows of the next product quantised by their producer (the split-KV
+  // merge for o, the 6144-wide gate / up for down): operand words [MAXM][384][4], scales [MAXM][384]
+  DBuf q8w, q8s;
   DBuf po5, pm5, pl5;  // split partials at head dim 512
   // the Gemma-4-E2B layout (g4v_model_create_gemma): per-layer geometry, the per-layer-input
   // branch, the owners' caches and the row buffers of its passes
@@ -1087,6 +1090,8 @@ static int model_alloc(g4v_ctx* c, int V, int NL, int I, int ctxcap) {
   ALLOC(c->stepd, sizeof(StepDev));
   ALLOC(c->vatt, (size_t)MAXM * NQ * HD * 4);
   ALLOC(c->vags, (size_t)MAXM * NQ * HD / 32 * 4);
+  ALLOC(c->q8w, (size_t)MAXM * 384 * 32);
+  ALLOC(c->q8s, (size_t)MAXM * 384 * 4);
   ALLOC(c->vsc, (size_t)8 * MAXM * ctxcap * 4);
   ALLOC(c->resd, sizeof(VerifyResultDev));
   HIPCHK(hipStreamSynchronize(st));  // rt goes out of scope
@@ -1536,13 +1541,17 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     } else {
       if (path == 0)  // W4A8: the merge on its own (E:1019-1059), staged, then the product
         launch_attn_merge(c->po.as<float>(), c->pm.as<float>(), c->pl.as<float>(), M, T, c->vatt.as<float>(), NQ * HD,
-                          c->vags.as<float>(), st);
+                          c->vags.as<float>(), st, c->q8w.as<uint64_t>(), c->q8s.as<float>());
       ao.xs = c->vatt.as<float4>();  // group sums formed in LDS from the staged copy
     }
     ao.K = NQ * HD;
     ao.M = M;
     if (a8) {
       ao.mat[0] = a8t(A.m[3]);
+      if (path == 0) {  // the merge quantised the rows
+        ao.xq = c->q8w.as<uint64_t>();
+        ao.xqs = c->q8s.as<float>();
+      }
       (void)launch_gemv_a8(ao, st);
     } else {
       launch_gemv_t(ao, st, c->gcfg[1][0], c->gcfg[1][1]);
@@ -1565,6 +1574,10 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     if (a8) {  // the gate and up matrices' own tiles (the pair-tiled copy is the exact GEMV's)
       gu.mat[0] = a8t(A.m[4]);
       gu.mat[1] = a8t(A.m[5]);
+      if (a8_gateup_quantises(I)) {  // the activation quantised for down by the same blocks
+        gu.yq = c->q8w.as<uint64_t>();
+        gu.yqs = c->q8s.as<float>();
+      }
       (void)launch_gemv_a8(gu, st);
     } else {
       launch_gemv_t(gu, st, c->gcfg[2][0], c->gcfg[2][1]);
@@ -1580,6 +1593,10 @@ static void enqueue_verify(g4v_ctx* c, int M, int na, int nb, int T, int path) {
     ad.M = M;
     if (a8) {
       ad.mat[0] = a8t(A.m[6]);
+      if (a8_gateup_quantises(I)) {
+        ad.xq = c->q8w.as<uint64_t>();
+        ad.xqs = c->q8s.as<float>();
+      }
       (void)launch_gemv_a8(ad, st);
     } else {
       launch_gemv_t(ad, st, I > 6144 ? 1 : c->gcfg[3][0], c->gcfg[3][1]);  // (K 12288: one row per block)
@@ -2159,15 +2176,18 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
     const float* sn = cs + (size_t)c->ctxcap * (hd / 2);
     launch_pf_qkv(R.q, R.k, R.v, qn, kn, cs, sn, KCo, VCo, pos0, M, st, sib, hd, own, dpos);
     const float* ogs = nullptr;  // group sums of the staged attention rows (split path)
+    bool oq = false;             // W4A8: the merge also quantised the rows for o
     if (split) pmark(c, PT_ATTN, 1, 0);  // the split-KV attention (E:1327 T_ATT)
     if (split && spd) {
       const int ty = hd == 512;
+      oq = a8 && hd == HD;
       if (hd == 512)
         launch_attn_geom_dev_hd(KCo, VCo, R.q, NQ * 512, geo + ty, M, nsplit, NQ, c->po5.as<float>(),
                                 c->pm5.as<float>(), c->pl5.as<float>(), R.att, NQ * 512, st, attgs);
       else
         launch_attn_geom_dev(KCo, VCo, R.q, NQ * HD, geo + ty, M, nsplit, c->po.as<float>(), c->pm.as<float>(),
-                             c->pl.as<float>(), R.att, NQ * HD, st, NQ, attgs);
+                             c->pl.as<float>(), R.att, NQ * HD, st, NQ, attgs, oq ? c->q8w.as<uint64_t>() : nullptr,
+                             oq ? c->q8s.as<float>() : nullptr);
       ogs = attgs;
     } else if (split) {
       AttnGeom ag{};
@@ -2202,6 +2222,10 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.ldy[0] = H;
       a.xs = reinterpret_cast<const float4*>(R.att);
       a.gs = ogs;
+      if (oq) {
+        a.xq = c->q8w.as<uint64_t>();
+        a.xqs = c->q8s.as<float>();
+      }
       a.K = NQ * hd;
       a.M = M;
       const Mat* ms[1] = {&lay.m[3]};
@@ -2224,6 +2248,10 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       if (a8) {  // the gate and up matrices' own a8 tiles (their pairs meet in one block)
         a.mat[0] = a8t(lay.m[4]);
         a.mat[1] = a8t(lay.m[5]);
+        if (a8_gateup_quantises(G.I)) {  // the activation quantised for down by the same blocks
+          a.yq = c->q8w.as<uint64_t>();
+          a.yqs = c->q8s.as<float>();
+        }
         (void)launch_gemv_a8(a, st);
       } else {
         launch_gemv_t(a, st, rows_of(2), tile_of(2));
@@ -2236,6 +2264,10 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
       a.y[0] = R.o;
       a.ldy[0] = H;
       a.xs = reinterpret_cast<const float4*>(R.act);
+      if (a8_gateup_quantises(G.I)) {
+        a.xq = c->q8w.as<uint64_t>();
+        a.xqs = c->q8s.as<float>();
+      }
       a.K = G.I;
       a.M = M;
       (void)launch_gemv_a8(a, st);

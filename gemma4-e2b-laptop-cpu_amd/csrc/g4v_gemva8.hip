@@ -32,32 +32,6 @@ namespace g4v {
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-// quant of one 32-group (engine/w4a8_avx2.h:33-41) into its four operand words.  q = RNE(x * inv)
-// clamped to [-128, 127] is formed as y = med3(x * inv, -128, 127) + 1.5 * 2^23: the add rounds to
-// the nearest integer, ties to even (the ulp there is 1), as cvtps_epi32 does in the default mode,
-// and clamping before rounding gives the same integer (the bounds are integers, rounding is
-// monotonic); the low byte of y's bits is then q in two's complement.
-__device__ __forceinline__ float a8_quant_group(const float (&v)[32], uint64_t (&aq)[4]) {
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  const float sx = amax / 127.0f, inv = sx > 0.f ? 1.0f / sx : 0.0f;
-  uint32_t qb[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i)
-    qb[i] = __float_as_uint(__builtin_amdgcn_fmed3f(v[i] * inv, -128.0f, 127.0f) + 12582912.0f);
-  // operand word h: low dword elements 8h + 0, 2, 4, 6, high dword 8h + 1, 3, 5, 7 (low bytes)
-  auto pack4 = [](uint32_t a, uint32_t b, uint32_t c, uint32_t d) -> uint32_t {
-    return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | (__builtin_amdgcn_perm(d, c, 0x0c0c0400u) << 16);
-  };
-#pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    const uint32_t* q = qb + 8 * h;
-    aq[h] = (uint64_t)pack4(q[0], q[2], q[4], q[6]) | ((uint64_t)pack4(q[1], q[3], q[5], q[7]) << 32);
-  }
-  return sx;
-}
-
 // the B operand of one group: the lane's dword of weight nibbles (elements 8h .. 8h+7 of its
 // output row) as the eight signed bytes u - 8, low nibbles first
 __device__ __forceinline__ long a8_wbytes(uint32_t d) {
@@ -103,7 +77,7 @@ constexpr size_t a8p_lds() {
   return (size_t)128 * (PG + 4) * 4 + (size_t)2 * 8 * (PG + 4) * 4 + (size_t)2 * (PG / 8) * 16 * 16 +
          (size_t)PG * A8P_QS * 8;
 }
-template <int PG>
+template <int PG, bool PQ>
 __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
   constexpr int PC = PG / 4, NU = PC / 8, S = PG + 4, QT = 384, QR = (PG * 8 + QT - 1) / QT;
   static_assert(PC % 8 == 0 && 2 * PG <= QT && QR <= 2, "whole chunks per wave; a scale word per staging thread");
@@ -126,19 +100,28 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
   // the staged floats of a producer's tasks (k = tq + QT r: group k >> msh of the phase, row
   // k & (2^msh - 1)); float4 jj of a group holds elements 2jj, 16 + 2jj, 2jj + 1, 17 + 2jj.  A task
   // past the rows or the groups reads zeros (offset past the resource).
-  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(a.xs, (uint32_t)M * K * 4);
-  float4 xr[QR][8];
+  // PQ (rows quantised by their producer): a task fetches its group's four operand words and
+  // scale instead (a8_quant_group's output for the same floats)
+  const __amdgpu_buffer_rsrc_t xrs =
+      PQ ? buf_rsrc(a.xq, (uint32_t)M * G * 32) : buf_rsrc(a.xs, (uint32_t)M * K * 4);
+  const __amdgpu_buffer_rsrc_t xsr = buf_rsrc(a.xqs, PQ ? (uint32_t)M * G * 4 : 0u);
+  constexpr int XW = PQ ? 2 : 8;  // 16-byte words a task fetches
+  float4 xr[QR][XW];
+  float xsv[QR];
   auto issue_x = [&](int p) {
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
       const int k = tq + QT * r, g = p * PG + (k >> msh), m = k & ((1 << msh) - 1);
       const bool ok = tq >= 0 && k < (PG << msh) && m < M && g < G;
-      const uint32_t off = ok ? ((uint32_t)m * K + 32u * g) * 4u : 0x7FFFFF00u;
+      const uint32_t off = ok ? (PQ ? ((uint32_t)m * G + g) * 32u : ((uint32_t)m * K + 32u * g) * 4u) : 0x7FFFFF00u;
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
+      for (int jj = 0; jj < XW; ++jj) {
         const uint4 u = buf_load16(xrs, off + 16 * jj);
         xr[r][jj] = make_float4(as_f32(u.x), as_f32(u.y), as_f32(u.z), as_f32(u.w));
       }
+      if constexpr (PQ)
+        xsv[r] = as_f32((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+            xsr, ok ? (int)(((uint32_t)m * G + g) * 4u) : 0x7FFFFF00, 0, 0));
     }
   };
   // the phase's weight scales (producer thread tq < 2 PG: a word of the tile's scales; other
@@ -157,16 +140,27 @@ __global__ __launch_bounds__(512) void k_gemv_a8p(GemvTArgs a) {
     for (int r = 0; r < QR; ++r) {
       const int k = tq + QT * r, gl = k >> msh, m = k & ((1 << msh) - 1);
       if (k < (PG << msh)) {
-        float v[32];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          v[2 * jj] = xr[r][jj].x;
-          v[16 + 2 * jj] = xr[r][jj].y;
-          v[2 * jj + 1] = xr[r][jj].z;
-          v[17 + 2 * jj] = xr[r][jj].w;
-        }
         uint64_t aq[4];
-        float sx = a8_quant_group(v, aq);
+        float sx;
+        if constexpr (PQ) {
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const float4 f = xr[r][h >> 1];
+            aq[h] = (h & 1) ? ((uint64_t)__float_as_uint(f.w) << 32 | __float_as_uint(f.z))
+                            : ((uint64_t)__float_as_uint(f.y) << 32 | __float_as_uint(f.x));
+          }
+          sx = xsv[r];
+        } else {
+          float v[32];
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            v[2 * jj] = xr[r][jj].x;
+            v[16 + 2 * jj] = xr[r][jj].y;
+            v[2 * jj + 1] = xr[r][jj].z;
+            v[17 + 2 * jj] = xr[r][jj].w;
+          }
+          sx = a8_quant_group(v, aq);
+        }
         if (m >= M || p * PG + gl >= G) {
           sx = 0.f;
 #pragma unroll
@@ -533,7 +527,26 @@ __global__ __launch_bounds__(512) void k_gemv_a8n(GemvTArgs a) {
     if (tid < CG * 64 && cm < M) {  // pair tile pt = tid / 128: gate group 2 pt, up group 2 pt + 1
       const int pt = tid >> 7;
       const float g = YL[((2 * pt) * 8 + cm) * 16 + cn], u = YL[((2 * pt + 1) * 8 + cm) * 16 + cn];
-      a.y[0][(size_t)cm * a.ldy[0] + staged_index(16 * (mt0 + pt) + cn)] = r16(r16(gelu8(r16(g))) * r16(u));
+      const float act = r16(r16(gelu8(r16(g))) * r16(u));
+      a.y[0][(size_t)cm * a.ldy[0] + staged_index(16 * (mt0 + pt) + cn)] = act;
+      if (CG == 4) U[cm * 32 + 16 * pt + cn] = act;  // (the chains are done with U)
+    }
+    if constexpr (CG == 4) {
+      // the block's 32 outputs are group mt0 / 2 of every row: quantised here for the down
+      // product (engine/w4a8_avx2.h:33-41 on the same floats it would quantise)
+      if (a.yq) {  // (uniform)
+        __syncthreads();
+        if (tid < M) {
+          float v[32];
+#pragma unroll
+          for (int k = 0; k < 32; ++k) v[k] = U[tid * 32 + k];
+          uint64_t q[4];
+          const size_t gq = (size_t)tid * (a.mat[0].N / 32) + (mt0 >> 1);
+          a.yqs[gq] = a8_quant_group(v, q);
+#pragma unroll
+          for (int hw = 0; hw < 4; ++hw) a.yq[gq * 4 + hw] = q[hw];
+        }
+      }
     }
   } else if (chain) {
     const int n = 16 * mt0 + cn;
@@ -562,14 +575,20 @@ int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
   }
   const dim3 b(512);
   if (!a.nrm_mode) {
-    if (!a.xs || a.gateup || a.epi_pli || a.K > 32 * A8P_PG * A8P_NPM) return 0;
+    if (!(a.xq ? a.xqs != nullptr : a.xs != nullptr) || a.gateup || a.epi_pli || a.K > 32 * A8P_PG * A8P_NPM)
+      return 0;
     static bool raised_p = false;  // more than 64 KB of LDS (gfx950: up to 160 KB on request)
     if (!raised_p) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_a8p<A8P_PG>),
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_a8p<A8P_PG, false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)a8p_lds<A8P_PG>());
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_a8p<A8P_PG, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)a8p_lds<A8P_PG>());
       raised_p = true;
     }
-    hipLaunchKernelGGL(k_gemv_a8p<A8P_PG>, dim3(tiles), b, a8p_lds<A8P_PG>(), st, a);
+    if (a.xq)
+      hipLaunchKernelGGL((k_gemv_a8p<A8P_PG, true>), dim3(tiles), b, a8p_lds<A8P_PG>(), st, a);
+    else
+      hipLaunchKernelGGL((k_gemv_a8p<A8P_PG, false>), dim3(tiles), b, a8p_lds<A8P_PG>(), st, a);
     return tiles;
   }
   if (a.K != H) return 0;
@@ -585,11 +604,12 @@ int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
     if (a.epi_pli || a.mat[0].N != a.mat[1].N || a.mat[2].N) return 0;
     // 4 tiles a block while that leaves one block per CU (a 6144-wide MLP: 192 blocks), else 2
     // (two blocks a CU: the 12288-wide MLP's 768 blocks)
-    if (a.mat[0].N % 32 == 0 && a.mat[0].N / 32 <= 256) {
+    if (a8_gateup_quantises(a.mat[0].N)) {
       const int grid = a.mat[0].N / 32;
       hipLaunchKernelGGL((k_gemv_a8n<0, 4>), dim3(grid), b, (a8n_lds<4>()), st, a);
       return grid;
     }
+    if (a.yq) return 0;  // (two tiles a block own half a group)
     const int grid = a.mat[0].N / 16;
     hipLaunchKernelGGL((k_gemv_a8n<0, 2>), dim3(grid), b, (a8n_lds<2>()), st, a);
     return grid;

@@ -78,6 +78,32 @@ __host__ __device__ __forceinline__ int staged_index(int n) {
 // without clamped duplicate fetches).  The base must be uniform over the wave.  Being intrinsic
 // calls rather than plain loads, a ring of them carried across a loop's back edge stays a ring
 // (plain loads there get folded into loads at the top of the next iteration).
+// quant of one 32-group (engine/w4a8_avx2.h:33-41) into its four operand words.  q = RNE(x * inv)
+// clamped to [-128, 127] is formed as y = med3(x * inv, -128, 127) + 1.5 * 2^23: the add rounds to
+// the nearest integer, ties to even (the ulp there is 1), as cvtps_epi32 does in the default mode,
+// and clamping before rounding gives the same integer (the bounds are integers, rounding is
+// monotonic); the low byte of y's bits is then q in two's complement.
+__device__ __forceinline__ float a8_quant_group(const float (&v)[32], uint64_t (&aq)[4]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float sx = amax / 127.0f, inv = sx > 0.f ? 1.0f / sx : 0.0f;
+  uint32_t qb[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    qb[i] = __float_as_uint(__builtin_amdgcn_fmed3f(v[i] * inv, -128.0f, 127.0f) + 12582912.0f);
+  // operand word h: low dword elements 8h + 0, 2, 4, 6, high dword 8h + 1, 3, 5, 7 (low bytes)
+  auto pack4 = [](uint32_t a, uint32_t b, uint32_t c, uint32_t d) -> uint32_t {
+    return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | (__builtin_amdgcn_perm(d, c, 0x0c0c0400u) << 16);
+  };
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const uint32_t* q = qb + 8 * h;
+    aq[h] = (uint64_t)pack4(q[0], q[2], q[4], q[6]) | ((uint64_t)pack4(q[1], q[3], q[5], q[7]) << 32);
+  }
+  return sx;
+}
+
 // A block barrier that orders LDS only: each wave's LDS operations complete before it, while
 // its global loads stay in flight across it (__syncthreads' workgroup fence also waits for every
 // outstanding global load, so register prefetches issued before it would all land there).  For
@@ -260,6 +286,13 @@ struct GemvTArgs {
   // bit mi set: matrix mi's outputs are written in the 16-lane head order (head16_index), the
   // order the verify pass's attention reads its query, key and value rows in
   int yperm;
+  // W4A8 products (launch_gemv_a8): xq / xqs, the staged rows already quantised (operand words
+  // [M][K/32][4], scales [M][K/32]) in place of xs; yq / yqs (gate / up of the 6144-wide MLP): the
+  // activation also quantised, group c of row m at yq[(m * N / 32 + c) * 4] and yqs[m * N / 32 + c]
+  const uint64_t* xq;
+  const float* xqs;
+  uint64_t* yq;
+  float* yqs;
 };
 // W4A8 (g4v_w4a8.hip): operand tiles of a matrix from its original bytes [N][K/2] and scales
 // [N][K/32] (N % 16 == 0): tw [N/16][K/128][64] uint4, ts [N/16][K/256][16] uint4
@@ -300,6 +333,9 @@ int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr);
 // staged input xs (quantised in the product's blocks) or a norm prologue (modes 1 and 2, or 3
 // with epi_pli).  Returns the grid size of the product (0: refused, nothing launched).
 int launch_gemv_a8(const GemvTArgs& a, hipStream_t st);
+// whether launch_gemv_a8's gate / up launch of N pairs honours yq / yqs (four tiles a block: each
+// block owns one 32-group of every row)
+inline bool a8_gateup_quantises(int N) { return N % 32 == 0 && N / 32 <= 256; }
 // returns the grid size used (the number of EPI_SCREEN partials per activation row)
 int launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
 // grid launch_gemv would use

@@ -180,8 +180,10 @@ struct AttnGeom {
 };
 // E:1019-1059 alone: the merge of T splits' partials po [T][M][8][256], pm, pl (as k_attn_rows leaves
 // them) into out [M][ldo]; with gs, out staged (staged_index) with its group sums [M][ldo / 32]
+// xq / xqs not null (with gs): the rows also quantised for a W4A8 product, the four operand words of
+// group g of row m at xq[(m * ldo / 32 + g) * 4] and its scale at xqs[m * ldo / 32 + g]
 void launch_attn_merge(const float* po, const float* pm, const float* pl, int M, int T, float* out, int ldo,
-                       float* gs, hipStream_t st);
+                       float* gs, hipStream_t st, uint64_t* xq = nullptr, float* xqs = nullptr);
 // nh query heads (a multiple of 2, at most 8) of q rows [M][ldq]; partials keep the 8-head layout
 // gs not null: out written in the staged GEMV input layout (staged_index) with its group sums
 // [M][ldo / 32]
@@ -203,7 +205,7 @@ void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float
 // the same with the geometry read from device memory (M rows and T splits fixed by the launch)
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
                           int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ,
-                          float* gs = nullptr);
+                          float* gs = nullptr, uint64_t* xq = nullptr, float* xqs = nullptr);
 // E:1325-1326 the split geometry of a verify pass from its step parameters: geo[0] for the
 // sliding-window layers, geo[1] for the global ones (window 512 from each row's RoPE position),
 // T splits
