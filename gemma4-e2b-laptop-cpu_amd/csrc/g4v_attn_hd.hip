@@ -164,11 +164,13 @@ __global__ __launch_bounds__(D) void k_attn_split_d(const uint16_t* __restrict__
 }
 
 // E:1019-1059, one block per (row m, head h), one thread per dim; out staged (the o-projection
-// input, staged_index) with its group sums when gs is given, else plain [M][ldo]
+// input, staged_index) with its group sums when gs is given, else plain [M][ldo]; with gs and xq,
+// the rows also quantised for a W4A8 product (words of group g of row m at xq[(m ldo / 32 + g) 4])
 template <int D>
 __global__ __launch_bounds__(D) void k_attn_merge_d(const float* __restrict__ po, const float* __restrict__ pm,
                                                     const float* __restrict__ pl, int M, int T, float* __restrict__ out,
-                                                    int ldo, float* __restrict__ gs) {
+                                                    int ldo, float* __restrict__ gs, uint64_t* __restrict__ xq,
+                                                    float* __restrict__ xqs) {
   __shared__ __align__(16) float ys[D];
   const int m = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
   float M0 = -1e30f;
@@ -209,6 +211,16 @@ __global__ __launch_bounds__(D) void k_attn_merge_d(const float* __restrict__ po
     }
     gs[(size_t)m * (ldo / 32) + h * (D / 32) + i] = s;
   }
+  if (xq && i < D / 32) {  // engine/w4a8_avx2.h:33-41 on the head's groups (ys in plain order)
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = ys[i * 32 + k];
+    uint64_t q[4];
+    const size_t gq = (size_t)m * (ldo / 32) + h * (D / 32) + i;
+    xqs[gq] = a8_quant_group(v, q);
+#pragma unroll
+    for (int hw = 0; hw < 4; ++hw) xq[gq * 4 + hw] = q[hw];
+  }
 }
 
 int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom& g, int hd,
@@ -218,18 +230,19 @@ int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, 
   if (len < 1 || (len + g.T - 1) / g.T + 1 > ATT_SPLIT_MAX) return -1;
   hipLaunchKernelGGL(k_attn_split_d<512>, dim3(g.T, g.M, NQ), dim3(512), 0, st, KC, VC, q, ldq, g,
                      (const AttnGeom*)nullptr, po, pm, pl);
-  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(g.M, NQ), dim3(512), 0, st, po, pm, pl, g.M, g.T, out, ldo, gs);
+  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(g.M, NQ), dim3(512), 0, st, po, pm, pl, g.M, g.T, out, ldo, gs,
+                     (uint64_t*)nullptr, (float*)nullptr);
   return 0;
 }
 
 void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev,
                              int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st,
-                             float* gs) {
+                             float* gs, uint64_t* xq, float* xqs) {
   AttnGeom g{};
   g.M = M;
   g.T = T;
   hipLaunchKernelGGL(k_attn_split_d<512>, dim3(T, M, nh), dim3(512), 0, st, KC, VC, q, ldq, g, gdev, po, pm, pl);
-  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(M, nh), dim3(512), 0, st, po, pm, pl, M, T, out, ldo, gs);
+  hipLaunchKernelGGL(k_attn_merge_d<512>, dim3(M, nh), dim3(512), 0, st, po, pm, pl, M, T, out, ldo, gs, xq, xqs);
 }
 
 }  // namespace g4v

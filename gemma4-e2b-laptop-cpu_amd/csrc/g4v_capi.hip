@@ -2180,10 +2180,11 @@ void gm_verify_forward(g4v_ctx* c, int M, int pos0, int nsplit, int sib, float* 
     if (split) pmark(c, PT_ATTN, 1, 0);  // the split-KV attention (E:1327 T_ATT)
     if (split && spd) {
       const int ty = hd == 512;
-      oq = a8 && hd == HD;
+      oq = a8;
       if (hd == 512)
         launch_attn_geom_dev_hd(KCo, VCo, R.q, NQ * 512, geo + ty, M, nsplit, NQ, c->po5.as<float>(),
-                                c->pm5.as<float>(), c->pl5.as<float>(), R.att, NQ * 512, st, attgs);
+                                c->pm5.as<float>(), c->pl5.as<float>(), R.att, NQ * 512, st, attgs,
+                                oq ? c->q8w.as<uint64_t>() : nullptr, oq ? c->q8s.as<float>() : nullptr);
       else
         launch_attn_geom_dev(KCo, VCo, R.q, NQ * HD, geo + ty, M, nsplit, c->po.as<float>(), c->pm.as<float>(),
                              c->pl.as<float>(), R.att, NQ * HD, st, NQ, attgs, oq ? c->q8w.as<uint64_t>() : nullptr,

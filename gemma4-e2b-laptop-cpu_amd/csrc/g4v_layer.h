@@ -201,7 +201,7 @@ int launch_attn_geom_hd(const uint16_t* KC, const uint16_t* VC, const float* q, 
 // or, with gs, staged with its group sums
 void launch_attn_geom_dev_hd(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev,
                              int M, int T, int nh, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st,
-                             float* gs = nullptr);
+                             float* gs = nullptr, uint64_t* xq = nullptr, float* xqs = nullptr);
 // the same with the geometry read from device memory (M rows and T splits fixed by the launch)
 void launch_attn_geom_dev(const uint16_t* KC, const uint16_t* VC, const float* q, int ldq, const AttnGeom* gdev, int M,
                           int T, float* po, float* pm, float* pl, float* out, int ldo, hipStream_t st, int nh = NQ,
