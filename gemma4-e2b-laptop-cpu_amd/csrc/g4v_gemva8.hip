@@ -602,8 +602,7 @@ int launch_gemv_a8(const GemvTArgs& a, hipStream_t st) {
   }
   if (a.gateup) {
     if (a.epi_pli || a.mat[0].N != a.mat[1].N || a.mat[2].N) return 0;
-    // 4 tiles a block while that leaves one block per CU (a 6144-wide MLP: 192 blocks), else 2
-    // (two blocks a CU: the 12288-wide MLP's 768 blocks)
+    // 4 tiles a block (each block owns one 32-group of every row, quantised here for down)
     if (a8_gateup_quantises(a.mat[0].N)) {
       const int grid = a.mat[0].N / 32;
       hipLaunchKernelGGL((k_gemv_a8n<0, 4>), dim3(grid), b, (a8n_lds<4>()), st, a);

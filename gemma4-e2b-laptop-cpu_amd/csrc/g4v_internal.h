@@ -335,7 +335,7 @@ int launch_gemv_t(const GemvTArgs& a, hipStream_t st, int mpl, int tr);
 int launch_gemv_a8(const GemvTArgs& a, hipStream_t st);
 // whether launch_gemv_a8's gate / up launch of N pairs honours yq / yqs (four tiles a block: each
 // block owns one 32-group of every row)
-inline bool a8_gateup_quantises(int N) { return N % 32 == 0 && N / 32 <= 256; }
+inline bool a8_gateup_quantises(int N) { return N % 32 == 0; }
 // returns the grid size used (the number of EPI_SCREEN partials per activation row)
 int launch_gemv(const GemvArgs& a, int epi, hipStream_t st, int grid_cap = 0);
 // grid launch_gemv would use
