@@ -317,12 +317,15 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(GemvArgs a) {
       }
       have_A = false;
       for (int cb = p0; cb < pend; cb += B) {
-        load_batch(wB, cb + B, pend - 1);  // next batch in flight while this one is used
+        const bool more = cb + B < pend;             // (uniform)
+        if (more) load_batch(wB, cb + B, pend - 1);  // next batch in flight while this one is used
 #pragma unroll
         for (int b = 0; b < B; ++b)
           if (cb + b < pend) chunk(wA[b], cb + b, (cb + b - p0) * 8);  // uniform condition
+        if (more) {
 #pragma unroll
-        for (int b = 0; b < B; ++b) wA[b] = wB[b];
+          for (int b = 0; b < B; ++b) wA[b] = wB[b];
+        }
       }
     }
     // 8-lane tree sum per activation row; lane j keeps the sum of row m0 + j
