@@ -21,11 +21,14 @@
 //   k_gemv_a8p       a product of staged rows (o, down, the per-layer projection): a block per
 //                    16 outputs walks K in phases of PG groups, quantises the phase's groups of
 //                    every row into LDS, the next phase's weight words and row floats in flight
-//                    while the current one is multiplied and chained;
+//                    while the current one is multiplied and chained; with PQ it copies instead
+//                    the operand words that the rows' producer wrote (the split-KV merges for o,
+//                    the gate / up blocks for down: a8_quant_group on the same floats);
 //   k_gemv_a8n       a product whose prologue forms its rows as k_gemv_t's norm prologue does
 //                    (q/k/v, gate/up, the per-layer-input gate; K = 1536, one phase) and
-//                    quantises them in LDS; epilogues: y, the gate / up activation (staged) or
-//                    the per-layer-input gate (staged).
+//                    quantises them in LDS; epilogues: y, the gate / up activation (staged; four
+//                    tiles a block, each block one 32-group of every row, also quantised for down)
+//                    or the per-layer-input gate (staged).
 #include "g4v_internal.h"
 
 namespace g4v {
@@ -60,7 +63,8 @@ __device__ __forceinline__ float a8_scale(uint4 s4, int e) {  // bf16 scale e of
 //     and store each (row, output, group)'s a32 as float, chain-major (rows past M are not
 //     stored);
 //   - waves 0-1 (a lane per (row, output)) run the phase's chain, forming sw * sx from the
-//     staged scales as they go, while waves 2-7 quantise the next phase.
+//     staged scales as they go, while waves 2-7 quantise the next phase (PQ: copy its operand
+//     words and row scales, fetched during the previous phase).
 // The block's LDS traffic bounds the phases (a CU's LDS moves about 128 bytes a cycle): the
 // chain reads 16-byte words of 4 groups, and only the matrix-core results go through LDS.
 // One LDS barrier after the quantisation, one after the products (the weight words stay in
